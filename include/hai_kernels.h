@@ -1,0 +1,222 @@
+/* hai_kernels.h -- C ABI of the gfx950 kernels for the HybridAI MTP verify path.
+ *
+ * This is the thin layer through which the C++ host (MI355X Backend and the
+ * verify engine) reaches HIP.  It replaces the reference's launcher free
+ * functions (src/backends/hip/hip_kernels.h:12-95,
+ * src/backends/hip/hip_fused_kernels.h:14-26) and the rocBLAS call inside
+ * HipBackend::gemm (src/backends/hip/hip_backend.cc:697-809).
+ *
+ * Rules shared by every entry point:
+ *   - pointers are device pointers owned by the caller; nothing here
+ *     allocates except hai_malloc; workspaces are passed in;
+ *   - calls are asynchronous on `stream` (NULL = the null stream); the return
+ *     value is the argument-check / launch status, device faults surface at
+ *     the next synchronisation;
+ *   - bf16 tensors are uint16 bit patterns, stores round to nearest even;
+ *   - the arithmetic is the canonical order documented in DESIGN.md
+ *     (bit-identical to the CPU oracle).
+ */
+#ifndef HAI_KERNELS_H
+#define HAI_KERNELS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes; the numbers match hybridai::StatusCode (src/core/status.h:9-21). */
+enum {
+    HAI_OK = 0,
+    HAI_ERR_INVALID_ARGUMENT = 1,
+    HAI_ERR_OUT_OF_MEMORY = 2,
+    HAI_ERR_NOT_IMPLEMENTED = 3,
+    HAI_ERR_INVALID_DEVICE = 5,
+    HAI_ERR_BACKEND = 9,
+};
+
+/* Text of the last error raised on the calling thread. */
+const char* hai_last_error(void);
+
+/* ------------------------------------------------------------------ runtime
+ * Replaces the HIP runtime calls made by HipBackend (hip_backend.cc:425-695). */
+int hai_device_count(int* count);
+int hai_set_device(int device);
+int hai_get_device(int* device);
+int hai_malloc(void** ptr, size_t bytes);
+int hai_free(void* ptr);
+int hai_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream);
+int hai_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream);
+int hai_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream);
+int hai_memset(void* dst, int value, size_t bytes, void* stream);
+int hai_stream_create(void** stream);
+int hai_stream_destroy(void* stream);
+int hai_stream_synchronize(void* stream);
+int hai_device_synchronize(void);
+int hai_event_create(void** event);
+int hai_event_destroy(void* event);
+int hai_event_record(void* event, void* stream);
+int hai_event_synchronize(void* event);
+int hai_event_elapsed_ms(void* start, void* stop, float* ms);
+/* Stream capture into a replayable graph (replaces per-op launches). */
+int hai_graph_begin_capture(void* stream);
+int hai_graph_end_capture(void* stream, void** graph_exec);
+int hai_graph_launch(void* graph_exec, void* stream);
+int hai_graph_destroy(void* graph_exec);
+
+/* ------------------------------------------------------------------ linear
+ * Y[m, n] = sum_k X[m, k] W[n, k] with W stored [N, K] row-major
+ * (Linear::forward_into, linear.cc:117-179; rocblas_gemm_ex at
+ * hip_backend.cc:784-789).  Requirements: K % 8 == 0, ldx % 8 == 0,
+ * 16-byte aligned X and W, M <= 16 per call (callers split larger M; rows
+ * are independent so the split does not change any bit).
+ * Epilogues:
+ *   HAI_EPI_STORE     y = bf16(acc)
+ *   HAI_EPI_RESIDUAL  y = bf16(res + bf16(acc))   (make_residual fused,
+ *                     qwen_reference.cc:121-144; y may alias res)
+ *   HAI_EPI_SILU_MUL  weight rows interleave (gate_f, up_f); writes N/2
+ *                     columns y = bf16(silu(bf16(g)) * bf16(u))
+ *                     (qwen_mlp_reference + silu_mul_kernel,
+ *                     qwen_reference.cc:146-175, hip_kernels.hip:164-175). */
+enum { HAI_EPI_STORE = 0, HAI_EPI_RESIDUAL = 1, HAI_EPI_SILU_MUL = 2 };
+int hai_gemm_bf16(void* y, int64_t ldy, const void* x, int64_t ldx,
+                  const void* w, int64_t M, int64_t N, int64_t K, int epilogue,
+                  const void* res, int64_t ld_res, void* stream);
+
+/* ------------------------------------------------------------------ norms
+ * rmsnorm_kernel (hip_kernels.hip:105-137): y = x * inv * (w + offset),
+ * inv = 1/sqrt(sum x^2 / H + eps).  Strided rows so the MTP concat
+ * (generator.cc:24-66) is written in place. */
+int hai_rmsnorm_bf16(void* y, int64_t ldy, const void* x, int64_t ldx,
+                     const void* w, int64_t rows, int64_t H, float eps,
+                     int unit_offset, void* stream);
+/* add_kernel (hip_kernels.hip:43-51). */
+int hai_add_bf16(void* y, const void* a, const void* b, int64_t n, void* stream);
+/* silu_mul_kernel (hip_kernels.hip:164-175). */
+int hai_silu_mul_bf16(void* y, const void* g, const void* u, int64_t n,
+                      void* stream);
+/* embedding_gather_kernel (hip_kernels.hip:88-103); ids are int64, ids out
+ * of [0, V) produce a zero row. */
+int hai_embedding_gather_bf16(void* y, const void* table, const int64_t* ids,
+                              int64_t n_ids, int64_t V, int64_t H, void* stream);
+
+/* RoPE tables: cos/sin[pos][p] of theta = pos / base^(2p/R), p < R/2,
+ * computed by the caller on the host in double precision. */
+
+/* q_gate_rmsnorm_rope_kernel (hip_fused_kernels.hip:87-141).  Row m = b*T+t
+ * of src holds nq heads of [q(D) | gate(D)] starting at column 0.  Query
+ * position = (lens ? lens[b] : 0) + pos_add + t. */
+int hai_q_gate_rmsnorm_rope_bf16(void* q_out, void* gate_out, const void* src,
+                                 int64_t ld_src, const void* q_norm,
+                                 const float* rope_cos, const float* rope_sin,
+                                 int64_t rope_positions, int64_t B, int64_t T,
+                                 int64_t nq, int64_t D, int64_t R,
+                                 const int32_t* lens, int32_t pos_add,
+                                 float eps, void* stream);
+/* K path of GatedGQAAttention (attention.cc:459-464: RMSNorm(+1) -> bf16
+ * -> partial RoPE -> bf16) fused with append_kv_cache_kernel
+ * (hip_kernels.hip:295-308).  Caches are [B][cap][nkv][D]; row t of
+ * sequence b goes to position (lens ? lens[b] : 0) + pos_add + t.  Values
+ * are copied unchanged. */
+int hai_kv_rmsnorm_rope_append_bf16(void* k_cache, void* v_cache, int64_t cap,
+                                    const void* src_k, const void* src_v,
+                                    int64_t ld_src, const void* k_norm,
+                                    const float* rope_cos,
+                                    const float* rope_sin,
+                                    int64_t rope_positions, int64_t B,
+                                    int64_t T, int64_t nkv, int64_t D,
+                                    int64_t R, const int32_t* lens,
+                                    int32_t pos_add, float eps, void* stream);
+/* Plain row append (append_kv_cache_kernel) for callers that already hold
+ * the final K/V rows (Backend::append_kv_cache). */
+int hai_append_kv_bf16(void* k_cache, void* v_cache, int64_t cap,
+                       const void* k, const void* v, int64_t B, int64_t T,
+                       int64_t row_width, const int32_t* lens, int32_t pos_add,
+                       void* stream);
+
+/* ------------------------------------------------------------------ attention
+ * Multi-query causal gated GQA over the cache (cached_gqa_head256_wave64
+ * kernel, hip_kernels.hip:759-844, and the T=1 variant :567-675).  The
+ * cache of sequence b holds L_b = (lens ? lens[b] : 0) + len_add rows
+ * including the T new ones; query t attends keys 0..L_b-T+t.  q/gate/out
+ * are [B*T][nq][D]; gate may be NULL.  scratch must hold
+ * hai_gqa_scratch_bytes(B, T, nq, D, max_len) bytes; max_len bounds every
+ * L_b and sizes the launch. */
+size_t hai_gqa_scratch_bytes(int64_t B, int64_t T, int64_t nq, int64_t D,
+                             int64_t max_len);
+int hai_gqa_verify_bf16(void* out, const void* q, const void* gate,
+                        const void* k_cache, const void* v_cache, int64_t cap,
+                        void* scratch, int64_t B, int64_t T, int64_t nq,
+                        int64_t nkv, int64_t D, const int32_t* lens,
+                        int32_t len_add, int64_t max_len, void* stream);
+
+/* ------------------------------------------------------------------ DeltaNet
+ * Fused grouped causal conv (deltanet_grouped_conv_kernel,
+ * hip_kernels.hip:871-912) + gated delta rule (deltanet_recurrent_kernel,
+ * :985-1095) + gated RMSNorm, for T tokens of B sequences.
+ *   proj rows (ld_proj) hold [qkv(C) | z(nv*dv) | a(nv) | b(nv)] at the given
+ *     column offsets, C = 2*nk*dk + nv*dv in flat [Q|K|V] channel order;
+ *   conv_ring is [B][ring][C] raw inputs indexed by position % ring;
+ *   state is [nslots][B][nv][dv][dk] fp32 (value-major); the state after
+ *     sequence length L lives in slot L % nslots;
+ *   token t of sequence b has position (lens ? lens[b] : 0) + pos_add + t.
+ * With write_all_slots the state after every token is kept (rollback by
+ * length only, no copies); otherwise only the final state is written.
+ * Needs T + Kc - 1 <= ring, and nslots >= T when write_all_slots. */
+int hai_deltanet_verify_bf16(void* out, int64_t ld_out, const void* proj,
+                             int64_t ld_proj, int64_t off_qkv, int64_t off_z,
+                             int64_t off_a, int64_t off_b, const void* conv_w,
+                             void* conv_ring, int64_t ring, float* state,
+                             int64_t nslots, int write_all_slots,
+                             const void* a_log, const void* dt_bias,
+                             const void* norm_w, const int32_t* lens,
+                             int32_t pos_add, int64_t B, int64_t T, int64_t nk,
+                             int64_t nv, int64_t dk, int64_t dv, int64_t Kc,
+                             float eps, void* stream);
+
+/* ------------------------------------------------------------------ argmax / accept
+ * argmax_rows_kernel (hip_kernels.hip:1243-1274) with the CPU tie-break of
+ * argmax_rows_reference (generator.cc:343-360): first maximum, NaN and -inf
+ * never win, an all-invalid row gives 0.  scratch must hold
+ * hai_argmax_scratch_bytes(rows, V). */
+size_t hai_argmax_scratch_bytes(int64_t rows, int64_t V);
+int hai_argmax_rows_bf16(int64_t* out, const void* logits, int64_t ld,
+                         int64_t rows, int64_t V, void* scratch, void* stream);
+
+/* Greedy acceptance of generator.cc:909-916 computed on the device, fused
+ * with the argmax of the T = k+1 verify rows.  For sequence b:
+ *   preds[b*T+t] = argmax(logits row b*T+t);
+ *   a = longest prefix with preds[t] == ids[b*T+1+t] (t < k_b);
+ *   result[b*4+0] = a, [1] = (a == k_b), [2] = 0, [3] = 0;
+ *   target_len[b] += a + 1 (rows 0..a are committed, the rest rolls back);
+ *   mtp_len[b] -= k_b - a unless fully accepted (MTP checkpoint[a]);
+ *   next[b] = preds[b*T+a] (the target token after the committed rows);
+ *   hidden row a is copied to rec_hidden[b] and, on full acceptance, row
+ *   T-1 to h_prev[b].
+ * n_draft holds k_b per sequence (T - 1 for every b when NULL). */
+int hai_verify_argmax_accept_bf16(const void* logits, int64_t V,
+                                  const void* hidden, int64_t H,
+                                  const int64_t* ids, const int32_t* n_draft,
+                                  int64_t B, int64_t T, int64_t* preds,
+                                  int32_t* result, int32_t* target_len,
+                                  int32_t* mtp_len, int64_t* next,
+                                  void* rec_hidden, void* h_prev,
+                                  void* scratch, void* stream);
+
+/* ------------------------------------------------------------------ synthetic data / checks
+ * Synthetic weights: element (r, c) of a [rows, cols] tensor (row stride
+ * ld) gets bf16(std * IrwinHall4(splitmix64(key(seed, tensor_id) + r*cols+c))),
+ * the generator the CPU oracle uses. */
+int hai_fill_synthetic_bf16(void* dst, int64_t rows, int64_t cols, int64_t ld,
+                            uint64_t seed, uint32_t tensor_id, float std_dev,
+                            void* stream);
+/* Evaluates one canonical primitive elementwise (0 exp, 1 log1p, 2 sigmoid,
+ * 3 silu, 4 sqrt, 5 1/x, 6 bf16 round) so tests can pin device bits. */
+int hai_debug_math_f32(float* y, const float* x, int64_t n, int fn, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HAI_KERNELS_H */

@@ -1,0 +1,358 @@
+"""Kernel-level parity: every hai_* entry point against the CPU oracle on the
+same seeded inputs, bit-exact on the bf16 outputs (the oracle follows the
+same canonical reduction order, see oracle/oracle_numerics.h)."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from _hai import assert_bits_equal, hai, orc, rand_bf16
+
+pytestmark = pytest.mark.gpu
+K = None
+
+
+def kern():
+    global K
+    if K is None:
+        K = hai.kernels()
+    return K
+
+
+def dev(a):
+    return hai.DeviceBuffer.from_array(np.ascontiguousarray(a))
+
+
+def out_buf(nbytes):
+    b = hai.DeviceBuffer(nbytes)
+    b.zero()
+    return b
+
+
+# ----------------------------------------------------------------- primitives
+def _special_inputs(rng):
+    xs = [rng.standard_normal(200000).astype(np.float32) * s for s in (0.1, 1.0, 5.0, 30.0, 100.0)]
+    xs.append(np.array([0.0, -0.0, 1e-45, -1e-45, 1e-38, 88.7, 88.72, 88.73, -87.3, -103.9, -104.0,
+                        -110.0, 1e30, -1e30, np.inf, -np.inf, np.nan, 0.5, -0.5, 1.0, -1.0, 2.0,
+                        0.693147, -0.693147, 1e-7, -1e-7], np.float32))
+    return np.concatenate(xs)
+
+
+@pytest.mark.parametrize("fn,name", [(0, "exp"), (1, "log1p"), (2, "sigmoid"), (3, "silu"), (4, "sqrt"),
+                                     (5, "recip"), (6, "bf16")])
+def test_primitives_bit_exact(fn, name):
+    rng = np.random.default_rng(100 + fn)
+    x = _special_inputs(rng)
+    if name == "log1p":
+        x = np.concatenate([np.abs(x) % 1.0, x[x > -1.0], rng.uniform(-0.999, 1.0, 100000).astype(np.float32)])
+    if name == "sqrt":
+        x = np.abs(x)
+    x = x.astype(np.float32)
+    dx, dy = dev(x), out_buf(x.nbytes)
+    hai.check(kern().hai_debug_math_f32(dy.ptr, dx.ptr, x.size, fn, None), "debug_math")
+    got = dy.download(np.float32)
+    if name == "exp":
+        want = orc.cexp(x)
+    elif name == "log1p":
+        want = orc.clog1p(x)
+    elif name == "sigmoid":
+        want = (np.float32(1.0) / (np.float32(1.0) + orc.cexp(-x))).astype(np.float32)
+    elif name == "silu":
+        want = (x / (np.float32(1.0) + orc.cexp(-x))).astype(np.float32)
+    elif name == "sqrt":
+        want = np.sqrt(x)
+    elif name == "recip":
+        with np.errstate(divide="ignore"):
+            want = (np.float32(1.0) / x).astype(np.float32)
+    else:
+        want = orc.round_bf16(x)
+    gb, wb = got.view(np.uint32), want.view(np.uint32)
+    nan_ok = np.isnan(got) & np.isnan(want)
+    bad = np.nonzero((gb != wb) & ~nan_ok)[0]
+    assert bad.size == 0, f"{name}: {bad.size} mismatches, e.g. x={x[bad[:5]]} got={got[bad[:5]]} want={want[bad[:5]]}"
+
+
+# ----------------------------------------------------------------- gemm
+@pytest.mark.parametrize("M,N,K_", [(1, 37, 8), (2, 256, 256), (2, 1536, 256), (3, 4096, 256),
+                                    (4, 100, 1000), (7, 64, 520), (16, 512, 768), (2, 5120, 17408),
+                                    (1, 16480, 5120), (2, 9, 1024)])
+def test_gemm_store(M, N, K_):
+    rng = np.random.default_rng(M * 1000 + N + K_)
+    x, xb = rand_bf16(rng, (M, K_))
+    w, wb = rand_bf16(rng, (N, K_), 0.05)
+    dx, dw, dy = dev(xb), dev(wb), out_buf(M * N * 2)
+    hai.check(kern().hai_gemm_bf16(dy.ptr, N, dx.ptr, K_, dw.ptr, M, N, K_, hai.EPI_STORE, None, 0, None), "gemm")
+    assert_bits_equal(dy.download(np.uint16), orc.gemm(x, w), f"gemm {M}x{N}x{K_}")
+
+
+@pytest.mark.parametrize("M,N,K_", [(2, 256, 256), (4, 5120, 6144), (16, 300, 512)])
+def test_gemm_residual(M, N, K_):
+    rng = np.random.default_rng(7 + M + N)
+    x, xb = rand_bf16(rng, (M, K_))
+    w, wb = rand_bf16(rng, (N, K_), 0.05)
+    h, hb = rand_bf16(rng, (M, N))
+    dx, dw, dh = dev(xb), dev(wb), dev(hb)
+    hai.check(kern().hai_gemm_bf16(dh.ptr, N, dx.ptr, K_, dw.ptr, M, N, K_, hai.EPI_RESIDUAL, dh.ptr, N, None),
+              "gemm residual")
+    want = orc.add(h, orc.gemm(x, w))
+    assert_bits_equal(dh.download(np.uint16), want, "gemm residual")
+
+
+@pytest.mark.parametrize("M,F,K_", [(2, 768, 256), (1, 17408, 5120), (5, 96, 512)])
+def test_gemm_silu_mul(M, F, K_):
+    rng = np.random.default_rng(11 + M + F)
+    x, xb = rand_bf16(rng, (M, K_))
+    g, gb = rand_bf16(rng, (F, K_), 0.05)
+    u, ub = rand_bf16(rng, (F, K_), 0.05)
+    wb = np.empty((2 * F, K_), np.uint16)
+    wb[0::2] = gb
+    wb[1::2] = ub
+    dx, dw, dy = dev(xb), dev(wb), out_buf(M * F * 2)
+    hai.check(kern().hai_gemm_bf16(dy.ptr, F, dx.ptr, K_, dw.ptr, M, 2 * F, K_, hai.EPI_SILU_MUL, None, 0, None),
+              "gemm silu")
+    want = orc.silu_mul(orc.gemm(x, g), orc.gemm(x, u))
+    assert_bits_equal(dy.download(np.uint16), want, "gemm silu_mul")
+
+
+def test_gemm_rejects_bad_shapes():
+    d = out_buf(64)
+    assert kern().hai_gemm_bf16(d.ptr, 4, d.ptr, 12, d.ptr, 2, 4, 12, 0, None, 0, None) == 1  # K % 8
+    assert kern().hai_gemm_bf16(d.ptr, 4, d.ptr, 8, d.ptr, 17, 4, 8, 0, None, 0, None) == 1   # M > 16
+
+
+# ----------------------------------------------------------------- norms
+@pytest.mark.parametrize("rows,H", [(1, 256), (5, 256), (2, 5120), (3, 64)])
+def test_rmsnorm(rows, H):
+    rng = np.random.default_rng(rows + H)
+    x, xb = rand_bf16(rng, (rows, H))
+    w, wb = rand_bf16(rng, (H,), 0.02)
+    dx, dw, dy = dev(xb), dev(wb), out_buf(rows * H * 2)
+    hai.check(kern().hai_rmsnorm_bf16(dy.ptr, H, dx.ptr, H, dw.ptr, rows, H, 1e-6, 1, None), "rmsnorm")
+    assert_bits_equal(dy.download(np.uint16), orc.rmsnorm(x, w, 1e-6, True), "rmsnorm")
+
+
+def test_embedding_and_elementwise():
+    rng = np.random.default_rng(5)
+    V, H = 50, 64
+    tab, tb = rand_bf16(rng, (V, H))
+    ids = np.array([3, 0, 49, 50, -1, 7], np.int64)
+    dt, di, dy = dev(tb), dev(ids), out_buf(ids.size * H * 2)
+    hai.check(kern().hai_embedding_gather_bf16(dy.ptr, dt.ptr, di.ptr, ids.size, V, H, None), "embedding")
+    assert_bits_equal(dy.download(np.uint16), orc.embedding(tab, ids), "embedding")
+    a, ab = rand_bf16(rng, (1000,))
+    b, bb = rand_bf16(rng, (1000,))
+    da, db, dz = dev(ab), dev(bb), out_buf(2000)
+    hai.check(kern().hai_add_bf16(dz.ptr, da.ptr, db.ptr, 1000, None), "add")
+    assert_bits_equal(dz.download(np.uint16), orc.add(a, b), "add")
+    hai.check(kern().hai_silu_mul_bf16(dz.ptr, da.ptr, db.ptr, 1000, None), "silu_mul")
+    assert_bits_equal(dz.download(np.uint16), orc.silu_mul(a, b), "silu_mul")
+
+
+def _rope_dev(npos, R, base):
+    c, s = orc.rope_table(0, npos, R, base)
+    return dev(c), dev(s)
+
+
+@pytest.mark.parametrize("B,T,nq,D,R,base", [(1, 2, 4, 64, 16, 1e7), (1, 4, 24, 256, 64, 1e7),
+                                               (2, 3, 2, 64, 64, 1e4)])
+def test_q_gate_rmsnorm_rope(B, T, nq, D, R, base):
+    rng = np.random.default_rng(B * 7 + T + D)
+    src, sb = rand_bf16(rng, (B * T, nq * 2 * D))
+    w, wb = rand_bf16(rng, (D,), 0.02)
+    lens = np.array([5 + 11 * b for b in range(B)], np.int32)
+    npos = 64
+    cd, sd = _rope_dev(npos, R, base)
+    dsrc, dw, dl = dev(sb), dev(wb), dev(lens)
+    dq, dg = out_buf(B * T * nq * D * 2), out_buf(B * T * nq * D * 2)
+    hai.check(kern().hai_q_gate_rmsnorm_rope_bf16(dq.ptr, dg.ptr, dsrc.ptr, nq * 2 * D, dw.ptr, cd.ptr, sd.ptr,
+                                                  npos, B, T, nq, D, R, dl.ptr, 1, 1e-6, None), "q_gate")
+    gq, gg = dq.download(np.uint16), dg.download(np.uint16)
+    for b in range(B):
+        q, g = orc.q_gate_rmsnorm_rope(src[b * T:(b + 1) * T], w, T, nq, D, R, int(lens[b]) + 1, base)
+        n = T * nq * D
+        assert_bits_equal(gq[b * n:(b + 1) * n], q, "q")
+        assert_bits_equal(gg[b * n:(b + 1) * n], g, "gate")
+
+
+@pytest.mark.parametrize("B,T,nkv,D,R", [(1, 2, 2, 64, 16), (1, 4, 4, 256, 64), (2, 1, 1, 64, 64)])
+def test_kv_norm_rope_append(B, T, nkv, D, R):
+    rng = np.random.default_rng(B + T * 3 + D)
+    base = 1e7
+    cap = 40
+    ld = 2 * nkv * D + 8
+    src, sb = rand_bf16(rng, (B * T, ld))
+    w, wb = rand_bf16(rng, (D,), 0.02)
+    lens = np.array([3 + 17 * b for b in range(B)], np.int32)
+    cd, sd = _rope_dev(cap, R, base)
+    dsrc, dw, dl = dev(sb), dev(wb), dev(lens)
+    kc, vc = out_buf(B * cap * nkv * D * 2), out_buf(B * cap * nkv * D * 2)
+    hai.check(kern().hai_kv_rmsnorm_rope_append_bf16(kc.ptr, vc.ptr, cap, dsrc.ptr, dsrc.ptr + nkv * D * 2, ld,
+                                                     dw.ptr, cd.ptr, sd.ptr, cap, B, T, nkv, D, R, dl.ptr, 0,
+                                                     1e-6, None), "kv append")
+    K_ = kc.download(np.uint16).reshape(B, cap, nkv * D)
+    V_ = vc.download(np.uint16).reshape(B, cap, nkv * D)
+    for b in range(B):
+        rows = src[b * T:(b + 1) * T]
+        k = orc.k_rmsnorm_rope(rows[:, :nkv * D], w, T, nkv, D, R, int(lens[b]), base)
+        p = int(lens[b])
+        assert_bits_equal(K_[b, p:p + T], k, "k cache")
+        assert_bits_equal(V_[b, p:p + T], rows[:, nkv * D:2 * nkv * D], "v cache")
+        assert not K_[b, :p].any() and not K_[b, p + T:].any()
+
+
+# ----------------------------------------------------------------- attention
+@pytest.mark.parametrize("B,T,nq,nkv,D,lens", [
+    (1, 2, 4, 2, 64, [30]), (1, 1, 4, 2, 64, [0]), (1, 4, 24, 4, 256, [60]), (1, 2, 24, 4, 256, [1278]),
+    (2, 3, 4, 1, 128, [63, 200]), (1, 16, 4, 2, 64, [100]), (3, 1, 2, 2, 64, [0, 1, 64])])
+def test_gqa_verify(B, T, nq, nkv, D, lens):
+    rng = np.random.default_rng(B * 100 + T * 10 + D + sum(lens))
+    lens = np.array(lens, np.int32)
+    cap = int(lens.max()) + T + 5
+    q, qb = rand_bf16(rng, (B * T, nq, D))
+    g, gb = rand_bf16(rng, (B * T, nq, D))
+    kcache, kb = rand_bf16(rng, (B, cap, nkv, D))
+    vcache, vb = rand_bf16(rng, (B, cap, nkv, D))
+    dq, dg, dk, dv, dl = dev(qb), dev(gb), dev(kb), dev(vb), dev(lens)
+    max_len = cap
+    scratch = out_buf(kern().hai_gqa_scratch_bytes(B, T, nq, D, max_len))
+    dout = out_buf(B * T * nq * D * 2)
+    hai.check(kern().hai_gqa_verify_bf16(dout.ptr, dq.ptr, dg.ptr, dk.ptr, dv.ptr, cap, scratch.ptr, B, T, nq,
+                                         nkv, D, dl.ptr, T, max_len, None), "gqa")
+    got = dout.download(np.uint16).reshape(B, T * nq * D)
+    for b in range(B):
+        L = int(lens[b]) + T
+        want = orc.attention(q[b * T:(b + 1) * T], g[b * T:(b + 1) * T], kcache[b], vcache[b], T, L, nq, nkv, D)
+        assert_bits_equal(got[b], want, f"gqa b={b}")
+
+
+# ----------------------------------------------------------------- deltanet
+def _deltanet_case(rng, B, nk, nv, dk, dv, Kc=4):
+    kw, vw = nk * dk, nv * dv
+    C = 2 * kw + vw
+    conv_w, cwb = rand_bf16(rng, (C, Kc), 0.3)
+    a_log, alb = rand_bf16(rng, (nv,), 0.5)
+    dt_bias, dtb = rand_bf16(rng, (nv,), 0.5)
+    norm_w, nwb = rand_bf16(rng, (dv,), 0.5)
+    return dict(C=C, conv_w=conv_w, cwb=cwb, a_log=a_log, alb=alb, dt_bias=dt_bias, dtb=dtb, norm_w=norm_w,
+                nwb=nwb, Kc=Kc)
+
+
+def _to_value_major(state, nv, dk, dv):
+    return np.ascontiguousarray(state.reshape(nv, dk, dv).transpose(0, 2, 1))
+
+
+@pytest.mark.parametrize("nk,nv,dk,dv,steps", [(4, 4, 64, 64, [2, 1, 3]), (16, 48, 128, 128, [4, 2]),
+                                               (2, 6, 64, 64, [16, 1])])
+def test_deltanet_verify_rollback(nk, nv, dk, dv, steps):
+    """Chained verify steps with partial acceptance: the kernel's committed
+    state/conv ring after each accepted prefix must equal the oracle's
+    sequential processing of the accepted tokens only."""
+    rng = np.random.default_rng(nk * 1000 + nv + dk)
+    B = 1
+    c = _deltanet_case(rng, B, nk, nv, dk, dv)
+    C, Kc = c["C"], c["Kc"]
+    vw = nv * dv
+    width = C + vw + 2 * nv
+    ring, nslots = 32, 17
+    dring, dstate = out_buf(B * ring * C * 2), out_buf(nslots * B * nv * dk * dv * 4)
+    dcw, dal, ddt, dnw = dev(c["cwb"]), dev(c["alb"]), dev(c["dtb"]), dev(c["nwb"])
+    # oracle state in reference layout
+    conv_state = np.zeros((C, Kc - 1), np.float32)
+    state = np.zeros((nv, dk, dv), np.float32)
+    L = 0
+    lens = dev(np.array([0], np.int32))
+    for si, T in enumerate(steps):
+        proj, pb = rand_bf16(rng, (T, width))
+        dproj, dout = dev(pb), out_buf(T * vw * 2)
+        lens.upload(np.array([L], np.int32))
+        hai.check(kern().hai_deltanet_verify_bf16(dout.ptr, vw, dproj.ptr, width, 0, C, C + vw, C + vw + nv,
+                                                  dcw.ptr, dring.ptr, ring, dstate.ptr, nslots, 1, dal.ptr, ddt.ptr,
+                                                  dnw.ptr, lens.ptr, 0, B, T, nk, nv, dk, dv, Kc, 1e-6, None),
+                  "deltanet")
+        got = dout.download(np.uint16).reshape(T, vw)
+        # oracle over all T tokens from the committed state
+        q, k, v, cs_all = orc.deltanet_conv(proj[:, :C], c["conv_w"], conv_state, T, nk, nv, dk, dv, Kc)
+        out, st_all = orc.deltanet_recurrent(q, k, v, proj[:, C + vw:C + vw + nv], proj[:, C + vw + nv:],
+                                             proj[:, C:C + vw], c["a_log"], c["dt_bias"], c["norm_w"], state, T,
+                                             nk, nv, dk, dv)
+        assert_bits_equal(got, out, f"deltanet step {si} out")
+        # accept a prefix of length acc (1..T) and advance the oracle by exactly those tokens
+        acc = 1 + (si % T)
+        q2, k2, v2, conv_state = orc.deltanet_conv(proj[:acc, :C], c["conv_w"], conv_state, acc, nk, nv, dk, dv, Kc)
+        _, state = orc.deltanet_recurrent(q2, k2, v2, proj[:acc, C + vw:C + vw + nv], proj[:acc, C + vw + nv:],
+                                          proj[:acc, C:C + vw], c["a_log"], c["dt_bias"], c["norm_w"], state, acc,
+                                          nk, nv, dk, dv)
+        L += acc
+        slot = L % nslots
+        dev_state = dstate.download(np.float32).reshape(nslots, B, nv, dv, dk)[slot, 0]
+        want_state = _to_value_major(state, nv, dk, dv)
+        assert np.array_equal(dev_state.view(np.uint32), want_state.view(np.uint32)), f"state after step {si}"
+
+
+# ----------------------------------------------------------------- argmax / accept
+def test_argmax_rows_ties_nan():
+    rng = np.random.default_rng(3)
+    rows, V = 7, 248320
+    x, xb = rand_bf16(rng, (rows, V))
+    x[1, 100] = x[1, 5000] = 50.0
+    x[2, :] = np.nan
+    x[3, :] = -np.inf
+    x[4, 7] = np.nan
+    x[4, 9] = 60.0
+    x[5, 0] = -0.0
+    x[5, :] = -1.0
+    x[5, 10] = -0.0
+    x[5, 11] = 0.0
+    x[6, 248319] = 70.0
+    xb = hai.bf16_bits(x)
+    d, o = dev(xb), out_buf(rows * 8)
+    scratch = out_buf(kern().hai_argmax_scratch_bytes(rows, V))
+    hai.check(kern().hai_argmax_rows_bf16(o.ptr, d.ptr, V, rows, V, scratch.ptr, None), "argmax")
+    got = o.download(np.int64)
+    want = orc.argmax_rows(hai.bf16_to_f32(xb).reshape(rows, V))
+    assert list(got) == list(want)
+    assert got[1] == 100 and got[2] == 0 and got[3] == 0 and got[4] == 9 and got[5] == 10 and got[6] == 248319
+
+
+def test_verify_accept_kernel():
+    rng = np.random.default_rng(9)
+    T, V, H = 4, 1000, 64
+    x, xb = rand_bf16(rng, (T, V))
+    preds = orc.argmax_rows(x)
+    hid, hb = rand_bf16(rng, (T, H))
+    for a_expect in range(T):
+        ids = np.array([17] + [int(p) for p in preds[:T - 1]], np.int64)
+        if a_expect < T - 1:
+            ids[1 + a_expect] = (ids[1 + a_expect] + 1) % V
+        dl, dh, di = dev(xb), dev(hb), dev(ids)
+        dp, dres, dnext = out_buf(T * 8), out_buf(16), out_buf(8)
+        tl, ml = dev(np.array([100], np.int32)), dev(np.array([50], np.int32))
+        rec, hp = out_buf(H * 2), out_buf(H * 2)
+        scratch = out_buf(kern().hai_argmax_scratch_bytes(T, V))
+        hai.check(kern().hai_verify_argmax_accept_bf16(dl.ptr, V, dh.ptr, H, di.ptr, None, 1, T, dp.ptr, dres.ptr,
+                                                       tl.ptr, ml.ptr, dnext.ptr, rec.ptr, hp.ptr, scratch.ptr,
+                                                       None), "accept")
+        res = dres.download(np.int32)
+        a, full = int(res[0]), int(res[1])
+        assert a == a_expect and full == int(a_expect == T - 1)
+        assert list(dp.download(np.int64)) == list(preds)
+        assert int(tl.download(np.int32)[0]) == 100 + a + 1
+        assert int(ml.download(np.int32)[0]) == 50 - (0 if full else (T - 1 - a))
+        assert int(dnext.download(np.int64)[0]) == int(preds[a])
+        assert np.array_equal(rec.download(np.uint16), hb[a])
+        if full:
+            assert np.array_equal(hp.download(np.uint16), hb[T - 1])
+
+
+# ----------------------------------------------------------------- synthetic weights
+def test_fill_synthetic_matches_oracle():
+    m = orc.Model(orc.TINY, seed=0)
+    for tid, shape in [(orc.tensor_id(0, 0), (4096, 256)), (orc.tensor_id(2, 2), (768, 256)),
+                       (orc.tensor_id(5, 11), (512, 256)), (orc.tensor_id(1, 0), (256, 512))]:
+        want = m.tensor(tid).reshape(shape)
+        rows, cols = shape
+        ld = cols + 8
+        d = out_buf(rows * ld * 2)
+        hai.check(kern().hai_fill_synthetic_bf16(d.ptr, rows, cols, ld, 0, tid, 0.02, None), "fill")
+        got = d.download(np.uint16).reshape(rows, ld)[:, :cols]
+        assert_bits_equal(got, want, f"tensor {tid}")

@@ -1,0 +1,172 @@
+// hai_argmax.hip -- per-row argmax of bf16 logits and the fused greedy
+// acceptance of the verify step (argmax_rows_kernel, hip_kernels.hip:
+// 1243-1274; acceptance generator.cc:909-1021).
+//
+// Ties: the reference's CPU scan keeps the first maximum, NaN never wins and
+// -inf never wins (generator.cc:343-360); the reference GPU kernel's result
+// depends on thread striding.  Here each candidate is a 64-bit key
+// (ordered value << 32 | ~index) reduced with max, which yields the CPU
+// answer for any launch shape; invalid values map to key 0 (index 0).
+#include "hai_common.h"
+#include "hai_device.h"
+
+namespace {
+
+using namespace hai;
+
+constexpr int kSlices = 64;  // partial blocks per row
+
+__device__ __forceinline__ uint64_t make_key(float v, int64_t idx) {
+    if (!(v > __uint_as_float(0xff800000u))) return 0ull;  // NaN or -inf
+    uint32_t u = __float_as_uint(v);
+    if ((u & 0x7fffffffu) == 0u) u = 0u;  // -0 ties with +0
+    const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return (static_cast<uint64_t>(ord) << 32) | static_cast<uint64_t>(0xffffffffu - static_cast<uint32_t>(idx));
+}
+__device__ __forceinline__ int64_t key_index(uint64_t key) {
+    if (key == 0ull) return 0;
+    return static_cast<int64_t>(0xffffffffu - static_cast<uint32_t>(key & 0xffffffffull));
+}
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int s) {
+    const uint32_t lo = __shfl_xor(static_cast<uint32_t>(v), s, 64);
+    const uint32_t hi = __shfl_xor(static_cast<uint32_t>(v >> 32), s, 64);
+    return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+__device__ __forceinline__ uint64_t block_max_u64(uint64_t v, uint64_t* sh) {
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) {
+        const uint64_t o = shfl_xor_u64(v, s);
+        v = o > v ? o : v;
+    }
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) sh[wave] = v;
+    __syncthreads();
+    uint64_t best = 0ull;
+    for (int w = 0; w < static_cast<int>(blockDim.x >> 6); ++w) best = sh[w] > best ? sh[w] : best;
+    __syncthreads();
+    return best;
+}
+
+__global__ __launch_bounds__(256) void argmax_partial_kernel(uint64_t* __restrict__ part,
+                                                             const uint16_t* __restrict__ logits,
+                                                             int64_t ld, int64_t V) {
+    __shared__ uint64_t sh[4];
+    const int64_t row = blockIdx.y;
+    const int slice = blockIdx.x;
+    const int64_t per = (V + kSlices - 1) / kSlices;
+    const int64_t start = static_cast<int64_t>(slice) * per;
+    const int64_t end = min(V, start + per);
+    const uint16_t* lr = logits + row * ld;
+    uint64_t best = 0ull;
+    for (int64_t i = start + threadIdx.x; i < end; i += blockDim.x) {
+        const uint64_t k = make_key(bf2f(lr[i]), i);
+        best = k > best ? k : best;
+    }
+    best = block_max_u64(best, sh);
+    if (threadIdx.x == 0) part[row * kSlices + slice] = best;
+}
+
+__global__ __launch_bounds__(256) void argmax_final_kernel(int64_t* __restrict__ out,
+                                                           const uint64_t* __restrict__ part, int64_t rows) {
+    for (int64_t r = threadIdx.x; r < rows; r += blockDim.x) {
+        uint64_t best = 0ull;
+        for (int s = 0; s < kSlices; ++s) {
+            const uint64_t k = part[r * kSlices + s];
+            best = k > best ? k : best;
+        }
+        out[r] = key_index(best);
+    }
+}
+
+// One block: final argmax of the B*T verify rows, then per sequence the
+// accepted prefix, the committed-length update and the hidden-row copies.
+__global__ __launch_bounds__(256) void verify_accept_kernel(
+    const uint64_t* __restrict__ part, const uint16_t* __restrict__ hidden, int64_t H,
+    const int64_t* __restrict__ ids, const int32_t* n_draft, int B, int T, int64_t* __restrict__ preds,
+    int32_t* __restrict__ result, int32_t* target_len, int32_t* mtp_len, int64_t* __restrict__ next,
+    uint16_t* rec_hidden, uint16_t* h_prev) {
+    __shared__ int acc_sh[64];
+    __shared__ int full_sh[64];
+    const int rows = B * T;
+    for (int r = threadIdx.x; r < rows; r += blockDim.x) {
+        uint64_t best = 0ull;
+        for (int s = 0; s < kSlices; ++s) {
+            const uint64_t k = part[static_cast<int64_t>(r) * kSlices + s];
+            best = k > best ? k : best;
+        }
+        preds[r] = key_index(best);
+    }
+    __syncthreads();
+    for (int b = threadIdx.x; b < B; b += blockDim.x) {
+        const int k = n_draft ? n_draft[b] : T - 1;
+        int a = 0;
+        while (a < k && preds[b * T + a] == ids[b * T + 1 + a]) ++a;
+        const int full = a == k ? 1 : 0;
+        result[b * 4 + 0] = a;
+        result[b * 4 + 1] = full;
+        result[b * 4 + 2] = 0;
+        result[b * 4 + 3] = 0;
+        if (target_len) target_len[b] += a + 1;
+        if (mtp_len && !full) mtp_len[b] -= k - a;
+        next[b] = preds[b * T + a];
+        if (b < 64) { acc_sh[b] = a; full_sh[b] = full; }
+    }
+    __syncthreads();
+    if (hidden == nullptr) return;
+    for (int b = 0; b < B && b < 64; ++b) {
+        const int a = acc_sh[b];
+        const uint16_t* src = hidden + (static_cast<int64_t>(b) * T + a) * H;
+        if (rec_hidden)
+            for (int64_t k = threadIdx.x; k < H; k += blockDim.x) rec_hidden[b * H + k] = src[k];
+        if (h_prev && full_sh[b])
+            for (int64_t k = threadIdx.x; k < H; k += blockDim.x) h_prev[b * H + k] = src[k];
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t hai_argmax_scratch_bytes(int64_t rows, int64_t V) {
+    (void)V;
+    return static_cast<size_t>(rows < 1 ? 1 : rows) * kSlices * sizeof(uint64_t);
+}
+
+int hai_argmax_rows_bf16(int64_t* out, const void* logits, int64_t ld, int64_t rows, int64_t V,
+                         void* scratch, void* stream) {
+    if (out == nullptr || logits == nullptr || scratch == nullptr || rows < 0 || V <= 0 || ld < V ||
+        V > 0xfffffffell)
+        return invalid("argmax_rows");
+    if (rows == 0) return HAI_OK;
+    const auto s = as_stream(stream);
+    argmax_partial_kernel<<<dim3(kSlices, static_cast<unsigned>(rows)), dim3(256), 0, s>>>(
+        static_cast<uint64_t*>(scratch), static_cast<const uint16_t*>(logits), ld, V);
+    int rc = launched("argmax_partial_kernel");
+    if (rc != HAI_OK) return rc;
+    argmax_final_kernel<<<dim3(1), dim3(256), 0, s>>>(out, static_cast<const uint64_t*>(scratch), rows);
+    return launched("argmax_final_kernel");
+}
+
+int hai_verify_argmax_accept_bf16(const void* logits, int64_t V, const void* hidden, int64_t H,
+                                  const int64_t* ids, const int32_t* n_draft, int64_t B, int64_t T,
+                                  int64_t* preds, int32_t* result, int32_t* target_len, int32_t* mtp_len,
+                                  int64_t* next, void* rec_hidden, void* h_prev, void* scratch,
+                                  void* stream) {
+    if (logits == nullptr || ids == nullptr || preds == nullptr || result == nullptr || next == nullptr ||
+        scratch == nullptr)
+        return invalid("verify_argmax_accept: null pointer");
+    if (B <= 0 || B > 64 || T <= 0 || V <= 0 || V > 0xfffffffell || (hidden != nullptr && H <= 0))
+        return invalid("verify_argmax_accept: shape (1 <= B <= 64)");
+    const auto s = as_stream(stream);
+    argmax_partial_kernel<<<dim3(kSlices, static_cast<unsigned>(B * T)), dim3(256), 0, s>>>(
+        static_cast<uint64_t*>(scratch), static_cast<const uint16_t*>(logits), V, V);
+    int rc = launched("argmax_partial_kernel");
+    if (rc != HAI_OK) return rc;
+    verify_accept_kernel<<<dim3(1), dim3(256), 0, s>>>(
+        static_cast<const uint64_t*>(scratch), static_cast<const uint16_t*>(hidden), H, ids, n_draft, int(B),
+        int(T), preds, result, target_len, mtp_len, next, static_cast<uint16_t*>(rec_hidden),
+        static_cast<uint16_t*>(h_prev));
+    return launched("verify_accept_kernel");
+}
+
+}  // extern "C"

@@ -1,0 +1,145 @@
+// hai_device.h -- device-side numerics shared by every gfx950 kernel.
+//
+// The verify path must produce the same token ids as a CPU restatement, so
+// each rounding point is fixed:
+//   * bf16 stores round to nearest even; NaN stays a quiet NaN.
+//   * exp / log1p are computed by the canonical algorithms below (fma-based,
+//     no hardware transcendental instructions, no libdevice).
+//   * division and sqrt are IEEE correctly rounded (the build passes
+//     -fhip-fp32-correctly-rounded-divide-sqrt; __fsqrt_rn is avoided because
+//     it maps to the native approximation on this toolchain).
+//   * a row reduction is the "L64 order": element k belongs to lane
+//     (k/8)%64, each lane accumulates its elements in increasing k with fma,
+//     then the 64 partials are combined by the xor butterfly 32,16,8,4,2,1.
+// Everything is built with -ffp-contract=off so that a*b+c written without
+// fma stays two roundings.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace hai {
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float bf2f(uint16_t h) {
+    return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+__device__ __forceinline__ uint16_t f2bf(float f) {
+    const uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+    return static_cast<uint16_t>((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+__device__ __forceinline__ float bfr(float f) { return bf2f(f2bf(f)); }
+
+// Two bf16 packed in a dword: element 0 in the low half.
+__device__ __forceinline__ float lo_bf(uint32_t d) { return __uint_as_float(d << 16); }
+__device__ __forceinline__ float hi_bf(uint32_t d) { return __uint_as_float(d & 0xffff0000u); }
+
+__device__ __forceinline__ float fma_(float a, float b, float c) { return __builtin_fmaf(a, b, c); }
+
+__device__ __forceinline__ float pow2i(int e) {  // e in [-126, 127]
+    return __uint_as_float(static_cast<uint32_t>(e + 127) << 23);
+}
+
+// Canonical exp: Cody-Waite reduction with ln2 = hi + lo, degree-8 Taylor
+// polynomial in Horner form with fma, exact scaling by 2^n (two steps when
+// the result is subnormal).
+__device__ __forceinline__ float cexp(float x) {
+    if (x != x) return x;
+    if (x > 88.72283935546875f) return __uint_as_float(0x7f800000u);
+    if (x < -103.97208404541015625f) return 0.0f;
+    const float t = x * 0x1.715476p+0f;
+    const float n = __builtin_rintf(t);
+    float r = fma_(n, -0x1.62e4p-1f, x);
+    r = fma_(n, -0x1.7f7d1cp-20f, r);
+    float p = 0x1.a01a02p-16f;
+    p = fma_(p, r, 0x1.a01a02p-13f);
+    p = fma_(p, r, 0x1.6c16c2p-10f);
+    p = fma_(p, r, 0x1.111112p-7f);
+    p = fma_(p, r, 0x1.555556p-5f);
+    p = fma_(p, r, 0x1.555556p-3f);
+    p = fma_(p, r, 0.5f);
+    p = fma_(p, r, 1.0f);
+    p = fma_(p, r, 1.0f);
+    int e = static_cast<int>(n);
+    if (e > 127) { p = p * 2.0f; e -= 1; }
+    if (e < -126) { p = p * pow2i(e + 64); return p * 0x1p-64f; }
+    return p * pow2i(e);
+}
+
+// Canonical log1p for x > -1: y = 1 + x with first-order correction
+// (x - (y - 1)) / y, y = m * 2^k with m in [sqrt(1/2), sqrt(2)), and
+// log(m) = 2 atanh(f / (2 + f)) by its odd series to z^4.
+__device__ __forceinline__ float clog1p(float x) {
+    if (x != x) return x;
+    if (x == 0.0f) return x;
+    if (x == __uint_as_float(0x7f800000u)) return x;
+    if (x <= -1.0f) return x == -1.0f ? __uint_as_float(0xff800000u) : __uint_as_float(0x7fc00000u);
+    const float y = 1.0f + x;
+    const float c = (x - (y - 1.0f)) / y;
+    const uint32_t b = __float_as_uint(y);
+    int k = static_cast<int>((b >> 23) & 0xffu) - 126;
+    float m = __uint_as_float((b & 0x807fffffu) | (126u << 23));
+    if (m < 0x1.6a09e6p-1f) { m = m * 2.0f; k -= 1; }
+    const float f = m - 1.0f;
+    const float s = f / (2.0f + f);
+    const float z = s * s;
+    float w = fma_(z, 0x1.c71c72p-3f, 0x1.24924ap-2f);
+    w = fma_(w, z, 0x1.99999ap-2f);
+    w = fma_(w, z, 0x1.555556p-1f);
+    const float logm = fma_(s * z, w, 2.0f * s);
+    const float kf = static_cast<float>(k);
+    float tt = logm + c;
+    tt = fma_(kf, 0x1.7f7d1cp-20f, tt);
+    return fma_(kf, 0x1.62e4p-1f, tt);
+}
+
+__device__ __forceinline__ float csigmoid(float x) { return 1.0f / (1.0f + cexp(-x)); }
+__device__ __forceinline__ float csilu(float x) { return x / (1.0f + cexp(-x)); }
+__device__ __forceinline__ float csqrt(float x) { return __builtin_sqrtf(x); }
+
+// xor butterfly over the 64 lanes of a wave; all lanes get the same bits.
+__device__ __forceinline__ float wave_sum64(float v) {
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) v = v + __shfl_xor(v, s, 64);
+    return v;
+}
+__device__ __forceinline__ float wave_max64(float v) {
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) v = fmaxf(v, __shfl_xor(v, s, 64));
+    return v;
+}
+
+// L64-order sum of squares of a bf16 vector of length n (n % 8 == 0),
+// computed by one wave (lane = threadIdx.x % 64).
+__device__ __forceinline__ float l64_sumsq_bf16(const uint16_t* __restrict__ x, int n, int lane) {
+    float acc = 0.0f;
+    for (int k0 = lane * 8; k0 < n; k0 += 512) {
+        const uint4 d = *reinterpret_cast<const uint4*>(x + k0);
+        const uint32_t w[4] = {d.x, d.y, d.z, d.w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float a = lo_bf(w[q]);
+            const float b = hi_bf(w[q]);
+            acc = fma_(a, a, acc);
+            acc = fma_(b, b, acc);
+        }
+    }
+    return wave_sum64(acc);
+}
+
+// Same order for an fp32 vector held in LDS or global memory.
+__device__ __forceinline__ float l64_sumsq_f32(const float* x, int n, int lane) {
+    float acc = 0.0f;
+    for (int k0 = lane * 8; k0 < n; k0 += 512) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int k = k0 + j;
+            if (k < n) acc = fma_(x[k], x[k], acc);
+        }
+    }
+    return wave_sum64(acc);
+}
+
+}  // namespace hai

@@ -1,0 +1,287 @@
+// hai_norm.hip -- row-wise small ops of the verify step: RMSNorm, the fused
+// Q/gate RMSNorm+RoPE, the fused K RMSNorm+RoPE+cache append, embedding
+// gather and the elementwise residual / SwiGLU kernels used by the Backend
+// adaptor.  One 64-lane wave owns one row so that every reduction follows the
+// canonical L64 order.
+#include "hai_common.h"
+#include "hai_device.h"
+
+namespace {
+
+using namespace hai;
+
+constexpr int kMaxHeadDim = 512;
+
+// rmsnorm_kernel (hip_kernels.hip:105-137): 4 rows per 256-thread block.
+__global__ __launch_bounds__(256) void rmsnorm_kernel(uint16_t* __restrict__ y, int64_t ldy,
+                                                      const uint16_t* __restrict__ x, int64_t ldx,
+                                                      const uint16_t* __restrict__ w, int64_t rows,
+                                                      int H, float eps, float off) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const uint16_t* xr = x + row * ldx;
+    const float ss = l64_sumsq_bf16(xr, H, lane);
+    const float inv = 1.0f / csqrt(ss / static_cast<float>(H) + eps);
+    uint16_t* yr = y + row * ldy;
+    for (int k0 = lane * 8; k0 < H; k0 += 512) {
+        const uint4 xd = *reinterpret_cast<const uint4*>(xr + k0);
+        const uint4 wd = *reinterpret_cast<const uint4*>(w + k0);
+        const uint32_t xs[4] = {xd.x, xd.y, xd.z, xd.w};
+        const uint32_t ws[4] = {wd.x, wd.y, wd.z, wd.w};
+        uint32_t o[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint16_t a = f2bf((lo_bf(xs[q]) * inv) * (lo_bf(ws[q]) + off));
+            const uint16_t b = f2bf((hi_bf(xs[q]) * inv) * (hi_bf(ws[q]) + off));
+            o[q] = static_cast<uint32_t>(a) | (static_cast<uint32_t>(b) << 16);
+        }
+        *reinterpret_cast<uint4*>(yr + k0) = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+}
+
+// Rotate-half on the normalised values held in LDS (row of D fp32), first R
+// dims: out_p = x c - y s, out_{p+R/2} = y c + x s (hip_kernels.hip:213-220).
+__device__ __forceinline__ float rope_at(const float* row, int d, int R, const float* cs,
+                                         const float* sn) {
+    if (d >= R) return row[d];
+    const int half = R / 2;
+    const int p = d < half ? d : d - half;
+    const float xv = row[p];
+    const float yv = row[p + half];
+    if (d < half) return fma_(xv, cs[p], -(yv * sn[p]));
+    return fma_(yv, cs[p], xv * sn[p]);
+}
+
+// q_gate_rmsnorm_rope_kernel (hip_fused_kernels.hip:87-141): one wave per
+// (row, head); q is normalised with (w+1), rotated and stored once; the gate
+// half is copied.
+__global__ __launch_bounds__(256) void q_gate_rmsnorm_rope_kernel(
+    uint16_t* __restrict__ q_out, uint16_t* __restrict__ g_out, const uint16_t* __restrict__ src,
+    int64_t ld_src, const uint16_t* __restrict__ wq, const float* __restrict__ rc,
+    const float* __restrict__ rs, int64_t rope_pos, int B, int T, int nq, int D, int R,
+    const int32_t* lens, int pos_add, float eps) {
+    __shared__ float qn[4][kMaxHeadDim];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int64_t pair = static_cast<int64_t>(blockIdx.x) * 4 + wave;
+    const bool active = pair < static_cast<int64_t>(B) * T * nq;
+    int64_t m = 0;
+    int h = 0;
+    float inv = 0.0f;
+    const uint16_t* s = src;
+    if (active) {
+        m = pair / nq;
+        h = static_cast<int>(pair % nq);
+        s = src + m * ld_src + static_cast<int64_t>(h) * 2 * D;
+        const float ss = l64_sumsq_bf16(s, D, lane);
+        inv = 1.0f / csqrt(ss / static_cast<float>(D) + eps);
+        for (int d = lane; d < D; d += 64) qn[wave][d] = (bf2f(s[d]) * inv) * (bf2f(wq[d]) + 1.0f);
+    }
+    __syncthreads();
+    if (!active) return;
+    const int b = static_cast<int>(m / T);
+    const int t = static_cast<int>(m % T);
+    int64_t pos = static_cast<int64_t>(lens ? lens[b] : 0) + pos_add + t;
+    pos = pos < 0 ? 0 : (pos >= rope_pos ? rope_pos - 1 : pos);
+    const float* cs = rc + pos * (R / 2);
+    const float* sn = rs + pos * (R / 2);
+    uint16_t* qo = q_out + (m * nq + h) * D;
+    uint16_t* go = g_out + (m * nq + h) * D;
+    for (int d = lane; d < D; d += 64) {
+        qo[d] = f2bf(rope_at(qn[wave], d, R, cs, sn));
+        go[d] = s[D + d];
+    }
+}
+
+// K path (attention.cc:459-464) fused with append_kv_cache_kernel
+// (hip_kernels.hip:295-308): kn = bf16(k*inv*(w+1)), then bf16(rope(kn))
+// written to the cache row; V copied unchanged.
+__global__ __launch_bounds__(256) void kv_rmsnorm_rope_append_kernel(
+    uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int64_t cap,
+    const uint16_t* __restrict__ sk, const uint16_t* __restrict__ sv, int64_t ld_src,
+    const uint16_t* __restrict__ wk, const float* __restrict__ rc, const float* __restrict__ rs,
+    int64_t rope_pos, int B, int T, int nkv, int D, int R, const int32_t* lens, int pos_add,
+    float eps) {
+    __shared__ float kn[4][kMaxHeadDim];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int64_t pair = static_cast<int64_t>(blockIdx.x) * 4 + wave;
+    const bool active = pair < static_cast<int64_t>(B) * T * nkv;
+    int64_t m = 0;
+    int h = 0;
+    if (active) {
+        m = pair / nkv;
+        h = static_cast<int>(pair % nkv);
+        const uint16_t* s = sk + m * ld_src + static_cast<int64_t>(h) * D;
+        const float ss = l64_sumsq_bf16(s, D, lane);
+        const float inv = 1.0f / csqrt(ss / static_cast<float>(D) + eps);
+        for (int d = lane; d < D; d += 64) kn[wave][d] = bfr((bf2f(s[d]) * inv) * (bf2f(wk[d]) + 1.0f));
+    }
+    __syncthreads();
+    if (!active) return;
+    const int b = static_cast<int>(m / T);
+    const int t = static_cast<int>(m % T);
+    const int64_t pos = static_cast<int64_t>(lens ? lens[b] : 0) + pos_add + t;
+    if (pos < 0 || pos >= cap) return;
+    const int64_t rp = pos >= rope_pos ? rope_pos - 1 : pos;
+    const float* cs = rc + rp * (R / 2);
+    const float* sn = rs + rp * (R / 2);
+    const int64_t dst = ((static_cast<int64_t>(b) * cap + pos) * nkv + h) * D;
+    const uint16_t* v = sv + m * ld_src + static_cast<int64_t>(h) * D;
+    for (int d = lane; d < D; d += 64) {
+        kc[dst + d] = f2bf(rope_at(kn[wave], d, R, cs, sn));
+        vc[dst + d] = v[d];
+    }
+}
+
+__global__ void append_kv_kernel(uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int64_t cap,
+                                 const uint16_t* __restrict__ k, const uint16_t* __restrict__ v, int B,
+                                 int T, int64_t row_width, const int32_t* lens, int pos_add) {
+    const int64_t total = static_cast<int64_t>(B) * T * row_width;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int64_t m = i / row_width;
+        const int64_t c = i - m * row_width;
+        const int b = static_cast<int>(m / T);
+        const int t = static_cast<int>(m % T);
+        const int64_t pos = static_cast<int64_t>(lens ? lens[b] : 0) + pos_add + t;
+        if (pos < 0 || pos >= cap) continue;
+        const int64_t dst = (static_cast<int64_t>(b) * cap + pos) * row_width + c;
+        kc[dst] = k[i];
+        vc[dst] = v[i];
+    }
+}
+
+__global__ void add_kernel(uint16_t* y, const uint16_t* a, const uint16_t* b, int64_t n) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+        y[i] = f2bf(bf2f(a[i]) + bf2f(b[i]));
+}
+
+__global__ void silu_mul_kernel(uint16_t* y, const uint16_t* g, const uint16_t* u, int64_t n) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+        y[i] = f2bf(csilu(bf2f(g[i])) * bf2f(u[i]));
+}
+
+// embedding_gather_kernel (hip_kernels.hip:88-103): one block per id.
+__global__ void embedding_kernel(uint16_t* __restrict__ y, const uint16_t* __restrict__ table,
+                                 const int64_t* __restrict__ ids, int64_t V, int64_t H) {
+    const int64_t r = blockIdx.x;
+    const int64_t id = ids[r];
+    const bool ok = id >= 0 && id < V;
+    for (int64_t k = threadIdx.x; k < H; k += blockDim.x)
+        y[r * H + k] = ok ? table[id * H + k] : static_cast<uint16_t>(0);
+}
+
+unsigned grid_for(int64_t n) {
+    const int64_t b = (n + 255) / 256;
+    return static_cast<unsigned>(b < 1 ? 1 : (b > 65536 ? 65536 : b));
+}
+
+}  // namespace
+
+extern "C" {
+
+int hai_rmsnorm_bf16(void* y, int64_t ldy, const void* x, int64_t ldx, const void* w, int64_t rows,
+                     int64_t H, float eps, int unit_offset, void* stream) {
+    if (y == nullptr || x == nullptr || w == nullptr) return invalid("rmsnorm: null pointer");
+    if (rows < 0 || H <= 0 || H % 8 != 0 || ldx % 8 != 0 || ldy % 8 != 0 || ldx < H || ldy < H)
+        return invalid("rmsnorm: shape (need H%8==0, 8-aligned strides)");
+    if (!aligned16(x) || !aligned16(y) || !aligned16(w)) return invalid("rmsnorm: 16-byte alignment");
+    if (rows == 0) return HAI_OK;
+    rmsnorm_kernel<<<dim3(static_cast<unsigned>((rows + 3) / 4)), dim3(256), 0, as_stream(stream)>>>(
+        static_cast<uint16_t*>(y), ldy, static_cast<const uint16_t*>(x), ldx,
+        static_cast<const uint16_t*>(w), rows, static_cast<int>(H), eps, unit_offset ? 1.0f : 0.0f);
+    return launched("rmsnorm_kernel");
+}
+
+int hai_add_bf16(void* y, const void* a, const void* b, int64_t n, void* stream) {
+    if (y == nullptr || a == nullptr || b == nullptr || n < 0) return invalid("add");
+    if (n == 0) return HAI_OK;
+    add_kernel<<<dim3(grid_for(n)), dim3(256), 0, as_stream(stream)>>>(
+        static_cast<uint16_t*>(y), static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(b), n);
+    return launched("add_kernel");
+}
+
+int hai_silu_mul_bf16(void* y, const void* g, const void* u, int64_t n, void* stream) {
+    if (y == nullptr || g == nullptr || u == nullptr || n < 0) return invalid("silu_mul");
+    if (n == 0) return HAI_OK;
+    silu_mul_kernel<<<dim3(grid_for(n)), dim3(256), 0, as_stream(stream)>>>(
+        static_cast<uint16_t*>(y), static_cast<const uint16_t*>(g), static_cast<const uint16_t*>(u), n);
+    return launched("silu_mul_kernel");
+}
+
+int hai_embedding_gather_bf16(void* y, const void* table, const int64_t* ids, int64_t n_ids, int64_t V,
+                              int64_t H, void* stream) {
+    if (y == nullptr || table == nullptr || ids == nullptr || n_ids < 0 || V <= 0 || H <= 0)
+        return invalid("embedding_gather");
+    if (n_ids == 0) return HAI_OK;
+    embedding_kernel<<<dim3(static_cast<unsigned>(n_ids)), dim3(256), 0, as_stream(stream)>>>(
+        static_cast<uint16_t*>(y), static_cast<const uint16_t*>(table), ids, V, H);
+    return launched("embedding_kernel");
+}
+
+int hai_q_gate_rmsnorm_rope_bf16(void* q_out, void* gate_out, const void* src, int64_t ld_src,
+                                 const void* q_norm, const float* rope_cos, const float* rope_sin,
+                                 int64_t rope_positions, int64_t B, int64_t T, int64_t nq, int64_t D,
+                                 int64_t R, const int32_t* lens, int32_t pos_add, float eps,
+                                 void* stream) {
+    if (q_out == nullptr || gate_out == nullptr || src == nullptr || q_norm == nullptr ||
+        rope_cos == nullptr || rope_sin == nullptr)
+        return invalid("q_gate_rmsnorm_rope: null pointer");
+    if (B < 0 || T < 0 || nq <= 0 || D <= 0 || D % 8 != 0 || D > kMaxHeadDim || R < 0 || R > D ||
+        R % 2 != 0 || ld_src < 2 * nq * D || rope_positions <= 0)
+        return invalid("q_gate_rmsnorm_rope: shape");
+    if (!aligned16(src) || ld_src % 8 != 0) return invalid("q_gate_rmsnorm_rope: alignment");
+    const int64_t pairs = B * T * nq;
+    if (pairs == 0) return HAI_OK;
+    q_gate_rmsnorm_rope_kernel<<<dim3(static_cast<unsigned>((pairs + 3) / 4)), dim3(256), 0,
+                                 as_stream(stream)>>>(
+        static_cast<uint16_t*>(q_out), static_cast<uint16_t*>(gate_out), static_cast<const uint16_t*>(src),
+        ld_src, static_cast<const uint16_t*>(q_norm), rope_cos, rope_sin, rope_positions, int(B), int(T),
+        int(nq), int(D), int(R), lens, pos_add, eps);
+    return launched("q_gate_rmsnorm_rope_kernel");
+}
+
+int hai_kv_rmsnorm_rope_append_bf16(void* k_cache, void* v_cache, int64_t cap, const void* src_k,
+                                    const void* src_v, int64_t ld_src, const void* k_norm,
+                                    const float* rope_cos, const float* rope_sin, int64_t rope_positions,
+                                    int64_t B, int64_t T, int64_t nkv, int64_t D, int64_t R,
+                                    const int32_t* lens, int32_t pos_add, float eps, void* stream) {
+    if (k_cache == nullptr || v_cache == nullptr || src_k == nullptr || src_v == nullptr ||
+        k_norm == nullptr || rope_cos == nullptr || rope_sin == nullptr)
+        return invalid("kv_rmsnorm_rope_append: null pointer");
+    if (cap <= 0 || B < 0 || T < 0 || nkv <= 0 || D <= 0 || D % 8 != 0 || D > kMaxHeadDim || R < 0 ||
+        R > D || R % 2 != 0 || ld_src < nkv * D || rope_positions <= 0)
+        return invalid("kv_rmsnorm_rope_append: shape");
+    if (!aligned16(src_k) || ld_src % 8 != 0) return invalid("kv_rmsnorm_rope_append: alignment");
+    const int64_t pairs = B * T * nkv;
+    if (pairs == 0) return HAI_OK;
+    kv_rmsnorm_rope_append_kernel<<<dim3(static_cast<unsigned>((pairs + 3) / 4)), dim3(256), 0,
+                                    as_stream(stream)>>>(
+        static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache), cap,
+        static_cast<const uint16_t*>(src_k), static_cast<const uint16_t*>(src_v), ld_src,
+        static_cast<const uint16_t*>(k_norm), rope_cos, rope_sin, rope_positions, int(B), int(T), int(nkv),
+        int(D), int(R), lens, pos_add, eps);
+    return launched("kv_rmsnorm_rope_append_kernel");
+}
+
+int hai_append_kv_bf16(void* k_cache, void* v_cache, int64_t cap, const void* k, const void* v, int64_t B,
+                       int64_t T, int64_t row_width, const int32_t* lens, int32_t pos_add, void* stream) {
+    if (k_cache == nullptr || v_cache == nullptr || k == nullptr || v == nullptr || cap <= 0 || B < 0 ||
+        T < 0 || row_width <= 0)
+        return invalid("append_kv");
+    if (lens == nullptr && (pos_add < 0 || pos_add + T > cap))
+        return invalid("append_kv: rows exceed cache capacity");
+    const int64_t n = B * T * row_width;
+    if (n == 0) return HAI_OK;
+    append_kv_kernel<<<dim3(grid_for(n)), dim3(256), 0, as_stream(stream)>>>(
+        static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache), cap,
+        static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v), int(B), int(T), row_width, lens,
+        pos_add);
+    return launched("append_kv_kernel");
+}
+
+}  // extern "C"
