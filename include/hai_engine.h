@@ -1,0 +1,124 @@
+/* hai_engine.h -- C ABI of the MI355X verify engine (C++ host, libhybridai.so).
+ *
+ * The engine owns a synthetic Qwen3.5-style hybrid model resident in HBM and
+ * runs the speculative MTP decode of Generator::generate
+ * (src/generator.cc:545-1117 in the reference) on one GPU:
+ *   prefill -> MTP prefill -> rounds of {draft x k, verify (k+1 rows),
+ *   fused argmax/accept, commit or correction + MTP recovery}.
+ * Differences of mechanism, not of result:
+ *   - no cache clones: the KV cache and DeltaNet state roll back by committed
+ *     length (state slots + a conv-input ring), the MTP cache by length;
+ *   - the reject-path replay (generator.cc:935-1003) is replaced by one
+ *     forward of the correction token on top of the committed prefix, and the
+ *     MTP recovery row only computes what the cache keeps (K and V).
+ *   Every emitted token, candidate and accepted count equals the reference
+ *   state machine's (tests compare round by round with the CPU oracle).
+ */
+#ifndef HAI_ENGINE_H
+#define HAI_ENGINE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Qwen3Config fields used by the path (src/models/qwen3_config.h:16-47). */
+typedef struct hai_model_config {
+    int32_t hidden;
+    int32_t num_layers;
+    int32_t full_attention_interval; /* layer i is GQA iff (i+1) % interval == 0 */
+    int32_t num_q_heads;
+    int32_t num_kv_heads;
+    int32_t head_dim;
+    int32_t rope_dim;
+    int32_t lin_qk_heads;
+    int32_t lin_v_heads;
+    int32_t lin_k_dim;
+    int32_t lin_v_dim;
+    int32_t conv_kernel;
+    int32_t ffn;
+    int32_t vocab;
+    int32_t mtp_layers;
+    float rms_eps;
+    float rope_theta;
+} hai_model_config;
+
+typedef struct hai_engine_options {
+    int32_t max_context;      /* KV capacity per sequence (prompt + new + slack) */
+    int32_t max_verify_tokens;/* largest k+1; also the prefill chunk (<= 16) */
+    int32_t device;           /* HIP device ordinal */
+    int32_t use_graphs;       /* replay captured forwards (0 = plain launches) */
+} hai_engine_options;
+
+/* Counters of GenerationResult (include/hybrid.h:65-94) that the path fills. */
+typedef struct hai_spec_stats {
+    int64_t rounds;
+    int64_t proposed;
+    int64_t accepted;
+    int64_t rejected;
+    int64_t corrections;
+    int64_t replay_tokens;        /* correction tokens forwarded */
+    int64_t mtp_recovery_tokens;
+    int64_t max_proposal_width;
+    int64_t emitted;
+    double prefill_seconds;
+    double decode_seconds;        /* first round start .. last token */
+    double draft_seconds;         /* host wall time, includes queueing */
+    double verify_seconds;
+    double correction_seconds;
+} hai_spec_stats;
+
+/* Per-round record, int32 x 16: [proposal_count, accepted, full,
+ * correction(-1), next_target, emitted_before, mtp_len_after,
+ * target_len_after, cand0..cand7] -- the CPU oracle writes the same. */
+#define HAI_ROUND_RECORD 16
+
+void* hai_engine_create(const hai_model_config* cfg, const hai_engine_options* opt);
+void hai_engine_destroy(void* engine);
+const char* hai_engine_last_error(void* engine);
+/* Fill every weight with the synthetic generator (bit-identical to the
+ * oracle's orc_model_create with the same seed/std). */
+int hai_engine_init_synthetic(void* engine, uint64_t seed, float std_dev);
+/* Copy one weight tensor (bf16 bits, reference layout) to host memory. */
+int64_t hai_engine_read_tensor(void* engine, uint32_t tensor_id, uint16_t* out, int64_t capacity);
+uint64_t hai_engine_weight_bytes(void* engine);
+
+/* generate_* return the number of emitted tokens, or -status on failure. */
+
+/* Prefill-only forward from empty caches: post-final-norm hidden [T,H] and
+ * logits [T,V] as bf16 bits (either may be NULL). */
+int hai_engine_forward(void* engine, const int32_t* ids, int64_t T, uint16_t* hidden, uint16_t* logits);
+int hai_engine_generate_greedy(void* engine, const int32_t* prompt, int64_t P, int64_t max_new,
+                               const int32_t* eos, int64_t n_eos, int32_t* out_tokens);
+int hai_engine_generate_speculative(void* engine, const int32_t* prompt, int64_t P, int64_t max_new,
+                                    int64_t width, const int32_t* eos, int64_t n_eos,
+                                    const int32_t* draft_override, int64_t n_override,
+                                    int32_t* out_tokens, hai_spec_stats* stats, int32_t* round_log,
+                                    int64_t round_log_cap);
+
+/* Benchmark hooks.  hai_engine_prefill + hai_engine_spec_rounds run the same
+ * loop as generate_speculative split so the caller can time rounds; the
+ * verify-step profile replays n verify forwards of T rows at the current
+ * context with events around the whole step and around every GEMM launch. */
+typedef struct hai_verify_profile {
+    double verify_ms;          /* mean wall of one verify step (forward+accept) */
+    double gemm_ms;            /* mean summed GEMM kernel time per step */
+    double gemm_bytes;         /* weight bytes streamed by GEMMs per step */
+    double gemm_launches;      /* GEMM launches per step */
+    double step_bytes;         /* algorithmic bytes per step (weights+KV+state) */
+    double draft_ms;           /* mean wall of one draft step (MTP fwd+lm_head+argmax) */
+    double draft_bytes;
+} hai_verify_profile;
+
+int hai_engine_prefill(void* engine, const int32_t* prompt, int64_t P, int64_t max_new);
+int hai_engine_spec_rounds(void* engine, int64_t rounds, int64_t width, int32_t* out_tokens,
+                           int64_t out_capacity, int64_t* n_out, hai_spec_stats* stats);
+int hai_engine_profile_verify(void* engine, int64_t T, int64_t iters, hai_verify_profile* out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HAI_ENGINE_H */

@@ -188,7 +188,8 @@ int hai_argmax_rows_bf16(int64_t* out, const void* logits, int64_t ld,
  * with the argmax of the T = k+1 verify rows.  For sequence b:
  *   preds[b*T+t] = argmax(logits row b*T+t);
  *   a = longest prefix with preds[t] == ids[b*T+1+t] (t < k_b);
- *   result[b*4+0] = a, [1] = (a == k_b), [2] = 0, [3] = 0;
+ *   result[b*4+0] = a, [1] = (a == k_b), [2] = ids[b*T] (the round's
+ *   next_target), [3] = preds[b*T+a];
  *   target_len[b] += a + 1 (rows 0..a are committed, the rest rolls back);
  *   mtp_len[b] -= k_b - a unless fully accepted (MTP checkpoint[a]);
  *   next[b] = preds[b*T+a] (the target token after the committed rows);
@@ -203,6 +204,11 @@ int hai_verify_argmax_accept_bf16(const void* logits, int64_t V,
                                   int32_t* mtp_len, int64_t* next,
                                   void* rec_hidden, void* h_prev,
                                   void* scratch, void* stream);
+
+/* dst[i] += (delta ? delta[i] : 0) + add for i < n: committed-length updates
+ * kept on the stream (AttentionKVCache::length / DeltaNetCache::length
+ * bookkeeping, attention.h:11-42, delta_net.h:11-55). */
+int hai_add_i32(int32_t* dst, const int32_t* delta, int32_t add, int64_t n, void* stream);
 
 /* ------------------------------------------------------------------ synthetic data / checks
  * Synthetic weights: element (r, c) of a [rows, cols] tensor (row stride

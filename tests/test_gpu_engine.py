@@ -1,0 +1,92 @@
+"""End-to-end parity of the verify engine with the CPU oracle on the tiny
+config of BASELINE.json (4 layers D,D,D,G, hidden 256, vocab 4096, 1 MTP
+layer, bf16 ~ N(0, 0.02) synthetic weights seed 0, 32-token prompt, 64 new
+tokens, MTP width 1): token ids and every round's candidates / accepted
+count must be bit-identical, logits bit-identical."""
+import numpy as np
+import pytest
+
+from _hai import hai, orc
+
+pytestmark = pytest.mark.gpu
+
+P, NEW = 32, 64
+
+
+@pytest.fixture(scope="module")
+def engines():
+    from hybridai_amd import engine as E
+    eng = E.Engine(E.TINY, max_context=P + NEW + 32, max_verify_tokens=16)
+    eng.init_synthetic(seed=0, std=0.02)
+    ref = orc.Model(orc.TINY, seed=0)
+    prompt = orc.synthetic_prompt(0, P, orc.TINY["vocab"])
+    yield eng, ref, prompt
+    eng.close()
+    ref.close()
+
+
+def test_weights_match_oracle(engines):
+    eng, ref, _ = engines
+    for slot in (0, 1, 2, 3, 4, 5, 1024):
+        for kind in range(20):
+            tid = slot * 64 + kind
+            try:
+                want = ref.tensor(tid)
+            except KeyError:
+                continue
+            got = eng.read_tensor(tid)
+            assert np.array_equal(hai.bf16_to_f32(got), want), f"tensor {tid}"
+
+
+def test_prefill_logits_bit_exact(engines):
+    eng, ref, prompt = engines
+    hid, lg = eng.forward(prompt)
+    rh, rl = ref.forward(prompt)
+    assert np.array_equal(hai.bf16_to_f32(hid), rh)
+    assert np.array_equal(hai.bf16_to_f32(lg), rl)
+
+
+def test_greedy_tokens_bit_exact(engines):
+    eng, ref, prompt = engines
+    assert list(eng.greedy(prompt, NEW)) == list(ref.greedy(prompt, NEW))
+
+
+@pytest.mark.parametrize("width", [1, 2, 3])
+def test_speculative_matches_reference_state_machine(engines, width):
+    eng, ref, prompt = engines
+    toks, st, log = eng.speculative(prompt, NEW, width)
+    rtoks, rst, rlog = ref.speculative(prompt, NEW, width)
+    assert list(toks) == list(rtoks)
+    assert st["rounds"] == rst["rounds"] and st["accepted"] == rst["accepted"]
+    assert st["proposed"] == rst["proposed"] and st["corrections"] == rst["corrections"]
+    assert st["mtp_recovery_tokens"] == rst["mtp_recovery_tokens"]
+    assert np.array_equal(log, rlog)
+    # speculative decoding emits exactly the greedy continuation
+    assert list(toks) == list(ref.greedy(prompt, NEW))
+
+
+@pytest.mark.parametrize("width,perturb", [(1, ()), (3, ()), (3, (5, 20, 21, 40)), (2, (1, 2, 3, 30))])
+def test_forced_acceptance_patterns(engines, width, perturb):
+    """Draft override: candidates taken from the greedy continuation (full
+    acceptance) with some positions perturbed (partial acceptance)."""
+    eng, ref, prompt = engines
+    g = ref.greedy(prompt, NEW)
+    ov = g.copy()
+    for i in perturb:
+        ov[i] = (ov[i] + 7) % orc.TINY["vocab"]
+    toks, st, log = eng.speculative(prompt, NEW, width, draft_override=ov)
+    rtoks, rst, rlog = ref.speculative(prompt, NEW, width, draft_override=ov)
+    assert list(toks) == list(rtoks) == list(g)
+    assert np.array_equal(log, rlog)
+    assert st["accepted"] == rst["accepted"] > 0
+
+
+def test_eos_stops_like_reference(engines):
+    eng, ref, prompt = engines
+    g = ref.greedy(prompt, NEW)
+    eos = [int(g[10]), int(g[37])]
+    toks, st, log = eng.speculative(prompt, NEW, 2, eos=eos, draft_override=g)
+    rtoks, rst, rlog = ref.speculative(prompt, NEW, 2, eos=eos, draft_override=g)
+    assert list(toks) == list(rtoks)
+    assert toks[-1] in eos
+    assert np.array_equal(log, rlog)

@@ -104,8 +104,8 @@ __global__ __launch_bounds__(256) void verify_accept_kernel(
         const int full = a == k ? 1 : 0;
         result[b * 4 + 0] = a;
         result[b * 4 + 1] = full;
-        result[b * 4 + 2] = 0;
-        result[b * 4 + 3] = 0;
+        result[b * 4 + 2] = static_cast<int32_t>(ids[b * T]);
+        result[b * 4 + 3] = static_cast<int32_t>(preds[b * T + a]);
         if (target_len) target_len[b] += a + 1;
         if (mtp_len && !full) mtp_len[b] -= k - a;
         next[b] = preds[b * T + a];
@@ -123,9 +123,22 @@ __global__ __launch_bounds__(256) void verify_accept_kernel(
     }
 }
 
+__global__ void add_i32_kernel(int32_t* dst, const int32_t* delta, int32_t add, int64_t n) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n) dst[i] += (delta ? delta[i] : 0) + add;
+}
+
 }  // namespace
 
 extern "C" {
+
+int hai_add_i32(int32_t* dst, const int32_t* delta, int32_t add, int64_t n, void* stream) {
+    if (dst == nullptr || n < 0) return invalid("add_i32");
+    if (n == 0) return HAI_OK;
+    add_i32_kernel<<<dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, as_stream(stream)>>>(dst, delta, add,
+                                                                                                        n);
+    return launched("add_i32_kernel");
+}
 
 size_t hai_argmax_scratch_bytes(int64_t rows, int64_t V) {
     (void)V;

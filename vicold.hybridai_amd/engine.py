@@ -1,0 +1,182 @@
+"""ctypes binding of the C++ verify engine (include/hai_engine.h)."""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+VP = ctypes.c_void_p
+I64 = ctypes.c_int64
+I32P = ctypes.POINTER(ctypes.c_int32)
+U16P = ctypes.POINTER(ctypes.c_uint16)
+ROUND_RECORD = 16
+
+
+class ModelConfig(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int32) for n in (
+        "hidden", "num_layers", "full_attention_interval", "num_q_heads", "num_kv_heads", "head_dim",
+        "rope_dim", "lin_qk_heads", "lin_v_heads", "lin_k_dim", "lin_v_dim", "conv_kernel", "ffn", "vocab",
+        "mtp_layers")] + [("rms_eps", ctypes.c_float), ("rope_theta", ctypes.c_float)]
+
+
+class EngineOptions(ctypes.Structure):
+    _fields_ = [("max_context", ctypes.c_int32), ("max_verify_tokens", ctypes.c_int32),
+                ("device", ctypes.c_int32), ("use_graphs", ctypes.c_int32)]
+
+
+class SpecStats(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int64) for n in (
+        "rounds", "proposed", "accepted", "rejected", "corrections", "replay_tokens", "mtp_recovery_tokens",
+        "max_proposal_width", "emitted")] + [(n, ctypes.c_double) for n in (
+            "prefill_seconds", "decode_seconds", "draft_seconds", "verify_seconds", "correction_seconds")]
+
+    def as_dict(self):
+        return {n: getattr(self, n) for n, _ in self._fields_}
+
+
+class VerifyProfile(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_double) for n in (
+        "verify_ms", "gemm_ms", "gemm_bytes", "gemm_launches", "step_bytes", "draft_ms", "draft_bytes")]
+
+    def as_dict(self):
+        return {n: getattr(self, n) for n, _ in self._fields_}
+
+
+TINY = dict(hidden=256, num_layers=4, full_attention_interval=4, num_q_heads=4, num_kv_heads=2, head_dim=64,
+            rope_dim=16, lin_qk_heads=4, lin_v_heads=4, lin_k_dim=64, lin_v_dim=64, conv_kernel=4, ffn=768,
+            vocab=4096, mtp_layers=1, rms_eps=1e-6, rope_theta=1e7)
+QWEN27B = dict(hidden=5120, num_layers=64, full_attention_interval=4, num_q_heads=24, num_kv_heads=4,
+               head_dim=256, rope_dim=64, lin_qk_heads=16, lin_v_heads=48, lin_k_dim=128, lin_v_dim=128,
+               conv_kernel=4, ffn=17408, vocab=248320, mtp_layers=1, rms_eps=1e-6, rope_theta=1e7)
+
+
+def bind(lib: ctypes.CDLL) -> ctypes.CDLL:
+    lib.hai_engine_create.restype = VP
+    lib.hai_engine_create.argtypes = [ctypes.POINTER(ModelConfig), ctypes.POINTER(EngineOptions)]
+    lib.hai_engine_destroy.restype = None
+    lib.hai_engine_destroy.argtypes = [VP]
+    lib.hai_engine_last_error.restype = ctypes.c_char_p
+    lib.hai_engine_last_error.argtypes = [VP]
+    lib.hai_engine_init_synthetic.argtypes = [VP, ctypes.c_uint64, ctypes.c_float]
+    lib.hai_engine_read_tensor.restype = I64
+    lib.hai_engine_read_tensor.argtypes = [VP, ctypes.c_uint32, U16P, I64]
+    lib.hai_engine_weight_bytes.restype = ctypes.c_uint64
+    lib.hai_engine_weight_bytes.argtypes = [VP]
+    lib.hai_engine_forward.argtypes = [VP, I32P, I64, U16P, U16P]
+    lib.hai_engine_generate_greedy.argtypes = [VP, I32P, I64, I64, I32P, I64, I32P]
+    lib.hai_engine_generate_speculative.argtypes = [VP, I32P, I64, I64, I64, I32P, I64, I32P, I64, I32P,
+                                                    ctypes.POINTER(SpecStats), I32P, I64]
+    lib.hai_engine_prefill.argtypes = [VP, I32P, I64, I64]
+    lib.hai_engine_spec_rounds.argtypes = [VP, I64, I64, I32P, I64, ctypes.POINTER(ctypes.c_int64),
+                                           ctypes.POINTER(SpecStats)]
+    lib.hai_engine_profile_verify.argtypes = [VP, I64, I64, ctypes.POINTER(VerifyProfile)]
+    for n in ("hai_engine_init_synthetic", "hai_engine_forward", "hai_engine_generate_greedy",
+              "hai_engine_generate_speculative", "hai_engine_prefill", "hai_engine_spec_rounds",
+              "hai_engine_profile_verify"):
+        getattr(lib, n).restype = ctypes.c_int
+    return lib
+
+
+def _i32(a):
+    return np.ascontiguousarray(a, dtype=np.int32)
+
+
+class Engine:
+    """One verify engine on one GPU (synthetic weights)."""
+
+    def __init__(self, cfg: dict, max_context: int, max_verify_tokens: int = 16, device: int = 0,
+                 use_graphs: bool = False):
+        from . import host
+        self.lib = host()
+        self.cfg = dict(cfg)
+        c = ModelConfig(**cfg)
+        o = EngineOptions(max_context, max_verify_tokens, device, int(use_graphs))
+        self.h = self.lib.hai_engine_create(ctypes.byref(c), ctypes.byref(o))
+        if not self.h:
+            raise RuntimeError("hai_engine_create: " + self.lib.hai_engine_last_error(None).decode())
+
+    def _check(self, rc, what):
+        if rc != 0:
+            raise RuntimeError(f"{what} ({rc}): " + self.lib.hai_engine_last_error(self.h).decode())
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.lib.hai_engine_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def init_synthetic(self, seed=0, std=0.02):
+        self._check(self.lib.hai_engine_init_synthetic(self.h, seed, std), "init_synthetic")
+
+    def weight_bytes(self) -> int:
+        return int(self.lib.hai_engine_weight_bytes(self.h))
+
+    def read_tensor(self, tid: int) -> np.ndarray:
+        n = self.lib.hai_engine_read_tensor(self.h, tid, None, 0)
+        if n < 0:
+            raise KeyError(tid)
+        out = np.empty(n, np.uint16)
+        got = self.lib.hai_engine_read_tensor(self.h, tid, out.ctypes.data_as(U16P), n)
+        if got != n:
+            raise RuntimeError("read_tensor failed")
+        return out
+
+    def forward(self, ids):
+        ids = _i32(ids)
+        T = ids.size
+        H, V = self.cfg["hidden"], self.cfg["vocab"]
+        hid = np.empty((T, H), np.uint16)
+        lg = np.empty((T, V), np.uint16)
+        self._check(self.lib.hai_engine_forward(self.h, ids.ctypes.data_as(I32P), T, hid.ctypes.data_as(U16P),
+                                                lg.ctypes.data_as(U16P)), "forward")
+        return hid, lg
+
+    def greedy(self, prompt, max_new, eos=()):
+        p = _i32(prompt)
+        e = _i32(list(eos))
+        out = np.empty(max_new, np.int32)
+        n = self.lib.hai_engine_generate_greedy(self.h, p.ctypes.data_as(I32P), p.size, max_new,
+                                                e.ctypes.data_as(I32P), e.size, out.ctypes.data_as(I32P))
+        if n < 0:
+            self._check(-n, "generate_greedy")
+        return out[:n]
+
+    def speculative(self, prompt, max_new, width=1, eos=(), draft_override=None, max_rounds=4096):
+        p = _i32(prompt)
+        e = _i32(list(eos))
+        out = np.empty(max_new, np.int32)
+        st = SpecStats()
+        log = np.full((max_rounds, ROUND_RECORD), -1, np.int32)
+        if draft_override is not None:
+            ov = _i32(draft_override)
+            ovp, nov = ov.ctypes.data_as(I32P), ov.size
+        else:
+            ovp, nov = None, 0
+        n = self.lib.hai_engine_generate_speculative(self.h, p.ctypes.data_as(I32P), p.size, max_new, width,
+                                                     e.ctypes.data_as(I32P), e.size, ovp, nov,
+                                                     out.ctypes.data_as(I32P), ctypes.byref(st),
+                                                     log.ctypes.data_as(I32P), max_rounds)
+        if n < 0:
+            self._check(-n, "generate_speculative")
+        return out[:n], st.as_dict(), log[:st.rounds]
+
+    def prefill(self, prompt, max_new):
+        p = _i32(prompt)
+        self._check(self.lib.hai_engine_prefill(self.h, p.ctypes.data_as(I32P), p.size, max_new), "prefill")
+
+    def spec_rounds(self, rounds, width, out: np.ndarray):
+        n = ctypes.c_int64(0)
+        st = SpecStats()
+        self._check(self.lib.hai_engine_spec_rounds(self.h, rounds, width, out.ctypes.data_as(I32P), out.size,
+                                                    ctypes.byref(n), ctypes.byref(st)), "spec_rounds")
+        return int(n.value), st.as_dict()
+
+    def profile_verify(self, T, iters):
+        pr = VerifyProfile()
+        self._check(self.lib.hai_engine_profile_verify(self.h, T, iters, ctypes.byref(pr)), "profile_verify")
+        return pr.as_dict()

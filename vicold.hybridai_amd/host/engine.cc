@@ -1,0 +1,716 @@
+// engine.cc -- MI355X verify engine (see engine.h).
+#include "engine.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+
+#include "hai_kernels.h"
+
+namespace hybridai::mi355x {
+
+namespace {
+
+// Tensor ids shared with the synthetic generator: slot * 64 + kind.
+enum Kind : uint32_t {
+    kInputLN = 0, kPostLN = 1, kInQKV = 2, kInZ = 3, kInA = 4, kInB = 5, kConv = 6, kALog = 7,
+    kDtBias = 8, kLinNorm = 9, kOutProj = 10, kQProj = 11, kKProj = 12, kVProj = 13, kOProj = 14,
+    kQNorm = 15, kKNorm = 16, kGate = 17, kUp = 18, kDown = 19,
+};
+constexpr uint32_t tid(uint32_t slot, uint32_t kind) { return slot * 64u + kind; }
+constexpr uint32_t kSlotShared = 0, kSlotMtpShared = 1, kSlotLayer0 = 2, kSlotMtpLayer0 = 1024;
+
+constexpr size_t kAlign = 256;
+size_t align_up(size_t n) { return (n + kAlign - 1) / kAlign * kAlign; }
+
+// Bump allocator over one device arena: first pass sizes, second pass hands
+// out pointers.
+class Carver {
+public:
+    explicit Carver(char* base) : base_(base) {}
+    template <typename T>
+    T* take(size_t count) {
+        const size_t off = used_;
+        used_ += align_up(count * sizeof(T));
+        return base_ ? reinterpret_cast<T*>(base_ + off) : nullptr;
+    }
+    size_t used() const { return used_; }
+
+private:
+    char* base_;
+    size_t used_ = 0;
+};
+
+bool in_set(const int32_t* s, int64_t n, int64_t v) {
+    for (int64_t i = 0; i < n; ++i)
+        if (s[i] == v) return true;
+    return false;
+}
+
+using Clock = std::chrono::steady_clock;
+double seconds_since(Clock::time_point t) {
+    return std::chrono::duration<double>(Clock::now() - t).count();
+}
+
+}  // namespace
+
+#define HAI_TRY(expr)                                                 \
+    do {                                                              \
+        const int _rc = (expr);                                       \
+        if (_rc != HAI_OK) return fail(_rc, #expr);                   \
+    } while (0)
+
+Engine::Engine(const hai_model_config& cfg, const hai_engine_options& opt) : cfg_(cfg), opt_(opt) {
+    d_.H = cfg.hidden;
+    d_.F = cfg.ffn;
+    d_.V = cfg.vocab;
+    d_.nq = cfg.num_q_heads;
+    d_.nkv = cfg.num_kv_heads;
+    d_.D = cfg.head_dim;
+    d_.R = cfg.rope_dim;
+    d_.nk = cfg.lin_qk_heads;
+    d_.nv = cfg.lin_v_heads;
+    d_.dk = cfg.lin_k_dim;
+    d_.dv = cfg.lin_v_dim;
+    d_.Kc = cfg.conv_kernel;
+    d_.C = 2 * d_.nk * d_.dk + d_.nv * d_.dv;
+    d_.vw = d_.nv * d_.dv;
+    d_.Nin = d_.C + d_.vw + 2 * d_.nv;
+    d_.qw = d_.nq * d_.D;
+    d_.kvw = d_.nkv * d_.D;
+    d_.Nqkv = 2 * d_.qw + 2 * d_.kvw;
+    tmax_ = std::max<int64_t>(2, std::min<int64_t>(16, opt.max_verify_tokens));
+    cap_ = std::max<int64_t>(opt.max_context, tmax_ + 1);
+    ring_ = 32;
+    nslots_ = tmax_ + 1;
+    if (cfg.hidden <= 0 || cfg.hidden % 8 != 0 || cfg.num_layers <= 0 || cfg.full_attention_interval <= 0 ||
+        cfg.num_kv_heads <= 0 || cfg.num_q_heads % cfg.num_kv_heads != 0 || cfg.lin_qk_heads <= 0 ||
+        cfg.lin_v_heads % cfg.lin_qk_heads != 0 || cfg.ffn % 8 != 0 || cfg.mtp_layers != 1 ||
+        cfg.rope_dim > cfg.head_dim || cfg.rope_dim % 2 != 0 || cfg.conv_kernel < 2 || cfg.conv_kernel > 8 ||
+        d_.vw % 8 != 0 || d_.qw % 8 != 0) {
+        error_ = "unsupported model configuration";
+        return;
+    }
+    if (hai_set_device(opt.device) != HAI_OK || hai_stream_create(&stream_) != HAI_OK) {
+        error_ = std::string("device setup failed: ") + hai_last_error();
+        return;
+    }
+    if (alloc_all() != HAI_OK) return;
+    if (upload_rope_tables() != HAI_OK) return;
+    ok_ = true;
+}
+
+Engine::~Engine() {
+    if (stream_) hai_stream_synchronize(stream_);
+    for (void* e : prof_events_) hai_event_destroy(e);
+    if (weights_) hai_free(weights_);
+    if (caches_) hai_free(caches_);
+    if (work_) hai_free(work_);
+    if (stream_) hai_stream_destroy(stream_);
+}
+
+int Engine::fail(int rc, const std::string& what) {
+    error_ = what + ": " + hai_last_error();
+    return rc;
+}
+
+int Engine::alloc_all() {
+    const auto& d = d_;
+    const int64_t H = d.H;
+    layers_.assign(static_cast<size_t>(cfg_.num_layers), LayerWeights{});
+    for (int64_t i = 0; i < cfg_.num_layers; ++i)
+        layers_[i].attn = (i + 1) % cfg_.full_attention_interval == 0;
+    mtp_.attn = true;
+
+    // ---- weights ----
+    auto carve_weights = [&](Carver& cv) {
+        tensors_.clear();
+        auto add = [&](uint16_t*& dst, uint32_t id, int64_t rows, int64_t cols) {
+            dst = cv.take<uint16_t>(static_cast<size_t>(rows * cols));
+            tensors_.push_back({id, dst, rows, cols, cols});
+        };
+        auto layer = [&](LayerWeights& L, uint32_t slot) {
+            add(L.in_ln, tid(slot, kInputLN), 1, H);
+            add(L.post_ln, tid(slot, kPostLN), 1, H);
+            if (L.attn) {
+                L.w_qkv = cv.take<uint16_t>(static_cast<size_t>(d.Nqkv * H));
+                tensors_.push_back({tid(slot, kQProj), L.w_qkv, 2 * d.qw, H, H});
+                tensors_.push_back({tid(slot, kKProj), L.w_qkv ? L.w_qkv + 2 * d.qw * H : nullptr, d.kvw, H, H});
+                tensors_.push_back({tid(slot, kVProj), L.w_qkv ? L.w_qkv + (2 * d.qw + d.kvw) * H : nullptr,
+                                    d.kvw, H, H});
+                add(L.q_norm, tid(slot, kQNorm), 1, d.D);
+                add(L.k_norm, tid(slot, kKNorm), 1, d.D);
+                add(L.w_o, tid(slot, kOProj), H, d.qw);
+            } else {
+                L.w_in = cv.take<uint16_t>(static_cast<size_t>(d.Nin * H));
+                uint16_t* b = L.w_in;
+                auto at = [&](int64_t row) { return b ? b + row * H : nullptr; };
+                tensors_.push_back({tid(slot, kInQKV), at(0), d.C, H, H});
+                tensors_.push_back({tid(slot, kInZ), at(d.C), d.vw, H, H});
+                tensors_.push_back({tid(slot, kInA), at(d.C + d.vw), d.nv, H, H});
+                tensors_.push_back({tid(slot, kInB), at(d.C + d.vw + d.nv), d.nv, H, H});
+                add(L.conv_w, tid(slot, kConv), d.C, d.Kc);
+                add(L.a_log, tid(slot, kALog), 1, d.nv);
+                add(L.dt_bias, tid(slot, kDtBias), 1, d.nv);
+                add(L.lin_norm, tid(slot, kLinNorm), 1, d.dv);
+                add(L.w_out, tid(slot, kOutProj), H, d.vw);
+            }
+            L.w_gu = cv.take<uint16_t>(static_cast<size_t>(2 * d.F * H));
+            tensors_.push_back({tid(slot, kGate), L.w_gu, d.F, H, 2 * H});
+            tensors_.push_back({tid(slot, kUp), L.w_gu ? L.w_gu + H : nullptr, d.F, H, 2 * H});
+            add(L.w_down, tid(slot, kDown), H, d.F);
+        };
+        add(embed_, tid(kSlotShared, 0), d.V, H);
+        add(final_norm_, tid(kSlotShared, 1), 1, H);
+        add(lm_head_, tid(kSlotShared, 2), d.V, H);
+        add(fc_, tid(kSlotMtpShared, 0), H, 2 * H);
+        add(mtp_norm_, tid(kSlotMtpShared, 1), 1, H);
+        add(pre_emb_, tid(kSlotMtpShared, 2), 1, H);
+        add(pre_hid_, tid(kSlotMtpShared, 3), 1, H);
+        for (size_t i = 0; i < layers_.size(); ++i) layer(layers_[i], kSlotLayer0 + static_cast<uint32_t>(i));
+        layer(mtp_, kSlotMtpLayer0);
+    };
+    {
+        Carver sizing(nullptr);
+        carve_weights(sizing);
+        weight_bytes_ = sizing.used();
+        HAI_TRY(hai_malloc(&weights_, weight_bytes_));
+        Carver real(static_cast<char*>(weights_));
+        carve_weights(real);
+    }
+
+    // ---- caches ----
+    auto carve_caches = [&](Carver& cv) {
+        for (auto& L : layers_) {
+            if (L.attn) {
+                L.k_cache = cv.take<uint16_t>(static_cast<size_t>(cap_ * d.kvw));
+                L.v_cache = cv.take<uint16_t>(static_cast<size_t>(cap_ * d.kvw));
+            } else {
+                L.ring = cv.take<uint16_t>(static_cast<size_t>(ring_ * d.C));
+                L.state = cv.take<float>(static_cast<size_t>(nslots_ * d.nv * d.dv * d.dk));
+            }
+        }
+        mtp_.k_cache = cv.take<uint16_t>(static_cast<size_t>(cap_ * d.kvw));
+        mtp_.v_cache = cv.take<uint16_t>(static_cast<size_t>(cap_ * d.kvw));
+    };
+    {
+        Carver sizing(nullptr);
+        carve_caches(sizing);
+        HAI_TRY(hai_malloc(&caches_, sizing.used()));
+        Carver real(static_cast<char*>(caches_));
+        carve_caches(real);
+        HAI_TRY(hai_memset(caches_, 0, sizing.used(), stream_));
+    }
+
+    // ---- workspace ----
+    nproj_ = std::max(d.Nin, d.Nqkv);
+    const int64_t T = tmax_;
+    auto carve_work = [&](Carver& cv) {
+        d_ids_ = cv.take<int64_t>(T);
+        d_vids_ = cv.take<int64_t>(T + 1);
+        d_preds_ = cv.take<int64_t>(T);
+        d_result_ = cv.take<int32_t>(4);
+        d_tlen_ = cv.take<int32_t>(1);
+        d_mlen_ = cv.take<int32_t>(1);
+        d_plen_ = cv.take<int32_t>(8);
+        d_pnext_ = cv.take<int64_t>(8);
+        h_ = cv.take<uint16_t>(T * H);
+        xn_ = cv.take<uint16_t>(T * 2 * H);
+        emb_ = cv.take<uint16_t>(T * H);
+        proj_ = cv.take<uint16_t>(T * nproj_);
+        q_ = cv.take<uint16_t>(T * d.qw);
+        gate_ = cv.take<uint16_t>(T * d.qw);
+        att_ = cv.take<uint16_t>(T * d.qw);
+        dnout_ = cv.take<uint16_t>(T * d.vw);
+        act_ = cv.take<uint16_t>(T * d.F);
+        hf_ = cv.take<uint16_t>(T * H);
+        logits_ = cv.take<uint16_t>(T * d.V);
+        mh_[0] = cv.take<uint16_t>(H);
+        mh_[1] = cv.take<uint16_t>(H);
+        h_prev_ = cv.take<uint16_t>(H);
+        rec_hidden_ = cv.take<uint16_t>(H);
+        gqa_scratch_ = cv.take<char>(hai_gqa_scratch_bytes(1, T, d.nq, d.D, cap_));
+        argmax_scratch_ = cv.take<char>(hai_argmax_scratch_bytes(T, d.V));
+        rope_cos_ = cv.take<float>(cap_ * std::max<int64_t>(1, d.R / 2));
+        rope_sin_ = cv.take<float>(cap_ * std::max<int64_t>(1, d.R / 2));
+    };
+    {
+        Carver sizing(nullptr);
+        carve_work(sizing);
+        HAI_TRY(hai_malloc(&work_, sizing.used()));
+        Carver real(static_cast<char*>(work_));
+        carve_work(real);
+        HAI_TRY(hai_memset(work_, 0, sizing.used(), stream_));
+    }
+    return sync();
+}
+
+// cos/sin of theta = pos / base^(2p/R) in double, rounded to fp32
+// (partial_rope_kernel, hip_kernels.hip:209-213).
+int Engine::upload_rope_tables() {
+    const int64_t half = std::max<int64_t>(1, d_.R / 2);
+    std::vector<float> c(static_cast<size_t>(cap_ * half)), s(c.size());
+    for (int64_t pos = 0; pos < cap_; ++pos)
+        for (int64_t p = 0; p < d_.R / 2; ++p) {
+            const double theta = static_cast<double>(pos) /
+                std::pow(static_cast<double>(cfg_.rope_theta),
+                         static_cast<double>(2 * p) / static_cast<double>(d_.R));
+            c[pos * half + p] = static_cast<float>(std::cos(theta));
+            s[pos * half + p] = static_cast<float>(std::sin(theta));
+        }
+    HAI_TRY(hai_memcpy_h2d(rope_cos_, c.data(), c.size() * 4, stream_));
+    HAI_TRY(hai_memcpy_h2d(rope_sin_, s.data(), s.size() * 4, stream_));
+    return sync();
+}
+
+int Engine::sync() {
+    const int rc = hai_stream_synchronize(stream_);
+    if (rc != HAI_OK) return fail(rc, "stream synchronize");
+    return HAI_OK;
+}
+
+int Engine::read_i64(const int64_t* d, int64_t* h, int64_t n) {
+    HAI_TRY(hai_memcpy_d2h(h, d, static_cast<size_t>(n) * 8, stream_));
+    return sync();
+}
+
+int Engine::init_synthetic(uint64_t seed, float std_dev) {
+    for (const auto& t : tensors_)
+        HAI_TRY(hai_fill_synthetic_bf16(t.ptr, t.rows, t.cols, t.ld, seed, t.id, std_dev, stream_));
+    return sync();
+}
+
+int64_t Engine::read_tensor(uint32_t id, uint16_t* out, int64_t capacity) {
+    for (const auto& t : tensors_) {
+        if (t.id != id) continue;
+        const int64_t n = t.rows * t.cols;
+        if (out == nullptr) return n;
+        if (capacity < n) return -1;
+        std::vector<uint16_t> tmp(static_cast<size_t>((t.rows - 1) * t.ld + t.cols));
+        if (hai_memcpy_d2h(tmp.data(), t.ptr, tmp.size() * 2, stream_) != HAI_OK || sync() != HAI_OK) return -1;
+        for (int64_t r = 0; r < t.rows; ++r)
+            std::memcpy(out + r * t.cols, tmp.data() + r * t.ld, static_cast<size_t>(t.cols) * 2);
+        return n;
+    }
+    return -1;
+}
+
+int Engine::gemm(uint16_t* y, int64_t ldy, const uint16_t* x, int64_t ldx, const uint16_t* w, int64_t M,
+                 int64_t N, int64_t K, int epi, const uint16_t* res, int64_t ldres) {
+    if (prof_gemm_) {
+        while (prof_events_.size() < prof_used_ + 2) {
+            void* e = nullptr;
+            HAI_TRY(hai_event_create(&e));
+            prof_events_.push_back(e);
+        }
+        HAI_TRY(hai_event_record(prof_events_[prof_used_++], stream_));
+    }
+    HAI_TRY(hai_gemm_bf16(y, ldy, x, ldx, w, M, N, K, epi, res, ldres, stream_));
+    if (prof_gemm_) {
+        HAI_TRY(hai_event_record(prof_events_[prof_used_++], stream_));
+        prof_bytes_ += static_cast<double>(N) * static_cast<double>(K) * 2.0;
+        ++prof_launches_;
+    }
+    return HAI_OK;
+}
+
+int Engine::reset_state() {
+    // Committed lengths to zero; the DeltaNet state slot 0 of every layer must
+    // start at zero (conv history before position 0 is read as zero).
+    HAI_TRY(hai_memset(d_tlen_, 0, 4, stream_));
+    HAI_TRY(hai_memset(d_mlen_, 0, 4, stream_));
+    const size_t slot_bytes = static_cast<size_t>(d_.nv * d_.dv * d_.dk) * 4;
+    for (auto& L : layers_)
+        if (!L.attn) HAI_TRY(hai_memset(L.state, 0, slot_bytes, stream_));
+    rs_ = RoundState{};
+    return HAI_OK;
+}
+
+// One gated-GQA sub-layer on the normalised rows in xn_, residual added into h
+// (qwen_attention_reference -> GatedGQAAttention::forward_impl,
+// attention.cc:301-599).
+int Engine::attention_layer(const LayerWeights& L, int64_t T, uint16_t* h, const int32_t* lens, uint16_t* kc,
+                            uint16_t* vc) {
+    const auto& d = d_;
+    HAI_TRY(gemm(proj_, d.Nqkv, xn_, d.H, L.w_qkv, T, d.Nqkv, d.H, HAI_EPI_STORE, nullptr, 0));
+    HAI_TRY(hai_q_gate_rmsnorm_rope_bf16(q_, gate_, proj_, d.Nqkv, L.q_norm, rope_cos_, rope_sin_, cap_, 1, T,
+                                         d.nq, d.D, d.R, lens, 0, cfg_.rms_eps, stream_));
+    HAI_TRY(hai_kv_rmsnorm_rope_append_bf16(kc, vc, cap_, proj_ + 2 * d.qw, proj_ + 2 * d.qw + d.kvw, d.Nqkv,
+                                            L.k_norm, rope_cos_, rope_sin_, cap_, 1, T, d.nkv, d.D, d.R, lens, 0,
+                                            cfg_.rms_eps, stream_));
+    HAI_TRY(hai_gqa_verify_bf16(att_, q_, gate_, kc, vc, cap_, gqa_scratch_, 1, T, d.nq, d.nkv, d.D, lens,
+                                static_cast<int32_t>(T), cap_, stream_));
+    return gemm(h, d.H, att_, d.qw, L.w_o, T, d.H, d.qw, HAI_EPI_RESIDUAL, h, d.H);
+}
+
+// qwen_mlp_reference (qwen_reference.cc:146-175): post-norm, SwiGLU, down
+// projection with the residual add fused.
+int Engine::mlp(const LayerWeights& L, int64_t T, uint16_t* h) {
+    const auto& d = d_;
+    HAI_TRY(hai_rmsnorm_bf16(xn_, d.H, h, d.H, L.post_ln, T, d.H, cfg_.rms_eps, 1, stream_));
+    HAI_TRY(gemm(act_, d.F, xn_, d.H, L.w_gu, T, 2 * d.F, d.H, HAI_EPI_SILU_MUL, nullptr, 0));
+    return gemm(h, d.H, act_, d.F, L.w_down, T, d.H, d.F, HAI_EPI_RESIDUAL, h, d.H);
+}
+
+// target_forward (generator.cc:550-634): T rows of one sequence on top of
+// the committed caches; hf_ = post-final-norm hidden, logits_ = lm_head.
+// Committed lengths are not advanced here.
+int Engine::forward_target(const int64_t* d_ids, int64_t T, bool write_all_slots) {
+    const auto& d = d_;
+    HAI_TRY(hai_embedding_gather_bf16(h_, embed_, d_ids, T, d.V, d.H, stream_));
+    for (auto& L : layers_) {
+        HAI_TRY(hai_rmsnorm_bf16(xn_, d.H, h_, d.H, L.in_ln, T, d.H, cfg_.rms_eps, 1, stream_));
+        if (L.attn) {
+            HAI_TRY(attention_layer(L, T, h_, d_tlen_, L.k_cache, L.v_cache));
+        } else {
+            // qwen_deltanet_reference (qwen_reference.cc:205-258)
+            HAI_TRY(gemm(proj_, d.Nin, xn_, d.H, L.w_in, T, d.Nin, d.H, HAI_EPI_STORE, nullptr, 0));
+            HAI_TRY(hai_deltanet_verify_bf16(dnout_, d.vw, proj_, d.Nin, 0, d.C, d.C + d.vw, d.C + d.vw + d.nv,
+                                             L.conv_w, L.ring, ring_, L.state, nslots_, write_all_slots ? 1 : 0,
+                                             L.a_log, L.dt_bias, L.lin_norm, d_tlen_, 0, 1, T, d.nk, d.nv, d.dk,
+                                             d.dv, d.Kc, cfg_.rms_eps, stream_));
+            HAI_TRY(gemm(h_, d.H, dnout_, d.vw, L.w_out, T, d.H, d.vw, HAI_EPI_RESIDUAL, h_, d.H));
+        }
+        HAI_TRY(mlp(L, T, h_));
+    }
+    HAI_TRY(hai_rmsnorm_bf16(hf_, d.H, h_, d.H, final_norm_, T, d.H, cfg_.rms_eps, 1, stream_));
+    return gemm(logits_, d.V, hf_, d.H, lm_head_, T, d.V, d.H, HAI_EPI_STORE, nullptr, 0);
+}
+
+// MTP input rows x = fc([RMSNorm(emb) | RMSNorm(hidden)]) (generator.cc:152-160)
+// followed by only the part of the MTP decoder layer that the cache keeps:
+// input RMSNorm, the K/V projection rows and the K RMSNorm+RoPE append.  The
+// reference's prompt prefill and correction recovery discard the MTP output
+// (generator.cc:673-699, 977-1003), so the cache state is identical.
+int Engine::mtp_kv_rows(const int64_t* d_ids, const uint16_t* d_hidden, int64_t T) {
+    const auto& d = d_;
+    HAI_TRY(hai_embedding_gather_bf16(emb_, embed_, d_ids, T, d.V, d.H, stream_));
+    HAI_TRY(hai_rmsnorm_bf16(xn_, 2 * d.H, emb_, d.H, pre_emb_, T, d.H, cfg_.rms_eps, 1, stream_));
+    HAI_TRY(hai_rmsnorm_bf16(xn_ + d.H, 2 * d.H, d_hidden, d.H, pre_hid_, T, d.H, cfg_.rms_eps, 1, stream_));
+    HAI_TRY(gemm(h_, d.H, xn_, 2 * d.H, fc_, T, d.H, 2 * d.H, HAI_EPI_STORE, nullptr, 0));
+    HAI_TRY(hai_rmsnorm_bf16(xn_, d.H, h_, d.H, mtp_.in_ln, T, d.H, cfg_.rms_eps, 1, stream_));
+    // K and V rows of the fused attention projection only.
+    HAI_TRY(gemm(proj_, 2 * d.kvw, xn_, d.H, mtp_.w_qkv + 2 * d.qw * d.H, T, 2 * d.kvw, d.H, HAI_EPI_STORE,
+                 nullptr, 0));
+    HAI_TRY(hai_kv_rmsnorm_rope_append_bf16(mtp_.k_cache, mtp_.v_cache, cap_, proj_, proj_ + d.kvw, 2 * d.kvw,
+                                            mtp_.k_norm, rope_cos_, rope_sin_, cap_, 1, T, d.nkv, d.D, d.R, d_mlen_,
+                                            0, cfg_.rms_eps, stream_));
+    return hai_add_i32(d_mlen_, nullptr, static_cast<int32_t>(T), 1, stream_) == HAI_OK
+               ? HAI_OK
+               : fail(HAI_ERR_BACKEND, "mtp length update");
+}
+
+// One draft step: the full MTP forward (qwen_mtp_forward_reference,
+// generator.cc:139-183) of one row, lm_head and argmax (generator.cc:784-811).
+// The MTP cache grows by one row.
+int Engine::mtp_draft_step(const int64_t* d_id, const uint16_t* d_hin, uint16_t* d_mh, int64_t* d_cand) {
+    const auto& d = d_;
+    HAI_TRY(hai_embedding_gather_bf16(emb_, embed_, d_id, 1, d.V, d.H, stream_));
+    HAI_TRY(hai_rmsnorm_bf16(xn_, 2 * d.H, emb_, d.H, pre_emb_, 1, d.H, cfg_.rms_eps, 1, stream_));
+    HAI_TRY(hai_rmsnorm_bf16(xn_ + d.H, 2 * d.H, d_hin, d.H, pre_hid_, 1, d.H, cfg_.rms_eps, 1, stream_));
+    HAI_TRY(gemm(h_, d.H, xn_, 2 * d.H, fc_, 1, d.H, 2 * d.H, HAI_EPI_STORE, nullptr, 0));
+    HAI_TRY(hai_rmsnorm_bf16(xn_, d.H, h_, d.H, mtp_.in_ln, 1, d.H, cfg_.rms_eps, 1, stream_));
+    HAI_TRY(attention_layer(mtp_, 1, h_, d_mlen_, mtp_.k_cache, mtp_.v_cache));
+    HAI_TRY(mlp(mtp_, 1, h_));
+    HAI_TRY(hai_rmsnorm_bf16(d_mh, d.H, h_, d.H, mtp_norm_, 1, d.H, cfg_.rms_eps, 1, stream_));
+    HAI_TRY(gemm(logits_, d.V, d_mh, d.H, lm_head_, 1, d.V, d.H, HAI_EPI_STORE, nullptr, 0));
+    HAI_TRY(hai_argmax_rows_bf16(d_cand, logits_, d.V, 1, d.V, argmax_scratch_, stream_));
+    HAI_TRY(hai_add_i32(d_mlen_, nullptr, 1, 1, stream_));
+    return HAI_OK;
+}
+
+// Prompt prefill in chunks of tmax_ rows (rows are independent and the
+// recurrences are sequential, so chunking does not change a bit), each chunk
+// followed by its MTP prompt rows (emb(t_i) paired with the hidden of t_i).
+int Engine::prefill_chunks(const int32_t* ids, int64_t P, uint16_t* hidden_out, uint16_t* logits_out) {
+    std::vector<int64_t> ids64(ids, ids + P);
+    for (int64_t off = 0; off < P; off += tmax_) {
+        const int64_t T = std::min<int64_t>(tmax_, P - off);
+        HAI_TRY(hai_memcpy_h2d(d_ids_, ids64.data() + off, static_cast<size_t>(T) * 8, stream_));
+        HAI_TRY(forward_target(d_ids_, T, false));
+        HAI_TRY(hai_add_i32(d_tlen_, nullptr, static_cast<int32_t>(T), 1, stream_));
+        if (hidden_out) HAI_TRY(hai_memcpy_d2h(hidden_out + off * d_.H, hf_, static_cast<size_t>(T * d_.H) * 2, stream_));
+        if (logits_out) HAI_TRY(hai_memcpy_d2h(logits_out + off * d_.V, logits_, static_cast<size_t>(T * d_.V) * 2, stream_));
+        HAI_TRY(mtp_kv_rows(d_ids_, hf_, T));
+        if (off + T == P) {
+            HAI_TRY(hai_argmax_rows_bf16(d_vids_, logits_ + (T - 1) * d_.V, d_.V, 1, d_.V, argmax_scratch_, stream_));
+            HAI_TRY(hai_memcpy_d2d(h_prev_, hf_ + (T - 1) * d_.H, static_cast<size_t>(d_.H) * 2, stream_));
+        }
+        if (hidden_out || logits_out) HAI_TRY(sync());
+    }
+    rs_.target_len = P;
+    rs_.mtp_len = P;
+    return HAI_OK;
+}
+
+int Engine::forward_rows(const int32_t* ids, int64_t T, uint16_t* hidden, uint16_t* logits) {
+    if (T <= 0 || T > cap_) return fail(HAI_ERR_INVALID_ARGUMENT, "forward_rows: T out of range");
+    HAI_TRY(reset_state());
+    HAI_TRY(prefill_chunks(ids, T, hidden, logits));
+    return sync();
+}
+
+int Engine::prefill(const int32_t* prompt, int64_t P, int64_t max_new) {
+    if (P <= 0 || max_new <= 0 || P + max_new + tmax_ > cap_)
+        return fail(HAI_ERR_INVALID_ARGUMENT, "prefill: prompt + max_new exceeds max_context");
+    HAI_TRY(reset_state());
+    HAI_TRY(prefill_chunks(prompt, P, nullptr, nullptr));
+    int64_t next = 0;
+    HAI_TRY(read_i64(d_vids_, &next, 1));
+    rs_.next_target = next;
+    rs_.max_new = max_new;
+    rs_.emitted = 0;
+    rs_.done = false;
+    return HAI_OK;
+}
+
+int Engine::generate_greedy(const int32_t* prompt, int64_t P, int64_t max_new, const int32_t* eos, int64_t n_eos,
+                            int32_t* out, int64_t* n_out) {
+    HAI_TRY(prefill(prompt, P, max_new));
+    int64_t emitted = 0;
+    int64_t next = rs_.next_target;
+    while (true) {
+        out[emitted++] = static_cast<int32_t>(next);
+        if (emitted >= max_new || in_set(eos, n_eos, next)) break;
+        HAI_TRY(forward_target(d_vids_, 1, false));
+        HAI_TRY(hai_add_i32(d_tlen_, nullptr, 1, 1, stream_));
+        HAI_TRY(hai_argmax_rows_bf16(d_vids_, logits_, d_.V, 1, d_.V, argmax_scratch_, stream_));
+        HAI_TRY(read_i64(d_vids_, &next, 1));
+    }
+    *n_out = emitted;
+    return HAI_OK;
+}
+
+// One round of the reference loop body (generator.cc:720-1028).
+int Engine::one_round(RoundState& st, int64_t width, const int32_t* eos, int64_t n_eos,
+                      const int32_t* override_tokens, int64_t n_override, int32_t* out, hai_spec_stats* stats,
+                      int32_t* rec) {
+    const int64_t remaining = st.max_new - st.emitted;
+    if (in_set(eos, n_eos, st.next_target) || remaining == 1) {
+        out[st.emitted++] = static_cast<int32_t>(st.next_target);
+        st.done = true;
+        return HAI_OK;
+    }
+    const int64_t pc = std::min<int64_t>(std::min<int64_t>(width, remaining - 1), tmax_ - 1);
+    stats->max_proposal_width = std::max(stats->max_proposal_width, pc);
+    ++stats->rounds;
+    const int64_t mtp_len0 = st.mtp_len;
+    const int64_t target_len0 = st.target_len;
+
+    // ---- draft (chained MTP proposals) ----
+    auto t0 = Clock::now();
+    const uint16_t* hin = h_prev_;
+    int64_t k = 0;
+    for (int64_t i = 0; i < pc; ++i) {
+        HAI_TRY(mtp_draft_step(d_vids_ + i, hin, mh_[i % 2], d_vids_ + i + 1));
+        const int64_t pos = st.emitted + 1 + i;
+        if (override_tokens != nullptr && pos < n_override) {
+            const int64_t tok = override_tokens[pos];
+            HAI_TRY(hai_memcpy_h2d(d_vids_ + i + 1, &tok, 8, stream_));
+            HAI_TRY(sync());  // tok lives on the host stack
+        }
+        ++k;
+        ++stats->proposed;
+        hin = mh_[i % 2];
+        if (n_eos > 0) {
+            int64_t cand = 0;
+            HAI_TRY(read_i64(d_vids_ + i + 1, &cand, 1));
+            if (in_set(eos, n_eos, cand)) break;
+        }
+    }
+    stats->draft_seconds += seconds_since(t0);
+
+    // ---- verify + fused argmax/accept ----
+    t0 = Clock::now();
+    const int64_t T = k + 1;
+    HAI_TRY(forward_target(d_vids_, T, true));
+    HAI_TRY(hai_verify_argmax_accept_bf16(logits_, d_.V, hf_, d_.H, d_vids_, nullptr, 1, T, d_preds_, d_result_,
+                                          d_tlen_, d_mlen_, d_vids_, rec_hidden_, h_prev_, argmax_scratch_,
+                                          stream_));
+    int32_t res[4];
+    int64_t preds[17], cands[17];
+    HAI_TRY(hai_memcpy_d2h(res, d_result_, sizeof(res), stream_));
+    HAI_TRY(hai_memcpy_d2h(preds, d_preds_, static_cast<size_t>(T) * 8, stream_));
+    HAI_TRY(hai_memcpy_d2h(cands, d_vids_ + 1, static_cast<size_t>(k) * 8, stream_));
+    HAI_TRY(sync());
+    stats->verify_seconds += seconds_since(t0);
+    const int64_t a = res[0];
+    const bool full = res[1] != 0;
+    if (rec != nullptr) {
+        std::fill(rec, rec + HAI_ROUND_RECORD, -1);
+        rec[0] = static_cast<int32_t>(k);
+        rec[1] = static_cast<int32_t>(a);
+        rec[4] = static_cast<int32_t>(st.next_target);
+        rec[5] = static_cast<int32_t>(st.emitted);
+        for (int64_t i = 0; i < k && i < 8; ++i) rec[8 + i] = static_cast<int32_t>(cands[i]);
+    }
+    out[st.emitted++] = static_cast<int32_t>(st.next_target);
+    if (full) {
+        for (int64_t i = 0; i < k; ++i) out[st.emitted++] = static_cast<int32_t>(cands[i]);
+        stats->accepted += a;
+        st.next_target = preds[k];
+        st.target_len = target_len0 + T;
+        st.mtp_len = mtp_len0 + k;
+        if (rec) { rec[2] = 1; rec[3] = -1; }
+    } else {
+        const int64_t corr = preds[a];
+        stats->rejected += k - a;
+        ++stats->corrections;
+        for (int64_t i = 0; i < a; ++i) out[st.emitted++] = static_cast<int32_t>(cands[i]);
+        if (st.emitted < st.max_new) out[st.emitted++] = static_cast<int32_t>(corr);
+        stats->accepted += a;
+        if (rec) { rec[2] = 0; rec[3] = static_cast<int32_t>(corr); }
+        // The reference replays [next, accepted..., corr] on the committed
+        // caches; the rows before corr are already committed above.
+        st.target_len = target_len0 + a + 2;
+        if (st.emitted >= st.max_new || in_set(eos, n_eos, corr)) {
+            st.mtp_len = mtp_len0;  // the reference stops before restoring the MTP checkpoint
+            st.done = true;
+        } else {
+            t0 = Clock::now();
+            // MTP checkpoint[a] (length already rolled back by the accept
+            // kernel) plus the recovery row (emb(corr), hidden of row a).
+            HAI_TRY(mtp_kv_rows(d_vids_, rec_hidden_, 1));
+            ++stats->mtp_recovery_tokens;
+            // Correction forward: next_target = argmax after corr.
+            HAI_TRY(forward_target(d_vids_, 1, false));
+            HAI_TRY(hai_add_i32(d_tlen_, nullptr, 1, 1, stream_));
+            HAI_TRY(hai_argmax_rows_bf16(d_vids_, logits_, d_.V, 1, d_.V, argmax_scratch_, stream_));
+            HAI_TRY(hai_memcpy_d2d(h_prev_, hf_, static_cast<size_t>(d_.H) * 2, stream_));
+            ++stats->replay_tokens;
+            int64_t next = 0;
+            HAI_TRY(read_i64(d_vids_, &next, 1));
+            st.next_target = next;
+            st.mtp_len = mtp_len0 + a + 1;
+            stats->correction_seconds += seconds_since(t0);
+        }
+    }
+    if (rec) {
+        rec[6] = static_cast<int32_t>(st.mtp_len);
+        rec[7] = static_cast<int32_t>(st.target_len);
+    }
+    if (!st.done && (st.emitted >= st.max_new || in_set(eos, n_eos, out[st.emitted - 1]))) st.done = true;
+    return HAI_OK;
+}
+
+int Engine::generate_speculative(const int32_t* prompt, int64_t P, int64_t max_new, int64_t width,
+                                 const int32_t* eos, int64_t n_eos, const int32_t* override_tokens,
+                                 int64_t n_override, int32_t* out, hai_spec_stats* stats, int32_t* round_log,
+                                 int64_t round_log_cap, int64_t* n_out) {
+    if (width < 1) return fail(HAI_ERR_INVALID_ARGUMENT, "width must be >= 1");
+    hai_spec_stats st{};
+    auto t0 = Clock::now();
+    HAI_TRY(prefill(prompt, P, max_new));
+    st.prefill_seconds = seconds_since(t0);
+    auto t1 = Clock::now();
+    int64_t nlog = 0;
+    while (!rs_.done && rs_.emitted < max_new) {
+        int32_t* rec = (round_log != nullptr && nlog < round_log_cap) ? round_log + nlog * HAI_ROUND_RECORD : nullptr;
+        const int64_t before = st.rounds;
+        HAI_TRY(one_round(rs_, width, eos, n_eos, override_tokens, n_override, out, &st, rec));
+        if (st.rounds > before) ++nlog;
+    }
+    st.decode_seconds = seconds_since(t1);
+    st.emitted = rs_.emitted;
+    if (stats) *stats = st;
+    *n_out = rs_.emitted;
+    return HAI_OK;
+}
+
+int Engine::spec_rounds(int64_t rounds, int64_t width, int32_t* out, int64_t cap, int64_t* n_out,
+                        hai_spec_stats* stats) {
+    if (out == nullptr || cap < rs_.max_new) return fail(HAI_ERR_INVALID_ARGUMENT, "spec_rounds: out capacity < max_new");
+    hai_spec_stats local{};
+    hai_spec_stats* st = stats ? stats : &local;
+    const int64_t start = rs_.emitted;
+    auto t0 = Clock::now();
+    for (int64_t r = 0; r < rounds && !rs_.done && rs_.emitted < rs_.max_new; ++r)
+        HAI_TRY(one_round(rs_, width, nullptr, 0, nullptr, 0, out, st, nullptr));
+    HAI_TRY(sync());
+    st->decode_seconds += seconds_since(t0);
+    st->emitted += rs_.emitted - start;
+    if (n_out) *n_out = rs_.emitted;
+    return HAI_OK;
+}
+
+// Replays verify steps of T rows at the current committed context without
+// committing them (the accept kernel runs on scratch lengths), timing the
+// whole step with events and every GEMM launch individually.
+int Engine::profile_verify(int64_t T, int64_t iters, hai_verify_profile* out) {
+    if (T < 1 || T > tmax_ || iters < 1) return fail(HAI_ERR_INVALID_ARGUMENT, "profile_verify: T or iters");
+    const auto& d = d_;
+    void *e0 = nullptr, *e1 = nullptr;
+    HAI_TRY(hai_event_create(&e0));
+    HAI_TRY(hai_event_create(&e1));
+    int32_t* scratch_len = d_plen_;  // lengths copied here so the real ones stay untouched
+    std::vector<int64_t> ids(static_cast<size_t>(T), 1);
+    HAI_TRY(hai_memcpy_h2d(d_ids_, ids.data(), static_cast<size_t>(T) * 8, stream_));
+    double verify_ms = 0.0, gemm_ms = 0.0, draft_ms = 0.0;
+    double gemm_bytes = 0.0, launches = 0.0;
+    for (int64_t it = 0; it < iters + 1; ++it) {  // first iteration warms up
+        prof_gemm_ = true;
+        prof_used_ = 0;
+        prof_bytes_ = 0.0;
+        prof_launches_ = 0;
+        HAI_TRY(hai_event_record(e0, stream_));
+        HAI_TRY(forward_target(d_ids_, T, true));
+        HAI_TRY(hai_memcpy_d2d(scratch_len, d_tlen_, 4, stream_));
+        HAI_TRY(hai_memcpy_d2d(scratch_len + 1, d_mlen_, 4, stream_));
+        HAI_TRY(hai_verify_argmax_accept_bf16(logits_, d.V, hf_, d.H, d_ids_, nullptr, 1, T, d_preds_,
+                                              scratch_len + 4, scratch_len, scratch_len + 1, d_pnext_, nullptr,
+                                              nullptr, argmax_scratch_, stream_));
+        HAI_TRY(hai_event_record(e1, stream_));
+        prof_gemm_ = false;
+        HAI_TRY(sync());
+        float ms = 0.0f;
+        HAI_TRY(hai_event_elapsed_ms(e0, e1, &ms));
+        double g = 0.0;
+        for (size_t i = 0; i + 1 < prof_used_; i += 2) {
+            float gm = 0.0f;
+            HAI_TRY(hai_event_elapsed_ms(prof_events_[i], prof_events_[i + 1], &gm));
+            g += gm;
+        }
+        if (it > 0) {
+            verify_ms += ms;
+            gemm_ms += g;
+            gemm_bytes += prof_bytes_;
+            launches += static_cast<double>(prof_launches_);
+        }
+    }
+    // Draft step timing (one MTP forward + lm_head + argmax) without events
+    // inside, on a scratch MTP length.
+    for (int64_t it = 0; it < iters + 1; ++it) {
+        HAI_TRY(hai_memcpy_d2d(scratch_len, d_mlen_, 4, stream_));
+        HAI_TRY(hai_event_record(e0, stream_));
+        HAI_TRY(mtp_draft_step(d_ids_, h_prev_, mh_[0], d_pnext_));
+        HAI_TRY(hai_event_record(e1, stream_));
+        HAI_TRY(hai_memcpy_d2d(d_mlen_, scratch_len, 4, stream_));
+        HAI_TRY(sync());
+        float ms = 0.0f;
+        HAI_TRY(hai_event_elapsed_ms(e0, e1, &ms));
+        if (it > 0) draft_ms += ms;
+    }
+    hai_event_destroy(e0);
+    hai_event_destroy(e1);
+    const double n = static_cast<double>(iters);
+    out->verify_ms = verify_ms / n;
+    out->gemm_ms = gemm_ms / n;
+    out->gemm_bytes = gemm_bytes / n;
+    out->gemm_launches = launches / n;
+    // algorithmic bytes of one verify step: weights streamed + KV read +
+    // DeltaNet state read and T states written.
+    int64_t n_attn = 0, n_dn = 0;
+    for (const auto& L : layers_) (L.attn ? n_attn : n_dn) += 1;
+    const double L = static_cast<double>(rs_.target_len + T);
+    const double kv = static_cast<double>(n_attn) * 2.0 * L * static_cast<double>(d.kvw) * 2.0;
+    const double state = static_cast<double>(n_dn) * static_cast<double>(d.nv * d.dk * d.dv) * 4.0 *
+                         (1.0 + static_cast<double>(T));
+    out->step_bytes = out->gemm_bytes + kv + state;
+    out->draft_ms = draft_ms / n;
+    out->draft_bytes = static_cast<double>(d.H) * 2 * d.H * 2.0 +
+                       static_cast<double>(d.Nqkv + d.qw + 3 * d.F) * d.H * 2.0 +
+                       static_cast<double>(d.V) * d.H * 2.0;
+    return HAI_OK;
+}
+
+}  // namespace hybridai::mi355x

@@ -1,0 +1,191 @@
+// engine.h -- MI355X verify engine: a synthetic Qwen3.5-style hybrid model
+// resident in HBM plus the speculative MTP decode loop of the reference's
+// Generator::generate (src/generator.cc:545-1117).
+//
+// Host code only: every device action goes through the hai_* C ABI
+// (include/hai_kernels.h).  Layout in HBM:
+//   * weights: one arena, each Linear stored [N, K] row-major as in the
+//     checkpoint, with the projections of a layer concatenated so that one
+//     weight-streaming launch covers them: DeltaNet in_proj = [qkv | z | a | b]
+//     rows, attention = [q(+gate) | k | v] rows, MLP gate/up interleaved row by
+//     row (gate_f, up_f) for the fused SwiGLU epilogue;
+//   * caches: KV [cap][nkv][D] per attention layer; DeltaNet conv inputs in a
+//     ring [ring][C] indexed by position and the fp32 state in slots
+//     [nslots][nv][dv][dk], the slot of sequence length L being L % nslots;
+//     committed lengths live on the device and are advanced by the accept
+//     kernel, so rollback is a length update, never a copy.
+#pragma once
+
+#include <chrono>
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "hai_engine.h"
+
+namespace hybridai::mi355x {
+
+struct LayerWeights {
+    bool attn = false;
+    uint16_t* in_ln = nullptr;
+    uint16_t* post_ln = nullptr;
+    // Gated DeltaNet
+    uint16_t* w_in = nullptr;     // [C + nv*dv + 2*nv, H]
+    uint16_t* conv_w = nullptr;   // [C, Kc]
+    uint16_t* a_log = nullptr;    // [nv]
+    uint16_t* dt_bias = nullptr;  // [nv]
+    uint16_t* lin_norm = nullptr; // [dv]
+    uint16_t* w_out = nullptr;    // [H, nv*dv]
+    // gated GQA
+    uint16_t* w_qkv = nullptr;    // [nq*2D + 2*nkv*D, H]
+    uint16_t* q_norm = nullptr;   // [D]
+    uint16_t* k_norm = nullptr;   // [D]
+    uint16_t* w_o = nullptr;      // [H, nq*D]
+    // SwiGLU MLP
+    uint16_t* w_gu = nullptr;     // [2F, H], rows interleaved gate/up
+    uint16_t* w_down = nullptr;   // [H, F]
+    // caches
+    uint16_t* k_cache = nullptr;  // [cap][nkv][D]
+    uint16_t* v_cache = nullptr;
+    uint16_t* ring = nullptr;     // [ring][C]
+    float* state = nullptr;       // [nslots][nv][dv][dk]
+};
+
+struct TensorEntry {
+    uint32_t id;
+    uint16_t* ptr;
+    int64_t rows, cols, ld;
+};
+
+struct Dims {
+    int64_t H, F, V, nq, nkv, D, R, nk, nv, dk, dv, Kc, C, Nin, Nqkv, qw, kvw, vw;
+};
+
+class Engine {
+public:
+    Engine(const hai_model_config& cfg, const hai_engine_options& opt);
+    ~Engine();
+    Engine(const Engine&) = delete;
+    Engine& operator=(const Engine&) = delete;
+
+    bool ok() const { return ok_; }
+    const std::string& error() const { return error_; }
+
+    int init_synthetic(uint64_t seed, float std_dev);
+    int64_t read_tensor(uint32_t id, uint16_t* out, int64_t capacity);
+    uint64_t weight_bytes() const { return weight_bytes_; }
+    const Dims& dims() const { return d_; }
+
+    int forward_rows(const int32_t* ids, int64_t T, uint16_t* hidden, uint16_t* logits);
+    int generate_greedy(const int32_t* prompt, int64_t P, int64_t max_new, const int32_t* eos,
+                        int64_t n_eos, int32_t* out, int64_t* n_out);
+    int generate_speculative(const int32_t* prompt, int64_t P, int64_t max_new, int64_t width,
+                             const int32_t* eos, int64_t n_eos, const int32_t* override_tokens,
+                             int64_t n_override, int32_t* out, hai_spec_stats* stats,
+                             int32_t* round_log, int64_t round_log_cap, int64_t* n_out);
+
+    // benchmark split of generate_speculative
+    int prefill(const int32_t* prompt, int64_t P, int64_t max_new);
+    int spec_rounds(int64_t rounds, int64_t width, int32_t* out, int64_t cap, int64_t* n_out,
+                    hai_spec_stats* stats);
+    int profile_verify(int64_t T, int64_t iters, hai_verify_profile* out);
+
+private:
+    struct RoundState {
+        int64_t max_new = 0;
+        int64_t emitted = 0;
+        int64_t next_target = 0;
+        int64_t target_len = 0;  // host mirror of the device committed length
+        int64_t mtp_len = 0;
+        bool done = false;
+    };
+
+    int fail(int rc, const std::string& what);
+    int alloc_all();
+    int reset_state();
+    int upload_rope_tables();
+
+    // device pieces of a step
+    int gemm(uint16_t* y, int64_t ldy, const uint16_t* x, int64_t ldx, const uint16_t* w, int64_t M,
+             int64_t N, int64_t K, int epi, const uint16_t* res, int64_t ldres);
+    int forward_target(const int64_t* d_ids, int64_t T, bool write_all_slots);
+    int attention_layer(const LayerWeights& L, int64_t T, uint16_t* h, const int32_t* lens,
+                        uint16_t* kc, uint16_t* vc);
+    int mlp(const LayerWeights& L, int64_t T, uint16_t* h);
+    int mtp_kv_rows(const int64_t* d_ids, const uint16_t* d_hidden, int64_t T);
+    int mtp_draft_step(const int64_t* d_id, const uint16_t* d_hin, uint16_t* d_mh, int64_t* d_cand);
+    int prefill_chunks(const int32_t* ids, int64_t P, uint16_t* hidden_out, uint16_t* logits_out);
+    int one_round(RoundState& st, int64_t width, const int32_t* eos, int64_t n_eos,
+                  const int32_t* override_tokens, int64_t n_override, int32_t* out,
+                  hai_spec_stats* stats, int32_t* log_rec);
+    int sync();
+    int read_i64(const int64_t* d, int64_t* h, int64_t n);
+
+    hai_model_config cfg_{};
+    hai_engine_options opt_{};
+    Dims d_{};
+    bool ok_ = false;
+    std::string error_;
+
+    void* stream_ = nullptr;
+    void* weights_ = nullptr;
+    void* caches_ = nullptr;
+    void* work_ = nullptr;
+    uint64_t weight_bytes_ = 0;
+
+    int64_t cap_ = 0;     // KV capacity per sequence
+    int64_t tmax_ = 0;    // largest verify T / prefill chunk
+    int64_t ring_ = 0;
+    int64_t nslots_ = 0;
+
+    std::vector<LayerWeights> layers_;
+    LayerWeights mtp_;
+    uint16_t* embed_ = nullptr;
+    uint16_t* final_norm_ = nullptr;
+    uint16_t* lm_head_ = nullptr;
+    uint16_t* fc_ = nullptr;
+    uint16_t* mtp_norm_ = nullptr;
+    uint16_t* pre_emb_ = nullptr;
+    uint16_t* pre_hid_ = nullptr;
+    std::vector<TensorEntry> tensors_;
+
+    // workspace
+    int64_t* d_ids_ = nullptr;    // [tmax] prefill / forward ids
+    int64_t* d_vids_ = nullptr;   // [tmax+1] next_target + candidates
+    int64_t* d_preds_ = nullptr;  // [tmax]
+    int32_t* d_result_ = nullptr; // [4]
+    int32_t* d_tlen_ = nullptr;   // committed target length
+    int32_t* d_mlen_ = nullptr;   // MTP cache length
+    int32_t* d_plen_ = nullptr;   // [8] profiling scratch lengths/results
+    int64_t* d_pnext_ = nullptr;  // [8] profiling scratch tokens
+    uint16_t* h_ = nullptr;       // [tmax, H] residual stream
+    uint16_t* xn_ = nullptr;      // [tmax, 2H]
+    uint16_t* emb_ = nullptr;     // [tmax, H]
+    uint16_t* proj_ = nullptr;    // [tmax, max(Nin, Nqkv)]
+    uint16_t* q_ = nullptr;       // [tmax, nq*D]
+    uint16_t* gate_ = nullptr;
+    uint16_t* att_ = nullptr;
+    uint16_t* dnout_ = nullptr;   // [tmax, nv*dv]
+    uint16_t* act_ = nullptr;     // [tmax, F]
+    uint16_t* hf_ = nullptr;      // [tmax, H] post-final-norm hidden
+    uint16_t* logits_ = nullptr;  // [tmax, V]
+    uint16_t* mh_[2] = {nullptr, nullptr};  // MTP outputs (chained drafts)
+    uint16_t* h_prev_ = nullptr;  // target hidden feeding the next draft
+    uint16_t* rec_hidden_ = nullptr;
+    void* gqa_scratch_ = nullptr;
+    void* argmax_scratch_ = nullptr;
+    float* rope_cos_ = nullptr;
+    float* rope_sin_ = nullptr;
+    int64_t nproj_ = 0;
+
+    // profiling of GEMM launches (profile_verify only)
+    bool prof_gemm_ = false;
+    std::vector<void*> prof_events_;
+    size_t prof_used_ = 0;
+    double prof_bytes_ = 0.0;
+    int64_t prof_launches_ = 0;
+
+    RoundState rs_;
+};
+
+}  // namespace hybridai::mi355x
