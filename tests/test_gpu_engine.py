@@ -13,10 +13,14 @@ pytestmark = pytest.mark.gpu
 P, NEW = 32, 64
 
 
-@pytest.fixture(scope="module")
-def engines():
+@pytest.fixture(scope="module", params=[False, True], ids=["launches", "graphs"])
+def engines(request):
+    """The engine with plain launches and with captured HIP graphs (every
+    round replays the draft/verify/correction graphs with host
+    synchronisations in between; each replay is checked through the round
+    logs)."""
     from hybridai_amd import engine as E
-    eng = E.Engine(E.TINY, max_context=P + NEW + 32, max_verify_tokens=16)
+    eng = E.Engine(E.TINY, max_context=P + NEW + 32, max_verify_tokens=16, use_graphs=request.param)
     eng.init_synthetic(seed=0, std=0.02)
     ref = orc.Model(orc.TINY, seed=0)
     prompt = orc.synthetic_prompt(0, P, orc.TINY["vocab"])

@@ -99,6 +99,21 @@ __device__ __forceinline__ float csigmoid(float x) { return 1.0f / (1.0f + cexp(
 __device__ __forceinline__ float csilu(float x) { return x / (1.0f + cexp(-x)); }
 __device__ __forceinline__ float csqrt(float x) { return __builtin_sqrtf(x); }
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Raw buffer resource over [base, base + bytes): loads whose byte offset is
+// at or past `bytes` return zero, which masks rows past N or M without
+// branches (dword3 = 0x00020000 is the gfx9 raw-buffer format word).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
+                                             static_cast<int>(bytes), 0x00020000);
+}
+__device__ __forceinline__ u32x4 bload(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(voff),
+                                                                           static_cast<int>(soff), 0));
+}
+constexpr uint32_t kOutOfRange = 0xfffffff0u;
+
 // xor butterfly over the 64 lanes of a wave; all lanes get the same bits.
 __device__ __forceinline__ float wave_sum64(float v) {
 #pragma unroll

@@ -34,32 +34,35 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(
     if (row0 >= N) return;
     const int nrows = static_cast<int>(min(static_cast<int64_t>(RW), static_cast<int64_t>(N) - row0));
 
+    // Byte offsets fit 32 bits: the caller bounds N*K*2 and M*ldx*2 below 4 GiB.
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, static_cast<uint32_t>(static_cast<int64_t>(N) * K * 2));
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, static_cast<uint32_t>(static_cast<int64_t>(M) * ldx * 2));
+    uint32_t woff[RW], xoff[MB];
+#pragma unroll
+    for (int r = 0; r < RW; ++r)
+        woff[r] = static_cast<uint32_t>(((row0 + r) * static_cast<int64_t>(K) + lane * 8) * 2);
+#pragma unroll
+    for (int m = 0; m < MB; ++m) xoff[m] = static_cast<uint32_t>((static_cast<int64_t>(m) * ldx + lane * 8) * 2);
+
     float acc[RW][MB];
 #pragma unroll
     for (int r = 0; r < RW; ++r)
 #pragma unroll
         for (int m = 0; m < MB; ++m) acc[r][m] = 0.0f;
 
-    const int nck = (K + 511) / 512;
-    const uint16_t* wl = w + row0 * static_cast<int64_t>(K) + lane * 8;
-    const uint16_t* xl = x + lane * 8;
-    const uint4 zero4 = make_uint4(0u, 0u, 0u, 0u);
-
-    auto body = [&](const uint4 (&wv)[RW], const uint4 (&xv)[MB]) {
+    auto body = [&](const u32x4 (&wv)[RW], const u32x4 (&xv)[MB]) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             float xa[MB], xb[MB];
 #pragma unroll
             for (int m = 0; m < MB; ++m) {
-                const uint32_t d = (q == 0) ? xv[m].x : (q == 1) ? xv[m].y : (q == 2) ? xv[m].z : xv[m].w;
-                xa[m] = lo_bf(d);
-                xb[m] = hi_bf(d);
+                xa[m] = lo_bf(xv[m][q]);
+                xb[m] = hi_bf(xv[m][q]);
             }
 #pragma unroll
             for (int r = 0; r < RW; ++r) {
-                const uint32_t d = (q == 0) ? wv[r].x : (q == 1) ? wv[r].y : (q == 2) ? wv[r].z : wv[r].w;
-                const float wa = lo_bf(d);
-                const float wb = hi_bf(d);
+                const float wa = lo_bf(wv[r][q]);
+                const float wb = hi_bf(wv[r][q]);
 #pragma unroll
                 for (int m = 0; m < MB; ++m) {
                     acc[r][m] = fma_(xa[m], wa, acc[r][m]);
@@ -69,43 +72,28 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(
         }
     };
 
-    int c = 0;
-    for (; c + U <= nck; c += U) {
-        uint4 wv[U][RW];
-        uint4 xv[U][MB];
+    // Groups of U chunks.  A chunk past K (ragged tail or group padding)
+    // reads zeros through an out-of-range offset; fma(0, 0, acc) == acc
+    // because acc is never -0 (it starts at +0 and round-to-nearest only
+    // produces -0 from (-0) + (-0)), so padding does not change a bit.
+    const int nck = (K + 511) / 512;
+    const int nfull = K / 512;
+    for (int c0 = 0; c0 < nck; c0 += U) {
+        u32x4 wv[U][RW];
+        u32x4 xv[U][MB];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int64_t koff = static_cast<int64_t>(c + u) * 512;
-            const bool valid = koff + lane * 8 < K;
+            const int c = c0 + u;
+            // full chunk: every lane valid; ragged chunk: lanes past K masked
+            const bool ok = c < nfull || (c < nck && c * 512 + lane * 8 < K);
+            const uint32_t so = ok ? static_cast<uint32_t>(c) * 1024u : 0u;
 #pragma unroll
-            for (int r = 0; r < RW; ++r)
-                wv[u][r] = (valid && r < nrows)
-                    ? *reinterpret_cast<const uint4*>(wl + static_cast<int64_t>(r) * K + koff)
-                    : zero4;
+            for (int r = 0; r < RW; ++r) wv[u][r] = bload(rw, ok ? woff[r] : kOutOfRange, so);
 #pragma unroll
-            for (int m = 0; m < MB; ++m)
-                xv[u][m] = (valid && m < M)
-                    ? *reinterpret_cast<const uint4*>(xl + static_cast<int64_t>(m) * ldx + koff)
-                    : zero4;
+            for (int m = 0; m < MB; ++m) xv[u][m] = bload(rx, ok ? xoff[m] : kOutOfRange, so);
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) body(wv[u], xv[u]);
-    }
-    for (; c < nck; ++c) {
-        uint4 wv[RW];
-        uint4 xv[MB];
-        const int64_t koff = static_cast<int64_t>(c) * 512;
-        const bool valid = koff + lane * 8 < K;
-#pragma unroll
-        for (int r = 0; r < RW; ++r)
-            wv[r] = (valid && r < nrows)
-                ? *reinterpret_cast<const uint4*>(wl + static_cast<int64_t>(r) * K + koff)
-                : zero4;
-#pragma unroll
-        for (int m = 0; m < MB; ++m)
-            xv[m] = (valid && m < M) ? *reinterpret_cast<const uint4*>(xl + static_cast<int64_t>(m) * ldx + koff)
-                                     : zero4;
-        body(wv, xv);
     }
 
 #pragma unroll
@@ -143,7 +131,7 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(
 template <int MB, int RW, int EPI>
 void launch_gemm(uint16_t* y, int64_t ldy, const uint16_t* x, int64_t ldx, const uint16_t* w,
                  const uint16_t* res, int64_t ldres, int M, int N, int K, hipStream_t s) {
-    constexpr int U = MB <= 2 ? 4 : (MB <= 4 ? 2 : 1);
+    constexpr int U = MB <= 2 ? 4 : (MB <= 8 ? 2 : 1);
     const int64_t waves = (static_cast<int64_t>(N) + RW - 1) / RW;
     const unsigned blocks = static_cast<unsigned>((waves + 3) / 4);
     gemm_bf16_kernel<MB, RW, U, EPI><<<dim3(blocks), dim3(256), 0, s>>>(y, ldy, x, ldx, w, res, ldres, M,
@@ -153,10 +141,10 @@ void launch_gemm(uint16_t* y, int64_t ldy, const uint16_t* x, int64_t ldx, const
 template <int MB, int EPI>
 void dispatch_rw(uint16_t* y, int64_t ldy, const uint16_t* x, int64_t ldx, const uint16_t* w,
                  const uint16_t* res, int64_t ldres, int M, int N, int K, hipStream_t s) {
-    // Wide layers keep 4 rows per wave; narrow ones use 2 so that the grid
-    // still holds several waves per SIMD across the 256 CUs.
-    if (N >= 4 * 2048) launch_gemm<MB, 4, EPI>(y, ldy, x, ldx, w, res, ldres, M, N, K, s);
-    else launch_gemm<MB, 2, EPI>(y, ldy, x, ldx, w, res, ldres, M, N, K, s);
+    // Two rows per wave keeps the register footprint small enough for eight
+    // waves per SIMD, which is what keeps enough bytes in flight on gfx950
+    // (measured faster than 4 rows per wave or software-pipelined variants).
+    launch_gemm<MB, 2, EPI>(y, ldy, x, ldx, w, res, ldres, M, N, K, s);
 }
 
 template <int EPI>
@@ -178,6 +166,8 @@ extern "C" int hai_gemm_bf16(void* y, int64_t ldy, const void* x, int64_t ldx, c
     if (M < 0 || M > 16 || N < 0 || K <= 0 || K % 8 != 0 || ldx % 8 != 0 || ldx < K)
         return invalid("gemm: shape (need 0<=M<=16, K%8==0, ldx%8==0, ldx>=K)");
     if (N > INT32_MAX || K > INT32_MAX) return invalid("gemm: dimension too large");
+    if ((N + 4) * K * 2 >= (int64_t{1} << 32) || M * ldx * 2 >= (int64_t{1} << 32))
+        return invalid("gemm: W or X exceeds the 4 GiB buffer-offset range");
     if (!aligned16(x) || !aligned16(w)) return invalid("gemm: x and w must be 16-byte aligned");
     if (M == 0 || N == 0) return HAI_OK;
     const auto* xs = static_cast<const uint16_t*>(x);

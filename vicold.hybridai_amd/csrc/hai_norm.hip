@@ -13,6 +13,9 @@ using namespace hai;
 constexpr int kMaxHeadDim = 512;
 
 // rmsnorm_kernel (hip_kernels.hip:105-137): 4 rows per 256-thread block.
+// Rows up to 8192 wide are loaded once into registers (all loads in flight
+// before the first use), reduced in L64 order and normalised from registers.
+template <int NC>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(uint16_t* __restrict__ y, int64_t ldy,
                                                       const uint16_t* __restrict__ x, int64_t ldx,
                                                       const uint16_t* __restrict__ w, int64_t rows,
@@ -20,15 +23,37 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(uint16_t* __restrict__ y, 
     const int lane = threadIdx.x & 63;
     const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
     if (row >= rows) return;
-    const uint16_t* xr = x + row * ldx;
-    const float ss = l64_sumsq_bf16(xr, H, lane);
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + row * ldx, static_cast<uint32_t>(H) * 2u);
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, static_cast<uint32_t>(H) * 2u);
+    u32x4 xd[NC], wd[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const uint32_t off = static_cast<uint32_t>(c * 512 + lane * 8) * 2u;  // past H reads zero
+        xd[c] = bload(rx, off, 0);
+        wd[c] = bload(rw, off, 0);
+    }
+    float acc = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        if (c * 512 + lane * 8 >= H) continue;
+        const uint32_t xs[4] = {xd[c][0], xd[c][1], xd[c][2], xd[c][3]};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float a = lo_bf(xs[q]);
+            const float b = hi_bf(xs[q]);
+            acc = fma_(a, a, acc);
+            acc = fma_(b, b, acc);
+        }
+    }
+    const float ss = wave_sum64(acc);
     const float inv = 1.0f / csqrt(ss / static_cast<float>(H) + eps);
     uint16_t* yr = y + row * ldy;
-    for (int k0 = lane * 8; k0 < H; k0 += 512) {
-        const uint4 xd = *reinterpret_cast<const uint4*>(xr + k0);
-        const uint4 wd = *reinterpret_cast<const uint4*>(w + k0);
-        const uint32_t xs[4] = {xd.x, xd.y, xd.z, xd.w};
-        const uint32_t ws[4] = {wd.x, wd.y, wd.z, wd.w};
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const int k0 = c * 512 + lane * 8;
+        if (k0 >= H) continue;
+        const uint32_t xs[4] = {xd[c][0], xd[c][1], xd[c][2], xd[c][3]};
+        const uint32_t ws[4] = {wd[c][0], wd[c][1], wd[c][2], wd[c][3]};
         uint32_t o[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -190,10 +215,18 @@ int hai_rmsnorm_bf16(void* y, int64_t ldy, const void* x, int64_t ldx, const voi
     if (rows < 0 || H <= 0 || H % 8 != 0 || ldx % 8 != 0 || ldy % 8 != 0 || ldx < H || ldy < H)
         return invalid("rmsnorm: shape (need H%8==0, 8-aligned strides)");
     if (!aligned16(x) || !aligned16(y) || !aligned16(w)) return invalid("rmsnorm: 16-byte alignment");
+    if (H > 16 * 512) return invalid("rmsnorm: H above 8192");
     if (rows == 0) return HAI_OK;
-    rmsnorm_kernel<<<dim3(static_cast<unsigned>((rows + 3) / 4)), dim3(256), 0, as_stream(stream)>>>(
-        static_cast<uint16_t*>(y), ldy, static_cast<const uint16_t*>(x), ldx,
-        static_cast<const uint16_t*>(w), rows, static_cast<int>(H), eps, unit_offset ? 1.0f : 0.0f);
+    const dim3 grid(static_cast<unsigned>((rows + 3) / 4));
+    auto* yy = static_cast<uint16_t*>(y);
+    const auto* xx = static_cast<const uint16_t*>(x);
+    const auto* ww = static_cast<const uint16_t*>(w);
+    const float off = unit_offset ? 1.0f : 0.0f;
+    const auto s = as_stream(stream);
+    if (H <= 512) rmsnorm_kernel<1><<<grid, dim3(256), 0, s>>>(yy, ldy, xx, ldx, ww, rows, int(H), eps, off);
+    else if (H <= 2048) rmsnorm_kernel<4><<<grid, dim3(256), 0, s>>>(yy, ldy, xx, ldx, ww, rows, int(H), eps, off);
+    else if (H <= 6144) rmsnorm_kernel<12><<<grid, dim3(256), 0, s>>>(yy, ldy, xx, ldx, ww, rows, int(H), eps, off);
+    else rmsnorm_kernel<16><<<grid, dim3(256), 0, s>>>(yy, ldy, xx, ldx, ww, rows, int(H), eps, off);
     return launched("rmsnorm_kernel");
 }
 

@@ -180,3 +180,19 @@ class Engine:
         pr = VerifyProfile()
         self._check(self.lib.hai_engine_profile_verify(self.h, T, iters, ctypes.byref(pr)), "profile_verify")
         return pr.as_dict()
+
+
+def _splitmix64(x: np.ndarray) -> np.ndarray:
+    x = x + np.uint64(0x9E3779B97F4A7C15)
+    x = (x ^ (x >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+    x = (x ^ (x >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+    return x ^ (x >> np.uint64(31))
+
+
+def synthetic_prompt(seed: int, n: int, vocab: int) -> np.ndarray:
+    """Uniform prompt ids: splitmix64 counter stream 0xFFFF of the seed, mod
+    vocab (the same stream the CPU oracle uses for its prompts)."""
+    with np.errstate(over="ignore"):
+        key = _splitmix64(np.array([np.uint64(seed) ^ (np.uint64(0xFFFF) << np.uint64(32))], np.uint64))[0]
+        h = _splitmix64(key + np.arange(n, dtype=np.uint64))
+    return (h % np.uint64(vocab)).astype(np.int32)

@@ -83,6 +83,9 @@ Engine::Engine(const hai_model_config& cfg, const hai_engine_options& opt) : cfg
     cap_ = std::max<int64_t>(opt.max_context, tmax_ + 1);
     ring_ = 32;
     nslots_ = tmax_ + 1;
+    use_graphs_ = opt.use_graphs != 0;
+    draft_graphs_.assign(static_cast<size_t>(tmax_), nullptr);
+    verify_graphs_.assign(static_cast<size_t>(tmax_ + 1), nullptr);
     if (cfg.hidden <= 0 || cfg.hidden % 8 != 0 || cfg.num_layers <= 0 || cfg.full_attention_interval <= 0 ||
         cfg.num_kv_heads <= 0 || cfg.num_q_heads % cfg.num_kv_heads != 0 || cfg.lin_qk_heads <= 0 ||
         cfg.lin_v_heads % cfg.lin_qk_heads != 0 || cfg.ffn % 8 != 0 || cfg.mtp_layers != 1 ||
@@ -102,6 +105,9 @@ Engine::Engine(const hai_model_config& cfg, const hai_engine_options& opt) : cfg
 
 Engine::~Engine() {
     if (stream_) hai_stream_synchronize(stream_);
+    for (void* g : draft_graphs_) if (g) hai_graph_destroy(g);
+    for (void* g : verify_graphs_) if (g) hai_graph_destroy(g);
+    if (corr_graph_) hai_graph_destroy(corr_graph_);
     for (void* e : prof_events_) hai_event_destroy(e);
     if (weights_) hai_free(weights_);
     if (caches_) hai_free(caches_);
@@ -481,6 +487,55 @@ int Engine::generate_greedy(const int32_t* prompt, int64_t P, int64_t max_new, c
     return HAI_OK;
 }
 
+template <typename F>
+int Engine::replay(void** slot, F&& enqueue) {
+    if (!use_graphs_ || prof_gemm_) return enqueue();
+    if (*slot == nullptr) {
+        HAI_TRY(hai_graph_begin_capture(stream_));
+        const int rc = enqueue();
+        void* exec = nullptr;
+        const int rc_end = hai_graph_end_capture(stream_, &exec);
+        if (rc != HAI_OK) return rc;
+        if (rc_end != HAI_OK) return fail(rc_end, "graph capture");
+        *slot = exec;
+    }
+    HAI_TRY(hai_graph_launch(*slot, stream_));
+    return HAI_OK;
+}
+
+// Draft i reads candidate i (vids[i]; vids[0] is next_target) and the hidden
+// that produced it, writes candidate i+1.
+int Engine::draft_step_at(int64_t i) {
+    const uint16_t* hin = i == 0 ? h_prev_ : mh_[(i - 1) % 2];
+    return replay(&draft_graphs_[static_cast<size_t>(i)],
+                  [&] { return mtp_draft_step(d_vids_ + i, hin, mh_[i % 2], d_vids_ + i + 1); });
+}
+
+// Verify forward of T rows + fused argmax/acceptance (commits on device).
+int Engine::verify_step(int64_t T) {
+    return replay(&verify_graphs_[static_cast<size_t>(T)], [&]() -> int {
+        HAI_TRY(forward_target(d_vids_, T, true));
+        HAI_TRY(hai_verify_argmax_accept_bf16(logits_, d_.V, hf_, d_.H, d_vids_, nullptr, 1, T, d_preds_,
+                                              d_result_, d_tlen_, d_mlen_, d_vids_, rec_hidden_, h_prev_,
+                                              argmax_scratch_, stream_));
+        return HAI_OK;
+    });
+}
+
+// Mismatch path: MTP recovery row (emb(corr), hidden of the last accepted
+// row), then the forward of corr on the committed prefix; its argmax is the
+// next target and its hidden feeds the next draft.
+int Engine::correction_step() {
+    return replay(&corr_graph_, [&]() -> int {
+        HAI_TRY(mtp_kv_rows(d_vids_, rec_hidden_, 1));
+        HAI_TRY(forward_target(d_vids_, 1, false));
+        HAI_TRY(hai_add_i32(d_tlen_, nullptr, 1, 1, stream_));
+        HAI_TRY(hai_argmax_rows_bf16(d_vids_, logits_, d_.V, 1, d_.V, argmax_scratch_, stream_));
+        HAI_TRY(hai_memcpy_d2d(h_prev_, hf_, static_cast<size_t>(d_.H) * 2, stream_));
+        return HAI_OK;
+    });
+}
+
 // One round of the reference loop body (generator.cc:720-1028).
 int Engine::one_round(RoundState& st, int64_t width, const int32_t* eos, int64_t n_eos,
                       const int32_t* override_tokens, int64_t n_override, int32_t* out, hai_spec_stats* stats,
@@ -499,10 +554,9 @@ int Engine::one_round(RoundState& st, int64_t width, const int32_t* eos, int64_t
 
     // ---- draft (chained MTP proposals) ----
     auto t0 = Clock::now();
-    const uint16_t* hin = h_prev_;
     int64_t k = 0;
     for (int64_t i = 0; i < pc; ++i) {
-        HAI_TRY(mtp_draft_step(d_vids_ + i, hin, mh_[i % 2], d_vids_ + i + 1));
+        HAI_TRY(draft_step_at(i));
         const int64_t pos = st.emitted + 1 + i;
         if (override_tokens != nullptr && pos < n_override) {
             const int64_t tok = override_tokens[pos];
@@ -511,7 +565,6 @@ int Engine::one_round(RoundState& st, int64_t width, const int32_t* eos, int64_t
         }
         ++k;
         ++stats->proposed;
-        hin = mh_[i % 2];
         if (n_eos > 0) {
             int64_t cand = 0;
             HAI_TRY(read_i64(d_vids_ + i + 1, &cand, 1));
@@ -523,10 +576,7 @@ int Engine::one_round(RoundState& st, int64_t width, const int32_t* eos, int64_t
     // ---- verify + fused argmax/accept ----
     t0 = Clock::now();
     const int64_t T = k + 1;
-    HAI_TRY(forward_target(d_vids_, T, true));
-    HAI_TRY(hai_verify_argmax_accept_bf16(logits_, d_.V, hf_, d_.H, d_vids_, nullptr, 1, T, d_preds_, d_result_,
-                                          d_tlen_, d_mlen_, d_vids_, rec_hidden_, h_prev_, argmax_scratch_,
-                                          stream_));
+    HAI_TRY(verify_step(T));
     int32_t res[4];
     int64_t preds[17], cands[17];
     HAI_TRY(hai_memcpy_d2h(res, d_result_, sizeof(res), stream_));
@@ -570,13 +620,8 @@ int Engine::one_round(RoundState& st, int64_t width, const int32_t* eos, int64_t
             t0 = Clock::now();
             // MTP checkpoint[a] (length already rolled back by the accept
             // kernel) plus the recovery row (emb(corr), hidden of row a).
-            HAI_TRY(mtp_kv_rows(d_vids_, rec_hidden_, 1));
+            HAI_TRY(correction_step());
             ++stats->mtp_recovery_tokens;
-            // Correction forward: next_target = argmax after corr.
-            HAI_TRY(forward_target(d_vids_, 1, false));
-            HAI_TRY(hai_add_i32(d_tlen_, nullptr, 1, 1, stream_));
-            HAI_TRY(hai_argmax_rows_bf16(d_vids_, logits_, d_.V, 1, d_.V, argmax_scratch_, stream_));
-            HAI_TRY(hai_memcpy_d2d(h_prev_, hf_, static_cast<size_t>(d_.H) * 2, stream_));
             ++stats->replay_tokens;
             int64_t next = 0;
             HAI_TRY(read_i64(d_vids_, &next, 1));

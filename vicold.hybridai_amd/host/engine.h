@@ -120,6 +120,13 @@ private:
                   hai_spec_stats* stats, int32_t* log_rec);
     int sync();
     int read_i64(const int64_t* d, int64_t* h, int64_t n);
+    // Replays the captured graph in *slot (capturing `enqueue` on first use)
+    // when graphs are enabled; otherwise launches `enqueue` directly.
+    template <typename F>
+    int replay(void** slot, F&& enqueue);
+    int draft_step_at(int64_t i);
+    int verify_step(int64_t T);
+    int correction_step();
 
     hai_model_config cfg_{};
     hai_engine_options opt_{};
@@ -186,6 +193,11 @@ private:
     int64_t prof_launches_ = 0;
 
     RoundState rs_;
+
+    bool use_graphs_ = false;
+    std::vector<void*> draft_graphs_;   // by draft index
+    std::vector<void*> verify_graphs_;  // by verify width T
+    void* corr_graph_ = nullptr;
 };
 
 }  // namespace hybridai::mi355x
