@@ -158,8 +158,11 @@ int hai_gqa_verify_bf16(void* out, const void* q, const void* gate,
  *   proj rows (ld_proj) hold [qkv(C) | z(nv*dv) | a(nv) | b(nv)] at the given
  *     column offsets, C = 2*nk*dk + nv*dv in flat [Q|K|V] channel order;
  *   conv_ring is [B][ring][C] raw inputs indexed by position % ring;
- *   state is [nslots][B][nv][dv][dk] fp32 (value-major); the state after
- *     sequence length L lives in slot L % nslots;
+ *   state is [nslots][B][nv][dk*dv] fp32, each head column-tiled: entry
+ *     (key i, value j) of the reference's [dk][dv] matrix, with
+ *     i = g*(dk/4) + 4m + e (g, e < 4), is float ((m*dv + j)*4 + g)*4 + e;
+ *     the state after sequence length L lives in slot L % nslots;
+ *   at most 16 tokens per launch;
  *   token t of sequence b has position (lens ? lens[b] : 0) + pos_add + t.
  * With write_all_slots the state after every token is kept (rollback by
  * length only, no copies); otherwise only the final state is written.

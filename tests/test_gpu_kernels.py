@@ -237,8 +237,11 @@ def _deltanet_case(rng, B, nk, nv, dk, dv, Kc=4):
                 nwb=nwb, Kc=Kc)
 
 
-def _to_value_major(state, nv, dk, dv):
-    return np.ascontiguousarray(state.reshape(nv, dk, dv).transpose(0, 2, 1))
+def _to_tiled(state, nv, dk, dv):
+    """Reference [nv][dk][dv] state -> the kernel's column-tiled head layout:
+    key i = g*(dk/4) + 4m + e, value j at ((m*dv + j)*4 + g)*4 + e."""
+    t = state.reshape(nv, 4, dk // 16, 4, dv).transpose(0, 2, 4, 1, 3)
+    return np.ascontiguousarray(t).reshape(nv, dv, dk)
 
 
 @pytest.mark.parametrize("nk,nv,dk,dv,steps", [(4, 4, 64, 64, [2, 1, 3]), (16, 48, 128, 128, [4, 2]),
@@ -285,7 +288,7 @@ def test_deltanet_verify_rollback(nk, nv, dk, dv, steps):
         L += acc
         slot = L % nslots
         dev_state = dstate.download(np.float32).reshape(nslots, B, nv, dv, dk)[slot, 0]
-        want_state = _to_value_major(state, nv, dk, dv)
+        want_state = _to_tiled(state, nv, dk, dv)
         assert np.array_equal(dev_state.view(np.uint32), want_state.view(np.uint32)), f"state after step {si}"
 
 

@@ -4,14 +4,15 @@
 //
 // The reference walks every key serially in one wave per (head, query).
 // Here the keys are split into fixed 64-key chunks by absolute index:
-//   pass 1 (one block per chunk x KV head x sequence): the chunk's K and V
-//     tiles are staged once in LDS and shared by every query of that KV head
-//     (T tokens x nq/nkv heads); lane = key computes the score with a
-//     sequential fma over D, the chunk max and the exp-sum are wave
-//     reductions, and P.V is a sequential fma over the chunk's keys with
-//     lane = output dim;
+//   pass 1 (one block per chunk x group of four queries of one KV head x
+//     sequence): the chunk's K and V tiles are staged in LDS with all loads
+//     in flight at once; each wave takes one query: lane = key computes the
+//     score with a sequential fma over D, the chunk max and the exp-sum are
+//     wave reductions, and P.V is a sequential fma over the chunk's keys with
+//     lane = pair of output dims;
 //   pass 2 (one wave per query): chunk partials are merged against the
-//     global max in chunk order, then divided, gated and stored.
+//     global max in chunk order (loads batched eight chunks deep), then
+//     divided, gated and stored.
 // The chunking is by absolute key index, so a query's result does not depend
 // on T, on the batch or on how many blocks run: verify rows and replayed
 // rows are bit-identical, and the CPU oracle follows the same order.
@@ -23,113 +24,137 @@ namespace {
 using namespace hai;
 
 constexpr int kChunk = 64;
-constexpr int kQBatch = 32;  // queries processed per pass over the staged tile
+constexpr int kQPerBlock = 4;  // one query per wave
 
 __host__ __device__ constexpr int64_t partial_stride(int D) { return D + 2; }
 
+// grid (chunk, query group x KV head, sequence): the block stages one 64-key
+// chunk of one KV head and serves up to four of that head's queries.
 template <int D>
 __global__ __launch_bounds__(256) void gqa_partial_kernel(
     float* __restrict__ scratch, const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, int64_t cap, int T, int nq, int nkv, const int32_t* lens,
     int len_add, int nchunk, float scale) {
-    constexpr int KP = D / 2 + 1;  // padded dword stride of a K row in LDS
+    constexpr int KP = D / 2 + 4;          // dword stride of a staged K row (16-byte pad)
+    constexpr int VP = D / 2;              // dword stride of a staged V row
+    constexpr int ROW16 = D / 8;           // 16-byte pieces per row
+    constexpr int NLD = kChunk * ROW16 / 256;  // pieces per thread and tile
+    static_assert(NLD >= 1 && kChunk * ROW16 % 256 == 0, "tile must split over 256 threads");
     __shared__ uint32_t Ks[kChunk * KP];
-    __shared__ uint16_t Vs[kChunk * D];
-    __shared__ float Qs[kQBatch * D];
-    __shared__ float Ps[kQBatch * kChunk];
+    __shared__ uint32_t Vs[kChunk * VP];
+    __shared__ float Qs[kQPerBlock][D];
+    __shared__ float Ps[kQPerBlock][kChunk];
 
     const int chunk = blockIdx.x;
-    const int kvh = blockIdx.y;
+    const int kvh = blockIdx.y % nkv;
+    const int qgrp = blockIdx.y / nkv;
     const int b = blockIdx.z;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int64_t L = static_cast<int64_t>(lens ? lens[b] : 0) + len_add;
     const int64_t key0 = static_cast<int64_t>(chunk) * kChunk;
-    if (key0 >= L) return;
-    const int nkeys = static_cast<int>(min(static_cast<int64_t>(kChunk), L - key0));
     const int group = nq / nkv;
     const int nqry = T * group;
+    if (key0 >= L || qgrp * kQPerBlock >= nqry) return;
+    const int nkeys = static_cast<int>(min(static_cast<int64_t>(kChunk), L - key0));
 
-    // Stage K (padded, bf16 pairs) and V tiles of this chunk; rows past L are zero.
-    const int64_t seq_base = static_cast<int64_t>(b) * cap;
-    for (int e = tid; e < kChunk * (D / 8); e += 256) {
-        const int j = e / (D / 8);
-        const int d8 = (e % (D / 8)) * 8;
-        uint4 kd = make_uint4(0u, 0u, 0u, 0u), vd = kd;
-        if (j < nkeys) {
-            const int64_t off = ((seq_base + key0 + j) * nkv + kvh) * D + d8;
-            kd = *reinterpret_cast<const uint4*>(kc + off);
-            vd = *reinterpret_cast<const uint4*>(vc + off);
+    // Stage the chunk's K and V rows: every load is issued before the first
+    // LDS store; rows past the cache length read as zeros (buffer range).
+    {
+        const int64_t off0 = ((static_cast<int64_t>(b) * cap + key0) * nkv + kvh) * D;
+        const uint32_t bytes = static_cast<uint32_t>((static_cast<int64_t>(nkeys - 1) * nkv * D + D) * 2);
+        const __amdgpu_buffer_rsrc_t rk = make_rsrc(kc + off0, bytes);
+        const __amdgpu_buffer_rsrc_t rv = make_rsrc(vc + off0, bytes);
+        u32x4 kd[NLD], vd[NLD];
+#pragma unroll
+        for (int i = 0; i < NLD; ++i) {
+            const int e = tid + 256 * i;
+            const int j = e / ROW16;
+            const uint32_t off = static_cast<uint32_t>((j * nkv * D + (e % ROW16) * 8) * 2);
+            kd[i] = bload(rk, off, 0);
+            vd[i] = bload(rv, off, 0);
         }
-        uint32_t* kr = Ks + j * KP + d8 / 2;
-        kr[0] = kd.x; kr[1] = kd.y; kr[2] = kd.z; kr[3] = kd.w;
-        *reinterpret_cast<uint4*>(Vs + j * D + d8) = vd;
+#pragma unroll
+        for (int i = 0; i < NLD; ++i) {
+            const int e = tid + 256 * i;
+            const int j = e / ROW16;
+            const int p = (e % ROW16) * 4;
+            *reinterpret_cast<u32x4*>(Ks + j * KP + p) = kd[i];
+            *reinterpret_cast<u32x4*>(Vs + j * VP + p) = vd[i];
+        }
     }
+    // This wave's query.
+    const int qi = qgrp * kQPerBlock + wave;
+    const bool has_q = qi < nqry;
+    const int t = has_q ? qi / group : 0;
+    const int h = kvh * group + (has_q ? qi % group : 0);
+    const int64_t qpos = L - T + t;
+    if (has_q) {
+        const uint16_t* qrow = q + ((static_cast<int64_t>(b) * T + t) * nq + h) * D;
+#pragma unroll
+        for (int d = lane; d < D; d += 64) Qs[wave][d] = bf2f(qrow[d]);
+    }
+    __syncthreads();
+    if (!has_q) return;
 
-    for (int qb = 0; qb < nqry; qb += kQBatch) {
-        const int nb = min(kQBatch, nqry - qb);
-        __syncthreads();
-        for (int e = tid; e < nb * D; e += 256) {
-            const int i = e / D;
-            const int d = e % D;
-            const int qi = qb + i;
-            const int t = qi / group;
-            const int h = kvh * group + qi % group;
-            Qs[i * D + d] = bf2f(q[((static_cast<int64_t>(b) * T + t) * nq + h) * D + d]);
+    // Scores: lane = key, sequential fma over D.
+    const int64_t kj = key0 + lane;
+    const bool valid = lane < nkeys && kj <= qpos;
+    float s = 0.0f;
+    {
+        const uint32_t* kr = Ks + lane * KP;
+        const float* qr = Qs[wave];
+#pragma unroll 4
+        for (int p = 0; p < D / 2; p += 4) {
+            const u32x4 kk = *reinterpret_cast<const u32x4*>(kr + p);
+            const float4 qa = *reinterpret_cast<const float4*>(qr + 2 * p);
+            const float4 qb = *reinterpret_cast<const float4*>(qr + 2 * p + 4);
+            s = fma_(qa.x, lo_bf(kk[0]), s);
+            s = fma_(qa.y, hi_bf(kk[0]), s);
+            s = fma_(qa.z, lo_bf(kk[1]), s);
+            s = fma_(qa.w, hi_bf(kk[1]), s);
+            s = fma_(qb.x, lo_bf(kk[2]), s);
+            s = fma_(qb.y, hi_bf(kk[2]), s);
+            s = fma_(qb.z, lo_bf(kk[3]), s);
+            s = fma_(qb.w, hi_bf(kk[3]), s);
         }
-        __syncthreads();
-        // Scores, chunk max and exp-sum: one query per wave at a time.
-        for (int i = wave; i < nb; i += 4) {
-            const int qi = qb + i;
-            const int t = qi / group;
-            const int h = kvh * group + qi % group;
-            const int64_t qpos = L - T + t;
-            const int64_t kj = key0 + lane;
-            const bool valid = lane < nkeys && kj <= qpos;
-            float s = 0.0f;
-            if (valid) {
-                const uint32_t* kr = Ks + lane * KP;
-                const float* qr = Qs + i * D;
-#pragma unroll 8
-                for (int d2 = 0; d2 < D / 2; ++d2) {
-                    const uint32_t kk = kr[d2];
-                    s = fma_(qr[2 * d2], lo_bf(kk), s);
-                    s = fma_(qr[2 * d2 + 1], hi_bf(kk), s);
-                }
-                s = s * scale;
-            }
-            const float m = wave_max64(valid ? s : __uint_as_float(0xff800000u));
-            const float p = valid ? cexp(s - m) : 0.0f;
-            const float l = wave_sum64(p);
-            Ps[i * kChunk + lane] = p;
-            if (lane == 0) {
-                float* part = scratch + ((((static_cast<int64_t>(b) * T + t) * nq + h) * nchunk) + chunk) *
-                                            partial_stride(D);
-                part[0] = m;
-                part[1] = l;
-            }
+        s = s * scale;
+    }
+    const float m = wave_max64(valid ? s : __uint_as_float(0xff800000u));
+    const float pr = valid ? cexp(s - m) : 0.0f;
+    const float l = wave_sum64(pr);
+    Ps[wave][lane] = pr;
+    float* part = scratch + ((((static_cast<int64_t>(b) * T + t) * nq + h) * nchunk) + chunk) * partial_stride(D);
+    if (lane == 0) {
+        part[0] = m;
+        part[1] = l;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // P.V: lane owns value pairs (2i, 2i+1), i = lane + 64r; sequential over keys.
+    const int64_t lim = qpos - key0 + 1;
+    const int nj = static_cast<int>(lim < nkeys ? (lim < 0 ? 0 : lim) : nkeys);
+    constexpr int NPAIR = (D / 2 + 63) / 64;
+#pragma unroll
+    for (int r = 0; r < NPAIR; ++r) {
+        const int pi = lane + 64 * r;
+        if (pi >= D / 2) break;
+        float o0 = 0.0f, o1 = 0.0f;
+        for (int j = 0; j < nj; ++j) {
+            const float pj = Ps[wave][j];
+            const uint32_t vv = Vs[j * VP + pi];
+            o0 = fma_(pj, lo_bf(vv), o0);
+            o1 = fma_(pj, hi_bf(vv), o1);
         }
-        __syncthreads();
-        // P.V: lane = output dim, sequential over the chunk's keys.
-        for (int i = wave; i < nb; i += 4) {
-            const int qi = qb + i;
-            const int t = qi / group;
-            const int h = kvh * group + qi % group;
-            const int64_t qpos = L - T + t;
-            const int64_t lim = qpos - key0 + 1;
-            const int nj = static_cast<int>(lim < nkeys ? (lim < 0 ? 0 : lim) : nkeys);
-            float* part = scratch + ((((static_cast<int64_t>(b) * T + t) * nq + h) * nchunk) + chunk) *
-                                        partial_stride(D);
-            for (int d = lane; d < D; d += 64) {
-                float o = 0.0f;
-                for (int j = 0; j < nj; ++j) o = fma_(Ps[i * kChunk + j], bf2f(Vs[j * D + d]), o);
-                part[2 + d] = o;
-            }
-        }
+        *reinterpret_cast<float2*>(part + 2 + 2 * pi) = make_float2(o0, o1);
     }
 }
 
+// One wave per query: chunk partials merged in chunk order against the
+// global max, then divided, gated and rounded.
 template <int D>
 __global__ __launch_bounds__(256) void gqa_combine_kernel(
     uint16_t* __restrict__ out, const float* __restrict__ scratch, const uint16_t* gate, int B, int T,
@@ -143,33 +168,51 @@ __global__ __launch_bounds__(256) void gqa_combine_kernel(
     const int64_t L = static_cast<int64_t>(lens ? lens[b] : 0) + len_add;
     const int64_t qpos = L - T + t;
     const int nch = static_cast<int>(qpos / kChunk) + 1;
-    const float* base = scratch + qidx * nchunk * partial_stride(D);
+    constexpr int64_t PS = partial_stride(D);
+    const float* base = scratch + qidx * nchunk * PS;
     float M = __uint_as_float(0xff800000u);
-    for (int c = lane; c < nch; c += 64) M = fmaxf(M, base[c * partial_stride(D)]);
+    for (int c = lane; c < nch; c += 64) M = fmaxf(M, base[c * PS]);
     M = wave_max64(M);
-    constexpr int PER = (D + 63) / 64;
+    constexpr int PER = D / 64;
     float O[PER];
 #pragma unroll
     for (int r = 0; r < PER; ++r) O[r] = 0.0f;
     float Ls = 0.0f;
-    for (int c = 0; c < nch; ++c) {
-        const float* part = base + c * partial_stride(D);
-        const float wgt = cexp(part[0] - M);
-        Ls = fma_(part[1], wgt, Ls);
+    for (int c0 = 0; c0 < nch; c0 += 64) {
+        const int nt = min(64, nch - c0);
+        float w = 0.0f, lc = 0.0f;
+        if (lane < nt) {
+            const float* part = base + (c0 + lane) * PS;
+            w = cexp(part[0] - M);
+            lc = part[1];
+        }
+        for (int cb = 0; cb < nt; cb += 8) {
+            float pv[8][PER];
 #pragma unroll
-        for (int r = 0; r < PER; ++r) {
-            const int d = lane + 64 * r;
-            if (d < D) O[r] = fma_(part[2 + d], wgt, O[r]);
+            for (int u = 0; u < 8; ++u) {
+                const int cc = min(cb + u, nt - 1);
+                const float* part = base + (c0 + cc) * PS + 2;
+#pragma unroll
+                for (int r = 0; r < PER; ++r) pv[u][r] = part[lane + 64 * r];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                if (cb + u < nt) {
+                    const float wc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), cb + u));
+                    const float lcc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lc), cb + u));
+                    Ls = fma_(lcc, wc, Ls);
+#pragma unroll
+                    for (int r = 0; r < PER; ++r) O[r] = fma_(pv[u][r], wc, O[r]);
+                }
+            }
         }
     }
 #pragma unroll
     for (int r = 0; r < PER; ++r) {
         const int d = lane + 64 * r;
-        if (d < D) {
-            float o = O[r] / Ls;
-            if (gate != nullptr) o = o * csigmoid(bf2f(gate[qidx * D + d]));
-            out[qidx * D + d] = f2bf(o);
-        }
+        float o = O[r] / Ls;
+        if (gate != nullptr) o = o * csigmoid(bf2f(gate[qidx * D + d]));
+        out[qidx * D + d] = f2bf(o);
     }
 }
 
@@ -178,8 +221,9 @@ int launch(uint16_t* out, const uint16_t* q, const uint16_t* gate, const uint16_
            int64_t cap, float* scratch, int B, int T, int nq, int nkv, const int32_t* lens, int len_add,
            int nchunk, hipStream_t s) {
     const float scale = 1.0f / __builtin_sqrtf(static_cast<float>(D));
-    gqa_partial_kernel<D><<<dim3(nchunk, nkv, B), dim3(256), 0, s>>>(scratch, q, kc, vc, cap, T, nq, nkv,
-                                                                     lens, len_add, nchunk, scale);
+    const int qgroups = (T * (nq / nkv) + kQPerBlock - 1) / kQPerBlock;
+    gqa_partial_kernel<D><<<dim3(nchunk, nkv * qgroups, B), dim3(256), 0, s>>>(
+        scratch, q, kc, vc, cap, T, nq, nkv, lens, len_add, nchunk, scale);
     int rc = launched("gqa_partial_kernel");
     if (rc != HAI_OK) return rc;
     const int64_t nqry = static_cast<int64_t>(B) * T * nq;

@@ -3,12 +3,18 @@
 // (deltanet_recurrent_kernel, :985-1095) + gated RMSNorm, over the T tokens
 // of a verify step.
 //
-// One block per (value head, sequence), 4 threads per state column:
+// One block per (value head, sequence), 4 threads per state column.  Every
+// global load of the step (state, conv history, taps and inputs, gates, z) is
+// issued before the first use, and the token loop has no block barrier: the
+// q/k norms of all T tokens are computed first and the gated RMSNorm of all
+// outputs last.
 //   * thread (j, g) keeps the dk/4 state entries S[g*dk/4 .. ][j] of column j
 //     in registers for all T tokens; the key-dim reductions are fma chains
 //     within the group followed by a 4-lane xor butterfly, (g0+g1)+(g2+g3);
-//   * the state is stored value-major [dv][dk] so the 4 threads of a column
-//     read and write 512 contiguous bytes;
+//   * the state of a head is stored column-tiled: entry (key i, column j),
+//     i = g*dk/4 + 4m + e, sits at float ((m*dv + j)*4 + g)*4 + e, so load or
+//     store m of thread (j, g) = tid is float4 number m*4*dv + tid and every
+//     instruction of the block covers one contiguous span;
 //   * rollback needs no copies: the state after sequence length L is kept in
 //     slot L % nslots and the conv inputs in a ring indexed by position, so
 //     accepting a prefix only moves the committed length.
@@ -21,6 +27,9 @@ namespace {
 
 using namespace hai;
 
+constexpr int kMaxT = 16;   // tokens per launch (verify width k + 1 <= 16)
+constexpr int kMaxKc = 8;   // conv taps
+
 template <int DK, int DV>
 __global__ __launch_bounds__(DV * 4) void deltanet_verify_kernel(
     uint16_t* __restrict__ out, int64_t ld_out, const uint16_t* __restrict__ proj, int64_t ld_proj,
@@ -30,14 +39,15 @@ __global__ __launch_bounds__(DV * 4) void deltanet_verify_kernel(
     const uint16_t* __restrict__ norm_w, const int32_t* lens, int pos_add, int B, int T, int nk, int nv,
     int Kc, float eps) {
     constexpr int NT = DV * 4;
-    constexpr int GI = DK / 4;  // key dims per thread
+    constexpr int NW = NT / 64;
+    constexpr int GI = DK / 4;            // key dims per thread
+    constexpr int ZP = kMaxT * DV / NT;   // output elements per thread (all tokens)
     extern __shared__ float smem[];
-    float* qs = smem;                  // [T][DK]
-    float* ks = qs + T * DK;           // [T][DK]
-    float* vs = ks + T * DK;           // [T][DV]
-    __shared__ float osh[DV];
-    __shared__ float sc[4];            // q scale, k scale, decay, beta
-    __shared__ float rms_sh;
+    float* qs = smem;                  // [T][DK] conv output, q channels
+    float* ks = qs + T * DK;           // [T][DK] k channels
+    float* vs = ks + T * DK;           // [T][DV] v channels
+    float* os = vs + T * DV;           // [T][DV] unrounded recurrent output
+    __shared__ float s_q[kMaxT], s_k[kMaxT], s_decay[kMaxT], s_beta[kMaxT], s_rms[kMaxT];
 
     const int h = blockIdx.x;
     const int b = blockIdx.y;
@@ -53,75 +63,120 @@ __global__ __launch_bounds__(DV * 4) void deltanet_verify_kernel(
     const int64_t C = 2 * kw + vw;
     const int64_t p0 = static_cast<int64_t>(lens ? lens[b] : 0) + pos_add;
     const int hist = Kc - 1;
+    const int64_t row0 = static_cast<int64_t>(b) * T;
 
-    // ---- grouped causal conv + SiLU for this head's q, k and v channels ----
-    for (int cl = tid; cl < 2 * DK + DV; cl += NT) {
-        int64_t c;
-        float* dst;
-        int di;
-        int dstride;
-        if (cl < DK) { c = static_cast<int64_t>(gq) * DK + cl; dst = qs; di = cl; dstride = DK; }
-        else if (cl < 2 * DK) { c = kw + static_cast<int64_t>(gq) * DK + (cl - DK); dst = ks; di = cl - DK; dstride = DK; }
-        else { c = 2 * kw + static_cast<int64_t>(h) * DV + (cl - 2 * DK); dst = vs; di = cl - 2 * DK; dstride = DV; }
-        float win[8];  // history window (Kc <= 8)
-        for (int i = 0; i < hist; ++i) {
-            const int64_t pos = p0 - hist + i;
-            win[i] = pos < 0 ? 0.0f
-                             : bf2f(ring[(static_cast<int64_t>(b) * ring_n + (pos % ring_n)) * C + c]);
-        }
-        float wc[8];
-        for (int i = 0; i < Kc; ++i) wc[i] = bf2f(conv_w[c * Kc + i]);
-        const bool writer = cl >= 2 * DK || (h % group) == 0;
-        for (int t = 0; t < T; ++t) {
-            const uint16_t xb = proj[(static_cast<int64_t>(b) * T + t) * ld_proj + off_qkv + c];
-            const float x = bf2f(xb);
-            float acc;
-            if (hist > 0) {
-                acc = win[0] * wc[0];
-                for (int i = 1; i < hist; ++i) acc = fma_(win[i], wc[i], acc);
-                acc = fma_(x, wc[hist], acc);
-            } else {
-                acc = x * wc[0];
-            }
-            dst[t * dstride + di] = bfr(csilu(acc));
-            for (int i = 0; i + 1 < hist; ++i) win[i] = win[i + 1];
-            if (hist > 0) win[hist - 1] = x;
-            if (writer) ring[(static_cast<int64_t>(b) * ring_n + ((p0 + t) % ring_n)) * C + c] = xb;
-        }
-    }
-
-    // ---- load the committed state (slot p0 % nslots) ----
+    // ---- issue every global load of the step up front ----
+    // committed state (slot p0 % nslots), column j, key dims [g*GI, g*GI+GI)
     float S[GI];
     {
         const int64_t slot = p0 % nslots;
-        const float* src = state + (((slot * B + b) * nv + h) * static_cast<int64_t>(DV) + j) * DK + g * GI;
+        const float4* src = reinterpret_cast<const float4*>(state + ((slot * B + b) * nv + h) * static_cast<int64_t>(DV) * DK) + tid;
 #pragma unroll
-        for (int i = 0; i < GI; i += 4) {
-            const float4 v4 = *reinterpret_cast<const float4*>(src + i);
-            S[i] = v4.x; S[i + 1] = v4.y; S[i + 2] = v4.z; S[i + 3] = v4.w;
+        for (int m = 0; m < GI / 4; ++m) {
+            const float4 v4 = src[m * NT];
+            S[4 * m] = v4.x; S[4 * m + 1] = v4.y; S[4 * m + 2] = v4.z; S[4 * m + 3] = v4.w;
+        }
+    }
+    // conv channel of this thread: [0, DK) q, [DK, 2DK) k, [2DK, 2DK+DV) v
+    const int cl = tid;
+    const bool has_ch = cl < 2 * DK + DV;
+    int64_t c = 0;
+    if (cl < DK) c = static_cast<int64_t>(gq) * DK + cl;
+    else if (cl < 2 * DK) c = kw + static_cast<int64_t>(gq) * DK + (cl - DK);
+    else c = 2 * kw + static_cast<int64_t>(h) * DV + (cl - 2 * DK);
+    // window: vals[i] = input at position p0 - hist + i (history, then the T new tokens)
+    uint16_t vals[kMaxT + kMaxKc - 1];
+    float wc[kMaxKc];
+    if (has_ch) {
+#pragma unroll
+        for (int i = 0; i < kMaxKc - 1; ++i) {
+            const int64_t pos = p0 - hist + i;
+            vals[i] = (i < hist && pos >= 0)
+                          ? ring[(static_cast<int64_t>(b) * ring_n + (pos % ring_n)) * C + c]
+                          : uint16_t{0};
+        }
+#pragma unroll
+        for (int i = 0; i < kMaxKc; ++i) wc[i] = i < Kc ? bf2f(conv_w[c * Kc + i]) : 0.0f;
+#pragma unroll
+        for (int t = 0; t < kMaxT; ++t) {
+            uint16_t x = 0;
+            if (t < T) x = proj[(row0 + t) * ld_proj + off_qkv + c];
+            // shift the new tokens in right after the hist history entries
+#pragma unroll
+            for (int hh = 0; hh < kMaxKc; ++hh)
+                if (hh == hist) vals[t + hh] = x;
+        }
+    }
+    // per-token gate scalars (last wave, lane = token)
+    float a_in = 0.0f, b_in = 0.0f, dtb = 0.0f, alog = 0.0f;
+    const bool scal = wave == NW - 1 && lane < T;
+    if (scal) {
+        a_in = bf2f(proj[(row0 + lane) * ld_proj + off_a + h]);
+        b_in = bf2f(proj[(row0 + lane) * ld_proj + off_b + h]);
+        dtb = bf2f(dt_bias[h]);
+        alog = bf2f(a_log[h]);
+    }
+    // gate z and norm weight for the output elements (t, jo) = (tid / DV + r * NT / DV, tid % DV)
+    const int jo = tid % DV;
+    float zr[ZP];
+#pragma unroll
+    for (int r = 0; r < ZP; ++r) {
+        const int t = tid / DV + r * (NT / DV);
+        zr[r] = t < T ? bf2f(proj[(row0 + t) * ld_proj + off_z + static_cast<int64_t>(h) * DV + jo]) : 0.0f;
+    }
+    const float nwj = bf2f(norm_w[jo]);
+
+    // ---- grouped causal conv + SiLU ----
+    if (has_ch) {
+        float* dst;
+        int di, dstride;
+        if (cl < DK) { dst = qs; di = cl; dstride = DK; }
+        else if (cl < 2 * DK) { dst = ks; di = cl - DK; dstride = DK; }
+        else { dst = vs; di = cl - 2 * DK; dstride = DV; }
+        const bool writer = cl >= 2 * DK || (h % group) == 0;
+#pragma unroll
+        for (int t = 0; t < kMaxT; ++t) {
+            if (t < T) {
+                float acc = bf2f(vals[t]) * wc[0];
+#pragma unroll
+                for (int i = 1; i < kMaxKc; ++i)
+                    if (i < Kc) acc = fma_(bf2f(vals[t + i]), wc[i], acc);
+                dst[t * dstride + di] = bfr(csilu(acc));
+                if (writer) {
+                    uint16_t xv = 0;
+#pragma unroll
+                    for (int hh = 0; hh < kMaxKc; ++hh)
+                        if (hh == hist) xv = vals[t + hh];
+                    ring[(static_cast<int64_t>(b) * ring_n + ((p0 + t) % ring_n)) * C + c] = xv;
+                }
+            }
+        }
+    }
+    if (scal) {
+        const float dtv = dtb + a_in;
+        const float sp = fmaxf(dtv, 0.0f) + clog1p(cexp(-fabsf(dtv)));
+        s_decay[lane] = cexp(-(cexp(alog) * sp));
+        s_beta[lane] = csigmoid(b_in);
+    }
+    __syncthreads();
+
+    // ---- L2 norms of q and k for every token (one wave per vector) ----
+    const float rs_dk = 1.0f / csqrt(static_cast<float>(DK));
+    for (int task = wave; task < 2 * T; task += NW) {
+        const int t = task >> 1;
+        if ((task & 1) == 0) {
+            const float ssq = l64_sumsq_f32(qs + t * DK, DK, lane);
+            if (lane == 0) s_q[t] = (1.0f / csqrt(ssq + 1.0e-6f)) * rs_dk;
+        } else {
+            const float ssk = l64_sumsq_f32(ks + t * DK, DK, lane);
+            if (lane == 0) s_k[t] = 1.0f / csqrt(ssk + 1.0e-6f);
         }
     }
     __syncthreads();
 
-    const float rs_dk = 1.0f / csqrt(static_cast<float>(DK));
+    // ---- gated delta rule, token by token (column-local: no block barrier) ----
     for (int t = 0; t < T; ++t) {
-        const int64_t row = static_cast<int64_t>(b) * T + t;
-        if (wave == 0) {
-            const float ssq = l64_sumsq_f32(qs + t * DK, DK, lane);
-            if (lane == 0) sc[0] = (1.0f / csqrt(ssq + 1.0e-6f)) * rs_dk;
-        } else if (wave == 1) {
-            const float ssk = l64_sumsq_f32(ks + t * DK, DK, lane);
-            if (lane == 0) sc[1] = 1.0f / csqrt(ssk + 1.0e-6f);
-        } else if (wave == 2 && lane == 0) {
-            const float av = bf2f(proj[row * ld_proj + off_a + h]);
-            const float bv = bf2f(proj[row * ld_proj + off_b + h]);
-            const float dtv = bf2f(dt_bias[h]) + av;
-            const float sp = fmaxf(dtv, 0.0f) + clog1p(cexp(-fabsf(dtv)));
-            sc[2] = cexp(-(cexp(bf2f(a_log[h])) * sp));
-            sc[3] = csigmoid(bv);
-        }
-        __syncthreads();
-        const float qsc = sc[0], ksc = sc[1], decay = sc[2], beta = sc[3];
+        const float qsc = s_q[t], ksc = s_k[t], decay = s_decay[t], beta = s_beta[t];
         const float* qt = qs + t * DK + g * GI;
         const float* kt = ks + t * DK + g * GI;
         float r = 0.0f;
@@ -143,25 +198,29 @@ __global__ __launch_bounds__(DV * 4) void deltanet_verify_kernel(
         o = o + __shfl_xor(o, 2, 64);
         if (write_all || t == T - 1) {
             const int64_t slot = (p0 + t + 1) % nslots;
-            float* dstp = state + (((slot * B + b) * nv + h) * static_cast<int64_t>(DV) + j) * DK + g * GI;
+            float4* dstp = reinterpret_cast<float4*>(state + ((slot * B + b) * nv + h) * static_cast<int64_t>(DV) * DK) + tid;
 #pragma unroll
-            for (int i = 0; i < GI; i += 4)
-                *reinterpret_cast<float4*>(dstp + i) = make_float4(S[i], S[i + 1], S[i + 2], S[i + 3]);
+            for (int m = 0; m < GI / 4; ++m)
+                dstp[m * NT] = make_float4(S[4 * m], S[4 * m + 1], S[4 * m + 2], S[4 * m + 3]);
         }
-        if (g == 0) osh[j] = o;
-        __syncthreads();
-        if (wave == 0) {
-            const float sso = l64_sumsq_f32(osh, DV, lane);
-            if (lane == 0) rms_sh = 1.0f / csqrt(sso / static_cast<float>(DV) + eps);
+        if (g == 0) os[t * DV + j] = o;
+    }
+    __syncthreads();
+
+    // ---- gated RMSNorm: rms from the unrounded output, one wave per token ----
+    for (int t = wave; t < T; t += NW) {
+        const float sso = l64_sumsq_f32(os + t * DV, DV, lane);
+        if (lane == 0) s_rms[t] = 1.0f / csqrt(sso / static_cast<float>(DV) + eps);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < ZP; ++r) {
+        const int t = tid / DV + r * (NT / DV);
+        if (t < T) {
+            const float ob = bfr(os[t * DV + jo]);
+            out[(row0 + t) * ld_out + static_cast<int64_t>(h) * DV + jo] =
+                f2bf(((ob * s_rms[t]) * nwj) * csilu(zr[r]));
         }
-        __syncthreads();
-        if (g == 0) {
-            const float ob = bfr(o);
-            const float z = bf2f(proj[row * ld_proj + off_z + static_cast<int64_t>(h) * DV + j]);
-            out[row * ld_out + static_cast<int64_t>(h) * DV + j] =
-                f2bf(((ob * rms_sh) * bf2f(norm_w[j])) * csilu(z));
-        }
-        __syncthreads();
     }
 }
 
@@ -171,7 +230,7 @@ int launch(uint16_t* out, int64_t ld_out, const uint16_t* proj, int64_t ld_proj,
            float* state, int nslots, int write_all, const uint16_t* a_log, const uint16_t* dt_bias,
            const uint16_t* norm_w, const int32_t* lens, int pos_add, int B, int T, int nk, int nv, int Kc,
            float eps, hipStream_t s) {
-    const size_t shmem = static_cast<size_t>(T) * (2 * DK + DV) * sizeof(float);
+    const size_t shmem = static_cast<size_t>(T) * (2 * DK + 2 * DV) * sizeof(float);
     deltanet_verify_kernel<DK, DV><<<dim3(nv, B), dim3(DV * 4), shmem, s>>>(
         out, ld_out, proj, ld_proj, off_qkv, off_z, off_a, off_b, conv_w, ring, ring_n, state, nslots,
         write_all, a_log, dt_bias, norm_w, lens, pos_add, B, T, nk, nv, Kc, eps);
@@ -197,7 +256,7 @@ extern "C" int hai_deltanet_verify_bf16(void* out, int64_t ld_out, const void* p
     if (lens == nullptr && pos_add < 0) return invalid("deltanet_verify: negative position");
     if (!aligned16(state)) return invalid("deltanet_verify: state alignment");
     if (B == 0 || T == 0) return HAI_OK;
-    if (T * (2 * dk + dv) * 4 > 64 * 1024) return invalid("deltanet_verify: T too large for LDS staging");
+    if (T > kMaxT) return invalid("deltanet_verify: at most 16 tokens per launch");
     const auto s = as_stream(stream);
     auto* o = static_cast<uint16_t*>(out);
     const auto* pr = static_cast<const uint16_t*>(proj);
