@@ -83,6 +83,21 @@ enum { HAI_EPI_STORE = 0, HAI_EPI_RESIDUAL = 1, HAI_EPI_SILU_MUL = 2 };
 int hai_gemm_bf16(void* y, int64_t ldy, const void* x, int64_t ldx,
                   const void* w, int64_t M, int64_t N, int64_t K, int epilogue,
                   const void* res, int64_t ld_res, void* stream);
+/* The model's RMSNorm followed by a linear layer in one launch: the
+ * qwen_rmsnorm_reference -> Linear pair of qwen_reference.cc:108-119 and
+ * linear.cc:117-179 (the input / post-attention norms before the first
+ * projection of every sub-layer, and the final norm before lm_head).
+ * y = epilogue(rmsnorm(x; norm_w, eps, unit_offset) . W^T), bit-identical to
+ * hai_rmsnorm_bf16 then hai_gemm_bf16.  xn_out, if not null, also receives
+ * the normalised rows (ld_xn).  When M * K exceeds
+ * HAI_GEMM_RMSNORM_FUSED_MAX the rows do not fit the on-chip prologue: the
+ * call then runs the two kernels and needs xn_out as their intermediate. */
+#define HAI_GEMM_RMSNORM_FUSED_MAX 16384
+int hai_gemm_rmsnorm_bf16(void* y, int64_t ldy, const void* x, int64_t ldx,
+                          const void* norm_w, float eps, int unit_offset,
+                          void* xn_out, int64_t ld_xn, const void* w,
+                          int64_t M, int64_t N, int64_t K, int epilogue,
+                          const void* res, int64_t ld_res, void* stream);
 
 /* ------------------------------------------------------------------ norms
  * rmsnorm_kernel (hip_kernels.hip:105-137): y = x * inv * (w + offset),

@@ -120,6 +120,47 @@ def test_gemm_rejects_bad_shapes():
     assert kern().hai_gemm_bf16(d.ptr, 4, d.ptr, 8, d.ptr, 17, 4, 8, 0, None, 0, None) == 1   # M > 16
 
 
+@pytest.mark.parametrize("M,N,K_,epi", [(1, 4096, 256, 0), (2, 16480, 5120, 0), (2, 17408, 5120, 2),
+                                        (3, 520, 5120, 1), (16, 300, 1024, 0), (2, 77, 1000, 0),
+                                        (4, 64, 5120, 0), (8, 512, 2048, 2)])
+@pytest.mark.parametrize("with_xn", [False, True])
+def test_gemm_rmsnorm_fused(M, N, K_, epi, with_xn):
+    """hai_gemm_rmsnorm_bf16 == rmsnorm then gemm, on both sides of the fused
+    limit (M*K <= 16384 runs the LDS prologue, above it the two kernels)."""
+    rng = np.random.default_rng(31 + M * 7 + N + K_ + epi)
+    x, xb = rand_bf16(rng, (M, K_))
+    nw, nwb = rand_bf16(rng, (K_,), 0.02)
+    w, wb = rand_bf16(rng, (N, K_), 0.05)
+    xn_want = orc.rmsnorm(x, nw, 1e-6, True)
+    y_lin = orc.gemm(xn_want, w)
+    ncols = N // 2 if epi == hai.EPI_SILU_MUL else N
+    need_xn = with_xn or M * K_ > 16384
+    dx, dnw, dw = dev(xb), dev(nwb), dev(wb)
+    dxn = out_buf(M * K_ * 2) if need_xn else None
+    h, hb = rand_bf16(rng, (M, ncols))
+    dy = dev(hb) if epi == hai.EPI_RESIDUAL else out_buf(M * ncols * 2)
+    hai.check(kern().hai_gemm_rmsnorm_bf16(dy.ptr, ncols, dx.ptr, K_, dnw.ptr, 1e-6, 1,
+                                           dxn.ptr if dxn else None, K_, dw.ptr, M, N, K_, epi,
+                                           dy.ptr if epi == hai.EPI_RESIDUAL else None, ncols, None),
+              "gemm_rmsnorm")
+    if epi == hai.EPI_STORE:
+        want = y_lin
+    elif epi == hai.EPI_RESIDUAL:
+        want = orc.add(h, y_lin)
+    else:
+        want = orc.silu_mul(y_lin[:, 0::2], y_lin[:, 1::2])
+    assert_bits_equal(dy.download(np.uint16), want, f"gemm_rmsnorm {M}x{N}x{K_} epi {epi}")
+    if dxn is not None:
+        assert_bits_equal(dxn.download(np.uint16), xn_want, "normalised rows")
+
+
+def test_gemm_rmsnorm_needs_xn_above_fused_limit():
+    d = out_buf(1 << 16)
+    # M*K = 4*5120 > 16384 without an xn_out buffer
+    assert kern().hai_gemm_rmsnorm_bf16(d.ptr, 8, d.ptr, 5120, d.ptr, 1e-6, 1, None, 0, d.ptr, 4, 8, 5120, 0,
+                                        None, 0, None) == 1
+
+
 # ----------------------------------------------------------------- norms
 @pytest.mark.parametrize("rows,H", [(1, 256), (5, 256), (2, 5120), (3, 64)])
 def test_rmsnorm(rows, H):

@@ -56,6 +56,8 @@ _KERNEL_SIGS = {
     "hai_graph_launch": [VP, VP],
     "hai_graph_destroy": [VP],
     "hai_gemm_bf16": [VP, I64, VP, I64, VP, I64, I64, I64, ctypes.c_int, VP, I64, VP],
+    "hai_gemm_rmsnorm_bf16": [VP, I64, VP, I64, VP, F32, ctypes.c_int, VP, I64, VP, I64, I64, I64, ctypes.c_int,
+                              VP, I64, VP],
     "hai_rmsnorm_bf16": [VP, I64, VP, I64, VP, I64, I64, F32, ctypes.c_int, VP],
     "hai_add_bf16": [VP, VP, VP, I64, VP],
     "hai_silu_mul_bf16": [VP, VP, VP, I64, VP],
@@ -70,6 +72,7 @@ _KERNEL_SIGS = {
                                  VP, VP, I32, I64, I64, I64, I64, I64, I64, I64, F32, VP],
     "hai_argmax_rows_bf16": [VP, VP, I64, I64, I64, VP, VP],
     "hai_verify_argmax_accept_bf16": [VP, I64, VP, I64, VP, VP, I64, I64, VP, VP, VP, VP, VP, VP, VP, VP, VP],
+    "hai_add_i32": [VP, VP, I32, I64, VP],
     "hai_fill_synthetic_bf16": [VP, I64, I64, I64, ctypes.c_uint64, ctypes.c_uint32, F32, VP],
     "hai_debug_math_f32": [VP, VP, I64, ctypes.c_int, VP],
 }

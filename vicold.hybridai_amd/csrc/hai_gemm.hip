@@ -20,148 +20,291 @@
 #include "hai_common.h"
 #include "hai_device.h"
 
+#include <mutex>
+#include <vector>
+
 namespace {
 
 using namespace hai;
 
-template <int MB, int RW, int U, int EPI>
+// Optional RMSNorm prologue (NORM): the block stages its M activation rows
+// in LDS, reduces each row's sum of squares in L64 order, and normalises in
+// place, y_k = bf16((x_k * inv) * (w_k + off)), exactly as rmsnorm_kernel;
+// the main loop then reads x from LDS.  Needs M * K <= kNormMaxElems.
+struct NormArgs {
+    const uint16_t* w = nullptr;  // norm weight [K]
+    float eps = 0.0f;
+    float off = 0.0f;             // 1 for the (w + 1) model norms
+    uint16_t* xn = nullptr;       // optional copy of the normalised rows (block 0 writes it)
+    int64_t ldxn = 0;
+};
+
+constexpr int kNormMaxElems = HAI_GEMM_RMSNORM_FUSED_MAX;  // M * K: 32 KB of LDS
+
+template <int MB, int RW, int U, int EPI, bool NORM>
 __global__ __launch_bounds__(256) void gemm_bf16_kernel(
     uint16_t* __restrict__ y, int64_t ldy, const uint16_t* __restrict__ x, int64_t ldx,
-    const uint16_t* __restrict__ w, const uint16_t* res, int64_t ldres, int M, int N, int K) {
+    const uint16_t* __restrict__ w, const uint16_t* res, int64_t ldres, int M, int N, int K, NormArgs na) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * 4 + wave) * RW;
-    if (row0 >= N) return;
-    const int nrows = static_cast<int>(min(static_cast<int64_t>(RW), static_cast<int64_t>(N) - row0));
+    extern __shared__ u32x4 xs[];  // NORM: [M][K/8] normalised rows
+    const int npr = K >> 3;        // 16-byte pieces per row
+    if constexpr (NORM) {
+        // Raw rows and the norm weight are fetched together (one latency), the
+        // rows parked in LDS while one wave per row reduces its sum of squares.
+        __shared__ float inv_sh[16];
+        const int total = M * npr;
+        for (int e0 = 0; e0 < total; e0 += 1024) {
+            u32x4 xr[4], wr[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int e = e0 + threadIdx.x + 256 * i;
+                const int r = e / npr;
+                const int p = e - r * npr;
+                if (e < total) xr[i] = *reinterpret_cast<const u32x4*>(x + r * ldx + p * 8);
+                if (e < npr) wr[i] = *reinterpret_cast<const u32x4*>(na.w + p * 8);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int e = e0 + threadIdx.x + 256 * i;
+                if (e < total) xs[e] = xr[i];
+                if (e < npr) xs[total + e] = wr[i];  // norm weight staged once, behind the rows
+            }
+        }
+        __syncthreads();
+        for (int r = wave; r < M; r += 4) {
+            float acc = 0.0f;
+            for (int p = lane; p < npr; p += 64) {
+                const u32x4 d = xs[r * npr + p];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const float a = lo_bf(d[q]);
+                    const float b = hi_bf(d[q]);
+                    acc = fma_(a, a, acc);
+                    acc = fma_(b, b, acc);
+                }
+            }
+            const float ss = wave_sum64(acc);
+            if (lane == 0) inv_sh[r] = 1.0f / csqrt(ss / static_cast<float>(K) + na.eps);
+        }
+        __syncthreads();
+        for (int e = threadIdx.x; e < total; e += 256) {
+            const int r = e / npr;
+            const int p = e - r * npr;
+            const float inv = inv_sh[r];
+            const u32x4 xv0 = xs[e];
+            const u32x4 wv0 = xs[total + p];
+            u32x4 o;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint16_t a = f2bf((lo_bf(xv0[q]) * inv) * (lo_bf(wv0[q]) + na.off));
+                const uint16_t b = f2bf((hi_bf(xv0[q]) * inv) * (hi_bf(wv0[q]) + na.off));
+                o[q] = static_cast<uint32_t>(a) | (static_cast<uint32_t>(b) << 16);
+            }
+            xs[e] = o;
+            if (na.xn != nullptr && blockIdx.x == 0)
+                *reinterpret_cast<u32x4*>(na.xn + r * na.ldxn + p * 8) = o;
+        }
+        __syncthreads();
+    }
 
     // Byte offsets fit 32 bits: the caller bounds N*K*2 and M*ldx*2 below 4 GiB.
     const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, static_cast<uint32_t>(static_cast<int64_t>(N) * K * 2));
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, static_cast<uint32_t>(static_cast<int64_t>(M) * ldx * 2));
-    uint32_t woff[RW], xoff[MB];
-#pragma unroll
-    for (int r = 0; r < RW; ++r)
-        woff[r] = static_cast<uint32_t>(((row0 + r) * static_cast<int64_t>(K) + lane * 8) * 2);
+    uint32_t xoff[MB];
 #pragma unroll
     for (int m = 0; m < MB; ++m) xoff[m] = static_cast<uint32_t>((static_cast<int64_t>(m) * ldx + lane * 8) * 2);
-
-    float acc[RW][MB];
-#pragma unroll
-    for (int r = 0; r < RW; ++r)
-#pragma unroll
-        for (int m = 0; m < MB; ++m) acc[r][m] = 0.0f;
-
-    auto body = [&](const u32x4 (&wv)[RW], const u32x4 (&xv)[MB]) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            float xa[MB], xb[MB];
-#pragma unroll
-            for (int m = 0; m < MB; ++m) {
-                xa[m] = lo_bf(xv[m][q]);
-                xb[m] = hi_bf(xv[m][q]);
-            }
-#pragma unroll
-            for (int r = 0; r < RW; ++r) {
-                const float wa = lo_bf(wv[r][q]);
-                const float wb = hi_bf(wv[r][q]);
-#pragma unroll
-                for (int m = 0; m < MB; ++m) {
-                    acc[r][m] = fma_(xa[m], wa, acc[r][m]);
-                    acc[r][m] = fma_(xb[m], wb, acc[r][m]);
-                }
-            }
-        }
-    };
-
-    // Groups of U chunks.  A chunk past K (ragged tail or group padding)
-    // reads zeros through an out-of-range offset; fma(0, 0, acc) == acc
-    // because acc is never -0 (it starts at +0 and round-to-nearest only
-    // produces -0 from (-0) + (-0)), so padding does not change a bit.
     const int nck = (K + 511) / 512;
     const int nfull = K / 512;
-    for (int c0 = 0; c0 < nck; c0 += U) {
-        u32x4 wv[U][RW];
-        u32x4 xv[U][MB];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int c = c0 + u;
-            // full chunk: every lane valid; ragged chunk: lanes past K masked
-            const bool ok = c < nfull || (c < nck && c * 512 + lane * 8 < K);
-            const uint32_t so = ok ? static_cast<uint32_t>(c) * 1024u : 0u;
-#pragma unroll
-            for (int r = 0; r < RW; ++r) wv[u][r] = bload(rw, ok ? woff[r] : kOutOfRange, so);
-#pragma unroll
-            for (int m = 0; m < MB; ++m) xv[u][m] = bload(rx, ok ? xoff[m] : kOutOfRange, so);
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) body(wv[u], xv[u]);
-    }
 
+    // Row groups (4 waves x RW rows) strided over the grid; the plain kernel
+    // is launched with one block per group, the NORM kernel with a grid sized
+    // to the machine so that the prologue is paid once per resident block.
+    const int64_t ngroups = (static_cast<int64_t>(N) + 4 * RW - 1) / (4 * RW);
+    for (int64_t grp = blockIdx.x; grp < ngroups; grp += gridDim.x) {
+        const int64_t row0 = (grp * 4 + wave) * RW;
+        if (row0 >= N) continue;
+        const int nrows = static_cast<int>(min(static_cast<int64_t>(RW), static_cast<int64_t>(N) - row0));
+        uint32_t woff[RW];
 #pragma unroll
-    for (int r = 0; r < RW; ++r)
-#pragma unroll
-        for (int m = 0; m < MB; ++m) acc[r][m] = wave_sum64(acc[r][m]);
+        for (int r = 0; r < RW; ++r)
+            woff[r] = static_cast<uint32_t>(((row0 + r) * static_cast<int64_t>(K) + lane * 8) * 2);
 
-    if (EPI == HAI_EPI_SILU_MUL) {
-        // rows (2p, 2p+1) = (gate_f, up_f), output column f = row0/2 + p.
-#pragma unroll
-        for (int p = 0; p < RW / 2; ++p)
-#pragma unroll
-            for (int m = 0; m < MB; ++m) {
-                if (lane == p * MB + m && m < M && 2 * p + 1 < nrows) {
-                    const float g = bfr(acc[2 * p][m]);
-                    const float u = bfr(acc[2 * p + 1][m]);
-                    y[static_cast<int64_t>(m) * ldy + row0 / 2 + p] = f2bf(csilu(g) * u);
-                }
-            }
-    } else {
+        float acc[RW][MB];
 #pragma unroll
         for (int r = 0; r < RW; ++r)
 #pragma unroll
-            for (int m = 0; m < MB; ++m) {
-                if (lane == r * MB + m && m < M && r < nrows) {
-                    const int64_t n = row0 + r;
-                    float v = bfr(acc[r][m]);
-                    if (EPI == HAI_EPI_RESIDUAL) v = bf2f(res[static_cast<int64_t>(m) * ldres + n]) + v;
-                    y[static_cast<int64_t>(m) * ldy + n] = f2bf(v);
+            for (int m = 0; m < MB; ++m) acc[r][m] = 0.0f;
+
+        auto body = [&](const u32x4 (&wv)[RW], const u32x4 (&xv)[MB]) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                float xa[MB], xb[MB];
+#pragma unroll
+                for (int m = 0; m < MB; ++m) {
+                    xa[m] = lo_bf(xv[m][q]);
+                    xb[m] = hi_bf(xv[m][q]);
+                }
+#pragma unroll
+                for (int r = 0; r < RW; ++r) {
+                    const float wa = lo_bf(wv[r][q]);
+                    const float wb = hi_bf(wv[r][q]);
+#pragma unroll
+                    for (int m = 0; m < MB; ++m) {
+                        acc[r][m] = fma_(xa[m], wa, acc[r][m]);
+                        acc[r][m] = fma_(xb[m], wb, acc[r][m]);
+                    }
                 }
             }
+        };
+
+        // Groups of U chunks.  A chunk past K (ragged tail or group padding)
+        // reads zeros through an out-of-range offset; fma(0, 0, acc) == acc
+        // because acc is never -0 (it starts at +0 and round-to-nearest only
+        // produces -0 from (-0) + (-0)), so padding does not change a bit.
+        for (int c0 = 0; c0 < nck; c0 += U) {
+            u32x4 wv[U][RW];
+            u32x4 xv[U][MB];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int c = c0 + u;
+                // full chunk: every lane valid; ragged chunk: lanes past K masked
+                const bool ok = c < nfull || (c < nck && c * 512 + lane * 8 < K);
+                const uint32_t so = ok ? static_cast<uint32_t>(c) * 1024u : 0u;
+#pragma unroll
+                for (int r = 0; r < RW; ++r) wv[u][r] = bload(rw, ok ? woff[r] : kOutOfRange, so);
+#pragma unroll
+                for (int m = 0; m < MB; ++m) {
+                    if constexpr (NORM)
+                        xv[u][m] = (ok && m < M) ? xs[m * npr + c * 64 + lane] : u32x4{0u, 0u, 0u, 0u};
+                    else
+                        xv[u][m] = bload(rx, ok ? xoff[m] : kOutOfRange, so);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) body(wv[u], xv[u]);
+        }
+
+#pragma unroll
+        for (int r = 0; r < RW; ++r)
+#pragma unroll
+            for (int m = 0; m < MB; ++m) acc[r][m] = wave_sum64(acc[r][m]);
+
+        if (EPI == HAI_EPI_SILU_MUL) {
+            // rows (2p, 2p+1) = (gate_f, up_f), output column f = row0/2 + p.
+#pragma unroll
+            for (int p = 0; p < RW / 2; ++p)
+#pragma unroll
+                for (int m = 0; m < MB; ++m) {
+                    if (lane == p * MB + m && m < M && 2 * p + 1 < nrows) {
+                        const float g = bfr(acc[2 * p][m]);
+                        const float u = bfr(acc[2 * p + 1][m]);
+                        y[static_cast<int64_t>(m) * ldy + row0 / 2 + p] = f2bf(csilu(g) * u);
+                    }
+                }
+        } else {
+#pragma unroll
+            for (int r = 0; r < RW; ++r)
+#pragma unroll
+                for (int m = 0; m < MB; ++m) {
+                    if (lane == r * MB + m && m < M && r < nrows) {
+                        const int64_t n = row0 + r;
+                        float v = bfr(acc[r][m]);
+                        if (EPI == HAI_EPI_RESIDUAL) v = bf2f(res[static_cast<int64_t>(m) * ldres + n]) + v;
+                        y[static_cast<int64_t>(m) * ldy + n] = f2bf(v);
+                    }
+                }
+        }
     }
 }
 
-template <int MB, int RW, int EPI>
-void launch_gemm(uint16_t* y, int64_t ldy, const uint16_t* x, int64_t ldx, const uint16_t* w,
-                 const uint16_t* res, int64_t ldres, int M, int N, int K, hipStream_t s) {
-    constexpr int U = MB <= 2 ? 4 : (MB <= 8 ? 2 : 1);
-    const int64_t waves = (static_cast<int64_t>(N) + RW - 1) / RW;
-    const unsigned blocks = static_cast<unsigned>((waves + 3) / 4);
-    gemm_bf16_kernel<MB, RW, U, EPI><<<dim3(blocks), dim3(256), 0, s>>>(y, ldy, x, ldx, w, res, ldres, M,
-                                                                        N, K);
+struct GemmArgs {
+    uint16_t* y;
+    int64_t ldy;
+    const uint16_t* x;
+    int64_t ldx;
+    const uint16_t* w;
+    const uint16_t* res;
+    int64_t ldres;
+    int M, N, K;
+    NormArgs na;
+};
+
+// Resident blocks per CU of one NORM instance at the given LDS size, and
+// the CU count, queried once per (device, instance, size).
+template <typename Kern>
+int64_t resident_blocks(Kern kern, size_t shmem) {
+    struct Entry {
+        int dev;
+        size_t shmem;
+        int64_t blocks;
+    };
+    static std::mutex mu;
+    static std::vector<Entry> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    std::lock_guard<std::mutex> lock(mu);
+    for (const auto& e : cache)
+        if (e.dev == dev && e.shmem == shmem) return e.blocks;
+    int per_cu = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 256, shmem) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return 0;
+    const int64_t blocks = static_cast<int64_t>(per_cu < 1 ? 1 : per_cu) * (cus < 1 ? 1 : cus);
+    cache.push_back({dev, shmem, blocks});
+    return blocks;
 }
 
-template <int MB, int EPI>
-void dispatch_rw(uint16_t* y, int64_t ldy, const uint16_t* x, int64_t ldx, const uint16_t* w,
-                 const uint16_t* res, int64_t ldres, int M, int N, int K, hipStream_t s) {
+template <int MB, int RW, int EPI, bool NORM>
+void launch_gemm(const GemmArgs& a, hipStream_t s) {
+    constexpr int U = MB <= 2 ? 4 : (MB <= 8 ? 2 : 1);
+    auto* kern = gemm_bf16_kernel<MB, RW, U, EPI, NORM>;
+    const int64_t groups = (static_cast<int64_t>(a.N) + 4 * RW - 1) / (4 * RW);
+    // NORM: LDS holds the M rows and the norm weight staged behind them.
+    const size_t shmem = NORM ? static_cast<size_t>(a.M + 1) * a.K * 2 : 0;
+    int64_t blocks = groups;
+    if (NORM) {
+        const int64_t resident = resident_blocks(kern, shmem);
+        if (resident > 0 && resident < blocks) blocks = resident;
+    }
+    kern<<<dim3(static_cast<unsigned>(blocks)), dim3(256), shmem, s>>>(a.y, a.ldy, a.x, a.ldx, a.w, a.res,
+                                                                     a.ldres, a.M, a.N, a.K, a.na);
+}
+
+template <int EPI, bool NORM>
+void dispatch_mb(const GemmArgs& a, hipStream_t s) {
     // Two rows per wave keeps the register footprint small enough for eight
     // waves per SIMD, which is what keeps enough bytes in flight on gfx950
     // (measured faster than 4 rows per wave or software-pipelined variants).
-    launch_gemm<MB, 2, EPI>(y, ldy, x, ldx, w, res, ldres, M, N, K, s);
+    if (a.M <= 1) launch_gemm<1, 2, EPI, NORM>(a, s);
+    else if (a.M <= 2) launch_gemm<2, 2, EPI, NORM>(a, s);
+    else if (a.M <= 4) launch_gemm<4, 2, EPI, NORM>(a, s);
+    else if (a.M <= 8) launch_gemm<8, 2, EPI, NORM>(a, s);
+    else launch_gemm<16, 2, EPI, NORM>(a, s);
 }
 
-template <int EPI>
-void dispatch_mb(uint16_t* y, int64_t ldy, const uint16_t* x, int64_t ldx, const uint16_t* w,
-                 const uint16_t* res, int64_t ldres, int M, int N, int K, hipStream_t s) {
-    if (M <= 1) dispatch_rw<1, EPI>(y, ldy, x, ldx, w, res, ldres, M, N, K, s);
-    else if (M <= 2) dispatch_rw<2, EPI>(y, ldy, x, ldx, w, res, ldres, M, N, K, s);
-    else if (M <= 4) dispatch_rw<4, EPI>(y, ldy, x, ldx, w, res, ldres, M, N, K, s);
-    else if (M <= 8) dispatch_rw<8, EPI>(y, ldy, x, ldx, w, res, ldres, M, N, K, s);
-    else dispatch_rw<16, EPI>(y, ldy, x, ldx, w, res, ldres, M, N, K, s);
+template <bool NORM>
+int dispatch_epi(const GemmArgs& a, int epilogue, hipStream_t s) {
+    switch (epilogue) {
+        case HAI_EPI_STORE:
+            if (a.ldy < a.N) return invalid("gemm: ldy < N");
+            dispatch_mb<HAI_EPI_STORE, NORM>(a, s);
+            break;
+        case HAI_EPI_RESIDUAL:
+            if (a.res == nullptr || a.ldy < a.N || a.ldres < a.N) return invalid("gemm: residual operands");
+            dispatch_mb<HAI_EPI_RESIDUAL, NORM>(a, s);
+            break;
+        case HAI_EPI_SILU_MUL:
+            if (a.N % 2 != 0 || a.ldy < a.N / 2) return invalid("gemm: silu_mul needs even N and ldy >= N/2");
+            dispatch_mb<HAI_EPI_SILU_MUL, NORM>(a, s);
+            break;
+        default:
+            return invalid("gemm: unknown epilogue");
+    }
+    return launched("gemm_bf16_kernel");
 }
 
-}  // namespace
-
-extern "C" int hai_gemm_bf16(void* y, int64_t ldy, const void* x, int64_t ldx, const void* w, int64_t M,
-                             int64_t N, int64_t K, int epilogue, const void* res, int64_t ld_res,
-                             void* stream) {
+int check_shape(const void* y, const void* x, const void* w, int64_t M, int64_t N, int64_t K, int64_t ldx) {
     if (y == nullptr || x == nullptr || w == nullptr) return invalid("gemm: null pointer");
     if (M < 0 || M > 16 || N < 0 || K <= 0 || K % 8 != 0 || ldx % 8 != 0 || ldx < K)
         return invalid("gemm: shape (need 0<=M<=16, K%8==0, ldx%8==0, ldx>=K)");
@@ -169,27 +312,53 @@ extern "C" int hai_gemm_bf16(void* y, int64_t ldy, const void* x, int64_t ldx, c
     if ((N + 4) * K * 2 >= (int64_t{1} << 32) || M * ldx * 2 >= (int64_t{1} << 32))
         return invalid("gemm: W or X exceeds the 4 GiB buffer-offset range");
     if (!aligned16(x) || !aligned16(w)) return invalid("gemm: x and w must be 16-byte aligned");
+    return HAI_OK;
+}
+
+}  // namespace
+
+extern "C" int hai_gemm_bf16(void* y, int64_t ldy, const void* x, int64_t ldx, const void* w, int64_t M,
+                             int64_t N, int64_t K, int epilogue, const void* res, int64_t ld_res,
+                             void* stream) {
+    const int rc = check_shape(y, x, w, M, N, K, ldx);
+    if (rc != HAI_OK) return rc;
     if (M == 0 || N == 0) return HAI_OK;
-    const auto* xs = static_cast<const uint16_t*>(x);
-    const auto* ws = static_cast<const uint16_t*>(w);
-    auto* ys = static_cast<uint16_t*>(y);
-    const auto* rs = static_cast<const uint16_t*>(res);
+    const GemmArgs a{static_cast<uint16_t*>(y), ldy, static_cast<const uint16_t*>(x), ldx,
+                     static_cast<const uint16_t*>(w), static_cast<const uint16_t*>(res), ld_res,
+                     int(M), int(N), int(K), NormArgs{}};
+    return dispatch_epi<false>(a, epilogue, as_stream(stream));
+}
+
+extern "C" int hai_gemm_rmsnorm_bf16(void* y, int64_t ldy, const void* x, int64_t ldx, const void* norm_w,
+                                     float eps, int unit_offset, void* xn_out, int64_t ld_xn, const void* w,
+                                     int64_t M, int64_t N, int64_t K, int epilogue, const void* res,
+                                     int64_t ld_res, void* stream) {
+    const int rc = check_shape(y, x, w, M, N, K, ldx);
+    if (rc != HAI_OK) return rc;
+    if (norm_w == nullptr) return invalid("gemm_rmsnorm: null norm weight");
+    if (xn_out != nullptr && (ld_xn < K || ld_xn % 8 != 0 || !aligned16(xn_out)))
+        return invalid("gemm_rmsnorm: xn_out needs ld_xn >= K, ld_xn % 8 == 0 and 16-byte alignment");
+    if (!aligned16(norm_w)) return invalid("gemm_rmsnorm: norm weight must be 16-byte aligned");
+    if (M == 0) return HAI_OK;
     const hipStream_t s = as_stream(stream);
-    switch (epilogue) {
-        case HAI_EPI_STORE:
-            if (ldy < N) return invalid("gemm: ldy < N");
-            dispatch_mb<HAI_EPI_STORE>(ys, ldy, xs, ldx, ws, nullptr, 0, int(M), int(N), int(K), s);
-            break;
-        case HAI_EPI_RESIDUAL:
-            if (res == nullptr || ldy < N || ld_res < N) return invalid("gemm: residual operands");
-            dispatch_mb<HAI_EPI_RESIDUAL>(ys, ldy, xs, ldx, ws, rs, ld_res, int(M), int(N), int(K), s);
-            break;
-        case HAI_EPI_SILU_MUL:
-            if (N % 2 != 0 || ldy < N / 2) return invalid("gemm: silu_mul needs even N and ldy >= N/2");
-            dispatch_mb<HAI_EPI_SILU_MUL>(ys, ldy, xs, ldx, ws, nullptr, 0, int(M), int(N), int(K), s);
-            break;
-        default:
-            return invalid("gemm: unknown epilogue");
+    if (M * K > kNormMaxElems) {
+        // Rows too large for the LDS prologue: normalise into xn_out, then multiply.
+        if (xn_out == nullptr) return invalid("gemm_rmsnorm: M*K above the fused limit needs xn_out");
+        const int r = hai_rmsnorm_bf16(xn_out, ld_xn, x, ldx, norm_w, M, K, eps, unit_offset, stream);
+        if (r != HAI_OK) return r;
+        return hai_gemm_bf16(y, ldy, xn_out, ld_xn, w, M, N, K, epilogue, res, ld_res, stream);
     }
-    return launched("gemm_bf16_kernel");
+    if (N == 0)
+        return xn_out != nullptr ? hai_rmsnorm_bf16(xn_out, ld_xn, x, ldx, norm_w, M, K, eps, unit_offset, stream)
+                                 : HAI_OK;
+    NormArgs na;
+    na.w = static_cast<const uint16_t*>(norm_w);
+    na.eps = eps;
+    na.off = unit_offset ? 1.0f : 0.0f;
+    na.xn = static_cast<uint16_t*>(xn_out);
+    na.ldxn = ld_xn;
+    const GemmArgs a{static_cast<uint16_t*>(y), ldy, static_cast<const uint16_t*>(x), ldx,
+                     static_cast<const uint16_t*>(w), static_cast<const uint16_t*>(res), ld_res,
+                     int(M), int(N), int(K), na};
+    return dispatch_epi<true>(a, epilogue, s);
 }

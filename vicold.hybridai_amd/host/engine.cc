@@ -21,6 +21,8 @@ constexpr uint32_t tid(uint32_t slot, uint32_t kind) { return slot * 64u + kind;
 constexpr uint32_t kSlotShared = 0, kSlotMtpShared = 1, kSlotLayer0 = 2, kSlotMtpLayer0 = 1024;
 
 constexpr size_t kAlign = 256;
+// Widest linear layer that takes its input RMSNorm fused into the GEMM.
+constexpr int64_t kFusedNormMaxN = 65536;
 size_t align_up(size_t n) { return (n + kAlign - 1) / kAlign * kAlign; }
 
 // Bump allocator over one device arena: first pass sizes, second pass hands
@@ -320,6 +322,36 @@ int Engine::gemm(uint16_t* y, int64_t ldy, const uint16_t* x, int64_t ldx, const
     return HAI_OK;
 }
 
+int Engine::norm_gemm(uint16_t* y, int64_t ldy, const uint16_t* x, const uint16_t* nw, uint16_t* xn_out,
+                      const uint16_t* w, int64_t M, int64_t N, int epi, const uint16_t* res, int64_t ldres) {
+    const int64_t H = d_.H;
+    // lm_head-sized outputs stream faster from the plain kernel than the norm
+    // prologue saves (measured on MI355X), so they normalise separately.
+    if (N > kFusedNormMaxN) {
+        uint16_t* xn = xn_out != nullptr ? xn_out : xn_;
+        HAI_TRY(hai_rmsnorm_bf16(xn, H, x, H, nw, M, H, cfg_.rms_eps, 1, stream_));
+        return gemm(y, ldy, xn, H, w, M, N, H, epi, res, ldres);
+    }
+    // Above the fused limit the call runs RMSNorm then GEMM through xn_.
+    if (xn_out == nullptr && M * H > HAI_GEMM_RMSNORM_FUSED_MAX) xn_out = xn_;
+    if (prof_gemm_) {
+        while (prof_events_.size() < prof_used_ + 2) {
+            void* e = nullptr;
+            HAI_TRY(hai_event_create(&e));
+            prof_events_.push_back(e);
+        }
+        HAI_TRY(hai_event_record(prof_events_[prof_used_++], stream_));
+    }
+    HAI_TRY(hai_gemm_rmsnorm_bf16(y, ldy, x, H, nw, cfg_.rms_eps, 1, xn_out, H, w, M, N, H, epi, res, ldres,
+                                  stream_));
+    if (prof_gemm_) {
+        HAI_TRY(hai_event_record(prof_events_[prof_used_++], stream_));
+        prof_bytes_ += static_cast<double>(N) * static_cast<double>(H) * 2.0;
+        ++prof_launches_;
+    }
+    return HAI_OK;
+}
+
 int Engine::reset_state() {
     // Committed lengths to zero; the DeltaNet state slot 0 of every layer must
     // start at zero (conv history before position 0 is read as zero).
@@ -332,13 +364,13 @@ int Engine::reset_state() {
     return HAI_OK;
 }
 
-// One gated-GQA sub-layer on the normalised rows in xn_, residual added into h
-// (qwen_attention_reference -> GatedGQAAttention::forward_impl,
-// attention.cc:301-599).
+// One gated-GQA sub-layer: input RMSNorm fused into the q|gate,k,v
+// projection, residual added into h (qwen_attention_reference ->
+// GatedGQAAttention::forward_impl, attention.cc:301-599).
 int Engine::attention_layer(const LayerWeights& L, int64_t T, uint16_t* h, const int32_t* lens, uint16_t* kc,
                             uint16_t* vc) {
     const auto& d = d_;
-    HAI_TRY(gemm(proj_, d.Nqkv, xn_, d.H, L.w_qkv, T, d.Nqkv, d.H, HAI_EPI_STORE, nullptr, 0));
+    HAI_TRY(norm_gemm(proj_, d.Nqkv, h, L.in_ln, nullptr, L.w_qkv, T, d.Nqkv, HAI_EPI_STORE, nullptr, 0));
     HAI_TRY(hai_q_gate_rmsnorm_rope_bf16(q_, gate_, proj_, d.Nqkv, L.q_norm, rope_cos_, rope_sin_, cap_, 1, T,
                                          d.nq, d.D, d.R, lens, 0, cfg_.rms_eps, stream_));
     HAI_TRY(hai_kv_rmsnorm_rope_append_bf16(kc, vc, cap_, proj_ + 2 * d.qw, proj_ + 2 * d.qw + d.kvw, d.Nqkv,
@@ -353,8 +385,7 @@ int Engine::attention_layer(const LayerWeights& L, int64_t T, uint16_t* h, const
 // projection with the residual add fused.
 int Engine::mlp(const LayerWeights& L, int64_t T, uint16_t* h) {
     const auto& d = d_;
-    HAI_TRY(hai_rmsnorm_bf16(xn_, d.H, h, d.H, L.post_ln, T, d.H, cfg_.rms_eps, 1, stream_));
-    HAI_TRY(gemm(act_, d.F, xn_, d.H, L.w_gu, T, 2 * d.F, d.H, HAI_EPI_SILU_MUL, nullptr, 0));
+    HAI_TRY(norm_gemm(act_, d.F, h, L.post_ln, nullptr, L.w_gu, T, 2 * d.F, HAI_EPI_SILU_MUL, nullptr, 0));
     return gemm(h, d.H, act_, d.F, L.w_down, T, d.H, d.F, HAI_EPI_RESIDUAL, h, d.H);
 }
 
@@ -365,12 +396,11 @@ int Engine::forward_target(const int64_t* d_ids, int64_t T, bool write_all_slots
     const auto& d = d_;
     HAI_TRY(hai_embedding_gather_bf16(h_, embed_, d_ids, T, d.V, d.H, stream_));
     for (auto& L : layers_) {
-        HAI_TRY(hai_rmsnorm_bf16(xn_, d.H, h_, d.H, L.in_ln, T, d.H, cfg_.rms_eps, 1, stream_));
         if (L.attn) {
             HAI_TRY(attention_layer(L, T, h_, d_tlen_, L.k_cache, L.v_cache));
         } else {
             // qwen_deltanet_reference (qwen_reference.cc:205-258)
-            HAI_TRY(gemm(proj_, d.Nin, xn_, d.H, L.w_in, T, d.Nin, d.H, HAI_EPI_STORE, nullptr, 0));
+            HAI_TRY(norm_gemm(proj_, d.Nin, h_, L.in_ln, nullptr, L.w_in, T, d.Nin, HAI_EPI_STORE, nullptr, 0));
             HAI_TRY(hai_deltanet_verify_bf16(dnout_, d.vw, proj_, d.Nin, 0, d.C, d.C + d.vw, d.C + d.vw + d.nv,
                                              L.conv_w, L.ring, ring_, L.state, nslots_, write_all_slots ? 1 : 0,
                                              L.a_log, L.dt_bias, L.lin_norm, d_tlen_, 0, 1, T, d.nk, d.nv, d.dk,
@@ -379,8 +409,7 @@ int Engine::forward_target(const int64_t* d_ids, int64_t T, bool write_all_slots
         }
         HAI_TRY(mlp(L, T, h_));
     }
-    HAI_TRY(hai_rmsnorm_bf16(hf_, d.H, h_, d.H, final_norm_, T, d.H, cfg_.rms_eps, 1, stream_));
-    return gemm(logits_, d.V, hf_, d.H, lm_head_, T, d.V, d.H, HAI_EPI_STORE, nullptr, 0);
+    return norm_gemm(logits_, d.V, h_, final_norm_, hf_, lm_head_, T, d.V, HAI_EPI_STORE, nullptr, 0);
 }
 
 // MTP input rows x = fc([RMSNorm(emb) | RMSNorm(hidden)]) (generator.cc:152-160)
@@ -394,10 +423,9 @@ int Engine::mtp_kv_rows(const int64_t* d_ids, const uint16_t* d_hidden, int64_t 
     HAI_TRY(hai_rmsnorm_bf16(xn_, 2 * d.H, emb_, d.H, pre_emb_, T, d.H, cfg_.rms_eps, 1, stream_));
     HAI_TRY(hai_rmsnorm_bf16(xn_ + d.H, 2 * d.H, d_hidden, d.H, pre_hid_, T, d.H, cfg_.rms_eps, 1, stream_));
     HAI_TRY(gemm(h_, d.H, xn_, 2 * d.H, fc_, T, d.H, 2 * d.H, HAI_EPI_STORE, nullptr, 0));
-    HAI_TRY(hai_rmsnorm_bf16(xn_, d.H, h_, d.H, mtp_.in_ln, T, d.H, cfg_.rms_eps, 1, stream_));
     // K and V rows of the fused attention projection only.
-    HAI_TRY(gemm(proj_, 2 * d.kvw, xn_, d.H, mtp_.w_qkv + 2 * d.qw * d.H, T, 2 * d.kvw, d.H, HAI_EPI_STORE,
-                 nullptr, 0));
+    HAI_TRY(norm_gemm(proj_, 2 * d.kvw, h_, mtp_.in_ln, nullptr, mtp_.w_qkv + 2 * d.qw * d.H, T, 2 * d.kvw,
+                      HAI_EPI_STORE, nullptr, 0));
     HAI_TRY(hai_kv_rmsnorm_rope_append_bf16(mtp_.k_cache, mtp_.v_cache, cap_, proj_, proj_ + d.kvw, 2 * d.kvw,
                                             mtp_.k_norm, rope_cos_, rope_sin_, cap_, 1, T, d.nkv, d.D, d.R, d_mlen_,
                                             0, cfg_.rms_eps, stream_));
@@ -415,11 +443,9 @@ int Engine::mtp_draft_step(const int64_t* d_id, const uint16_t* d_hin, uint16_t*
     HAI_TRY(hai_rmsnorm_bf16(xn_, 2 * d.H, emb_, d.H, pre_emb_, 1, d.H, cfg_.rms_eps, 1, stream_));
     HAI_TRY(hai_rmsnorm_bf16(xn_ + d.H, 2 * d.H, d_hin, d.H, pre_hid_, 1, d.H, cfg_.rms_eps, 1, stream_));
     HAI_TRY(gemm(h_, d.H, xn_, 2 * d.H, fc_, 1, d.H, 2 * d.H, HAI_EPI_STORE, nullptr, 0));
-    HAI_TRY(hai_rmsnorm_bf16(xn_, d.H, h_, d.H, mtp_.in_ln, 1, d.H, cfg_.rms_eps, 1, stream_));
     HAI_TRY(attention_layer(mtp_, 1, h_, d_mlen_, mtp_.k_cache, mtp_.v_cache));
     HAI_TRY(mlp(mtp_, 1, h_));
-    HAI_TRY(hai_rmsnorm_bf16(d_mh, d.H, h_, d.H, mtp_norm_, 1, d.H, cfg_.rms_eps, 1, stream_));
-    HAI_TRY(gemm(logits_, d.V, d_mh, d.H, lm_head_, 1, d.V, d.H, HAI_EPI_STORE, nullptr, 0));
+    HAI_TRY(norm_gemm(logits_, d.V, h_, mtp_norm_, d_mh, lm_head_, 1, d.V, HAI_EPI_STORE, nullptr, 0));
     HAI_TRY(hai_argmax_rows_bf16(d_cand, logits_, d.V, 1, d.V, argmax_scratch_, stream_));
     HAI_TRY(hai_add_i32(d_mlen_, nullptr, 1, 1, stream_));
     return HAI_OK;

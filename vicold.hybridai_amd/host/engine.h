@@ -11,7 +11,8 @@
 //     row (gate_f, up_f) for the fused SwiGLU epilogue;
 //   * caches: KV [cap][nkv][D] per attention layer; DeltaNet conv inputs in a
 //     ring [ring][C] indexed by position and the fp32 state in slots
-//     [nslots][nv][dv][dk], the slot of sequence length L being L % nslots;
+//     [nslots][nv][dk*dv] (each head column-tiled, as hai_deltanet_verify_bf16
+//     documents), the slot of sequence length L being L % nslots;
 //     committed lengths live on the device and are advanced by the accept
 //     kernel, so rollback is a length update, never a copy.
 #pragma once
@@ -48,7 +49,7 @@ struct LayerWeights {
     uint16_t* k_cache = nullptr;  // [cap][nkv][D]
     uint16_t* v_cache = nullptr;
     uint16_t* ring = nullptr;     // [ring][C]
-    float* state = nullptr;       // [nslots][nv][dv][dk]
+    float* state = nullptr;       // [nslots][nv][dk*dv], column-tiled heads
 };
 
 struct TensorEntry {
@@ -108,6 +109,10 @@ private:
     // device pieces of a step
     int gemm(uint16_t* y, int64_t ldy, const uint16_t* x, int64_t ldx, const uint16_t* w, int64_t M,
              int64_t N, int64_t K, int epi, const uint16_t* res, int64_t ldres);
+    // RMSNorm(+1) of the H-wide rows x (norm weight nw) fused into the linear
+    // layer W [N, H]; xn_out (optional) receives the normalised rows.
+    int norm_gemm(uint16_t* y, int64_t ldy, const uint16_t* x, const uint16_t* nw, uint16_t* xn_out,
+                  const uint16_t* w, int64_t M, int64_t N, int epi, const uint16_t* res, int64_t ldres);
     int forward_target(const int64_t* d_ids, int64_t T, bool write_all_slots);
     int attention_layer(const LayerWeights& L, int64_t T, uint16_t* h, const int32_t* lens,
                         uint16_t* kc, uint16_t* vc);
