@@ -148,6 +148,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--graphs", action="store_true",
                     help="replay captured HIP graphs (rocprofv3 kernel tracing cannot follow graph launches)")
+    ap.add_argument("--copy-bytes", type=int, default=0,
+                    help="first run one device-to-device copy of this many bytes (the known-size reference "
+                         "dispatch that scales rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the path runs on a single MI355X); "
@@ -156,6 +159,14 @@ def main():
 
     hai = load_package()
     from hybridai_amd import engine as E
+
+    if args.copy_bytes > 0:
+        src, dst = hai.DeviceBuffer(args.copy_bytes), hai.DeviceBuffer(args.copy_bytes)
+        src.zero()
+        hai.check(hai.kernels().hai_memcpy_d2d(dst.ptr, src.ptr, args.copy_bytes, None), "calibration copy")
+        hai.synchronize()
+        log(f"calibration copy of {args.copy_bytes} bytes done")
+        del src, dst
 
     cfg = E.QWEN27B
     P, NEW = args.prompt, args.new

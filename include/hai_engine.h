@@ -104,7 +104,8 @@ int hai_engine_generate_speculative(void* engine, const int32_t* prompt, int64_t
  * context with events around the whole step and around every GEMM launch. */
 typedef struct hai_verify_profile {
     double verify_ms;          /* mean wall of one verify step (forward+accept) */
-    double gemm_ms;            /* mean summed GEMM kernel time per step */
+    double gemm_ms;            /* mean time of the step's GEMM launches replayed
+                                  back to back between two events */
     double gemm_bytes;         /* weight bytes streamed by GEMMs per step */
     double gemm_launches;      /* GEMM launches per step */
     double step_bytes;         /* algorithmic bytes per step (weights+KV+state) */

@@ -110,7 +110,6 @@ Engine::~Engine() {
     for (void* g : draft_graphs_) if (g) hai_graph_destroy(g);
     for (void* g : verify_graphs_) if (g) hai_graph_destroy(g);
     if (corr_graph_) hai_graph_destroy(corr_graph_);
-    for (void* e : prof_events_) hai_event_destroy(e);
     if (weights_) hai_free(weights_);
     if (caches_) hai_free(caches_);
     if (work_) hai_free(work_);
@@ -305,20 +304,8 @@ int64_t Engine::read_tensor(uint32_t id, uint16_t* out, int64_t capacity) {
 
 int Engine::gemm(uint16_t* y, int64_t ldy, const uint16_t* x, int64_t ldx, const uint16_t* w, int64_t M,
                  int64_t N, int64_t K, int epi, const uint16_t* res, int64_t ldres) {
-    if (prof_gemm_) {
-        while (prof_events_.size() < prof_used_ + 2) {
-            void* e = nullptr;
-            HAI_TRY(hai_event_create(&e));
-            prof_events_.push_back(e);
-        }
-        HAI_TRY(hai_event_record(prof_events_[prof_used_++], stream_));
-    }
+    if (prof_record_) prof_calls_.push_back({y, ldy, x, ldx, w, M, N, K, epi, res, ldres, nullptr, nullptr});
     HAI_TRY(hai_gemm_bf16(y, ldy, x, ldx, w, M, N, K, epi, res, ldres, stream_));
-    if (prof_gemm_) {
-        HAI_TRY(hai_event_record(prof_events_[prof_used_++], stream_));
-        prof_bytes_ += static_cast<double>(N) * static_cast<double>(K) * 2.0;
-        ++prof_launches_;
-    }
     return HAI_OK;
 }
 
@@ -334,21 +321,9 @@ int Engine::norm_gemm(uint16_t* y, int64_t ldy, const uint16_t* x, const uint16_
     }
     // Above the fused limit the call runs RMSNorm then GEMM through xn_.
     if (xn_out == nullptr && M * H > HAI_GEMM_RMSNORM_FUSED_MAX) xn_out = xn_;
-    if (prof_gemm_) {
-        while (prof_events_.size() < prof_used_ + 2) {
-            void* e = nullptr;
-            HAI_TRY(hai_event_create(&e));
-            prof_events_.push_back(e);
-        }
-        HAI_TRY(hai_event_record(prof_events_[prof_used_++], stream_));
-    }
+    if (prof_record_) prof_calls_.push_back({y, ldy, x, H, w, M, N, H, epi, res, ldres, nw, xn_out});
     HAI_TRY(hai_gemm_rmsnorm_bf16(y, ldy, x, H, nw, cfg_.rms_eps, 1, xn_out, H, w, M, N, H, epi, res, ldres,
                                   stream_));
-    if (prof_gemm_) {
-        HAI_TRY(hai_event_record(prof_events_[prof_used_++], stream_));
-        prof_bytes_ += static_cast<double>(N) * static_cast<double>(H) * 2.0;
-        ++prof_launches_;
-    }
     return HAI_OK;
 }
 
@@ -515,7 +490,7 @@ int Engine::generate_greedy(const int32_t* prompt, int64_t P, int64_t max_new, c
 
 template <typename F>
 int Engine::replay(void** slot, F&& enqueue) {
-    if (!use_graphs_ || prof_gemm_) return enqueue();
+    if (!use_graphs_) return enqueue();
     if (*slot == nullptr) {
         HAI_TRY(hai_graph_begin_capture(stream_));
         const int rc = enqueue();
@@ -717,12 +692,9 @@ int Engine::profile_verify(int64_t T, int64_t iters, hai_verify_profile* out) {
     std::vector<int64_t> ids(static_cast<size_t>(T), 1);
     HAI_TRY(hai_memcpy_h2d(d_ids_, ids.data(), static_cast<size_t>(T) * 8, stream_));
     double verify_ms = 0.0, gemm_ms = 0.0, draft_ms = 0.0;
-    double gemm_bytes = 0.0, launches = 0.0;
-    for (int64_t it = 0; it < iters + 1; ++it) {  // first iteration warms up
-        prof_gemm_ = true;
-        prof_used_ = 0;
-        prof_bytes_ = 0.0;
-        prof_launches_ = 0;
+    for (int64_t it = 0; it < iters + 1; ++it) {  // first iteration warms up and records the GEMMs
+        prof_record_ = it == 0;
+        if (prof_record_) prof_calls_.clear();
         HAI_TRY(hai_event_record(e0, stream_));
         HAI_TRY(forward_target(d_ids_, T, true));
         HAI_TRY(hai_memcpy_d2d(scratch_len, d_tlen_, 4, stream_));
@@ -731,23 +703,33 @@ int Engine::profile_verify(int64_t T, int64_t iters, hai_verify_profile* out) {
                                               scratch_len + 4, scratch_len, scratch_len + 1, d_pnext_, nullptr,
                                               nullptr, argmax_scratch_, stream_));
         HAI_TRY(hai_event_record(e1, stream_));
-        prof_gemm_ = false;
+        prof_record_ = false;
         HAI_TRY(sync());
         float ms = 0.0f;
         HAI_TRY(hai_event_elapsed_ms(e0, e1, &ms));
-        double g = 0.0;
-        for (size_t i = 0; i + 1 < prof_used_; i += 2) {
-            float gm = 0.0f;
-            HAI_TRY(hai_event_elapsed_ms(prof_events_[i], prof_events_[i + 1], &gm));
-            g += gm;
-        }
-        if (it > 0) {
-            verify_ms += ms;
-            gemm_ms += g;
-            gemm_bytes += prof_bytes_;
-            launches += static_cast<double>(prof_launches_);
-        }
+        if (it > 0) verify_ms += ms;
     }
+    // The step's GEMM launches replayed back to back (same shapes, weights and
+    // buffers; the outputs are scratch here), two events around each replay.
+    double gemm_bytes = 0.0;
+    for (const auto& c : prof_calls_) gemm_bytes += static_cast<double>(c.N) * static_cast<double>(c.K) * 2.0;
+    for (int64_t it = 0; it < iters + 1; ++it) {
+        HAI_TRY(hai_event_record(e0, stream_));
+        for (const auto& c : prof_calls_) {
+            if (c.nw != nullptr)
+                HAI_TRY(hai_gemm_rmsnorm_bf16(c.y, c.ldy, c.x, c.ldx, c.nw, cfg_.rms_eps, 1, c.xn, c.ldx, c.w, c.M,
+                                              c.N, c.K, c.epi, c.res, c.ldres, stream_));
+            else
+                HAI_TRY(hai_gemm_bf16(c.y, c.ldy, c.x, c.ldx, c.w, c.M, c.N, c.K, c.epi, c.res, c.ldres,
+                                      stream_));
+        }
+        HAI_TRY(hai_event_record(e1, stream_));
+        HAI_TRY(sync());
+        float ms = 0.0f;
+        HAI_TRY(hai_event_elapsed_ms(e0, e1, &ms));
+        if (it > 0) gemm_ms += ms;
+    }
+    const double launches = static_cast<double>(prof_calls_.size());
     // Draft step timing (one MTP forward + lm_head + argmax) without events
     // inside, on a scratch MTP length.
     for (int64_t it = 0; it < iters + 1; ++it) {
@@ -766,8 +748,8 @@ int Engine::profile_verify(int64_t T, int64_t iters, hai_verify_profile* out) {
     const double n = static_cast<double>(iters);
     out->verify_ms = verify_ms / n;
     out->gemm_ms = gemm_ms / n;
-    out->gemm_bytes = gemm_bytes / n;
-    out->gemm_launches = launches / n;
+    out->gemm_bytes = gemm_bytes;
+    out->gemm_launches = launches;
     // algorithmic bytes of one verify step: weights streamed + KV read +
     // DeltaNet state read and T states written.
     int64_t n_attn = 0, n_dn = 0;

@@ -191,11 +191,23 @@ private:
     int64_t nproj_ = 0;
 
     // profiling of GEMM launches (profile_verify only)
-    bool prof_gemm_ = false;
-    std::vector<void*> prof_events_;
-    size_t prof_used_ = 0;
-    double prof_bytes_ = 0.0;
-    int64_t prof_launches_ = 0;
+    // profile_verify: the GEMM launches of one verify step, recorded so that
+    // they can be replayed back to back between two events.
+    struct GemmCall {
+        uint16_t* y;
+        int64_t ldy;
+        const uint16_t* x;
+        int64_t ldx;
+        const uint16_t* w;
+        int64_t M, N, K;
+        int epi;
+        const uint16_t* res;
+        int64_t ldres;
+        const uint16_t* nw;  // non-null: RMSNorm-fused launch
+        uint16_t* xn;
+    };
+    bool prof_record_ = false;
+    std::vector<GemmCall> prof_calls_;
 
     RoundState rs_;
 
