@@ -1,0 +1,49 @@
+"""The C ABI without a GPU: both shared libraries load, export every entry
+point that include/*.h declares, and the argument checks that run before any
+device call reject bad shapes with HAI_ERR_INVALID_ARGUMENT."""
+import ctypes
+import re
+
+import pytest
+
+from _hai import ROOT, hai
+
+HEADERS = sorted((ROOT / "include").glob("*.h"))
+DECL = re.compile(r"^\s*(?:const\s+)?[A-Za-z_][A-Za-z0-9_]*\s*\*?\s*(hai_[a-z0-9_]+)\s*\(", re.M)
+
+
+def declared(header):
+    return sorted(set(DECL.findall(header.read_text())))
+
+
+def test_headers_declare_entry_points():
+    names = {h.name: declared(h) for h in HEADERS}
+    assert names["hai_kernels.h"] and names["hai_engine.h"]
+
+
+@pytest.mark.parametrize("header", HEADERS, ids=lambda p: p.name)
+def test_every_declared_symbol_is_exported(header):
+    libs = [ctypes.CDLL(str(hai.KERNELS_SO)), ctypes.CDLL(str(hai.HOST_SO))]
+    missing = [n for n in declared(header) if not any(hasattr(lib, n) for lib in libs)]
+    assert not missing, f"{header.name}: not exported by the built libraries: {missing}"
+
+
+def test_kernel_signatures_cover_the_header():
+    """Every kernels-header entry point has a ctypes signature in the package."""
+    sigs = set(hai._KERNEL_SIGS) | set(hai._SIZE_SIGS) | {"hai_last_error"}
+    missing = [n for n in declared(ROOT / "include" / "hai_kernels.h") if n not in sigs]
+    assert not missing, missing
+
+
+def test_argument_checks_need_no_device():
+    k = hai.kernels()
+    p = ctypes.c_void_p(16)  # never dereferenced: every call below fails its host-side checks
+    assert k.hai_gemm_bf16(p, 4, p, 12, p, 2, 4, 12, 0, None, 0, None) == hai.ERR_INVALID  # K % 8
+    assert k.hai_gemm_bf16(p, 4, p, 8, p, 17, 4, 8, 0, None, 0, None) == hai.ERR_INVALID   # M > 16
+    assert k.hai_gemm_bf16(None, 4, p, 8, p, 1, 4, 8, 0, None, 0, None) == hai.ERR_INVALID
+    assert k.hai_gemm_rmsnorm_bf16(p, 8, p, 5120, p, 1e-6, 1, None, 0, p, 4, 8, 5120, 0, None, 0,
+                                   None) == hai.ERR_INVALID  # above the fused limit without xn_out
+    assert k.hai_deltanet_verify_bf16(p, 8, p, 8, 0, 0, 0, 0, p, p, 4, p, 1, 1, p, p, p, None, 0, 1, 17, 1, 1,
+                                      128, 128, 4, 1e-6, None) == hai.ERR_INVALID  # T > 16
+    assert k.hai_gqa_verify_bf16(p, p, p, p, p, 8, p, 1, 4, 4, 3, 64, None, 4, 8, None) == hai.ERR_INVALID
+    assert b"gqa_verify" in k.hai_last_error()
