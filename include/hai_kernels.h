@@ -13,8 +13,10 @@
  *     value is the argument-check / launch status, device faults surface at
  *     the next synchronisation;
  *   - bf16 tensors are uint16 bit patterns, stores round to nearest even;
- *   - the arithmetic is the canonical order documented in DESIGN.md
- *     (bit-identical to the CPU oracle).
+ *   - the arithmetic follows one canonical order shared with the CPU oracle
+ *     (IEEE fma on the VALU; long sums in "L64" order: element k to lane
+ *     (k/8) mod 64, per-lane fma in increasing k, xor-butterfly 32..1), so
+ *     results are bit-identical to it and independent of batch and tiling.
  */
 #ifndef HAI_KERNELS_H
 #define HAI_KERNELS_H
@@ -143,6 +145,15 @@ int hai_kv_rmsnorm_rope_append_bf16(void* k_cache, void* v_cache, int64_t cap,
                                     int64_t T, int64_t nkv, int64_t D,
                                     int64_t R, const int32_t* lens,
                                     int32_t pos_add, float eps, void* stream);
+/* partial_rope_kernel (hip_kernels.hip:192-221) as called by
+ * Backend::partial_rope: rotate-half on the first R dims of each of the
+ * `heads` D-wide heads of T rows, position pos0 + t, dims past R copied;
+ * rope_cos / rope_sin are [rope_positions][R/2] tables (theta =
+ * pos / base^(2p/R), evaluated in double and rounded to float). */
+int hai_partial_rope_bf16(void* dst, const void* src, int64_t T, int64_t heads,
+                          int64_t D, int64_t R, const float* rope_cos,
+                          const float* rope_sin, int64_t rope_positions,
+                          int64_t pos0, void* stream);
 /* Plain row append (append_kv_cache_kernel) for callers that already hold
  * the final K/V rows (Backend::append_kv_cache). */
 int hai_append_kv_bf16(void* k_cache, void* v_cache, int64_t cap,
@@ -192,6 +203,29 @@ int hai_deltanet_verify_bf16(void* out, int64_t ld_out, const void* proj,
                              int32_t pos_add, int64_t B, int64_t T, int64_t nk,
                              int64_t nv, int64_t dk, int64_t dv, int64_t Kc,
                              float eps, void* stream);
+/* The reference's two-kernel DeltaNet contract (Backend::deltanet_grouped_conv
+ * and Backend::deltanet_recurrent, hip_backend.cc:1357-1470), on the
+ * reference's cache layouts:
+ *   hai_deltanet_conv_bf16: qkv [T][C] flat [Q|K|V] -> q, k [T][nk*dk] and
+ *     v [T][nv*dv] after the causal conv + SiLU; conv_state [C][Kc-1] (oldest
+ *     first) is shifted in place (deltanet_grouped_conv_kernel,
+ *     hip_kernels.hip:871-912);
+ *   hai_deltanet_recurrent_bf16: gated delta rule + gated RMSNorm over T
+ *     tokens with the fp32 state [nv][dk][dv] updated in place; a, b are the
+ *     raw [T][nv] projections (decay and beta computed inside), z [T][nv*dv]
+ *     (deltanet_recurrent_kernel, :985-1095).  Any T (16 tokens per launch,
+ *     chained).  (dk, dv) in {(128,128), (64,64)}. */
+int hai_deltanet_conv_bf16(void* q, void* k, void* v, void* conv_state,
+                           const void* qkv, const void* conv_w, int64_t T,
+                           int64_t nk, int64_t nv, int64_t dk, int64_t dv,
+                           int64_t Kc, void* stream);
+int hai_deltanet_recurrent_bf16(void* out, float* state, const void* q,
+                                const void* k, const void* v, const void* a,
+                                const void* b, const void* a_log,
+                                const void* dt_bias, const void* norm_w,
+                                const void* z, int64_t T, int64_t nk,
+                                int64_t nv, int64_t dk, int64_t dv, float eps,
+                                void* stream);
 
 /* ------------------------------------------------------------------ argmax / accept
  * argmax_rows_kernel (hip_kernels.hip:1243-1274) with the CPU tie-break of

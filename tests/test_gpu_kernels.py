@@ -400,3 +400,65 @@ def test_fill_synthetic_matches_oracle():
         hai.check(kern().hai_fill_synthetic_bf16(d.ptr, rows, cols, ld, 0, tid, 0.02, None), "fill")
         got = d.download(np.uint16).reshape(rows, ld)[:, :cols]
         assert_bits_equal(got, want, f"tensor {tid}")
+
+
+# ----------------------------------------------------------------- Backend-contract launchers
+@pytest.mark.parametrize("T,heads,D,R,pos0", [(3, 4, 64, 16, 0), (5, 6, 256, 64, 1000), (1, 2, 128, 128, 7)])
+def test_partial_rope(T, heads, D, R, pos0):
+    rng = np.random.default_rng(T * 100 + D + pos0)
+    x, xb = rand_bf16(rng, (T * heads, D))
+    npos = pos0 + T + 3
+    cs, sn = orc.rope_table(0, npos, R, 1.0e7)
+    dx, dy = dev(xb), out_buf(xb.nbytes)
+    dc, ds = dev(cs.astype(np.float32)), dev(sn.astype(np.float32))
+    hai.check(kern().hai_partial_rope_bf16(dy.ptr, dx.ptr, T, heads, D, R, dc.ptr, ds.ptr, npos, pos0, None),
+              "partial_rope")
+    want = orc.partial_rope(x, T, heads, D, R, pos0, 1.0e7, round_out=True)
+    assert_bits_equal(dy.download(np.uint16), want, "partial_rope")
+    # positions past the table are rejected before launch
+    assert kern().hai_partial_rope_bf16(dy.ptr, dx.ptr, T, heads, D, R, dc.ptr, ds.ptr, npos, npos - T + 1,
+                                        None) == hai.ERR_INVALID
+
+
+@pytest.mark.parametrize("nk,nv,dk,Kc,T", [(4, 4, 64, 4, 5), (16, 48, 128, 4, 2), (2, 4, 64, 3, 1)])
+def test_deltanet_conv_reference_layout(nk, nv, dk, Kc, T):
+    rng = np.random.default_rng(nk + nv + T)
+    dv = dk
+    C = 2 * nk * dk + nv * dv
+    qkv, qkvb = rand_bf16(rng, (T, C))
+    w, wb = rand_bf16(rng, (C, Kc), 0.5)
+    st, stb = rand_bf16(rng, (C, Kc - 1))
+    dq, dk_, dvv = out_buf(T * nk * dk * 2), out_buf(T * nk * dk * 2), out_buf(T * nv * dv * 2)
+    dst, dqkv, dw = dev(stb), dev(qkvb), dev(wb)
+    hai.check(kern().hai_deltanet_conv_bf16(dq.ptr, dk_.ptr, dvv.ptr, dst.ptr, dqkv.ptr, dw.ptr, T, nk, nv, dk,
+                                            dv, Kc, None), "deltanet_conv")
+    q, k, v, st2 = orc.deltanet_conv(qkv, w, st, T, nk, nv, dk, dv, Kc)
+    assert_bits_equal(dq.download(np.uint16), q, "conv q")
+    assert_bits_equal(dk_.download(np.uint16), k, "conv k")
+    assert_bits_equal(dvv.download(np.uint16), v, "conv v")
+    assert_bits_equal(dst.download(np.uint16), st2, "conv state")
+
+
+@pytest.mark.parametrize("nk,nv,dk,T", [(4, 4, 64, 3), (2, 6, 128, 21)])
+def test_deltanet_recurrent_reference_layout(nk, nv, dk, T):
+    """State [nv][dk][dv] updated in place; T > 16 runs as chained launches."""
+    rng = np.random.default_rng(nk * 10 + T)
+    dv = dk
+    q, qb = rand_bf16(rng, (T, nk * dk))
+    k, kb = rand_bf16(rng, (T, nk * dk))
+    v, vb = rand_bf16(rng, (T, nv * dv))
+    a, ab = rand_bf16(rng, (T, nv))
+    b, bb = rand_bf16(rng, (T, nv))
+    z, zb = rand_bf16(rng, (T, nv * dv))
+    al, alb = rand_bf16(rng, (nv,), 0.5)
+    dt, dtb = rand_bf16(rng, (nv,), 0.5)
+    nw, nwb = rand_bf16(rng, (dv,), 0.1)
+    state = (rng.standard_normal((nv, dk, dv)) * 0.1).astype(np.float32)
+    dbufs = [dev(t) for t in (qb, kb, vb, ab, bb, alb, dtb, nwb, zb)]
+    dstate, dout = dev(state), out_buf(T * nv * dv * 2)
+    hai.check(kern().hai_deltanet_recurrent_bf16(dout.ptr, dstate.ptr, *[d.ptr for d in dbufs], T, nk, nv, dk, dv,
+                                                 1e-6, None), "deltanet_recurrent")
+    out, st2 = orc.deltanet_recurrent(q, k, v, a, b, z, al, dt, nw, state, T, nk, nv, dk, dv)
+    assert_bits_equal(dout.download(np.uint16), out, "recurrent out")
+    got_state = dstate.download(np.float32).reshape(st2.shape)
+    assert np.array_equal(got_state.view(np.uint32), st2.view(np.uint32)), "recurrent state"

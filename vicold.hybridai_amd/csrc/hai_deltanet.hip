@@ -30,18 +30,40 @@ using namespace hai;
 constexpr int kMaxT = 16;   // tokens per launch (verify width k + 1 <= 16)
 constexpr int kMaxKc = 8;   // conv taps
 
-template <int DK, int DV>
-__global__ __launch_bounds__(DV * 4) void deltanet_verify_kernel(
-    uint16_t* __restrict__ out, int64_t ld_out, const uint16_t* __restrict__ proj, int64_t ld_proj,
-    int64_t off_qkv, int64_t off_z, int64_t off_a, int64_t off_b, const uint16_t* __restrict__ conv_w,
-    uint16_t* __restrict__ ring, int ring_n, float* __restrict__ state, int nslots, int write_all,
-    const uint16_t* __restrict__ a_log, const uint16_t* __restrict__ dt_bias,
-    const uint16_t* __restrict__ norm_w, const int32_t* lens, int pos_add, int B, int T, int nk, int nv,
-    int Kc, float eps) {
+struct DnArgs {
+    uint16_t* out;
+    int64_t ld_out;
+    // fused verify: projection rows [qkv | z | a | b], conv ring, state slots
+    const uint16_t* proj;
+    int64_t ld_proj, off_qkv, off_z, off_a, off_b;
+    const uint16_t* conv_w;
+    uint16_t* ring;
+    int ring_n, nslots, write_all;
+    const int32_t* lens;
+    int pos_add;
+    // reference layout (Backend::deltanet_recurrent): separate conv outputs
+    const uint16_t *q, *k, *v, *a, *bv, *z;
+    float* state;
+    const uint16_t *a_log, *dt_bias, *norm_w;
+    int B, T, nk, nv, Kc;
+    float eps;
+};
+
+// Gated delta rule over T tokens for one (value head, sequence).
+// REF = false: fused verify step -- grouped causal conv + SiLU from the
+//   projection rows and the conv ring, state read from slot p0 % nslots of
+//   the column-tiled layout and written after every token (write_all) or the
+//   last one, to slot (p0 + t + 1) % nslots.
+// REF = true: the reference's deltanet_recurrent contract -- q, k, v already
+//   convolved, a/b/z in their own [T, ...] buffers, one fp32 state
+//   [nv][dk][dv] (hip_kernels.hip:985-1095) updated in place.
+template <int DK, int DV, bool REF>
+__global__ __launch_bounds__(DV * 4) void deltanet_kernel(DnArgs A) {
     constexpr int NT = DV * 4;
     constexpr int NW = NT / 64;
     constexpr int GI = DK / 4;            // key dims per thread
     constexpr int ZP = kMaxT * DV / NT;   // output elements per thread (all tokens)
+    const int T = A.T;
     extern __shared__ float smem[];
     float* qs = smem;                  // [T][DK] conv output, q channels
     float* ks = qs + T * DK;           // [T][DK] k channels
@@ -56,65 +78,91 @@ __global__ __launch_bounds__(DV * 4) void deltanet_verify_kernel(
     const int wave = tid >> 6;
     const int j = tid >> 2;
     const int g = tid & 3;
-    const int group = nv / nk;
+    const int nv = A.nv;
+    const int group = nv / A.nk;
     const int gq = h / group;
-    const int64_t kw = static_cast<int64_t>(nk) * DK;
+    const int64_t kw = static_cast<int64_t>(A.nk) * DK;
     const int64_t vw = static_cast<int64_t>(nv) * DV;
     const int64_t C = 2 * kw + vw;
-    const int64_t p0 = static_cast<int64_t>(lens ? lens[b] : 0) + pos_add;
-    const int hist = Kc - 1;
+    const int64_t p0 = REF ? 0 : static_cast<int64_t>(A.lens ? A.lens[b] : 0) + A.pos_add;
+    const int hist = A.Kc - 1;
     const int64_t row0 = static_cast<int64_t>(b) * T;
 
     // ---- issue every global load of the step up front ----
-    // committed state (slot p0 % nslots), column j, key dims [g*GI, g*GI+GI)
-    float S[GI];
-    {
-        const int64_t slot = p0 % nslots;
-        const float4* src = reinterpret_cast<const float4*>(state + ((slot * B + b) * nv + h) * static_cast<int64_t>(DV) * DK) + tid;
+    float S[GI];  // column j, key dims [g*GI, g*GI+GI)
+    if constexpr (REF) {
+        const float* src = A.state + static_cast<int64_t>(h) * DK * DV + static_cast<int64_t>(g) * GI * DV + j;
+#pragma unroll
+        for (int i = 0; i < GI; ++i) S[i] = src[i * DV];
+    } else {
+        const int64_t slot = p0 % A.nslots;
+        const float4* src =
+            reinterpret_cast<const float4*>(A.state + ((slot * A.B + b) * nv + h) * static_cast<int64_t>(DV) * DK) +
+            tid;
 #pragma unroll
         for (int m = 0; m < GI / 4; ++m) {
             const float4 v4 = src[m * NT];
             S[4 * m] = v4.x; S[4 * m + 1] = v4.y; S[4 * m + 2] = v4.z; S[4 * m + 3] = v4.w;
         }
     }
-    // conv channel of this thread: [0, DK) q, [DK, 2DK) k, [2DK, 2DK+DV) v
+    // channel of this thread: [0, DK) q, [DK, 2DK) k, [2DK, 2DK+DV) v
     const int cl = tid;
     const bool has_ch = cl < 2 * DK + DV;
+    float* dst = qs;
+    int di = cl, dstride = DK;
+    if (cl >= DK && cl < 2 * DK) { dst = ks; di = cl - DK; }
+    else if (cl >= 2 * DK) { dst = vs; di = cl - 2 * DK; dstride = DV; }
+    // window: vals[i] = input at position p0 - hist + i (history, then the T new tokens)
+    uint16_t vals[kMaxT + kMaxKc - 1];
+    float wc[kMaxKc];
     int64_t c = 0;
     if (cl < DK) c = static_cast<int64_t>(gq) * DK + cl;
     else if (cl < 2 * DK) c = kw + static_cast<int64_t>(gq) * DK + (cl - DK);
     else c = 2 * kw + static_cast<int64_t>(h) * DV + (cl - 2 * DK);
-    // window: vals[i] = input at position p0 - hist + i (history, then the T new tokens)
-    uint16_t vals[kMaxT + kMaxKc - 1];
-    float wc[kMaxKc];
     if (has_ch) {
+        if constexpr (REF) {
+            // convolved q/k/v rows straight from their buffers
+            const uint16_t* srcp;
+            int64_t ld, col;
+            if (cl < DK) { srcp = A.q; ld = kw; col = static_cast<int64_t>(gq) * DK + cl; }
+            else if (cl < 2 * DK) { srcp = A.k; ld = kw; col = static_cast<int64_t>(gq) * DK + cl - DK; }
+            else { srcp = A.v; ld = vw; col = static_cast<int64_t>(h) * DV + cl - 2 * DK; }
 #pragma unroll
-        for (int i = 0; i < kMaxKc - 1; ++i) {
-            const int64_t pos = p0 - hist + i;
-            vals[i] = (i < hist && pos >= 0)
-                          ? ring[(static_cast<int64_t>(b) * ring_n + (pos % ring_n)) * C + c]
-                          : uint16_t{0};
-        }
+            for (int t = 0; t < kMaxT; ++t) vals[t] = t < T ? srcp[t * ld + col] : uint16_t{0};
+        } else {
 #pragma unroll
-        for (int i = 0; i < kMaxKc; ++i) wc[i] = i < Kc ? bf2f(conv_w[c * Kc + i]) : 0.0f;
+            for (int i = 0; i < kMaxKc - 1; ++i) {
+                const int64_t pos = p0 - hist + i;
+                vals[i] = (i < hist && pos >= 0)
+                              ? A.ring[(static_cast<int64_t>(b) * A.ring_n + (pos % A.ring_n)) * C + c]
+                              : uint16_t{0};
+            }
 #pragma unroll
-        for (int t = 0; t < kMaxT; ++t) {
-            uint16_t x = 0;
-            if (t < T) x = proj[(row0 + t) * ld_proj + off_qkv + c];
-            // shift the new tokens in right after the hist history entries
+            for (int i = 0; i < kMaxKc; ++i) wc[i] = i < A.Kc ? bf2f(A.conv_w[c * A.Kc + i]) : 0.0f;
 #pragma unroll
-            for (int hh = 0; hh < kMaxKc; ++hh)
-                if (hh == hist) vals[t + hh] = x;
+            for (int t = 0; t < kMaxT; ++t) {
+                uint16_t x = 0;
+                if (t < T) x = A.proj[(row0 + t) * A.ld_proj + A.off_qkv + c];
+                // shift the new tokens in right after the hist history entries
+#pragma unroll
+                for (int hh = 0; hh < kMaxKc; ++hh)
+                    if (hh == hist) vals[t + hh] = x;
+            }
         }
     }
     // per-token gate scalars (last wave, lane = token)
     float a_in = 0.0f, b_in = 0.0f, dtb = 0.0f, alog = 0.0f;
     const bool scal = wave == NW - 1 && lane < T;
     if (scal) {
-        a_in = bf2f(proj[(row0 + lane) * ld_proj + off_a + h]);
-        b_in = bf2f(proj[(row0 + lane) * ld_proj + off_b + h]);
-        dtb = bf2f(dt_bias[h]);
-        alog = bf2f(a_log[h]);
+        if constexpr (REF) {
+            a_in = bf2f(A.a[static_cast<int64_t>(lane) * nv + h]);
+            b_in = bf2f(A.bv[static_cast<int64_t>(lane) * nv + h]);
+        } else {
+            a_in = bf2f(A.proj[(row0 + lane) * A.ld_proj + A.off_a + h]);
+            b_in = bf2f(A.proj[(row0 + lane) * A.ld_proj + A.off_b + h]);
+        }
+        dtb = bf2f(A.dt_bias[h]);
+        alog = bf2f(A.a_log[h]);
     }
     // gate z and norm weight for the output elements (t, jo) = (tid / DV + r * NT / DV, tid % DV)
     const int jo = tid % DV;
@@ -122,32 +170,38 @@ __global__ __launch_bounds__(DV * 4) void deltanet_verify_kernel(
 #pragma unroll
     for (int r = 0; r < ZP; ++r) {
         const int t = tid / DV + r * (NT / DV);
-        zr[r] = t < T ? bf2f(proj[(row0 + t) * ld_proj + off_z + static_cast<int64_t>(h) * DV + jo]) : 0.0f;
+        float zv = 0.0f;
+        if (t < T) {
+            if constexpr (REF) zv = bf2f(A.z[t * vw + static_cast<int64_t>(h) * DV + jo]);
+            else zv = bf2f(A.proj[(row0 + t) * A.ld_proj + A.off_z + static_cast<int64_t>(h) * DV + jo]);
+        }
+        zr[r] = zv;
     }
-    const float nwj = bf2f(norm_w[jo]);
+    const float nwj = bf2f(A.norm_w[jo]);
 
-    // ---- grouped causal conv + SiLU ----
+    // ---- grouped causal conv + SiLU (REF: inputs are already convolved) ----
     if (has_ch) {
-        float* dst;
-        int di, dstride;
-        if (cl < DK) { dst = qs; di = cl; dstride = DK; }
-        else if (cl < 2 * DK) { dst = ks; di = cl - DK; dstride = DK; }
-        else { dst = vs; di = cl - 2 * DK; dstride = DV; }
-        const bool writer = cl >= 2 * DK || (h % group) == 0;
+        if constexpr (REF) {
 #pragma unroll
-        for (int t = 0; t < kMaxT; ++t) {
-            if (t < T) {
-                float acc = bf2f(vals[t]) * wc[0];
+            for (int t = 0; t < kMaxT; ++t)
+                if (t < T) dst[t * dstride + di] = bf2f(vals[t]);
+        } else {
+            const bool writer = cl >= 2 * DK || (h % group) == 0;
 #pragma unroll
-                for (int i = 1; i < kMaxKc; ++i)
-                    if (i < Kc) acc = fma_(bf2f(vals[t + i]), wc[i], acc);
-                dst[t * dstride + di] = bfr(csilu(acc));
-                if (writer) {
-                    uint16_t xv = 0;
+            for (int t = 0; t < kMaxT; ++t) {
+                if (t < T) {
+                    float acc = bf2f(vals[t]) * wc[0];
 #pragma unroll
-                    for (int hh = 0; hh < kMaxKc; ++hh)
-                        if (hh == hist) xv = vals[t + hh];
-                    ring[(static_cast<int64_t>(b) * ring_n + ((p0 + t) % ring_n)) * C + c] = xv;
+                    for (int i = 1; i < kMaxKc; ++i)
+                        if (i < A.Kc) acc = fma_(bf2f(vals[t + i]), wc[i], acc);
+                    dst[t * dstride + di] = bfr(csilu(acc));
+                    if (writer) {
+                        uint16_t xv = 0;
+#pragma unroll
+                        for (int hh = 0; hh < kMaxKc; ++hh)
+                            if (hh == hist) xv = vals[t + hh];
+                        A.ring[(static_cast<int64_t>(b) * A.ring_n + ((p0 + t) % A.ring_n)) * C + c] = xv;
+                    }
                 }
             }
         }
@@ -196,9 +250,17 @@ __global__ __launch_bounds__(DV * 4) void deltanet_verify_kernel(
         }
         o = o + __shfl_xor(o, 1, 64);
         o = o + __shfl_xor(o, 2, 64);
-        if (write_all || t == T - 1) {
-            const int64_t slot = (p0 + t + 1) % nslots;
-            float4* dstp = reinterpret_cast<float4*>(state + ((slot * B + b) * nv + h) * static_cast<int64_t>(DV) * DK) + tid;
+        if constexpr (REF) {
+            if (t == T - 1) {
+                float* dstp = A.state + static_cast<int64_t>(h) * DK * DV + static_cast<int64_t>(g) * GI * DV + j;
+#pragma unroll
+                for (int i = 0; i < GI; ++i) dstp[i * DV] = S[i];
+            }
+        } else if (A.write_all || t == T - 1) {
+            const int64_t slot = (p0 + t + 1) % A.nslots;
+            float4* dstp =
+                reinterpret_cast<float4*>(A.state + ((slot * A.B + b) * nv + h) * static_cast<int64_t>(DV) * DK) +
+                tid;
 #pragma unroll
             for (int m = 0; m < GI / 4; ++m)
                 dstp[m * NT] = make_float4(S[4 * m], S[4 * m + 1], S[4 * m + 2], S[4 * m + 3]);
@@ -210,7 +272,7 @@ __global__ __launch_bounds__(DV * 4) void deltanet_verify_kernel(
     // ---- gated RMSNorm: rms from the unrounded output, one wave per token ----
     for (int t = wave; t < T; t += NW) {
         const float sso = l64_sumsq_f32(os + t * DV, DV, lane);
-        if (lane == 0) s_rms[t] = 1.0f / csqrt(sso / static_cast<float>(DV) + eps);
+        if (lane == 0) s_rms[t] = 1.0f / csqrt(sso / static_cast<float>(DV) + A.eps);
     }
     __syncthreads();
 #pragma unroll
@@ -218,23 +280,75 @@ __global__ __launch_bounds__(DV * 4) void deltanet_verify_kernel(
         const int t = tid / DV + r * (NT / DV);
         if (t < T) {
             const float ob = bfr(os[t * DV + jo]);
-            out[(row0 + t) * ld_out + static_cast<int64_t>(h) * DV + jo] =
+            A.out[(row0 + t) * A.ld_out + static_cast<int64_t>(h) * DV + jo] =
                 f2bf(((ob * s_rms[t]) * nwj) * csilu(zr[r]));
         }
     }
 }
 
-template <int DK, int DV>
-int launch(uint16_t* out, int64_t ld_out, const uint16_t* proj, int64_t ld_proj, int64_t off_qkv,
-           int64_t off_z, int64_t off_a, int64_t off_b, const uint16_t* conv_w, uint16_t* ring, int ring_n,
-           float* state, int nslots, int write_all, const uint16_t* a_log, const uint16_t* dt_bias,
-           const uint16_t* norm_w, const int32_t* lens, int pos_add, int B, int T, int nk, int nv, int Kc,
-           float eps, hipStream_t s) {
-    const size_t shmem = static_cast<size_t>(T) * (2 * DK + 2 * DV) * sizeof(float);
-    deltanet_verify_kernel<DK, DV><<<dim3(nv, B), dim3(DV * 4), shmem, s>>>(
-        out, ld_out, proj, ld_proj, off_qkv, off_z, off_a, off_b, conv_w, ring, ring_n, state, nslots,
-        write_all, a_log, dt_bias, norm_w, lens, pos_add, B, T, nk, nv, Kc, eps);
-    return launched("deltanet_verify_kernel");
+// deltanet_grouped_conv_kernel (hip_kernels.hip:871-912) over the reference's
+// conv state [C][Kc-1] (oldest first): one thread per flat [Q|K|V] channel,
+// the canonical conv order of the fused kernel, state shifted in place.
+__global__ __launch_bounds__(256) void deltanet_conv_kernel(uint16_t* __restrict__ q, uint16_t* __restrict__ k,
+                                                            uint16_t* __restrict__ v, uint16_t* __restrict__ cs,
+                                                            const uint16_t* __restrict__ qkv,
+                                                            const uint16_t* __restrict__ w, int64_t T, int64_t kw,
+                                                            int64_t vw, int Kc) {
+    const int64_t C = 2 * kw + vw;
+    const int64_t c = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (c >= C) return;
+    const int hist = Kc - 1;
+    uint16_t* st = cs + c * hist;
+    float wc[kMaxKc], win[kMaxKc];
+#pragma unroll
+    for (int i = 0; i < kMaxKc; ++i) {
+        wc[i] = i < Kc ? bf2f(w[c * Kc + i]) : 0.0f;
+        win[i] = i < hist ? bf2f(st[i]) : 0.0f;
+    }
+    uint16_t* dstp;
+    int64_t ld, col;
+    if (c < kw) { dstp = q; ld = kw; col = c; }
+    else if (c < 2 * kw) { dstp = k; ld = kw; col = c - kw; }
+    else { dstp = v; ld = vw; col = c - 2 * kw; }
+    for (int64_t t = 0; t < T; ++t) {
+        const float x = bf2f(qkv[t * C + c]);
+        float acc;
+        if (hist > 0) {
+            acc = win[0] * wc[0];
+#pragma unroll
+            for (int i = 1; i < kMaxKc - 1; ++i)
+                if (i < hist) acc = fma_(win[i], wc[i], acc);
+#pragma unroll
+            for (int i = 1; i < kMaxKc; ++i)
+                if (i == hist) acc = fma_(x, wc[i], acc);
+        } else {
+            acc = x * wc[0];
+        }
+        dstp[t * ld + col] = f2bf(csilu(acc));
+#pragma unroll
+        for (int i = 0; i + 1 < kMaxKc; ++i)
+            if (i + 1 < hist) win[i] = win[i + 1];
+#pragma unroll
+        for (int i = 0; i < kMaxKc; ++i)
+            if (i == hist - 1) win[i] = x;
+    }
+#pragma unroll
+    for (int i = 0; i < kMaxKc; ++i)
+        if (i < hist) st[i] = f2bf(win[i]);
+}
+
+template <int DK, int DV, bool REF>
+int launch(const DnArgs& a, hipStream_t s) {
+    const size_t shmem = static_cast<size_t>(a.T) * (2 * DK + 2 * DV) * sizeof(float);
+    deltanet_kernel<DK, DV, REF><<<dim3(a.nv, REF ? 1 : a.B), dim3(DV * 4), shmem, s>>>(a);
+    return launched(REF ? "deltanet_recurrent_kernel" : "deltanet_verify_kernel");
+}
+
+template <bool REF>
+int dispatch(const DnArgs& a, int64_t dk, int64_t dv, hipStream_t s) {
+    if (dk == 128 && dv == 128) return launch<128, 128, REF>(a, s);
+    if (dk == 64 && dv == 64) return launch<64, 64, REF>(a, s);
+    return invalid("deltanet: (dk, dv) must be (128,128) or (64,64)");
 }
 
 }  // namespace
@@ -249,29 +363,95 @@ extern "C" int hai_deltanet_verify_bf16(void* out, int64_t ld_out, const void* p
     if (out == nullptr || proj == nullptr || conv_w == nullptr || conv_ring == nullptr || state == nullptr ||
         a_log == nullptr || dt_bias == nullptr || norm_w == nullptr)
         return invalid("deltanet_verify: null pointer");
-    if (B < 0 || T < 0 || nk <= 0 || nv <= 0 || nv % nk != 0 || Kc < 1 || Kc > 8 || nslots < 1)
+    if (B < 0 || T < 0 || nk <= 0 || nv <= 0 || nv % nk != 0 || Kc < 1 || Kc > kMaxKc || nslots < 1)
         return invalid("deltanet_verify: shape");
     if (T + Kc - 1 > ring) return invalid("deltanet_verify: conv ring too short for T");
     if (write_all_slots && nslots < T) return invalid("deltanet_verify: fewer state slots than tokens");
     if (lens == nullptr && pos_add < 0) return invalid("deltanet_verify: negative position");
     if (!aligned16(state)) return invalid("deltanet_verify: state alignment");
-    if (B == 0 || T == 0) return HAI_OK;
     if (T > kMaxT) return invalid("deltanet_verify: at most 16 tokens per launch");
-    const auto s = as_stream(stream);
-    auto* o = static_cast<uint16_t*>(out);
-    const auto* pr = static_cast<const uint16_t*>(proj);
-    const auto* cw = static_cast<const uint16_t*>(conv_w);
-    auto* rg = static_cast<uint16_t*>(conv_ring);
-    const auto* al = static_cast<const uint16_t*>(a_log);
-    const auto* db = static_cast<const uint16_t*>(dt_bias);
-    const auto* nw = static_cast<const uint16_t*>(norm_w);
-    if (dk == 128 && dv == 128)
-        return launch<128, 128>(o, ld_out, pr, ld_proj, off_qkv, off_z, off_a, off_b, cw, rg, int(ring), state,
-                                int(nslots), write_all_slots, al, db, nw, lens, pos_add, int(B), int(T), int(nk),
-                                int(nv), int(Kc), eps, s);
-    if (dk == 64 && dv == 64)
-        return launch<64, 64>(o, ld_out, pr, ld_proj, off_qkv, off_z, off_a, off_b, cw, rg, int(ring), state,
-                              int(nslots), write_all_slots, al, db, nw, lens, pos_add, int(B), int(T), int(nk),
-                              int(nv), int(Kc), eps, s);
-    return invalid("deltanet_verify: (dk, dv) must be (128,128) or (64,64)");
+    if (B == 0 || T == 0) return HAI_OK;
+    DnArgs a{};
+    a.out = static_cast<uint16_t*>(out);
+    a.ld_out = ld_out;
+    a.proj = static_cast<const uint16_t*>(proj);
+    a.ld_proj = ld_proj;
+    a.off_qkv = off_qkv;
+    a.off_z = off_z;
+    a.off_a = off_a;
+    a.off_b = off_b;
+    a.conv_w = static_cast<const uint16_t*>(conv_w);
+    a.ring = static_cast<uint16_t*>(conv_ring);
+    a.ring_n = int(ring);
+    a.nslots = int(nslots);
+    a.write_all = write_all_slots;
+    a.lens = lens;
+    a.pos_add = pos_add;
+    a.state = state;
+    a.a_log = static_cast<const uint16_t*>(a_log);
+    a.dt_bias = static_cast<const uint16_t*>(dt_bias);
+    a.norm_w = static_cast<const uint16_t*>(norm_w);
+    a.B = int(B);
+    a.T = int(T);
+    a.nk = int(nk);
+    a.nv = int(nv);
+    a.Kc = int(Kc);
+    a.eps = eps;
+    return dispatch<false>(a, dk, dv, as_stream(stream));
+}
+
+extern "C" int hai_deltanet_conv_bf16(void* q, void* k, void* v, void* conv_state, const void* qkv,
+                                      const void* conv_w, int64_t T, int64_t nk, int64_t nv, int64_t dk,
+                                      int64_t dv, int64_t Kc, void* stream) {
+    if (q == nullptr || k == nullptr || v == nullptr || qkv == nullptr || conv_w == nullptr ||
+        (Kc > 1 && conv_state == nullptr))
+        return invalid("deltanet_conv: null pointer");
+    if (T < 0 || nk <= 0 || nv <= 0 || dk <= 0 || dv <= 0 || Kc < 1 || Kc > kMaxKc)
+        return invalid("deltanet_conv: shape");
+    const int64_t kw = nk * dk, vw = nv * dv, C = 2 * kw + vw;
+    if (T == 0) return HAI_OK;
+    deltanet_conv_kernel<<<dim3(static_cast<unsigned>((C + 255) / 256)), dim3(256), 0, as_stream(stream)>>>(
+        static_cast<uint16_t*>(q), static_cast<uint16_t*>(k), static_cast<uint16_t*>(v),
+        static_cast<uint16_t*>(conv_state), static_cast<const uint16_t*>(qkv), static_cast<const uint16_t*>(conv_w),
+        T, kw, vw, int(Kc));
+    return launched("deltanet_conv_kernel");
+}
+
+extern "C" int hai_deltanet_recurrent_bf16(void* out, float* state, const void* q, const void* k, const void* v,
+                                           const void* a, const void* b, const void* a_log, const void* dt_bias,
+                                           const void* norm_w, const void* z, int64_t T, int64_t nk, int64_t nv,
+                                           int64_t dk, int64_t dv, float eps, void* stream) {
+    if (out == nullptr || state == nullptr || q == nullptr || k == nullptr || v == nullptr || a == nullptr ||
+        b == nullptr || a_log == nullptr || dt_bias == nullptr || norm_w == nullptr || z == nullptr)
+        return invalid("deltanet_recurrent: null pointer");
+    if (T < 0 || nk <= 0 || nv <= 0 || nv % nk != 0) return invalid("deltanet_recurrent: shape");
+    if (T == 0) return HAI_OK;
+    const hipStream_t s = as_stream(stream);
+    const int64_t vw = nv * dv, kw = nk * dk;
+    // the recurrence is sequential, so chunks of 16 tokens carry the state exactly
+    for (int64_t t0 = 0; t0 < T; t0 += kMaxT) {
+        const int64_t n = T - t0 < kMaxT ? T - t0 : kMaxT;
+        DnArgs d{};
+        d.out = static_cast<uint16_t*>(out) + t0 * vw;
+        d.ld_out = vw;
+        d.q = static_cast<const uint16_t*>(q) + t0 * kw;
+        d.k = static_cast<const uint16_t*>(k) + t0 * kw;
+        d.v = static_cast<const uint16_t*>(v) + t0 * vw;
+        d.a = static_cast<const uint16_t*>(a) + t0 * nv;
+        d.bv = static_cast<const uint16_t*>(b) + t0 * nv;
+        d.z = static_cast<const uint16_t*>(z) + t0 * vw;
+        d.state = state;
+        d.a_log = static_cast<const uint16_t*>(a_log);
+        d.dt_bias = static_cast<const uint16_t*>(dt_bias);
+        d.norm_w = static_cast<const uint16_t*>(norm_w);
+        d.B = 1;
+        d.T = int(n);
+        d.nk = int(nk);
+        d.nv = int(nv);
+        d.Kc = 1;
+        d.eps = eps;
+        const int rc = dispatch<true>(d, dk, dv, s);
+        if (rc != HAI_OK) return rc;
+    }
+    return HAI_OK;
 }

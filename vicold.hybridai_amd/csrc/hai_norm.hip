@@ -200,6 +200,32 @@ __global__ void embedding_kernel(uint16_t* __restrict__ y, const uint16_t* __res
         y[r * H + k] = ok ? table[id * H + k] : static_cast<uint16_t>(0);
 }
 
+// partial_rope_kernel (hip_kernels.hip:192-221): rotate-half on the first R
+// dims of every head, the rest copied; one thread per element.
+__global__ void partial_rope_kernel(uint16_t* __restrict__ dst, const uint16_t* __restrict__ src, int64_t n,
+                                    int heads, int D, int R, const float* __restrict__ rc,
+                                    const float* __restrict__ rs, int64_t rope_pos, int64_t pos0) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int d = static_cast<int>(i % D);
+        if (d >= R) {
+            dst[i] = src[i];
+            continue;
+        }
+        const int64_t head = i / D;
+        const int64_t t = head / heads;
+        int64_t pos = pos0 + t;
+        pos = pos < 0 ? 0 : (pos >= rope_pos ? rope_pos - 1 : pos);
+        const int half = R / 2;
+        const int p = d < half ? d : d - half;
+        const float* cs = rc + pos * half;
+        const float* sn = rs + pos * half;
+        const float xv = bf2f(src[head * D + p]);
+        const float yv = bf2f(src[head * D + p + half]);
+        dst[i] = f2bf(d < half ? fma_(xv, cs[p], -(yv * sn[p])) : fma_(yv, cs[p], xv * sn[p]));
+    }
+}
+
 unsigned grid_for(int64_t n) {
     const int64_t b = (n + 255) / 256;
     return static_cast<unsigned>(b < 1 ? 1 : (b > 65536 ? 65536 : b));
@@ -299,6 +325,22 @@ int hai_kv_rmsnorm_rope_append_bf16(void* k_cache, void* v_cache, int64_t cap, c
         static_cast<const uint16_t*>(k_norm), rope_cos, rope_sin, rope_positions, int(B), int(T), int(nkv),
         int(D), int(R), lens, pos_add, eps);
     return launched("kv_rmsnorm_rope_append_kernel");
+}
+
+int hai_partial_rope_bf16(void* dst, const void* src, int64_t T, int64_t heads, int64_t D, int64_t R,
+                          const float* rope_cos, const float* rope_sin, int64_t rope_positions, int64_t pos0,
+                          void* stream) {
+    if (dst == nullptr || src == nullptr || rope_cos == nullptr || rope_sin == nullptr)
+        return invalid("partial_rope: null pointer");
+    if (T < 0 || heads <= 0 || D <= 0 || R < 0 || R > D || R % 2 != 0 || rope_positions <= 0)
+        return invalid("partial_rope: shape");
+    if (pos0 < 0 || pos0 + T > rope_positions) return invalid("partial_rope: positions beyond the RoPE table");
+    const int64_t n = T * heads * D;
+    if (n == 0) return HAI_OK;
+    partial_rope_kernel<<<dim3(grid_for(n)), dim3(256), 0, as_stream(stream)>>>(
+        static_cast<uint16_t*>(dst), static_cast<const uint16_t*>(src), n, int(heads), int(D), int(R), rope_cos,
+        rope_sin, rope_positions, pos0);
+    return launched("partial_rope_kernel");
 }
 
 int hai_append_kv_bf16(void* k_cache, void* v_cache, int64_t cap, const void* k, const void* v, int64_t B,
