@@ -51,6 +51,11 @@ int hai_free(void* ptr);
 int hai_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream);
 int hai_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream);
 int hai_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream);
+/* Copy in whichever direction the two addresses imply (hipMemcpyDefault). */
+int hai_memcpy(void* dst, const void* src, size_t bytes, void* stream);
+/* Page-locked host memory (MemoryType::HostPinned buffers). */
+int hai_host_malloc(void** ptr, size_t bytes);
+int hai_host_free(void* ptr);
 int hai_memset(void* dst, int value, size_t bytes, void* stream);
 int hai_stream_create(void** stream);
 int hai_stream_destroy(void* stream);
@@ -60,6 +65,8 @@ int hai_event_create(void** event);
 int hai_event_destroy(void* event);
 int hai_event_record(void* event, void* stream);
 int hai_event_synchronize(void* event);
+/* Work queued on `stream` after this call waits for `event` (Event::wait). */
+int hai_stream_wait_event(void* stream, void* event);
 int hai_event_elapsed_ms(void* start, void* stop, float* ms);
 /* Stream capture into a replayable graph (replaces per-op launches). */
 int hai_graph_begin_capture(void* stream);

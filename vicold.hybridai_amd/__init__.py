@@ -44,6 +44,10 @@ _KERNEL_SIGS = {
     "hai_memcpy_d2h": [VP, VP, ctypes.c_size_t, VP],
     "hai_memcpy_d2d": [VP, VP, ctypes.c_size_t, VP],
     "hai_memset": [VP, ctypes.c_int, ctypes.c_size_t, VP],
+    "hai_memcpy": [VP, VP, ctypes.c_size_t, VP],
+    "hai_host_malloc": [ctypes.POINTER(VP), ctypes.c_size_t],
+    "hai_host_free": [VP],
+    "hai_stream_wait_event": [VP, VP],
     "hai_stream_create": [ctypes.POINTER(VP)],
     "hai_stream_destroy": [VP],
     "hai_stream_synchronize": [VP],

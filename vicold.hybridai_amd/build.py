@@ -72,7 +72,8 @@ def build_kernels(jobs: int = 8) -> Path:
 
 
 def build_host(jobs: int = 8) -> Path | None:
-    srcs = sorted(HOST.glob("*.cc")) if HOST.exists() else []
+    # host sources plus the standalone registries of the Backend ABI (refabi/)
+    srcs = sorted(HOST.glob("*.cc")) + sorted(HOST.glob("refabi/*.cc")) if HOST.exists() else []
     if not srcs:
         return None
     OBJ.mkdir(exist_ok=True)

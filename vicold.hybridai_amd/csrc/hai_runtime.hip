@@ -52,6 +52,20 @@ int hai_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream) {
     return check_hip(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, as_stream(stream)),
                      "hipMemcpyAsync(D2D)");
 }
+int hai_memcpy(void* dst, const void* src, size_t bytes, void* stream) {
+    return check_hip(hipMemcpyAsync(dst, src, bytes, hipMemcpyDefault, as_stream(stream)),
+                     "hipMemcpyAsync(default)");
+}
+int hai_host_malloc(void** ptr, size_t bytes) {
+    if (ptr == nullptr) return invalid("ptr");
+    const hipError_t e = hipHostMalloc(ptr, bytes == 0 ? 256 : bytes, hipHostMallocDefault);
+    if (e == hipErrorOutOfMemory) {
+        set_error("hipHostMalloc: out of memory");
+        return HAI_ERR_OUT_OF_MEMORY;
+    }
+    return check_hip(e, "hipHostMalloc");
+}
+int hai_host_free(void* ptr) { return check_hip(hipHostFree(ptr), "hipHostFree"); }
 int hai_memset(void* dst, int value, size_t bytes, void* stream) {
     return check_hip(hipMemsetAsync(dst, value, bytes, as_stream(stream)), "hipMemsetAsync");
 }
@@ -82,6 +96,10 @@ int hai_event_destroy(void* event) {
 int hai_event_record(void* event, void* stream) {
     return check_hip(hipEventRecord(reinterpret_cast<hipEvent_t>(event), as_stream(stream)),
                      "hipEventRecord");
+}
+int hai_stream_wait_event(void* stream, void* event) {
+    return check_hip(hipStreamWaitEvent(as_stream(stream), reinterpret_cast<hipEvent_t>(event), 0),
+                     "hipStreamWaitEvent");
 }
 int hai_event_synchronize(void* event) {
     return check_hip(hipEventSynchronize(reinterpret_cast<hipEvent_t>(event)), "hipEventSynchronize");
