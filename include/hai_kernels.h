@@ -108,6 +108,20 @@ int hai_gemm_rmsnorm_bf16(void* y, int64_t ldy, const void* x, int64_t ldx,
                           int64_t M, int64_t N, int64_t K, int epilogue,
                           const void* res, int64_t ld_res, void* stream);
 
+/* FP8 E4M3 weights with 128x128 fp32 block scales (QuantizedWeight,
+ * ScaleLayout::Block2D, qwen3_weights.cc:131-182), dequantized in the weight
+ * stream exactly as FP8Dequantizer::dequantize_2d (fp8_dequant.cc:12-146):
+ * w[n,k] = decode_e4m3(wq[n,k]) * scales[n/128][k/128] (fp32), then the bf16
+ * GEMM's arithmetic and epilogues.  wq is [N, K] bytes, scales
+ * [ceil(N/128)][ceil(K/128)] fp32; for HAI_EPI_SILU_MUL the rows interleave
+ * (gate_f, up_f) and scales are [2][ceil(N/2/128)][ceil(K/128)] (gate blocks,
+ * then up blocks).  K <= 32768, M <= 16 per call; x 16-byte and wq 8-byte
+ * aligned. */
+int hai_gemm_fp8_bf16(void* y, int64_t ldy, const void* x, int64_t ldx,
+                      const void* wq, const float* scales, int64_t M,
+                      int64_t N, int64_t K, int epilogue, const void* res,
+                      int64_t ld_res, void* stream);
+
 /* ------------------------------------------------------------------ norms
  * rmsnorm_kernel (hip_kernels.hip:105-137): y = x * inv * (w + offset),
  * inv = 1/sqrt(sum x^2 / H + eps).  Strided rows so the MTP concat

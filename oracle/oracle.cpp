@@ -384,4 +384,81 @@ void orc_argmax_rows(const float* x, int64_t* out, int64_t rows, int64_t cols) {
     }
 }
 
+// ---- FP8 (A15) ---------------------------------------------------------------
+// FP8Dequantizer::decode_e4m3 (fp8_dequant.cc:12-26): exponent 0 is the
+// subnormal m * 2^-9, exponents 1..15 the normal (1 + m/8) * 2^(e-7); there
+// is no NaN code (0x7F / 0xFF decode as +-480).
+float orc_fp8_decode(uint8_t v) {
+    const int e = (v >> 3) & 0xf;
+    const int m = v & 7;
+    const float r = e == 0 ? std::ldexp(static_cast<float>(m), -9)
+                           : std::ldexp(1.0f + static_cast<float>(m) / 8.0f, e - 7);
+    return (v & 0x80) ? -r : r;
+}
+
+void orc_fp8_decode_array(const uint8_t* q, float* y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = orc_fp8_decode(q[i]);
+}
+
+// Round-to-nearest-even E4M3 encoding, saturating at +-448 (code 0x7E) so the
+// +-480 codes are never produced; NaN encodes as 0.  (The quantizer of the
+// C5 synthetic weights: clamp(round(w / s), +-448).)
+void orc_fp8_encode_array(const float* x, uint8_t* q, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) {
+        const float v = x[i];
+        uint8_t sign = std::signbit(v) ? 0x80 : 0;
+        const float a = std::fabs(v);
+        uint8_t code;
+        if (std::isnan(v)) {
+            code = 0;
+            sign = 0;
+        } else if (a >= 448.0f) {
+            code = 0x7e;
+        } else if (a < std::ldexp(1.0f, -6)) {
+            // subnormal grid 2^-9; rounding up to 8 lands on the first normal (code 0x08)
+            code = static_cast<uint8_t>(std::nearbyint(a * 512.0f));
+        } else {
+            int E = 0;
+            const float f = std::frexp(a, &E);  // a = f * 2^E, f in [0.5, 1)
+            int e = E - 1 + 7;
+            int m = static_cast<int>(std::nearbyint((2.0f * f - 1.0f) * 8.0f));
+            if (m == 8) {
+                m = 0;
+                ++e;
+            }
+            code = (e > 15 || (e == 15 && m == 7)) ? uint8_t{0x7e} : static_cast<uint8_t>((e << 3) | m);
+        }
+        q[i] = sign | code;
+    }
+}
+
+// FP8Dequantizer::dequantize_2d (fp8_dequant.cc:89-146): w = decode(q) * s
+// with s[r / block_rows][c / block_cols], fp32.
+void orc_fp8_dequant_2d(const uint8_t* q, const float* s, float* w, int64_t rows, int64_t cols, int64_t br,
+                        int64_t bc) {
+    const int64_t sc = (cols + bc - 1) / bc;
+    for (int64_t r = 0; r < rows; ++r)
+        for (int64_t c = 0; c < cols; ++c)
+            w[r * cols + c] = orc_fp8_decode(q[r * cols + c]) * s[(r / br) * sc + c / bc];
+}
+
+// Linear over Block2D(128x128) FP8 weights (qwen3_weights.cc:131-182 loads
+// them; Linear::validate, linear.cc:45-50, rejects them on the reference's
+// path, so the arithmetic is the dequantized fp32 weight of dequantize_2d fed
+// to the canonical L64 dot): y[m,n] = bf16(sum_k x[m,k] * (decode(q[n,k]) *
+// s[n/128][k/128])).
+void orc_gemm_fp8(const float* x, const uint8_t* q, const float* s, float* y, int64_t M, int64_t N, int64_t K,
+                  int round_out) {
+    const int64_t sk = (K + 127) / 128;
+#pragma omp parallel
+    {
+        std::vector<float> w(static_cast<size_t>(K));
+#pragma omp for schedule(static)
+        for (int64_t n = 0; n < N; ++n) {
+            for (int64_t k = 0; k < K; ++k) w[k] = orc_fp8_decode(q[n * K + k]) * s[(n / 128) * sk + k / 128];
+            for (int64_t m = 0; m < M; ++m) y[m * N + n] = store(l64_dot(x + m * K, w.data(), K), round_out);
+        }
+    }
+}
+
 }  // extern "C"

@@ -82,6 +82,18 @@ void orc_deltanet_recurrent(const float* q, const float* k, const float* v,
 /* argmax_rows (generator.cc:325-360): first maximum, NaN never wins. */
 void orc_argmax_rows(const float* x, int64_t* out, int64_t rows, int64_t cols);
 
+/* ---- FP8 E4M3 weights (fp8_dequant.cc:12-146) ---- */
+float orc_fp8_decode(uint8_t v);
+void orc_fp8_decode_array(const uint8_t* q, float* y, int64_t n);
+/* RNE encode saturating at +-448; NaN -> 0. */
+void orc_fp8_encode_array(const float* x, uint8_t* q, int64_t n);
+void orc_fp8_dequant_2d(const uint8_t* q, const float* s, float* w, int64_t rows,
+                        int64_t cols, int64_t block_rows, int64_t block_cols);
+/* y = bf16(x . (decode(q) * s[n/128][k/128])^T), L64 order; scales are
+ * [ceil(N/128)][ceil(K/128)] fp32. */
+void orc_gemm_fp8(const float* x, const uint8_t* q, const float* s, float* y,
+                  int64_t M, int64_t N, int64_t K, int round_out);
+
 /* ---- synthetic model ---- */
 typedef struct orc_config {
     int32_t hidden;

@@ -223,6 +223,41 @@ def argmax_rows(x):
     return out
 
 
+# ---------------------------------------------------------------- FP8
+U8P = ctypes.POINTER(ctypes.c_uint8)
+
+
+def _u8(a):
+    return np.ascontiguousarray(a, dtype=np.uint8)
+
+
+def fp8_decode(q):
+    q = _u8(q); y = np.empty(q.shape, np.float32)
+    lib().orc_fp8_decode_array(q.ctypes.data_as(U8P), _f(y), ctypes.c_int64(q.size)); return y
+
+
+def fp8_encode(x):
+    x = _c32(x); q = np.empty(x.shape, np.uint8)
+    lib().orc_fp8_encode_array(_f(x), q.ctypes.data_as(U8P), ctypes.c_int64(x.size)); return q
+
+
+def fp8_dequant_2d(q, s, block_rows, block_cols):
+    q = _u8(q); s = _c32(s); rows, cols = q.shape
+    w = np.empty((rows, cols), np.float32)
+    lib().orc_fp8_dequant_2d(q.ctypes.data_as(U8P), _f(s), _f(w), ctypes.c_int64(rows), ctypes.c_int64(cols),
+                             ctypes.c_int64(block_rows), ctypes.c_int64(block_cols))
+    return w
+
+
+def gemm_fp8(x, q, s, round_out=True):
+    x = _c32(x); q = _u8(q); s = _c32(s)
+    M, K = x.shape; N = q.shape[0]
+    y = np.empty((M, N), np.float32)
+    lib().orc_gemm_fp8(_f(x), q.ctypes.data_as(U8P), _f(s), _f(y), ctypes.c_int64(M), ctypes.c_int64(N),
+                       ctypes.c_int64(K), ctypes.c_int(int(round_out)))
+    return y
+
+
 # ---------------------------------------------------------------- model
 TINY = dict(hidden=256, num_layers=4, full_attention_interval=4, num_q_heads=4, num_kv_heads=2,
             head_dim=64, rope_dim=16, lin_qk_heads=4, lin_v_heads=4, lin_k_dim=64, lin_v_dim=64,

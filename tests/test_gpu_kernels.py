@@ -462,3 +462,51 @@ def test_deltanet_recurrent_reference_layout(nk, nv, dk, T):
     assert_bits_equal(dout.download(np.uint16), out, "recurrent out")
     got_state = dstate.download(np.float32).reshape(st2.shape)
     assert np.array_equal(got_state.view(np.uint32), st2.view(np.uint32)), "recurrent state"
+
+
+# ----------------------------------------------------------------- FP8 weights
+def _fp8_weights(rng, N, K, nan_codes=False):
+    """Block-scaled E4M3 weights as the C5 config builds them: scales
+    U(0.5, 2)/448 per 128x128 block, q = clamp(round(w / s), +-448)."""
+    sb = ((N + 127) // 128, (K + 127) // 128)
+    s = (rng.uniform(0.5, 2.0, sb) / 448.0).astype(np.float32)
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    q = orc.fp8_encode(w / np.repeat(np.repeat(s, 128, 0), 128, 1)[:N, :K])
+    if nan_codes:  # the reference decodes 0x7F / 0xFF as +-480
+        q.reshape(-1)[rng.choice(q.size, 64, replace=False)] = rng.choice([0x7F, 0xFF], 64)
+    return q, s
+
+
+@pytest.mark.parametrize("M,N,K,nan_codes", [(1, 300, 256, False), (2, 1536, 5120, True), (3, 257, 1000, True),
+                                             (16, 384, 768, False), (2, 5120, 17408, False)])
+def test_gemm_fp8_store(M, N, K, nan_codes):
+    rng = np.random.default_rng(M * 31 + N + K)
+    x, xb = rand_bf16(rng, (M, K))
+    q, s = _fp8_weights(rng, N, K, nan_codes)
+    dx, dq, ds, dy = dev(xb), dev(q), dev(s), out_buf(M * N * 2)
+    hai.check(kern().hai_gemm_fp8_bf16(dy.ptr, N, dx.ptr, K, dq.ptr, ds.ptr, M, N, K, hai.EPI_STORE, None, 0, None),
+              "gemm_fp8")
+    assert_bits_equal(dy.download(np.uint16), orc.gemm_fp8(x, q, s), f"gemm_fp8 {M}x{N}x{K}")
+
+
+def test_gemm_fp8_residual_and_swiglu():
+    rng = np.random.default_rng(77)
+    M, F, K = 2, 640, 512
+    x, xb = rand_bf16(rng, (M, K))
+    # residual
+    q, s = _fp8_weights(rng, 300, K)
+    h, hb = rand_bf16(rng, (M, 300))
+    dx, dq, ds, dh = dev(xb), dev(q), dev(s), dev(hb)
+    hai.check(kern().hai_gemm_fp8_bf16(dh.ptr, 300, dx.ptr, K, dq.ptr, ds.ptr, M, 300, K, hai.EPI_RESIDUAL, dh.ptr,
+                                       300, None), "gemm_fp8 residual")
+    assert_bits_equal(dh.download(np.uint16), orc.add(h, orc.gemm_fp8(x, q, s)), "gemm_fp8 residual")
+    # SwiGLU over interleaved (gate_f, up_f) rows with per-matrix scale planes
+    qg, sg = _fp8_weights(rng, F, K, True)
+    qu, su = _fp8_weights(rng, F, K)
+    qi = np.empty((2 * F, K), np.uint8)
+    qi[0::2], qi[1::2] = qg, qu
+    dqi, dsi, dy = dev(qi), dev(np.stack([sg, su])), out_buf(M * F * 2)
+    hai.check(kern().hai_gemm_fp8_bf16(dy.ptr, F, dx.ptr, K, dqi.ptr, dsi.ptr, M, 2 * F, K, hai.EPI_SILU_MUL, None,
+                                       0, None), "gemm_fp8 silu")
+    want = orc.silu_mul(orc.gemm_fp8(x, qg, sg), orc.gemm_fp8(x, qu, su))
+    assert_bits_equal(dy.download(np.uint16), want, "gemm_fp8 silu_mul")

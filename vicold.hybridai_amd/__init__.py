@@ -64,6 +64,7 @@ _KERNEL_SIGS = {
     "hai_gemm_bf16": [VP, I64, VP, I64, VP, I64, I64, I64, ctypes.c_int, VP, I64, VP],
     "hai_gemm_rmsnorm_bf16": [VP, I64, VP, I64, VP, F32, ctypes.c_int, VP, I64, VP, I64, I64, I64, ctypes.c_int,
                               VP, I64, VP],
+    "hai_gemm_fp8_bf16": [VP, I64, VP, I64, VP, VP, I64, I64, I64, ctypes.c_int, VP, I64, VP],
     "hai_rmsnorm_bf16": [VP, I64, VP, I64, VP, I64, I64, F32, ctypes.c_int, VP],
     "hai_add_bf16": [VP, VP, VP, I64, VP],
     "hai_silu_mul_bf16": [VP, VP, VP, I64, VP],

@@ -1,0 +1,252 @@
+// hai_gemm_fp8.hip -- skinny linear layer over FP8 E4M3 weights with 128x128
+// fp32 block scales (QuantizedWeight with ScaleLayout::Block2D,
+// qwen3_weights.cc:131-182; dequantization of fp8_dequant.cc:12-146 fused
+// into the weight stream).
+//
+// Arithmetic: w = decode_e4m3(q) * s[n/128][k/128] in fp32 (the reference's
+// dequantize_2d), then the same canonical L64 fma order as the bf16 GEMM, so
+// the result equals the bf16 path run on the dequantized weights.
+//   * Lane l of a wave owns weight bytes 512c + 8l .. +7 of every chunk c
+//     (8-byte loads, the L64 element-to-lane map) and the matching 8 bf16
+//     activations (16-byte loads).
+//   * Decode: gfx950's packed E4M3 -> fp32 conversion (2 codes per
+//     instruction) agrees with the reference's decode_e4m3 on every code
+//     except 0x7F / 0xFF (NaN in OCP E4M3, +-480 in the reference); words
+//     holding those codes take an exact bit-level decode.
+//   * A block covers 8 consecutive weight rows, so all of them share one
+//     128-row scale block; the block's scale row (ceil(K/128) floats) is
+//     staged in LDS once.  With paired scales (fused SwiGLU over gate/up rows
+//     interleaved as (gate_f, up_f)) row r reads plane r & 1, block
+//     (r >> 1) / 128 of a [2][ceil(F/128)][ceil(K/128)] scale tensor.
+#include "hai_common.h"
+#include "hai_device.h"
+
+namespace {
+
+using namespace hai;
+
+constexpr int kMaxKBlocks = 256;  // K <= 32768
+
+typedef float f2v __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ u32x2 bload8(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
+}
+
+// decode_e4m3 of fp8_dequant.cc:12-26, exact for every code.
+__device__ __forceinline__ float e4m3_exact(uint32_t b) {
+    const uint32_t t = b & 0x7fu;
+    float v;
+    if (t >= 8u) {
+        v = __uint_as_float((t << 20) + 0x3c000000u);  // (1 + m/8) * 2^(e-7)
+    } else {
+        // m * 2^-9 = (1 + m/8) * 2^-6 - 2^-6, exact
+        v = __uint_as_float((t << 20) + 0x3c800000u) - 0x1p-6f;
+    }
+    return (b & 0x80u) ? -v : v;
+}
+
+// Eight consecutive codes (two little-endian words) -> floats.
+__device__ __forceinline__ void decode8(u32x2 w, float (&f)[8]) {
+    const f2v a = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w[0]), false);
+    const f2v b = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w[0]), true);
+    const f2v c = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w[1]), false);
+    const f2v d = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w[1]), true);
+    f[0] = a.x; f[1] = a.y; f[2] = b.x; f[3] = b.y;
+    f[4] = c.x; f[5] = c.y; f[6] = d.x; f[7] = d.y;
+    // a byte whose low 7 bits are all ones (0x7F / 0xFF) decodes to NaN in hardware
+    const uint32_t t0 = (w[0] & 0x7f7f7f7fu) ^ 0x7f7f7f7fu;
+    const uint32_t t1 = (w[1] & 0x7f7f7f7fu) ^ 0x7f7f7f7fu;
+    const uint32_t z = ((t0 - 0x01010101u) & ~t0) | ((t1 - 0x01010101u) & ~t1);
+    if (__builtin_expect((z & 0x80808080u) != 0u, 0)) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) f[j] = e4m3_exact((w[j >> 2] >> (8 * (j & 3))) & 0xffu);
+    }
+}
+
+template <int MB, int RW, int U, int EPI>
+__global__ __launch_bounds__(256) void gemm_fp8_kernel(uint16_t* __restrict__ y, int64_t ldy,
+                                                       const uint16_t* __restrict__ x, int64_t ldx,
+                                                       const uint8_t* __restrict__ wq,
+                                                       const float* __restrict__ scales, int paired,
+                                                       const uint16_t* res, int64_t ldres, int M, int N, int K) {
+    __shared__ float srow[2][kMaxKBlocks];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int nkb = (K + 127) / 128;
+    {
+        // this block's weight rows [8b, 8b + 8) lie in one 128-row scale block
+        const int64_t rb = static_cast<int64_t>(blockIdx.x) * 4 * RW;
+        const int64_t sblk = paired ? (rb >> 1) / 128 : rb / 128;
+        const int64_t nsb = paired ? ((N >> 1) + 127) / 128 : (N + 127) / 128;
+        for (int i = threadIdx.x; i < nkb; i += 256) {
+            srow[0][i] = scales[sblk * nkb + i];
+            if (paired) srow[1][i] = scales[(nsb + sblk) * nkb + i];
+        }
+    }
+    __syncthreads();
+    const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * 4 + wave) * RW;
+    if (row0 >= N) return;
+    const int nrows = static_cast<int>(min(static_cast<int64_t>(RW), static_cast<int64_t>(N) - row0));
+
+    // Byte offsets fit 32 bits: the caller bounds N*K and M*ldx*2 below 4 GiB.
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(wq, static_cast<uint32_t>(static_cast<int64_t>(N) * K));
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, static_cast<uint32_t>(static_cast<int64_t>(M) * ldx * 2));
+    uint32_t woff[RW], xoff[MB];
+#pragma unroll
+    for (int r = 0; r < RW; ++r) woff[r] = static_cast<uint32_t>((row0 + r) * static_cast<int64_t>(K) + lane * 8);
+#pragma unroll
+    for (int m = 0; m < MB; ++m) xoff[m] = static_cast<uint32_t>((static_cast<int64_t>(m) * ldx + lane * 8) * 2);
+
+    float acc[RW][MB];
+#pragma unroll
+    for (int r = 0; r < RW; ++r)
+#pragma unroll
+        for (int m = 0; m < MB; ++m) acc[r][m] = 0.0f;
+
+    const int nck = (K + 511) / 512;
+    const int nfull = K / 512;
+    for (int c0 = 0; c0 < nck; c0 += U) {
+        u32x2 wv[U][RW];
+        u32x4 xv[U][MB];
+        bool okv[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int c = c0 + u;
+            const bool ok = c < nfull || (c < nck && c * 512 + lane * 8 < K);
+            okv[u] = ok;
+#pragma unroll
+            for (int r = 0; r < RW; ++r)
+                wv[u][r] = bload8(rw, ok ? woff[r] : kOutOfRange, ok ? static_cast<uint32_t>(c) * 512u : 0u);
+#pragma unroll
+            for (int m = 0; m < MB; ++m)
+                xv[u][m] = bload(rx, ok ? xoff[m] : kOutOfRange, ok ? static_cast<uint32_t>(c) * 1024u : 0u);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            // scale of k-block 4c + lane/16; lanes past K multiply zeros
+            const int kb = min(4 * (c0 + u) + (lane >> 4), kMaxKBlocks - 1);
+            float xf[MB][8];
+#pragma unroll
+            for (int m = 0; m < MB; ++m)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    xf[m][2 * q] = lo_bf(xv[u][m][q]);
+                    xf[m][2 * q + 1] = hi_bf(xv[u][m][q]);
+                }
+#pragma unroll
+            for (int r = 0; r < RW; ++r) {
+                const float s = okv[u] ? srow[paired ? ((row0 + r) & 1) : 0][kb] : 0.0f;
+                float wf[8];
+                decode8(wv[u][r], wf);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float we = wf[j] * s;
+#pragma unroll
+                    for (int m = 0; m < MB; ++m) acc[r][m] = fma_(xf[m][j], we, acc[r][m]);
+                }
+            }
+        }
+    }
+
+#pragma unroll
+    for (int r = 0; r < RW; ++r)
+#pragma unroll
+        for (int m = 0; m < MB; ++m) acc[r][m] = wave_sum64(acc[r][m]);
+
+    if (EPI == HAI_EPI_SILU_MUL) {
+#pragma unroll
+        for (int p = 0; p < RW / 2; ++p)
+#pragma unroll
+            for (int m = 0; m < MB; ++m) {
+                if (lane == p * MB + m && m < M && 2 * p + 1 < nrows) {
+                    const float g = bfr(acc[2 * p][m]);
+                    const float u = bfr(acc[2 * p + 1][m]);
+                    y[static_cast<int64_t>(m) * ldy + row0 / 2 + p] = f2bf(csilu(g) * u);
+                }
+            }
+    } else {
+#pragma unroll
+        for (int r = 0; r < RW; ++r)
+#pragma unroll
+            for (int m = 0; m < MB; ++m) {
+                if (lane == r * MB + m && m < M && r < nrows) {
+                    const int64_t n = row0 + r;
+                    float v = bfr(acc[r][m]);
+                    if (EPI == HAI_EPI_RESIDUAL) v = bf2f(res[static_cast<int64_t>(m) * ldres + n]) + v;
+                    y[static_cast<int64_t>(m) * ldy + n] = f2bf(v);
+                }
+            }
+    }
+}
+
+struct Fp8Args {
+    uint16_t* y;
+    int64_t ldy;
+    const uint16_t* x;
+    int64_t ldx;
+    const uint8_t* wq;
+    const float* scales;
+    int paired;
+    const uint16_t* res;
+    int64_t ldres;
+    int M, N, K;
+};
+
+template <int MB, int EPI>
+void launch_fp8(const Fp8Args& a, hipStream_t s) {
+    constexpr int RW = 2;
+    constexpr int U = MB <= 2 ? 4 : (MB <= 8 ? 2 : 1);
+    const int64_t groups = (static_cast<int64_t>(a.N) + 4 * RW - 1) / (4 * RW);
+    gemm_fp8_kernel<MB, RW, U, EPI><<<dim3(static_cast<unsigned>(groups)), dim3(256), 0, s>>>(
+        a.y, a.ldy, a.x, a.ldx, a.wq, a.scales, a.paired, a.res, a.ldres, a.M, a.N, a.K);
+}
+
+template <int EPI>
+void dispatch_fp8(const Fp8Args& a, hipStream_t s) {
+    if (a.M <= 1) launch_fp8<1, EPI>(a, s);
+    else if (a.M <= 2) launch_fp8<2, EPI>(a, s);
+    else if (a.M <= 4) launch_fp8<4, EPI>(a, s);
+    else if (a.M <= 8) launch_fp8<8, EPI>(a, s);
+    else launch_fp8<16, EPI>(a, s);
+}
+
+}  // namespace
+
+extern "C" int hai_gemm_fp8_bf16(void* y, int64_t ldy, const void* x, int64_t ldx, const void* wq,
+                                 const float* scales, int64_t M, int64_t N, int64_t K, int epilogue,
+                                 const void* res, int64_t ld_res, void* stream) {
+    if (y == nullptr || x == nullptr || wq == nullptr || scales == nullptr)
+        return invalid("gemm_fp8: null pointer");
+    if (M < 0 || M > 16 || N < 0 || K <= 0 || K % 8 != 0 || ldx % 8 != 0 || ldx < K)
+        return invalid("gemm_fp8: shape (need 0<=M<=16, K%8==0, ldx%8==0, ldx>=K)");
+    if ((K + 127) / 128 > kMaxKBlocks) return invalid("gemm_fp8: K above 32768");
+    if ((N + 8) * K >= (int64_t{1} << 32) || M * ldx * 2 >= (int64_t{1} << 32))
+        return invalid("gemm_fp8: W or X exceeds the 4 GiB buffer-offset range");
+    if (!aligned16(x) || reinterpret_cast<uintptr_t>(wq) % 8 != 0)
+        return invalid("gemm_fp8: x must be 16-byte and wq 8-byte aligned");
+    if (M == 0 || N == 0) return HAI_OK;
+    Fp8Args a{static_cast<uint16_t*>(y), ldy, static_cast<const uint16_t*>(x), ldx,
+              static_cast<const uint8_t*>(wq), scales, 0, static_cast<const uint16_t*>(res), ld_res,
+              int(M), int(N), int(K)};
+    const hipStream_t s = as_stream(stream);
+    switch (epilogue) {
+        case HAI_EPI_STORE:
+            if (ldy < N) return invalid("gemm_fp8: ldy < N");
+            dispatch_fp8<HAI_EPI_STORE>(a, s);
+            break;
+        case HAI_EPI_RESIDUAL:
+            if (res == nullptr || ldy < N || ld_res < N) return invalid("gemm_fp8: residual operands");
+            dispatch_fp8<HAI_EPI_RESIDUAL>(a, s);
+            break;
+        case HAI_EPI_SILU_MUL:
+            if (N % 2 != 0 || ldy < N / 2) return invalid("gemm_fp8: silu_mul needs even N and ldy >= N/2");
+            a.paired = 1;
+            dispatch_fp8<HAI_EPI_SILU_MUL>(a, s);
+            break;
+        default:
+            return invalid("gemm_fp8: unknown epilogue");
+    }
+    return launched("gemm_fp8_kernel");
+}
