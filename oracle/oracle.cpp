@@ -40,14 +40,14 @@ void orc_bf16_round_array(const float* x, float* y, int64_t n) {
 }
 
 // Linear::forward_into (linear.cc:137-155) -> rocBLAS gemm_ex with fp32
-// compute and a bf16 store.  Canonical L64 order per output element.
+// compute and a bf16 store.  Canonical segmented-L64 order per output.
 void orc_gemm(const float* x, const float* w, float* y, int64_t M, int64_t N,
               int64_t K, int round_out) {
 #pragma omp parallel for schedule(static)
     for (int64_t n = 0; n < N; ++n) {
         const float* wr = w + n * K;
         for (int64_t m = 0; m < M; ++m)
-            y[m * N + n] = store(l64_dot(x + m * K, wr, K), round_out);
+            y[m * N + n] = store(gemm_dot(x + m * K, wr, K), round_out);
     }
 }
 
@@ -445,7 +445,7 @@ void orc_fp8_dequant_2d(const uint8_t* q, const float* s, float* w, int64_t rows
 // Linear over Block2D(128x128) FP8 weights (qwen3_weights.cc:131-182 loads
 // them; Linear::validate, linear.cc:45-50, rejects them on the reference's
 // path, so the arithmetic is the dequantized fp32 weight of dequantize_2d fed
-// to the canonical L64 dot): y[m,n] = bf16(sum_k x[m,k] * (decode(q[n,k]) *
+// to the canonical GEMM dot): y[m,n] = bf16(sum_k x[m,k] * (decode(q[n,k]) *
 // s[n/128][k/128])).
 void orc_gemm_fp8(const float* x, const uint8_t* q, const float* s, float* y, int64_t M, int64_t N, int64_t K,
                   int round_out) {
@@ -456,7 +456,7 @@ void orc_gemm_fp8(const float* x, const uint8_t* q, const float* s, float* y, in
 #pragma omp for schedule(static)
         for (int64_t n = 0; n < N; ++n) {
             for (int64_t k = 0; k < K; ++k) w[k] = orc_fp8_decode(q[n * K + k]) * s[(n / 128) * sk + k / 128];
-            for (int64_t m = 0; m < M; ++m) y[m * N + n] = store(l64_dot(x + m * K, w.data(), K), round_out);
+            for (int64_t m = 0; m < M; ++m) y[m * N + n] = store(gemm_dot(x + m * K, w.data(), K), round_out);
         }
     }
 }

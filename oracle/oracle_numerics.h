@@ -128,6 +128,28 @@ inline float l64_dot(const float* a, const float* b, int64_t n) {
     return butterfly64(acc);
 }
 
+// Linear-layer dot product ("segmented L64"): the L64 element-to-lane map,
+// but each lane's fma chain restarts every kGemmSeg elements and the segment
+// partials are folded in segment order before the butterfly.  Segments let
+// several GPU waves share the K range of one output (each wave owns whole
+// segments) without changing a bit; for K <= kGemmSeg it is l64_dot.
+constexpr int64_t kGemmSeg = 2048;
+inline float gemm_dot(const float* a, const float* b, int64_t n) {
+    float tot[64];
+    for (int l = 0; l < 64; ++l) tot[l] = 0.0f;
+    for (int64_t s0 = 0; s0 < n; s0 += kGemmSeg) {
+        float part[64];
+        for (int l = 0; l < 64; ++l) part[l] = 0.0f;
+        const int64_t e = s0 + kGemmSeg < n ? s0 + kGemmSeg : n;
+        for (int64_t k = s0; k < e; ++k) {
+            const int l = static_cast<int>((k >> 3) & 63);
+            part[l] = fmaf_(a[k], b[k], part[l]);
+        }
+        for (int l = 0; l < 64; ++l) tot[l] = tot[l] + part[l];
+    }
+    return butterfly64(tot);
+}
+
 // Sequential fma dot (attention scores: one lane owns one key).
 inline float seq_dot(const float* a, const float* b, int64_t n) {
     float acc = 0.0f;

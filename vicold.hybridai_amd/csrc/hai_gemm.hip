@@ -130,11 +130,22 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(
         for (int r = 0; r < RW; ++r)
             woff[r] = static_cast<uint32_t>(((row0 + r) * static_cast<int64_t>(K) + lane * 8) * 2);
 
-        float acc[RW][MB];
+        // acc: the current 2048-element segment's fma chain; tot: the segments
+        // folded in order (the canonical segmented-L64 order)
+        float acc[RW][MB], tot[RW][MB];
 #pragma unroll
         for (int r = 0; r < RW; ++r)
 #pragma unroll
-            for (int m = 0; m < MB; ++m) acc[r][m] = 0.0f;
+            for (int m = 0; m < MB; ++m) acc[r][m] = tot[r][m] = 0.0f;
+        auto fold = [&]() {
+#pragma unroll
+            for (int r = 0; r < RW; ++r)
+#pragma unroll
+                for (int m = 0; m < MB; ++m) {
+                    tot[r][m] = tot[r][m] + acc[r][m];
+                    acc[r][m] = 0.0f;
+                }
+        };
 
         auto body = [&](const u32x4 (&wv)[RW], const u32x4 (&xv)[MB]) {
 #pragma unroll
@@ -183,12 +194,15 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(
             }
 #pragma unroll
             for (int u = 0; u < U; ++u) body(wv[u], xv[u]);
+            // a segment is four 512-element chunks (U divides 4)
+            if (((c0 + U) & 3) == 0) fold();
         }
+        fold();
 
 #pragma unroll
         for (int r = 0; r < RW; ++r)
 #pragma unroll
-            for (int m = 0; m < MB; ++m) acc[r][m] = wave_sum64(acc[r][m]);
+            for (int m = 0; m < MB; ++m) acc[r][m] = wave_sum64(tot[r][m]);
 
         if (EPI == HAI_EPI_SILU_MUL) {
             // rows (2p, 2p+1) = (gate_f, up_f), output column f = row0/2 + p.

@@ -4,7 +4,7 @@
 // into the weight stream).
 //
 // Arithmetic: w = decode_e4m3(q) * s[n/128][k/128] in fp32 (the reference's
-// dequantize_2d), then the same canonical L64 fma order as the bf16 GEMM, so
+// dequantize_2d), then the same canonical segmented-L64 order as the bf16 GEMM, so
 // the result equals the bf16 path run on the dequantized weights.
 //   * Lane l of a wave owns weight bytes 512c + 8l .. +7 of every chunk c
 //     (8-byte loads, the L64 element-to-lane map) and the matching 8 bf16
@@ -99,11 +99,21 @@ __global__ __launch_bounds__(256) void gemm_fp8_kernel(uint16_t* __restrict__ y,
 #pragma unroll
     for (int m = 0; m < MB; ++m) xoff[m] = static_cast<uint32_t>((static_cast<int64_t>(m) * ldx + lane * 8) * 2);
 
-    float acc[RW][MB];
+    // acc: the current 2048-element segment; tot: segments folded in order
+    float acc[RW][MB], tot[RW][MB];
 #pragma unroll
     for (int r = 0; r < RW; ++r)
 #pragma unroll
-        for (int m = 0; m < MB; ++m) acc[r][m] = 0.0f;
+        for (int m = 0; m < MB; ++m) acc[r][m] = tot[r][m] = 0.0f;
+    auto fold = [&]() {
+#pragma unroll
+        for (int r = 0; r < RW; ++r)
+#pragma unroll
+            for (int m = 0; m < MB; ++m) {
+                tot[r][m] = tot[r][m] + acc[r][m];
+                acc[r][m] = 0.0f;
+            }
+    };
 
     const int nck = (K + 511) / 512;
     const int nfull = K / 512;
@@ -148,12 +158,15 @@ __global__ __launch_bounds__(256) void gemm_fp8_kernel(uint16_t* __restrict__ y,
                 }
             }
         }
+        // a segment is four 512-element chunks (U divides 4)
+        if (((c0 + U) & 3) == 0) fold();
     }
+    fold();
 
 #pragma unroll
     for (int r = 0; r < RW; ++r)
 #pragma unroll
-        for (int m = 0; m < MB; ++m) acc[r][m] = wave_sum64(acc[r][m]);
+        for (int m = 0; m < MB; ++m) acc[r][m] = wave_sum64(tot[r][m]);
 
     if (EPI == HAI_EPI_SILU_MUL) {
 #pragma unroll
@@ -197,7 +210,9 @@ struct Fp8Args {
 template <int MB, int EPI>
 void launch_fp8(const Fp8Args& a, hipStream_t s) {
     constexpr int RW = 2;
-    constexpr int U = MB <= 2 ? 4 : (MB <= 8 ? 2 : 1);
+    // two 512-byte chunk groups in flight measured best (M=1: 4.2-5.6 TB/s of
+    // FP8 bytes on the 27B shapes; M=2: 3.1-4.3)
+    constexpr int U = MB <= 2 ? 2 : 1;
     const int64_t groups = (static_cast<int64_t>(a.N) + 4 * RW - 1) / (4 * RW);
     gemm_fp8_kernel<MB, RW, U, EPI><<<dim3(static_cast<unsigned>(groups)), dim3(256), 0, s>>>(
         a.y, a.ldy, a.x, a.ldx, a.wq, a.scales, a.paired, a.res, a.ldres, a.M, a.N, a.K);
