@@ -85,7 +85,8 @@ def test_gemm_store(M, N, K_):
     assert_bits_equal(dy.download(np.uint16), orc.gemm(x, w), f"gemm {M}x{N}x{K_}")
 
 
-@pytest.mark.parametrize("M,N,K_", [(2, 256, 256), (4, 5120, 6144), (16, 300, 512)])
+@pytest.mark.parametrize("M,N,K_", [(2, 256, 256), (4, 5120, 6144), (16, 300, 512), (1, 5120, 6144),
+                                    (2, 5120, 17408), (1, 77, 9000), (2, 130, 8192)])
 def test_gemm_residual(M, N, K_):
     rng = np.random.default_rng(7 + M + N)
     x, xb = rand_bf16(rng, (M, K_))
@@ -98,7 +99,7 @@ def test_gemm_residual(M, N, K_):
     assert_bits_equal(dh.download(np.uint16), want, "gemm residual")
 
 
-@pytest.mark.parametrize("M,F,K_", [(2, 768, 256), (1, 17408, 5120), (5, 96, 512)])
+@pytest.mark.parametrize("M,F,K_", [(2, 768, 256), (1, 17408, 5120), (5, 96, 512), (1, 2000, 9000), (2, 300, 8192)])
 def test_gemm_silu_mul(M, F, K_):
     rng = np.random.default_rng(11 + M + F)
     x, xb = rand_bf16(rng, (M, K_))

@@ -232,6 +232,117 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(
     }
 }
 
+// K-split variant for short, wide-K layers (out / o / down projections:
+// N = 5120 rows over K up to 17408 give too few row pairs to fill the
+// GPU).  W waves share one group of RW rows; wave `sub` of the group takes
+// the 2048-element segments s = sub, sub + W, ...; each segment's lane
+// partials go to LDS and the group's first wave folds them in segment order,
+// so the result is the canonical segmented-L64 sum, bit-identical to the
+// one-wave kernel.  M <= 2 rows of x (U = 4 chunks = one segment).
+template <int MB, int RW, int W, int EPI>
+__global__ __launch_bounds__(256) void gemm_bf16_ksplit_kernel(
+    uint16_t* __restrict__ y, int64_t ldy, const uint16_t* __restrict__ x, int64_t ldx,
+    const uint16_t* __restrict__ w, const uint16_t* res, int64_t ldres, int M, int N, int K) {
+    constexpr int G = 4 / W;  // row groups per block
+    extern __shared__ float part[];  // [G][nseg][RW][MB][64]
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int g = wave / W;
+    const int sub = wave % W;
+    const int nck = (K + 511) / 512;
+    const int nfull = K / 512;
+    const int nseg = (nck + 3) / 4;
+    const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * G + g) * RW;
+    const bool active = row0 < N;
+    const int nrows = active ? static_cast<int>(min(static_cast<int64_t>(RW), static_cast<int64_t>(N) - row0)) : 0;
+    float* gpart = part + static_cast<int64_t>(g) * nseg * RW * MB * 64;
+
+    if (active) {
+        const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, static_cast<uint32_t>(static_cast<int64_t>(N) * K * 2));
+        const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, static_cast<uint32_t>(static_cast<int64_t>(M) * ldx * 2));
+        uint32_t woff[RW], xoff[MB];
+#pragma unroll
+        for (int r = 0; r < RW; ++r)
+            woff[r] = static_cast<uint32_t>(((row0 + r) * static_cast<int64_t>(K) + lane * 8) * 2);
+#pragma unroll
+        for (int m = 0; m < MB; ++m)
+            xoff[m] = static_cast<uint32_t>((static_cast<int64_t>(m) * ldx + lane * 8) * 2);
+        for (int sg = sub; sg < nseg; sg += W) {
+            u32x4 wv[4][RW];
+            u32x4 xv[4][MB];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int c = 4 * sg + u;
+                const bool ok = c < nfull || (c < nck && c * 512 + lane * 8 < K);
+                const uint32_t so = ok ? static_cast<uint32_t>(c) * 1024u : 0u;
+#pragma unroll
+                for (int r = 0; r < RW; ++r) wv[u][r] = bload(rw, ok ? woff[r] : kOutOfRange, so);
+#pragma unroll
+                for (int m = 0; m < MB; ++m) xv[u][m] = bload(rx, ok ? xoff[m] : kOutOfRange, so);
+            }
+            float acc[RW][MB];
+#pragma unroll
+            for (int r = 0; r < RW; ++r)
+#pragma unroll
+                for (int m = 0; m < MB; ++m) acc[r][m] = 0.0f;
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+#pragma unroll
+                    for (int r = 0; r < RW; ++r) {
+                        const float wa = lo_bf(wv[u][r][q]);
+                        const float wb = hi_bf(wv[u][r][q]);
+#pragma unroll
+                        for (int m = 0; m < MB; ++m) {
+                            acc[r][m] = fma_(lo_bf(xv[u][m][q]), wa, acc[r][m]);
+                            acc[r][m] = fma_(hi_bf(xv[u][m][q]), wb, acc[r][m]);
+                        }
+                    }
+                }
+#pragma unroll
+            for (int r = 0; r < RW; ++r)
+#pragma unroll
+                for (int m = 0; m < MB; ++m) gpart[((static_cast<int64_t>(sg) * RW + r) * MB + m) * 64 + lane] = acc[r][m];
+        }
+    }
+    __syncthreads();
+    if (!active || sub != 0) return;
+    float tot[RW][MB];
+#pragma unroll
+    for (int r = 0; r < RW; ++r)
+#pragma unroll
+        for (int m = 0; m < MB; ++m) {
+            float t = 0.0f;
+            for (int sg = 0; sg < nseg; ++sg) t = t + gpart[((static_cast<int64_t>(sg) * RW + r) * MB + m) * 64 + lane];
+            tot[r][m] = wave_sum64(t);
+        }
+    if (EPI == HAI_EPI_SILU_MUL) {
+#pragma unroll
+        for (int p = 0; p < RW / 2; ++p)
+#pragma unroll
+            for (int m = 0; m < MB; ++m) {
+                if (lane == p * MB + m && m < M && 2 * p + 1 < nrows) {
+                    const float gv = bfr(tot[2 * p][m]);
+                    const float uv = bfr(tot[2 * p + 1][m]);
+                    y[static_cast<int64_t>(m) * ldy + row0 / 2 + p] = f2bf(csilu(gv) * uv);
+                }
+            }
+    } else {
+#pragma unroll
+        for (int r = 0; r < RW; ++r)
+#pragma unroll
+            for (int m = 0; m < MB; ++m) {
+                if (lane == r * MB + m && m < M && r < nrows) {
+                    const int64_t n = row0 + r;
+                    float v = bfr(tot[r][m]);
+                    if (EPI == HAI_EPI_RESIDUAL) v = bf2f(res[static_cast<int64_t>(m) * ldres + n]) + v;
+                    y[static_cast<int64_t>(m) * ldy + n] = f2bf(v);
+                }
+            }
+    }
+}
+
 struct GemmArgs {
     uint16_t* y;
     int64_t ldy;
@@ -285,8 +396,34 @@ void launch_gemm(const GemmArgs& a, hipStream_t s) {
                                                                      a.ldres, a.M, a.N, a.K, a.na);
 }
 
+template <int MB, int EPI>
+void launch_ksplit(const GemmArgs& a, hipStream_t s) {
+    constexpr int RW = 2, W = 4;
+    const int nseg = ((a.K + 511) / 512 + 3) / 4;
+    const size_t shmem = static_cast<size_t>(4 / W) * nseg * RW * MB * 64 * sizeof(float);
+    const int64_t blocks = (static_cast<int64_t>(a.N) + (4 / W) * RW - 1) / ((4 / W) * RW);
+    gemm_bf16_ksplit_kernel<MB, RW, W, EPI><<<dim3(static_cast<unsigned>(blocks)), dim3(256), shmem, s>>>(
+        a.y, a.ldy, a.x, a.ldx, a.w, a.res, a.ldres, a.M, a.N, a.K);
+}
+
+// Four waves per row pair, each on its own K segments, for the short,
+// wide-K layers where that measured faster on MI355X: M <= 2 with K >= 8192
+// (down projection, +3 % at M=2, +6 % at M=1) and M = 1 with N <= 8192
+// (out / o projections, +7 %).  LDS holds the segment partials (<= 64 KB).
+bool use_ksplit(const GemmArgs& a) {
+    if (a.M > 2 || a.N > 8192) return false;
+    const int64_t nseg = ((a.K + 511) / 512 + 3) / 4;
+    if (nseg * 2 * a.M * 64 * 4 > 64 * 1024) return false;
+    return a.K >= 8192 || a.M == 1;
+}
+
 template <int EPI, bool NORM>
 void dispatch_mb(const GemmArgs& a, hipStream_t s) {
+    if (!NORM && use_ksplit(a)) {
+        if (a.M <= 1) launch_ksplit<1, EPI>(a, s);
+        else launch_ksplit<2, EPI>(a, s);
+        return;
+    }
     // Two rows per wave keeps the register footprint small enough for eight
     // waves per SIMD, which is what keeps enough bytes in flight on gfx950
     // (measured faster than 4 rows per wave or software-pipelined variants).
