@@ -245,7 +245,8 @@ def test_kv_norm_rope_append(B, T, nkv, D, R):
 # ----------------------------------------------------------------- attention
 @pytest.mark.parametrize("B,T,nq,nkv,D,lens", [
     (1, 2, 4, 2, 64, [30]), (1, 1, 4, 2, 64, [0]), (1, 4, 24, 4, 256, [60]), (1, 2, 24, 4, 256, [1278]),
-    (2, 3, 4, 1, 128, [63, 200]), (1, 16, 4, 2, 64, [100]), (3, 1, 2, 2, 64, [0, 1, 64])])
+    (2, 3, 4, 1, 128, [63, 200]), (1, 16, 4, 2, 64, [100]), (3, 1, 2, 2, 64, [0, 1, 64]),
+    (1, 4, 24, 4, 256, [4092])])  # the last: C2 micro-bench shape (cache 4096 incl. the 4 new rows)
 def test_gqa_verify(B, T, nq, nkv, D, lens):
     rng = np.random.default_rng(B * 100 + T * 10 + D + sum(lens))
     lens = np.array(lens, np.int32)
@@ -440,7 +441,7 @@ def test_deltanet_conv_reference_layout(nk, nv, dk, Kc, T):
     assert_bits_equal(dst.download(np.uint16), st2, "conv state")
 
 
-@pytest.mark.parametrize("nk,nv,dk,T", [(4, 4, 64, 3), (2, 6, 128, 21)])
+@pytest.mark.parametrize("nk,nv,dk,T", [(4, 4, 64, 3), (2, 6, 128, 21), (16, 48, 128, 4)])  # last: C2 shape
 def test_deltanet_recurrent_reference_layout(nk, nv, dk, T):
     """State [nv][dk][dv] updated in place; T > 16 runs as chained launches."""
     rng = np.random.default_rng(nk * 10 + T)
