@@ -1,0 +1,218 @@
+// generator.cc -- hybridai::Generator (include/hybrid.h:96-113) on the
+// MI355X verify engine: load_model() builds the engine, generate() runs the
+// greedy or the MTP speculative decode (GenerationOptions::
+// enable_speculative_mtp, generator.cc:545-1117) entirely on the device and
+// fills GenerationResult's counters (hybrid.h:65-94).
+//
+// What this build accepts (checkpoint IO and the tokenizer are not part of
+// it):
+//   * GeneratorOptions::model_dir = "synthetic:<tiny|27b>[?seed=S&std=X&context=C]"
+//     -- the counter-based synthetic weights shared with the CPU oracle
+//     (tiny = BASELINE config C1, 27b = the 27B shape of C3); any other path
+//     returns FileNotFound (missing) or NotImplemented (a checkpoint);
+//   * GeneratorOptions::backend = "hip" (or "mi355x");
+//   * GenerationOptions::prompt = "ids:1,2,3" -- token ids; result.text holds
+//     the generated ids in the same form.  The synthetic models have no EOS.
+#include <sys/stat.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cstdlib>
+#include <sstream>
+
+#include "engine.h"
+#include "hai_kernels.h"
+#include "refabi/hybrid_api.h"
+
+namespace hybridai {
+
+ApiStatus::ApiStatus(ApiStatusCode code, std::string message) : code_(code), message_(std::move(message)) {}
+bool ApiStatus::ok() const noexcept { return code_ == ApiStatusCode::OK; }
+ApiStatusCode ApiStatus::code() const noexcept { return code_; }
+const std::string& ApiStatus::message() const noexcept { return message_; }
+
+namespace {
+
+hai_model_config tiny_config() {
+    hai_model_config c{};
+    c.hidden = 256; c.num_layers = 4; c.full_attention_interval = 4; c.num_q_heads = 4; c.num_kv_heads = 2;
+    c.head_dim = 64; c.rope_dim = 16; c.lin_qk_heads = 4; c.lin_v_heads = 4; c.lin_k_dim = 64; c.lin_v_dim = 64;
+    c.conv_kernel = 4; c.ffn = 768; c.vocab = 4096; c.mtp_layers = 1; c.rms_eps = 1e-6f; c.rope_theta = 1e7f;
+    return c;
+}
+
+hai_model_config qwen27b_config() {
+    hai_model_config c{};
+    c.hidden = 5120; c.num_layers = 64; c.full_attention_interval = 4; c.num_q_heads = 24; c.num_kv_heads = 4;
+    c.head_dim = 256; c.rope_dim = 64; c.lin_qk_heads = 16; c.lin_v_heads = 48; c.lin_k_dim = 128;
+    c.lin_v_dim = 128; c.conv_kernel = 4; c.ffn = 17408; c.vocab = 248320; c.mtp_layers = 1; c.rms_eps = 1e-6f;
+    c.rope_theta = 1e7f;
+    return c;
+}
+
+ApiStatusCode api_code(int hai_rc) {
+    switch (hai_rc) {
+        case HAI_ERR_INVALID_ARGUMENT: return ApiStatusCode::InvalidArgument;
+        case HAI_ERR_OUT_OF_MEMORY: return ApiStatusCode::OutOfMemory;
+        case HAI_ERR_NOT_IMPLEMENTED: return ApiStatusCode::NotImplemented;
+        case HAI_ERR_INVALID_DEVICE: return ApiStatusCode::InvalidDevice;
+        default: return ApiStatusCode::BackendError;
+    }
+}
+
+// "ids:1,2,3" (commas and/or spaces) -> ids; false on anything else.
+bool parse_ids(const std::string& text, std::vector<int32_t>* ids) {
+    if (text.rfind("ids:", 0) != 0) return false;
+    std::string body = text.substr(4);
+    std::replace(body.begin(), body.end(), ',', ' ');
+    std::istringstream in(body);
+    long long v;
+    while (in >> v) {
+        if (v < 0 || v > INT32_MAX) return false;
+        ids->push_back(static_cast<int32_t>(v));
+    }
+    return in.eof() && !ids->empty();
+}
+
+}  // namespace
+
+class Generator::Impl {
+public:
+    explicit Impl(GeneratorOptions options) : options_(std::move(options)) {}
+
+    ApiStatus load() {
+        if (options_.backend != "hip" && options_.backend != "mi355x")
+            return {ApiStatusCode::NotImplemented,
+                    "this library provides the MI355X (\"hip\") backend only, not \"" + options_.backend + "\""};
+        const std::string& dir = options_.model_dir;
+        if (dir.rfind("synthetic:", 0) != 0) {
+            struct stat st{};
+            if (dir.empty() || stat(dir.c_str(), &st) != 0)
+                return {ApiStatusCode::FileNotFound, "model directory not found: " + dir};
+            return {ApiStatusCode::NotImplemented,
+                    "checkpoint loading is not part of this build; use model_dir = \"synthetic:tiny\" or "
+                    "\"synthetic:27b\""};
+        }
+        std::string spec = dir.substr(10), query;
+        if (const auto q = spec.find('?'); q != std::string::npos) {
+            query = spec.substr(q + 1);
+            spec = spec.substr(0, q);
+        }
+        if (spec == "tiny") cfg_ = tiny_config();
+        else if (spec == "27b") cfg_ = qwen27b_config();
+        else return {ApiStatusCode::InvalidModel, "unknown synthetic model \"" + spec + "\" (tiny or 27b)"};
+        uint64_t seed = 0;
+        float std_dev = 0.02f;
+        int32_t context = 4096;
+        std::istringstream qs(query);
+        for (std::string kv; std::getline(qs, kv, '&');) {
+            const auto eq = kv.find('=');
+            if (eq == std::string::npos) continue;
+            const std::string key = kv.substr(0, eq), val = kv.substr(eq + 1);
+            if (key == "seed") seed = std::strtoull(val.c_str(), nullptr, 10);
+            else if (key == "std") std_dev = std::strtof(val.c_str(), nullptr);
+            else if (key == "context") context = static_cast<int32_t>(std::strtol(val.c_str(), nullptr, 10));
+            else return {ApiStatusCode::InvalidArgument, "unknown model option \"" + key + "\""};
+        }
+        hai_engine_options eo{};
+        eo.max_context = context;
+        eo.max_verify_tokens = 16;
+        eo.device = 0;
+        eo.use_graphs = 0;
+        engine_ = std::make_unique<mi355x::Engine>(cfg_, eo);
+        if (!engine_->ok()) {
+            const std::string why = engine_->error();
+            engine_.reset();
+            return {ApiStatusCode::BackendError, "engine creation failed: " + why};
+        }
+        if (const int rc = engine_->init_synthetic(seed, std_dev); rc != HAI_OK) {
+            const std::string why = engine_->error();
+            engine_.reset();
+            return {api_code(rc), "synthetic weights: " + why};
+        }
+        context_ = context;
+        return {};
+    }
+
+    ApiStatus generate(const GenerationOptions& o, GenerationResult* result) {
+        if (result == nullptr) return {ApiStatusCode::InvalidArgument, "result must not be null"};
+        if (!engine_) return {ApiStatusCode::InvalidModel, "load_model() has not succeeded"};
+        std::vector<int32_t> prompt;
+        if (!parse_ids(o.prompt, &prompt))
+            return {ApiStatusCode::InvalidArgument,
+                    "the tokenizer is not part of this build: pass the prompt as \"ids:1,2,3\""};
+        for (int32_t id : prompt)
+            if (id >= cfg_.vocab) return {ApiStatusCode::InvalidArgument, "prompt id outside the vocabulary"};
+        if (o.max_new_tokens < 0) return {ApiStatusCode::InvalidArgument, "max_new_tokens must be >= 0"};
+        if (static_cast<int64_t>(prompt.size()) + o.max_new_tokens + 16 > context_)
+            return {ApiStatusCode::InvalidArgument, "prompt + max_new_tokens exceed the model context"};
+        *result = GenerationResult{};
+        std::vector<int32_t> out(static_cast<size_t>(std::max(1, o.max_new_tokens)));
+        int64_t n = 0;
+        hai_spec_stats st{};
+        const auto t0 = std::chrono::steady_clock::now();
+        int rc;
+        if (o.enable_speculative_mtp) {
+            rc = engine_->generate_speculative(prompt.data(), static_cast<int64_t>(prompt.size()), o.max_new_tokens,
+                                               1, nullptr, 0, nullptr, 0, out.data(), &st, nullptr, 0, &n);
+        } else {
+            rc = engine_->generate_greedy(prompt.data(), static_cast<int64_t>(prompt.size()), o.max_new_tokens,
+                                          nullptr, 0, out.data(), &n);
+        }
+        if (rc != HAI_OK) return {api_code(rc), "generation failed: " + engine_->error()};
+        result->elapsed_seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+        result->token_ids.assign(out.begin(), out.begin() + n);
+        std::ostringstream text;
+        text << "ids:";
+        for (int64_t i = 0; i < n; ++i) text << (i ? "," : "") << out[static_cast<size_t>(i)];
+        result->text = text.str();
+        result->prompt_tokens = static_cast<int64_t>(prompt.size());
+        if (o.enable_speculative_mtp) {
+            result->prefill_seconds = st.prefill_seconds;
+            result->time_to_first_token_seconds = st.prefill_seconds;
+            result->decode_seconds = st.decode_seconds;
+            result->mtp_proposed_tokens = st.proposed;
+            result->mtp_accepted_tokens = st.accepted;
+            result->mtp_acceptance_rate =
+                st.proposed > 0 ? static_cast<double>(st.accepted) / static_cast<double>(st.proposed) : 0.0;
+            result->speculative_proposal_seconds = st.draft_seconds;
+            result->speculative_verification_seconds = st.verify_seconds;
+            result->speculative_replay_seconds = st.correction_seconds;
+            result->speculative_rounds = st.rounds;
+            result->mtp_rejected_tokens = st.rejected;
+            result->mtp_correction_tokens = st.corrections;
+            result->speculative_replay_tokens = st.replay_tokens;
+            result->speculative_mtp_recovery_tokens = st.mtp_recovery_tokens;
+            result->speculative_max_proposal_width = st.max_proposal_width;
+            // rollback is by committed length: no cache is ever cloned
+        } else {
+            result->decode_seconds = result->elapsed_seconds;
+        }
+        if (result->decode_seconds > 0.0)
+            result->decode_tokens_per_second = static_cast<double>(n) / result->decode_seconds;
+        return {};
+    }
+
+    ApiStatus reset() {
+        // Every generate() starts from empty caches; the weights stay resident.
+        return {};
+    }
+
+private:
+    GeneratorOptions options_;
+    hai_model_config cfg_{};
+    int32_t context_ = 0;
+    std::unique_ptr<mi355x::Engine> engine_;
+};
+
+Generator::Generator(GeneratorOptions options) : impl_(std::make_unique<Impl>(std::move(options))) {}
+Generator::~Generator() = default;
+Generator::Generator(Generator&&) noexcept = default;
+Generator& Generator::operator=(Generator&&) noexcept = default;
+ApiStatus Generator::load_model() { return impl_->load(); }
+ApiStatus Generator::reset() { return impl_->reset(); }
+ApiStatus Generator::generate(const GenerationOptions& options, GenerationResult* result) {
+    return impl_->generate(options, result);
+}
+
+}  // namespace hybridai
