@@ -45,11 +45,18 @@ typedef struct hai_model_config {
     float rope_theta;
 } hai_model_config;
 
+/* Weight formats: every Linear bf16, or the Linears the reference loads as
+ * QuantizedWeight (qwen3_weights.cc:242-283, 347-366) stored FP8 E4M3 with
+ * 128x128 fp32 block scales (embed, lm_head, MTP fc, in_proj_a/b stay bf16). */
+#define HAI_WEIGHTS_BF16 0
+#define HAI_WEIGHTS_FP8_BLOCK128 1
+
 typedef struct hai_engine_options {
     int32_t max_context;      /* KV capacity per sequence (prompt + new + slack) */
     int32_t max_verify_tokens;/* largest k+1; also the prefill chunk (<= 16) */
     int32_t device;           /* HIP device ordinal */
     int32_t use_graphs;       /* replay captured forwards (0 = plain launches) */
+    int32_t weight_format;    /* HAI_WEIGHTS_* */
 } hai_engine_options;
 
 /* Counters of GenerationResult (include/hybrid.h:65-94) that the path fills. */
@@ -79,9 +86,12 @@ void* hai_engine_create(const hai_model_config* cfg, const hai_engine_options* o
 void hai_engine_destroy(void* engine);
 const char* hai_engine_last_error(void* engine);
 /* Fill every weight with the synthetic generator (bit-identical to the
- * oracle's orc_model_create with the same seed/std). */
+ * oracle's orc_model_create with the same seed/std; with FP8 weights, to
+ * orc_model_create + orc_model_quantize_fp8: the bf16 weight quantised with
+ * synthetic U(0.5,2)/448 block scales). */
 int hai_engine_init_synthetic(void* engine, uint64_t seed, float std_dev);
-/* Copy one weight tensor (bf16 bits, reference layout) to host memory. */
+/* Copy one bf16 weight tensor (reference layout) to host memory; -1 for an
+ * unknown id or a tensor held as FP8. */
 int64_t hai_engine_read_tensor(void* engine, uint32_t tensor_id, uint16_t* out, int64_t capacity);
 uint64_t hai_engine_weight_bytes(void* engine);
 

@@ -111,16 +111,35 @@ int hai_gemm_rmsnorm_bf16(void* y, int64_t ldy, const void* x, int64_t ldx,
 /* FP8 E4M3 weights with 128x128 fp32 block scales (QuantizedWeight,
  * ScaleLayout::Block2D, qwen3_weights.cc:131-182), dequantized in the weight
  * stream exactly as FP8Dequantizer::dequantize_2d (fp8_dequant.cc:12-146):
- * w[n,k] = decode_e4m3(wq[n,k]) * scales[n/128][k/128] (fp32), then the bf16
- * GEMM's arithmetic and epilogues.  wq is [N, K] bytes, scales
- * [ceil(N/128)][ceil(K/128)] fp32; for HAI_EPI_SILU_MUL the rows interleave
- * (gate_f, up_f) and scales are [2][ceil(N/2/128)][ceil(K/128)] (gate blocks,
- * then up blocks).  K <= 32768, M <= 16 per call; x 16-byte and wq 8-byte
- * aligned. */
+ * w[n,k] = decode_e4m3(wq[n,k]) * scales[sr(n)][k/128] (fp32), then the bf16
+ * GEMM's arithmetic and epilogues.  wq is [N, K] bytes; each scale row holds
+ * ceil(K/128) floats.  sr(n) = scale_rows[n] when scale_rows is given (rows
+ * of several checkpoint tensors concatenated, each with its own 128x128
+ * grid), else n / 128; for HAI_EPI_SILU_MUL without a map the rows
+ * interleave (gate_f, up_f) and scales are [2][ceil(N/2/128)][...] (gate
+ * blocks, then up blocks).  K <= 32768, M <= 16 per call; x 16-byte and wq
+ * 8-byte aligned. */
 int hai_gemm_fp8_bf16(void* y, int64_t ldy, const void* x, int64_t ldx,
-                      const void* wq, const float* scales, int64_t M,
-                      int64_t N, int64_t K, int epilogue, const void* res,
-                      int64_t ld_res, void* stream);
+                      const void* wq, const float* scales,
+                      const int32_t* scale_rows, int64_t M, int64_t N,
+                      int64_t K, int epilogue, const void* res, int64_t ld_res,
+                      void* stream);
+/* Block-scaled E4M3 quantisation of a bf16 weight [rows, cols] (row pitch
+ * ldw elements) into codes with row pitch ldq bytes, given its scales
+ * [ceil(rows/128)][ceil(cols/128)] fp32: q = E4M3 of the fp32 quotient w / s,
+ * rounded to nearest even and saturated at +-448 (codes 0x7F / 0xFF are
+ * never produced).  The quantiser of the synthetic FP8 checkpoints; no
+ * reference counterpart (the reference loads FP8 checkpoints as stored,
+ * qwen3_weights.cc:131-182). */
+int hai_fp8_quantize_bf16(void* q, int64_t ldq, const void* w, int64_t ldw,
+                          const float* scales, int64_t rows, int64_t cols,
+                          void* stream);
+/* Synthetic block scales s_i = (0.5 + 1.5 u_i) / 448 (fp32 arithmetic),
+ * u_i = (splitmix64(key + i) >> 40) * 2^-24, key the synthetic-weight stream
+ * key of tensor id tensor_id + 2^20: U(0.5, 2)/448 as the FP8 benchmark
+ * configuration states, bit-identical to the CPU oracle's. */
+int hai_fill_synthetic_scales_f32(float* scales, int64_t n, uint64_t seed,
+                                  uint32_t tensor_id, void* stream);
 
 /* ------------------------------------------------------------------ norms
  * rmsnorm_kernel (hip_kernels.hip:105-137): y = x * inv * (w + offset),

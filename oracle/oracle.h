@@ -140,6 +140,19 @@ void orc_synthetic_prompt(uint64_t seed, int64_t n, int64_t vocab,
 
 void* orc_model_create(const orc_config* cfg, uint64_t seed, float std_dev);
 void orc_model_destroy(void* model);
+/* Synthetic FP8 block scales of one tensor: s_i = (0.5 + 1.5 u_i) / 448 in
+ * fp32, u_i = (splitmix64(key + i) >> 40) * 2^-24 with key the stream key
+ * of id tensor_id + 2^20 (row-major over the [ceil(rows/128)][ceil(cols/128)]
+ * block grid). */
+void orc_fp8_synthetic_scales(uint64_t seed, uint32_t tensor_id, int64_t n,
+                              float* out);
+/* Turns every Linear the reference loads as a QuantizedWeight
+ * (qwen3_weights.cc:242-283, 347-366: in_proj_qkv, in_proj_z, out_proj,
+ * q/k/v/o_proj, gate/up/down_proj) into its FP8 E4M3 Block2D(128x128)
+ * form: q = encode(w / s), and the Linear then uses dequantize_2d's
+ * decode(q) * s (fp8_dequant.cc:28-146).  in_proj_a/b, conv, norms, fc,
+ * embed and lm_head stay bf16, as the reference loads them. */
+int orc_model_quantize_fp8(void* model);
 /* Copies one synthetic tensor (decoded fp32) into out; returns elements or
  * -1 when the id is unknown. */
 int64_t orc_model_tensor(void* model, uint32_t tensor_id, float* out,

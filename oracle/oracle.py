@@ -72,6 +72,8 @@ def lib():
         _lib.orc_synthetic_weight_bits.argtypes = [ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint64,
                                                    ctypes.c_float]
         _lib.orc_synthetic_prompt.argtypes = [ctypes.c_uint64, ctypes.c_int64, ctypes.c_int64, I32P]
+        _lib.orc_model_quantize_fp8.argtypes = [ctypes.c_void_p]
+        _lib.orc_fp8_synthetic_scales.argtypes = [ctypes.c_uint64, ctypes.c_uint32, ctypes.c_int64, F32P]
     return _lib
 
 
@@ -258,6 +260,12 @@ def gemm_fp8(x, q, s, round_out=True):
     return y
 
 
+def fp8_synthetic_scales(seed, tensor_id, n):
+    out = np.empty(n, np.float32)
+    lib().orc_fp8_synthetic_scales(ctypes.c_uint64(seed), ctypes.c_uint32(tensor_id), ctypes.c_int64(n), _f(out))
+    return out
+
+
 # ---------------------------------------------------------------- model
 TINY = dict(hidden=256, num_layers=4, full_attention_interval=4, num_q_heads=4, num_kv_heads=2,
             head_dim=64, rope_dim=16, lin_qk_heads=4, lin_v_heads=4, lin_k_dim=64, lin_v_dim=64,
@@ -286,10 +294,12 @@ def tensor_id(slot, kind):
 class Model:
     """Synthetic hybrid model held by the oracle."""
 
-    def __init__(self, cfg: dict, seed: int = 0, std: float = 0.02):
+    def __init__(self, cfg: dict, seed: int = 0, std: float = 0.02, fp8: bool = False):
         self.cfg = dict(cfg)
         self._c = make_config(cfg)
         self.h = lib().orc_model_create(ctypes.byref(self._c), ctypes.c_uint64(seed), ctypes.c_float(std))
+        if fp8 and lib().orc_model_quantize_fp8(self.h) != 0:
+            raise RuntimeError("orc_model_quantize_fp8 failed")
 
     def close(self):
         if self.h:

@@ -315,9 +315,67 @@ Caches fresh_caches(const Model& m) {
     return cs;
 }
 
+
+// Synthetic FP8 scales: U(0.5, 2)/448 from the top 24 bits of the stream.
+void fp8_scales(uint64_t seed, uint32_t id, int64_t n, float* out) {
+    const uint64_t key = stream_key(seed, id + (1u << 20));
+    for (int64_t i = 0; i < n; ++i) {
+        const uint64_t h = splitmix64(key + static_cast<uint64_t>(i));
+        const float u = static_cast<float>(static_cast<uint32_t>(h >> 40)) * 0x1p-24f;
+        out[i] = (0.5f + 1.5f * u) / 448.0f;
+    }
+}
+
+// One tensor [rows, cols] of the bf16 model -> decode(encode(w / s)) * s.
+void quantize_tensor(const Model& m, std::vector<float>& w, uint32_t id, int64_t rows, int64_t cols) {
+    const int64_t nbr = (rows + 127) / 128, nbc = (cols + 127) / 128;
+    std::vector<float> s(static_cast<size_t>(nbr * nbc));
+    fp8_scales(m.seed, id, nbr * nbc, s.data());
+    std::vector<float> t(static_cast<size_t>(cols));
+    std::vector<uint8_t> q(static_cast<size_t>(cols));
+    for (int64_t r = 0; r < rows; ++r) {
+        float* row = w.data() + r * cols;
+        for (int64_t c = 0; c < cols; ++c) t[c] = row[c] / s[(r / 128) * nbc + c / 128];
+        orc_fp8_encode_array(t.data(), q.data(), cols);
+        for (int64_t c = 0; c < cols; ++c) row[c] = orc_fp8_decode(q[c]) * s[(r / 128) * nbc + c / 128];
+    }
+}
+
+void quantize_layer(Model& m, Layer& L, uint32_t slot) {
+    const auto& c = m.c;
+    const int64_t H = c.hidden, F = c.ffn;
+    if (L.attn) {
+        const int64_t qw = int64_t(c.num_q_heads) * c.head_dim, kvw = int64_t(c.num_kv_heads) * c.head_dim;
+        quantize_tensor(m, L.q, tid(slot, kQProj), 2 * qw, H);
+        quantize_tensor(m, L.k, tid(slot, kKProj), kvw, H);
+        quantize_tensor(m, L.v, tid(slot, kVProj), kvw, H);
+        quantize_tensor(m, L.o, tid(slot, kOProj), H, qw);
+    } else {
+        const int64_t kw = int64_t(c.lin_qk_heads) * c.lin_k_dim, vw = int64_t(c.lin_v_heads) * c.lin_v_dim;
+        quantize_tensor(m, L.qkv, tid(slot, kInQKV), 2 * kw + vw, H);
+        quantize_tensor(m, L.z, tid(slot, kInZ), vw, H);
+        quantize_tensor(m, L.out_proj, tid(slot, kOutProj), H, vw);
+    }
+    quantize_tensor(m, L.gate, tid(slot, kGate), F, H);
+    quantize_tensor(m, L.up, tid(slot, kUp), F, H);
+    quantize_tensor(m, L.down, tid(slot, kDown), H, F);
+}
+
 }  // namespace
 
 extern "C" {
+
+void orc_fp8_synthetic_scales(uint64_t seed, uint32_t tensor_id, int64_t n, float* out) {
+    fp8_scales(seed, tensor_id, n, out);
+}
+
+int orc_model_quantize_fp8(void* model) {
+    auto* m = static_cast<Model*>(model);
+    if (m == nullptr) return 1;
+    for (size_t i = 0; i < m->layers.size(); ++i) quantize_layer(*m, m->layers[i], 2 + static_cast<uint32_t>(i));
+    for (size_t j = 0; j < m->mtp.size(); ++j) quantize_layer(*m, m->mtp[j], 1024 + static_cast<uint32_t>(j));
+    return 0;
+}
 
 uint16_t orc_synthetic_weight_bits(uint64_t seed, uint32_t tensor_id,
                                    uint64_t index, float std_dev) {

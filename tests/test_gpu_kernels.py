@@ -486,7 +486,7 @@ def test_gemm_fp8_store(M, N, K, nan_codes):
     x, xb = rand_bf16(rng, (M, K))
     q, s = _fp8_weights(rng, N, K, nan_codes)
     dx, dq, ds, dy = dev(xb), dev(q), dev(s), out_buf(M * N * 2)
-    hai.check(kern().hai_gemm_fp8_bf16(dy.ptr, N, dx.ptr, K, dq.ptr, ds.ptr, M, N, K, hai.EPI_STORE, None, 0, None),
+    hai.check(kern().hai_gemm_fp8_bf16(dy.ptr, N, dx.ptr, K, dq.ptr, ds.ptr, None, M, N, K, hai.EPI_STORE, None, 0, None),
               "gemm_fp8")
     assert_bits_equal(dy.download(np.uint16), orc.gemm_fp8(x, q, s), f"gemm_fp8 {M}x{N}x{K}")
 
@@ -499,7 +499,7 @@ def test_gemm_fp8_residual_and_swiglu():
     q, s = _fp8_weights(rng, 300, K)
     h, hb = rand_bf16(rng, (M, 300))
     dx, dq, ds, dh = dev(xb), dev(q), dev(s), dev(hb)
-    hai.check(kern().hai_gemm_fp8_bf16(dh.ptr, 300, dx.ptr, K, dq.ptr, ds.ptr, M, 300, K, hai.EPI_RESIDUAL, dh.ptr,
+    hai.check(kern().hai_gemm_fp8_bf16(dh.ptr, 300, dx.ptr, K, dq.ptr, ds.ptr, None, M, 300, K, hai.EPI_RESIDUAL, dh.ptr,
                                        300, None), "gemm_fp8 residual")
     assert_bits_equal(dh.download(np.uint16), orc.add(h, orc.gemm_fp8(x, q, s)), "gemm_fp8 residual")
     # SwiGLU over interleaved (gate_f, up_f) rows with per-matrix scale planes
@@ -508,7 +508,65 @@ def test_gemm_fp8_residual_and_swiglu():
     qi = np.empty((2 * F, K), np.uint8)
     qi[0::2], qi[1::2] = qg, qu
     dqi, dsi, dy = dev(qi), dev(np.stack([sg, su])), out_buf(M * F * 2)
-    hai.check(kern().hai_gemm_fp8_bf16(dy.ptr, F, dx.ptr, K, dqi.ptr, dsi.ptr, M, 2 * F, K, hai.EPI_SILU_MUL, None,
+    hai.check(kern().hai_gemm_fp8_bf16(dy.ptr, F, dx.ptr, K, dqi.ptr, dsi.ptr, None, M, 2 * F, K, hai.EPI_SILU_MUL, None,
                                        0, None), "gemm_fp8 silu")
     want = orc.silu_mul(orc.gemm_fp8(x, qg, sg), orc.gemm_fp8(x, qu, su))
     assert_bits_equal(dy.download(np.uint16), want, "gemm_fp8 silu_mul")
+
+
+def test_gemm_fp8_scale_rows_map():
+    """Rows of several checkpoint tensors stacked in one launch, each tensor
+    with its own 128x128 grid (row counts not multiples of 128), through the
+    per-row scale map; also a sub-range of the stack (map and codes offset)."""
+    rng = np.random.default_rng(91)
+    K = 1000
+    parts = [(200, False), (64, True), (64, False), (130, True)]
+    qs, ss, mp, g0 = [], [], [], 0
+    for rows, nan in parts:
+        q, s = _fp8_weights(rng, rows, K, nan)
+        qs.append(q); ss.append(s)
+        mp.extend(g0 + r // 128 for r in range(rows))
+        g0 += s.shape[0]
+    q = np.concatenate(qs); s = np.concatenate(ss); mp = np.array(mp, np.int32)
+    N = q.shape[0]
+    want_w = np.concatenate([orc.fp8_dequant_2d(qq, sq, 128, 128) for qq, sq in zip(qs, ss)])
+    dq, ds, dm = dev(q), dev(s), dev(mp)
+    for M in (1, 2, 5):
+        x, xb = rand_bf16(rng, (M, K))
+        dx, dy = dev(xb), out_buf(M * N * 2)
+        hai.check(kern().hai_gemm_fp8_bf16(dy.ptr, N, dx.ptr, K, dq.ptr, ds.ptr, dm.ptr, M, N, K, hai.EPI_STORE,
+                                           None, 0, None), "gemm_fp8 map")
+        assert_bits_equal(dy.download(np.uint16), orc.gemm(x, want_w), f"gemm_fp8 map M={M}")
+    # rows 264.. (the third and fourth tensors) alone
+    r0 = 264
+    x, xb = rand_bf16(rng, (2, K))
+    dx, dy = dev(xb), out_buf(2 * (N - r0) * 2)
+    hai.check(kern().hai_gemm_fp8_bf16(dy.ptr, N - r0, dx.ptr, K, dq.ptr + r0 * K, ds.ptr, dm.ptr + 4 * r0, 2,
+                                       N - r0, K, hai.EPI_STORE, None, 0, None), "gemm_fp8 map rows")
+    assert_bits_equal(dy.download(np.uint16), orc.gemm(x, want_w[r0:]), "gemm_fp8 map rows")
+
+
+@pytest.mark.parametrize("rows,cols,ldq,ldw", [(300, 200, 200, 208), (128, 1024, 2048, 1024), (1, 8, 8, 8)])
+def test_fp8_quantize_matches_oracle(rows, cols, ldq, ldw):
+    rng = np.random.default_rng(rows + cols)
+    sb = ((rows + 127) // 128, (cols + 127) // 128)
+    s = (rng.uniform(0.5, 2.0, sb) / 448.0).astype(np.float32)
+    w = rng.standard_normal((rows, cols)).astype(np.float32) * 0.02
+    # saturating, subnormal-range, zero and negative-zero entries
+    flat = w.reshape(-1)
+    flat[: min(flat.size, 6)] = [5.0, -5.0, 1e-7, -1e-7, 0.0, -0.0][: min(flat.size, 6)]
+    wb = orc.f32_to_bf16_bits(w)
+    wf = hai.bf16_to_f32(wb)
+    wpad = np.zeros((rows, ldw), np.uint16); wpad[:, :cols] = wb
+    dw, ds, dq = dev(wpad), dev(s), out_buf(rows * ldq)
+    hai.check(kern().hai_fp8_quantize_bf16(dq.ptr, ldq, dw.ptr, ldw, ds.ptr, rows, cols, None), "fp8_quantize")
+    got = dq.download(np.uint8).reshape(rows, ldq)[:, :cols]
+    want = orc.fp8_encode(wf / np.repeat(np.repeat(s, 128, 0), 128, 1)[:rows, :cols])
+    assert np.array_equal(got, want)
+
+
+def test_fp8_synthetic_scales_match_oracle():
+    for seed, tid, n in ((0, 2 * 64 + 17, 1000), (7, 1024 * 64 + 11, 333)):
+        d = out_buf(n * 4)
+        hai.check(kern().hai_fill_synthetic_scales_f32(d.ptr, n, seed, tid, None), "fill_scales")
+        assert np.array_equal(d.download(np.float32), orc.fp8_synthetic_scales(seed, tid, n))

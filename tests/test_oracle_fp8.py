@@ -75,3 +75,52 @@ def test_gemm_fp8_equals_dequantized_gemm(M, N, K):
     assert np.array_equal(got, orc.gemm(x, orc.fp8_dequant_2d(q, s, 128, 128)))
     ref = x.astype(np.float64) @ (orc.fp8_decode(q).astype(np.float64) * srow).T
     assert np.allclose(got, ref, rtol=1e-2, atol=1e-3)
+
+
+def test_synthetic_scales_are_uniform_half_to_two_over_448():
+    s = orc.fp8_synthetic_scales(0, 2 * 64 + 17, 200000).astype(np.float64) * 448.0
+    assert s.min() >= 0.5 and s.max() < 2.0
+    # U(0.5, 2): mean 1.25, variance 1.5^2 / 12, deciles evenly spaced
+    assert abs(s.mean() - 1.25) < 0.005 and abs(s.var() - 0.1875) < 0.003
+    dec = np.quantile(s, np.linspace(0.1, 0.9, 9))
+    assert np.allclose(dec, 0.5 + 1.5 * np.linspace(0.1, 0.9, 9), atol=0.01)
+    # independent streams per tensor and seed, reproducible
+    assert np.array_equal(orc.fp8_synthetic_scales(0, 145, 64), orc.fp8_synthetic_scales(0, 145, 64))
+    assert not np.array_equal(orc.fp8_synthetic_scales(0, 145, 64), orc.fp8_synthetic_scales(1, 145, 64))
+    assert not np.array_equal(orc.fp8_synthetic_scales(0, 145, 64), orc.fp8_synthetic_scales(0, 146, 64))
+
+
+def test_fp8_model_quantizes_exactly_the_quantized_weight_linears():
+    """orc_model_quantize_fp8 on the tiny config: the Linears the reference
+    loads as QuantizedWeight become dequantize_2d(encode(w / s), s) on their
+    own 128x128 grid; every other tensor keeps its bf16 value."""
+    cfg = orc.TINY
+    bf = orc.Model(cfg, seed=5)
+    q8 = orc.Model(cfg, seed=5, fp8=True)
+    H, F = cfg["hidden"], cfg["ffn"]
+    qw, kvw = cfg["num_q_heads"] * cfg["head_dim"], cfg["num_kv_heads"] * cfg["head_dim"]
+    vw = cfg["lin_v_heads"] * cfg["lin_v_dim"]
+    C = 2 * cfg["lin_qk_heads"] * cfg["lin_k_dim"] + vw
+    shapes = {2: (C, H), 3: (vw, H), 10: (H, vw), 11: (2 * qw, H), 12: (kvw, H), 13: (kvw, H), 14: (H, qw),
+              17: (F, H), 18: (F, H), 19: (H, F)}
+    n_quant = 0
+    for slot in (0, 1, 2, 3, 4, 5, 1024):
+        for kind in range(20):
+            tid = slot * 64 + kind
+            try:
+                w = bf.tensor(tid)
+            except KeyError:
+                continue
+            got = q8.tensor(tid)
+            if slot >= 2 and kind in shapes:
+                rows, cols = shapes[kind]
+                sb = ((rows + 127) // 128, (cols + 127) // 128)
+                s = orc.fp8_synthetic_scales(5, tid, sb[0] * sb[1]).reshape(sb)
+                wq = orc.fp8_encode(w.reshape(rows, cols) / np.repeat(np.repeat(s, 128, 0), 128, 1)[:rows, :cols])
+                assert np.array_equal(got.reshape(rows, cols), orc.fp8_dequant_2d(wq, s, 128, 128)), tid
+                assert not np.array_equal(got, w)
+                n_quant += 1
+            else:
+                assert np.array_equal(got, w), tid
+    assert n_quant == 3 * 6 + 2 * 7   # 3 DeltaNet layers x 6, attention + MTP layer x 7
+    bf.close(); q8.close()

@@ -13,11 +13,13 @@
 //     instruction) agrees with the reference's decode_e4m3 on every code
 //     except 0x7F / 0xFF (NaN in OCP E4M3, +-480 in the reference); words
 //     holding those codes take an exact bit-level decode.
-//   * A block covers 8 consecutive weight rows, so all of them share one
-//     128-row scale block; the block's scale row (ceil(K/128) floats) is
-//     staged in LDS once.  With paired scales (fused SwiGLU over gate/up rows
-//     interleaved as (gate_f, up_f)) row r reads plane r & 1, block
-//     (r >> 1) / 128 of a [2][ceil(F/128)][ceil(K/128)] scale tensor.
+//   * The scale row (ceil(K/128) floats) of each of a block's 8 weight rows
+//     is staged in LDS once: row r reads scale row scale_rows[r] when the
+//     caller passes that map (projections of several checkpoint tensors
+//     concatenated, each with its own 128x128 grid), else r / 128; with
+//     paired scales (fused SwiGLU over gate/up rows interleaved as
+//     (gate_f, up_f)) row r reads plane r & 1, block (r >> 1) / 128 of a
+//     [2][ceil(F/128)][ceil(K/128)] scale tensor.
 #include "hai_common.h"
 #include "hai_device.h"
 
@@ -69,20 +71,25 @@ template <int MB, int RW, int U, int EPI>
 __global__ __launch_bounds__(256) void gemm_fp8_kernel(uint16_t* __restrict__ y, int64_t ldy,
                                                        const uint16_t* __restrict__ x, int64_t ldx,
                                                        const uint8_t* __restrict__ wq,
-                                                       const float* __restrict__ scales, int paired,
+                                                       const float* __restrict__ scales,
+                                                       const int32_t* __restrict__ scale_rows, int paired,
                                                        const uint16_t* res, int64_t ldres, int M, int N, int K) {
-    __shared__ float srow[2][kMaxKBlocks];
+    constexpr int BR = 4 * RW;  // weight rows per block
+    __shared__ float srow[BR][kMaxKBlocks];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int nkb = (K + 127) / 128;
     {
-        // this block's weight rows [8b, 8b + 8) lie in one 128-row scale block
-        const int64_t rb = static_cast<int64_t>(blockIdx.x) * 4 * RW;
-        const int64_t sblk = paired ? (rb >> 1) / 128 : rb / 128;
-        const int64_t nsb = paired ? ((N >> 1) + 127) / 128 : (N + 127) / 128;
-        for (int i = threadIdx.x; i < nkb; i += 256) {
-            srow[0][i] = scales[sblk * nkb + i];
-            if (paired) srow[1][i] = scales[(nsb + sblk) * nkb + i];
+        // the scale row of each of this block's weight rows: the caller's map,
+        // or the 128-row block of a plain / paired (gate, up) layout
+        const int64_t rb = static_cast<int64_t>(blockIdx.x) * BR;
+        const int64_t nsb = ((N >> 1) + 127) / 128;
+        for (int i = threadIdx.x; i < BR * nkb; i += 256) {
+            const int rl = i / nkb;
+            const int kb = i - rl * nkb;
+            const int64_t r = min(rb + rl, static_cast<int64_t>(N) - 1);
+            const int64_t sr = scale_rows ? scale_rows[r] : (paired ? (r & 1) * nsb + (r >> 1) / 128 : r / 128);
+            srow[rl][kb] = scales[sr * nkb + kb];
         }
     }
     __syncthreads();
@@ -147,7 +154,7 @@ __global__ __launch_bounds__(256) void gemm_fp8_kernel(uint16_t* __restrict__ y,
                 }
 #pragma unroll
             for (int r = 0; r < RW; ++r) {
-                const float s = okv[u] ? srow[paired ? ((row0 + r) & 1) : 0][kb] : 0.0f;
+                const float s = okv[u] ? srow[wave * RW + r][kb] : 0.0f;
                 float wf[8];
                 decode8(wv[u][r], wf);
 #pragma unroll
@@ -201,6 +208,7 @@ struct Fp8Args {
     int64_t ldx;
     const uint8_t* wq;
     const float* scales;
+    const int32_t* scale_rows;
     int paired;
     const uint16_t* res;
     int64_t ldres;
@@ -215,7 +223,7 @@ void launch_fp8(const Fp8Args& a, hipStream_t s) {
     constexpr int U = MB <= 2 ? 2 : 1;
     const int64_t groups = (static_cast<int64_t>(a.N) + 4 * RW - 1) / (4 * RW);
     gemm_fp8_kernel<MB, RW, U, EPI><<<dim3(static_cast<unsigned>(groups)), dim3(256), 0, s>>>(
-        a.y, a.ldy, a.x, a.ldx, a.wq, a.scales, a.paired, a.res, a.ldres, a.M, a.N, a.K);
+        a.y, a.ldy, a.x, a.ldx, a.wq, a.scales, a.scale_rows, a.paired, a.res, a.ldres, a.M, a.N, a.K);
 }
 
 template <int EPI>
@@ -227,11 +235,55 @@ void dispatch_fp8(const Fp8Args& a, hipStream_t s) {
     else launch_fp8<16, EPI>(a, s);
 }
 
+// E4M3 code of v, rounded to nearest even, saturated at +-448; NaN -> 0.
+__device__ __forceinline__ uint32_t e4m3_encode(float v) {
+    const uint32_t b = __float_as_uint(v);
+    const uint32_t sign = (b >> 24) & 0x80u;
+    const uint32_t a = b & 0x7fffffffu;
+    if (a > 0x7f800000u) return 0u;
+    if (a >= 0x43e00000u) return sign | 0x7eu;  // |v| >= 448
+    if (a < 0x3c800000u) {
+        // below 2^-6: multiples of 2^-9 (a * 512 is exact); 8 is code 0x08 = 2^-6
+        return sign | static_cast<uint32_t>(__builtin_rintf(__uint_as_float(a) * 512.0f));
+    }
+    // normal: biased exponent 1..15, three mantissa bits; a carry out of the
+    // mantissa moves to the next binade
+    const uint32_t m = a & 0x7fffffu;
+    uint32_t code = ((((a >> 23) - 127u + 7u)) << 3) | (m >> 20);
+    const uint32_t rem = m & 0xfffffu;
+    if (rem > 0x80000u || (rem == 0x80000u && (code & 1u))) ++code;
+    return sign | min(code, 0x7eu);
+}
+
+__global__ void fp8_quantize_kernel(uint8_t* __restrict__ q, int64_t ldq, const uint16_t* __restrict__ w,
+                                    int64_t ldw, const float* __restrict__ scales, int64_t rows, int64_t cols) {
+    const int64_t nkb = (cols + 127) / 128;
+    const int64_t n = rows * cols;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int64_t r = i / cols;
+        const int64_t c = i - r * cols;
+        const float s = scales[(r / 128) * nkb + c / 128];
+        q[r * ldq + c] = static_cast<uint8_t>(e4m3_encode(bf2f(w[r * ldw + c]) / s));
+    }
+}
+
 }  // namespace
 
+extern "C" int hai_fp8_quantize_bf16(void* q, int64_t ldq, const void* w, int64_t ldw, const float* scales,
+                                     int64_t rows, int64_t cols, void* stream) {
+    if (q == nullptr || w == nullptr || scales == nullptr) return invalid("fp8_quantize: null pointer");
+    if (rows < 0 || cols < 0 || ldq < cols || ldw < cols) return invalid("fp8_quantize: shape");
+    if (rows == 0 || cols == 0) return HAI_OK;
+    const int64_t blocks = std::min<int64_t>((rows * cols + 255) / 256, 65536);
+    fp8_quantize_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0, as_stream(stream)>>>(
+        static_cast<uint8_t*>(q), ldq, static_cast<const uint16_t*>(w), ldw, scales, rows, cols);
+    return launched("fp8_quantize_kernel");
+}
+
 extern "C" int hai_gemm_fp8_bf16(void* y, int64_t ldy, const void* x, int64_t ldx, const void* wq,
-                                 const float* scales, int64_t M, int64_t N, int64_t K, int epilogue,
-                                 const void* res, int64_t ld_res, void* stream) {
+                                 const float* scales, const int32_t* scale_rows, int64_t M, int64_t N,
+                                 int64_t K, int epilogue, const void* res, int64_t ld_res, void* stream) {
     if (y == nullptr || x == nullptr || wq == nullptr || scales == nullptr)
         return invalid("gemm_fp8: null pointer");
     if (M < 0 || M > 16 || N < 0 || K <= 0 || K % 8 != 0 || ldx % 8 != 0 || ldx < K)
@@ -243,7 +295,7 @@ extern "C" int hai_gemm_fp8_bf16(void* y, int64_t ldy, const void* x, int64_t ld
         return invalid("gemm_fp8: x must be 16-byte and wq 8-byte aligned");
     if (M == 0 || N == 0) return HAI_OK;
     Fp8Args a{static_cast<uint16_t*>(y), ldy, static_cast<const uint16_t*>(x), ldx,
-              static_cast<const uint8_t*>(wq), scales, 0, static_cast<const uint16_t*>(res), ld_res,
+              static_cast<const uint8_t*>(wq), scales, scale_rows, 0, static_cast<const uint16_t*>(res), ld_res,
               int(M), int(N), int(K)};
     const hipStream_t s = as_stream(stream);
     switch (epilogue) {

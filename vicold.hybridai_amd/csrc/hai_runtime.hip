@@ -160,6 +160,17 @@ __global__ void fill_synthetic_kernel(uint16_t* __restrict__ dst, int64_t rows, 
     }
 }
 
+// Synthetic FP8 block scales: (0.5 + 1.5 u) / 448, u the top 24 bits of the
+// stream value (exact in fp32).
+__global__ void fill_scales_kernel(float* __restrict__ dst, int64_t n, uint64_t key) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const uint64_t h = splitmix64(key + static_cast<uint64_t>(i));
+        const float u = static_cast<float>(static_cast<uint32_t>(h >> 40)) * 0x1p-24f;
+        dst[i] = (0.5f + 1.5f * u) / 448.0f;
+    }
+}
+
 __global__ void debug_math_kernel(float* y, const float* x, int64_t n, int fn) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (i >= n) return;
@@ -200,6 +211,16 @@ int hai_fill_synthetic_bf16(void* dst, int64_t rows, int64_t cols, int64_t ld, u
     fill_synthetic_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0, as_stream(stream)>>>(
         static_cast<uint16_t*>(dst), rows, cols, ld, key, scale);
     return launched("fill_synthetic_kernel");
+}
+
+int hai_fill_synthetic_scales_f32(float* scales, int64_t n, uint64_t seed, uint32_t tensor_id, void* stream) {
+    if (scales == nullptr || n < 0 || tensor_id >= 0xfff00000u) return invalid("fill_synthetic_scales");
+    if (n == 0) return HAI_OK;
+    const uint32_t sid = tensor_id + (1u << 20);
+    const uint64_t key = host_splitmix64(seed ^ (static_cast<uint64_t>(sid) << 32));
+    const int64_t blocks = std::min<int64_t>((n + 255) / 256, 65536);
+    fill_scales_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0, as_stream(stream)>>>(scales, n, key);
+    return launched("fill_scales_kernel");
 }
 
 int hai_debug_math_f32(float* y, const float* x, int64_t n, int fn, void* stream) {

@@ -19,9 +19,12 @@ class ModelConfig(ctypes.Structure):
         "mtp_layers")] + [("rms_eps", ctypes.c_float), ("rope_theta", ctypes.c_float)]
 
 
+WEIGHTS_BF16, WEIGHTS_FP8_BLOCK128 = 0, 1
+
+
 class EngineOptions(ctypes.Structure):
     _fields_ = [("max_context", ctypes.c_int32), ("max_verify_tokens", ctypes.c_int32),
-                ("device", ctypes.c_int32), ("use_graphs", ctypes.c_int32)]
+                ("device", ctypes.c_int32), ("use_graphs", ctypes.c_int32), ("weight_format", ctypes.c_int32)]
 
 
 class SpecStats(ctypes.Structure):
@@ -85,12 +88,14 @@ class Engine:
     """One verify engine on one GPU (synthetic weights)."""
 
     def __init__(self, cfg: dict, max_context: int, max_verify_tokens: int = 16, device: int = 0,
-                 use_graphs: bool = False):
+                 use_graphs: bool = False, fp8: bool = False):
         from . import host
         self.lib = host()
         self.cfg = dict(cfg)
+        self.fp8 = fp8
         c = ModelConfig(**cfg)
-        o = EngineOptions(max_context, max_verify_tokens, device, int(use_graphs))
+        o = EngineOptions(max_context, max_verify_tokens, device, int(use_graphs),
+                          WEIGHTS_FP8_BLOCK128 if fp8 else WEIGHTS_BF16)
         self.h = self.lib.hai_engine_create(ctypes.byref(c), ctypes.byref(o))
         if not self.h:
             raise RuntimeError("hai_engine_create: " + self.lib.hai_engine_last_error(None).decode())

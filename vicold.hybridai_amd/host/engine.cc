@@ -86,6 +86,7 @@ Engine::Engine(const hai_model_config& cfg, const hai_engine_options& opt) : cfg
     ring_ = 32;
     nslots_ = tmax_ + 1;
     use_graphs_ = opt.use_graphs != 0;
+    fp8_ = opt.weight_format == HAI_WEIGHTS_FP8_BLOCK128;
     draft_graphs_.assign(static_cast<size_t>(tmax_), nullptr);
     verify_graphs_.assign(static_cast<size_t>(tmax_ + 1), nullptr);
     if (cfg.hidden <= 0 || cfg.hidden % 8 != 0 || cfg.num_layers <= 0 || cfg.full_attention_interval <= 0 ||
@@ -94,6 +95,10 @@ Engine::Engine(const hai_model_config& cfg, const hai_engine_options& opt) : cfg
         cfg.rope_dim > cfg.head_dim || cfg.rope_dim % 2 != 0 || cfg.conv_kernel < 2 || cfg.conv_kernel > 8 ||
         d_.vw % 8 != 0 || d_.qw % 8 != 0) {
         error_ = "unsupported model configuration";
+        return;
+    }
+    if (opt.weight_format != HAI_WEIGHTS_BF16 && opt.weight_format != HAI_WEIGHTS_FP8_BLOCK128) {
+        error_ = "unknown weight_format";
         return;
     }
     if (hai_set_device(opt.device) != HAI_OK || hai_stream_create(&stream_) != HAI_OK) {
@@ -132,40 +137,93 @@ int Engine::alloc_all() {
     // ---- weights ----
     auto carve_weights = [&](Carver& cv) {
         tensors_.clear();
+        quant_.clear();
+        maps_.clear();
         auto add = [&](uint16_t*& dst, uint32_t id, int64_t rows, int64_t cols) {
             dst = cv.take<uint16_t>(static_cast<size_t>(rows * cols));
             tensors_.push_back({id, dst, rows, cols, cols});
+        };
+        // FP8 matrix [sum rows, K] made of checkpoint tensors stacked
+        // (interleave: row r of part i is stored row r * nparts + i).
+        struct Part {
+            uint32_t id;
+            int64_t rows;
+        };
+        auto fp8mat = [&](Fp8Linear& f, int64_t K, std::vector<Part> parts, bool interleave) {
+            const int64_t nkb = (K + 127) / 128;
+            const int64_t np = static_cast<int64_t>(parts.size());
+            int64_t total = 0, grid = 0;
+            for (const auto& p : parts) {
+                total += p.rows;
+                grid += (p.rows + 127) / 128;
+            }
+            f.q = cv.take<uint8_t>(static_cast<size_t>(total * K));
+            f.s = cv.take<float>(static_cast<size_t>(grid * nkb));
+            f.map = cv.take<int32_t>(static_cast<size_t>(total));
+            if (f.q == nullptr) return;  // sizing pass
+            std::vector<int32_t> map(static_cast<size_t>(total));
+            int64_t row0 = 0, g0 = 0;
+            for (int64_t i = 0; i < np; ++i) {
+                const Part& p = parts[static_cast<size_t>(i)];
+                for (int64_t r = 0; r < p.rows; ++r)
+                    map[static_cast<size_t>(interleave ? r * np + i : row0 + r)] = static_cast<int32_t>(g0 + r / 128);
+                quant_.push_back({p.id, interleave ? f.q + i * K : f.q + row0 * K, interleave ? np * K : K,
+                                  f.s + g0 * nkb, p.rows, K});
+                row0 += p.rows;
+                g0 += (p.rows + 127) / 128;
+            }
+            maps_.emplace_back(f.map, std::move(map));
         };
         auto layer = [&](LayerWeights& L, uint32_t slot) {
             add(L.in_ln, tid(slot, kInputLN), 1, H);
             add(L.post_ln, tid(slot, kPostLN), 1, H);
             if (L.attn) {
-                L.w_qkv = cv.take<uint16_t>(static_cast<size_t>(d.Nqkv * H));
-                tensors_.push_back({tid(slot, kQProj), L.w_qkv, 2 * d.qw, H, H});
-                tensors_.push_back({tid(slot, kKProj), L.w_qkv ? L.w_qkv + 2 * d.qw * H : nullptr, d.kvw, H, H});
-                tensors_.push_back({tid(slot, kVProj), L.w_qkv ? L.w_qkv + (2 * d.qw + d.kvw) * H : nullptr,
-                                    d.kvw, H, H});
+                if (fp8_) {
+                    fp8mat(L.f_qkv, H, {{tid(slot, kQProj), 2 * d.qw}, {tid(slot, kKProj), d.kvw},
+                                        {tid(slot, kVProj), d.kvw}}, false);
+                } else {
+                    L.w_qkv = cv.take<uint16_t>(static_cast<size_t>(d.Nqkv * H));
+                    tensors_.push_back({tid(slot, kQProj), L.w_qkv, 2 * d.qw, H, H});
+                    tensors_.push_back(
+                        {tid(slot, kKProj), L.w_qkv ? L.w_qkv + 2 * d.qw * H : nullptr, d.kvw, H, H});
+                    tensors_.push_back({tid(slot, kVProj), L.w_qkv ? L.w_qkv + (2 * d.qw + d.kvw) * H : nullptr,
+                                        d.kvw, H, H});
+                }
                 add(L.q_norm, tid(slot, kQNorm), 1, d.D);
                 add(L.k_norm, tid(slot, kKNorm), 1, d.D);
-                add(L.w_o, tid(slot, kOProj), H, d.qw);
+                if (fp8_) fp8mat(L.f_o, d.qw, {{tid(slot, kOProj), H}}, false);
+                else add(L.w_o, tid(slot, kOProj), H, d.qw);
             } else {
-                L.w_in = cv.take<uint16_t>(static_cast<size_t>(d.Nin * H));
-                uint16_t* b = L.w_in;
-                auto at = [&](int64_t row) { return b ? b + row * H : nullptr; };
-                tensors_.push_back({tid(slot, kInQKV), at(0), d.C, H, H});
-                tensors_.push_back({tid(slot, kInZ), at(d.C), d.vw, H, H});
-                tensors_.push_back({tid(slot, kInA), at(d.C + d.vw), d.nv, H, H});
-                tensors_.push_back({tid(slot, kInB), at(d.C + d.vw + d.nv), d.nv, H, H});
+                if (fp8_) {
+                    fp8mat(L.f_in, H, {{tid(slot, kInQKV), d.C}, {tid(slot, kInZ), d.vw}}, false);
+                    L.w_ab = cv.take<uint16_t>(static_cast<size_t>(2 * d.nv * H));
+                    tensors_.push_back({tid(slot, kInA), L.w_ab, d.nv, H, H});
+                    tensors_.push_back({tid(slot, kInB), L.w_ab ? L.w_ab + d.nv * H : nullptr, d.nv, H, H});
+                } else {
+                    L.w_in = cv.take<uint16_t>(static_cast<size_t>(d.Nin * H));
+                    uint16_t* b = L.w_in;
+                    auto at = [&](int64_t row) { return b ? b + row * H : nullptr; };
+                    tensors_.push_back({tid(slot, kInQKV), at(0), d.C, H, H});
+                    tensors_.push_back({tid(slot, kInZ), at(d.C), d.vw, H, H});
+                    tensors_.push_back({tid(slot, kInA), at(d.C + d.vw), d.nv, H, H});
+                    tensors_.push_back({tid(slot, kInB), at(d.C + d.vw + d.nv), d.nv, H, H});
+                }
                 add(L.conv_w, tid(slot, kConv), d.C, d.Kc);
                 add(L.a_log, tid(slot, kALog), 1, d.nv);
                 add(L.dt_bias, tid(slot, kDtBias), 1, d.nv);
                 add(L.lin_norm, tid(slot, kLinNorm), 1, d.dv);
-                add(L.w_out, tid(slot, kOutProj), H, d.vw);
+                if (fp8_) fp8mat(L.f_out, d.vw, {{tid(slot, kOutProj), H}}, false);
+                else add(L.w_out, tid(slot, kOutProj), H, d.vw);
             }
-            L.w_gu = cv.take<uint16_t>(static_cast<size_t>(2 * d.F * H));
-            tensors_.push_back({tid(slot, kGate), L.w_gu, d.F, H, 2 * H});
-            tensors_.push_back({tid(slot, kUp), L.w_gu ? L.w_gu + H : nullptr, d.F, H, 2 * H});
-            add(L.w_down, tid(slot, kDown), H, d.F);
+            if (fp8_) {
+                fp8mat(L.f_gu, H, {{tid(slot, kGate), d.F}, {tid(slot, kUp), d.F}}, true);
+                fp8mat(L.f_down, d.F, {{tid(slot, kDown), H}}, false);
+            } else {
+                L.w_gu = cv.take<uint16_t>(static_cast<size_t>(2 * d.F * H));
+                tensors_.push_back({tid(slot, kGate), L.w_gu, d.F, H, 2 * H});
+                tensors_.push_back({tid(slot, kUp), L.w_gu ? L.w_gu + H : nullptr, d.F, H, 2 * H});
+                add(L.w_down, tid(slot, kDown), H, d.F);
+            }
         };
         add(embed_, tid(kSlotShared, 0), d.V, H);
         add(final_norm_, tid(kSlotShared, 1), 1, H);
@@ -184,6 +242,10 @@ int Engine::alloc_all() {
         HAI_TRY(hai_malloc(&weights_, weight_bytes_));
         Carver real(static_cast<char*>(weights_));
         carve_weights(real);
+        for (const auto& m : maps_)
+            HAI_TRY(hai_memcpy_h2d(m.first, m.second.data(), m.second.size() * 4, stream_));
+        HAI_TRY(sync());
+        maps_.clear();
     }
 
     // ---- caches ----
@@ -284,7 +346,26 @@ int Engine::read_i64(const int64_t* d, int64_t* h, int64_t n) {
 int Engine::init_synthetic(uint64_t seed, float std_dev) {
     for (const auto& t : tensors_)
         HAI_TRY(hai_fill_synthetic_bf16(t.ptr, t.rows, t.cols, t.ld, seed, t.id, std_dev, stream_));
-    return sync();
+    if (quant_.empty()) return sync();
+    // FP8 tensors: the bf16 synthetic tensor in a staging buffer, its block
+    // scales, then the quantised codes into the stored layout.
+    int64_t most = 0;
+    for (const auto& e : quant_) most = std::max(most, e.rows * e.cols);
+    void* tmp = nullptr;
+    HAI_TRY(hai_malloc(&tmp, static_cast<size_t>(most) * 2));
+    int rc = HAI_OK;
+    for (const auto& e : quant_) {
+        const int64_t nblk = ((e.rows + 127) / 128) * ((e.cols + 127) / 128);
+        rc = hai_fill_synthetic_bf16(tmp, e.rows, e.cols, e.cols, seed, e.id, std_dev, stream_);
+        if (rc == HAI_OK) rc = hai_fill_synthetic_scales_f32(e.s, nblk, seed, e.id, stream_);
+        if (rc == HAI_OK) rc = hai_fp8_quantize_bf16(e.q, e.ldq, tmp, e.cols, e.s, e.rows, e.cols, stream_);
+        if (rc != HAI_OK) break;
+    }
+    const int rc_sync = hai_stream_synchronize(stream_);
+    hai_free(tmp);
+    if (rc != HAI_OK) return fail(rc, "fp8 synthetic weights");
+    if (rc_sync != HAI_OK) return fail(rc_sync, "stream synchronize");
+    return HAI_OK;
 }
 
 int64_t Engine::read_tensor(uint32_t id, uint16_t* out, int64_t capacity) {
@@ -302,19 +383,23 @@ int64_t Engine::read_tensor(uint32_t id, uint16_t* out, int64_t capacity) {
     return -1;
 }
 
-int Engine::gemm(uint16_t* y, int64_t ldy, const uint16_t* x, int64_t ldx, const uint16_t* w, int64_t M,
-                 int64_t N, int64_t K, int epi, const uint16_t* res, int64_t ldres) {
+int Engine::gemm(uint16_t* y, int64_t ldy, const uint16_t* x, int64_t ldx, const Lin& w, int64_t M, int64_t N,
+                 int64_t K, int epi, const uint16_t* res, int64_t ldres) {
     if (prof_record_) prof_calls_.push_back({y, ldy, x, ldx, w, M, N, K, epi, res, ldres, nullptr, nullptr});
-    HAI_TRY(hai_gemm_bf16(y, ldy, x, ldx, w, M, N, K, epi, res, ldres, stream_));
+    if (w.q != nullptr)
+        HAI_TRY(hai_gemm_fp8_bf16(y, ldy, x, ldx, w.q, w.s, w.map, M, N, K, epi, res, ldres, stream_));
+    else
+        HAI_TRY(hai_gemm_bf16(y, ldy, x, ldx, w.w, M, N, K, epi, res, ldres, stream_));
     return HAI_OK;
 }
 
 int Engine::norm_gemm(uint16_t* y, int64_t ldy, const uint16_t* x, const uint16_t* nw, uint16_t* xn_out,
-                      const uint16_t* w, int64_t M, int64_t N, int epi, const uint16_t* res, int64_t ldres) {
+                      const Lin& w, int64_t M, int64_t N, int epi, const uint16_t* res, int64_t ldres) {
     const int64_t H = d_.H;
     // lm_head-sized outputs stream faster from the plain kernel than the norm
-    // prologue saves (measured on MI355X), so they normalise separately.
-    if (N > kFusedNormMaxN) {
+    // prologue saves (measured on MI355X), so they normalise separately; the
+    // FP8 GEMM has no norm prologue.
+    if (N > kFusedNormMaxN || w.q != nullptr) {
         uint16_t* xn = xn_out != nullptr ? xn_out : xn_;
         HAI_TRY(hai_rmsnorm_bf16(xn, H, x, H, nw, M, H, cfg_.rms_eps, 1, stream_));
         return gemm(y, ldy, xn, H, w, M, N, H, epi, res, ldres);
@@ -322,7 +407,7 @@ int Engine::norm_gemm(uint16_t* y, int64_t ldy, const uint16_t* x, const uint16_
     // Above the fused limit the call runs RMSNorm then GEMM through xn_.
     if (xn_out == nullptr && M * H > HAI_GEMM_RMSNORM_FUSED_MAX) xn_out = xn_;
     if (prof_record_) prof_calls_.push_back({y, ldy, x, H, w, M, N, H, epi, res, ldres, nw, xn_out});
-    HAI_TRY(hai_gemm_rmsnorm_bf16(y, ldy, x, H, nw, cfg_.rms_eps, 1, xn_out, H, w, M, N, H, epi, res, ldres,
+    HAI_TRY(hai_gemm_rmsnorm_bf16(y, ldy, x, H, nw, cfg_.rms_eps, 1, xn_out, H, w.w, M, N, H, epi, res, ldres,
                                   stream_));
     return HAI_OK;
 }
@@ -345,7 +430,8 @@ int Engine::reset_state() {
 int Engine::attention_layer(const LayerWeights& L, int64_t T, uint16_t* h, const int32_t* lens, uint16_t* kc,
                             uint16_t* vc) {
     const auto& d = d_;
-    HAI_TRY(norm_gemm(proj_, d.Nqkv, h, L.in_ln, nullptr, L.w_qkv, T, d.Nqkv, HAI_EPI_STORE, nullptr, 0));
+    HAI_TRY(norm_gemm(proj_, d.Nqkv, h, L.in_ln, nullptr, lin(L.w_qkv, L.f_qkv), T, d.Nqkv, HAI_EPI_STORE,
+                      nullptr, 0));
     HAI_TRY(hai_q_gate_rmsnorm_rope_bf16(q_, gate_, proj_, d.Nqkv, L.q_norm, rope_cos_, rope_sin_, cap_, 1, T,
                                          d.nq, d.D, d.R, lens, 0, cfg_.rms_eps, stream_));
     HAI_TRY(hai_kv_rmsnorm_rope_append_bf16(kc, vc, cap_, proj_ + 2 * d.qw, proj_ + 2 * d.qw + d.kvw, d.Nqkv,
@@ -353,15 +439,16 @@ int Engine::attention_layer(const LayerWeights& L, int64_t T, uint16_t* h, const
                                             cfg_.rms_eps, stream_));
     HAI_TRY(hai_gqa_verify_bf16(att_, q_, gate_, kc, vc, cap_, gqa_scratch_, 1, T, d.nq, d.nkv, d.D, lens,
                                 static_cast<int32_t>(T), cap_, stream_));
-    return gemm(h, d.H, att_, d.qw, L.w_o, T, d.H, d.qw, HAI_EPI_RESIDUAL, h, d.H);
+    return gemm(h, d.H, att_, d.qw, lin(L.w_o, L.f_o), T, d.H, d.qw, HAI_EPI_RESIDUAL, h, d.H);
 }
 
 // qwen_mlp_reference (qwen_reference.cc:146-175): post-norm, SwiGLU, down
 // projection with the residual add fused.
 int Engine::mlp(const LayerWeights& L, int64_t T, uint16_t* h) {
     const auto& d = d_;
-    HAI_TRY(norm_gemm(act_, d.F, h, L.post_ln, nullptr, L.w_gu, T, 2 * d.F, HAI_EPI_SILU_MUL, nullptr, 0));
-    return gemm(h, d.H, act_, d.F, L.w_down, T, d.H, d.F, HAI_EPI_RESIDUAL, h, d.H);
+    HAI_TRY(norm_gemm(act_, d.F, h, L.post_ln, nullptr, lin(L.w_gu, L.f_gu), T, 2 * d.F, HAI_EPI_SILU_MUL,
+                      nullptr, 0));
+    return gemm(h, d.H, act_, d.F, lin(L.w_down, L.f_down), T, d.H, d.F, HAI_EPI_RESIDUAL, h, d.H);
 }
 
 // target_forward (generator.cc:550-634): T rows of one sequence on top of
@@ -375,12 +462,21 @@ int Engine::forward_target(const int64_t* d_ids, int64_t T, bool write_all_slots
             HAI_TRY(attention_layer(L, T, h_, d_tlen_, L.k_cache, L.v_cache));
         } else {
             // qwen_deltanet_reference (qwen_reference.cc:205-258)
-            HAI_TRY(norm_gemm(proj_, d.Nin, h_, L.in_ln, nullptr, L.w_in, T, d.Nin, HAI_EPI_STORE, nullptr, 0));
+            if (fp8_) {
+                // a|b (bf16) with the norm fused, writing the normalised rows
+                // that the FP8 qkv|z projection then reads
+                HAI_TRY(norm_gemm(proj_ + d.C + d.vw, d.Nin, h_, L.in_ln, xn_, L.w_ab, T, 2 * d.nv,
+                                  HAI_EPI_STORE, nullptr, 0));
+                HAI_TRY(gemm(proj_, d.Nin, xn_, d.H, Lin(L.f_in), T, d.C + d.vw, d.H, HAI_EPI_STORE, nullptr, 0));
+            } else {
+                HAI_TRY(norm_gemm(proj_, d.Nin, h_, L.in_ln, nullptr, L.w_in, T, d.Nin, HAI_EPI_STORE, nullptr,
+                                  0));
+            }
             HAI_TRY(hai_deltanet_verify_bf16(dnout_, d.vw, proj_, d.Nin, 0, d.C, d.C + d.vw, d.C + d.vw + d.nv,
                                              L.conv_w, L.ring, ring_, L.state, nslots_, write_all_slots ? 1 : 0,
                                              L.a_log, L.dt_bias, L.lin_norm, d_tlen_, 0, 1, T, d.nk, d.nv, d.dk,
                                              d.dv, d.Kc, cfg_.rms_eps, stream_));
-            HAI_TRY(gemm(h_, d.H, dnout_, d.vw, L.w_out, T, d.H, d.vw, HAI_EPI_RESIDUAL, h_, d.H));
+            HAI_TRY(gemm(h_, d.H, dnout_, d.vw, lin(L.w_out, L.f_out), T, d.H, d.vw, HAI_EPI_RESIDUAL, h_, d.H));
         }
         HAI_TRY(mlp(L, T, h_));
     }
@@ -399,8 +495,8 @@ int Engine::mtp_kv_rows(const int64_t* d_ids, const uint16_t* d_hidden, int64_t 
     HAI_TRY(hai_rmsnorm_bf16(xn_ + d.H, 2 * d.H, d_hidden, d.H, pre_hid_, T, d.H, cfg_.rms_eps, 1, stream_));
     HAI_TRY(gemm(h_, d.H, xn_, 2 * d.H, fc_, T, d.H, 2 * d.H, HAI_EPI_STORE, nullptr, 0));
     // K and V rows of the fused attention projection only.
-    HAI_TRY(norm_gemm(proj_, 2 * d.kvw, h_, mtp_.in_ln, nullptr, mtp_.w_qkv + 2 * d.qw * d.H, T, 2 * d.kvw,
-                      HAI_EPI_STORE, nullptr, 0));
+    HAI_TRY(norm_gemm(proj_, 2 * d.kvw, h_, mtp_.in_ln, nullptr, lin(mtp_.w_qkv, mtp_.f_qkv).rows(2 * d.qw, d.H),
+                      T, 2 * d.kvw, HAI_EPI_STORE, nullptr, 0));
     HAI_TRY(hai_kv_rmsnorm_rope_append_bf16(mtp_.k_cache, mtp_.v_cache, cap_, proj_, proj_ + d.kvw, 2 * d.kvw,
                                             mtp_.k_norm, rope_cos_, rope_sin_, cap_, 1, T, d.nkv, d.D, d.R, d_mlen_,
                                             0, cfg_.rms_eps, stream_));
@@ -712,15 +808,22 @@ int Engine::profile_verify(int64_t T, int64_t iters, hai_verify_profile* out) {
     // The step's GEMM launches replayed back to back (same shapes, weights and
     // buffers; the outputs are scratch here), two events around each replay.
     double gemm_bytes = 0.0;
-    for (const auto& c : prof_calls_) gemm_bytes += static_cast<double>(c.N) * static_cast<double>(c.K) * 2.0;
+    for (const auto& c : prof_calls_) {
+        // weights (+ the FP8 scale grid rows and scale map)
+        gemm_bytes += static_cast<double>(c.N) * static_cast<double>(c.K) * (c.w.q ? 1.0 : 2.0);
+        if (c.w.q) gemm_bytes += static_cast<double>((c.N + 127) / 128 * ((c.K + 127) / 128)) * 4.0 + c.N * 4.0;
+    }
     for (int64_t it = 0; it < iters + 1; ++it) {
         HAI_TRY(hai_event_record(e0, stream_));
         for (const auto& c : prof_calls_) {
             if (c.nw != nullptr)
-                HAI_TRY(hai_gemm_rmsnorm_bf16(c.y, c.ldy, c.x, c.ldx, c.nw, cfg_.rms_eps, 1, c.xn, c.ldx, c.w, c.M,
-                                              c.N, c.K, c.epi, c.res, c.ldres, stream_));
+                HAI_TRY(hai_gemm_rmsnorm_bf16(c.y, c.ldy, c.x, c.ldx, c.nw, cfg_.rms_eps, 1, c.xn, c.ldx, c.w.w,
+                                              c.M, c.N, c.K, c.epi, c.res, c.ldres, stream_));
+            else if (c.w.q != nullptr)
+                HAI_TRY(hai_gemm_fp8_bf16(c.y, c.ldy, c.x, c.ldx, c.w.q, c.w.s, c.w.map, c.M, c.N, c.K, c.epi,
+                                          c.res, c.ldres, stream_));
             else
-                HAI_TRY(hai_gemm_bf16(c.y, c.ldy, c.x, c.ldx, c.w, c.M, c.N, c.K, c.epi, c.res, c.ldres,
+                HAI_TRY(hai_gemm_bf16(c.y, c.ldy, c.x, c.ldx, c.w.w, c.M, c.N, c.K, c.epi, c.res, c.ldres,
                                       stream_));
         }
         HAI_TRY(hai_event_record(e1, stream_));
@@ -761,7 +864,7 @@ int Engine::profile_verify(int64_t T, int64_t iters, hai_verify_profile* out) {
     out->step_bytes = out->gemm_bytes + kv + state;
     out->draft_ms = draft_ms / n;
     out->draft_bytes = static_cast<double>(d.H) * 2 * d.H * 2.0 +
-                       static_cast<double>(d.Nqkv + d.qw + 3 * d.F) * d.H * 2.0 +
+                       static_cast<double>(d.Nqkv + d.qw + 3 * d.F) * d.H * (fp8_ ? 1.0 : 2.0) +
                        static_cast<double>(d.V) * d.H * 2.0;
     return HAI_OK;
 }

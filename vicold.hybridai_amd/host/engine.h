@@ -20,11 +20,43 @@
 #include <chrono>
 #include <cstdint>
 #include <string>
+#include <utility>
 #include <vector>
 
 #include "hai_engine.h"
 
 namespace hybridai::mi355x {
+
+// A Linear stored as FP8 E4M3 codes [N, K] with 128x128 fp32 block scales:
+// s holds the block grids of the checkpoint tensors concatenated into the
+// matrix (each ceil(rows/128) x ceil(K/128)), map[n] the scale row of stored
+// row n (hai_gemm_fp8_bf16's scale_rows).
+struct Fp8Linear {
+    uint8_t* q = nullptr;
+    float* s = nullptr;
+    int32_t* map = nullptr;
+};
+
+// The weight operand of one linear layer: bf16 rows (w) or FP8 (q, s, map).
+struct Lin {
+    const uint16_t* w = nullptr;
+    const uint8_t* q = nullptr;
+    const float* s = nullptr;
+    const int32_t* map = nullptr;
+    Lin() = default;
+    Lin(const uint16_t* bf16) : w(bf16) {}  // NOLINT: bf16 pointers convert implicitly
+    explicit Lin(const Fp8Linear& f) : q(f.q), s(f.s), map(f.map) {}
+    // rows [r0, ...) of a [N, K] matrix
+    Lin rows(int64_t r0, int64_t K) const {
+        Lin o = *this;
+        if (w) o.w = w + r0 * K;
+        if (q) {
+            o.q = q + r0 * K;
+            o.map = map + r0;
+        }
+        return o;
+    }
+};
 
 struct LayerWeights {
     bool attn = false;
@@ -45,6 +77,11 @@ struct LayerWeights {
     // SwiGLU MLP
     uint16_t* w_gu = nullptr;     // [2F, H], rows interleaved gate/up
     uint16_t* w_down = nullptr;   // [H, F]
+    // FP8 weight format: the same matrices as E4M3 (in_proj without a|b),
+    // in_proj_a | in_proj_b kept bf16 as the reference loads them
+    Fp8Linear f_in;               // [C + nv*dv, H]
+    uint16_t* w_ab = nullptr;     // [2*nv, H]
+    Fp8Linear f_out, f_qkv, f_o, f_gu, f_down;
     // caches
     uint16_t* k_cache = nullptr;  // [cap][nkv][D]
     uint16_t* v_cache = nullptr;
@@ -56,6 +93,15 @@ struct TensorEntry {
     uint32_t id;
     uint16_t* ptr;
     int64_t rows, cols, ld;
+};
+
+// One checkpoint tensor held as FP8: where its codes and scale grid live.
+struct QuantEntry {
+    uint32_t id;
+    uint8_t* q;
+    int64_t ldq;
+    float* s;
+    int64_t rows, cols;
 };
 
 struct Dims {
@@ -107,12 +153,13 @@ private:
     int upload_rope_tables();
 
     // device pieces of a step
-    int gemm(uint16_t* y, int64_t ldy, const uint16_t* x, int64_t ldx, const uint16_t* w, int64_t M,
-             int64_t N, int64_t K, int epi, const uint16_t* res, int64_t ldres);
+    int gemm(uint16_t* y, int64_t ldy, const uint16_t* x, int64_t ldx, const Lin& w, int64_t M, int64_t N,
+             int64_t K, int epi, const uint16_t* res, int64_t ldres);
     // RMSNorm(+1) of the H-wide rows x (norm weight nw) fused into the linear
     // layer W [N, H]; xn_out (optional) receives the normalised rows.
     int norm_gemm(uint16_t* y, int64_t ldy, const uint16_t* x, const uint16_t* nw, uint16_t* xn_out,
-                  const uint16_t* w, int64_t M, int64_t N, int epi, const uint16_t* res, int64_t ldres);
+                  const Lin& w, int64_t M, int64_t N, int epi, const uint16_t* res, int64_t ldres);
+    Lin lin(const uint16_t* w, const Fp8Linear& f) const { return fp8_ ? Lin(f) : Lin(w); }
     int forward_target(const int64_t* d_ids, int64_t T, bool write_all_slots);
     int attention_layer(const LayerWeights& L, int64_t T, uint16_t* h, const int32_t* lens,
                         uint16_t* kc, uint16_t* vc);
@@ -160,6 +207,9 @@ private:
     uint16_t* pre_emb_ = nullptr;
     uint16_t* pre_hid_ = nullptr;
     std::vector<TensorEntry> tensors_;
+    bool fp8_ = false;  // quantizable Linears stored FP8 (hai_engine_options::weight_format)
+    std::vector<QuantEntry> quant_;
+    std::vector<std::pair<int32_t*, std::vector<int32_t>>> maps_;  // scale maps uploaded at init
 
     // workspace
     int64_t* d_ids_ = nullptr;    // [tmax] prefill / forward ids
@@ -198,7 +248,7 @@ private:
         int64_t ldy;
         const uint16_t* x;
         int64_t ldx;
-        const uint16_t* w;
+        Lin w;
         int64_t M, N, K;
         int epi;
         const uint16_t* res;
