@@ -235,6 +235,48 @@ def c2_ops(hai, reps: int = 50, cpu: bool = True) -> dict:
     return out
 
 
+def run_decode(hai, E, args, fp8: bool, steps: int):
+    """Engine on the 27B shape (bf16 or FP8 weights): prefill, warmup rounds,
+    `steps` timed speculative rounds, then the verify-step profile."""
+    cfg = E.QWEN27B
+    P, NEW = args.prompt, args.new
+    tag = "fp8" if fp8 else "bf16"
+    t0 = time.perf_counter()
+    eng = E.Engine(cfg, max_context=P + NEW + 32, max_verify_tokens=16, use_graphs=args.graphs, fp8=fp8)
+    eng.init_synthetic(seed=0, std=0.02)
+    hai.synchronize()
+    log(f"[{tag}] engine up: {eng.weight_bytes() / 1e9:.2f} GB weights in HBM, {time.perf_counter() - t0:.1f}s")
+    prompt = E.synthetic_prompt(0, P, cfg["vocab"])
+    t0 = time.perf_counter()
+    eng.prefill(prompt, NEW)
+    prefill_s = time.perf_counter() - t0
+    log(f"[{tag}] prefill of {P} tokens: {prefill_s:.2f}s")
+
+    out = np.zeros(NEW, np.int32)
+    n0, _ = eng.spec_rounds(args.warmup, args.width, out)
+    hai.synchronize()
+    t0 = time.perf_counter()
+    n1, st = eng.spec_rounds(steps, args.width, out)
+    hai.synchronize()
+    dt = time.perf_counter() - t0
+    rounds = st["rounds"]
+    emitted = n1 - n0
+    if rounds <= 0 or emitted <= 0:
+        raise RuntimeError("no speculative rounds ran (increase --new)")
+    value = emitted / dt
+    log(f"[{tag}] timed {rounds} rounds, {emitted} tokens in {dt:.3f}s -> {value:.2f} tok/s "
+        f"(accepted {st['accepted']}/{st['proposed']})")
+    prof = eng.profile_verify(args.width + 1, args.profile_iters)
+    verify_ms = prof["verify_ms"]
+    gemm_gbs = prof["gemm_bytes"] / (prof["gemm_ms"] * 1e-3) / 1e9
+    step_gbs = prof["step_bytes"] / (verify_ms * 1e-3) / 1e9
+    log(f"[{tag}] verify step {verify_ms:.3f} ms ({step_gbs:.0f} GB/s of {prof['step_bytes'] / 1e9:.2f} GB), "
+        f"GEMM {prof['gemm_ms']:.3f} ms over {prof['gemm_launches']:.0f} launches ({gemm_gbs:.0f} GB/s), "
+        f"draft {prof['draft_ms']:.3f} ms")
+    eng.close()
+    return value, dt, rounds, emitted, st, prof, prefill_s
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -247,6 +289,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--graphs", action="store_true",
                     help="replay captured HIP graphs (rocprofv3 kernel tracing cannot follow graph launches)")
+    ap.add_argument("--no-fp8", action="store_true",
+                    help="skip the FP8-weight leg (C5 weight format at batch 1, reported under fp8_weights)")
+    ap.add_argument("--fp8-steps", type=int, default=60)
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="first run one device-to-device copy of this many bytes (the known-size reference "
                          "dispatch that scales rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -267,41 +312,11 @@ def main():
         log(f"calibration copy of {args.copy_bytes} bytes done")
         del src, dst
 
-    cfg = E.QWEN27B
     P, NEW = args.prompt, args.new
-    t0 = time.perf_counter()
-    eng = E.Engine(cfg, max_context=P + NEW + 32, max_verify_tokens=16, use_graphs=args.graphs)
-    eng.init_synthetic(seed=0, std=0.02)
-    hai.synchronize()
-    log(f"engine up: {eng.weight_bytes() / 1e9:.2f} GB weights in HBM, {time.perf_counter() - t0:.1f}s")
-    prompt = E.synthetic_prompt(0, P, cfg["vocab"])
-    t0 = time.perf_counter()
-    eng.prefill(prompt, NEW)
-    prefill_s = time.perf_counter() - t0
-    log(f"prefill of {P} tokens: {prefill_s:.2f}s")
-
-    out = np.zeros(NEW, np.int32)
-    n0, _ = eng.spec_rounds(args.warmup, args.width, out)
-    hai.synchronize()
-    t0 = time.perf_counter()
-    n1, st = eng.spec_rounds(args.steps, args.width, out)
-    hai.synchronize()
-    dt = time.perf_counter() - t0
-    rounds = st["rounds"]
-    emitted = n1 - n0
-    if rounds <= 0 or emitted <= 0:
-        raise RuntimeError("no speculative rounds ran (increase --new)")
-    value = emitted / dt
-    log(f"timed {rounds} rounds, {emitted} tokens in {dt:.3f}s -> {value:.2f} tok/s "
-        f"(accepted {st['accepted']}/{st['proposed']})")
-
-    prof = eng.profile_verify(args.width + 1, args.profile_iters)
+    value, dt, rounds, emitted, st, prof, prefill_s = run_decode(hai, E, args, fp8=False, steps=args.steps)
     verify_ms = prof["verify_ms"]
     gemm_gbs = prof["gemm_bytes"] / (prof["gemm_ms"] * 1e-3) / 1e9
     step_gbs = prof["step_bytes"] / (verify_ms * 1e-3) / 1e9
-    log(f"verify step {verify_ms:.3f} ms ({step_gbs:.0f} GB/s of {prof['step_bytes'] / 1e9:.2f} GB), "
-        f"GEMM {prof['gemm_ms']:.3f} ms over {prof['gemm_launches']:.0f} launches ({gemm_gbs:.0f} GB/s), "
-        f"draft {prof['draft_ms']:.3f} ms")
 
     result = {
         "metric": METRIC,
@@ -340,7 +355,25 @@ def main():
             "ms_per_launch": round(prof["gemm_ms"] / prof["gemm_launches"], 5),
         },
     }
-    eng.close()
+    if not args.no_fp8:
+        fv, fdt, frounds, femitted, fst, fprof, _ = run_decode(hai, E, args, fp8=True, steps=args.fp8_steps)
+        fgemm = fprof["gemm_bytes"] / (fprof["gemm_ms"] * 1e-3) / 1e9
+        fstep = fprof["step_bytes"] / (fprof["verify_ms"] * 1e-3) / 1e9
+        result["fp8_weights"] = {
+            "workload": "C3 shape with the C5 weight format: QuantizedWeight Linears FP8 E4M3, 128x128 fp32 "
+                        "block scales U(0.5,2)/448, quantised from the bf16 init; embed, lm_head, MTP fc, "
+                        "in_proj_a/b bf16; bs=1, MTP k=%d" % args.width,
+            "value": round(fv, 3), "unit": "tok/s", "steps": frounds,
+            "ms_per_step": round(fdt / frounds * 1e3, 4),
+            "verify_ms": round(fprof["verify_ms"], 4),
+            "verify_steps_per_s": round(1e3 / fprof["verify_ms"], 3),
+            "verify_bytes": round(fprof["step_bytes"]),
+            "verify_hbm_frac": round(fstep / HBM_PEAK_GBS, 4),
+            "gemm_gb_s": round(fgemm, 1), "gemm_hbm_frac": round(fgemm / HBM_PEAK_GBS, 4),
+            "gemm_launches": fprof["gemm_launches"],
+            "draft_ms": round(fprof["draft_ms"], 4),
+            "acceptance_rate": round(fst["accepted"] / max(1, fst["proposed"]), 4),
+        }
     result["c2_ops"] = c2_ops(hai, cpu=not args.no_cpu_baseline)
     log("C2 ops: " + ", ".join(f"{k} {v['us']} us ({v['gb_s']} GB/s)" for k, v in result["c2_ops"].items()
                                if isinstance(v, dict)))

@@ -118,7 +118,11 @@ int hai_gemm_rmsnorm_bf16(void* y, int64_t ldy, const void* x, int64_t ldx,
  * grid), else n / 128; for HAI_EPI_SILU_MUL without a map the rows
  * interleave (gate_f, up_f) and scales are [2][ceil(N/2/128)][...] (gate
  * blocks, then up blocks).  K <= 32768, M <= 16 per call; x 16-byte and wq
- * 8-byte aligned. */
+ * 8-byte aligned.  epilogue may carry HAI_FP8_NO_SPECIAL_CODES: the caller
+ * guarantees that wq holds no 0x7F / 0xFF code (the +-480 codes of the
+ * reference's decoder, NaN in OCP E4M3, which a quantiser saturating at 448
+ * never writes), and the per-word check for them is skipped. */
+enum { HAI_FP8_NO_SPECIAL_CODES = 0x100 };
 int hai_gemm_fp8_bf16(void* y, int64_t ldy, const void* x, int64_t ldx,
                       const void* wq, const float* scales,
                       const int32_t* scale_rows, int64_t M, int64_t N,

@@ -114,6 +114,43 @@ __device__ __forceinline__ u32x4 bload(__amdgpu_buffer_rsrc_t r, uint32_t voff, 
 }
 constexpr uint32_t kOutOfRange = 0xfffffff0u;
 
+// Cache-policy operand of the weight-stream loads: 2 = nt (non-temporal).
+// Each weight byte is read once per launch; streaming it non-temporally keeps
+// it from displacing the activations and other reused data in the caches
+// (measured +5-8 % on the 27B-shape skinny GEMMs on MI355X).
+#ifndef HAI_WLOAD_AUX
+#define HAI_WLOAD_AUX 2
+#endif
+__device__ __forceinline__ u32x4 bload_w(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(voff),
+                                                                           static_cast<int>(soff), HAI_WLOAD_AUX));
+}
+
+// Index of the calling wave in its block, as a wave-uniform (scalar) value:
+// derived from threadIdx.x, the compiler would otherwise treat it as
+// per-lane.
+__device__ __forceinline__ int wave_index() {
+    return __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+}
+
+// Offsets of one chunk load at byte offset `off` from the lane's base offset.
+// The scalar operand of a buffer load must be wave-uniform: a lane-dependent
+// value there makes the compiler repeat the load once per distinct value (a
+// readfirstlane loop around every load).  So a chunk that lies inside the
+// range for every lane (`full`, uniform) passes `off` as the scalar offset;
+// a ragged chunk folds `off` into the per-lane offset and sends the lanes
+// past the end (ok false) out of range, where the load returns zeros.
+struct ChunkOffset {
+    bool full, ok;
+    uint32_t s;    // scalar offset operand
+    uint32_t off;
+    __device__ __forceinline__ ChunkOffset(bool full_, bool ok_, uint32_t off_)
+        : full(full_), ok(ok_), s(full_ ? off_ : 0u), off(off_) {}
+    __device__ __forceinline__ uint32_t v(uint32_t base) const {
+        return full ? base : (ok ? base + off : kOutOfRange);
+    }
+};
+
 // xor butterfly over the 64 lanes of a wave; all lanes get the same bits.
 __device__ __forceinline__ float wave_sum64(float v) {
 #pragma unroll

@@ -46,7 +46,7 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(
     uint16_t* __restrict__ y, int64_t ldy, const uint16_t* __restrict__ x, int64_t ldx,
     const uint16_t* __restrict__ w, const uint16_t* res, int64_t ldres, int M, int N, int K, NormArgs na) {
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = wave_index();
     extern __shared__ u32x4 xs[];  // NORM: [M][K/8] normalised rows
     const int npr = K >> 3;        // 16-byte pieces per row
     if constexpr (NORM) {
@@ -181,15 +181,15 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(
                 const int c = c0 + u;
                 // full chunk: every lane valid; ragged chunk: lanes past K masked
                 const bool ok = c < nfull || (c < nck && c * 512 + lane * 8 < K);
-                const uint32_t so = ok ? static_cast<uint32_t>(c) * 1024u : 0u;
+                const ChunkOffset co(c < nfull, ok, static_cast<uint32_t>(c) * 1024u);
 #pragma unroll
-                for (int r = 0; r < RW; ++r) wv[u][r] = bload(rw, ok ? woff[r] : kOutOfRange, so);
+                for (int r = 0; r < RW; ++r) wv[u][r] = bload_w(rw, co.v(woff[r]), co.s);
 #pragma unroll
                 for (int m = 0; m < MB; ++m) {
                     if constexpr (NORM)
                         xv[u][m] = (ok && m < M) ? xs[m * npr + c * 64 + lane] : u32x4{0u, 0u, 0u, 0u};
                     else
-                        xv[u][m] = bload(rx, ok ? xoff[m] : kOutOfRange, so);
+                        xv[u][m] = bload(rx, co.v(xoff[m]), co.s);
                 }
             }
 #pragma unroll
@@ -246,7 +246,7 @@ __global__ __launch_bounds__(256) void gemm_bf16_ksplit_kernel(
     constexpr int G = 4 / W;  // row groups per block
     extern __shared__ float part[];  // [G][nseg][RW][MB][64]
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = wave_index();
     const int g = wave / W;
     const int sub = wave % W;
     const int nck = (K + 511) / 512;
@@ -274,11 +274,11 @@ __global__ __launch_bounds__(256) void gemm_bf16_ksplit_kernel(
             for (int u = 0; u < 4; ++u) {
                 const int c = 4 * sg + u;
                 const bool ok = c < nfull || (c < nck && c * 512 + lane * 8 < K);
-                const uint32_t so = ok ? static_cast<uint32_t>(c) * 1024u : 0u;
+                const ChunkOffset co(c < nfull, ok, static_cast<uint32_t>(c) * 1024u);
 #pragma unroll
-                for (int r = 0; r < RW; ++r) wv[u][r] = bload(rw, ok ? woff[r] : kOutOfRange, so);
+                for (int r = 0; r < RW; ++r) wv[u][r] = bload_w(rw, co.v(woff[r]), co.s);
 #pragma unroll
-                for (int m = 0; m < MB; ++m) xv[u][m] = bload(rx, ok ? xoff[m] : kOutOfRange, so);
+                for (int m = 0; m < MB; ++m) xv[u][m] = bload(rx, co.v(xoff[m]), co.s);
             }
             float acc[RW][MB];
 #pragma unroll

@@ -33,7 +33,7 @@ typedef float f2v __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ u32x2 bload8(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-    return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
+    return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, HAI_WLOAD_AUX));
 }
 
 // decode_e4m3 of fp8_dequant.cc:12-26, exact for every code.
@@ -49,7 +49,9 @@ __device__ __forceinline__ float e4m3_exact(uint32_t b) {
     return (b & 0x80u) ? -v : v;
 }
 
-// Eight consecutive codes (two little-endian words) -> floats.
+// Eight consecutive codes (two little-endian words) -> floats.  Without
+// CHECK the caller guarantees that no code is 0x7F / 0xFF.
+template <bool CHECK>
 __device__ __forceinline__ void decode8(u32x2 w, float (&f)[8]) {
     const f2v a = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w[0]), false);
     const f2v b = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w[0]), true);
@@ -57,17 +59,87 @@ __device__ __forceinline__ void decode8(u32x2 w, float (&f)[8]) {
     const f2v d = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w[1]), true);
     f[0] = a.x; f[1] = a.y; f[2] = b.x; f[3] = b.y;
     f[4] = c.x; f[5] = c.y; f[6] = d.x; f[7] = d.y;
-    // a byte whose low 7 bits are all ones (0x7F / 0xFF) decodes to NaN in hardware
-    const uint32_t t0 = (w[0] & 0x7f7f7f7fu) ^ 0x7f7f7f7fu;
-    const uint32_t t1 = (w[1] & 0x7f7f7f7fu) ^ 0x7f7f7f7fu;
-    const uint32_t z = ((t0 - 0x01010101u) & ~t0) | ((t1 - 0x01010101u) & ~t1);
+    if (!CHECK) return;
+    // a byte whose low 7 bits are all ones (0x7F / 0xFF) decodes to NaN in
+    // hardware; adding 1 to the low 7 bits carries into bit 7 only there
+    // (never across bytes)
+    const uint32_t z = ((w[0] & 0x7f7f7f7fu) + 0x01010101u) | ((w[1] & 0x7f7f7f7fu) + 0x01010101u);
     if (__builtin_expect((z & 0x80808080u) != 0u, 0)) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) f[j] = e4m3_exact((w[j >> 2] >> (8 * (j & 3))) & 0xffu);
     }
 }
 
-template <int MB, int RW, int U, int EPI>
+// Scale rows of weight rows [rb, rb + nr) into srow[0 .. nr) (all 256 threads).
+__device__ __forceinline__ void stage_scales(float (*srow)[kMaxKBlocks], int64_t rb, int nr, const float* scales,
+                                             const int32_t* scale_rows, int paired, int N, int nkb) {
+    const int64_t nsb = ((N >> 1) + 127) / 128;
+    for (int i = threadIdx.x; i < nr * nkb; i += blockDim.x) {
+        const int rl = i / nkb;
+        const int kb = i - rl * nkb;
+        const int64_t r = min(rb + rl, static_cast<int64_t>(N) - 1);
+        const int64_t sr = scale_rows ? scale_rows[r] : (paired ? (r & 1) * nsb + (r >> 1) / 128 : r / 128);
+        srow[rl][kb] = scales[sr * nkb + kb];
+    }
+}
+
+// One 512-element chunk of RW rows x MB activations: the wave's lanes hold 8
+// codes per row (wv) and 8 bf16 activations per row of x (xv).
+template <int MB, int RW, bool CHECK>
+__device__ __forceinline__ void fp8_chunk(float (&acc)[RW][MB], const u32x2 (&wv)[RW], const u32x4 (&xv)[MB],
+                                          const float (&s)[RW]) {
+    float xf[MB][8];
+#pragma unroll
+    for (int m = 0; m < MB; ++m)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            xf[m][2 * q] = lo_bf(xv[m][q]);
+            xf[m][2 * q + 1] = hi_bf(xv[m][q]);
+        }
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+        float wf[8];
+        decode8<CHECK>(wv[r], wf);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float we = wf[j] * s[r];
+#pragma unroll
+            for (int m = 0; m < MB; ++m) acc[r][m] = fma_(xf[m][j], we, acc[r][m]);
+        }
+    }
+}
+
+// Final bf16 stores of one row group (tot already reduced over the wave).
+template <int MB, int RW, int EPI>
+__device__ __forceinline__ void fp8_store(uint16_t* y, int64_t ldy, const uint16_t* res, int64_t ldres,
+                                          const float (&tot)[RW][MB], int lane, int64_t row0, int nrows, int M) {
+    if (EPI == HAI_EPI_SILU_MUL) {
+#pragma unroll
+        for (int p = 0; p < RW / 2; ++p)
+#pragma unroll
+            for (int m = 0; m < MB; ++m) {
+                if (lane == p * MB + m && m < M && 2 * p + 1 < nrows) {
+                    const float g = bfr(tot[2 * p][m]);
+                    const float u = bfr(tot[2 * p + 1][m]);
+                    y[static_cast<int64_t>(m) * ldy + row0 / 2 + p] = f2bf(csilu(g) * u);
+                }
+            }
+    } else {
+#pragma unroll
+        for (int r = 0; r < RW; ++r)
+#pragma unroll
+            for (int m = 0; m < MB; ++m) {
+                if (lane == r * MB + m && m < M && r < nrows) {
+                    const int64_t n = row0 + r;
+                    float v = bfr(tot[r][m]);
+                    if (EPI == HAI_EPI_RESIDUAL) v = bf2f(res[static_cast<int64_t>(m) * ldres + n]) + v;
+                    y[static_cast<int64_t>(m) * ldy + n] = f2bf(v);
+                }
+            }
+    }
+}
+
+template <int MB, int RW, int U, int EPI, bool CHECK>
 __global__ __launch_bounds__(256) void gemm_fp8_kernel(uint16_t* __restrict__ y, int64_t ldy,
                                                        const uint16_t* __restrict__ x, int64_t ldx,
                                                        const uint8_t* __restrict__ wq,
@@ -77,21 +149,11 @@ __global__ __launch_bounds__(256) void gemm_fp8_kernel(uint16_t* __restrict__ y,
     constexpr int BR = 4 * RW;  // weight rows per block
     __shared__ float srow[BR][kMaxKBlocks];
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = wave_index();
     const int nkb = (K + 127) / 128;
-    {
-        // the scale row of each of this block's weight rows: the caller's map,
-        // or the 128-row block of a plain / paired (gate, up) layout
-        const int64_t rb = static_cast<int64_t>(blockIdx.x) * BR;
-        const int64_t nsb = ((N >> 1) + 127) / 128;
-        for (int i = threadIdx.x; i < BR * nkb; i += 256) {
-            const int rl = i / nkb;
-            const int kb = i - rl * nkb;
-            const int64_t r = min(rb + rl, static_cast<int64_t>(N) - 1);
-            const int64_t sr = scale_rows ? scale_rows[r] : (paired ? (r & 1) * nsb + (r >> 1) / 128 : r / 128);
-            srow[rl][kb] = scales[sr * nkb + kb];
-        }
-    }
+    // the scale row of each of this block's weight rows: the caller's map, or
+    // the 128-row block of a plain / paired (gate, up) layout
+    stage_scales(srow, static_cast<int64_t>(blockIdx.x) * BR, BR, scales, scale_rows, paired, N, nkb);
     __syncthreads();
     const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * 4 + wave) * RW;
     if (row0 >= N) return;
@@ -133,37 +195,21 @@ __global__ __launch_bounds__(256) void gemm_fp8_kernel(uint16_t* __restrict__ y,
             const int c = c0 + u;
             const bool ok = c < nfull || (c < nck && c * 512 + lane * 8 < K);
             okv[u] = ok;
+            const ChunkOffset cw(c < nfull, ok, static_cast<uint32_t>(c) * 512u);
+            const ChunkOffset cx(c < nfull, ok, static_cast<uint32_t>(c) * 1024u);
 #pragma unroll
-            for (int r = 0; r < RW; ++r)
-                wv[u][r] = bload8(rw, ok ? woff[r] : kOutOfRange, ok ? static_cast<uint32_t>(c) * 512u : 0u);
+            for (int r = 0; r < RW; ++r) wv[u][r] = bload8(rw, cw.v(woff[r]), cw.s);
 #pragma unroll
-            for (int m = 0; m < MB; ++m)
-                xv[u][m] = bload(rx, ok ? xoff[m] : kOutOfRange, ok ? static_cast<uint32_t>(c) * 1024u : 0u);
+            for (int m = 0; m < MB; ++m) xv[u][m] = bload(rx, cx.v(xoff[m]), cx.s);
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             // scale of k-block 4c + lane/16; lanes past K multiply zeros
             const int kb = min(4 * (c0 + u) + (lane >> 4), kMaxKBlocks - 1);
-            float xf[MB][8];
+            float sv[RW];
 #pragma unroll
-            for (int m = 0; m < MB; ++m)
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    xf[m][2 * q] = lo_bf(xv[u][m][q]);
-                    xf[m][2 * q + 1] = hi_bf(xv[u][m][q]);
-                }
-#pragma unroll
-            for (int r = 0; r < RW; ++r) {
-                const float s = okv[u] ? srow[wave * RW + r][kb] : 0.0f;
-                float wf[8];
-                decode8(wv[u][r], wf);
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const float we = wf[j] * s;
-#pragma unroll
-                    for (int m = 0; m < MB; ++m) acc[r][m] = fma_(xf[m][j], we, acc[r][m]);
-                }
-            }
+            for (int r = 0; r < RW; ++r) sv[r] = okv[u] ? srow[wave * RW + r][kb] : 0.0f;
+            fp8_chunk<MB, RW, CHECK>(acc, wv[u], xv[u], sv);
         }
         // a segment is four 512-element chunks (U divides 4)
         if (((c0 + U) & 3) == 0) fold();
@@ -173,32 +219,96 @@ __global__ __launch_bounds__(256) void gemm_fp8_kernel(uint16_t* __restrict__ y,
 #pragma unroll
     for (int r = 0; r < RW; ++r)
 #pragma unroll
-        for (int m = 0; m < MB; ++m) acc[r][m] = wave_sum64(tot[r][m]);
+        for (int m = 0; m < MB; ++m) tot[r][m] = wave_sum64(tot[r][m]);
+    fp8_store<MB, RW, EPI>(y, ldy, res, ldres, tot, lane, row0, nrows, M);
+}
 
-    if (EPI == HAI_EPI_SILU_MUL) {
+// K-split form: W waves share each row group, wave `sub` taking the
+// 2048-element segments sub, sub + W, ...; the segment partials meet in LDS
+// and the group's first wave folds them in segment order, which keeps the
+// canonical sum (tot = tot + segment, then the 64-lane butterfly).
+template <int MB, int RW, int W, int EPI, bool CHECK>
+__global__ __launch_bounds__(256) void gemm_fp8_ksplit_kernel(uint16_t* __restrict__ y, int64_t ldy,
+                                                              const uint16_t* __restrict__ x, int64_t ldx,
+                                                              const uint8_t* __restrict__ wq,
+                                                              const float* __restrict__ scales,
+                                                              const int32_t* __restrict__ scale_rows, int paired,
+                                                              const uint16_t* res, int64_t ldres, int M, int N,
+                                                              int K) {
+    constexpr int G = 4 / W;   // row groups per block
+    constexpr int BR = G * RW;  // weight rows per block
+    __shared__ float srow[BR][kMaxKBlocks];
+    extern __shared__ float part[];  // [G][nseg][RW][MB][64]
+    const int lane = threadIdx.x & 63;
+    const int wave = wave_index();
+    const int g = wave / W;
+    const int sub = wave % W;
+    const int nkb = (K + 127) / 128;
+    const int nck = (K + 511) / 512;
+    const int nfull = K / 512;
+    const int nseg = (nck + 3) / 4;
+    stage_scales(srow, static_cast<int64_t>(blockIdx.x) * BR, BR, scales, scale_rows, paired, N, nkb);
+    __syncthreads();
+    const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * G + g) * RW;
+    const bool active = row0 < N;
+    const int nrows = active ? static_cast<int>(min(static_cast<int64_t>(RW), static_cast<int64_t>(N) - row0)) : 0;
+    float* gpart = part + static_cast<int64_t>(g) * nseg * RW * MB * 64;
+
+    if (active) {
+        const __amdgpu_buffer_rsrc_t rw = make_rsrc(wq, static_cast<uint32_t>(static_cast<int64_t>(N) * K));
+        const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, static_cast<uint32_t>(static_cast<int64_t>(M) * ldx * 2));
+        uint32_t woff[RW], xoff[MB];
 #pragma unroll
-        for (int p = 0; p < RW / 2; ++p)
+        for (int r = 0; r < RW; ++r) woff[r] = static_cast<uint32_t>((row0 + r) * static_cast<int64_t>(K) + lane * 8);
 #pragma unroll
-            for (int m = 0; m < MB; ++m) {
-                if (lane == p * MB + m && m < M && 2 * p + 1 < nrows) {
-                    const float g = bfr(acc[2 * p][m]);
-                    const float u = bfr(acc[2 * p + 1][m]);
-                    y[static_cast<int64_t>(m) * ldy + row0 / 2 + p] = f2bf(csilu(g) * u);
-                }
+        for (int m = 0; m < MB; ++m) xoff[m] = static_cast<uint32_t>((static_cast<int64_t>(m) * ldx + lane * 8) * 2);
+        for (int sg = sub; sg < nseg; sg += W) {
+            u32x2 wv[4][RW];
+            u32x4 xv[4][MB];
+            bool okv[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int c = 4 * sg + u;
+                const bool ok = c < nfull || (c < nck && c * 512 + lane * 8 < K);
+                okv[u] = ok;
+                const ChunkOffset cw(c < nfull, ok, static_cast<uint32_t>(c) * 512u);
+                const ChunkOffset cx(c < nfull, ok, static_cast<uint32_t>(c) * 1024u);
+#pragma unroll
+                for (int r = 0; r < RW; ++r) wv[u][r] = bload8(rw, cw.v(woff[r]), cw.s);
+#pragma unroll
+                for (int m = 0; m < MB; ++m) xv[u][m] = bload(rx, cx.v(xoff[m]), cx.s);
             }
-    } else {
+            float acc[RW][MB];
 #pragma unroll
-        for (int r = 0; r < RW; ++r)
+            for (int r = 0; r < RW; ++r)
 #pragma unroll
-            for (int m = 0; m < MB; ++m) {
-                if (lane == r * MB + m && m < M && r < nrows) {
-                    const int64_t n = row0 + r;
-                    float v = bfr(acc[r][m]);
-                    if (EPI == HAI_EPI_RESIDUAL) v = bf2f(res[static_cast<int64_t>(m) * ldres + n]) + v;
-                    y[static_cast<int64_t>(m) * ldy + n] = f2bf(v);
-                }
+                for (int m = 0; m < MB; ++m) acc[r][m] = 0.0f;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int kb = min(4 * (4 * sg + u) + (lane >> 4), kMaxKBlocks - 1);
+                float sv[RW];
+#pragma unroll
+                for (int r = 0; r < RW; ++r) sv[r] = okv[u] ? srow[g * RW + r][kb] : 0.0f;
+                fp8_chunk<MB, RW, CHECK>(acc, wv[u], xv[u], sv);
             }
+#pragma unroll
+            for (int r = 0; r < RW; ++r)
+#pragma unroll
+                for (int m = 0; m < MB; ++m) gpart[((static_cast<int64_t>(sg) * RW + r) * MB + m) * 64 + lane] = acc[r][m];
+        }
     }
+    __syncthreads();
+    if (!active || sub != 0) return;
+    float tot[RW][MB];
+#pragma unroll
+    for (int r = 0; r < RW; ++r)
+#pragma unroll
+        for (int m = 0; m < MB; ++m) {
+            float t = 0.0f;
+            for (int sg = 0; sg < nseg; ++sg) t = t + gpart[((static_cast<int64_t>(sg) * RW + r) * MB + m) * 64 + lane];
+            tot[r][m] = wave_sum64(t);
+        }
+    fp8_store<MB, RW, EPI>(y, ldy, res, ldres, tot, lane, row0, nrows, M);
 }
 
 struct Fp8Args {
@@ -215,24 +325,57 @@ struct Fp8Args {
     int M, N, K;
 };
 
-template <int MB, int EPI>
+template <int MB, int EPI, bool CHECK>
 void launch_fp8(const Fp8Args& a, hipStream_t s) {
     constexpr int RW = 2;
     // two 512-byte chunk groups in flight measured best (M=1: 4.2-5.6 TB/s of
     // FP8 bytes on the 27B shapes; M=2: 3.1-4.3)
     constexpr int U = MB <= 2 ? 2 : 1;
     const int64_t groups = (static_cast<int64_t>(a.N) + 4 * RW - 1) / (4 * RW);
-    gemm_fp8_kernel<MB, RW, U, EPI><<<dim3(static_cast<unsigned>(groups)), dim3(256), 0, s>>>(
+    gemm_fp8_kernel<MB, RW, U, EPI, CHECK><<<dim3(static_cast<unsigned>(groups)), dim3(256), 0, s>>>(
         a.y, a.ldy, a.x, a.ldx, a.wq, a.scales, a.scale_rows, a.paired, a.res, a.ldres, a.M, a.N, a.K);
 }
 
-template <int EPI>
+constexpr int kKsplitRW = 2, kKsplitW = 4;
+
+template <int MB, int EPI, bool CHECK>
+void launch_fp8_ksplit(const Fp8Args& a, hipStream_t s) {
+    constexpr int G = 4 / kKsplitW;
+    const int64_t blocks = (static_cast<int64_t>(a.N) + G * kKsplitRW - 1) / (G * kKsplitRW);
+    const int64_t nseg = ((a.K + 511) / 512 + 3) / 4;
+    const size_t shmem = static_cast<size_t>(G * nseg * kKsplitRW * MB * 64) * sizeof(float);
+    gemm_fp8_ksplit_kernel<MB, kKsplitRW, kKsplitW, EPI, CHECK>
+        <<<dim3(static_cast<unsigned>(blocks)), dim3(256), shmem, s>>>(a.y, a.ldy, a.x, a.ldx, a.wq, a.scales,
+                                                                       a.scale_rows, a.paired, a.res, a.ldres, a.M,
+                                                                       a.N, a.K);
+}
+
+// Short, wide-K layers (M <= 2, N <= 8192) spread each row pair over four
+// waves; LDS holds the segment partials (<= 64 KB).
+bool use_ksplit_fp8(const Fp8Args& a) {
+    if (a.M > 2 || a.N > 8192) return false;
+    const int64_t nseg = ((a.K + 511) / 512 + 3) / 4;
+    return nseg * kKsplitRW * a.M * 64 * 4 <= 64 * 1024;
+}
+
+template <int EPI, bool CHECK>
 void dispatch_fp8(const Fp8Args& a, hipStream_t s) {
-    if (a.M <= 1) launch_fp8<1, EPI>(a, s);
-    else if (a.M <= 2) launch_fp8<2, EPI>(a, s);
-    else if (a.M <= 4) launch_fp8<4, EPI>(a, s);
-    else if (a.M <= 8) launch_fp8<8, EPI>(a, s);
-    else launch_fp8<16, EPI>(a, s);
+    if (use_ksplit_fp8(a)) {
+        if (a.M <= 1) launch_fp8_ksplit<1, EPI, CHECK>(a, s);
+        else launch_fp8_ksplit<2, EPI, CHECK>(a, s);
+        return;
+    }
+    if (a.M <= 1) launch_fp8<1, EPI, CHECK>(a, s);
+    else if (a.M <= 2) launch_fp8<2, EPI, CHECK>(a, s);
+    else if (a.M <= 4) launch_fp8<4, EPI, CHECK>(a, s);
+    else if (a.M <= 8) launch_fp8<8, EPI, CHECK>(a, s);
+    else launch_fp8<16, EPI, CHECK>(a, s);
+}
+
+template <int EPI>
+void dispatch_fp8_codes(const Fp8Args& a, bool check, hipStream_t s) {
+    if (check) dispatch_fp8<EPI, true>(a, s);
+    else dispatch_fp8<EPI, false>(a, s);
 }
 
 // E4M3 code of v, rounded to nearest even, saturated at +-448; NaN -> 0.
@@ -298,19 +441,20 @@ extern "C" int hai_gemm_fp8_bf16(void* y, int64_t ldy, const void* x, int64_t ld
               static_cast<const uint8_t*>(wq), scales, scale_rows, 0, static_cast<const uint16_t*>(res), ld_res,
               int(M), int(N), int(K)};
     const hipStream_t s = as_stream(stream);
-    switch (epilogue) {
+    const bool check = (epilogue & HAI_FP8_NO_SPECIAL_CODES) == 0;
+    switch (epilogue & ~HAI_FP8_NO_SPECIAL_CODES) {
         case HAI_EPI_STORE:
             if (ldy < N) return invalid("gemm_fp8: ldy < N");
-            dispatch_fp8<HAI_EPI_STORE>(a, s);
+            dispatch_fp8_codes<HAI_EPI_STORE>(a, check, s);
             break;
         case HAI_EPI_RESIDUAL:
             if (res == nullptr || ldy < N || ld_res < N) return invalid("gemm_fp8: residual operands");
-            dispatch_fp8<HAI_EPI_RESIDUAL>(a, s);
+            dispatch_fp8_codes<HAI_EPI_RESIDUAL>(a, check, s);
             break;
         case HAI_EPI_SILU_MUL:
             if (N % 2 != 0 || ldy < N / 2) return invalid("gemm_fp8: silu_mul needs even N and ldy >= N/2");
             a.paired = 1;
-            dispatch_fp8<HAI_EPI_SILU_MUL>(a, s);
+            dispatch_fp8_codes<HAI_EPI_SILU_MUL>(a, check, s);
             break;
         default:
             return invalid("gemm_fp8: unknown epilogue");
