@@ -480,7 +480,8 @@ def _fp8_weights(rng, N, K, nan_codes=False):
 
 
 @pytest.mark.parametrize("M,N,K,nan_codes", [(1, 300, 256, False), (2, 1536, 5120, True), (3, 257, 1000, True),
-                                             (16, 384, 768, False), (2, 5120, 17408, False)])
+                                             (16, 384, 768, False), (2, 5120, 17408, False),
+                                             (2, 16390, 1000, True), (1, 8200, 2056, False)])
 def test_gemm_fp8_store(M, N, K, nan_codes):
     rng = np.random.default_rng(M * 31 + N + K)
     x, xb = rand_bf16(rng, (M, K))
@@ -512,6 +513,26 @@ def test_gemm_fp8_residual_and_swiglu():
                                        0, None), "gemm_fp8 silu")
     want = orc.silu_mul(orc.gemm_fp8(x, qg, sg), orc.gemm_fp8(x, qu, su))
     assert_bits_equal(dy.download(np.uint16), want, "gemm_fp8 silu_mul")
+
+
+@pytest.mark.parametrize("special", [False, True])
+def test_gemm_fp8_wide_swiglu_and_no_special_codes_flag(special):
+    """M = 2 over 2F >= 16384 interleaved rows (the four-rows-per-wave launch);
+    with HAI_FP8_NO_SPECIAL_CODES on weights that hold no 0x7F / 0xFF the
+    result is unchanged."""
+    rng = np.random.default_rng(5 + special)
+    M, F, K = 2, 8200, 768
+    x, xb = rand_bf16(rng, (M, K))
+    qg, sg = _fp8_weights(rng, F, K, special)
+    qu, su = _fp8_weights(rng, F, K)
+    qi = np.empty((2 * F, K), np.uint8)
+    qi[0::2], qi[1::2] = qg, qu
+    dx, dqi, dsi, dy = dev(xb), dev(qi), dev(np.stack([sg, su])), out_buf(M * F * 2)
+    flag = 0 if special else hai.FP8_NO_SPECIAL_CODES
+    hai.check(kern().hai_gemm_fp8_bf16(dy.ptr, F, dx.ptr, K, dqi.ptr, dsi.ptr, None, M, 2 * F, K,
+                                       hai.EPI_SILU_MUL | flag, None, 0, None), "gemm_fp8 wide silu")
+    want = orc.silu_mul(orc.gemm_fp8(x, qg, sg), orc.gemm_fp8(x, qu, su))
+    assert_bits_equal(dy.download(np.uint16), want, "gemm_fp8 wide silu_mul")
 
 
 def test_gemm_fp8_scale_rows_map():

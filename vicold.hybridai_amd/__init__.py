@@ -30,6 +30,7 @@ I64P = ctypes.POINTER(ctypes.c_int64)
 F32P = ctypes.POINTER(ctypes.c_float)
 
 EPI_STORE, EPI_RESIDUAL, EPI_SILU_MUL = 0, 1, 2
+FP8_NO_SPECIAL_CODES = 0x100  # hai_gemm_fp8_bf16 epilogue flag: weights hold no 0x7F / 0xFF code
 # hai_status codes (include/hai_kernels.h)
 OK, ERR_INVALID, ERR_OOM, ERR_NOT_IMPLEMENTED, ERR_INVALID_DEVICE, ERR_BACKEND = 0, 1, 2, 3, 5, 9
 

@@ -189,26 +189,38 @@ __global__ __launch_bounds__(256) void gemm_fp8_kernel(uint16_t* __restrict__ y,
     for (int c0 = 0; c0 < nck; c0 += U) {
         u32x2 wv[U][RW];
         u32x4 xv[U][MB];
-        bool okv[U];
+        if (c0 + U <= nfull) {
+            // every lane inside K: chunk offsets go in the scalar operand
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int c = c0 + u;
-            const bool ok = c < nfull || (c < nck && c * 512 + lane * 8 < K);
-            okv[u] = ok;
-            const ChunkOffset cw(c < nfull, ok, static_cast<uint32_t>(c) * 512u);
-            const ChunkOffset cx(c < nfull, ok, static_cast<uint32_t>(c) * 1024u);
+            for (int u = 0; u < U; ++u) {
+                const uint32_t c = static_cast<uint32_t>(c0 + u);
 #pragma unroll
-            for (int r = 0; r < RW; ++r) wv[u][r] = bload8(rw, cw.v(woff[r]), cw.s);
+                for (int r = 0; r < RW; ++r) wv[u][r] = bload8(rw, woff[r], c * 512u);
 #pragma unroll
-            for (int m = 0; m < MB; ++m) xv[u][m] = bload(rx, cx.v(xoff[m]), cx.s);
+                for (int m = 0; m < MB; ++m) xv[u][m] = bload(rx, xoff[m], c * 1024u);
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int c = c0 + u;
+                const bool ok = c < nfull || (c < nck && c * 512 + lane * 8 < K);
+                const ChunkOffset cw(c < nfull, ok, static_cast<uint32_t>(c) * 512u);
+                const ChunkOffset cx(c < nfull, ok, static_cast<uint32_t>(c) * 1024u);
+#pragma unroll
+                for (int r = 0; r < RW; ++r) wv[u][r] = bload8(rw, cw.v(woff[r]), cw.s);
+#pragma unroll
+                for (int m = 0; m < MB; ++m) xv[u][m] = bload(rx, cx.v(xoff[m]), cx.s);
+            }
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            // scale of k-block 4c + lane/16; lanes past K multiply zeros
-            const int kb = min(4 * (c0 + u) + (lane >> 4), kMaxKBlocks - 1);
+            // scale of k-block 4c + lane/16, clamped to a staged (finite) scale:
+            // lanes past K hold zero codes and zero activations, and
+            // fma(0, 0 * s, acc) == acc
+            const int kb = min(4 * (c0 + u) + (lane >> 4), nkb - 1);
             float sv[RW];
 #pragma unroll
-            for (int r = 0; r < RW; ++r) sv[r] = okv[u] ? srow[wave * RW + r][kb] : 0.0f;
+            for (int r = 0; r < RW; ++r) sv[r] = srow[wave * RW + r][kb];
             fp8_chunk<MB, RW, CHECK>(acc, wv[u], xv[u], sv);
         }
         // a segment is four 512-element chunks (U divides 4)
@@ -265,12 +277,10 @@ __global__ __launch_bounds__(256) void gemm_fp8_ksplit_kernel(uint16_t* __restri
         for (int sg = sub; sg < nseg; sg += W) {
             u32x2 wv[4][RW];
             u32x4 xv[4][MB];
-            bool okv[4];
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
                 const int c = 4 * sg + u;
                 const bool ok = c < nfull || (c < nck && c * 512 + lane * 8 < K);
-                okv[u] = ok;
                 const ChunkOffset cw(c < nfull, ok, static_cast<uint32_t>(c) * 512u);
                 const ChunkOffset cx(c < nfull, ok, static_cast<uint32_t>(c) * 1024u);
 #pragma unroll
@@ -285,10 +295,10 @@ __global__ __launch_bounds__(256) void gemm_fp8_ksplit_kernel(uint16_t* __restri
                 for (int m = 0; m < MB; ++m) acc[r][m] = 0.0f;
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
-                const int kb = min(4 * (4 * sg + u) + (lane >> 4), kMaxKBlocks - 1);
+                const int kb = min(4 * (4 * sg + u) + (lane >> 4), nkb - 1);
                 float sv[RW];
 #pragma unroll
-                for (int r = 0; r < RW; ++r) sv[r] = okv[u] ? srow[g * RW + r][kb] : 0.0f;
+                for (int r = 0; r < RW; ++r) sv[r] = srow[g * RW + r][kb];
                 fp8_chunk<MB, RW, CHECK>(acc, wv[u], xv[u], sv);
             }
 #pragma unroll
@@ -325,11 +335,9 @@ struct Fp8Args {
     int M, N, K;
 };
 
-template <int MB, int EPI, bool CHECK>
+template <int MB, int RW, int EPI, bool CHECK>
 void launch_fp8(const Fp8Args& a, hipStream_t s) {
-    constexpr int RW = 2;
-    // two 512-byte chunk groups in flight measured best (M=1: 4.2-5.6 TB/s of
-    // FP8 bytes on the 27B shapes; M=2: 3.1-4.3)
+    // two 512-element chunk groups in flight measured best on MI355X
     constexpr int U = MB <= 2 ? 2 : 1;
     const int64_t groups = (static_cast<int64_t>(a.N) + 4 * RW - 1) / (4 * RW);
     gemm_fp8_kernel<MB, RW, U, EPI, CHECK><<<dim3(static_cast<unsigned>(groups)), dim3(256), 0, s>>>(
@@ -365,11 +373,15 @@ void dispatch_fp8(const Fp8Args& a, hipStream_t s) {
         else launch_fp8_ksplit<2, EPI, CHECK>(a, s);
         return;
     }
-    if (a.M <= 1) launch_fp8<1, EPI, CHECK>(a, s);
-    else if (a.M <= 2) launch_fp8<2, EPI, CHECK>(a, s);
-    else if (a.M <= 4) launch_fp8<4, EPI, CHECK>(a, s);
-    else if (a.M <= 8) launch_fp8<8, EPI, CHECK>(a, s);
-    else launch_fp8<16, EPI, CHECK>(a, s);
+    // Two rows per wave; at M = 2 on wide layers, four rows per wave share
+    // each activation load and conversion (+10-12 % at N >= 16384, fewer
+    // waves hurt narrower layers).
+    if (a.M <= 1) launch_fp8<1, 2, EPI, CHECK>(a, s);
+    else if (a.M <= 2 && a.N >= 16384) launch_fp8<2, 4, EPI, CHECK>(a, s);
+    else if (a.M <= 2) launch_fp8<2, 2, EPI, CHECK>(a, s);
+    else if (a.M <= 4) launch_fp8<4, 2, EPI, CHECK>(a, s);
+    else if (a.M <= 8) launch_fp8<8, 2, EPI, CHECK>(a, s);
+    else launch_fp8<16, 2, EPI, CHECK>(a, s);
 }
 
 template <int EPI>
@@ -432,7 +444,7 @@ extern "C" int hai_gemm_fp8_bf16(void* y, int64_t ldy, const void* x, int64_t ld
     if (M < 0 || M > 16 || N < 0 || K <= 0 || K % 8 != 0 || ldx % 8 != 0 || ldx < K)
         return invalid("gemm_fp8: shape (need 0<=M<=16, K%8==0, ldx%8==0, ldx>=K)");
     if ((K + 127) / 128 > kMaxKBlocks) return invalid("gemm_fp8: K above 32768");
-    if ((N + 8) * K >= (int64_t{1} << 32) || M * ldx * 2 >= (int64_t{1} << 32))
+    if ((N + 16) * K >= (int64_t{1} << 32) || M * ldx * 2 >= (int64_t{1} << 32))
         return invalid("gemm_fp8: W or X exceeds the 4 GiB buffer-offset range");
     if (!aligned16(x) || reinterpret_cast<uintptr_t>(wq) % 8 != 0)
         return invalid("gemm_fp8: x must be 16-byte and wq 8-byte aligned");

@@ -386,8 +386,10 @@ int64_t Engine::read_tensor(uint32_t id, uint16_t* out, int64_t capacity) {
 int Engine::gemm(uint16_t* y, int64_t ldy, const uint16_t* x, int64_t ldx, const Lin& w, int64_t M, int64_t N,
                  int64_t K, int epi, const uint16_t* res, int64_t ldres) {
     if (prof_record_) prof_calls_.push_back({y, ldy, x, ldx, w, M, N, K, epi, res, ldres, nullptr, nullptr});
+    // the engine's codes come from the saturating quantiser: never 0x7F / 0xFF
     if (w.q != nullptr)
-        HAI_TRY(hai_gemm_fp8_bf16(y, ldy, x, ldx, w.q, w.s, w.map, M, N, K, epi, res, ldres, stream_));
+        HAI_TRY(hai_gemm_fp8_bf16(y, ldy, x, ldx, w.q, w.s, w.map, M, N, K, epi | HAI_FP8_NO_SPECIAL_CODES, res,
+                                  ldres, stream_));
     else
         HAI_TRY(hai_gemm_bf16(y, ldy, x, ldx, w.w, M, N, K, epi, res, ldres, stream_));
     return HAI_OK;
@@ -820,8 +822,8 @@ int Engine::profile_verify(int64_t T, int64_t iters, hai_verify_profile* out) {
                 HAI_TRY(hai_gemm_rmsnorm_bf16(c.y, c.ldy, c.x, c.ldx, c.nw, cfg_.rms_eps, 1, c.xn, c.ldx, c.w.w,
                                               c.M, c.N, c.K, c.epi, c.res, c.ldres, stream_));
             else if (c.w.q != nullptr)
-                HAI_TRY(hai_gemm_fp8_bf16(c.y, c.ldy, c.x, c.ldx, c.w.q, c.w.s, c.w.map, c.M, c.N, c.K, c.epi,
-                                          c.res, c.ldres, stream_));
+                HAI_TRY(hai_gemm_fp8_bf16(c.y, c.ldy, c.x, c.ldx, c.w.q, c.w.s, c.w.map, c.M, c.N, c.K,
+                                          c.epi | HAI_FP8_NO_SPECIAL_CODES, c.res, c.ldres, stream_));
             else
                 HAI_TRY(hai_gemm_bf16(c.y, c.ldy, c.x, c.ldx, c.w.w, c.M, c.N, c.K, c.epi, c.res, c.ldres,
                                       stream_));
