@@ -128,6 +128,21 @@ int hai_gemm_fp8_bf16(void* y, int64_t ldy, const void* x, int64_t ldx,
                       const int32_t* scale_rows, int64_t M, int64_t N,
                       int64_t K, int epilogue, const void* res, int64_t ld_res,
                       void* stream);
+/* RMSNorm(+offset) of the rows x [M, K] fused into the FP8 linear layer, as
+ * hai_gemm_rmsnorm_bf16 is for bf16 weights: the qwen_rmsnorm_reference ->
+ * Linear pair of qwen_reference.cc:108-119 and linear.cc:117-179 over a
+ * QuantizedWeight (qwen3_weights.cc:131-182).  The normalised rows are
+ * bit-identical to hai_rmsnorm_bf16's;
+ * xn_out (optional) receives the normalised rows.  Above
+ * HAI_GEMM_RMSNORM_FUSED_MAX elements it runs rmsnorm then the GEMM and needs
+ * xn_out. */
+int hai_gemm_rmsnorm_fp8_bf16(void* y, int64_t ldy, const void* x,
+                              int64_t ldx, const void* norm_w, float eps,
+                              int unit_offset, void* xn_out, int64_t ld_xn,
+                              const void* wq, const float* scales,
+                              const int32_t* scale_rows, int64_t M, int64_t N,
+                              int64_t K, int epilogue, const void* res,
+                              int64_t ld_res, void* stream);
 /* Block-scaled E4M3 quantisation of a bf16 weight [rows, cols] (row pitch
  * ldw elements) into codes with row pitch ldq bytes, given its scales
  * [ceil(rows/128)][ceil(cols/128)] fp32: q = E4M3 of the fp32 quotient w / s,

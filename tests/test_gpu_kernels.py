@@ -591,3 +591,58 @@ def test_fp8_synthetic_scales_match_oracle():
         d = out_buf(n * 4)
         hai.check(kern().hai_fill_synthetic_scales_f32(d.ptr, n, seed, tid, None), "fill_scales")
         assert np.array_equal(d.download(np.float32), orc.fp8_synthetic_scales(seed, tid, n))
+
+
+@pytest.mark.parametrize("M,N,K_,epi,with_xn,mapped", [
+    (1, 700, 5120, 0, False, False), (2, 2 * 8200, 1000, 2, True, False), (2, 640, 2048, 1, False, True),
+    (3, 300, 5120, 0, True, False), (16, 256, 1024, 2, False, False), (2, 16400, 768, 0, True, True)])
+def test_gemm_rmsnorm_fp8_fused(M, N, K_, epi, with_xn, mapped):
+    """hai_gemm_rmsnorm_fp8_bf16 == rmsnorm then the FP8 GEMM (LDS prologue
+    below the fused limit, two kernels above it), with and without a
+    per-row scale map (two stacked tensors, the second starting mid-block)."""
+    rng = np.random.default_rng(131 + M * 7 + N + K_ + epi)
+    x, xb = rand_bf16(rng, (M, K_))
+    nw, nwb = rand_bf16(rng, (K_,), 0.02)
+    xn_want = orc.rmsnorm(x, nw, 1e-6, True)
+    if epi == hai.EPI_SILU_MUL:
+        F = N // 2
+        qg, sg = _fp8_weights(rng, F, K_)
+        qu, su = _fp8_weights(rng, F, K_)
+        q = np.empty((N, K_), np.uint8)
+        q[0::2], q[1::2] = qg, qu
+        s = np.stack([sg, su])
+        y_lin = None
+        want_lin = orc.silu_mul(orc.gemm_fp8(xn_want, qg, sg), orc.gemm_fp8(xn_want, qu, su))
+        mp = None
+    elif mapped:
+        n0 = N // 2 + 64
+        q0, s0 = _fp8_weights(rng, n0, K_)
+        q1, s1 = _fp8_weights(rng, N - n0, K_)
+        q, s = np.concatenate([q0, q1]), np.concatenate([s0, s1])
+        mp = np.array([r // 128 for r in range(n0)] + [s0.shape[0] + r // 128 for r in range(N - n0)], np.int32)
+        y_lin = np.concatenate([orc.gemm_fp8(xn_want, q0, s0), orc.gemm_fp8(xn_want, q1, s1)], axis=1)
+    else:
+        q, s = _fp8_weights(rng, N, K_)
+        mp = None
+        y_lin = orc.gemm_fp8(xn_want, q, s)
+    ncols = N // 2 if epi == hai.EPI_SILU_MUL else N
+    need_xn = with_xn or M * K_ > 16384
+    dx, dnw, dq, ds = dev(xb), dev(nwb), dev(q), dev(s)
+    dm = dev(mp) if mp is not None else None
+    dxn = out_buf(M * K_ * 2) if need_xn else None
+    h, hb = rand_bf16(rng, (M, ncols))
+    dy = dev(hb) if epi == hai.EPI_RESIDUAL else out_buf(M * ncols * 2)
+    hai.check(kern().hai_gemm_rmsnorm_fp8_bf16(dy.ptr, ncols, dx.ptr, K_, dnw.ptr, 1e-6, 1,
+                                               dxn.ptr if dxn else None, K_, dq.ptr, ds.ptr,
+                                               dm.ptr if dm else None, M, N, K_, epi,
+                                               dy.ptr if epi == hai.EPI_RESIDUAL else None, ncols, None),
+              "gemm_rmsnorm_fp8")
+    if epi == hai.EPI_STORE:
+        want = y_lin
+    elif epi == hai.EPI_RESIDUAL:
+        want = orc.add(h, y_lin)
+    else:
+        want = want_lin
+    assert_bits_equal(dy.download(np.uint16), want, f"gemm_rmsnorm_fp8 {M}x{N}x{K_} epi {epi}")
+    if dxn is not None:
+        assert_bits_equal(dxn.download(np.uint16), xn_want, "normalised rows")

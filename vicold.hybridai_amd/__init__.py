@@ -66,6 +66,8 @@ _KERNEL_SIGS = {
     "hai_gemm_rmsnorm_bf16": [VP, I64, VP, I64, VP, F32, ctypes.c_int, VP, I64, VP, I64, I64, I64, ctypes.c_int,
                               VP, I64, VP],
     "hai_gemm_fp8_bf16": [VP, I64, VP, I64, VP, VP, VP, I64, I64, I64, ctypes.c_int, VP, I64, VP],
+    "hai_gemm_rmsnorm_fp8_bf16": [VP, I64, VP, I64, VP, F32, ctypes.c_int, VP, I64, VP, VP, VP, I64, I64, I64,
+                                  ctypes.c_int, VP, I64, VP],
     "hai_fp8_quantize_bf16": [VP, I64, VP, I64, VP, I64, I64, VP],
     "hai_fill_synthetic_scales_f32": [VP, I64, ctypes.c_uint64, ctypes.c_uint32, VP],
     "hai_rmsnorm_bf16": [VP, I64, VP, I64, VP, I64, I64, F32, ctypes.c_int, VP],

@@ -17,8 +17,7 @@
 //     reproduce, so it is not used on the bit-exact path.
 //   * Epilogues fuse the residual add (h = bf16(h + bf16(acc))) and the
 //     SwiGLU product for interleaved gate/up rows.
-#include "hai_common.h"
-#include "hai_device.h"
+#include "hai_gemm_common.h"
 
 #include <mutex>
 #include <vector>
@@ -27,86 +26,15 @@ namespace {
 
 using namespace hai;
 
-// Optional RMSNorm prologue (NORM): the block stages its M activation rows
-// in LDS, reduces each row's sum of squares in L64 order, and normalises in
-// place, y_k = bf16((x_k * inv) * (w_k + off)), exactly as rmsnorm_kernel;
-// the main loop then reads x from LDS.  Needs M * K <= kNormMaxElems.
-struct NormArgs {
-    const uint16_t* w = nullptr;  // norm weight [K]
-    float eps = 0.0f;
-    float off = 0.0f;             // 1 for the (w + 1) model norms
-    uint16_t* xn = nullptr;       // optional copy of the normalised rows (block 0 writes it)
-    int64_t ldxn = 0;
-};
-
-constexpr int kNormMaxElems = HAI_GEMM_RMSNORM_FUSED_MAX;  // M * K: 32 KB of LDS
-
 template <int MB, int RW, int U, int EPI, bool NORM>
 __global__ __launch_bounds__(256) void gemm_bf16_kernel(
     uint16_t* __restrict__ y, int64_t ldy, const uint16_t* __restrict__ x, int64_t ldx,
     const uint16_t* __restrict__ w, const uint16_t* res, int64_t ldres, int M, int N, int K, NormArgs na) {
     const int lane = threadIdx.x & 63;
     const int wave = wave_index();
-    extern __shared__ u32x4 xs[];  // NORM: [M][K/8] normalised rows
+    extern __shared__ u32x4 xs[];  // NORM: [M][K/8] normalised rows, then the norm weight
     const int npr = K >> 3;        // 16-byte pieces per row
-    if constexpr (NORM) {
-        // Raw rows and the norm weight are fetched together (one latency), the
-        // rows parked in LDS while one wave per row reduces its sum of squares.
-        __shared__ float inv_sh[16];
-        const int total = M * npr;
-        for (int e0 = 0; e0 < total; e0 += 1024) {
-            u32x4 xr[4], wr[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int e = e0 + threadIdx.x + 256 * i;
-                const int r = e / npr;
-                const int p = e - r * npr;
-                if (e < total) xr[i] = *reinterpret_cast<const u32x4*>(x + r * ldx + p * 8);
-                if (e < npr) wr[i] = *reinterpret_cast<const u32x4*>(na.w + p * 8);
-            }
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int e = e0 + threadIdx.x + 256 * i;
-                if (e < total) xs[e] = xr[i];
-                if (e < npr) xs[total + e] = wr[i];  // norm weight staged once, behind the rows
-            }
-        }
-        __syncthreads();
-        for (int r = wave; r < M; r += 4) {
-            float acc = 0.0f;
-            for (int p = lane; p < npr; p += 64) {
-                const u32x4 d = xs[r * npr + p];
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const float a = lo_bf(d[q]);
-                    const float b = hi_bf(d[q]);
-                    acc = fma_(a, a, acc);
-                    acc = fma_(b, b, acc);
-                }
-            }
-            const float ss = wave_sum64(acc);
-            if (lane == 0) inv_sh[r] = 1.0f / csqrt(ss / static_cast<float>(K) + na.eps);
-        }
-        __syncthreads();
-        for (int e = threadIdx.x; e < total; e += 256) {
-            const int r = e / npr;
-            const int p = e - r * npr;
-            const float inv = inv_sh[r];
-            const u32x4 xv0 = xs[e];
-            const u32x4 wv0 = xs[total + p];
-            u32x4 o;
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const uint16_t a = f2bf((lo_bf(xv0[q]) * inv) * (lo_bf(wv0[q]) + na.off));
-                const uint16_t b = f2bf((hi_bf(xv0[q]) * inv) * (hi_bf(wv0[q]) + na.off));
-                o[q] = static_cast<uint32_t>(a) | (static_cast<uint32_t>(b) << 16);
-            }
-            xs[e] = o;
-            if (na.xn != nullptr && blockIdx.x == 0)
-                *reinterpret_cast<u32x4*>(na.xn + r * na.ldxn + p * 8) = o;
-        }
-        __syncthreads();
-    }
+    if constexpr (NORM) rmsnorm_rows_to_lds(xs, x, ldx, M, K, na);
 
     // Byte offsets fit 32 bits: the caller bounds N*K*2 and M*ldx*2 below 4 GiB.
     const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, static_cast<uint32_t>(static_cast<int64_t>(N) * K * 2));
@@ -355,31 +283,6 @@ struct GemmArgs {
     NormArgs na;
 };
 
-// Resident blocks per CU of one NORM instance at the given LDS size, and
-// the CU count, queried once per (device, instance, size).
-template <typename Kern>
-int64_t resident_blocks(Kern kern, size_t shmem) {
-    struct Entry {
-        int dev;
-        size_t shmem;
-        int64_t blocks;
-    };
-    static std::mutex mu;
-    static std::vector<Entry> cache;
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return 0;
-    std::lock_guard<std::mutex> lock(mu);
-    for (const auto& e : cache)
-        if (e.dev == dev && e.shmem == shmem) return e.blocks;
-    int per_cu = 0, cus = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 256, shmem) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-        return 0;
-    const int64_t blocks = static_cast<int64_t>(per_cu < 1 ? 1 : per_cu) * (cus < 1 ? 1 : cus);
-    cache.push_back({dev, shmem, blocks});
-    return blocks;
-}
-
 template <int MB, int RW, int EPI, bool NORM>
 void launch_gemm(const GemmArgs& a, hipStream_t s) {
     constexpr int U = MB <= 2 ? 4 : (MB <= 8 ? 2 : 1);
@@ -389,7 +292,7 @@ void launch_gemm(const GemmArgs& a, hipStream_t s) {
     const size_t shmem = NORM ? static_cast<size_t>(a.M + 1) * a.K * 2 : 0;
     int64_t blocks = groups;
     if (NORM) {
-        const int64_t resident = resident_blocks(kern, shmem);
+        const int64_t resident = resident_blocks(reinterpret_cast<const void*>(kern), shmem);
         if (resident > 0 && resident < blocks) blocks = resident;
     }
     kern<<<dim3(static_cast<unsigned>(blocks)), dim3(256), shmem, s>>>(a.y, a.ldy, a.x, a.ldx, a.w, a.res,
@@ -408,13 +311,15 @@ void launch_ksplit(const GemmArgs& a, hipStream_t s) {
 
 // Four waves per row pair, each on its own K segments, for the short,
 // wide-K layers where that measured faster on MI355X: M <= 2 with K >= 8192
-// (down projection, +3 % at M=2, +6 % at M=1) and M = 1 with N <= 8192
-// (out / o projections, +7 %).  LDS holds the segment partials (<= 64 KB).
+// (down projection, +3 % at M=2, +6 % at M=1), M = 1 with N <= 8192
+// (out / o projections, +7 %), and any layer of at most 1024 rows, which
+// one wave per row pair leaves mostly idle (in_proj_a|b: 14 -> 5 us).  LDS
+// holds the segment partials (<= 64 KB).
 bool use_ksplit(const GemmArgs& a) {
     if (a.M > 2 || a.N > 8192) return false;
     const int64_t nseg = ((a.K + 511) / 512 + 3) / 4;
     if (nseg * 2 * a.M * 64 * 4 > 64 * 1024) return false;
-    return a.K >= 8192 || a.M == 1;
+    return a.K >= 8192 || a.M == 1 || a.N <= 1024;
 }
 
 template <int EPI, bool NORM>
@@ -467,6 +372,33 @@ int check_shape(const void* y, const void* x, const void* w, int64_t M, int64_t 
 }
 
 }  // namespace
+
+namespace hai {
+
+int64_t resident_blocks(const void* kernel, size_t shmem) {
+    struct Entry {
+        int dev;
+        const void* kernel;
+        size_t shmem;
+        int64_t blocks;
+    };
+    static std::mutex mu;
+    static std::vector<Entry> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    std::lock_guard<std::mutex> lock(mu);
+    for (const auto& e : cache)
+        if (e.dev == dev && e.kernel == kernel && e.shmem == shmem) return e.blocks;
+    int per_cu = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, shmem) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return 0;
+    const int64_t blocks = static_cast<int64_t>(per_cu < 1 ? 1 : per_cu) * (cus < 1 ? 1 : cus);
+    cache.push_back({dev, kernel, shmem, blocks});
+    return blocks;
+}
+
+}  // namespace hai
 
 extern "C" int hai_gemm_bf16(void* y, int64_t ldy, const void* x, int64_t ldx, const void* w, int64_t M,
                              int64_t N, int64_t K, int epilogue, const void* res, int64_t ld_res,

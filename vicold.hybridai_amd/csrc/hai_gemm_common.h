@@ -1,0 +1,94 @@
+// hai_gemm_common.h -- pieces shared by the skinny bf16 and FP8 GEMMs: the
+// RMSNorm prologue that stages normalised activation rows in LDS, and the
+// resident-block query that sizes persistent grids.
+#pragma once
+
+#include "hai_common.h"
+#include "hai_device.h"
+
+namespace hai {
+
+// RMSNorm prologue arguments: y_k = bf16((x_k * inv) * (w_k + off)), exactly
+// as rmsnorm_kernel.  Needs M * K <= kNormMaxElems (LDS holds the rows and
+// the norm weight).
+struct NormArgs {
+    const uint16_t* w = nullptr;  // norm weight [K]
+    float eps = 0.0f;
+    float off = 0.0f;             // 1 for the (w + 1) model norms
+    uint16_t* xn = nullptr;       // optional copy of the normalised rows (block 0 writes it)
+    int64_t ldxn = 0;
+};
+
+constexpr int kNormMaxElems = HAI_GEMM_RMSNORM_FUSED_MAX;  // M * K: 32 KB of LDS
+
+// Stages the M activation rows [M, K] (row pitch ldx) in xs as 16-byte
+// pieces, normalised: the raw rows and the norm weight are fetched together
+// (one latency), one wave per row reduces the sum of squares in L64 order,
+// then every element is scaled in place.  xs holds (M + 1) * K / 8 pieces;
+// a 256-thread block; ends with a block barrier.
+__device__ __forceinline__ void rmsnorm_rows_to_lds(u32x4* xs, const uint16_t* __restrict__ x, int64_t ldx,
+                                                    int M, int K, const NormArgs& na) {
+    __shared__ float inv_sh[16];
+    const int lane = threadIdx.x & 63;
+    const int wave = wave_index();
+    const int npr = K >> 3;  // 16-byte pieces per row
+    const int total = M * npr;
+    for (int e0 = 0; e0 < total; e0 += 1024) {
+        u32x4 xr[4], wr[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int e = e0 + threadIdx.x + 256 * i;
+            const int r = e / npr;
+            const int p = e - r * npr;
+            if (e < total) xr[i] = *reinterpret_cast<const u32x4*>(x + r * ldx + p * 8);
+            if (e < npr) wr[i] = *reinterpret_cast<const u32x4*>(na.w + p * 8);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int e = e0 + threadIdx.x + 256 * i;
+            if (e < total) xs[e] = xr[i];
+            if (e < npr) xs[total + e] = wr[i];  // norm weight staged once, behind the rows
+        }
+    }
+    __syncthreads();
+    for (int r = wave; r < M; r += 4) {
+        float acc = 0.0f;
+        for (int p = lane; p < npr; p += 64) {
+            const u32x4 d = xs[r * npr + p];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float a = lo_bf(d[q]);
+                const float b = hi_bf(d[q]);
+                acc = fma_(a, a, acc);
+                acc = fma_(b, b, acc);
+            }
+        }
+        const float ss = wave_sum64(acc);
+        if (lane == 0) inv_sh[r] = 1.0f / csqrt(ss / static_cast<float>(K) + na.eps);
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < total; e += 256) {
+        const int r = e / npr;
+        const int p = e - r * npr;
+        const float inv = inv_sh[r];
+        const u32x4 xv0 = xs[e];
+        const u32x4 wv0 = xs[total + p];
+        u32x4 o;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint16_t a = f2bf((lo_bf(xv0[q]) * inv) * (lo_bf(wv0[q]) + na.off));
+            const uint16_t b = f2bf((hi_bf(xv0[q]) * inv) * (hi_bf(wv0[q]) + na.off));
+            o[q] = static_cast<uint32_t>(a) | (static_cast<uint32_t>(b) << 16);
+        }
+        xs[e] = o;
+        if (na.xn != nullptr && blockIdx.x == 0) *reinterpret_cast<u32x4*>(na.xn + r * na.ldxn + p * 8) = o;
+    }
+    __syncthreads();
+}
+
+// Blocks of 256 threads of `kernel` with `shmem` bytes of dynamic LDS that
+// the current device holds at once (occupancy x CUs); 0 if unknown.  Cached
+// per (device, kernel, shmem).
+int64_t resident_blocks(const void* kernel, size_t shmem);
+
+}  // namespace hai

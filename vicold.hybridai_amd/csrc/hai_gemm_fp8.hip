@@ -20,8 +20,7 @@
 //     paired scales (fused SwiGLU over gate/up rows interleaved as
 //     (gate_f, up_f)) row r reads plane r & 1, block (r >> 1) / 128 of a
 //     [2][ceil(F/128)][ceil(K/128)] scale tensor.
-#include "hai_common.h"
-#include "hai_device.h"
+#include "hai_gemm_common.h"
 
 namespace {
 
@@ -139,100 +138,158 @@ __device__ __forceinline__ void fp8_store(uint16_t* y, int64_t ldy, const uint16
     }
 }
 
-template <int MB, int RW, int U, int EPI, bool CHECK>
+// One group = RW consecutive weight rows of one wave.  The plain launch runs
+// one group per wave.  The NORM launch (RMSNorm prologue, activations read
+// from LDS) has a grid sized to the machine so that the prologue is paid once
+// per resident block; each wave then walks a contiguous run of groups.  A
+// wave keeps its rows' scale rows in its own LDS rows and restages a row
+// slot only when the scale row changes (every 128 rows of a tensor), so
+// waves never wait for each other after the prologue.
+template <int MB, int RW, int U, int EPI, bool CHECK, bool NORM>
 __global__ __launch_bounds__(256) void gemm_fp8_kernel(uint16_t* __restrict__ y, int64_t ldy,
                                                        const uint16_t* __restrict__ x, int64_t ldx,
                                                        const uint8_t* __restrict__ wq,
                                                        const float* __restrict__ scales,
                                                        const int32_t* __restrict__ scale_rows, int paired,
-                                                       const uint16_t* res, int64_t ldres, int M, int N, int K) {
-    constexpr int BR = 4 * RW;  // weight rows per block
-    __shared__ float srow[BR][kMaxKBlocks];
+                                                       const uint16_t* res, int64_t ldres, int M, int N, int K,
+                                                       NormArgs na) {
+    __shared__ float srow[4 * RW][kMaxKBlocks];
+    extern __shared__ u32x4 xs[];  // NORM: [M][K/8] normalised rows, then the norm weight
     const int lane = threadIdx.x & 63;
     const int wave = wave_index();
     const int nkb = (K + 127) / 128;
-    // the scale row of each of this block's weight rows: the caller's map, or
-    // the 128-row block of a plain / paired (gate, up) layout
-    stage_scales(srow, static_cast<int64_t>(blockIdx.x) * BR, BR, scales, scale_rows, paired, N, nkb);
-    __syncthreads();
-    const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * 4 + wave) * RW;
-    if (row0 >= N) return;
-    const int nrows = static_cast<int>(min(static_cast<int64_t>(RW), static_cast<int64_t>(N) - row0));
+    const int npr = K >> 3;
+    if constexpr (NORM) rmsnorm_rows_to_lds(xs, x, ldx, M, K, na);
+    float (*wsrow)[kMaxKBlocks] = srow + wave * RW;
+    const int64_t nsb = ((N >> 1) + 127) / 128;
+    auto scale_row = [&](int64_t r) -> int64_t {
+        return scale_rows ? scale_rows[r] : (paired ? (r & 1) * nsb + (r >> 1) / 128 : r / 128);
+    };
 
     // Byte offsets fit 32 bits: the caller bounds N*K and M*ldx*2 below 4 GiB.
     const __amdgpu_buffer_rsrc_t rw = make_rsrc(wq, static_cast<uint32_t>(static_cast<int64_t>(N) * K));
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, static_cast<uint32_t>(static_cast<int64_t>(M) * ldx * 2));
-    uint32_t woff[RW], xoff[MB];
+    const int nck = (K + 511) / 512;
+    const int nfull = K / 512;
+    const int64_t nwg = (static_cast<int64_t>(N) + RW - 1) / RW;
+    int64_t staged[RW];  // scale row held by each of the wave's LDS row slots
 #pragma unroll
-    for (int r = 0; r < RW; ++r) woff[r] = static_cast<uint32_t>((row0 + r) * static_cast<int64_t>(K) + lane * 8);
-#pragma unroll
-    for (int m = 0; m < MB; ++m) xoff[m] = static_cast<uint32_t>((static_cast<int64_t>(m) * ldx + lane * 8) * 2);
+    for (int r = 0; r < RW; ++r) staged[r] = -1;
 
-    // acc: the current 2048-element segment; tot: segments folded in order
-    float acc[RW][MB], tot[RW][MB];
+    auto group = [&](int64_t g) {
+        const int64_t row0 = g * RW;
+        const int nrows = static_cast<int>(min(static_cast<int64_t>(RW), static_cast<int64_t>(N) - row0));
+        // (re)stage the slots whose scale row changed; LDS accesses of one wave
+        // complete in order, so the previous group's reads are done
+        bool restage = false;
+        int64_t want[RW];
 #pragma unroll
-    for (int r = 0; r < RW; ++r)
+        for (int r = 0; r < RW; ++r) {
+            want[r] = scale_row(min(row0 + r, static_cast<int64_t>(N) - 1));
+            restage |= want[r] != staged[r];
+        }
+        if (restage) {
 #pragma unroll
-        for (int m = 0; m < MB; ++m) acc[r][m] = tot[r][m] = 0.0f;
-    auto fold = [&]() {
+            for (int r = 0; r < RW; ++r) {
+                if (want[r] == staged[r]) continue;
+                for (int kb = lane; kb < nkb; kb += 64) wsrow[r][kb] = scales[want[r] * nkb + kb];
+                staged[r] = want[r];
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
+
+        uint32_t woff[RW], xoff[MB];
+#pragma unroll
+        for (int r = 0; r < RW; ++r) woff[r] = static_cast<uint32_t>((row0 + r) * static_cast<int64_t>(K) + lane * 8);
+#pragma unroll
+        for (int m = 0; m < MB; ++m) xoff[m] = static_cast<uint32_t>((static_cast<int64_t>(m) * ldx + lane * 8) * 2);
+
+        // acc: the current 2048-element segment; tot: segments folded in order
+        float acc[RW][MB], tot[RW][MB];
 #pragma unroll
         for (int r = 0; r < RW; ++r)
 #pragma unroll
-            for (int m = 0; m < MB; ++m) {
-                tot[r][m] = tot[r][m] + acc[r][m];
-                acc[r][m] = 0.0f;
+            for (int m = 0; m < MB; ++m) acc[r][m] = tot[r][m] = 0.0f;
+        auto fold = [&]() {
+#pragma unroll
+            for (int r = 0; r < RW; ++r)
+#pragma unroll
+                for (int m = 0; m < MB; ++m) {
+                    tot[r][m] = tot[r][m] + acc[r][m];
+                    acc[r][m] = 0.0f;
+                }
+        };
+
+        for (int c0 = 0; c0 < nck; c0 += U) {
+            u32x2 wv[U][RW];
+            u32x4 xv[U][MB];
+            if (c0 + U <= nfull) {
+                // every lane inside K: chunk offsets go in the scalar operand
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const uint32_t c = static_cast<uint32_t>(c0 + u);
+#pragma unroll
+                    for (int r = 0; r < RW; ++r) wv[u][r] = bload8(rw, woff[r], c * 512u);
+#pragma unroll
+                    for (int m = 0; m < MB; ++m) {
+                        if constexpr (NORM)
+                            xv[u][m] = m < M ? xs[m * npr + c * 64 + lane] : u32x4{0u, 0u, 0u, 0u};
+                        else
+                            xv[u][m] = bload(rx, xoff[m], c * 1024u);
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const int c = c0 + u;
+                    const bool ok = c < nfull || (c < nck && c * 512 + lane * 8 < K);
+                    const ChunkOffset cw(c < nfull, ok, static_cast<uint32_t>(c) * 512u);
+                    const ChunkOffset cx(c < nfull, ok, static_cast<uint32_t>(c) * 1024u);
+#pragma unroll
+                    for (int r = 0; r < RW; ++r) wv[u][r] = bload8(rw, cw.v(woff[r]), cw.s);
+#pragma unroll
+                    for (int m = 0; m < MB; ++m) {
+                        if constexpr (NORM)
+                            xv[u][m] = (ok && m < M) ? xs[m * npr + c * 64 + lane] : u32x4{0u, 0u, 0u, 0u};
+                        else
+                            xv[u][m] = bload(rx, cx.v(xoff[m]), cx.s);
+                    }
+                }
             }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                // scale of k-block 4c + lane/16, clamped to a staged (finite)
+                // scale: lanes past K hold zero codes and zero activations,
+                // and fma(0, 0 * s, acc) == acc
+                const int kb = min(4 * (c0 + u) + (lane >> 4), nkb - 1);
+                float sv[RW];
+#pragma unroll
+                for (int r = 0; r < RW; ++r) sv[r] = wsrow[r][kb];
+                fp8_chunk<MB, RW, CHECK>(acc, wv[u], xv[u], sv);
+            }
+            // a segment is four 512-element chunks (U divides 4)
+            if (((c0 + U) & 3) == 0) fold();
+        }
+        fold();
+
+#pragma unroll
+        for (int r = 0; r < RW; ++r)
+#pragma unroll
+            for (int m = 0; m < MB; ++m) tot[r][m] = wave_sum64(tot[r][m]);
+        fp8_store<MB, RW, EPI>(y, ldy, res, ldres, tot, lane, row0, nrows, M);
     };
 
-    const int nck = (K + 511) / 512;
-    const int nfull = K / 512;
-    for (int c0 = 0; c0 < nck; c0 += U) {
-        u32x2 wv[U][RW];
-        u32x4 xv[U][MB];
-        if (c0 + U <= nfull) {
-            // every lane inside K: chunk offsets go in the scalar operand
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const uint32_t c = static_cast<uint32_t>(c0 + u);
-#pragma unroll
-                for (int r = 0; r < RW; ++r) wv[u][r] = bload8(rw, woff[r], c * 512u);
-#pragma unroll
-                for (int m = 0; m < MB; ++m) xv[u][m] = bload(rx, xoff[m], c * 1024u);
-            }
-        } else {
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const int c = c0 + u;
-                const bool ok = c < nfull || (c < nck && c * 512 + lane * 8 < K);
-                const ChunkOffset cw(c < nfull, ok, static_cast<uint32_t>(c) * 512u);
-                const ChunkOffset cx(c < nfull, ok, static_cast<uint32_t>(c) * 1024u);
-#pragma unroll
-                for (int r = 0; r < RW; ++r) wv[u][r] = bload8(rw, cw.v(woff[r]), cw.s);
-#pragma unroll
-                for (int m = 0; m < MB; ++m) xv[u][m] = bload(rx, cx.v(xoff[m]), cx.s);
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            // scale of k-block 4c + lane/16, clamped to a staged (finite) scale:
-            // lanes past K hold zero codes and zero activations, and
-            // fma(0, 0 * s, acc) == acc
-            const int kb = min(4 * (c0 + u) + (lane >> 4), nkb - 1);
-            float sv[RW];
-#pragma unroll
-            for (int r = 0; r < RW; ++r) sv[r] = srow[wave * RW + r][kb];
-            fp8_chunk<MB, RW, CHECK>(acc, wv[u], xv[u], sv);
-        }
-        // a segment is four 512-element chunks (U divides 4)
-        if (((c0 + U) & 3) == 0) fold();
+    const int64_t w = static_cast<int64_t>(blockIdx.x) * 4 + wave;
+    if constexpr (NORM) {
+        const int64_t waves = static_cast<int64_t>(gridDim.x) * 4;
+        const int64_t per = (nwg + waves - 1) / waves;
+        const int64_t g1 = min(nwg, (w + 1) * per);
+        for (int64_t g = w * per; g < g1; ++g) group(g);
+    } else {
+        if (w < nwg) group(w);
     }
-    fold();
-
-#pragma unroll
-    for (int r = 0; r < RW; ++r)
-#pragma unroll
-        for (int m = 0; m < MB; ++m) tot[r][m] = wave_sum64(tot[r][m]);
-    fp8_store<MB, RW, EPI>(y, ldy, res, ldres, tot, lane, row0, nrows, M);
 }
 
 // K-split form: W waves share each row group, wave `sub` taking the
@@ -333,15 +390,24 @@ struct Fp8Args {
     const uint16_t* res;
     int64_t ldres;
     int M, N, K;
+    NormArgs na;
 };
 
-template <int MB, int RW, int EPI, bool CHECK>
+template <int MB, int RW, int EPI, bool CHECK, bool NORM>
 void launch_fp8(const Fp8Args& a, hipStream_t s) {
     // two 512-element chunk groups in flight measured best on MI355X
     constexpr int U = MB <= 2 ? 2 : 1;
-    const int64_t groups = (static_cast<int64_t>(a.N) + 4 * RW - 1) / (4 * RW);
-    gemm_fp8_kernel<MB, RW, U, EPI, CHECK><<<dim3(static_cast<unsigned>(groups)), dim3(256), 0, s>>>(
-        a.y, a.ldy, a.x, a.ldx, a.wq, a.scales, a.scale_rows, a.paired, a.res, a.ldres, a.M, a.N, a.K);
+    auto* kern = gemm_fp8_kernel<MB, RW, U, EPI, CHECK, NORM>;
+    int64_t blocks = (static_cast<int64_t>(a.N) + 4 * RW - 1) / (4 * RW);
+    // NORM: LDS holds the M rows and the norm weight staged behind them.
+    const size_t shmem = NORM ? static_cast<size_t>(a.M + 1) * a.K * 2 : 0;
+    if (NORM) {
+        const int64_t resident = resident_blocks(reinterpret_cast<const void*>(kern), shmem);
+        if (resident > 0 && resident < blocks) blocks = resident;
+    }
+    kern<<<dim3(static_cast<unsigned>(blocks)), dim3(256), shmem, s>>>(a.y, a.ldy, a.x, a.ldx, a.wq, a.scales,
+                                                                     a.scale_rows, a.paired, a.res, a.ldres, a.M,
+                                                                     a.N, a.K, a.na);
 }
 
 constexpr int kKsplitRW = 2, kKsplitW = 4;
@@ -366,9 +432,9 @@ bool use_ksplit_fp8(const Fp8Args& a) {
     return nseg * kKsplitRW * a.M * 64 * 4 <= 64 * 1024;
 }
 
-template <int EPI, bool CHECK>
+template <int EPI, bool CHECK, bool NORM>
 void dispatch_fp8(const Fp8Args& a, hipStream_t s) {
-    if (use_ksplit_fp8(a)) {
+    if (!NORM && use_ksplit_fp8(a)) {
         if (a.M <= 1) launch_fp8_ksplit<1, EPI, CHECK>(a, s);
         else launch_fp8_ksplit<2, EPI, CHECK>(a, s);
         return;
@@ -376,18 +442,18 @@ void dispatch_fp8(const Fp8Args& a, hipStream_t s) {
     // Two rows per wave; at M = 2 on wide layers, four rows per wave share
     // each activation load and conversion (+10-12 % at N >= 16384, fewer
     // waves hurt narrower layers).
-    if (a.M <= 1) launch_fp8<1, 2, EPI, CHECK>(a, s);
-    else if (a.M <= 2 && a.N >= 16384) launch_fp8<2, 4, EPI, CHECK>(a, s);
-    else if (a.M <= 2) launch_fp8<2, 2, EPI, CHECK>(a, s);
-    else if (a.M <= 4) launch_fp8<4, 2, EPI, CHECK>(a, s);
-    else if (a.M <= 8) launch_fp8<8, 2, EPI, CHECK>(a, s);
-    else launch_fp8<16, 2, EPI, CHECK>(a, s);
+    if (a.M <= 1) launch_fp8<1, 2, EPI, CHECK, NORM>(a, s);
+    else if (a.M <= 2 && a.N >= 16384) launch_fp8<2, 4, EPI, CHECK, NORM>(a, s);
+    else if (a.M <= 2) launch_fp8<2, 2, EPI, CHECK, NORM>(a, s);
+    else if (a.M <= 4) launch_fp8<4, 2, EPI, CHECK, NORM>(a, s);
+    else if (a.M <= 8) launch_fp8<8, 2, EPI, CHECK, NORM>(a, s);
+    else launch_fp8<16, 2, EPI, CHECK, NORM>(a, s);
 }
 
-template <int EPI>
+template <int EPI, bool NORM>
 void dispatch_fp8_codes(const Fp8Args& a, bool check, hipStream_t s) {
-    if (check) dispatch_fp8<EPI, true>(a, s);
-    else dispatch_fp8<EPI, false>(a, s);
+    if (check) dispatch_fp8<EPI, true, NORM>(a, s);
+    else dispatch_fp8<EPI, false, NORM>(a, s);
 }
 
 // E4M3 code of v, rounded to nearest even, saturated at +-448; NaN -> 0.
@@ -436,9 +502,10 @@ extern "C" int hai_fp8_quantize_bf16(void* q, int64_t ldq, const void* w, int64_
     return launched("fp8_quantize_kernel");
 }
 
-extern "C" int hai_gemm_fp8_bf16(void* y, int64_t ldy, const void* x, int64_t ldx, const void* wq,
-                                 const float* scales, const int32_t* scale_rows, int64_t M, int64_t N,
-                                 int64_t K, int epilogue, const void* res, int64_t ld_res, void* stream) {
+namespace {
+
+int check_fp8(const void* y, const void* x, const void* wq, const float* scales, int64_t M, int64_t N, int64_t K,
+              int64_t ldx) {
     if (y == nullptr || x == nullptr || wq == nullptr || scales == nullptr)
         return invalid("gemm_fp8: null pointer");
     if (M < 0 || M > 16 || N < 0 || K <= 0 || K % 8 != 0 || ldx % 8 != 0 || ldx < K)
@@ -448,28 +515,76 @@ extern "C" int hai_gemm_fp8_bf16(void* y, int64_t ldy, const void* x, int64_t ld
         return invalid("gemm_fp8: W or X exceeds the 4 GiB buffer-offset range");
     if (!aligned16(x) || reinterpret_cast<uintptr_t>(wq) % 8 != 0)
         return invalid("gemm_fp8: x must be 16-byte and wq 8-byte aligned");
-    if (M == 0 || N == 0) return HAI_OK;
-    Fp8Args a{static_cast<uint16_t*>(y), ldy, static_cast<const uint16_t*>(x), ldx,
-              static_cast<const uint8_t*>(wq), scales, scale_rows, 0, static_cast<const uint16_t*>(res), ld_res,
-              int(M), int(N), int(K)};
-    const hipStream_t s = as_stream(stream);
+    return HAI_OK;
+}
+
+template <bool NORM>
+int dispatch_fp8_epi(Fp8Args& a, int epilogue, hipStream_t s) {
     const bool check = (epilogue & HAI_FP8_NO_SPECIAL_CODES) == 0;
     switch (epilogue & ~HAI_FP8_NO_SPECIAL_CODES) {
         case HAI_EPI_STORE:
-            if (ldy < N) return invalid("gemm_fp8: ldy < N");
-            dispatch_fp8_codes<HAI_EPI_STORE>(a, check, s);
+            if (a.ldy < a.N) return invalid("gemm_fp8: ldy < N");
+            dispatch_fp8_codes<HAI_EPI_STORE, NORM>(a, check, s);
             break;
         case HAI_EPI_RESIDUAL:
-            if (res == nullptr || ldy < N || ld_res < N) return invalid("gemm_fp8: residual operands");
-            dispatch_fp8_codes<HAI_EPI_RESIDUAL>(a, check, s);
+            if (a.res == nullptr || a.ldy < a.N || a.ldres < a.N) return invalid("gemm_fp8: residual operands");
+            dispatch_fp8_codes<HAI_EPI_RESIDUAL, NORM>(a, check, s);
             break;
         case HAI_EPI_SILU_MUL:
-            if (N % 2 != 0 || ldy < N / 2) return invalid("gemm_fp8: silu_mul needs even N and ldy >= N/2");
+            if (a.N % 2 != 0 || a.ldy < a.N / 2) return invalid("gemm_fp8: silu_mul needs even N and ldy >= N/2");
             a.paired = 1;
-            dispatch_fp8_codes<HAI_EPI_SILU_MUL>(a, check, s);
+            dispatch_fp8_codes<HAI_EPI_SILU_MUL, NORM>(a, check, s);
             break;
         default:
             return invalid("gemm_fp8: unknown epilogue");
     }
     return launched("gemm_fp8_kernel");
+}
+
+}  // namespace
+
+extern "C" int hai_gemm_fp8_bf16(void* y, int64_t ldy, const void* x, int64_t ldx, const void* wq,
+                                 const float* scales, const int32_t* scale_rows, int64_t M, int64_t N,
+                                 int64_t K, int epilogue, const void* res, int64_t ld_res, void* stream) {
+    const int rc = check_fp8(y, x, wq, scales, M, N, K, ldx);
+    if (rc != HAI_OK) return rc;
+    if (M == 0 || N == 0) return HAI_OK;
+    Fp8Args a{static_cast<uint16_t*>(y), ldy, static_cast<const uint16_t*>(x), ldx,
+              static_cast<const uint8_t*>(wq), scales, scale_rows, 0, static_cast<const uint16_t*>(res), ld_res,
+              int(M), int(N), int(K), NormArgs{}};
+    return dispatch_fp8_epi<false>(a, epilogue, as_stream(stream));
+}
+
+extern "C" int hai_gemm_rmsnorm_fp8_bf16(void* y, int64_t ldy, const void* x, int64_t ldx, const void* norm_w,
+                                         float eps, int unit_offset, void* xn_out, int64_t ld_xn, const void* wq,
+                                         const float* scales, const int32_t* scale_rows, int64_t M, int64_t N,
+                                         int64_t K, int epilogue, const void* res, int64_t ld_res, void* stream) {
+    const int rc = check_fp8(y, x, wq, scales, M, N, K, ldx);
+    if (rc != HAI_OK) return rc;
+    if (norm_w == nullptr) return invalid("gemm_rmsnorm_fp8: null norm weight");
+    if (xn_out != nullptr && (ld_xn < K || ld_xn % 8 != 0 || !aligned16(xn_out)))
+        return invalid("gemm_rmsnorm_fp8: xn_out needs ld_xn >= K, ld_xn % 8 == 0 and 16-byte alignment");
+    if (!aligned16(norm_w)) return invalid("gemm_rmsnorm_fp8: norm weight must be 16-byte aligned");
+    if (M == 0) return HAI_OK;
+    if (M * K > kNormMaxElems) {
+        // Rows too large for the LDS prologue: normalise into xn_out, then multiply.
+        if (xn_out == nullptr) return invalid("gemm_rmsnorm_fp8: M*K above the fused limit needs xn_out");
+        const int r = hai_rmsnorm_bf16(xn_out, ld_xn, x, ldx, norm_w, M, K, eps, unit_offset, stream);
+        if (r != HAI_OK) return r;
+        return hai_gemm_fp8_bf16(y, ldy, xn_out, ld_xn, wq, scales, scale_rows, M, N, K, epilogue, res, ld_res,
+                                 stream);
+    }
+    if (N == 0)
+        return xn_out != nullptr ? hai_rmsnorm_bf16(xn_out, ld_xn, x, ldx, norm_w, M, K, eps, unit_offset, stream)
+                                 : HAI_OK;
+    NormArgs na;
+    na.w = static_cast<const uint16_t*>(norm_w);
+    na.eps = eps;
+    na.off = unit_offset ? 1.0f : 0.0f;
+    na.xn = static_cast<uint16_t*>(xn_out);
+    na.ldxn = ld_xn;
+    Fp8Args a{static_cast<uint16_t*>(y), ldy, static_cast<const uint16_t*>(x), ldx,
+              static_cast<const uint8_t*>(wq), scales, scale_rows, 0, static_cast<const uint16_t*>(res), ld_res,
+              int(M), int(N), int(K), na};
+    return dispatch_fp8_epi<true>(a, epilogue, as_stream(stream));
 }

@@ -399,9 +399,8 @@ int Engine::norm_gemm(uint16_t* y, int64_t ldy, const uint16_t* x, const uint16_
                       const Lin& w, int64_t M, int64_t N, int epi, const uint16_t* res, int64_t ldres) {
     const int64_t H = d_.H;
     // lm_head-sized outputs stream faster from the plain kernel than the norm
-    // prologue saves (measured on MI355X), so they normalise separately; the
-    // FP8 GEMM has no norm prologue.
-    if (N > kFusedNormMaxN || w.q != nullptr) {
+    // prologue saves (measured on MI355X), so they normalise separately.
+    if (N > kFusedNormMaxN) {
         uint16_t* xn = xn_out != nullptr ? xn_out : xn_;
         HAI_TRY(hai_rmsnorm_bf16(xn, H, x, H, nw, M, H, cfg_.rms_eps, 1, stream_));
         return gemm(y, ldy, xn, H, w, M, N, H, epi, res, ldres);
@@ -409,8 +408,12 @@ int Engine::norm_gemm(uint16_t* y, int64_t ldy, const uint16_t* x, const uint16_
     // Above the fused limit the call runs RMSNorm then GEMM through xn_.
     if (xn_out == nullptr && M * H > HAI_GEMM_RMSNORM_FUSED_MAX) xn_out = xn_;
     if (prof_record_) prof_calls_.push_back({y, ldy, x, H, w, M, N, H, epi, res, ldres, nw, xn_out});
-    HAI_TRY(hai_gemm_rmsnorm_bf16(y, ldy, x, H, nw, cfg_.rms_eps, 1, xn_out, H, w.w, M, N, H, epi, res, ldres,
-                                  stream_));
+    if (w.q != nullptr)
+        HAI_TRY(hai_gemm_rmsnorm_fp8_bf16(y, ldy, x, H, nw, cfg_.rms_eps, 1, xn_out, H, w.q, w.s, w.map, M, N, H,
+                                          epi | HAI_FP8_NO_SPECIAL_CODES, res, ldres, stream_));
+    else
+        HAI_TRY(hai_gemm_rmsnorm_bf16(y, ldy, x, H, nw, cfg_.rms_eps, 1, xn_out, H, w.w, M, N, H, epi, res, ldres,
+                                      stream_));
     return HAI_OK;
 }
 
@@ -465,11 +468,12 @@ int Engine::forward_target(const int64_t* d_ids, int64_t T, bool write_all_slots
         } else {
             // qwen_deltanet_reference (qwen_reference.cc:205-258)
             if (fp8_) {
-                // a|b (bf16) with the norm fused, writing the normalised rows
-                // that the FP8 qkv|z projection then reads
-                HAI_TRY(norm_gemm(proj_ + d.C + d.vw, d.Nin, h_, L.in_ln, xn_, L.w_ab, T, 2 * d.nv,
-                                  HAI_EPI_STORE, nullptr, 0));
-                HAI_TRY(gemm(proj_, d.Nin, xn_, d.H, Lin(L.f_in), T, d.C + d.vw, d.H, HAI_EPI_STORE, nullptr, 0));
+                // FP8 qkv|z with the norm fused, writing the normalised rows
+                // that the bf16 a|b projection then reads
+                HAI_TRY(norm_gemm(proj_, d.Nin, h_, L.in_ln, xn_, Lin(L.f_in), T, d.C + d.vw, HAI_EPI_STORE,
+                                  nullptr, 0));
+                HAI_TRY(gemm(proj_ + d.C + d.vw, d.Nin, xn_, d.H, L.w_ab, T, 2 * d.nv, d.H, HAI_EPI_STORE,
+                             nullptr, 0));
             } else {
                 HAI_TRY(norm_gemm(proj_, d.Nin, h_, L.in_ln, nullptr, L.w_in, T, d.Nin, HAI_EPI_STORE, nullptr,
                                   0));
@@ -818,7 +822,11 @@ int Engine::profile_verify(int64_t T, int64_t iters, hai_verify_profile* out) {
     for (int64_t it = 0; it < iters + 1; ++it) {
         HAI_TRY(hai_event_record(e0, stream_));
         for (const auto& c : prof_calls_) {
-            if (c.nw != nullptr)
+            if (c.nw != nullptr && c.w.q != nullptr)
+                HAI_TRY(hai_gemm_rmsnorm_fp8_bf16(c.y, c.ldy, c.x, c.ldx, c.nw, cfg_.rms_eps, 1, c.xn, c.ldx, c.w.q,
+                                                  c.w.s, c.w.map, c.M, c.N, c.K, c.epi | HAI_FP8_NO_SPECIAL_CODES,
+                                                  c.res, c.ldres, stream_));
+            else if (c.nw != nullptr)
                 HAI_TRY(hai_gemm_rmsnorm_bf16(c.y, c.ldy, c.x, c.ldx, c.nw, cfg_.rms_eps, 1, c.xn, c.ldx, c.w.w,
                                               c.M, c.N, c.K, c.epi, c.res, c.ldres, stream_));
             else if (c.w.q != nullptr)
