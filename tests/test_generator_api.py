@@ -9,7 +9,7 @@ from pathlib import Path
 
 import pytest
 
-from _hai import ROOT
+from _hai import ROOT, orc
 
 DRIVER = ROOT / "tests" / "backend" / "_build" / "generator_run"
 REF = Path("/root/reference")
@@ -50,9 +50,9 @@ def test_struct_members_match_reference(struct):
     assert got and got == _members(ref, struct)
 
 
-def _run(mode, max_new=64):
-    prompt = "ids:" + ",".join(str(t) for t in GOLD["prompt"])
-    r = subprocess.run([_driver(), "synthetic:tiny?seed=0&std=0.02&context=256", mode, prompt, str(max_new)],
+def _run(mode, max_new=64, model="synthetic:tiny?seed=0&std=0.02&context=256", prompt_ids=None):
+    prompt = "ids:" + ",".join(str(t) for t in (GOLD["prompt"] if prompt_ids is None else prompt_ids))
+    r = subprocess.run([_driver(), model, mode, prompt, str(max_new)],
                        capture_output=True, text=True, timeout=300)
     assert r.returncode == 0, r.stdout + r.stderr
     lines = dict(line.split(" ", 1) for line in r.stdout.strip().splitlines())
@@ -77,3 +77,20 @@ def test_speculative_through_public_api():
                       ("rejected", "rejected"), ("corrections", "corrections"),
                       ("mtp_recovery_tokens", "mtp_recovery_tokens")):
         assert int(stats[name]) == g["stats"][key], key
+
+
+@pytest.mark.gpu
+def test_fp8_weights_through_public_api():
+    """model_dir "...&weights=fp8": the C5 weight format; the speculative
+    decode equals the oracle's greedy decode of its FP8 model."""
+    prompt = orc.synthetic_prompt(3, 24, orc.TINY["vocab"])
+    toks, stats = _run("spec", 40, "synthetic:tiny?seed=3&std=0.02&context=256&weights=fp8", list(prompt))
+    ref = orc.Model(orc.TINY, seed=3, fp8=True)
+    assert toks == list(ref.greedy(prompt, 40))
+    ref.close()
+
+
+def test_unknown_weight_format_is_rejected():
+    r = subprocess.run([_driver(), "synthetic:tiny?weights=int4", "greedy", "ids:1,2", "4"], capture_output=True,
+                       text=True, timeout=120)
+    assert r.returncode != 0 and "weights=int4" in (r.stdout + r.stderr)

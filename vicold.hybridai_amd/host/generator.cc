@@ -6,10 +6,13 @@
 //
 // What this build accepts (checkpoint IO and the tokenizer are not part of
 // it):
-//   * GeneratorOptions::model_dir = "synthetic:<tiny|27b>[?seed=S&std=X&context=C]"
+//   * GeneratorOptions::model_dir =
+//     "synthetic:<tiny|27b>[?seed=S&std=X&context=C&weights=bf16|fp8]"
 //     -- the counter-based synthetic weights shared with the CPU oracle
-//     (tiny = BASELINE config C1, 27b = the 27B shape of C3); any other path
-//     returns FileNotFound (missing) or NotImplemented (a checkpoint);
+//     (tiny = BASELINE config C1, 27b = the 27B shape of C3; weights=fp8 the
+//     C5 format: QuantizedWeight Linears as E4M3 with 128x128 block scales);
+//     any other path returns FileNotFound (missing) or NotImplemented (a
+//     checkpoint);
 //   * GeneratorOptions::backend = "hip" (or "mi355x");
 //   * GenerationOptions::prompt = "ids:1,2,3" -- token ids; result.text holds
 //     the generated ids in the same form.  The synthetic models have no EOS.
@@ -104,6 +107,7 @@ public:
         uint64_t seed = 0;
         float std_dev = 0.02f;
         int32_t context = 4096;
+        int32_t weight_format = HAI_WEIGHTS_BF16;
         std::istringstream qs(query);
         for (std::string kv; std::getline(qs, kv, '&');) {
             const auto eq = kv.find('=');
@@ -112,13 +116,16 @@ public:
             if (key == "seed") seed = std::strtoull(val.c_str(), nullptr, 10);
             else if (key == "std") std_dev = std::strtof(val.c_str(), nullptr);
             else if (key == "context") context = static_cast<int32_t>(std::strtol(val.c_str(), nullptr, 10));
-            else return {ApiStatusCode::InvalidArgument, "unknown model option \"" + key + "\""};
+            else if (key == "weights" && (val == "bf16" || val == "fp8"))
+                weight_format = val == "fp8" ? HAI_WEIGHTS_FP8_BLOCK128 : HAI_WEIGHTS_BF16;
+            else return {ApiStatusCode::InvalidArgument, "unknown model option \"" + kv + "\""};
         }
         hai_engine_options eo{};
         eo.max_context = context;
         eo.max_verify_tokens = 16;
         eo.device = 0;
         eo.use_graphs = 0;
+        eo.weight_format = weight_format;
         engine_ = std::make_unique<mi355x::Engine>(cfg_, eo);
         if (!engine_->ok()) {
             const std::string why = engine_->error();
