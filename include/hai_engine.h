@@ -57,6 +57,10 @@ typedef struct hai_engine_options {
     int32_t device;           /* HIP device ordinal */
     int32_t use_graphs;       /* replay captured forwards (0 = plain launches) */
     int32_t weight_format;    /* HAI_WEIGHTS_* */
+    int32_t max_batch;        /* sequences decoded in lockstep (0 or 1 = one) */
+    int32_t mfma;             /* 1: GEMM launches of more than 16 rows (batches) on
+                                 the matrix cores (tolerance mode, bf16 weights);
+                                 0: every GEMM on the bit-exact kernels */
 } hai_engine_options;
 
 /* Counters of GenerationResult (include/hybrid.h:65-94) that the path fills. */
@@ -108,6 +112,26 @@ int hai_engine_generate_speculative(void* engine, const int32_t* prompt, int64_t
                                     int32_t* out_tokens, hai_spec_stats* stats, int32_t* round_log,
                                     int64_t round_log_cap);
 
+/* Batched decode: the engine's B = max_batch sequences, prompts [B][P] of
+ * one length, decoded in lockstep rounds (one batched draft per chain
+ * position, one verify of B x (k+1) rows, one batched correction forward for
+ * the rejected sequences).  Each sequence follows the reference state
+ * machine on its own: its tokens, round records and counters equal its
+ * single-sequence decode.  out_tokens [B][max_new], n_out [B], stats [B],
+ * round_log [B][round_log_cap][HAI_ROUND_RECORD] (NULL allowed),
+ * draft_override [B][n_override] (NULL allowed).  Returns 0 or -status. */
+int hai_engine_generate_speculative_batch(void* engine, const int32_t* prompts, int64_t P,
+                                          int64_t max_new, int64_t width, const int32_t* eos,
+                                          int64_t n_eos, const int32_t* draft_override,
+                                          int64_t n_override, int32_t* out_tokens, int64_t* n_out,
+                                          hai_spec_stats* stats, int32_t* round_log,
+                                          int64_t round_log_cap);
+/* Prefill-only forward of ids [B][T] for all B sequences: hidden [B][T][H],
+ * logits [B][T][V] (either may be NULL). */
+int hai_engine_forward_batch(void* engine, const int32_t* ids, int64_t T, uint16_t* hidden,
+                             uint16_t* logits);
+int64_t hai_engine_batch(void* engine);
+
 /* Benchmark hooks.  hai_engine_prefill + hai_engine_spec_rounds run the same
  * loop as generate_speculative split so the caller can time rounds; the
  * verify-step profile replays n verify forwards of T rows at the current
@@ -123,6 +147,8 @@ typedef struct hai_verify_profile {
     double draft_bytes;
 } hai_verify_profile;
 
+/* prompt is [B][P]; out_tokens [B][out_capacity]; n_out [B]; stats summed
+ * over the sequences. */
 int hai_engine_prefill(void* engine, const int32_t* prompt, int64_t P, int64_t max_new);
 int hai_engine_spec_rounds(void* engine, int64_t rounds, int64_t width, int32_t* out_tokens,
                            int64_t out_capacity, int64_t* n_out, hai_spec_stats* stats);

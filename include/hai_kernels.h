@@ -321,6 +321,33 @@ int hai_verify_argmax_accept_bf16(const void* logits, int64_t V,
  * bookkeeping, attention.h:11-42, delta_net.h:11-55). */
 int hai_add_i32(int32_t* dst, const int32_t* delta, int32_t add, int64_t n, void* stream);
 
+/* dst[i * dst_stride] = src[i * src_stride] for i < n (token ids between the
+ * [B][T] verify layout and per-sequence [B] vectors). */
+int hai_copy_i64_strided(int64_t* dst, int64_t dst_stride, const int64_t* src,
+                         int64_t src_stride, int64_t n, void* stream);
+/* After the correction forward of a batch (one row per sequence): for every
+ * sequence b whose round ended in a rejection (result[b*4+1] == 0, the
+ * layout of hai_verify_argmax_accept_bf16), next[b] = corr_next[b],
+ * h_prev[b] = corr_hidden[b] ([B][H] bf16), target_len[b] += 1 and
+ * mtp_len[b] += 1 (the correction row and its MTP recovery row are
+ * committed, generator.cc:960-1003); fully accepted sequences keep their
+ * verify outcome. */
+int hai_correction_commit_bf16(const int32_t* result, const int64_t* corr_next,
+                               const void* corr_hidden, int64_t H, int64_t B,
+                               int64_t* next, void* h_prev,
+                               int32_t* target_len, int32_t* mtp_len,
+                               void* stream);
+/* Batched-verify linear layer on the matrix cores (M up to 128 rows: C4/C5
+ * batches), the same contract and epilogues as hai_gemm_bf16 but computed
+ * with v_mfma_f32_16x16x32_bf16: equal to the canonical result within fp32
+ * accumulation error (~1e-6 relative before the bf16 output rounding), not
+ * bit for bit.  Replaces rocblas_gemm_ex (hip_backend.cc:697-809) for
+ * M > 16. x and w 16-byte aligned, K % 8 == 0. */
+int hai_gemm_bf16_mfma(void* y, int64_t ldy, const void* x, int64_t ldx,
+                       const void* w, int64_t M, int64_t N, int64_t K,
+                       int epilogue, const void* res, int64_t ld_res,
+                       void* stream);
+
 /* ------------------------------------------------------------------ synthetic data / checks
  * Synthetic weights: element (r, c) of a [rows, cols] tensor (row stride
  * ld) gets bf16(std * IrwinHall4(splitmix64(key(seed, tensor_id) + r*cols+c))),

@@ -646,3 +646,33 @@ def test_gemm_rmsnorm_fp8_fused(M, N, K_, epi, with_xn, mapped):
     assert_bits_equal(dy.download(np.uint16), want, f"gemm_rmsnorm_fp8 {M}x{N}x{K_} epi {epi}")
     if dxn is not None:
         assert_bits_equal(dxn.download(np.uint16), xn_want, "normalised rows")
+
+
+# ----------------------------------------------------------------- MFMA (tolerance mode)
+@pytest.mark.parametrize("M,N,K,epi", [(17, 300, 256, 0), (32, 1536, 5120, 1), (64, 1000, 1000, 2),
+                                       (128, 640, 2048, 0), (40, 16480, 512, 0)])
+def test_gemm_mfma_within_tolerance(M, N, K, epi):
+    """hai_gemm_bf16_mfma against the canonical GEMM: the bf16 outputs differ
+    by at most a couple of bf16 ulps (fp32 accumulation in another order)."""
+    rng = np.random.default_rng(M + N + K + epi)
+    x, xb = rand_bf16(rng, (M, K))
+    w, wb = rand_bf16(rng, (N, K), 0.05)
+    ncols = N // 2 if epi == hai.EPI_SILU_MUL else N
+    h, hb = rand_bf16(rng, (M, ncols))
+    dx, dw = dev(xb), dev(wb)
+    dy = dev(hb) if epi == hai.EPI_RESIDUAL else out_buf(M * ncols * 2)
+    hai.check(kern().hai_gemm_bf16_mfma(dy.ptr, ncols, dx.ptr, K, dw.ptr, M, N, K, epi,
+                                        dy.ptr if epi == hai.EPI_RESIDUAL else None, ncols, None), "gemm_mfma")
+    y = orc.gemm(x, w)
+    if epi == hai.EPI_STORE:
+        want = y
+    elif epi == hai.EPI_RESIDUAL:
+        want = orc.add(h, y)
+    else:
+        want = orc.silu_mul(y[:, 0::2], y[:, 1::2])
+    got = hai.bf16_to_f32(dy.download(np.uint16).reshape(M, ncols))
+    exact64 = x.astype(np.float64) @ w.astype(np.float64).T
+    scale = np.abs(exact64).max()
+    assert np.allclose(got, want, rtol=2 ** -6, atol=2e-3 * scale), float(np.abs(got - want).max())
+    if epi == hai.EPI_STORE:
+        assert np.abs(got - exact64).max() <= 2 ** -7 * np.abs(exact64).max() + 1e-6

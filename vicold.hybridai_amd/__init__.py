@@ -88,6 +88,9 @@ _KERNEL_SIGS = {
     "hai_argmax_rows_bf16": [VP, VP, I64, I64, I64, VP, VP],
     "hai_verify_argmax_accept_bf16": [VP, I64, VP, I64, VP, VP, I64, I64, VP, VP, VP, VP, VP, VP, VP, VP, VP],
     "hai_add_i32": [VP, VP, I32, I64, VP],
+    "hai_copy_i64_strided": [VP, I64, VP, I64, I64, VP],
+    "hai_correction_commit_bf16": [VP, VP, VP, I64, I64, VP, VP, VP, VP, VP],
+    "hai_gemm_bf16_mfma": [VP, I64, VP, I64, VP, I64, I64, I64, ctypes.c_int, VP, I64, VP],
     "hai_fill_synthetic_bf16": [VP, I64, I64, I64, ctypes.c_uint64, ctypes.c_uint32, F32, VP],
     "hai_debug_math_f32": [VP, VP, I64, ctypes.c_int, VP],
 }

@@ -128,6 +128,26 @@ __global__ void add_i32_kernel(int32_t* dst, const int32_t* delta, int32_t add, 
     if (i < n) dst[i] += (delta ? delta[i] : 0) + add;
 }
 
+__global__ void copy_i64_strided_kernel(int64_t* dst, int64_t ds, const int64_t* src, int64_t ss, int64_t n) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n) dst[i * ds] = src[i * ss];
+}
+
+// One block per sequence; only the sequences whose round ended in a
+// rejection (result[b*4+1] == 0) take the correction row's outcome.
+__global__ void correction_commit_kernel(const int32_t* __restrict__ result, const int64_t* __restrict__ corr_next,
+                                         const uint16_t* __restrict__ corr_hidden, int64_t H, int64_t* next,
+                                         uint16_t* h_prev, int32_t* target_len, int32_t* mtp_len) {
+    const int b = blockIdx.x;
+    if (result[b * 4 + 1] != 0) return;
+    for (int64_t i = threadIdx.x; i < H; i += blockDim.x) h_prev[b * H + i] = corr_hidden[b * H + i];
+    if (threadIdx.x == 0) {
+        next[b] = corr_next[b];
+        target_len[b] += 1;
+        mtp_len[b] += 1;
+    }
+}
+
 }  // namespace
 
 extern "C" {
@@ -138,6 +158,28 @@ int hai_add_i32(int32_t* dst, const int32_t* delta, int32_t add, int64_t n, void
     add_i32_kernel<<<dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, as_stream(stream)>>>(dst, delta, add,
                                                                                                         n);
     return launched("add_i32_kernel");
+}
+
+int hai_copy_i64_strided(int64_t* dst, int64_t dst_stride, const int64_t* src, int64_t src_stride, int64_t n,
+                         void* stream) {
+    if (dst == nullptr || src == nullptr || n < 0) return invalid("copy_i64_strided");
+    if (n == 0) return HAI_OK;
+    copy_i64_strided_kernel<<<dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, as_stream(stream)>>>(
+        dst, dst_stride, src, src_stride, n);
+    return launched("copy_i64_strided_kernel");
+}
+
+int hai_correction_commit_bf16(const int32_t* result, const int64_t* corr_next, const void* corr_hidden, int64_t H,
+                               int64_t B, int64_t* next, void* h_prev, int32_t* target_len, int32_t* mtp_len,
+                               void* stream) {
+    if (result == nullptr || corr_next == nullptr || corr_hidden == nullptr || next == nullptr ||
+        h_prev == nullptr || target_len == nullptr || mtp_len == nullptr || B < 0 || H <= 0)
+        return invalid("correction_commit");
+    if (B == 0) return HAI_OK;
+    correction_commit_kernel<<<dim3(static_cast<unsigned>(B)), dim3(256), 0, as_stream(stream)>>>(
+        result, corr_next, static_cast<const uint16_t*>(corr_hidden), H, next, static_cast<uint16_t*>(h_prev),
+        target_len, mtp_len);
+    return launched("correction_commit_kernel");
 }
 
 size_t hai_argmax_scratch_bytes(int64_t rows, int64_t V) {

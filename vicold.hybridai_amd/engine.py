@@ -24,7 +24,8 @@ WEIGHTS_BF16, WEIGHTS_FP8_BLOCK128 = 0, 1
 
 class EngineOptions(ctypes.Structure):
     _fields_ = [("max_context", ctypes.c_int32), ("max_verify_tokens", ctypes.c_int32),
-                ("device", ctypes.c_int32), ("use_graphs", ctypes.c_int32), ("weight_format", ctypes.c_int32)]
+                ("device", ctypes.c_int32), ("use_graphs", ctypes.c_int32), ("weight_format", ctypes.c_int32),
+                ("max_batch", ctypes.c_int32), ("mfma", ctypes.c_int32)]
 
 
 class SpecStats(ctypes.Structure):
@@ -73,9 +74,15 @@ def bind(lib: ctypes.CDLL) -> ctypes.CDLL:
     lib.hai_engine_spec_rounds.argtypes = [VP, I64, I64, I32P, I64, ctypes.POINTER(ctypes.c_int64),
                                            ctypes.POINTER(SpecStats)]
     lib.hai_engine_profile_verify.argtypes = [VP, I64, I64, ctypes.POINTER(VerifyProfile)]
+    lib.hai_engine_forward_batch.argtypes = [VP, I32P, I64, U16P, U16P]
+    lib.hai_engine_generate_speculative_batch.argtypes = [VP, I32P, I64, I64, I64, I32P, I64, I32P, I64, I32P,
+                                                          ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(SpecStats),
+                                                          I32P, I64]
+    lib.hai_engine_batch.restype = I64
+    lib.hai_engine_batch.argtypes = [VP]
     for n in ("hai_engine_init_synthetic", "hai_engine_forward", "hai_engine_generate_greedy",
               "hai_engine_generate_speculative", "hai_engine_prefill", "hai_engine_spec_rounds",
-              "hai_engine_profile_verify"):
+              "hai_engine_profile_verify", "hai_engine_forward_batch", "hai_engine_generate_speculative_batch"):
         getattr(lib, n).restype = ctypes.c_int
     return lib
 
@@ -88,14 +95,15 @@ class Engine:
     """One verify engine on one GPU (synthetic weights)."""
 
     def __init__(self, cfg: dict, max_context: int, max_verify_tokens: int = 16, device: int = 0,
-                 use_graphs: bool = False, fp8: bool = False):
+                 use_graphs: bool = False, fp8: bool = False, batch: int = 1, mfma: bool = False):
         from . import host
         self.lib = host()
         self.cfg = dict(cfg)
         self.fp8 = fp8
+        self.batch = batch
         c = ModelConfig(**cfg)
         o = EngineOptions(max_context, max_verify_tokens, device, int(use_graphs),
-                          WEIGHTS_FP8_BLOCK128 if fp8 else WEIGHTS_BF16)
+                          WEIGHTS_FP8_BLOCK128 if fp8 else WEIGHTS_BF16, batch, int(mfma))
         self.h = self.lib.hai_engine_create(ctypes.byref(c), ctypes.byref(o))
         if not self.h:
             raise RuntimeError("hai_engine_create: " + self.lib.hai_engine_last_error(None).decode())
@@ -170,16 +178,55 @@ class Engine:
             self._check(-n, "generate_speculative")
         return out[:n], st.as_dict(), log[:st.rounds]
 
+    def forward_batch(self, ids):
+        """ids [B][T] -> hidden [B][T][H], logits [B][T][V] (bf16 bits)."""
+        ids = _i32(ids).reshape(self.batch, -1)
+        T = ids.shape[1]
+        H, V = self.cfg["hidden"], self.cfg["vocab"]
+        hid = np.empty((self.batch, T, H), np.uint16)
+        lg = np.empty((self.batch, T, V), np.uint16)
+        self._check(self.lib.hai_engine_forward_batch(self.h, ids.ctypes.data_as(I32P), T,
+                                                      hid.ctypes.data_as(U16P), lg.ctypes.data_as(U16P)),
+                    "forward_batch")
+        return hid, lg
+
+    def speculative_batch(self, prompts, max_new, width=1, eos=(), draft_override=None, max_rounds=4096):
+        """prompts [B][P] -> per sequence (tokens, stats, round log)."""
+        p = _i32(prompts).reshape(self.batch, -1)
+        e = _i32(list(eos))
+        B = self.batch
+        out = np.empty((B, max_new), np.int32)
+        n = np.zeros(B, np.int64)
+        st = (SpecStats * B)()
+        log = np.full((B, max_rounds, ROUND_RECORD), -1, np.int32)
+        if draft_override is not None:
+            ov = _i32(draft_override).reshape(B, -1)
+            ovp, nov = ov.ctypes.data_as(I32P), ov.shape[1]
+        else:
+            ovp, nov = None, 0
+        rc = self.lib.hai_engine_generate_speculative_batch(
+            self.h, p.ctypes.data_as(I32P), p.shape[1], max_new, width, e.ctypes.data_as(I32P), e.size, ovp, nov,
+            out.ctypes.data_as(I32P), n.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)), st,
+            log.ctypes.data_as(I32P), max_rounds)
+        if rc < 0:
+            self._check(-rc, "generate_speculative_batch")
+        return [(out[b, :n[b]], st[b].as_dict(), log[b, :st[b].rounds]) for b in range(B)]
+
     def prefill(self, prompt, max_new):
-        p = _i32(prompt)
-        self._check(self.lib.hai_engine_prefill(self.h, p.ctypes.data_as(I32P), p.size, max_new), "prefill")
+        """prompt [P] (one sequence) or [B][P]."""
+        p = _i32(prompt).reshape(self.batch, -1)
+        self._check(self.lib.hai_engine_prefill(self.h, p.ctypes.data_as(I32P), p.shape[1], max_new), "prefill")
 
     def spec_rounds(self, rounds, width, out: np.ndarray):
-        n = ctypes.c_int64(0)
+        """out [cap] or [B][cap]; returns (tokens emitted so far, summed over
+        the sequences) and the summed stats of these rounds."""
+        out2 = out.reshape(self.batch, -1)
+        n = np.zeros(self.batch, np.int64)
         st = SpecStats()
-        self._check(self.lib.hai_engine_spec_rounds(self.h, rounds, width, out.ctypes.data_as(I32P), out.size,
-                                                    ctypes.byref(n), ctypes.byref(st)), "spec_rounds")
-        return int(n.value), st.as_dict()
+        self._check(self.lib.hai_engine_spec_rounds(self.h, rounds, width, out2.ctypes.data_as(I32P),
+                                                    out2.shape[1], n.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)),
+                                                    ctypes.byref(st)), "spec_rounds")
+        return int(n.sum()), st.as_dict()
 
     def profile_verify(self, T, iters):
         pr = VerifyProfile()

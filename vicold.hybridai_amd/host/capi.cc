@@ -51,9 +51,16 @@ int64_t hai_engine_read_tensor(void* engine, uint32_t tensor_id, uint16_t* out, 
 uint64_t hai_engine_weight_bytes(void* engine) { return engine ? as_engine(engine)->weight_bytes() : 0; }
 
 int hai_engine_forward(void* engine, const int32_t* ids, int64_t T, uint16_t* hidden, uint16_t* logits) {
+    if (!engine || !ids || as_engine(engine)->batch() != 1) return HAI_ERR_INVALID_ARGUMENT;
+    return as_engine(engine)->forward_rows(ids, T, hidden, logits);
+}
+
+int hai_engine_forward_batch(void* engine, const int32_t* ids, int64_t T, uint16_t* hidden, uint16_t* logits) {
     if (!engine || !ids) return HAI_ERR_INVALID_ARGUMENT;
     return as_engine(engine)->forward_rows(ids, T, hidden, logits);
 }
+
+int64_t hai_engine_batch(void* engine) { return engine ? as_engine(engine)->batch() : 0; }
 
 int hai_engine_generate_greedy(void* engine, const int32_t* prompt, int64_t P, int64_t max_new,
                                const int32_t* eos, int64_t n_eos, int32_t* out_tokens) {
@@ -67,12 +74,24 @@ int hai_engine_generate_speculative(void* engine, const int32_t* prompt, int64_t
                                     int64_t width, const int32_t* eos, int64_t n_eos,
                                     const int32_t* draft_override, int64_t n_override, int32_t* out_tokens,
                                     hai_spec_stats* stats, int32_t* round_log, int64_t round_log_cap) {
-    if (!engine || !prompt || !out_tokens) return -HAI_ERR_INVALID_ARGUMENT;
+    if (!engine || !prompt || !out_tokens || as_engine(engine)->batch() != 1) return -HAI_ERR_INVALID_ARGUMENT;
     int64_t n = 0;
     const int rc = as_engine(engine)->generate_speculative(prompt, P, max_new, width, eos, n_eos, draft_override,
                                                            n_override, out_tokens, stats, round_log,
                                                            round_log_cap, &n);
     return rc == HAI_OK ? static_cast<int>(n) : -rc;
+}
+
+int hai_engine_generate_speculative_batch(void* engine, const int32_t* prompts, int64_t P, int64_t max_new,
+                                          int64_t width, const int32_t* eos, int64_t n_eos,
+                                          const int32_t* draft_override, int64_t n_override, int32_t* out_tokens,
+                                          int64_t* n_out, hai_spec_stats* stats, int32_t* round_log,
+                                          int64_t round_log_cap) {
+    if (!engine || !prompts || !out_tokens || !n_out) return -HAI_ERR_INVALID_ARGUMENT;
+    const int rc = as_engine(engine)->generate_speculative(prompts, P, max_new, width, eos, n_eos, draft_override,
+                                                           n_override, out_tokens, stats, round_log,
+                                                           round_log_cap, n_out);
+    return rc == HAI_OK ? 0 : -rc;
 }
 
 int hai_engine_prefill(void* engine, const int32_t* prompt, int64_t P, int64_t max_new) {

@@ -82,13 +82,16 @@ Engine::Engine(const hai_model_config& cfg, const hai_engine_options& opt) : cfg
     d_.kvw = d_.nkv * d_.D;
     d_.Nqkv = 2 * d_.qw + 2 * d_.kvw;
     tmax_ = std::max<int64_t>(2, std::min<int64_t>(16, opt.max_verify_tokens));
+    B_ = std::max<int64_t>(1, opt.max_batch);
     cap_ = std::max<int64_t>(opt.max_context, tmax_ + 1);
     ring_ = 32;
     nslots_ = tmax_ + 1;
     use_graphs_ = opt.use_graphs != 0;
     fp8_ = opt.weight_format == HAI_WEIGHTS_FP8_BLOCK128;
-    draft_graphs_.assign(static_cast<size_t>(tmax_), nullptr);
+    mfma_ = opt.mfma != 0;
+    draft_graphs_.assign(static_cast<size_t>((tmax_ + 1) * tmax_), nullptr);
     verify_graphs_.assign(static_cast<size_t>(tmax_ + 1), nullptr);
+    rs_.assign(static_cast<size_t>(B_), RoundState{});
     if (cfg.hidden <= 0 || cfg.hidden % 8 != 0 || cfg.num_layers <= 0 || cfg.full_attention_interval <= 0 ||
         cfg.num_kv_heads <= 0 || cfg.num_q_heads % cfg.num_kv_heads != 0 || cfg.lin_qk_heads <= 0 ||
         cfg.lin_v_heads % cfg.lin_qk_heads != 0 || cfg.ffn % 8 != 0 || cfg.mtp_layers != 1 ||
@@ -99,6 +102,10 @@ Engine::Engine(const hai_model_config& cfg, const hai_engine_options& opt) : cfg
     }
     if (opt.weight_format != HAI_WEIGHTS_BF16 && opt.weight_format != HAI_WEIGHTS_FP8_BLOCK128) {
         error_ = "unknown weight_format";
+        return;
+    }
+    if (B_ > 64) {
+        error_ = "max_batch above 64";
         return;
     }
     if (hai_set_device(opt.device) != HAI_OK || hai_stream_create(&stream_) != HAI_OK) {
@@ -249,18 +256,19 @@ int Engine::alloc_all() {
     }
 
     // ---- caches ----
+    const size_t Bz = static_cast<size_t>(B_);
     auto carve_caches = [&](Carver& cv) {
         for (auto& L : layers_) {
             if (L.attn) {
-                L.k_cache = cv.take<uint16_t>(static_cast<size_t>(cap_ * d.kvw));
-                L.v_cache = cv.take<uint16_t>(static_cast<size_t>(cap_ * d.kvw));
+                L.k_cache = cv.take<uint16_t>(Bz * static_cast<size_t>(cap_ * d.kvw));
+                L.v_cache = cv.take<uint16_t>(Bz * static_cast<size_t>(cap_ * d.kvw));
             } else {
-                L.ring = cv.take<uint16_t>(static_cast<size_t>(ring_ * d.C));
-                L.state = cv.take<float>(static_cast<size_t>(nslots_ * d.nv * d.dv * d.dk));
+                L.ring = cv.take<uint16_t>(Bz * static_cast<size_t>(ring_ * d.C));
+                L.state = cv.take<float>(Bz * static_cast<size_t>(nslots_ * d.nv * d.dv * d.dk));
             }
         }
-        mtp_.k_cache = cv.take<uint16_t>(static_cast<size_t>(cap_ * d.kvw));
-        mtp_.v_cache = cv.take<uint16_t>(static_cast<size_t>(cap_ * d.kvw));
+        mtp_.k_cache = cv.take<uint16_t>(Bz * static_cast<size_t>(cap_ * d.kvw));
+        mtp_.v_cache = cv.take<uint16_t>(Bz * static_cast<size_t>(cap_ * d.kvw));
     };
     {
         Carver sizing(nullptr);
@@ -274,32 +282,38 @@ int Engine::alloc_all() {
     // ---- workspace ----
     nproj_ = std::max(d.Nin, d.Nqkv);
     const int64_t T = tmax_;
+    const int64_t R = B_ * tmax_;  // rows of one launch
     auto carve_work = [&](Carver& cv) {
-        d_ids_ = cv.take<int64_t>(T);
-        d_vids_ = cv.take<int64_t>(T + 1);
-        d_preds_ = cv.take<int64_t>(T);
-        d_result_ = cv.take<int32_t>(4);
-        d_tlen_ = cv.take<int32_t>(1);
-        d_mlen_ = cv.take<int32_t>(1);
-        d_plen_ = cv.take<int32_t>(8);
-        d_pnext_ = cv.take<int64_t>(8);
-        h_ = cv.take<uint16_t>(T * H);
-        xn_ = cv.take<uint16_t>(T * 2 * H);
-        emb_ = cv.take<uint16_t>(T * H);
-        proj_ = cv.take<uint16_t>(T * nproj_);
-        q_ = cv.take<uint16_t>(T * d.qw);
-        gate_ = cv.take<uint16_t>(T * d.qw);
-        att_ = cv.take<uint16_t>(T * d.qw);
-        dnout_ = cv.take<uint16_t>(T * d.vw);
-        act_ = cv.take<uint16_t>(T * d.F);
-        hf_ = cv.take<uint16_t>(T * H);
-        logits_ = cv.take<uint16_t>(T * d.V);
-        mh_[0] = cv.take<uint16_t>(H);
-        mh_[1] = cv.take<uint16_t>(H);
-        h_prev_ = cv.take<uint16_t>(H);
-        rec_hidden_ = cv.take<uint16_t>(H);
-        gqa_scratch_ = cv.take<char>(hai_gqa_scratch_bytes(1, T, d.nq, d.D, cap_));
-        argmax_scratch_ = cv.take<char>(hai_argmax_scratch_bytes(T, d.V));
+        d_ids_ = cv.take<int64_t>(R);
+        d_vids_ = cv.take<int64_t>(R + 1);
+        d_next_ = cv.take<int64_t>(B_);
+        d_dids_ = cv.take<int64_t>(B_);
+        d_cand_ = cv.take<int64_t>(B_);
+        d_preds_ = cv.take<int64_t>(R);
+        d_result_ = cv.take<int32_t>(4 * B_);
+        d_tlen_ = cv.take<int32_t>(B_);
+        d_mlen_ = cv.take<int32_t>(B_);
+        d_ndraft_ = cv.take<int32_t>(B_);
+        d_delta_ = cv.take<int32_t>(B_);
+        d_plen_ = cv.take<int32_t>(7 * B_);
+        d_pnext_ = cv.take<int64_t>(B_);
+        h_ = cv.take<uint16_t>(R * H);
+        xn_ = cv.take<uint16_t>(R * 2 * H);
+        emb_ = cv.take<uint16_t>(R * H);
+        proj_ = cv.take<uint16_t>(R * nproj_);
+        q_ = cv.take<uint16_t>(R * d.qw);
+        gate_ = cv.take<uint16_t>(R * d.qw);
+        att_ = cv.take<uint16_t>(R * d.qw);
+        dnout_ = cv.take<uint16_t>(R * d.vw);
+        act_ = cv.take<uint16_t>(R * d.F);
+        hf_ = cv.take<uint16_t>(R * H);
+        logits_ = cv.take<uint16_t>(R * d.V);
+        mh_[0] = cv.take<uint16_t>(B_ * H);
+        mh_[1] = cv.take<uint16_t>(B_ * H);
+        h_prev_ = cv.take<uint16_t>(B_ * H);
+        rec_hidden_ = cv.take<uint16_t>(B_ * H);
+        gqa_scratch_ = cv.take<char>(hai_gqa_scratch_bytes(B_, T, d.nq, d.D, cap_));
+        argmax_scratch_ = cv.take<char>(hai_argmax_scratch_bytes(R, d.V));
         rope_cos_ = cv.take<float>(cap_ * std::max<int64_t>(1, d.R / 2));
         rope_sin_ = cv.take<float>(cap_ * std::max<int64_t>(1, d.R / 2));
     };
@@ -386,12 +400,28 @@ int64_t Engine::read_tensor(uint32_t id, uint16_t* out, int64_t capacity) {
 int Engine::gemm(uint16_t* y, int64_t ldy, const uint16_t* x, int64_t ldx, const Lin& w, int64_t M, int64_t N,
                  int64_t K, int epi, const uint16_t* res, int64_t ldres) {
     if (prof_record_) prof_calls_.push_back({y, ldy, x, ldx, w, M, N, K, epi, res, ldres, nullptr, nullptr});
-    // the engine's codes come from the saturating quantiser: never 0x7F / 0xFF
-    if (w.q != nullptr)
-        HAI_TRY(hai_gemm_fp8_bf16(y, ldy, x, ldx, w.q, w.s, w.map, M, N, K, epi | HAI_FP8_NO_SPECIAL_CODES, res,
-                                  ldres, stream_));
-    else
-        HAI_TRY(hai_gemm_bf16(y, ldy, x, ldx, w.w, M, N, K, epi, res, ldres, stream_));
+    if (mfma_ && w.q == nullptr && M > 16) {
+        for (int64_t m0 = 0; m0 < M; m0 += 128) {
+            const int64_t mm = std::min<int64_t>(128, M - m0);
+            HAI_TRY(hai_gemm_bf16_mfma(y + m0 * ldy, ldy, x + m0 * ldx, ldx, w.w, mm, N, K, epi,
+                                       res ? res + m0 * ldres : nullptr, ldres, stream_));
+        }
+        return HAI_OK;
+    }
+    // the skinny kernels take 16 rows per launch; rows are independent, so
+    // the split does not change a bit
+    for (int64_t m0 = 0; m0 < M; m0 += 16) {
+        const int64_t mm = std::min<int64_t>(16, M - m0);
+        uint16_t* ym = y + m0 * ldy;
+        const uint16_t* xm = x + m0 * ldx;
+        const uint16_t* rm = res ? res + m0 * ldres : nullptr;
+        // the engine's codes come from the saturating quantiser: never 0x7F / 0xFF
+        if (w.q != nullptr)
+            HAI_TRY(hai_gemm_fp8_bf16(ym, ldy, xm, ldx, w.q, w.s, w.map, mm, N, K, epi | HAI_FP8_NO_SPECIAL_CODES, rm,
+                                      ldres, stream_));
+        else
+            HAI_TRY(hai_gemm_bf16(ym, ldy, xm, ldx, w.w, mm, N, K, epi, rm, ldres, stream_));
+    }
     return HAI_OK;
 }
 
@@ -399,8 +429,9 @@ int Engine::norm_gemm(uint16_t* y, int64_t ldy, const uint16_t* x, const uint16_
                       const Lin& w, int64_t M, int64_t N, int epi, const uint16_t* res, int64_t ldres) {
     const int64_t H = d_.H;
     // lm_head-sized outputs stream faster from the plain kernel than the norm
-    // prologue saves (measured on MI355X), so they normalise separately.
-    if (N > kFusedNormMaxN) {
+    // prologue saves (measured on MI355X), so they normalise separately; so
+    // do launches of more than 16 rows.
+    if (N > kFusedNormMaxN || M > 16) {
         uint16_t* xn = xn_out != nullptr ? xn_out : xn_;
         HAI_TRY(hai_rmsnorm_bf16(xn, H, x, H, nw, M, H, cfg_.rms_eps, 1, stream_));
         return gemm(y, ldy, xn, H, w, M, N, H, epi, res, ldres);
@@ -418,50 +449,56 @@ int Engine::norm_gemm(uint16_t* y, int64_t ldy, const uint16_t* x, const uint16_
 }
 
 int Engine::reset_state() {
-    // Committed lengths to zero; the DeltaNet state slot 0 of every layer must
-    // start at zero (conv history before position 0 is read as zero).
-    HAI_TRY(hai_memset(d_tlen_, 0, 4, stream_));
-    HAI_TRY(hai_memset(d_mlen_, 0, 4, stream_));
-    const size_t slot_bytes = static_cast<size_t>(d_.nv * d_.dv * d_.dk) * 4;
+    // Committed lengths to zero; the DeltaNet state slot 0 of every layer and
+    // sequence must start at zero (conv history before position 0 is read as
+    // zero).
+    HAI_TRY(hai_memset(d_tlen_, 0, static_cast<size_t>(B_) * 4, stream_));
+    HAI_TRY(hai_memset(d_mlen_, 0, static_cast<size_t>(B_) * 4, stream_));
+    const size_t slot_bytes = static_cast<size_t>(B_ * d_.nv * d_.dv * d_.dk) * 4;
     for (auto& L : layers_)
         if (!L.attn) HAI_TRY(hai_memset(L.state, 0, slot_bytes, stream_));
-    rs_ = RoundState{};
+    rs_.assign(static_cast<size_t>(B_), RoundState{});
+    ndraft_host_.clear();
     return HAI_OK;
 }
 
-// One gated-GQA sub-layer: input RMSNorm fused into the q|gate,k,v
-// projection, residual added into h (qwen_attention_reference ->
-// GatedGQAAttention::forward_impl, attention.cc:301-599).
+// One gated-GQA sub-layer over T rows of each sequence: input RMSNorm fused
+// into the q|gate,k,v projection, residual added into h
+// (qwen_attention_reference -> GatedGQAAttention::forward_impl,
+// attention.cc:301-599).
 int Engine::attention_layer(const LayerWeights& L, int64_t T, uint16_t* h, const int32_t* lens, uint16_t* kc,
                             uint16_t* vc) {
     const auto& d = d_;
-    HAI_TRY(norm_gemm(proj_, d.Nqkv, h, L.in_ln, nullptr, lin(L.w_qkv, L.f_qkv), T, d.Nqkv, HAI_EPI_STORE,
+    const int64_t rows = B_ * T;
+    HAI_TRY(norm_gemm(proj_, d.Nqkv, h, L.in_ln, nullptr, lin(L.w_qkv, L.f_qkv), rows, d.Nqkv, HAI_EPI_STORE,
                       nullptr, 0));
-    HAI_TRY(hai_q_gate_rmsnorm_rope_bf16(q_, gate_, proj_, d.Nqkv, L.q_norm, rope_cos_, rope_sin_, cap_, 1, T,
+    HAI_TRY(hai_q_gate_rmsnorm_rope_bf16(q_, gate_, proj_, d.Nqkv, L.q_norm, rope_cos_, rope_sin_, cap_, B_, T,
                                          d.nq, d.D, d.R, lens, 0, cfg_.rms_eps, stream_));
     HAI_TRY(hai_kv_rmsnorm_rope_append_bf16(kc, vc, cap_, proj_ + 2 * d.qw, proj_ + 2 * d.qw + d.kvw, d.Nqkv,
-                                            L.k_norm, rope_cos_, rope_sin_, cap_, 1, T, d.nkv, d.D, d.R, lens, 0,
+                                            L.k_norm, rope_cos_, rope_sin_, cap_, B_, T, d.nkv, d.D, d.R, lens, 0,
                                             cfg_.rms_eps, stream_));
-    HAI_TRY(hai_gqa_verify_bf16(att_, q_, gate_, kc, vc, cap_, gqa_scratch_, 1, T, d.nq, d.nkv, d.D, lens,
+    HAI_TRY(hai_gqa_verify_bf16(att_, q_, gate_, kc, vc, cap_, gqa_scratch_, B_, T, d.nq, d.nkv, d.D, lens,
                                 static_cast<int32_t>(T), cap_, stream_));
-    return gemm(h, d.H, att_, d.qw, lin(L.w_o, L.f_o), T, d.H, d.qw, HAI_EPI_RESIDUAL, h, d.H);
+    return gemm(h, d.H, att_, d.qw, lin(L.w_o, L.f_o), rows, d.H, d.qw, HAI_EPI_RESIDUAL, h, d.H);
 }
 
 // qwen_mlp_reference (qwen_reference.cc:146-175): post-norm, SwiGLU, down
 // projection with the residual add fused.
 int Engine::mlp(const LayerWeights& L, int64_t T, uint16_t* h) {
     const auto& d = d_;
-    HAI_TRY(norm_gemm(act_, d.F, h, L.post_ln, nullptr, lin(L.w_gu, L.f_gu), T, 2 * d.F, HAI_EPI_SILU_MUL,
+    const int64_t rows = B_ * T;
+    HAI_TRY(norm_gemm(act_, d.F, h, L.post_ln, nullptr, lin(L.w_gu, L.f_gu), rows, 2 * d.F, HAI_EPI_SILU_MUL,
                       nullptr, 0));
-    return gemm(h, d.H, act_, d.F, lin(L.w_down, L.f_down), T, d.H, d.F, HAI_EPI_RESIDUAL, h, d.H);
+    return gemm(h, d.H, act_, d.F, lin(L.w_down, L.f_down), rows, d.H, d.F, HAI_EPI_RESIDUAL, h, d.H);
 }
 
-// target_forward (generator.cc:550-634): T rows of one sequence on top of
-// the committed caches; hf_ = post-final-norm hidden, logits_ = lm_head.
-// Committed lengths are not advanced here.
+// target_forward (generator.cc:550-634): T rows of every sequence (row b*T+t)
+// on top of its committed caches; hf_ = post-final-norm hidden, logits_ =
+// lm_head.  Committed lengths are not advanced here.
 int Engine::forward_target(const int64_t* d_ids, int64_t T, bool write_all_slots) {
     const auto& d = d_;
-    HAI_TRY(hai_embedding_gather_bf16(h_, embed_, d_ids, T, d.V, d.H, stream_));
+    const int64_t rows = B_ * T;
+    HAI_TRY(hai_embedding_gather_bf16(h_, embed_, d_ids, rows, d.V, d.H, stream_));
     for (auto& L : layers_) {
         if (L.attn) {
             HAI_TRY(attention_layer(L, T, h_, d_tlen_, L.k_cache, L.v_cache));
@@ -470,85 +507,104 @@ int Engine::forward_target(const int64_t* d_ids, int64_t T, bool write_all_slots
             if (fp8_) {
                 // FP8 qkv|z with the norm fused, writing the normalised rows
                 // that the bf16 a|b projection then reads
-                HAI_TRY(norm_gemm(proj_, d.Nin, h_, L.in_ln, xn_, Lin(L.f_in), T, d.C + d.vw, HAI_EPI_STORE,
+                HAI_TRY(norm_gemm(proj_, d.Nin, h_, L.in_ln, xn_, Lin(L.f_in), rows, d.C + d.vw, HAI_EPI_STORE,
                                   nullptr, 0));
-                HAI_TRY(gemm(proj_ + d.C + d.vw, d.Nin, xn_, d.H, L.w_ab, T, 2 * d.nv, d.H, HAI_EPI_STORE,
+                HAI_TRY(gemm(proj_ + d.C + d.vw, d.Nin, xn_, d.H, L.w_ab, rows, 2 * d.nv, d.H, HAI_EPI_STORE,
                              nullptr, 0));
             } else {
-                HAI_TRY(norm_gemm(proj_, d.Nin, h_, L.in_ln, nullptr, L.w_in, T, d.Nin, HAI_EPI_STORE, nullptr,
+                HAI_TRY(norm_gemm(proj_, d.Nin, h_, L.in_ln, nullptr, L.w_in, rows, d.Nin, HAI_EPI_STORE, nullptr,
                                   0));
             }
             HAI_TRY(hai_deltanet_verify_bf16(dnout_, d.vw, proj_, d.Nin, 0, d.C, d.C + d.vw, d.C + d.vw + d.nv,
                                              L.conv_w, L.ring, ring_, L.state, nslots_, write_all_slots ? 1 : 0,
-                                             L.a_log, L.dt_bias, L.lin_norm, d_tlen_, 0, 1, T, d.nk, d.nv, d.dk,
+                                             L.a_log, L.dt_bias, L.lin_norm, d_tlen_, 0, B_, T, d.nk, d.nv, d.dk,
                                              d.dv, d.Kc, cfg_.rms_eps, stream_));
-            HAI_TRY(gemm(h_, d.H, dnout_, d.vw, lin(L.w_out, L.f_out), T, d.H, d.vw, HAI_EPI_RESIDUAL, h_, d.H));
+            HAI_TRY(gemm(h_, d.H, dnout_, d.vw, lin(L.w_out, L.f_out), rows, d.H, d.vw, HAI_EPI_RESIDUAL, h_, d.H));
         }
         HAI_TRY(mlp(L, T, h_));
     }
-    return norm_gemm(logits_, d.V, h_, final_norm_, hf_, lm_head_, T, d.V, HAI_EPI_STORE, nullptr, 0);
+    return norm_gemm(logits_, d.V, h_, final_norm_, hf_, lm_head_, rows, d.V, HAI_EPI_STORE, nullptr, 0);
 }
 
 // MTP input rows x = fc([RMSNorm(emb) | RMSNorm(hidden)]) (generator.cc:152-160)
 // followed by only the part of the MTP decoder layer that the cache keeps:
 // input RMSNorm, the K/V projection rows and the K RMSNorm+RoPE append.  The
 // reference's prompt prefill and correction recovery discard the MTP output
-// (generator.cc:673-699, 977-1003), so the cache state is identical.
-int Engine::mtp_kv_rows(const int64_t* d_ids, const uint16_t* d_hidden, int64_t T) {
+// (generator.cc:673-699, 977-1003), so the cache state is identical.  T rows
+// per sequence; add_len advances every MTP length by T.
+int Engine::mtp_kv_rows(const int64_t* d_ids, const uint16_t* d_hidden, int64_t T, bool add_len) {
     const auto& d = d_;
-    HAI_TRY(hai_embedding_gather_bf16(emb_, embed_, d_ids, T, d.V, d.H, stream_));
-    HAI_TRY(hai_rmsnorm_bf16(xn_, 2 * d.H, emb_, d.H, pre_emb_, T, d.H, cfg_.rms_eps, 1, stream_));
-    HAI_TRY(hai_rmsnorm_bf16(xn_ + d.H, 2 * d.H, d_hidden, d.H, pre_hid_, T, d.H, cfg_.rms_eps, 1, stream_));
-    HAI_TRY(gemm(h_, d.H, xn_, 2 * d.H, fc_, T, d.H, 2 * d.H, HAI_EPI_STORE, nullptr, 0));
+    const int64_t rows = B_ * T;
+    HAI_TRY(hai_embedding_gather_bf16(emb_, embed_, d_ids, rows, d.V, d.H, stream_));
+    HAI_TRY(hai_rmsnorm_bf16(xn_, 2 * d.H, emb_, d.H, pre_emb_, rows, d.H, cfg_.rms_eps, 1, stream_));
+    HAI_TRY(hai_rmsnorm_bf16(xn_ + d.H, 2 * d.H, d_hidden, d.H, pre_hid_, rows, d.H, cfg_.rms_eps, 1, stream_));
+    HAI_TRY(gemm(h_, d.H, xn_, 2 * d.H, fc_, rows, d.H, 2 * d.H, HAI_EPI_STORE, nullptr, 0));
     // K and V rows of the fused attention projection only.
     HAI_TRY(norm_gemm(proj_, 2 * d.kvw, h_, mtp_.in_ln, nullptr, lin(mtp_.w_qkv, mtp_.f_qkv).rows(2 * d.qw, d.H),
-                      T, 2 * d.kvw, HAI_EPI_STORE, nullptr, 0));
+                      rows, 2 * d.kvw, HAI_EPI_STORE, nullptr, 0));
     HAI_TRY(hai_kv_rmsnorm_rope_append_bf16(mtp_.k_cache, mtp_.v_cache, cap_, proj_, proj_ + d.kvw, 2 * d.kvw,
-                                            mtp_.k_norm, rope_cos_, rope_sin_, cap_, 1, T, d.nkv, d.D, d.R, d_mlen_,
+                                            mtp_.k_norm, rope_cos_, rope_sin_, cap_, B_, T, d.nkv, d.D, d.R, d_mlen_,
                                             0, cfg_.rms_eps, stream_));
-    return hai_add_i32(d_mlen_, nullptr, static_cast<int32_t>(T), 1, stream_) == HAI_OK
-               ? HAI_OK
-               : fail(HAI_ERR_BACKEND, "mtp length update");
-}
-
-// One draft step: the full MTP forward (qwen_mtp_forward_reference,
-// generator.cc:139-183) of one row, lm_head and argmax (generator.cc:784-811).
-// The MTP cache grows by one row.
-int Engine::mtp_draft_step(const int64_t* d_id, const uint16_t* d_hin, uint16_t* d_mh, int64_t* d_cand) {
-    const auto& d = d_;
-    HAI_TRY(hai_embedding_gather_bf16(emb_, embed_, d_id, 1, d.V, d.H, stream_));
-    HAI_TRY(hai_rmsnorm_bf16(xn_, 2 * d.H, emb_, d.H, pre_emb_, 1, d.H, cfg_.rms_eps, 1, stream_));
-    HAI_TRY(hai_rmsnorm_bf16(xn_ + d.H, 2 * d.H, d_hin, d.H, pre_hid_, 1, d.H, cfg_.rms_eps, 1, stream_));
-    HAI_TRY(gemm(h_, d.H, xn_, 2 * d.H, fc_, 1, d.H, 2 * d.H, HAI_EPI_STORE, nullptr, 0));
-    HAI_TRY(attention_layer(mtp_, 1, h_, d_mlen_, mtp_.k_cache, mtp_.v_cache));
-    HAI_TRY(mlp(mtp_, 1, h_));
-    HAI_TRY(norm_gemm(logits_, d.V, h_, mtp_norm_, d_mh, lm_head_, 1, d.V, HAI_EPI_STORE, nullptr, 0));
-    HAI_TRY(hai_argmax_rows_bf16(d_cand, logits_, d.V, 1, d.V, argmax_scratch_, stream_));
-    HAI_TRY(hai_add_i32(d_mlen_, nullptr, 1, 1, stream_));
+    if (add_len) HAI_TRY(hai_add_i32(d_mlen_, nullptr, static_cast<int32_t>(T), B_, stream_));
     return HAI_OK;
 }
 
-// Prompt prefill in chunks of tmax_ rows (rows are independent and the
-// recurrences are sequential, so chunking does not change a bit), each chunk
-// followed by its MTP prompt rows (emb(t_i) paired with the hidden of t_i).
+// One draft step of every sequence: the full MTP forward
+// (qwen_mtp_forward_reference, generator.cc:139-183) of one row per
+// sequence, lm_head and argmax (generator.cc:784-811).  d_id / d_cand are
+// [B], d_hin / d_mh [B][H]; every MTP cache grows by one row.
+int Engine::mtp_draft_step(const int64_t* d_id, const uint16_t* d_hin, uint16_t* d_mh, int64_t* d_cand) {
+    const auto& d = d_;
+    HAI_TRY(hai_embedding_gather_bf16(emb_, embed_, d_id, B_, d.V, d.H, stream_));
+    HAI_TRY(hai_rmsnorm_bf16(xn_, 2 * d.H, emb_, d.H, pre_emb_, B_, d.H, cfg_.rms_eps, 1, stream_));
+    HAI_TRY(hai_rmsnorm_bf16(xn_ + d.H, 2 * d.H, d_hin, d.H, pre_hid_, B_, d.H, cfg_.rms_eps, 1, stream_));
+    HAI_TRY(gemm(h_, d.H, xn_, 2 * d.H, fc_, B_, d.H, 2 * d.H, HAI_EPI_STORE, nullptr, 0));
+    HAI_TRY(attention_layer(mtp_, 1, h_, d_mlen_, mtp_.k_cache, mtp_.v_cache));
+    HAI_TRY(mlp(mtp_, 1, h_));
+    HAI_TRY(norm_gemm(logits_, d.V, h_, mtp_norm_, d_mh, lm_head_, B_, d.V, HAI_EPI_STORE, nullptr, 0));
+    HAI_TRY(hai_argmax_rows_bf16(d_cand, logits_, d.V, B_, d.V, argmax_scratch_, stream_));
+    HAI_TRY(hai_add_i32(d_mlen_, nullptr, 1, B_, stream_));
+    return HAI_OK;
+}
+
+// Prompt prefill in chunks of tmax_ rows per sequence (rows are independent
+// and the recurrences are sequential, so chunking does not change a bit),
+// each chunk followed by its MTP prompt rows (emb(t_i) paired with the
+// hidden of t_i).  ids [B][P]; hidden_out [B][P][H], logits_out [B][P][V].
 int Engine::prefill_chunks(const int32_t* ids, int64_t P, uint16_t* hidden_out, uint16_t* logits_out) {
-    std::vector<int64_t> ids64(ids, ids + P);
+    const auto& d = d_;
+    std::vector<int64_t> chunk(static_cast<size_t>(B_ * tmax_));
     for (int64_t off = 0; off < P; off += tmax_) {
         const int64_t T = std::min<int64_t>(tmax_, P - off);
-        HAI_TRY(hai_memcpy_h2d(d_ids_, ids64.data() + off, static_cast<size_t>(T) * 8, stream_));
+        for (int64_t b = 0; b < B_; ++b)
+            for (int64_t t = 0; t < T; ++t) chunk[static_cast<size_t>(b * T + t)] = ids[b * P + off + t];
+        HAI_TRY(hai_memcpy_h2d(d_ids_, chunk.data(), static_cast<size_t>(B_ * T) * 8, stream_));
         HAI_TRY(forward_target(d_ids_, T, false));
-        HAI_TRY(hai_add_i32(d_tlen_, nullptr, static_cast<int32_t>(T), 1, stream_));
-        if (hidden_out) HAI_TRY(hai_memcpy_d2h(hidden_out + off * d_.H, hf_, static_cast<size_t>(T * d_.H) * 2, stream_));
-        if (logits_out) HAI_TRY(hai_memcpy_d2h(logits_out + off * d_.V, logits_, static_cast<size_t>(T * d_.V) * 2, stream_));
-        HAI_TRY(mtp_kv_rows(d_ids_, hf_, T));
+        HAI_TRY(hai_add_i32(d_tlen_, nullptr, static_cast<int32_t>(T), B_, stream_));
+        for (int64_t b = 0; b < B_; ++b) {
+            if (hidden_out)
+                HAI_TRY(hai_memcpy_d2h(hidden_out + (b * P + off) * d.H, hf_ + b * T * d.H,
+                                       static_cast<size_t>(T * d.H) * 2, stream_));
+            if (logits_out)
+                HAI_TRY(hai_memcpy_d2h(logits_out + (b * P + off) * d.V, logits_ + b * T * d.V,
+                                       static_cast<size_t>(T * d.V) * 2, stream_));
+        }
+        HAI_TRY(mtp_kv_rows(d_ids_, hf_, T, true));
         if (off + T == P) {
-            HAI_TRY(hai_argmax_rows_bf16(d_vids_, logits_ + (T - 1) * d_.V, d_.V, 1, d_.V, argmax_scratch_, stream_));
-            HAI_TRY(hai_memcpy_d2d(h_prev_, hf_ + (T - 1) * d_.H, static_cast<size_t>(d_.H) * 2, stream_));
+            // the last prompt row of every sequence: its argmax is the first
+            // target and its hidden feeds the first draft
+            HAI_TRY(hai_argmax_rows_bf16(d_next_, logits_ + (T - 1) * d.V, T * d.V, B_, d.V, argmax_scratch_,
+                                         stream_));
+            for (int64_t b = 0; b < B_; ++b)
+                HAI_TRY(hai_memcpy_d2d(h_prev_ + b * d.H, hf_ + (b * T + T - 1) * d.H, static_cast<size_t>(d.H) * 2,
+                                       stream_));
         }
         if (hidden_out || logits_out) HAI_TRY(sync());
     }
-    rs_.target_len = P;
-    rs_.mtp_len = P;
+    for (auto& r : rs_) {
+        r.target_len = P;
+        r.mtp_len = P;
+    }
     return HAI_OK;
 }
 
@@ -559,32 +615,36 @@ int Engine::forward_rows(const int32_t* ids, int64_t T, uint16_t* hidden, uint16
     return sync();
 }
 
-int Engine::prefill(const int32_t* prompt, int64_t P, int64_t max_new) {
+int Engine::prefill(const int32_t* prompts, int64_t P, int64_t max_new) {
     if (P <= 0 || max_new <= 0 || P + max_new + tmax_ > cap_)
         return fail(HAI_ERR_INVALID_ARGUMENT, "prefill: prompt + max_new exceeds max_context");
     HAI_TRY(reset_state());
-    HAI_TRY(prefill_chunks(prompt, P, nullptr, nullptr));
-    int64_t next = 0;
-    HAI_TRY(read_i64(d_vids_, &next, 1));
-    rs_.next_target = next;
-    rs_.max_new = max_new;
-    rs_.emitted = 0;
-    rs_.done = false;
+    HAI_TRY(prefill_chunks(prompts, P, nullptr, nullptr));
+    std::vector<int64_t> next(static_cast<size_t>(B_));
+    HAI_TRY(read_i64(d_next_, next.data(), B_));
+    for (int64_t b = 0; b < B_; ++b) {
+        auto& r = rs_[static_cast<size_t>(b)];
+        r.next_target = next[static_cast<size_t>(b)];
+        r.max_new = max_new;
+        r.emitted = 0;
+        r.done = false;
+    }
     return HAI_OK;
 }
 
 int Engine::generate_greedy(const int32_t* prompt, int64_t P, int64_t max_new, const int32_t* eos, int64_t n_eos,
                             int32_t* out, int64_t* n_out) {
+    if (B_ != 1) return fail(HAI_ERR_INVALID_ARGUMENT, "generate_greedy: one sequence only");
     HAI_TRY(prefill(prompt, P, max_new));
     int64_t emitted = 0;
-    int64_t next = rs_.next_target;
+    int64_t next = rs_[0].next_target;
     while (true) {
         out[emitted++] = static_cast<int32_t>(next);
         if (emitted >= max_new || in_set(eos, n_eos, next)) break;
-        HAI_TRY(forward_target(d_vids_, 1, false));
+        HAI_TRY(forward_target(d_next_, 1, false));
         HAI_TRY(hai_add_i32(d_tlen_, nullptr, 1, 1, stream_));
-        HAI_TRY(hai_argmax_rows_bf16(d_vids_, logits_, d_.V, 1, d_.V, argmax_scratch_, stream_));
-        HAI_TRY(read_i64(d_vids_, &next, 1));
+        HAI_TRY(hai_argmax_rows_bf16(d_next_, logits_, d_.V, 1, d_.V, argmax_scratch_, stream_));
+        HAI_TRY(read_i64(d_next_, &next, 1));
     }
     *n_out = emitted;
     return HAI_OK;
@@ -606,204 +666,345 @@ int Engine::replay(void** slot, F&& enqueue) {
     return HAI_OK;
 }
 
-// Draft i reads candidate i (vids[i]; vids[0] is next_target) and the hidden
-// that produced it, writes candidate i+1.
-int Engine::draft_step_at(int64_t i) {
+// Draft i of a round of verify width T reads candidate i of every sequence
+// (vids[b*T + i]; column 0 is next_target) and the hidden that produced it,
+// and writes candidate i+1.
+int Engine::draft_step_at(int64_t i, int64_t T) {
     const uint16_t* hin = i == 0 ? h_prev_ : mh_[(i - 1) % 2];
-    return replay(&draft_graphs_[static_cast<size_t>(i)],
-                  [&] { return mtp_draft_step(d_vids_ + i, hin, mh_[i % 2], d_vids_ + i + 1); });
+    return replay(&draft_graphs_[static_cast<size_t>(T * tmax_ + i)], [&]() -> int {
+        if (B_ == 1) return mtp_draft_step(d_vids_ + i, hin, mh_[i % 2], d_vids_ + i + 1);
+        HAI_TRY(hai_copy_i64_strided(d_dids_, 1, d_vids_ + i, T, B_, stream_));
+        HAI_TRY(mtp_draft_step(d_dids_, hin, mh_[i % 2], d_cand_));
+        HAI_TRY(hai_copy_i64_strided(d_vids_ + i + 1, T, d_cand_, 1, B_, stream_));
+        return HAI_OK;
+    });
 }
 
-// Verify forward of T rows + fused argmax/acceptance (commits on device).
+// Verify forward of T rows per sequence + fused argmax/acceptance (commits on
+// device).  The next target of every sequence lands in d_next_.
 int Engine::verify_step(int64_t T) {
     return replay(&verify_graphs_[static_cast<size_t>(T)], [&]() -> int {
         HAI_TRY(forward_target(d_vids_, T, true));
-        HAI_TRY(hai_verify_argmax_accept_bf16(logits_, d_.V, hf_, d_.H, d_vids_, nullptr, 1, T, d_preds_,
-                                              d_result_, d_tlen_, d_mlen_, d_vids_, rec_hidden_, h_prev_,
+        HAI_TRY(hai_verify_argmax_accept_bf16(logits_, d_.V, hf_, d_.H, d_vids_, d_ndraft_, B_, T, d_preds_,
+                                              d_result_, d_tlen_, d_mlen_, d_next_, rec_hidden_, h_prev_,
                                               argmax_scratch_, stream_));
         return HAI_OK;
     });
 }
 
-// Mismatch path: MTP recovery row (emb(corr), hidden of the last accepted
-// row), then the forward of corr on the committed prefix; its argmax is the
-// next target and its hidden feeds the next draft.
+// Mismatch path, batched over every sequence: MTP recovery row (emb(corr),
+// hidden of the last accepted row), then the forward of corr on the
+// committed prefix; for the sequences whose round ended in a rejection its
+// argmax becomes the next target and its hidden feeds the next draft, and
+// both rows are committed (hai_correction_commit_bf16).  Fully accepted
+// sequences compute a row past their committed length that the next round
+// overwrites.
 int Engine::correction_step() {
     return replay(&corr_graph_, [&]() -> int {
-        HAI_TRY(mtp_kv_rows(d_vids_, rec_hidden_, 1));
-        HAI_TRY(forward_target(d_vids_, 1, false));
-        HAI_TRY(hai_add_i32(d_tlen_, nullptr, 1, 1, stream_));
-        HAI_TRY(hai_argmax_rows_bf16(d_vids_, logits_, d_.V, 1, d_.V, argmax_scratch_, stream_));
-        HAI_TRY(hai_memcpy_d2d(h_prev_, hf_, static_cast<size_t>(d_.H) * 2, stream_));
+        HAI_TRY(mtp_kv_rows(d_next_, rec_hidden_, 1, false));
+        HAI_TRY(forward_target(d_next_, 1, false));
+        HAI_TRY(hai_argmax_rows_bf16(d_cand_, logits_, d_.V, B_, d_.V, argmax_scratch_, stream_));
+        HAI_TRY(hai_correction_commit_bf16(d_result_, d_cand_, hf_, d_.H, B_, d_next_, h_prev_, d_tlen_, d_mlen_,
+                                           stream_));
         return HAI_OK;
     });
 }
 
-// One round of the reference loop body (generator.cc:720-1028).
-int Engine::one_round(RoundState& st, int64_t width, const int32_t* eos, int64_t n_eos,
-                      const int32_t* override_tokens, int64_t n_override, int32_t* out, hai_spec_stats* stats,
-                      int32_t* rec) {
-    const int64_t remaining = st.max_new - st.emitted;
-    if (in_set(eos, n_eos, st.next_target) || remaining == 1) {
-        out[st.emitted++] = static_cast<int32_t>(st.next_target);
-        st.done = true;
-        return HAI_OK;
+// One lockstep round of the reference loop body (generator.cc:720-1028) for
+// every sequence still generating.
+int Engine::one_round(int64_t width, const RoundIo& io, bool* any_live) {
+    const size_t Bz = static_cast<size_t>(B_);
+    // sequences whose next target ends the generation emit it without a round
+    std::vector<int64_t> pc(Bz, 0);
+    int64_t k = 0;
+    bool live = false;
+    for (size_t b = 0; b < Bz; ++b) {
+        auto& st = rs_[b];
+        if (st.done) continue;
+        const int64_t remaining = st.max_new - st.emitted;
+        if (in_set(io.eos, io.n_eos, st.next_target) || remaining <= 1) {
+            io.out[static_cast<int64_t>(b) * io.out_ld + st.emitted++] = static_cast<int32_t>(st.next_target);
+            st.done = true;
+            continue;
+        }
+        pc[b] = std::min<int64_t>(std::min<int64_t>(width, remaining - 1), tmax_ - 1);
+        k = std::max(k, pc[b]);
+        live = true;
     }
-    const int64_t pc = std::min<int64_t>(std::min<int64_t>(width, remaining - 1), tmax_ - 1);
-    stats->max_proposal_width = std::max(stats->max_proposal_width, pc);
-    ++stats->rounds;
-    const int64_t mtp_len0 = st.mtp_len;
-    const int64_t target_len0 = st.target_len;
+    *any_live = live;
+    if (!live) return HAI_OK;
+    const int64_t T = k + 1;
+    std::vector<int64_t> mtp_len0(Bz), target_len0(Bz);
+    for (size_t b = 0; b < Bz; ++b) {
+        mtp_len0[b] = rs_[b].mtp_len;
+        target_len0[b] = rs_[b].target_len;
+    }
+    // this round's next targets into column 0 of the [B][T] id block
+    HAI_TRY(hai_copy_i64_strided(d_vids_, T, d_next_, 1, B_, stream_));
 
     // ---- draft (chained MTP proposals) ----
     auto t0 = Clock::now();
-    int64_t k = 0;
-    for (int64_t i = 0; i < pc; ++i) {
-        HAI_TRY(draft_step_at(i));
-        const int64_t pos = st.emitted + 1 + i;
-        if (override_tokens != nullptr && pos < n_override) {
-            const int64_t tok = override_tokens[pos];
-            HAI_TRY(hai_memcpy_h2d(d_vids_ + i + 1, &tok, 8, stream_));
-            HAI_TRY(sync());  // tok lives on the host stack
+    std::vector<int64_t> kd(Bz, 0);  // drafts counted per sequence (EOS cuts a chain short)
+    std::vector<bool> open(Bz);
+    for (size_t b = 0; b < Bz; ++b) open[b] = pc[b] > 0;
+    for (int64_t i = 0; i < k; ++i) {
+        HAI_TRY(draft_step_at(i, T));
+        bool need_read = false;
+        for (size_t b = 0; b < Bz; ++b) {
+            if (!open[b]) continue;
+            const int64_t pos = rs_[b].emitted + 1 + i;
+            if (io.override_tokens != nullptr && pos < io.n_override) {
+                const int64_t tok = io.override_tokens[static_cast<int64_t>(b) * io.n_override + pos];
+                HAI_TRY(hai_memcpy_h2d(d_vids_ + static_cast<int64_t>(b) * T + i + 1, &tok, 8, stream_));
+                HAI_TRY(sync());  // tok lives on the host stack
+            }
+            ++kd[b];
+            ++io.stats[b].proposed;
+            need_read = need_read || io.n_eos > 0;
         }
-        ++k;
-        ++stats->proposed;
-        if (n_eos > 0) {
-            int64_t cand = 0;
-            HAI_TRY(read_i64(d_vids_ + i + 1, &cand, 1));
-            if (in_set(eos, n_eos, cand)) break;
+        if (need_read) {
+            std::vector<int64_t> cand(Bz);
+            HAI_TRY(hai_copy_i64_strided(d_cand_, 1, d_vids_ + i + 1, T, B_, stream_));
+            HAI_TRY(read_i64(d_cand_, cand.data(), B_));
+            for (size_t b = 0; b < Bz; ++b)
+                if (open[b] && in_set(io.eos, io.n_eos, cand[b])) open[b] = false;
         }
+        for (size_t b = 0; b < Bz; ++b)
+            if (open[b] && kd[b] >= pc[b]) open[b] = false;
     }
-    stats->draft_seconds += seconds_since(t0);
+    // Drafts beyond a sequence's own count leave MTP rows the accept kernel
+    // must not see: roll the lengths back and pass the counts.
+    std::vector<int32_t> nd(Bz), delta(Bz);
+    bool uneven = false;
+    for (size_t b = 0; b < Bz; ++b) {
+        nd[b] = static_cast<int32_t>(kd[b]);
+        delta[b] = static_cast<int32_t>(kd[b] - k);
+        uneven = uneven || delta[b] != 0;
+    }
+    if (uneven) {
+        HAI_TRY(hai_memcpy_h2d(d_delta_, delta.data(), Bz * 4, stream_));
+        HAI_TRY(hai_add_i32(d_mlen_, d_delta_, 0, B_, stream_));
+    }
+    if (nd != ndraft_host_) {
+        HAI_TRY(hai_memcpy_h2d(d_ndraft_, nd.data(), Bz * 4, stream_));
+        HAI_TRY(sync());  // nd lives on the host stack
+        ndraft_host_ = nd;
+    }
+    const double draft_s = seconds_since(t0);
 
     // ---- verify + fused argmax/accept ----
     t0 = Clock::now();
-    const int64_t T = k + 1;
     HAI_TRY(verify_step(T));
-    int32_t res[4];
-    int64_t preds[17], cands[17];
-    HAI_TRY(hai_memcpy_d2h(res, d_result_, sizeof(res), stream_));
-    HAI_TRY(hai_memcpy_d2h(preds, d_preds_, static_cast<size_t>(T) * 8, stream_));
-    HAI_TRY(hai_memcpy_d2h(cands, d_vids_ + 1, static_cast<size_t>(k) * 8, stream_));
+    std::vector<int32_t> res(4 * Bz);
+    std::vector<int64_t> preds(Bz * static_cast<size_t>(T)), ids(Bz * static_cast<size_t>(T));
+    HAI_TRY(hai_memcpy_d2h(res.data(), d_result_, res.size() * 4, stream_));
+    HAI_TRY(hai_memcpy_d2h(preds.data(), d_preds_, preds.size() * 8, stream_));
+    HAI_TRY(hai_memcpy_d2h(ids.data(), d_vids_, ids.size() * 8, stream_));
     HAI_TRY(sync());
-    stats->verify_seconds += seconds_since(t0);
-    const int64_t a = res[0];
-    const bool full = res[1] != 0;
-    if (rec != nullptr) {
-        std::fill(rec, rec + HAI_ROUND_RECORD, -1);
-        rec[0] = static_cast<int32_t>(k);
-        rec[1] = static_cast<int32_t>(a);
-        rec[4] = static_cast<int32_t>(st.next_target);
-        rec[5] = static_cast<int32_t>(st.emitted);
-        for (int64_t i = 0; i < k && i < 8; ++i) rec[8 + i] = static_cast<int32_t>(cands[i]);
-    }
-    out[st.emitted++] = static_cast<int32_t>(st.next_target);
-    if (full) {
-        for (int64_t i = 0; i < k; ++i) out[st.emitted++] = static_cast<int32_t>(cands[i]);
-        stats->accepted += a;
-        st.next_target = preds[k];
-        st.target_len = target_len0 + T;
-        st.mtp_len = mtp_len0 + k;
-        if (rec) { rec[2] = 1; rec[3] = -1; }
-    } else {
-        const int64_t corr = preds[a];
-        stats->rejected += k - a;
-        ++stats->corrections;
-        for (int64_t i = 0; i < a; ++i) out[st.emitted++] = static_cast<int32_t>(cands[i]);
-        if (st.emitted < st.max_new) out[st.emitted++] = static_cast<int32_t>(corr);
-        stats->accepted += a;
-        if (rec) { rec[2] = 0; rec[3] = static_cast<int32_t>(corr); }
-        // The reference replays [next, accepted..., corr] on the committed
-        // caches; the rows before corr are already committed above.
-        st.target_len = target_len0 + a + 2;
-        if (st.emitted >= st.max_new || in_set(eos, n_eos, corr)) {
-            st.mtp_len = mtp_len0;  // the reference stops before restoring the MTP checkpoint
-            st.done = true;
+    const double verify_s = seconds_since(t0);
+
+    std::vector<bool> correct(Bz, false);
+    std::vector<int32_t*> recs(Bz, nullptr);
+    bool any_correct = false;
+    for (size_t b = 0; b < Bz; ++b) {
+        if (pc[b] == 0) continue;  // finished before this round
+        auto& st = rs_[b];
+        hai_spec_stats& stats = io.stats[b];
+        int32_t* out = io.out + static_cast<int64_t>(b) * io.out_ld;
+        const int64_t kb = kd[b];
+        stats.max_proposal_width = std::max(stats.max_proposal_width, pc[b]);
+        ++stats.rounds;
+        stats.draft_seconds += draft_s;
+        stats.verify_seconds += verify_s;
+        int32_t* rec = nullptr;
+        if (io.round_log != nullptr && io.n_log[b] < io.log_cap)
+            rec = io.round_log + (static_cast<int64_t>(b) * io.log_cap + io.n_log[b]++) * HAI_ROUND_RECORD;
+        recs[b] = rec;
+        const int64_t a = res[4 * b];
+        const bool full = res[4 * b + 1] != 0;
+        const int64_t* cands = ids.data() + b * static_cast<size_t>(T) + 1;
+        const int64_t* pr = preds.data() + b * static_cast<size_t>(T);
+        if (rec != nullptr) {
+            std::fill(rec, rec + HAI_ROUND_RECORD, -1);
+            rec[0] = static_cast<int32_t>(kb);
+            rec[1] = static_cast<int32_t>(a);
+            rec[4] = static_cast<int32_t>(st.next_target);
+            rec[5] = static_cast<int32_t>(st.emitted);
+            for (int64_t i = 0; i < kb && i < 8; ++i) rec[8 + i] = static_cast<int32_t>(cands[i]);
+        }
+        out[st.emitted++] = static_cast<int32_t>(st.next_target);
+        if (full) {
+            for (int64_t i = 0; i < kb; ++i) out[st.emitted++] = static_cast<int32_t>(cands[i]);
+            stats.accepted += a;
+            st.next_target = pr[kb];
+            st.target_len = target_len0[b] + kb + 1;
+            st.mtp_len = mtp_len0[b] + kb;
+            if (rec) { rec[2] = 1; rec[3] = -1; }
         } else {
-            t0 = Clock::now();
-            // MTP checkpoint[a] (length already rolled back by the accept
-            // kernel) plus the recovery row (emb(corr), hidden of row a).
-            HAI_TRY(correction_step());
-            ++stats->mtp_recovery_tokens;
-            ++stats->replay_tokens;
-            int64_t next = 0;
-            HAI_TRY(read_i64(d_vids_, &next, 1));
-            st.next_target = next;
-            st.mtp_len = mtp_len0 + a + 1;
-            stats->correction_seconds += seconds_since(t0);
+            const int64_t corr = pr[a];
+            stats.rejected += kb - a;
+            ++stats.corrections;
+            for (int64_t i = 0; i < a; ++i) out[st.emitted++] = static_cast<int32_t>(cands[i]);
+            if (st.emitted < st.max_new) out[st.emitted++] = static_cast<int32_t>(corr);
+            stats.accepted += a;
+            if (rec) { rec[2] = 0; rec[3] = static_cast<int32_t>(corr); }
+            // The reference replays [next, accepted..., corr] on the committed
+            // caches; the rows before corr are already committed above.
+            st.target_len = target_len0[b] + a + 2;
+            if (st.emitted >= st.max_new || in_set(io.eos, io.n_eos, corr)) {
+                st.mtp_len = mtp_len0[b];  // the reference stops before restoring the MTP checkpoint
+                st.done = true;
+            } else {
+                correct[b] = true;
+                any_correct = true;
+                ++stats.mtp_recovery_tokens;
+                ++stats.replay_tokens;
+                st.mtp_len = mtp_len0[b] + a + 1;
+            }
         }
     }
-    if (rec) {
-        rec[6] = static_cast<int32_t>(st.mtp_len);
-        rec[7] = static_cast<int32_t>(st.target_len);
+    if (any_correct) {
+        // MTP checkpoint[a] (length already rolled back by the accept kernel)
+        // plus the recovery row (emb(corr), hidden of row a)
+        t0 = Clock::now();
+        HAI_TRY(correction_step());
+        std::vector<int64_t> next(Bz);
+        HAI_TRY(read_i64(d_next_, next.data(), B_));
+        const double corr_s = seconds_since(t0);
+        for (size_t b = 0; b < Bz; ++b) {
+            if (!correct[b]) continue;
+            rs_[b].next_target = next[b];
+            io.stats[b].correction_seconds += corr_s;
+        }
     }
-    if (!st.done && (st.emitted >= st.max_new || in_set(eos, n_eos, out[st.emitted - 1]))) st.done = true;
+    for (size_t b = 0; b < Bz; ++b) {
+        if (pc[b] == 0) continue;
+        auto& st = rs_[b];
+        if (recs[b] != nullptr) {
+            recs[b][6] = static_cast<int32_t>(st.mtp_len);
+            recs[b][7] = static_cast<int32_t>(st.target_len);
+        }
+        const int32_t* out = io.out + static_cast<int64_t>(b) * io.out_ld;
+        if (!st.done && (st.emitted >= st.max_new || in_set(io.eos, io.n_eos, out[st.emitted - 1]))) st.done = true;
+    }
     return HAI_OK;
 }
 
-int Engine::generate_speculative(const int32_t* prompt, int64_t P, int64_t max_new, int64_t width,
+int Engine::generate_speculative(const int32_t* prompts, int64_t P, int64_t max_new, int64_t width,
                                  const int32_t* eos, int64_t n_eos, const int32_t* override_tokens,
                                  int64_t n_override, int32_t* out, hai_spec_stats* stats, int32_t* round_log,
                                  int64_t round_log_cap, int64_t* n_out) {
     if (width < 1) return fail(HAI_ERR_INVALID_ARGUMENT, "width must be >= 1");
-    hai_spec_stats st{};
+    // a finished sequence keeps running with the batch: leave room for its
+    // rows until the slowest sequence ends
+    if (B_ > 1 && P + (width + 2) * max_new + tmax_ > cap_)
+        return fail(HAI_ERR_INVALID_ARGUMENT, "generate_speculative: batched decode needs max_context >= "
+                                              "P + (width + 2) * max_new + max_verify_tokens");
+    const size_t Bz = static_cast<size_t>(B_);
+    std::vector<hai_spec_stats> st(Bz, hai_spec_stats{});
     auto t0 = Clock::now();
-    HAI_TRY(prefill(prompt, P, max_new));
-    st.prefill_seconds = seconds_since(t0);
+    HAI_TRY(prefill(prompts, P, max_new));
+    const double prefill_s = seconds_since(t0);
     auto t1 = Clock::now();
-    int64_t nlog = 0;
-    while (!rs_.done && rs_.emitted < max_new) {
-        int32_t* rec = (round_log != nullptr && nlog < round_log_cap) ? round_log + nlog * HAI_ROUND_RECORD : nullptr;
-        const int64_t before = st.rounds;
-        HAI_TRY(one_round(rs_, width, eos, n_eos, override_tokens, n_override, out, &st, rec));
-        if (st.rounds > before) ++nlog;
+    std::vector<int64_t> nlog(Bz, 0);
+    RoundIo io;
+    io.eos = eos;
+    io.n_eos = n_eos;
+    io.override_tokens = override_tokens;
+    io.n_override = override_tokens ? n_override : 0;
+    io.out = out;
+    io.out_ld = max_new;
+    io.stats = st.data();
+    io.round_log = round_log;
+    io.log_cap = round_log_cap;
+    io.n_log = nlog.data();
+    bool live = true;
+    while (live) HAI_TRY(one_round(width, io, &live));
+    const double decode_s = seconds_since(t1);
+    for (size_t b = 0; b < Bz; ++b) {
+        st[b].prefill_seconds = prefill_s;
+        st[b].decode_seconds = decode_s;
+        st[b].emitted = rs_[b].emitted;
+        if (stats) stats[b] = st[b];
+        n_out[b] = rs_[b].emitted;
     }
-    st.decode_seconds = seconds_since(t1);
-    st.emitted = rs_.emitted;
-    if (stats) *stats = st;
-    *n_out = rs_.emitted;
     return HAI_OK;
 }
 
 int Engine::spec_rounds(int64_t rounds, int64_t width, int32_t* out, int64_t cap, int64_t* n_out,
                         hai_spec_stats* stats) {
-    if (out == nullptr || cap < rs_.max_new) return fail(HAI_ERR_INVALID_ARGUMENT, "spec_rounds: out capacity < max_new");
-    hai_spec_stats local{};
-    hai_spec_stats* st = stats ? stats : &local;
-    const int64_t start = rs_.emitted;
+    for (const auto& r : rs_)
+        if (out == nullptr || cap < r.max_new) return fail(HAI_ERR_INVALID_ARGUMENT, "spec_rounds: out capacity < max_new");
+    const size_t Bz = static_cast<size_t>(B_);
+    std::vector<hai_spec_stats> st(Bz, hai_spec_stats{});
+    std::vector<int64_t> start(Bz);
+    for (size_t b = 0; b < Bz; ++b) start[b] = rs_[b].emitted;
+    RoundIo io;
+    io.out = out;
+    io.out_ld = cap;
+    io.stats = st.data();
     auto t0 = Clock::now();
-    for (int64_t r = 0; r < rounds && !rs_.done && rs_.emitted < rs_.max_new; ++r)
-        HAI_TRY(one_round(rs_, width, nullptr, 0, nullptr, 0, out, st, nullptr));
+    bool live = true;
+    for (int64_t r = 0; r < rounds && live; ++r) HAI_TRY(one_round(width, io, &live));
     HAI_TRY(sync());
-    st->decode_seconds += seconds_since(t0);
-    st->emitted += rs_.emitted - start;
-    if (n_out) *n_out = rs_.emitted;
+    const double dt = seconds_since(t0);
+    hai_spec_stats sum{};
+    for (size_t b = 0; b < Bz; ++b) {
+        const auto& s = st[b];
+        sum.rounds = std::max(sum.rounds, s.rounds);
+        sum.proposed += s.proposed;
+        sum.accepted += s.accepted;
+        sum.rejected += s.rejected;
+        sum.corrections += s.corrections;
+        sum.replay_tokens += s.replay_tokens;
+        sum.mtp_recovery_tokens += s.mtp_recovery_tokens;
+        sum.max_proposal_width = std::max(sum.max_proposal_width, s.max_proposal_width);
+        sum.emitted += rs_[b].emitted - start[b];
+        if (n_out) n_out[b] = rs_[b].emitted;
+    }
+    sum.decode_seconds = dt;
+    if (stats) {
+        stats->rounds += sum.rounds;
+        stats->proposed += sum.proposed;
+        stats->accepted += sum.accepted;
+        stats->rejected += sum.rejected;
+        stats->corrections += sum.corrections;
+        stats->replay_tokens += sum.replay_tokens;
+        stats->mtp_recovery_tokens += sum.mtp_recovery_tokens;
+        stats->max_proposal_width = std::max(stats->max_proposal_width, sum.max_proposal_width);
+        stats->emitted += sum.emitted;
+        stats->decode_seconds += dt;
+    }
     return HAI_OK;
 }
 
-// Replays verify steps of T rows at the current committed context without
-// committing them (the accept kernel runs on scratch lengths), timing the
-// whole step with events and every GEMM launch individually.
+// Replays verify steps of T rows per sequence at the current committed
+// context without committing them (the accept kernel runs on scratch
+// lengths), timing the whole step with events and every GEMM launch
+// individually.
 int Engine::profile_verify(int64_t T, int64_t iters, hai_verify_profile* out) {
     if (T < 1 || T > tmax_ || iters < 1) return fail(HAI_ERR_INVALID_ARGUMENT, "profile_verify: T or iters");
     const auto& d = d_;
     void *e0 = nullptr, *e1 = nullptr;
     HAI_TRY(hai_event_create(&e0));
     HAI_TRY(hai_event_create(&e1));
-    int32_t* scratch_len = d_plen_;  // lengths copied here so the real ones stay untouched
-    std::vector<int64_t> ids(static_cast<size_t>(T), 1);
-    HAI_TRY(hai_memcpy_h2d(d_ids_, ids.data(), static_cast<size_t>(T) * 8, stream_));
+    // scratch lengths: target [B], MTP [B], result [4B]; the real ones stay untouched
+    int32_t* s_tlen = d_plen_;
+    int32_t* s_mlen = d_plen_ + B_;
+    int32_t* s_res = d_plen_ + 3 * B_;
+    std::vector<int64_t> ids(static_cast<size_t>(B_ * T), 1);
+    HAI_TRY(hai_memcpy_h2d(d_ids_, ids.data(), ids.size() * 8, stream_));
     double verify_ms = 0.0, gemm_ms = 0.0, draft_ms = 0.0;
     for (int64_t it = 0; it < iters + 1; ++it) {  // first iteration warms up and records the GEMMs
         prof_record_ = it == 0;
         if (prof_record_) prof_calls_.clear();
         HAI_TRY(hai_event_record(e0, stream_));
         HAI_TRY(forward_target(d_ids_, T, true));
-        HAI_TRY(hai_memcpy_d2d(scratch_len, d_tlen_, 4, stream_));
-        HAI_TRY(hai_memcpy_d2d(scratch_len + 1, d_mlen_, 4, stream_));
-        HAI_TRY(hai_verify_argmax_accept_bf16(logits_, d.V, hf_, d.H, d_ids_, nullptr, 1, T, d_preds_,
-                                              scratch_len + 4, scratch_len, scratch_len + 1, d_pnext_, nullptr,
-                                              nullptr, argmax_scratch_, stream_));
+        HAI_TRY(hai_memcpy_d2d(s_tlen, d_tlen_, static_cast<size_t>(B_) * 4, stream_));
+        HAI_TRY(hai_memcpy_d2d(s_mlen, d_mlen_, static_cast<size_t>(B_) * 4, stream_));
+        HAI_TRY(hai_verify_argmax_accept_bf16(logits_, d.V, hf_, d.H, d_ids_, nullptr, B_, T, d_preds_, s_res,
+                                              s_tlen, s_mlen, d_pnext_, nullptr, nullptr, argmax_scratch_,
+                                              stream_));
         HAI_TRY(hai_event_record(e1, stream_));
         prof_record_ = false;
         HAI_TRY(sync());
@@ -829,12 +1030,8 @@ int Engine::profile_verify(int64_t T, int64_t iters, hai_verify_profile* out) {
             else if (c.nw != nullptr)
                 HAI_TRY(hai_gemm_rmsnorm_bf16(c.y, c.ldy, c.x, c.ldx, c.nw, cfg_.rms_eps, 1, c.xn, c.ldx, c.w.w,
                                               c.M, c.N, c.K, c.epi, c.res, c.ldres, stream_));
-            else if (c.w.q != nullptr)
-                HAI_TRY(hai_gemm_fp8_bf16(c.y, c.ldy, c.x, c.ldx, c.w.q, c.w.s, c.w.map, c.M, c.N, c.K,
-                                          c.epi | HAI_FP8_NO_SPECIAL_CODES, c.res, c.ldres, stream_));
             else
-                HAI_TRY(hai_gemm_bf16(c.y, c.ldy, c.x, c.ldx, c.w.w, c.M, c.N, c.K, c.epi, c.res, c.ldres,
-                                      stream_));
+                HAI_TRY(gemm(c.y, c.ldy, c.x, c.ldx, c.w, c.M, c.N, c.K, c.epi, c.res, c.ldres));
         }
         HAI_TRY(hai_event_record(e1, stream_));
         HAI_TRY(sync());
@@ -842,15 +1039,20 @@ int Engine::profile_verify(int64_t T, int64_t iters, hai_verify_profile* out) {
         HAI_TRY(hai_event_elapsed_ms(e0, e1, &ms));
         if (it > 0) gemm_ms += ms;
     }
-    const double launches = static_cast<double>(prof_calls_.size());
-    // Draft step timing (one MTP forward + lm_head + argmax) without events
-    // inside, on a scratch MTP length.
+    // one entry per GEMM call of the engine; a call of more than 16 rows is
+    // several launches on the bit-exact kernels
+    double launches = 0.0;
+    for (const auto& c : prof_calls_)
+        launches += (mfma_ && c.w.q == nullptr && c.M > 16) ? static_cast<double>((c.M + 127) / 128)
+                                                            : static_cast<double>((c.M + 15) / 16);
+    // Draft step timing (one MTP forward + lm_head + argmax per sequence)
+    // without events inside, on scratch MTP lengths.
     for (int64_t it = 0; it < iters + 1; ++it) {
-        HAI_TRY(hai_memcpy_d2d(scratch_len, d_mlen_, 4, stream_));
+        HAI_TRY(hai_memcpy_d2d(s_mlen, d_mlen_, static_cast<size_t>(B_) * 4, stream_));
         HAI_TRY(hai_event_record(e0, stream_));
         HAI_TRY(mtp_draft_step(d_ids_, h_prev_, mh_[0], d_pnext_));
         HAI_TRY(hai_event_record(e1, stream_));
-        HAI_TRY(hai_memcpy_d2d(d_mlen_, scratch_len, 4, stream_));
+        HAI_TRY(hai_memcpy_d2d(d_mlen_, s_mlen, static_cast<size_t>(B_) * 4, stream_));
         HAI_TRY(sync());
         float ms = 0.0f;
         HAI_TRY(hai_event_elapsed_ms(e0, e1, &ms));
@@ -864,13 +1066,15 @@ int Engine::profile_verify(int64_t T, int64_t iters, hai_verify_profile* out) {
     out->gemm_bytes = gemm_bytes;
     out->gemm_launches = launches;
     // algorithmic bytes of one verify step: weights streamed + KV read +
-    // DeltaNet state read and T states written.
+    // DeltaNet state read and T states written, per sequence.
     int64_t n_attn = 0, n_dn = 0;
     for (const auto& L : layers_) (L.attn ? n_attn : n_dn) += 1;
-    const double L = static_cast<double>(rs_.target_len + T);
-    const double kv = static_cast<double>(n_attn) * 2.0 * L * static_cast<double>(d.kvw) * 2.0;
-    const double state = static_cast<double>(n_dn) * static_cast<double>(d.nv * d.dk * d.dv) * 4.0 *
-                         (1.0 + static_cast<double>(T));
+    double kv = 0.0;
+    for (const auto& r : rs_)
+        kv += static_cast<double>(n_attn) * 2.0 * static_cast<double>(r.target_len + T) *
+              static_cast<double>(d.kvw) * 2.0;
+    const double state = static_cast<double>(B_) * static_cast<double>(n_dn) *
+                         static_cast<double>(d.nv * d.dk * d.dv) * 4.0 * (1.0 + static_cast<double>(T));
     out->step_bytes = out->gemm_bytes + kv + state;
     out->draft_ms = draft_ms / n;
     out->draft_bytes = static_cast<double>(d.H) * 2 * d.H * 2.0 +

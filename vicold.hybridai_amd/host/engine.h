@@ -3,16 +3,20 @@
 // Generator::generate (src/generator.cc:545-1117).
 //
 // Host code only: every device action goes through the hai_* C ABI
-// (include/hai_kernels.h).  Layout in HBM:
+// (include/hai_kernels.h).  The engine holds B sequences (B = max_batch) that
+// run the speculative rounds in lockstep; every per-sequence quantity (cache
+// rows, lengths, round state) is indexed by the sequence, and a verify row
+// is row b*T + t of the batch.  Layout in HBM:
 //   * weights: one arena, each Linear stored [N, K] row-major as in the
 //     checkpoint, with the projections of a layer concatenated so that one
 //     weight-streaming launch covers them: DeltaNet in_proj = [qkv | z | a | b]
 //     rows, attention = [q(+gate) | k | v] rows, MLP gate/up interleaved row by
 //     row (gate_f, up_f) for the fused SwiGLU epilogue;
-//   * caches: KV [cap][nkv][D] per attention layer; DeltaNet conv inputs in a
-//     ring [ring][C] indexed by position and the fp32 state in slots
-//     [nslots][nv][dk*dv] (each head column-tiled, as hai_deltanet_verify_bf16
-//     documents), the slot of sequence length L being L % nslots;
+//   * caches: KV [B][cap][nkv][D] per attention layer; DeltaNet conv inputs
+//     in a ring [B][ring][C] indexed by position and the fp32 state in slots
+//     [nslots][B][nv][dk*dv] (each head column-tiled, as
+//     hai_deltanet_verify_bf16 documents), the slot of sequence length L
+//     being L % nslots;
 //     committed lengths live on the device and are advanced by the accept
 //     kernel, so rollback is a length update, never a copy.
 #pragma once
@@ -83,10 +87,10 @@ struct LayerWeights {
     uint16_t* w_ab = nullptr;     // [2*nv, H]
     Fp8Linear f_out, f_qkv, f_o, f_gu, f_down;
     // caches
-    uint16_t* k_cache = nullptr;  // [cap][nkv][D]
+    uint16_t* k_cache = nullptr;  // [B][cap][nkv][D]
     uint16_t* v_cache = nullptr;
-    uint16_t* ring = nullptr;     // [ring][C]
-    float* state = nullptr;       // [nslots][nv][dk*dv], column-tiled heads
+    uint16_t* ring = nullptr;     // [B][ring][C]
+    float* state = nullptr;       // [nslots][B][nv][dk*dv], column-tiled heads
 };
 
 struct TensorEntry {
@@ -122,17 +126,23 @@ public:
     int64_t read_tensor(uint32_t id, uint16_t* out, int64_t capacity);
     uint64_t weight_bytes() const { return weight_bytes_; }
     const Dims& dims() const { return d_; }
+    int64_t batch() const { return B_; }
 
+    // Per-sequence arrays below are [B][...]: prompts [B][P], ids [B][T],
+    // hidden [B][T][H], logits [B][T][V], out [B][max_new or cap], n_out [B],
+    // stats [B], round_log [B][round_log_cap][HAI_ROUND_RECORD],
+    // override_tokens [B][n_override].
     int forward_rows(const int32_t* ids, int64_t T, uint16_t* hidden, uint16_t* logits);
     int generate_greedy(const int32_t* prompt, int64_t P, int64_t max_new, const int32_t* eos,
                         int64_t n_eos, int32_t* out, int64_t* n_out);
-    int generate_speculative(const int32_t* prompt, int64_t P, int64_t max_new, int64_t width,
+    int generate_speculative(const int32_t* prompts, int64_t P, int64_t max_new, int64_t width,
                              const int32_t* eos, int64_t n_eos, const int32_t* override_tokens,
                              int64_t n_override, int32_t* out, hai_spec_stats* stats,
                              int32_t* round_log, int64_t round_log_cap, int64_t* n_out);
 
-    // benchmark split of generate_speculative
-    int prefill(const int32_t* prompt, int64_t P, int64_t max_new);
+    // benchmark split of generate_speculative; spec_rounds sums the stats of
+    // all sequences
+    int prefill(const int32_t* prompts, int64_t P, int64_t max_new);
     int spec_rounds(int64_t rounds, int64_t width, int32_t* out, int64_t cap, int64_t* n_out,
                     hai_spec_stats* stats);
     int profile_verify(int64_t T, int64_t iters, hai_verify_profile* out);
@@ -146,6 +156,19 @@ private:
         int64_t mtp_len = 0;
         bool done = false;
     };
+    // Inputs of one lockstep round that vary per sequence.
+    struct RoundIo {
+        const int32_t* eos = nullptr;
+        int64_t n_eos = 0;
+        const int32_t* override_tokens = nullptr;  // [B][n_override]
+        int64_t n_override = 0;
+        int32_t* out = nullptr;                    // [B][out_ld]
+        int64_t out_ld = 0;
+        hai_spec_stats* stats = nullptr;           // [B]
+        int32_t* round_log = nullptr;              // [B][log_cap][HAI_ROUND_RECORD]
+        int64_t log_cap = 0;
+        int64_t* n_log = nullptr;                  // [B] records written
+    };
 
     int fail(int rc, const std::string& what);
     int alloc_all();
@@ -153,6 +176,9 @@ private:
     int upload_rope_tables();
 
     // device pieces of a step
+    // M rows of any count: launches of <= 16 rows on the bit-exact kernels,
+    // or one MFMA launch per <= 128 rows when the engine runs in tolerance
+    // mode (hai_engine_options::mfma, bf16 weights, M > 16).
     int gemm(uint16_t* y, int64_t ldy, const uint16_t* x, int64_t ldx, const Lin& w, int64_t M, int64_t N,
              int64_t K, int epi, const uint16_t* res, int64_t ldres);
     // RMSNorm(+1) of the H-wide rows x (norm weight nw) fused into the linear
@@ -164,19 +190,19 @@ private:
     int attention_layer(const LayerWeights& L, int64_t T, uint16_t* h, const int32_t* lens,
                         uint16_t* kc, uint16_t* vc);
     int mlp(const LayerWeights& L, int64_t T, uint16_t* h);
-    int mtp_kv_rows(const int64_t* d_ids, const uint16_t* d_hidden, int64_t T);
+    int mtp_kv_rows(const int64_t* d_ids, const uint16_t* d_hidden, int64_t T, bool add_len);
     int mtp_draft_step(const int64_t* d_id, const uint16_t* d_hin, uint16_t* d_mh, int64_t* d_cand);
     int prefill_chunks(const int32_t* ids, int64_t P, uint16_t* hidden_out, uint16_t* logits_out);
-    int one_round(RoundState& st, int64_t width, const int32_t* eos, int64_t n_eos,
-                  const int32_t* override_tokens, int64_t n_override, int32_t* out,
-                  hai_spec_stats* stats, int32_t* log_rec);
+    // One lockstep round of every live sequence; returns false in *any_live
+    // when every sequence has finished.
+    int one_round(int64_t width, const RoundIo& io, bool* any_live);
     int sync();
     int read_i64(const int64_t* d, int64_t* h, int64_t n);
     // Replays the captured graph in *slot (capturing `enqueue` on first use)
     // when graphs are enabled; otherwise launches `enqueue` directly.
     template <typename F>
     int replay(void** slot, F&& enqueue);
-    int draft_step_at(int64_t i);
+    int draft_step_at(int64_t i, int64_t T);
     int verify_step(int64_t T);
     int correction_step();
 
@@ -192,8 +218,10 @@ private:
     void* work_ = nullptr;
     uint64_t weight_bytes_ = 0;
 
+    int64_t B_ = 1;       // sequences
     int64_t cap_ = 0;     // KV capacity per sequence
-    int64_t tmax_ = 0;    // largest verify T / prefill chunk
+    int64_t tmax_ = 0;    // largest verify T / prefill chunk (rows per sequence)
+    bool mfma_ = false;   // MFMA GEMMs for launches of more than 16 rows
     int64_t ring_ = 0;
     int64_t nslots_ = 0;
 
@@ -211,29 +239,34 @@ private:
     std::vector<QuantEntry> quant_;
     std::vector<std::pair<int32_t*, std::vector<int32_t>>> maps_;  // scale maps uploaded at init
 
-    // workspace
-    int64_t* d_ids_ = nullptr;    // [tmax] prefill / forward ids
-    int64_t* d_vids_ = nullptr;   // [tmax+1] next_target + candidates
-    int64_t* d_preds_ = nullptr;  // [tmax]
-    int32_t* d_result_ = nullptr; // [4]
-    int32_t* d_tlen_ = nullptr;   // committed target length
-    int32_t* d_mlen_ = nullptr;   // MTP cache length
-    int32_t* d_plen_ = nullptr;   // [8] profiling scratch lengths/results
-    int64_t* d_pnext_ = nullptr;  // [8] profiling scratch tokens
-    uint16_t* h_ = nullptr;       // [tmax, H] residual stream
-    uint16_t* xn_ = nullptr;      // [tmax, 2H]
-    uint16_t* emb_ = nullptr;     // [tmax, H]
-    uint16_t* proj_ = nullptr;    // [tmax, max(Nin, Nqkv)]
-    uint16_t* q_ = nullptr;       // [tmax, nq*D]
+    // workspace (rows = B * tmax)
+    int64_t* d_ids_ = nullptr;    // [rows] prefill / forward ids
+    int64_t* d_vids_ = nullptr;   // [B][T] per sequence: next_target, candidates
+    int64_t* d_next_ = nullptr;   // [B] next target after the round (accept / correction)
+    int64_t* d_dids_ = nullptr;   // [B] draft inputs
+    int64_t* d_cand_ = nullptr;   // [B] draft outputs / correction argmax
+    int64_t* d_preds_ = nullptr;  // [rows]
+    int32_t* d_result_ = nullptr; // [B][4]
+    int32_t* d_tlen_ = nullptr;   // [B] committed target lengths
+    int32_t* d_mlen_ = nullptr;   // [B] MTP cache lengths
+    int32_t* d_ndraft_ = nullptr; // [B] drafts counted per sequence this round
+    int32_t* d_delta_ = nullptr;  // [B] MTP length corrections
+    int32_t* d_plen_ = nullptr;   // [3B + 4B] profiling scratch lengths/results
+    int64_t* d_pnext_ = nullptr;  // [B] profiling scratch tokens
+    uint16_t* h_ = nullptr;       // [rows, H] residual stream
+    uint16_t* xn_ = nullptr;      // [rows, 2H]
+    uint16_t* emb_ = nullptr;     // [rows, H]
+    uint16_t* proj_ = nullptr;    // [rows, max(Nin, Nqkv)]
+    uint16_t* q_ = nullptr;       // [rows, nq*D]
     uint16_t* gate_ = nullptr;
     uint16_t* att_ = nullptr;
-    uint16_t* dnout_ = nullptr;   // [tmax, nv*dv]
-    uint16_t* act_ = nullptr;     // [tmax, F]
-    uint16_t* hf_ = nullptr;      // [tmax, H] post-final-norm hidden
-    uint16_t* logits_ = nullptr;  // [tmax, V]
-    uint16_t* mh_[2] = {nullptr, nullptr};  // MTP outputs (chained drafts)
-    uint16_t* h_prev_ = nullptr;  // target hidden feeding the next draft
-    uint16_t* rec_hidden_ = nullptr;
+    uint16_t* dnout_ = nullptr;   // [rows, nv*dv]
+    uint16_t* act_ = nullptr;     // [rows, F]
+    uint16_t* hf_ = nullptr;      // [rows, H] post-final-norm hidden
+    uint16_t* logits_ = nullptr;  // [rows, V]
+    uint16_t* mh_[2] = {nullptr, nullptr};  // [B, H] MTP outputs (chained drafts)
+    uint16_t* h_prev_ = nullptr;  // [B, H] target hidden feeding the next draft
+    uint16_t* rec_hidden_ = nullptr;  // [B, H]
     void* gqa_scratch_ = nullptr;
     void* argmax_scratch_ = nullptr;
     float* rope_cos_ = nullptr;
@@ -259,10 +292,11 @@ private:
     bool prof_record_ = false;
     std::vector<GemmCall> prof_calls_;
 
-    RoundState rs_;
+    std::vector<RoundState> rs_;          // [B]
+    std::vector<int32_t> ndraft_host_;    // last uploaded d_ndraft_ contents
 
     bool use_graphs_ = false;
-    std::vector<void*> draft_graphs_;   // by draft index
+    std::vector<void*> draft_graphs_;   // by (verify width T, draft index)
     std::vector<void*> verify_graphs_;  // by verify width T
     void* corr_graph_ = nullptr;
 };
