@@ -338,15 +338,19 @@ int hai_correction_commit_bf16(const int32_t* result, const int64_t* corr_next,
                                int32_t* target_len, int32_t* mtp_len,
                                void* stream);
 /* Batched-verify linear layer on the matrix cores (M up to 128 rows: C4/C5
- * batches), the same contract and epilogues as hai_gemm_bf16 but computed
- * with v_mfma_f32_16x16x32_bf16: equal to the canonical result within fp32
- * accumulation error (~1e-6 relative before the bf16 output rounding), not
- * bit for bit.  Replaces rocblas_gemm_ex (hip_backend.cc:697-809) for
- * M > 16. x and w 16-byte aligned, K % 8 == 0. */
+ * batches and batched prompt chunks), the same contract and epilogues as
+ * hai_gemm_bf16 but computed with v_mfma_f32_16x16x32_bf16: equal to the
+ * canonical result within fp32 accumulation error (~1e-6 relative before
+ * the bf16 output rounding), not bit for bit.  Replaces rocblas_gemm_ex
+ * (hip_backend.cc:697-809) for M > 16.  x and w 16-byte aligned, K % 8 == 0.
+ * workspace (may be NULL) lets narrow layers split K across blocks; with
+ * hai_gemm_mfma_workspace_bytes(M, N) bytes every split is available, with
+ * less the call uses fewer splits.  The result does not depend on it. */
+size_t hai_gemm_mfma_workspace_bytes(int64_t M, int64_t N);
 int hai_gemm_bf16_mfma(void* y, int64_t ldy, const void* x, int64_t ldx,
                        const void* w, int64_t M, int64_t N, int64_t K,
                        int epilogue, const void* res, int64_t ld_res,
-                       void* stream);
+                       void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------ synthetic data / checks
  * Synthetic weights: element (r, c) of a [rows, cols] tensor (row stride

@@ -649,9 +649,11 @@ def test_gemm_rmsnorm_fp8_fused(M, N, K_, epi, with_xn, mapped):
 
 
 # ----------------------------------------------------------------- MFMA (tolerance mode)
-@pytest.mark.parametrize("M,N,K,epi", [(17, 300, 256, 0), (32, 1536, 5120, 1), (64, 1000, 1000, 2),
-                                       (128, 640, 2048, 0), (40, 16480, 512, 0)])
-def test_gemm_mfma_within_tolerance(M, N, K, epi):
+@pytest.mark.parametrize("M,N,K,epi,with_ws", [(17, 300, 256, 0, True), (32, 1536, 5120, 1, True),
+                                               (64, 1000, 1000, 2, True), (128, 640, 2048, 0, False),
+                                               (40, 16480, 512, 0, True), (33, 2050, 2056, 2, True),
+                                               (32, 1536, 5120, 1, False), (96, 5120, 6144, 1, True)])
+def test_gemm_mfma_within_tolerance(M, N, K, epi, with_ws):
     """hai_gemm_bf16_mfma against the canonical GEMM: the bf16 outputs differ
     by at most a couple of bf16 ulps (fp32 accumulation in another order)."""
     rng = np.random.default_rng(M + N + K + epi)
@@ -661,8 +663,11 @@ def test_gemm_mfma_within_tolerance(M, N, K, epi):
     h, hb = rand_bf16(rng, (M, ncols))
     dx, dw = dev(xb), dev(wb)
     dy = dev(hb) if epi == hai.EPI_RESIDUAL else out_buf(M * ncols * 2)
+    wsb = kern().hai_gemm_mfma_workspace_bytes(M, N)
+    dws = out_buf(max(wsb, 16)) if with_ws else None
     hai.check(kern().hai_gemm_bf16_mfma(dy.ptr, ncols, dx.ptr, K, dw.ptr, M, N, K, epi,
-                                        dy.ptr if epi == hai.EPI_RESIDUAL else None, ncols, None), "gemm_mfma")
+                                        dy.ptr if epi == hai.EPI_RESIDUAL else None, ncols,
+                                        dws.ptr if dws else None, wsb if dws else 0, None), "gemm_mfma")
     y = orc.gemm(x, w)
     if epi == hai.EPI_STORE:
         want = y

@@ -1,28 +1,30 @@
 // hai_gemm_mfma.hip -- batched-verify linear layer on the gfx950 matrix cores:
 // Y[M, N] = X[M, K] . W[N, K]^T for M = (k+1) tokens x batch rows beyond the
-// skinny kernel's 16 (the C4 / C5 batches: 32-64 rows), replacing
-// rocblas_gemm_ex in HipBackend::gemm (hip_backend.cc:697-809) for that case.
+// skinny kernel's 16 (the C4 / C5 batches and batched prompt chunks: 17-128
+// rows), replacing rocblas_gemm_ex in HipBackend::gemm (hip_backend.cc:697-809)
+// for that case.
 //
 // Tolerance mode: v_mfma_f32_16x16x32_bf16 sums each 32-product group with
 // its own internal rounding, so results match the canonical fp32 order to
 // ~1e-6 relative before the bf16 output rounding, not bit for bit.  The
 // bit-exact path (hai_gemm_bf16) stays the one for M <= 16.
 //
-// Design (weight-streaming bound: 2M flop per weight pair of bytes, far below
-// the MFMA ridge even at M = 128):
-//   * A block owns 16 * NT consecutive weight rows; its KS waves split K by
-//     512-element chunks (wave w takes chunks w, w + KS, ...), so every weight
-//     byte is read once and narrow layers still get KS waves per row tile.
-//   * Operands come straight from global memory in the MFMA register layout:
-//     lane l supplies row (l % 16) and the 8 consecutive k of slab l / 16.
-//     Any K order works if A and B use the same one; within a 512-element
-//     chunk, slab g of step j is k = 32 j + 8 g, so the four lanes of a row
-//     read 64 contiguous bytes per load instruction (16 rows x 64 B per
-//     instruction; 16-byte non-temporal loads).
-//   * The KS partial tiles meet in LDS and are summed in wave order (the
-//     result does not depend on timing), then one epilogue writes bf16 with
-//     the skinny GEMM's epilogues (store, residual add, SwiGLU over
-//     interleaved gate/up rows).
+// Design (weight-streaming bound: 2M flop per pair of weight bytes, far
+// below the MFMA ridge even at M = 128):
+//   * A block (4 waves) owns 64 consecutive weight rows, 16 per wave, and
+//     walks K in 256-element chunks.  Every wave streams its rows with
+//     row-contiguous 16-byte loads (two rows per instruction, non-temporal)
+//     into its own LDS tile; the chunk's activation rows [M x 256] are loaded
+//     once per block, coalesced, into a shared LDS tile.  The next chunk's
+//     loads are in flight (registers) while the current one is multiplied.
+//   * MFMA operands are read from LDS in the register layout of the 16x16x32
+//     instruction: lane l takes row l % 16 and k-slab 8 (l / 16) + 32 j.
+//     Rows are padded by 16 bytes, so those reads are bank-conflict free.
+//   * Narrow layers (N <= 20480) also split K across 2 or 4 blocks when the
+//     caller passes a workspace: the blocks write fp32 partials and a second
+//     pass sums them in split order (deterministic) and applies the epilogue.
+//   * Epilogues as in the skinny GEMM: store, residual add, SwiGLU over
+//     interleaved (gate_f, up_f) rows.
 #include "hai_common.h"
 #include "hai_device.h"
 
@@ -34,104 +36,157 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kMaxMfmaRows = 128;
+constexpr int kChunk = 256;           // k elements per chunk
+constexpr int kLdsRow = kChunk + 8;   // padded LDS row, bf16 elements
+constexpr int kBlockRows = 64;        // weight rows per block
 
 __device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
                                                    0, 0, 0);
 }
 
-template <int MT, int NT, int KS, int JG, int EPI>
-__global__ __launch_bounds__(64 * KS) void gemm_bf16_mfma_kernel(uint16_t* __restrict__ y, int64_t ldy,
-                                                                 const uint16_t* __restrict__ x, int64_t ldx,
-                                                                 const uint16_t* __restrict__ w, const uint16_t* res,
-                                                                 int64_t ldres, int M, int N, int K) {
-    __shared__ f32x4 part[KS][NT][MT][64];
-    const int lane = threadIdx.x & 63;
+// Epilogue of one output element pair held by lane (li, kg): value v of row m,
+// column n (SwiGLU pairs columns n, n ^ 1 across lanes li, li ^ 1).
+template <int EPI>
+__device__ __forceinline__ void mfma_store(uint16_t* y, int64_t ldy, const uint16_t* res, int64_t ldres, float v,
+                                           int m, int64_t n, int M, int N, int li) {
+    if (EPI == HAI_EPI_SILU_MUL) {
+        const float g = bfr(v);
+        const float u = __shfl_xor(g, 1);
+        if ((li & 1) == 0 && m < M && n + 1 < N) y[static_cast<int64_t>(m) * ldy + n / 2] = f2bf(csilu(g) * u);
+    } else if (m < M && n < N) {
+        float o = bfr(v);
+        if (EPI == HAI_EPI_RESIDUAL) o = bf2f(res[static_cast<int64_t>(m) * ldres + n]) + o;
+        y[static_cast<int64_t>(m) * ldy + n] = f2bf(o);
+    }
+}
+
+// grid (ceil(N / 64), KSB); with KSB > 1 the blocks of split s take chunks
+// s, s + KSB, ... and write fp32 partials part[s][m][n].
+template <int MT, int EPI>
+__global__ __launch_bounds__(256) void gemm_bf16_mfma_kernel(uint16_t* __restrict__ y, int64_t ldy,
+                                                             const uint16_t* __restrict__ x, int64_t ldx,
+                                                             const uint16_t* __restrict__ w, const uint16_t* res,
+                                                             int64_t ldres, int M, int N, int K,
+                                                             float* __restrict__ part, int KSB) {
+    extern __shared__ __align__(16) uint16_t lds[];
+    uint16_t* xs = lds;                          // [16 MT][kLdsRow] activation rows
+    uint16_t* ws = lds + 16 * MT * kLdsRow;      // [4 waves][16][kLdsRow] weight rows
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
     const int wave = wave_index();
     const int li = lane & 15;
     const int kg = lane >> 4;
-    const int64_t row_base = static_cast<int64_t>(blockIdx.x) * (16 * NT);
+    const int64_t row_base = static_cast<int64_t>(blockIdx.x) * kBlockRows + wave * 16;
 
-    // Byte offsets fit 32 bits: the caller bounds N*K*2 and M*ldx*2 below 4 GiB.
-    // Rows past N or M start at or past the buffer end and read zeros.
+    // Byte offsets fit 32 bits: the caller bounds N*K*2 and M*ldx*2 below 4
+    // GiB.  Rows past N or M start at or past the buffer end and read zeros.
     const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, static_cast<uint32_t>(static_cast<int64_t>(N) * K * 2));
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, static_cast<uint32_t>(static_cast<int64_t>(M) * ldx * 2));
-    uint32_t woff[NT], xoff[MT];
+    // weight loads: instruction i covers rows 2i and 2i+1 (lanes 0-31 / 32-63)
+    const int w_half = lane >> 5;
+    const int w_col = (lane & 31) * 8;
+    const uint32_t woff0 = static_cast<uint32_t>(((row_base + w_half) * static_cast<int64_t>(K) + w_col) * 2);
+    const uint32_t two_rows = static_cast<uint32_t>(K) * 4u;
+    // activation loads: 16 MT rows x 256 elements, 32 lanes per row
+    constexpr int XL = 2 * MT;
+    uint32_t xoff[XL];
+    int xrow[XL], xcol[XL];
 #pragma unroll
-    for (int t = 0; t < NT; ++t)
-        woff[t] = static_cast<uint32_t>(((row_base + 16 * t + li) * static_cast<int64_t>(K) + 8 * kg) * 2);
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-        xoff[mt] = static_cast<uint32_t>((static_cast<int64_t>(16 * mt + li) * ldx + 8 * kg) * 2);
+    for (int i = 0; i < XL; ++i) {
+        const int e = tid + 256 * i;
+        xrow[i] = e >> 5;
+        xcol[i] = (e & 31) * 8;
+        xoff[i] = static_cast<uint32_t>((static_cast<int64_t>(xrow[i]) * ldx + xcol[i]) * 2);
+    }
 
-    f32x4 acc[NT][MT];
+    f32x4 acc[MT];
 #pragma unroll
-    for (int t = 0; t < NT; ++t)
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) acc[t][mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    const int nck = (K + 511) / 512;
-    const int nfull = K / 512;
-    for (int c = wave; c < nck; c += KS) {
-        const bool full = c < nfull;
+    const int nck = (K + kChunk - 1) / kChunk;
+    const int nfull = K / kChunk;
+    const int split = blockIdx.y;
+    u32x4 wv[8], xv[XL];
+    auto load = [&](int c) {
+        const uint32_t off = static_cast<uint32_t>(c) * (kChunk * 2);
+        if (c < nfull) {
 #pragma unroll
-        for (int j0 = 0; j0 < 16; j0 += JG) {
-            u32x4 bw[JG][NT], ax[JG][MT];
+            for (int i = 0; i < 8; ++i) wv[i] = bload_w(rw, woff0 + i * two_rows, off);
 #pragma unroll
-            for (int jj = 0; jj < JG; ++jj) {
-                const int j = j0 + jj;
-                const uint32_t koff = static_cast<uint32_t>(c) * 1024u + static_cast<uint32_t>(j) * 64u;
-                // ragged chunk: this lane's 8 elements are all in range or all
-                // out (K % 8 == 0)
-                const bool ok = full || (c * 512 + 32 * j + 8 * kg < K);
-                const ChunkOffset co(full, ok, koff);
+            for (int i = 0; i < XL; ++i) xv[i] = bload(rx, xoff[i], off);
+        } else {
+            // ragged chunk: a lane's 8 elements are all in K or all past it
+            const bool okw = c * kChunk + w_col < K;
 #pragma unroll
-                for (int t = 0; t < NT; ++t) bw[jj][t] = bload_w(rw, co.v(woff[t]), co.s);
+            for (int i = 0; i < 8; ++i) wv[i] = bload_w(rw, okw ? woff0 + i * two_rows + off : kOutOfRange, 0u);
 #pragma unroll
-                for (int mt = 0; mt < MT; ++mt) ax[jj][mt] = bload(rx, co.v(xoff[mt]), co.s);
+            for (int i = 0; i < XL; ++i) xv[i] = bload(rx, c * kChunk + xcol[i] < K ? xoff[i] + off : kOutOfRange, 0u);
+        }
+    };
+    int c = split;
+    if (c < nck) load(c);
+    for (; c < nck; c += KSB) {
+        __syncthreads();  // the previous chunk's LDS reads are done
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            *reinterpret_cast<u32x4*>(&ws[(wave * 16 + 2 * i + w_half) * kLdsRow + w_col]) = wv[i];
+#pragma unroll
+        for (int i = 0; i < XL; ++i) *reinterpret_cast<u32x4*>(&xs[xrow[i] * kLdsRow + xcol[i]]) = xv[i];
+        __syncthreads();
+        if (c + KSB < nck) load(c + KSB);
+#pragma unroll
+        for (int j = 0; j < kChunk / 32; ++j) {
+            const u32x4 b = *reinterpret_cast<const u32x4*>(&ws[(wave * 16 + li) * kLdsRow + 32 * j + 8 * kg]);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                const u32x4 a = *reinterpret_cast<const u32x4*>(&xs[(16 * mt + li) * kLdsRow + 32 * j + 8 * kg]);
+                acc[mt] = mfma16(a, b, acc[mt]);
             }
-#pragma unroll
-            for (int jj = 0; jj < JG; ++jj)
-#pragma unroll
-                for (int t = 0; t < NT; ++t)
-#pragma unroll
-                    for (int mt = 0; mt < MT; ++mt) acc[t][mt] = mfma16(ax[jj][mt], bw[jj][t], acc[t][mt]);
         }
     }
 
+    // D layout: lane (li, kg) holds rows 16 mt + 4 kg + i of column row_base + li
+    const int64_t n = row_base + li;
 #pragma unroll
-    for (int t = 0; t < NT; ++t)
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) part[wave][t][mt][lane] = acc[t][mt];
-    __syncthreads();
-
-    // Tiles (t, mt) are finished by the waves in turn; partials summed in wave
-    // order.  Lane l holds D rows 16 mt + 4 (l / 16) + i, column n = l % 16 of
-    // tile t.
-    for (int tile = wave; tile < NT * MT; tile += KS) {
-        const int t = tile / MT;
-        const int mt = tile - t * MT;
-        f32x4 s = part[0][t][mt][lane];
-#pragma unroll
-        for (int q = 1; q < KS; ++q) {
-            const f32x4 p = part[q][t][mt][lane];
-            s = f32x4{s[0] + p[0], s[1] + p[1], s[2] + p[2], s[3] + p[3]};
-        }
-        const int64_t n = row_base + 16 * t + li;
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int m = 16 * mt + 4 * kg + i;
-            if (EPI == HAI_EPI_SILU_MUL) {
-                // rows (2f, 2f+1) = (gate_f, up_f) sit in lanes (2p, 2p+1)
-                const float g = bfr(s[i]);
-                const float u = __shfl_xor(g, 1);
-                if ((li & 1) == 0 && m < M && n + 1 < N) y[static_cast<int64_t>(m) * ldy + n / 2] = f2bf(csilu(g) * u);
-            } else if (m < M && n < N) {
-                float v = bfr(s[i]);
-                if (EPI == HAI_EPI_RESIDUAL) v = bf2f(res[static_cast<int64_t>(m) * ldres + n]) + v;
-                y[static_cast<int64_t>(m) * ldy + n] = f2bf(v);
-            }
+            if (KSB == 1)
+                mfma_store<EPI>(y, ldy, res, ldres, acc[mt][i], m, n, M, N, li);
+            else if (m < M && n < N)
+                part[(static_cast<int64_t>(split) * M + m) * N + n] = acc[mt][i];
         }
+}
+
+// Sums the KSB partials of every element in split order and applies the
+// epilogue; one thread per output column pair (n even, n + 1).
+template <int EPI>
+__global__ void mfma_finalize_kernel(uint16_t* __restrict__ y, int64_t ldy, const float* __restrict__ part, int KSB,
+                                     const uint16_t* res, int64_t ldres, int M, int N) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int64_t np = (static_cast<int64_t>(N) + 1) / 2;
+    if (i >= static_cast<int64_t>(M) * np) return;
+    const int m = static_cast<int>(i / np);
+    const int64_t n = (i - m * np) * 2;
+    float v[2] = {0.0f, 0.0f};
+    for (int e = 0; e < 2; ++e) {
+        if (n + e >= N) continue;
+        const int64_t at = static_cast<int64_t>(m) * N + n + e;
+        float s = part[at];
+        for (int q = 1; q < KSB; ++q) s = s + part[static_cast<int64_t>(q) * M * N + at];
+        v[e] = s;
+    }
+    if (EPI == HAI_EPI_SILU_MUL) {
+        if (n + 1 < N) y[static_cast<int64_t>(m) * ldy + n / 2] = f2bf(csilu(bfr(v[0])) * bfr(v[1]));
+        return;
+    }
+    for (int e = 0; e < 2; ++e) {
+        if (n + e >= N) continue;
+        float o = bfr(v[e]);
+        if (EPI == HAI_EPI_RESIDUAL) o = bf2f(res[static_cast<int64_t>(m) * ldres + n + e]) + o;
+        y[static_cast<int64_t>(m) * ldy + n + e] = f2bf(o);
     }
 }
 
@@ -144,56 +199,82 @@ struct MfmaArgs {
     const uint16_t* res;
     int64_t ldres;
     int M, N, K;
+    float* part;
+    int KSB;
 };
 
 template <int MT, int EPI>
-void launch_mfma(const MfmaArgs& a, hipStream_t s) {
-    constexpr int NT = 2, KS = 4, JG = 4;
-    const int64_t blocks = (static_cast<int64_t>(a.N) + 16 * NT - 1) / (16 * NT);
-    gemm_bf16_mfma_kernel<MT, NT, KS, JG, EPI><<<dim3(static_cast<unsigned>(blocks)), dim3(64 * KS), 0, s>>>(
-        a.y, a.ldy, a.x, a.ldx, a.w, a.res, a.ldres, a.M, a.N, a.K);
+int launch_mfma(const MfmaArgs& a, hipStream_t s) {
+    auto* kern = gemm_bf16_mfma_kernel<MT, EPI>;
+    const size_t shmem = static_cast<size_t>(16 * MT + 4 * 16) * kLdsRow * 2;
+    static bool attr = false;  // LDS above the 64 KB default needs the attribute once per instance
+    if (!attr) {
+        const int rc = check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                     static_cast<int>(shmem)),
+                                 "hipFuncSetAttribute");
+        if (rc != HAI_OK) return rc;
+        attr = true;
+    }
+    const dim3 grid(static_cast<unsigned>((a.N + kBlockRows - 1) / kBlockRows), static_cast<unsigned>(a.KSB));
+    kern<<<grid, dim3(256), shmem, s>>>(a.y, a.ldy, a.x, a.ldx, a.w, a.res, a.ldres, a.M, a.N, a.K, a.part, a.KSB);
+    int rc = launched("gemm_bf16_mfma_kernel");
+    if (rc != HAI_OK || a.KSB == 1) return rc;
+    const int64_t n = static_cast<int64_t>(a.M) * ((a.N + 1) / 2);
+    mfma_finalize_kernel<EPI><<<dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s>>>(
+        a.y, a.ldy, a.part, a.KSB, a.res, a.ldres, a.M, a.N);
+    return launched("mfma_finalize_kernel");
 }
 
 template <int EPI>
-void dispatch_mfma(const MfmaArgs& a, hipStream_t s) {
-    if (a.M <= 16) launch_mfma<1, EPI>(a, s);
-    else if (a.M <= 32) launch_mfma<2, EPI>(a, s);
-    else if (a.M <= 64) launch_mfma<4, EPI>(a, s);
-    else launch_mfma<8, EPI>(a, s);
+int dispatch_mfma(const MfmaArgs& a, hipStream_t s) {
+    if (a.M <= 32) return launch_mfma<2, EPI>(a, s);
+    if (a.M <= 64) return launch_mfma<4, EPI>(a, s);
+    return launch_mfma<8, EPI>(a, s);
 }
 
 }  // namespace
 
+extern "C" size_t hai_gemm_mfma_workspace_bytes(int64_t M, int64_t N) {
+    // largest split the dispatcher picks for this shape (4 at N <= 8192, 2 at N <= 20480)
+    const int64_t ksb = N <= 8192 ? 4 : (N <= 20480 ? 2 : 1);
+    return ksb > 1 ? static_cast<size_t>(ksb * M * N) * sizeof(float) : 0;
+}
+
 extern "C" int hai_gemm_bf16_mfma(void* y, int64_t ldy, const void* x, int64_t ldx, const void* w, int64_t M,
                                   int64_t N, int64_t K, int epilogue, const void* res, int64_t ld_res,
-                                  void* stream) {
+                                  void* workspace, size_t workspace_bytes, void* stream) {
     if (y == nullptr || x == nullptr || w == nullptr) return invalid("gemm_mfma: null pointer");
     if (M < 0 || M > kMaxMfmaRows || N < 0 || K <= 0 || K % 8 != 0 || ldx % 8 != 0 || ldx < K)
         return invalid("gemm_mfma: shape (need 0<=M<=128, K%8==0, ldx%8==0, ldx>=K)");
     if (N > INT32_MAX || K > INT32_MAX) return invalid("gemm_mfma: dimension too large");
-    if ((N + 32) * K * 2 >= (int64_t{1} << 32) || (kMaxMfmaRows + M) * ldx * 2 >= (int64_t{1} << 32))
+    if ((N + kBlockRows) * K * 2 >= (int64_t{1} << 32) || (kMaxMfmaRows + M) * ldx * 2 >= (int64_t{1} << 32))
         return invalid("gemm_mfma: W or X exceeds the 4 GiB buffer-offset range");
     if (!aligned16(x) || !aligned16(w)) return invalid("gemm_mfma: x and w must be 16-byte aligned");
     if (M == 0 || N == 0) return HAI_OK;
+    // K split across blocks for narrow layers (measured on MI355X at M = 32:
+    // N = 5120 4 splits +115 %, N = 16384 2 splits +9 %), if the workspace
+    // holds the partials and every split gets at least two chunks
+    const int64_t nck = (K + kChunk - 1) / kChunk;
+    int ksb = N <= 8192 ? 4 : (N <= 20480 ? 2 : 1);
+    while (ksb > 1 && (nck < 2 * ksb || workspace == nullptr ||
+                       workspace_bytes < static_cast<size_t>(ksb * M * N) * sizeof(float)))
+        ksb /= 2;
     const MfmaArgs a{static_cast<uint16_t*>(y), ldy, static_cast<const uint16_t*>(x), ldx,
                      static_cast<const uint16_t*>(w), static_cast<const uint16_t*>(res), ld_res,
-                     int(M), int(N), int(K)};
+                     int(M), int(N), int(K), static_cast<float*>(workspace), ksb};
     const hipStream_t s = as_stream(stream);
     switch (epilogue) {
         case HAI_EPI_STORE:
             if (ldy < N) return invalid("gemm_mfma: ldy < N");
-            dispatch_mfma<HAI_EPI_STORE>(a, s);
-            break;
+            return dispatch_mfma<HAI_EPI_STORE>(a, s);
         case HAI_EPI_RESIDUAL:
             if (res == nullptr || ldy < N || ld_res < N) return invalid("gemm_mfma: residual operands");
-            dispatch_mfma<HAI_EPI_RESIDUAL>(a, s);
-            break;
+            return dispatch_mfma<HAI_EPI_RESIDUAL>(a, s);
         case HAI_EPI_SILU_MUL:
             if (N % 2 != 0 || ldy < N / 2) return invalid("gemm_mfma: silu_mul needs even N and ldy >= N/2");
-            dispatch_mfma<HAI_EPI_SILU_MUL>(a, s);
-            break;
+            return dispatch_mfma<HAI_EPI_SILU_MUL>(a, s);
         default:
             return invalid("gemm_mfma: unknown epilogue");
     }
-    return launched("gemm_bf16_mfma_kernel");
 }

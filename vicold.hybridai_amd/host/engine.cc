@@ -313,6 +313,14 @@ int Engine::alloc_all() {
         h_prev_ = cv.take<uint16_t>(B_ * H);
         rec_hidden_ = cv.take<uint16_t>(B_ * H);
         gqa_scratch_ = cv.take<char>(hai_gqa_scratch_bytes(B_, T, d.nq, d.D, cap_));
+        if (mfma_) {
+            const int64_t mrows = std::min<int64_t>(128, R);
+            size_t ws = 0;
+            for (int64_t n : {d.Nqkv, d.H, d.Nin, d.C + d.vw, 2 * d.nv, 2 * d.F, 2 * d.kvw, d.V})
+                ws = std::max(ws, hai_gemm_mfma_workspace_bytes(mrows, n));
+            mfma_ws_bytes_ = ws;
+            mfma_ws_ = ws > 0 ? cv.take<char>(ws) : nullptr;
+        }
         argmax_scratch_ = cv.take<char>(hai_argmax_scratch_bytes(R, d.V));
         rope_cos_ = cv.take<float>(cap_ * std::max<int64_t>(1, d.R / 2));
         rope_sin_ = cv.take<float>(cap_ * std::max<int64_t>(1, d.R / 2));
@@ -404,7 +412,7 @@ int Engine::gemm(uint16_t* y, int64_t ldy, const uint16_t* x, int64_t ldx, const
         for (int64_t m0 = 0; m0 < M; m0 += 128) {
             const int64_t mm = std::min<int64_t>(128, M - m0);
             HAI_TRY(hai_gemm_bf16_mfma(y + m0 * ldy, ldy, x + m0 * ldx, ldx, w.w, mm, N, K, epi,
-                                       res ? res + m0 * ldres : nullptr, ldres, stream_));
+                                       res ? res + m0 * ldres : nullptr, ldres, mfma_ws_, mfma_ws_bytes_, stream_));
         }
         return HAI_OK;
     }

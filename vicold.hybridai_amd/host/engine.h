@@ -268,6 +268,8 @@ private:
     uint16_t* h_prev_ = nullptr;  // [B, H] target hidden feeding the next draft
     uint16_t* rec_hidden_ = nullptr;  // [B, H]
     void* gqa_scratch_ = nullptr;
+    void* mfma_ws_ = nullptr;     // K-split partials of the MFMA GEMMs
+    size_t mfma_ws_bytes_ = 0;
     void* argmax_scratch_ = nullptr;
     float* rope_cos_ = nullptr;
     float* rope_sin_ = nullptr;
