@@ -277,6 +277,52 @@ def run_decode(hai, E, args, fp8: bool, steps: int):
     return value, dt, rounds, emitted, st, prof, prefill_s
 
 
+def run_batch(hai, E, args, name: str, B: int, P: int, NEW: int, width: int, fp8: bool, rounds: int) -> dict:
+    """A batched configuration of BASELINE.json (C4 / C5): B sequences of
+    P-token synthetic prompts decoded in lockstep speculative rounds; bf16
+    launches of more than 16 rows run on the MFMA GEMM (tolerance mode)."""
+    cfg = E.QWEN27B
+    t0 = time.perf_counter()
+    cap = P + (width + 2) * NEW + 32
+    eng = E.Engine(cfg, max_context=cap, max_verify_tokens=16, fp8=fp8, batch=B, mfma=True)
+    eng.init_synthetic(seed=0, std=0.02)
+    hai.synchronize()
+    log(f"[{name}] engine up: B={B}, {eng.weight_bytes() / 1e9:.2f} GB weights, {time.perf_counter() - t0:.1f}s")
+    prompts = np.stack([E.synthetic_prompt(b, P, cfg["vocab"]) for b in range(B)])
+    t0 = time.perf_counter()
+    eng.prefill(prompts, NEW)
+    hai.synchronize()
+    prefill_s = time.perf_counter() - t0
+    log(f"[{name}] prefill of {B} x {P} tokens: {prefill_s:.2f}s ({B * P / prefill_s:.0f} tok/s)")
+    out = np.zeros((B, NEW), np.int32)
+    n0, _ = eng.spec_rounds(2, width, out)
+    hai.synchronize()
+    t0 = time.perf_counter()
+    n1, st = eng.spec_rounds(rounds, width, out)
+    hai.synchronize()
+    dt = time.perf_counter() - t0
+    emitted = n1 - n0
+    prof = eng.profile_verify(width + 1, 3)
+    eng.close()
+    gemm_gbs = prof["gemm_bytes"] / (prof["gemm_ms"] * 1e-3) / 1e9
+    step_gbs = prof["step_bytes"] / (prof["verify_ms"] * 1e-3) / 1e9
+    res = {
+        "workload": f"{name}: 27B shape, batch {B} x {P}-token prompts, MTP k={width}, "
+                    f"{'FP8 E4M3 128x128-block weights' if fp8 else 'bf16 weights'}; GEMMs of more than 16 rows "
+                    f"on MFMA (bf16) / bit-exact kernels in 16-row launches (FP8)",
+        "value": round(emitted / dt, 2), "unit": "tok/s (all sequences)", "rounds": st["rounds"],
+        "ms_per_round": round(dt / max(1, st["rounds"]) * 1e3, 3),
+        "verify_ms": round(prof["verify_ms"], 3), "verify_rows": B * (width + 1),
+        "verify_bytes": round(prof["step_bytes"]), "verify_hbm_frac": round(step_gbs / HBM_PEAK_GBS, 4),
+        "gemm_gb_s": round(gemm_gbs, 1), "gemm_launches": prof["gemm_launches"],
+        "draft_ms": round(prof["draft_ms"], 3), "prefill_s": round(prefill_s, 2),
+        "acceptance_rate": round(st["accepted"] / max(1, st["proposed"]), 4),
+    }
+    log(f"[{name}] {emitted} tokens in {dt:.2f}s -> {res['value']} tok/s; verify {prof['verify_ms']:.2f} ms "
+        f"({step_gbs:.0f} GB/s), GEMM {gemm_gbs:.0f} GB/s, draft {prof['draft_ms']:.2f} ms")
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -292,6 +338,11 @@ def main():
     ap.add_argument("--no-fp8", action="store_true",
                     help="skip the FP8-weight leg (C5 weight format at batch 1, reported under fp8_weights)")
     ap.add_argument("--fp8-steps", type=int, default=60)
+    ap.add_argument("--c4", action="store_true",
+                    help="also run C4 (batch 8 x 8192-token prompts, k=3; reported under batch_c4)")
+    ap.add_argument("--c5", action="store_true",
+                    help="also run C5 (FP8 weights, batch 32 x 512-token prompts, k=1; reported under batch_c5)")
+    ap.add_argument("--batch-rounds", type=int, default=12)
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="first run one device-to-device copy of this many bytes (the known-size reference "
                          "dispatch that scales rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -374,6 +425,10 @@ def main():
             "draft_ms": round(fprof["draft_ms"], 4),
             "acceptance_rate": round(fst["accepted"] / max(1, fst["proposed"]), 4),
         }
+    if args.c4:
+        result["batch_c4"] = run_batch(hai, E, args, "C4", 8, 8192, 128, 3, False, args.batch_rounds)
+    if args.c5:
+        result["batch_c5"] = run_batch(hai, E, args, "C5", 32, 512, 128, 1, True, args.batch_rounds)
     result["c2_ops"] = c2_ops(hai, cpu=not args.no_cpu_baseline)
     log("C2 ops: " + ", ".join(f"{k} {v['us']} us ({v['gb_s']} GB/s)" for k, v in result["c2_ops"].items()
                                if isinstance(v, dict)))

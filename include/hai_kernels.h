@@ -347,6 +347,15 @@ int hai_correction_commit_bf16(const int32_t* result, const int64_t* corr_next,
  * hai_gemm_mfma_workspace_bytes(M, N) bytes every split is available, with
  * less the call uses fewer splits.  The result does not depend on it. */
 size_t hai_gemm_mfma_workspace_bytes(int64_t M, int64_t N);
+/* The FP8 block-scaled Linear (arguments as hai_gemm_fp8_bf16, K % 16 == 0)
+ * on the matrix cores for M up to 128: codes decoded exactly to bf16, each
+ * 128-k scale block summed on its own and scaled in fp32.  Tolerance mode as
+ * hai_gemm_bf16_mfma; workspace as there. */
+int hai_gemm_fp8_mfma(void* y, int64_t ldy, const void* x, int64_t ldx,
+                      const void* wq, const float* scales,
+                      const int32_t* scale_rows, int64_t M, int64_t N,
+                      int64_t K, int epilogue, const void* res, int64_t ld_res,
+                      void* workspace, size_t workspace_bytes, void* stream);
 int hai_gemm_bf16_mfma(void* y, int64_t ldy, const void* x, int64_t ldx,
                        const void* w, int64_t M, int64_t N, int64_t K,
                        int epilogue, const void* res, int64_t ld_res,

@@ -681,3 +681,51 @@ def test_gemm_mfma_within_tolerance(M, N, K, epi, with_ws):
     assert np.allclose(got, want, rtol=2 ** -6, atol=2e-3 * scale), float(np.abs(got - want).max())
     if epi == hai.EPI_STORE:
         assert np.abs(got - exact64).max() <= 2 ** -7 * np.abs(exact64).max() + 1e-6
+
+
+@pytest.mark.parametrize("M,N,K,epi,mapped,special", [(32, 1536, 5120, 0, False, True), (64, 2 * 640, 1024, 2, False, False),
+                                                      (17, 700, 1008, 1, True, False), (128, 5120, 2048, 1, False, False),
+                                                      (48, 16400, 512, 0, True, True)])
+def test_gemm_fp8_mfma_within_tolerance(M, N, K, epi, mapped, special):
+    """hai_gemm_fp8_mfma against the canonical FP8 GEMM (dequantised weights,
+    fp32 dot): bf16 outputs within a couple of bf16 ulps; 0x7F / 0xFF codes
+    decode to +-480 as in the reference."""
+    rng = np.random.default_rng(7 * M + N + K + epi)
+    x, xb = rand_bf16(rng, (M, K))
+    if epi == hai.EPI_SILU_MUL:
+        F = N // 2
+        qg, sg = _fp8_weights(rng, F, K, special)
+        qu, su = _fp8_weights(rng, F, K)
+        q = np.empty((N, K), np.uint8)
+        q[0::2], q[1::2] = qg, qu
+        s, mp = np.stack([sg, su]), None
+        y_lin = None
+        want = orc.silu_mul(orc.gemm_fp8(x, qg, sg), orc.gemm_fp8(x, qu, su))
+        ncols = F
+    else:
+        if mapped:
+            n0 = N // 2 + 64
+            q0, s0 = _fp8_weights(rng, n0, K, special)
+            q1, s1 = _fp8_weights(rng, N - n0, K)
+            q, s = np.concatenate([q0, q1]), np.concatenate([s0, s1])
+            mp = np.array([r // 128 for r in range(n0)] + [s0.shape[0] + r // 128 for r in range(N - n0)], np.int32)
+            y_lin = np.concatenate([orc.gemm_fp8(x, q0, s0), orc.gemm_fp8(x, q1, s1)], axis=1)
+        else:
+            q, s = _fp8_weights(rng, N, K, special)
+            mp = None
+            y_lin = orc.gemm_fp8(x, q, s)
+        ncols = N
+        h, hb = rand_bf16(rng, (M, N))
+        want = y_lin if epi == hai.EPI_STORE else orc.add(h, y_lin)
+    dx, dq, ds = dev(xb), dev(q), dev(s)
+    dm = dev(mp) if mp is not None else None
+    dy = dev(hb) if epi == hai.EPI_RESIDUAL else out_buf(M * ncols * 2)
+    wsb = kern().hai_gemm_mfma_workspace_bytes(M, N)
+    dws = out_buf(max(wsb, 16))
+    flag = 0 if special else hai.FP8_NO_SPECIAL_CODES
+    hai.check(kern().hai_gemm_fp8_mfma(dy.ptr, ncols, dx.ptr, K, dq.ptr, ds.ptr, dm.ptr if dm else None, M, N, K,
+                                       epi | flag, dy.ptr if epi == hai.EPI_RESIDUAL else None, ncols, dws.ptr, wsb,
+                                       None), "gemm_fp8_mfma")
+    got = hai.bf16_to_f32(dy.download(np.uint16).reshape(M, ncols))
+    scale = np.abs(want).max()
+    assert np.allclose(got, want, rtol=2 ** -6, atol=2e-3 * scale), float(np.abs(got - want).max())

@@ -91,6 +91,8 @@ _KERNEL_SIGS = {
     "hai_copy_i64_strided": [VP, I64, VP, I64, I64, VP],
     "hai_correction_commit_bf16": [VP, VP, VP, I64, I64, VP, VP, VP, VP, VP],
     "hai_gemm_bf16_mfma": [VP, I64, VP, I64, VP, I64, I64, I64, ctypes.c_int, VP, I64, VP, ctypes.c_size_t, VP],
+    "hai_gemm_fp8_mfma": [VP, I64, VP, I64, VP, VP, VP, I64, I64, I64, ctypes.c_int, VP, I64, VP, ctypes.c_size_t,
+                          VP],
     "hai_fill_synthetic_bf16": [VP, I64, I64, I64, ctypes.c_uint64, ctypes.c_uint32, F32, VP],
     "hai_debug_math_f32": [VP, VP, I64, ctypes.c_int, VP],
 }

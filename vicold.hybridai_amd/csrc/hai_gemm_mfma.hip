@@ -190,6 +190,162 @@ __global__ void mfma_finalize_kernel(uint16_t* __restrict__ y, int64_t ldy, cons
     }
 }
 
+// E4M3 codes (4 per word) -> 4 bf16 of the same values (exact: every E4M3
+// value, the reference's +-480 included, has at most 4 significant bits);
+// CHECK handles 0x7F / 0xFF, which the hardware conversion maps to NaN.
+template <bool CHECK>
+__device__ __forceinline__ void e4m3x4_to_bf16(uint32_t w, uint32_t& lo, uint32_t& hi) {
+    typedef float f2v __attribute__((ext_vector_type(2)));
+    f2v a = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), false);
+    f2v b = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), true);
+    if (CHECK && ((((w & 0x7f7f7f7fu) + 0x01010101u) & 0x80808080u) != 0u)) {
+        // exact decode of fp8_dequant.cc:12-26 for the word holding a special code
+        float f[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t c = (w >> (8 * j)) & 0xffu;
+            const uint32_t t = c & 0x7fu;
+            float v = t >= 8u ? __uint_as_float((t << 20) + 0x3c000000u)
+                              : __uint_as_float((t << 20) + 0x3c800000u) - 0x1p-6f;
+            f[j] = (c & 0x80u) ? -v : v;
+        }
+        a = f2v{f[0], f[1]};
+        b = f2v{f[2], f[3]};
+    }
+    lo = (__float_as_uint(a.x) >> 16) | (__float_as_uint(a.y) & 0xffff0000u);
+    hi = (__float_as_uint(b.x) >> 16) | (__float_as_uint(b.y) & 0xffff0000u);
+}
+
+// FP8 weights [N, K] with 128x128 fp32 block scales (QuantizedWeight,
+// qwen3_weights.cc:131-182): each wave decodes its 16 rows' codes exactly to
+// bf16 into its LDS tile, the matrix cores sum every 128-k scale block on
+// its own, and the block's scale of the output column (weight row) is
+// applied in fp32: y = sum_kb s[sr(n)][kb] * (x . decode(q))_kb.
+template <int MT, int EPI, bool CHECK>
+__global__ __launch_bounds__(256) void gemm_fp8_mfma_kernel(uint16_t* __restrict__ y, int64_t ldy,
+                                                            const uint16_t* __restrict__ x, int64_t ldx,
+                                                            const uint8_t* __restrict__ wq,
+                                                            const float* __restrict__ scales,
+                                                            const int32_t* __restrict__ scale_rows, int paired,
+                                                            const uint16_t* res, int64_t ldres, int M, int N, int K,
+                                                            float* __restrict__ part, int KSB) {
+    extern __shared__ __align__(16) uint16_t lds[];
+    uint16_t* xs = lds;                          // [16 MT][kLdsRow]
+    uint16_t* ws = lds + 16 * MT * kLdsRow;      // [4 waves][16][kLdsRow], decoded bf16
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = wave_index();
+    const int li = lane & 15;
+    const int kg = lane >> 4;
+    const int64_t row_base = static_cast<int64_t>(blockIdx.x) * kBlockRows + wave * 16;
+    const int nkb = (K + 127) / 128;
+
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(wq, static_cast<uint32_t>(static_cast<int64_t>(N) * K));
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, static_cast<uint32_t>(static_cast<int64_t>(M) * ldx * 2));
+    // code loads: instruction i covers rows 4i .. 4i+3, 16 lanes x 16 codes each
+    const int w_quarter = lane >> 4;
+    const int w_col = (lane & 15) * 16;
+    const uint32_t woff0 = static_cast<uint32_t>((row_base + w_quarter) * static_cast<int64_t>(K) + w_col);
+    const uint32_t four_rows = static_cast<uint32_t>(K) * 4u;
+    constexpr int XL = 2 * MT;
+    uint32_t xoff[XL];
+    int xrow[XL], xcol[XL];
+#pragma unroll
+    for (int i = 0; i < XL; ++i) {
+        const int e = tid + 256 * i;
+        xrow[i] = e >> 5;
+        xcol[i] = (e & 31) * 8;
+        xoff[i] = static_cast<uint32_t>((static_cast<int64_t>(xrow[i]) * ldx + xcol[i]) * 2);
+    }
+    // scale row of this lane's output column (weight row row_base + li)
+    const int64_t ncol = min(row_base + li, static_cast<int64_t>(N) - 1);
+    const int64_t nsb = ((N >> 1) + 127) / 128;
+    const int64_t srow = scale_rows ? scale_rows[ncol] : (paired ? (ncol & 1) * nsb + (ncol >> 1) / 128 : ncol / 128);
+    const float* srp = scales + srow * nkb;
+
+    f32x4 tot[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) tot[mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    const int nck = (K + kChunk - 1) / kChunk;
+    const int nfull = K / kChunk;
+    const int split = blockIdx.y;
+    u32x4 wv[4], xv[XL];
+    float sv[2];
+    auto load = [&](int c) {
+        if (c < nfull) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) wv[i] = bload_w(rw, woff0 + i * four_rows, static_cast<uint32_t>(c) * kChunk);
+#pragma unroll
+            for (int i = 0; i < XL; ++i) xv[i] = bload(rx, xoff[i], static_cast<uint32_t>(c) * (kChunk * 2));
+        } else {
+            const bool okw = c * kChunk + w_col < K;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                wv[i] = bload_w(rw, okw ? woff0 + i * four_rows + static_cast<uint32_t>(c) * kChunk : kOutOfRange, 0u);
+#pragma unroll
+            for (int i = 0; i < XL; ++i)
+                xv[i] = bload(rx, c * kChunk + xcol[i] < K ? xoff[i] + static_cast<uint32_t>(c) * (kChunk * 2)
+                                                           : kOutOfRange, 0u);
+        }
+        // k-blocks 2c and 2c + 1 (a past-K block gets a finite stand-in; its
+        // products are zero)
+        sv[0] = srp[min(2 * c, nkb - 1)];
+        sv[1] = srp[min(2 * c + 1, nkb - 1)];
+    };
+    int c = split;
+    if (c < nck) load(c);
+    for (; c < nck; c += KSB) {
+        __syncthreads();  // the previous chunk's LDS reads are done
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            uint32_t d[8];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) e4m3x4_to_bf16<CHECK>(wv[i][q], d[2 * q], d[2 * q + 1]);
+            uint16_t* dst = &ws[(wave * 16 + 4 * i + w_quarter) * kLdsRow + w_col];
+            *reinterpret_cast<u32x4*>(dst) = u32x4{d[0], d[1], d[2], d[3]};
+            *reinterpret_cast<u32x4*>(dst + 8) = u32x4{d[4], d[5], d[6], d[7]};
+        }
+#pragma unroll
+        for (int i = 0; i < XL; ++i) *reinterpret_cast<u32x4*>(&xs[xrow[i] * kLdsRow + xcol[i]]) = xv[i];
+        const float s0 = sv[0], s1 = sv[1];
+        __syncthreads();
+        if (c + KSB < nck) load(c + KSB);
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            f32x4 acc[MT];
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int j = 4 * kb; j < 4 * kb + 4; ++j) {
+                const u32x4 b = *reinterpret_cast<const u32x4*>(&ws[(wave * 16 + li) * kLdsRow + 32 * j + 8 * kg]);
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    const u32x4 a = *reinterpret_cast<const u32x4*>(&xs[(16 * mt + li) * kLdsRow + 32 * j + 8 * kg]);
+                    acc[mt] = mfma16(a, b, acc[mt]);
+                }
+            }
+            const float sc = kb == 0 ? s0 : s1;
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) tot[mt][i] = fma_(sc, acc[mt][i], tot[mt][i]);
+        }
+    }
+
+    const int64_t n = row_base + li;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int m = 16 * mt + 4 * kg + i;
+            if (KSB == 1)
+                mfma_store<EPI>(y, ldy, res, ldres, tot[mt][i], m, n, M, N, li);
+            else if (m < M && n < N)
+                part[(static_cast<int64_t>(split) * M + m) * N + n] = tot[mt][i];
+        }
+}
+
 struct MfmaArgs {
     uint16_t* y;
     int64_t ldy;
@@ -201,24 +357,46 @@ struct MfmaArgs {
     int M, N, K;
     float* part;
     int KSB;
+    // FP8 weights (wq != nullptr)
+    const uint8_t* wq = nullptr;
+    const float* scales = nullptr;
+    const int32_t* scale_rows = nullptr;
+    int paired = 0;
+    bool check = true;
 };
+
+// LDS above the 64 KB default needs the attribute, once per kernel instance.
+int allow_lds(const void* kern, size_t shmem, bool* done) {
+    if (*done) return HAI_OK;
+    const int rc = check_hip(hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 static_cast<int>(shmem)),
+                             "hipFuncSetAttribute");
+    if (rc == HAI_OK) *done = true;
+    return rc;
+}
 
 template <int MT, int EPI>
 int launch_mfma(const MfmaArgs& a, hipStream_t s) {
-    auto* kern = gemm_bf16_mfma_kernel<MT, EPI>;
     const size_t shmem = static_cast<size_t>(16 * MT + 4 * 16) * kLdsRow * 2;
-    static bool attr = false;  // LDS above the 64 KB default needs the attribute once per instance
-    if (!attr) {
-        const int rc = check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                                     hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                     static_cast<int>(shmem)),
-                                 "hipFuncSetAttribute");
-        if (rc != HAI_OK) return rc;
-        attr = true;
-    }
     const dim3 grid(static_cast<unsigned>((a.N + kBlockRows - 1) / kBlockRows), static_cast<unsigned>(a.KSB));
-    kern<<<grid, dim3(256), shmem, s>>>(a.y, a.ldy, a.x, a.ldx, a.w, a.res, a.ldres, a.M, a.N, a.K, a.part, a.KSB);
-    int rc = launched("gemm_bf16_mfma_kernel");
+    int rc;
+    if (a.wq != nullptr) {
+        auto* kern = a.check ? gemm_fp8_mfma_kernel<MT, EPI, true> : gemm_fp8_mfma_kernel<MT, EPI, false>;
+        static bool attr[2] = {false, false};
+        rc = allow_lds(reinterpret_cast<const void*>(kern), shmem, &attr[a.check ? 1 : 0]);
+        if (rc != HAI_OK) return rc;
+        kern<<<grid, dim3(256), shmem, s>>>(a.y, a.ldy, a.x, a.ldx, a.wq, a.scales, a.scale_rows, a.paired, a.res,
+                                            a.ldres, a.M, a.N, a.K, a.part, a.KSB);
+        rc = launched("gemm_fp8_mfma_kernel");
+    } else {
+        auto* kern = gemm_bf16_mfma_kernel<MT, EPI>;
+        static bool attr = false;
+        rc = allow_lds(reinterpret_cast<const void*>(kern), shmem, &attr);
+        if (rc != HAI_OK) return rc;
+        kern<<<grid, dim3(256), shmem, s>>>(a.y, a.ldy, a.x, a.ldx, a.w, a.res, a.ldres, a.M, a.N, a.K, a.part,
+                                            a.KSB);
+        rc = launched("gemm_bf16_mfma_kernel");
+    }
     if (rc != HAI_OK || a.KSB == 1) return rc;
     const int64_t n = static_cast<int64_t>(a.M) * ((a.N + 1) / 2);
     mfma_finalize_kernel<EPI><<<dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s>>>(
@@ -241,40 +419,74 @@ extern "C" size_t hai_gemm_mfma_workspace_bytes(int64_t M, int64_t N) {
     return ksb > 1 ? static_cast<size_t>(ksb * M * N) * sizeof(float) : 0;
 }
 
-extern "C" int hai_gemm_bf16_mfma(void* y, int64_t ldy, const void* x, int64_t ldx, const void* w, int64_t M,
-                                  int64_t N, int64_t K, int epilogue, const void* res, int64_t ld_res,
-                                  void* workspace, size_t workspace_bytes, void* stream) {
-    if (y == nullptr || x == nullptr || w == nullptr) return invalid("gemm_mfma: null pointer");
-    if (M < 0 || M > kMaxMfmaRows || N < 0 || K <= 0 || K % 8 != 0 || ldx % 8 != 0 || ldx < K)
-        return invalid("gemm_mfma: shape (need 0<=M<=128, K%8==0, ldx%8==0, ldx>=K)");
-    if (N > INT32_MAX || K > INT32_MAX) return invalid("gemm_mfma: dimension too large");
-    if ((N + kBlockRows) * K * 2 >= (int64_t{1} << 32) || (kMaxMfmaRows + M) * ldx * 2 >= (int64_t{1} << 32))
-        return invalid("gemm_mfma: W or X exceeds the 4 GiB buffer-offset range");
-    if (!aligned16(x) || !aligned16(w)) return invalid("gemm_mfma: x and w must be 16-byte aligned");
-    if (M == 0 || N == 0) return HAI_OK;
+namespace {
+
+int mfma_entry(MfmaArgs& a, int epilogue, void* workspace, size_t workspace_bytes, hipStream_t s) {
+    if (a.M == 0 || a.N == 0) return HAI_OK;
     // K split across blocks for narrow layers (measured on MI355X at M = 32:
     // N = 5120 4 splits +115 %, N = 16384 2 splits +9 %), if the workspace
     // holds the partials and every split gets at least two chunks
-    const int64_t nck = (K + kChunk - 1) / kChunk;
-    int ksb = N <= 8192 ? 4 : (N <= 20480 ? 2 : 1);
+    const int64_t nck = (a.K + kChunk - 1) / kChunk;
+    int ksb = a.N <= 8192 ? 4 : (a.N <= 20480 ? 2 : 1);
     while (ksb > 1 && (nck < 2 * ksb || workspace == nullptr ||
-                       workspace_bytes < static_cast<size_t>(ksb * M * N) * sizeof(float)))
+                       workspace_bytes < static_cast<size_t>(int64_t{ksb} * a.M * a.N) * sizeof(float)))
         ksb /= 2;
-    const MfmaArgs a{static_cast<uint16_t*>(y), ldy, static_cast<const uint16_t*>(x), ldx,
-                     static_cast<const uint16_t*>(w), static_cast<const uint16_t*>(res), ld_res,
-                     int(M), int(N), int(K), static_cast<float*>(workspace), ksb};
-    const hipStream_t s = as_stream(stream);
+    a.part = static_cast<float*>(workspace);
+    a.KSB = ksb;
     switch (epilogue) {
         case HAI_EPI_STORE:
-            if (ldy < N) return invalid("gemm_mfma: ldy < N");
+            if (a.ldy < a.N) return invalid("gemm_mfma: ldy < N");
             return dispatch_mfma<HAI_EPI_STORE>(a, s);
         case HAI_EPI_RESIDUAL:
-            if (res == nullptr || ldy < N || ld_res < N) return invalid("gemm_mfma: residual operands");
+            if (a.res == nullptr || a.ldy < a.N || a.ldres < a.N) return invalid("gemm_mfma: residual operands");
             return dispatch_mfma<HAI_EPI_RESIDUAL>(a, s);
         case HAI_EPI_SILU_MUL:
-            if (N % 2 != 0 || ldy < N / 2) return invalid("gemm_mfma: silu_mul needs even N and ldy >= N/2");
+            if (a.N % 2 != 0 || a.ldy < a.N / 2) return invalid("gemm_mfma: silu_mul needs even N and ldy >= N/2");
+            a.paired = a.wq != nullptr ? 1 : 0;
             return dispatch_mfma<HAI_EPI_SILU_MUL>(a, s);
         default:
             return invalid("gemm_mfma: unknown epilogue");
     }
+}
+
+int check_mfma(const void* y, const void* x, const void* w, int64_t M, int64_t N, int64_t K, int64_t ldx,
+               int elem_bytes) {
+    if (y == nullptr || x == nullptr || w == nullptr) return invalid("gemm_mfma: null pointer");
+    if (M < 0 || M > kMaxMfmaRows || N < 0 || K <= 0 || K % 8 != 0 || ldx % 8 != 0 || ldx < K)
+        return invalid("gemm_mfma: shape (need 0<=M<=128, K%8==0, ldx%8==0, ldx>=K)");
+    if (N > INT32_MAX || K > INT32_MAX) return invalid("gemm_mfma: dimension too large");
+    if ((N + kBlockRows) * K * elem_bytes >= (int64_t{1} << 32) || (kMaxMfmaRows + M) * ldx * 2 >= (int64_t{1} << 32))
+        return invalid("gemm_mfma: W or X exceeds the 4 GiB buffer-offset range");
+    if (!aligned16(x) || !aligned16(w)) return invalid("gemm_mfma: x and w must be 16-byte aligned");
+    return HAI_OK;
+}
+
+}  // namespace
+
+extern "C" int hai_gemm_bf16_mfma(void* y, int64_t ldy, const void* x, int64_t ldx, const void* w, int64_t M,
+                                  int64_t N, int64_t K, int epilogue, const void* res, int64_t ld_res,
+                                  void* workspace, size_t workspace_bytes, void* stream) {
+    const int rc = check_mfma(y, x, w, M, N, K, ldx, 2);
+    if (rc != HAI_OK) return rc;
+    MfmaArgs a{static_cast<uint16_t*>(y), ldy, static_cast<const uint16_t*>(x), ldx,
+               static_cast<const uint16_t*>(w), static_cast<const uint16_t*>(res), ld_res,
+               int(M), int(N), int(K), nullptr, 1};
+    return mfma_entry(a, epilogue, workspace, workspace_bytes, as_stream(stream));
+}
+
+extern "C" int hai_gemm_fp8_mfma(void* y, int64_t ldy, const void* x, int64_t ldx, const void* wq,
+                                 const float* scales, const int32_t* scale_rows, int64_t M, int64_t N, int64_t K,
+                                 int epilogue, const void* res, int64_t ld_res, void* workspace,
+                                 size_t workspace_bytes, void* stream) {
+    if (scales == nullptr) return invalid("gemm_fp8_mfma: null scales");
+    const int rc = check_mfma(y, x, wq, M, N, K, ldx, 1);
+    if (rc != HAI_OK) return rc;
+    if (K % 16 != 0) return invalid("gemm_fp8_mfma: K % 16 != 0");
+    MfmaArgs a{static_cast<uint16_t*>(y), ldy, static_cast<const uint16_t*>(x), ldx, nullptr,
+               static_cast<const uint16_t*>(res), ld_res, int(M), int(N), int(K), nullptr, 1};
+    a.wq = static_cast<const uint8_t*>(wq);
+    a.scales = scales;
+    a.scale_rows = scale_rows;
+    a.check = (epilogue & HAI_FP8_NO_SPECIAL_CODES) == 0;
+    return mfma_entry(a, epilogue & ~HAI_FP8_NO_SPECIAL_CODES, workspace, workspace_bytes, as_stream(stream));
 }

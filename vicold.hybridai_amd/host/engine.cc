@@ -408,11 +408,17 @@ int64_t Engine::read_tensor(uint32_t id, uint16_t* out, int64_t capacity) {
 int Engine::gemm(uint16_t* y, int64_t ldy, const uint16_t* x, int64_t ldx, const Lin& w, int64_t M, int64_t N,
                  int64_t K, int epi, const uint16_t* res, int64_t ldres) {
     if (prof_record_) prof_calls_.push_back({y, ldy, x, ldx, w, M, N, K, epi, res, ldres, nullptr, nullptr});
-    if (mfma_ && w.q == nullptr && M > 16) {
+    if (mfma_ && M > 16) {
         for (int64_t m0 = 0; m0 < M; m0 += 128) {
             const int64_t mm = std::min<int64_t>(128, M - m0);
-            HAI_TRY(hai_gemm_bf16_mfma(y + m0 * ldy, ldy, x + m0 * ldx, ldx, w.w, mm, N, K, epi,
-                                       res ? res + m0 * ldres : nullptr, ldres, mfma_ws_, mfma_ws_bytes_, stream_));
+            const uint16_t* rm = res ? res + m0 * ldres : nullptr;
+            if (w.q != nullptr)
+                HAI_TRY(hai_gemm_fp8_mfma(y + m0 * ldy, ldy, x + m0 * ldx, ldx, w.q, w.s, w.map, mm, N, K,
+                                          epi | HAI_FP8_NO_SPECIAL_CODES, rm, ldres, mfma_ws_, mfma_ws_bytes_,
+                                          stream_));
+            else
+                HAI_TRY(hai_gemm_bf16_mfma(y + m0 * ldy, ldy, x + m0 * ldx, ldx, w.w, mm, N, K, epi, rm, ldres,
+                                           mfma_ws_, mfma_ws_bytes_, stream_));
         }
         return HAI_OK;
     }
@@ -1051,8 +1057,8 @@ int Engine::profile_verify(int64_t T, int64_t iters, hai_verify_profile* out) {
     // several launches on the bit-exact kernels
     double launches = 0.0;
     for (const auto& c : prof_calls_)
-        launches += (mfma_ && c.w.q == nullptr && c.M > 16) ? static_cast<double>((c.M + 127) / 128)
-                                                            : static_cast<double>((c.M + 15) / 16);
+        launches += (mfma_ && c.M > 16) ? static_cast<double>((c.M + 127) / 128)
+                                        : static_cast<double>((c.M + 15) / 16);
     // Draft step timing (one MTP forward + lm_head + argmax per sequence)
     // without events inside, on scratch MTP lengths.
     for (int64_t it = 0; it < iters + 1; ++it) {
