@@ -343,6 +343,8 @@ def main():
     ap.add_argument("--no-c5", action="store_true",
                     help="skip C5 (FP8 weights, batch 32 x 512-token prompts, k=1; reported under batch_c5)")
     ap.add_argument("--batch-rounds", type=int, default=12)
+    ap.add_argument("--c4-prompt", type=int, default=8192,
+                    help="C4 prompt length (8192 is the configuration; shorter only for counter passes)")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="first run one device-to-device copy of this many bytes (the known-size reference "
                          "dispatch that scales rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -427,7 +429,7 @@ def main():
         }
     # The batched configurations are extra fields; an error there (raised by
     # the engine, not a device fault) is recorded without losing the line.
-    for flag, key, run in ((args.no_c4, "batch_c4", ("C4", 8, 8192, 128, 3, False)),
+    for flag, key, run in ((args.no_c4, "batch_c4", ("C4", 8, args.c4_prompt, 128, 3, False)),
                            (args.no_c5, "batch_c5", ("C5", 32, 512, 128, 1, True))):
         if flag:
             continue

@@ -729,3 +729,28 @@ def test_gemm_fp8_mfma_within_tolerance(M, N, K, epi, mapped, special):
     got = hai.bf16_to_f32(dy.download(np.uint16).reshape(M, ncols))
     scale = np.abs(want).max()
     assert np.allclose(got, want, rtol=2 ** -6, atol=2e-3 * scale), float(np.abs(got - want).max())
+
+
+@pytest.mark.parametrize("M,N,K,epi", [(32, 34816, 5120, 2), (32, 5120, 17408, 1), (64, 16480, 5120, 0)])
+def test_gemm_mfma_27b_shapes(M, N, K, epi):
+    """The batched-verify GEMMs at their C4 (M = 8 sequences x 4 rows) and C5
+    (M = 32 x 2) shapes: gate/up with SwiGLU, down with the residual add,
+    DeltaNet in_proj; within tolerance of the canonical oracle GEMM."""
+    rng = np.random.default_rng(N + K)
+    x, xb = rand_bf16(rng, (M, K))
+    w, wb = rand_bf16(rng, (N, K), 0.02)
+    ncols = N // 2 if epi == hai.EPI_SILU_MUL else N
+    h, hb = rand_bf16(rng, (M, ncols))
+    dx, dw = dev(xb), dev(wb)
+    dy = dev(hb) if epi == hai.EPI_RESIDUAL else out_buf(M * ncols * 2)
+    wsb = kern().hai_gemm_mfma_workspace_bytes(M, N)
+    dws = out_buf(max(wsb, 16))
+    hai.check(kern().hai_gemm_bf16_mfma(dy.ptr, ncols, dx.ptr, K, dw.ptr, M, N, K, epi,
+                                        dy.ptr if epi == hai.EPI_RESIDUAL else None, ncols, dws.ptr, wsb, None),
+              "gemm_mfma 27b")
+    y = orc.gemm(x, w)
+    want = {hai.EPI_STORE: lambda: y, hai.EPI_RESIDUAL: lambda: orc.add(h, y),
+            hai.EPI_SILU_MUL: lambda: orc.silu_mul(y[:, 0::2], y[:, 1::2])}[epi]()
+    got = hai.bf16_to_f32(dy.download(np.uint16).reshape(M, ncols))
+    scale = np.abs(want).max()
+    assert np.allclose(got, want, rtol=2 ** -6, atol=2e-3 * scale), float(np.abs(got - want).max())
