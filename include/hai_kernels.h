@@ -342,7 +342,8 @@ int hai_correction_commit_bf16(const int32_t* result, const int64_t* corr_next,
  * hai_gemm_bf16 but computed with v_mfma_f32_16x16x32_bf16: equal to the
  * canonical result within fp32 accumulation error (~1e-6 relative before
  * the bf16 output rounding), not bit for bit.  Replaces rocblas_gemm_ex
- * (hip_backend.cc:697-809) for M > 16.  x and w 16-byte aligned, K % 8 == 0.
+ * (hip_backend.cc:697-809) for batched rows.  x and w 16-byte aligned,
+ * K % 8 == 0, M <= 128.
  * workspace (may be NULL) lets narrow layers split K across blocks; with
  * hai_gemm_mfma_workspace_bytes(M, N) bytes every split is available, with
  * less the call uses fewer splits.  The result does not depend on it. */

@@ -2,7 +2,7 @@
 oracle's single-sequence restatement of the reference state machine: on the
 bit-exact GEMMs every sequence's tokens, round records and counters equal its
 own single-sequence decode; with the MFMA GEMMs (tolerance mode, launches of
-more than 16 rows) the batch's logits stay within the 2e-2 abs / 1e-2 rel
+4 or more rows) the batch's logits stay within the 2e-2 abs / 1e-2 rel
 bound of the oracle's."""
 import numpy as np
 import pytest

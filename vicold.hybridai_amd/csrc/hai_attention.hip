@@ -4,12 +4,15 @@
 //
 // The reference walks every key serially in one wave per (head, query).
 // Here the keys are split into fixed 64-key chunks by absolute index:
-//   pass 1 (one block per chunk x group of four queries of one KV head x
+//   pass 1 (one block per chunk x group of queries of one KV head x
 //     sequence): the chunk's K and V tiles are staged in LDS with all loads
-//     in flight at once; each wave takes one query: lane = key computes the
-//     score with a sequential fma over D, the chunk max and the exp-sum are
-//     wave reductions, and P.V is a sequential fma over the chunk's keys with
-//     lane = pair of output dims;
+//     in flight at once; the waves take the group's queries in turn: lane =
+//     key computes the score with a sequential fma over D, the chunk max and
+//     the exp-sum are wave reductions, and P.V is a sequential fma over the
+//     chunk's keys with lane = pair of output dims.  The group is every query
+//     of the KV head (all T x nq/nkv of them: K and V are read once) when the
+//     chunks alone give the grid enough blocks (long caches, batches), else
+//     four queries per block;
 //   pass 2 (one wave per query): chunk partials are merged against the
 //     global max in chunk order (loads batched eight chunks deep), then
 //     divided, gated and stored.
@@ -24,26 +27,29 @@ namespace {
 using namespace hai;
 
 constexpr int kChunk = 64;
-constexpr int kQPerBlock = 4;  // one query per wave
+constexpr int kWaves = 4;
+// grid size above which a block serves every query of its KV head
+constexpr int64_t kFullGroupBlocks = 2048;
 
 __host__ __device__ constexpr int64_t partial_stride(int D) { return D + 2; }
 
 // grid (chunk, query group x KV head, sequence): the block stages one 64-key
-// chunk of one KV head and serves up to four of that head's queries.
+// chunk of one KV head and serves qpb of that head's queries (qpb % 4 == 0).
 template <int D>
 __global__ __launch_bounds__(256) void gqa_partial_kernel(
     float* __restrict__ scratch, const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, int64_t cap, int T, int nq, int nkv, const int32_t* lens,
-    int len_add, int nchunk, float scale) {
+    int len_add, int nchunk, float scale, int qpb) {
     constexpr int KP = D / 2 + 4;          // dword stride of a staged K row (16-byte pad)
     constexpr int VP = D / 2;              // dword stride of a staged V row
     constexpr int ROW16 = D / 8;           // 16-byte pieces per row
     constexpr int NLD = kChunk * ROW16 / 256;  // pieces per thread and tile
+    constexpr int QPL = D / 64;            // query elements per lane
     static_assert(NLD >= 1 && kChunk * ROW16 % 256 == 0, "tile must split over 256 threads");
     __shared__ uint32_t Ks[kChunk * KP];
     __shared__ uint32_t Vs[kChunk * VP];
-    __shared__ float Qs[kQPerBlock][D];
-    __shared__ float Ps[kQPerBlock][kChunk];
+    __shared__ float Qs[kWaves][D];
+    __shared__ float Ps[kWaves][kChunk];
 
     const int chunk = blockIdx.x;
     const int kvh = blockIdx.y % nkv;
@@ -56,8 +62,22 @@ __global__ __launch_bounds__(256) void gqa_partial_kernel(
     const int64_t key0 = static_cast<int64_t>(chunk) * kChunk;
     const int group = nq / nkv;
     const int nqry = T * group;
-    if (key0 >= L || qgrp * kQPerBlock >= nqry) return;
+    const int q_begin = qgrp * qpb;
+    const int q_end = min(nqry, q_begin + qpb);
+    if (key0 >= L || q_begin >= nqry) return;
     const int nkeys = static_cast<int>(min(static_cast<int64_t>(kChunk), L - key0));
+
+    // query qi of this KV head: token qi / group, head kvh * group + qi % group
+    auto q_row = [&](int qi) {
+        return q + ((static_cast<int64_t>(b) * T + qi / group) * nq + kvh * group + qi % group) * D;
+    };
+    // The wave's first query is loaded alongside the K / V tiles.
+    uint16_t qv[QPL];
+    if (q_begin + wave < q_end) {
+        const uint16_t* qrow = q_row(q_begin + wave);
+#pragma unroll
+        for (int r = 0; r < QPL; ++r) qv[r] = qrow[lane + 64 * r];
+    }
 
     // Stage the chunk's K and V rows: every load is issued before the first
     // LDS store; rows past the cache length read as zeros (buffer range).
@@ -84,72 +104,79 @@ __global__ __launch_bounds__(256) void gqa_partial_kernel(
             *reinterpret_cast<u32x4*>(Vs + j * VP + p) = vd[i];
         }
     }
-    // This wave's query.
-    const int qi = qgrp * kQPerBlock + wave;
-    const bool has_q = qi < nqry;
-    const int t = has_q ? qi / group : 0;
-    const int h = kvh * group + (has_q ? qi % group : 0);
-    const int64_t qpos = L - T + t;
-    if (has_q) {
-        const uint16_t* qrow = q + ((static_cast<int64_t>(b) * T + t) * nq + h) * D;
-#pragma unroll
-        for (int d = lane; d < D; d += 64) Qs[wave][d] = bf2f(qrow[d]);
-    }
     __syncthreads();
-    if (!has_q) return;
 
-    // Scores: lane = key, sequential fma over D.
-    const int64_t kj = key0 + lane;
-    const bool valid = lane < nkeys && kj <= qpos;
-    float s = 0.0f;
-    {
-        const uint32_t* kr = Ks + lane * KP;
-        const float* qr = Qs[wave];
-#pragma unroll 4
-        for (int p = 0; p < D / 2; p += 4) {
-            const u32x4 kk = *reinterpret_cast<const u32x4*>(kr + p);
-            const float4 qa = *reinterpret_cast<const float4*>(qr + 2 * p);
-            const float4 qb = *reinterpret_cast<const float4*>(qr + 2 * p + 4);
-            s = fma_(qa.x, lo_bf(kk[0]), s);
-            s = fma_(qa.y, hi_bf(kk[0]), s);
-            s = fma_(qa.z, lo_bf(kk[1]), s);
-            s = fma_(qa.w, hi_bf(kk[1]), s);
-            s = fma_(qb.x, lo_bf(kk[2]), s);
-            s = fma_(qb.y, hi_bf(kk[2]), s);
-            s = fma_(qb.z, lo_bf(kk[3]), s);
-            s = fma_(qb.w, hi_bf(kk[3]), s);
-        }
-        s = s * scale;
-    }
-    const float m = wave_max64(valid ? s : __uint_as_float(0xff800000u));
-    const float pr = valid ? cexp(s - m) : 0.0f;
-    const float l = wave_sum64(pr);
-    Ps[wave][lane] = pr;
-    float* part = scratch + ((((static_cast<int64_t>(b) * T + t) * nq + h) * nchunk) + chunk) * partial_stride(D);
-    if (lane == 0) {
-        part[0] = m;
-        part[1] = l;
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-    // P.V: lane owns value pairs (2i, 2i+1), i = lane + 64r; sequential over keys.
-    const int64_t lim = qpos - key0 + 1;
-    const int nj = static_cast<int>(lim < nkeys ? (lim < 0 ? 0 : lim) : nkeys);
-    constexpr int NPAIR = (D / 2 + 63) / 64;
+    auto wave_sync = [] {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+    for (int qi = q_begin + wave; qi < q_end; qi += kWaves) {
+        const int t = qi / group;
+        const int h = kvh * group + qi % group;
+        const int64_t qpos = L - T + t;
 #pragma unroll
-    for (int r = 0; r < NPAIR; ++r) {
-        const int pi = lane + 64 * r;
-        if (pi >= D / 2) break;
-        float o0 = 0.0f, o1 = 0.0f;
-        for (int j = 0; j < nj; ++j) {
-            const float pj = Ps[wave][j];
-            const uint32_t vv = Vs[j * VP + pi];
-            o0 = fma_(pj, lo_bf(vv), o0);
-            o1 = fma_(pj, hi_bf(vv), o1);
+        for (int r = 0; r < QPL; ++r) Qs[wave][lane + 64 * r] = bf2f(qv[r]);
+        // the wave's next query is in flight while this one is computed
+        if (qi + kWaves < q_end) {
+            const uint16_t* qrow = q_row(qi + kWaves);
+#pragma unroll
+            for (int r = 0; r < QPL; ++r) qv[r] = qrow[lane + 64 * r];
         }
-        *reinterpret_cast<float2*>(part + 2 + 2 * pi) = make_float2(o0, o1);
+        wave_sync();
+
+        // Scores: lane = key, sequential fma over D.
+        const int64_t kj = key0 + lane;
+        const bool valid = lane < nkeys && kj <= qpos;
+        float s = 0.0f;
+        {
+            const uint32_t* kr = Ks + lane * KP;
+            const float* qr = Qs[wave];
+#pragma unroll 4
+            for (int p = 0; p < D / 2; p += 4) {
+                const u32x4 kk = *reinterpret_cast<const u32x4*>(kr + p);
+                const float4 qa = *reinterpret_cast<const float4*>(qr + 2 * p);
+                const float4 qb = *reinterpret_cast<const float4*>(qr + 2 * p + 4);
+                s = fma_(qa.x, lo_bf(kk[0]), s);
+                s = fma_(qa.y, hi_bf(kk[0]), s);
+                s = fma_(qa.z, lo_bf(kk[1]), s);
+                s = fma_(qa.w, hi_bf(kk[1]), s);
+                s = fma_(qb.x, lo_bf(kk[2]), s);
+                s = fma_(qb.y, hi_bf(kk[2]), s);
+                s = fma_(qb.z, lo_bf(kk[3]), s);
+                s = fma_(qb.w, hi_bf(kk[3]), s);
+            }
+            s = s * scale;
+        }
+        const float m = wave_max64(valid ? s : __uint_as_float(0xff800000u));
+        const float pr = valid ? cexp(s - m) : 0.0f;
+        const float l = wave_sum64(pr);
+        Ps[wave][lane] = pr;
+        float* part = scratch + ((((static_cast<int64_t>(b) * T + t) * nq + h) * nchunk) + chunk) * partial_stride(D);
+        if (lane == 0) {
+            part[0] = m;
+            part[1] = l;
+        }
+        wave_sync();
+
+        // P.V: lane owns value pairs (2i, 2i+1), i = lane + 64r; sequential over keys.
+        const int64_t lim = qpos - key0 + 1;
+        const int nj = static_cast<int>(lim < nkeys ? (lim < 0 ? 0 : lim) : nkeys);
+        constexpr int NPAIR = (D / 2 + 63) / 64;
+#pragma unroll
+        for (int r = 0; r < NPAIR; ++r) {
+            const int pi = lane + 64 * r;
+            if (pi >= D / 2) break;
+            float o0 = 0.0f, o1 = 0.0f;
+            for (int j = 0; j < nj; ++j) {
+                const float pj = Ps[wave][j];
+                const uint32_t vv = Vs[j * VP + pi];
+                o0 = fma_(pj, lo_bf(vv), o0);
+                o1 = fma_(pj, hi_bf(vv), o1);
+            }
+            *reinterpret_cast<float2*>(part + 2 + 2 * pi) = make_float2(o0, o1);
+        }
+        wave_sync();  // Qs / Ps are rewritten by the next query
     }
 }
 
@@ -221,13 +248,21 @@ int launch(uint16_t* out, const uint16_t* q, const uint16_t* gate, const uint16_
            int64_t cap, float* scratch, int B, int T, int nq, int nkv, const int32_t* lens, int len_add,
            int nchunk, hipStream_t s) {
     const float scale = 1.0f / __builtin_sqrtf(static_cast<float>(D));
-    const int qgroups = (T * (nq / nkv) + kQPerBlock - 1) / kQPerBlock;
+    // Queries per block: all of the KV head's when the chunks alone fill the
+    // GPU (K / V read once), else the fewest multiple of four that does.
+    const int nqry = T * (nq / nkv);
+    const int64_t base = static_cast<int64_t>(nchunk) * nkv * B;
+    const int64_t max_groups = (nqry + kWaves - 1) / kWaves;
+    const int64_t want = base >= kFullGroupBlocks ? 1 : (kFullGroupBlocks + base - 1) / base;
+    const int64_t groups = want < max_groups ? want : max_groups;
+    const int qpb = static_cast<int>(kWaves * ((max_groups + groups - 1) / groups));
+    const int qgroups = (nqry + qpb - 1) / qpb;
     gqa_partial_kernel<D><<<dim3(nchunk, nkv * qgroups, B), dim3(256), 0, s>>>(
-        scratch, q, kc, vc, cap, T, nq, nkv, lens, len_add, nchunk, scale);
+        scratch, q, kc, vc, cap, T, nq, nkv, lens, len_add, nchunk, scale, qpb);
     int rc = launched("gqa_partial_kernel");
     if (rc != HAI_OK) return rc;
-    const int64_t nqry = static_cast<int64_t>(B) * T * nq;
-    gqa_combine_kernel<D><<<dim3(static_cast<unsigned>((nqry + 3) / 4)), dim3(256), 0, s>>>(
+    const int64_t nall = static_cast<int64_t>(B) * T * nq;
+    gqa_combine_kernel<D><<<dim3(static_cast<unsigned>((nall + 3) / 4)), dim3(256), 0, s>>>(
         out, scratch, gate, B, T, nq, lens, len_add, nchunk);
     return launched("gqa_combine_kernel");
 }

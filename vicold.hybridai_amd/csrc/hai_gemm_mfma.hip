@@ -1,8 +1,8 @@
 // hai_gemm_mfma.hip -- batched-verify linear layer on the gfx950 matrix cores:
-// Y[M, N] = X[M, K] . W[N, K]^T for M = (k+1) tokens x batch rows beyond the
-// skinny kernel's 16 (the C4 / C5 batches and batched prompt chunks: 17-128
-// rows), replacing rocblas_gemm_ex in HipBackend::gemm (hip_backend.cc:697-809)
-// for that case.
+// Y[M, N] = X[M, K] . W[N, K]^T for M <= 128 rows of (k+1) tokens x batch
+// (the C4 / C5 batches, their drafts and corrections, batched prompt chunks),
+// replacing rocblas_gemm_ex in HipBackend::gemm (hip_backend.cc:697-809) for
+// that case.
 //
 // Tolerance mode: v_mfma_f32_16x16x32_bf16 sums each 32-product group with
 // its own internal rounding, so results match the canonical fp32 order to
@@ -23,6 +23,9 @@
 //   * Narrow layers (N <= 20480) also split K across 2 or 4 blocks when the
 //     caller passes a workspace: the blocks write fp32 partials and a second
 //     pass sums them in split order (deterministic) and applies the epilogue.
+//     (Folding that pass into the last block of each tile needs a device-scope
+//     release per block, an L2 write-back that serialises within an XCD:
+//     measured 1.8x slower than the second launch on MI355X.)
 //   * Epilogues as in the skinny GEMM: store, residual add, SwiGLU over
 //     interleaved (gate_f, up_f) rows.
 #include "hai_common.h"
@@ -406,6 +409,7 @@ int launch_mfma(const MfmaArgs& a, hipStream_t s) {
 
 template <int EPI>
 int dispatch_mfma(const MfmaArgs& a, hipStream_t s) {
+    if (a.M <= 16) return launch_mfma<1, EPI>(a, s);
     if (a.M <= 32) return launch_mfma<2, EPI>(a, s);
     if (a.M <= 64) return launch_mfma<4, EPI>(a, s);
     return launch_mfma<8, EPI>(a, s);

@@ -408,7 +408,7 @@ int64_t Engine::read_tensor(uint32_t id, uint16_t* out, int64_t capacity) {
 int Engine::gemm(uint16_t* y, int64_t ldy, const uint16_t* x, int64_t ldx, const Lin& w, int64_t M, int64_t N,
                  int64_t K, int epi, const uint16_t* res, int64_t ldres) {
     if (prof_record_) prof_calls_.push_back({y, ldy, x, ldx, w, M, N, K, epi, res, ldres, nullptr, nullptr});
-    if (mfma_ && M > 16) {
+    if (use_mfma(M)) {
         for (int64_t m0 = 0; m0 < M; m0 += 128) {
             const int64_t mm = std::min<int64_t>(128, M - m0);
             const uint16_t* rm = res ? res + m0 * ldres : nullptr;
@@ -445,7 +445,7 @@ int Engine::norm_gemm(uint16_t* y, int64_t ldy, const uint16_t* x, const uint16_
     // lm_head-sized outputs stream faster from the plain kernel than the norm
     // prologue saves (measured on MI355X), so they normalise separately; so
     // do launches of more than 16 rows.
-    if (N > kFusedNormMaxN || M > 16) {
+    if (N > kFusedNormMaxN || M > 16 || use_mfma(M)) {
         uint16_t* xn = xn_out != nullptr ? xn_out : xn_;
         HAI_TRY(hai_rmsnorm_bf16(xn, H, x, H, nw, M, H, cfg_.rms_eps, 1, stream_));
         return gemm(y, ldy, xn, H, w, M, N, H, epi, res, ldres);
@@ -1057,8 +1057,7 @@ int Engine::profile_verify(int64_t T, int64_t iters, hai_verify_profile* out) {
     // several launches on the bit-exact kernels
     double launches = 0.0;
     for (const auto& c : prof_calls_)
-        launches += (mfma_ && c.M > 16) ? static_cast<double>((c.M + 127) / 128)
-                                        : static_cast<double>((c.M + 15) / 16);
+        launches += use_mfma(c.M) ? static_cast<double>((c.M + 127) / 128) : static_cast<double>((c.M + 15) / 16);
     // Draft step timing (one MTP forward + lm_head + argmax per sequence)
     // without events inside, on scratch MTP lengths.
     for (int64_t it = 0; it < iters + 1; ++it) {

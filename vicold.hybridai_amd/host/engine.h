@@ -178,7 +178,9 @@ private:
     // device pieces of a step
     // M rows of any count: launches of <= 16 rows on the bit-exact kernels,
     // or one MFMA launch per <= 128 rows when the engine runs in tolerance
-    // mode (hai_engine_options::mfma, bf16 weights, M > 16).
+    // mode (hai_engine_options::mfma) and M >= kMfmaMinRows.
+    static constexpr int64_t kMfmaMinRows = 4;
+    bool use_mfma(int64_t M) const { return mfma_ && M >= kMfmaMinRows; }
     int gemm(uint16_t* y, int64_t ldy, const uint16_t* x, int64_t ldx, const Lin& w, int64_t M, int64_t N,
              int64_t K, int epi, const uint16_t* res, int64_t ldres);
     // RMSNorm(+1) of the H-wide rows x (norm weight nw) fused into the linear
