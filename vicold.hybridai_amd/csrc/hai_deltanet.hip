@@ -64,11 +64,12 @@ __global__ __launch_bounds__(DV * 4) void deltanet_kernel(DnArgs A) {
     constexpr int GI = DK / 4;            // key dims per thread
     constexpr int ZP = kMaxT * DV / NT;   // output elements per thread (all tokens)
     const int T = A.T;
-    extern __shared__ float smem[];
-    float* qs = smem;                  // [T][DK] conv output, q channels
-    float* ks = qs + T * DK;           // [T][DK] k channels
+    extern __shared__ __align__(16) float smem[];
+    float* qs = smem;                  // [T][DK] conv output, q channels (then q * q-norm scale)
+    float* ks = qs + T * DK;           // [T][DK] k channels (then k * k-norm scale)
     float* vs = ks + T * DK;           // [T][DV] v channels
     float* os = vs + T * DV;           // [T][DV] unrounded recurrent output
+    float* bks = os + T * DV;          // [T][DK] beta * normalised k
     __shared__ float s_q[kMaxT], s_k[kMaxT], s_decay[kMaxT], s_beta[kMaxT], s_rms[kMaxT];
 
     const int h = blockIdx.x;
@@ -84,27 +85,11 @@ __global__ __launch_bounds__(DV * 4) void deltanet_kernel(DnArgs A) {
     const int64_t kw = static_cast<int64_t>(A.nk) * DK;
     const int64_t vw = static_cast<int64_t>(nv) * DV;
     const int64_t C = 2 * kw + vw;
-    const int64_t p0 = REF ? 0 : static_cast<int64_t>(A.lens ? A.lens[b] : 0) + A.pos_add;
     const int hist = A.Kc - 1;
     const int64_t row0 = static_cast<int64_t>(b) * T;
 
-    // ---- issue every global load of the step up front ----
-    float S[GI];  // column j, key dims [g*GI, g*GI+GI)
-    if constexpr (REF) {
-        const float* src = A.state + static_cast<int64_t>(h) * DK * DV + static_cast<int64_t>(g) * GI * DV + j;
-#pragma unroll
-        for (int i = 0; i < GI; ++i) S[i] = src[i * DV];
-    } else {
-        const int64_t slot = p0 % A.nslots;
-        const float4* src =
-            reinterpret_cast<const float4*>(A.state + ((slot * A.B + b) * nv + h) * static_cast<int64_t>(DV) * DK) +
-            tid;
-#pragma unroll
-        for (int m = 0; m < GI / 4; ++m) {
-            const float4 v4 = src[m * NT];
-            S[4 * m] = v4.x; S[4 * m + 1] = v4.y; S[4 * m + 2] = v4.z; S[4 * m + 3] = v4.w;
-        }
-    }
+    // ---- issue every global load of the step up front: first those that do
+    // not depend on the cache length (its load is still in flight) ----
     // channel of this thread: [0, DK) q, [DK, 2DK) k, [2DK, 2DK+DV) v
     const int cl = tid;
     const bool has_ch = cl < 2 * DK + DV;
@@ -114,6 +99,8 @@ __global__ __launch_bounds__(DV * 4) void deltanet_kernel(DnArgs A) {
     else if (cl >= 2 * DK) { dst = vs; di = cl - 2 * DK; dstride = DV; }
     // window: vals[i] = input at position p0 - hist + i (history, then the T new tokens)
     uint16_t vals[kMaxT + kMaxKc - 1];
+#pragma unroll
+    for (int i = 0; i < kMaxT + kMaxKc - 1; ++i) vals[i] = 0;
     float wc[kMaxKc];
     int64_t c = 0;
     if (cl < DK) c = static_cast<int64_t>(gq) * DK + cl;
@@ -131,19 +118,12 @@ __global__ __launch_bounds__(DV * 4) void deltanet_kernel(DnArgs A) {
             for (int t = 0; t < kMaxT; ++t) vals[t] = t < T ? srcp[t * ld + col] : uint16_t{0};
         } else {
 #pragma unroll
-            for (int i = 0; i < kMaxKc - 1; ++i) {
-                const int64_t pos = p0 - hist + i;
-                vals[i] = (i < hist && pos >= 0)
-                              ? A.ring[(static_cast<int64_t>(b) * A.ring_n + (pos % A.ring_n)) * C + c]
-                              : uint16_t{0};
-            }
-#pragma unroll
             for (int i = 0; i < kMaxKc; ++i) wc[i] = i < A.Kc ? bf2f(A.conv_w[c * A.Kc + i]) : 0.0f;
 #pragma unroll
             for (int t = 0; t < kMaxT; ++t) {
                 uint16_t x = 0;
                 if (t < T) x = A.proj[(row0 + t) * A.ld_proj + A.off_qkv + c];
-                // shift the new tokens in right after the hist history entries
+                // the new tokens go right after the hist history entries
 #pragma unroll
                 for (int hh = 0; hh < kMaxKc; ++hh)
                     if (hh == hist) vals[t + hh] = x;
@@ -179,6 +159,46 @@ __global__ __launch_bounds__(DV * 4) void deltanet_kernel(DnArgs A) {
     }
     const float nwj = bf2f(A.norm_w[jo]);
 
+    // ---- then the length-dependent ones: the state slot and the conv
+    // history (one modulo each; later positions advance with a wrap) ----
+    const int64_t p0 = REF ? 0 : static_cast<int64_t>(A.lens ? A.lens[b] : 0) + A.pos_add;
+    float S[GI];  // column j, key dims [g*GI, g*GI+GI)
+    int64_t slot_w = 0, ring_w = 0;  // state slot after token 0, ring entry of token 0
+    if constexpr (REF) {
+        const float* src = A.state + static_cast<int64_t>(h) * DK * DV + static_cast<int64_t>(g) * GI * DV + j;
+#pragma unroll
+        for (int i = 0; i < GI; ++i) S[i] = src[i * DV];
+    } else {
+        const int64_t slot = p0 % A.nslots;
+        slot_w = slot + 1 == A.nslots ? 0 : slot + 1;
+        const float4* src =
+            reinterpret_cast<const float4*>(A.state + ((slot * A.B + b) * nv + h) * static_cast<int64_t>(DV) * DK) +
+            tid;
+#pragma unroll
+        for (int m = 0; m < GI / 4; ++m) {
+            const float4 v4 = src[m * NT];
+            S[4 * m] = v4.x; S[4 * m + 1] = v4.y; S[4 * m + 2] = v4.z; S[4 * m + 3] = v4.w;
+        }
+        // ring entry of position p0 - hist (negative positions read as zero)
+        const int64_t base = p0 - hist;
+        int64_t rp = base % A.ring_n;
+        if (rp < 0) rp += A.ring_n;
+        if (has_ch) {
+#pragma unroll
+            for (int i = 0; i < kMaxKc - 1; ++i) {
+                if (i < hist) {
+                    if (base + i >= 0) vals[i] = A.ring[(static_cast<int64_t>(b) * A.ring_n + rp) * C + c];
+                    rp = rp + 1 == A.ring_n ? 0 : rp + 1;
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < kMaxKc - 1; ++i)
+                if (i < hist) rp = rp + 1 == A.ring_n ? 0 : rp + 1;
+        }
+        ring_w = rp;
+    }
+
     // ---- grouped causal conv + SiLU (REF: inputs are already convolved) ----
     if (has_ch) {
         if constexpr (REF) {
@@ -187,6 +207,7 @@ __global__ __launch_bounds__(DV * 4) void deltanet_kernel(DnArgs A) {
                 if (t < T) dst[t * dstride + di] = bf2f(vals[t]);
         } else {
             const bool writer = cl >= 2 * DK || (h % group) == 0;
+            int64_t rw = ring_w;  // ring entry of position p0 + t
 #pragma unroll
             for (int t = 0; t < kMaxT; ++t) {
                 if (t < T) {
@@ -200,8 +221,9 @@ __global__ __launch_bounds__(DV * 4) void deltanet_kernel(DnArgs A) {
 #pragma unroll
                         for (int hh = 0; hh < kMaxKc; ++hh)
                             if (hh == hist) xv = vals[t + hh];
-                        A.ring[(static_cast<int64_t>(b) * A.ring_n + ((p0 + t) % A.ring_n)) * C + c] = xv;
+                        A.ring[(static_cast<int64_t>(b) * A.ring_n + rw) * C + c] = xv;
                     }
+                    rw = rw + 1 == A.ring_n ? 0 : rw + 1;
                 }
             }
         }
@@ -228,42 +250,66 @@ __global__ __launch_bounds__(DV * 4) void deltanet_kernel(DnArgs A) {
     }
     __syncthreads();
 
+    // ---- every token's q * q-scale, k * k-scale and beta * (k * k-scale),
+    // computed once for all columns (the same products the columns used) ----
+    for (int e = tid; e < T * DK; e += NT) {
+        const int t = e / DK;
+        qs[e] = qs[e] * s_q[t];
+        const float kh = ks[e] * s_k[t];
+        ks[e] = kh;
+        bks[e] = s_beta[t] * kh;
+    }
+    __syncthreads();
+
     // ---- gated delta rule, token by token (column-local: no block barrier) ----
     for (int t = 0; t < T; ++t) {
-        const float qsc = s_q[t], ksc = s_k[t], decay = s_decay[t], beta = s_beta[t];
-        const float* qt = qs + t * DK + g * GI;
-        const float* kt = ks + t * DK + g * GI;
+        const float decay = s_decay[t];
+        const float4* qt = reinterpret_cast<const float4*>(qs + t * DK + g * GI);
+        const float4* kt = reinterpret_cast<const float4*>(ks + t * DK + g * GI);
+        const float4* bt = reinterpret_cast<const float4*>(bks + t * DK + g * GI);
         float r = 0.0f;
 #pragma unroll
-        for (int i = 0; i < GI; ++i) {
-            S[i] = S[i] * decay;
-            r = fma_(kt[i] * ksc, S[i], r);
+        for (int m = 0; m < GI / 4; ++m) {
+            const float4 k4 = kt[m];
+            const float kv[4] = {k4.x, k4.y, k4.z, k4.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                S[4 * m + e] = S[4 * m + e] * decay;
+                r = fma_(kv[e], S[4 * m + e], r);
+            }
         }
-        r = r + __shfl_xor(r, 1, 64);
-        r = r + __shfl_xor(r, 2, 64);
+        r = r + quad_xor1(r);
+        r = r + quad_xor2(r);
         const float cj = vs[t * DV + j] - r;
         float o = 0.0f;
 #pragma unroll
-        for (int i = 0; i < GI; ++i) {
-            S[i] = fma_(beta * (kt[i] * ksc), cj, S[i]);
-            o = fma_(qt[i] * qsc, S[i], o);
+        for (int m = 0; m < GI / 4; ++m) {
+            const float4 b4 = bt[m], q4 = qt[m];
+            const float bv[4] = {b4.x, b4.y, b4.z, b4.w}, qv[4] = {q4.x, q4.y, q4.z, q4.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                S[4 * m + e] = fma_(bv[e], cj, S[4 * m + e]);
+                o = fma_(qv[e], S[4 * m + e], o);
+            }
         }
-        o = o + __shfl_xor(o, 1, 64);
-        o = o + __shfl_xor(o, 2, 64);
+        o = o + quad_xor1(o);
+        o = o + quad_xor2(o);
         if constexpr (REF) {
             if (t == T - 1) {
                 float* dstp = A.state + static_cast<int64_t>(h) * DK * DV + static_cast<int64_t>(g) * GI * DV + j;
 #pragma unroll
                 for (int i = 0; i < GI; ++i) dstp[i * DV] = S[i];
             }
-        } else if (A.write_all || t == T - 1) {
-            const int64_t slot = (p0 + t + 1) % A.nslots;
-            float4* dstp =
-                reinterpret_cast<float4*>(A.state + ((slot * A.B + b) * nv + h) * static_cast<int64_t>(DV) * DK) +
-                tid;
+        } else {
+            if (A.write_all || t == T - 1) {
+                float4* dstp =
+                    reinterpret_cast<float4*>(A.state + ((slot_w * A.B + b) * nv + h) * static_cast<int64_t>(DV) * DK) +
+                    tid;
 #pragma unroll
-            for (int m = 0; m < GI / 4; ++m)
-                dstp[m * NT] = make_float4(S[4 * m], S[4 * m + 1], S[4 * m + 2], S[4 * m + 3]);
+                for (int m = 0; m < GI / 4; ++m)
+                    dstp[m * NT] = make_float4(S[4 * m], S[4 * m + 1], S[4 * m + 2], S[4 * m + 3]);
+            }
+            slot_w = slot_w + 1 == A.nslots ? 0 : slot_w + 1;  // state after token t + 1
         }
         if (g == 0) os[t * DV + j] = o;
     }
@@ -339,7 +385,7 @@ __global__ __launch_bounds__(256) void deltanet_conv_kernel(uint16_t* __restrict
 
 template <int DK, int DV, bool REF>
 int launch(const DnArgs& a, hipStream_t s) {
-    const size_t shmem = static_cast<size_t>(a.T) * (2 * DK + 2 * DV) * sizeof(float);
+    const size_t shmem = static_cast<size_t>(a.T) * (3 * DK + 2 * DV) * sizeof(float);
     deltanet_kernel<DK, DV, REF><<<dim3(a.nv, REF ? 1 : a.B), dim3(DV * 4), shmem, s>>>(a);
     return launched(REF ? "deltanet_recurrent_kernel" : "deltanet_verify_kernel");
 }

@@ -152,15 +152,25 @@ struct ChunkOffset {
 };
 
 // xor butterfly over the 64 lanes of a wave; all lanes get the same bits.
+// The value of lane (lane ^ 1) / (lane ^ 2): a DPP quad permutation, no LDS
+// round trip (same operands as __shfl_xor with those masks).
+__device__ __forceinline__ float quad_xor1(float x) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0xB1, 0xF, 0xF, false));  // [1,0,3,2]
+}
+__device__ __forceinline__ float quad_xor2(float x) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x4E, 0xF, 0xF, false));  // [2,3,0,1]
+}
 __device__ __forceinline__ float wave_sum64(float v) {
 #pragma unroll
-    for (int s = 32; s >= 1; s >>= 1) v = v + __shfl_xor(v, s, 64);
-    return v;
+    for (int s = 32; s >= 4; s >>= 1) v = v + __shfl_xor(v, s, 64);
+    v = v + quad_xor2(v);
+    return v + quad_xor1(v);
 }
 __device__ __forceinline__ float wave_max64(float v) {
 #pragma unroll
-    for (int s = 32; s >= 1; s >>= 1) v = fmaxf(v, __shfl_xor(v, s, 64));
-    return v;
+    for (int s = 32; s >= 4; s >>= 1) v = fmaxf(v, __shfl_xor(v, s, 64));
+    v = fmaxf(v, quad_xor2(v));
+    return fmaxf(v, quad_xor1(v));
 }
 
 // L64-order sum of squares of a bf16 vector of length n (n % 8 == 0),
