@@ -9,7 +9,9 @@
 //     in flight at once; the waves take the group's queries in turn: lane =
 //     key computes the score with a sequential fma over D, the chunk max and
 //     the exp-sum are wave reductions, and P.V is a sequential fma over the
-//     chunk's keys with lane = pair of output dims.  The group is every query
+//     chunk's keys with lane = pair of output dims; a wave carries up to six
+//     queries at once, so each K / V element is unpacked once for all of
+//     them.  The group is every query
 //     of the KV head (all T x nq/nkv of them: K and V are read once) when the
 //     chunks alone give the grid enough blocks (long caches, batches), else
 //     four queries per block;
@@ -34,22 +36,26 @@ constexpr int64_t kFullGroupBlocks = 2048;
 __host__ __device__ constexpr int64_t partial_stride(int D) { return D + 2; }
 
 // grid (chunk, query group x KV head, sequence): the block stages one 64-key
-// chunk of one KV head and serves qpb of that head's queries (qpb % 4 == 0).
-template <int D>
-__global__ __launch_bounds__(256) void gqa_partial_kernel(
+// chunk of one KV head and serves qpb of that head's queries.  Each wave takes
+// up to QG of them at a time: a K or V element is unpacked once and feeds the
+// QG queries' fma chains (each chain keeps its own sequential order).
+template <int D, int QG, int W>
+__global__ __launch_bounds__(64 * W) void gqa_partial_kernel(
     float* __restrict__ scratch, const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, int64_t cap, int T, int nq, int nkv, const int32_t* lens,
     int len_add, int nchunk, float scale, int qpb) {
     constexpr int KP = D / 2 + 4;          // dword stride of a staged K row (16-byte pad)
     constexpr int VP = D / 2;              // dword stride of a staged V row
     constexpr int ROW16 = D / 8;           // 16-byte pieces per row
-    constexpr int NLD = kChunk * ROW16 / 256;  // pieces per thread and tile
+    constexpr int NT = 64 * W;             // threads
+    constexpr int NLD = kChunk * ROW16 / NT;   // pieces per thread and tile
     constexpr int QPL = D / 64;            // query elements per lane
-    static_assert(NLD >= 1 && kChunk * ROW16 % 256 == 0, "tile must split over 256 threads");
+    constexpr int NPAIR = (D / 2 + 63) / 64;  // value pairs per lane (lanes past D / 2 idle when D = 64)
+    static_assert(NLD >= 1 && kChunk * ROW16 % NT == 0, "tile must split over the block");
     __shared__ uint32_t Ks[kChunk * KP];
     __shared__ uint32_t Vs[kChunk * VP];
-    __shared__ float Qs[kWaves][D];
-    __shared__ float Ps[kWaves][kChunk];
+    __shared__ __align__(16) float Qs[W][QG][D];
+    __shared__ __align__(16) float Ps[W][QG][kChunk];
 
     const int chunk = blockIdx.x;
     const int kvh = blockIdx.y % nkv;
@@ -57,7 +63,7 @@ __global__ __launch_bounds__(256) void gqa_partial_kernel(
     const int b = blockIdx.z;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = wave_index();
     const int64_t L = static_cast<int64_t>(lens ? lens[b] : 0) + len_add;
     const int64_t key0 = static_cast<int64_t>(chunk) * kChunk;
     const int group = nq / nkv;
@@ -71,13 +77,19 @@ __global__ __launch_bounds__(256) void gqa_partial_kernel(
     auto q_row = [&](int qi) {
         return q + ((static_cast<int64_t>(b) * T + qi / group) * nq + kvh * group + qi % group) * D;
     };
-    // The wave's first query is loaded alongside the K / V tiles.
-    uint16_t qv[QPL];
-    if (q_begin + wave < q_end) {
-        const uint16_t* qrow = q_row(q_begin + wave);
+    // pass p of wave w serves queries q_begin + (W p + w) QG + [0, QG)
+    uint16_t qv[QG][QPL];
+    auto load_q = [&](int base) {
 #pragma unroll
-        for (int r = 0; r < QPL; ++r) qv[r] = qrow[lane + 64 * r];
-    }
+        for (int qq = 0; qq < QG; ++qq)
+            if (base + qq < q_end) {
+                const uint16_t* qrow = q_row(base + qq);
+#pragma unroll
+                for (int r = 0; r < QPL; ++r) qv[qq][r] = qrow[lane + 64 * r];
+            }
+    };
+    // The wave's first queries are loaded alongside the K / V tiles.
+    load_q(q_begin + wave * QG);
 
     // Stage the chunk's K and V rows: every load is issued before the first
     // LDS store; rows past the cache length read as zeros (buffer range).
@@ -89,7 +101,7 @@ __global__ __launch_bounds__(256) void gqa_partial_kernel(
         u32x4 kd[NLD], vd[NLD];
 #pragma unroll
         for (int i = 0; i < NLD; ++i) {
-            const int e = tid + 256 * i;
+            const int e = tid + NT * i;
             const int j = e / ROW16;
             const uint32_t off = static_cast<uint32_t>((j * nkv * D + (e % ROW16) * 8) * 2);
             kd[i] = bload(rk, off, 0);
@@ -97,7 +109,7 @@ __global__ __launch_bounds__(256) void gqa_partial_kernel(
         }
 #pragma unroll
         for (int i = 0; i < NLD; ++i) {
-            const int e = tid + 256 * i;
+            const int e = tid + NT * i;
             const int j = e / ROW16;
             const int p = (e % ROW16) * 4;
             *reinterpret_cast<u32x4*>(Ks + j * KP + p) = kd[i];
@@ -111,72 +123,124 @@ __global__ __launch_bounds__(256) void gqa_partial_kernel(
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     };
-    for (int qi = q_begin + wave; qi < q_end; qi += kWaves) {
-        const int t = qi / group;
-        const int h = kvh * group + qi % group;
-        const int64_t qpos = L - T + t;
+    for (int base = q_begin + wave * QG; base < q_end; base += W * QG) {
+        const int nw = min(QG, q_end - base);
 #pragma unroll
-        for (int r = 0; r < QPL; ++r) Qs[wave][lane + 64 * r] = bf2f(qv[r]);
-        // the wave's next query is in flight while this one is computed
-        if (qi + kWaves < q_end) {
-            const uint16_t* qrow = q_row(qi + kWaves);
+        for (int qq = 0; qq < QG; ++qq)
 #pragma unroll
-            for (int r = 0; r < QPL; ++r) qv[r] = qrow[lane + 64 * r];
-        }
+            for (int r = 0; r < QPL; ++r) Qs[wave][qq][lane + 64 * r] = qq < nw ? bf2f(qv[qq][r]) : 0.0f;
+        // the wave's next queries are in flight while these are computed
+        if (base + W * QG < q_end) load_q(base + W * QG);
         wave_sync();
 
-        // Scores: lane = key, sequential fma over D.
-        const int64_t kj = key0 + lane;
-        const bool valid = lane < nkeys && kj <= qpos;
-        float s = 0.0f;
+        // Scores: lane = key, sequential fma over D for every query.
+        float s[QG];
+#pragma unroll
+        for (int qq = 0; qq < QG; ++qq) s[qq] = 0.0f;
         {
             const uint32_t* kr = Ks + lane * KP;
-            const float* qr = Qs[wave];
-#pragma unroll 4
+#pragma unroll 2
             for (int p = 0; p < D / 2; p += 4) {
                 const u32x4 kk = *reinterpret_cast<const u32x4*>(kr + p);
-                const float4 qa = *reinterpret_cast<const float4*>(qr + 2 * p);
-                const float4 qb = *reinterpret_cast<const float4*>(qr + 2 * p + 4);
-                s = fma_(qa.x, lo_bf(kk[0]), s);
-                s = fma_(qa.y, hi_bf(kk[0]), s);
-                s = fma_(qa.z, lo_bf(kk[1]), s);
-                s = fma_(qa.w, hi_bf(kk[1]), s);
-                s = fma_(qb.x, lo_bf(kk[2]), s);
-                s = fma_(qb.y, hi_bf(kk[2]), s);
-                s = fma_(qb.z, lo_bf(kk[3]), s);
-                s = fma_(qb.w, hi_bf(kk[3]), s);
+                const float k8[8] = {lo_bf(kk[0]), hi_bf(kk[0]), lo_bf(kk[1]), hi_bf(kk[1]),
+                                     lo_bf(kk[2]), hi_bf(kk[2]), lo_bf(kk[3]), hi_bf(kk[3])};
+#pragma unroll
+                for (int qq = 0; qq < QG; ++qq) {
+                    const float4 qa = *reinterpret_cast<const float4*>(&Qs[wave][qq][2 * p]);
+                    const float4 qb = *reinterpret_cast<const float4*>(&Qs[wave][qq][2 * p + 4]);
+                    float sv = s[qq];
+                    sv = fma_(qa.x, k8[0], sv);
+                    sv = fma_(qa.y, k8[1], sv);
+                    sv = fma_(qa.z, k8[2], sv);
+                    sv = fma_(qa.w, k8[3], sv);
+                    sv = fma_(qb.x, k8[4], sv);
+                    sv = fma_(qb.y, k8[5], sv);
+                    sv = fma_(qb.z, k8[6], sv);
+                    sv = fma_(qb.w, k8[7], sv);
+                    s[qq] = sv;
+                }
             }
-            s = s * scale;
         }
-        const float m = wave_max64(valid ? s : __uint_as_float(0xff800000u));
-        const float pr = valid ? cexp(s - m) : 0.0f;
-        const float l = wave_sum64(pr);
-        Ps[wave][lane] = pr;
-        float* part = scratch + ((((static_cast<int64_t>(b) * T + t) * nq + h) * nchunk) + chunk) * partial_stride(D);
-        if (lane == 0) {
-            part[0] = m;
-            part[1] = l;
+        // per query: chunk max, exp-sum and probabilities (zero past the causal limit)
+        int nj_max = 0;
+#pragma unroll
+        for (int qq = 0; qq < QG; ++qq) {
+            if (qq < nw) {
+                const int qi = base + qq;
+                const int t = qi / group;
+                const int h = kvh * group + qi % group;
+                const int64_t qpos = L - T + t;
+                const bool valid = lane < nkeys && key0 + lane <= qpos;
+                const float sc = s[qq] * scale;
+                const float m = wave_max64(valid ? sc : __uint_as_float(0xff800000u));
+                const float pr = valid ? cexp(sc - m) : 0.0f;
+                const float l = wave_sum64(pr);
+                Ps[wave][qq][lane] = pr;
+                float* part =
+                    scratch + ((((static_cast<int64_t>(b) * T + t) * nq + h) * nchunk) + chunk) * partial_stride(D);
+                if (lane == 0) {
+                    part[0] = m;
+                    part[1] = l;
+                }
+                const int64_t lim = qpos - key0 + 1;
+                const int nj = static_cast<int>(lim < nkeys ? (lim < 0 ? 0 : lim) : nkeys);
+                nj_max = max(nj_max, nj);
+            } else {
+                Ps[wave][qq][lane] = 0.0f;
+            }
         }
         wave_sync();
 
-        // P.V: lane owns value pairs (2i, 2i+1), i = lane + 64r; sequential over keys.
-        const int64_t lim = qpos - key0 + 1;
-        const int nj = static_cast<int>(lim < nkeys ? (lim < 0 ? 0 : lim) : nkeys);
-        constexpr int NPAIR = (D / 2 + 63) / 64;
+        // P.V: lane owns value pairs (2i, 2i+1), i = lane + 64r; sequential over
+        // keys.  Keys past a query's causal limit carry probability 0, and
+        // fma(0, v, o) == o for the finite staged values, so running every
+        // query to the longest limit does not change a bit.
+        float o[QG][NPAIR][2];
 #pragma unroll
-        for (int r = 0; r < NPAIR; ++r) {
-            const int pi = lane + 64 * r;
-            if (pi >= D / 2) break;
-            float o0 = 0.0f, o1 = 0.0f;
-            for (int j = 0; j < nj; ++j) {
-                const float pj = Ps[wave][j];
-                const uint32_t vv = Vs[j * VP + pi];
-                o0 = fma_(pj, lo_bf(vv), o0);
-                o1 = fma_(pj, hi_bf(vv), o1);
+        for (int qq = 0; qq < QG; ++qq)
+#pragma unroll
+            for (int r = 0; r < NPAIR; ++r) o[qq][r][0] = o[qq][r][1] = 0.0f;
+        const int nj4 = (nj_max + 3) & ~3;
+        for (int j0 = 0; j0 < nj4; j0 += 4) {
+            float4 p4[QG];
+#pragma unroll
+            for (int qq = 0; qq < QG; ++qq) p4[qq] = *reinterpret_cast<const float4*>(&Ps[wave][qq][j0]);
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) {
+                float vlo[NPAIR], vhi[NPAIR];
+#pragma unroll
+                for (int r = 0; r < NPAIR; ++r) {
+                    const uint32_t vv = lane + 64 * r < D / 2 ? Vs[(j0 + jj) * VP + lane + 64 * r] : 0u;
+                    vlo[r] = lo_bf(vv);
+                    vhi[r] = hi_bf(vv);
+                }
+#pragma unroll
+                for (int qq = 0; qq < QG; ++qq) {
+                    const float pj = jj == 0 ? p4[qq].x : jj == 1 ? p4[qq].y : jj == 2 ? p4[qq].z : p4[qq].w;
+#pragma unroll
+                    for (int r = 0; r < NPAIR; ++r) {
+                        o[qq][r][0] = fma_(pj, vlo[r], o[qq][r][0]);
+                        o[qq][r][1] = fma_(pj, vhi[r], o[qq][r][1]);
+                    }
+                }
             }
-            *reinterpret_cast<float2*>(part + 2 + 2 * pi) = make_float2(o0, o1);
         }
-        wave_sync();  // Qs / Ps are rewritten by the next query
+#pragma unroll
+        for (int qq = 0; qq < QG; ++qq) {
+            if (qq < nw) {
+                const int qi = base + qq;
+                const int t = qi / group;
+                const int h = kvh * group + qi % group;
+                float* part =
+                    scratch + ((((static_cast<int64_t>(b) * T + t) * nq + h) * nchunk) + chunk) * partial_stride(D);
+#pragma unroll
+                for (int r = 0; r < NPAIR; ++r)
+                    if (lane + 64 * r < D / 2)
+                        *reinterpret_cast<float2*>(part + 2 + 2 * (lane + 64 * r)) =
+                            make_float2(o[qq][r][0], o[qq][r][1]);
+            }
+        }
+        wave_sync();  // Qs / Ps are rewritten by the next pass
     }
 }
 
@@ -257,8 +321,22 @@ int launch(uint16_t* out, const uint16_t* q, const uint16_t* gate, const uint16_
     const int64_t groups = want < max_groups ? want : max_groups;
     const int qpb = static_cast<int>(kWaves * ((max_groups + groups - 1) / groups));
     const int qgroups = (nqry + qpb - 1) / qpb;
-    gqa_partial_kernel<D><<<dim3(nchunk, nkv * qgroups, B), dim3(256), 0, s>>>(
-        scratch, q, kc, vc, cap, T, nq, nkv, lens, len_add, nchunk, scale, qpb);
+    // Waves and queries per wave: up to 8 queries per block on 4 waves (two
+    // blocks fit a CU), more on 8 waves of up to 3 (one block per CU, the K /
+    // V tile shared by all of them); larger groups take several passes.
+    const dim3 grid(nchunk, nkv * qgroups, B);
+    if (qpb <= 4)
+        gqa_partial_kernel<D, 1, 4><<<grid, dim3(256), 0, s>>>(scratch, q, kc, vc, cap, T, nq, nkv, lens, len_add,
+                                                               nchunk, scale, qpb);
+    else if (qpb <= 8)
+        gqa_partial_kernel<D, 2, 4><<<grid, dim3(256), 0, s>>>(scratch, q, kc, vc, cap, T, nq, nkv, lens, len_add,
+                                                               nchunk, scale, qpb);
+    else if (qpb <= 16)
+        gqa_partial_kernel<D, 2, 8><<<grid, dim3(512), 0, s>>>(scratch, q, kc, vc, cap, T, nq, nkv, lens, len_add,
+                                                               nchunk, scale, qpb);
+    else
+        gqa_partial_kernel<D, 3, 8><<<grid, dim3(512), 0, s>>>(scratch, q, kc, vc, cap, T, nq, nkv, lens, len_add,
+                                                               nchunk, scale, qpb);
     int rc = launched("gqa_partial_kernel");
     if (rc != HAI_OK) return rc;
     const int64_t nall = static_cast<int64_t>(B) * T * nq;
