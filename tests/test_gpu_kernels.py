@@ -247,9 +247,10 @@ def test_kv_norm_rope_append(B, T, nkv, D, R):
     (1, 2, 4, 2, 64, [30]), (1, 1, 4, 2, 64, [0]), (1, 4, 24, 4, 256, [60]), (1, 2, 24, 4, 256, [1278]),
     (2, 3, 4, 1, 128, [63, 200]), (1, 16, 4, 2, 64, [100]), (3, 1, 2, 2, 64, [0, 1, 64]),
     (1, 4, 24, 4, 256, [4092]),  # C2 micro-bench shape (cache 4096 incl. the 4 new rows)
-    (2, 4, 24, 4, 256, [6390, 100]),  # 800 chunk blocks: 8 of the 24 queries per block, 2 per wave
-    (4, 4, 24, 4, 256, [8186, 3000, 64, 5000]),  # 2048 chunk blocks (C4-like): all 24 per block, 6 per wave
-    (4, 2, 24, 4, 256, [8180, 10, 4000, 8100]),  # all 12 per block, 3 per wave
+    (1, 4, 24, 4, 256, [1590]),  # 100 chunk blocks: 8 of the 24 queries per block, 2 per wave
+    (2, 4, 24, 4, 256, [6390, 100]),  # 800 chunk blocks: all 24 per block, 3 per wave on 8 waves
+    (4, 4, 24, 4, 256, [8186, 3000, 64, 5000]),  # C4-like: all 24 per block
+    (4, 2, 24, 4, 256, [8180, 10, 4000, 8100]),  # all 12 per block, 2 per wave on 8 waves
     (4, 4, 24, 4, 128, [8186, 300, 7000, 1]),  # head_dim 128, 6 per wave
     (8, 6, 8, 2, 64, [8100, 8000, 3, 64, 128, 4000, 8120, 500])])  # head_dim 64 (half the lanes in P.V)
 def test_gqa_verify(B, T, nq, nkv, D, lens):
