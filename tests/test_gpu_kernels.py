@@ -760,3 +760,38 @@ def test_gemm_mfma_27b_shapes(M, N, K, epi):
     got = hai.bf16_to_f32(dy.download(np.uint16).reshape(M, ncols))
     scale = np.abs(want).max()
     assert np.allclose(got, want, rtol=2 ** -6, atol=2e-3 * scale), float(np.abs(got - want).max())
+
+
+@pytest.mark.parametrize("M,N,K,epi", [(64, 34816, 5120, 2), (64, 5120, 17408, 1), (64, 16384, 5120, 0)])
+def test_gemm_fp8_mfma_27b_shapes(M, N, K, epi):
+    """The C5 batched-verify GEMMs (32 sequences x 2 rows, FP8 E4M3 weights
+    with 128x128 scales): gate/up with SwiGLU over paired scale grids, down
+    with the residual add, DeltaNet in_proj qkv|z; within tolerance of the
+    oracle's FP8 GEMM (decode(q) * s, canonical fp32 dot)."""
+    rng = np.random.default_rng(N + K + 64)
+    x, xb = rand_bf16(rng, (M, K))
+    if epi == hai.EPI_SILU_MUL:
+        F = N // 2
+        qg, sg = _fp8_weights(rng, F, K)
+        qu, su = _fp8_weights(rng, F, K)
+        q = np.empty((N, K), np.uint8)
+        q[0::2], q[1::2] = qg, qu
+        s = np.stack([sg, su])
+        want = orc.silu_mul(orc.gemm_fp8(x, qg, sg), orc.gemm_fp8(x, qu, su))
+        ncols = F
+    else:
+        q, s = _fp8_weights(rng, N, K)
+        ncols = N
+        h, hb = rand_bf16(rng, (M, N))
+        y = orc.gemm_fp8(x, q, s)
+        want = y if epi == hai.EPI_STORE else orc.add(h, y)
+    dx, dq, ds = dev(xb), dev(q), dev(s)
+    dy = dev(hb) if epi == hai.EPI_RESIDUAL else out_buf(M * ncols * 2)
+    wsb = kern().hai_gemm_mfma_workspace_bytes(M, N)
+    dws = out_buf(max(wsb, 16))
+    hai.check(kern().hai_gemm_fp8_mfma(dy.ptr, ncols, dx.ptr, K, dq.ptr, ds.ptr, None, M, N, K,
+                                       epi | hai.FP8_NO_SPECIAL_CODES, dy.ptr if epi == hai.EPI_RESIDUAL else None,
+                                       ncols, dws.ptr, wsb, None), "gemm_fp8_mfma 27b")
+    got = hai.bf16_to_f32(dy.download(np.uint16).reshape(M, ncols))
+    scale = np.abs(want).max()
+    assert np.allclose(got, want, rtol=2 ** -6, atol=2e-3 * scale), float(np.abs(got - want).max())
