@@ -29,6 +29,9 @@ import numpy as np
 
 ROOT = Path(__file__).resolve().parent
 HBM_PEAK_GBS = 8000.0
+# HBM traffic / algorithmic weight bytes of the verify-step GEMMs (rocprofv3 FETCH_SIZE x 2.0 +
+# WRITE_SIZE, scaled by a known-size copy): profiles/gemm_bf16_kernel_c3_traffic.txt
+GEMM_TRAFFIC_RATIO = 1.0033
 METRIC = "accepted tok/s + verify steps/s (27B-shape bf16, bs=1, MTP k=1); % HBM peak"
 
 
@@ -402,7 +405,11 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gemm_gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            # HBM bytes per launch: the live algorithmic bytes x the FETCH_SIZE + WRITE_SIZE
+            # ratio measured by rocprofv3 on the same kernels at the C3 shapes
+            # (profiles/gemm_bf16_kernel_c3_traffic.txt; counters cannot be read inside this run)
+            "traffic": round(prof["gemm_bytes"] / prof["gemm_launches"] * GEMM_TRAFFIC_RATIO),
+            "traffic_ratio": GEMM_TRAFFIC_RATIO,
             "kernel": "gemm_bf16_kernel (skinny bf16 GEMM, verify T=%d)" % (args.width + 1),
             "bytes_per_launch": round(prof["gemm_bytes"] / prof["gemm_launches"]),
             "ms_per_launch": round(prof["gemm_ms"] / prof["gemm_launches"], 5),

@@ -155,6 +155,52 @@ def test_gemm_rmsnorm_fused(M, N, K_, epi, with_xn):
         assert_bits_equal(dxn.download(np.uint16), xn_want, "normalised rows")
 
 
+# The C3 verify step's weight streams at M = 2 rows, called as the engine
+# calls them (fused input RMSNorm on in_proj / qkv / gate-up, residual on the
+# out / o / down projections, lm_head after a separate norm); bit-exact.  Also
+# the workload of the rocprofv3 FETCH_SIZE / WRITE_SIZE passes that give the
+# HBM traffic per launch.
+C3_VERIFY_GEMMS = [("deltanet_in_proj", 16480, 5120, 0, True), ("out_proj", 5120, 6144, 1, False),
+                   ("gate_up", 34816, 5120, 2, True), ("down", 5120, 17408, 1, False),
+                   ("attn_qkv", 14336, 5120, 0, True), ("lm_head", 248320, 5120, 0, False)]
+
+
+@pytest.mark.parametrize("name,N,K_,epi,norm", C3_VERIFY_GEMMS)
+def test_gemm_c3_verify_shapes(name, N, K_, epi, norm):
+    M = 2
+    rng = np.random.default_rng(N + K_ + epi)
+    x, xb = rand_bf16(rng, (M, K_))
+    w, wb = rand_bf16(rng, (N, K_), 0.02)
+    ncols = N // 2 if epi == hai.EPI_SILU_MUL else N
+    h, hb = rand_bf16(rng, (M, ncols))
+    dx, dw = dev(xb), dev(wb)
+    dy = dev(hb) if epi == hai.EPI_RESIDUAL else out_buf(M * ncols * 2)
+    res = dy.ptr if epi == hai.EPI_RESIDUAL else None
+    if norm:
+        nw, nwb = rand_bf16(rng, (K_,), 0.02)
+        dnw = dev(nwb)
+        xin = orc.rmsnorm(x, nw, 1e-6, True)
+        hai.check(kern().hai_gemm_rmsnorm_bf16(dy.ptr, ncols, dx.ptr, K_, dnw.ptr, 1e-6, 1, None, K_, dw.ptr, M, N,
+                                               K_, epi, res, ncols, None), name)
+    else:
+        xin = x
+        hai.check(kern().hai_gemm_bf16(dy.ptr, ncols, dx.ptr, K_, dw.ptr, M, N, K_, epi, res, ncols, None), name)
+    y = orc.gemm(xin, w)
+    want = {hai.EPI_STORE: lambda: y, hai.EPI_RESIDUAL: lambda: orc.add(h, y),
+            hai.EPI_SILU_MUL: lambda: orc.silu_mul(y[:, 0::2], y[:, 1::2])}[epi]()
+    assert_bits_equal(dy.download(np.uint16), want, name)
+
+
+def test_copy_calibration():
+    """One device-to-device copy of 256 MiB: the dispatch of known size that
+    scales the rocprofv3 FETCH_SIZE / WRITE_SIZE counters to bytes."""
+    n = 256 << 20
+    src, dst = out_buf(n), hai.DeviceBuffer(n)
+    hai.check(kern().hai_memcpy_d2d(dst.ptr, src.ptr, n, None), "calibration copy")
+    hai.synchronize()
+    assert not dst.download(np.uint8)[:: 1 << 16].any()
+
+
 def test_gemm_rmsnorm_needs_xn_above_fused_limit():
     d = out_buf(1 << 16)
     # M*K = 4*5120 > 16384 without an xn_out buffer
