@@ -94,3 +94,22 @@ def test_eos_stops_like_reference(engines):
     assert list(toks) == list(rtoks)
     assert toks[-1] in eos
     assert np.array_equal(log, rlog)
+
+
+def test_token_ids_outside_vocabulary_are_rejected(engines):
+    """Prompt and draft-override ids index the embedding table: ids outside
+    [0, vocab) are an argument error before anything runs, and the engine
+    decodes normally afterwards."""
+    eng, ref, prompt = engines
+    bad = prompt.copy()
+    bad[3] = orc.TINY["vocab"]
+    with pytest.raises(RuntimeError, match="outside the vocabulary"):
+        eng.speculative(bad, NEW, 1)
+    ov = ref.greedy(prompt, NEW).copy()
+    ov[5] = -1
+    with pytest.raises(RuntimeError, match="outside the vocabulary"):
+        eng.speculative(prompt, NEW, 2, draft_override=ov)
+    with pytest.raises(RuntimeError, match="outside the vocabulary"):
+        eng.forward(bad)
+    toks, _, _ = eng.speculative(prompt, NEW, 1)
+    assert list(toks) == list(ref.greedy(prompt, NEW))

@@ -1,0 +1,100 @@
+"""Parity at the 27B shape of the benchmark configurations (C3 bf16, the C5
+weight format), where the CPU oracle is too slow to run the model, through
+size-independent properties of the path:
+
+* speculative decoding is lossless: the tokens of the speculative rounds
+  (widths 1 and 3, every draft accepted, some drafts rejected, none accepted)
+  equal greedy decoding of the same model, token by token;
+* greedy decoding's tokens equal the argmax of the last row of a fresh
+  forward over the whole sequence (prefill path, 16-row chunks): a verify row,
+  a correction row and a prefill row of the same position agree;
+* the round records add up (proposed = accepted + rejected, one correction
+  per rejected round).
+
+Random N(0, 0.02) weights give almost no natural acceptance, so acceptance
+patterns are forced with draft overrides (the reference path takes the same
+decisions for any draft source)."""
+import numpy as np
+import pytest
+
+from _hai import hai
+
+pytestmark = pytest.mark.gpu
+
+P, NEW = 40, 10
+
+
+def _refeed_greedy(eng, prompt, tokens):
+    """argmax of the last row of a fresh forward over prompt + tokens[:i]."""
+    seq = list(prompt)
+    got = []
+    for i in range(len(tokens)):
+        _, lg = eng.forward(np.array(seq, np.int32))
+        got.append(int(np.argmax(hai.bf16_to_f32(lg[-1]))))
+        seq.append(int(tokens[i]))
+    return got
+
+
+def _check_lossless(eng, prompt, vocab):
+    g = eng.greedy(prompt, NEW)
+    assert len(g) == NEW
+    assert list(g) == _refeed_greedy(eng, prompt, g)
+    rng = np.random.default_rng(5)
+    perturbed = g.copy()
+    for i in (2, 3, 7):
+        perturbed[i] = (perturbed[i] + 1) % vocab
+    cases = [(1, None), (3, None), (3, g), (1, perturbed), (3, perturbed),
+             (2, rng.integers(0, vocab, NEW).astype(np.int32))]
+    for width, ov in cases:
+        toks, st, log = eng.speculative(prompt, NEW, width, draft_override=ov)
+        assert list(toks) == list(g), (width, None if ov is None else list(ov))
+        assert st["proposed"] == st["accepted"] + st["rejected"]
+        assert st["corrections"] <= st["rounds"]
+        if ov is not None and ov is g:
+            assert st["accepted"] > 0 and st["corrections"] == 0
+
+
+def test_27b_bf16_speculative_is_lossless():
+    from hybridai_amd import engine as E
+    eng = E.Engine(E.QWEN27B, max_context=P + 5 * NEW + 32, max_verify_tokens=16)
+    try:
+        eng.init_synthetic(seed=0, std=0.02)
+        _check_lossless(eng, E.synthetic_prompt(1, P, E.QWEN27B["vocab"]), E.QWEN27B["vocab"])
+    finally:
+        eng.close()
+
+
+def test_27b_fp8_speculative_is_lossless():
+    from hybridai_amd import engine as E
+    eng = E.Engine(E.QWEN27B, max_context=P + 5 * NEW + 32, max_verify_tokens=16, fp8=True)
+    try:
+        eng.init_synthetic(seed=0, std=0.02)
+        _check_lossless(eng, E.synthetic_prompt(2, P, E.QWEN27B["vocab"]), E.QWEN27B["vocab"])
+    finally:
+        eng.close()
+
+
+def test_27b_batch_equals_single_sequences():
+    """Two sequences in lockstep (the C4 round structure, bit-exact GEMMs)
+    give each sequence's single-sequence tokens and round records."""
+    from hybridai_amd import engine as E
+    B = 2
+    prompts = np.stack([E.synthetic_prompt(10 + b, P, E.QWEN27B["vocab"]) for b in range(B)])
+    single = E.Engine(E.QWEN27B, max_context=P + 5 * NEW + 32, max_verify_tokens=16)
+    rand = np.random.default_rng(3).integers(0, E.QWEN27B["vocab"], NEW).astype(np.int32)
+    try:
+        single.init_synthetic(seed=0, std=0.02)
+        g = [single.greedy(prompts[b], NEW) for b in range(B)]
+        ov = np.stack([g[0], rand])  # sequence 0 accepts every draft, sequence 1 almost none
+        want = [single.speculative(prompts[b], NEW, 3, draft_override=ov[b]) for b in range(B)]
+    finally:
+        single.close()
+    eng = E.Engine(E.QWEN27B, max_context=P + 5 * NEW + 32, max_verify_tokens=16, batch=B)
+    try:
+        eng.init_synthetic(seed=0, std=0.02)
+        got = eng.speculative_batch(prompts, NEW, 3, draft_override=ov)
+    finally:
+        eng.close()
+    for b in range(B):
+        assert list(got[b][0]) == list(want[b][0]) == list(g[b]), b
+        assert np.array_equal(got[b][2], want[b][2]), b

@@ -56,10 +56,14 @@ double seconds_since(Clock::time_point t) {
 
 }  // namespace
 
+// A failing call is reported with its expression, followed by the engine's
+// own message when the callee set one (an argument check) and otherwise by
+// the kernel library's last error.
 #define HAI_TRY(expr)                                                 \
     do {                                                              \
+        const uint64_t _seq = err_seq_;                               \
         const int _rc = (expr);                                       \
-        if (_rc != HAI_OK) return fail(_rc, #expr);                   \
+        if (_rc != HAI_OK) return propagate(_rc, #expr, _seq);        \
     } while (0)
 
 Engine::Engine(const hai_model_config& cfg, const hai_engine_options& opt) : cfg_(cfg), opt_(opt) {
@@ -129,7 +133,20 @@ Engine::~Engine() {
 }
 
 int Engine::fail(int rc, const std::string& what) {
+    error_ = what;
+    ++err_seq_;
+    return rc;
+}
+
+int Engine::lib_fail(int rc, const std::string& what) {
     error_ = what + ": " + hai_last_error();
+    ++err_seq_;
+    return rc;
+}
+
+int Engine::propagate(int rc, const char* what, uint64_t seq_before) {
+    error_ = std::string(what) + ": " + (err_seq_ != seq_before ? error_ : std::string(hai_last_error()));
+    ++err_seq_;
     return rc;
 }
 
@@ -356,7 +373,7 @@ int Engine::upload_rope_tables() {
 
 int Engine::sync() {
     const int rc = hai_stream_synchronize(stream_);
-    if (rc != HAI_OK) return fail(rc, "stream synchronize");
+    if (rc != HAI_OK) return lib_fail(rc, "stream synchronize");
     return HAI_OK;
 }
 
@@ -385,8 +402,8 @@ int Engine::init_synthetic(uint64_t seed, float std_dev) {
     }
     const int rc_sync = hai_stream_synchronize(stream_);
     hai_free(tmp);
-    if (rc != HAI_OK) return fail(rc, "fp8 synthetic weights");
-    if (rc_sync != HAI_OK) return fail(rc_sync, "stream synchronize");
+    if (rc != HAI_OK) return lib_fail(rc, "fp8 synthetic weights");
+    if (rc_sync != HAI_OK) return lib_fail(rc_sync, "stream synchronize");
     return HAI_OK;
 }
 
@@ -622,8 +639,18 @@ int Engine::prefill_chunks(const int32_t* ids, int64_t P, uint16_t* hidden_out, 
     return HAI_OK;
 }
 
+int Engine::check_ids(const int32_t* ids, int64_t n, const char* what) {
+    if (n > 0 && ids == nullptr) return fail(HAI_ERR_INVALID_ARGUMENT, std::string(what) + ": null token ids");
+    for (int64_t i = 0; i < n; ++i)
+        if (ids[i] < 0 || ids[i] >= d_.V)
+            return fail(HAI_ERR_INVALID_ARGUMENT, std::string(what) + ": token id " + std::to_string(ids[i]) +
+                                                      " outside the vocabulary");
+    return HAI_OK;
+}
+
 int Engine::forward_rows(const int32_t* ids, int64_t T, uint16_t* hidden, uint16_t* logits) {
     if (T <= 0 || T > cap_) return fail(HAI_ERR_INVALID_ARGUMENT, "forward_rows: T out of range");
+    HAI_TRY(check_ids(ids, B_ * T, "forward"));
     HAI_TRY(reset_state());
     HAI_TRY(prefill_chunks(ids, T, hidden, logits));
     return sync();
@@ -632,6 +659,7 @@ int Engine::forward_rows(const int32_t* ids, int64_t T, uint16_t* hidden, uint16
 int Engine::prefill(const int32_t* prompts, int64_t P, int64_t max_new) {
     if (P <= 0 || max_new <= 0 || P + max_new + tmax_ > cap_)
         return fail(HAI_ERR_INVALID_ARGUMENT, "prefill: prompt + max_new exceeds max_context");
+    HAI_TRY(check_ids(prompts, B_ * P, "prefill"));
     HAI_TRY(reset_state());
     HAI_TRY(prefill_chunks(prompts, P, nullptr, nullptr));
     std::vector<int64_t> next(static_cast<size_t>(B_));
@@ -673,7 +701,7 @@ int Engine::replay(void** slot, F&& enqueue) {
         void* exec = nullptr;
         const int rc_end = hai_graph_end_capture(stream_, &exec);
         if (rc != HAI_OK) return rc;
-        if (rc_end != HAI_OK) return fail(rc_end, "graph capture");
+        if (rc_end != HAI_OK) return lib_fail(rc_end, "graph capture");
         *slot = exec;
     }
     HAI_TRY(hai_graph_launch(*slot, stream_));
@@ -909,6 +937,7 @@ int Engine::generate_speculative(const int32_t* prompts, int64_t P, int64_t max_
                                  int64_t n_override, int32_t* out, hai_spec_stats* stats, int32_t* round_log,
                                  int64_t round_log_cap, int64_t* n_out) {
     if (width < 1) return fail(HAI_ERR_INVALID_ARGUMENT, "width must be >= 1");
+    if (override_tokens != nullptr) HAI_TRY(check_ids(override_tokens, B_ * n_override, "draft override"));
     // a finished sequence keeps running with the batch: leave room for its
     // rows until the slowest sequence ends
     if (B_ > 1 && P + (width + 2) * max_new + tmax_ > cap_)

@@ -170,7 +170,11 @@ private:
         int64_t* n_log = nullptr;                  // [B] records written
     };
 
-    int fail(int rc, const std::string& what);
+    int fail(int rc, const std::string& what);       // the engine's own message
+    int lib_fail(int rc, const std::string& what);   // what + the kernel library's last error
+    int propagate(int rc, const char* what, uint64_t seq_before);
+    // every id in [0, vocab): token ids index the embedding table
+    int check_ids(const int32_t* ids, int64_t n, const char* what);
     int alloc_all();
     int reset_state();
     int upload_rope_tables();
@@ -213,6 +217,7 @@ private:
     Dims d_{};
     bool ok_ = false;
     std::string error_;
+    uint64_t err_seq_ = 0;  // bumped by every failure report
 
     void* stream_ = nullptr;
     void* weights_ = nullptr;
