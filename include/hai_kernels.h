@@ -361,6 +361,25 @@ int hai_gemm_bf16_mfma(void* y, int64_t ldy, const void* x, int64_t ldx,
                        const void* w, int64_t M, int64_t N, int64_t K,
                        int epilogue, const void* res, int64_t ld_res,
                        void* workspace, size_t workspace_bytes, void* stream);
+/* Epilogue flag for the MFMA GEMMs with HAI_EPI_RESIDUAL: when the call
+ * splits K (hai_gemm_mfma_splits > 1) it leaves the fp32 partials
+ * [splits][M][N] at the start of the workspace instead of finishing y; the
+ * caller completes y = res (in place) with hai_mfma_residual_rmsnorm_bf16.
+ * With one split the call finishes y itself. */
+enum { HAI_MFMA_KEEP_PARTIALS = 0x200 };
+/* The number of K splits the MFMA GEMM takes for this shape and workspace. */
+int hai_gemm_mfma_splits(int64_t M, int64_t N, int64_t K, const void* workspace,
+                         size_t workspace_bytes);
+/* Completes a residual MFMA GEMM called with HAI_MFMA_KEEP_PARTIALS, fused
+ * with the RMSNorm(+1 when unit_offset) that follows it in the decoder
+ * (qwen_reference.cc:108-144): h[M, N] (the residual, ld h) becomes
+ * bf16(h + bf16(sum of the partials in split order)), bit-identical to the
+ * unfused call, and xn = hai_rmsnorm_bf16(h) bit for bit; norm_w null skips
+ * the norm.  N % 8 == 0, N <= 8192, M <= 128, splits <= 4. */
+int hai_mfma_residual_rmsnorm_bf16(void* h, int64_t ldh, const void* workspace,
+                                   int64_t M, int64_t N, int64_t splits,
+                                   const void* norm_w, float eps, int unit_offset,
+                                   void* xn, int64_t ld_xn, void* stream);
 
 /* ------------------------------------------------------------------ synthetic data / checks
  * Synthetic weights: element (r, c) of a [rows, cols] tensor (row stride

@@ -98,3 +98,43 @@ def test_27b_batch_equals_single_sequences():
     for b in range(B):
         assert list(got[b][0]) == list(want[b][0]) == list(g[b]), b
         assert np.array_equal(got[b][2], want[b][2]), b
+
+
+@pytest.mark.parametrize("fp8", [False, True], ids=["bf16", "fp8"])
+def test_27b_mfma_batch_logits_within_rounding_sensitivity(fp8):
+    """The C4 / C5 tolerance mode at the 27B shape: a batch forward whose
+    GEMMs run on the matrix cores (32 rows per launch, narrow layers split K
+    and finish inside the next RMSNorm) against the bit-exact engine.
+
+    64 layers of random weights amplify any rounding-level change: scaling
+    every weight by (1 + 2^-8), half a bf16 ulp, moves the logits by ~0.1 on
+    average (measured on MI355X: 0.108 bf16, 0.339 FP8), so the 2e-2 / 1e-2
+    logit bound, met at the tiny depth (tests/test_gpu_engine_batch.py), is
+    not a property any differently-rounded path can have here.  The bound
+    checked is that the matrix-core path moves the logits no more than that
+    half-ulp weight change does (measured: 0.060 / 0.056 mean)."""
+    from hybridai_amd import engine as E
+    B, T = 2, 16
+    prompts = np.stack([E.synthetic_prompt(30 + b, T, E.QWEN27B["vocab"]) for b in range(B)])
+
+    def exact_logits(std):
+        eng = E.Engine(E.QWEN27B, max_context=T + 32, max_verify_tokens=16, fp8=fp8)
+        try:
+            eng.init_synthetic(seed=0, std=std)
+            return np.stack([hai.bf16_to_f32(eng.forward(prompts[b])[1]) for b in range(B)])
+        finally:
+            eng.close()
+
+    want = exact_logits(0.02)
+    nudged = exact_logits(0.02 * (1 + 2 ** -8))
+    eng = E.Engine(E.QWEN27B, max_context=T + 32, max_verify_tokens=16, fp8=fp8, batch=B, mfma=True)
+    try:
+        eng.init_synthetic(seed=0, std=0.02)
+        got = hai.bf16_to_f32(eng.forward_batch(prompts)[1])
+    finally:
+        eng.close()
+    d_mfma, d_nudge = np.abs(got - want), np.abs(nudged - want)
+    assert np.isfinite(got).all()
+    assert d_mfma.mean() <= d_nudge.mean(), (float(d_mfma.mean()), float(d_nudge.mean()))
+    assert np.percentile(d_mfma, 99) <= np.percentile(d_nudge, 99)
+    assert np.mean(got.argmax(-1) == want.argmax(-1)) >= np.mean(nudged.argmax(-1) == want.argmax(-1))

@@ -841,3 +841,53 @@ def test_gemm_fp8_mfma_27b_shapes(M, N, K, epi):
     got = hai.bf16_to_f32(dy.download(np.uint16).reshape(M, ncols))
     scale = np.abs(want).max()
     assert np.allclose(got, want, rtol=2 ** -6, atol=2e-3 * scale), float(np.abs(got - want).max())
+
+
+@pytest.mark.parametrize("M,N,K,fp8", [(32, 5120, 6144, False), (64, 5120, 17408, True), (17, 1536, 4096, False),
+                                       (128, 5120, 2048, True)])
+def test_mfma_keep_partials_then_residual_rmsnorm(M, N, K, fp8):
+    """A residual MFMA GEMM that keeps its K-split partials, completed by
+    hai_mfma_residual_rmsnorm_bf16, equals the unfused call bit for bit, and
+    its normalised rows equal hai_rmsnorm_bf16 of them; without a norm weight
+    only the residual rows are written."""
+    rng = np.random.default_rng(M + N + K + fp8)
+    x, xb = rand_bf16(rng, (M, K))
+    h0, hb = rand_bf16(rng, (M, N))
+    nw, nwb = rand_bf16(rng, (N,), 0.02)
+    if fp8:
+        q, s = _fp8_weights(rng, N, K)
+        dq, ds = dev(q), dev(s)
+    else:
+        w, wb = rand_bf16(rng, (N, K), 0.02)
+        dw = dev(wb)
+    dx, dnw = dev(xb), dev(nwb)
+    wsb = kern().hai_gemm_mfma_workspace_bytes(M, N)
+    dws = out_buf(max(wsb, 16))
+    splits = kern().hai_gemm_mfma_splits(M, N, K, dws.ptr, wsb)
+    assert splits > 1
+
+    def gemm(dh, flags):
+        if fp8:
+            return kern().hai_gemm_fp8_mfma(dh.ptr, N, dx.ptr, K, dq.ptr, ds.ptr, None, M, N, K,
+                                            hai.EPI_RESIDUAL | hai.FP8_NO_SPECIAL_CODES | flags, dh.ptr, N,
+                                            dws.ptr, wsb, None)
+        return kern().hai_gemm_bf16_mfma(dh.ptr, N, dx.ptr, K, dw.ptr, M, N, K, hai.EPI_RESIDUAL | flags, dh.ptr, N,
+                                         dws.ptr, wsb, None)
+
+    ref_h, ref_xn = dev(hb), out_buf(M * N * 2)
+    hai.check(gemm(ref_h, 0), "unfused gemm")
+    hai.check(kern().hai_rmsnorm_bf16(ref_xn.ptr, N, ref_h.ptr, N, dnw.ptr, M, N, 1e-6, 1, None), "rmsnorm")
+    dh, dxn = dev(hb), out_buf(M * N * 2)
+    hai.check(gemm(dh, hai.MFMA_KEEP_PARTIALS), "gemm keeping partials")
+    hai.check(kern().hai_mfma_residual_rmsnorm_bf16(dh.ptr, N, dws.ptr, M, N, splits, dnw.ptr, 1e-6, 1, dxn.ptr, N,
+                                                    None), "residual rmsnorm")
+    assert_bits_equal(dh.download(np.uint16), hai.bf16_to_f32(ref_h.download(np.uint16)), "residual rows")
+    assert_bits_equal(dxn.download(np.uint16), hai.bf16_to_f32(ref_xn.download(np.uint16)), "normalised rows")
+    dh2 = dev(hb)
+    hai.check(gemm(dh2, hai.MFMA_KEEP_PARTIALS), "gemm keeping partials")
+    hai.check(kern().hai_mfma_residual_rmsnorm_bf16(dh2.ptr, N, dws.ptr, M, N, splits, None, 0.0, 0, None, 0, None),
+              "residual only")
+    assert_bits_equal(dh2.download(np.uint16), hai.bf16_to_f32(ref_h.download(np.uint16)), "residual rows, no norm")
+    # keeping partials is only for the residual epilogue
+    assert kern().hai_gemm_bf16_mfma(dh.ptr, N, dx.ptr, K, dx.ptr, M, N, K, hai.EPI_STORE | hai.MFMA_KEEP_PARTIALS,
+                                     None, 0, dws.ptr, wsb, None) == hai.ERR_INVALID

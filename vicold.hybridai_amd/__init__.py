@@ -31,6 +31,7 @@ F32P = ctypes.POINTER(ctypes.c_float)
 
 EPI_STORE, EPI_RESIDUAL, EPI_SILU_MUL = 0, 1, 2
 FP8_NO_SPECIAL_CODES = 0x100  # hai_gemm_fp8_bf16 epilogue flag: weights hold no 0x7F / 0xFF code
+MFMA_KEEP_PARTIALS = 0x200  # MFMA GEMM residual epilogue flag: leave the K-split partials
 # hai_status codes (include/hai_kernels.h)
 OK, ERR_INVALID, ERR_OOM, ERR_NOT_IMPLEMENTED, ERR_INVALID_DEVICE, ERR_BACKEND = 0, 1, 2, 3, 5, 9
 
@@ -93,6 +94,8 @@ _KERNEL_SIGS = {
     "hai_gemm_bf16_mfma": [VP, I64, VP, I64, VP, I64, I64, I64, ctypes.c_int, VP, I64, VP, ctypes.c_size_t, VP],
     "hai_gemm_fp8_mfma": [VP, I64, VP, I64, VP, VP, VP, I64, I64, I64, ctypes.c_int, VP, I64, VP, ctypes.c_size_t,
                           VP],
+    "hai_gemm_mfma_splits": [I64, I64, I64, VP, ctypes.c_size_t],
+    "hai_mfma_residual_rmsnorm_bf16": [VP, I64, VP, I64, I64, I64, VP, F32, ctypes.c_int, VP, I64, VP],
     "hai_fill_synthetic_bf16": [VP, I64, I64, I64, ctypes.c_uint64, ctypes.c_uint32, F32, VP],
     "hai_debug_math_f32": [VP, VP, I64, ctypes.c_int, VP],
 }

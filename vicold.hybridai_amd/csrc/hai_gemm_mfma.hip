@@ -193,6 +193,104 @@ __global__ void mfma_finalize_kernel(uint16_t* __restrict__ y, int64_t ldy, cons
     }
 }
 
+// The finalize pass of a residual GEMM fused with the RMSNorm(+offset) of
+// the same rows: one 256-thread block per row.  Thread t completes the
+// 8-column groups t, t + 256, ... (every load issued before the first use):
+// h = bf16(res + bf16(sum of the KSB partials in split order)) exactly as
+// mfma_finalize_kernel<HAI_EPI_RESIDUAL> writes it.  The row is staged in LDS
+// and the first wave takes the sum of squares in L64 order, then every
+// thread writes xn = bf16((h * inv) * (w + off)) exactly as rmsnorm_kernel
+// computes them (norm_w null: h only).
+constexpr int kMaxResidualNormCols = 8192;
+template <int G>
+__global__ __launch_bounds__(256) void mfma_residual_rmsnorm_kernel(uint16_t* __restrict__ h, int64_t ldh,
+                                                                    const float* __restrict__ part, int KSB,
+                                                                    int M, int N, const uint16_t* __restrict__ w,
+                                                                    float eps, float off, uint16_t* __restrict__ xn,
+                                                                    int64_t ldxn) {
+    __shared__ __align__(16) uint16_t hs[kMaxResidualNormCols];
+    __shared__ float s_inv;
+    const int tid = threadIdx.x;
+    const int64_t m = blockIdx.x;
+    uint16_t* hr = h + m * ldh;
+    float4 pa[G][4][2];  // [group][split][half]
+    u32x4 r[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const int k0 = (tid + 256 * g) * 8;
+        if (k0 >= N) continue;
+        r[g] = *reinterpret_cast<const u32x4*>(hr + k0);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            if (q < KSB) {
+                const float4* pq = reinterpret_cast<const float4*>(part + (static_cast<int64_t>(q) * M + m) * N + k0);
+                pa[g][q][0] = pq[0];
+                pa[g][q][1] = pq[1];
+            }
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const int k0 = (tid + 256 * g) * 8;
+        if (k0 >= N) continue;
+        float v[8] = {pa[g][0][0].x, pa[g][0][0].y, pa[g][0][0].z, pa[g][0][0].w,
+                      pa[g][0][1].x, pa[g][0][1].y, pa[g][0][1].z, pa[g][0][1].w};
+#pragma unroll
+        for (int q = 1; q < 4; ++q)
+            if (q < KSB) {
+                v[0] = v[0] + pa[g][q][0].x; v[1] = v[1] + pa[g][q][0].y;
+                v[2] = v[2] + pa[g][q][0].z; v[3] = v[3] + pa[g][q][0].w;
+                v[4] = v[4] + pa[g][q][1].x; v[5] = v[5] + pa[g][q][1].y;
+                v[6] = v[6] + pa[g][q][1].z; v[7] = v[7] + pa[g][q][1].w;
+            }
+        uint32_t o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint16_t lo = f2bf(lo_bf(r[g][e]) + bfr(v[2 * e]));
+            const uint16_t hi = f2bf(hi_bf(r[g][e]) + bfr(v[2 * e + 1]));
+            o[e] = static_cast<uint32_t>(lo) | (static_cast<uint32_t>(hi) << 16);
+        }
+        const u32x4 hv = u32x4{o[0], o[1], o[2], o[3]};
+        *reinterpret_cast<u32x4*>(hr + k0) = hv;
+        *reinterpret_cast<u32x4*>(hs + k0) = hv;
+    }
+    if (w == nullptr) return;
+    __syncthreads();
+    if (tid < 64) {
+        // the rmsnorm_kernel order: lane l takes elements c*512 + 8l .. + 7, c increasing
+        float acc = 0.0f;
+        for (int k0 = tid * 8; k0 < N; k0 += 512) {
+            const u32x4 hv = *reinterpret_cast<const u32x4*>(hs + k0);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float a = lo_bf(hv[q]);
+                const float b = hi_bf(hv[q]);
+                acc = fma_(a, a, acc);
+                acc = fma_(b, b, acc);
+            }
+        }
+        const float ss = wave_sum64(acc);
+        if (tid == 0) s_inv = 1.0f / csqrt(ss / static_cast<float>(N) + eps);
+    }
+    __syncthreads();
+    const float inv = s_inv;
+    uint16_t* xr = xn + m * ldxn;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const int k0 = (tid + 256 * g) * 8;
+        if (k0 >= N) continue;
+        const u32x4 hv = *reinterpret_cast<const u32x4*>(hs + k0);
+        const u32x4 wd = *reinterpret_cast<const u32x4*>(w + k0);
+        uint32_t o[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint16_t a = f2bf((lo_bf(hv[q]) * inv) * (lo_bf(wd[q]) + off));
+            const uint16_t b = f2bf((hi_bf(hv[q]) * inv) * (hi_bf(wd[q]) + off));
+            o[q] = static_cast<uint32_t>(a) | (static_cast<uint32_t>(b) << 16);
+        }
+        *reinterpret_cast<u32x4*>(xr + k0) = u32x4{o[0], o[1], o[2], o[3]};
+    }
+}
+
 // E4M3 codes (4 per word) -> 4 bf16 of the same values (exact: every E4M3
 // value, the reference's +-480 included, has at most 4 significant bits);
 // CHECK handles 0x7F / 0xFF, which the hardware conversion maps to NaN.
@@ -403,6 +501,7 @@ struct MfmaArgs {
     const int32_t* scale_rows = nullptr;
     int paired = 0;
     bool check = true;
+    bool keep = false;  // leave the K-split partials for hai_mfma_residual_rmsnorm_bf16
 };
 
 // LDS above the 64 KB default needs the attribute, once per kernel instance.
@@ -440,7 +539,7 @@ int launch_mfma(const MfmaArgs& a, hipStream_t s) {
                                             a.KSB);
         rc = launched("gemm_bf16_mfma_kernel");
     }
-    if (rc != HAI_OK || a.KSB == 1) return rc;
+    if (rc != HAI_OK || a.KSB == 1 || a.keep) return rc;
     const int64_t n = static_cast<int64_t>(a.M) * ((a.N + 1) / 2);
     mfma_finalize_kernel<EPI><<<dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s>>>(
         a.y, a.ldy, a.part, a.KSB, a.res, a.ldres, a.M, a.N);
@@ -465,18 +564,25 @@ extern "C" size_t hai_gemm_mfma_workspace_bytes(int64_t M, int64_t N) {
 
 namespace {
 
+// K split across blocks for narrow layers (measured on MI355X at M = 32:
+// N = 5120 4 splits +115 %, N = 16384 2 splits +9 %), if the workspace holds
+// the partials and every split gets at least two chunks.
+int choose_splits(int64_t M, int64_t N, int64_t K, const void* workspace, size_t workspace_bytes) {
+    const int64_t nck = (K + kChunk - 1) / kChunk;
+    int ksb = N <= 8192 ? 4 : (N <= 20480 ? 2 : 1);
+    while (ksb > 1 && (nck < 2 * ksb || workspace == nullptr ||
+                       workspace_bytes < static_cast<size_t>(int64_t{ksb} * M * N) * sizeof(float)))
+        ksb /= 2;
+    return ksb;
+}
+
 int mfma_entry(MfmaArgs& a, int epilogue, void* workspace, size_t workspace_bytes, hipStream_t s) {
     if (a.M == 0 || a.N == 0) return HAI_OK;
-    // K split across blocks for narrow layers (measured on MI355X at M = 32:
-    // N = 5120 4 splits +115 %, N = 16384 2 splits +9 %), if the workspace
-    // holds the partials and every split gets at least two chunks
-    const int64_t nck = (a.K + kChunk - 1) / kChunk;
-    int ksb = a.N <= 8192 ? 4 : (a.N <= 20480 ? 2 : 1);
-    while (ksb > 1 && (nck < 2 * ksb || workspace == nullptr ||
-                       workspace_bytes < static_cast<size_t>(int64_t{ksb} * a.M * a.N) * sizeof(float)))
-        ksb /= 2;
+    a.keep = (epilogue & HAI_MFMA_KEEP_PARTIALS) != 0;
+    epilogue &= ~HAI_MFMA_KEEP_PARTIALS;
+    if (a.keep && epilogue != HAI_EPI_RESIDUAL) return invalid("gemm_mfma: keeping partials needs the residual epilogue");
     a.part = static_cast<float*>(workspace);
-    a.KSB = ksb;
+    a.KSB = choose_splits(a.M, a.N, a.K, workspace, workspace_bytes);
     switch (epilogue) {
         case HAI_EPI_STORE:
             if (a.ldy < a.N) return invalid("gemm_mfma: ldy < N");
@@ -506,6 +612,40 @@ int check_mfma(const void* y, const void* x, const void* w, int64_t M, int64_t N
 }
 
 }  // namespace
+
+extern "C" int hai_gemm_mfma_splits(int64_t M, int64_t N, int64_t K, const void* workspace,
+                                    size_t workspace_bytes) {
+    if (M <= 0 || N <= 0 || K <= 0) return 1;
+    return choose_splits(M, N, K, workspace, workspace_bytes);
+}
+
+extern "C" int hai_mfma_residual_rmsnorm_bf16(void* h, int64_t ldh, const void* workspace, int64_t M, int64_t N,
+                                              int64_t splits, const void* norm_w, float eps, int unit_offset,
+                                              void* xn, int64_t ld_xn, void* stream) {
+    if (h == nullptr || workspace == nullptr) return invalid("mfma_residual_rmsnorm: null pointer");
+    if (M < 0 || M > kMaxMfmaRows || N <= 0 || N % 8 != 0 || N > kMaxResidualNormCols || ldh < N || ldh % 8 != 0 ||
+        splits < 1 || splits > 4)
+        return invalid("mfma_residual_rmsnorm: shape (need N % 8 == 0, N <= 8192, 1 <= splits <= 4)");
+    if (norm_w != nullptr && (xn == nullptr || ld_xn < N || ld_xn % 8 != 0 || !aligned16(norm_w) || !aligned16(xn)))
+        return invalid("mfma_residual_rmsnorm: normalised output needs xn, ld_xn >= N, 16-byte alignment");
+    if (!aligned16(h) || !aligned16(workspace)) return invalid("mfma_residual_rmsnorm: 16-byte alignment");
+    if (M == 0) return HAI_OK;
+    const dim3 grid(static_cast<unsigned>(M));
+    auto* hh = static_cast<uint16_t*>(h);
+    const auto* part = static_cast<const float*>(workspace);
+    const auto* w = static_cast<const uint16_t*>(norm_w);
+    auto* x = static_cast<uint16_t*>(xn);
+    const float off = unit_offset ? 1.0f : 0.0f;
+    const auto s = as_stream(stream);
+    const int n = int(N), m = int(M), k = int(splits);
+    if (N <= 2048)
+        mfma_residual_rmsnorm_kernel<1><<<grid, dim3(256), 0, s>>>(hh, ldh, part, k, m, n, w, eps, off, x, ld_xn);
+    else if (N <= 6144)
+        mfma_residual_rmsnorm_kernel<3><<<grid, dim3(256), 0, s>>>(hh, ldh, part, k, m, n, w, eps, off, x, ld_xn);
+    else
+        mfma_residual_rmsnorm_kernel<4><<<grid, dim3(256), 0, s>>>(hh, ldh, part, k, m, n, w, eps, off, x, ld_xn);
+    return launched("mfma_residual_rmsnorm_kernel");
+}
 
 extern "C" int hai_gemm_bf16_mfma(void* y, int64_t ldy, const void* x, int64_t ldx, const void* w, int64_t M,
                                   int64_t N, int64_t K, int epilogue, const void* res, int64_t ld_res,

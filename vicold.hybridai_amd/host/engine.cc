@@ -422,9 +422,34 @@ int64_t Engine::read_tensor(uint32_t id, uint16_t* out, int64_t capacity) {
     return -1;
 }
 
+int Engine::flush_pending() {
+    if (pending_.h == nullptr) return HAI_OK;
+    const PendingResidual p = pending_;
+    pending_ = PendingResidual{};
+    return hai_mfma_residual_rmsnorm_bf16(p.h, p.ld, mfma_ws_, p.M, p.N, p.splits, nullptr, 0.0f, 0, nullptr, 0,
+                                          stream_);
+}
+
 int Engine::gemm(uint16_t* y, int64_t ldy, const uint16_t* x, int64_t ldx, const Lin& w, int64_t M, int64_t N,
                  int64_t K, int epi, const uint16_t* res, int64_t ldres) {
+    HAI_TRY(flush_pending());  // the workspace is about to be reused
     if (prof_record_) prof_calls_.push_back({y, ldy, x, ldx, w, M, N, K, epi, res, ldres, nullptr, nullptr});
+    if (use_mfma(M) && epi == HAI_EPI_RESIDUAL && res == y && ldres == ldy && M <= 128 && N % 8 == 0 && N <= 8192 &&
+        !prof_record_) {
+        // residual in place: leave the split partials for the next RMSNorm
+        const int splits = hai_gemm_mfma_splits(M, N, K, mfma_ws_, mfma_ws_bytes_);
+        if (splits > 1) {
+            const int keep = HAI_EPI_RESIDUAL | HAI_MFMA_KEEP_PARTIALS;
+            if (w.q != nullptr)
+                HAI_TRY(hai_gemm_fp8_mfma(y, ldy, x, ldx, w.q, w.s, w.map, M, N, K, keep | HAI_FP8_NO_SPECIAL_CODES,
+                                          res, ldres, mfma_ws_, mfma_ws_bytes_, stream_));
+            else
+                HAI_TRY(hai_gemm_bf16_mfma(y, ldy, x, ldx, w.w, M, N, K, keep, res, ldres, mfma_ws_,
+                                           mfma_ws_bytes_, stream_));
+            pending_ = PendingResidual{y, ldy, M, N, splits};
+            return HAI_OK;
+        }
+    }
     if (use_mfma(M)) {
         for (int64_t m0 = 0; m0 < M; m0 += 128) {
             const int64_t mm = std::min<int64_t>(128, M - m0);
@@ -464,9 +489,19 @@ int Engine::norm_gemm(uint16_t* y, int64_t ldy, const uint16_t* x, const uint16_
     // do launches of more than 16 rows.
     if (N > kFusedNormMaxN || M > 16 || use_mfma(M)) {
         uint16_t* xn = xn_out != nullptr ? xn_out : xn_;
-        HAI_TRY(hai_rmsnorm_bf16(xn, H, x, H, nw, M, H, cfg_.rms_eps, 1, stream_));
+        if (pending_.h != nullptr && pending_.h == x && pending_.M == M && pending_.N == H && pending_.ld == H) {
+            // the previous residual GEMM's split sum, residual add and this norm in one launch
+            const PendingResidual p = pending_;
+            pending_ = PendingResidual{};
+            HAI_TRY(hai_mfma_residual_rmsnorm_bf16(p.h, p.ld, mfma_ws_, M, H, p.splits, nw, cfg_.rms_eps, 1, xn, H,
+                                                   stream_));
+        } else {
+            HAI_TRY(flush_pending());
+            HAI_TRY(hai_rmsnorm_bf16(xn, H, x, H, nw, M, H, cfg_.rms_eps, 1, stream_));
+        }
         return gemm(y, ldy, xn, H, w, M, N, H, epi, res, ldres);
     }
+    HAI_TRY(flush_pending());
     // Above the fused limit the call runs RMSNorm then GEMM through xn_.
     if (xn_out == nullptr && M * H > HAI_GEMM_RMSNORM_FUSED_MAX) xn_out = xn_;
     if (prof_record_) prof_calls_.push_back({y, ldy, x, H, w, M, N, H, epi, res, ldres, nw, xn_out});
@@ -527,6 +562,8 @@ int Engine::mlp(const LayerWeights& L, int64_t T, uint16_t* h) {
 // on top of its committed caches; hf_ = post-final-norm hidden, logits_ =
 // lm_head.  Committed lengths are not advanced here.
 int Engine::forward_target(const int64_t* d_ids, int64_t T, bool write_all_slots) {
+    pending_ = PendingResidual{};  // a forward ends with a norm, which completes any residual; only
+                                   // a failed one leaves a record, for rows this forward overwrites
     const auto& d = d_;
     const int64_t rows = B_ * T;
     HAI_TRY(hai_embedding_gather_bf16(h_, embed_, d_ids, rows, d.V, d.H, stream_));
@@ -564,6 +601,8 @@ int Engine::forward_target(const int64_t* d_ids, int64_t T, bool write_all_slots
 // (generator.cc:673-699, 977-1003), so the cache state is identical.  T rows
 // per sequence; add_len advances every MTP length by T.
 int Engine::mtp_kv_rows(const int64_t* d_ids, const uint16_t* d_hidden, int64_t T, bool add_len) {
+    pending_ = PendingResidual{};  // a forward ends with a norm, which completes any residual; only
+                                   // a failed one leaves a record, for rows this forward overwrites
     const auto& d = d_;
     const int64_t rows = B_ * T;
     HAI_TRY(hai_embedding_gather_bf16(emb_, embed_, d_ids, rows, d.V, d.H, stream_));
@@ -585,6 +624,8 @@ int Engine::mtp_kv_rows(const int64_t* d_ids, const uint16_t* d_hidden, int64_t 
 // sequence, lm_head and argmax (generator.cc:784-811).  d_id / d_cand are
 // [B], d_hin / d_mh [B][H]; every MTP cache grows by one row.
 int Engine::mtp_draft_step(const int64_t* d_id, const uint16_t* d_hin, uint16_t* d_mh, int64_t* d_cand) {
+    pending_ = PendingResidual{};  // a forward ends with a norm, which completes any residual; only
+                                   // a failed one leaves a record, for rows this forward overwrites
     const auto& d = d_;
     HAI_TRY(hai_embedding_gather_bf16(emb_, embed_, d_id, B_, d.V, d.H, stream_));
     HAI_TRY(hai_rmsnorm_bf16(xn_, 2 * d.H, emb_, d.H, pre_emb_, B_, d.H, cfg_.rms_eps, 1, stream_));

@@ -185,6 +185,16 @@ private:
     // mode (hai_engine_options::mfma) and M >= kMfmaMinRows.
     static constexpr int64_t kMfmaMinRows = 4;
     bool use_mfma(int64_t M) const { return mfma_ && M >= kMfmaMinRows; }
+    // A residual MFMA GEMM whose K-split partials wait in the workspace: the
+    // RMSNorm of the same rows completes them (hai_mfma_residual_rmsnorm_bf16)
+    // in one launch; anything else completes them first (flush_pending).
+    struct PendingResidual {
+        uint16_t* h = nullptr;
+        int64_t ld = 0, M = 0, N = 0;
+        int splits = 0;
+    };
+    PendingResidual pending_;
+    int flush_pending();
     int gemm(uint16_t* y, int64_t ldy, const uint16_t* x, int64_t ldx, const Lin& w, int64_t M, int64_t N,
              int64_t K, int epi, const uint16_t* res, int64_t ldres);
     // RMSNorm(+1) of the H-wide rows x (norm weight nw) fused into the linear
