@@ -204,6 +204,21 @@ int hai_kv_rmsnorm_rope_append_bf16(void* k_cache, void* v_cache, int64_t cap,
                                     int64_t T, int64_t nkv, int64_t D,
                                     int64_t R, const int32_t* lens,
                                     int32_t pos_add, float eps, void* stream);
+/* Both of the above in one launch for the attention projection rows
+ * [q+gate (2 nq D) | k (nkv D) | v (nkv D)] of src (the layout of the fused
+ * q|gate|k|v Linear): the same outputs bit for bit, one kernel instead of
+ * two. */
+int hai_qkv_rmsnorm_rope_append_bf16(void* q_out, void* gate_out,
+                                     void* k_cache, void* v_cache, int64_t cap,
+                                     const void* src, int64_t ld_src,
+                                     const void* q_norm, const void* k_norm,
+                                     const float* rope_cos,
+                                     const float* rope_sin,
+                                     int64_t rope_positions, int64_t B,
+                                     int64_t T, int64_t nq, int64_t nkv,
+                                     int64_t D, int64_t R,
+                                     const int32_t* lens, int32_t pos_add,
+                                     float eps, void* stream);
 /* partial_rope_kernel (hip_kernels.hip:192-221) as called by
  * Backend::partial_rope: rotate-half on the first R dims of each of the
  * `heads` D-wide heads of T rows, position pos0 + t, dims past R copied;

@@ -288,6 +288,39 @@ def test_kv_norm_rope_append(B, T, nkv, D, R):
         assert not K_[b, :p].any() and not K_[b, p + T:].any()
 
 
+@pytest.mark.parametrize("B,T,nq,nkv,D,R", [(1, 2, 24, 4, 256, 64), (2, 3, 4, 2, 64, 16), (3, 1, 6, 1, 128, 128)])
+def test_qkv_norm_rope_append_equals_the_two_launches(B, T, nq, nkv, D, R):
+    """hai_qkv_rmsnorm_rope_append_bf16 on [q+gate | k | v] projection rows
+    writes the same q, gate and cache rows as the q/gate and K/V launches."""
+    rng = np.random.default_rng(B * 7 + T + nq + D)
+    cap, base = 48, 1e7
+    ld = (2 * nq + 2 * nkv) * D
+    src, sb = rand_bf16(rng, (B * T, ld))
+    wq, wqb = rand_bf16(rng, (D,), 0.02)
+    wk, wkb = rand_bf16(rng, (D,), 0.02)
+    lens = np.array([5 + 11 * b for b in range(B)], np.int32)
+    cd, sd = _rope_dev(cap, R, base)
+    dsrc, dwq, dwk, dl = dev(sb), dev(wqb), dev(wkb), dev(lens)
+    outs = []
+    for fused in (False, True):
+        q, g = out_buf(B * T * nq * D * 2), out_buf(B * T * nq * D * 2)
+        kc, vc = out_buf(B * cap * nkv * D * 2), out_buf(B * cap * nkv * D * 2)
+        if fused:
+            hai.check(kern().hai_qkv_rmsnorm_rope_append_bf16(q.ptr, g.ptr, kc.ptr, vc.ptr, cap, dsrc.ptr, ld,
+                                                               dwq.ptr, dwk.ptr, cd.ptr, sd.ptr, cap, B, T, nq, nkv,
+                                                               D, R, dl.ptr, 0, 1e-6, None), "qkv")
+        else:
+            hai.check(kern().hai_q_gate_rmsnorm_rope_bf16(q.ptr, g.ptr, dsrc.ptr, ld, dwq.ptr, cd.ptr, sd.ptr, cap,
+                                                           B, T, nq, D, R, dl.ptr, 0, 1e-6, None), "q gate")
+            ks = dsrc.ptr + 2 * nq * D * 2
+            hai.check(kern().hai_kv_rmsnorm_rope_append_bf16(kc.ptr, vc.ptr, cap, ks, ks + nkv * D * 2, ld, dwk.ptr,
+                                                             cd.ptr, sd.ptr, cap, B, T, nkv, D, R, dl.ptr, 0, 1e-6,
+                                                             None), "kv")
+        outs.append([buf.download(np.uint16) for buf in (q, g, kc, vc)])
+    for name, a, b in zip(("q", "gate", "k cache", "v cache"), outs[0], outs[1]):
+        assert np.array_equal(a, b), name
+
+
 # ----------------------------------------------------------------- attention
 @pytest.mark.parametrize("B,T,nq,nkv,D,lens", [
     (1, 2, 4, 2, 64, [30]), (1, 1, 4, 2, 64, [0]), (1, 4, 24, 4, 256, [60]), (1, 2, 24, 4, 256, [1278]),

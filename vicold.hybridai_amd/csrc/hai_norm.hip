@@ -80,16 +80,12 @@ __device__ __forceinline__ float rope_at(const float* row, int d, int R, const f
 
 // q_gate_rmsnorm_rope_kernel (hip_fused_kernels.hip:87-141): one wave per
 // (row, head); q is normalised with (w+1), rotated and stored once; the gate
-// half is copied.
-__global__ __launch_bounds__(256) void q_gate_rmsnorm_rope_kernel(
-    uint16_t* __restrict__ q_out, uint16_t* __restrict__ g_out, const uint16_t* __restrict__ src,
-    int64_t ld_src, const uint16_t* __restrict__ wq, const float* __restrict__ rc,
-    const float* __restrict__ rs, int64_t rope_pos, int B, int T, int nq, int D, int R,
-    const int32_t* lens, int pos_add, float eps) {
-    __shared__ float qn[4][kMaxHeadDim];
+// half is copied.  `pair` = row * nq + head of this wave; qn = its LDS row.
+__device__ __forceinline__ void q_gate_rmsnorm_rope_pair(
+    uint16_t* __restrict__ q_out, uint16_t* __restrict__ g_out, const uint16_t* __restrict__ src, int64_t ld_src,
+    const uint16_t* __restrict__ wq, const float* __restrict__ rc, const float* __restrict__ rs, int64_t rope_pos,
+    int B, int T, int nq, int D, int R, const int32_t* lens, int pos_add, float eps, int64_t pair, float* qn) {
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int64_t pair = static_cast<int64_t>(blockIdx.x) * 4 + wave;
     const bool active = pair < static_cast<int64_t>(B) * T * nq;
     int64_t m = 0;
     int h = 0;
@@ -101,7 +97,7 @@ __global__ __launch_bounds__(256) void q_gate_rmsnorm_rope_kernel(
         s = src + m * ld_src + static_cast<int64_t>(h) * 2 * D;
         const float ss = l64_sumsq_bf16(s, D, lane);
         inv = 1.0f / csqrt(ss / static_cast<float>(D) + eps);
-        for (int d = lane; d < D; d += 64) qn[wave][d] = (bf2f(s[d]) * inv) * (bf2f(wq[d]) + 1.0f);
+        for (int d = lane; d < D; d += 64) qn[d] = (bf2f(s[d]) * inv) * (bf2f(wq[d]) + 1.0f);
     }
     __syncthreads();
     if (!active) return;
@@ -114,24 +110,20 @@ __global__ __launch_bounds__(256) void q_gate_rmsnorm_rope_kernel(
     uint16_t* qo = q_out + (m * nq + h) * D;
     uint16_t* go = g_out + (m * nq + h) * D;
     for (int d = lane; d < D; d += 64) {
-        qo[d] = f2bf(rope_at(qn[wave], d, R, cs, sn));
+        qo[d] = f2bf(rope_at(qn, d, R, cs, sn));
         go[d] = s[D + d];
     }
 }
 
 // K path (attention.cc:459-464) fused with append_kv_cache_kernel
 // (hip_kernels.hip:295-308): kn = bf16(k*inv*(w+1)), then bf16(rope(kn))
-// written to the cache row; V copied unchanged.
-__global__ __launch_bounds__(256) void kv_rmsnorm_rope_append_kernel(
-    uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int64_t cap,
-    const uint16_t* __restrict__ sk, const uint16_t* __restrict__ sv, int64_t ld_src,
-    const uint16_t* __restrict__ wk, const float* __restrict__ rc, const float* __restrict__ rs,
-    int64_t rope_pos, int B, int T, int nkv, int D, int R, const int32_t* lens, int pos_add,
-    float eps) {
-    __shared__ float kn[4][kMaxHeadDim];
+// written to the cache row; V copied unchanged.  `pair` = row * nkv + head.
+__device__ __forceinline__ void kv_rmsnorm_rope_append_pair(
+    uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int64_t cap, const uint16_t* __restrict__ sk,
+    const uint16_t* __restrict__ sv, int64_t ld_src, const uint16_t* __restrict__ wk, const float* __restrict__ rc,
+    const float* __restrict__ rs, int64_t rope_pos, int B, int T, int nkv, int D, int R, const int32_t* lens,
+    int pos_add, float eps, int64_t pair, float* kn) {
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int64_t pair = static_cast<int64_t>(blockIdx.x) * 4 + wave;
     const bool active = pair < static_cast<int64_t>(B) * T * nkv;
     int64_t m = 0;
     int h = 0;
@@ -141,7 +133,7 @@ __global__ __launch_bounds__(256) void kv_rmsnorm_rope_append_kernel(
         const uint16_t* s = sk + m * ld_src + static_cast<int64_t>(h) * D;
         const float ss = l64_sumsq_bf16(s, D, lane);
         const float inv = 1.0f / csqrt(ss / static_cast<float>(D) + eps);
-        for (int d = lane; d < D; d += 64) kn[wave][d] = bfr((bf2f(s[d]) * inv) * (bf2f(wk[d]) + 1.0f));
+        for (int d = lane; d < D; d += 64) kn[d] = bfr((bf2f(s[d]) * inv) * (bf2f(wk[d]) + 1.0f));
     }
     __syncthreads();
     if (!active) return;
@@ -155,8 +147,58 @@ __global__ __launch_bounds__(256) void kv_rmsnorm_rope_append_kernel(
     const int64_t dst = ((static_cast<int64_t>(b) * cap + pos) * nkv + h) * D;
     const uint16_t* v = sv + m * ld_src + static_cast<int64_t>(h) * D;
     for (int d = lane; d < D; d += 64) {
-        kc[dst + d] = f2bf(rope_at(kn[wave], d, R, cs, sn));
+        kc[dst + d] = f2bf(rope_at(kn, d, R, cs, sn));
         vc[dst + d] = v[d];
+    }
+}
+
+__global__ __launch_bounds__(256) void q_gate_rmsnorm_rope_kernel(
+    uint16_t* __restrict__ q_out, uint16_t* __restrict__ g_out, const uint16_t* __restrict__ src,
+    int64_t ld_src, const uint16_t* __restrict__ wq, const float* __restrict__ rc,
+    const float* __restrict__ rs, int64_t rope_pos, int B, int T, int nq, int D, int R,
+    const int32_t* lens, int pos_add, float eps) {
+    __shared__ float qn[4][kMaxHeadDim];
+    const int wave = threadIdx.x >> 6;
+    q_gate_rmsnorm_rope_pair(q_out, g_out, src, ld_src, wq, rc, rs, rope_pos, B, T, nq, D, R, lens, pos_add, eps,
+                             static_cast<int64_t>(blockIdx.x) * 4 + wave, qn[wave]);
+}
+
+__global__ __launch_bounds__(256) void kv_rmsnorm_rope_append_kernel(
+    uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int64_t cap,
+    const uint16_t* __restrict__ sk, const uint16_t* __restrict__ sv, int64_t ld_src,
+    const uint16_t* __restrict__ wk, const float* __restrict__ rc, const float* __restrict__ rs,
+    int64_t rope_pos, int B, int T, int nkv, int D, int R, const int32_t* lens, int pos_add,
+    float eps) {
+    __shared__ float kn[4][kMaxHeadDim];
+    const int wave = threadIdx.x >> 6;
+    kv_rmsnorm_rope_append_pair(kc, vc, cap, sk, sv, ld_src, wk, rc, rs, rope_pos, B, T, nkv, D, R, lens, pos_add,
+                                eps, static_cast<int64_t>(blockIdx.x) * 4 + wave, kn[wave]);
+}
+
+// Both of the above in one launch: the first qblocks blocks take the q /
+// gate heads, the rest the K / V heads (the two are independent).
+struct QkvNormArgs {
+    uint16_t *q_out, *g_out, *kc, *vc;
+    const uint16_t *src, *wq, *wk;
+    int64_t ld_src, cap, rope_pos;
+    const float *rc, *rs;
+    const int32_t* lens;
+    int B, T, nq, nkv, D, R, pos_add, qblocks;
+    float eps;
+};
+__global__ __launch_bounds__(256) void qkv_rmsnorm_rope_append_kernel(QkvNormArgs a) {
+    __shared__ float buf[4][kMaxHeadDim];
+    const int wave = threadIdx.x >> 6;
+    if (static_cast<int>(blockIdx.x) < a.qblocks) {
+        q_gate_rmsnorm_rope_pair(a.q_out, a.g_out, a.src, a.ld_src, a.wq, a.rc, a.rs, a.rope_pos, a.B, a.T, a.nq,
+                                 a.D, a.R, a.lens, a.pos_add, a.eps, static_cast<int64_t>(blockIdx.x) * 4 + wave,
+                                 buf[wave]);
+    } else {
+        const uint16_t* sk = a.src + 2 * static_cast<int64_t>(a.nq) * a.D;
+        const uint16_t* sv = sk + static_cast<int64_t>(a.nkv) * a.D;
+        kv_rmsnorm_rope_append_pair(a.kc, a.vc, a.cap, sk, sv, a.ld_src, a.wk, a.rc, a.rs, a.rope_pos, a.B, a.T,
+                                    a.nkv, a.D, a.R, a.lens, a.pos_add, a.eps,
+                                    static_cast<int64_t>(blockIdx.x - a.qblocks) * 4 + wave, buf[wave]);
     }
 }
 
@@ -325,6 +367,48 @@ int hai_kv_rmsnorm_rope_append_bf16(void* k_cache, void* v_cache, int64_t cap, c
         static_cast<const uint16_t*>(k_norm), rope_cos, rope_sin, rope_positions, int(B), int(T), int(nkv),
         int(D), int(R), lens, pos_add, eps);
     return launched("kv_rmsnorm_rope_append_kernel");
+}
+
+int hai_qkv_rmsnorm_rope_append_bf16(void* q_out, void* gate_out, void* k_cache, void* v_cache, int64_t cap,
+                                     const void* src, int64_t ld_src, const void* q_norm, const void* k_norm,
+                                     const float* rope_cos, const float* rope_sin, int64_t rope_positions,
+                                     int64_t B, int64_t T, int64_t nq, int64_t nkv, int64_t D, int64_t R,
+                                     const int32_t* lens, int32_t pos_add, float eps, void* stream) {
+    if (q_out == nullptr || gate_out == nullptr || k_cache == nullptr || v_cache == nullptr || src == nullptr ||
+        q_norm == nullptr || k_norm == nullptr || rope_cos == nullptr || rope_sin == nullptr)
+        return invalid("qkv_rmsnorm_rope_append: null pointer");
+    if (cap <= 0 || B < 0 || T < 0 || nq <= 0 || nkv <= 0 || D <= 0 || D % 8 != 0 || D > kMaxHeadDim || R < 0 ||
+        R > D || R % 2 != 0 || ld_src < (2 * nq + 2 * nkv) * D || rope_positions <= 0)
+        return invalid("qkv_rmsnorm_rope_append: shape");
+    if (!aligned16(src) || ld_src % 8 != 0) return invalid("qkv_rmsnorm_rope_append: alignment");
+    const int64_t qpairs = B * T * nq, kvpairs = B * T * nkv;
+    if (qpairs == 0) return HAI_OK;
+    QkvNormArgs a;
+    a.q_out = static_cast<uint16_t*>(q_out);
+    a.g_out = static_cast<uint16_t*>(gate_out);
+    a.kc = static_cast<uint16_t*>(k_cache);
+    a.vc = static_cast<uint16_t*>(v_cache);
+    a.src = static_cast<const uint16_t*>(src);
+    a.wq = static_cast<const uint16_t*>(q_norm);
+    a.wk = static_cast<const uint16_t*>(k_norm);
+    a.ld_src = ld_src;
+    a.cap = cap;
+    a.rope_pos = rope_positions;
+    a.rc = rope_cos;
+    a.rs = rope_sin;
+    a.lens = lens;
+    a.B = int(B);
+    a.T = int(T);
+    a.nq = int(nq);
+    a.nkv = int(nkv);
+    a.D = int(D);
+    a.R = int(R);
+    a.pos_add = pos_add;
+    a.qblocks = int((qpairs + 3) / 4);
+    a.eps = eps;
+    const unsigned blocks = static_cast<unsigned>(a.qblocks + (kvpairs + 3) / 4);
+    qkv_rmsnorm_rope_append_kernel<<<dim3(blocks), dim3(256), 0, as_stream(stream)>>>(a);
+    return launched("qkv_rmsnorm_rope_append_kernel");
 }
 
 int hai_partial_rope_bf16(void* dst, const void* src, int64_t T, int64_t heads, int64_t D, int64_t R,
