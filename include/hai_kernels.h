@@ -321,7 +321,8 @@ int hai_argmax_rows_bf16(int64_t* out, const void* logits, int64_t ld,
  *   next[b] = preds[b*T+a] (the target token after the committed rows);
  *   hidden row a is copied to rec_hidden[b] and, on full acceptance, row
  *   T-1 to h_prev[b].
- * n_draft holds k_b per sequence (T - 1 for every b when NULL). */
+ * n_draft holds k_b per sequence (T - 1 for every b when NULL); B <= 64
+ * sequences of T <= 64 rows, one block per sequence. */
 int hai_verify_argmax_accept_bf16(const void* logits, int64_t V,
                                   const void* hidden, int64_t H,
                                   const int64_t* ids, const int32_t* n_draft,

@@ -15,6 +15,7 @@ namespace {
 using namespace hai;
 
 constexpr int kSlices = 64;  // partial blocks per row
+constexpr int kMaxAcceptRows = 64;  // verify rows (k + 1) per sequence
 
 __device__ __forceinline__ uint64_t make_key(float v, int64_t idx) {
     if (!(v > __uint_as_float(0xff800000u))) return 0ull;  // NaN or -inf
@@ -78,49 +79,50 @@ __global__ __launch_bounds__(256) void argmax_final_kernel(int64_t* __restrict__
     }
 }
 
-// One block: final argmax of the B*T verify rows, then per sequence the
-// accepted prefix, the committed-length update and the hidden-row copies.
+// One block per sequence b: the final argmax of its T verify rows, its
+// accepted prefix, the committed-length update and its hidden-row copies.
 __global__ __launch_bounds__(256) void verify_accept_kernel(
     const uint64_t* __restrict__ part, const uint16_t* __restrict__ hidden, int64_t H,
     const int64_t* __restrict__ ids, const int32_t* n_draft, int B, int T, int64_t* __restrict__ preds,
     int32_t* __restrict__ result, int32_t* target_len, int32_t* mtp_len, int64_t* __restrict__ next,
     uint16_t* rec_hidden, uint16_t* h_prev) {
-    __shared__ int acc_sh[64];
-    __shared__ int full_sh[64];
-    const int rows = B * T;
-    for (int r = threadIdx.x; r < rows; r += blockDim.x) {
+    __shared__ int64_t pred_sh[kMaxAcceptRows];
+    __shared__ int acc_sh, full_sh;
+    const int b = blockIdx.x;
+    for (int t = threadIdx.x; t < T; t += blockDim.x) {
+        const int64_t r = static_cast<int64_t>(b) * T + t;
         uint64_t best = 0ull;
         for (int s = 0; s < kSlices; ++s) {
-            const uint64_t k = part[static_cast<int64_t>(r) * kSlices + s];
+            const uint64_t k = part[r * kSlices + s];
             best = k > best ? k : best;
         }
-        preds[r] = key_index(best);
+        const int64_t p = key_index(best);
+        preds[r] = p;
+        pred_sh[t] = p;
     }
     __syncthreads();
-    for (int b = threadIdx.x; b < B; b += blockDim.x) {
+    if (threadIdx.x == 0) {
         const int k = n_draft ? n_draft[b] : T - 1;
         int a = 0;
-        while (a < k && preds[b * T + a] == ids[b * T + 1 + a]) ++a;
+        while (a < k && pred_sh[a] == ids[static_cast<int64_t>(b) * T + 1 + a]) ++a;
         const int full = a == k ? 1 : 0;
         result[b * 4 + 0] = a;
         result[b * 4 + 1] = full;
-        result[b * 4 + 2] = static_cast<int32_t>(ids[b * T]);
-        result[b * 4 + 3] = static_cast<int32_t>(preds[b * T + a]);
+        result[b * 4 + 2] = static_cast<int32_t>(ids[static_cast<int64_t>(b) * T]);
+        result[b * 4 + 3] = static_cast<int32_t>(pred_sh[a]);
         if (target_len) target_len[b] += a + 1;
         if (mtp_len && !full) mtp_len[b] -= k - a;
-        next[b] = preds[b * T + a];
-        if (b < 64) { acc_sh[b] = a; full_sh[b] = full; }
+        next[b] = pred_sh[a];
+        acc_sh = a;
+        full_sh = full;
     }
     __syncthreads();
     if (hidden == nullptr) return;
-    for (int b = 0; b < B && b < 64; ++b) {
-        const int a = acc_sh[b];
-        const uint16_t* src = hidden + (static_cast<int64_t>(b) * T + a) * H;
-        if (rec_hidden)
-            for (int64_t k = threadIdx.x; k < H; k += blockDim.x) rec_hidden[b * H + k] = src[k];
-        if (h_prev && full_sh[b])
-            for (int64_t k = threadIdx.x; k < H; k += blockDim.x) h_prev[b * H + k] = src[k];
-    }
+    const uint16_t* src = hidden + (static_cast<int64_t>(b) * T + acc_sh) * H;
+    if (rec_hidden)
+        for (int64_t k = threadIdx.x; k < H; k += blockDim.x) rec_hidden[b * H + k] = src[k];
+    if (h_prev && full_sh)
+        for (int64_t k = threadIdx.x; k < H; k += blockDim.x) h_prev[b * H + k] = src[k];
 }
 
 __global__ void add_i32_kernel(int32_t* dst, const int32_t* delta, int32_t add, int64_t n) {
@@ -210,14 +212,15 @@ int hai_verify_argmax_accept_bf16(const void* logits, int64_t V, const void* hid
     if (logits == nullptr || ids == nullptr || preds == nullptr || result == nullptr || next == nullptr ||
         scratch == nullptr)
         return invalid("verify_argmax_accept: null pointer");
-    if (B <= 0 || B > 64 || T <= 0 || V <= 0 || V > 0xfffffffell || (hidden != nullptr && H <= 0))
-        return invalid("verify_argmax_accept: shape (1 <= B <= 64)");
+    if (B <= 0 || B > 64 || T <= 0 || T > kMaxAcceptRows || V <= 0 || V > 0xfffffffell ||
+        (hidden != nullptr && H <= 0))
+        return invalid("verify_argmax_accept: shape (1 <= B <= 64, 1 <= T <= 64)");
     const auto s = as_stream(stream);
     argmax_partial_kernel<<<dim3(kSlices, static_cast<unsigned>(B * T)), dim3(256), 0, s>>>(
         static_cast<uint64_t*>(scratch), static_cast<const uint16_t*>(logits), V, V);
     int rc = launched("argmax_partial_kernel");
     if (rc != HAI_OK) return rc;
-    verify_accept_kernel<<<dim3(1), dim3(256), 0, s>>>(
+    verify_accept_kernel<<<dim3(static_cast<unsigned>(B)), dim3(256), 0, s>>>(
         static_cast<const uint64_t*>(scratch), static_cast<const uint16_t*>(hidden), H, ids, n_draft, int(B),
         int(T), preds, result, target_len, mtp_len, next, static_cast<uint16_t*>(rec_hidden),
         static_cast<uint16_t*>(h_prev));
