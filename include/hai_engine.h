@@ -58,10 +58,10 @@ typedef struct hai_engine_options {
     int32_t use_graphs;       /* replay captured forwards (0 = plain launches) */
     int32_t weight_format;    /* HAI_WEIGHTS_* */
     int32_t max_batch;        /* sequences decoded in lockstep (0 or 1 = one) */
-    int32_t mfma;             /* 1: GEMMs of 4 or more rows (batches) on the
-                                 matrix cores (tolerance mode, bf16 or FP8
-                                 weights); 0: every GEMM on the bit-exact
-                                 kernels */
+    int32_t mfma;             /* 1: tolerance mode: GEMMs of 4 or more rows
+                                 (batches) and the attention on the matrix
+                                 cores (bf16 or FP8 weights); 0: every GEMM
+                                 and the attention on the bit-exact kernels */
 } hai_engine_options;
 
 /* Counters of GenerationResult (include/hybrid.h:65-94) that the path fills. */

@@ -250,6 +250,23 @@ int hai_gqa_verify_bf16(void* out, const void* q, const void* gate,
                         void* scratch, int64_t B, int64_t T, int64_t nq,
                         int64_t nkv, int64_t D, const int32_t* lens,
                         int32_t len_add, int64_t max_len, void* stream);
+/* The same attention in tolerance mode, on the matrix cores (same reference
+ * kernels as above; the batched verify / draft steps).  Q.K^T and P.V run
+ * as bf16 MFMA with fp32 accumulation (P rounded to bf16), one online
+ * softmax per wave over its own keys, merged per block and then across
+ * blocks: results agree with hai_gqa_verify_bf16 to bf16 rounding, not bit
+ * for bit.  A block serves up to 32 of a KV head's T * nq / nkv queries
+ * (more take several blocks); q, the caches and scratch 16-byte aligned;
+ * scratch must hold
+ * hai_gqa_mfma_scratch_bytes(B, T, nq, D, max_len) bytes. */
+size_t hai_gqa_mfma_scratch_bytes(int64_t B, int64_t T, int64_t nq, int64_t D,
+                                  int64_t max_len);
+int hai_gqa_verify_mfma_bf16(void* out, const void* q, const void* gate,
+                             const void* k_cache, const void* v_cache,
+                             int64_t cap, void* scratch, int64_t B, int64_t T,
+                             int64_t nq, int64_t nkv, int64_t D,
+                             const int32_t* lens, int32_t len_add,
+                             int64_t max_len, void* stream);
 
 /* ------------------------------------------------------------------ DeltaNet
  * Fused grouped causal conv (deltanet_grouped_conv_kernel,

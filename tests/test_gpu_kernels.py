@@ -353,6 +353,67 @@ def test_gqa_verify(B, T, nq, nkv, D, lens):
         assert_bits_equal(got[b], want, f"gqa b={b}")
 
 
+def _attention_f64(q, g, kc, vc, T, L, nq, nkv, D):
+    """Gated causal GQA in float64 for one sequence: the output and, per
+    element, sigmoid(gate) * sum_i p_i |v_i| / sum_i p_i (the scale of the
+    P-rounding error)."""
+    group = nq // nkv
+    out = np.zeros((T, nq, D))
+    mag = np.zeros((T, nq, D))
+    pos = L - T + np.arange(T)
+    for h in range(nq):
+        k = kc[:L, h // group].astype(np.float64)
+        v = vc[:L, h // group].astype(np.float64)
+        s = q[:, h].astype(np.float64) @ k.T / np.sqrt(D)
+        s[np.arange(L)[None, :] > pos[:, None]] = -np.inf
+        p = np.exp(s - s.max(1, keepdims=True))
+        l = p.sum(1, keepdims=True)
+        sig = 1.0 / (1.0 + np.exp(-g[:, h].astype(np.float64)))
+        out[:, h] = (p @ v) / l * sig
+        mag[:, h] = (p @ np.abs(v)) / l * sig
+    return out, mag
+
+
+@pytest.mark.parametrize("B,T,nq,nkv,D,lens", [
+    (1, 2, 4, 2, 64, [30]), (1, 1, 4, 2, 64, [0]), (3, 1, 2, 2, 64, [0, 1, 64]), (2, 3, 4, 1, 128, [63, 200]),
+    (1, 16, 4, 2, 64, [100]),  # 32 queries: two query tiles
+    (1, 16, 8, 2, 64, [300]),  # 64 queries: two blocks per KV head
+    (1, 4, 24, 4, 256, [4092]),  # C2 micro-bench shape
+    (4, 4, 24, 4, 256, [8186, 3000, 64, 5000]),  # C4 verify-like (24 queries per KV head)
+    (8, 1, 24, 4, 256, [8190, 8000, 1, 63, 64, 127, 128, 4097]),  # C4 draft-like
+    (6, 2, 24, 4, 256, [580, 10, 600, 511, 512, 513]),  # C5 verify-like
+    (4, 4, 24, 4, 128, [8186, 300, 7000, 1]),
+    (8, 6, 8, 2, 64, [8100, 8000, 3, 64, 128, 4000, 8120, 500])])
+def test_gqa_verify_mfma(B, T, nq, nkv, D, lens):
+    """Tolerance-mode attention on the matrix cores against float64.  P is
+    rounded to bf16 (unit roundoff 2^-8 per weight) before P.V, so an output
+    element may move by 2^-8 * sum p |v| / sum p (times the gate); the
+    output's own bf16 rounding adds 2^-8 |out|.  The bound is that sum with
+    25 % slack for the fp32 accumulation and exp2 errors (~2^-22 relative)."""
+    rng = np.random.default_rng(B * 100 + T * 10 + D + sum(lens) + 7)
+    lens = np.array(lens, np.int32)
+    cap = int(lens.max()) + T + 5
+    q, qb = rand_bf16(rng, (B * T, nq, D))
+    g, gb = rand_bf16(rng, (B * T, nq, D))
+    kcache, kb = rand_bf16(rng, (B, cap, nkv, D))
+    vcache, vb = rand_bf16(rng, (B, cap, nkv, D))
+    dq, dg, dk, dv, dl = dev(qb), dev(gb), dev(kb), dev(vb), dev(lens)
+    max_len = cap
+    scratch = out_buf(kern().hai_gqa_mfma_scratch_bytes(B, T, nq, D, max_len))
+    dout = out_buf(B * T * nq * D * 2)
+    hai.check(kern().hai_gqa_verify_mfma_bf16(dout.ptr, dq.ptr, dg.ptr, dk.ptr, dv.ptr, cap, scratch.ptr, B, T, nq,
+                                              nkv, D, dl.ptr, T, max_len, None), "gqa mfma")
+    got = hai.bf16_to_f32(dout.download(np.uint16)).reshape(B, T, nq, D)
+    for b in range(B):
+        L = int(lens[b]) + T
+        want, mag = _attention_f64(q[b * T:(b + 1) * T], g[b * T:(b + 1) * T], kcache[b], vcache[b], T, L, nq,
+                                   nkv, D)
+        err = np.abs(got[b] - want)
+        bound = 1.25 * 2.0 ** -8 * (mag + np.abs(want)) + 1e-6
+        assert np.isfinite(got[b]).all(), b
+        assert (err <= bound).all(), (b, float((err / bound).max()))
+
+
 # ----------------------------------------------------------------- deltanet
 def _deltanet_case(rng, B, nk, nv, dk, dv, Kc=4):
     kw, vw = nk * dk, nv * dv

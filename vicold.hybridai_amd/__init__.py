@@ -86,6 +86,7 @@ _KERNEL_SIGS = {
     "hai_qkv_rmsnorm_rope_append_bf16": [VP, VP, VP, VP, I64, VP, I64, VP, VP, VP, VP, I64, I64, I64, I64, I64, I64,
                                          I64, VP, I32, F32, VP],
     "hai_gqa_verify_bf16": [VP, VP, VP, VP, VP, I64, VP, I64, I64, I64, I64, I64, VP, I32, I64, VP],
+    "hai_gqa_verify_mfma_bf16": [VP, VP, VP, VP, VP, I64, VP, I64, I64, I64, I64, I64, VP, I32, I64, VP],
     "hai_deltanet_verify_bf16": [VP, I64, VP, I64, I64, I64, I64, I64, VP, VP, I64, VP, I64, ctypes.c_int, VP, VP,
                                  VP, VP, I32, I64, I64, I64, I64, I64, I64, I64, F32, VP],
     "hai_argmax_rows_bf16": [VP, VP, I64, I64, I64, VP, VP],
@@ -104,6 +105,7 @@ _KERNEL_SIGS = {
 _SIZE_SIGS = {
     "hai_gemm_mfma_workspace_bytes": [I64, I64],
     "hai_gqa_scratch_bytes": [I64, I64, I64, I64, I64],
+    "hai_gqa_mfma_scratch_bytes": [I64, I64, I64, I64, I64],
     "hai_argmax_scratch_bytes": [I64, I64],
 }
 

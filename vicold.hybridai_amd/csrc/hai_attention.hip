@@ -347,6 +347,429 @@ int launch(uint16_t* out, const uint16_t* q, const uint16_t* gate, const uint16_
     return launched("gqa_combine_kernel");
 }
 
+// ---------------------------------------------------------------------------
+// Tolerance mode: the same attention with Q.K^T and P.V on the matrix cores
+// (v_mfma_f32_16x16x32_bf16), for the batched verify / draft steps whose
+// exact form is VALU-bound (one fp32 fma per K or V element per query).
+//
+// A wave is an independent flash-decoder over its own keys: each step it
+// takes KS consecutive keys (32, or 64 at D = 64), computes S^T = K . Q^T for
+// up to 32 queries (one or two 16-query tiles; K rows are the A operand, read
+// straight from the cache, Q rows the B operand, kept in registers), updates
+// a running max and exp-sum per query (base-2, scores pre-scaled by
+// log2(e) / sqrt(D)), and accumulates O^T = V^T . P^T with P rounded to bf16.
+// V^T is the A operand, so the step's V rows are transposed 8 x 8 in
+// registers and staged in the wave's own LDS tile.  Block waves interleave
+// their steps over the block's key range (wave w takes keys 4s + w in units
+// of KS), the block merges its four waves in LDS and writes one partial per
+// query: O[D], max, sum.  A second pass merges the partials of the splits.
+// Every step's loads for the next step are in flight while it computes.
+// ---------------------------------------------------------------------------
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kMfmaWaves = 4;
+constexpr int kMfmaMaxSteps = 16;          // steps per wave and block
+constexpr int64_t kMfmaTargetBlocks = 512; // blocks the split count aims for
+constexpr int kMfmaMinBlockKeys = 128;     // keys of the smallest block (one 32-key step per wave)
+
+__host__ __device__ constexpr int mfma_step_keys(int D) { return D == 64 ? 64 : 32; }
+__host__ __device__ constexpr int64_t mfma_part_stride(int D) { return D + 4; }
+
+__device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+}
+
+// two bf16 (round to nearest even) in one dword, a in the low half
+__device__ __forceinline__ uint32_t pack_bf2(float a, float b) {
+    return static_cast<uint32_t>(f2bf(a)) | (static_cast<uint32_t>(f2bf(b)) << 16);
+}
+
+template <int D, int QT>
+struct MfmaAttnShape {
+    static constexpr int KS = mfma_step_keys(D);  // keys per wave step
+    static constexpr int NKT = KS / 16;           // 16-key score tiles per step
+    static constexpr int NJ = D / 32;             // 32-dim slabs of a score
+    static constexpr int NDT = D / 16;            // 16-dim output tiles
+    static constexpr int PR = D / 8;              // 16-byte pieces of a K / V row
+    static constexpr int KG = 64 / PR;            // keys per V load instruction
+    static constexpr int NB = KS / (8 * KG);      // 8 x 8 transposes per lane and step
+    static constexpr int VTP = KS + 8;            // staged V^T row: KS keys + 16-byte pad
+    static constexpr int QROWS = 16 * QT;
+    static constexpr int MP = D + 4;              // merge-buffer row, floats
+    static constexpr int VT_BYTES = kMfmaWaves * D * VTP * 2;
+    static constexpr int MERGE_BYTES = 2 * QROWS * MP * 4 + 4 * QROWS * 4;
+    static constexpr int QP = D + 8;              // staged Q row, bf16 elements
+    static constexpr int Q_BYTES = QROWS * QP * 2;
+    static constexpr int LDS_BYTES = (VT_BYTES > MERGE_BYTES ? VT_BYTES : MERGE_BYTES) + Q_BYTES;
+    static_assert(NB >= 1 && NB * 8 * KG == KS, "a step's V rows must split into 8 x 8 transposes");
+};
+
+// grid (split, query group x KV head, sequence); block = 4 waves.
+template <int D, int QT>
+__global__ __launch_bounds__(256) void gqa_mfma_partial_kernel(
+    float* __restrict__ part, const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
+    const uint16_t* __restrict__ vc, int64_t cap, int T, int nq, int nkv, const int32_t* lens, int len_add,
+    int nsplit, int steps, float scale_log2) {
+    using S = MfmaAttnShape<D, QT>;
+    constexpr int KS = S::KS, NKT = S::NKT, NJ = S::NJ, NDT = S::NDT, PR = S::PR, KG = S::KG, NB = S::NB;
+    constexpr int VTP = S::VTP, QROWS = S::QROWS, MP = S::MP;
+    constexpr float kNegInf = -__builtin_huge_valf();
+    __shared__ __align__(16) unsigned char lds[S::LDS_BYTES];
+
+    const int split = blockIdx.x;
+    const int kvh = blockIdx.y % nkv;
+    const int qgrp = blockIdx.y / nkv;
+    const int b = blockIdx.z;
+    const int lane = threadIdx.x & 63;
+    const int wave = wave_index();
+    const int li = lane & 15;
+    const int kg = lane >> 4;
+    const int64_t L = static_cast<int64_t>(lens ? lens[b] : 0) + len_add;
+    const int block_keys = steps * kMfmaWaves * KS;
+    const int64_t kb0 = static_cast<int64_t>(split) * block_keys;
+    if (kb0 >= L) return;  // uniform over the block: no partial (the merge pass skips it)
+    const int nkeys = static_cast<int>(min(static_cast<int64_t>(block_keys), L - kb0));
+    const int group = nq / nkv;
+    const int nqry = T * group;
+    const int q_begin = qgrp * QROWS;
+
+    // The group's Q rows, staged once in LDS (the B operand of the scores:
+    // lane (li, kg) reads query 16 qt + li, dims 32 j + 8 kg + [0, 8)).
+    // Padding queries are zero and get the last token's causal limit; their
+    // results are not stored.
+    uint16_t* qs = reinterpret_cast<uint16_t*>(lds + (S::LDS_BYTES - S::Q_BYTES));
+    for (int e = threadIdx.x; e < QROWS * PR; e += 256) {
+        const int r = e / PR, c = (e % PR) * 8;
+        const int qi = q_begin + r;
+        u32x4 v = u32x4{0, 0, 0, 0};
+        if (qi < nqry) {
+            const int64_t row = (static_cast<int64_t>(b) * T + qi / group) * nq + kvh * group + qi % group;
+            v = *reinterpret_cast<const u32x4*>(q + row * D + c);
+        }
+        *reinterpret_cast<u32x4*>(qs + r * S::QP + c) = v;
+    }
+    int64_t qpos[QT];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+        const int qi = q_begin + 16 * qt + li;
+        qpos[qt] = L - T + (qi < nqry ? qi / group : T - 1);
+    }
+
+    // The block's K / V rows: keys [kb0, kb0 + nkeys) of head kvh; loads past
+    // them return zeros and their scores are masked.
+    const uint32_t kst = static_cast<uint32_t>(nkv * D * 2);  // bytes between consecutive keys
+    const int64_t off0 = ((static_cast<int64_t>(b) * cap + kb0) * nkv + kvh) * D;
+    const uint32_t bytes = static_cast<uint32_t>((static_cast<int64_t>(nkeys - 1) * nkv * D + D) * 2);
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(kc + off0, bytes);
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(vc + off0, bytes);
+    // wave steps that hold at least one of the block's keys
+    int wsteps = 0;
+    while (wsteps < steps && (wsteps * kMfmaWaves + wave) * KS < nkeys) ++wsteps;
+
+    u32x4 kr[NKT][NJ];
+    u32x4 vr[NB][8];
+    // K rows (A operand): lane (li, kg) takes key 16 kt + li, dims 32 j + 8 kg + [0, 8)
+    auto load_k = [&](int s) {
+        const uint32_t k0 = static_cast<uint32_t>((s * kMfmaWaves + wave) * KS);
+#pragma unroll
+        for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+            for (int j = 0; j < NJ; ++j)
+                kr[kt][j] = bload(rk, (k0 + 16 * kt + li) * kst + (32 * j + 8 * kg) * 2, 0);
+    };
+    // V rows for the transpose: lane takes piece lane % PR (dims 8 (lane % PR)
+    // + [0, 8)) of keys 8 (KG bb + lane / PR) + i, i = 0..7
+    const int vp = lane % PR;
+    const int vh = lane / PR;
+    auto load_v = [&](int s) {
+        const uint32_t k0 = static_cast<uint32_t>((s * kMfmaWaves + wave) * KS);
+#pragma unroll
+        for (int bb = 0; bb < NB; ++bb)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) vr[bb][i] = bload(rv, (k0 + 8 * (KG * bb + vh) + i) * kst + vp * 16, 0);
+    };
+    // V^T tile of the wave: row d holds the step's KS keys of dim d
+    uint16_t* vt = reinterpret_cast<uint16_t*>(lds) + wave * D * VTP;
+    auto stage_v = [&] {
+#pragma unroll
+        for (int bb = 0; bb < NB; ++bb)
+#pragma unroll
+            for (int r = 0; r < 8; ++r) {
+                // dword w of row r: keys 2w, 2w + 1 of dim 8 vp + r
+                const uint32_t sel = (r & 1) ? 0x07060302u : 0x05040100u;
+                u32x4 o;
+#pragma unroll
+                for (int w = 0; w < 4; ++w)
+                    o[w] = __builtin_amdgcn_perm(vr[bb][2 * w + 1][r >> 1], vr[bb][2 * w][r >> 1], sel);
+                *reinterpret_cast<u32x4*>(vt + (8 * vp + r) * VTP + 8 * (KG * bb + vh)) = o;
+            }
+    };
+    auto wave_sync = [] {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+
+    float m[QT], l[QT];
+    f32x4 o[QT][NDT];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+        m[qt] = kNegInf;
+        l[qt] = 0.0f;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) o[qt][dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+
+    if (wsteps > 0) {
+        load_k(0);
+        load_v(0);
+    }
+    __syncthreads();  // Q staged
+    for (int s = 0; s < wsteps; ++s) {
+        wave_sync();  // the previous step's V^T reads precede these writes
+        stage_v();
+        if (s + 1 < wsteps) load_v(s + 1);
+        f32x4 st[NKT][QT];
+#pragma unroll
+        for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt) {
+                st[kt][qt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) {
+                    const u32x4 qv = *reinterpret_cast<const u32x4*>(qs + (16 * qt + li) * S::QP + 32 * j + 8 * kg);
+                    st[kt][qt] = mfma16(kr[kt][j], qv, st[kt][qt]);
+                }
+            }
+        if (s + 1 < wsteps) load_k(s + 1);
+
+        // lane (li, kg) holds the scores of query li for keys 16 kt + 4 kg + i
+        const int64_t key_l = kb0 + static_cast<int64_t>(s * kMfmaWaves + wave) * KS + 4 * kg;
+        const int64_t key_end = kb0 + nkeys;
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+            float mx = kNegInf;
+#pragma unroll
+            for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int64_t key = key_l + 16 * kt + i;
+                    const float x = key < key_end && key <= qpos[qt] ? st[kt][qt][i] * scale_log2 : kNegInf;
+                    st[kt][qt][i] = x;
+                    mx = fmaxf(mx, x);
+                }
+            mx = fmaxf(mx, __shfl_xor(mx, 16));
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            const float mn = fmaxf(m[qt], mx);
+            const bool empty = mn == kNegInf;  // no key of the query yet
+            const float alpha = empty ? 1.0f : __builtin_amdgcn_exp2f(m[qt] - mn);
+            const float sub = empty ? 0.0f : mn;
+            float ps = 0.0f;
+#pragma unroll
+            for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float p = __builtin_amdgcn_exp2f(st[kt][qt][i] - sub);
+                    st[kt][qt][i] = p;
+                    ps += p;
+                }
+            l[qt] = fma_(l[qt], alpha, ps);
+            m[qt] = mn;
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) o[qt][dt] *= alpha;
+        }
+        wave_sync();  // V^T of this step is in LDS
+#pragma unroll
+        for (int ks = 0; ks < NKT / 2; ++ks) {
+            // P^T operand: keys 32 ks + 4 kg + [0, 4) then 32 ks + 16 + 4 kg + [0, 4)
+            u32x4 pop[QT];
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt) {
+                const f32x4 a = st[2 * ks][qt], c = st[2 * ks + 1][qt];
+                pop[qt] = u32x4{pack_bf2(a[0], a[1]), pack_bf2(a[2], a[3]), pack_bf2(c[0], c[1]), pack_bf2(c[2], c[3])};
+            }
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) {
+                const uint16_t* vrow = vt + (16 * dt + li) * VTP + 32 * ks + 4 * kg;
+                const uint2 lo = *reinterpret_cast<const uint2*>(vrow);
+                const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 16);
+                const u32x4 a = u32x4{lo.x, lo.y, hi.x, hi.y};
+#pragma unroll
+                for (int qt = 0; qt < QT; ++qt) o[qt][dt] = mfma16(a, pop[qt], o[qt][dt]);
+            }
+        }
+    }
+    // full exp-sum of each query over the lane's four key groups
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+        l[qt] += __shfl_xor(l[qt], 16);
+        l[qt] += __shfl_xor(l[qt], 32);
+    }
+
+    // Merge the four waves: 2 -> 0 and 3 -> 1, then 1 -> 0.  O^T layout: lane
+    // (li, kg) holds dims 16 dt + 4 kg + [0, 4) of query 16 qt + li.
+    __syncthreads();  // every wave is done with its V^T tile
+    float* mb = reinterpret_cast<float*>(lds);  // [2][QROWS][MP]
+    float* ml = mb + 2 * QROWS * MP;            // [2][2][QROWS]: max, sum
+    auto put = [&](int slot) {
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+            float* row = mb + (slot * QROWS + 16 * qt + li) * MP + 4 * kg;
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) *reinterpret_cast<f32x4*>(row + 16 * dt) = o[qt][dt];
+            if (kg == 0) {
+                ml[(slot * 2) * QROWS + 16 * qt + li] = m[qt];
+                ml[(slot * 2 + 1) * QROWS + 16 * qt + li] = l[qt];
+            }
+        }
+    };
+    auto merge = [&](int slot) {
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+            const float mo = ml[(slot * 2) * QROWS + 16 * qt + li];
+            const float lo = ml[(slot * 2 + 1) * QROWS + 16 * qt + li];
+            const float M = fmaxf(m[qt], mo);
+            const bool empty = M == kNegInf;
+            const float a = empty ? 0.0f : __builtin_amdgcn_exp2f(m[qt] - M);
+            const float c = empty ? 0.0f : __builtin_amdgcn_exp2f(mo - M);
+            l[qt] = fma_(l[qt], a, lo * c);
+            m[qt] = M;
+            const float* row = mb + (slot * QROWS + 16 * qt + li) * MP + 4 * kg;
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) {
+                const f32x4 v = *reinterpret_cast<const f32x4*>(row + 16 * dt);
+                o[qt][dt] = o[qt][dt] * a + v * c;
+            }
+        }
+    };
+    if (wave >= 2) put(wave - 2);
+    __syncthreads();
+    if (wave < 2) merge(wave);
+    __syncthreads();
+    if (wave == 1) put(0);
+    __syncthreads();
+    if (wave != 0) return;
+    merge(0);
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+        const int qi = q_begin + 16 * qt + li;
+        if (qi >= nqry) continue;
+        const int64_t row = (static_cast<int64_t>(b) * T + qi / group) * nq + kvh * group + qi % group;
+        float* dst = part + (row * nsplit + split) * mfma_part_stride(D);
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) *reinterpret_cast<f32x4*>(dst + 16 * dt + 4 * kg) = o[qt][dt];
+        if (kg == 0) {
+            dst[D] = m[qt];
+            dst[D + 1] = l[qt];
+        }
+    }
+}
+
+// One wave per query: the splits' partials merged against the global max
+// (base 2), divided, gated and rounded.
+template <int D>
+__global__ __launch_bounds__(256) void gqa_mfma_combine_kernel(uint16_t* __restrict__ out,
+                                                               const float* __restrict__ part, const uint16_t* gate,
+                                                               int B, int T, int nq, const int32_t* lens,
+                                                               int len_add, int nsplit, int block_keys) {
+    const int lane = threadIdx.x & 63;
+    const int64_t qidx = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (qidx >= static_cast<int64_t>(B) * T * nq) return;
+    const int b = static_cast<int>(qidx / (static_cast<int64_t>(T) * nq));
+    const int64_t L = static_cast<int64_t>(lens ? lens[b] : 0) + len_add;
+    const int nv = static_cast<int>(min(static_cast<int64_t>(nsplit), (L + block_keys - 1) / block_keys));
+    constexpr int64_t PS = mfma_part_stride(D);
+    const float* base = part + qidx * nsplit * PS;
+    float M = -__builtin_huge_valf();
+    for (int c = lane; c < nv; c += 64) M = fmaxf(M, base[c * PS + D]);
+    M = wave_max64(M);
+    constexpr int PER = D / 64;
+    float O[PER];
+#pragma unroll
+    for (int r = 0; r < PER; ++r) O[r] = 0.0f;
+    float Ls = 0.0f;
+    int c = 0;
+    for (; c + 4 <= nv; c += 4) {
+        float mv[4], lv[4], ov[4][PER];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const float* p = base + (c + u) * PS;
+            mv[u] = p[D];
+            lv[u] = p[D + 1];
+#pragma unroll
+            for (int r = 0; r < PER; ++r) ov[u][r] = p[lane + 64 * r];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const float w = __builtin_amdgcn_exp2f(mv[u] - M);
+            Ls = fma_(lv[u], w, Ls);
+#pragma unroll
+            for (int r = 0; r < PER; ++r) O[r] = fma_(ov[u][r], w, O[r]);
+        }
+    }
+    for (; c < nv; ++c) {
+        const float* p = base + c * PS;
+        const float w = __builtin_amdgcn_exp2f(p[D] - M);
+        Ls = fma_(p[D + 1], w, Ls);
+#pragma unroll
+        for (int r = 0; r < PER; ++r) O[r] = fma_(p[lane + 64 * r], w, O[r]);
+    }
+#pragma unroll
+    for (int r = 0; r < PER; ++r) {
+        const int d = lane + 64 * r;
+        float v = O[r] / Ls;
+        if (gate != nullptr) v = v * csigmoid(bf2f(gate[qidx * D + d]));
+        out[qidx * D + d] = f2bf(v);
+    }
+}
+
+// Split plan of the matrix-core path: steps per wave (block = 4 waves x steps
+// x KS keys) and the number of splits covering max_len.
+struct MfmaPlan {
+    int qt, qgroups, steps, nsplit, block_keys;
+};
+
+inline MfmaPlan mfma_plan(int D, int64_t B, int64_t T, int64_t nq, int64_t nkv, int64_t max_len) {
+    MfmaPlan p{};
+    const int64_t nqry = T * (nq / nkv);
+    p.qt = nqry <= 16 ? 1 : 2;
+    p.qgroups = static_cast<int>((nqry + 16 * p.qt - 1) / (16 * p.qt));
+    const int step_keys = kMfmaWaves * mfma_step_keys(D);
+    const int64_t units = (max_len + step_keys - 1) / step_keys;  // block steps covering max_len
+    const int64_t pairs = nkv * p.qgroups * B;
+    const int64_t per_pair = (kMfmaTargetBlocks + pairs - 1) / pairs;  // splits wanted per (head, sequence)
+    int64_t steps = (units + per_pair - 1) / per_pair;
+    steps = steps < 1 ? 1 : (steps > kMfmaMaxSteps ? kMfmaMaxSteps : steps);
+    p.steps = static_cast<int>(steps);
+    p.block_keys = p.steps * step_keys;
+    p.nsplit = static_cast<int>((max_len + p.block_keys - 1) / p.block_keys);
+    return p;
+}
+
+template <int D>
+int launch_mfma(uint16_t* out, const uint16_t* q, const uint16_t* gate, const uint16_t* kc, const uint16_t* vc,
+                int64_t cap, float* scratch, int B, int T, int nq, int nkv, const int32_t* lens, int len_add,
+                int64_t max_len, hipStream_t s) {
+    const MfmaPlan p = mfma_plan(D, B, T, nq, nkv, max_len);
+    const float scale_log2 = 1.4426950408889634f / __builtin_sqrtf(static_cast<float>(D));
+    const dim3 grid(p.nsplit, nkv * p.qgroups, B);
+    if (p.qt == 1)
+        gqa_mfma_partial_kernel<D, 1><<<grid, dim3(256), 0, s>>>(scratch, q, kc, vc, cap, T, nq, nkv, lens, len_add,
+                                                                 p.nsplit, p.steps, scale_log2);
+    else
+        gqa_mfma_partial_kernel<D, 2><<<grid, dim3(256), 0, s>>>(scratch, q, kc, vc, cap, T, nq, nkv, lens, len_add,
+                                                                 p.nsplit, p.steps, scale_log2);
+    int rc = launched("gqa_mfma_partial_kernel");
+    if (rc != HAI_OK) return rc;
+    const int64_t nall = static_cast<int64_t>(B) * T * nq;
+    gqa_mfma_combine_kernel<D><<<dim3(static_cast<unsigned>((nall + 3) / 4)), dim3(256), 0, s>>>(
+        out, scratch, gate, B, T, nq, lens, len_add, p.nsplit, p.block_keys);
+    return launched("gqa_mfma_combine_kernel");
+}
+
 }  // namespace
 
 extern "C" {
@@ -383,6 +806,41 @@ int hai_gqa_verify_bf16(void* out, const void* q, const void* gate, const void* 
         case 128: return launch<128>(o, qq, g, kc, vc, cap, sc, int(B), int(T), int(nq), int(nkv), lens, len_add, nchunk, s);
         case 256: return launch<256>(o, qq, g, kc, vc, cap, sc, int(B), int(T), int(nq), int(nkv), lens, len_add, nchunk, s);
         default: return invalid("gqa_verify: head_dim must be 64, 128 or 256");
+    }
+}
+
+size_t hai_gqa_mfma_scratch_bytes(int64_t B, int64_t T, int64_t nq, int64_t D, int64_t max_len) {
+    // at most one split per kMfmaMinBlockKeys keys
+    const int64_t nsplit = (max_len + kMfmaMinBlockKeys - 1) / kMfmaMinBlockKeys;
+    return static_cast<size_t>(B * T * nq * (nsplit < 1 ? 1 : nsplit) * mfma_part_stride(int(D))) * sizeof(float);
+}
+
+int hai_gqa_verify_mfma_bf16(void* out, const void* q, const void* gate, const void* k_cache,
+                             const void* v_cache, int64_t cap, void* scratch, int64_t B, int64_t T, int64_t nq,
+                             int64_t nkv, int64_t D, const int32_t* lens, int32_t len_add, int64_t max_len,
+                             void* stream) {
+    if (out == nullptr || q == nullptr || k_cache == nullptr || v_cache == nullptr || scratch == nullptr)
+        return invalid("gqa_verify_mfma: null pointer");
+    if (B < 0 || T < 0 || nq <= 0 || nkv <= 0 || nq % nkv != 0 || cap <= 0 || max_len <= 0 ||
+        max_len > cap || T > max_len)
+        return invalid("gqa_verify_mfma: shape");
+    if (lens == nullptr && (len_add < T || len_add > max_len))
+        return invalid("gqa_verify_mfma: cache length must cover the T new rows and stay within max_len");
+    if (!aligned16(k_cache) || !aligned16(v_cache) || !aligned16(q) || !aligned16(scratch))
+        return invalid("gqa_verify_mfma: alignment");
+    if (B == 0 || T == 0) return HAI_OK;
+    const auto s = as_stream(stream);
+    auto* o = static_cast<uint16_t*>(out);
+    const auto* qq = static_cast<const uint16_t*>(q);
+    const auto* g = static_cast<const uint16_t*>(gate);
+    const auto* kc = static_cast<const uint16_t*>(k_cache);
+    const auto* vc = static_cast<const uint16_t*>(v_cache);
+    auto* sc = static_cast<float*>(scratch);
+    switch (D) {
+        case 64: return launch_mfma<64>(o, qq, g, kc, vc, cap, sc, int(B), int(T), int(nq), int(nkv), lens, len_add, max_len, s);
+        case 128: return launch_mfma<128>(o, qq, g, kc, vc, cap, sc, int(B), int(T), int(nq), int(nkv), lens, len_add, max_len, s);
+        case 256: return launch_mfma<256>(o, qq, g, kc, vc, cap, sc, int(B), int(T), int(nq), int(nkv), lens, len_add, max_len, s);
+        default: return invalid("gqa_verify_mfma: head_dim must be 64, 128 or 256");
     }
 }
 

@@ -329,7 +329,8 @@ int Engine::alloc_all() {
         mh_[1] = cv.take<uint16_t>(B_ * H);
         h_prev_ = cv.take<uint16_t>(B_ * H);
         rec_hidden_ = cv.take<uint16_t>(B_ * H);
-        gqa_scratch_ = cv.take<char>(hai_gqa_scratch_bytes(B_, T, d.nq, d.D, cap_));
+        gqa_scratch_ = cv.take<char>(std::max(hai_gqa_scratch_bytes(B_, T, d.nq, d.D, cap_),
+                                              mfma_ ? hai_gqa_mfma_scratch_bytes(B_, T, d.nq, d.D, cap_) : 0));
         if (mfma_) {
             const int64_t mrows = std::min<int64_t>(128, R);
             size_t ws = 0;
@@ -541,8 +542,10 @@ int Engine::attention_layer(const LayerWeights& L, int64_t T, uint16_t* h, const
     HAI_TRY(hai_qkv_rmsnorm_rope_append_bf16(q_, gate_, kc, vc, cap_, proj_, d.Nqkv, L.q_norm, L.k_norm, rope_cos_,
                                              rope_sin_, cap_, B_, T, d.nq, d.nkv, d.D, d.R, lens, 0, cfg_.rms_eps,
                                              stream_));
-    HAI_TRY(hai_gqa_verify_bf16(att_, q_, gate_, kc, vc, cap_, gqa_scratch_, B_, T, d.nq, d.nkv, d.D, lens,
-                                static_cast<int32_t>(T), cap_, stream_));
+    // tolerance mode: Q.K^T and P.V on the matrix cores
+    const auto attend = mfma_ ? hai_gqa_verify_mfma_bf16 : hai_gqa_verify_bf16;
+    HAI_TRY(attend(att_, q_, gate_, kc, vc, cap_, gqa_scratch_, B_, T, d.nq, d.nkv, d.D, lens,
+                   static_cast<int32_t>(T), cap_, stream_));
     return gemm(h, d.H, att_, d.qw, lin(L.w_o, L.f_o), rows, d.H, d.qw, HAI_EPI_RESIDUAL, h, d.H);
 }
 

@@ -238,7 +238,7 @@ private:
     int64_t B_ = 1;       // sequences
     int64_t cap_ = 0;     // KV capacity per sequence
     int64_t tmax_ = 0;    // largest verify T / prefill chunk (rows per sequence)
-    bool mfma_ = false;   // MFMA GEMMs for launches of more than 16 rows
+    bool mfma_ = false;   // tolerance mode: MFMA GEMMs (4+ rows) and attention
     int64_t ring_ = 0;
     int64_t nslots_ = 0;
 
