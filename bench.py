@@ -195,6 +195,11 @@ def c2_ops(hai, reps: int = 50, cpu: bool = True) -> dict:
                                                         nq, nkv, D, None, L, L, None), "gqa"))
     gqa_bytes = 2 * L * nkv * D * 2
     out["gqa_verify"] = {"us": round(us, 2), "bytes": gqa_bytes, "gb_s": round(gqa_bytes / us / 1e3, 1)}
+    # the same op in tolerance mode (matrix cores, P in bf16), as the batched configurations run it
+    dsc_m = hai.DeviceBuffer(k.hai_gqa_mfma_scratch_bytes(1, T, nq, D, L))
+    us = timed(lambda: hai.check(k.hai_gqa_verify_mfma_bf16(dout.ptr, dq.ptr, dg.ptr, dkc.ptr, dvc.ptr, L, dsc_m.ptr,
+                                                             1, T, nq, nkv, D, None, L, L, None), "gqa mfma"))
+    out["gqa_verify_mfma"] = {"us": round(us, 2), "bytes": gqa_bytes, "gb_s": round(gqa_bytes / us / 1e3, 1)}
     # ---- DeltaNet recurrence (reference contract: state [48][128][128] in place)
     nk, nv, dk, dv = 16, 48, 128, 128
     kw, vw = nk * dk, nv * dv

@@ -382,10 +382,14 @@ __device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
                                                    0, 0, 0);
 }
 
-// two bf16 (round to nearest even) in one dword, a in the low half
-__device__ __forceinline__ uint32_t pack_bf2(float a, float b) {
-    return static_cast<uint32_t>(f2bf(a)) | (static_cast<uint32_t>(f2bf(b)) << 16);
+__device__ __forceinline__ f32x4 mfma16(u32x4 a, bf16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), b, c, 0, 0, 0);
 }
+
+// The running max of a query moves only when a score exceeds it by more than
+// this (base-2 units), so most steps skip rescaling O; probabilities then stay
+// below 2^kRescaleSlack, far inside bf16 / fp32 range.
+constexpr float kRescaleSlack = 8.0f;
 
 template <int D, int QT>
 struct MfmaAttnShape {
@@ -451,11 +455,14 @@ __global__ __launch_bounds__(256) void gqa_mfma_partial_kernel(
         }
         *reinterpret_cast<u32x4*>(qs + r * S::QP + c) = v;
     }
-    int64_t qpos[QT];
+    // keys [kb0, kb0 + lim) of the block are visible to the lane's queries
+    int lim[QT];
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
         const int qi = q_begin + 16 * qt + li;
-        qpos[qt] = L - T + (qi < nqry ? qi / group : T - 1);
+        const int64_t qpos = L - T + (qi < nqry ? qi / group : T - 1);
+        const int64_t n = qpos - kb0 + 1;
+        lim[qt] = static_cast<int>(n < 0 ? 0 : (n < nkeys ? n : nkeys));
     }
 
     // The block's K / V rows: keys [kb0, kb0 + nkeys) of head kvh; loads past
@@ -547,8 +554,8 @@ __global__ __launch_bounds__(256) void gqa_mfma_partial_kernel(
         if (s + 1 < wsteps) load_k(s + 1);
 
         // lane (li, kg) holds the scores of query li for keys 16 kt + 4 kg + i
-        const int64_t key_l = kb0 + static_cast<int64_t>(s * kMfmaWaves + wave) * KS + 4 * kg;
-        const int64_t key_end = kb0 + nkeys;
+        // (block-relative key index key_l + 16 kt + i)
+        const int key_l = (s * kMfmaWaves + wave) * KS + 4 * kg;
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt) {
             float mx = kNegInf;
@@ -556,17 +563,22 @@ __global__ __launch_bounds__(256) void gqa_mfma_partial_kernel(
             for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const int64_t key = key_l + 16 * kt + i;
-                    const float x = key < key_end && key <= qpos[qt] ? st[kt][qt][i] * scale_log2 : kNegInf;
+                    const float x = key_l + 16 * kt + i < lim[qt] ? st[kt][qt][i] * scale_log2 : kNegInf;
                     st[kt][qt][i] = x;
                     mx = fmaxf(mx, x);
                 }
             mx = fmaxf(mx, __shfl_xor(mx, 16));
             mx = fmaxf(mx, __shfl_xor(mx, 32));
-            const float mn = fmaxf(m[qt], mx);
-            const bool empty = mn == kNegInf;  // no key of the query yet
-            const float alpha = empty ? 1.0f : __builtin_amdgcn_exp2f(m[qt] - mn);
-            const float sub = empty ? 0.0f : mn;
+            const bool grow = mx > m[qt] + kRescaleSlack;  // true for the first visible key
+            if (__builtin_amdgcn_ballot_w64(grow) != 0) {  // wave-uniform
+                const float mn = grow ? mx : m[qt];
+                const float alpha = grow ? __builtin_amdgcn_exp2f(m[qt] - mn) : 1.0f;  // 0 from -inf
+                l[qt] *= alpha;
+#pragma unroll
+                for (int dt = 0; dt < NDT; ++dt) o[qt][dt] *= alpha;
+                m[qt] = mn;
+            }
+            const float sub = m[qt] == kNegInf ? 0.0f : m[qt];  // no visible key yet: every p is 0
             float ps = 0.0f;
 #pragma unroll
             for (int kt = 0; kt < NKT; ++kt)
@@ -576,20 +588,19 @@ __global__ __launch_bounds__(256) void gqa_mfma_partial_kernel(
                     st[kt][qt][i] = p;
                     ps += p;
                 }
-            l[qt] = fma_(l[qt], alpha, ps);
-            m[qt] = mn;
-#pragma unroll
-            for (int dt = 0; dt < NDT; ++dt) o[qt][dt] *= alpha;
+            l[qt] += ps;
         }
         wave_sync();  // V^T of this step is in LDS
 #pragma unroll
         for (int ks = 0; ks < NKT / 2; ++ks) {
             // P^T operand: keys 32 ks + 4 kg + [0, 4) then 32 ks + 16 + 4 kg + [0, 4)
-            u32x4 pop[QT];
+            bf16x8 pop[QT];
 #pragma unroll
             for (int qt = 0; qt < QT; ++qt) {
                 const f32x4 a = st[2 * ks][qt], c = st[2 * ks + 1][qt];
-                pop[qt] = u32x4{pack_bf2(a[0], a[1]), pack_bf2(a[2], a[3]), pack_bf2(c[0], c[1]), pack_bf2(c[2], c[3])};
+                pop[qt] = bf16x8{static_cast<__bf16>(a[0]), static_cast<__bf16>(a[1]), static_cast<__bf16>(a[2]),
+                                 static_cast<__bf16>(a[3]), static_cast<__bf16>(c[0]), static_cast<__bf16>(c[1]),
+                                 static_cast<__bf16>(c[2]), static_cast<__bf16>(c[3])};
             }
 #pragma unroll
             for (int dt = 0; dt < NDT; ++dt) {
