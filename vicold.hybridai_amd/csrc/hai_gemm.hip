@@ -20,6 +20,7 @@
 #include "hai_gemm_common.h"
 
 #include <mutex>
+#include <type_traits>
 #include <vector>
 
 namespace {
@@ -34,7 +35,6 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(
     const int wave = wave_index();
     extern __shared__ u32x4 xs[];  // NORM: [M][K/8] normalised rows, then the norm weight
     const int npr = K >> 3;        // 16-byte pieces per row
-    if constexpr (NORM) rmsnorm_rows_to_lds(xs, x, ldx, M, K, na);
 
     // Byte offsets fit 32 bits: the caller bounds N*K*2 and M*ldx*2 below 4 GiB.
     const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, static_cast<uint32_t>(static_cast<int64_t>(N) * K * 2));
@@ -49,9 +49,34 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(
     // is launched with one block per group, the NORM kernel with a grid sized
     // to the machine so that the prologue is paid once per resident block.
     const int64_t ngroups = (static_cast<int64_t>(N) + 4 * RW - 1) / (4 * RW);
-    for (int64_t grp = blockIdx.x; grp < ngroups; grp += gridDim.x) {
+
+    // The first U chunks of the block's first rows do not depend on the
+    // activations: with the fused RMSNorm they are requested before the
+    // prologue, whose latency then overlaps theirs.
+    u32x4 wpre[U][RW];
+    const int64_t grp0 = blockIdx.x;
+    if constexpr (NORM) {
+        const int64_t row0 = (grp0 * 4 + wave) * RW;
+        if (grp0 < ngroups && row0 < N) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const bool ok = u < nfull || (u < nck && u * 512 + lane * 8 < K);
+                const ChunkOffset co(u < nfull, ok, static_cast<uint32_t>(u) * 1024u);
+#pragma unroll
+                for (int r = 0; r < RW; ++r)
+                    wpre[u][r] = bload_w(rw, co.v(static_cast<uint32_t>(((row0 + r) * static_cast<int64_t>(K) + lane * 8) * 2)), co.s);
+            }
+        }
+        rmsnorm_rows_to_lds(xs, x, ldx, M, K, na);
+    }
+
+    // One row group; FIRST: the block's first group, whose first U chunks
+    // were requested before the prologue (a separate instantiation, so the
+    // preloaded registers are dead once that group's first step is done).
+    auto run_group = [&](int64_t grp, auto first) {
+        constexpr bool FIRST = decltype(first)::value;
         const int64_t row0 = (grp * 4 + wave) * RW;
-        if (row0 >= N) continue;
+        if (row0 >= N) return;
         const int nrows = static_cast<int>(min(static_cast<int64_t>(RW), static_cast<int64_t>(N) - row0));
         uint32_t woff[RW];
 #pragma unroll
@@ -101,17 +126,13 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(
         // reads zeros through an out-of-range offset; fma(0, 0, acc) == acc
         // because acc is never -0 (it starts at +0 and round-to-nearest only
         // produces -0 from (-0) + (-0)), so padding does not change a bit.
-        for (int c0 = 0; c0 < nck; c0 += U) {
-            u32x4 wv[U][RW];
+        auto step = [&](int c0, const u32x4 (&wv)[U][RW]) {
             u32x4 xv[U][MB];
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 const int c = c0 + u;
-                // full chunk: every lane valid; ragged chunk: lanes past K masked
                 const bool ok = c < nfull || (c < nck && c * 512 + lane * 8 < K);
                 const ChunkOffset co(c < nfull, ok, static_cast<uint32_t>(c) * 1024u);
-#pragma unroll
-                for (int r = 0; r < RW; ++r) wv[u][r] = bload_w(rw, co.v(woff[r]), co.s);
 #pragma unroll
                 for (int m = 0; m < MB; ++m) {
                     if constexpr (NORM)
@@ -124,6 +145,24 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(
             for (int u = 0; u < U; ++u) body(wv[u], xv[u]);
             // a segment is four 512-element chunks (U divides 4)
             if (((c0 + U) & 3) == 0) fold();
+        };
+        int c0 = 0;
+        if constexpr (FIRST) {
+            step(0, wpre);
+            c0 = U;
+        }
+        for (; c0 < nck; c0 += U) {
+            u32x4 wv[U][RW];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int c = c0 + u;
+                // full chunk: every lane valid; ragged chunk: lanes past K masked
+                const bool ok = c < nfull || (c < nck && c * 512 + lane * 8 < K);
+                const ChunkOffset co(c < nfull, ok, static_cast<uint32_t>(c) * 1024u);
+#pragma unroll
+                for (int r = 0; r < RW; ++r) wv[u][r] = bload_w(rw, co.v(woff[r]), co.s);
+            }
+            step(c0, wv);
         }
         fold();
 
@@ -157,7 +196,13 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(
                     }
                 }
         }
+    };
+    int64_t grp = blockIdx.x;
+    if constexpr (NORM) {
+        if (grp < ngroups) run_group(grp, std::true_type{});
+        grp += gridDim.x;
     }
+    for (; grp < ngroups; grp += gridDim.x) run_group(grp, std::false_type{});
 }
 
 // K-split variant for short, wide-K layers (out / o / down projections:
