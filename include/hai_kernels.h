@@ -294,6 +294,24 @@ int hai_deltanet_verify_bf16(void* out, int64_t ld_out, const void* proj,
                              int32_t pos_add, int64_t B, int64_t T, int64_t nk,
                              int64_t nv, int64_t dk, int64_t dv, int64_t Kc,
                              float eps, void* stream);
+/* hai_deltanet_verify_bf16 with the a|b projection formed in the kernel
+ * instead of read from proj: the in_proj_a / in_proj_b Linears of
+ * qwen_reference.cc:205-258 (bf16 weights also when the model's other
+ * Linears are FP8, qwen3_weights.cc:242-283), a_t[h] = xn_t . w_ab[h] and
+ * b_t[h] = xn_t . w_ab[nv + h] over the normalised input rows xn (ld_xn, row
+ * b*T + t), each computed in hai_gemm_bf16's order and rounded to bf16, so
+ * the result is bit-identical to running that GEMM into the proj columns
+ * first.  w_ab is [2*nv, H] row-major; 0 < H <= 8192, H % 8 == 0. */
+int hai_deltanet_verify_ab_bf16(void* out, int64_t ld_out, const void* proj,
+                                int64_t ld_proj, int64_t off_qkv, int64_t off_z,
+                                const void* xn, int64_t ld_xn, const void* w_ab,
+                                int64_t H, const void* conv_w, void* conv_ring,
+                                int64_t ring, float* state, int64_t nslots,
+                                int write_all_slots, const void* a_log,
+                                const void* dt_bias, const void* norm_w,
+                                const int32_t* lens, int32_t pos_add, int64_t B,
+                                int64_t T, int64_t nk, int64_t nv, int64_t dk,
+                                int64_t dv, int64_t Kc, float eps, void* stream);
 /* The reference's two-kernel DeltaNet contract (Backend::deltanet_grouped_conv
  * and Backend::deltanet_recurrent, hip_backend.cc:1357-1470), on the
  * reference's cache layouts:

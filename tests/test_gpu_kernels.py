@@ -985,3 +985,49 @@ def test_mfma_keep_partials_then_residual_rmsnorm(M, N, K, fp8):
     # keeping partials is only for the residual epilogue
     assert kern().hai_gemm_bf16_mfma(dh.ptr, N, dx.ptr, K, dx.ptr, M, N, K, hai.EPI_STORE | hai.MFMA_KEEP_PARTIALS,
                                      None, 0, dws.ptr, wsb, None) == hai.ERR_INVALID
+
+
+@pytest.mark.parametrize("H,nk,nv,dk,dv,B,T", [(256, 4, 4, 64, 64, 1, 2), (256, 2, 6, 64, 64, 3, 16),
+                                               (5120, 16, 48, 128, 128, 1, 2), (5120, 16, 48, 128, 128, 4, 4),
+                                               (1000, 4, 4, 64, 64, 2, 3)])
+def test_deltanet_verify_ab_matches_projection_then_kernel(H, nk, nv, dk, dv, B, T):
+    """hai_deltanet_verify_ab_bf16 forms the in_proj_a|b Linear of each head
+    itself: outputs, every state slot and the conv ring must equal running
+    that Linear with hai_gemm_bf16 into the proj columns (pinned to the
+    oracle by the GEMM tests) and then hai_deltanet_verify_bf16."""
+    rng = np.random.default_rng(H + nv + B * 10 + T)
+    c = _deltanet_case(rng, B, nk, nv, dk, dv)
+    C, Kc = c["C"], c["Kc"]
+    vw = nv * dv
+    width = C + vw + 2 * nv
+    ring, nslots = 32, 17
+    rows = B * T
+    _, xnb = rand_bf16(rng, (rows, H))
+    _, wab = rand_bf16(rng, (2 * nv, H), 0.05)
+    _, pb = rand_bf16(rng, (rows, width))
+    dcw, dal, ddt, dnw = dev(c["cwb"]), dev(c["alb"]), dev(c["dtb"]), dev(c["nwb"])
+    dxn, dwab = dev(xnb), dev(wab)
+    lens = dev(np.array([5 + 3 * b for b in range(B)], np.int32))
+    res = []
+    for mode in ("gemm", "ab"):
+        dproj = dev(pb)
+        dring = dev(rng.integers(0, 1 << 16, B * ring * C, dtype=np.uint16) * 0 + np.uint16(0x3f80))
+        dstate = dev(np.full(nslots * B * nv * dk * dv, 0.25, np.float32))
+        dout = out_buf(rows * vw * 2)
+        if mode == "gemm":
+            for m0 in range(0, rows, 16):  # the skinny GEMM takes 16 rows per call
+                hai.check(kern().hai_gemm_bf16(dproj.ptr + ((C + vw) + m0 * width) * 2, width, dxn.ptr + m0 * H * 2,
+                                               H, dwab.ptr, min(16, rows - m0), 2 * nv, H, hai.EPI_STORE, None, 0,
+                                               None), "a|b gemm")
+            hai.check(kern().hai_deltanet_verify_bf16(dout.ptr, vw, dproj.ptr, width, 0, C, C + vw, C + vw + nv,
+                                                      dcw.ptr, dring.ptr, ring, dstate.ptr, nslots, 1, dal.ptr,
+                                                      ddt.ptr, dnw.ptr, lens.ptr, 0, B, T, nk, nv, dk, dv, Kc, 1e-6,
+                                                      None), "deltanet")
+        else:
+            hai.check(kern().hai_deltanet_verify_ab_bf16(dout.ptr, vw, dproj.ptr, width, 0, C, dxn.ptr, H, dwab.ptr,
+                                                         H, dcw.ptr, dring.ptr, ring, dstate.ptr, nslots, 1, dal.ptr,
+                                                         ddt.ptr, dnw.ptr, lens.ptr, 0, B, T, nk, nv, dk, dv, Kc,
+                                                         1e-6, None), "deltanet_ab")
+        res.append([dout.download(np.uint16), dstate.download(np.uint32), dring.download(np.uint16)])
+    for name, g, w in zip(("out", "state", "ring"), res[1], res[0]):
+        np.testing.assert_array_equal(g, w, err_msg=name)

@@ -89,6 +89,8 @@ _KERNEL_SIGS = {
     "hai_gqa_verify_mfma_bf16": [VP, VP, VP, VP, VP, I64, VP, I64, I64, I64, I64, I64, VP, I32, I64, VP],
     "hai_deltanet_verify_bf16": [VP, I64, VP, I64, I64, I64, I64, I64, VP, VP, I64, VP, I64, ctypes.c_int, VP, VP,
                                  VP, VP, I32, I64, I64, I64, I64, I64, I64, I64, F32, VP],
+    "hai_deltanet_verify_ab_bf16": [VP, I64, VP, I64, I64, I64, VP, I64, VP, I64, VP, VP, I64, VP, I64, ctypes.c_int,
+                                    VP, VP, VP, VP, I32, I64, I64, I64, I64, I64, I64, I64, F32, VP],
     "hai_argmax_rows_bf16": [VP, VP, I64, I64, I64, VP, VP],
     "hai_verify_argmax_accept_bf16": [VP, I64, VP, I64, VP, VP, I64, I64, VP, VP, VP, VP, VP, VP, VP, VP, VP],
     "hai_add_i32": [VP, VP, I32, I64, VP],

@@ -47,7 +47,15 @@ struct DnArgs {
     const uint16_t *a_log, *dt_bias, *norm_w;
     int B, T, nk, nv, Kc;
     float eps;
+    // a|b from the normalised rows (ld_xn) and the [2 nv, H] a|b weight
+    // instead of proj columns off_a / off_b (null: read proj)
+    const uint16_t* xn;
+    int64_t ld_xn;
+    const uint16_t* w_ab;
+    int H;
 };
+
+constexpr int kSeg = 2048;  // the linear layers' fma segment (elements)
 
 // Gated delta rule over T tokens for one (value head, sequence).
 // REF = false: fused verify step -- grouped causal conv + SiLU from the
@@ -70,6 +78,7 @@ __global__ __launch_bounds__(DV * 4) void deltanet_kernel(DnArgs A) {
     float* vs = ks + T * DK;           // [T][DV] v channels
     float* os = vs + T * DV;           // [T][DV] unrounded recurrent output
     float* bks = os + T * DV;          // [T][DK] beta * normalised k
+    float* abp = bks + T * DK;         // w_ab: [T][2][nseg][64] lane partials of the a / b dot segments
     __shared__ float s_q[kMaxT], s_k[kMaxT], s_decay[kMaxT], s_beta[kMaxT], s_rms[kMaxT];
 
     const int h = blockIdx.x;
@@ -133,7 +142,7 @@ __global__ __launch_bounds__(DV * 4) void deltanet_kernel(DnArgs A) {
     // per-token gate scalars (last wave, lane = token)
     float a_in = 0.0f, b_in = 0.0f, dtb = 0.0f, alog = 0.0f;
     const bool scal = wave == NW - 1 && lane < T;
-    if (scal) {
+    if (scal && (REF || A.w_ab == nullptr)) {
         if constexpr (REF) {
             a_in = bf2f(A.a[static_cast<int64_t>(lane) * nv + h]);
             b_in = bf2f(A.bv[static_cast<int64_t>(lane) * nv + h]);
@@ -199,6 +208,43 @@ __global__ __launch_bounds__(DV * 4) void deltanet_kernel(DnArgs A) {
         ring_w = rp;
     }
 
+    // ---- a|b projection of this head (w_ab mode): the 2T dot products of
+    // the normalised rows with weight rows h (a) and nv + h (b), in the
+    // linear layers' order (hai_gemm_bf16 bit for bit); one wave per
+    // (token, a|b, 2048-element segment), lane partials to LDS ----
+    const int nseg = (A.H + kSeg - 1) / kSeg;
+    if constexpr (!REF) {
+        if (A.w_ab != nullptr) {
+            for (int task = wave; task < 2 * T * nseg; task += NW) {
+                const int sg = task % nseg;
+                const int d = task / nseg;  // = 2 t + (0 a | 1 b)
+                const int t = d >> 1;
+                const uint16_t* xr = A.xn + (row0 + t) * A.ld_xn;
+                const uint16_t* wr = A.w_ab + (static_cast<int64_t>(d & 1) * nv + h) * A.H;
+                uint4 xd[4], wd[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int k0 = sg * kSeg + u * 512 + lane * 8;
+                    const bool ok = k0 < A.H;
+                    xd[u] = ok ? *reinterpret_cast<const uint4*>(xr + k0) : make_uint4(0u, 0u, 0u, 0u);
+                    wd[u] = ok ? *reinterpret_cast<const uint4*>(wr + k0) : make_uint4(0u, 0u, 0u, 0u);
+                }
+                float acc = 0.0f;
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const uint32_t xw[4] = {xd[u].x, xd[u].y, xd[u].z, xd[u].w};
+                    const uint32_t ww[4] = {wd[u].x, wd[u].y, wd[u].z, wd[u].w};
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        acc = fma_(lo_bf(xw[q]), lo_bf(ww[q]), acc);
+                        acc = fma_(hi_bf(xw[q]), hi_bf(ww[q]), acc);
+                    }
+                }
+                abp[task * 64 + lane] = acc;
+            }
+        }
+    }
+
     // ---- grouped causal conv + SiLU (REF: inputs are already convolved) ----
     if (has_ch) {
         if constexpr (REF) {
@@ -228,13 +274,36 @@ __global__ __launch_bounds__(DV * 4) void deltanet_kernel(DnArgs A) {
             }
         }
     }
-    if (scal) {
+    const bool ab_dots = !REF && A.w_ab != nullptr;
+    if (scal && !ab_dots) {
         const float dtv = dtb + a_in;
         const float sp = fmaxf(dtv, 0.0f) + clog1p(cexp(-fabsf(dtv)));
         s_decay[lane] = cexp(-(cexp(alog) * sp));
         s_beta[lane] = csigmoid(b_in);
     }
     __syncthreads();
+
+    // w_ab mode: fold each dot's segments in order and butterfly (the GEMM's
+    // reduction), round to bf16 as the projection output, then the gates
+    if (ab_dots) {
+        const float dtb_h = bf2f(A.dt_bias[h]);
+        const float alog_h = bf2f(A.a_log[h]);
+        for (int t = NW - 1 - wave; t < T; t += NW) {
+            float ab[2];
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                float tot = 0.0f;
+                for (int sg = 0; sg < nseg; ++sg) tot = tot + abp[((2 * t + e) * nseg + sg) * 64 + lane];
+                ab[e] = bfr(wave_sum64(tot));
+            }
+            if (lane == 0) {
+                const float dtv = dtb_h + ab[0];
+                const float sp = fmaxf(dtv, 0.0f) + clog1p(cexp(-fabsf(dtv)));
+                s_decay[t] = cexp(-(cexp(alog_h) * sp));
+                s_beta[t] = csigmoid(ab[1]);
+            }
+        }
+    }
 
     // ---- L2 norms of q and k for every token (one wave per vector) ----
     const float rs_dk = 1.0f / csqrt(static_cast<float>(DK));
@@ -385,7 +454,8 @@ __global__ __launch_bounds__(256) void deltanet_conv_kernel(uint16_t* __restrict
 
 template <int DK, int DV, bool REF>
 int launch(const DnArgs& a, hipStream_t s) {
-    const size_t shmem = static_cast<size_t>(a.T) * (3 * DK + 2 * DV) * sizeof(float);
+    const size_t ab = a.w_ab != nullptr ? static_cast<size_t>(2 * a.T) * ((a.H + kSeg - 1) / kSeg) * 64 : 0;
+    const size_t shmem = (static_cast<size_t>(a.T) * (3 * DK + 2 * DV) + ab) * sizeof(float);
     deltanet_kernel<DK, DV, REF><<<dim3(a.nv, REF ? 1 : a.B), dim3(DV * 4), shmem, s>>>(a);
     return launched(REF ? "deltanet_recurrent_kernel" : "deltanet_verify_kernel");
 }
@@ -399,13 +469,13 @@ int dispatch(const DnArgs& a, int64_t dk, int64_t dv, hipStream_t s) {
 
 }  // namespace
 
-extern "C" int hai_deltanet_verify_bf16(void* out, int64_t ld_out, const void* proj, int64_t ld_proj,
-                                        int64_t off_qkv, int64_t off_z, int64_t off_a, int64_t off_b,
-                                        const void* conv_w, void* conv_ring, int64_t ring, float* state,
-                                        int64_t nslots, int write_all_slots, const void* a_log,
-                                        const void* dt_bias, const void* norm_w, const int32_t* lens,
-                                        int32_t pos_add, int64_t B, int64_t T, int64_t nk, int64_t nv,
-                                        int64_t dk, int64_t dv, int64_t Kc, float eps, void* stream) {
+namespace {
+
+int verify(void* out, int64_t ld_out, const void* proj, int64_t ld_proj, int64_t off_qkv, int64_t off_z,
+           int64_t off_a, int64_t off_b, const void* conv_w, void* conv_ring, int64_t ring, float* state,
+           int64_t nslots, int write_all_slots, const void* a_log, const void* dt_bias, const void* norm_w,
+           const int32_t* lens, int32_t pos_add, int64_t B, int64_t T, int64_t nk, int64_t nv, int64_t dk, int64_t dv,
+           int64_t Kc, float eps, const void* xn, int64_t ld_xn, const void* w_ab, int64_t H, void* stream) {
     if (out == nullptr || proj == nullptr || conv_w == nullptr || conv_ring == nullptr || state == nullptr ||
         a_log == nullptr || dt_bias == nullptr || norm_w == nullptr)
         return invalid("deltanet_verify: null pointer");
@@ -416,6 +486,12 @@ extern "C" int hai_deltanet_verify_bf16(void* out, int64_t ld_out, const void* p
     if (lens == nullptr && pos_add < 0) return invalid("deltanet_verify: negative position");
     if (!aligned16(state)) return invalid("deltanet_verify: state alignment");
     if (T > kMaxT) return invalid("deltanet_verify: at most 16 tokens per launch");
+    if (w_ab != nullptr) {
+        if (xn == nullptr || H <= 0 || H % 8 != 0 || H > 4 * kSeg || ld_xn < H || ld_xn % 8 != 0 || !aligned16(xn) ||
+            !aligned16(w_ab))
+            return invalid("deltanet_verify_ab: xn / w_ab (need 0 < H <= 8192, H % 8 == 0, ld_xn >= H, "
+                           "ld_xn % 8 == 0, 16-byte alignment)");
+    }
     if (B == 0 || T == 0) return HAI_OK;
     DnArgs a{};
     a.out = static_cast<uint16_t*>(out);
@@ -443,7 +519,39 @@ extern "C" int hai_deltanet_verify_bf16(void* out, int64_t ld_out, const void* p
     a.nv = int(nv);
     a.Kc = int(Kc);
     a.eps = eps;
+    a.xn = static_cast<const uint16_t*>(xn);
+    a.ld_xn = ld_xn;
+    a.w_ab = static_cast<const uint16_t*>(w_ab);
+    a.H = w_ab != nullptr ? int(H) : 0;
     return dispatch<false>(a, dk, dv, as_stream(stream));
+}
+
+}  // namespace
+
+extern "C" int hai_deltanet_verify_bf16(void* out, int64_t ld_out, const void* proj, int64_t ld_proj,
+                                        int64_t off_qkv, int64_t off_z, int64_t off_a, int64_t off_b,
+                                        const void* conv_w, void* conv_ring, int64_t ring, float* state,
+                                        int64_t nslots, int write_all_slots, const void* a_log,
+                                        const void* dt_bias, const void* norm_w, const int32_t* lens,
+                                        int32_t pos_add, int64_t B, int64_t T, int64_t nk, int64_t nv,
+                                        int64_t dk, int64_t dv, int64_t Kc, float eps, void* stream) {
+    return verify(out, ld_out, proj, ld_proj, off_qkv, off_z, off_a, off_b, conv_w, conv_ring, ring, state, nslots,
+                  write_all_slots, a_log, dt_bias, norm_w, lens, pos_add, B, T, nk, nv, dk, dv, Kc, eps, nullptr, 0,
+                  nullptr, 0, stream);
+}
+
+extern "C" int hai_deltanet_verify_ab_bf16(void* out, int64_t ld_out, const void* proj, int64_t ld_proj,
+                                           int64_t off_qkv, int64_t off_z, const void* xn, int64_t ld_xn,
+                                           const void* w_ab, int64_t H, const void* conv_w, void* conv_ring,
+                                           int64_t ring, float* state, int64_t nslots, int write_all_slots,
+                                           const void* a_log, const void* dt_bias, const void* norm_w,
+                                           const int32_t* lens, int32_t pos_add, int64_t B, int64_t T, int64_t nk,
+                                           int64_t nv, int64_t dk, int64_t dv, int64_t Kc, float eps,
+                                           void* stream) {
+    if (w_ab == nullptr) return invalid("deltanet_verify_ab: null w_ab");
+    return verify(out, ld_out, proj, ld_proj, off_qkv, off_z, 0, 0, conv_w, conv_ring, ring, state, nslots,
+                  write_all_slots, a_log, dt_bias, norm_w, lens, pos_add, B, T, nk, nv, dk, dv, Kc, eps, xn, ld_xn,
+                  w_ab, H, stream);
 }
 
 extern "C" int hai_deltanet_conv_bf16(void* q, void* k, void* v, void* conv_state, const void* qkv,

@@ -574,20 +574,24 @@ int Engine::forward_target(const int64_t* d_ids, int64_t T, bool write_all_slots
         } else {
             // qwen_deltanet_reference (qwen_reference.cc:205-258)
             if (fp8_) {
-                // FP8 qkv|z with the norm fused, writing the normalised rows
-                // that the bf16 a|b projection then reads
+                // FP8 qkv|z with the norm fused, writing the normalised rows;
+                // the bf16 a|b projection of each head is formed from them
+                // inside the DeltaNet kernel (no launch of its own)
                 HAI_TRY(norm_gemm(proj_, d.Nin, h_, L.in_ln, xn_, Lin(L.f_in), rows, d.C + d.vw, HAI_EPI_STORE,
                                   nullptr, 0));
-                HAI_TRY(gemm(proj_ + d.C + d.vw, d.Nin, xn_, d.H, L.w_ab, rows, 2 * d.nv, d.H, HAI_EPI_STORE,
-                             nullptr, 0));
+                HAI_TRY(flush_pending());
+                HAI_TRY(hai_deltanet_verify_ab_bf16(dnout_, d.vw, proj_, d.Nin, 0, d.C, xn_, d.H, L.w_ab, d.H,
+                                                    L.conv_w, L.ring, ring_, L.state, nslots_,
+                                                    write_all_slots ? 1 : 0, L.a_log, L.dt_bias, L.lin_norm, d_tlen_,
+                                                    0, B_, T, d.nk, d.nv, d.dk, d.dv, d.Kc, cfg_.rms_eps, stream_));
             } else {
                 HAI_TRY(norm_gemm(proj_, d.Nin, h_, L.in_ln, nullptr, L.w_in, rows, d.Nin, HAI_EPI_STORE, nullptr,
                                   0));
+                HAI_TRY(hai_deltanet_verify_bf16(dnout_, d.vw, proj_, d.Nin, 0, d.C, d.C + d.vw, d.C + d.vw + d.nv,
+                                                 L.conv_w, L.ring, ring_, L.state, nslots_, write_all_slots ? 1 : 0,
+                                                 L.a_log, L.dt_bias, L.lin_norm, d_tlen_, 0, B_, T, d.nk, d.nv, d.dk,
+                                                 d.dv, d.Kc, cfg_.rms_eps, stream_));
             }
-            HAI_TRY(hai_deltanet_verify_bf16(dnout_, d.vw, proj_, d.Nin, 0, d.C, d.C + d.vw, d.C + d.vw + d.nv,
-                                             L.conv_w, L.ring, ring_, L.state, nslots_, write_all_slots ? 1 : 0,
-                                             L.a_log, L.dt_bias, L.lin_norm, d_tlen_, 0, B_, T, d.nk, d.nv, d.dk,
-                                             d.dv, d.Kc, cfg_.rms_eps, stream_));
             HAI_TRY(gemm(h_, d.H, dnout_, d.vw, lin(L.w_out, L.f_out), rows, d.H, d.vw, HAI_EPI_RESIDUAL, h_, d.H));
         }
         HAI_TRY(mlp(L, T, h_));
