@@ -23,6 +23,7 @@
 // rows are bit-identical, and the CPU oracle follows the same order.
 #include "hai_common.h"
 #include "hai_device.h"
+#include "hai_gemm_common.h"
 
 namespace {
 
@@ -371,7 +372,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kMfmaWaves = 4;
 constexpr int kMfmaMaxSteps = 16;          // steps per wave and block
-constexpr int64_t kMfmaTargetBlocks = 512; // blocks the split count aims for
+constexpr int64_t kMfmaTargetBlocks = 512; // blocks the split count aims for when the occupancy is unknown
 constexpr int kMfmaMinBlockKeys = 128;     // keys of the smallest block (one 32-key step per wave)
 
 __host__ __device__ constexpr int mfma_step_keys(int D) { return D == 64 ? 64 : 32; }
@@ -743,7 +744,11 @@ struct MfmaPlan {
     int qt, qgroups, steps, nsplit, block_keys;
 };
 
-inline MfmaPlan mfma_plan(int D, int64_t B, int64_t T, int64_t nq, int64_t nkv, int64_t max_len) {
+// `target`: the blocks the device holds at once (occupancy x CUs), so that
+// every split runs in one round: at D = 256 a wave takes a whole SIMD and
+// 512 blocks would leave a second, partly empty round (C4: 416 blocks on 256
+// CUs).
+inline MfmaPlan mfma_plan(int D, int64_t B, int64_t T, int64_t nq, int64_t nkv, int64_t max_len, int64_t target) {
     MfmaPlan p{};
     const int64_t nqry = T * (nq / nkv);
     p.qt = nqry <= 16 ? 1 : 2;
@@ -751,7 +756,7 @@ inline MfmaPlan mfma_plan(int D, int64_t B, int64_t T, int64_t nq, int64_t nkv, 
     const int step_keys = kMfmaWaves * mfma_step_keys(D);
     const int64_t units = (max_len + step_keys - 1) / step_keys;  // block steps covering max_len
     const int64_t pairs = nkv * p.qgroups * B;
-    const int64_t per_pair = (kMfmaTargetBlocks + pairs - 1) / pairs;  // splits wanted per (head, sequence)
+    const int64_t per_pair = target >= pairs ? target / pairs : 1;  // splits per (head, sequence)
     int64_t steps = (units + per_pair - 1) / per_pair;
     steps = steps < 1 ? 1 : (steps > kMfmaMaxSteps ? kMfmaMaxSteps : steps);
     p.steps = static_cast<int>(steps);
@@ -764,7 +769,11 @@ template <int D>
 int launch_mfma(uint16_t* out, const uint16_t* q, const uint16_t* gate, const uint16_t* kc, const uint16_t* vc,
                 int64_t cap, float* scratch, int B, int T, int nq, int nkv, const int32_t* lens, int len_add,
                 int64_t max_len, hipStream_t s) {
-    const MfmaPlan p = mfma_plan(D, B, T, nq, nkv, max_len);
+    const int64_t nqry = static_cast<int64_t>(T) * (nq / nkv);
+    const void* kern = nqry <= 16 ? reinterpret_cast<const void*>(gqa_mfma_partial_kernel<D, 1>)
+                                  : reinterpret_cast<const void*>(gqa_mfma_partial_kernel<D, 2>);
+    const int64_t resident = resident_blocks(kern, 0);
+    const MfmaPlan p = mfma_plan(D, B, T, nq, nkv, max_len, resident > 0 ? resident : kMfmaTargetBlocks);
     const float scale_log2 = 1.4426950408889634f / __builtin_sqrtf(static_cast<float>(D));
     const dim3 grid(p.nsplit, nkv * p.qgroups, B);
     if (p.qt == 1)
