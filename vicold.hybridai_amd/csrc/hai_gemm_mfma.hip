@@ -30,6 +30,7 @@
 //     interleaved (gate_f, up_f) rows.
 #include "hai_common.h"
 #include "hai_device.h"
+#include "hai_gemm_common.h"
 
 namespace {
 
@@ -64,14 +65,24 @@ __device__ __forceinline__ void mfma_store(uint16_t* y, int64_t ldy, const uint1
     }
 }
 
+// Stream-K split (sk > 0 blocks): the ntiles x nck (tile, chunk) items are
+// cut into sk equal contiguous ranges, block b taking [b I / sk, (b+1) I /
+// sk).  Used when the tiles exceed one round of resident blocks, so a block
+// takes more than one tile's chunks and a tile spans at most two blocks: the
+// block holding its first chunk writes partial plane 0, the other plane 1.
+// Tiles inside one block are finished in place.
+__host__ __device__ inline int64_t sk_block_of(int64_t item, int64_t items, int64_t sk) {
+    return ((item + 1) * sk - 1) / items;
+}
+
 // grid (ceil(N / 64), KSB); with KSB > 1 the blocks of split s take chunks
 // s, s + KSB, ... and write fp32 partials part[s][m][n].
-template <int MT, int EPI>
+template <int MT, int EPI, bool SK>
 __global__ __launch_bounds__(256) void gemm_bf16_mfma_kernel(uint16_t* __restrict__ y, int64_t ldy,
                                                              const uint16_t* __restrict__ x, int64_t ldx,
                                                              const uint16_t* __restrict__ w, const uint16_t* res,
                                                              int64_t ldres, int M, int N, int K,
-                                                             float* __restrict__ part, int KSB) {
+                                                             float* __restrict__ part, int KSB, int sk) {
     extern __shared__ __align__(16) uint16_t lds[];
     uint16_t* xs = lds;                          // [16 MT][kLdsRow] activation rows
     uint16_t* ws = lds + 16 * MT * kLdsRow;      // [4 waves][16][kLdsRow] weight rows
@@ -80,7 +91,12 @@ __global__ __launch_bounds__(256) void gemm_bf16_mfma_kernel(uint16_t* __restric
     const int wave = wave_index();
     const int li = lane & 15;
     const int kg = lane >> 4;
-    const int64_t row_base = static_cast<int64_t>(blockIdx.x) * kBlockRows + wave * 16;
+    const int nck = (K + kChunk - 1) / kChunk;
+    const int nfull = K / kChunk;
+    // one tile (64 weight rows) over chunks cbeg, cbeg + cstep, ... < cend;
+    // plane < 0: finish y, else write partial plane `plane`
+    auto piece = [&](int64_t tile, int cbeg, int cend, int cstep, int plane) {
+    const int64_t row_base = tile * kBlockRows + wave * 16;
 
     // Byte offsets fit 32 bits: the caller bounds N*K*2 and M*ldx*2 below 4
     // GiB.  Rows past N or M start at or past the buffer end and read zeros.
@@ -107,9 +123,6 @@ __global__ __launch_bounds__(256) void gemm_bf16_mfma_kernel(uint16_t* __restric
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    const int nck = (K + kChunk - 1) / kChunk;
-    const int nfull = K / kChunk;
-    const int split = blockIdx.y;
     u32x4 wv[8], xv[XL];
     auto load = [&](int c) {
         const uint32_t off = static_cast<uint32_t>(c) * (kChunk * 2);
@@ -127,9 +140,9 @@ __global__ __launch_bounds__(256) void gemm_bf16_mfma_kernel(uint16_t* __restric
             for (int i = 0; i < XL; ++i) xv[i] = bload(rx, c * kChunk + xcol[i] < K ? xoff[i] + off : kOutOfRange, 0u);
         }
     };
-    int c = split;
-    if (c < nck) load(c);
-    for (; c < nck; c += KSB) {
+    int c = cbeg;
+    if (c < cend) load(c);
+    for (; c < cend; c += cstep) {
         __syncthreads();  // the previous chunk's LDS reads are done
 #pragma unroll
         for (int i = 0; i < 8; ++i)
@@ -137,7 +150,7 @@ __global__ __launch_bounds__(256) void gemm_bf16_mfma_kernel(uint16_t* __restric
 #pragma unroll
         for (int i = 0; i < XL; ++i) *reinterpret_cast<u32x4*>(&xs[xrow[i] * kLdsRow + xcol[i]]) = xv[i];
         __syncthreads();
-        if (c + KSB < nck) load(c + KSB);
+        if (c + cstep < cend) load(c + cstep);
 #pragma unroll
         for (int j = 0; j < kChunk / 32; ++j) {
             const u32x4 b = *reinterpret_cast<const u32x4*>(&ws[(wave * 16 + li) * kLdsRow + 32 * j + 8 * kg]);
@@ -156,11 +169,28 @@ __global__ __launch_bounds__(256) void gemm_bf16_mfma_kernel(uint16_t* __restric
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int m = 16 * mt + 4 * kg + i;
-            if (KSB == 1)
+            if (plane < 0)
                 mfma_store<EPI>(y, ldy, res, ldres, acc[mt][i], m, n, M, N, li);
             else if (m < M && n < N)
-                part[(static_cast<int64_t>(split) * M + m) * N + n] = acc[mt][i];
+                part[(static_cast<int64_t>(plane) * M + m) * N + n] = acc[mt][i];
         }
+    };
+    if constexpr (!SK) {
+        piece(blockIdx.x, blockIdx.y, nck, KSB, KSB == 1 ? -1 : static_cast<int>(blockIdx.y));
+        return;
+    }
+    const int64_t ntiles = (N + kBlockRows - 1) / kBlockRows;
+    const int64_t items = ntiles * nck;
+    const int64_t lo = static_cast<int64_t>(blockIdx.x) * items / sk;
+    const int64_t hi = (static_cast<int64_t>(blockIdx.x) + 1) * items / sk;
+    for (int64_t it = lo; it < hi;) {
+        const int64_t tile = it / nck;
+        const int c0 = static_cast<int>(it - tile * nck);
+        const int c1 = static_cast<int>(min(hi - tile * nck, static_cast<int64_t>(nck)));
+        const int plane = (c0 == 0 && c1 == nck) ? -1 : (sk_block_of(tile * nck, items, sk) == blockIdx.x ? 0 : 1);
+        piece(tile, c0, c1, 1, plane);  // (a piece's first chunk waits for the LDS reads of the last one)
+        it = tile * nck + c1;
+    }
 }
 
 // Sums the KSB partials of every element in split order and applies the
@@ -180,6 +210,38 @@ __global__ void mfma_finalize_kernel(uint16_t* __restrict__ y, int64_t ldy, cons
         float s = part[at];
         for (int q = 1; q < KSB; ++q) s = s + part[static_cast<int64_t>(q) * M * N + at];
         v[e] = s;
+    }
+    if (EPI == HAI_EPI_SILU_MUL) {
+        if (n + 1 < N) y[static_cast<int64_t>(m) * ldy + n / 2] = f2bf(csilu(bfr(v[0])) * bfr(v[1]));
+        return;
+    }
+    for (int e = 0; e < 2; ++e) {
+        if (n + e >= N) continue;
+        float o = bfr(v[e]);
+        if (EPI == HAI_EPI_RESIDUAL) o = bf2f(res[static_cast<int64_t>(m) * ldres + n + e]) + o;
+        y[static_cast<int64_t>(m) * ldy + n + e] = f2bf(o);
+    }
+}
+
+// Stream-K finalize: the tiles that two blocks share get plane 0 + plane 1
+// (the order of the K-split pass) and the epilogue; the others were finished
+// by their block.
+template <int EPI>
+__global__ void mfma_sk_finalize_kernel(uint16_t* __restrict__ y, int64_t ldy, const float* __restrict__ part,
+                                        const uint16_t* res, int64_t ldres, int M, int N, int nck, int sk) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int64_t np = (static_cast<int64_t>(N) + 1) / 2;
+    if (i >= static_cast<int64_t>(M) * np) return;
+    const int m = static_cast<int>(i / np);
+    const int64_t n = (i - m * np) * 2;
+    const int64_t tile = n / kBlockRows;
+    const int64_t items = ((static_cast<int64_t>(N) + kBlockRows - 1) / kBlockRows) * nck;
+    if (sk_block_of(tile * nck, items, sk) == sk_block_of(tile * nck + nck - 1, items, sk)) return;
+    float v[2] = {0.0f, 0.0f};
+    for (int e = 0; e < 2; ++e) {
+        if (n + e >= N) continue;
+        const int64_t at = static_cast<int64_t>(m) * N + n + e;
+        v[e] = part[at] + part[static_cast<int64_t>(M) * N + at];
     }
     if (EPI == HAI_EPI_SILU_MUL) {
         if (n + 1 < N) y[static_cast<int64_t>(m) * ldy + n / 2] = f2bf(csilu(bfr(v[0])) * bfr(v[1]));
@@ -322,14 +384,14 @@ __device__ __forceinline__ void e4m3x4_to_bf16(uint32_t w, uint32_t& lo, uint32_
 // bf16 into its LDS tile, the matrix cores sum every 128-k scale block on
 // its own, and the block's scale of the output column (weight row) is
 // applied in fp32: y = sum_kb s[sr(n)][kb] * (x . decode(q))_kb.
-template <int MT, int EPI, bool CHECK, bool DB>
+template <int MT, int EPI, bool CHECK, bool DB, bool SK>
 __global__ __launch_bounds__(256) void gemm_fp8_mfma_kernel(uint16_t* __restrict__ y, int64_t ldy,
                                                             const uint16_t* __restrict__ x, int64_t ldx,
                                                             const uint8_t* __restrict__ wq,
                                                             const float* __restrict__ scales,
                                                             const int32_t* __restrict__ scale_rows, int paired,
                                                             const uint16_t* res, int64_t ldres, int M, int N, int K,
-                                                            float* __restrict__ part, int KSB) {
+                                                            float* __restrict__ part, int KSB, int sk) {
     extern __shared__ __align__(16) uint16_t lds[];
     uint16_t* xs = lds;                          // [16 MT][kLdsRow]
     uint16_t* ws = lds + 16 * MT * kLdsRow;      // [4 waves][16][kLdsRow], decoded bf16
@@ -338,8 +400,13 @@ __global__ __launch_bounds__(256) void gemm_fp8_mfma_kernel(uint16_t* __restrict
     const int wave = wave_index();
     const int li = lane & 15;
     const int kg = lane >> 4;
-    const int64_t row_base = static_cast<int64_t>(blockIdx.x) * kBlockRows + wave * 16;
     const int nkb = (K + 127) / 128;
+    const int nck = (K + kChunk - 1) / kChunk;
+    const int nfull = K / kChunk;
+    // one tile (64 weight rows) over chunks cbeg, cbeg + cstep, ... < cend;
+    // plane < 0: finish y, else write partial plane `plane`
+    auto piece = [&](int64_t tile, int cbeg, int cend, int cstep, int plane) {
+    const int64_t row_base = tile * kBlockRows + wave * 16;
 
     const __amdgpu_buffer_rsrc_t rw = make_rsrc(wq, static_cast<uint32_t>(static_cast<int64_t>(N) * K));
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, static_cast<uint32_t>(static_cast<int64_t>(M) * ldx * 2));
@@ -368,9 +435,6 @@ __global__ __launch_bounds__(256) void gemm_fp8_mfma_kernel(uint16_t* __restrict
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) tot[mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    const int nck = (K + kChunk - 1) / kChunk;
-    const int nfull = K / kChunk;
-    const int split = blockIdx.y;
     u32x4 xv[XL];
     // codes of chunk c and the scales of its k-blocks 2c, 2c + 1 (a past-K
     // block gets a finite stand-in; its products are zero)
@@ -438,14 +502,14 @@ __global__ __launch_bounds__(256) void gemm_fp8_mfma_kernel(uint16_t* __restrict
     };
     u32x4 wA[4];
     float sA[2];
-    int c = split;
+    int c = cbeg;
     if constexpr (!DB) {
         // one chunk in flight while the current one is multiplied
-        if (c < nck) { load_w(wA, sA, c); load_x(c); }
-        for (; c < nck; c += KSB) {
+        if (c < cend) { load_w(wA, sA, c); load_x(c); }
+        for (; c < cend; c += cstep) {
             stage(wA);
             const float s0 = sA[0], s1 = sA[1];
-            if (c + KSB < nck) { load_w(wA, sA, c + KSB); load_x(c + KSB); }
+            if (c + cstep < cend) { load_w(wA, sA, c + cstep); load_x(c + cstep); }
             compute(s0, s1);
         }
     } else {
@@ -454,19 +518,19 @@ __global__ __launch_bounds__(256) void gemm_fp8_mfma_kernel(uint16_t* __restrict
         // so waiting for them leaves those codes outstanding
         u32x4 wB[4];
         float sB[2];
-        if (c < nck) { load_w(wA, sA, c); load_x(c); }
-        if (c + KSB < nck) load_w(wB, sB, c + KSB);
-        for (; c < nck; c += 2 * KSB) {
+        if (c < cend) { load_w(wA, sA, c); load_x(c); }
+        if (c + cstep < cend) load_w(wB, sB, c + cstep);
+        for (; c < cend; c += 2 * cstep) {
             stage(wA);
             const float a0 = sA[0], a1 = sA[1];
-            if (c + KSB < nck) load_x(c + KSB);
-            if (c + 2 * KSB < nck) load_w(wA, sA, c + 2 * KSB);
+            if (c + cstep < cend) load_x(c + cstep);
+            if (c + 2 * cstep < cend) load_w(wA, sA, c + 2 * cstep);
             compute(a0, a1);
-            if (c + KSB >= nck) break;
+            if (c + cstep >= cend) break;
             stage(wB);
             const float b0 = sB[0], b1 = sB[1];
-            if (c + 2 * KSB < nck) load_x(c + 2 * KSB);
-            if (c + 3 * KSB < nck) load_w(wB, sB, c + 3 * KSB);
+            if (c + 2 * cstep < cend) load_x(c + 2 * cstep);
+            if (c + 3 * cstep < cend) load_w(wB, sB, c + 3 * cstep);
             compute(b0, b1);
         }
     }
@@ -477,11 +541,28 @@ __global__ __launch_bounds__(256) void gemm_fp8_mfma_kernel(uint16_t* __restrict
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int m = 16 * mt + 4 * kg + i;
-            if (KSB == 1)
+            if (plane < 0)
                 mfma_store<EPI>(y, ldy, res, ldres, tot[mt][i], m, n, M, N, li);
             else if (m < M && n < N)
-                part[(static_cast<int64_t>(split) * M + m) * N + n] = tot[mt][i];
+                part[(static_cast<int64_t>(plane) * M + m) * N + n] = tot[mt][i];
         }
+    };
+    if constexpr (!SK) {
+        piece(blockIdx.x, blockIdx.y, nck, KSB, KSB == 1 ? -1 : static_cast<int>(blockIdx.y));
+        return;
+    }
+    const int64_t ntiles = (N + kBlockRows - 1) / kBlockRows;
+    const int64_t items = ntiles * nck;
+    const int64_t lo = static_cast<int64_t>(blockIdx.x) * items / sk;
+    const int64_t hi = (static_cast<int64_t>(blockIdx.x) + 1) * items / sk;
+    for (int64_t it = lo; it < hi;) {
+        const int64_t tile = it / nck;
+        const int c0 = static_cast<int>(it - tile * nck);
+        const int c1 = static_cast<int>(min(hi - tile * nck, static_cast<int64_t>(nck)));
+        const int plane = (c0 == 0 && c1 == nck) ? -1 : (sk_block_of(tile * nck, items, sk) == blockIdx.x ? 0 : 1);
+        piece(tile, c0, c1, 1, plane);  // (a piece's first chunk waits for the LDS reads of the last one)
+        it = tile * nck + c1;
+    }
 }
 
 struct MfmaArgs {
@@ -502,6 +583,7 @@ struct MfmaArgs {
     int paired = 0;
     bool check = true;
     bool keep = false;  // leave the K-split partials for hai_mfma_residual_rmsnorm_bf16
+    size_t ws_bytes = 0;
 };
 
 // LDS above the 64 KB default needs the attribute, once per kernel instance.
@@ -514,33 +596,85 @@ int allow_lds(const void* kern, size_t shmem, bool* done) {
     return rc;
 }
 
+// Stream-K when the plain grid would load the CUs unevenly.  The time of a
+// matrix-core GEMM follows its busiest CU: 544 tiles of 64 rows on 256 CUs
+// put 3 blocks on 32 CUs and 2 on the rest, and those take 1.5x as long
+// (MI355X, M = 32: 512 tiles 56 us, 544 tiles 74 us; at M = 64, two
+// resident blocks per CU, the 32 extra tiles even form a second round: 63 ->
+// 94 us).  With ntiles = (k + f) x CUs, 1 <= k <= the blocks a CU holds and
+// 0 < f <= 0.25, stream-K runs k x CUs blocks of (k + f) / k tiles each
+// (544 tiles: M = 64 FP8 94 -> 80 us, M = 32 bf16 74 -> 70 us, with the
+// finalize pass); every tile then spans at most two blocks.  At f = 0.5 (640
+// tiles) or more than k blocks per CU the plain grid measured as fast or
+// faster.
+int sk_blocks(const void* kern, size_t shmem, const MfmaArgs& a) {
+    if (a.KSB != 1 || a.keep || a.part == nullptr ||
+        a.ws_bytes < static_cast<size_t>(2) * a.M * a.N * sizeof(float))
+        return 0;
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        return 0;
+    const int64_t ntiles = (static_cast<int64_t>(a.N) + kBlockRows - 1) / kBlockRows;
+    const int64_t per_cu = resident_blocks(kern, shmem) / cus;
+    const int64_t k = ntiles / cus;
+    const int64_t rem = ntiles - k * cus;  // f x CUs
+    if (k < 1 || k > per_cu || rem == 0 || 4 * rem > cus) return 0;
+    return static_cast<int>(k * cus);
+}
+
 template <int MT, int EPI>
 int launch_mfma(const MfmaArgs& a, hipStream_t s) {
     const size_t shmem = static_cast<size_t>(16 * MT + 4 * 16) * kLdsRow * 2;
     const dim3 grid(static_cast<unsigned>((a.N + kBlockRows - 1) / kBlockRows), static_cast<unsigned>(a.KSB));
     int rc;
+    int sk = 0;
     if (a.wq != nullptr) {
         // two chunks of codes in flight from 64 rows (measured on MI355X at
         // M = 64: gate/up 108 -> 90 us; at M = 32 one chunk is faster)
         constexpr bool kDB = MT >= 4;
-        auto* kern = a.check ? gemm_fp8_mfma_kernel<MT, EPI, true, kDB> : gemm_fp8_mfma_kernel<MT, EPI, false, kDB>;
-        static bool attr[2] = {false, false};
+        auto* kern = a.check ? gemm_fp8_mfma_kernel<MT, EPI, true, kDB, false>
+                             : gemm_fp8_mfma_kernel<MT, EPI, false, kDB, false>;
+        auto* kern_sk = a.check ? gemm_fp8_mfma_kernel<MT, EPI, true, kDB, true>
+                                : gemm_fp8_mfma_kernel<MT, EPI, false, kDB, true>;
+        static bool attr[4] = {false, false, false, false};
         rc = allow_lds(reinterpret_cast<const void*>(kern), shmem, &attr[a.check ? 1 : 0]);
+        if (rc == HAI_OK) rc = allow_lds(reinterpret_cast<const void*>(kern_sk), shmem, &attr[a.check ? 3 : 2]);
         if (rc != HAI_OK) return rc;
-        kern<<<grid, dim3(256), shmem, s>>>(a.y, a.ldy, a.x, a.ldx, a.wq, a.scales, a.scale_rows, a.paired, a.res,
-                                            a.ldres, a.M, a.N, a.K, a.part, a.KSB);
+        sk = sk_blocks(reinterpret_cast<const void*>(kern_sk), shmem, a);
+        if (sk)
+            kern_sk<<<dim3(static_cast<unsigned>(sk)), dim3(256), shmem, s>>>(
+                a.y, a.ldy, a.x, a.ldx, a.wq, a.scales, a.scale_rows, a.paired, a.res, a.ldres, a.M, a.N, a.K, a.part,
+                a.KSB, sk);
+        else
+            kern<<<grid, dim3(256), shmem, s>>>(a.y, a.ldy, a.x, a.ldx, a.wq, a.scales, a.scale_rows, a.paired,
+                                                a.res, a.ldres, a.M, a.N, a.K, a.part, a.KSB, 0);
         rc = launched("gemm_fp8_mfma_kernel");
     } else {
-        auto* kern = gemm_bf16_mfma_kernel<MT, EPI>;
-        static bool attr = false;
-        rc = allow_lds(reinterpret_cast<const void*>(kern), shmem, &attr);
+        auto* kern = gemm_bf16_mfma_kernel<MT, EPI, false>;
+        auto* kern_sk = gemm_bf16_mfma_kernel<MT, EPI, true>;
+        static bool attr[2] = {false, false};
+        rc = allow_lds(reinterpret_cast<const void*>(kern), shmem, &attr[0]);
+        if (rc == HAI_OK) rc = allow_lds(reinterpret_cast<const void*>(kern_sk), shmem, &attr[1]);
         if (rc != HAI_OK) return rc;
-        kern<<<grid, dim3(256), shmem, s>>>(a.y, a.ldy, a.x, a.ldx, a.w, a.res, a.ldres, a.M, a.N, a.K, a.part,
-                                            a.KSB);
+        sk = sk_blocks(reinterpret_cast<const void*>(kern_sk), shmem, a);
+        if (sk)
+            kern_sk<<<dim3(static_cast<unsigned>(sk)), dim3(256), shmem, s>>>(a.y, a.ldy, a.x, a.ldx, a.w, a.res,
+                                                                             a.ldres, a.M, a.N, a.K, a.part, a.KSB,
+                                                                             sk);
+        else
+            kern<<<grid, dim3(256), shmem, s>>>(a.y, a.ldy, a.x, a.ldx, a.w, a.res, a.ldres, a.M, a.N, a.K, a.part,
+                                                a.KSB, 0);
         rc = launched("gemm_bf16_mfma_kernel");
     }
-    if (rc != HAI_OK || a.KSB == 1 || a.keep) return rc;
+    if (rc != HAI_OK) return rc;
     const int64_t n = static_cast<int64_t>(a.M) * ((a.N + 1) / 2);
+    if (sk) {
+        mfma_sk_finalize_kernel<EPI><<<dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s>>>(
+            a.y, a.ldy, a.part, a.res, a.ldres, a.M, a.N, (a.K + kChunk - 1) / kChunk, sk);
+        return launched("mfma_sk_finalize_kernel");
+    }
+    if (a.KSB == 1 || a.keep) return HAI_OK;
     mfma_finalize_kernel<EPI><<<dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s>>>(
         a.y, a.ldy, a.part, a.KSB, a.res, a.ldres, a.M, a.N);
     return launched("mfma_finalize_kernel");
@@ -557,8 +691,10 @@ int dispatch_mfma(const MfmaArgs& a, hipStream_t s) {
 }  // namespace
 
 extern "C" size_t hai_gemm_mfma_workspace_bytes(int64_t M, int64_t N) {
-    // largest split the dispatcher picks for this shape (4 at N <= 8192, 2 at N <= 20480)
-    const int64_t ksb = N <= 8192 ? 4 : (N <= 20480 ? 2 : 1);
+    // largest split the dispatcher picks for this shape (4 at N <= 8192, 2 at
+    // N <= 20480), or the two stream-K planes of the wider layers that need
+    // between one and two rounds of blocks (N up to 2 x 1024 tiles of 64)
+    const int64_t ksb = N <= 8192 ? 4 : (N <= 20480 ? 2 : (N <= 131072 ? 2 : 1));
     return ksb > 1 ? static_cast<size_t>(ksb * M * N) * sizeof(float) : 0;
 }
 
@@ -582,6 +718,7 @@ int mfma_entry(MfmaArgs& a, int epilogue, void* workspace, size_t workspace_byte
     epilogue &= ~HAI_MFMA_KEEP_PARTIALS;
     if (a.keep && epilogue != HAI_EPI_RESIDUAL) return invalid("gemm_mfma: keeping partials needs the residual epilogue");
     a.part = static_cast<float*>(workspace);
+    a.ws_bytes = workspace != nullptr ? workspace_bytes : 0;
     a.KSB = choose_splits(a.M, a.N, a.K, workspace, workspace_bytes);
     switch (epilogue) {
         case HAI_EPI_STORE:
