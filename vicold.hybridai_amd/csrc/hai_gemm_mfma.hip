@@ -702,13 +702,44 @@ namespace {
 
 // K split across blocks for narrow layers (measured on MI355X at M = 32:
 // N = 5120 4 splits +115 %, N = 16384 2 splits +9 %), if the workspace holds
-// the partials and every split gets at least two chunks.
+// the partials and every split gets at least two chunks.  For N <= 8192 the
+// split count is the one that loads the busiest CU least (tiles x splits
+// blocks on the CUs, ties to more splits): the time of these launches
+// follows their busiest CU, so N = 5120 (80 tiles) takes 3 splits, 240
+// blocks, rather than 4, whose 320 blocks double up on 64 CUs.
+int device_cus() {
+    static int cached = 0;
+    if (cached > 0) return cached;
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0)
+        cached = cus;
+    return cached > 0 ? cached : 256;
+}
+
 int choose_splits(int64_t M, int64_t N, int64_t K, const void* workspace, size_t workspace_bytes) {
     const int64_t nck = (K + kChunk - 1) / kChunk;
-    int ksb = N <= 8192 ? 4 : (N <= 20480 ? 2 : 1);
-    while (ksb > 1 && (nck < 2 * ksb || workspace == nullptr ||
-                       workspace_bytes < static_cast<size_t>(int64_t{ksb} * M * N) * sizeof(float)))
-        ksb /= 2;
+    auto fits = [&](int64_t ksb) {
+        return nck >= 2 * ksb && workspace != nullptr &&
+               workspace_bytes >= static_cast<size_t>(ksb * M * N) * sizeof(float);
+    };
+    if (N <= 8192) {
+        const int64_t cus = device_cus();
+        const int64_t ntiles = (N + kBlockRows - 1) / kBlockRows;
+        int best = 1;
+        double best_load = static_cast<double>((ntiles + cus - 1) / cus);
+        for (int ksb = 2; ksb <= 4; ++ksb) {
+            if (!fits(ksb) || ntiles * ksb > 2 * cus) continue;  // at most two blocks per CU
+            const double load = static_cast<double>((ntiles * ksb + cus - 1) / cus) / ksb;
+            if (load <= best_load) {
+                best = ksb;
+                best_load = load;
+            }
+        }
+        return best;
+    }
+    int ksb = N <= 20480 ? 2 : 1;
+    while (ksb > 1 && !fits(ksb)) ksb /= 2;
     return ksb;
 }
 
