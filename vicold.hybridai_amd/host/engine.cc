@@ -584,6 +584,19 @@ int Engine::forward_target(const int64_t* d_ids, int64_t T, bool write_all_slots
                                                     L.conv_w, L.ring, ring_, L.state, nslots_,
                                                     write_all_slots ? 1 : 0, L.a_log, L.dt_bias, L.lin_norm, d_tlen_,
                                                     0, B_, T, d.nk, d.nv, d.dk, d.dv, d.Kc, cfg_.rms_eps, stream_));
+            } else if (use_mfma(rows)) {
+                // matrix-core mode: the qkv|z rows only (16384 rows at the 27B
+                // shape, whole 64-row tiles that load every CU alike, where
+                // [qkv|z|a|b] leaves a half tile); a|b formed in the DeltaNet
+                // kernel from the normalised rows, as with FP8 weights
+                HAI_TRY(norm_gemm(proj_, d.Nin, h_, L.in_ln, xn_, L.w_in, rows, d.C + d.vw, HAI_EPI_STORE, nullptr,
+                                  0));
+                HAI_TRY(flush_pending());
+                HAI_TRY(hai_deltanet_verify_ab_bf16(dnout_, d.vw, proj_, d.Nin, 0, d.C, xn_, d.H,
+                                                    L.w_in + (d.C + d.vw) * d.H, d.H, L.conv_w, L.ring, ring_,
+                                                    L.state, nslots_, write_all_slots ? 1 : 0, L.a_log, L.dt_bias,
+                                                    L.lin_norm, d_tlen_, 0, B_, T, d.nk, d.nv, d.dk, d.dv, d.Kc,
+                                                    cfg_.rms_eps, stream_));
             } else {
                 HAI_TRY(norm_gemm(proj_, d.Nin, h_, L.in_ln, nullptr, L.w_in, rows, d.Nin, HAI_EPI_STORE, nullptr,
                                   0));
