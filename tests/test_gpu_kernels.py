@@ -982,9 +982,12 @@ def test_mfma_keep_partials_then_residual_rmsnorm(M, N, K, fp8):
     hai.check(kern().hai_mfma_residual_rmsnorm_bf16(dh2.ptr, N, dws.ptr, M, N, splits, None, 0.0, 0, None, 0, None),
               "residual only")
     assert_bits_equal(dh2.download(np.uint16), hai.bf16_to_f32(ref_h.download(np.uint16)), "residual rows, no norm")
-    # keeping partials is only for the residual epilogue
-    assert kern().hai_gemm_bf16_mfma(dh.ptr, N, dx.ptr, K, dx.ptr, M, N, K, hai.EPI_STORE | hai.MFMA_KEEP_PARTIALS,
-                                     None, 0, dws.ptr, wsb, None) == hai.ERR_INVALID
+    # keeping partials is for the residual epilogue only (operands sized for
+    # the call, so even an accepted call would stay in bounds)
+    if not fp8:
+        for epi, ldy in ((hai.EPI_STORE, N), (hai.EPI_SILU_MUL, N // 2)):
+            assert kern().hai_gemm_bf16_mfma(dh.ptr, ldy, dx.ptr, K, dw.ptr, M, N, K, epi | hai.MFMA_KEEP_PARTIALS,
+                                             None, 0, dws.ptr, wsb, None) == hai.ERR_INVALID
 
 
 @pytest.mark.parametrize("H,nk,nv,dk,dv,B,T", [(256, 4, 4, 64, 64, 1, 2), (256, 2, 6, 64, 64, 3, 16),
