@@ -28,6 +28,8 @@
 //     measured 1.8x slower than the second launch on MI355X.)
 //   * Epilogues as in the skinny GEMM: store, residual add, SwiGLU over
 //     interleaved (gate_f, up_f) rows.
+#include <atomic>
+
 #include "hai_common.h"
 #include "hai_device.h"
 #include "hai_gemm_common.h"
@@ -708,13 +710,16 @@ namespace {
 // follows their busiest CU, so N = 5120 (80 tiles) takes 3 splits, 240
 // blocks, rather than 4, whose 320 blocks double up on 64 CUs.
 int device_cus() {
-    static int cached = 0;
-    if (cached > 0) return cached;
+    static std::atomic<int> cached{0};  // one GPU model per process; retried until a device answers
+    const int known = cached.load(std::memory_order_relaxed);
+    if (known > 0) return known;
     int dev = 0, cus = 0;
     if (hipGetDevice(&dev) == hipSuccess &&
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0)
-        cached = cus;
-    return cached > 0 ? cached : 256;
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0) {
+        cached.store(cus, std::memory_order_relaxed);
+        return cus;
+    }
+    return 256;  // MI355X
 }
 
 int choose_splits(int64_t M, int64_t N, int64_t K, const void* workspace, size_t workspace_bytes) {
