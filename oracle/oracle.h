@@ -174,6 +174,20 @@ int orc_generate_speculative(void* model, const int32_t* prompt, int64_t P,
                              orc_spec_stats* stats, int32_t* round_log,
                              int64_t round_log_cap);
 
+/* ---- inspection hooks for the parity tests ---- */
+/* Overwrites one tensor (n elements, the tensor's size); 0 or -1. */
+int orc_model_set_tensor(void* model, uint32_t tensor_id, const float* data,
+                         int64_t n);
+/* qwen_mtp_forward_reference (generator.cc:139-183) over `rows` rows on a
+ * fresh MTP cache, as the MTP prompt prefill runs it (generator.cc:673-699):
+ * row r pairs emb(ids[r]) with hidden[r] at RoPE position r.  out [rows,H];
+ * k_cache / v_cache (optional) receive the cache rows [rows, nkv, D]. */
+int orc_mtp_forward(void* model, const int32_t* ids, const float* hidden,
+                    int64_t rows, float* out, float* k_cache, float* v_cache);
+/* The MTP cache the last orc_generate_speculative call left (its length is
+ * returned; up to cap_rows rows [len, nkv, D] are copied). */
+int64_t orc_last_mtp_cache(void* model, float* k, float* v, int64_t cap_rows);
+
 #ifdef __cplusplus
 }
 #endif

@@ -74,6 +74,10 @@ def lib():
         _lib.orc_synthetic_prompt.argtypes = [ctypes.c_uint64, ctypes.c_int64, ctypes.c_int64, I32P]
         _lib.orc_model_quantize_fp8.argtypes = [ctypes.c_void_p]
         _lib.orc_fp8_synthetic_scales.argtypes = [ctypes.c_uint64, ctypes.c_uint32, ctypes.c_int64, F32P]
+        _lib.orc_model_set_tensor.argtypes = [ctypes.c_void_p, ctypes.c_uint32, F32P, ctypes.c_int64]
+        _lib.orc_mtp_forward.argtypes = [ctypes.c_void_p, I32P, F32P, ctypes.c_int64, F32P, F32P, F32P]
+        _lib.orc_last_mtp_cache.restype = ctypes.c_int64
+        _lib.orc_last_mtp_cache.argtypes = [ctypes.c_void_p, F32P, F32P, ctypes.c_int64]
     return _lib
 
 
@@ -319,6 +323,34 @@ class Model:
         out = np.empty(n, np.float32)
         lib().orc_model_tensor(self.h, ctypes.c_uint32(tid), _f(out), ctypes.c_int64(n))
         return out
+
+    def set_tensor(self, tid: int, values) -> None:
+        v = _c32(np.asarray(values).ravel())
+        if lib().orc_model_set_tensor(self.h, ctypes.c_uint32(tid), _f(v), ctypes.c_int64(v.size)) != 0:
+            raise KeyError(f"tensor {tid}: unknown id or wrong size {v.size}")
+
+    def mtp_forward(self, ids, hidden):
+        """MTP forward over rows (emb(ids[r]), hidden[r]) on a fresh MTP
+        cache: returns (out [rows, H], K rows, V rows [rows, nkv, D])."""
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        hidden = _c32(hidden)
+        rows = ids.size
+        H, nkv, D = self.cfg["hidden"], self.cfg["num_kv_heads"], self.cfg["head_dim"]
+        out = np.empty((rows, H), np.float32)
+        k = np.empty((rows, nkv, D), np.float32); v = np.empty_like(k)
+        if lib().orc_mtp_forward(self.h, ids.ctypes.data_as(I32P), _f(hidden), ctypes.c_int64(rows), _f(out), _f(k),
+                                 _f(v)) != 0:
+            raise RuntimeError("orc_mtp_forward failed")
+        return out, k, v
+
+    def last_mtp_cache(self):
+        """(K, V) rows [len, nkv, D] of the MTP cache the last speculative
+        decode left."""
+        n = lib().orc_last_mtp_cache(self.h, None, None, ctypes.c_int64(0))
+        nkv, D = self.cfg["num_kv_heads"], self.cfg["head_dim"]
+        k = np.empty((n, nkv, D), np.float32); v = np.empty_like(k)
+        lib().orc_last_mtp_cache(self.h, _f(k), _f(v), ctypes.c_int64(n))
+        return k, v
 
     def forward(self, ids):
         ids = np.ascontiguousarray(ids, dtype=np.int32)

@@ -61,6 +61,11 @@ enum MtpKind : uint32_t { kFc = 0, kMtpNorm = 1, kPreEmb = 2, kPreHid = 3 };
 
 inline uint32_t tid(uint32_t slot, uint32_t kind) { return slot * 64u + kind; }
 
+struct AttnCache {  // AttentionKVCache (attention.h:11-42)
+    std::vector<float> k, v;
+    int64_t len = 0, cap = 0;
+};
+
 struct Layer {
     bool attn = false;
     std::vector<float> in_ln, post_ln;
@@ -76,7 +81,10 @@ struct Model {
     std::vector<float> embed, final_norm, lm_head;
     std::vector<float> fc, mtp_norm, pre_emb, pre_hid;
     std::vector<Layer> layers, mtp;
-    std::vector<std::pair<uint32_t, const std::vector<float>*>> registry;
+    std::vector<std::pair<uint32_t, std::vector<float>*>> registry;
+    // MTP cache left by the last orc_generate_speculative call (inspection
+    // for the cache-protocol tests)
+    mutable std::vector<AttnCache> last_mtp;
 };
 
 void fill(Model& m, std::vector<float>& dst, uint32_t id, int64_t n) {
@@ -125,10 +133,6 @@ bool is_attention_layer(const orc_config& c, int64_t i) {
 }
 
 // ---- caches (reference semantics: deep-copied on clone) -----------------
-struct AttnCache {  // AttentionKVCache (attention.h:11-42)
-    std::vector<float> k, v;
-    int64_t len = 0, cap = 0;
-};
 struct DeltaCache {  // DeltaNetCache (delta_net.h:11-55)
     std::vector<float> conv, state;
     int64_t len = 0;
@@ -593,7 +597,49 @@ int orc_generate_speculative(void* model, const int32_t* prompt, int64_t P,
             break;
     }
     if (stats) *stats = st;
+    m.last_mtp = mtp_cache;
     return static_cast<int>(emitted);
+}
+
+int orc_model_set_tensor(void* model, uint32_t tensor_id, const float* data, int64_t n) {
+    auto* m = static_cast<Model*>(model);
+    if (m == nullptr || data == nullptr) return -1;
+    for (auto& e : m->registry) {
+        if (e.first != tensor_id) continue;
+        if (static_cast<int64_t>(e.second->size()) != n) return -1;
+        std::memcpy(e.second->data(), data, static_cast<size_t>(n) * 4);
+        return 0;
+    }
+    return -1;
+}
+
+// qwen_mtp_forward_reference (generator.cc:139-183) on a fresh MTP cache of
+// `rows` rows, as the MTP prompt prefill calls it (generator.cc:673-699):
+// row r pairs emb(ids[r]) with hidden[r] at RoPE position r.
+int orc_mtp_forward(void* model, const int32_t* ids, const float* hidden, int64_t rows, float* out,
+                    float* k_cache, float* v_cache) {
+    const Model& m = *static_cast<Model*>(model);
+    if (rows <= 0 || m.mtp.empty()) return -1;
+    const int64_t H = m.c.hidden;
+    std::vector<float> e = embed(m, ids, rows), h(hidden, hidden + rows * H), o;
+    std::vector<AttnCache> caches;
+    if (!mtp_forward(m, e, h, rows, caches, rows, o)) return -1;
+    if (out) std::memcpy(out, o.data(), o.size() * 4);
+    const size_t kv = static_cast<size_t>(rows) * m.c.num_kv_heads * m.c.head_dim;
+    if (k_cache) std::memcpy(k_cache, caches[0].k.data(), kv * 4);
+    if (v_cache) std::memcpy(v_cache, caches[0].v.data(), kv * 4);
+    return 0;
+}
+
+int64_t orc_last_mtp_cache(void* model, float* k, float* v, int64_t cap_rows) {
+    const Model& m = *static_cast<Model*>(model);
+    if (m.last_mtp.empty()) return 0;
+    const AttnCache& c = m.last_mtp[0];
+    const int64_t row = static_cast<int64_t>(m.c.num_kv_heads) * m.c.head_dim;
+    const int64_t n = std::min(c.len, cap_rows);
+    if (k) std::memcpy(k, c.k.data(), static_cast<size_t>(n * row) * 4);
+    if (v) std::memcpy(v, c.v.data(), static_cast<size_t>(n * row) * 4);
+    return c.len;
 }
 
 }  // extern "C"
