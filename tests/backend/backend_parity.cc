@@ -222,6 +222,43 @@ void check_gpu(Backend* be) {
         orc_attention(q1.f.data(), g1.f.data(), k.f.data(), v.f.data(), want1.data(), 1, L, nq, nkv, D, 1);
         same_bits(d.down<uint16_t>(dy1.get(), want1.size()), want1, "cached_gqa_with_current_token");
     }
+    {  // cached_gqa_with_current_token as a T=1 decode drives it (attention.cc:561-571): the
+       // current K/V row is passed separately, the call stores it at cache_len-1
+       // (hip_kernels.hip:466-476) and the caller only advances the length
+        const int64_t nq = 4, nkv = 2, D = 64, cap = 80, L = 65, row = nkv * D;
+        auto k = random_bf16(rng, (L + 1) * row), v = random_bf16(rng, (L + 1) * row);
+        auto kc = d.make(cap * row * 2), vc = d.make(cap * row * 2);
+        expect_ok(be->memset(kc.get(), 0, cap * row * 2), "zero K cache");
+        expect_ok(be->memset(vc.get(), 0, cap * row * 2), "zero V cache");
+        auto dk = d.up(std::vector<uint16_t>(k.bits.begin(), k.bits.begin() + (L - 1) * row));
+        auto dv = d.up(std::vector<uint16_t>(v.bits.begin(), v.bits.begin() + (L - 1) * row));
+        expect_ok(be->append_kv_cache(kc.get(), vc.get(), dk.get(), dv.get(), DType::BF16, L - 1, nkv, D, 0, cap),
+                  "prefix rows");
+        for (int64_t step = 0; step < 2; ++step) {
+            const int64_t len = L + step;  // rows 0..len-2 cached, row len-1 is the current token
+            auto q = random_bf16(rng, nq * D), g = random_bf16(rng, nq * D);
+            auto dq = d.up(q.bits), dg = d.up(g.bits), dy = d.make(nq * D * 2);
+            auto ck = d.up(std::vector<uint16_t>(k.bits.begin() + (len - 1) * row, k.bits.begin() + len * row));
+            auto cv = d.up(std::vector<uint16_t>(v.bits.begin() + (len - 1) * row, v.bits.begin() + len * row));
+            const std::string tag = " (decode step " + std::to_string(step) + ")";
+            expect_ok(be->cached_gqa_with_current_token(dy.get(), dq.get(), kc.get(), vc.get(), ck.get(), cv.get(),
+                                                        dg.get(), DType::BF16, len, nq, nkv, D),
+                      "cached_gqa_with_current_token" + tag);
+            std::vector<float> want(nq * D);
+            orc_attention(q.f.data(), g.f.data(), k.f.data(), v.f.data(), want.data(), 1, len, nq, nkv, D, 1);
+            same_bits(d.down<uint16_t>(dy.get(), want.size()), want, "current-token output" + tag);
+            expect(d.down<uint16_t>(kc.get(), len * row) ==
+                       std::vector<uint16_t>(k.bits.begin(), k.bits.begin() + len * row),
+                   "K cache holds the current row" + tag);
+            expect(d.down<uint16_t>(vc.get(), len * row) ==
+                       std::vector<uint16_t>(v.bits.begin(), v.bits.begin() + len * row),
+                   "V cache holds the current row" + tag);
+        }
+        auto dq = d.make(nq * D * 2), dy = d.make(nq * D * 2), small = d.make((L - 1) * row * 2);
+        Status st = be->cached_gqa_with_current_token(dy.get(), dq.get(), small.get(), small.get(), dq.get(),
+                                                      dq.get(), nullptr, DType::BF16, L, nq, nkv, D);
+        expect(st.code() == StatusCode::InvalidArgument, "caches must hold cache_len rows");
+    }
     {  // deltanet_grouped_conv + deltanet_recurrent on the reference layouts
         const int64_t nk = 2, nv = 4, dk = 64, dv = 64, Kc = 4, T = 5;
         const int64_t kw = nk * dk, vw = nv * dv, C = 2 * kw + vw;
@@ -298,6 +335,21 @@ void check_gpu(Backend* be) {
             ok = ok && got[i] == want;
         }
         expect(ok, "copy_to_offset contents");
+        {  // create_buffer recycles blocks of released buffers (the reference's pool, hip_backend.cc:380-500)
+            auto* mb = dynamic_cast<MI355XBackend*>(be);
+            expect(mb != nullptr, "backend type");
+            void* first = nullptr;
+            {
+                auto t = be->create_buffer(3000, MemoryType::Device);
+                expect(t != nullptr && t->size() == 3000, "pooled buffer size");
+                first = t->data();
+            }
+            expect(mb->pooled_bytes(MemoryType::Device) >= 3072, "released block kept for reuse");
+            auto t2 = be->create_buffer(2900, MemoryType::Device);  // same 3072-byte class
+            expect(t2 != nullptr && t2->data() == first, "block reused for a request of the same class");
+            auto big = be->create_buffer(size_t{16} << 20, MemoryType::Device);
+            expect(big != nullptr && big->size() == (size_t{16} << 20), "large buffer bypasses the pool");
+        }
         auto pinned = be->create_buffer(64, MemoryType::HostPinned);
         expect(pinned != nullptr && pinned->memory_type() == MemoryType::HostPinned, "pinned buffer");
         expect_ok(be->synchronize(), "synchronize");

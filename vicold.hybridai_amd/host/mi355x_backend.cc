@@ -6,6 +6,9 @@
 #include <cstdlib>
 #include <cstring>
 #include <limits>
+#include <map>
+#include <memory>
+#include <mutex>
 #include <string>
 
 #include "hai_kernels.h"
@@ -145,10 +148,89 @@ private:
     MemoryType t_;
 };
 
+// Recycles the transient buffers of the reference's ops, which allocate
+// every output through create_buffer: the same bounds as the reference's
+// pool (hip_backend.cc:380-408: blocks up to 8 MiB pooled, at most 256 MiB
+// cached per device and memory type; larger blocks go straight to the
+// allocator), with size classes of at most 1.25x the request (256-byte
+// steps up to 4 KiB, then four classes per power of two).  A block returns
+// to its class's free list when its Buffer dies, without a device
+// synchronisation: like the reference's, the pool relies on the ops running
+// in stream order on one stream.
+class BlockPool {
+public:
+    static constexpr size_t kMaxBlock = size_t{8} << 20;
+    static constexpr size_t kMaxCached = size_t{256} << 20;
+
+    explicit BlockPool(MemoryType t) : t_(t) {}
+
+    static size_t size_class(size_t n) {
+        if (n <= 4096) return std::max<size_t>(256, (n + 255) & ~size_t{255});
+        size_t base = 4096;
+        while (base * 2 < n) base *= 2;
+        const size_t step = base / 4;
+        return base + (n - base + step - 1) / step * step;
+    }
+
+    Status take(size_t n, void** p, size_t* cls) {
+        *cls = n <= kMaxBlock ? size_class(n) : 0;
+        if (*cls != 0) {
+            std::lock_guard<std::mutex> lock(mu_);
+            auto& fl = free_[*cls];
+            if (!fl.empty()) {
+                *p = fl.back();
+                fl.pop_back();
+                cached_ -= *cls;
+                return Status::OK();
+            }
+        }
+        return raw_alloc(t_, *cls != 0 ? *cls : n, p);
+    }
+
+    void give(void* p, size_t cls) {
+        if (p == nullptr) return;
+        if (cls != 0) {
+            std::lock_guard<std::mutex> lock(mu_);
+            if (cached_ + cls <= kMaxCached) {
+                free_[cls].push_back(p);
+                cached_ += cls;
+                return;
+            }
+        }
+        raw_free(t_, p);
+    }
+
+    size_t cached_bytes() {
+        std::lock_guard<std::mutex> lock(mu_);
+        return cached_;
+    }
+
+private:
+    MemoryType t_;
+    std::mutex mu_;
+    std::map<size_t, std::vector<void*>> free_;
+    size_t cached_ = 0;
+};
+
+// One pool per (device, memory type), shared by every backend instance of
+// the process and kept until it ends (the cached blocks go with it).
+std::shared_ptr<BlockPool> pool_for(int device, MemoryType type) {
+    static std::mutex mu;
+    static auto* pools = new std::map<std::pair<int, int>, std::shared_ptr<BlockPool>>();
+    std::lock_guard<std::mutex> lock(mu);
+    auto& p = (*pools)[{device, static_cast<int>(type)}];
+    if (!p) p = std::make_shared<BlockPool>(type);
+    return p;
+}
+
 class HaiBuffer final : public Buffer {
 public:
-    HaiBuffer(void* p, size_t n, Device d, MemoryType t) : p_(p), n_(n), d_(std::move(d)), t_(t) {}
-    ~HaiBuffer() override { raw_free(t_, p_); }
+    HaiBuffer(void* p, size_t n, Device d, MemoryType t, std::shared_ptr<BlockPool> pool, size_t cls)
+        : p_(p), n_(n), d_(std::move(d)), t_(t), pool_(std::move(pool)), cls_(cls) {}
+    ~HaiBuffer() override {
+        if (pool_) pool_->give(p_, cls_);
+        else raw_free(t_, p_);
+    }
     void* data() noexcept override { return p_; }
     const void* data() const noexcept override { return p_; }
     size_t size() const noexcept override { return n_; }
@@ -160,6 +242,8 @@ private:
     size_t n_;
     Device d_;
     MemoryType t_;
+    std::shared_ptr<BlockPool> pool_;
+    size_t cls_;
 };
 
 // Kernel operands must be device buffers of this backend's device holding
@@ -192,7 +276,7 @@ MI355XBackend::MI355XBackend(const Device& device) : device_(device) {}
 
 MI355XBackend::~MI355XBackend() {
     if (is_available()) hai_set_device(device_.id());
-    for (Scratch* s : {&gqa_, &argmax_, &kv_k_, &kv_v_})
+    for (Scratch* s : {&gqa_, &argmax_})
         if (s->ptr) hai_free(s->ptr);
     for (auto& kv : rope_) {
         hai_free(kv.second.cos);
@@ -292,11 +376,20 @@ std::unique_ptr<Event> MI355XBackend::create_event() {
 }
 
 std::shared_ptr<Buffer> MI355XBackend::create_buffer(size_t size, MemoryType type) {
-    if (type != MemoryType::Host && !select().ok()) return nullptr;
+    if (type == MemoryType::Host) {
+        void* p = nullptr;
+        if (!raw_alloc(type, size, &p).ok()) return nullptr;
+        return std::make_shared<HaiBuffer>(p, size, device_, type, nullptr, 0);
+    }
+    if (!select().ok()) return nullptr;
+    auto pool = pool_for(device_.id(), type);
     void* p = nullptr;
-    if (!raw_alloc(type, size, &p).ok()) return nullptr;
-    return std::make_shared<HaiBuffer>(p, size, device_, type);
+    size_t cls = 0;
+    if (!pool->take(size, &p, &cls).ok()) return nullptr;
+    return std::make_shared<HaiBuffer>(p, size, device_, type, std::move(pool), cls);
 }
+
+size_t MI355XBackend::pooled_bytes(MemoryType type) const { return pool_for(device_.id(), type)->cached_bytes(); }
 
 // ---- copies -----------------------------------------------------------------------
 
@@ -543,6 +636,14 @@ Status MI355XBackend::cached_gqa(Buffer* dst, const Buffer* query, const Buffer*
     return Status::OK();
 }
 
+// cached_gqa_current_token_kernel (hip_kernels.hip:396-478): attend one query row
+// to cache rows 0..cache_len-2 plus the current K/V row, and store the
+// current row into the caches at cache_len-1 (the reference kernel's store,
+// :466-476, which attention.cc:561-571 relies on: it only advances the
+// cache length afterwards).  The row is stored first and the attention
+// runs over the cache in place; the result is the same because row
+// cache_len-1 then is the current row.  The caches are declared const by
+// the Backend virtual, as in the reference, and written all the same.
 Status MI355XBackend::cached_gqa_with_current_token(Buffer* dst, const Buffer* query, const Buffer* key_cache,
                                                     const Buffer* value_cache, const Buffer* current_key,
                                                     const Buffer* current_value, const Buffer* gate, DType dtype,
@@ -552,11 +653,11 @@ Status MI355XBackend::cached_gqa_with_current_token(Buffer* dst, const Buffer* q
     if (cache_len < 1 || cache_len > std::numeric_limits<int32_t>::max()) return invalid("cache length");
     const int64_t row = num_kv_heads * head_dim;
     const size_t q_bytes = static_cast<size_t>(num_query_heads * head_dim) * 2;
-    const size_t old_bytes = static_cast<size_t>((cache_len - 1) * row) * 2;
+    const size_t cache_bytes = static_cast<size_t>(cache_len * row) * 2;
     RETURN_IF_ERROR(need(dst, device_, q_bytes, "dst"));
     RETURN_IF_ERROR(need(query, device_, q_bytes, "query"));
-    RETURN_IF_ERROR(need(key_cache, device_, old_bytes, "key_cache"));
-    RETURN_IF_ERROR(need(value_cache, device_, old_bytes, "value_cache"));
+    RETURN_IF_ERROR(need(key_cache, device_, cache_bytes, "key_cache"));
+    RETURN_IF_ERROR(need(value_cache, device_, cache_bytes, "value_cache"));
     RETURN_IF_ERROR(need(current_key, device_, static_cast<size_t>(row) * 2, "current_key"));
     RETURN_IF_ERROR(need(current_value, device_, static_cast<size_t>(row) * 2, "current_value"));
     if (gate != nullptr) RETURN_IF_ERROR(need(gate, device_, q_bytes, "gate"));
@@ -564,20 +665,13 @@ Status MI355XBackend::cached_gqa_with_current_token(Buffer* dst, const Buffer* q
     RETURN_IF_ERROR(native(stream, &s));
     RETURN_IF_ERROR(select());
     std::lock_guard<std::mutex> lock(mu_);
-    // The cache rows and the current row side by side, then one T=1 verify.
-    const size_t all_bytes = old_bytes + static_cast<size_t>(row) * 2;
-    void *kc = nullptr, *vc = nullptr, *ws = nullptr;
-    RETURN_IF_ERROR(scratch(kv_k_, all_bytes, &kc));
-    RETURN_IF_ERROR(scratch(kv_v_, all_bytes, &vc));
+    void* kc = const_cast<void*>(key_cache->data());
+    void* vc = const_cast<void*>(value_cache->data());
+    HAI_STATUS(hai_append_kv_bf16(kc, vc, cache_len, current_key->data(), current_value->data(), 1, 1, row, nullptr,
+                                  static_cast<int32_t>(cache_len - 1), s),
+               "current K/V row store");
+    void* ws = nullptr;
     RETURN_IF_ERROR(scratch(gqa_, hai_gqa_scratch_bytes(1, 1, num_query_heads, head_dim, cache_len), &ws));
-    if (old_bytes > 0) {
-        HAI_STATUS(hai_memcpy_d2d(kc, key_cache->data(), old_bytes, s), "current-token K copy");
-        HAI_STATUS(hai_memcpy_d2d(vc, value_cache->data(), old_bytes, s), "current-token V copy");
-    }
-    HAI_STATUS(hai_memcpy_d2d(static_cast<char*>(kc) + old_bytes, current_key->data(), row * 2, s),
-               "current K row");
-    HAI_STATUS(hai_memcpy_d2d(static_cast<char*>(vc) + old_bytes, current_value->data(), row * 2, s),
-               "current V row");
     HAI_STATUS(hai_gqa_verify_bf16(dst->data(), query->data(), gate ? gate->data() : nullptr, kc, vc, cache_len, ws,
                                    1, 1, num_query_heads, num_kv_heads, head_dim, nullptr,
                                    static_cast<int32_t>(cache_len), cache_len, s),

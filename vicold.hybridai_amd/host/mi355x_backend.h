@@ -38,6 +38,8 @@ public:
     std::unique_ptr<Stream> create_stream() override;
     std::unique_ptr<Event> create_event() override;
     std::shared_ptr<Buffer> create_buffer(size_t size, MemoryType type) override;
+    // Bytes the buffer pool of this device and memory type holds for reuse.
+    size_t pooled_bytes(MemoryType type) const;
 
     Status memcpy_h2d(Buffer* dst, const void* src, size_t size, Stream* stream = nullptr) override;
     Status memcpy_d2h(void* dst, const Buffer* src, size_t size, Stream* stream = nullptr) override;
@@ -114,7 +116,7 @@ private:
     Device device_;
     bool kernels_registered_ = false;
     std::mutex mu_;
-    Scratch gqa_, argmax_, kv_k_, kv_v_;
+    Scratch gqa_, argmax_;
     std::map<std::pair<int64_t, float>, RopeTable> rope_;
 };
 
