@@ -53,7 +53,9 @@ typedef struct hai_model_config {
 
 typedef struct hai_engine_options {
     int32_t max_context;      /* KV capacity per sequence (prompt + new + slack) */
-    int32_t max_verify_tokens;/* largest k+1; also the prefill chunk (<= 16) */
+    int32_t max_verify_tokens;/* largest k+1: up to 17 (width 16) for one
+                                 sequence, 16 for batches; prompts prefill
+                                 in chunks of min(this, 16) rows */
     int32_t device;           /* HIP device ordinal */
     int32_t use_graphs;       /* replay captured forwards (0 = plain launches) */
     int32_t weight_format;    /* HAI_WEIGHTS_* */
@@ -71,7 +73,10 @@ typedef struct hai_spec_stats {
     int64_t accepted;
     int64_t rejected;
     int64_t corrections;
-    int64_t replay_tokens;        /* correction tokens forwarded */
+    int64_t replay_tokens;        /* the reference's replay count: next +
+                                     accepted + correction per rejected
+                                     round (this engine forwards only the
+                                     correction row of those) */
     int64_t mtp_recovery_tokens;
     int64_t max_proposal_width;
     int64_t emitted;

@@ -426,11 +426,15 @@ int hai_gemm_mfma_splits(int64_t M, int64_t N, int64_t K, const void* workspace,
  * (qwen_reference.cc:108-144): h[M, N] (the residual, ld h) becomes
  * bf16(h + bf16(sum of the partials in split order)), bit-identical to the
  * unfused call, and xn = hai_rmsnorm_bf16(h) bit for bit; norm_w null skips
- * the norm.  N % 8 == 0, N <= 8192, M <= 128, splits <= 4. */
+ * the norm.  N % 8 == 0, N <= 8192, M <= 128; splits is the count the GEMM
+ * took (hai_gemm_mfma_splits), 2 <= splits <= 4 (with one split the GEMM
+ * finished h itself and left no partials), and the workspace must hold
+ * splits * M * N floats (workspace_bytes). */
 int hai_mfma_residual_rmsnorm_bf16(void* h, int64_t ldh, const void* workspace,
-                                   int64_t M, int64_t N, int64_t splits,
-                                   const void* norm_w, float eps, int unit_offset,
-                                   void* xn, int64_t ld_xn, void* stream);
+                                   size_t workspace_bytes, int64_t M, int64_t N,
+                                   int64_t splits, const void* norm_w, float eps,
+                                   int unit_offset, void* xn, int64_t ld_xn,
+                                   void* stream);
 
 /* ------------------------------------------------------------------ synthetic data / checks
  * Synthetic weights: element (r, c) of a [rows, cols] tensor (row stride
@@ -439,6 +443,11 @@ int hai_mfma_residual_rmsnorm_bf16(void* h, int64_t ldh, const void* workspace,
 int hai_fill_synthetic_bf16(void* dst, int64_t rows, int64_t cols, int64_t ld,
                             uint64_t seed, uint32_t tensor_id, float std_dev,
                             void* stream);
+/* The host-side operand check the launchers run when the environment sets
+ * HAI_CHECK_BOUNDS=1, applied here unconditionally and without launching
+ * anything: HAI_OK when [p, p + bytes) lies inside one device allocation,
+ * HAI_ERR_INVALID_ARGUMENT otherwise. */
+int hai_debug_check_extent(const void* p, size_t bytes);
 /* Evaluates one canonical primitive elementwise (0 exp, 1 log1p, 2 sigmoid,
  * 3 silu, 4 sqrt, 5 1/x, 6 bf16 round) so tests can pin device bits. */
 int hai_debug_math_f32(float* y, const float* x, int64_t n, int fn, void* stream);

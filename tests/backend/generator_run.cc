@@ -89,12 +89,13 @@ int main(int argc, char** argv) {
     std::printf("tokens");
     for (int64_t t : r.token_ids) std::printf(" %lld", static_cast<long long>(t));
     std::printf("\nstats prompt_tokens=%lld rounds=%lld proposed=%lld accepted=%lld rejected=%lld corrections=%lld "
-                "replay_tokens=%lld mtp_recovery_tokens=%lld decode_tps=%.3f text_ok=%d\n",
+                "replay_tokens=%lld mtp_recovery_tokens=%lld max_width=%lld decode_tps=%.3f text_ok=%d\n",
                 static_cast<long long>(r.prompt_tokens), static_cast<long long>(r.speculative_rounds),
                 static_cast<long long>(r.mtp_proposed_tokens), static_cast<long long>(r.mtp_accepted_tokens),
                 static_cast<long long>(r.mtp_rejected_tokens), static_cast<long long>(r.mtp_correction_tokens),
                 static_cast<long long>(r.speculative_replay_tokens),
-                static_cast<long long>(r.speculative_mtp_recovery_tokens), r.decode_tokens_per_second,
+                static_cast<long long>(r.speculative_mtp_recovery_tokens),
+                static_cast<long long>(r.speculative_max_proposal_width), r.decode_tokens_per_second,
                 r.text.rfind("ids:", 0) == 0 ? 1 : 0);
     return 0;
 }

@@ -1,3 +1,9 @@
+import os
+
+# Every launcher that supports it verifies on the host, before launching,
+# that its operands lie inside their device allocations (hai_common.h).
+os.environ.setdefault("HAI_CHECK_BOUNDS", "1")
+
 import pytest
 
 from _hai import gpu_available

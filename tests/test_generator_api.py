@@ -3,6 +3,7 @@ paths on the CPU, a compile of the implementation against the reference's
 own hybrid.h, the declared struct members compared with it, and (GPU) the
 tiny C1 decode through the public API against the golden vectors."""
 import json
+import os
 import re
 import subprocess
 from pathlib import Path
@@ -50,10 +51,13 @@ def test_struct_members_match_reference(struct):
     assert got and got == _members(ref, struct)
 
 
-def _run(mode, max_new=64, model="synthetic:tiny?seed=0&std=0.02&context=256", prompt_ids=None):
+def _run(mode, max_new=64, model="synthetic:tiny?seed=0&std=0.02&context=256", prompt_ids=None, width=None):
     prompt = "ids:" + ",".join(str(t) for t in (GOLD["prompt"] if prompt_ids is None else prompt_ids))
+    env = {k: v for k, v in os.environ.items() if k != "HYBRIDAI_SPECULATIVE_WIDTH"}
+    if width is not None:
+        env["HYBRIDAI_SPECULATIVE_WIDTH"] = str(width)
     r = subprocess.run([_driver(), model, mode, prompt, str(max_new)],
-                       capture_output=True, text=True, timeout=300)
+                       capture_output=True, text=True, timeout=300, env=env)
     assert r.returncode == 0, r.stdout + r.stderr
     lines = dict(line.split(" ", 1) for line in r.stdout.strip().splitlines())
     toks = [int(t) for t in lines["tokens"].split()]
@@ -69,14 +73,33 @@ def test_greedy_through_public_api():
 
 
 @pytest.mark.gpu
-def test_speculative_through_public_api():
-    toks, stats = _run("spec")
-    g = GOLD["speculative"]["1"]
+@pytest.mark.parametrize("width", [1, 2, 3])
+def test_speculative_through_public_api(width):
+    """HYBRIDAI_SPECULATIVE_WIDTH selects the proposal width
+    (generator.cc:124-137); tokens and counters equal the golden vectors."""
+    toks, stats = _run("spec", width=width)
+    g = GOLD["speculative"][str(width)]
     assert toks == g["tokens"] == GOLD["greedy"]
     for key, name in (("rounds", "rounds"), ("proposed", "proposed"), ("accepted", "accepted"),
                       ("rejected", "rejected"), ("corrections", "corrections"),
-                      ("mtp_recovery_tokens", "mtp_recovery_tokens")):
+                      ("mtp_recovery_tokens", "mtp_recovery_tokens"), ("max_proposal_width", "max_width")):
         assert int(stats[name]) == g["stats"][key], key
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("env,width", [(None, 8), ("", 8), ("16", 16), ("0", 8), ("17", 8), ("4x", 8)])
+def test_speculative_width_from_environment(env, width):
+    """Unset, empty or invalid values give the reference's default width
+    8; 16, the largest, verifies 17 rows.  Tokens and counters equal the
+    oracle's restatement of the state machine at that width."""
+    toks, stats = _run("spec", 40, width=env)
+    ref = orc.Model(orc.TINY, seed=0)
+    rt, rs, _ = ref.speculative(GOLD["prompt"], 40, width)
+    ref.close()
+    assert toks == [int(t) for t in rt] == GOLD["greedy"][:40]
+    assert int(stats["max_width"]) == rs["max_proposal_width"] == width
+    for key in ("rounds", "proposed", "accepted", "rejected", "corrections", "mtp_recovery_tokens"):
+        assert int(stats[key]) == rs[key], key
 
 
 @pytest.mark.gpu

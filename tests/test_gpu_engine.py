@@ -20,7 +20,7 @@ def engines(request):
     synchronisations in between; each replay is checked through the round
     logs)."""
     from hybridai_amd import engine as E
-    eng = E.Engine(E.TINY, max_context=P + NEW + 32, max_verify_tokens=16, use_graphs=request.param)
+    eng = E.Engine(E.TINY, max_context=P + NEW + 32, max_verify_tokens=17, use_graphs=request.param)
     eng.init_synthetic(seed=0, std=0.02)
     ref = orc.Model(orc.TINY, seed=0)
     prompt = orc.synthetic_prompt(0, P, orc.TINY["vocab"])
@@ -64,12 +64,14 @@ def test_speculative_matches_reference_state_machine(engines, width):
     assert st["rounds"] == rst["rounds"] and st["accepted"] == rst["accepted"]
     assert st["proposed"] == rst["proposed"] and st["corrections"] == rst["corrections"]
     assert st["mtp_recovery_tokens"] == rst["mtp_recovery_tokens"]
+    assert st["replay_tokens"] == rst["replay_tokens"] and st["rejected"] == rst["rejected"]
     assert np.array_equal(log, rlog)
     # speculative decoding emits exactly the greedy continuation
     assert list(toks) == list(ref.greedy(prompt, NEW))
 
 
-@pytest.mark.parametrize("width,perturb", [(1, ()), (3, ()), (3, (5, 20, 21, 40)), (2, (1, 2, 3, 30))])
+@pytest.mark.parametrize("width,perturb", [(1, ()), (3, ()), (3, (5, 20, 21, 40)), (2, (1, 2, 3, 30)),
+                                           (8, (9, 10, 33)), (16, ()), (16, (4, 22, 23, 45))])
 def test_forced_acceptance_patterns(engines, width, perturb):
     """Draft override: candidates taken from the greedy continuation (full
     acceptance) with some positions perturbed (partial acceptance)."""
@@ -83,6 +85,17 @@ def test_forced_acceptance_patterns(engines, width, perturb):
     assert list(toks) == list(rtoks) == list(g)
     assert np.array_equal(log, rlog)
     assert st["accepted"] == rst["accepted"] > 0
+
+
+def test_width_beyond_the_verify_rows_is_rejected(engines):
+    """Width 16 (17 verify rows, the largest the reference allows) runs;
+    a wider proposal than the engine verifies is an argument error, not a
+    silent clamp."""
+    eng, ref, prompt = engines
+    with pytest.raises(RuntimeError, match="max_verify_tokens"):
+        eng.speculative(prompt, NEW, 17)
+    toks, st, _ = eng.speculative(prompt, NEW, 16)
+    assert list(toks) == list(ref.greedy(prompt, NEW)) and st["max_proposal_width"] == 16
 
 
 def test_eos_stops_like_reference(engines):

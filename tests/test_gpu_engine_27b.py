@@ -3,7 +3,8 @@ weight format), where the CPU oracle is too slow to run the model, through
 size-independent properties of the path:
 
 * speculative decoding is lossless: the tokens of the speculative rounds
-  (widths 1 and 3, every draft accepted, some drafts rejected, none accepted)
+  (widths 1, 3, 8 and 16 -- 17 verify rows, two DeltaNet launches per
+  layer -- every draft accepted, some drafts rejected, none accepted)
   equal greedy decoding of the same model, token by token;
 * greedy decoding's tokens equal the argmax of the last row of a fresh
   forward over the whole sequence (prefill path, 16-row chunks): a verify row,
@@ -21,7 +22,7 @@ from _hai import hai
 
 pytestmark = pytest.mark.gpu
 
-P, NEW = 40, 10
+P, NEW = 40, 24
 
 
 def _refeed_greedy(eng, prompt, tokens):
@@ -44,7 +45,7 @@ def _check_lossless(eng, prompt, vocab):
     for i in (2, 3, 7):
         perturbed[i] = (perturbed[i] + 1) % vocab
     cases = [(1, None), (3, None), (3, g), (1, perturbed), (3, perturbed),
-             (2, rng.integers(0, vocab, NEW).astype(np.int32))]
+             (2, rng.integers(0, vocab, NEW).astype(np.int32)), (8, None), (16, g), (16, perturbed)]
     for width, ov in cases:
         toks, st, log = eng.speculative(prompt, NEW, width, draft_override=ov)
         assert list(toks) == list(g), (width, None if ov is None else list(ov))
@@ -56,7 +57,7 @@ def _check_lossless(eng, prompt, vocab):
 
 def test_27b_bf16_speculative_is_lossless():
     from hybridai_amd import engine as E
-    eng = E.Engine(E.QWEN27B, max_context=P + 5 * NEW + 32, max_verify_tokens=16)
+    eng = E.Engine(E.QWEN27B, max_context=P + 5 * NEW + 32, max_verify_tokens=17)
     try:
         eng.init_synthetic(seed=0, std=0.02)
         _check_lossless(eng, E.synthetic_prompt(1, P, E.QWEN27B["vocab"]), E.QWEN27B["vocab"])
@@ -66,7 +67,7 @@ def test_27b_bf16_speculative_is_lossless():
 
 def test_27b_fp8_speculative_is_lossless():
     from hybridai_amd import engine as E
-    eng = E.Engine(E.QWEN27B, max_context=P + 5 * NEW + 32, max_verify_tokens=16, fp8=True)
+    eng = E.Engine(E.QWEN27B, max_context=P + 5 * NEW + 32, max_verify_tokens=17, fp8=True)
     try:
         eng.init_synthetic(seed=0, std=0.02)
         _check_lossless(eng, E.synthetic_prompt(2, P, E.QWEN27B["vocab"]), E.QWEN27B["vocab"])

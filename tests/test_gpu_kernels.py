@@ -973,14 +973,14 @@ def test_mfma_keep_partials_then_residual_rmsnorm(M, N, K, fp8):
     hai.check(kern().hai_rmsnorm_bf16(ref_xn.ptr, N, ref_h.ptr, N, dnw.ptr, M, N, 1e-6, 1, None), "rmsnorm")
     dh, dxn = dev(hb), out_buf(M * N * 2)
     hai.check(gemm(dh, hai.MFMA_KEEP_PARTIALS), "gemm keeping partials")
-    hai.check(kern().hai_mfma_residual_rmsnorm_bf16(dh.ptr, N, dws.ptr, M, N, splits, dnw.ptr, 1e-6, 1, dxn.ptr, N,
-                                                    None), "residual rmsnorm")
+    hai.check(kern().hai_mfma_residual_rmsnorm_bf16(dh.ptr, N, dws.ptr, wsb, M, N, splits, dnw.ptr, 1e-6, 1, dxn.ptr,
+                                                    N, None), "residual rmsnorm")
     assert_bits_equal(dh.download(np.uint16), hai.bf16_to_f32(ref_h.download(np.uint16)), "residual rows")
     assert_bits_equal(dxn.download(np.uint16), hai.bf16_to_f32(ref_xn.download(np.uint16)), "normalised rows")
     dh2 = dev(hb)
     hai.check(gemm(dh2, hai.MFMA_KEEP_PARTIALS), "gemm keeping partials")
-    hai.check(kern().hai_mfma_residual_rmsnorm_bf16(dh2.ptr, N, dws.ptr, M, N, splits, None, 0.0, 0, None, 0, None),
-              "residual only")
+    hai.check(kern().hai_mfma_residual_rmsnorm_bf16(dh2.ptr, N, dws.ptr, wsb, M, N, splits, None, 0.0, 0, None, 0,
+                                                    None), "residual only")
     assert_bits_equal(dh2.download(np.uint16), hai.bf16_to_f32(ref_h.download(np.uint16)), "residual rows, no norm")
     # keeping partials is for the residual epilogue only (operands sized for
     # the call, so even an accepted call would stay in bounds)
@@ -988,6 +988,36 @@ def test_mfma_keep_partials_then_residual_rmsnorm(M, N, K, fp8):
         for epi, ldy in ((hai.EPI_STORE, N), (hai.EPI_SILU_MUL, N // 2)):
             assert kern().hai_gemm_bf16_mfma(dh.ptr, ldy, dx.ptr, K, dw.ptr, M, N, K, epi | hai.MFMA_KEEP_PARTIALS,
                                              None, 0, dws.ptr, wsb, None) == hai.ERR_INVALID
+
+
+@pytest.mark.gpu
+def test_operand_bounds_check():
+    """The host-side check the launchers run under HAI_CHECK_BOUNDS (set for
+    the whole test session): ranges inside an allocation pass, ranges that
+    run past its end do not.  Nothing is launched."""
+    import os
+    assert os.environ.get("HAI_CHECK_BOUNDS") == "1"
+    b = hai.DeviceBuffer(1 << 20)
+    assert kern().hai_debug_check_extent(b.ptr, 1 << 20) == hai.OK
+    assert kern().hai_debug_check_extent(b.ptr + 4096, (1 << 20) - 4096) == hai.OK
+    assert kern().hai_debug_check_extent(b.ptr, 1 << 30) == hai.ERR_INVALID
+    assert kern().hai_debug_check_extent(b.ptr + (1 << 19), 1 << 29) == hai.ERR_INVALID
+
+
+@pytest.mark.gpu
+def test_residual_rmsnorm_rejects_workspace_and_split_mistakes():
+    """hai_mfma_residual_rmsnorm_bf16 refuses, before launching, a workspace
+    smaller than splits * M * N floats and a split count of one (the GEMM
+    then finished its rows itself and left no partials)."""
+    M, N = 8, 1024
+    h, ws = out_buf(M * N * 2), out_buf(4 * M * N * 4)
+    k = kern()
+    assert k.hai_mfma_residual_rmsnorm_bf16(h.ptr, N, ws.ptr, 3 * M * N * 4 - 4, M, N, 3, None, 0.0, 0, None, 0,
+                                            None) == hai.ERR_INVALID
+    assert k.hai_mfma_residual_rmsnorm_bf16(h.ptr, N, ws.ptr, 4 * M * N * 4, M, N, 1, None, 0.0, 0, None, 0,
+                                            None) == hai.ERR_INVALID
+    assert k.hai_mfma_residual_rmsnorm_bf16(h.ptr, N, ws.ptr, 4 * M * N * 4, M, N, 5, None, 0.0, 0, None, 0,
+                                            None) == hai.ERR_INVALID
 
 
 @pytest.mark.parametrize("H,nk,nv,dk,dv,B,T", [(256, 4, 4, 64, 64, 1, 2), (256, 2, 6, 64, 64, 3, 16),

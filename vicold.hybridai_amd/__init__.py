@@ -100,9 +100,11 @@ _KERNEL_SIGS = {
     "hai_gemm_fp8_mfma": [VP, I64, VP, I64, VP, VP, VP, I64, I64, I64, ctypes.c_int, VP, I64, VP, ctypes.c_size_t,
                           VP],
     "hai_gemm_mfma_splits": [I64, I64, I64, VP, ctypes.c_size_t],
-    "hai_mfma_residual_rmsnorm_bf16": [VP, I64, VP, I64, I64, I64, VP, F32, ctypes.c_int, VP, I64, VP],
+    "hai_mfma_residual_rmsnorm_bf16": [VP, I64, VP, ctypes.c_size_t, I64, I64, I64, VP, F32, ctypes.c_int, VP, I64,
+                                       VP],
     "hai_fill_synthetic_bf16": [VP, I64, I64, I64, ctypes.c_uint64, ctypes.c_uint32, F32, VP],
     "hai_debug_math_f32": [VP, VP, I64, ctypes.c_int, VP],
+    "hai_debug_check_extent": [VP, ctypes.c_size_t],
 }
 _SIZE_SIGS = {
     "hai_gemm_mfma_workspace_bytes": [I64, I64],
@@ -118,12 +120,32 @@ class HaiError(RuntimeError):
     pass
 
 
+def _check_fresh(so: Path) -> None:
+    """Refuses a library whose sources changed after it was built: build.py
+    records a digest of the sources of each library, recomputed here from the
+    tree, so a stale .so can never run silently against newer sources."""
+    import importlib.util
+    import json
+    manifest = LIB_DIR / "build_manifest.json"
+    if not manifest.exists():
+        raise HaiError(f"{manifest} is missing: run __graft_entry__.build()")
+    spec = importlib.util.spec_from_file_location("_hai_build", PKG_DIR / "build.py")
+    build = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(build)
+    inputs = build.kernel_inputs() if so.name == KERNELS_SO.name else build.host_inputs()
+    recorded = json.loads(manifest.read_text()).get(so.name)
+    if recorded != build.source_digest(inputs):
+        raise HaiError(f"{so.name} is older than its sources: run __graft_entry__.build()")
+
+
 def kernels() -> ctypes.CDLL:
-    """Load libhai_kernels.so (raises when it has not been built)."""
+    """Load libhai_kernels.so (raises when it has not been built or is
+    older than its sources)."""
     global _kern
     if _kern is None:
         if not KERNELS_SO.exists():
             raise HaiError(f"{KERNELS_SO} is missing: run __graft_entry__.build()")
+        _check_fresh(KERNELS_SO)
         lib = ctypes.CDLL(str(KERNELS_SO))
         for name, args in _KERNEL_SIGS.items():
             f = getattr(lib, name)
@@ -228,6 +250,7 @@ def host() -> ctypes.CDLL:
         kernels()
         if not HOST_SO.exists():
             raise HaiError(f"{HOST_SO} is missing: run __graft_entry__.build()")
+        _check_fresh(HOST_SO)
         from . import engine as _engine  # noqa: F401  (sets signatures)
         _host = _engine.bind(ctypes.CDLL(str(HOST_SO)))
     return _host

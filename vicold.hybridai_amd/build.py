@@ -12,6 +12,8 @@ from __future__ import annotations
 
 import argparse
 import concurrent.futures as cf
+import hashlib
+import json
 import os
 import shutil
 import subprocess
@@ -45,6 +47,35 @@ KERNEL_SOURCES = ["hai_runtime.hip", "hai_gemm.hip", "hai_gemm_fp8.hip", "hai_ge
                   "hai_deltanet.hip", "hai_argmax.hip"]
 
 
+MANIFEST = LIB / "build_manifest.json"
+
+
+def kernel_inputs() -> list[Path]:
+    return sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.h")) + sorted(INCLUDE.glob("*.h"))
+
+
+def host_inputs() -> list[Path]:
+    return (sorted(HOST.glob("*.cc")) + sorted(HOST.glob("*.h")) + sorted(HOST.glob("refabi/*"))
+            + sorted(INCLUDE.glob("*.h")))
+
+
+def source_digest(paths) -> str:
+    """sha256 over the names and bytes of the sources a library is built from."""
+    h = hashlib.sha256()
+    for p in paths:
+        h.update(str(p.relative_to(ROOT)).encode())
+        h.update(p.read_bytes())
+    return h.hexdigest()
+
+
+def _record(lib: str, digest: str) -> None:
+    m = json.loads(MANIFEST.read_text()) if MANIFEST.exists() else {}
+    m[lib] = digest
+    tmp = MANIFEST.with_suffix(".tmp")
+    tmp.write_text(json.dumps(m, indent=1) + "\n")
+    os.replace(tmp, MANIFEST)
+
+
 def _run(cmd):
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
@@ -56,6 +87,7 @@ def _run(cmd):
 def build_kernels(jobs: int = 8) -> Path:
     OBJ.mkdir(exist_ok=True)
     LIB.mkdir(exist_ok=True)
+    digest = source_digest(kernel_inputs())  # before compiling: an edit during the build leaves it stale
     objs = []
     cmds = []
     for src in KERNEL_SOURCES:
@@ -68,6 +100,7 @@ def build_kernels(jobs: int = 8) -> Path:
     tmp = LIB / "libhai_kernels.so.tmp"
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)])
     os.replace(tmp, out)
+    _record(out.name, digest)
     return out
 
 
@@ -77,6 +110,7 @@ def build_host(jobs: int = 8) -> Path | None:
     if not srcs:
         return None
     OBJ.mkdir(exist_ok=True)
+    digest = source_digest(host_inputs())
     objs = []
     cmds = []
     for src in srcs:
@@ -90,6 +124,7 @@ def build_host(jobs: int = 8) -> Path | None:
     _run([CXX, "-shared", "-fPIC", "-o", str(tmp), *map(str, objs), f"-L{LIB}", "-lhai_kernels",
           "-Wl,-rpath,$ORIGIN", "-lpthread"])
     os.replace(tmp, out)
+    _record(out.name, digest)
     return out
 
 

@@ -448,7 +448,8 @@ int64_t resident_blocks(const void* kernel, size_t shmem) {
 extern "C" int hai_gemm_bf16(void* y, int64_t ldy, const void* x, int64_t ldx, const void* w, int64_t M,
                              int64_t N, int64_t K, int epilogue, const void* res, int64_t ld_res,
                              void* stream) {
-    const int rc = check_shape(y, x, w, M, N, K, ldx);
+    int rc = check_shape(y, x, w, M, N, K, ldx);
+    if (rc == HAI_OK) rc = check_gemm_extents(y, ldy, x, ldx, w, 2, M, N, K, epilogue, res, ld_res);
     if (rc != HAI_OK) return rc;
     if (M == 0 || N == 0) return HAI_OK;
     const GemmArgs a{static_cast<uint16_t*>(y), ldy, static_cast<const uint16_t*>(x), ldx,
@@ -461,7 +462,10 @@ extern "C" int hai_gemm_rmsnorm_bf16(void* y, int64_t ldy, const void* x, int64_
                                      float eps, int unit_offset, void* xn_out, int64_t ld_xn, const void* w,
                                      int64_t M, int64_t N, int64_t K, int epilogue, const void* res,
                                      int64_t ld_res, void* stream) {
-    const int rc = check_shape(y, x, w, M, N, K, ldx);
+    int rc = check_shape(y, x, w, M, N, K, ldx);
+    if (rc == HAI_OK) rc = check_gemm_extents(y, ldy, x, ldx, w, 2, M, N, K, epilogue, res, ld_res);
+    if (rc == HAI_OK) rc = check_extent(norm_w, static_cast<size_t>(K) * 2, "gemm_rmsnorm norm_w");
+    if (rc == HAI_OK && xn_out != nullptr) rc = check_extent(xn_out, rows_extent(M, K, ld_xn, 2), "gemm_rmsnorm xn");
     if (rc != HAI_OK) return rc;
     if (norm_w == nullptr) return invalid("gemm_rmsnorm: null norm weight");
     if (xn_out != nullptr && (ld_xn < K || ld_xn % 8 != 0 || !aligned16(xn_out)))

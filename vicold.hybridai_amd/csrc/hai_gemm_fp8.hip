@@ -546,7 +546,8 @@ int dispatch_fp8_epi(Fp8Args& a, int epilogue, hipStream_t s) {
 extern "C" int hai_gemm_fp8_bf16(void* y, int64_t ldy, const void* x, int64_t ldx, const void* wq,
                                  const float* scales, const int32_t* scale_rows, int64_t M, int64_t N,
                                  int64_t K, int epilogue, const void* res, int64_t ld_res, void* stream) {
-    const int rc = check_fp8(y, x, wq, scales, M, N, K, ldx);
+    int rc = check_fp8(y, x, wq, scales, M, N, K, ldx);
+    if (rc == HAI_OK) rc = check_gemm_extents(y, ldy, x, ldx, wq, 1, M, N, K, epilogue, res, ld_res);
     if (rc != HAI_OK) return rc;
     if (M == 0 || N == 0) return HAI_OK;
     Fp8Args a{static_cast<uint16_t*>(y), ldy, static_cast<const uint16_t*>(x), ldx,
@@ -559,7 +560,11 @@ extern "C" int hai_gemm_rmsnorm_fp8_bf16(void* y, int64_t ldy, const void* x, in
                                          float eps, int unit_offset, void* xn_out, int64_t ld_xn, const void* wq,
                                          const float* scales, const int32_t* scale_rows, int64_t M, int64_t N,
                                          int64_t K, int epilogue, const void* res, int64_t ld_res, void* stream) {
-    const int rc = check_fp8(y, x, wq, scales, M, N, K, ldx);
+    int rc = check_fp8(y, x, wq, scales, M, N, K, ldx);
+    if (rc == HAI_OK) rc = check_gemm_extents(y, ldy, x, ldx, wq, 1, M, N, K, epilogue, res, ld_res);
+    if (rc == HAI_OK) rc = check_extent(norm_w, static_cast<size_t>(K) * 2, "gemm_rmsnorm_fp8 norm_w");
+    if (rc == HAI_OK && xn_out != nullptr)
+        rc = check_extent(xn_out, rows_extent(M, K, ld_xn, 2), "gemm_rmsnorm_fp8 xn");
     if (rc != HAI_OK) return rc;
     if (norm_w == nullptr) return invalid("gemm_rmsnorm_fp8: null norm weight");
     if (xn_out != nullptr && (ld_xn < K || ld_xn % 8 != 0 || !aligned16(xn_out)))

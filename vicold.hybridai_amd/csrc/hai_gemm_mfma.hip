@@ -749,6 +749,16 @@ int choose_splits(int64_t M, int64_t N, int64_t K, const void* workspace, size_t
 }
 
 int mfma_entry(MfmaArgs& a, int epilogue, void* workspace, size_t workspace_bytes, hipStream_t s) {
+    {
+        const int rc = check_gemm_extents(a.y, a.ldy, a.x, a.ldx, a.wq != nullptr ? static_cast<const void*>(a.wq)
+                                                                                   : static_cast<const void*>(a.w),
+                                          a.wq != nullptr ? 1 : 2, a.M, a.N, a.K, epilogue, a.res, a.ldres);
+        if (rc != HAI_OK) return rc;
+        if (workspace != nullptr && workspace_bytes > 0) {
+            const int r2 = check_extent(workspace, workspace_bytes, "gemm_mfma workspace");
+            if (r2 != HAI_OK) return r2;
+        }
+    }
     if (a.M == 0 || a.N == 0) return HAI_OK;
     a.keep = (epilogue & HAI_MFMA_KEEP_PARTIALS) != 0;
     epilogue &= ~HAI_MFMA_KEEP_PARTIALS;
@@ -792,13 +802,24 @@ extern "C" int hai_gemm_mfma_splits(int64_t M, int64_t N, int64_t K, const void*
     return choose_splits(M, N, K, workspace, workspace_bytes);
 }
 
-extern "C" int hai_mfma_residual_rmsnorm_bf16(void* h, int64_t ldh, const void* workspace, int64_t M, int64_t N,
-                                              int64_t splits, const void* norm_w, float eps, int unit_offset,
-                                              void* xn, int64_t ld_xn, void* stream) {
+extern "C" int hai_mfma_residual_rmsnorm_bf16(void* h, int64_t ldh, const void* workspace, size_t workspace_bytes,
+                                              int64_t M, int64_t N, int64_t splits, const void* norm_w, float eps,
+                                              int unit_offset, void* xn, int64_t ld_xn, void* stream) {
     if (h == nullptr || workspace == nullptr) return invalid("mfma_residual_rmsnorm: null pointer");
     if (M < 0 || M > kMaxMfmaRows || N <= 0 || N % 8 != 0 || N > kMaxResidualNormCols || ldh < N || ldh % 8 != 0 ||
-        splits < 1 || splits > 4)
-        return invalid("mfma_residual_rmsnorm: shape (need N % 8 == 0, N <= 8192, 1 <= splits <= 4)");
+        splits < 2 || splits > 4)
+        return invalid("mfma_residual_rmsnorm: shape (need N % 8 == 0, N <= 8192, 2 <= splits <= 4; a GEMM that "
+                       "takes one split finishes its rows itself and leaves no partials)");
+    if (static_cast<size_t>(splits) * static_cast<size_t>(M) * static_cast<size_t>(N) * sizeof(float) >
+        workspace_bytes)
+        return invalid("mfma_residual_rmsnorm: workspace_bytes below splits * M * N * 4");
+    {
+        int rc = check_extent(workspace, static_cast<size_t>(splits * M * N) * sizeof(float), "residual_rmsnorm ws");
+        if (rc == HAI_OK) rc = check_extent(h, rows_extent(M, N, ldh, 2), "residual_rmsnorm h");
+        if (rc == HAI_OK && norm_w != nullptr) rc = check_extent(norm_w, static_cast<size_t>(N) * 2, "norm_w");
+        if (rc == HAI_OK && norm_w != nullptr) rc = check_extent(xn, rows_extent(M, N, ld_xn, 2), "residual xn");
+        if (rc != HAI_OK) return rc;
+    }
     if (norm_w != nullptr && (xn == nullptr || ld_xn < N || ld_xn % 8 != 0 || !aligned16(norm_w) || !aligned16(xn)))
         return invalid("mfma_residual_rmsnorm: normalised output needs xn, ld_xn >= N, 16-byte alignment");
     if (!aligned16(h) || !aligned16(workspace)) return invalid("mfma_residual_rmsnorm: 16-byte alignment");

@@ -3,6 +3,7 @@
 #include "hai_common.h"
 #include "hai_device.h"
 
+#include <cstdlib>
 #include <string>
 
 namespace hai {
@@ -13,7 +14,45 @@ thread_local std::string g_last_error;
 
 void set_error(const std::string& message) { g_last_error = message; }
 
+bool bounds_checking() {
+    static const bool on = [] {
+        const char* e = std::getenv("HAI_CHECK_BOUNDS");
+        return e != nullptr && e[0] != '\0' && e[0] != '0';
+    }();
+    return on;
+}
+
+namespace {
+int extent_in_allocation(const void* p, size_t bytes, const char* what) {
+    if (bytes == 0) return HAI_OK;
+    if (p == nullptr) return invalid(what);
+    hipDeviceptr_t base = nullptr;
+    size_t size = 0;
+    if (hipMemGetAddressRange(&base, &size, const_cast<void*>(p)) != hipSuccess) {
+        (void)hipGetLastError();
+        set_error(std::string("bounds check: ") + what + " is not inside a device allocation");
+        return HAI_ERR_INVALID_ARGUMENT;
+    }
+    const uintptr_t b = reinterpret_cast<uintptr_t>(base);
+    const uintptr_t q = reinterpret_cast<uintptr_t>(p);
+    if (q + bytes > b + size) {
+        set_error(std::string("bounds check: ") + what + " needs " + std::to_string(bytes) + " bytes from offset " +
+                  std::to_string(q - b) + " of a " + std::to_string(size) + "-byte allocation");
+        return HAI_ERR_INVALID_ARGUMENT;
+    }
+    return HAI_OK;
+}
+}  // namespace
+
+int check_extent(const void* p, size_t bytes, const char* what) {
+    return bounds_checking() ? extent_in_allocation(p, bytes, what) : HAI_OK;
+}
+
 }  // namespace hai
+
+extern "C" int hai_debug_check_extent(const void* p, size_t bytes) {
+    return hai::extent_in_allocation(p, bytes, "range");
+}
 
 using namespace hai;
 

@@ -85,8 +85,12 @@ Engine::Engine(const hai_model_config& cfg, const hai_engine_options& opt) : cfg
     d_.qw = d_.nq * d_.D;
     d_.kvw = d_.nkv * d_.D;
     d_.Nqkv = 2 * d_.qw + 2 * d_.kvw;
-    tmax_ = std::max<int64_t>(2, std::min<int64_t>(16, opt.max_verify_tokens));
     B_ = std::max<int64_t>(1, opt.max_batch);
+    // verify rows per sequence: up to 17 (width 16, the reference's largest,
+    // generator.cc:124-137) for one sequence; batches keep 16 (one DeltaNet
+    // launch per forward)
+    tmax_ = std::max<int64_t>(2, std::min<int64_t>(B_ == 1 ? kMaxVerifyRows : kDeltaNetMaxT, opt.max_verify_tokens));
+    pchunk_ = std::min<int64_t>(tmax_, kDeltaNetMaxT);
     cap_ = std::max<int64_t>(opt.max_context, tmax_ + 1);
     ring_ = 32;
     nslots_ = tmax_ + 1;
@@ -427,8 +431,8 @@ int Engine::flush_pending() {
     if (pending_.h == nullptr) return HAI_OK;
     const PendingResidual p = pending_;
     pending_ = PendingResidual{};
-    return hai_mfma_residual_rmsnorm_bf16(p.h, p.ld, mfma_ws_, p.M, p.N, p.splits, nullptr, 0.0f, 0, nullptr, 0,
-                                          stream_);
+    return hai_mfma_residual_rmsnorm_bf16(p.h, p.ld, mfma_ws_, mfma_ws_bytes_, p.M, p.N, p.splits, nullptr, 0.0f, 0,
+                                          nullptr, 0, stream_);
 }
 
 int Engine::gemm(uint16_t* y, int64_t ldy, const uint16_t* x, int64_t ldx, const Lin& w, int64_t M, int64_t N,
@@ -494,8 +498,8 @@ int Engine::norm_gemm(uint16_t* y, int64_t ldy, const uint16_t* x, const uint16_
             // the previous residual GEMM's split sum, residual add and this norm in one launch
             const PendingResidual p = pending_;
             pending_ = PendingResidual{};
-            HAI_TRY(hai_mfma_residual_rmsnorm_bf16(p.h, p.ld, mfma_ws_, M, H, p.splits, nw, cfg_.rms_eps, 1, xn, H,
-                                                   stream_));
+            HAI_TRY(hai_mfma_residual_rmsnorm_bf16(p.h, p.ld, mfma_ws_, mfma_ws_bytes_, M, H, p.splits, nw,
+                                                   cfg_.rms_eps, 1, xn, H, stream_));
         } else {
             HAI_TRY(flush_pending());
             HAI_TRY(hai_rmsnorm_bf16(xn, H, x, H, nw, M, H, cfg_.rms_eps, 1, stream_));
@@ -572,7 +576,11 @@ int Engine::forward_target(const int64_t* d_ids, int64_t T, bool write_all_slots
         if (L.attn) {
             HAI_TRY(attention_layer(L, T, h_, d_tlen_, L.k_cache, L.v_cache));
         } else {
-            // qwen_deltanet_reference (qwen_reference.cc:205-258)
+            // qwen_deltanet_reference (qwen_reference.cc:205-258).  The
+            // DeltaNet kernel takes at most 16 tokens per launch: a verify
+            // of 17 rows (width 16, one sequence) runs as two launches, the
+            // second starting from the state the first left in slot
+            // (L + 16) % nslots and reading its conv history from the ring.
             if (fp8_) {
                 // FP8 qkv|z with the norm fused, writing the normalised rows;
                 // the bf16 a|b projection of each head is formed from them
@@ -580,10 +588,12 @@ int Engine::forward_target(const int64_t* d_ids, int64_t T, bool write_all_slots
                 HAI_TRY(norm_gemm(proj_, d.Nin, h_, L.in_ln, xn_, Lin(L.f_in), rows, d.C + d.vw, HAI_EPI_STORE,
                                   nullptr, 0));
                 HAI_TRY(flush_pending());
-                HAI_TRY(hai_deltanet_verify_ab_bf16(dnout_, d.vw, proj_, d.Nin, 0, d.C, xn_, d.H, L.w_ab, d.H,
-                                                    L.conv_w, L.ring, ring_, L.state, nslots_,
-                                                    write_all_slots ? 1 : 0, L.a_log, L.dt_bias, L.lin_norm, d_tlen_,
-                                                    0, B_, T, d.nk, d.nv, d.dk, d.dv, d.Kc, cfg_.rms_eps, stream_));
+                for (int64_t t0 = 0; t0 < T; t0 += kDeltaNetMaxT)
+                    HAI_TRY(hai_deltanet_verify_ab_bf16(
+                        dnout_ + t0 * d.vw, d.vw, proj_ + t0 * d.Nin, d.Nin, 0, d.C, xn_ + t0 * d.H, d.H, L.w_ab, d.H,
+                        L.conv_w, L.ring, ring_, L.state, nslots_, write_all_slots ? 1 : 0, L.a_log, L.dt_bias,
+                        L.lin_norm, d_tlen_, static_cast<int32_t>(t0), B_, std::min(kDeltaNetMaxT, T - t0), d.nk,
+                        d.nv, d.dk, d.dv, d.Kc, cfg_.rms_eps, stream_));
             } else if (use_mfma(rows)) {
                 // matrix-core mode: the qkv|z rows only (16384 rows at the 27B
                 // shape, whole 64-row tiles that load every CU alike, where
@@ -592,18 +602,21 @@ int Engine::forward_target(const int64_t* d_ids, int64_t T, bool write_all_slots
                 HAI_TRY(norm_gemm(proj_, d.Nin, h_, L.in_ln, xn_, L.w_in, rows, d.C + d.vw, HAI_EPI_STORE, nullptr,
                                   0));
                 HAI_TRY(flush_pending());
-                HAI_TRY(hai_deltanet_verify_ab_bf16(dnout_, d.vw, proj_, d.Nin, 0, d.C, xn_, d.H,
-                                                    L.w_in + (d.C + d.vw) * d.H, d.H, L.conv_w, L.ring, ring_,
-                                                    L.state, nslots_, write_all_slots ? 1 : 0, L.a_log, L.dt_bias,
-                                                    L.lin_norm, d_tlen_, 0, B_, T, d.nk, d.nv, d.dk, d.dv, d.Kc,
-                                                    cfg_.rms_eps, stream_));
+                for (int64_t t0 = 0; t0 < T; t0 += kDeltaNetMaxT)
+                    HAI_TRY(hai_deltanet_verify_ab_bf16(
+                        dnout_ + t0 * d.vw, d.vw, proj_ + t0 * d.Nin, d.Nin, 0, d.C, xn_ + t0 * d.H, d.H,
+                        L.w_in + (d.C + d.vw) * d.H, d.H, L.conv_w, L.ring, ring_, L.state, nslots_,
+                        write_all_slots ? 1 : 0, L.a_log, L.dt_bias, L.lin_norm, d_tlen_, static_cast<int32_t>(t0),
+                        B_, std::min(kDeltaNetMaxT, T - t0), d.nk, d.nv, d.dk, d.dv, d.Kc, cfg_.rms_eps, stream_));
             } else {
                 HAI_TRY(norm_gemm(proj_, d.Nin, h_, L.in_ln, nullptr, L.w_in, rows, d.Nin, HAI_EPI_STORE, nullptr,
                                   0));
-                HAI_TRY(hai_deltanet_verify_bf16(dnout_, d.vw, proj_, d.Nin, 0, d.C, d.C + d.vw, d.C + d.vw + d.nv,
-                                                 L.conv_w, L.ring, ring_, L.state, nslots_, write_all_slots ? 1 : 0,
-                                                 L.a_log, L.dt_bias, L.lin_norm, d_tlen_, 0, B_, T, d.nk, d.nv, d.dk,
-                                                 d.dv, d.Kc, cfg_.rms_eps, stream_));
+                for (int64_t t0 = 0; t0 < T; t0 += kDeltaNetMaxT)
+                    HAI_TRY(hai_deltanet_verify_bf16(
+                        dnout_ + t0 * d.vw, d.vw, proj_ + t0 * d.Nin, d.Nin, 0, d.C, d.C + d.vw, d.C + d.vw + d.nv,
+                        L.conv_w, L.ring, ring_, L.state, nslots_, write_all_slots ? 1 : 0, L.a_log, L.dt_bias,
+                        L.lin_norm, d_tlen_, static_cast<int32_t>(t0), B_, std::min(kDeltaNetMaxT, T - t0), d.nk,
+                        d.nv, d.dk, d.dv, d.Kc, cfg_.rms_eps, stream_));
             }
             HAI_TRY(gemm(h_, d.H, dnout_, d.vw, lin(L.w_out, L.f_out), rows, d.H, d.vw, HAI_EPI_RESIDUAL, h_, d.H));
         }
@@ -657,15 +670,15 @@ int Engine::mtp_draft_step(const int64_t* d_id, const uint16_t* d_hin, uint16_t*
     return HAI_OK;
 }
 
-// Prompt prefill in chunks of tmax_ rows per sequence (rows are independent
+// Prompt prefill in chunks of pchunk_ rows per sequence (rows are independent
 // and the recurrences are sequential, so chunking does not change a bit),
 // each chunk followed by its MTP prompt rows (emb(t_i) paired with the
 // hidden of t_i).  ids [B][P]; hidden_out [B][P][H], logits_out [B][P][V].
 int Engine::prefill_chunks(const int32_t* ids, int64_t P, uint16_t* hidden_out, uint16_t* logits_out) {
     const auto& d = d_;
-    std::vector<int64_t> chunk(static_cast<size_t>(B_ * tmax_));
-    for (int64_t off = 0; off < P; off += tmax_) {
-        const int64_t T = std::min<int64_t>(tmax_, P - off);
+    std::vector<int64_t> chunk(static_cast<size_t>(B_ * pchunk_));
+    for (int64_t off = 0; off < P; off += pchunk_) {
+        const int64_t T = std::min<int64_t>(pchunk_, P - off);
         for (int64_t b = 0; b < B_; ++b)
             for (int64_t t = 0; t < T; ++t) chunk[static_cast<size_t>(b * T + t)] = ids[b * P + off + t];
         HAI_TRY(hai_memcpy_h2d(d_ids_, chunk.data(), static_cast<size_t>(B_ * T) * 8, stream_));
@@ -828,7 +841,7 @@ int Engine::one_round(int64_t width, const RoundIo& io, bool* any_live) {
             st.done = true;
             continue;
         }
-        pc[b] = std::min<int64_t>(std::min<int64_t>(width, remaining - 1), tmax_ - 1);
+        pc[b] = std::min<int64_t>(width, remaining - 1);  // width <= tmax_ - 1, checked by the callers
         k = std::max(k, pc[b]);
         live = true;
     }
@@ -952,6 +965,9 @@ int Engine::one_round(int64_t width, const RoundIo& io, bool* any_live) {
             // The reference replays [next, accepted..., corr] on the committed
             // caches; the rows before corr are already committed above.
             st.target_len = target_len0[b] + a + 2;
+            // the reference's replay count (generator.cc:941-950): next,
+            // the accepted candidates and the correction
+            stats.replay_tokens += a + 2;
             if (st.emitted >= st.max_new || in_set(io.eos, io.n_eos, corr)) {
                 st.mtp_len = mtp_len0[b];  // the reference stops before restoring the MTP checkpoint
                 st.done = true;
@@ -959,7 +975,6 @@ int Engine::one_round(int64_t width, const RoundIo& io, bool* any_live) {
                 correct[b] = true;
                 any_correct = true;
                 ++stats.mtp_recovery_tokens;
-                ++stats.replay_tokens;
                 st.mtp_len = mtp_len0[b] + a + 1;
             }
         }
@@ -996,6 +1011,10 @@ int Engine::generate_speculative(const int32_t* prompts, int64_t P, int64_t max_
                                  int64_t n_override, int32_t* out, hai_spec_stats* stats, int32_t* round_log,
                                  int64_t round_log_cap, int64_t* n_out) {
     if (width < 1) return fail(HAI_ERR_INVALID_ARGUMENT, "width must be >= 1");
+    if (width > tmax_ - 1)
+        return fail(HAI_ERR_INVALID_ARGUMENT, "width " + std::to_string(width) + " needs max_verify_tokens >= " +
+                                                  std::to_string(width + 1) + " (this engine verifies " +
+                                                  std::to_string(tmax_) + " rows)");
     if (override_tokens != nullptr) HAI_TRY(check_ids(override_tokens, B_ * n_override, "draft override"));
     // a finished sequence keeps running with the batch: leave room for its
     // rows until the slowest sequence ends
@@ -1035,6 +1054,8 @@ int Engine::generate_speculative(const int32_t* prompts, int64_t P, int64_t max_
 
 int Engine::spec_rounds(int64_t rounds, int64_t width, int32_t* out, int64_t cap, int64_t* n_out,
                         hai_spec_stats* stats) {
+    if (width < 1 || width > tmax_ - 1)
+        return fail(HAI_ERR_INVALID_ARGUMENT, "spec_rounds: width must be in 1 .. max_verify_tokens - 1");
     for (const auto& r : rs_)
         if (out == nullptr || cap < r.max_new) return fail(HAI_ERR_INVALID_ARGUMENT, "spec_rounds: out capacity < max_new");
     const size_t Bz = static_cast<size_t>(B_);

@@ -112,6 +112,11 @@ struct Dims {
     int64_t H, F, V, nq, nkv, D, R, nk, nv, dk, dv, Kc, C, Nin, Nqkv, qw, kvw, vw;
 };
 
+// Tokens per DeltaNet kernel launch, and the largest verify (width 16 + 1,
+// the reference's widest proposal, generator.cc:124-137).
+constexpr int64_t kDeltaNetMaxT = 16;
+constexpr int64_t kMaxVerifyRows = 17;
+
 class Engine {
 public:
     Engine(const hai_model_config& cfg, const hai_engine_options& opt);
@@ -237,7 +242,8 @@ private:
 
     int64_t B_ = 1;       // sequences
     int64_t cap_ = 0;     // KV capacity per sequence
-    int64_t tmax_ = 0;    // largest verify T / prefill chunk (rows per sequence)
+    int64_t tmax_ = 0;    // largest verify T (rows per sequence)
+    int64_t pchunk_ = 0;  // prompt rows per prefill forward (<= 16: one DeltaNet launch)
     bool mfma_ = false;   // tolerance mode: MFMA GEMMs (4+ rows) and attention
     int64_t ring_ = 0;
     int64_t nslots_ = 0;

@@ -15,7 +15,9 @@
 //     checkpoint);
 //   * GeneratorOptions::backend = "hip" (or "mi355x");
 //   * GenerationOptions::prompt = "ids:1,2,3" -- token ids; result.text holds
-//     the generated ids in the same form.  The synthetic models have no EOS.
+//     the generated ids in the same form.  The synthetic models have no EOS;
+//   * the speculative proposal width is HYBRIDAI_SPECULATIVE_WIDTH (1..16,
+//     default 8), read at every generate() as the reference does.
 #include <sys/stat.h>
 
 #include <algorithm>
@@ -77,6 +79,19 @@ bool parse_ids(const std::string& text, std::vector<int32_t>* ids) {
     return in.eof() && !ids->empty();
 }
 
+// speculative_proposal_width (generator.cc:124-137): the MTP proposal width
+// comes from HYBRIDAI_SPECULATIVE_WIDTH, a decimal in 1..16; unset, empty or
+// anything else gives the default of 8.
+int64_t speculative_width_from_env() {
+    constexpr int64_t kDefault = 8, kMax = 16;
+    const char* v = std::getenv("HYBRIDAI_SPECULATIVE_WIDTH");
+    if (v == nullptr || v[0] == '\0') return kDefault;
+    char* end = nullptr;
+    const unsigned long n = std::strtoul(v, &end, 10);
+    if (end == v || *end != '\0' || n == 0 || n > static_cast<unsigned long>(kMax)) return kDefault;
+    return static_cast<int64_t>(n);
+}
+
 }  // namespace
 
 class Generator::Impl {
@@ -122,7 +137,7 @@ public:
         }
         hai_engine_options eo{};
         eo.max_context = context;
-        eo.max_verify_tokens = 16;
+        eo.max_verify_tokens = static_cast<int32_t>(mi355x::kMaxVerifyRows);  // any width the env var allows
         eo.device = 0;
         eo.use_graphs = 0;
         eo.weight_format = weight_format;
@@ -151,7 +166,7 @@ public:
         for (int32_t id : prompt)
             if (id >= cfg_.vocab) return {ApiStatusCode::InvalidArgument, "prompt id outside the vocabulary"};
         if (o.max_new_tokens < 0) return {ApiStatusCode::InvalidArgument, "max_new_tokens must be >= 0"};
-        if (static_cast<int64_t>(prompt.size()) + o.max_new_tokens + 16 > context_)
+        if (static_cast<int64_t>(prompt.size()) + o.max_new_tokens + mi355x::kMaxVerifyRows > context_)
             return {ApiStatusCode::InvalidArgument, "prompt + max_new_tokens exceed the model context"};
         *result = GenerationResult{};
         std::vector<int32_t> out(static_cast<size_t>(std::max(1, o.max_new_tokens)));
@@ -161,7 +176,8 @@ public:
         int rc;
         if (o.enable_speculative_mtp) {
             rc = engine_->generate_speculative(prompt.data(), static_cast<int64_t>(prompt.size()), o.max_new_tokens,
-                                               1, nullptr, 0, nullptr, 0, out.data(), &st, nullptr, 0, &n);
+                                               speculative_width_from_env(), nullptr, 0, nullptr, 0, out.data(), &st,
+                                               nullptr, 0, &n);
         } else {
             rc = engine_->generate_greedy(prompt.data(), static_cast<int64_t>(prompt.size()), o.max_new_tokens,
                                           nullptr, 0, out.data(), &n);
