@@ -250,6 +250,23 @@ int hai_gqa_verify_bf16(void* out, const void* q, const void* gate,
                         void* scratch, int64_t B, int64_t T, int64_t nq,
                         int64_t nkv, int64_t D, const int32_t* lens,
                         int32_t len_add, int64_t max_len, void* stream);
+/* hai_gqa_verify_bf16 for callers that cannot allocate (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc): the
+ * same kernels and bit-identical results, with the split-KV partials in a
+ * fixed 16 MiB device array the library holds on each GPU it runs on until
+ * the process ends (HAI_GQA_NOALLOC_SCRATCH_BYTES), so no scratch argument
+ * and no allocation.  No counterpart in the reference.  Calls whose
+ * hai_gqa_scratch_bytes(B, T, nq, D, max_len) exceeds that size are
+ * rejected.  All calls on one GPU share its array: calls that overlap on a
+ * GPU (two streams, two threads) race and must be serialised by the caller.
+ * The first call on a device resolves the array's address there
+ * (hipGetSymbolAddress) with that device current. */
+#define HAI_GQA_NOALLOC_SCRATCH_BYTES (16u << 20)
+int hai_gqa_verify_noalloc_bf16(void* out, const void* q, const void* gate,
+                                const void* k_cache, const void* v_cache,
+                                int64_t cap, int64_t B, int64_t T, int64_t nq,
+                                int64_t nkv, int64_t D, const int32_t* lens,
+                                int32_t len_add, int64_t max_len, void* stream);
 /* The same attention in tolerance mode, on the matrix cores (same reference
  * kernels as above; the batched verify / draft steps).  Q.K^T and P.V run
  * as bf16 MFMA with fp32 accumulation (P rounded to bf16), one online

@@ -21,6 +21,10 @@
 // The chunking is by absolute key index, so a query's result does not depend
 // on T, on the batch or on how many blocks run: verify rows and replayed
 // rows are bit-identical, and the CPU oracle follows the same order.
+#include <atomic>
+#include <mutex>
+#include <string>
+
 #include "hai_common.h"
 #include "hai_device.h"
 #include "hai_gemm_common.h"
@@ -790,9 +794,61 @@ int launch_mfma(uint16_t* out, const uint16_t* q, const uint16_t* gate, const ui
     return launched("gqa_mfma_combine_kernel");
 }
 
+// ---- the allocation-free entry point --------------------------------------
+// hai_gqa_verify_noalloc_bf16 keeps its split-KV partials in this file-scope
+// device array instead of a caller workspace: each GPU the library runs on
+// holds its own copy (kGqaNoAllocScratchBytes) from module load until the
+// process ends.  Host code never passes the array's name to a kernel (on
+// the host it is only a stand-in for the symbol): the device address comes
+// from hipGetSymbolAddress, resolved once per device with that device
+// current on the entry point's first call there, and kept per device.
+constexpr size_t kGqaNoAllocScratchBytes = size_t{16} << 20;
+static __device__ __align__(256) float gqa_noalloc_scratch[kGqaNoAllocScratchBytes / sizeof(float)];
+
+constexpr int kMaxNoAllocDevices = 64;
+std::atomic<float*> g_noalloc_ptr[kMaxNoAllocDevices];
+std::mutex g_noalloc_mu;
+
+int noalloc_scratch(float** out) {
+    int dev = 0;
+    int rc = check_hip(hipGetDevice(&dev), "hipGetDevice");
+    if (rc != HAI_OK) return rc;
+    if (dev < 0 || dev >= kMaxNoAllocDevices) return invalid("gqa_verify_noalloc: device ordinal above 63");
+    float* p = g_noalloc_ptr[dev].load(std::memory_order_acquire);
+    if (p == nullptr) {
+        std::lock_guard<std::mutex> lock(g_noalloc_mu);
+        p = g_noalloc_ptr[dev].load(std::memory_order_acquire);
+        if (p == nullptr) {
+            void* sym = nullptr;
+            rc = check_hip(hipGetSymbolAddress(&sym, HIP_SYMBOL(gqa_noalloc_scratch)), "hipGetSymbolAddress");
+            if (rc != HAI_OK) return rc;
+            p = static_cast<float*>(sym);
+            g_noalloc_ptr[dev].store(p, std::memory_order_release);
+        }
+    }
+    *out = p;
+    return HAI_OK;
+}
+
 }  // namespace
 
 extern "C" {
+
+int hai_gqa_verify_noalloc_bf16(void* out, const void* q, const void* gate, const void* k_cache,
+                                const void* v_cache, int64_t cap, int64_t B, int64_t T, int64_t nq, int64_t nkv,
+                                int64_t D, const int32_t* lens, int32_t len_add, int64_t max_len, void* stream) {
+    if (B < 0 || T < 0 || nq <= 0 || max_len <= 0) return invalid("gqa_verify_noalloc: shape");
+    const size_t need = hai_gqa_scratch_bytes(B, T, nq, D, max_len);
+    if (need > kGqaNoAllocScratchBytes)
+        return invalid(("gqa_verify_noalloc: the partials need " + std::to_string(need) +
+                        " bytes, above the fixed 16 MiB scratch (use hai_gqa_verify_bf16 with a workspace)")
+                           .c_str());
+    float* ptr = nullptr;
+    const int rc = noalloc_scratch(&ptr);
+    if (rc != HAI_OK) return rc;
+    return hai_gqa_verify_bf16(out, q, gate, k_cache, v_cache, cap, ptr, B, T, nq, nkv, D, lens, len_add, max_len,
+                               stream);
+}
 
 size_t hai_gqa_scratch_bytes(int64_t B, int64_t T, int64_t nq, int64_t D, int64_t max_len) {
     const int64_t nchunk = (max_len + kChunk - 1) / kChunk;
