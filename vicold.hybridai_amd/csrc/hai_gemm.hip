@@ -50,16 +50,31 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(
     // to the machine so that the prologue is paid once per resident block.
     const int64_t ngroups = (static_cast<int64_t>(N) + 4 * RW - 1) / (4 * RW);
 
-    // The first U chunks of the block's first rows do not depend on the
-    // activations: with the fused RMSNorm they are requested before the
-    // prologue, whose latency then overlaps theirs.
-    u32x4 wpre[U][RW];
+    // The block's first weight chunks do not depend on the activations: with
+    // the fused RMSNorm they are requested before the prologue, whose
+    // latency then overlaps theirs.  Two-row launches (the verify of one
+    // sequence at k = 1) stage the rows by global -> LDS copies issued ahead
+    // of PG = 2 chunk groups of weights and wait for the copies alone, so
+    // both the row fetch and the normalisation run with those weights in
+    // flight (measured on MI355X at the 27B shapes: in_proj 32.2 -> 29.3 us,
+    // gate/up 58.2 -> 56.0, q|gate|k|v 27.8 -> 26.0).  The other row counts
+    // fetch the rows through registers; a wait for them then also waits for
+    // the chunks requested before (loads complete in order), which measured
+    // as fast there.
+    constexpr bool kDmaStage = NORM && MB == 2;
+    constexpr int PG = kDmaStage ? 2 : 1;
+    u32x4 wpre[PG * U][RW];
     const int64_t grp0 = blockIdx.x;
     if constexpr (NORM) {
         const int64_t row0 = (grp0 * 4 + wave) * RW;
-        if (grp0 < ngroups && row0 < N) {
+        const bool pre_ok = grp0 < ngroups && row0 < N;
+        if constexpr (kDmaStage) {
+            stage_rows_lds_dma(xs, x, ldx, M, K, na.w);
+            __builtin_amdgcn_sched_barrier(0);  // the weight requests stay behind the copies
+        }
+        if (pre_ok) {
 #pragma unroll
-            for (int u = 0; u < U; ++u) {
+            for (int u = 0; u < PG * U; ++u) {
                 const bool ok = u < nfull || (u < nck && u * 512 + lane * 8 < K);
                 const ChunkOffset co(u < nfull, ok, static_cast<uint32_t>(u) * 1024u);
 #pragma unroll
@@ -67,7 +82,19 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(
                     wpre[u][r] = bload_w(rw, co.v(static_cast<uint32_t>(((row0 + r) * static_cast<int64_t>(K) + lane * 8) * 2)), co.s);
             }
         }
-        rmsnorm_rows_to_lds(xs, x, ldx, M, K, na);
+        if constexpr (kDmaStage) {
+            // wait for this wave's copies only: at most the PG * U * RW
+            // weight requests issued after them may still be in flight (a
+            // wave without rows issued none, and waits for its copies)
+            __builtin_amdgcn_sched_barrier(0);
+            wait_vmcnt<PG * U * RW>();
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_barrier();  // every wave's copies have landed
+            __builtin_amdgcn_sched_barrier(0);
+            normalize_staged_rows(xs, M, K, na);
+        } else {
+            rmsnorm_rows_to_lds(xs, x, ldx, M, K, na);
+        }
     }
 
     // One row group; FIRST: the block's first group, whose first U chunks
@@ -126,20 +153,42 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(
         // reads zeros through an out-of-range offset; fma(0, 0, acc) == acc
         // because acc is never -0 (it starts at +0 and round-to-nearest only
         // produces -0 from (-0) + (-0)), so padding does not change a bit.
-        auto step = [&](int c0, const u32x4 (&wv)[U][RW]) {
-            u32x4 xv[U][MB];
+        // Activation rows of a chunk group from global memory (the plain
+        // kernel).  Two-row launches request them ahead of the group's
+        // weights: the first fma of the group then waits for its own chunk,
+        // not for every weight chunk of the group (loads complete in order;
+        // out / o projection at M = 2: 14.1 -> 13.3 us on MI355X).
+        constexpr bool kXFirst = !NORM && MB == 2;
+        auto load_x = [&](int c0, u32x4 (&xv)[U][MB]) {
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 const int c = c0 + u;
                 const bool ok = c < nfull || (c < nck && c * 512 + lane * 8 < K);
                 const ChunkOffset co(c < nfull, ok, static_cast<uint32_t>(c) * 1024u);
 #pragma unroll
-                for (int m = 0; m < MB; ++m) {
-                    if constexpr (NORM)
+                for (int m = 0; m < MB; ++m) xv[u][m] = bload(rx, co.v(xoff[m]), co.s);
+            }
+        };
+        // xin: the group's activation rows when they were requested ahead
+        // of the weights (kXFirst), else unused
+        auto step = [&](int c0, const u32x4 (&wv)[U][RW], const u32x4 (*xin)[MB]) {
+            u32x4 xv[U][MB];
+            if constexpr (kXFirst) {
+#pragma unroll
+                for (int u = 0; u < U; ++u)
+#pragma unroll
+                    for (int m = 0; m < MB; ++m) xv[u][m] = xin[u][m];
+            } else if constexpr (NORM) {
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const int c = c0 + u;
+                    const bool ok = c < nfull || (c < nck && c * 512 + lane * 8 < K);
+#pragma unroll
+                    for (int m = 0; m < MB; ++m)
                         xv[u][m] = (ok && m < M) ? xs[m * npr + c * 64 + lane] : u32x4{0u, 0u, 0u, 0u};
-                    else
-                        xv[u][m] = bload(rx, co.v(xoff[m]), co.s);
                 }
+            } else {
+                load_x(c0, xv);
             }
 #pragma unroll
             for (int u = 0; u < U; ++u) body(wv[u], xv[u]);
@@ -148,11 +197,28 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(
         };
         int c0 = 0;
         if constexpr (FIRST) {
-            step(0, wpre);
-            c0 = U;
+            // (only the NORM kernel prefetches: kXFirst is never FIRST)
+            if constexpr (PG == 1) {
+                step(0, wpre, nullptr);
+                c0 = U;
+            } else {
+#pragma unroll
+                for (int g = 0; g < PG; ++g) {
+                    if (c0 < nck) {
+                        u32x4 wv[U][RW];
+#pragma unroll
+                        for (int u = 0; u < U; ++u)
+#pragma unroll
+                            for (int r = 0; r < RW; ++r) wv[u][r] = wpre[g * U + u][r];
+                        step(c0, wv, nullptr);
+                        c0 += U;
+                    }
+                }
+            }
         }
         for (; c0 < nck; c0 += U) {
-            u32x4 wv[U][RW];
+            u32x4 wv[U][RW], xv[U][MB];
+            if constexpr (kXFirst) load_x(c0, xv);
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 const int c = c0 + u;
@@ -162,7 +228,7 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(
 #pragma unroll
                 for (int r = 0; r < RW; ++r) wv[u][r] = bload_w(rw, co.v(woff[r]), co.s);
             }
-            step(c0, wv);
+            step(c0, wv, xv);
         }
         fold();
 
@@ -330,7 +396,10 @@ struct GemmArgs {
 
 template <int MB, int RW, int EPI, bool NORM>
 void launch_gemm(const GemmArgs& a, hipStream_t s) {
-    constexpr int U = MB <= 2 ? 4 : (MB <= 8 ? 2 : 1);
+    // chunks per group: two-row launches take 2 (with their two-group
+    // prefetch or activations-first order; measured faster than 4 there),
+    // one row 4, more rows fewer to bound the registers
+    constexpr int U = MB == 1 ? 4 : (MB <= 8 ? 2 : 1);
     auto* kern = gemm_bf16_kernel<MB, RW, U, EPI, NORM>;
     const int64_t groups = (static_cast<int64_t>(a.N) + 4 * RW - 1) / (4 * RW);
     // NORM: LDS holds the M rows and the norm weight staged behind them.

@@ -21,36 +21,16 @@ struct NormArgs {
 
 constexpr int kNormMaxElems = HAI_GEMM_RMSNORM_FUSED_MAX;  // M * K: 32 KB of LDS
 
-// Stages the M activation rows [M, K] (row pitch ldx) in xs as 16-byte
-// pieces, normalised: the raw rows and the norm weight are fetched together
-// (one latency), one wave per row reduces the sum of squares in L64 order,
-// then every element is scaled in place.  xs holds (M + 1) * K / 8 pieces;
-// a 256-thread block; ends with a block barrier.
-__device__ __forceinline__ void rmsnorm_rows_to_lds(u32x4* xs, const uint16_t* __restrict__ x, int64_t ldx,
-                                                    int M, int K, const NormArgs& na) {
+// The normalisation step of the prologue: the M raw rows are staged in xs
+// as 16-byte pieces [M][K/8] with the norm weight behind them (visible to
+// the whole block), one wave per row reduces the sum of squares in L64
+// order, then every element is scaled in place; ends with a block barrier.
+__device__ __forceinline__ void normalize_staged_rows(u32x4* xs, int M, int K, const NormArgs& na) {
     __shared__ float inv_sh[16];
     const int lane = threadIdx.x & 63;
     const int wave = wave_index();
     const int npr = K >> 3;  // 16-byte pieces per row
     const int total = M * npr;
-    for (int e0 = 0; e0 < total; e0 += 1024) {
-        u32x4 xr[4], wr[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int e = e0 + threadIdx.x + 256 * i;
-            const int r = e / npr;
-            const int p = e - r * npr;
-            if (e < total) xr[i] = *reinterpret_cast<const u32x4*>(x + r * ldx + p * 8);
-            if (e < npr) wr[i] = *reinterpret_cast<const u32x4*>(na.w + p * 8);
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int e = e0 + threadIdx.x + 256 * i;
-            if (e < total) xs[e] = xr[i];
-            if (e < npr) xs[total + e] = wr[i];  // norm weight staged once, behind the rows
-        }
-    }
-    __syncthreads();
     for (int r = wave; r < M; r += 4) {
         float acc = 0.0f;
         for (int p = lane; p < npr; p += 64) {
@@ -84,6 +64,70 @@ __device__ __forceinline__ void rmsnorm_rows_to_lds(u32x4* xs, const uint16_t* _
         if (na.xn != nullptr && blockIdx.x == 0) *reinterpret_cast<u32x4*>(na.xn + r * na.ldxn + p * 8) = o;
     }
     __syncthreads();
+}
+
+// Stages the M activation rows [M, K] (row pitch ldx) in xs as 16-byte
+// pieces, normalised: the raw rows and the norm weight are fetched together
+// (one latency), then normalize_staged_rows.  xs holds (M + 1) * K / 8
+// pieces; a 256-thread block; ends with a block barrier.
+__device__ __forceinline__ void rmsnorm_rows_to_lds(u32x4* xs, const uint16_t* __restrict__ x, int64_t ldx,
+                                                    int M, int K, const NormArgs& na) {
+    const int npr = K >> 3;  // 16-byte pieces per row
+    const int total = M * npr;
+    for (int e0 = 0; e0 < total; e0 += 1024) {
+        u32x4 xr[4], wr[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int e = e0 + threadIdx.x + 256 * i;
+            const int r = e / npr;
+            const int p = e - r * npr;
+            if (e < total) xr[i] = *reinterpret_cast<const u32x4*>(x + r * ldx + p * 8);
+            if (e < npr) wr[i] = *reinterpret_cast<const u32x4*>(na.w + p * 8);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int e = e0 + threadIdx.x + 256 * i;
+            if (e < total) xs[e] = xr[i];
+            if (e < npr) xs[total + e] = wr[i];  // norm weight staged once, behind the rows
+        }
+    }
+    __syncthreads();
+    normalize_staged_rows(xs, M, K, na);
+}
+
+// The same staging done by the memory system: every piece of the raw rows
+// and of the norm weight is copied global -> LDS by global_load_lds (16 bytes
+// per lane, no registers), so that the caller can request its first weight
+// chunks behind these copies and wait for the copies alone: loads complete
+// in order, so s_waitcnt vmcnt(n), with n the loads issued after the copies,
+// leaves those weight chunks in flight while the prologue computes.  Issues
+// kStageOps copy instructions per wave (lanes past the data masked off).
+// Needs (M + 1) * K / 8 <= 256 * kStageOps pieces, 16-byte aligned rows.
+constexpr int kStageOps = 12;  // (M + 1) * K <= 24576: M * K <= HAI_GEMM_RMSNORM_FUSED_MAX, K <= 8192
+__device__ __forceinline__ void stage_rows_lds_dma(u32x4* xs, const uint16_t* __restrict__ x, int64_t ldx, int M,
+                                                   int K, const uint16_t* __restrict__ norm_w) {
+    const int wave = wave_index();
+    const int npr = K >> 3;
+    const int total = M * npr;
+#pragma unroll
+    for (int i = 0; i < kStageOps; ++i) {
+        const int e = static_cast<int>(threadIdx.x) + 256 * i;
+        if (e < total + npr) {
+            const int r = e / npr;
+            const uint16_t* src = e < total ? x + r * ldx + (e - r * npr) * 8 : norm_w + (e - total) * 8;
+            // (a C-style cast: the generic -> LDS address-space conversion)
+            __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(xs + wave * 64 + 256 * i),
+                                             16, 0, 0);
+        }
+    }
+}
+
+// s_waitcnt with vmcnt(n) and the other counters left alone (gfx9 encoding:
+// vmcnt bits [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8]).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
 // Blocks of 256 threads of `kernel` with `shmem` bytes of dynamic LDS that
