@@ -1,0 +1,53 @@
+"""The skinny GEMM kernels that stage activation rows by global -> LDS copies
+wait for those copies with s_waitcnt vmcnt(n), where n is the number of
+weight requests issued after the copies: vector-memory loads of a wave
+complete in issue order, so the wait retires every copy while n weight
+chunks stay in flight.  The wait is only right when exactly n requests sit
+between the last copy and the wait in the code the compiler emits (a request
+sunk below the wait leaves copies unretired: a race on the staged rows).
+This test compiles hai_gemm.hip for gfx950 with the build's flags and checks
+that count in every kernel that stages by copies.  CPU only (hipcc
+cross-compiles)."""
+import re
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+sys.path.insert(0, str(ROOT / "vicold.hybridai_amd"))
+
+
+def _kernels(asm: str):
+    lines = asm.split("\n")
+    for i, line in enumerate(lines):
+        m = re.match(r"^(_Z\S*gemm_bf16\S*kernel\S*):", line)
+        if not m:
+            continue
+        end = next(j for j in range(i, len(lines)) if "s_endpgm" in lines[j])
+        yield m.group(1), lines[i:end]
+
+
+def test_staged_copy_waits_count_the_requests_behind_them(tmp_path):
+    import build
+    if not Path(build.HIPCC).exists() and shutil.which("hipcc") is None:
+        pytest.skip("hipcc not available")
+    out = tmp_path / "gemm.s"
+    flags = [f for f in build.HIP_FLAGS if f != "-fPIC"]
+    subprocess.run([build.HIPCC, *flags, "--cuda-device-only", "-S", str(build.CSRC / "hai_gemm.hip"), "-o", str(out)],
+                   check=True, capture_output=True, timeout=600)
+    checked = 0
+    for name, body in _kernels(out.read_text()):
+        copies = [k for k, l in enumerate(body) if "global_load_lds" in l]
+        if not copies:
+            continue
+        last = copies[-1]
+        wait = next(k for k in range(last, len(body)) if "s_waitcnt" in body[k] and "vmcnt(" in body[k])
+        n = int(re.search(r"vmcnt\((\d+)\)", body[wait]).group(1))
+        issued = sum(1 for k in range(last + 1, wait) if "buffer_load" in body[k] or
+                     ("global_load" in body[k] and "lds" not in body[k]))
+        assert issued == n, f"{name}: {issued} requests between the copies and s_waitcnt vmcnt({n})"
+        checked += 1
+    assert checked >= 4, f"only {checked} staging kernels found"

@@ -75,7 +75,7 @@ def test_primitives_bit_exact(fn, name):
 # ----------------------------------------------------------------- gemm
 @pytest.mark.parametrize("M,N,K_", [(1, 37, 8), (2, 256, 256), (2, 1536, 256), (3, 4096, 256),
                                     (4, 100, 1000), (7, 64, 520), (16, 512, 768), (2, 5120, 17408),
-                                    (1, 16480, 5120), (2, 9, 1024)])
+                                    (1, 16480, 5120), (2, 9, 1024), (2, 1030, 2056), (2, 8192, 20480)])
 def test_gemm_store(M, N, K_):
     rng = np.random.default_rng(M * 1000 + N + K_)
     x, xb = rand_bf16(rng, (M, K_))
@@ -86,7 +86,8 @@ def test_gemm_store(M, N, K_):
 
 
 @pytest.mark.parametrize("M,N,K_", [(2, 256, 256), (4, 5120, 6144), (16, 300, 512), (1, 5120, 6144),
-                                    (2, 5120, 17408), (1, 77, 9000), (2, 130, 8192)])
+                                    (2, 5120, 17408), (1, 77, 9000), (2, 130, 8192), (2, 2050, 8200),
+                                    (2, 1031, 6152)])
 def test_gemm_residual(M, N, K_):
     rng = np.random.default_rng(7 + M + N)
     x, xb = rand_bf16(rng, (M, K_))
@@ -97,6 +98,24 @@ def test_gemm_residual(M, N, K_):
               "gemm residual")
     want = orc.add(h, orc.gemm(x, w))
     assert_bits_equal(dh.download(np.uint16), want, "gemm residual")
+
+
+def test_gemm_two_rows_with_row_pitch():
+    """Two-row residual launch of the short layers (activation rows staged
+    in LDS) with row pitches above the row lengths: x rows K + 24 apart,
+    h rows N + 40 apart, only the first N columns of h touched."""
+    M, N, K_, ldx, ldh = 2, 3000, 6144, 6168, 3040
+    rng = np.random.default_rng(11)
+    xp, xpb = rand_bf16(rng, (M, ldx))
+    w, wb = rand_bf16(rng, (N, K_), 0.05)
+    hp, hpb = rand_bf16(rng, (M, ldh))
+    dx, dw, dh = dev(xpb), dev(wb), dev(hpb)
+    hai.check(kern().hai_gemm_bf16(dh.ptr, ldh, dx.ptr, ldx, dw.ptr, M, N, K_, hai.EPI_RESIDUAL, dh.ptr, ldh, None),
+              "gemm residual with pitch")
+    got = dh.download(np.uint16).reshape(M, ldh)
+    want = orc.add(hp[:, :N], orc.gemm(xp[:, :K_], w))
+    assert_bits_equal(got[:, :N], want, "gemm residual with pitch")
+    assert np.array_equal(got[:, N:], hpb.reshape(M, ldh)[:, N:])
 
 
 @pytest.mark.parametrize("M,F,K_", [(2, 768, 256), (1, 17408, 5120), (5, 96, 512), (1, 2000, 9000), (2, 300, 8192)])
@@ -123,7 +142,7 @@ def test_gemm_rejects_bad_shapes():
 
 @pytest.mark.parametrize("M,N,K_,epi", [(1, 4096, 256, 0), (2, 16480, 5120, 0), (2, 17408, 5120, 2),
                                         (3, 520, 5120, 1), (16, 300, 1024, 0), (2, 77, 1000, 0),
-                                        (4, 64, 5120, 0), (8, 512, 2048, 2)])
+                                        (4, 64, 5120, 0), (8, 512, 2048, 2), (2, 1030, 5120, 1)])
 @pytest.mark.parametrize("with_xn", [False, True])
 def test_gemm_rmsnorm_fused(M, N, K_, epi, with_xn):
     """hai_gemm_rmsnorm_bf16 == rmsnorm then gemm, on both sides of the fused

@@ -19,6 +19,7 @@
 //     SwiGLU product for interleaved gate/up rows.
 #include "hai_gemm_common.h"
 
+#include <atomic>
 #include <mutex>
 #include <type_traits>
 #include <vector>
@@ -30,7 +31,7 @@ using namespace hai;
 template <int MB, int RW, int U, int EPI, bool NORM>
 __global__ __launch_bounds__(256) void gemm_bf16_kernel(
     uint16_t* __restrict__ y, int64_t ldy, const uint16_t* __restrict__ x, int64_t ldx,
-    const uint16_t* __restrict__ w, const uint16_t* res, int64_t ldres, int M, int N, int K, NormArgs na) {
+    const uint16_t* w, const uint16_t* res, int64_t ldres, int M, int N, int K, NormArgs na) {
     const int lane = threadIdx.x & 63;
     const int wave = wave_index();
     extern __shared__ u32x4 xs[];  // NORM: [M][K/8] normalised rows, then the norm weight
@@ -70,22 +71,27 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(
         const bool pre_ok = grp0 < ngroups && row0 < N;
         if constexpr (kDmaStage) {
             stage_rows_lds_dma(xs, x, ldx, M, K, na.w);
+            pin_memory_order();
             __builtin_amdgcn_sched_barrier(0);  // the weight requests stay behind the copies
         }
-        if (pre_ok) {
+        // every wave issues the PG * U * RW requests (a wave without rows
+        // through out-of-range offsets, which read zeros), so that the wait
+        // below counts the same requests in every wave
 #pragma unroll
-            for (int u = 0; u < PG * U; ++u) {
-                const bool ok = u < nfull || (u < nck && u * 512 + lane * 8 < K);
-                const ChunkOffset co(u < nfull, ok, static_cast<uint32_t>(u) * 1024u);
+        for (int u = 0; u < PG * U; ++u) {
+            const bool ok = u < nfull || (u < nck && u * 512 + lane * 8 < K);
+            const ChunkOffset co(u < nfull && pre_ok, ok && pre_ok, static_cast<uint32_t>(u) * 1024u);
 #pragma unroll
-                for (int r = 0; r < RW; ++r)
-                    wpre[u][r] = bload_w(rw, co.v(static_cast<uint32_t>(((row0 + r) * static_cast<int64_t>(K) + lane * 8) * 2)), co.s);
-            }
+            for (int r = 0; r < RW; ++r)
+                wpre[u][r] = bload_w(rw,
+                                     co.v(pre_ok ? static_cast<uint32_t>(((row0 + r) * static_cast<int64_t>(K) + lane * 8) * 2)
+                                                 : kOutOfRange),
+                                     co.s);
         }
         if constexpr (kDmaStage) {
-            // wait for this wave's copies only: at most the PG * U * RW
-            // weight requests issued after them may still be in flight (a
-            // wave without rows issued none, and waits for its copies)
+            // wait for this wave's copies only: the PG * U * RW weight
+            // requests issued after them (pinned there) stay in flight
+            pin_memory_order();
             __builtin_amdgcn_sched_barrier(0);
             wait_vmcnt<PG * U * RW>();
             __builtin_amdgcn_sched_barrier(0);
@@ -382,6 +388,159 @@ __global__ __launch_bounds__(256) void gemm_bf16_ksplit_kernel(
     }
 }
 
+// Two-row variant for the short residual layers of the one-sequence verify
+// (out / o projection, K = 6144; down projection, K = 17408; N = 5120):
+// every wave streams RW whole rows over the full K (the canonical order of
+// gemm_bf16_kernel, bit-identical), and a block of WPB waves first copies
+// both activation rows to LDS with global -> LDS copies, so that the rows
+// are fetched once per block instead of once per wave (the K-split kernel
+// re-read them from L2 in every block: 180 MB of L2 reads per 178 MB of
+// down weights).  N / (WPB * RW) blocks make one balanced round on the
+// machine (5120 rows: 512 or 256 blocks, every wave with the same work).
+// As in the NORM prologue, PG groups of U weight chunks are requested behind
+// the copies and the wave waits for its copies alone.  Measured on MI355X at
+// M = 2: down 34.6 -> 31.3 us (WPB 10, U 2), out 14.3 -> 13.3 us (WPB 5,
+// U 4).  LDS: M * K * 2 bytes.
+template <int RW, int U, int WPB, int PG, int EPI>
+__global__ __launch_bounds__(64 * WPB) void gemm_bf16_staged_kernel(
+    uint16_t* __restrict__ y, int64_t ldy, const uint16_t* __restrict__ x, int64_t ldx,
+    const uint16_t* w, const uint16_t* res, int64_t ldres, int M, int N, int K) {
+    constexpr int MB = 2;
+    extern __shared__ u32x4 xs[];  // [M][K/8] activation rows
+    const int lane = threadIdx.x & 63;
+    const int wave = wave_index();
+    const int npr = K >> 3;
+    const int nck = (K + 511) / 512;
+    const int nfull = K / 512;
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, static_cast<uint32_t>(static_cast<int64_t>(N) * K * 2));
+    const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * WPB + wave) * RW;
+    const bool live = row0 < N;
+
+    // the copies: piece e = m * npr + p of the rows to xs[e]; each wave
+    // instruction writes 64 consecutive pieces at its wave-uniform base
+    const int total = M * npr;
+    for (int e0 = 0; e0 < total; e0 += 64 * WPB) {
+        const int e = e0 + static_cast<int>(threadIdx.x);
+        if (e < total) {
+            const int m = e / npr;
+            // (a C-style cast: the generic -> LDS address-space conversion)
+            __builtin_amdgcn_global_load_lds(x + m * ldx + (e - m * npr) * 8,
+                                             (__attribute__((address_space(3))) void*)(xs + e0 + wave * 64), 16,
+                                             0, 0);
+        }
+    }
+    pin_memory_order();
+    __builtin_amdgcn_sched_barrier(0);  // the weight requests stay behind the copies
+    uint32_t woff[RW];
+#pragma unroll
+    for (int r = 0; r < RW; ++r)
+        woff[r] = live ? static_cast<uint32_t>(((row0 + r) * static_cast<int64_t>(K) + lane * 8) * 2) : kOutOfRange;
+    u32x4 wpre[PG * U][RW];
+#pragma unroll
+    for (int u = 0; u < PG * U; ++u) {
+        const bool ok = u < nfull || (u < nck && u * 512 + lane * 8 < K);
+        const ChunkOffset co(u < nfull && live, ok && live, static_cast<uint32_t>(u) * 1024u);
+#pragma unroll
+        for (int r = 0; r < RW; ++r) wpre[u][r] = bload_w(rw, co.v(woff[r]), co.s);
+    }
+    // wait for this wave's copies only (the PG * U * RW weight requests
+    // issued after them, pinned there, stay in flight), then for every wave's
+    pin_memory_order();
+    __builtin_amdgcn_sched_barrier(0);
+    wait_vmcnt<PG * U * RW>();
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    if (!live) return;  // no barrier follows
+
+    float acc[RW][MB], tot[RW][MB];
+#pragma unroll
+    for (int r = 0; r < RW; ++r)
+#pragma unroll
+        for (int m = 0; m < MB; ++m) acc[r][m] = tot[r][m] = 0.0f;
+    // U chunks against the staged rows; a segment is four 512-element chunks
+    // (U divides 4): fold it into tot in order.  Chunks past K read zeros
+    // (weights through an out-of-range offset, rows masked here).
+    auto step = [&](int c0, const u32x4 (&wv)[U][RW]) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int c = c0 + u;
+            const bool ok = c < nfull || (c < nck && c * 512 + lane * 8 < K);
+            u32x4 xv[MB];
+#pragma unroll
+            for (int m = 0; m < MB; ++m) xv[m] = (ok && m < M) ? xs[m * npr + c * 64 + lane] : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                float xa[MB], xb[MB];
+#pragma unroll
+                for (int m = 0; m < MB; ++m) {
+                    xa[m] = lo_bf(xv[m][q]);
+                    xb[m] = hi_bf(xv[m][q]);
+                }
+#pragma unroll
+                for (int r = 0; r < RW; ++r) {
+                    const float wa = lo_bf(wv[u][r][q]);
+                    const float wb = hi_bf(wv[u][r][q]);
+#pragma unroll
+                    for (int m = 0; m < MB; ++m) {
+                        acc[r][m] = fma_(xa[m], wa, acc[r][m]);
+                        acc[r][m] = fma_(xb[m], wb, acc[r][m]);
+                    }
+                }
+            }
+        }
+        if (((c0 + U) & 3) == 0) {
+#pragma unroll
+            for (int r = 0; r < RW; ++r)
+#pragma unroll
+                for (int m = 0; m < MB; ++m) {
+                    tot[r][m] = tot[r][m] + acc[r][m];
+                    acc[r][m] = 0.0f;
+                }
+        }
+    };
+    int c0 = 0;
+#pragma unroll
+    for (int g = 0; g < PG; ++g) {
+        if (c0 < nck) {
+            u32x4 wv[U][RW];
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+#pragma unroll
+                for (int r = 0; r < RW; ++r) wv[u][r] = wpre[g * U + u][r];
+            step(c0, wv);
+        }
+        c0 += U;
+    }
+    for (; c0 < nck; c0 += U) {
+        u32x4 wv[U][RW];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int c = c0 + u;
+            const bool ok = c < nfull || (c < nck && c * 512 + lane * 8 < K);
+            const ChunkOffset co(c < nfull, ok, static_cast<uint32_t>(c) * 1024u);
+#pragma unroll
+            for (int r = 0; r < RW; ++r) wv[u][r] = bload_w(rw, co.v(woff[r]), co.s);
+        }
+        step(c0, wv);
+    }
+#pragma unroll
+    for (int r = 0; r < RW; ++r)
+#pragma unroll
+        for (int m = 0; m < MB; ++m) acc[r][m] = wave_sum64(tot[r][m] + acc[r][m]);
+#pragma unroll
+    for (int r = 0; r < RW; ++r)
+#pragma unroll
+        for (int m = 0; m < MB; ++m) {
+            if (lane == r * MB + m && m < M && row0 + r < N) {
+                const int64_t n = row0 + r;
+                float v = bfr(acc[r][m]);
+                if (EPI == HAI_EPI_RESIDUAL) v = bf2f(res[static_cast<int64_t>(m) * ldres + n]) + v;
+                y[static_cast<int64_t>(m) * ldy + n] = f2bf(v);
+            }
+        }
+}
+
 struct GemmArgs {
     uint16_t* y;
     int64_t ldy;
@@ -423,6 +582,41 @@ void launch_ksplit(const GemmArgs& a, hipStream_t s) {
         a.y, a.ldy, a.x, a.ldx, a.w, a.res, a.ldres, a.M, a.N, a.K);
 }
 
+// Two-row launches of the short layers (N <= 8192) with K from 2048 up to
+// 20480 (LDS of the two rows <= 80 KB, two blocks per CU): the staged kernel.
+// Narrower layers (N <= 1024) keep the K-split kernel, whose four waves per
+// row pair fill more of the machine.
+bool use_staged(const GemmArgs& a) {
+    return a.M == 2 && a.N > 1024 && a.N <= 8192 && a.K >= 2048 && a.K <= 20480;
+}
+
+template <int EPI>
+int launch_staged(const GemmArgs& a, hipStream_t s) {
+    // LDS above the 64 KB default needs the attribute: once per device and
+    // kernel instance
+    static std::atomic<uint8_t> allowed[2][64] = {};
+    auto go = [&](auto kern, int wpb, int rw, int variant) -> int {
+        const size_t shmem = static_cast<size_t>(a.M) * a.K * 2;
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return invalid("gemm: device index");
+        if (shmem > 64 * 1024 && !allowed[variant][dev].load(std::memory_order_acquire)) {
+            const int rc = check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                                         hipFuncAttributeMaxDynamicSharedMemorySize, 80 * 1024),
+                                     "hipFuncSetAttribute");
+            if (rc != HAI_OK) return rc;
+            allowed[variant][dev].store(1, std::memory_order_release);
+        }
+        const int64_t blocks = (static_cast<int64_t>(a.N) + wpb * rw - 1) / (wpb * rw);
+        kern<<<dim3(static_cast<unsigned>(blocks)), dim3(64 * wpb), shmem, s>>>(a.y, a.ldy, a.x, a.ldx, a.w, a.res,
+                                                                               a.ldres, a.M, a.N, a.K);
+        return HAI_OK;
+    };
+    // down-like K: ten waves, two chunks per group (one block per CU);
+    // out-like K: five waves, four chunks per group
+    if (a.K >= 8192) return go(gemm_bf16_staged_kernel<2, 2, 10, 2, EPI>, 10, 2, 0);
+    return go(gemm_bf16_staged_kernel<2, 4, 5, 2, EPI>, 5, 2, 1);
+}
+
 // Four waves per row pair, each on its own K segments, for the short,
 // wide-K layers where that measured faster on MI355X: M <= 2 with K >= 8192
 // (down projection, +3 % at M=2, +6 % at M=1), M = 1 with N <= 8192
@@ -437,11 +631,14 @@ bool use_ksplit(const GemmArgs& a) {
 }
 
 template <int EPI, bool NORM>
-void dispatch_mb(const GemmArgs& a, hipStream_t s) {
+int dispatch_mb(const GemmArgs& a, hipStream_t s) {
+    if constexpr (!NORM && EPI != HAI_EPI_SILU_MUL) {
+        if (use_staged(a)) return launch_staged<EPI>(a, s);
+    }
     if (!NORM && use_ksplit(a)) {
         if (a.M <= 1) launch_ksplit<1, EPI>(a, s);
         else launch_ksplit<2, EPI>(a, s);
-        return;
+        return HAI_OK;
     }
     // Two rows per wave keeps the register footprint small enough for eight
     // waves per SIMD, which is what keeps enough bytes in flight on gfx950
@@ -451,6 +648,7 @@ void dispatch_mb(const GemmArgs& a, hipStream_t s) {
     else if (a.M <= 4) launch_gemm<4, 2, EPI, NORM>(a, s);
     else if (a.M <= 8) launch_gemm<8, 2, EPI, NORM>(a, s);
     else launch_gemm<16, 2, EPI, NORM>(a, s);
+    return HAI_OK;
 }
 
 template <bool NORM>
@@ -458,15 +656,15 @@ int dispatch_epi(const GemmArgs& a, int epilogue, hipStream_t s) {
     switch (epilogue) {
         case HAI_EPI_STORE:
             if (a.ldy < a.N) return invalid("gemm: ldy < N");
-            dispatch_mb<HAI_EPI_STORE, NORM>(a, s);
+            if (const int rc = dispatch_mb<HAI_EPI_STORE, NORM>(a, s); rc != HAI_OK) return rc;
             break;
         case HAI_EPI_RESIDUAL:
             if (a.res == nullptr || a.ldy < a.N || a.ldres < a.N) return invalid("gemm: residual operands");
-            dispatch_mb<HAI_EPI_RESIDUAL, NORM>(a, s);
+            if (const int rc = dispatch_mb<HAI_EPI_RESIDUAL, NORM>(a, s); rc != HAI_OK) return rc;
             break;
         case HAI_EPI_SILU_MUL:
             if (a.N % 2 != 0 || a.ldy < a.N / 2) return invalid("gemm: silu_mul needs even N and ldy >= N/2");
-            dispatch_mb<HAI_EPI_SILU_MUL, NORM>(a, s);
+            if (const int rc = dispatch_mb<HAI_EPI_SILU_MUL, NORM>(a, s); rc != HAI_OK) return rc;
             break;
         default:
             return invalid("gemm: unknown epilogue");

@@ -122,6 +122,17 @@ __device__ __forceinline__ void stage_rows_lds_dma(u32x4* xs, const uint16_t* __
     }
 }
 
+// A compiler-only memory fence (no instruction): loads are neither hoisted
+// above nor sunk below it.  It brackets the weight requests that a wait for
+// the global -> LDS copies counts (s_waitcnt vmcnt(n) with n those requests):
+// without it the compiler may sink a request whose value is used only on a
+// conditional path below the wait, and the wait then no longer covers every
+// copy (seen on gfx950: 6 of 8 requests left above the wait).  The weight
+// pointer of such a kernel must not be __restrict__: loads through a
+// restrict-qualified read-only argument count as invariant, and the fence
+// does not hold them.
+__device__ __forceinline__ void pin_memory_order() { asm volatile("" ::: "memory"); }
+
 // s_waitcnt with vmcnt(n) and the other counters left alone (gfx9 encoding:
 // vmcnt bits [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8]).
 template <int N>
