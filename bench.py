@@ -228,6 +228,15 @@ def c2_ops(hai, reps: int = 50, cpu: bool = True) -> dict:
                                                              None), "deltanet verify"))
     fused_bytes = (1 + T) * nv * dk * dv * 4
     out["deltanet_verify_fused"] = {"us": round(us, 2), "bytes": fused_bytes, "gb_s": round(fused_bytes / us / 1e3, 1)}
+    # the same with each head's value columns over several blocks (the engine's path at one sequence)
+    wsb = k.hai_deltanet_workspace_bytes(1, nv, dv)
+    dws = hai.DeviceBuffer(wsb)
+    dws.zero()
+    us = timed(lambda: hai.check(k.hai_deltanet_verify_ws_bf16(dout2.ptr, vw, dproj.ptr, Nin, 0, C, C + vw, C + vw + nv,
+                                                                dcw.ptr, dring.ptr, ring, dslots.ptr, nslots, 1,
+                                                                zeros.ptr, zeros.ptr, dnw.ptr, None, 3, 1, T, nk, nv, dk,
+                                                                dv, 4, 1e-6, dws.ptr, wsb, None), "deltanet split"))
+    out["deltanet_verify_split"] = {"us": round(us, 2), "bytes": fused_bytes, "gb_s": round(fused_bytes / us / 1e3, 1)}
     if cpu:
         from oracle import oracle as orc  # cpu_baseline leg only
         f = lambda a: hai.bf16_to_f32(a).reshape(a.shape)

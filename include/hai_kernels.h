@@ -311,6 +311,31 @@ int hai_deltanet_verify_bf16(void* out, int64_t ld_out, const void* proj,
                              int32_t pos_add, int64_t B, int64_t T, int64_t nk,
                              int64_t nv, int64_t dk, int64_t dv, int64_t Kc,
                              float eps, void* stream);
+/* hai_deltanet_verify_bf16 (same arguments, same bits) with each head's
+ * value columns spread over several blocks (deltanet_recurrent_kernel,
+ * hip_kernels.hip:985-1095, updates the columns independently) when B * nv
+ * heads alone leave most CUs idle (fewer than 256).  The last block of a
+ * head finishes its gated norm behind device-scope fences; measured on
+ * MI355X this is slower than one block per head at the verify shapes (48
+ * heads, T = 2: 31.6 us against 10.0 us; 11.5 us even without the fences),
+ * so the engine does not use it.  The workspace
+ * holds one counter per (sequence, head) and the heads' unrounded outputs;
+ * it must be zeroed once before the first call (every call leaves the
+ * counters zero again) and hold hai_deltanet_workspace_bytes(B, nv, dv)
+ * bytes, 16-byte aligned.  Calls that overlap in time must not share a
+ * workspace. */
+size_t hai_deltanet_workspace_bytes(int64_t B, int64_t nv, int64_t dv);
+int hai_deltanet_verify_ws_bf16(void* out, int64_t ld_out, const void* proj,
+                                int64_t ld_proj, int64_t off_qkv, int64_t off_z,
+                                int64_t off_a, int64_t off_b, const void* conv_w,
+                                void* conv_ring, int64_t ring, float* state,
+                                int64_t nslots, int write_all_slots,
+                                const void* a_log, const void* dt_bias,
+                                const void* norm_w, const int32_t* lens,
+                                int32_t pos_add, int64_t B, int64_t T, int64_t nk,
+                                int64_t nv, int64_t dk, int64_t dv, int64_t Kc,
+                                float eps, void* workspace,
+                                int64_t workspace_bytes, void* stream);
 /* hai_deltanet_verify_bf16 with the a|b projection formed in the kernel
  * instead of read from proj: the in_proj_a / in_proj_b Linears of
  * qwen_reference.cc:205-258 (bf16 weights also when the model's other

@@ -6,8 +6,9 @@ chunks stay in flight.  The wait is only right when exactly n requests sit
 between the last copy and the wait in the code the compiler emits (a request
 sunk below the wait leaves copies unretired: a race on the staged rows).
 This test compiles hai_gemm.hip for gfx950 with the build's flags and checks
-that count in every kernel that stages by copies.  CPU only (hipcc
-cross-compiles)."""
+that count in every kernel that stages by copies, and that no later wait of
+the prologue (its LDS barriers) drains the requests it prefetched.  CPU only
+(hipcc cross-compiles)."""
 import re
 import shutil
 import subprocess
@@ -49,5 +50,12 @@ def test_staged_copy_waits_count_the_requests_behind_them(tmp_path):
         issued = sum(1 for k in range(last + 1, wait) if "buffer_load" in body[k] or
                      ("global_load" in body[k] and "lds" not in body[k]))
         assert issued == n, f"{name}: {issued} requests between the copies and s_waitcnt vmcnt({n})"
+        # the prologue's block barriers (LDS data only) must not wait for the
+        # prefetched requests: the next vector-memory wait still leaves some
+        # of them in flight
+        nxt = next((k for k in range(wait + 1, len(body)) if "s_waitcnt" in body[k] and "vmcnt(" in body[k]), None)
+        if nxt is not None:
+            m = int(re.search(r"vmcnt\((\d+)\)", body[nxt]).group(1))
+            assert m > 0, f"{name}: the prologue waits for every prefetched request ({body[nxt].strip()})"
         checked += 1
     assert checked >= 4, f"only {checked} staging kernels found"

@@ -452,12 +452,15 @@ def _to_tiled(state, nv, dk, dv):
     return np.ascontiguousarray(t).reshape(nv, dv, dk)
 
 
+@pytest.mark.parametrize("split", [False, True], ids=["one_block", "column_split"])
 @pytest.mark.parametrize("nk,nv,dk,dv,steps", [(4, 4, 64, 64, [2, 1, 3]), (16, 48, 128, 128, [4, 2]),
                                                (2, 6, 64, 64, [16, 1])])
-def test_deltanet_verify_rollback(nk, nv, dk, dv, steps):
+def test_deltanet_verify_rollback(nk, nv, dk, dv, steps, split):
     """Chained verify steps with partial acceptance: the kernel's committed
     state/conv ring after each accepted prefix must equal the oracle's
-    sequential processing of the accepted tokens only."""
+    sequential processing of the accepted tokens only.  column_split: the
+    workspace entry point (each head's value columns over 4 blocks at these
+    head counts)."""
     rng = np.random.default_rng(nk * 1000 + nv + dk)
     B = 1
     c = _deltanet_case(rng, B, nk, nv, dk, dv)
@@ -472,14 +475,18 @@ def test_deltanet_verify_rollback(nk, nv, dk, dv, steps):
     state = np.zeros((nv, dk, dv), np.float32)
     L = 0
     lens = dev(np.array([0], np.int32))
+    wsb = kern().hai_deltanet_workspace_bytes(B, nv, dv)
+    dws = out_buf(wsb)
     for si, T in enumerate(steps):
         proj, pb = rand_bf16(rng, (T, width))
         dproj, dout = dev(pb), out_buf(T * vw * 2)
         lens.upload(np.array([L], np.int32))
-        hai.check(kern().hai_deltanet_verify_bf16(dout.ptr, vw, dproj.ptr, width, 0, C, C + vw, C + vw + nv,
-                                                  dcw.ptr, dring.ptr, ring, dstate.ptr, nslots, 1, dal.ptr, ddt.ptr,
-                                                  dnw.ptr, lens.ptr, 0, B, T, nk, nv, dk, dv, Kc, 1e-6, None),
-                  "deltanet")
+        args = (dout.ptr, vw, dproj.ptr, width, 0, C, C + vw, C + vw + nv, dcw.ptr, dring.ptr, ring, dstate.ptr,
+                nslots, 1, dal.ptr, ddt.ptr, dnw.ptr, lens.ptr, 0, B, T, nk, nv, dk, dv, Kc, 1e-6)
+        if split:
+            hai.check(kern().hai_deltanet_verify_ws_bf16(*args, dws.ptr, wsb, None), "deltanet split")
+        else:
+            hai.check(kern().hai_deltanet_verify_bf16(*args, None), "deltanet")
         got = dout.download(np.uint16).reshape(T, vw)
         # oracle over all T tokens from the committed state
         q, k, v, cs_all = orc.deltanet_conv(proj[:, :C], c["conv_w"], conv_state, T, nk, nv, dk, dv, Kc)
@@ -498,6 +505,57 @@ def test_deltanet_verify_rollback(nk, nv, dk, dv, steps):
         dev_state = dstate.download(np.float32).reshape(nslots, B, nv, dv, dk)[slot, 0]
         want_state = _to_tiled(state, nv, dk, dv)
         assert np.array_equal(dev_state.view(np.uint32), want_state.view(np.uint32)), f"state after step {si}"
+
+
+@pytest.mark.parametrize("B,nk,nv,dk,T,Kc", [(1, 16, 48, 128, 2, 4), (3, 16, 48, 128, 4, 4), (2, 2, 6, 64, 16, 3),
+                                             (1, 16, 48, 128, 17, 4)])
+def test_deltanet_column_split_matches_one_block(B, nk, nv, dk, T, Kc):
+    """The workspace entry point (value columns of a head over 4 blocks at
+    48 heads, over 2 at 144) against the one-block kernel, bit for bit: the
+    outputs, every state slot written, the conv ring, and the workspace
+    counters back at zero.  Two launches in a row (the second from the state
+    the first left), T = 17 as the two launches of a width-16 verify."""
+    rng = np.random.default_rng(B * 100 + nv + T)
+    dv = dk
+    kw, vw = nk * dk, nv * dv
+    C = 2 * kw + vw
+    width = C + vw + 2 * nv
+    ring, nslots = 40, 18
+    cw, cwb = rand_bf16(rng, (C, Kc), 0.3)
+    al, alb = rand_bf16(rng, (nv,), 0.5)
+    dt, dtb = rand_bf16(rng, (nv,), 0.5)
+    nw, nwb = rand_bf16(rng, (dv,), 0.5)
+    st0 = (rng.standard_normal(nslots * B * nv * dk * dv) * 0.1).astype(np.float32)
+    rg0 = hai.bf16_bits(rng.standard_normal(B * ring * C).astype(np.float32))
+    lens0 = np.array([5 + 3 * b for b in range(B)], np.int32)
+    proj, pb = rand_bf16(rng, (B * T, width))
+    wsb = kern().hai_deltanet_workspace_bytes(B, nv, dv)
+    results = []
+    for split in (False, True):
+        dstate, dring, dws = dev(st0), dev(rg0), out_buf(wsb)
+        dcw, dal, ddt, dnw, dproj, lens = dev(cwb), dev(alb), dev(dtb), dev(nwb), dev(pb), dev(lens0)
+        dout = out_buf(B * T * vw * 2)
+        for t0 in range(0, T, 16):
+            n = min(16, T - t0)
+            # rows of launch t0: the projection rows t0.. of every sequence
+            sub = np.ascontiguousarray(pb.reshape(B, T, width)[:, t0:t0 + n].reshape(B * n, width))
+            dsub, dsout = dev(sub), out_buf(B * n * vw * 2)
+            args = (dsout.ptr, vw, dsub.ptr, width, 0, C, C + vw, C + vw + nv, dcw.ptr, dring.ptr, ring, dstate.ptr,
+                    nslots, 1, dal.ptr, ddt.ptr, dnw.ptr, lens.ptr, t0, B, n, nk, nv, dk, dv, Kc, 1e-6)
+            if split:
+                hai.check(kern().hai_deltanet_verify_ws_bf16(*args, dws.ptr, wsb, None), "deltanet split")
+            else:
+                hai.check(kern().hai_deltanet_verify_bf16(*args, None), "deltanet")
+            results.append((split, t0, dsout.download(np.uint16)))
+        results.append((split, "state", dstate.download(np.uint32)))
+        results.append((split, "ring", dring.download(np.uint16)))
+        if split:
+            counters = dws.download(np.uint32)[: B * nv]
+            assert not counters.any(), "workspace counters not reset"
+    half = len(results) // 2
+    for (s0, k0, a), (s1, k1, b) in zip(results[:half], results[half:]):
+        assert k0 == k1 and not s0 and s1
+        assert np.array_equal(a, b), f"column split differs from one block: {k0}"
 
 
 # ----------------------------------------------------------------- argmax / accept

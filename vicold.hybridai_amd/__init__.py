@@ -90,6 +90,8 @@ _KERNEL_SIGS = {
     "hai_gqa_verify_noalloc_bf16": [VP, VP, VP, VP, VP, I64, I64, I64, I64, I64, I64, VP, I32, I64, VP],
     "hai_deltanet_verify_bf16": [VP, I64, VP, I64, I64, I64, I64, I64, VP, VP, I64, VP, I64, ctypes.c_int, VP, VP,
                                  VP, VP, I32, I64, I64, I64, I64, I64, I64, I64, F32, VP],
+    "hai_deltanet_verify_ws_bf16": [VP, I64, VP, I64, I64, I64, I64, I64, VP, VP, I64, VP, I64, ctypes.c_int, VP,
+                                    VP, VP, VP, I32, I64, I64, I64, I64, I64, I64, I64, F32, VP, I64, VP],
     "hai_deltanet_verify_ab_bf16": [VP, I64, VP, I64, I64, I64, VP, I64, VP, I64, VP, VP, I64, VP, I64, ctypes.c_int,
                                     VP, VP, VP, VP, I32, I64, I64, I64, I64, I64, I64, I64, F32, VP],
     "hai_argmax_rows_bf16": [VP, VP, I64, I64, I64, VP, VP],
@@ -112,6 +114,7 @@ _SIZE_SIGS = {
     "hai_gqa_scratch_bytes": [I64, I64, I64, I64, I64],
     "hai_gqa_mfma_scratch_bytes": [I64, I64, I64, I64, I64],
     "hai_argmax_scratch_bytes": [I64, I64],
+    "hai_deltanet_workspace_bytes": [I64, I64, I64],
 }
 
 _kern = None

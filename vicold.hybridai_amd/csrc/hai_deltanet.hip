@@ -401,6 +401,282 @@ __global__ __launch_bounds__(DV * 4) void deltanet_kernel(DnArgs A) {
     }
 }
 
+// Column-split fused verify (no a|b dots): CS blocks per (value head,
+// sequence), block cs owning value columns [cs*DV/CS, (cs+1)*DV/CS).  The
+// columns of the delta rule are independent (hip_kernels.hip:1055-1075), so
+// each block runs the recurrence of its columns exactly as deltanet_kernel
+// does (4 threads per column, the same fma chains and xor butterflies); the
+// per-head work (conv of the q/k channels, q/k norms, gates) is repeated in
+// every block.  Only the gated RMSNorm needs the whole head: every block
+// stores its unrounded outputs in the workspace and counts itself in the
+// head's counter (a device-scope atomic behind a device-scope fence); the
+// block that arrives last reads the head's outputs back and finishes the
+// norm in deltanet_kernel's order, so the result is bit-identical.  No block
+// waits for another, and the last one resets the counter for the next launch.
+// A head's state and conv traffic is then spread over CS CUs (one block per
+// head used 48 of 256 CUs at B = 1).
+template <int DK, int DV, int CS>
+__global__ __launch_bounds__(DV / CS * 4 > 256 ? DV / CS * 4 : 256) void deltanet_cols_kernel(
+    DnArgs A, float* __restrict__ o_ws, uint32_t* __restrict__ counters) {
+    constexpr int DC = DV / CS;                 // value columns of this block
+    constexpr int RT = DC * 4;                  // recurrence threads (4 per column)
+    constexpr int NT = RT > 256 ? RT : 256;
+    constexpr int NW = NT / 64;
+    constexpr int GI = DK / 4;
+    constexpr int NCH = 2 * DK + DC;            // conv channels: q, k, the block's v columns
+    constexpr int CPT = (NCH + NT - 1) / NT;    // channels per thread
+    constexpr int ZP = (kMaxT * DV + NT - 1) / NT;  // finishing block: outputs per thread
+    const int T = A.T;
+    extern __shared__ __align__(16) float smem[];
+    float* qs = smem;              // [T][DK] q (then q * q-norm scale)
+    float* ks = qs + T * DK;       // [T][DK] k (then k * k-norm scale)
+    float* bks = ks + T * DK;      // [T][DK] beta * normalised k
+    float* vs = bks + T * DK;      // [T][DC] v of the block's columns
+    float* os = vs + T * DC;       // [T][DV] the head's unrounded outputs (finishing block)
+    __shared__ float s_q[kMaxT], s_k[kMaxT], s_decay[kMaxT], s_beta[kMaxT], s_rms[kMaxT];
+    __shared__ uint32_t s_last;
+
+    const int h = blockIdx.x;
+    const int b = blockIdx.y;
+    const int j0 = static_cast<int>(blockIdx.z) * DC;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int jl = tid >> 2;  // recurrence: column j0 + jl, key quarter g
+    const int g = tid & 3;
+    const bool rec = tid < RT;
+    const int nv = A.nv;
+    const int group = nv / A.nk;
+    const int gq = h / group;
+    const int64_t kw = static_cast<int64_t>(A.nk) * DK;
+    const int64_t vw = static_cast<int64_t>(nv) * DV;
+    const int64_t C = 2 * kw + vw;
+    const int hist = A.Kc - 1;
+    const int64_t row0 = static_cast<int64_t>(b) * T;
+    const int64_t head = static_cast<int64_t>(b) * nv + h;
+
+    // ---- loads that do not depend on the cache length ----
+    uint16_t vals[CPT][kMaxT + kMaxKc - 1];  // input at position p0 - hist + i
+    float wc[CPT][kMaxKc];
+    int64_t chan[CPT];
+#pragma unroll
+    for (int ci = 0; ci < CPT; ++ci) {
+        const int cl = tid + NT * ci;
+#pragma unroll
+        for (int i = 0; i < kMaxT + kMaxKc - 1; ++i) vals[ci][i] = 0;
+        if (cl < DK) chan[ci] = static_cast<int64_t>(gq) * DK + cl;
+        else if (cl < 2 * DK) chan[ci] = kw + static_cast<int64_t>(gq) * DK + (cl - DK);
+        else chan[ci] = 2 * kw + static_cast<int64_t>(h) * DV + j0 + (cl - 2 * DK);
+        if (cl < NCH) {
+#pragma unroll
+            for (int i = 0; i < kMaxKc; ++i) wc[ci][i] = i < A.Kc ? bf2f(A.conv_w[chan[ci] * A.Kc + i]) : 0.0f;
+#pragma unroll
+            for (int t = 0; t < kMaxT; ++t) {
+                uint16_t x = 0;
+                if (t < T) x = A.proj[(row0 + t) * A.ld_proj + A.off_qkv + chan[ci]];
+#pragma unroll
+                for (int hh = 0; hh < kMaxKc; ++hh)
+                    if (hh == hist) vals[ci][t + hh] = x;
+            }
+        }
+    }
+    float a_in = 0.0f, b_in = 0.0f, dtb = 0.0f, alog = 0.0f;
+    const bool scal = wave == NW - 1 && lane < T;
+    if (scal) {
+        a_in = bf2f(A.proj[(row0 + lane) * A.ld_proj + A.off_a + h]);
+        b_in = bf2f(A.proj[(row0 + lane) * A.ld_proj + A.off_b + h]);
+        dtb = bf2f(A.dt_bias[h]);
+        alog = bf2f(A.a_log[h]);
+    }
+    // gate z and norm weight of the outputs this thread writes if its block
+    // finishes the head: element e = tid + r * NT of [T][DV]
+    float zr[ZP], nwr[ZP];
+#pragma unroll
+    for (int r = 0; r < ZP; ++r) {
+        const int e = tid + r * NT;
+        const int t = e / DV;
+        const int jo = e - t * DV;
+        zr[r] = t < T ? bf2f(A.proj[(row0 + t) * A.ld_proj + A.off_z + static_cast<int64_t>(h) * DV + jo]) : 0.0f;
+        nwr[r] = t < T ? bf2f(A.norm_w[jo]) : 0.0f;
+    }
+
+    // ---- the length-dependent ones: state slot (this block's columns) and
+    // conv history ----
+    const int64_t p0 = static_cast<int64_t>(A.lens ? A.lens[b] : 0) + A.pos_add;
+    const int64_t slot = p0 % A.nslots;
+    int64_t slot_w = slot + 1 == A.nslots ? 0 : slot + 1;
+    float S[GI];
+    if (rec) {
+        // column-tiled head: float4 number m * 4 * DV + 4 * j + g holds keys
+        // g * GI + 4m .. + 3 of column j
+        const float4* src =
+            reinterpret_cast<const float4*>(A.state + ((slot * A.B + b) * nv + h) * static_cast<int64_t>(DV) * DK) +
+            4 * j0 + tid;
+#pragma unroll
+        for (int m = 0; m < GI / 4; ++m) {
+            const float4 v4 = src[m * 4 * DV];
+            S[4 * m] = v4.x; S[4 * m + 1] = v4.y; S[4 * m + 2] = v4.z; S[4 * m + 3] = v4.w;
+        }
+    }
+    const int64_t base = p0 - hist;
+    int64_t rp0 = base % A.ring_n;
+    if (rp0 < 0) rp0 += A.ring_n;
+    int64_t ring_w = rp0;  // ring entry of position p0
+#pragma unroll
+    for (int i = 0; i < kMaxKc - 1; ++i)
+        if (i < hist) ring_w = ring_w + 1 == A.ring_n ? 0 : ring_w + 1;
+#pragma unroll
+    for (int ci = 0; ci < CPT; ++ci) {
+        if (tid + NT * ci < NCH) {
+            int64_t rp = rp0;
+#pragma unroll
+            for (int i = 0; i < kMaxKc - 1; ++i) {
+                if (i < hist) {
+                    if (base + i >= 0) vals[ci][i] = A.ring[(static_cast<int64_t>(b) * A.ring_n + rp) * C + chan[ci]];
+                    rp = rp + 1 == A.ring_n ? 0 : rp + 1;
+                }
+            }
+        }
+    }
+
+    // ---- grouped causal conv + SiLU; new inputs into the ring (q/k channels
+    // by the first block of the head group's first head) ----
+#pragma unroll
+    for (int ci = 0; ci < CPT; ++ci) {
+        const int cl = tid + NT * ci;
+        if (cl < NCH) {
+            float* dst = qs;
+            int di = cl, dstride = DK;
+            if (cl >= DK && cl < 2 * DK) { dst = ks; di = cl - DK; }
+            else if (cl >= 2 * DK) { dst = vs; di = cl - 2 * DK; dstride = DC; }
+            const bool writer = cl >= 2 * DK || ((h % group) == 0 && j0 == 0);
+            int64_t rw = ring_w;
+#pragma unroll
+            for (int t = 0; t < kMaxT; ++t) {
+                if (t < T) {
+                    float acc = bf2f(vals[ci][t]) * wc[ci][0];
+#pragma unroll
+                    for (int i = 1; i < kMaxKc; ++i)
+                        if (i < A.Kc) acc = fma_(bf2f(vals[ci][t + i]), wc[ci][i], acc);
+                    dst[t * dstride + di] = bfr(csilu(acc));
+                    if (writer) {
+                        uint16_t xv = 0;
+#pragma unroll
+                        for (int hh = 0; hh < kMaxKc; ++hh)
+                            if (hh == hist) xv = vals[ci][t + hh];
+                        A.ring[(static_cast<int64_t>(b) * A.ring_n + rw) * C + chan[ci]] = xv;
+                    }
+                    rw = rw + 1 == A.ring_n ? 0 : rw + 1;
+                }
+            }
+        }
+    }
+    if (scal) {
+        const float dtv = dtb + a_in;
+        const float sp = fmaxf(dtv, 0.0f) + clog1p(cexp(-fabsf(dtv)));
+        s_decay[lane] = cexp(-(cexp(alog) * sp));
+        s_beta[lane] = csigmoid(b_in);
+    }
+    __syncthreads();
+
+    // ---- q / k L2 norms, then the scaled q, k and beta * k ----
+    const float rs_dk = 1.0f / csqrt(static_cast<float>(DK));
+    for (int task = wave; task < 2 * T; task += NW) {
+        const int t = task >> 1;
+        if ((task & 1) == 0) {
+            const float ssq = l64_sumsq_f32(qs + t * DK, DK, lane);
+            if (lane == 0) s_q[t] = (1.0f / csqrt(ssq + 1.0e-6f)) * rs_dk;
+        } else {
+            const float ssk = l64_sumsq_f32(ks + t * DK, DK, lane);
+            if (lane == 0) s_k[t] = 1.0f / csqrt(ssk + 1.0e-6f);
+        }
+    }
+    __syncthreads();
+    for (int e = tid; e < T * DK; e += NT) {
+        const int t = e / DK;
+        qs[e] = qs[e] * s_q[t];
+        const float kh = ks[e] * s_k[t];
+        ks[e] = kh;
+        bks[e] = s_beta[t] * kh;
+    }
+    __syncthreads();
+
+    // ---- gated delta rule of the block's columns ----
+    float* ow = o_ws + head * kMaxT * DV;
+    if (rec) {
+        for (int t = 0; t < T; ++t) {
+            const float decay = s_decay[t];
+            const float4* qt = reinterpret_cast<const float4*>(qs + t * DK + g * GI);
+            const float4* kt = reinterpret_cast<const float4*>(ks + t * DK + g * GI);
+            const float4* bt = reinterpret_cast<const float4*>(bks + t * DK + g * GI);
+            float r = 0.0f;
+#pragma unroll
+            for (int m = 0; m < GI / 4; ++m) {
+                const float4 k4 = kt[m];
+                const float kv[4] = {k4.x, k4.y, k4.z, k4.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    S[4 * m + e] = S[4 * m + e] * decay;
+                    r = fma_(kv[e], S[4 * m + e], r);
+                }
+            }
+            r = r + quad_xor1(r);
+            r = r + quad_xor2(r);
+            const float cj = vs[t * DC + jl] - r;
+            float o = 0.0f;
+#pragma unroll
+            for (int m = 0; m < GI / 4; ++m) {
+                const float4 b4 = bt[m], q4 = qt[m];
+                const float bv[4] = {b4.x, b4.y, b4.z, b4.w}, qv[4] = {q4.x, q4.y, q4.z, q4.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    S[4 * m + e] = fma_(bv[e], cj, S[4 * m + e]);
+                    o = fma_(qv[e], S[4 * m + e], o);
+                }
+            }
+            o = o + quad_xor1(o);
+            o = o + quad_xor2(o);
+            if (A.write_all || t == T - 1) {
+                float4* dstp = reinterpret_cast<float4*>(A.state + ((slot_w * A.B + b) * nv + h) *
+                                                                       static_cast<int64_t>(DV) * DK) +
+                               4 * j0 + tid;
+#pragma unroll
+                for (int m = 0; m < GI / 4; ++m)
+                    dstp[m * 4 * DV] = make_float4(S[4 * m], S[4 * m + 1], S[4 * m + 2], S[4 * m + 3]);
+            }
+            slot_w = slot_w + 1 == A.nslots ? 0 : slot_w + 1;
+            if (g == 0) ow[t * DV + j0 + jl] = o;
+        }
+    }
+
+    // ---- completion: the last block of the head finishes the gated norm ----
+    __threadfence();  // this block's outputs are visible device-wide before it counts itself
+    __syncthreads();
+    if (tid == 0) s_last = atomicAdd(counters + head, 1u) == static_cast<uint32_t>(CS - 1) ? 1u : 0u;
+    __syncthreads();
+    if (s_last == 0u) return;
+    __threadfence();  // and read only after every block has counted itself
+    if (tid == 0) atomicExch(counters + head, 0u);
+    for (int e = tid; e < T * DV; e += NT) os[e] = ow[e];
+    __syncthreads();
+    for (int t = wave; t < T; t += NW) {
+        const float sso = l64_sumsq_f32(os + t * DV, DV, lane);
+        if (lane == 0) s_rms[t] = 1.0f / csqrt(sso / static_cast<float>(DV) + A.eps);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < ZP; ++r) {
+        const int e = tid + r * NT;
+        const int t = e / DV;
+        if (t < T) {
+            const int jo = e - t * DV;
+            const float ob = bfr(os[e]);
+            A.out[(row0 + t) * A.ld_out + static_cast<int64_t>(h) * DV + jo] =
+                f2bf(((ob * s_rms[t]) * nwr[r]) * csilu(zr[r]));
+        }
+    }
+}
+
 // deltanet_grouped_conv_kernel (hip_kernels.hip:871-912) over the reference's
 // conv state [C][Kc-1] (oldest first): one thread per flat [Q|K|V] channel,
 // the canonical conv order of the fused kernel, state shifted in place.
@@ -460,6 +736,35 @@ int launch(const DnArgs& a, hipStream_t s) {
     return launched(REF ? "deltanet_recurrent_kernel" : "deltanet_verify_kernel");
 }
 
+// Workspace of the column-split kernel: one counter per (sequence, head),
+// then the heads' unrounded outputs [B][nv][16][dv] fp32.
+int64_t counters_bytes(int64_t B, int64_t nv) { return (B * nv * 4 + 255) / 256 * 256; }
+int64_t cols_workspace_bytes(int64_t B, int64_t nv, int64_t dv) {
+    return counters_bytes(B, nv) + B * nv * kMaxT * dv * 4;
+}
+
+template <int DK, int DV, int CS>
+int launch_cols(const DnArgs& a, void* ws, hipStream_t s) {
+    constexpr int DC = DV / CS;
+    constexpr int NT = DC * 4 > 256 ? DC * 4 : 256;
+    const size_t shmem = static_cast<size_t>(a.T) * (3 * DK + DC + DV) * sizeof(float);
+    auto* counters = static_cast<uint32_t*>(ws);
+    auto* o_ws = reinterpret_cast<float*>(static_cast<char*>(ws) + counters_bytes(a.B, a.nv));
+    deltanet_cols_kernel<DK, DV, CS><<<dim3(a.nv, a.B, CS), dim3(NT), shmem, s>>>(a, o_ws, counters);
+    return launched("deltanet_cols_kernel");
+}
+
+// Column blocks per head: enough blocks for the machine at small batches
+// (B * nv heads, 256 CUs); one block per head once the heads alone fill it.
+int column_splits(int64_t heads) { return heads < 128 ? 4 : (heads < 256 ? 2 : 1); }
+
+int dispatch_cols(const DnArgs& a, int64_t dk, int64_t dv, void* ws, hipStream_t s) {
+    const int cs = column_splits(static_cast<int64_t>(a.B) * a.nv);
+    if (dk == 128 && dv == 128) return cs == 4 ? launch_cols<128, 128, 4>(a, ws, s) : launch_cols<128, 128, 2>(a, ws, s);
+    if (dk == 64 && dv == 64) return cs == 4 ? launch_cols<64, 64, 4>(a, ws, s) : launch_cols<64, 64, 2>(a, ws, s);
+    return invalid("deltanet: (dk, dv) must be (128,128) or (64,64)");
+}
+
 template <bool REF>
 int dispatch(const DnArgs& a, int64_t dk, int64_t dv, hipStream_t s) {
     if (dk == 128 && dv == 128) return launch<128, 128, REF>(a, s);
@@ -475,7 +780,8 @@ int verify(void* out, int64_t ld_out, const void* proj, int64_t ld_proj, int64_t
            int64_t off_a, int64_t off_b, const void* conv_w, void* conv_ring, int64_t ring, float* state,
            int64_t nslots, int write_all_slots, const void* a_log, const void* dt_bias, const void* norm_w,
            const int32_t* lens, int32_t pos_add, int64_t B, int64_t T, int64_t nk, int64_t nv, int64_t dk, int64_t dv,
-           int64_t Kc, float eps, const void* xn, int64_t ld_xn, const void* w_ab, int64_t H, void* stream) {
+           int64_t Kc, float eps, const void* xn, int64_t ld_xn, const void* w_ab, int64_t H, void* ws,
+           int64_t ws_bytes, void* stream) {
     if (out == nullptr || proj == nullptr || conv_w == nullptr || conv_ring == nullptr || state == nullptr ||
         a_log == nullptr || dt_bias == nullptr || norm_w == nullptr)
         return invalid("deltanet_verify: null pointer");
@@ -523,6 +829,12 @@ int verify(void* out, int64_t ld_out, const void* proj, int64_t ld_proj, int64_t
     a.ld_xn = ld_xn;
     a.w_ab = static_cast<const uint16_t*>(w_ab);
     a.H = w_ab != nullptr ? int(H) : 0;
+    if (ws != nullptr) {
+        if (ws_bytes < cols_workspace_bytes(B, nv, dv) || !aligned16(ws))
+            return invalid("deltanet_verify_ws: workspace smaller than hai_deltanet_workspace_bytes(B, nv, dv) or "
+                           "not 16-byte aligned");
+        if (w_ab == nullptr && column_splits(B * nv) > 1) return dispatch_cols(a, dk, dv, ws, as_stream(stream));
+    }
     return dispatch<false>(a, dk, dv, as_stream(stream));
 }
 
@@ -537,7 +849,29 @@ extern "C" int hai_deltanet_verify_bf16(void* out, int64_t ld_out, const void* p
                                         int64_t dk, int64_t dv, int64_t Kc, float eps, void* stream) {
     return verify(out, ld_out, proj, ld_proj, off_qkv, off_z, off_a, off_b, conv_w, conv_ring, ring, state, nslots,
                   write_all_slots, a_log, dt_bias, norm_w, lens, pos_add, B, T, nk, nv, dk, dv, Kc, eps, nullptr, 0,
-                  nullptr, 0, stream);
+                  nullptr, 0, nullptr, 0, stream);
+}
+
+extern "C" size_t hai_deltanet_workspace_bytes(int64_t B, int64_t nv, int64_t dv) {
+    if (B < 0 || nv < 0 || dv < 0) return 0;
+    return static_cast<size_t>(cols_workspace_bytes(B, nv, dv));
+}
+
+extern "C" int hai_deltanet_verify_ws_bf16(void* out, int64_t ld_out, const void* proj, int64_t ld_proj,
+                                           int64_t off_qkv, int64_t off_z, int64_t off_a, int64_t off_b,
+                                           const void* conv_w, void* conv_ring, int64_t ring, float* state,
+                                           int64_t nslots, int write_all_slots, const void* a_log,
+                                           const void* dt_bias, const void* norm_w, const int32_t* lens,
+                                           int32_t pos_add, int64_t B, int64_t T, int64_t nk, int64_t nv,
+                                           int64_t dk, int64_t dv, int64_t Kc, float eps, void* workspace,
+                                           int64_t workspace_bytes, void* stream) {
+    if (workspace == nullptr) return invalid("deltanet_verify_ws: null workspace");
+    if (workspace_bytes < 0) return invalid("deltanet_verify_ws: negative workspace size");
+    if (const int rc = check_extent(workspace, static_cast<size_t>(workspace_bytes), "deltanet workspace"); rc != HAI_OK)
+        return rc;
+    return verify(out, ld_out, proj, ld_proj, off_qkv, off_z, off_a, off_b, conv_w, conv_ring, ring, state, nslots,
+                  write_all_slots, a_log, dt_bias, norm_w, lens, pos_add, B, T, nk, nv, dk, dv, Kc, eps, nullptr, 0,
+                  nullptr, 0, workspace, workspace_bytes, stream);
 }
 
 extern "C" int hai_deltanet_verify_ab_bf16(void* out, int64_t ld_out, const void* proj, int64_t ld_proj,
@@ -551,7 +885,7 @@ extern "C" int hai_deltanet_verify_ab_bf16(void* out, int64_t ld_out, const void
     if (w_ab == nullptr) return invalid("deltanet_verify_ab: null w_ab");
     return verify(out, ld_out, proj, ld_proj, off_qkv, off_z, 0, 0, conv_w, conv_ring, ring, state, nslots,
                   write_all_slots, a_log, dt_bias, norm_w, lens, pos_add, B, T, nk, nv, dk, dv, Kc, eps, xn, ld_xn,
-                  w_ab, H, stream);
+                  w_ab, H, nullptr, 0, stream);
 }
 
 extern "C" int hai_deltanet_conv_bf16(void* q, void* k, void* v, void* conv_state, const void* qkv,

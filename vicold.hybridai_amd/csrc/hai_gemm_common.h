@@ -21,10 +21,40 @@ struct NormArgs {
 
 constexpr int kNormMaxElems = HAI_GEMM_RMSNORM_FUSED_MAX;  // M * K: 32 KB of LDS
 
+// A compiler-only memory fence (no instruction): loads are neither hoisted
+// above nor sunk below it.  It brackets the weight requests that a wait for
+// the global -> LDS copies counts (s_waitcnt vmcnt(n) with n those requests):
+// without it the compiler may sink a request whose value is used only on a
+// conditional path below the wait, and the wait then no longer covers every
+// copy (seen on gfx950: 6 of 8 requests left above the wait).  The weight
+// pointer of such a kernel must not be __restrict__: loads through a
+// restrict-qualified read-only argument count as invariant, and the fence
+// does not hold them.
+__device__ __forceinline__ void pin_memory_order() { asm volatile("" ::: "memory"); }
+
+// Block barrier for LDS data with global loads left in flight: this wave's
+// LDS accesses complete (lgkmcnt(0)) and stay on their side of the barrier
+// (compiler fence), vmcnt is not waited for.  __syncthreads() carries a
+// workgroup release fence, which the compiler lowers to s_waitcnt vmcnt(0)
+// once the kernel has issued global -> LDS copies (it cannot tell them from
+// the weight requests behind them), so every block would wait for its
+// prefetched weight chunks there (measured on MI355X: 3.6 - 7.5 us of a
+// fused-norm launch's prologue).  Only for LDS data written by ds
+// instructions or by copies already retired.
+__device__ __forceinline__ void lds_barrier() {
+    pin_memory_order();
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt(63) and expcnt(7): no wait
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    pin_memory_order();
+}
+
 // The normalisation step of the prologue: the M raw rows are staged in xs
 // as 16-byte pieces [M][K/8] with the norm weight behind them (visible to
 // the whole block), one wave per row reduces the sum of squares in L64
-// order, then every element is scaled in place; ends with a block barrier.
+// order, then every element is scaled in place; ends with a block barrier
+// (lds_barrier: weight requests issued before stay in flight).
 __device__ __forceinline__ void normalize_staged_rows(u32x4* xs, int M, int K, const NormArgs& na) {
     __shared__ float inv_sh[16];
     const int lane = threadIdx.x & 63;
@@ -46,7 +76,7 @@ __device__ __forceinline__ void normalize_staged_rows(u32x4* xs, int M, int K, c
         const float ss = wave_sum64(acc);
         if (lane == 0) inv_sh[r] = 1.0f / csqrt(ss / static_cast<float>(K) + na.eps);
     }
-    __syncthreads();
+    lds_barrier();
     for (int e = threadIdx.x; e < total; e += 256) {
         const int r = e / npr;
         const int p = e - r * npr;
@@ -63,7 +93,7 @@ __device__ __forceinline__ void normalize_staged_rows(u32x4* xs, int M, int K, c
         xs[e] = o;
         if (na.xn != nullptr && blockIdx.x == 0) *reinterpret_cast<u32x4*>(na.xn + r * na.ldxn + p * 8) = o;
     }
-    __syncthreads();
+    lds_barrier();
 }
 
 // Stages the M activation rows [M, K] (row pitch ldx) in xs as 16-byte
@@ -121,17 +151,6 @@ __device__ __forceinline__ void stage_rows_lds_dma(u32x4* xs, const uint16_t* __
         }
     }
 }
-
-// A compiler-only memory fence (no instruction): loads are neither hoisted
-// above nor sunk below it.  It brackets the weight requests that a wait for
-// the global -> LDS copies counts (s_waitcnt vmcnt(n) with n those requests):
-// without it the compiler may sink a request whose value is used only on a
-// conditional path below the wait, and the wait then no longer covers every
-// copy (seen on gfx950: 6 of 8 requests left above the wait).  The weight
-// pointer of such a kernel must not be __restrict__: loads through a
-// restrict-qualified read-only argument count as invariant, and the fence
-// does not hold them.
-__device__ __forceinline__ void pin_memory_order() { asm volatile("" ::: "memory"); }
 
 // s_waitcnt with vmcnt(n) and the other counters left alone (gfx9 encoding:
 // vmcnt bits [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8]).
