@@ -158,6 +158,12 @@ typedef struct hai_verify_profile {
 int hai_engine_prefill(void* engine, const int32_t* prompt, int64_t P, int64_t max_new);
 int hai_engine_spec_rounds(void* engine, int64_t rounds, int64_t width, int32_t* out_tokens,
                            int64_t out_capacity, int64_t* n_out, hai_spec_stats* stats);
+/* Draft overrides for hai_engine_spec_rounds (benchmark legs with a chosen
+ * acceptance pattern): tokens [B][n] replace the MTP proposal for output
+ * position pos < n of each sequence, as the override of
+ * generate_speculative does, but from a device copy made once here (no host
+ * round trip per draft).  tokens == NULL or n == 0 clears them. */
+int hai_engine_set_draft_override(void* engine, const int32_t* tokens, int64_t n);
 int hai_engine_profile_verify(void* engine, int64_t T, int64_t iters, hai_verify_profile* out);
 
 #ifdef __cplusplus

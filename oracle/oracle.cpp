@@ -29,6 +29,14 @@ inline float store(float v, int round_out) { return round_out ? bf(v) : v; }
 
 extern "C" {
 
+// OpenMP threads of the oracle's parallel loops (the results do not depend
+// on it: every output's reduction runs in one thread in a fixed order);
+// returns the count in effect.
+int orc_set_threads(int n) {
+    if (n > 0) omp_set_num_threads(n);
+    return omp_get_max_threads();
+}
+
 void orc_exp_array(const float* x, float* y, int64_t n) {
     for (int64_t i = 0; i < n; ++i) y[i] = cexp(x[i]);
 }

@@ -135,6 +135,7 @@ typedef struct orc_spec_stats {
 
 uint16_t orc_synthetic_weight_bits(uint64_t seed, uint32_t tensor_id,
                                    uint64_t index, float std_dev);
+int orc_set_threads(int n);  /* OpenMP threads (n <= 0: query only) */
 void orc_synthetic_prompt(uint64_t seed, int64_t n, int64_t vocab,
                           int32_t* out);
 

@@ -72,6 +72,8 @@ def lib():
         _lib.orc_synthetic_weight_bits.argtypes = [ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint64,
                                                    ctypes.c_float]
         _lib.orc_synthetic_prompt.argtypes = [ctypes.c_uint64, ctypes.c_int64, ctypes.c_int64, I32P]
+        _lib.orc_set_threads.argtypes = [ctypes.c_int]
+        _lib.orc_set_threads.restype = ctypes.c_int
         _lib.orc_model_quantize_fp8.argtypes = [ctypes.c_void_p]
         _lib.orc_fp8_synthetic_scales.argtypes = [ctypes.c_uint64, ctypes.c_uint32, ctypes.c_int64, F32P]
         _lib.orc_model_set_tensor.argtypes = [ctypes.c_void_p, ctypes.c_uint32, F32P, ctypes.c_int64]
@@ -282,6 +284,12 @@ QWEN27B = dict(hidden=5120, num_layers=64, full_attention_interval=4, num_q_head
 
 def make_config(d: dict) -> OrcConfig:
     return OrcConfig(**d)
+
+
+def set_threads(n: int) -> int:
+    """OpenMP threads of the oracle's loops (n <= 0 only queries); returns
+    the count in effect.  Results do not depend on it."""
+    return int(lib().orc_set_threads(int(n)))
 
 
 def synthetic_prompt(seed, n, vocab):

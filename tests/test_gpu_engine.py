@@ -87,6 +87,34 @@ def test_forced_acceptance_patterns(engines, width, perturb):
     assert st["accepted"] == rst["accepted"] > 0
 
 
+@pytest.mark.parametrize("width,perturb", [(1, (3, 9, 10, 27)), (3, (5, 20, 21, 40))])
+def test_device_draft_override_in_spec_rounds(engines, width, perturb):
+    """The benchmark hook: prefill + spec_rounds with the overrides uploaded
+    once (set_draft_override) emit the tokens and counts of
+    generate_speculative with the same overrides, and leave later rounds on
+    the MTP proposals once cleared."""
+    eng, ref, prompt = engines
+    g = ref.greedy(prompt, NEW)
+    ov = g.copy()
+    for i in perturb:
+        ov[i] = (ov[i] + 7) % orc.TINY["vocab"]
+    want, wst, _ = ref.speculative(prompt, NEW, width, draft_override=ov)
+    eng.prefill(prompt, NEW)
+    eng.set_draft_override(ov)
+    out = np.zeros(NEW, np.int32)
+    try:
+        n, st = eng.spec_rounds(4096, width, out)
+    finally:
+        eng.set_draft_override(None)
+    assert n == NEW and list(out) == list(want) == list(g)
+    for key in ("rounds", "proposed", "accepted", "rejected", "corrections"):
+        assert st[key] == wst[key], key
+    # cleared: the MTP head proposes again (random weights: nothing accepted)
+    eng.prefill(prompt, NEW)
+    n, st = eng.spec_rounds(4096, width, out)
+    assert list(out[:n]) == list(g[:n]) and st["accepted"] < wst["accepted"]
+
+
 def test_width_beyond_the_verify_rows_is_rejected(engines):
     """Width 16 (17 verify rows, the largest the reference allows) runs;
     a wider proposal than the engine verifies is an argument error, not a

@@ -74,6 +74,7 @@ def bind(lib: ctypes.CDLL) -> ctypes.CDLL:
     lib.hai_engine_spec_rounds.argtypes = [VP, I64, I64, I32P, I64, ctypes.POINTER(ctypes.c_int64),
                                            ctypes.POINTER(SpecStats)]
     lib.hai_engine_profile_verify.argtypes = [VP, I64, I64, ctypes.POINTER(VerifyProfile)]
+    lib.hai_engine_set_draft_override.argtypes = [VP, I32P, I64]
     lib.hai_engine_forward_batch.argtypes = [VP, I32P, I64, U16P, U16P]
     lib.hai_engine_generate_speculative_batch.argtypes = [VP, I32P, I64, I64, I64, I32P, I64, I32P, I64, I32P,
                                                           ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(SpecStats),
@@ -82,7 +83,8 @@ def bind(lib: ctypes.CDLL) -> ctypes.CDLL:
     lib.hai_engine_batch.argtypes = [VP]
     for n in ("hai_engine_init_synthetic", "hai_engine_forward", "hai_engine_generate_greedy",
               "hai_engine_generate_speculative", "hai_engine_prefill", "hai_engine_spec_rounds",
-              "hai_engine_profile_verify", "hai_engine_forward_batch", "hai_engine_generate_speculative_batch"):
+              "hai_engine_profile_verify", "hai_engine_forward_batch", "hai_engine_generate_speculative_batch",
+              "hai_engine_set_draft_override"):
         getattr(lib, n).restype = ctypes.c_int
     return lib
 
@@ -227,6 +229,16 @@ class Engine:
                                                     out2.shape[1], n.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)),
                                                     ctypes.byref(st)), "spec_rounds")
         return int(n.sum()), st.as_dict()
+
+    def set_draft_override(self, tokens):
+        """tokens [n] or [B][n]: drafts of spec_rounds for output positions
+        < n (None clears)."""
+        if tokens is None:
+            self._check(self.lib.hai_engine_set_draft_override(self.h, None, 0), "set_draft_override")
+            return
+        t = _i32(tokens).reshape(self.batch, -1)
+        self._check(self.lib.hai_engine_set_draft_override(self.h, t.ctypes.data_as(I32P), t.shape[1]),
+                    "set_draft_override")
 
     def profile_verify(self, T, iters):
         pr = VerifyProfile()

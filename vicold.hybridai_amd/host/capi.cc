@@ -105,6 +105,11 @@ int hai_engine_spec_rounds(void* engine, int64_t rounds, int64_t width, int32_t*
     return as_engine(engine)->spec_rounds(rounds, width, out_tokens, out_capacity, n_out, stats);
 }
 
+int hai_engine_set_draft_override(void* engine, const int32_t* tokens, int64_t n) {
+    if (!engine) return HAI_ERR_INVALID_ARGUMENT;
+    return as_engine(engine)->set_draft_override(tokens, n);
+}
+
 int hai_engine_profile_verify(void* engine, int64_t T, int64_t iters, hai_verify_profile* out) {
     if (!engine || !out) return HAI_ERR_INVALID_ARGUMENT;
     return as_engine(engine)->profile_verify(T, iters, out);

@@ -133,6 +133,7 @@ Engine::~Engine() {
     if (weights_) hai_free(weights_);
     if (caches_) hai_free(caches_);
     if (work_) hai_free(work_);
+    if (d_override_) hai_free(d_override_);
     if (stream_) hai_stream_destroy(stream_);
 }
 
@@ -871,6 +872,9 @@ int Engine::one_round(int64_t width, const RoundIo& io, bool* any_live) {
                 const int64_t tok = io.override_tokens[static_cast<int64_t>(b) * io.n_override + pos];
                 HAI_TRY(hai_memcpy_h2d(d_vids_ + static_cast<int64_t>(b) * T + i + 1, &tok, 8, stream_));
                 HAI_TRY(sync());  // tok lives on the host stack
+            } else if (io.device_override && pos < n_override_) {
+                HAI_TRY(hai_memcpy_d2d(d_vids_ + static_cast<int64_t>(b) * T + i + 1,
+                                       d_override_ + static_cast<int64_t>(b) * n_override_ + pos, 8, stream_));
             }
             ++kd[b];
             ++io.stats[b].proposed;
@@ -1052,6 +1056,28 @@ int Engine::generate_speculative(const int32_t* prompts, int64_t P, int64_t max_
     return HAI_OK;
 }
 
+int Engine::set_draft_override(const int32_t* tokens, int64_t n) {
+    if (n < 0) return fail(HAI_ERR_INVALID_ARGUMENT, "set_draft_override: negative length");
+    if (tokens == nullptr || n == 0) {
+        n_override_ = 0;
+        return HAI_OK;
+    }
+    HAI_TRY(check_ids(tokens, B_ * n, "draft override"));
+    if (n > n_override_ || d_override_ == nullptr) {
+        HAI_TRY(sync());
+        if (d_override_) HAI_TRY(hai_free(d_override_));
+        d_override_ = nullptr;
+        void* p = nullptr;
+        HAI_TRY(hai_malloc(&p, static_cast<size_t>(B_ * n) * 8));
+        d_override_ = static_cast<int64_t*>(p);
+    }
+    std::vector<int64_t> wide(static_cast<size_t>(B_ * n));
+    for (size_t i = 0; i < wide.size(); ++i) wide[i] = tokens[i];
+    HAI_TRY(hai_memcpy_h2d(d_override_, wide.data(), wide.size() * 8, stream_));
+    n_override_ = n;
+    return sync();  // wide lives on the host stack
+}
+
 int Engine::spec_rounds(int64_t rounds, int64_t width, int32_t* out, int64_t cap, int64_t* n_out,
                         hai_spec_stats* stats) {
     if (width < 1 || width > tmax_ - 1)
@@ -1066,6 +1092,7 @@ int Engine::spec_rounds(int64_t rounds, int64_t width, int32_t* out, int64_t cap
     io.out = out;
     io.out_ld = cap;
     io.stats = st.data();
+    io.device_override = n_override_ > 0;
     auto t0 = Clock::now();
     bool live = true;
     for (int64_t r = 0; r < rounds && live; ++r) HAI_TRY(one_round(width, io, &live));

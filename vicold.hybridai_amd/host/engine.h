@@ -148,6 +148,11 @@ public:
     // benchmark split of generate_speculative; spec_rounds sums the stats of
     // all sequences
     int prefill(const int32_t* prompts, int64_t P, int64_t max_new);
+    // draft overrides for spec_rounds, uploaded once: tokens [B][n] replace
+    // the MTP proposal for output position pos < n of each sequence (the
+    // device copies them into the verify ids, no host round trip); n = 0 or
+    // null tokens clears them
+    int set_draft_override(const int32_t* tokens, int64_t n);
     int spec_rounds(int64_t rounds, int64_t width, int32_t* out, int64_t cap, int64_t* n_out,
                     hai_spec_stats* stats);
     int profile_verify(int64_t T, int64_t iters, hai_verify_profile* out);
@@ -173,6 +178,7 @@ private:
         int32_t* round_log = nullptr;              // [B][log_cap][HAI_ROUND_RECORD]
         int64_t log_cap = 0;
         int64_t* n_log = nullptr;                  // [B] records written
+        bool device_override = false;              // drafts from d_override_ (spec_rounds)
     };
 
     int fail(int rc, const std::string& what);       // the engine's own message
@@ -276,6 +282,8 @@ private:
     int32_t* d_delta_ = nullptr;  // [B] MTP length corrections
     int32_t* d_plen_ = nullptr;   // [3B + 4B] profiling scratch lengths/results
     int64_t* d_pnext_ = nullptr;  // [B] profiling scratch tokens
+    int64_t* d_override_ = nullptr;  // [B][n_override_] draft overrides of spec_rounds (own allocation)
+    int64_t n_override_ = 0;
     uint16_t* h_ = nullptr;       // [rows, H] residual stream
     uint16_t* xn_ = nullptr;      // [rows, 2H]
     uint16_t* emb_ = nullptr;     // [rows, H]
