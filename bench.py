@@ -38,7 +38,7 @@ ROOT = Path(__file__).resolve().parent
 HBM_PEAK_GBS = 8000.0
 # HBM traffic / algorithmic weight bytes of the verify-step GEMMs (rocprofv3 FETCH_SIZE x 2.0 +
 # WRITE_SIZE, scaled by a known-size copy): profiles/gemm_bf16_kernel_c3_traffic.txt
-GEMM_TRAFFIC_RATIO = 1.0033
+GEMM_TRAFFIC_RATIO = 1.0037
 METRIC = "accepted tok/s + verify steps/s (27B-shape bf16, bs=1, MTP k=1); % HBM peak"
 
 
@@ -474,6 +474,8 @@ def main():
     ap.add_argument("--no-c5", action="store_true",
                     help="skip C5 (FP8 weights, batch 32 x 512-token prompts, k=1; reported under batch_c5)")
     ap.add_argument("--batch-rounds", type=int, default=12)
+    ap.add_argument("--no-c1", action="store_true", help="skip the C1 tiny-model decode (reported under c1)")
+    ap.add_argument("--no-c2", action="store_true", help="skip the C2 op micro-bench (reported under c2_ops)")
     ap.add_argument("--c4-prompt", type=int, default=8192,
                     help="C4 prompt length (8192 is the configuration; shorter only for counter passes)")
     ap.add_argument("--copy-bytes", type=int, default=0,
@@ -590,11 +592,13 @@ def main():
         except RuntimeError as e:
             result[key] = {"error": str(e)}
             log(f"[{run[0]}] failed: {e}")
-    result["c1"] = c1_decode(hai, E, cpu=not args.no_cpu_baseline)
-    log("C1: " + json.dumps(result["c1"]))
-    result["c2_ops"] = c2_ops(hai, cpu=not args.no_cpu_baseline)
-    log("C2 ops: " + ", ".join(f"{k} {v['us']} us ({v['gb_s']} GB/s)" for k, v in result["c2_ops"].items()
-                               if isinstance(v, dict)))
+    if not args.no_c1:
+        result["c1"] = c1_decode(hai, E, cpu=not args.no_cpu_baseline)
+        log("C1: " + json.dumps(result["c1"]))
+    if not args.no_c2:
+        result["c2_ops"] = c2_ops(hai, cpu=not args.no_cpu_baseline)
+        log("C2 ops: " + ", ".join(f"{k} {v['us']} us ({v['gb_s']} GB/s)" for k, v in result["c2_ops"].items()
+                                   if isinstance(v, dict)))
     if not args.no_cpu_baseline:
         t0 = time.perf_counter()
         # the CPU oracle extrapolated to the same round mix as `value`
