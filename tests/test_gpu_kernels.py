@@ -1067,6 +1067,51 @@ def test_mfma_keep_partials_then_residual_rmsnorm(M, N, K, fp8):
                                              None, 0, dws.ptr, wsb, None) == hai.ERR_INVALID
 
 
+@pytest.mark.parametrize("M,N,K,fp8", [(32, 5120, 6144, False), (32, 5120, 17408, False), (64, 5120, 17408, True),
+                                       (17, 1536, 4096, False), (128, 5120, 2048, True)])
+def test_mfma_fp32_accumulators_within_1e3(M, N, K, fp8):
+    """The matrix-core GEMMs' fp32 accumulation, read directly: a residual
+    GEMM that keeps its K-split partials leaves splits planes of fp32 sums in
+    the workspace; their sum (in float64) is the GEMM's fp32-accumulated
+    x . w before any bf16 rounding, and must be within 1e-3 of the float64
+    product: |acc - exact| <= 1e-3 * max(|exact|, rms of the output row / 10).
+    FP8 weights: w = decode(q) * s per 128 x 128 block (the scale applied per
+    block in fp32 inside the kernel)."""
+    rng = np.random.default_rng(3 * M + N + K + fp8)
+    x, xb = rand_bf16(rng, (M, K))
+    zeros = np.zeros((M, N), np.uint16)
+    if fp8:
+        q, s = _fp8_weights(rng, N, K)
+        dq, ds = dev(q), dev(s)
+        w64 = orc.fp8_dequant_2d(q, s, 128, 128).astype(np.float64)
+    else:
+        w, wb = rand_bf16(rng, (N, K), 0.02)
+        dw = dev(wb)
+        w64 = w.astype(np.float64)
+    dx, dh = dev(xb), dev(zeros)
+    wsb = kern().hai_gemm_mfma_workspace_bytes(M, N)
+    dws = out_buf(max(wsb, 16))
+    splits = kern().hai_gemm_mfma_splits(M, N, K, dws.ptr, wsb)
+    assert splits > 1
+    if fp8:
+        rc = kern().hai_gemm_fp8_mfma(dh.ptr, N, dx.ptr, K, dq.ptr, ds.ptr, None, M, N, K,
+                                      hai.EPI_RESIDUAL | hai.FP8_NO_SPECIAL_CODES | hai.MFMA_KEEP_PARTIALS, dh.ptr, N,
+                                      dws.ptr, wsb, None)
+    else:
+        rc = kern().hai_gemm_bf16_mfma(dh.ptr, N, dx.ptr, K, dw.ptr, M, N, K, hai.EPI_RESIDUAL | hai.MFMA_KEEP_PARTIALS,
+                                       dh.ptr, N, dws.ptr, wsb, None)
+    hai.check(rc, "gemm keeping partials")
+    planes = dws.download(np.float32)[: splits * M * N].reshape(splits, M, N).astype(np.float64)
+    acc = planes.sum(0)
+    exact = x.astype(np.float64) @ w64.T
+    rms_row = np.sqrt(np.mean(exact ** 2, axis=1, keepdims=True))
+    err = np.abs(acc - exact) / np.maximum(np.abs(exact), rms_row / 10)
+    assert np.isfinite(acc).all()
+    assert err.max() <= 1e-3, f"fp32 accumulators: max relative error {err.max():.2e}"
+    # the planes are real partial sums, not one full sum and zeros
+    assert np.abs(planes[1]).max() > 0
+
+
 @pytest.mark.gpu
 def test_operand_bounds_check():
     """The host-side check the launchers run under HAI_CHECK_BOUNDS (set for
