@@ -103,6 +103,27 @@ int hai_engine_init_synthetic(void* engine, uint64_t seed, float std_dev);
 /* Copy one bf16 weight tensor (reference layout) to host memory; -1 for an
  * unknown id or a tensor held as FP8. */
 int64_t hai_engine_read_tensor(void* engine, uint32_t tensor_id, uint16_t* out, int64_t capacity);
+
+/* Checkpoints on disk (the reference's Qwen3Config::load_json,
+ * models/qwen3_config.cc:12-206, SafeTensorLoader, io/safetensor_loader.cc:
+ * 50-406, and Qwen3WeightLoader, models/qwen3_weights.cc:196-380).
+ *   hai_model_config_load: <dir>/config.json into cfg (text_config fields
+ *     first; head_dim from hidden / heads when absent; rope_theta and the
+ *     rotary fraction from rope_parameters; layer_types checked against the
+ *     interval), its eos_token_id(s) into eos_ids (n_eos = how many the
+ *     config lists) and, when weight_format is not null, the format of the
+ *     checkpoint's QuantizedWeight Linears (HAI_WEIGHTS_BF16: BF16;
+ *     HAI_WEIGHTS_FP8_BLOCK128: F8_E4M3 + weight_scale_inv); a message on
+ *     failure.  Host only: no device is touched.
+ *   hai_engine_load_checkpoint: every weight of an engine created from that
+ *     config and format, from <dir>/model.safetensors or the shards listed by
+ *     <dir>/model.safetensors.index.json, by the reference's tensor names
+ *     (model.language_model.layers.{i}.*, mtp.*, lm_head.weight); shapes and
+ *     dtypes checked (BF16, F32 holding bf16 numbers, FP8 E4M3 with a BF16 or
+ *     F32 128 x 128 scale grid). */
+int hai_model_config_load(const char* dir, hai_model_config* cfg, int64_t* eos_ids, int64_t eos_capacity,
+                          int64_t* n_eos, int32_t* weight_format, char* message, int64_t message_capacity);
+int hai_engine_load_checkpoint(void* engine, const char* dir);
 uint64_t hai_engine_weight_bytes(void* engine);
 
 /* generate_* return the number of emitted tokens, or -status on failure. */

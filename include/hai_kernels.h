@@ -35,6 +35,9 @@ enum {
     HAI_ERR_OUT_OF_MEMORY = 2,
     HAI_ERR_NOT_IMPLEMENTED = 3,
     HAI_ERR_INVALID_DEVICE = 5,
+    HAI_ERR_UNSUPPORTED_DTYPE = 6,
+    HAI_ERR_FILE_NOT_FOUND = 7,
+    HAI_ERR_INVALID_MODEL = 8,
     HAI_ERR_BACKEND = 9,
 };
 
@@ -51,6 +54,10 @@ int hai_free(void* ptr);
 int hai_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream);
 int hai_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream);
 int hai_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream);
+/* height rows of width bytes, host rows src_pitch apart to device rows
+ * dst_pitch apart (checkpoint tensors into stacked / interleaved weights). */
+int hai_memcpy_h2d_2d(void* dst, size_t dst_pitch, const void* src, size_t src_pitch, size_t width, size_t height,
+                      void* stream);
 /* Copy in whichever direction the two addresses imply (hipMemcpyDefault). */
 int hai_memcpy(void* dst, const void* src, size_t bytes, void* stream);
 /* Page-locked host memory (MemoryType::HostPinned buffers). */

@@ -34,7 +34,7 @@ int cpu_checks() {
     }
     {
         Generator g(GeneratorOptions{"/tmp", "hip", 1, false});
-        expect_code(g.load_model(), ApiStatusCode::NotImplemented, "checkpoint dir");
+        expect_code(g.load_model(), ApiStatusCode::FileNotFound, "checkpoint dir without config.json");
     }
     {
         Generator g(GeneratorOptions{"synthetic:huge", "hip", 1, false});

@@ -45,6 +45,7 @@ _KERNEL_SIGS = {
     "hai_memcpy_h2d": [VP, VP, ctypes.c_size_t, VP],
     "hai_memcpy_d2h": [VP, VP, ctypes.c_size_t, VP],
     "hai_memcpy_d2d": [VP, VP, ctypes.c_size_t, VP],
+    "hai_memcpy_h2d_2d": [VP, ctypes.c_size_t, VP, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_size_t, VP],
     "hai_memset": [VP, ctypes.c_int, ctypes.c_size_t, VP],
     "hai_memcpy": [VP, VP, ctypes.c_size_t, VP],
     "hai_host_malloc": [ctypes.POINTER(VP), ctypes.c_size_t],

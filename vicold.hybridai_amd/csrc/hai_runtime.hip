@@ -91,6 +91,15 @@ int hai_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream) {
     return check_hip(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, as_stream(stream)),
                      "hipMemcpyAsync(D2D)");
 }
+int hai_memcpy_h2d_2d(void* dst, size_t dst_pitch, const void* src, size_t src_pitch, size_t width, size_t height,
+                      void* stream) {
+    if (height == 0 || width == 0) return HAI_OK;
+    if (dst == nullptr || src == nullptr || width > dst_pitch || width > src_pitch)
+        return invalid("memcpy_h2d_2d: null pointer or width beyond a pitch");
+    return check_hip(hipMemcpy2DAsync(dst, dst_pitch, src, src_pitch, width, height, hipMemcpyHostToDevice,
+                                      as_stream(stream)),
+                     "hipMemcpy2DAsync(H2D)");
+}
 int hai_memcpy(void* dst, const void* src, size_t bytes, void* stream) {
     return check_hip(hipMemcpyAsync(dst, src, bytes, hipMemcpyDefault, as_stream(stream)),
                      "hipMemcpyAsync(default)");

@@ -75,6 +75,12 @@ def bind(lib: ctypes.CDLL) -> ctypes.CDLL:
                                            ctypes.POINTER(SpecStats)]
     lib.hai_engine_profile_verify.argtypes = [VP, I64, I64, ctypes.POINTER(VerifyProfile)]
     lib.hai_engine_set_draft_override.argtypes = [VP, I32P, I64]
+    lib.hai_model_config_load.argtypes = [ctypes.c_char_p, ctypes.POINTER(ModelConfig), ctypes.POINTER(ctypes.c_int64),
+                                          I64, ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int32),
+                                          ctypes.c_char_p, I64]
+    lib.hai_model_config_load.restype = ctypes.c_int
+    lib.hai_engine_load_checkpoint.argtypes = [VP, ctypes.c_char_p]
+    lib.hai_engine_load_checkpoint.restype = ctypes.c_int
     lib.hai_engine_forward_batch.argtypes = [VP, I32P, I64, U16P, U16P]
     lib.hai_engine_generate_speculative_batch.argtypes = [VP, I32P, I64, I64, I64, I32P, I64, I32P, I64, I32P,
                                                           ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(SpecStats),
@@ -93,8 +99,33 @@ def _i32(a):
     return np.ascontiguousarray(a, dtype=np.int32)
 
 
+class CheckpointError(RuntimeError):
+    def __init__(self, code, message):
+        super().__init__(f"({code}) {message}")
+        self.code = code
+
+
+def model_config_load(model_dir, weight_format=True):
+    """<model_dir>/config.json (and, with weight_format, the checkpoint's
+    Linear format) -> (config dict as TINY / QWEN27B, eos ids, format)."""
+    from . import host
+    lib = host()
+    c = ModelConfig()
+    eos = (ctypes.c_int64 * 64)()
+    n_eos = ctypes.c_int64(0)
+    fmt = ctypes.c_int32(-1)
+    msg = ctypes.create_string_buffer(1024)
+    rc = lib.hai_model_config_load(str(model_dir).encode(), ctypes.byref(c), eos, 64, ctypes.byref(n_eos),
+                                   ctypes.byref(fmt) if weight_format else None, msg, 1024)
+    if rc != 0:
+        raise CheckpointError(rc, msg.value.decode())
+    cfg = {n: getattr(c, n) for n, _ in ModelConfig._fields_}
+    return cfg, [int(eos[i]) for i in range(min(64, n_eos.value))], (fmt.value if weight_format else None)
+
+
 class Engine:
-    """One verify engine on one GPU (synthetic weights)."""
+    """One verify engine on one GPU (synthetic weights, or a checkpoint
+    through load_checkpoint)."""
 
     def __init__(self, cfg: dict, max_context: int, max_verify_tokens: int = 16, device: int = 0,
                  use_graphs: bool = False, fp8: bool = False, batch: int = 1, mfma: bool = False):
@@ -127,6 +158,9 @@ class Engine:
 
     def init_synthetic(self, seed=0, std=0.02):
         self._check(self.lib.hai_engine_init_synthetic(self.h, seed, std), "init_synthetic")
+
+    def load_checkpoint(self, model_dir):
+        self._check(self.lib.hai_engine_load_checkpoint(self.h, str(model_dir).encode()), "load_checkpoint")
 
     def weight_bytes(self) -> int:
         return int(self.lib.hai_engine_weight_bytes(self.h))

@@ -2,6 +2,11 @@
 #include <new>
 #include <string>
 
+#include <algorithm>
+#include <cstring>
+#include <vector>
+
+#include "checkpoint.h"
 #include "engine.h"
 #include "hai_kernels.h"
 
@@ -41,6 +46,51 @@ const char* hai_engine_last_error(void* engine) {
 int hai_engine_init_synthetic(void* engine, uint64_t seed, float std_dev) {
     if (!engine) return HAI_ERR_INVALID_ARGUMENT;
     return as_engine(engine)->init_synthetic(seed, std_dev);
+}
+
+int hai_model_config_load(const char* dir, hai_model_config* cfg, int64_t* eos_ids, int64_t eos_capacity,
+                          int64_t* n_eos, int32_t* weight_format, char* message, int64_t message_capacity) {
+    auto report = [&](int rc, const std::string& what) {
+        if (message != nullptr && message_capacity > 0) {
+            const size_t n = std::min(what.size(), static_cast<size_t>(message_capacity - 1));
+            std::memcpy(message, what.data(), n);
+            message[n] = '\0';
+        }
+        return rc;
+    };
+    if (dir == nullptr || cfg == nullptr) return report(HAI_ERR_INVALID_ARGUMENT, "null argument");
+    std::string err;
+    std::vector<int64_t> eos;
+    hai_model_config c{};
+    if (const int rc = hybridai::mi355x::read_model_config(dir, &c, &eos, &err); rc != HAI_OK) return report(rc, err);
+    if (weight_format != nullptr) {
+        hybridai::mi355x::SafeTensors st;
+        if (const int rc = st.open(dir, &err); rc != HAI_OK) return report(rc, err);
+        if (const int rc = hybridai::mi355x::detect_weight_format(st, c, weight_format, &err); rc != HAI_OK)
+            return report(rc, err);
+    }
+    if (n_eos != nullptr) *n_eos = static_cast<int64_t>(eos.size());
+    if (eos_ids != nullptr)
+        for (int64_t i = 0; i < eos_capacity && i < static_cast<int64_t>(eos.size()); ++i) eos_ids[i] = eos[i];
+    *cfg = c;
+    return report(HAI_OK, "");
+}
+
+int hai_engine_load_checkpoint(void* engine, const char* dir) {
+    if (!engine || !dir) return HAI_ERR_INVALID_ARGUMENT;
+    Engine* e = as_engine(engine);
+    hybridai::mi355x::SafeTensors st;
+    std::string err;
+    int rc = st.open(dir, &err);
+    int32_t fmt = HAI_WEIGHTS_BF16;
+    if (rc == HAI_OK) rc = hybridai::mi355x::detect_weight_format(st, e->config(), &fmt, &err);
+    if (rc == HAI_OK && (fmt == HAI_WEIGHTS_FP8_BLOCK128) != e->fp8_weights()) {
+        rc = HAI_ERR_INVALID_ARGUMENT;
+        err = std::string("the checkpoint stores its Linears as ") + (fmt == HAI_WEIGHTS_FP8_BLOCK128 ? "FP8" : "BF16") +
+              " but the engine was created for the other format";
+    }
+    if (rc != HAI_OK) return e->set_error(rc, "load_checkpoint: " + err);
+    return e->load_checkpoint(st);
 }
 
 int64_t hai_engine_read_tensor(void* engine, uint32_t tensor_id, uint16_t* out, int64_t capacity) {

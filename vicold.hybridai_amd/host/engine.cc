@@ -1,6 +1,8 @@
 // engine.cc -- MI355X verify engine (see engine.h).
 #include "engine.h"
 
+#include "checkpoint.h"
+
 #include <algorithm>
 #include <cmath>
 #include <cstring>
@@ -10,15 +12,6 @@
 namespace hybridai::mi355x {
 
 namespace {
-
-// Tensor ids shared with the synthetic generator: slot * 64 + kind.
-enum Kind : uint32_t {
-    kInputLN = 0, kPostLN = 1, kInQKV = 2, kInZ = 3, kInA = 4, kInB = 5, kConv = 6, kALog = 7,
-    kDtBias = 8, kLinNorm = 9, kOutProj = 10, kQProj = 11, kKProj = 12, kVProj = 13, kOProj = 14,
-    kQNorm = 15, kKNorm = 16, kGate = 17, kUp = 18, kDown = 19,
-};
-constexpr uint32_t tid(uint32_t slot, uint32_t kind) { return slot * 64u + kind; }
-constexpr uint32_t kSlotShared = 0, kSlotMtpShared = 1, kSlotLayer0 = 2, kSlotMtpLayer0 = 1024;
 
 constexpr size_t kAlign = 256;
 // Widest linear layer that takes its input RMSNorm fused into the GEMM.
@@ -410,6 +403,101 @@ int Engine::init_synthetic(uint64_t seed, float std_dev) {
     hai_free(tmp);
     if (rc != HAI_OK) return lib_fail(rc, "fp8 synthetic weights");
     if (rc_sync != HAI_OK) return lib_fail(rc_sync, "stream synchronize");
+    return HAI_OK;
+}
+
+int Engine::load_checkpoint(const SafeTensors& st, bool include_mtp) {
+    auto is_mtp = [](uint32_t id) { return id / 64u == kSlotMtpShared || id / 64u == kSlotMtpLayer0; };
+    std::string err;
+    std::vector<unsigned char> host;
+    auto missing = [&](const std::string& name) {
+        return fail(HAI_ERR_INVALID_MODEL, "Missing Qwen weight: " + name);
+    };
+    // shape of a checkpoint tensor against the engine's rows x cols: 2-D
+    // [rows, cols], a vector [cols] when rows == 1, the depthwise conv as
+    // [C, 1, Kc] or [C, Kc]
+    auto shape_ok = [](const StTensor& t, int64_t rows, int64_t cols) {
+        const auto& s = t.shape;
+        if (s.size() == 2) return s[0] == rows && s[1] == cols;
+        if (s.size() == 1) return rows == 1 && s[0] == cols;
+        if (s.size() == 3) return s[0] == rows && s[1] == 1 && s[2] == cols;
+        return false;
+    };
+    auto shape_text = [](const StTensor& t) {
+        std::string r = "[";
+        for (size_t i = 0; i < t.shape.size(); ++i) r += (i ? ", " : "") + std::to_string(t.shape[i]);
+        return r + "]";
+    };
+    // BF16 bits of a tensor (F32 accepted when every value is a bf16 number)
+    auto read_bf16 = [&](const std::string& name, const StTensor& t, std::vector<uint16_t>* out) -> int {
+        out->resize(static_cast<size_t>(t.numel()));
+        if (t.dtype == StDType::BF16) {
+            if (const int rc = st.read(t, out->data(), &err); rc != HAI_OK) return fail(rc, err);
+            return HAI_OK;
+        }
+        if (t.dtype != StDType::F32)
+            return fail(HAI_ERR_UNSUPPORTED_DTYPE,
+                        "Qwen weight " + name + " is " + st_dtype_name(t.dtype) + "; the engine stores BF16");
+        std::vector<float> f(static_cast<size_t>(t.numel()));
+        if (const int rc = st.read(t, f.data(), &err); rc != HAI_OK) return fail(rc, err);
+        for (size_t i = 0; i < f.size(); ++i)
+            if (!exact_bf16(f[i], &(*out)[i]))
+                return fail(HAI_ERR_UNSUPPORTED_DTYPE,
+                            "Qwen weight " + name + " is F32 with values that are not bf16 numbers");
+        return HAI_OK;
+    };
+    std::vector<uint16_t> bits;
+    for (const auto& e : tensors_) {
+        if (!include_mtp && is_mtp(e.id)) continue;
+        const std::string name = checkpoint_name(e.id);
+        const StTensor* t = st.find(name);
+        if (name.empty() || t == nullptr) return missing(name.empty() ? std::to_string(e.id) : name);
+        if (!shape_ok(*t, e.rows, e.cols))
+            return fail(HAI_ERR_INVALID_MODEL, "Qwen weight " + name + " has shape " + shape_text(*t) + ", expected [" +
+                                                   std::to_string(e.rows) + ", " + std::to_string(e.cols) + "]");
+        if (const int rc = read_bf16(name, *t, &bits); rc != HAI_OK) return rc;
+        HAI_TRY(hai_memcpy_h2d_2d(e.ptr, static_cast<size_t>(e.ld) * 2, bits.data(), static_cast<size_t>(e.cols) * 2,
+                                  static_cast<size_t>(e.cols) * 2, static_cast<size_t>(e.rows), stream_));
+        HAI_TRY(sync());  // bits is reused
+    }
+    for (const auto& e : quant_) {
+        if (!include_mtp && is_mtp(e.id)) continue;
+        const std::string name = checkpoint_name(e.id);
+        const StTensor* t = st.find(name);
+        if (name.empty() || t == nullptr) return missing(name.empty() ? std::to_string(e.id) : name);
+        const std::string sname = name.substr(0, name.size() - 7) + ".weight_scale_inv";
+        const StTensor* s = st.find(sname);
+        if (t->dtype != StDType::F8_E4M3 || s == nullptr)
+            return fail(HAI_ERR_UNSUPPORTED_DTYPE, "Expected scaled FP8 Qwen weight: " + name);
+        if (!shape_ok(*t, e.rows, e.cols) || t->shape.size() != 2)
+            return fail(HAI_ERR_INVALID_MODEL, "Qwen weight " + name + " has shape " + shape_text(*t));
+        const int64_t sr = (e.rows + 127) / 128, sc = (e.cols + 127) / 128;
+        if (s->shape.size() != 2 || s->shape[0] != sr || s->shape[1] != sc)
+            return fail(HAI_ERR_INVALID_MODEL, "Qwen scale " + sname + " has shape " + shape_text(*s) +
+                                                   ", expected the 128 x 128 block grid [" + std::to_string(sr) +
+                                                   ", " + std::to_string(sc) + "]");
+        host.resize(static_cast<size_t>(t->bytes()));
+        if (const int rc = st.read(*t, host.data(), &err); rc != HAI_OK) return fail(rc, err);
+        HAI_TRY(hai_memcpy_h2d_2d(e.q, static_cast<size_t>(e.ldq), host.data(), static_cast<size_t>(e.cols),
+                                  static_cast<size_t>(e.cols), static_cast<size_t>(e.rows), stream_));
+        HAI_TRY(sync());
+        // block scales to fp32 (load_as_fp32: BF16 widened exactly)
+        std::vector<float> scales(static_cast<size_t>(sr * sc));
+        if (s->dtype == StDType::F32) {
+            if (const int rc = st.read(*s, scales.data(), &err); rc != HAI_OK) return fail(rc, err);
+        } else if (s->dtype == StDType::BF16) {
+            std::vector<uint16_t> sb(scales.size());
+            if (const int rc = st.read(*s, sb.data(), &err); rc != HAI_OK) return fail(rc, err);
+            for (size_t i = 0; i < sb.size(); ++i) {
+                const uint32_t u = static_cast<uint32_t>(sb[i]) << 16;
+                std::memcpy(&scales[i], &u, 4);
+            }
+        } else {
+            return fail(HAI_ERR_UNSUPPORTED_DTYPE, "Only BF16 and FP32 can be loaded as FP32: " + sname);
+        }
+        HAI_TRY(hai_memcpy_h2d(e.s, scales.data(), scales.size() * 4, stream_));
+        HAI_TRY(sync());
+    }
     return HAI_OK;
 }
 

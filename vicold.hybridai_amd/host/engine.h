@@ -93,6 +93,19 @@ struct LayerWeights {
     float* state = nullptr;       // [nslots][B][nv][dk*dv], column-tiled heads
 };
 
+// Tensor ids shared with the synthetic generator, the CPU oracle and the
+// checkpoint names: slot * 64 + kind (slot 0 shared, 1 MTP shared, 2 + i
+// decoder layer i, 1024 the MTP decoder layer).
+enum Kind : uint32_t {
+    kInputLN = 0, kPostLN = 1, kInQKV = 2, kInZ = 3, kInA = 4, kInB = 5, kConv = 6, kALog = 7,
+    kDtBias = 8, kLinNorm = 9, kOutProj = 10, kQProj = 11, kKProj = 12, kVProj = 13, kOProj = 14,
+    kQNorm = 15, kKNorm = 16, kGate = 17, kUp = 18, kDown = 19,
+};
+constexpr uint32_t tid(uint32_t slot, uint32_t kind) { return slot * 64u + kind; }
+constexpr uint32_t kSlotShared = 0, kSlotMtpShared = 1, kSlotLayer0 = 2, kSlotMtpLayer0 = 1024;
+
+class SafeTensors;
+
 struct TensorEntry {
     uint32_t id;
     uint16_t* ptr;
@@ -126,12 +139,23 @@ public:
 
     bool ok() const { return ok_; }
     const std::string& error() const { return error_; }
+    int set_error(int rc, const std::string& what) { return fail(rc, what); }
 
     int init_synthetic(uint64_t seed, float std_dev);
+    // Every weight from a Qwen checkpoint (models/qwen3_weights.cc:196-380):
+    // each engine tensor read under its checkpoint name, shape and dtype
+    // checked (BF16, or F32 whose values are all bf16 numbers; FP8 E4M3 codes
+    // with their weight_scale_inv grid when the engine stores FP8), and
+    // copied into the engine's stacked / interleaved layout.
+    // include_mtp = false leaves the MTP weights unloaded (a checkpoint
+    // without them decodes greedily only).
+    int load_checkpoint(const SafeTensors& st, bool include_mtp = true);
     int64_t read_tensor(uint32_t id, uint16_t* out, int64_t capacity);
     uint64_t weight_bytes() const { return weight_bytes_; }
     const Dims& dims() const { return d_; }
     int64_t batch() const { return B_; }
+    bool fp8_weights() const { return fp8_; }
+    const hai_model_config& config() const { return cfg_; }
 
     // Per-sequence arrays below are [B][...]: prompts [B][P], ids [B][T],
     // hidden [B][T][H], logits [B][T][V], out [B][max_new or cap], n_out [B],

@@ -25,6 +25,7 @@
 #include <cstdlib>
 #include <sstream>
 
+#include "checkpoint.h"
 #include "engine.h"
 #include "hai_kernels.h"
 #include "refabi/hybrid_api.h"
@@ -61,6 +62,9 @@ ApiStatusCode api_code(int hai_rc) {
         case HAI_ERR_OUT_OF_MEMORY: return ApiStatusCode::OutOfMemory;
         case HAI_ERR_NOT_IMPLEMENTED: return ApiStatusCode::NotImplemented;
         case HAI_ERR_INVALID_DEVICE: return ApiStatusCode::InvalidDevice;
+        case HAI_ERR_UNSUPPORTED_DTYPE: return ApiStatusCode::InvalidModel;  // no such ApiStatusCode
+        case HAI_ERR_FILE_NOT_FOUND: return ApiStatusCode::FileNotFound;
+        case HAI_ERR_INVALID_MODEL: return ApiStatusCode::InvalidModel;
         default: return ApiStatusCode::BackendError;
     }
 }
@@ -103,14 +107,7 @@ public:
             return {ApiStatusCode::NotImplemented,
                     "this library provides the MI355X (\"hip\") backend only, not \"" + options_.backend + "\""};
         const std::string& dir = options_.model_dir;
-        if (dir.rfind("synthetic:", 0) != 0) {
-            struct stat st{};
-            if (dir.empty() || stat(dir.c_str(), &st) != 0)
-                return {ApiStatusCode::FileNotFound, "model directory not found: " + dir};
-            return {ApiStatusCode::NotImplemented,
-                    "checkpoint loading is not part of this build; use model_dir = \"synthetic:tiny\" or "
-                    "\"synthetic:27b\""};
-        }
+        if (dir.rfind("synthetic:", 0) != 0) return load_checkpoint_dir(dir);
         std::string spec = dir.substr(10), query;
         if (const auto q = spec.find('?'); q != std::string::npos) {
             query = spec.substr(q + 1);
@@ -156,9 +153,60 @@ public:
         return {};
     }
 
+    // generator.cc:390-431 for a Qwen checkpoint directory: config.json,
+    // the weights (the MTP layer's when enable_mtp), the EOS ids of the
+    // config; the engine's KV capacity is the smaller of
+    // max_position_embeddings and 32768 positions.
+    ApiStatus load_checkpoint_dir(const std::string& dir) {
+        struct stat sb{};
+        if (dir.empty() || stat(dir.c_str(), &sb) != 0 || !S_ISDIR(sb.st_mode))
+            return {ApiStatusCode::FileNotFound, "model directory does not exist: " + dir};
+        std::string err;
+        std::vector<int64_t> eos;
+        int64_t max_pos = 0;
+        int rc = mi355x::read_model_config(dir, &cfg_, &eos, &err, &max_pos);
+        if (rc != HAI_OK) return {api_code(rc), err};
+        mi355x::SafeTensors st;
+        rc = st.open(dir, &err);
+        int32_t fmt = HAI_WEIGHTS_BF16;
+        if (rc == HAI_OK) rc = mi355x::detect_weight_format(st, cfg_, &fmt, &err);
+        if (rc != HAI_OK) return {api_code(rc), err};
+        if (options_.enable_mtp && cfg_.mtp_layers <= 0)
+            return {ApiStatusCode::InvalidModel, "Checkpoint does not contain Qwen MTP layers"};
+        if (cfg_.mtp_layers > 1)
+            return {ApiStatusCode::NotImplemented, "checkpoints with more than one MTP layer are not supported"};
+        hai_engine_options eo{};
+        eo.max_context = static_cast<int32_t>(std::min<int64_t>(max_pos, 32768));
+        eo.max_verify_tokens = static_cast<int32_t>(mi355x::kMaxVerifyRows);
+        eo.device = 0;
+        eo.use_graphs = 0;
+        eo.weight_format = fmt;
+        engine_ = std::make_unique<mi355x::Engine>(cfg_, eo);
+        if (!engine_->ok()) {
+            const std::string why = engine_->error();
+            engine_.reset();
+            return {ApiStatusCode::BackendError, "engine creation failed: " + why};
+        }
+        if (rc = engine_->load_checkpoint(st, options_.enable_mtp); rc != HAI_OK) {
+            const std::string why = engine_->error();
+            engine_.reset();
+            return {api_code(rc), why};
+        }
+        eos_.clear();
+        for (int64_t id : eos)
+            if (id >= 0 && id < cfg_.vocab) eos_.push_back(static_cast<int32_t>(id));
+        std::sort(eos_.begin(), eos_.end());
+        eos_.erase(std::unique(eos_.begin(), eos_.end()), eos_.end());
+        context_ = eo.max_context;
+        mtp_loaded_ = options_.enable_mtp;
+        return {};
+    }
+
     ApiStatus generate(const GenerationOptions& o, GenerationResult* result) {
         if (result == nullptr) return {ApiStatusCode::InvalidArgument, "result must not be null"};
         if (!engine_) return {ApiStatusCode::InvalidModel, "load_model() has not succeeded"};
+        if (o.enable_speculative_mtp && !mtp_loaded_)
+            return {ApiStatusCode::InvalidArgument, "speculative MTP requires GeneratorOptions::enable_mtp"};
         std::vector<int32_t> prompt;
         if (!parse_ids(o.prompt, &prompt))
             return {ApiStatusCode::InvalidArgument,
@@ -176,11 +224,12 @@ public:
         int rc;
         if (o.enable_speculative_mtp) {
             rc = engine_->generate_speculative(prompt.data(), static_cast<int64_t>(prompt.size()), o.max_new_tokens,
-                                               speculative_width_from_env(), nullptr, 0, nullptr, 0, out.data(), &st,
+                                               speculative_width_from_env(), eos_.data(),
+                                               static_cast<int64_t>(eos_.size()), nullptr, 0, out.data(), &st,
                                                nullptr, 0, &n);
         } else {
             rc = engine_->generate_greedy(prompt.data(), static_cast<int64_t>(prompt.size()), o.max_new_tokens,
-                                          nullptr, 0, out.data(), &n);
+                                          eos_.data(), static_cast<int64_t>(eos_.size()), out.data(), &n);
         }
         if (rc != HAI_OK) return {api_code(rc), "generation failed: " + engine_->error()};
         result->elapsed_seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
@@ -225,6 +274,8 @@ private:
     GeneratorOptions options_;
     hai_model_config cfg_{};
     int32_t context_ = 0;
+    bool mtp_loaded_ = true;     // synthetic models always carry their MTP layer
+    std::vector<int32_t> eos_;   // the checkpoint config's eos_token_id(s)
     std::unique_ptr<mi355x::Engine> engine_;
 };
 
