@@ -2,8 +2,11 @@
 // caller such as demo/generate does, against this library.
 //
 //   generator_run --cpu                      error paths that need no device
-//   generator_run <model_dir> <greedy|spec> <prompt> <max_new>
-//       prints "tokens <id> <id> ..." and "stats <name>=<value> ...".
+//   generator_run <model_dir> <greedy|spec> <prompt> <max_new> [plain|chat|chat-think]
+//       prints "tokens <id> <id> ...", "stats <name>=<value> ..." and
+//       "text_hex <result text as hex, - when empty>"; the last argument sets
+//       GenerationOptions::use_chat_template / enable_thinking (default: the
+//       struct's defaults, chat without thinking).
 #include <cstdio>
 #include <cstring>
 #include <string>
@@ -58,10 +61,12 @@ int cpu_checks() {
 
 int main(int argc, char** argv) {
     if (argc > 1 && std::strcmp(argv[1], "--cpu") == 0) return cpu_checks();
-    if (argc != 5) {
-        std::fprintf(stderr, "usage: %s <model_dir> <greedy|spec> <prompt> <max_new>\n", argv[0]);
+    if (argc != 5 && argc != 6) {
+        std::fprintf(stderr, "usage: %s <model_dir> <greedy|spec> <prompt> <max_new> [plain|chat|chat-think]\n",
+                     argv[0]);
         return 2;
     }
+    const std::string layout = argc == 6 ? argv[5] : "chat";
     Generator g(GeneratorOptions{argv[1], "hip", 1, true});
     ApiStatus st = g.load_model();
     if (!st.ok()) {
@@ -72,18 +77,30 @@ int main(int argc, char** argv) {
     o.prompt = argv[3];
     o.max_new_tokens = std::atoi(argv[4]);
     o.enable_speculative_mtp = std::strcmp(argv[2], "spec") == 0;
+    o.use_chat_template = layout != "plain";
+    o.enable_thinking = layout == "chat-think";
     GenerationResult r;
     st = g.generate(o, &r);
     if (!st.ok()) {
         std::printf("generate failed: %d %s\n", static_cast<int>(st.code()), st.message().c_str());
         return 1;
     }
-    // a bad prompt after a successful load is rejected, and the engine stays usable
+    // bad arguments after a successful load are rejected (generator.cc:458-461),
+    // and a model without a tokenizer refuses text prompts
     GenerationResult bad;
     GenerationOptions ob = o;
+    ob.prompt = "";
+    const bool empty_refused = g.generate(ob, &bad).code() == ApiStatusCode::InvalidArgument;
+    ob = o;
+    ob.max_new_tokens = 0;
+    const bool zero_refused = g.generate(ob, &bad).code() == ApiStatusCode::InvalidArgument;
+    ob = o;
     ob.prompt = "hello";
-    if (g.generate(ob, &bad).code() != ApiStatusCode::InvalidArgument) {
-        std::printf("FAIL text prompt accepted\n");
+    const bool ids_model = o.prompt.rfind("ids:", 0) == 0;
+    const bool text_refused = g.generate(ob, &bad).code() == ApiStatusCode::InvalidArgument;
+    if (!empty_refused || !zero_refused || (ids_model && !text_refused)) {
+        std::printf("FAIL bad arguments accepted (empty %d, zero %d, text %d)\n", empty_refused, zero_refused,
+                    text_refused);
         return 1;
     }
     std::printf("tokens");
@@ -97,5 +114,8 @@ int main(int argc, char** argv) {
                 static_cast<long long>(r.speculative_mtp_recovery_tokens),
                 static_cast<long long>(r.speculative_max_proposal_width), r.decode_tokens_per_second,
                 r.text.rfind("ids:", 0) == 0 ? 1 : 0);
+    std::printf("text_hex %s", r.text.empty() ? "-" : "");
+    for (unsigned char c : r.text) std::printf("%02x", c);
+    std::printf("\n");
     return 0;
 }

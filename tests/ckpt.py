@@ -5,7 +5,8 @@ model.language_model.layers.{i}.*, mtp.*, lm_head.weight).  With fp8=True the
 QuantizedWeight Linears are stored as F8_E4M3 codes with a 128 x 128
 weight_scale_inv grid -- the codes and scales of the oracle's own FP8 model
 (its synthetic scales, its encoder) -- so that a loaded checkpoint must
-reproduce the oracle's bf16 or FP8 model bit for bit.  Test helper only."""
+reproduce the oracle's bf16 or FP8 model bit for bit.  The directory also
+gets the small byte-level tokenizer of tests/tok.py.  Test helper only."""
 import json
 from pathlib import Path
 
@@ -13,6 +14,7 @@ import numpy as np
 import torch
 from safetensors.torch import save_file
 
+import tok
 from _hai import orc
 
 # layer tensor kinds (slot * 64 + kind), as the engine and the oracle number them
@@ -68,7 +70,7 @@ def config_json(c, eos=None, **overrides):
             "tie_word_embeddings": False}
 
 
-def write_tiny_checkpoint(path, fp8=False, shards=1, eos=None, scale_dtype=torch.float32):
+def write_tiny_checkpoint(path, fp8=False, shards=1, eos=None, scale_dtype=torch.float32, generation_eos=None):
     path = Path(path)
     path.mkdir(parents=True, exist_ok=True)
     c = orc.TINY
@@ -101,4 +103,7 @@ def write_tiny_checkpoint(path, fp8=False, shards=1, eos=None, scale_dtype=torch
             save_file({n: tensors[n] for n in part}, str(path / fname))
             weight_map.update({n: fname for n in part})
         (path / "model.safetensors.index.json").write_text(json.dumps({"metadata": {}, "weight_map": weight_map}))
+    # the tokenizer (tests/tok.py: ids below the tiny vocabulary) and, when
+    # given, generation_config.json's stop ids
+    tok.write_tokenizer(path, generation=None if generation_eos is None else {"eos_token_id": generation_eos})
     return path

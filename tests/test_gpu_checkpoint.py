@@ -4,7 +4,8 @@ hai_engine_load_checkpoint must give the engine the oracle's weights bit
 for bit, and so the oracle's tokens and round logs; with FP8 Linears
 (F8_E4M3 + weight_scale_inv, sharded, F32 or BF16-widened scales) the
 oracle's FP8 model.  Through hybridai::Generator, a checkpoint directory
-decodes the golden tokens and stops at the EOS ids of its config.json."""
+takes text prompts through its tokenizer, decodes the oracle's tokens and
+stops at the stop ids of its config.json and generation_config.json."""
 import json
 import os
 import subprocess
@@ -14,6 +15,7 @@ import pytest
 import torch
 
 import ckpt
+import tok
 from _hai import ROOT, hai, orc
 
 pytestmark = pytest.mark.gpu
@@ -95,25 +97,59 @@ def test_format_mismatch_and_bf16_scales(dirs, tmp_path):
         eng.close()
 
 
-def _generator(model_dir, mode, prompt, max_new, width=1):
+def _generator(model_dir, mode, prompt, max_new, width=1, layout="plain"):
+    """(tokens, stats, text) of hybridai::Generator through tests/backend/generator_run."""
     subprocess.run(["make", "-s", "-C", str(ROOT / "tests" / "backend")], check=True, capture_output=True)
     env = dict(os.environ, HYBRIDAI_SPECULATIVE_WIDTH=str(width))
     r = subprocess.run([str(ROOT / "tests" / "backend" / "_build" / "generator_run"), str(model_dir), mode, prompt,
-                        str(max_new)], capture_output=True, text=True, timeout=300, env=env)
+                        str(max_new), layout], capture_output=True, text=True, timeout=300, env=env)
     assert r.returncode == 0, r.stdout + r.stderr
-    return [int(t) for t in r.stdout.split("\n")[0].split()[1:]]
+    lines = dict(line.split(" ", 1) for line in r.stdout.strip().splitlines())
+    stats = dict(kv.split("=") for kv in lines["stats"].split())
+    text = b"" if lines["text_hex"] == "-" else bytes.fromhex(lines["text_hex"])
+    return [int(t) for t in lines["tokens"].split()], stats, text.decode(errors="replace")
 
 
-def test_generator_loads_a_checkpoint_directory(dirs, tmp_path):
-    """The golden C1 decode (tests/golden/tiny_c1.json) from a checkpoint
-    directory through the public API, at widths 1 and 3; then EOS ids read
-    from config.json stop greedy and speculative decoding at the first one
-    emitted."""
-    g = list(GOLD["greedy"])
-    prompt = "ids:" + ",".join(str(int(t)) for t in GOLD["prompt"])
-    assert _generator(dirs["bf16"], "spec", prompt, NEW, width=1) == g[:NEW]
-    assert _generator(dirs["bf16"], "spec", prompt, NEW, width=3) == g[:NEW]
-    stop = g[5]
-    d = ckpt.write_tiny_checkpoint(tmp_path / "eos", eos=[orc.TINY["vocab"] - 1, stop])
-    assert _generator(d, "spec", prompt, NEW) == g[:g.index(stop) + 1]
-    assert _generator(d, "greedy", prompt, NEW) == g[:g.index(stop) + 1]
+TEXT = "The quick brown fox can't wait: 你好, мир! 12 apples.\n"
+
+
+def test_generator_encodes_text_and_decodes_the_result(dirs):
+    """A text prompt through the public API: encoded by the checkpoint's
+    tokenizer.json (the ids the HF library gives), plain or in the chat
+    layout (generator.cc:468-474); the tokens equal the oracle's greedy
+    decode of those ids at widths 1 and 3, and result.text is their decoding
+    without special tokens (generator.cc:1032, 1275)."""
+    hf = tok.hf(dirs["bf16"])
+    ref = orc.Model(orc.TINY, seed=0)
+    try:
+        for layout, text in (("plain", TEXT), ("chat", f"<|im_start|>user\n{TEXT}<|im_end|>\n"
+                                                       "<|im_start|>assistant\n<think>\n\n</think>\n\n"),
+                             ("chat-think", f"<|im_start|>user\n{TEXT}<|im_end|>\n<|im_start|>assistant\n<think>\n")):
+            ids = hf.encode(text).ids
+            want = [int(t) for t in ref.greedy(ids, NEW)]
+            for width in (1, 3):
+                toks, stats, out = _generator(dirs["bf16"], "spec", TEXT, NEW, width=width, layout=layout)
+                assert toks == want, (layout, width)
+                assert int(stats["prompt_tokens"]) == len(ids)
+                assert out == hf.decode(want, skip_special_tokens=True)
+    finally:
+        ref.close()
+
+
+def test_generator_stop_ids_from_config_and_generation_config(tmp_path):
+    """Stop ids are config.json's eos_token_id joined with
+    generation_config.json's (generator.cc:476-480): greedy and speculative
+    decoding stop at the first one emitted, whichever file names it."""
+    d0 = ckpt.write_tiny_checkpoint(tmp_path / "plain")
+    ids = tok.hf(d0).encode(TEXT).ids
+    ref = orc.Model(orc.TINY, seed=0)
+    g = [int(t) for t in ref.greedy(ids, NEW)]
+    ref.close()
+    firsts = [k for k in range(3, NEW) if g[k] not in g[:k]]  # positions where a token first appears
+    b = g[firsts[0]]
+    a = g[next(k for k in firsts if k >= firsts[0] + 3)]
+    d = ckpt.write_tiny_checkpoint(tmp_path / "eos", eos=[orc.TINY["vocab"] - 1, a], generation_eos=[b])
+    for mode in ("spec", "greedy"):
+        assert _generator(d, mode, TEXT, NEW)[0] == g[:g.index(b) + 1]
+    d = ckpt.write_tiny_checkpoint(tmp_path / "eos2", eos=a, generation_eos=orc.TINY["vocab"] - 2)
+    assert _generator(d, "spec", TEXT, NEW)[0] == g[:g.index(a) + 1]

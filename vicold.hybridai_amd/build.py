@@ -55,8 +55,8 @@ def kernel_inputs() -> list[Path]:
 
 
 def host_inputs() -> list[Path]:
-    return (sorted(HOST.glob("*.cc")) + sorted(HOST.glob("*.h")) + sorted(HOST.glob("refabi/*"))
-            + sorted(INCLUDE.glob("*.h")))
+    return (sorted(HOST.glob("*.cc")) + sorted(HOST.glob("*.h")) + sorted(HOST.glob("*.inc"))
+            + sorted(HOST.glob("refabi/*")) + sorted(INCLUDE.glob("*.h")))
 
 
 def source_digest(paths) -> str:

@@ -9,6 +9,8 @@
 #include "checkpoint.h"
 #include "engine.h"
 #include "hai_kernels.h"
+#include "hai_tokenizer.h"
+#include "tokenizer.h"
 
 using hybridai::mi355x::Engine;
 
@@ -163,6 +165,118 @@ int hai_engine_set_draft_override(void* engine, const int32_t* tokens, int64_t n
 int hai_engine_profile_verify(void* engine, int64_t T, int64_t iters, hai_verify_profile* out) {
     if (!engine || !out) return HAI_ERR_INVALID_ARGUMENT;
     return as_engine(engine)->profile_verify(T, iters, out);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// tokenizer (include/hai_tokenizer.h)
+
+namespace {
+using hybridai::mi355x::QwenTokenizer;
+QwenTokenizer* as_tokenizer(void* t) { return static_cast<QwenTokenizer*>(t); }
+
+template <typename T>
+int32_t emit(const T* src, size_t n, T* out, int64_t capacity, int64_t* n_out) {
+    if (n_out == nullptr) return HAI_ERR_INVALID_ARGUMENT;
+    *n_out = static_cast<int64_t>(n);
+    if (static_cast<int64_t>(n) > capacity) return HAI_ERR_INVALID_ARGUMENT;
+    if (n > 0) {
+        if (out == nullptr) return HAI_ERR_INVALID_ARGUMENT;
+        std::memcpy(out, src, n * sizeof(T));
+    }
+    return HAI_OK;
+}
+
+int32_t emit_text(const std::string& s, char* out, int64_t capacity, int64_t* n_out) {
+    const int32_t rc = emit(s.data(), s.size(), out, capacity, n_out);
+    if (rc == HAI_OK && out != nullptr && capacity > static_cast<int64_t>(s.size())) out[s.size()] = '\0';
+    return rc;
+}
+}  // namespace
+
+extern "C" {
+
+void* hai_tokenizer_open(const char* dir, int32_t* status, char* message, int64_t message_capacity) {
+    auto report = [&](int32_t rc, const std::string& what) {
+        if (status != nullptr) *status = rc;
+        if (message != nullptr && message_capacity > 0) {
+            const size_t n = std::min(what.size(), static_cast<size_t>(message_capacity - 1));
+            std::memcpy(message, what.data(), n);
+            message[n] = '\0';
+        }
+    };
+    if (dir == nullptr) {
+        report(HAI_ERR_INVALID_ARGUMENT, "null directory");
+        return nullptr;
+    }
+    auto* t = new (std::nothrow) QwenTokenizer();
+    if (t == nullptr) {
+        report(HAI_ERR_OUT_OF_MEMORY, "out of host memory");
+        return nullptr;
+    }
+    std::string err;
+    if (const int rc = t->load(dir, &err); rc != HAI_OK) {
+        delete t;
+        report(rc, err);
+        return nullptr;
+    }
+    report(HAI_OK, "");
+    return t;
+}
+
+void hai_tokenizer_close(void* tokenizer) { delete as_tokenizer(tokenizer); }
+
+int32_t hai_tokenizer_encode(void* tokenizer, const char* text, int64_t text_bytes, int64_t* ids, int64_t capacity,
+                             int64_t* n_out) {
+    if (tokenizer == nullptr || text_bytes < 0 || (text == nullptr && text_bytes > 0)) return HAI_ERR_INVALID_ARGUMENT;
+    const std::vector<int64_t> v =
+        as_tokenizer(tokenizer)->encode(std::string(text ? text : "", static_cast<size_t>(text_bytes)));
+    return emit(v.data(), v.size(), ids, capacity, n_out);
+}
+
+int32_t hai_tokenizer_decode(void* tokenizer, const int64_t* ids, int64_t n_ids, int32_t skip_special, char* out,
+                             int64_t capacity, int64_t* n_out) {
+    if (tokenizer == nullptr || n_ids < 0 || (ids == nullptr && n_ids > 0)) return HAI_ERR_INVALID_ARGUMENT;
+    return emit_text(as_tokenizer(tokenizer)->decode(ids, static_cast<size_t>(n_ids), skip_special != 0), out,
+                     capacity, n_out);
+}
+
+int32_t hai_tokenizer_chat_prompt(const char* const* roles, const char* const* contents, int64_t n_messages,
+                                  int32_t add_generation_prompt, int32_t enable_thinking, char* out,
+                                  int64_t capacity, int64_t* n_out) {
+    if (n_messages < 0 || (n_messages > 0 && (roles == nullptr || contents == nullptr))) return HAI_ERR_INVALID_ARGUMENT;
+    std::vector<std::pair<std::string, std::string>> m;
+    for (int64_t i = 0; i < n_messages; ++i) {
+        if (roles[i] == nullptr || contents[i] == nullptr) return HAI_ERR_INVALID_ARGUMENT;
+        m.emplace_back(roles[i], contents[i]);
+    }
+    return emit_text(QwenTokenizer::chat_prompt(m, add_generation_prompt != 0, enable_thinking != 0), out, capacity,
+                     n_out);
+}
+
+int32_t hai_tokenizer_special_ids(void* tokenizer, int64_t* eos, int64_t eos_capacity, int64_t* n_eos, int64_t* pad,
+                                  int64_t* bos) {
+    if (tokenizer == nullptr) return HAI_ERR_INVALID_ARGUMENT;
+    const QwenTokenizer* t = as_tokenizer(tokenizer);
+    if (pad != nullptr) *pad = t->pad_token_id();
+    if (bos != nullptr) *bos = t->bos_token_id();
+    return emit(t->eos_token_ids().data(), t->eos_token_ids().size(), eos, eos_capacity, n_eos);
+}
+
+int32_t hai_tokenizer_pieces(void* tokenizer, const char* text, int64_t text_bytes, int64_t* bounds,
+                             int64_t capacity, int64_t* n_out) {
+    if (tokenizer == nullptr || text_bytes < 0 || (text == nullptr && text_bytes > 0)) return HAI_ERR_INVALID_ARGUMENT;
+    const auto p = as_tokenizer(tokenizer)->pieces(std::string(text ? text : "", static_cast<size_t>(text_bytes)));
+    std::vector<int64_t> flat;
+    flat.reserve(2 * p.size());
+    for (const auto& r : p) {
+        flat.push_back(static_cast<int64_t>(r.first));
+        flat.push_back(static_cast<int64_t>(r.second));
+    }
+    const int32_t rc = emit(flat.data(), flat.size(), bounds, capacity, n_out);
+    if (n_out != nullptr) *n_out = static_cast<int64_t>(p.size());
+    return rc;
 }
 
 }  // extern "C"

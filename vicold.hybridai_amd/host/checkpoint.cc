@@ -465,4 +465,8 @@ bool exact_bf16(float v, uint16_t* bits) {
     return true;
 }
 
+bool is_regular_file(const std::string& path) { return file_exists(path); }
+bool read_whole_file(const std::string& path, std::string* out) { return read_file(path, out); }
+std::string path_join(const std::string& dir, const std::string& name) { return join(dir, name); }
+
 }  // namespace hybridai::mi355x

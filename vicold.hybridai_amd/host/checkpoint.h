@@ -70,4 +70,9 @@ std::string checkpoint_name(uint32_t id);
 // value would change)
 bool exact_bf16(float v, uint16_t* bits);
 
+// file helpers shared by the checkpoint readers
+bool is_regular_file(const std::string& path);
+bool read_whole_file(const std::string& path, std::string* out);
+std::string path_join(const std::string& dir, const std::string& name);
+
 }  // namespace hybridai::mi355x

@@ -4,18 +4,23 @@
 // enable_speculative_mtp, generator.cc:545-1117) entirely on the device and
 // fills GenerationResult's counters (hybrid.h:65-94).
 //
-// What this build accepts (checkpoint IO and the tokenizer are not part of
-// it):
-//   * GeneratorOptions::model_dir =
+// What this build accepts:
+//   * GeneratorOptions::model_dir = a Qwen checkpoint directory
+//     (config.json, model.safetensors or its sharded index, tokenizer.json,
+//     optionally generation_config.json), loaded as Impl::load does
+//     (generator.cc:390-431): prompts are text, wrapped in the chat layout
+//     when GenerationOptions::use_chat_template, encoded by the checkpoint's
+//     tokenizer; the stop ids are the config's and the generation config's;
+//     result.text is the decoded continuation without special tokens;
+//   * or model_dir =
 //     "synthetic:<tiny|27b>[?seed=S&std=X&context=C&weights=bf16|fp8]"
 //     -- the counter-based synthetic weights shared with the CPU oracle
 //     (tiny = BASELINE config C1, 27b = the 27B shape of C3; weights=fp8 the
-//     C5 format: QuantizedWeight Linears as E4M3 with 128x128 block scales);
-//     any other path returns FileNotFound (missing) or NotImplemented (a
-//     checkpoint);
+//     C5 format: QuantizedWeight Linears as E4M3 with 128x128 block scales).
+//     These have no tokenizer: GenerationOptions::prompt = "ids:1,2,3" gives
+//     token ids, result.text holds the generated ids in the same form, and
+//     there is no EOS;
 //   * GeneratorOptions::backend = "hip" (or "mi355x");
-//   * GenerationOptions::prompt = "ids:1,2,3" -- token ids; result.text holds
-//     the generated ids in the same form.  The synthetic models have no EOS;
 //   * the speculative proposal width is HYBRIDAI_SPECULATIVE_WIDTH (1..16,
 //     default 8), read at every generate() as the reference does.
 #include <sys/stat.h>
@@ -29,6 +34,7 @@
 #include "engine.h"
 #include "hai_kernels.h"
 #include "refabi/hybrid_api.h"
+#include "tokenizer.h"
 
 namespace hybridai {
 
@@ -107,6 +113,8 @@ public:
             return {ApiStatusCode::NotImplemented,
                     "this library provides the MI355X (\"hip\") backend only, not \"" + options_.backend + "\""};
         const std::string& dir = options_.model_dir;
+        if (dir.empty()) return {ApiStatusCode::InvalidArgument, "model_dir is empty"};
+        tokenizer_ = mi355x::QwenTokenizer();
         if (dir.rfind("synthetic:", 0) != 0) return load_checkpoint_dir(dir);
         std::string spec = dir.substr(10), query;
         if (const auto q = spec.find('?'); q != std::string::npos) {
@@ -192,6 +200,13 @@ public:
             engine_.reset();
             return {api_code(rc), why};
         }
+        // QwenTokenizer::load after the weights (generator.cc:423-424)
+        if (rc = tokenizer_.load(dir, &err); rc != HAI_OK) {
+            engine_.reset();
+            return {ApiStatusCode::InvalidModel, err};
+        }
+        // stop ids: the config's and the generation config's (generator.cc:476-480)
+        eos.insert(eos.end(), tokenizer_.eos_token_ids().begin(), tokenizer_.eos_token_ids().end());
         eos_.clear();
         for (int64_t id : eos)
             if (id >= 0 && id < cfg_.vocab) eos_.push_back(static_cast<int32_t>(id));
@@ -203,17 +218,30 @@ public:
     }
 
     ApiStatus generate(const GenerationOptions& o, GenerationResult* result) {
+        // argument checks in the order of generator.cc:452-465
         if (result == nullptr) return {ApiStatusCode::InvalidArgument, "result must not be null"};
         if (!engine_) return {ApiStatusCode::InvalidModel, "load_model() has not succeeded"};
+        if (o.prompt.empty() || o.max_new_tokens <= 0)
+            return {ApiStatusCode::InvalidArgument, "prompt must be non-empty and max_new_tokens must be positive"};
         if (o.enable_speculative_mtp && !mtp_loaded_)
             return {ApiStatusCode::InvalidArgument, "speculative MTP requires GeneratorOptions::enable_mtp"};
         std::vector<int32_t> prompt;
-        if (!parse_ids(o.prompt, &prompt))
-            return {ApiStatusCode::InvalidArgument,
-                    "the tokenizer is not part of this build: pass the prompt as \"ids:1,2,3\""};
+        if (tokenizer_.loaded()) {
+            // chat layout and encode (generator.cc:468-474)
+            const std::string text =
+                o.use_chat_template ? mi355x::QwenTokenizer::chat_prompt({{"user", o.prompt}}, true, o.enable_thinking)
+                                    : o.prompt;
+            for (int64_t id : tokenizer_.encode(text)) {
+                if (id < 0 || id >= cfg_.vocab)
+                    return {ApiStatusCode::InvalidArgument, "prompt token id outside the model's vocabulary"};
+                prompt.push_back(static_cast<int32_t>(id));
+            }
+            if (prompt.empty()) return {ApiStatusCode::InvalidArgument, "the prompt encodes to no tokens"};
+        } else if (!parse_ids(o.prompt, &prompt)) {
+            return {ApiStatusCode::InvalidArgument, "a model without a tokenizer takes the prompt as \"ids:1,2,3\""};
+        }
         for (int32_t id : prompt)
             if (id >= cfg_.vocab) return {ApiStatusCode::InvalidArgument, "prompt id outside the vocabulary"};
-        if (o.max_new_tokens < 0) return {ApiStatusCode::InvalidArgument, "max_new_tokens must be >= 0"};
         if (static_cast<int64_t>(prompt.size()) + o.max_new_tokens + mi355x::kMaxVerifyRows > context_)
             return {ApiStatusCode::InvalidArgument, "prompt + max_new_tokens exceed the model context"};
         *result = GenerationResult{};
@@ -234,10 +262,15 @@ public:
         if (rc != HAI_OK) return {api_code(rc), "generation failed: " + engine_->error()};
         result->elapsed_seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
         result->token_ids.assign(out.begin(), out.begin() + n);
-        std::ostringstream text;
-        text << "ids:";
-        for (int64_t i = 0; i < n; ++i) text << (i ? "," : "") << out[static_cast<size_t>(i)];
-        result->text = text.str();
+        if (tokenizer_.loaded()) {
+            // decode without special tokens (generator.cc:1032, 1275)
+            result->text = tokenizer_.decode(result->token_ids.data(), result->token_ids.size(), true);
+        } else {
+            std::ostringstream text;
+            text << "ids:";
+            for (int64_t i = 0; i < n; ++i) text << (i ? "," : "") << out[static_cast<size_t>(i)];
+            result->text = text.str();
+        }
         result->prompt_tokens = static_cast<int64_t>(prompt.size());
         if (o.enable_speculative_mtp) {
             result->prefill_seconds = st.prefill_seconds;
@@ -275,7 +308,8 @@ private:
     hai_model_config cfg_{};
     int32_t context_ = 0;
     bool mtp_loaded_ = true;     // synthetic models always carry their MTP layer
-    std::vector<int32_t> eos_;   // the checkpoint config's eos_token_id(s)
+    std::vector<int32_t> eos_;   // the checkpoint's stop ids (config and generation config)
+    mi355x::QwenTokenizer tokenizer_;  // loaded for checkpoint directories only
     std::unique_ptr<mi355x::Engine> engine_;
 };
 
