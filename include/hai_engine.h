@@ -64,6 +64,15 @@ typedef struct hai_engine_options {
                                  (batches) and the attention on the matrix
                                  cores (bf16 or FP8 weights); 0: every GEMM
                                  and the attention on the bit-exact kernels */
+    int32_t prefill_rows;     /* 0 (or at most the verify rows): prompts
+                                 prefill through the verify step, 16 rows
+                                 per sequence at a time (bit-exact when
+                                 mfma = 0).  Above that, up to 8192: prompts
+                                 prefill in chunks of this many rows per
+                                 sequence on the matrix cores (tiled GEMMs,
+                                 matrix-core attention, lm_head on the last
+                                 row only): tolerance mode for the prompt,
+                                 whatever mfma says for the decode */
 } hai_engine_options;
 
 /* Counters of GenerationResult (include/hybrid.h:65-94) that the path fills. */

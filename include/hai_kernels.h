@@ -285,6 +285,14 @@ int hai_gqa_verify_noalloc_bf16(void* out, const void* q, const void* gate,
  * hai_gqa_mfma_scratch_bytes(B, T, nq, D, max_len) bytes. */
 size_t hai_gqa_mfma_scratch_bytes(int64_t B, int64_t T, int64_t nq, int64_t D,
                                   int64_t max_len);
+/* The scratch the call with these arguments takes on the current device (its
+ * split plan depends on the blocks the device holds): at most
+ * hai_gqa_mfma_scratch_bytes, far less for prompt chunks, whose query groups
+ * alone fill the device.  Not monotonic in T: fewer rows can take more
+ * splits, so a buffer for calls of up to T rows takes the largest value over
+ * 1..T. */
+size_t hai_gqa_mfma_plan_scratch_bytes(int64_t B, int64_t T, int64_t nq, int64_t nkv,
+                                       int64_t D, int64_t max_len);
 int hai_gqa_verify_mfma_bf16(void* out, const void* q, const void* gate,
                              const void* k_cache, const void* v_cache,
                              int64_t cap, void* scratch, int64_t B, int64_t T,
@@ -303,11 +311,14 @@ int hai_gqa_verify_mfma_bf16(void* out, const void* q, const void* gate,
  *     (key i, value j) of the reference's [dk][dv] matrix, with
  *     i = g*(dk/4) + 4m + e (g, e < 4), is float ((m*dv + j)*4 + g)*4 + e;
  *     the state after sequence length L lives in slot L % nslots;
- *   at most 16 tokens per launch;
- *   token t of sequence b has position (lens ? lens[b] : 0) + pos_add + t.
+ *   rows b*T + t of proj / out belong to token t of sequence b, which has
+ *     position (lens ? lens[b] : 0) + pos_add + t;
+ *   a call of more than 16 tokens (prompt chunks) runs as launches of 16 in
+ *   order, each continuing from the state and conv inputs the previous one
+ *   left: the result equals one pass over the T tokens.
  * With write_all_slots the state after every token is kept (rollback by
  * length only, no copies); otherwise only the final state is written.
- * Needs T + Kc - 1 <= ring, and nslots >= T when write_all_slots. */
+ * Needs min(T, 16) + Kc - 1 <= ring, and nslots >= T when write_all_slots. */
 int hai_deltanet_verify_bf16(void* out, int64_t ld_out, const void* proj,
                              int64_t ld_proj, int64_t off_qkv, int64_t off_z,
                              int64_t off_a, int64_t off_b, const void* conv_w,
@@ -461,6 +472,23 @@ int hai_gemm_bf16_mfma(void* y, int64_t ldy, const void* x, int64_t ldx,
                        const void* w, int64_t M, int64_t N, int64_t K,
                        int epilogue, const void* res, int64_t ld_res,
                        void* workspace, size_t workspace_bytes, void* stream);
+/* Prompt-sized linear layers (prefill chunks: hundreds to thousands of rows)
+ * on the matrix cores, compute bound: 128 x 128 (or 128 x 64) output tiles
+ * with both operands staged in LDS.  Same contract, epilogues and tolerance
+ * as hai_gemm_bf16_mfma / hai_gemm_fp8_mfma (FP8: codes decoded exactly,
+ * each 128-k scale block scaled in fp32), any M; K % 64 == 0, ldx % 8 == 0,
+ * x and w 16-byte aligned, M * ldx * 2 and N * K * elem below 4 GiB.  The
+ * reference runs prefill GEMMs through rocblas_gemm_ex
+ * (hip_backend.cc:697-809). */
+int hai_gemm_bf16_tiled(void* y, int64_t ldy, const void* x, int64_t ldx,
+                        const void* w, int64_t M, int64_t N, int64_t K,
+                        int epilogue, const void* res, int64_t ld_res,
+                        void* stream);
+int hai_gemm_fp8_tiled(void* y, int64_t ldy, const void* x, int64_t ldx,
+                       const void* wq, const float* scales,
+                       const int32_t* scale_rows, int64_t M, int64_t N,
+                       int64_t K, int epilogue, const void* res, int64_t ld_res,
+                       void* stream);
 /* Epilogue flag for the MFMA GEMMs with HAI_EPI_RESIDUAL: when the call
  * splits K (hai_gemm_mfma_splits > 1) it leaves the fp32 partials
  * [splits][M][N] at the start of the workspace instead of finishing y; the

@@ -507,6 +507,63 @@ def test_deltanet_verify_rollback(nk, nv, dk, dv, steps, split):
         assert np.array_equal(dev_state.view(np.uint32), want_state.view(np.uint32)), f"state after step {si}"
 
 
+@pytest.mark.parametrize("B,nk,nv,dk,T,Kc,ab", [(3, 2, 6, 64, 40, 4, False), (2, 16, 48, 128, 33, 4, True),
+                                                (1, 4, 4, 64, 100, 3, False)])
+def test_deltanet_prompt_chunk_equals_16_token_launches(B, nk, nv, dk, T, Kc, ab):
+    """One call over a prompt chunk of T > 16 tokens of B sequences (rows
+    b*T + t) against the same tokens as launches of at most 16 with their
+    rows gathered per launch: outputs, the final state slot and the conv
+    ring bit for bit (with ab: the a|b projection formed in the kernel)."""
+    rng = np.random.default_rng(B * 1000 + T + nv)
+    dv = dk
+    kw, vw = nk * dk, nv * dv
+    C = 2 * kw + vw
+    H = 256
+    width = C + vw + 2 * nv
+    ring, nslots = 32, 18
+    cw, cwb = rand_bf16(rng, (C, Kc), 0.3)
+    al, alb = rand_bf16(rng, (nv,), 0.5)
+    dt, dtb = rand_bf16(rng, (nv,), 0.5)
+    nw, nwb = rand_bf16(rng, (dv,), 0.5)
+    xn, xnb = rand_bf16(rng, (B * T, H))
+    wab, wabb = rand_bf16(rng, (2 * nv, H), 0.05)
+    st0 = (rng.standard_normal(nslots * B * nv * dk * dv) * 0.1).astype(np.float32)
+    lens0 = np.array([3 + 5 * b for b in range(B)], np.int32)
+    proj, pb = rand_bf16(rng, (B * T, width))
+    dcw, dal, ddt, dnw, dwab = dev(cwb), dev(alb), dev(dtb), dev(nwb), dev(wabb)
+
+    def call(dout, dproj, dxn, rows, t0, n, dstate, dring, lens):
+        common = (dout.ptr, vw, dproj.ptr, width, 0, C)
+        tail = (dcw.ptr, dring.ptr, ring, dstate.ptr, nslots, 0, dal.ptr, ddt.ptr, dnw.ptr, lens.ptr, t0, B, n, nk,
+                nv, dk, dv, Kc, 1e-6)
+        if ab:
+            hai.check(kern().hai_deltanet_verify_ab_bf16(*common, dxn.ptr, H, dwab.ptr, H, *tail, None), "ab")
+        else:
+            hai.check(kern().hai_deltanet_verify_bf16(*common, C + vw, C + vw + nv, *tail, None), "deltanet")
+
+    got = {}
+    for mode in ("one_call", "launches"):
+        dstate, dring, lens = dev(st0), out_buf(B * ring * C * 2), dev(lens0)
+        if mode == "one_call":
+            dout = out_buf(B * T * vw * 2)
+            call(dout, dev(pb), dev(xnb), B * T, 0, T, dstate, dring, lens)
+            out = dout.download(np.uint16).reshape(B, T, vw)
+        else:
+            out = np.zeros((B, T, vw), np.uint16)
+            for t0 in range(0, T, 16):
+                n = min(16, T - t0)
+                sub = np.ascontiguousarray(pb.reshape(B, T, width)[:, t0:t0 + n].reshape(B * n, width))
+                subx = np.ascontiguousarray(xnb.reshape(B, T, H)[:, t0:t0 + n].reshape(B * n, H))
+                dsout = out_buf(B * n * vw * 2)
+                call(dsout, dev(sub), dev(subx), B * n, t0, n, dstate, dring, lens)
+                out[:, t0:t0 + n] = dsout.download(np.uint16).reshape(B, n, vw)
+        slots = dstate.download(np.uint32).reshape(nslots, B, -1)
+        final = np.stack([slots[(int(lens0[b]) + T) % nslots, b] for b in range(B)])
+        got[mode] = (out, final, dring.download(np.uint16))
+    for i, what in enumerate(("outputs", "final state", "conv ring")):
+        assert np.array_equal(got["one_call"][i], got["launches"][i]), what
+
+
 @pytest.mark.parametrize("B,nk,nv,dk,T,Kc", [(1, 16, 48, 128, 2, 4), (3, 16, 48, 128, 4, 4), (2, 2, 6, 64, 16, 3),
                                              (1, 16, 48, 128, 17, 4)])
 def test_deltanet_column_split_matches_one_block(B, nk, nv, dk, T, Kc):

@@ -477,9 +477,17 @@ __global__ __launch_bounds__(256) void gqa_mfma_partial_kernel(
     const uint32_t bytes = static_cast<uint32_t>((static_cast<int64_t>(nkeys - 1) * nkv * D + D) * 2);
     const __amdgpu_buffer_rsrc_t rk = make_rsrc(kc + off0, bytes);
     const __amdgpu_buffer_rsrc_t rv = make_rsrc(vc + off0, bytes);
-    // wave steps that hold at least one of the block's keys
+    // wave steps that hold at least one key visible to some query of the
+    // group (the group's last query sees the most: queries are in token
+    // order); steps past it would only add zero probabilities
+    int nvis = nkeys;
+    {
+        const int q_last = min(q_begin + QROWS, nqry) - 1;
+        const int64_t vis = (L - T + q_last / group) - kb0 + 1;
+        if (vis < nvis) nvis = static_cast<int>(vis < 0 ? 0 : vis);
+    }
     int wsteps = 0;
-    while (wsteps < steps && (wsteps * kMfmaWaves + wave) * KS < nkeys) ++wsteps;
+    while (wsteps < steps && (wsteps * kMfmaWaves + wave) * KS < nvis) ++wsteps;
 
     u32x4 kr[NKT][NJ];
     u32x4 vr[NB][8];
@@ -883,6 +891,25 @@ int hai_gqa_verify_bf16(void* out, const void* q, const void* gate, const void* 
         case 256: return launch<256>(o, qq, g, kc, vc, cap, sc, int(B), int(T), int(nq), int(nkv), lens, len_add, nchunk, s);
         default: return invalid("gqa_verify: head_dim must be 64, 128 or 256");
     }
+}
+
+size_t hai_gqa_mfma_plan_scratch_bytes(int64_t B, int64_t T, int64_t nq, int64_t nkv, int64_t D,
+                                       int64_t max_len) {
+    if (B <= 0 || T <= 0 || nq <= 0 || nkv <= 0 || nq % nkv != 0 || max_len <= 0) return 0;
+    if (D != 64 && D != 128 && D != 256) return hai_gqa_mfma_scratch_bytes(B, T, nq, D, max_len);
+    const int64_t nqry = T * (nq / nkv);
+    const void* kern = nullptr;
+    switch (D) {
+        case 64: kern = nqry <= 16 ? reinterpret_cast<const void*>(gqa_mfma_partial_kernel<64, 1>)
+                                   : reinterpret_cast<const void*>(gqa_mfma_partial_kernel<64, 2>); break;
+        case 128: kern = nqry <= 16 ? reinterpret_cast<const void*>(gqa_mfma_partial_kernel<128, 1>)
+                                    : reinterpret_cast<const void*>(gqa_mfma_partial_kernel<128, 2>); break;
+        default: kern = nqry <= 16 ? reinterpret_cast<const void*>(gqa_mfma_partial_kernel<256, 1>)
+                                   : reinterpret_cast<const void*>(gqa_mfma_partial_kernel<256, 2>); break;
+    }
+    const int64_t resident = resident_blocks(kern, 0);
+    const MfmaPlan p = mfma_plan(int(D), B, T, nq, nkv, max_len, resident > 0 ? resident : kMfmaTargetBlocks);
+    return static_cast<size_t>(B * T * nq * p.nsplit * mfma_part_stride(int(D))) * sizeof(float);
 }
 
 size_t hai_gqa_mfma_scratch_bytes(int64_t B, int64_t T, int64_t nq, int64_t D, int64_t max_len) {

@@ -53,6 +53,10 @@ struct DnArgs {
     int64_t ld_xn;
     const uint16_t* w_ab;
     int H;
+    // rows per sequence in proj / out / xn (0: T).  A call of more than
+    // kMaxT tokens runs as launches of kMaxT; each sees its own T but the
+    // whole call's row layout.
+    int64_t seq_rows;
 };
 
 constexpr int kSeg = 2048;  // the linear layers' fma segment (elements)
@@ -95,7 +99,7 @@ __global__ __launch_bounds__(DV * 4) void deltanet_kernel(DnArgs A) {
     const int64_t vw = static_cast<int64_t>(nv) * DV;
     const int64_t C = 2 * kw + vw;
     const int hist = A.Kc - 1;
-    const int64_t row0 = static_cast<int64_t>(b) * T;
+    const int64_t row0 = static_cast<int64_t>(b) * (A.seq_rows > 0 ? A.seq_rows : T);
 
     // ---- issue every global load of the step up front: first those that do
     // not depend on the cache length (its load is still in flight) ----
@@ -452,7 +456,7 @@ __global__ __launch_bounds__(DV / CS * 4 > 256 ? DV / CS * 4 : 256) void deltane
     const int64_t vw = static_cast<int64_t>(nv) * DV;
     const int64_t C = 2 * kw + vw;
     const int hist = A.Kc - 1;
-    const int64_t row0 = static_cast<int64_t>(b) * T;
+    const int64_t row0 = static_cast<int64_t>(b) * (A.seq_rows > 0 ? A.seq_rows : T);
     const int64_t head = static_cast<int64_t>(b) * nv + h;
 
     // ---- loads that do not depend on the cache length ----
@@ -787,11 +791,12 @@ int verify(void* out, int64_t ld_out, const void* proj, int64_t ld_proj, int64_t
         return invalid("deltanet_verify: null pointer");
     if (B < 0 || T < 0 || nk <= 0 || nv <= 0 || nv % nk != 0 || Kc < 1 || Kc > kMaxKc || nslots < 1)
         return invalid("deltanet_verify: shape");
-    if (T + Kc - 1 > ring) return invalid("deltanet_verify: conv ring too short for T");
+    if ((T < kMaxT ? T : kMaxT) + Kc - 1 > ring) return invalid("deltanet_verify: conv ring too short for T");
     if (write_all_slots && nslots < T) return invalid("deltanet_verify: fewer state slots than tokens");
     if (lens == nullptr && pos_add < 0) return invalid("deltanet_verify: negative position");
     if (!aligned16(state)) return invalid("deltanet_verify: state alignment");
-    if (T > kMaxT) return invalid("deltanet_verify: at most 16 tokens per launch");
+    if (T > INT32_MAX / 2 || static_cast<int64_t>(pos_add) + T > INT32_MAX)
+        return invalid("deltanet_verify: T too large");
     if (w_ab != nullptr) {
         if (xn == nullptr || H <= 0 || H % 8 != 0 || H > 4 * kSeg || ld_xn < H || ld_xn % 8 != 0 || !aligned16(xn) ||
             !aligned16(w_ab))
@@ -829,13 +834,25 @@ int verify(void* out, int64_t ld_out, const void* proj, int64_t ld_proj, int64_t
     a.ld_xn = ld_xn;
     a.w_ab = static_cast<const uint16_t*>(w_ab);
     a.H = w_ab != nullptr ? int(H) : 0;
-    if (ws != nullptr) {
-        if (ws_bytes < cols_workspace_bytes(B, nv, dv) || !aligned16(ws))
-            return invalid("deltanet_verify_ws: workspace smaller than hai_deltanet_workspace_bytes(B, nv, dv) or "
-                           "not 16-byte aligned");
-        if (w_ab == nullptr && column_splits(B * nv) > 1) return dispatch_cols(a, dk, dv, ws, as_stream(stream));
+    if (ws != nullptr && (ws_bytes < cols_workspace_bytes(B, nv, dv) || !aligned16(ws)))
+        return invalid("deltanet_verify_ws: workspace smaller than hai_deltanet_workspace_bytes(B, nv, dv) or "
+                       "not 16-byte aligned");
+    const bool cols = ws != nullptr && w_ab == nullptr && column_splits(B * nv) > 1;
+    // launches of at most kMaxT tokens, in order: each starts from the state
+    // slot and conv ring entries the previous one left (positions advance by
+    // its tokens), so the result equals one pass over all T
+    a.seq_rows = T;
+    for (int64_t t0 = 0; t0 < T; t0 += kMaxT) {
+        DnArgs s = a;
+        s.T = static_cast<int>(T - t0 < kMaxT ? T - t0 : kMaxT);
+        s.pos_add = pos_add + static_cast<int32_t>(t0);
+        s.proj = a.proj + t0 * ld_proj;
+        s.out = a.out + t0 * ld_out;
+        if (s.xn != nullptr) s.xn = a.xn + t0 * ld_xn;
+        const int rc = cols ? dispatch_cols(s, dk, dv, ws, as_stream(stream)) : dispatch<false>(s, dk, dv, as_stream(stream));
+        if (rc != HAI_OK) return rc;
     }
-    return dispatch<false>(a, dk, dv, as_stream(stream));
+    return HAI_OK;
 }
 
 }  // namespace

@@ -868,3 +868,305 @@ extern "C" int hai_gemm_fp8_mfma(void* y, int64_t ldy, const void* x, int64_t ld
     a.check = (epilogue & HAI_FP8_NO_SPECIAL_CODES) == 0;
     return mfma_entry(a, epilogue & ~HAI_FP8_NO_SPECIAL_CODES, workspace, workspace_bytes, as_stream(stream));
 }
+
+// ---------------------------------------------------------------------------
+// Prefill-sized linear layers: Y[M, N] = X[M, K] . W[N, K]^T for M of
+// hundreds to thousands of rows (prompt chunks of one or several sequences).
+// The weight-streaming kernel above re-reads every weight once per 128 rows;
+// here both operands are tiled and the layer is compute bound.
+//   * block = 4 waves, output tile 128 rows of X x BN rows of W (BN = 128, or
+//     64 when the 128-wide grid would not give every CU two tiles); wave
+//     (wm, wn) owns 64 x BN/2 outputs, 4 x BN/32 tiles of the 16x16x32 bf16
+//     MFMA with fp32 accumulators;
+//   * K in steps of 64: both operand tiles staged in LDS (two buffers, rows
+//     padded by 16 bytes), the next step's global loads in flight in
+//     registers while the current step is multiplied, one barrier per step;
+//   * FP8 weights: codes decoded exactly to bf16 as they are staged, each
+//     128-k scale block summed on its own and scaled in fp32 (the arithmetic
+//     of hai_gemm_fp8_mfma);
+//   * workgroups are dispatched to the 8 XCDs in turn, so block b is given
+//     tile base(b % 8) + b / 8: every XCD takes a contiguous range of tiles
+//     in weight-panel order, and the row tiles sharing a weight panel run on
+//     one XCD together and fetch it into that XCD's L2 once;
+//   * the epilogues of the other GEMMs (store, residual add, SwiGLU over
+//     interleaved gate / up rows).
+// Tolerance mode, as the other matrix-core GEMMs.
+// ---------------------------------------------------------------------------
+namespace {
+
+constexpr int kTileM = 128;
+constexpr int kTileK = 64;
+constexpr int kTileRow = kTileK + 8;  // padded LDS row, bf16 elements
+constexpr int kXcds = 8;
+
+struct TiledArgs {
+    uint16_t* y;
+    int64_t ldy;
+    const uint16_t* x;
+    int64_t ldx;
+    const void* w;               // bf16 [N][K], or E4M3 codes [N][K]
+    const float* scales;         // FP8: [rows][ceil(K/128)]
+    const int32_t* scale_rows;   // FP8: per-row scale row, or null
+    int paired;                  // FP8 SiLU-mul without a map: interleaved gate / up grids
+    const uint16_t* res;
+    int64_t ldres;
+    int M, N, K;
+    int mtiles, ntiles;
+};
+
+template <int WN>
+__host__ __device__ constexpr size_t tiled_lds_bytes() {
+    return static_cast<size_t>(2) * (kTileM + 32 * WN) * kTileRow * 2;
+}
+
+template <int WN, int EPI, bool FP8, bool CHECK>
+__global__ __launch_bounds__(256) void gemm_tiled_kernel(TiledArgs a) {
+    constexpr int BN = 32 * WN;
+    constexpr int XP = kTileM * kTileK / 8 / 256;             // 16-byte X pieces per thread
+    constexpr int WP = FP8 ? BN * kTileK / 16 / 256 : BN * kTileK / 8 / 256;  // W pieces per thread
+    static_assert(XP >= 1 && WP >= 1, "tile must split over the block");
+    extern __shared__ __align__(16) uint16_t lds[];
+    uint16_t* xs = lds;                          // [2][kTileM][kTileRow]
+    uint16_t* ws = lds + 2 * kTileM * kTileRow;  // [2][BN][kTileRow]
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = wave_index();
+    const int li = lane & 15;
+    const int kg = lane >> 4;
+    const int wm = wave >> 1;
+    const int wn = wave & 1;
+
+    // XCD-aware tile of this block (tiles in weight-panel order, row tiles fastest)
+    const int nb = static_cast<int>(gridDim.x);
+    const int bid = static_cast<int>(blockIdx.x);
+    const int xcd = bid % kXcds;
+    const int tile = xcd * (nb / kXcds) + min(xcd, nb % kXcds) + bid / kXcds;
+    const int tm = tile % a.mtiles;
+    const int tn = tile / a.mtiles;
+    const int64_t m0 = static_cast<int64_t>(tm) * kTileM;
+    const int64_t n0 = static_cast<int64_t>(tn) * BN;
+    const int M = a.M, N = a.N, K = a.K;
+
+    // Operand buffers start at the tile; rows past M / N read as zeros.  The
+    // host bounds M * ldx * 2 and N * K * elem below 4 GiB.
+    const __amdgpu_buffer_rsrc_t rx =
+        make_rsrc(a.x + m0 * a.ldx, static_cast<uint32_t>((M - m0) * a.ldx * 2));
+    const __amdgpu_buffer_rsrc_t rw =
+        FP8 ? make_rsrc(static_cast<const uint8_t*>(a.w) + n0 * K, static_cast<uint32_t>((N - n0) * K))
+            : make_rsrc(static_cast<const uint16_t*>(a.w) + n0 * K, static_cast<uint32_t>((N - n0) * K * 2));
+    uint32_t xoff[XP], woff[WP];
+    int xdst[XP], wdst[WP];
+#pragma unroll
+    for (int i = 0; i < XP; ++i) {
+        const int e = tid + 256 * i;
+        const int r = e >> 3, c = (e & 7) * 8;
+        xoff[i] = static_cast<uint32_t>((r * a.ldx + c) * 2);
+        xdst[i] = r * kTileRow + c;
+    }
+#pragma unroll
+    for (int i = 0; i < WP; ++i) {
+        const int e = tid + 256 * i;
+        if constexpr (FP8) {
+            const int r = e >> 2, c = (e & 3) * 16;
+            woff[i] = static_cast<uint32_t>(r * K + c);
+            wdst[i] = r * kTileRow + c;
+        } else {
+            const int r = e >> 3, c = (e & 7) * 8;
+            woff[i] = static_cast<uint32_t>((r * K + c) * 2);
+            wdst[i] = r * kTileRow + c;
+        }
+    }
+    u32x4 xv[XP], wv[WP];
+    auto load = [&](int step) {
+        const uint32_t k0 = static_cast<uint32_t>(step) * kTileK;
+#pragma unroll
+        for (int i = 0; i < XP; ++i) xv[i] = bload(rx, xoff[i], k0 * 2);
+#pragma unroll
+        for (int i = 0; i < WP; ++i) wv[i] = bload(rw, woff[i], FP8 ? k0 : k0 * 2);
+    };
+    auto stage = [&](int buf) {
+        uint16_t* xb = xs + buf * kTileM * kTileRow;
+        uint16_t* wb = ws + buf * BN * kTileRow;
+#pragma unroll
+        for (int i = 0; i < XP; ++i) *reinterpret_cast<u32x4*>(xb + xdst[i]) = xv[i];
+#pragma unroll
+        for (int i = 0; i < WP; ++i) {
+            if constexpr (FP8) {
+                uint32_t d[8];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) e4m3x4_to_bf16<CHECK>(wv[i][q], d[2 * q], d[2 * q + 1]);
+                *reinterpret_cast<u32x4*>(wb + wdst[i]) = u32x4{d[0], d[1], d[2], d[3]};
+                *reinterpret_cast<u32x4*>(wb + wdst[i] + 8) = u32x4{d[4], d[5], d[6], d[7]};
+            } else {
+                *reinterpret_cast<u32x4*>(wb + wdst[i]) = wv[i];
+            }
+        }
+    };
+
+    // FP8: the scale row of each of the lane's output columns
+    const int nkb = (K + 127) / 128;
+    const float* srow[WN];
+    if constexpr (FP8) {
+        const int64_t nsb = ((N >> 1) + 127) / 128;
+#pragma unroll
+        for (int ni = 0; ni < WN; ++ni) {
+            const int64_t n = min(n0 + wn * 16 * WN + ni * 16 + li, static_cast<int64_t>(N) - 1);
+            const int64_t sr = a.scale_rows ? a.scale_rows[n] : (a.paired ? (n & 1) * nsb + (n >> 1) / 128 : n / 128);
+            srow[ni] = a.scales + sr * nkb;
+        }
+    }
+
+    f32x4 acc[4][WN];   // the current 128-k scale block (FP8) or the whole sum (bf16)
+    f32x4 tot[4][WN];   // FP8: the scaled sum of the finished blocks
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < WN; ++ni) {
+            acc[mi][ni] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            tot[mi][ni] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+
+    const int nsteps = K / kTileK;
+    load(0);
+    stage(0);
+    __syncthreads();
+    for (int step = 0; step < nsteps; ++step) {
+        const int buf = step & 1;
+        if (step + 1 < nsteps) load(step + 1);
+        const uint16_t* xb = xs + buf * kTileM * kTileRow;
+        const uint16_t* wb = ws + buf * BN * kTileRow;
+#pragma unroll
+        for (int j = 0; j < kTileK / 32; ++j) {
+            u32x4 af[4], bf[WN];
+#pragma unroll
+            for (int mi = 0; mi < 4; ++mi)
+                af[mi] = *reinterpret_cast<const u32x4*>(xb + (wm * 64 + mi * 16 + li) * kTileRow + 32 * j + 8 * kg);
+#pragma unroll
+            for (int ni = 0; ni < WN; ++ni)
+                bf[ni] = *reinterpret_cast<const u32x4*>(wb + (wn * 16 * WN + ni * 16 + li) * kTileRow + 32 * j + 8 * kg);
+#pragma unroll
+            for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+                for (int ni = 0; ni < WN; ++ni) acc[mi][ni] = mfma16(af[mi], bf[ni], acc[mi][ni]);
+        }
+        if constexpr (FP8) {
+            // a 128-k scale block ends every second step (and at the end of K)
+            if ((step & 1) == 1 || step + 1 == nsteps) {
+                const int kb = step >> 1;
+#pragma unroll
+                for (int ni = 0; ni < WN; ++ni) {
+                    const float sc = srow[ni][kb];
+#pragma unroll
+                    for (int mi = 0; mi < 4; ++mi) {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) tot[mi][ni][i] = fma_(sc, acc[mi][ni][i], tot[mi][ni][i]);
+                        acc[mi][ni] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                    }
+                }
+            }
+        }
+        if (step + 1 < nsteps) stage(buf ^ 1);
+        __syncthreads();
+    }
+
+    // lane (li, kg) holds rows 4 kg + i of each 16-row tile, column li of each 16-column tile
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < WN; ++ni)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int m = static_cast<int>(m0) + wm * 64 + mi * 16 + 4 * kg + i;
+                const int64_t n = n0 + wn * 16 * WN + ni * 16 + li;
+                mfma_store<EPI>(a.y, a.ldy, a.res, a.ldres, FP8 ? tot[mi][ni][i] : acc[mi][ni][i], m, n, M, N, li);
+            }
+}
+
+template <int WN, int EPI, bool FP8, bool CHECK>
+int launch_tiled(TiledArgs a, hipStream_t s) {
+    constexpr size_t shmem = tiled_lds_bytes<WN>();
+    auto* kern = gemm_tiled_kernel<WN, EPI, FP8, CHECK>;
+    static std::atomic<uint8_t> allowed[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return invalid("gemm_tiled: device ordinal");
+    if (!allowed[dev].load(std::memory_order_acquire)) {
+        bool done = false;
+        const int rc = allow_lds(reinterpret_cast<const void*>(kern), shmem, &done);
+        if (rc != HAI_OK) return rc;
+        allowed[dev].store(1, std::memory_order_release);
+    }
+    a.ntiles = static_cast<int>((a.N + 32 * WN - 1) / (32 * WN));
+    const int64_t blocks = static_cast<int64_t>(a.mtiles) * a.ntiles;
+    kern<<<dim3(static_cast<unsigned>(blocks)), dim3(256), shmem, s>>>(a);
+    return launched("gemm_tiled_kernel");
+}
+
+template <int EPI, bool FP8, bool CHECK>
+int dispatch_tiled(TiledArgs a, hipStream_t s) {
+    // 128-wide weight tiles when they give every CU at least two tiles
+    const int64_t tiles128 = static_cast<int64_t>(a.mtiles) * ((a.N + 127) / 128);
+    if (tiles128 >= 512) return launch_tiled<4, EPI, FP8, CHECK>(a, s);
+    return launch_tiled<2, EPI, FP8, CHECK>(a, s);
+}
+
+template <bool FP8, bool CHECK>
+int tiled_entry(TiledArgs& a, int epilogue, hipStream_t s) {
+    switch (epilogue) {
+        case HAI_EPI_STORE:
+            if (a.ldy < a.N) return invalid("gemm_tiled: ldy < N");
+            return dispatch_tiled<HAI_EPI_STORE, FP8, CHECK>(a, s);
+        case HAI_EPI_RESIDUAL:
+            if (a.res == nullptr || a.ldy < a.N || a.ldres < a.N) return invalid("gemm_tiled: residual operands");
+            return dispatch_tiled<HAI_EPI_RESIDUAL, FP8, CHECK>(a, s);
+        case HAI_EPI_SILU_MUL:
+            if (a.N % 2 != 0 || a.ldy < a.N / 2) return invalid("gemm_tiled: silu_mul needs even N and ldy >= N/2");
+            a.paired = FP8 ? 1 : 0;
+            return dispatch_tiled<HAI_EPI_SILU_MUL, FP8, CHECK>(a, s);
+        default:
+            return invalid("gemm_tiled: unknown epilogue");
+    }
+}
+
+int check_tiled(const void* y, const void* x, const void* w, int64_t M, int64_t N, int64_t K, int64_t ldx,
+                int elem_bytes) {
+    if (y == nullptr || x == nullptr || w == nullptr) return invalid("gemm_tiled: null pointer");
+    if (M < 0 || N < 0 || K <= 0 || K % kTileK != 0 || ldx % 8 != 0 || ldx < K)
+        return invalid("gemm_tiled: shape (need K % 64 == 0, ldx % 8 == 0, ldx >= K)");
+    if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX) return invalid("gemm_tiled: dimension too large");
+    if (N * K * elem_bytes >= (int64_t{1} << 32) || M * ldx * 2 >= (int64_t{1} << 32))
+        return invalid("gemm_tiled: W or X exceeds the 4 GiB buffer-offset range");
+    if ((M + kTileM - 1) / kTileM * ((N + 63) / 64) >= (int64_t{1} << 31)) return invalid("gemm_tiled: grid too large");
+    if (!aligned16(x) || !aligned16(w)) return invalid("gemm_tiled: x and w must be 16-byte aligned");
+    return HAI_OK;
+}
+
+}  // namespace
+
+extern "C" int hai_gemm_bf16_tiled(void* y, int64_t ldy, const void* x, int64_t ldx, const void* w, int64_t M,
+                                   int64_t N, int64_t K, int epilogue, const void* res, int64_t ld_res,
+                                   void* stream) {
+    int rc = check_tiled(y, x, w, M, N, K, ldx, 2);
+    if (rc == HAI_OK) rc = check_gemm_extents(y, ldy, x, ldx, w, 2, M, N, K, epilogue, res, ld_res);
+    if (rc != HAI_OK) return rc;
+    if (M == 0 || N == 0) return HAI_OK;
+    TiledArgs a{static_cast<uint16_t*>(y), ldy, static_cast<const uint16_t*>(x), ldx, w, nullptr, nullptr, 0,
+                static_cast<const uint16_t*>(res), ld_res, int(M), int(N), int(K),
+                static_cast<int>((M + kTileM - 1) / kTileM), 0};
+    return tiled_entry<false, false>(a, epilogue, as_stream(stream));
+}
+
+extern "C" int hai_gemm_fp8_tiled(void* y, int64_t ldy, const void* x, int64_t ldx, const void* wq,
+                                  const float* scales, const int32_t* scale_rows, int64_t M, int64_t N, int64_t K,
+                                  int epilogue, const void* res, int64_t ld_res, void* stream) {
+    if (scales == nullptr) return invalid("gemm_fp8_tiled: null scales");
+    int rc = check_tiled(y, x, wq, M, N, K, ldx, 1);
+    const int epi = epilogue & ~HAI_FP8_NO_SPECIAL_CODES;
+    if (rc == HAI_OK) rc = check_gemm_extents(y, ldy, x, ldx, wq, 1, M, N, K, epi, res, ld_res);
+    if (rc != HAI_OK) return rc;
+    if (M == 0 || N == 0) return HAI_OK;
+    TiledArgs a{static_cast<uint16_t*>(y), ldy, static_cast<const uint16_t*>(x), ldx, wq, scales, scale_rows, 0,
+                static_cast<const uint16_t*>(res), ld_res, int(M), int(N), int(K),
+                static_cast<int>((M + kTileM - 1) / kTileM), 0};
+    if ((epilogue & HAI_FP8_NO_SPECIAL_CODES) != 0) return tiled_entry<true, false>(a, epi, as_stream(stream));
+    return tiled_entry<true, true>(a, epi, as_stream(stream));
+}

@@ -25,7 +25,7 @@ WEIGHTS_BF16, WEIGHTS_FP8_BLOCK128 = 0, 1
 class EngineOptions(ctypes.Structure):
     _fields_ = [("max_context", ctypes.c_int32), ("max_verify_tokens", ctypes.c_int32),
                 ("device", ctypes.c_int32), ("use_graphs", ctypes.c_int32), ("weight_format", ctypes.c_int32),
-                ("max_batch", ctypes.c_int32), ("mfma", ctypes.c_int32)]
+                ("max_batch", ctypes.c_int32), ("mfma", ctypes.c_int32), ("prefill_rows", ctypes.c_int32)]
 
 
 class SpecStats(ctypes.Structure):
@@ -128,7 +128,8 @@ class Engine:
     through load_checkpoint)."""
 
     def __init__(self, cfg: dict, max_context: int, max_verify_tokens: int = 16, device: int = 0,
-                 use_graphs: bool = False, fp8: bool = False, batch: int = 1, mfma: bool = False):
+                 use_graphs: bool = False, fp8: bool = False, batch: int = 1, mfma: bool = False,
+                 prefill_rows: int = 0):
         from . import host
         self.lib = host()
         self.cfg = dict(cfg)
@@ -136,7 +137,7 @@ class Engine:
         self.batch = batch
         c = ModelConfig(**cfg)
         o = EngineOptions(max_context, max_verify_tokens, device, int(use_graphs),
-                          WEIGHTS_FP8_BLOCK128 if fp8 else WEIGHTS_BF16, batch, int(mfma))
+                          WEIGHTS_FP8_BLOCK128 if fp8 else WEIGHTS_BF16, batch, int(mfma), int(prefill_rows))
         self.h = self.lib.hai_engine_create(ctypes.byref(c), ctypes.byref(o))
         if not self.h:
             raise RuntimeError("hai_engine_create: " + self.lib.hai_engine_last_error(None).decode())

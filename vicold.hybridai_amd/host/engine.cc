@@ -84,6 +84,10 @@ Engine::Engine(const hai_model_config& cfg, const hai_engine_options& opt) : cfg
     // launch per forward)
     tmax_ = std::max<int64_t>(2, std::min<int64_t>(B_ == 1 ? kMaxVerifyRows : kDeltaNetMaxT, opt.max_verify_tokens));
     pchunk_ = std::min<int64_t>(tmax_, kDeltaNetMaxT);
+    if (opt.prefill_rows > tmax_) {
+        pchunk_ = opt.prefill_rows;
+        fast_prefill_ = true;
+    }
     cap_ = std::max<int64_t>(opt.max_context, tmax_ + 1);
     ring_ = 32;
     nslots_ = tmax_ + 1;
@@ -107,6 +111,10 @@ Engine::Engine(const hai_model_config& cfg, const hai_engine_options& opt) : cfg
     }
     if (B_ > 64) {
         error_ = "max_batch above 64";
+        return;
+    }
+    if (opt.prefill_rows < 0 || opt.prefill_rows > 8192 || B_ * pchunk_ > 65536) {
+        error_ = "prefill_rows outside 0..8192 (or more than 65536 rows per chunk over the batch)";
         return;
     }
     if (hai_set_device(opt.device) != HAI_OK || hai_stream_create(&stream_) != HAI_OK) {
@@ -297,7 +305,7 @@ int Engine::alloc_all() {
     // ---- workspace ----
     nproj_ = std::max(d.Nin, d.Nqkv);
     const int64_t T = tmax_;
-    const int64_t R = B_ * tmax_;  // rows of one launch
+    const int64_t R = B_ * std::max(tmax_, pchunk_);  // rows of one forward (verify step or prompt chunk)
     auto carve_work = [&](Carver& cv) {
         d_ids_ = cv.take<int64_t>(R);
         d_vids_ = cv.take<int64_t>(R + 1);
@@ -327,8 +335,16 @@ int Engine::alloc_all() {
         mh_[1] = cv.take<uint16_t>(B_ * H);
         h_prev_ = cv.take<uint16_t>(B_ * H);
         rec_hidden_ = cv.take<uint16_t>(B_ * H);
-        gqa_scratch_ = cv.take<char>(std::max(hai_gqa_scratch_bytes(B_, T, d.nq, d.D, cap_),
-                                              mfma_ ? hai_gqa_mfma_scratch_bytes(B_, T, d.nq, d.D, cap_) : 0));
+        // a prompt chunk's split plan depends on its row count, and a short
+        // last chunk can take more splits (and more scratch) than a full one
+        size_t prefill_scratch = 0;
+        if (fast_prefill_)
+            for (int64_t t = 1; t <= pchunk_; ++t)
+                prefill_scratch =
+                    std::max(prefill_scratch, hai_gqa_mfma_plan_scratch_bytes(B_, t, d.nq, d.nkv, d.D, cap_));
+        gqa_scratch_ = cv.take<char>(std::max({hai_gqa_scratch_bytes(B_, T, d.nq, d.D, cap_),
+                                               mfma_ ? hai_gqa_mfma_scratch_bytes(B_, T, d.nq, d.D, cap_) : size_t{0},
+                                               prefill_scratch}));
         if (mfma_) {
             const int64_t mrows = std::min<int64_t>(128, R);
             size_t ws = 0;
@@ -528,6 +544,13 @@ int Engine::gemm(uint16_t* y, int64_t ldy, const uint16_t* x, int64_t ldx, const
                  int64_t K, int epi, const uint16_t* res, int64_t ldres) {
     HAI_TRY(flush_pending());  // the workspace is about to be reused
     if (prof_record_) prof_calls_.push_back({y, ldy, x, ldx, w, M, N, K, epi, res, ldres, nullptr, nullptr});
+    if (use_mfma(M) && M > kTiledMinRows && K % 64 == 0) {
+        // prompt-sized row counts: both operands tiled, compute bound
+        if (w.q != nullptr)
+            return hai_gemm_fp8_tiled(y, ldy, x, ldx, w.q, w.s, w.map, M, N, K, epi | HAI_FP8_NO_SPECIAL_CODES, res,
+                                      ldres, stream_);
+        return hai_gemm_bf16_tiled(y, ldy, x, ldx, w.w, M, N, K, epi, res, ldres, stream_);
+    }
     if (use_mfma(M) && epi == HAI_EPI_RESIDUAL && res == y && ldres == ldy && M <= 128 && N % 8 == 0 && N <= 8192 &&
         !prof_record_) {
         // residual in place: leave the split partials for the next RMSNorm
@@ -636,7 +659,7 @@ int Engine::attention_layer(const LayerWeights& L, int64_t T, uint16_t* h, const
                                              rope_sin_, cap_, B_, T, d.nq, d.nkv, d.D, d.R, lens, 0, cfg_.rms_eps,
                                              stream_));
     // tolerance mode: Q.K^T and P.V on the matrix cores
-    const auto attend = mfma_ ? hai_gqa_verify_mfma_bf16 : hai_gqa_verify_bf16;
+    const auto attend = (mfma_ || fast_) ? hai_gqa_verify_mfma_bf16 : hai_gqa_verify_bf16;
     HAI_TRY(attend(att_, q_, gate_, kc, vc, cap_, gqa_scratch_, B_, T, d.nq, d.nkv, d.D, lens,
                    static_cast<int32_t>(T), cap_, stream_));
     return gemm(h, d.H, att_, d.qw, lin(L.w_o, L.f_o), rows, d.H, d.qw, HAI_EPI_RESIDUAL, h, d.H);
@@ -655,7 +678,7 @@ int Engine::mlp(const LayerWeights& L, int64_t T, uint16_t* h) {
 // target_forward (generator.cc:550-634): T rows of every sequence (row b*T+t)
 // on top of its committed caches; hf_ = post-final-norm hidden, logits_ =
 // lm_head.  Committed lengths are not advanced here.
-int Engine::forward_target(const int64_t* d_ids, int64_t T, bool write_all_slots) {
+int Engine::forward_target(const int64_t* d_ids, int64_t T, bool write_all_slots, Logits logits) {
     pending_ = PendingResidual{};  // a forward ends with a norm, which completes any residual; only
                                    // a failed one leaves a record, for rows this forward overwrites
     const auto& d = d_;
@@ -667,9 +690,10 @@ int Engine::forward_target(const int64_t* d_ids, int64_t T, bool write_all_slots
         } else {
             // qwen_deltanet_reference (qwen_reference.cc:205-258).  The
             // DeltaNet kernel takes at most 16 tokens per launch: a verify
-            // of 17 rows (width 16, one sequence) runs as two launches, the
-            // second starting from the state the first left in slot
-            // (L + 16) % nslots and reading its conv history from the ring.
+            // of 17 rows (width 16, one sequence) or a prompt chunk runs as
+            // launches of 16, each starting from the state the previous one
+            // left in slot (L + 16) % nslots and reading its conv history
+            // from the ring (the library issues them).
             if (fp8_) {
                 // FP8 qkv|z with the norm fused, writing the normalised rows;
                 // the bf16 a|b projection of each head is formed from them
@@ -677,12 +701,10 @@ int Engine::forward_target(const int64_t* d_ids, int64_t T, bool write_all_slots
                 HAI_TRY(norm_gemm(proj_, d.Nin, h_, L.in_ln, xn_, Lin(L.f_in), rows, d.C + d.vw, HAI_EPI_STORE,
                                   nullptr, 0));
                 HAI_TRY(flush_pending());
-                for (int64_t t0 = 0; t0 < T; t0 += kDeltaNetMaxT)
-                    HAI_TRY(hai_deltanet_verify_ab_bf16(
-                        dnout_ + t0 * d.vw, d.vw, proj_ + t0 * d.Nin, d.Nin, 0, d.C, xn_ + t0 * d.H, d.H, L.w_ab, d.H,
-                        L.conv_w, L.ring, ring_, L.state, nslots_, write_all_slots ? 1 : 0, L.a_log, L.dt_bias,
-                        L.lin_norm, d_tlen_, static_cast<int32_t>(t0), B_, std::min(kDeltaNetMaxT, T - t0), d.nk,
-                        d.nv, d.dk, d.dv, d.Kc, cfg_.rms_eps, stream_));
+                HAI_TRY(hai_deltanet_verify_ab_bf16(dnout_, d.vw, proj_, d.Nin, 0, d.C, xn_, d.H, L.w_ab, d.H,
+                                                    L.conv_w, L.ring, ring_, L.state, nslots_, write_all_slots ? 1 : 0,
+                                                    L.a_log, L.dt_bias, L.lin_norm, d_tlen_, 0, B_, T, d.nk, d.nv,
+                                                    d.dk, d.dv, d.Kc, cfg_.rms_eps, stream_));
             } else if (use_mfma(rows)) {
                 // matrix-core mode: the qkv|z rows only (16384 rows at the 27B
                 // shape, whole 64-row tiles that load every CU alike, where
@@ -691,27 +713,31 @@ int Engine::forward_target(const int64_t* d_ids, int64_t T, bool write_all_slots
                 HAI_TRY(norm_gemm(proj_, d.Nin, h_, L.in_ln, xn_, L.w_in, rows, d.C + d.vw, HAI_EPI_STORE, nullptr,
                                   0));
                 HAI_TRY(flush_pending());
-                for (int64_t t0 = 0; t0 < T; t0 += kDeltaNetMaxT)
-                    HAI_TRY(hai_deltanet_verify_ab_bf16(
-                        dnout_ + t0 * d.vw, d.vw, proj_ + t0 * d.Nin, d.Nin, 0, d.C, xn_ + t0 * d.H, d.H,
-                        L.w_in + (d.C + d.vw) * d.H, d.H, L.conv_w, L.ring, ring_, L.state, nslots_,
-                        write_all_slots ? 1 : 0, L.a_log, L.dt_bias, L.lin_norm, d_tlen_, static_cast<int32_t>(t0),
-                        B_, std::min(kDeltaNetMaxT, T - t0), d.nk, d.nv, d.dk, d.dv, d.Kc, cfg_.rms_eps, stream_));
+                HAI_TRY(hai_deltanet_verify_ab_bf16(dnout_, d.vw, proj_, d.Nin, 0, d.C, xn_, d.H,
+                                                    L.w_in + (d.C + d.vw) * d.H, d.H, L.conv_w, L.ring, ring_,
+                                                    L.state, nslots_, write_all_slots ? 1 : 0, L.a_log, L.dt_bias,
+                                                    L.lin_norm, d_tlen_, 0, B_, T, d.nk, d.nv, d.dk, d.dv, d.Kc,
+                                                    cfg_.rms_eps, stream_));
             } else {
                 HAI_TRY(norm_gemm(proj_, d.Nin, h_, L.in_ln, nullptr, L.w_in, rows, d.Nin, HAI_EPI_STORE, nullptr,
                                   0));
-                for (int64_t t0 = 0; t0 < T; t0 += kDeltaNetMaxT)
-                    HAI_TRY(hai_deltanet_verify_bf16(
-                        dnout_ + t0 * d.vw, d.vw, proj_ + t0 * d.Nin, d.Nin, 0, d.C, d.C + d.vw, d.C + d.vw + d.nv,
-                        L.conv_w, L.ring, ring_, L.state, nslots_, write_all_slots ? 1 : 0, L.a_log, L.dt_bias,
-                        L.lin_norm, d_tlen_, static_cast<int32_t>(t0), B_, std::min(kDeltaNetMaxT, T - t0), d.nk,
-                        d.nv, d.dk, d.dv, d.Kc, cfg_.rms_eps, stream_));
+                HAI_TRY(hai_deltanet_verify_bf16(dnout_, d.vw, proj_, d.Nin, 0, d.C, d.C + d.vw, d.C + d.vw + d.nv,
+                                                 L.conv_w, L.ring, ring_, L.state, nslots_, write_all_slots ? 1 : 0,
+                                                 L.a_log, L.dt_bias, L.lin_norm, d_tlen_, 0, B_, T, d.nk, d.nv, d.dk,
+                                                 d.dv, d.Kc, cfg_.rms_eps, stream_));
             }
             HAI_TRY(gemm(h_, d.H, dnout_, d.vw, lin(L.w_out, L.f_out), rows, d.H, d.vw, HAI_EPI_RESIDUAL, h_, d.H));
         }
         HAI_TRY(mlp(L, T, h_));
     }
-    return norm_gemm(logits_, d.V, h_, final_norm_, hf_, lm_head_, rows, d.V, HAI_EPI_STORE, nullptr, 0);
+    if (logits == Logits::kAll)
+        return norm_gemm(logits_, d.V, h_, final_norm_, hf_, lm_head_, rows, d.V, HAI_EPI_STORE, nullptr, 0);
+    // a prompt chunk: the final norm of every row (the MTP rows read them),
+    // lm_head for the last row of each sequence (rows 0..B-1 of logits_) or none
+    HAI_TRY(flush_pending());
+    HAI_TRY(hai_rmsnorm_bf16(hf_, d.H, h_, d.H, final_norm_, rows, d.H, cfg_.rms_eps, 1, stream_));
+    if (logits == Logits::kNone) return HAI_OK;
+    return gemm(logits_, d.V, hf_ + (T - 1) * d.H, T * d.H, lm_head_, B_, d.V, d.H, HAI_EPI_STORE, nullptr, 0);
 }
 
 // MTP input rows x = fc([RMSNorm(emb) | RMSNorm(hidden)]) (generator.cc:152-160)
@@ -764,6 +790,12 @@ int Engine::mtp_draft_step(const int64_t* d_id, const uint16_t* d_hin, uint16_t*
 // each chunk followed by its MTP prompt rows (emb(t_i) paired with the
 // hidden of t_i).  ids [B][P]; hidden_out [B][P][H], logits_out [B][P][V].
 int Engine::prefill_chunks(const int32_t* ids, int64_t P, uint16_t* hidden_out, uint16_t* logits_out) {
+    // fast prefill: every GEMM and the attention of the chunks on the matrix cores
+    struct FastScope {
+        bool& flag;
+        FastScope(bool& f, bool on) : flag(f) { flag = on; }
+        ~FastScope() { flag = false; }
+    } scope(fast_, fast_prefill_);
     const auto& d = d_;
     std::vector<int64_t> chunk(static_cast<size_t>(B_ * pchunk_));
     for (int64_t off = 0; off < P; off += pchunk_) {
@@ -771,7 +803,14 @@ int Engine::prefill_chunks(const int32_t* ids, int64_t P, uint16_t* hidden_out, 
         for (int64_t b = 0; b < B_; ++b)
             for (int64_t t = 0; t < T; ++t) chunk[static_cast<size_t>(b * T + t)] = ids[b * P + off + t];
         HAI_TRY(hai_memcpy_h2d(d_ids_, chunk.data(), static_cast<size_t>(B_ * T) * 8, stream_));
-        HAI_TRY(forward_target(d_ids_, T, false));
+        // the verify-step prefill keeps every row's logits (one weight
+        // stream serves all rows); a fast chunk computes only the last row's,
+        // and only in the last chunk
+        const bool last_chunk = off + T == P;
+        const Logits lg = (!fast_prefill_ || logits_out != nullptr) ? Logits::kAll
+                          : last_chunk                             ? Logits::kLast
+                                                                   : Logits::kNone;
+        HAI_TRY(forward_target(d_ids_, T, false, lg));
         HAI_TRY(hai_add_i32(d_tlen_, nullptr, static_cast<int32_t>(T), B_, stream_));
         for (int64_t b = 0; b < B_; ++b) {
             if (hidden_out)
@@ -785,8 +824,11 @@ int Engine::prefill_chunks(const int32_t* ids, int64_t P, uint16_t* hidden_out, 
         if (off + T == P) {
             // the last prompt row of every sequence: its argmax is the first
             // target and its hidden feeds the first draft
-            HAI_TRY(hai_argmax_rows_bf16(d_next_, logits_ + (T - 1) * d.V, T * d.V, B_, d.V, argmax_scratch_,
-                                         stream_));
+            if (lg == Logits::kLast)
+                HAI_TRY(hai_argmax_rows_bf16(d_next_, logits_, d.V, B_, d.V, argmax_scratch_, stream_));
+            else
+                HAI_TRY(hai_argmax_rows_bf16(d_next_, logits_ + (T - 1) * d.V, T * d.V, B_, d.V, argmax_scratch_,
+                                             stream_));
             for (int64_t b = 0; b < B_; ++b)
                 HAI_TRY(hai_memcpy_d2d(h_prev_ + b * d.H, hf_ + (b * T + T - 1) * d.H, static_cast<size_t>(d.H) * 2,
                                        stream_));

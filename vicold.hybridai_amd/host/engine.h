@@ -219,7 +219,12 @@ private:
     // or one MFMA launch per <= 128 rows when the engine runs in tolerance
     // mode (hai_engine_options::mfma) and M >= kMfmaMinRows.
     static constexpr int64_t kMfmaMinRows = 4;
-    bool use_mfma(int64_t M) const { return mfma_ && M >= kMfmaMinRows; }
+    // above this many rows a matrix-core GEMM tiles both operands
+    // (hai_gemm_*_tiled) instead of streaming the weights once per 128 rows
+    static constexpr int64_t kTiledMinRows = 128;
+    bool use_mfma(int64_t M) const { return (mfma_ || fast_) && M >= kMfmaMinRows; }
+    // which rows of a forward get lm_head logits
+    enum class Logits { kAll, kLast, kNone };
     // A residual MFMA GEMM whose K-split partials wait in the workspace: the
     // RMSNorm of the same rows completes them (hai_mfma_residual_rmsnorm_bf16)
     // in one launch; anything else completes them first (flush_pending).
@@ -237,7 +242,7 @@ private:
     int norm_gemm(uint16_t* y, int64_t ldy, const uint16_t* x, const uint16_t* nw, uint16_t* xn_out,
                   const Lin& w, int64_t M, int64_t N, int epi, const uint16_t* res, int64_t ldres);
     Lin lin(const uint16_t* w, const Fp8Linear& f) const { return fp8_ ? Lin(f) : Lin(w); }
-    int forward_target(const int64_t* d_ids, int64_t T, bool write_all_slots);
+    int forward_target(const int64_t* d_ids, int64_t T, bool write_all_slots, Logits logits = Logits::kAll);
     int attention_layer(const LayerWeights& L, int64_t T, uint16_t* h, const int32_t* lens,
                         uint16_t* kc, uint16_t* vc);
     int mlp(const LayerWeights& L, int64_t T, uint16_t* h);
@@ -273,7 +278,9 @@ private:
     int64_t B_ = 1;       // sequences
     int64_t cap_ = 0;     // KV capacity per sequence
     int64_t tmax_ = 0;    // largest verify T (rows per sequence)
-    int64_t pchunk_ = 0;  // prompt rows per prefill forward (<= 16: one DeltaNet launch)
+    int64_t pchunk_ = 0;  // prompt rows per sequence and prefill forward
+    bool fast_prefill_ = false;  // prompts prefill in large chunks on the matrix cores
+    bool fast_ = false;          // inside such a chunk: matrix-core GEMMs and attention
     bool mfma_ = false;   // tolerance mode: MFMA GEMMs (4+ rows) and attention
     int64_t ring_ = 0;
     int64_t nslots_ = 0;
