@@ -507,6 +507,67 @@ def test_deltanet_verify_rollback(nk, nv, dk, dv, steps, split):
         assert np.array_equal(dev_state.view(np.uint32), want_state.view(np.uint32)), f"state after step {si}"
 
 
+@pytest.mark.parametrize("nk,nv,dk,T,Kc", [(2, 6, 64, 37, 4), (16, 48, 128, 100, 4), (4, 4, 64, 16, 3),
+                                         (16, 48, 128, 32, 4)])
+def test_deltanet_prefill_against_oracle(nk, nv, dk, T, Kc):
+    """hai_deltanet_prefill_bf16 (prompt chunks, 16 threads per value column,
+    tolerance mode) against the oracle's conv + recurrence of the same T
+    tokens for two sequences with different histories (conv inputs from the
+    ring, initial state from slot L % nslots): outputs within the bf16 / fp32
+    reassociation bound, the state within 1e-4 of its scale, and the conv
+    ring's entries for the chunk's last positions bit for bit.  T = 32
+    wraps the 32-entry ring onto the entries the chunk reads first."""
+    rng = np.random.default_rng(nv * 7 + T)
+    B, dv = 2, dk
+    kw, vw = nk * dk, nv * dv
+    C = 2 * kw + vw
+    hist = Kc - 1
+    width = C + vw + 2 * nv
+    ring, nslots = 32, 18
+    cw, cwb = rand_bf16(rng, (C, Kc), 0.3)
+    al, alb = rand_bf16(rng, (nv,), 0.5)
+    dt, dtb = rand_bf16(rng, (nv,), 0.5)
+    nw, nwb = rand_bf16(rng, (dv,), 0.5)
+    proj, pb = rand_bf16(rng, (B * T, width))
+    lens0 = np.array([5, 40], np.int32)
+    ring0 = rng.standard_normal((B, ring, C)).astype(np.float32)
+    ring0b = hai.bf16_bits(ring0)
+    ring0 = hai.bf16_to_f32(ring0b)
+    states = (rng.standard_normal((B, nv, dk, dv)) * 0.1).astype(np.float32)
+    st_dev = np.zeros((nslots, B, nv, dv, dk), np.float32)
+    for b in range(B):
+        st_dev[lens0[b] % nslots, b] = _to_tiled(states[b], nv, dk, dv)
+    dstate, dring, lens = dev(st_dev), dev(ring0b), dev(lens0)
+    dout = out_buf(B * T * vw * 2)
+    wsb = kern().hai_deltanet_prefill_workspace_bytes(B, T, nv, dv)
+    dws = out_buf(wsb)
+    # device copies held by name: a temporary's memory would be freed before the launch
+    dp, dcw, dal, ddt, dnw = dev(pb), dev(cwb), dev(alb), dev(dtb), dev(nwb)
+    hai.check(kern().hai_deltanet_prefill_bf16(dout.ptr, vw, dp.ptr, width, 0, C, C + vw, C + vw + nv, dcw.ptr,
+                                               dring.ptr, ring, dstate.ptr, nslots, dal.ptr, ddt.ptr, dnw.ptr,
+                                               lens.ptr, 0, B, T, nk, nv, dk, dv, Kc, 1e-6, dws.ptr, wsb, None),
+              "deltanet_prefill")
+    got = hai.bf16_to_f32(dout.download(np.uint16)).reshape(B, T, vw)
+    st_got = dstate.download(np.float32).reshape(nslots, B, nv, dv, dk)
+    ring_got = dring.download(np.uint16).reshape(B, ring, C)
+    for b in range(B):
+        L = int(lens0[b])
+        pr = proj[b * T:(b + 1) * T]
+        conv_state = np.stack([ring0[b, (L - hist + i) % ring] if L - hist + i >= 0 else np.zeros(C, np.float32)
+                               for i in range(hist)], axis=1)
+        q, k, v, _ = orc.deltanet_conv(pr[:, :C], cw, conv_state, T, nk, nv, dk, dv, Kc)
+        want, st = orc.deltanet_recurrent(q, k, v, pr[:, C + vw:C + vw + nv], pr[:, C + vw + nv:], pr[:, C:C + vw],
+                                          al, dt, nw, states[b], T, nk, nv, dk, dv)
+        err = np.abs(got[b] - want)
+        assert (err <= 2.0 ** -7 * np.abs(want) + 1e-3 * np.abs(want).max()).all(), (b, float(err.max()))
+        st_want = _to_tiled(st, nv, dk, dv)
+        st_err = np.abs(st_got[(L + T) % nslots, b] - st_want).max()
+        assert st_err <= 1e-4 * np.abs(st_want).max(), (b, float(st_err))
+        for i in range(hist):
+            pos = L + T - hist + i
+            assert np.array_equal(ring_got[b, pos % ring], pb.reshape(B, T, width)[b, T - hist + i, :C]), (b, i)
+
+
 @pytest.mark.parametrize("B,nk,nv,dk,T,Kc,ab", [(3, 2, 6, 64, 40, 4, False), (2, 16, 48, 128, 33, 4, True),
                                                 (1, 4, 4, 64, 100, 3, False)])
 def test_deltanet_prompt_chunk_equals_16_token_launches(B, nk, nv, dk, T, Kc, ab):

@@ -44,7 +44,7 @@ CXX_FLAGS = ["-O2", "-fPIC", "-std=c++20", "-Wall", "-Wextra", "-Wno-unused-para
              f"-I{INCLUDE}", f"-I{HOST}"]
 
 KERNEL_SOURCES = ["hai_runtime.hip", "hai_gemm.hip", "hai_gemm_fp8.hip", "hai_gemm_mfma.hip", "hai_norm.hip", "hai_attention.hip",
-                  "hai_deltanet.hip", "hai_argmax.hip"]
+                  "hai_deltanet.hip", "hai_deltanet_prefill.hip", "hai_argmax.hip"]
 
 
 MANIFEST = LIB / "build_manifest.json"

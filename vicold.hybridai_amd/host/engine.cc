@@ -353,6 +353,10 @@ int Engine::alloc_all() {
             mfma_ws_bytes_ = ws;
             mfma_ws_ = ws > 0 ? cv.take<char>(ws) : nullptr;
         }
+        if (fast_prefill_) {
+            dn_ws_bytes_ = static_cast<int64_t>(hai_deltanet_prefill_workspace_bytes(B_, pchunk_, d.nv, d.dv));
+            dn_ws_ = cv.take<char>(static_cast<size_t>(dn_ws_bytes_));
+        }
         argmax_scratch_ = cv.take<char>(hai_argmax_scratch_bytes(R, d.V));
         rope_cos_ = cv.take<float>(cap_ * std::max<int64_t>(1, d.R / 2));
         rope_sin_ = cv.take<float>(cap_ * std::max<int64_t>(1, d.R / 2));
@@ -694,7 +698,25 @@ int Engine::forward_target(const int64_t* d_ids, int64_t T, bool write_all_slots
             // launches of 16, each starting from the state the previous one
             // left in slot (L + 16) % nslots and reading its conv history
             // from the ring (the library issues them).
-            if (fp8_) {
+            if (fast_) {
+                // a prompt chunk: the whole in_proj [qkv | z | a | b] on the
+                // tiled GEMMs (FP8: the bf16 a|b rows as a GEMM of their own
+                // over the normalised rows), then the prefill DeltaNet kernel
+                if (fp8_) {
+                    HAI_TRY(norm_gemm(proj_, d.Nin, h_, L.in_ln, xn_, Lin(L.f_in), rows, d.C + d.vw, HAI_EPI_STORE,
+                                      nullptr, 0));
+                    HAI_TRY(gemm(proj_ + d.C + d.vw, d.Nin, xn_, d.H, L.w_ab, rows, 2 * d.nv, d.H, HAI_EPI_STORE,
+                                 nullptr, 0));
+                } else {
+                    HAI_TRY(norm_gemm(proj_, d.Nin, h_, L.in_ln, nullptr, L.w_in, rows, d.Nin, HAI_EPI_STORE, nullptr,
+                                      0));
+                }
+                HAI_TRY(flush_pending());
+                HAI_TRY(hai_deltanet_prefill_bf16(dnout_, d.vw, proj_, d.Nin, 0, d.C, d.C + d.vw, d.C + d.vw + d.nv,
+                                                  L.conv_w, L.ring, ring_, L.state, nslots_, L.a_log, L.dt_bias,
+                                                  L.lin_norm, d_tlen_, 0, B_, T, d.nk, d.nv, d.dk, d.dv, d.Kc,
+                                                  cfg_.rms_eps, dn_ws_, dn_ws_bytes_, stream_));
+            } else if (fp8_) {
                 // FP8 qkv|z with the norm fused, writing the normalised rows;
                 // the bf16 a|b projection of each head is formed from them
                 // inside the DeltaNet kernel (no launch of its own)

@@ -281,6 +281,8 @@ private:
     int64_t pchunk_ = 0;  // prompt rows per sequence and prefill forward
     bool fast_prefill_ = false;  // prompts prefill in large chunks on the matrix cores
     bool fast_ = false;          // inside such a chunk: matrix-core GEMMs and attention
+    char* dn_ws_ = nullptr;      // prefill DeltaNet outputs before the gated norm
+    int64_t dn_ws_bytes_ = 0;
     bool mfma_ = false;   // tolerance mode: MFMA GEMMs (4+ rows) and attention
     int64_t ring_ = 0;
     int64_t nslots_ = 0;
