@@ -322,15 +322,28 @@ def run_decode(hai, E, args, fp8: bool, steps: int):
     P, NEW = args.prompt, args.new
     tag = "fp8" if fp8 else "bf16"
     t0 = time.perf_counter()
-    eng = E.Engine(cfg, max_context=P + NEW + 32, max_verify_tokens=16, use_graphs=args.graphs, fp8=fp8)
+    eng = E.Engine(cfg, max_context=P + NEW + 32, max_verify_tokens=16, use_graphs=args.graphs, fp8=fp8,
+                   prefill_rows=args.prefill_rows)
     eng.init_synthetic(seed=0, std=0.02)
     hai.synchronize()
     log(f"[{tag}] engine up: {eng.weight_bytes() / 1e9:.2f} GB weights in HBM, {time.perf_counter() - t0:.1f}s")
     prompt = E.synthetic_prompt(0, P, cfg["vocab"])
+    prefill = {"tokens": P}
+    if not fp8:
+        # the prompt through the verify step (16 rows at a time, bit-exact), then the fast prefill
+        eng.set_prefill_rows(0)
+        t0 = time.perf_counter()
+        eng.prefill(prompt, NEW)
+        prefill["verify_path_s"] = round(time.perf_counter() - t0, 4)
+        prefill["verify_path_tok_s"] = round(P / prefill["verify_path_s"], 1)
+        eng.set_prefill_rows(args.prefill_rows)
     t0 = time.perf_counter()
     eng.prefill(prompt, NEW)
     prefill_s = time.perf_counter() - t0
-    log(f"[{tag}] prefill of {P} tokens: {prefill_s:.2f}s")
+    prefill.update({"rows_per_chunk": args.prefill_rows, "seconds": round(prefill_s, 4),
+                    "tok_s": round(P / prefill_s, 1)})
+    log(f"[{tag}] prefill of {P} tokens: {prefill_s:.3f}s in chunks of {args.prefill_rows} rows"
+        + (f" (verify path {prefill['verify_path_s']:.2f}s)" if "verify_path_s" in prefill else ""))
 
     out = np.zeros(NEW, np.int32)
     n0, _ = eng.spec_rounds(args.warmup, args.width, out)
@@ -357,7 +370,7 @@ def run_decode(hai, E, args, fp8: bool, steps: int):
     if not fp8 and args.forced_rounds > 0:
         forced = run_forced(hai, eng, E, args, prompt, tag)
     eng.close()
-    return value, dt, rounds, emitted, st, prof, prefill_s, forced
+    return value, dt, rounds, emitted, st, prof, prefill, forced
 
 
 def run_forced(hai, eng, E, args, prompt, tag: str) -> dict:
@@ -410,7 +423,8 @@ def run_batch(hai, E, args, name: str, B: int, P: int, NEW: int, width: int, fp8
     cfg = E.QWEN27B
     t0 = time.perf_counter()
     cap = P + (width + 2) * NEW + 32
-    eng = E.Engine(cfg, max_context=cap, max_verify_tokens=16, fp8=fp8, batch=B, mfma=True)
+    eng = E.Engine(cfg, max_context=cap, max_verify_tokens=16, fp8=fp8, batch=B, mfma=True,
+                   prefill_rows=args.batch_prefill_rows)
     eng.init_synthetic(seed=0, std=0.02)
     hai.synchronize()
     log(f"[{name}] engine up: B={B}, {eng.weight_bytes() / 1e9:.2f} GB weights, {time.perf_counter() - t0:.1f}s")
@@ -441,7 +455,8 @@ def run_batch(hai, E, args, name: str, B: int, P: int, NEW: int, width: int, fp8
         "verify_ms": round(prof["verify_ms"], 3), "verify_rows": B * (width + 1),
         "verify_bytes": round(prof["step_bytes"]), "verify_hbm_frac": round(step_gbs / HBM_PEAK_GBS, 4),
         "gemm_gb_s": round(gemm_gbs, 1), "gemm_launches": prof["gemm_launches"],
-        "draft_ms": round(prof["draft_ms"], 3), "prefill_s": round(prefill_s, 2),
+        "draft_ms": round(prof["draft_ms"], 3), "prefill_s": round(prefill_s, 3),
+        "prefill_tok_s": round(B * P / prefill_s, 1), "prefill_rows_per_chunk": args.batch_prefill_rows,
         "acceptance_rate": round(st["accepted"] / max(1, st["proposed"]), 4),
     }
     log(f"[{name}] {emitted} tokens in {dt:.2f}s -> {res['value']} tok/s; verify {prof['verify_ms']:.2f} ms "
@@ -455,6 +470,11 @@ def main():
     ap.add_argument("--steps", type=int, default=100, help="timed speculative rounds")
     ap.add_argument("--warmup", type=int, default=8, help="untimed rounds before timing")
     ap.add_argument("--prompt", type=int, default=1024)
+    ap.add_argument("--prefill-rows", type=int, default=1024,
+                    help="prompt rows per fast-prefill chunk of the bs=1 engines (the verify-path prefill is "
+                         "timed beside it)")
+    ap.add_argument("--batch-prefill-rows", type=int, default=512,
+                    help="prompt rows per sequence and fast-prefill chunk of the C4 / C5 engines")
     ap.add_argument("--new", type=int, default=256)
     ap.add_argument("--width", type=int, default=1)
     ap.add_argument("--profile-iters", type=int, default=5)
@@ -499,7 +519,7 @@ def main():
         del src, dst
 
     P, NEW = args.prompt, args.new
-    nat_value, dt, rounds, emitted, st, prof, prefill_s, forced = run_decode(hai, E, args, fp8=False,
+    nat_value, dt, rounds, emitted, st, prof, prefill, forced = run_decode(hai, E, args, fp8=False,
                                                                             steps=args.steps)
     verify_ms = prof["verify_ms"]
     gemm_gbs = prof["gemm_bytes"] / (prof["gemm_ms"] * 1e-3) / 1e9
@@ -545,7 +565,7 @@ def main():
         "draft_ms": round(prof["draft_ms"], 4),
         "acceptance_rate": forced["acceptance_rate"] if forced else round(st["accepted"] / max(1, st["proposed"]), 4),
         "tokens_per_round": round(v_tokens / v_rounds, 4),
-        "prefill_s": round(prefill_s, 3),
+        "prefill": prefill,
         "roofline": {
             "bound": "hbm",
             "achieved": round(gemm_gbs, 1),

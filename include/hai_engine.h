@@ -194,6 +194,12 @@ int hai_engine_spec_rounds(void* engine, int64_t rounds, int64_t width, int32_t*
  * generate_speculative does, but from a device copy made once here (no host
  * round trip per draft).  tokens == NULL or n == 0 clears them. */
 int hai_engine_set_draft_override(void* engine, const int32_t* tokens, int64_t n);
+/* Prefill mode of the next prompts: rows <= the verify rows (0 included)
+ * prefill through the verify step (bit-exact when mfma = 0), larger values
+ * up to the engine's hai_engine_options::prefill_rows run the fast prefill
+ * in chunks of that many rows.  Larger values than the engine was created
+ * for are rejected (its buffers are sized then). */
+int hai_engine_set_prefill_rows(void* engine, int64_t rows);
 int hai_engine_profile_verify(void* engine, int64_t T, int64_t iters, hai_verify_profile* out);
 
 #ifdef __cplusplus

@@ -75,6 +75,7 @@ def bind(lib: ctypes.CDLL) -> ctypes.CDLL:
                                            ctypes.POINTER(SpecStats)]
     lib.hai_engine_profile_verify.argtypes = [VP, I64, I64, ctypes.POINTER(VerifyProfile)]
     lib.hai_engine_set_draft_override.argtypes = [VP, I32P, I64]
+    lib.hai_engine_set_prefill_rows.argtypes = [VP, I64]
     lib.hai_model_config_load.argtypes = [ctypes.c_char_p, ctypes.POINTER(ModelConfig), ctypes.POINTER(ctypes.c_int64),
                                           I64, ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int32),
                                           ctypes.c_char_p, I64]
@@ -90,7 +91,7 @@ def bind(lib: ctypes.CDLL) -> ctypes.CDLL:
     for n in ("hai_engine_init_synthetic", "hai_engine_forward", "hai_engine_generate_greedy",
               "hai_engine_generate_speculative", "hai_engine_prefill", "hai_engine_spec_rounds",
               "hai_engine_profile_verify", "hai_engine_forward_batch", "hai_engine_generate_speculative_batch",
-              "hai_engine_set_draft_override"):
+              "hai_engine_set_draft_override", "hai_engine_set_prefill_rows"):
         getattr(lib, n).restype = ctypes.c_int
     return lib
 
@@ -274,6 +275,10 @@ class Engine:
         t = _i32(tokens).reshape(self.batch, -1)
         self._check(self.lib.hai_engine_set_draft_override(self.h, t.ctypes.data_as(I32P), t.shape[1]),
                     "set_draft_override")
+
+    def set_prefill_rows(self, rows):
+        """Prefill mode of the next prompts (0: through the verify step)."""
+        self._check(self.lib.hai_engine_set_prefill_rows(self.h, int(rows)), "set_prefill_rows")
 
     def profile_verify(self, T, iters):
         pr = VerifyProfile()

@@ -162,6 +162,11 @@ int hai_engine_set_draft_override(void* engine, const int32_t* tokens, int64_t n
     return as_engine(engine)->set_draft_override(tokens, n);
 }
 
+int hai_engine_set_prefill_rows(void* engine, int64_t rows) {
+    if (!engine) return HAI_ERR_INVALID_ARGUMENT;
+    return as_engine(engine)->set_prefill_rows(rows);
+}
+
 int hai_engine_profile_verify(void* engine, int64_t T, int64_t iters, hai_verify_profile* out) {
     if (!engine || !out) return HAI_ERR_INVALID_ARGUMENT;
     return as_engine(engine)->profile_verify(T, iters, out);

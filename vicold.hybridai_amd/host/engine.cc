@@ -88,6 +88,7 @@ Engine::Engine(const hai_model_config& cfg, const hai_engine_options& opt) : cfg
         pchunk_ = opt.prefill_rows;
         fast_prefill_ = true;
     }
+    pchunk_cap_ = pchunk_;
     cap_ = std::max<int64_t>(opt.max_context, tmax_ + 1);
     ring_ = 32;
     nslots_ = tmax_ + 1;
@@ -305,7 +306,7 @@ int Engine::alloc_all() {
     // ---- workspace ----
     nproj_ = std::max(d.Nin, d.Nqkv);
     const int64_t T = tmax_;
-    const int64_t R = B_ * std::max(tmax_, pchunk_);  // rows of one forward (verify step or prompt chunk)
+    const int64_t R = B_ * std::max(tmax_, pchunk_cap_);  // rows of one forward (verify step or prompt chunk)
     auto carve_work = [&](Carver& cv) {
         d_ids_ = cv.take<int64_t>(R);
         d_vids_ = cv.take<int64_t>(R + 1);
@@ -330,7 +331,7 @@ int Engine::alloc_all() {
         dnout_ = cv.take<uint16_t>(R * d.vw);
         act_ = cv.take<uint16_t>(R * d.F);
         hf_ = cv.take<uint16_t>(R * H);
-        logits_ = cv.take<uint16_t>(R * d.V);
+        logits_ = cv.take<uint16_t>(B_ * tmax_ * d.V);  // verify rows; prompt chunks compute theirs in slices
         mh_[0] = cv.take<uint16_t>(B_ * H);
         mh_[1] = cv.take<uint16_t>(B_ * H);
         h_prev_ = cv.take<uint16_t>(B_ * H);
@@ -339,7 +340,7 @@ int Engine::alloc_all() {
         // last chunk can take more splits (and more scratch) than a full one
         size_t prefill_scratch = 0;
         if (fast_prefill_)
-            for (int64_t t = 1; t <= pchunk_; ++t)
+            for (int64_t t = 1; t <= pchunk_cap_; ++t)
                 prefill_scratch =
                     std::max(prefill_scratch, hai_gqa_mfma_plan_scratch_bytes(B_, t, d.nq, d.nkv, d.D, cap_));
         gqa_scratch_ = cv.take<char>(std::max({hai_gqa_scratch_bytes(B_, T, d.nq, d.D, cap_),
@@ -354,7 +355,7 @@ int Engine::alloc_all() {
             mfma_ws_ = ws > 0 ? cv.take<char>(ws) : nullptr;
         }
         if (fast_prefill_) {
-            dn_ws_bytes_ = static_cast<int64_t>(hai_deltanet_prefill_workspace_bytes(B_, pchunk_, d.nv, d.dv));
+            dn_ws_bytes_ = static_cast<int64_t>(hai_deltanet_prefill_workspace_bytes(B_, pchunk_cap_, d.nv, d.dv));
             dn_ws_ = cv.take<char>(static_cast<size_t>(dn_ws_bytes_));
         }
         argmax_scratch_ = cv.take<char>(hai_argmax_scratch_bytes(R, d.V));
@@ -827,30 +828,42 @@ int Engine::prefill_chunks(const int32_t* ids, int64_t P, uint16_t* hidden_out, 
         HAI_TRY(hai_memcpy_h2d(d_ids_, chunk.data(), static_cast<size_t>(B_ * T) * 8, stream_));
         // the verify-step prefill keeps every row's logits (one weight
         // stream serves all rows); a fast chunk computes only the last row's,
-        // and only in the last chunk
+        // and only in the last chunk (lm_head of the other rows in slices
+        // when the caller asks for them)
         const bool last_chunk = off + T == P;
-        const Logits lg = (!fast_prefill_ || logits_out != nullptr) ? Logits::kAll
-                          : last_chunk                             ? Logits::kLast
-                                                                   : Logits::kNone;
+        const Logits lg = !fast_prefill_ ? Logits::kAll : last_chunk ? Logits::kLast : Logits::kNone;
         HAI_TRY(forward_target(d_ids_, T, false, lg));
         HAI_TRY(hai_add_i32(d_tlen_, nullptr, static_cast<int32_t>(T), B_, stream_));
-        for (int64_t b = 0; b < B_; ++b) {
-            if (hidden_out)
-                HAI_TRY(hai_memcpy_d2h(hidden_out + (b * P + off) * d.H, hf_ + b * T * d.H,
-                                       static_cast<size_t>(T * d.H) * 2, stream_));
-            if (logits_out)
-                HAI_TRY(hai_memcpy_d2h(logits_out + (b * P + off) * d.V, logits_ + b * T * d.V,
-                                       static_cast<size_t>(T * d.V) * 2, stream_));
-        }
-        HAI_TRY(mtp_kv_rows(d_ids_, hf_, T, true));
-        if (off + T == P) {
-            // the last prompt row of every sequence: its argmax is the first
-            // target and its hidden feeds the first draft
+        if (last_chunk) {
+            // the last prompt row of every sequence: its argmax is the first target
             if (lg == Logits::kLast)
                 HAI_TRY(hai_argmax_rows_bf16(d_next_, logits_, d.V, B_, d.V, argmax_scratch_, stream_));
             else
                 HAI_TRY(hai_argmax_rows_bf16(d_next_, logits_ + (T - 1) * d.V, T * d.V, B_, d.V, argmax_scratch_,
                                              stream_));
+        }
+        for (int64_t b = 0; b < B_; ++b) {
+            if (hidden_out)
+                HAI_TRY(hai_memcpy_d2h(hidden_out + (b * P + off) * d.H, hf_ + b * T * d.H,
+                                       static_cast<size_t>(T * d.H) * 2, stream_));
+            if (logits_out && lg == Logits::kAll) {
+                HAI_TRY(hai_memcpy_d2h(logits_out + (b * P + off) * d.V, logits_ + b * T * d.V,
+                                       static_cast<size_t>(T * d.V) * 2, stream_));
+            } else if (logits_out) {
+                const int64_t slice = B_ * tmax_;
+                for (int64_t t0 = 0; t0 < T; t0 += slice) {
+                    const int64_t n = std::min(slice, T - t0);
+                    HAI_TRY(gemm(logits_, d.V, hf_ + (b * T + t0) * d.H, d.H, lm_head_, n, d.V, d.H, HAI_EPI_STORE,
+                                 nullptr, 0));
+                    HAI_TRY(hai_memcpy_d2h(logits_out + (b * P + off + t0) * d.V, logits_,
+                                           static_cast<size_t>(n * d.V) * 2, stream_));
+                    HAI_TRY(sync());  // logits_ is rewritten by the next slice
+                }
+            }
+        }
+        HAI_TRY(mtp_kv_rows(d_ids_, hf_, T, true));
+        if (last_chunk) {
+            // and its hidden feeds the first draft
             for (int64_t b = 0; b < B_; ++b)
                 HAI_TRY(hai_memcpy_d2d(h_prev_ + b * d.H, hf_ + (b * T + T - 1) * d.H, static_cast<size_t>(d.H) * 2,
                                        stream_));
@@ -1204,6 +1217,22 @@ int Engine::generate_speculative(const int32_t* prompts, int64_t P, int64_t max_
         st[b].emitted = rs_[b].emitted;
         if (stats) stats[b] = st[b];
         n_out[b] = rs_[b].emitted;
+    }
+    return HAI_OK;
+}
+
+int Engine::set_prefill_rows(int64_t rows) {
+    if (rows < 0 || rows > std::max(pchunk_cap_, tmax_))
+        return fail(HAI_ERR_INVALID_ARGUMENT, "set_prefill_rows: above the prompt chunk the engine was created for (" +
+                                                  std::to_string(pchunk_cap_) + " rows)");
+    if (rows > tmax_) {
+        if (!fast_prefill_buffers()) return fail(HAI_ERR_INVALID_ARGUMENT, "set_prefill_rows: the engine was created "
+                                                                           "without fast-prefill buffers");
+        pchunk_ = rows;
+        fast_prefill_ = true;
+    } else {
+        pchunk_ = std::min<int64_t>(tmax_, kDeltaNetMaxT);
+        fast_prefill_ = false;
     }
     return HAI_OK;
 }

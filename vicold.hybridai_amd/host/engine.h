@@ -177,6 +177,8 @@ public:
     // device copies them into the verify ids, no host round trip); n = 0 or
     // null tokens clears them
     int set_draft_override(const int32_t* tokens, int64_t n);
+    int set_prefill_rows(int64_t rows);
+    bool fast_prefill_buffers() const { return dn_ws_ != nullptr; }
     int spec_rounds(int64_t rounds, int64_t width, int32_t* out, int64_t cap, int64_t* n_out,
                     hai_spec_stats* stats);
     int profile_verify(int64_t T, int64_t iters, hai_verify_profile* out);
@@ -280,6 +282,7 @@ private:
     int64_t tmax_ = 0;    // largest verify T (rows per sequence)
     int64_t pchunk_ = 0;  // prompt rows per sequence and prefill forward
     bool fast_prefill_ = false;  // prompts prefill in large chunks on the matrix cores
+    int64_t pchunk_cap_ = 0;     // the largest prompt chunk the buffers hold
     bool fast_ = false;          // inside such a chunk: matrix-core GEMMs and attention
     char* dn_ws_ = nullptr;      // prefill DeltaNet outputs before the gated norm
     int64_t dn_ws_bytes_ = 0;
