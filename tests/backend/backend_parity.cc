@@ -222,6 +222,23 @@ void check_gpu(Backend* be) {
         orc_attention(q1.f.data(), g1.f.data(), k.f.data(), v.f.data(), want1.data(), 1, L, nq, nkv, D, 1);
         same_bits(d.down<uint16_t>(dy1.get(), want1.size()), want1, "cached_gqa_with_current_token");
     }
+    for (bool gated : {true, false}) {  // causal_gqa (uncached prompt attention, hip_kernels.hip:223-293)
+        const int64_t nq = 4, nkv = 2, D = 64, S = 70;  // two query chunks of the backend's 64
+        auto q = random_bf16(rng, S * nq * D), g = random_bf16(rng, S * nq * D);
+        auto k = random_bf16(rng, S * nkv * D), v = random_bf16(rng, S * nkv * D);
+        auto dq = d.up(q.bits), dg = d.up(g.bits), dk = d.up(k.bits), dv = d.up(v.bits);
+        auto dy = d.make(S * nq * D * 2);
+        expect_ok(be->causal_gqa(dy.get(), dq.get(), dk.get(), dv.get(), gated ? dg.get() : nullptr, DType::BF16, S,
+                                 nq, nkv, D),
+                  "causal_gqa");
+        std::vector<float> want(S * nq * D);
+        orc_attention(q.f.data(), gated ? g.f.data() : nullptr, k.f.data(), v.f.data(), want.data(), S, S, nq, nkv,
+                      D, 1);
+        same_bits(d.down<uint16_t>(dy.get(), want.size()), want, gated ? "causal_gqa gated" : "causal_gqa");
+        auto small = d.make(16);
+        Status st = be->causal_gqa(small.get(), dq.get(), dk.get(), dv.get(), nullptr, DType::BF16, S, nq, nkv, D);
+        expect(st.code() == StatusCode::InvalidArgument, "causal_gqa short dst rejected");
+    }
     {  // cached_gqa_with_current_token as a T=1 decode drives it (attention.cc:561-571): the
        // current K/V row is passed separately, the call stores it at cache_len-1
        // (hip_kernels.hip:466-476) and the caller only advances the length

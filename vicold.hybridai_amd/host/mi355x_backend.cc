@@ -609,6 +609,49 @@ Status MI355XBackend::append_kv_cache(Buffer* key_cache, Buffer* value_cache, co
     return Status::OK();
 }
 
+// causal_gqa_kernel (hip_kernels.hip:223-293, launcher :1379-1415): query s of
+// [seq_len, nq, D] attends key / value rows 0..s of [seq_len, nkv, D], the
+// output gated by sigmoid(gate).  The key / value tensors are a cache of
+// seq_len rows, so this is the verify attention over it with every row a
+// query; queries run in chunks of kCausalChunk rows (chunk [t0, t0 + n) over
+// cache length t0 + n), which bounds the split-KV scratch and leaves each
+// query's keys, and so every bit, as one call would.
+Status MI355XBackend::causal_gqa(Buffer* dst, const Buffer* query, const Buffer* key, const Buffer* value,
+                                 const Buffer* gate, DType dtype, int64_t seq_len, int64_t num_query_heads,
+                                 int64_t num_kv_heads, int64_t head_dim, Stream* stream) {
+    RETURN_IF_ERROR(need_bf16(dtype, "causal_gqa"));
+    if (seq_len <= 0 || seq_len > std::numeric_limits<int32_t>::max()) return invalid("causal_gqa length");
+    const int64_t qrow = num_query_heads * head_dim;
+    const size_t q_bytes = static_cast<size_t>(seq_len * qrow) * 2;
+    const size_t kv_bytes = static_cast<size_t>(seq_len * num_kv_heads * head_dim) * 2;
+    RETURN_IF_ERROR(need(dst, device_, q_bytes, "dst"));
+    RETURN_IF_ERROR(need(query, device_, q_bytes, "query"));
+    RETURN_IF_ERROR(need(key, device_, kv_bytes, "key"));
+    RETURN_IF_ERROR(need(value, device_, kv_bytes, "value"));
+    if (gate != nullptr) RETURN_IF_ERROR(need(gate, device_, q_bytes, "gate"));
+    void* s = nullptr;
+    RETURN_IF_ERROR(native(stream, &s));
+    RETURN_IF_ERROR(select());
+    std::lock_guard<std::mutex> lock(mu_);
+    constexpr int64_t kCausalChunk = 64;
+    void* ws = nullptr;
+    RETURN_IF_ERROR(scratch(gqa_, hai_gqa_scratch_bytes(1, std::min(kCausalChunk, seq_len), num_query_heads,
+                                                        head_dim, seq_len),
+                            &ws));
+    auto* out = static_cast<uint16_t*>(dst->data());
+    const auto* q = static_cast<const uint16_t*>(query->data());
+    const auto* g = gate ? static_cast<const uint16_t*>(gate->data()) : nullptr;
+    for (int64_t t0 = 0; t0 < seq_len; t0 += kCausalChunk) {
+        const int64_t n = std::min(kCausalChunk, seq_len - t0);
+        const int64_t len = t0 + n;
+        HAI_STATUS(hai_gqa_verify_bf16(out + t0 * qrow, q + t0 * qrow, g ? g + t0 * qrow : nullptr, key->data(),
+                                       value->data(), seq_len, ws, 1, n, num_query_heads, num_kv_heads, head_dim,
+                                       nullptr, static_cast<int32_t>(len), len, s),
+                   "causal_gqa");
+    }
+    return Status::OK();
+}
+
 Status MI355XBackend::cached_gqa(Buffer* dst, const Buffer* query, const Buffer* key_cache,
                                  const Buffer* value_cache, const Buffer* gate, DType dtype, int64_t query_len,
                                  int64_t cache_len, int64_t num_query_heads, int64_t num_kv_heads, int64_t head_dim,

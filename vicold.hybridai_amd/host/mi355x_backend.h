@@ -7,7 +7,7 @@
 // Implemented natively: memory, streams, events, copies, and the virtuals of
 // the speculative verify path -- gemm (bf16 X * W^T, fp32 accumulation),
 // add, embedding_gather, rmsnorm, silu_mul, q_gate_rmsnorm_rope,
-// partial_rope, append_kv_cache, cached_gqa, cached_gqa_with_current_token,
+// partial_rope, append_kv_cache, causal_gqa, cached_gqa, cached_gqa_with_current_token,
 // deltanet_grouped_conv, deltanet_recurrent, argmax_last_row, argmax_rows,
 // copy_to_offset.  Everything else (other dtypes, FP32 GEMM, the prefill-only
 // kernels) returns NotImplemented, which the reference's ops treat as "use
@@ -65,6 +65,9 @@ public:
     Status append_kv_cache(Buffer* key_cache, Buffer* value_cache, const Buffer* key, const Buffer* value,
                            DType dtype, int64_t token_count, int64_t num_kv_heads, int64_t head_dim,
                            int64_t cache_offset, int64_t cache_capacity, Stream* stream = nullptr) override;
+    Status causal_gqa(Buffer* dst, const Buffer* query, const Buffer* key, const Buffer* value, const Buffer* gate,
+                      DType dtype, int64_t seq_len, int64_t num_query_heads, int64_t num_kv_heads, int64_t head_dim,
+                      Stream* stream = nullptr) override;
     Status cached_gqa(Buffer* dst, const Buffer* query, const Buffer* key_cache, const Buffer* value_cache,
                       const Buffer* gate, DType dtype, int64_t query_len, int64_t cache_len,
                       int64_t num_query_heads, int64_t num_kv_heads, int64_t head_dim,
