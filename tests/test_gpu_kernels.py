@@ -1026,7 +1026,8 @@ def test_gemm_mfma_within_tolerance(M, N, K, epi, with_ws):
 
 @pytest.mark.parametrize("M,N,K,epi,mapped,special", [(32, 1536, 5120, 0, False, True), (64, 2 * 640, 1024, 2, False, False),
                                                       (17, 700, 1008, 1, True, False), (128, 5120, 2048, 1, False, False),
-                                                      (48, 16400, 512, 0, True, True)])
+                                                      (48, 16400, 512, 0, True, True),
+                                                      (40, 2000, 2048, 1, True, True), (24, 4096, 1536, 2, False, False)])
 def test_gemm_fp8_mfma_within_tolerance(M, N, K, epi, mapped, special):
     """hai_gemm_fp8_mfma against the canonical FP8 GEMM (dequantised weights,
     fp32 dot): bf16 outputs within a couple of bf16 ulps; 0x7F / 0xFF codes

@@ -29,6 +29,7 @@
 //   * Epilogues as in the skinny GEMM: store, residual add, SwiGLU over
 //     interleaved (gate_f, up_f) rows.
 #include <atomic>
+#include <cstdlib>
 
 #include "hai_common.h"
 #include "hai_device.h"
@@ -567,6 +568,304 @@ __global__ __launch_bounds__(256) void gemm_fp8_mfma_kernel(uint16_t* __restrict
     }
 }
 
+// ---------------------------------------------------------------------------
+// Register-operand variant of the batched GEMMs (bf16 and FP8 weights, 32 or
+// 64 activation rows, K a multiple of 256).  The kernels above pass every
+// weight through LDS (written decoded, read back in the MFMA layout) and
+// give each wave 16 weight rows, so each activation operand read from LDS
+// feeds one MFMA; at 64 rows that is 14 LDS bytes per FP8 code and the
+// kernel is LDS-bound.  Here:
+//   * weights go straight into the MFMA B-operand registers: one load
+//     instruction covers 8 rows x 128 contiguous bytes (lane (li, kg) of
+//     load I0 takes row li % 8, 16-byte piece kg + 4 (li >= 8); I1 the rows
+//     8..15 with the halves swapped), and a select plus a DPP row rotate by 8
+//     lanes turn the pair into the operands of two MFMA k-slices (R0: piece
+//     kg of row li, R1: piece kg + 4).  Every instruction reads whole 128-byte
+//     lines; an MFMA-layout load (16 rows x 64 bytes per instruction)
+//     measured 3.9-4.7 TB/s against 6.1-7.1 for this form on MI355X;
+//   * a wave owns 32 weight rows (two MFMA column tiles), so each activation
+//     operand read feeds two MFMAs, and one half of every 256-k chunk (for
+//     FP8 exactly one 128-k scale block); the two k-halves of a tile meet in
+//     LDS at the end, added in a fixed order;
+//   * a chunk's activation rows are loaded one chunk ahead (rows past M read
+//     zeros) and written to LDS after the current chunk is multiplied, each
+//     row's 16-byte pieces XOR-swizzled by the row index so that the 16 rows
+//     an operand read touches fall in distinct banks; two chunk buffers, one
+//     barrier per chunk.  (Buffer -> LDS copies would save the registers,
+//     but the compiler cannot tell which buffer a copy writes and drains
+//     every outstanding load before the next LDS read: vmcnt(0) per chunk.)
+//   * the weights of the next two chunks are in flight while one is
+//     multiplied.
+// Same tiles (64 weight rows per block), K splits, stream-K and epilogues as
+// the kernels above; tolerance mode as they are.  Used where it measured
+// faster (use_rt below).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t row_ror8(uint32_t v) {
+    return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), 0x128, 0xF, 0xF, false));
+}
+
+constexpr int kRtChunk = 256;  // k per chunk (two 128-k halves)
+
+template <bool FP8>
+struct RtLoads {
+    static constexpr int kPerTile = FP8 ? 2 : 4;  // 16-byte weight loads per n-tile and chunk half
+    static constexpr int kPerChunk = 2 * kPerTile;
+};
+
+template <int MT, int EPI, bool FP8, bool CHECK, bool SK>
+__global__ __launch_bounds__(256) void gemm_rt_mfma_kernel(uint16_t* __restrict__ y, int64_t ldy,
+                                                           const uint16_t* __restrict__ x, int64_t ldx,
+                                                           const void* w, const float* __restrict__ scales,
+                                                           const int32_t* __restrict__ scale_rows, int paired,
+                                                           const uint16_t* res, int64_t ldres, int M, int N, int K,
+                                                           float* __restrict__ part, int KSB, int sk) {
+    constexpr int XR = 16 * MT;              // staged activation rows
+    constexpr int XBUF = XR * kRtChunk;      // bf16 elements per chunk buffer
+    constexpr int NW = RtLoads<FP8>::kPerChunk;
+    constexpr int EB = FP8 ? 1 : 2;          // weight bytes per element
+    extern __shared__ __align__(16) uint16_t lds[];  // [2][XR][256], pieces swizzled; then the k-half sums
+    const int lane = threadIdx.x & 63;
+    const int wave = wave_index();
+    const int li = lane & 15;
+    const int kg = lane >> 4;
+    const int nh = wave & 1;   // rows 32 nh .. 32 nh + 31 of the tile
+    const int kh = wave >> 1;  // k-half of every chunk
+    const bool low = li < 8;
+    const int nck = K / kRtChunk;
+    const int nkb = K / 128;
+
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, static_cast<uint32_t>(static_cast<int64_t>(M) * ldx * 2));
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, static_cast<uint32_t>(static_cast<int64_t>(N) * K * EB));
+    // activation pieces of a chunk: thread piece e = tid + 256 i is row e / 32,
+    // LDS position e % 32, holding the row's piece position ^ (row % 16);
+    // rows past M start past the buffer and read zeros
+    constexpr int XP = XR / 8;  // pieces per thread and chunk
+    uint32_t xoff[XP];
+    int xdst[XP];
+#pragma unroll
+    for (int i = 0; i < XP; ++i) {
+        const int e = static_cast<int>(threadIdx.x) + 256 * i;
+        const int r = e >> 5;
+        const int pos = e & 31;
+        xoff[i] = static_cast<uint32_t>((static_cast<int64_t>(r) * ldx + ((pos ^ (r & 15)) * 8)) * 2);
+        xdst[i] = r * kRtChunk + pos * 8;
+    }
+    auto load_x = [&](u32x4 (&xv)[XP], int c) {
+#pragma unroll
+        for (int i = 0; i < XP; ++i) xv[i] = bload(rx, xoff[i], static_cast<uint32_t>(c) * (kRtChunk * 2));
+    };
+    auto store_x = [&](const u32x4 (&xv)[XP], int buf) {
+#pragma unroll
+        for (int i = 0; i < XP; ++i) *reinterpret_cast<u32x4*>(lds + buf * XBUF + xdst[i]) = xv[i];
+    };
+    // A operand: 8 elements of row 16 mt + li at 16-byte piece p of the chunk
+    auto a_op = [&](int buf, int mt, int p) -> u32x4 {
+        return *reinterpret_cast<const u32x4*>(lds + buf * XBUF + (16 * mt + li) * kRtChunk + ((p ^ li) * 8));
+    };
+
+    auto piece = [&](int64_t tile, int cbeg, int cend, int cstep, int plane) {
+        const int64_t row_base = tile * kBlockRows + 32 * nh;
+        // per n-tile: byte offsets of loads I0 (rows 0..7) and I1 (rows 8..15) at chunk 0
+        uint32_t wo0[2], wo1[2];
+        const float* srp[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const int64_t ra = row_base + 16 * t + (li & 7);
+            const int p0 = kg + (low ? 0 : 4), p1 = kg + (low ? 4 : 0);
+            wo0[t] = static_cast<uint32_t>((ra * K + kh * 128) * EB + p0 * 16);
+            wo1[t] = static_cast<uint32_t>(((ra + 8) * K + kh * 128) * EB + p1 * 16);
+            if constexpr (FP8) {
+                const int64_t ncol = min(row_base + 16 * t + li, static_cast<int64_t>(N) - 1);
+                const int64_t nsb = ((N >> 1) + 127) / 128;
+                const int64_t srow =
+                    scale_rows ? scale_rows[ncol] : (paired ? (ncol & 1) * nsb + (ncol >> 1) / 128 : ncol / 128);
+                srp[t] = scales + srow * nkb + kh;
+            } else {
+                srp[t] = nullptr;
+            }
+        }
+        f32x4 tot[MT][2];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int t = 0; t < 2; ++t) tot[mt][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+        auto load_w = [&](u32x4 (&wv)[NW], int c) {
+            const uint32_t off = static_cast<uint32_t>(c) * (kRtChunk * EB);
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int j = 0; j < NW / 4; ++j) {  // bf16: two 64-k pairs per half, FP8: one
+                    wv[(t * (NW / 4) + j) * 2] = bload_w(rw, wo0[t] + j * 128, off);
+                    wv[(t * (NW / 4) + j) * 2 + 1] = bload_w(rw, wo1[t] + j * 128, off);
+                }
+        };
+        auto load_s = [&](float (&sv)[2], int c) {
+            if constexpr (FP8) {
+                sv[0] = srp[0][2 * c];
+                sv[1] = srp[1][2 * c];
+            }
+        };
+        // rearranged pair of one load pair: R0 = piece kg of row li, R1 = piece kg + 4
+        auto operands = [&](const u32x4& i0, const u32x4& i1, u32x4& r0, u32x4& r1) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                r0[q] = low ? i0[q] : i1[q];
+                r1[q] = row_ror8(low ? i1[q] : i0[q]);
+            }
+        };
+        auto compute = [&](const u32x4 (&wv)[NW], const float (&sv)[2], int buf) {
+            if constexpr (FP8) {
+                // 128 codes of the wave's half: R0 holds k 16 kg .. + 15, R1 k 64 + 16 kg .. + 15
+                u32x4 b[2][4];
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    u32x4 r0, r1;
+                    operands(wv[2 * t], wv[2 * t + 1], r0, r1);
+                    uint32_t d[16];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        e4m3x4_to_bf16<CHECK>(r0[q], d[2 * q], d[2 * q + 1]);
+                        e4m3x4_to_bf16<CHECK>(r1[q], d[8 + 2 * q], d[8 + 2 * q + 1]);
+                    }
+                    b[t][0] = u32x4{d[0], d[1], d[2], d[3]};
+                    b[t][1] = u32x4{d[4], d[5], d[6], d[7]};
+                    b[t][2] = u32x4{d[8], d[9], d[10], d[11]};
+                    b[t][3] = u32x4{d[12], d[13], d[14], d[15]};
+                }
+                const int pa = 16 * kh + 2 * kg;
+                const int poff[4] = {0, 1, 8, 9};
+                f32x4 acc[MT][2];
+#pragma unroll
+                for (int s4 = 0; s4 < 4; ++s4)
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) {
+                        const u32x4 a = a_op(buf, mt, pa + poff[s4]);
+#pragma unroll
+                        for (int t = 0; t < 2; ++t)
+                            acc[mt][t] = mfma16(a, b[t][s4], s4 == 0 ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : acc[mt][t]);
+                    }
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                    for (int t = 0; t < 2; ++t)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) tot[mt][t][i] = fma_(sv[t], acc[mt][t][i], tot[mt][t][i]);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    u32x4 b[2][2];
+#pragma unroll
+                    for (int t = 0; t < 2; ++t) operands(wv[(t * 2 + j) * 2], wv[(t * 2 + j) * 2 + 1], b[t][0], b[t][1]);
+                    const int pa = 16 * kh + 8 * j + kg;
+#pragma unroll
+                    for (int h = 0; h < 2; ++h)
+#pragma unroll
+                        for (int mt = 0; mt < MT; ++mt) {
+                            const u32x4 a = a_op(buf, mt, pa + 4 * h);
+#pragma unroll
+                            for (int t = 0; t < 2; ++t) tot[mt][t] = mfma16(a, b[t][h], tot[mt][t]);
+                        }
+                }
+            }
+        };
+
+        __syncthreads();  // the previous piece's LDS reads are done
+        u32x4 wA[NW], wB[NW], wC[NW], xv[XP];
+        float sA[2] = {0.0f, 0.0f}, sB[2] = {0.0f, 0.0f}, sC[2] = {0.0f, 0.0f};
+        // Loads are issued unconditionally (a chunk past the piece is clamped
+        // to the last one and its values are never used), so that the code
+        // between the waits is straight-line and the compiler's wait counts
+        // stay exact: a load inside a branch makes them drain everything.
+        auto clampc = [&](int c) { return min(c, nck - 1); };
+        if (cbeg < cend) {
+            load_x(xv, cbeg);
+            load_s(sA, cbeg);
+            load_w(wA, cbeg);
+            load_s(sB, clampc(cbeg + cstep));
+            load_w(wB, clampc(cbeg + cstep));
+            store_x(xv, 0);
+        }
+        // chunk i (its activations in buffer i % 2): barrier, request the
+        // activations of chunk i + 1 and the weights of chunk i + 2, multiply
+        // chunk i, write chunk i + 1's activations to the other buffer
+        auto step = [&](int i, u32x4 (&cur)[NW], const float (&scur)[2], u32x4 (&pre)[NW], float (&spre)[2]) {
+            const int c = cbeg + i * cstep;
+            if (c >= cend) return false;
+            lds_barrier();
+            load_x(xv, clampc(c + cstep));
+            load_s(spre, clampc(c + 2 * cstep));
+            load_w(pre, clampc(c + 2 * cstep));
+            // the requests stay ahead of the multiply (the scheduler would
+            // otherwise sink them below it to shorten register lifetimes)
+            pin_memory_order();
+            __builtin_amdgcn_sched_barrier(0);
+            compute(cur, scur, i & 1);
+            pin_memory_order();
+            __builtin_amdgcn_sched_barrier(0);
+            store_x(xv, (i + 1) & 1);
+            return true;
+        };
+        for (int i = 0;; i += 3) {
+            if (!step(i, wA, sA, wC, sC)) break;
+            if (!step(i + 1, wB, sB, wA, sA)) break;
+            if (!step(i + 2, wC, sC, wB, sB)) break;
+        }
+
+        // the two k-halves of the tile: half 1 through LDS, added to half 0
+        __syncthreads();
+        float* red = reinterpret_cast<float*>(lds);  // [2 nh][MT][2][64 lanes] f32x4
+        if (kh == 1) {
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int t = 0; t < 2; ++t)
+                    *reinterpret_cast<f32x4*>(red + (((nh * MT + mt) * 2 + t) * 64 + lane) * 4) = tot[mt][t];
+        }
+        __syncthreads();
+        if (kh == 1) return;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const f32x4 o = *reinterpret_cast<const f32x4*>(red + (((nh * MT + mt) * 2 + t) * 64 + lane) * 4);
+                tot[mt][t] = tot[mt][t] + o;
+            }
+        // D layout: lane (li, kg) holds rows 16 mt + 4 kg + i of column row_base + 16 t + li
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const int64_t n = row_base + 16 * t + li;
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int m = 16 * mt + 4 * kg + i;
+                    if (plane < 0)
+                        mfma_store<EPI>(y, ldy, res, ldres, tot[mt][t][i], m, n, M, N, li);
+                    else if (m < M && n < N)
+                        part[(static_cast<int64_t>(plane) * M + m) * N + n] = tot[mt][t][i];
+                }
+        }
+    };
+    // chunk indices below are in units of kRtChunk == kChunk
+    if constexpr (!SK) {
+        piece(blockIdx.x, blockIdx.y, nck, KSB, KSB == 1 ? -1 : static_cast<int>(blockIdx.y));
+        return;
+    }
+    const int64_t ntiles = (N + kBlockRows - 1) / kBlockRows;
+    const int64_t items = ntiles * nck;
+    const int64_t lo = static_cast<int64_t>(blockIdx.x) * items / sk;
+    const int64_t hi = (static_cast<int64_t>(blockIdx.x) + 1) * items / sk;
+    for (int64_t it = lo; it < hi;) {
+        const int64_t tile = it / nck;
+        const int c0 = static_cast<int>(it - tile * nck);
+        const int c1 = static_cast<int>(min(hi - tile * nck, static_cast<int64_t>(nck)));
+        const int plane = (c0 == 0 && c1 == nck) ? -1 : (sk_block_of(tile * nck, items, sk) == blockIdx.x ? 0 : 1);
+        piece(tile, c0, c1, 1, plane);
+        it = tile * nck + c1;
+    }
+}
+
 struct MfmaArgs {
     uint16_t* y;
     int64_t ldy;
@@ -623,6 +922,65 @@ int sk_blocks(const void* kern, size_t shmem, const MfmaArgs& a) {
     const int64_t rem = ntiles - k * cus;  // f x CUs
     if (k < 1 || k > per_cu || rem == 0 || 4 * rem > cus) return 0;
     return static_cast<int>(k * cus);
+}
+
+// The register-operand kernels serve K % 256 == 0 and up to 64 rows; the
+// environment variable HAI_MFMA_RT=0 selects the LDS-staged kernels instead
+// (read once per process).
+bool rt_enabled() {
+    static const bool on = [] {
+        const char* e = std::getenv("HAI_MFMA_RT");
+        return e == nullptr || e[0] != '0';
+    }();
+    return on;
+}
+
+template <int MT, int EPI>
+int launch_rt(const MfmaArgs& a, hipStream_t s) {
+    const size_t shmem = static_cast<size_t>(2) * 16 * MT * kRtChunk * 2;
+    const dim3 grid(static_cast<unsigned>((a.N + kBlockRows - 1) / kBlockRows), static_cast<unsigned>(a.KSB));
+    const void* w = a.wq != nullptr ? static_cast<const void*>(a.wq) : static_cast<const void*>(a.w);
+    using Kern = void (*)(uint16_t*, int64_t, const uint16_t*, int64_t, const void*, const float*, const int32_t*,
+                          int, const uint16_t*, int64_t, int, int, int, float*, int, int);
+    Kern kern, kern_sk;
+    int slot;
+    if (a.wq == nullptr) {
+        kern = gemm_rt_mfma_kernel<MT, EPI, false, false, false>;
+        kern_sk = gemm_rt_mfma_kernel<MT, EPI, false, false, true>;
+        slot = 0;
+    } else if (a.check) {
+        kern = gemm_rt_mfma_kernel<MT, EPI, true, true, false>;
+        kern_sk = gemm_rt_mfma_kernel<MT, EPI, true, true, true>;
+        slot = 1;
+    } else {
+        kern = gemm_rt_mfma_kernel<MT, EPI, true, false, false>;
+        kern_sk = gemm_rt_mfma_kernel<MT, EPI, true, false, true>;
+        slot = 2;
+    }
+    static bool attr[6] = {false, false, false, false, false, false};
+    int rc = allow_lds(reinterpret_cast<const void*>(kern), shmem, &attr[2 * slot]);
+    if (rc == HAI_OK) rc = allow_lds(reinterpret_cast<const void*>(kern_sk), shmem, &attr[2 * slot + 1]);
+    if (rc != HAI_OK) return rc;
+    const int sk = sk_blocks(reinterpret_cast<const void*>(kern_sk), shmem, a);
+    if (sk)
+        kern_sk<<<dim3(static_cast<unsigned>(sk)), dim3(256), shmem, s>>>(a.y, a.ldy, a.x, a.ldx, w, a.scales,
+                                                                         a.scale_rows, a.paired, a.res, a.ldres, a.M,
+                                                                         a.N, a.K, a.part, a.KSB, sk);
+    else
+        kern<<<grid, dim3(256), shmem, s>>>(a.y, a.ldy, a.x, a.ldx, w, a.scales, a.scale_rows, a.paired, a.res,
+                                            a.ldres, a.M, a.N, a.K, a.part, a.KSB, 0);
+    rc = launched("gemm_rt_mfma_kernel");
+    if (rc != HAI_OK) return rc;
+    const int64_t n = static_cast<int64_t>(a.M) * ((a.N + 1) / 2);
+    if (sk) {
+        mfma_sk_finalize_kernel<EPI><<<dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s>>>(
+            a.y, a.ldy, a.part, a.res, a.ldres, a.M, a.N, (a.K + kChunk - 1) / kChunk, sk);
+        return launched("mfma_sk_finalize_kernel");
+    }
+    if (a.KSB == 1 || a.keep) return HAI_OK;
+    mfma_finalize_kernel<EPI><<<dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s>>>(
+        a.y, a.ldy, a.part, a.KSB, a.res, a.ldres, a.M, a.N);
+    return launched("mfma_finalize_kernel");
 }
 
 template <int MT, int EPI>
@@ -682,8 +1040,24 @@ int launch_mfma(const MfmaArgs& a, hipStream_t s) {
     return launched("mfma_finalize_kernel");
 }
 
+// Where the register-operand kernels run: FP8 weights, 17-64 rows, the
+// narrow (N <= 8192, K-split) layers.  Measured on MI355X against the
+// LDS-staged kernels (C5 shapes): down 46.9 -> 37.3 us at M = 64 and 38.1
+// -> 27.1 us at M = 32, out / o 21.8 -> 19.9 and 16.9 -> 13.9 us.  The wide
+// layers (one tile per block over the whole K) lost with them (gate|up at
+// M = 64 83 -> 114 us: two resident blocks per CU keep too few weight
+// bytes in flight), and so did bf16 weights at 32 rows; those keep the
+// LDS-staged kernels.
+bool use_rt(const MfmaArgs& a) {
+    return a.wq != nullptr && a.K % kRtChunk == 0 && a.M > 16 && a.M <= 64 && a.N <= 8192 && rt_enabled();
+}
+
 template <int EPI>
 int dispatch_mfma(const MfmaArgs& a, hipStream_t s) {
+    if (use_rt(a)) {
+        if (a.M <= 32) return launch_rt<2, EPI>(a, s);
+        return launch_rt<4, EPI>(a, s);
+    }
     if (a.M <= 16) return launch_mfma<1, EPI>(a, s);
     if (a.M <= 32) return launch_mfma<2, EPI>(a, s);
     if (a.M <= 64) return launch_mfma<4, EPI>(a, s);
