@@ -251,15 +251,23 @@ __global__ __launch_bounds__(64 * W) void gqa_partial_kernel(
     }
 }
 
-// One wave per query: chunk partials merged in chunk order against the
-// global max, then divided, gated and rounded.
+// Chunk partials of one query merged in chunk order against the global
+// max, then divided, gated and rounded.
 template <int D>
-__global__ __launch_bounds__(256) void gqa_combine_kernel(
+__global__ __launch_bounds__(D) void gqa_combine_kernel(
     uint16_t* __restrict__ out, const float* __restrict__ scratch, const uint16_t* gate, int B, int T,
     int nq, const int32_t* lens, int len_add, int nchunk) {
-    const int lane = threadIdx.x & 63;
-    const int64_t qidx = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-    if (qidx >= static_cast<int64_t>(B) * T * nq) return;
+    // One block per query row, thread d owns output dimension d.  The chunk
+    // weights w_c = exp(m_c - M) and sums l_c are formed once per batch of D
+    // chunks into LDS; then each thread folds its dimension over the chunks
+    // in order, with a batch's loads all issued before the first fma (the
+    // latency of one batch, not of every eighth chunk).  The fma order per
+    // element, and Ls's, are those of the chunk loop they replace, so the
+    // result is unchanged bit for bit.
+    constexpr int kBatch = 32;  // chunk loads in flight per thread
+    __shared__ float w_sh[D], l_sh[D], red[D / 64];
+    const int tid = threadIdx.x;
+    const int64_t qidx = blockIdx.x;
     const int64_t m = qidx / nq;
     const int b = static_cast<int>(m / T);
     const int t = static_cast<int>(m % T);
@@ -269,49 +277,44 @@ __global__ __launch_bounds__(256) void gqa_combine_kernel(
     constexpr int64_t PS = partial_stride(D);
     const float* base = scratch + qidx * nchunk * PS;
     float M = __uint_as_float(0xff800000u);
-    for (int c = lane; c < nch; c += 64) M = fmaxf(M, base[c * PS]);
+    for (int c = tid; c < nch; c += D) M = fmaxf(M, base[c * PS]);
     M = wave_max64(M);
-    constexpr int PER = D / 64;
-    float O[PER];
+    if constexpr (D > 64) {
+        if ((tid & 63) == 0) red[tid >> 6] = M;
+        __syncthreads();
 #pragma unroll
-    for (int r = 0; r < PER; ++r) O[r] = 0.0f;
-    float Ls = 0.0f;
-    for (int c0 = 0; c0 < nch; c0 += 64) {
-        const int nt = min(64, nch - c0);
-        float w = 0.0f, lc = 0.0f;
-        if (lane < nt) {
-            const float* part = base + (c0 + lane) * PS;
-            w = cexp(part[0] - M);
-            lc = part[1];
+        for (int i = 0; i < D / 64; ++i) M = fmaxf(M, red[i]);
+    }
+    float O = 0.0f, Ls = 0.0f;
+    for (int c0 = 0; c0 < nch; c0 += D) {
+        const int nt = min(D, nch - c0);
+        __syncthreads();  // the previous batch's weights are read
+        if (tid < nt) {
+            const float* part = base + (c0 + tid) * PS;
+            w_sh[tid] = cexp(part[0] - M);
+            l_sh[tid] = part[1];
         }
-        for (int cb = 0; cb < nt; cb += 8) {
-            float pv[8][PER];
+        __syncthreads();
+        for (int cb = 0; cb < nt; cb += kBatch) {
+            float pv[kBatch];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
+            for (int u = 0; u < kBatch; ++u) {
                 const int cc = min(cb + u, nt - 1);
-                const float* part = base + (c0 + cc) * PS + 2;
-#pragma unroll
-                for (int r = 0; r < PER; ++r) pv[u][r] = part[lane + 64 * r];
+                pv[u] = base[(c0 + cc) * PS + 2 + tid];
             }
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
+            for (int u = 0; u < kBatch; ++u) {
                 if (cb + u < nt) {
-                    const float wc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), cb + u));
-                    const float lcc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lc), cb + u));
-                    Ls = fma_(lcc, wc, Ls);
-#pragma unroll
-                    for (int r = 0; r < PER; ++r) O[r] = fma_(pv[u][r], wc, O[r]);
+                    const float wc = w_sh[cb + u];
+                    Ls = fma_(l_sh[cb + u], wc, Ls);
+                    O = fma_(pv[u], wc, O);
                 }
             }
         }
     }
-#pragma unroll
-    for (int r = 0; r < PER; ++r) {
-        const int d = lane + 64 * r;
-        float o = O[r] / Ls;
-        if (gate != nullptr) o = o * csigmoid(bf2f(gate[qidx * D + d]));
-        out[qidx * D + d] = f2bf(o);
-    }
+    float o = O / Ls;
+    if (gate != nullptr) o = o * csigmoid(bf2f(gate[qidx * D + tid]));
+    out[qidx * D + tid] = f2bf(o);
 }
 
 template <int D>
@@ -347,8 +350,8 @@ int launch(uint16_t* out, const uint16_t* q, const uint16_t* gate, const uint16_
     int rc = launched("gqa_partial_kernel");
     if (rc != HAI_OK) return rc;
     const int64_t nall = static_cast<int64_t>(B) * T * nq;
-    gqa_combine_kernel<D><<<dim3(static_cast<unsigned>((nall + 3) / 4)), dim3(256), 0, s>>>(
-        out, scratch, gate, B, T, nq, lens, len_add, nchunk);
+    gqa_combine_kernel<D><<<dim3(static_cast<unsigned>(nall)), dim3(D), 0, s>>>(out, scratch, gate, B, T, nq, lens,
+                                                                             len_add, nchunk);
     return launched("gqa_combine_kernel");
 }
 
@@ -692,62 +695,61 @@ __global__ __launch_bounds__(256) void gqa_mfma_partial_kernel(
     }
 }
 
-// One wave per query: the splits' partials merged against the global max
-// (base 2), divided, gated and rounded.
+// The splits' partials of one query merged against the global max (base
+// 2), divided, gated and rounded: one block per query row, thread d owns
+// output dimension d, the split weights formed once per batch in LDS and a
+// batch's loads all issued before the first fma (the order of every sum is
+// the split order).
 template <int D>
-__global__ __launch_bounds__(256) void gqa_mfma_combine_kernel(uint16_t* __restrict__ out,
-                                                               const float* __restrict__ part, const uint16_t* gate,
-                                                               int B, int T, int nq, const int32_t* lens,
-                                                               int len_add, int nsplit, int block_keys) {
-    const int lane = threadIdx.x & 63;
-    const int64_t qidx = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-    if (qidx >= static_cast<int64_t>(B) * T * nq) return;
+__global__ __launch_bounds__(D) void gqa_mfma_combine_kernel(uint16_t* __restrict__ out,
+                                                             const float* __restrict__ part, const uint16_t* gate,
+                                                             int B, int T, int nq, const int32_t* lens,
+                                                             int len_add, int nsplit, int block_keys) {
+    constexpr int kBatch = 32;
+    __shared__ float w_sh[D], l_sh[D], red[D / 64];
+    const int tid = threadIdx.x;
+    const int64_t qidx = blockIdx.x;
     const int b = static_cast<int>(qidx / (static_cast<int64_t>(T) * nq));
     const int64_t L = static_cast<int64_t>(lens ? lens[b] : 0) + len_add;
     const int nv = static_cast<int>(min(static_cast<int64_t>(nsplit), (L + block_keys - 1) / block_keys));
     constexpr int64_t PS = mfma_part_stride(D);
     const float* base = part + qidx * nsplit * PS;
     float M = -__builtin_huge_valf();
-    for (int c = lane; c < nv; c += 64) M = fmaxf(M, base[c * PS + D]);
+    for (int c = tid; c < nv; c += D) M = fmaxf(M, base[c * PS + D]);
     M = wave_max64(M);
-    constexpr int PER = D / 64;
-    float O[PER];
+    if constexpr (D > 64) {
+        if ((tid & 63) == 0) red[tid >> 6] = M;
+        __syncthreads();
 #pragma unroll
-    for (int r = 0; r < PER; ++r) O[r] = 0.0f;
-    float Ls = 0.0f;
-    int c = 0;
-    for (; c + 4 <= nv; c += 4) {
-        float mv[4], lv[4], ov[4][PER];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const float* p = base + (c + u) * PS;
-            mv[u] = p[D];
-            lv[u] = p[D + 1];
-#pragma unroll
-            for (int r = 0; r < PER; ++r) ov[u][r] = p[lane + 64 * r];
+        for (int i = 0; i < D / 64; ++i) M = fmaxf(M, red[i]);
+    }
+    float O = 0.0f, Ls = 0.0f;
+    for (int c0 = 0; c0 < nv; c0 += D) {
+        const int nt = min(D, nv - c0);
+        __syncthreads();  // the previous batch's weights are read
+        if (tid < nt) {
+            const float* p = base + (c0 + tid) * PS;
+            w_sh[tid] = __builtin_amdgcn_exp2f(p[D] - M);
+            l_sh[tid] = p[D + 1];
         }
+        __syncthreads();
+        for (int cb = 0; cb < nt; cb += kBatch) {
+            float ov[kBatch];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const float w = __builtin_amdgcn_exp2f(mv[u] - M);
-            Ls = fma_(lv[u], w, Ls);
+            for (int u = 0; u < kBatch; ++u) ov[u] = base[(c0 + min(cb + u, nt - 1)) * PS + tid];
 #pragma unroll
-            for (int r = 0; r < PER; ++r) O[r] = fma_(ov[u][r], w, O[r]);
+            for (int u = 0; u < kBatch; ++u) {
+                if (cb + u < nt) {
+                    const float w = w_sh[cb + u];
+                    Ls = fma_(l_sh[cb + u], w, Ls);
+                    O = fma_(ov[u], w, O);
+                }
+            }
         }
     }
-    for (; c < nv; ++c) {
-        const float* p = base + c * PS;
-        const float w = __builtin_amdgcn_exp2f(p[D] - M);
-        Ls = fma_(p[D + 1], w, Ls);
-#pragma unroll
-        for (int r = 0; r < PER; ++r) O[r] = fma_(p[lane + 64 * r], w, O[r]);
-    }
-#pragma unroll
-    for (int r = 0; r < PER; ++r) {
-        const int d = lane + 64 * r;
-        float v = O[r] / Ls;
-        if (gate != nullptr) v = v * csigmoid(bf2f(gate[qidx * D + d]));
-        out[qidx * D + d] = f2bf(v);
-    }
+    float v = O / Ls;
+    if (gate != nullptr) v = v * csigmoid(bf2f(gate[qidx * D + tid]));
+    out[qidx * D + tid] = f2bf(v);
 }
 
 // Split plan of the matrix-core path: steps per wave (block = 4 waves x steps
@@ -797,7 +799,7 @@ int launch_mfma(uint16_t* out, const uint16_t* q, const uint16_t* gate, const ui
     int rc = launched("gqa_mfma_partial_kernel");
     if (rc != HAI_OK) return rc;
     const int64_t nall = static_cast<int64_t>(B) * T * nq;
-    gqa_mfma_combine_kernel<D><<<dim3(static_cast<unsigned>((nall + 3) / 4)), dim3(256), 0, s>>>(
+    gqa_mfma_combine_kernel<D><<<dim3(static_cast<unsigned>(nall)), dim3(D), 0, s>>>(
         out, scratch, gate, B, T, nq, lens, len_add, p.nsplit, p.block_keys);
     return launched("gqa_mfma_combine_kernel");
 }
