@@ -151,6 +151,27 @@ struct ChunkOffset {
     }
 };
 
+// The value of lane 16 r + (l + 8) % 16 for lane 16 r + l: a DPP rotate by
+// 8 lanes within each row of 16 (row_ror:8).
+__device__ __forceinline__ uint32_t row_ror8(uint32_t v) {
+    return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), 0x128, 0xF, 0xF, false));
+}
+
+// Matrix-operand loads of 16 rows x 64 contiguous bytes per instruction (row
+// li = lane % 16, 16-byte piece kg = lane / 16) stream poorly (16 rows per
+// quarter-wave).  Two loads of 8 rows x 128 bytes instead -- i0: row li % 8,
+// piece kg + 4 [li >= 8]; i1: row 8 + li % 8, piece kg + 4 [li < 8] -- read
+// whole lines, and this turns them into the operand layout: r0 = piece kg of
+// row li, r1 = piece kg + 4 of row li.
+template <typename V4>
+__device__ __forceinline__ void rows8x128_to_operands(const V4& i0, const V4& i1, bool low, V4& r0, V4& r1) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        r0[q] = low ? i0[q] : i1[q];
+        r1[q] = row_ror8(low ? i1[q] : i0[q]);
+    }
+}
+
 // xor butterfly over the 64 lanes of a wave; all lanes get the same bits.
 // The value of lane (lane ^ 1) / (lane ^ 2): a DPP quad permutation, no LDS
 // round trip (same operands as __shfl_xor with those masks).

@@ -600,10 +600,6 @@ __global__ __launch_bounds__(256) void gemm_fp8_mfma_kernel(uint16_t* __restrict
 // the kernels above; tolerance mode as they are.  Used where it measured
 // faster (use_rt below).
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ uint32_t row_ror8(uint32_t v) {
-    return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), 0x128, 0xF, 0xF, false));
-}
-
 constexpr int kRtChunk = 256;  // k per chunk (two 128-k halves)
 
 template <bool FP8>
@@ -708,11 +704,7 @@ __global__ __launch_bounds__(256) void gemm_rt_mfma_kernel(uint16_t* __restrict_
         };
         // rearranged pair of one load pair: R0 = piece kg of row li, R1 = piece kg + 4
         auto operands = [&](const u32x4& i0, const u32x4& i1, u32x4& r0, u32x4& r1) {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                r0[q] = low ? i0[q] : i1[q];
-                r1[q] = row_ror8(low ? i1[q] : i0[q]);
-            }
+            rows8x128_to_operands(i0, i1, low, r0, r1);
         };
         auto compute = [&](const u32x4 (&wv)[NW], const float (&sv)[2], int buf) {
             if constexpr (FP8) {
