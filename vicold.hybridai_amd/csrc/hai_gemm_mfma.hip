@@ -917,14 +917,15 @@ int sk_blocks(const void* kern, size_t shmem, const MfmaArgs& a) {
 }
 
 // The register-operand kernels serve K % 256 == 0 and up to 64 rows; the
-// environment variable HAI_MFMA_RT=0 selects the LDS-staged kernels instead
-// (read once per process).
-bool rt_enabled() {
-    static const bool on = [] {
+// environment variable HAI_MFMA_RT (read once per process) selects them for
+// the shapes use_rt names (unset or 1), never (0), or for every eligible
+// shape (2, for measurements).
+int rt_mode() {
+    static const int mode = [] {
         const char* e = std::getenv("HAI_MFMA_RT");
-        return e == nullptr || e[0] != '0';
+        return e == nullptr ? 1 : (e[0] == '0' ? 0 : (e[0] == '2' ? 2 : 1));
     }();
-    return on;
+    return mode;
 }
 
 template <int MT, int EPI>
@@ -1041,12 +1042,16 @@ int launch_mfma(const MfmaArgs& a, hipStream_t s) {
 // bytes in flight), and so did bf16 weights at 32 rows; those keep the
 // LDS-staged kernels.
 bool use_rt(const MfmaArgs& a) {
-    return a.wq != nullptr && a.K % kRtChunk == 0 && a.M > 16 && a.M <= 64 && a.N <= 8192 && rt_enabled();
+    if (a.K % kRtChunk != 0 || a.M > 64) return false;
+    const int mode = rt_mode();
+    if (mode == 2) return true;  // measurement: every eligible shape
+    return mode == 1 && a.wq != nullptr && a.M > 16 && a.N <= 8192;
 }
 
 template <int EPI>
 int dispatch_mfma(const MfmaArgs& a, hipStream_t s) {
     if (use_rt(a)) {
+        if (a.M <= 16) return launch_rt<1, EPI>(a, s);
         if (a.M <= 32) return launch_rt<2, EPI>(a, s);
         return launch_rt<4, EPI>(a, s);
     }
