@@ -1347,15 +1347,16 @@ __global__ __launch_bounds__(256) void gemm_tiled_kernel(TiledArgs a) {
             wdst[i] = r * kTileRow + c;
         }
     }
-    u32x4 xv[XP], wv[WP];
-    auto load = [&](int step) {
+    // operand registers of one step, two sets: a step's loads are issued two
+    // steps before they are multiplied (one before they are staged)
+    auto load = [&](u32x4 (&xv)[XP], u32x4 (&wv)[WP], int step) {
         const uint32_t k0 = static_cast<uint32_t>(step) * kTileK;
 #pragma unroll
         for (int i = 0; i < XP; ++i) xv[i] = bload(rx, xoff[i], k0 * 2);
 #pragma unroll
         for (int i = 0; i < WP; ++i) wv[i] = bload(rw, woff[i], FP8 ? k0 : k0 * 2);
     };
-    auto stage = [&](int buf) {
+    auto stage = [&](const u32x4 (&xv)[XP], const u32x4 (&wv)[WP], int buf) {
         uint16_t* xb = xs + buf * kTileM * kTileRow;
         uint16_t* wb = ws + buf * BN * kTileRow;
 #pragma unroll
@@ -1398,12 +1399,8 @@ __global__ __launch_bounds__(256) void gemm_tiled_kernel(TiledArgs a) {
         }
 
     const int nsteps = K / kTileK;
-    load(0);
-    stage(0);
-    __syncthreads();
-    for (int step = 0; step < nsteps; ++step) {
+    auto compute = [&](int step) {
         const int buf = step & 1;
-        if (step + 1 < nsteps) load(step + 1);
         const uint16_t* xb = xs + buf * kTileM * kTileRow;
         const uint16_t* wb = ws + buf * BN * kTileRow;
 #pragma unroll
@@ -1436,9 +1433,34 @@ __global__ __launch_bounds__(256) void gemm_tiled_kernel(TiledArgs a) {
                 }
             }
         }
-        if (step + 1 < nsteps) stage(buf ^ 1);
-        __syncthreads();
+    };
+    // Step s: request step s + 2 into one register set, multiply step s from
+    // LDS buffer s % 2, stage step s + 1 (requested a step earlier) into the
+    // other buffer, LDS-only barrier (the requests stay in flight).  Loads
+    // past the last step are clamped to it and never used, so the code
+    // between waits is straight-line and the compiler's wait counts exact.
+    auto clamps = [&](int st) { return min(st, nsteps - 1); };
+    u32x4 xA[XP], wA[WP], xB[XP], wB[WP];
+    load(xA, wA, 0);
+    load(xB, wB, clamps(1));
+    stage(xA, wA, 0);
+    lds_barrier();
+    auto step = [&](int st, u32x4 (&xl)[XP], u32x4 (&wl)[WP], const u32x4 (&xn)[XP], const u32x4 (&wn_)[WP]) {
+        load(xl, wl, clamps(st + 2));
+        pin_memory_order();
+        __builtin_amdgcn_sched_barrier(0);
+        compute(st);
+        pin_memory_order();
+        __builtin_amdgcn_sched_barrier(0);
+        stage(xn, wn_, (st + 1) & 1);
+        lds_barrier();
+    };
+    int st = 0;
+    for (; st + 2 <= nsteps; st += 2) {
+        step(st, xA, wA, xB, wB);
+        step(st + 1, xB, wB, xA, wA);
     }
+    if (st < nsteps) step(st, xA, wA, xB, wB);
 
     // lane (li, kg) holds rows 4 kg + i of each 16-row tile, column li of each 16-column tile
 #pragma unroll
