@@ -1,5 +1,6 @@
 """Prompt-sized linear layers on the matrix cores (hai_gemm_bf16_tiled /
-hai_gemm_fp8_tiled): every output within the tolerance of fp32 accumulation
+hai_gemm_fp8_tiled, and the bf16 prompt GEMMs through hipBLASLt,
+hai_gemm_bf16_blaslt): every output within the tolerance of fp32 accumulation
 and bf16 output rounding of the float64 product, at the 27B prefill shapes
 (gate|up with SwiGLU, down / o / out with the residual add) and at ragged
 ones (M, N not multiples of the tile, K with an odd number of 64-element
@@ -78,7 +79,7 @@ def check(got, y64, absdot, epi, h=None):
     assert np.allclose(got, want, rtol=2 ** -6, atol=2e-3 * scale), float(np.abs(got - want).max())
 
 
-def run(M, N, K, epi, fp8=False, special=False, mapped=False, seed=0):
+def run(M, N, K, epi, fp8=False, special=False, mapped=False, seed=0, blaslt=False):
     rng = np.random.default_rng(seed + M + 3 * N + 7 * K + epi)
     x, xb = rand_bf16(rng, (M, K))
     mp = None
@@ -115,6 +116,12 @@ def run(M, N, K, epi, fp8=False, special=False, mapped=False, seed=0):
         flag = 0 if special else hai.FP8_NO_SPECIAL_CODES
         hai.check(kern().hai_gemm_fp8_tiled(dy.ptr, ncols, dx.ptr, K, dq.ptr, ds.ptr, dm.ptr if dm else None, M, N, K,
                                             epi | flag, res, ncols, None), "gemm_fp8_tiled")
+    elif blaslt:
+        dw = dev(wb)
+        wsb = kern().hai_gemm_bf16_blaslt_workspace_bytes(M, N, epi)
+        dws = hai.DeviceBuffer(wsb)
+        hai.check(kern().hai_gemm_bf16_blaslt(dy.ptr, ncols, dx.ptr, K, dw.ptr, M, N, K, epi, res, ncols, dws.ptr, wsb,
+                                              None), "gemm_bf16_blaslt")
     else:
         dw = dev(wb)
         hai.check(kern().hai_gemm_bf16_tiled(dy.ptr, ncols, dx.ptr, K, dw.ptr, M, N, K, epi, res, ncols, None),
@@ -135,6 +142,25 @@ def run(M, N, K, epi, fp8=False, special=False, mapped=False, seed=0):
 ])
 def test_gemm_bf16_tiled(M, N, K, epi):
     run(M, N, K, epi)
+
+
+@pytest.mark.parametrize("M,N,K,epi", [
+    (512, 34816, 5120, 2),    # 27B gate|up, SwiGLU through the scratch and the pair kernel
+    (1024, 5120, 17408, 1),   # 27B down, residual as beta = 1 in place
+    (4096, 16480, 5120, 0),   # C4 chunk, in_proj with a|b
+    (300, 1000, 576, 0),      # ragged rows and columns
+    (130, 200, 64, 2),        # ragged SwiGLU pairs (100 outputs per row, not whole groups of 8)
+])
+def test_gemm_bf16_blaslt(M, N, K, epi):
+    run(M, N, K, epi, blaslt=True)
+
+
+def test_gemm_bf16_blaslt_refuses_short_workspace():
+    d = out_buf(1 << 16)
+    need = kern().hai_gemm_bf16_blaslt_workspace_bytes(64, 128, 2)
+    assert need > 64 * 128 * 2
+    assert kern().hai_gemm_bf16_blaslt(d.ptr, 64, d.ptr, 64, d.ptr, 64, 128, 64, 2, None, 0, d.ptr, need - 16,
+                                       None) == hai.ERR_INVALID
 
 
 @pytest.mark.parametrize("M,N,K,epi,special,mapped", [
