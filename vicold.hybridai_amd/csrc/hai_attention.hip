@@ -378,6 +378,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kMfmaWaves = 4;
+constexpr int kCombineBlockSplits = 16;  // splits per query row from which the merge takes a block per row
 constexpr int kMfmaMaxSteps = 16;          // steps per wave and block
 constexpr int64_t kMfmaTargetBlocks = 512; // blocks the split count aims for when the occupancy is unknown
 constexpr int kMfmaMinBlockKeys = 128;     // keys of the smallest block (one 32-key step per wave)
@@ -752,6 +753,64 @@ __global__ __launch_bounds__(D) void gqa_mfma_combine_kernel(uint16_t* __restric
     out[qidx * D + tid] = f2bf(v);
 }
 
+// The same merge with one wave per query row (four rows per block): the
+// form for prompt chunks, whose many query rows hold few splits each.
+template <int D>
+__global__ __launch_bounds__(256) void gqa_mfma_combine_wave_kernel(uint16_t* __restrict__ out,
+                                                               const float* __restrict__ part, const uint16_t* gate,
+                                                               int B, int T, int nq, const int32_t* lens,
+                                                               int len_add, int nsplit, int block_keys) {
+    const int lane = threadIdx.x & 63;
+    const int64_t qidx = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (qidx >= static_cast<int64_t>(B) * T * nq) return;
+    const int b = static_cast<int>(qidx / (static_cast<int64_t>(T) * nq));
+    const int64_t L = static_cast<int64_t>(lens ? lens[b] : 0) + len_add;
+    const int nv = static_cast<int>(min(static_cast<int64_t>(nsplit), (L + block_keys - 1) / block_keys));
+    constexpr int64_t PS = mfma_part_stride(D);
+    const float* base = part + qidx * nsplit * PS;
+    float M = -__builtin_huge_valf();
+    for (int c = lane; c < nv; c += 64) M = fmaxf(M, base[c * PS + D]);
+    M = wave_max64(M);
+    constexpr int PER = D / 64;
+    float O[PER];
+#pragma unroll
+    for (int r = 0; r < PER; ++r) O[r] = 0.0f;
+    float Ls = 0.0f;
+    int c = 0;
+    for (; c + 4 <= nv; c += 4) {
+        float mv[4], lv[4], ov[4][PER];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const float* p = base + (c + u) * PS;
+            mv[u] = p[D];
+            lv[u] = p[D + 1];
+#pragma unroll
+            for (int r = 0; r < PER; ++r) ov[u][r] = p[lane + 64 * r];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const float w = __builtin_amdgcn_exp2f(mv[u] - M);
+            Ls = fma_(lv[u], w, Ls);
+#pragma unroll
+            for (int r = 0; r < PER; ++r) O[r] = fma_(ov[u][r], w, O[r]);
+        }
+    }
+    for (; c < nv; ++c) {
+        const float* p = base + c * PS;
+        const float w = __builtin_amdgcn_exp2f(p[D] - M);
+        Ls = fma_(p[D + 1], w, Ls);
+#pragma unroll
+        for (int r = 0; r < PER; ++r) O[r] = fma_(p[lane + 64 * r], w, O[r]);
+    }
+#pragma unroll
+    for (int r = 0; r < PER; ++r) {
+        const int d = lane + 64 * r;
+        float v = O[r] / Ls;
+        if (gate != nullptr) v = v * csigmoid(bf2f(gate[qidx * D + d]));
+        out[qidx * D + d] = f2bf(v);
+    }
+}
+
 // Split plan of the matrix-core path: steps per wave (block = 4 waves x steps
 // x KS keys) and the number of splits covering max_len.
 struct MfmaPlan {
@@ -799,8 +858,15 @@ int launch_mfma(uint16_t* out, const uint16_t* q, const uint16_t* gate, const ui
     int rc = launched("gqa_mfma_partial_kernel");
     if (rc != HAI_OK) return rc;
     const int64_t nall = static_cast<int64_t>(B) * T * nq;
-    gqa_mfma_combine_kernel<D><<<dim3(static_cast<unsigned>(nall)), dim3(D), 0, s>>>(
-        out, scratch, gate, B, T, nq, lens, len_add, p.nsplit, p.block_keys);
+    // a block per query row when a row merges many splits (decode), a wave
+    // per row when there are many rows of few splits (prompt chunks); the
+    // two forms give the same bits
+    if (p.nsplit >= kCombineBlockSplits)
+        gqa_mfma_combine_kernel<D><<<dim3(static_cast<unsigned>(nall)), dim3(D), 0, s>>>(
+            out, scratch, gate, B, T, nq, lens, len_add, p.nsplit, p.block_keys);
+    else
+        gqa_mfma_combine_wave_kernel<D><<<dim3(static_cast<unsigned>((nall + 3) / 4)), dim3(256), 0, s>>>(
+            out, scratch, gate, B, T, nq, lens, len_add, p.nsplit, p.block_keys);
     return launched("gqa_mfma_combine_kernel");
 }
 
