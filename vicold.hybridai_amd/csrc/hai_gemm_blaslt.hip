@@ -54,9 +54,8 @@ __global__ __launch_bounds__(256) void swiglu_pairs_kernel(uint16_t* __restrict_
         uint32_t o[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const uint16_t lo = f2bf(csilu(lo_bf(w[2 * q])) * hi_bf(w[2 * q]));
-            const uint16_t hi = f2bf(csilu(lo_bf(w[2 * q + 1])) * hi_bf(w[2 * q + 1]));
-            o[q] = static_cast<uint32_t>(lo) | (static_cast<uint32_t>(hi) << 16);
+            o[q] = f2bf2(csilu(lo_bf(w[2 * q])) * hi_bf(w[2 * q]),
+                         csilu(lo_bf(w[2 * q + 1])) * hi_bf(w[2 * q + 1]));
         }
         if ((reinterpret_cast<uintptr_t>(yr) & 15u) == 0) {
             *reinterpret_cast<u32x4*>(yr) = u32x4{o[0], o[1], o[2], o[3]};

@@ -85,11 +85,9 @@ __device__ __forceinline__ void normalize_staged_rows(u32x4* xs, int M, int K, c
         const u32x4 wv0 = xs[total + p];
         u32x4 o;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const uint16_t a = f2bf((lo_bf(xv0[q]) * inv) * (lo_bf(wv0[q]) + na.off));
-            const uint16_t b = f2bf((hi_bf(xv0[q]) * inv) * (hi_bf(wv0[q]) + na.off));
-            o[q] = static_cast<uint32_t>(a) | (static_cast<uint32_t>(b) << 16);
-        }
+        for (int q = 0; q < 4; ++q)
+            o[q] = f2bf2((lo_bf(xv0[q]) * inv) * (lo_bf(wv0[q]) + na.off),
+                         (hi_bf(xv0[q]) * inv) * (hi_bf(wv0[q]) + na.off));
         xs[e] = o;
         if (na.xn != nullptr && blockIdx.x == 0) *reinterpret_cast<u32x4*>(na.xn + r * na.ldxn + p * 8) = o;
     }

@@ -310,9 +310,8 @@ __global__ __launch_bounds__(256) void mfma_residual_rmsnorm_kernel(uint16_t* __
         uint32_t o[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            const uint16_t lo = f2bf(lo_bf(r[g][e]) + bfr(v[2 * e]));
-            const uint16_t hi = f2bf(hi_bf(r[g][e]) + bfr(v[2 * e + 1]));
-            o[e] = static_cast<uint32_t>(lo) | (static_cast<uint32_t>(hi) << 16);
+            o[e] = f2bf2(lo_bf(r[g][e]) + bfr(v[2 * e]),
+                         hi_bf(r[g][e]) + bfr(v[2 * e + 1]));
         }
         const u32x4 hv = u32x4{o[0], o[1], o[2], o[3]};
         *reinterpret_cast<u32x4*>(hr + k0) = hv;
@@ -348,9 +347,8 @@ __global__ __launch_bounds__(256) void mfma_residual_rmsnorm_kernel(uint16_t* __
         uint32_t o[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const uint16_t a = f2bf((lo_bf(hv[q]) * inv) * (lo_bf(wd[q]) + off));
-            const uint16_t b = f2bf((hi_bf(hv[q]) * inv) * (hi_bf(wd[q]) + off));
-            o[q] = static_cast<uint32_t>(a) | (static_cast<uint32_t>(b) << 16);
+            o[q] = f2bf2((lo_bf(hv[q]) * inv) * (lo_bf(wd[q]) + off),
+                         (hi_bf(hv[q]) * inv) * (hi_bf(wd[q]) + off));
         }
         *reinterpret_cast<u32x4*>(xr + k0) = u32x4{o[0], o[1], o[2], o[3]};
     }

@@ -57,9 +57,8 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(uint16_t* __restrict__ y, 
         uint32_t o[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const uint16_t a = f2bf((lo_bf(xs[q]) * inv) * (lo_bf(ws[q]) + off));
-            const uint16_t b = f2bf((hi_bf(xs[q]) * inv) * (hi_bf(ws[q]) + off));
-            o[q] = static_cast<uint32_t>(a) | (static_cast<uint32_t>(b) << 16);
+            o[q] = f2bf2((lo_bf(xs[q]) * inv) * (lo_bf(ws[q]) + off),
+                         (hi_bf(xs[q]) * inv) * (hi_bf(ws[q]) + off));
         }
         *reinterpret_cast<uint4*>(yr + k0) = make_uint4(o[0], o[1], o[2], o[3]);
     }
