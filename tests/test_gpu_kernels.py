@@ -72,6 +72,31 @@ def test_primitives_bit_exact(fn, name):
     assert bad.size == 0, f"{name}: {bad.size} mismatches, e.g. x={x[bad[:5]]} got={got[bad[:5]]} want={want[bad[:5]]}"
 
 
+def test_bf16_rounding_bits_with_nans():
+    """The device's f32 -> bf16 rounding (gfx950 v_cvt_pk_bf16_f32 in every
+    kernel) equals the oracle's integer round-to-nearest-even bit for bit,
+    NaNs included (sign and upper payload kept, quiet bit set): NaN classes,
+    exact ties to even and odd, denormals, values that round up to inf."""
+    rng = np.random.default_rng(77)
+    pats = []
+    for s in (0, 0x80000000):
+        for m in (1, 0x10000, 0x8000, 0x18000, 0x3FFFFF, 0x400000, 0x7FFFFF, 0x1FFFF, 0x55AA55):
+            pats.append(s | 0x7F800000 | m)                       # NaNs, signalling and quiet
+        for x in (0x7F800000, 0, 1, 0x7FFF, 0x8000, 0x18000, 0x10000, 0x7F7FFFFF, 0x7F7F8000,
+                  0x7F7F7FFF, 0x3F808000, 0x3F818000, 0x3F80FFFF, 0x007FFFFF, 0x00008000, 0x00018000):
+            pats.append(s | x)                                    # inf, ties, denormals, overflow
+    pats = np.array(pats, np.uint32)
+    rand = rng.integers(0, 1 << 32, 1 << 18, dtype=np.uint64).astype(np.uint32)
+    x = np.concatenate([pats, rand]).view(np.float32)
+    dx, dy = dev(x), out_buf(x.nbytes)
+    hai.check(kern().hai_debug_math_f32(dy.ptr, dx.ptr, x.size, 6, None), "debug_math bf16")
+    got = dy.download(np.uint32)
+    want = orc.round_bf16(x).view(np.uint32)
+    bad = np.nonzero(got != want)[0]
+    assert bad.size == 0, (f"{bad.size} mismatches, e.g. x={x.view(np.uint32)[bad[:4]]} got={got[bad[:4]]} "
+                           f"want={want[bad[:4]]}")
+
+
 # ----------------------------------------------------------------- gemm
 @pytest.mark.parametrize("M,N,K_", [(1, 37, 8), (2, 256, 256), (2, 1536, 256), (3, 4096, 256),
                                     (4, 100, 1000), (7, 64, 520), (16, 512, 768), (2, 5120, 17408),
