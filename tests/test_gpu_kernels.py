@@ -1052,7 +1052,9 @@ def test_gemm_mfma_within_tolerance(M, N, K, epi, with_ws):
 @pytest.mark.parametrize("M,N,K,epi,mapped,special", [(32, 1536, 5120, 0, False, True), (64, 2 * 640, 1024, 2, False, False),
                                                       (17, 700, 1008, 1, True, False), (128, 5120, 2048, 1, False, False),
                                                       (48, 16400, 512, 0, True, True),
-                                                      (40, 2000, 2048, 1, True, True), (24, 4096, 1536, 2, False, False)])
+                                                      (40, 2000, 2048, 1, True, True), (24, 4096, 1536, 2, False, False),
+                                                      (40, 9000, 1024, 0, True, True), (20, 12000, 768, 1, False, True),
+                                                      (24, 8320, 256, 2, False, False)])
 def test_gemm_fp8_mfma_within_tolerance(M, N, K, epi, mapped, special):
     """hai_gemm_fp8_mfma against the canonical FP8 GEMM (dequantised weights,
     fp32 dot): bf16 outputs within a couple of bf16 ulps; 0x7F / 0xFF codes
@@ -1123,7 +1125,8 @@ def test_gemm_mfma_27b_shapes(M, N, K, epi):
     assert np.allclose(got, want, rtol=2 ** -6, atol=2e-3 * scale), float(np.abs(got - want).max())
 
 
-@pytest.mark.parametrize("M,N,K,epi", [(64, 34816, 5120, 2), (64, 5120, 17408, 1), (64, 16384, 5120, 0)])
+@pytest.mark.parametrize("M,N,K,epi", [(64, 34816, 5120, 2), (64, 5120, 17408, 1), (64, 16384, 5120, 0),
+                                       (64, 14336, 5120, 0), (32, 14336, 5120, 0)])
 def test_gemm_fp8_mfma_27b_shapes(M, N, K, epi):
     """The C5 batched-verify GEMMs (32 sequences x 2 rows, FP8 E4M3 weights
     with 128x128 scales): gate/up with SwiGLU over paired scale grids, down

@@ -856,6 +856,310 @@ __global__ __launch_bounds__(256) void gemm_rt_mfma_kernel(uint16_t* __restrict_
     }
 }
 
+// ---------------------------------------------------------------------------
+// Copy-staged variant for FP8 weights on the wide layers at 17-64 rows: the
+// register-operand kernel's tile, roles and arithmetic (a wave owns 32
+// weight rows and one 128-k half of every 256-k chunk, codes decoded
+// exactly to bf16 in its B operands, scale blocks applied in fp32), with
+// every operand staged by global -> LDS copies instead of registers, so
+// that the weight bytes in flight are bounded by LDS rather than by VGPRs:
+//   * three weight stages (64 rows x 256 codes, 16 KB, and behind them the
+//     chunk's scales, one 4-byte copy per lane and n-tile) and three
+//     activation stages (16 MT rows x 256 bf16); the weights, scales and
+//     activations of chunk i + 2 are requested before chunk i is
+//     multiplied, and one s_waitcnt counts them;
+//   * the stages are read by inline ds_read instructions that wait for
+//     their own results: the compiler's wait insertion cannot tell a copy
+//     into one stage from a read of another and would otherwise drain every
+//     outstanding copy (s_waitcnt vmcnt(0)) before each LDS read;
+//   * a wave copies and reads only its own weight region (32 rows x 128
+//     bytes, row r's 16-byte piece p at slot p ^ (r & 7)); the activation
+//     stages are filled by all four waves (row r's piece p at slot
+//     p ^ (r & 15), as the register-operand kernel stores them) and read by
+//     all behind a barrier.
+// Weight rows past N and activation rows past M are read from the last row
+// (their results are never stored); chunks past K from the last chunk
+// (never used).
+// ---------------------------------------------------------------------------
+// One global -> LDS copy per lane of 16 bytes (to lds + 16 * lane) or 4
+// bytes (to lds + 4 * lane).  __device__ functions rather than calls inside
+// the kernel's lambdas: the host pass instantiates those lambdas too, and
+// the builtin there made it drop the kernel's host stub.
+__device__ __forceinline__ void copy16_to_lds(const void* src, void* lds) {
+    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+}
+__device__ __forceinline__ void copy4_to_lds(const void* src, void* lds) {
+    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds, 4, 0, 0);
+}
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)p));
+}
+// Reads of the copy-staged kernel, each group complete when its asm ends.
+__device__ __forceinline__ void lds_b128x4_b32x2(const uint32_t (&a)[4], const uint32_t (&sa)[2], u32x4 (&r)[4],
+                                                 float (&f)[2]) {
+    asm volatile(
+        "ds_read_b128 %0, %6\n\tds_read_b128 %1, %7\n\tds_read_b128 %2, %8\n\tds_read_b128 %3, %9\n\t"
+        "ds_read_b32 %4, %10\n\tds_read_b32 %5, %11\n\ts_waitcnt lgkmcnt(0)"
+        : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(f[0]), "=&v"(f[1])
+        : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(sa[0]), "v"(sa[1])
+        : "memory");
+}
+__device__ __forceinline__ void lds_b128x4(const uint32_t (&a)[4], u32x4 (&r)[4]) {
+    asm volatile(
+        "ds_read_b128 %0, %4\n\tds_read_b128 %1, %5\n\tds_read_b128 %2, %6\n\tds_read_b128 %3, %7\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3])
+        : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3])
+        : "memory");
+}
+__device__ __forceinline__ void lds_b128x8(const uint32_t (&a)[8], u32x4 (&r)[8]) {
+    asm volatile(
+        "ds_read_b128 %0, %8\n\tds_read_b128 %1, %9\n\tds_read_b128 %2, %10\n\tds_read_b128 %3, %11\n\t"
+        "ds_read_b128 %4, %12\n\tds_read_b128 %5, %13\n\tds_read_b128 %6, %14\n\tds_read_b128 %7, %15\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]), "=&v"(r[7])
+        : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(a[4]), "v"(a[5]), "v"(a[6]), "v"(a[7])
+        : "memory");
+}
+
+// One block per 64-row tile over the whole K (the grid is the tiles).
+template <int MT, int EPI, bool CHECK>
+__global__ __launch_bounds__(256) void gemm_dma_mfma_kernel(uint16_t* __restrict__ y, int64_t ldy,
+                                                            const uint16_t* __restrict__ x, int64_t ldx,
+                                                            const uint8_t* w, const float* __restrict__ scales,
+                                                            const int32_t* __restrict__ scale_rows, int paired,
+                                                            const uint16_t* res, int64_t ldres, int M, int N,
+                                                            int K) {
+    static_assert(MT == 2 || MT == 4, "32 or 64 activation rows");
+    constexpr int XR = 16 * MT;                // staged activation rows
+    constexpr int XE = XR * kRtChunk;          // bf16 elements per activation stage
+    constexpr int WB = kBlockRows * kRtChunk;  // weight bytes per stage
+    constexpr int WS = WB + 4 * 2 * 256;       // + the scales: [wave][n-tile][64 lanes] floats
+    constexpr int XOPS = 2 * MT;               // 1 KB activation copies per wave and chunk
+    constexpr int kAhead = 12 + 4 * MT;        // requests issued after a chunk's activations
+    __shared__ __align__(16) uint16_t xs0[XE], xs1[XE], xs2[XE];
+    __shared__ __align__(16) uint8_t ws0[WS], ws1[WS], ws2[WS];
+    const int lane = threadIdx.x & 63;
+    const int wave = wave_index();
+    const int li = lane & 15;
+    const int kg = lane >> 4;
+    const int nh = wave & 1;
+    const int kh = wave >> 1;
+    const int nck = K / kRtChunk;
+    const int nkb = K / 128;
+
+    // activation copies: piece e = (wave * XOPS + i) * 64 + lane is row e / 32,
+    // slot e % 32, holding the row's piece slot ^ (row % 16)
+    const uint16_t* xsrc[XOPS];
+#pragma unroll
+    for (int i = 0; i < XOPS; ++i) {
+        const int e = (wave * XOPS + i) * 64 + lane;
+        const int r = e >> 5;
+        const int pos = e & 31;
+        xsrc[i] = x + static_cast<int64_t>(min(r, M - 1)) * ldx + (pos ^ (r & 15)) * 8;
+    }
+    auto copy_x = [&](uint16_t* st, int c) {
+#pragma unroll
+        for (int i = 0; i < XOPS; ++i)
+            copy16_to_lds(xsrc[i] + c * kRtChunk, st + (wave * XOPS + i) * 512);
+    };
+    // LDS byte offsets of the A operands within a stage: 8 elements of row
+    // 16 mt + li at 16-byte piece pa + poff[s4]
+    const int pa = 16 * kh + 2 * kg;
+    const int poff[4] = {0, 1, 8, 9};
+    uint32_t aoff[4][MT];
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+            aoff[s4][mt] = static_cast<uint32_t>(((16 * mt + li) * kRtChunk + (((pa + poff[s4]) ^ li) * 8)) * 2);
+    // B operands: row 16 t + li of the wave's region, pieces kg and kg + 4
+    uint32_t boff[4];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        boff[2 * t] = static_cast<uint32_t>(wave * 4096 + (16 * t + li) * 128 + ((kg ^ (li & 7)) * 16));
+        boff[2 * t + 1] = static_cast<uint32_t>(wave * 4096 + (16 * t + li) * 128 + (((kg + 4) ^ (li & 7)) * 16));
+    }
+    const uint32_t soff[2] = {static_cast<uint32_t>(WB + (wave * 2 + 0) * 256 + lane * 4),
+                              static_cast<uint32_t>(WB + (wave * 2 + 1) * 256 + lane * 4)};
+
+    {
+        const int64_t row_base = static_cast<int64_t>(blockIdx.x) * kBlockRows + 32 * nh;
+        // weight copies j = 0..3 of the wave's region: rows 8 j + lane / 8,
+        // slot lane % 8 holding piece slot ^ (lane / 8)
+        const uint8_t* wsrc[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int64_t row = min(row_base + 8 * j + (lane >> 3), static_cast<int64_t>(N) - 1);
+            wsrc[j] = w + row * K + kh * 128 + (((lane & 7) ^ (lane >> 3)) * 16);
+        }
+        const float* srp[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const int64_t ncol = min(row_base + 16 * t + li, static_cast<int64_t>(N) - 1);
+            const int64_t nsb = ((N >> 1) + 127) / 128;
+            const int64_t srow =
+                scale_rows ? scale_rows[ncol] : (paired ? (ncol & 1) * nsb + (ncol >> 1) / 128 : ncol / 128);
+            srp[t] = scales + srow * nkb + kh;
+        }
+        // the chunk's weights, then its two scales (copies of 16 and 4 bytes)
+        auto copy_w = [&](uint8_t* st, int c) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                copy16_to_lds(wsrc[j] + c * kRtChunk, st + wave * 4096 + j * 1024);
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+                copy4_to_lds(srp[t] + 2 * c, st + WB + (wave * 2 + t) * 256);
+        };
+        f32x4 tot[MT][2];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int t = 0; t < 2; ++t) tot[mt][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+        auto compute = [&](const uint8_t* wst, const uint16_t* xst) {
+            const uint32_t wb = lds_addr(wst), xb = lds_addr(xst);
+            // the B operands, the scales and the A operands of the first two k-steps
+            u32x4 rw[4];
+            float sv[2];
+            const uint32_t ba[4] = {wb + boff[0], wb + boff[1], wb + boff[2], wb + boff[3]};
+            const uint32_t sa[2] = {wb + soff[0], wb + soff[1]};
+            u32x4 av[4][MT];
+            if constexpr (MT == 4) {
+                lds_b128x4_b32x2(ba, sa, rw, sv);
+                const uint32_t aa[8] = {xb + aoff[0][0], xb + aoff[0][1], xb + aoff[0][2], xb + aoff[0][3],
+                                        xb + aoff[1][0], xb + aoff[1][1], xb + aoff[1][2], xb + aoff[1][3]};
+                u32x4 ar[8];
+                lds_b128x8(aa, ar);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) av[i / 4][i % 4] = ar[i];
+            } else {
+                lds_b128x4_b32x2(ba, sa, rw, sv);
+                const uint32_t aa[4] = {xb + aoff[0][0], xb + aoff[0][1], xb + aoff[1][0], xb + aoff[1][1]};
+                u32x4 ar[4];
+                lds_b128x4(aa, ar);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) av[i / 2][i % 2] = ar[i];
+            }
+            // 128 codes of the wave's half per row: piece kg holds k 16 kg .. + 15,
+            // piece kg + 4 k 64 + 16 kg .. + 15
+            u32x4 b[2][4];
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                uint32_t d[16];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    e4m3x4_to_bf16<CHECK>(rw[2 * t][q], d[2 * q], d[2 * q + 1]);
+                    e4m3x4_to_bf16<CHECK>(rw[2 * t + 1][q], d[8 + 2 * q], d[8 + 2 * q + 1]);
+                }
+                b[t][0] = u32x4{d[0], d[1], d[2], d[3]};
+                b[t][1] = u32x4{d[4], d[5], d[6], d[7]};
+                b[t][2] = u32x4{d[8], d[9], d[10], d[11]};
+                b[t][3] = u32x4{d[12], d[13], d[14], d[15]};
+            }
+            f32x4 acc[MT][2];
+#pragma unroll
+            for (int s4 = 0; s4 < 2; ++s4)
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                    for (int t = 0; t < 2; ++t)
+                        acc[mt][t] = mfma16(av[s4][mt], b[t][s4], s4 == 0 ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : acc[mt][t]);
+            // the A operands of the last two k-steps, read while those run
+            if constexpr (MT == 4) {
+                const uint32_t aa[8] = {xb + aoff[2][0], xb + aoff[2][1], xb + aoff[2][2], xb + aoff[2][3],
+                                        xb + aoff[3][0], xb + aoff[3][1], xb + aoff[3][2], xb + aoff[3][3]};
+                u32x4 ar[8];
+                lds_b128x8(aa, ar);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) av[2 + i / 4][i % 4] = ar[i];
+            } else {
+                const uint32_t aa[4] = {xb + aoff[2][0], xb + aoff[2][1], xb + aoff[3][0], xb + aoff[3][1]};
+                u32x4 ar[4];
+                lds_b128x4(aa, ar);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) av[2 + i / 2][i % 2] = ar[i];
+            }
+#pragma unroll
+            for (int s4 = 2; s4 < 4; ++s4)
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                    for (int t = 0; t < 2; ++t) acc[mt][t] = mfma16(av[s4][mt], b[t][s4], acc[mt][t]);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int t = 0; t < 2; ++t)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) tot[mt][t][i] = fma_(sv[t], acc[mt][t][i], tot[mt][t][i]);
+        };
+
+        auto clampc = [&](int c) { return min(c, nck - 1); };
+        // order (weights, then activations, per chunk): a chunk's activations
+        // are followed by exactly kAhead requests when its step waits
+        copy_w(ws0, 0);
+        copy_x(xs0, 0);
+        copy_w(ws1, clampc(1));
+        copy_x(xs1, clampc(1));
+        // chunk i: barrier (every wave is done with chunk i - 1), request the
+        // weights, scales and activations of chunk i + 2 into the stages
+        // chunk i - 1 used, wait for chunk i's copies, barrier (all waves'
+        // activation copies landed), multiply
+        auto step = [&](int i, const uint8_t* wcur, const uint16_t* xcur, uint8_t* wnext, uint16_t* xnext) {
+            if (i >= nck) return false;
+            lds_barrier();
+            pin_memory_order();
+            __builtin_amdgcn_sched_barrier(0);
+            copy_w(wnext, clampc(i + 2));
+            copy_x(xnext, clampc(i + 2));
+            pin_memory_order();
+            __builtin_amdgcn_sched_barrier(0);
+            wait_vmcnt<kAhead>();
+            __builtin_amdgcn_sched_barrier(0);
+            lds_barrier();
+            compute(wcur, xcur);
+            return true;
+        };
+        for (int i = 0;; i += 3) {
+            if (!step(i, ws0, xs0, ws2, xs2)) break;
+            if (!step(i + 1, ws1, xs1, ws0, xs0)) break;
+            if (!step(i + 2, ws2, xs2, ws1, xs1)) break;
+        }
+
+        // the two k-halves of the tile: half 1 through LDS, added to half 0
+        wait_vmcnt<0>();
+        __syncthreads();
+        float* red = reinterpret_cast<float*>(xs0);  // [2 nh][MT][2][64 lanes] f32x4
+        if (kh == 1) {
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int t = 0; t < 2; ++t)
+                    *reinterpret_cast<f32x4*>(red + (((nh * MT + mt) * 2 + t) * 64 + lane) * 4) = tot[mt][t];
+        }
+        __syncthreads();
+        if (kh == 0) {
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    const f32x4 o = *reinterpret_cast<const f32x4*>(red + (((nh * MT + mt) * 2 + t) * 64 + lane) * 4);
+                    tot[mt][t] = tot[mt][t] + o;
+                }
+            // D layout: lane (li, kg) holds rows 16 mt + 4 kg + i of column row_base + 16 t + li
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const int64_t n = row_base + 16 * t + li;
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        mfma_store<EPI>(y, ldy, res, ldres, tot[mt][t][i], 16 * mt + 4 * kg + i, n, M, N, li);
+            }
+        }
+    }
+}
+
 struct MfmaArgs {
     uint16_t* y;
     int64_t ldy;
@@ -876,6 +1180,8 @@ struct MfmaArgs {
     bool keep = false;  // leave the K-split partials for hai_mfma_residual_rmsnorm_bf16
     size_t ws_bytes = 0;
 };
+
+int device_cus();
 
 // LDS above the 64 KB default needs the attribute, once per kernel instance.
 int allow_lds(const void* kern, size_t shmem, bool* done) {
@@ -974,6 +1280,18 @@ int launch_rt(const MfmaArgs& a, hipStream_t s) {
     return launched("mfma_finalize_kernel");
 }
 
+// The copy-staged FP8 kernel: one block per 64-row tile (150 KB of LDS at
+// 64 rows, one block per CU), K not split.
+template <int MT, int EPI>
+int launch_dma(const MfmaArgs& a, hipStream_t s) {
+    auto* kern = a.check ? gemm_dma_mfma_kernel<MT, EPI, true> : gemm_dma_mfma_kernel<MT, EPI, false>;
+    const int64_t ntiles = (static_cast<int64_t>(a.N) + kBlockRows - 1) / kBlockRows;
+    kern<<<dim3(static_cast<unsigned>(ntiles)), dim3(256), 0, s>>>(a.y, a.ldy, a.x, a.ldx, a.wq, a.scales,
+                                                                  a.scale_rows, a.paired, a.res, a.ldres, a.M, a.N,
+                                                                  a.K);
+    return launched("gemm_dma_mfma_kernel");
+}
+
 template <int MT, int EPI>
 int launch_mfma(const MfmaArgs& a, hipStream_t s) {
     const size_t shmem = static_cast<size_t>(16 * MT + 4 * 16) * kLdsRow * 2;
@@ -1039,6 +1357,23 @@ int launch_mfma(const MfmaArgs& a, hipStream_t s) {
 // M = 64 83 -> 114 us: two resident blocks per CU keep too few weight
 // bytes in flight), and so did bf16 weights at 32 rows; those keep the
 // LDS-staged kernels.
+// The copy-staged kernel: FP8 weights, 17-64 rows, layers wider than 8192
+// rows with at most one 64-row tile per CU (in_proj qkv|z and q|gate|k|v
+// at the 27B shapes; measured on MI355X at M = 64: 39.7 -> 33.8 us and
+// 37.5 -> 32.9 us, at M = 32 in_proj 25.3 -> 21.5 us).  gate|up (544
+// tiles) keeps the LDS-staged kernel with stream-K: there a block takes
+// parts of three tiles and refills the copy pipeline for each (84.8 us
+// against 94.9).  HAI_MFMA_DMA=0 keeps the LDS-staged kernels everywhere.
+bool use_dma(const MfmaArgs& a) {
+    static const bool on = [] {
+        const char* e = std::getenv("HAI_MFMA_DMA");
+        return e == nullptr || e[0] != '0';
+    }();
+    const int64_t ntiles = (static_cast<int64_t>(a.N) + kBlockRows - 1) / kBlockRows;
+    return on && a.wq != nullptr && a.K % kRtChunk == 0 && a.M > 16 && a.M <= 64 && a.N > 8192 && !a.keep &&
+           ntiles <= device_cus();
+}
+
 bool use_rt(const MfmaArgs& a) {
     if (a.K % kRtChunk != 0 || a.M > 64) return false;
     const int mode = rt_mode();
@@ -1048,6 +1383,10 @@ bool use_rt(const MfmaArgs& a) {
 
 template <int EPI>
 int dispatch_mfma(const MfmaArgs& a, hipStream_t s) {
+    if (use_dma(a)) {
+        if (a.M <= 32) return launch_dma<2, EPI>(a, s);
+        return launch_dma<4, EPI>(a, s);
+    }
     if (use_rt(a)) {
         if (a.M <= 16) return launch_rt<1, EPI>(a, s);
         if (a.M <= 32) return launch_rt<2, EPI>(a, s);
