@@ -1360,7 +1360,8 @@ int launch_mfma(const MfmaArgs& a, hipStream_t s) {
 // The copy-staged kernel: FP8 weights, 17-64 rows, layers wider than 8192
 // rows with at most one 64-row tile per CU (in_proj qkv|z and q|gate|k|v
 // at the 27B shapes; measured on MI355X at M = 64: 39.7 -> 33.8 us and
-// 37.5 -> 32.9 us, at M = 32 in_proj 25.3 -> 21.5 us).  gate|up (544
+// 37.5 -> 32.9 us per call including the K-split finalize the other kernel
+// needs, at M = 32 in_proj 25.3 -> 21.5 us).  gate|up (544
 // tiles) keeps the LDS-staged kernel with stream-K: there a block takes
 // parts of three tiles and refills the copy pipeline for each (84.8 us
 // against 94.9).  HAI_MFMA_DMA=0 keeps the LDS-staged kernels everywhere.
