@@ -59,3 +59,43 @@ def test_staged_copy_waits_count_the_requests_behind_them(tmp_path):
             assert m > 0, f"{name}: the prologue waits for every prefetched request ({body[nxt].strip()})"
         checked += 1
     assert checked >= 4, f"only {checked} staging kernels found"
+
+
+def test_copy_staged_mfma_pipeline_waits(tmp_path):
+    """gemm_dma_mfma_kernel (hai_gemm_mfma.hip): every step issues the
+    chunk's 6 + 2 MT copies (weights, scales, activations) and then waits
+    with s_waitcnt vmcnt(12 + 4 MT) -- the copies of the two chunks behind
+    the one it multiplies -- and no other vector-memory wait stands between
+    that wait and the step's LDS reads (a vmcnt(0) there would drain the
+    pipeline); no scratch memory (spills would put such waits back)."""
+    import build
+    if not Path(build.HIPCC).exists() and shutil.which("hipcc") is None:
+        pytest.skip("hipcc not available")
+    out = tmp_path / "mfma.s"
+    flags = [f for f in build.HIP_FLAGS if f != "-fPIC"]
+    subprocess.run([build.HIPCC, *flags, "--cuda-device-only", "-S", str(build.CSRC / "hai_gemm_mfma.hip"), "-o",
+                    str(out)], check=True, capture_output=True, timeout=900)
+    lines = out.read_text().split("\n")
+    checked = 0
+    for i, line in enumerate(lines):
+        m = re.match(r"^(_Z\S*gemm_dma_mfma_kernelILi(\d)\S*):", line)
+        if not m:
+            continue
+        mt = int(m.group(2))
+        end = next(j for j in range(i, len(lines)) if "s_endpgm" in lines[j])
+        body = lines[i:end]
+        assert not any("scratch_" in l for l in body), f"{m.group(1)}: scratch memory"
+        ahead = 12 + 4 * mt
+        waits = [k for k, l in enumerate(body) if re.search(rf"s_waitcnt vmcnt\({ahead}\)", l)]
+        assert waits, f"{m.group(1)}: no s_waitcnt vmcnt({ahead})"
+        for k in waits:
+            start = max(b for b in range(k) if "s_barrier" in body[b])
+            copies = sum(1 for b in range(start, k) if "global_load_lds" in body[b])
+            other = sum(1 for b in range(start, k) if ("global_load" in body[b] or "buffer_load" in body[b])
+                        and "lds" not in body[b])
+            assert copies == 6 + 2 * mt and other == 0, f"{m.group(1)}: {copies} copies, {other} loads before the wait"
+            read = next(b for b in range(k, len(body)) if "ds_read_b128" in body[b])
+            stray = [body[b].strip() for b in range(k + 1, read) if "vmcnt(" in body[b]]
+            assert not stray, f"{m.group(1)}: {stray} between the pipeline wait and the reads"
+        checked += 1
+    assert checked >= 6, f"only {checked} copy-staged kernels found"
