@@ -531,6 +531,28 @@ int hai_gemm_bf16_blaslt(void* y, int64_t ldy, const void* x, int64_t ldx,
                          const void* w, int64_t M, int64_t N, int64_t K,
                          int epilogue, const void* res, int64_t ld_res,
                          void* workspace, size_t workspace_bytes, void* stream);
+/* FP8 E4M3 weights [N, K] with 128x128 fp32 block scales to bf16 rows
+ * out[n][k] = bf16(decode(q) * s): the reference's dequantize_2d
+ * (fp8_dequant.cc:12-146; 0x7F / 0xFF decode to +-480) rounded to bf16.
+ * Scale rows as in hai_gemm_fp8_mfma: scale_rows[n] when given, else the
+ * interleaved gate / up grids when paired, else n / 128.  K % 16 == 0. */
+int hai_fp8_dequant_bf16(void* out, int64_t ld_out, const void* wq,
+                         const float* scales, const int32_t* scale_rows,
+                         int64_t N, int64_t K, int paired, void* stream);
+/* The prompt-chunk FP8 GEMM through hipBLASLt (the rocblas_gemm_ex call
+ * site of HipBackend::gemm, hip_backend.cc:697-809, for dequantised
+ * weights): the weights expanded by hai_fp8_dequant_bf16 into the front of
+ * the workspace, then hai_gemm_bf16_blaslt on them (SwiGLU pairs the
+ * interleaved gate / up grids).  Tolerance mode: the scaled weights are
+ * rounded to bf16, then summed in fp32.  workspace holds
+ * hai_gemm_fp8_blaslt_workspace_bytes(M, N, K, epilogue) bytes, 16-byte
+ * aligned. */
+size_t hai_gemm_fp8_blaslt_workspace_bytes(int64_t M, int64_t N, int64_t K, int epilogue);
+int hai_gemm_fp8_blaslt(void* y, int64_t ldy, const void* x, int64_t ldx,
+                        const void* wq, const float* scales,
+                        const int32_t* scale_rows, int64_t M, int64_t N,
+                        int64_t K, int epilogue, const void* res, int64_t ld_res,
+                        void* workspace, size_t workspace_bytes, void* stream);
 /* Epilogue flag for the MFMA GEMMs with HAI_EPI_RESIDUAL: when the call
  * splits K (hai_gemm_mfma_splits > 1) it leaves the fp32 partials
  * [splits][M][N] at the start of the workspace instead of finishing y; the

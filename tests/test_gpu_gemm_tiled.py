@@ -80,6 +80,8 @@ def check(got, y64, absdot, epi, h=None):
 
 
 def run(M, N, K, epi, fp8=False, special=False, mapped=False, seed=0, blaslt=False):
+    """fp8 with blaslt: hai_gemm_fp8_blaslt, whose weights are bf16(decode(q) * s);
+    the float64 reference then takes those rounded weights."""
     rng = np.random.default_rng(seed + M + 3 * N + 7 * K + epi)
     x, xb = rand_bf16(rng, (M, K))
     mp = None
@@ -110,7 +112,15 @@ def run(M, N, K, epi, fp8=False, special=False, mapped=False, seed=0, blaslt=Fal
     dx = dev(xb)
     dy = dev(hb) if epi == hai.EPI_RESIDUAL else out_buf(M * ncols * 2)
     res = dy.ptr if epi == hai.EPI_RESIDUAL else None
-    if fp8:
+    if fp8 and blaslt:
+        dq, ds = dev(q), dev(s)
+        dm = dev(mp) if mp is not None else None
+        wsb = kern().hai_gemm_fp8_blaslt_workspace_bytes(M, N, K, epi)
+        dws = hai.DeviceBuffer(wsb)
+        hai.check(kern().hai_gemm_fp8_blaslt(dy.ptr, ncols, dx.ptr, K, dq.ptr, ds.ptr, dm.ptr if dm else None, M, N, K,
+                                             epi, res, ncols, dws.ptr, wsb, None), "gemm_fp8_blaslt")
+        w64 = orc.round_bf16(w64.astype(np.float32)).astype(np.float64)
+    elif fp8:
         dq, ds = dev(q), dev(s)
         dm = dev(mp) if mp is not None else None
         flag = 0 if special else hai.FP8_NO_SPECIAL_CODES
@@ -171,6 +181,39 @@ def test_gemm_bf16_blaslt_refuses_short_workspace():
 ])
 def test_gemm_fp8_tiled(M, N, K, epi, special, mapped):
     run(M, N, K, epi, fp8=True, special=special, mapped=mapped)
+
+
+@pytest.mark.parametrize("M,N,K,epi,special,mapped", [
+    (512, 34816, 5120, 2, False, False),   # gate|up: interleaved scale grids, SwiGLU through the scratch
+    (1024, 5120, 17408, 1, False, False),  # down, residual
+    (700, 2 * 640 + 130, 1088, 0, True, True),  # per-row scale map, +-480 codes, K/128 not whole
+])
+def test_gemm_fp8_blaslt(M, N, K, epi, special, mapped):
+    run(M, N, K, epi, fp8=True, special=special, mapped=mapped, blaslt=True)
+
+
+@pytest.mark.parametrize("N,K,mapped,special", [(300, 1040, False, True), (2 * 384, 768, True, False)])
+def test_fp8_dequant_bf16_bits(N, K, mapped, special):
+    """hai_fp8_dequant_bf16 == bf16(the oracle's dequantize_2d) bit for bit
+    (fp32 product of the decoded code and its block scale, then bf16)."""
+    rng = np.random.default_rng(N + K)
+    if mapped:
+        n0 = N // 2
+        q0, s0 = fp8_weights(rng, n0, K, special)
+        q1, s1 = fp8_weights(rng, N - n0, K)
+        q, s = np.concatenate([q0, q1]), np.concatenate([s0, s1])
+        mp = np.array([r // 128 for r in range(n0)] + [s0.shape[0] + r // 128 for r in range(N - n0)], np.int32)
+        want = np.concatenate([orc.fp8_dequant_2d(q0, s0, 128, 128), orc.fp8_dequant_2d(q1, s1, 128, 128)])
+    else:
+        q, s = fp8_weights(rng, N, K, special)
+        mp = None
+        want = orc.fp8_dequant_2d(q, s, 128, 128)
+    dq, ds, dout = dev(q), dev(s), out_buf(N * K * 2)
+    dm = dev(mp) if mp is not None else None
+    hai.check(kern().hai_fp8_dequant_bf16(dout.ptr, K, dq.ptr, ds.ptr, dm.ptr if dm else None, N, K, 0, None),
+              "fp8_dequant")
+    got = dout.download(np.uint16).reshape(N, K)
+    assert np.array_equal(got, hai.bf16_bits(want).reshape(N, K))
 
 
 def test_gemm_tiled_refuses_bad_shapes():
