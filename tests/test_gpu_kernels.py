@@ -235,6 +235,29 @@ def test_gemm_c3_verify_shapes(name, N, K_, epi, norm):
     assert_bits_equal(dy.download(np.uint16), want, name)
 
 
+@pytest.mark.parametrize("N,K_,epi,ldx", [(8200, 5120, 0, 5120), (16480, 5120, 0, 5144), (34816, 5120, 2, 5120),
+                                         (9000, 8192, 1, 8192), (12000, 5128, 1, 5136), (8194, 1000, 2, 1000)])
+def test_gemm_two_rows_wide_staged(N, K_, epi, ldx):
+    """Two-row launches of the wide layers (N > 8192) stage the rows in LDS
+    once per resident block (rows already normalised, e.g. by a residual
+    launch's norm tail): bit-exact for every epilogue, ragged K and N, row
+    pitch above K."""
+    M = 2
+    rng = np.random.default_rng(N + K_ + 3 * epi)
+    xp, xpb = rand_bf16(rng, (M, ldx))
+    w, wb = rand_bf16(rng, (N, K_), 0.02)
+    ncols = N // 2 if epi == hai.EPI_SILU_MUL else N
+    h, hb = rand_bf16(rng, (M, ncols))
+    dx, dw = dev(xpb), dev(wb)
+    dy = dev(hb) if epi == hai.EPI_RESIDUAL else out_buf(M * ncols * 2)
+    res = dy.ptr if epi == hai.EPI_RESIDUAL else None
+    hai.check(kern().hai_gemm_bf16(dy.ptr, ncols, dx.ptr, ldx, dw.ptr, M, N, K_, epi, res, ncols, None), "gemm")
+    y = orc.gemm(xp[:, :K_], w)
+    want = {hai.EPI_STORE: lambda: y, hai.EPI_RESIDUAL: lambda: orc.add(h, y),
+            hai.EPI_SILU_MUL: lambda: orc.silu_mul(y[:, 0::2], y[:, 1::2])}[epi]()
+    assert_bits_equal(dy.download(np.uint16), want, f"two-row staged {N}x{K_} epi {epi}")
+
+
 def test_copy_calibration():
     """One device-to-device copy of 256 MiB: the dispatch of known size that
     scales the rocprofv3 FETCH_SIZE / WRITE_SIZE counters to bytes."""

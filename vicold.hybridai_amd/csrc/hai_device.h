@@ -220,6 +220,50 @@ __device__ __forceinline__ float l64_sumsq_bf16(const uint16_t* __restrict__ x, 
     return wave_sum64(acc);
 }
 
+// RMSNorm of one bf16 row by one wave (rmsnorm_kernel, hip_kernels.hip:
+// 105-137): y_k = bf16((x_k * inv) * (w_k + off)), inv = 1 / sqrt(ss / H +
+// eps), ss the L64-order sum of squares.  Up to NC * 512 elements: every
+// load is issued before the first use; offsets past H read zeros.
+template <int NC>
+__device__ __forceinline__ void rmsnorm_row_wave(uint16_t* __restrict__ yr, const uint16_t* xr,
+                                                 const uint16_t* __restrict__ w, int H, float eps, float off,
+                                                 int lane) {
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(xr, static_cast<uint32_t>(H) * 2u);
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, static_cast<uint32_t>(H) * 2u);
+    u32x4 xd[NC], wd[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const uint32_t o = static_cast<uint32_t>(c * 512 + lane * 8) * 2u;
+        xd[c] = bload(rx, o, 0);
+        wd[c] = bload(rw, o, 0);
+    }
+    float acc = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        if (c * 512 + lane * 8 >= H) continue;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float a = lo_bf(xd[c][q]);
+            const float b = hi_bf(xd[c][q]);
+            acc = fma_(a, a, acc);
+            acc = fma_(b, b, acc);
+        }
+    }
+    const float ss = wave_sum64(acc);
+    const float inv = 1.0f / csqrt(ss / static_cast<float>(H) + eps);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const int k0 = c * 512 + lane * 8;
+        if (k0 >= H) continue;
+        uint32_t o[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            o[q] = f2bf2((lo_bf(xd[c][q]) * inv) * (lo_bf(wd[c][q]) + off),
+                         (hi_bf(xd[c][q]) * inv) * (hi_bf(wd[c][q]) + off));
+        *reinterpret_cast<uint4*>(yr + k0) = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+}
+
 // Same order for an fp32 vector held in LDS or global memory.
 __device__ __forceinline__ float l64_sumsq_f32(const float* x, int n, int lane) {
     float acc = 0.0f;

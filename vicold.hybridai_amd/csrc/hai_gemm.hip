@@ -20,6 +20,7 @@
 #include "hai_gemm_common.h"
 
 #include <atomic>
+#include <cstdlib>
 #include <mutex>
 #include <type_traits>
 #include <vector>
@@ -28,13 +29,24 @@ namespace {
 
 using namespace hai;
 
-template <int MB, int RW, int U, int EPI, bool NORM>
+// Prologue of gemm_bf16_kernel: none (activation rows read from global
+// memory per chunk group), the fused RMSNorm (rows and norm weight staged in
+// LDS and normalised there), or rows already normalised staged in LDS as
+// they are (a two-row launch whose input a residual launch's norm tail
+// wrote).
+enum { kProNone = 0, kProNorm = 1, kProStage = 2 };
+
+template <int MB, int RW, int U, int EPI, int PRO>
 __global__ __launch_bounds__(256) void gemm_bf16_kernel(
     uint16_t* __restrict__ y, int64_t ldy, const uint16_t* __restrict__ x, int64_t ldx,
     const uint16_t* w, const uint16_t* res, int64_t ldres, int M, int N, int K, NormArgs na) {
+    // NORM: the rows are read from LDS (staged by the prologue)
+    constexpr bool NORM = PRO != kProNone;
+    constexpr bool kNormalize = PRO == kProNorm;
+    static_assert(PRO != kProStage || MB == 2, "the stage-only prologue is the two-row copy-staged one");
     const int lane = threadIdx.x & 63;
     const int wave = wave_index();
-    extern __shared__ u32x4 xs[];  // NORM: [M][K/8] normalised rows, then the norm weight
+    extern __shared__ u32x4 xs[];  // NORM: [M][K/8] (normalised) rows, then the norm weight
     const int npr = K >> 3;        // 16-byte pieces per row
 
     // Byte offsets fit 32 bits: the caller bounds N*K*2 and M*ldx*2 below 4 GiB.
@@ -70,7 +82,7 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(
         const int64_t row0 = (grp0 * 4 + wave) * RW;
         const bool pre_ok = grp0 < ngroups && row0 < N;
         if constexpr (kDmaStage) {
-            stage_rows_lds_dma(xs, x, ldx, M, K, na.w);
+            stage_rows_lds_dma(xs, x, ldx, M, K, kNormalize ? na.w : nullptr);
             pin_memory_order();
             __builtin_amdgcn_sched_barrier(0);  // the weight requests stay behind the copies
         }
@@ -97,7 +109,8 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(
             __builtin_amdgcn_sched_barrier(0);
             __builtin_amdgcn_s_barrier();  // every wave's copies have landed
             __builtin_amdgcn_sched_barrier(0);
-            normalize_staged_rows(xs, M, K, na);
+            if constexpr (kNormalize) normalize_staged_rows(xs, M, K, na);
+            else lds_barrier();
         } else {
             rmsnorm_rows_to_lds(xs, x, ldx, M, K, na);
         }
@@ -448,71 +461,18 @@ __global__ __launch_bounds__(256) void gemm_bf16_ksplit_kernel(
     }
 }
 
-// Two-row variant for the short residual layers of the one-sequence verify
-// (out / o projection, K = 6144; down projection, K = 17408; N = 5120):
-// every wave streams RW whole rows over the full K (the canonical order of
-// gemm_bf16_kernel, bit-identical), and a block of WPB waves first copies
-// both activation rows to LDS with global -> LDS copies, so that the rows
-// are fetched once per block instead of once per wave (the K-split kernel
-// re-read them from L2 in every block: 180 MB of L2 reads per 178 MB of
-// down weights).  N / (WPB * RW) blocks make one balanced round on the
-// machine (5120 rows: 512 or 256 blocks, every wave with the same work).
-// As in the NORM prologue, PG groups of U weight chunks are requested behind
-// the copies and the wave waits for its copies alone.  Measured on MI355X at
-// M = 2: down 34.6 -> 31.3 us (WPB 10, U 2), out 14.3 -> 13.3 us (WPB 5,
-// U 4).  LDS: M * K * 2 bytes.
-template <int RW, int U, int WPB, int PG, int EPI>
-__global__ __launch_bounds__(64 * WPB) void gemm_bf16_staged_kernel(
-    uint16_t* __restrict__ y, int64_t ldy, const uint16_t* __restrict__ x, int64_t ldx,
-    const uint16_t* w, const uint16_t* res, int64_t ldres, int M, int N, int K) {
+// The streaming part of gemm_bf16_staged_kernel for one wave: its RW rows
+// against the two activation rows staged in xs, the first PG groups of U
+// chunks already requested (wpre).
+template <int RW, int U, int EPI, int PG>
+__device__ __forceinline__ void staged_rows_body(uint16_t* __restrict__ y, int64_t ldy, const u32x4* xs,
+                                                 __amdgpu_buffer_rsrc_t rw, const uint32_t (&woff)[RW],
+                                                 const u32x4 (&wpre)[PG * U][RW], const uint16_t* res,
+                                                 int64_t ldres, int M, int N, int K, int64_t row0, int lane) {
     constexpr int MB = 2;
-    extern __shared__ u32x4 xs[];  // [M][K/8] activation rows
-    const int lane = threadIdx.x & 63;
-    const int wave = wave_index();
     const int npr = K >> 3;
     const int nck = (K + 511) / 512;
     const int nfull = K / 512;
-    const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, static_cast<uint32_t>(static_cast<int64_t>(N) * K * 2));
-    const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * WPB + wave) * RW;
-    const bool live = row0 < N;
-
-    // the copies: piece e = m * npr + p of the rows to xs[e]; each wave
-    // instruction writes 64 consecutive pieces at its wave-uniform base
-    const int total = M * npr;
-    for (int e0 = 0; e0 < total; e0 += 64 * WPB) {
-        const int e = e0 + static_cast<int>(threadIdx.x);
-        if (e < total) {
-            const int m = e / npr;
-            // (a C-style cast: the generic -> LDS address-space conversion)
-            __builtin_amdgcn_global_load_lds(x + m * ldx + (e - m * npr) * 8,
-                                             (__attribute__((address_space(3))) void*)(xs + e0 + wave * 64), 16,
-                                             0, 0);
-        }
-    }
-    pin_memory_order();
-    __builtin_amdgcn_sched_barrier(0);  // the weight requests stay behind the copies
-    uint32_t woff[RW];
-#pragma unroll
-    for (int r = 0; r < RW; ++r)
-        woff[r] = live ? static_cast<uint32_t>(((row0 + r) * static_cast<int64_t>(K) + lane * 8) * 2) : kOutOfRange;
-    u32x4 wpre[PG * U][RW];
-#pragma unroll
-    for (int u = 0; u < PG * U; ++u) {
-        const bool ok = u < nfull || (u < nck && u * 512 + lane * 8 < K);
-        const ChunkOffset co(u < nfull && live, ok && live, static_cast<uint32_t>(u) * 1024u);
-#pragma unroll
-        for (int r = 0; r < RW; ++r) wpre[u][r] = bload_w(rw, co.v(woff[r]), co.s);
-    }
-    // wait for this wave's copies only (the PG * U * RW weight requests
-    // issued after them, pinned there, stay in flight), then for every wave's
-    pin_memory_order();
-    __builtin_amdgcn_sched_barrier(0);
-    wait_vmcnt<PG * U * RW>();
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_sched_barrier(0);
-    if (!live) return;  // no barrier follows
-
     float acc[RW][MB], tot[RW][MB];
 #pragma unroll
     for (int r = 0; r < RW; ++r)
@@ -615,6 +575,71 @@ __global__ __launch_bounds__(64 * WPB) void gemm_bf16_staged_kernel(
         }
 }
 
+// Two-row variant for the short residual layers of the one-sequence verify
+// (out / o projection, K = 6144; down projection, K = 17408; N = 5120):
+// every wave streams RW whole rows over the full K (the canonical order of
+// gemm_bf16_kernel, bit-identical), and a block of WPB waves first copies
+// both activation rows to LDS with global -> LDS copies, so that the rows
+// are fetched once per block instead of once per wave (the K-split kernel
+// re-read them from L2 in every block: 180 MB of L2 reads per 178 MB of
+// down weights).  N / (WPB * RW) blocks make one balanced round on the
+// machine (5120 rows: 512 or 256 blocks, every wave with the same work).
+// As in the NORM prologue, PG groups of U weight chunks are requested behind
+// the copies and the wave waits for its copies alone.  Measured on MI355X at
+// M = 2: down 34.6 -> 31.3 us (WPB 10, U 2), out 14.3 -> 13.3 us (WPB 5,
+// U 4).  LDS: M * K * 2 bytes.
+template <int RW, int U, int WPB, int PG, int EPI>
+__global__ __launch_bounds__(64 * WPB) void gemm_bf16_staged_kernel(
+    uint16_t* __restrict__ y, int64_t ldy, const uint16_t* __restrict__ x, int64_t ldx,
+    const uint16_t* w, const uint16_t* res, int64_t ldres, int M, int N, int K) {
+    extern __shared__ u32x4 xs[];  // [M][K/8] activation rows
+    const int lane = threadIdx.x & 63;
+    const int wave = wave_index();
+    const int npr = K >> 3;
+    const int nck = (K + 511) / 512;
+    const int nfull = K / 512;
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, static_cast<uint32_t>(static_cast<int64_t>(N) * K * 2));
+    const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * WPB + wave) * RW;
+    const bool live = row0 < N;
+
+    // the copies: piece e = m * npr + p of the rows to xs[e]; each wave
+    // instruction writes 64 consecutive pieces at its wave-uniform base
+    const int total = M * npr;
+    for (int e0 = 0; e0 < total; e0 += 64 * WPB) {
+        const int e = e0 + static_cast<int>(threadIdx.x);
+        if (e < total) {
+            const int m = e / npr;
+            // (a C-style cast: the generic -> LDS address-space conversion)
+            __builtin_amdgcn_global_load_lds(x + m * ldx + (e - m * npr) * 8,
+                                             (__attribute__((address_space(3))) void*)(xs + e0 + wave * 64), 16,
+                                             0, 0);
+        }
+    }
+    pin_memory_order();
+    __builtin_amdgcn_sched_barrier(0);  // the weight requests stay behind the copies
+    uint32_t woff[RW];
+#pragma unroll
+    for (int r = 0; r < RW; ++r)
+        woff[r] = live ? static_cast<uint32_t>(((row0 + r) * static_cast<int64_t>(K) + lane * 8) * 2) : kOutOfRange;
+    u32x4 wpre[PG * U][RW];
+#pragma unroll
+    for (int u = 0; u < PG * U; ++u) {
+        const bool ok = u < nfull || (u < nck && u * 512 + lane * 8 < K);
+        const ChunkOffset co(u < nfull && live, ok && live, static_cast<uint32_t>(u) * 1024u);
+#pragma unroll
+        for (int r = 0; r < RW; ++r) wpre[u][r] = bload_w(rw, co.v(woff[r]), co.s);
+    }
+    // wait for this wave's copies only (the PG * U * RW weight requests
+    // issued after them, pinned there, stay in flight), then for every wave's
+    pin_memory_order();
+    __builtin_amdgcn_sched_barrier(0);
+    wait_vmcnt<PG * U * RW>();
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    if (live) staged_rows_body<RW, U, EPI, PG>(y, ldy, xs, rw, woff, wpre, res, ldres, M, N, K, row0, lane);
+}
+
 struct GemmArgs {
     uint16_t* y;
     int64_t ldy;
@@ -627,18 +652,20 @@ struct GemmArgs {
     NormArgs na;
 };
 
-template <int MB, int RW, int EPI, bool NORM>
+template <int MB, int RW, int EPI, int PRO>
 void launch_gemm(const GemmArgs& a, hipStream_t s) {
     // chunks per group: two-row launches take 2 (with their two-group
     // prefetch or activations-first order; measured faster than 4 there),
     // one row 4, more rows fewer to bound the registers
     constexpr int U = MB == 1 ? 4 : (MB <= 8 ? 2 : 1);
-    auto* kern = gemm_bf16_kernel<MB, RW, U, EPI, NORM>;
+    auto* kern = gemm_bf16_kernel<MB, RW, U, EPI, PRO>;
     const int64_t groups = (static_cast<int64_t>(a.N) + 4 * RW - 1) / (4 * RW);
-    // NORM: LDS holds the M rows and the norm weight staged behind them.
-    const size_t shmem = NORM ? static_cast<size_t>(a.M + 1) * a.K * 2 : 0;
+    // LDS holds the M rows, with the fused norm also the norm weight behind them
+    const size_t shmem = PRO == kProNorm    ? static_cast<size_t>(a.M + 1) * a.K * 2
+                         : PRO == kProStage ? static_cast<size_t>(a.M) * a.K * 2
+                                            : 0;
     int64_t blocks = groups;
-    if (NORM) {
+    if (PRO != kProNone) {
         const int64_t resident = resident_blocks(reinterpret_cast<const void*>(kern), shmem);
         if (resident > 0 && resident < blocks) blocks = resident;
     }
@@ -704,8 +731,21 @@ bool use_ksplit(const GemmArgs& a) {
     return a.K >= 8192 || a.M == 1 || a.N <= 1024;
 }
 
+// Two-row launches of the wide layers (N > 8192, K <= 8192) without a fused
+// norm: the rows staged in LDS once per resident block by copies, as in the
+// fused-norm kernel, instead of re-read from L2 by every wave of every row
+// group (HAI_GEMM_STAGE=0 keeps the activations-first kernel).
+bool use_stage_rows(const GemmArgs& a) {
+    static const bool on = [] {
+        const char* e = std::getenv("HAI_GEMM_STAGE");
+        return e == nullptr || e[0] != '0';
+    }();
+    return on && a.M == 2 && a.N > 8192 && static_cast<int64_t>(a.M) * a.K <= kNormMaxElems;
+}
+
 template <int EPI, bool NORM>
 int dispatch_mb(const GemmArgs& a, hipStream_t s) {
+    constexpr int PRO = NORM ? kProNorm : kProNone;
     if constexpr (!NORM && EPI != HAI_EPI_SILU_MUL) {
         if (use_staged(a)) return launch_staged<EPI>(a, s);
     }
@@ -714,14 +754,18 @@ int dispatch_mb(const GemmArgs& a, hipStream_t s) {
         else launch_ksplit<2, EPI>(a, s);
         return HAI_OK;
     }
+    if (!NORM && use_stage_rows(a)) {
+        launch_gemm<2, 2, EPI, kProStage>(a, s);
+        return HAI_OK;
+    }
     // Two rows per wave keeps the register footprint small enough for eight
     // waves per SIMD, which is what keeps enough bytes in flight on gfx950
     // (measured faster than 4 rows per wave or software-pipelined variants).
-    if (a.M <= 1) launch_gemm<1, 2, EPI, NORM>(a, s);
-    else if (a.M <= 2) launch_gemm<2, 2, EPI, NORM>(a, s);
-    else if (a.M <= 4) launch_gemm<4, 2, EPI, NORM>(a, s);
-    else if (a.M <= 8) launch_gemm<8, 2, EPI, NORM>(a, s);
-    else launch_gemm<16, 2, EPI, NORM>(a, s);
+    if (a.M <= 1) launch_gemm<1, 2, EPI, PRO>(a, s);
+    else if (a.M <= 2) launch_gemm<2, 2, EPI, PRO>(a, s);
+    else if (a.M <= 4) launch_gemm<4, 2, EPI, PRO>(a, s);
+    else if (a.M <= 8) launch_gemm<8, 2, EPI, PRO>(a, s);
+    else launch_gemm<16, 2, EPI, PRO>(a, s);
     return HAI_OK;
 }
 

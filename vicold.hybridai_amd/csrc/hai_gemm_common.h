@@ -131,16 +131,19 @@ __device__ __forceinline__ void rmsnorm_rows_to_lds(u32x4* xs, const uint16_t* _
 // leaves those weight chunks in flight while the prologue computes.  Issues
 // kStageOps copy instructions per wave (lanes past the data masked off).
 // Needs (M + 1) * K / 8 <= 256 * kStageOps pieces, 16-byte aligned rows.
+// Without a norm weight (norm_w null: rows already normalised) only the M
+// rows are staged.
 constexpr int kStageOps = 12;  // (M + 1) * K <= 24576: M * K <= HAI_GEMM_RMSNORM_FUSED_MAX, K <= 8192
 __device__ __forceinline__ void stage_rows_lds_dma(u32x4* xs, const uint16_t* __restrict__ x, int64_t ldx, int M,
                                                    int K, const uint16_t* __restrict__ norm_w) {
     const int wave = wave_index();
     const int npr = K >> 3;
     const int total = M * npr;
+    const int pieces = total + (norm_w != nullptr ? npr : 0);
 #pragma unroll
     for (int i = 0; i < kStageOps; ++i) {
         const int e = static_cast<int>(threadIdx.x) + 256 * i;
-        if (e < total + npr) {
+        if (e < pieces) {
             const int r = e / npr;
             const uint16_t* src = e < total ? x + r * ldx + (e - r * npr) * 8 : norm_w + (e - total) * 8;
             // (a C-style cast: the generic -> LDS address-space conversion)

@@ -23,45 +23,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(uint16_t* __restrict__ y, 
     const int lane = threadIdx.x & 63;
     const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
     if (row >= rows) return;
-    const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + row * ldx, static_cast<uint32_t>(H) * 2u);
-    const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, static_cast<uint32_t>(H) * 2u);
-    u32x4 xd[NC], wd[NC];
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-        const uint32_t off = static_cast<uint32_t>(c * 512 + lane * 8) * 2u;  // past H reads zero
-        xd[c] = bload(rx, off, 0);
-        wd[c] = bload(rw, off, 0);
-    }
-    float acc = 0.0f;
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-        if (c * 512 + lane * 8 >= H) continue;
-        const uint32_t xs[4] = {xd[c][0], xd[c][1], xd[c][2], xd[c][3]};
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const float a = lo_bf(xs[q]);
-            const float b = hi_bf(xs[q]);
-            acc = fma_(a, a, acc);
-            acc = fma_(b, b, acc);
-        }
-    }
-    const float ss = wave_sum64(acc);
-    const float inv = 1.0f / csqrt(ss / static_cast<float>(H) + eps);
-    uint16_t* yr = y + row * ldy;
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-        const int k0 = c * 512 + lane * 8;
-        if (k0 >= H) continue;
-        const uint32_t xs[4] = {xd[c][0], xd[c][1], xd[c][2], xd[c][3]};
-        const uint32_t ws[4] = {wd[c][0], wd[c][1], wd[c][2], wd[c][3]};
-        uint32_t o[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            o[q] = f2bf2((lo_bf(xs[q]) * inv) * (lo_bf(ws[q]) + off),
-                         (hi_bf(xs[q]) * inv) * (hi_bf(ws[q]) + off));
-        }
-        *reinterpret_cast<uint4*>(yr + k0) = make_uint4(o[0], o[1], o[2], o[3]);
-    }
+    rmsnorm_row_wave<NC>(y + row * ldy, x + row * ldx, w, H, eps, off, lane);
 }
 
 // Rotate-half on the normalised values held in LDS (row of D fp32), first R
