@@ -9,6 +9,10 @@ random prompt, greedy speculative decode with MTP depth 1 (k=1, verify T=2).
 
 A "step" is one speculative round: MTP draft -> verify forward of k+1 rows
 -> fused argmax/accept -> (on a mismatch) correction forward + MTP recovery.
+The headline decode covers the configured 256 new tokens (context 1024 ->
+1280): --warmup untimed rounds, then --steps rounds spread evenly over the
+rest of the decode are timed, one round per engine call (every round ends
+with its host read, so the host clock brackets exactly one round).
 `value` = committed tokens per second over the timed rounds, inputs and
 weights resident in HBM, at the acceptance the reference quotes its
 speculative run at (95 % at width 1): random weights accept almost no MTP
@@ -367,59 +371,103 @@ def run_decode(hai, E, args, fp8: bool, steps: int):
         f"GEMM {prof['gemm_ms']:.3f} ms over {prof['gemm_launches']:.0f} launches ({gemm_gbs:.0f} GB/s), "
         f"draft {prof['draft_ms']:.3f} ms")
     forced = None
-    if not fp8 and args.forced_rounds > 0:
+    if not fp8 and not args.natural_only:
         forced = run_forced(hai, eng, E, args, prompt, tag)
     eng.close()
     return value, dt, rounds, emitted, st, prof, prefill, forced
 
 
+def sample_rounds(eng, width: int, out: np.ndarray, warm: int, steps: int) -> dict:
+    """Runs a prefilled engine's decode to its end, one speculative round per
+    call (every call ends with the round's host read, so the host clock
+    brackets exactly one round): `warm` untimed rounds, then every remaining
+    round, of which `steps`, evenly spaced over the rest of the decode, are
+    the timed sample.  Returns the sample and the whole post-warmup decode."""
+    n_prev, _ = eng.spec_rounds(warm, width, out)
+    times, toks, acc, prop = [], [], [], []
+    while True:
+        t0 = time.perf_counter()
+        n, st = eng.spec_rounds(1, width, out)
+        dt = time.perf_counter() - t0
+        if st["rounds"] == 0:
+            break
+        times.append(dt)
+        toks.append(n - n_prev)
+        acc.append(st["accepted"])
+        prop.append(st["proposed"])
+        n_prev = n
+    R = len(times)
+    if R == 0:
+        raise RuntimeError("no speculative rounds after the warmup (increase --new or lower --warmup)")
+    k = min(steps, R)
+    idx = sorted({min(R - 1, int((i + 0.5) * R / k)) for i in range(k)})
+    t_s, n_s = sum(times[i] for i in idx), sum(toks[i] for i in idx)
+    return {"rounds": len(idx), "tokens": n_s, "seconds": t_s, "value": n_s / t_s,
+            "accepted": sum(acc[i] for i in idx), "proposed": sum(prop[i] for i in idx),
+            "all_rounds": R, "all_tokens": sum(toks), "all_seconds": sum(times),
+            "all_accepted": sum(acc), "all_proposed": sum(prop), "emitted": n_prev}
+
+
+def perturbed(g: np.ndarray, frac: float, vocab: int, seed: int = 7) -> np.ndarray:
+    """A token sequence with a fraction `frac` of its positions (never the
+    first) replaced by another id."""
+    rng = np.random.default_rng(seed)
+    d = g.copy()
+    flip = rng.random(d.shape) < frac
+    flip[..., 0] = False
+    d[flip] = (d[flip] + 1 + rng.integers(0, vocab - 1, int(flip.sum()))) % vocab
+    return d
+
+
 def run_forced(hai, eng, E, args, prompt, tag: str) -> dict:
-    """The acceptance the reference quotes its speculative run at (95 % at
-    width 1, benchmark/performance.txt:244-254): random weights accept almost
-    no MTP proposal, so the proposals are replaced by the model's own greedy
-    continuation with a fraction --forced-perturb of its positions changed
-    (a mismatch there is rejected and corrected).  Every round still runs the
-    MTP draft forward, the verify forward, the accept and (after a rejection)
-    the correction; only the proposed token comes from the device copy of
-    the override.  Returns the timed leg."""
+    """The headline leg, at the acceptance the reference quotes its
+    speculative run at (95 % at width 1, benchmark/performance.txt:244-254):
+    random weights accept almost no MTP proposal, so the proposals are the
+    model's own greedy continuation with a fraction --forced-perturb of its
+    positions changed (a mismatch there is rejected and corrected).  Every
+    round still runs the MTP draft forward, the verify forward, the accept
+    and (after a rejection) the correction; only the proposed token comes
+    from the device copy of the override.  The decode covers the configured
+    --new tokens (context P -> P + new): --warmup untimed rounds, then
+    --steps rounds spread evenly over the rest are timed."""
     cfg = E.QWEN27B
-    rounds = args.forced_rounds
-    warm = 4
-    new = (warm + rounds) * (args.width + 1) + 8
+    new = args.new
     g = eng.greedy(prompt, new)
     if len(g) < new:
         raise RuntimeError("greedy continuation ended early")
-    rng = np.random.default_rng(7)
-    drafts = g.copy()
-    flip = rng.random(new) < args.forced_perturb
-    flip[0] = False
-    drafts[flip] = (drafts[flip] + 1 + rng.integers(0, cfg["vocab"] - 1, int(flip.sum()))) % cfg["vocab"]
     eng.prefill(prompt, new)
-    eng.set_draft_override(drafts)
+    eng.set_draft_override(perturbed(g, args.forced_perturb, cfg["vocab"]))
     out = np.zeros(new, np.int32)
-    n0, _ = eng.spec_rounds(warm, args.width, out)
-    hai.synchronize()
-    t0 = time.perf_counter()
-    n1, st = eng.spec_rounds(rounds, args.width, out)
-    hai.synchronize()
-    dt = time.perf_counter() - t0
+    r = sample_rounds(eng, args.width, out, args.warmup, args.steps)
     eng.set_draft_override(None)
-    emitted = n1 - n0
-    if not np.array_equal(out[:n1], g[:n1]):
+    if not np.array_equal(out[:r["emitted"]], g[:r["emitted"]]):
         raise RuntimeError("forced-acceptance decode differs from greedy decoding")
-    acc = st["accepted"] / max(1, st["proposed"])
-    log(f"[{tag}] forced acceptance: {st['rounds']} rounds, {emitted} tokens in {dt:.3f}s -> "
-        f"{emitted / dt:.2f} tok/s (accepted {st['accepted']}/{st['proposed']} = {acc:.3f}), tokens == greedy")
-    return {"value": round(emitted / dt, 3), "unit": "tok/s", "rounds": st["rounds"], "tokens": emitted,
-            "seconds": round(dt, 4), "ms_per_round": round(dt / max(1, st["rounds"]) * 1e3, 4),
-            "acceptance_rate": round(acc, 4), "tokens_per_round": round(emitted / max(1, st["rounds"]), 4),
-            "perturbed_fraction": args.forced_perturb, "tokens_equal_greedy": True}
+    acc = r["accepted"] / max(1, r["proposed"])
+    log(f"[{tag}] forced acceptance, {new}-token decode: {r['rounds']} of {r['all_rounds']} rounds after "
+        f"{args.warmup} warmup timed, {r['tokens']} tokens in {r['seconds']:.3f}s -> {r['value']:.2f} tok/s "
+        f"(accepted {r['accepted']}/{r['proposed']} = {acc:.3f}; whole decode "
+        f"{r['all_tokens'] / r['all_seconds']:.2f} tok/s), tokens == greedy")
+    return {"value": round(r["value"], 3), "unit": "tok/s", "rounds": r["rounds"], "tokens": r["tokens"],
+            "seconds": round(r["seconds"], 4), "ms_per_round": round(r["seconds"] / r["rounds"] * 1e3, 4),
+            "acceptance_rate": round(acc, 4), "tokens_per_round": round(r["tokens"] / r["rounds"], 4),
+            "perturbed_fraction": args.forced_perturb, "tokens_equal_greedy": True,
+            "decode": {"new_tokens": new, "context": [len(prompt), len(prompt) + new], "warmup_rounds": args.warmup,
+                       "rounds_after_warmup": r["all_rounds"], "tokens": r["all_tokens"],
+                       "tok_s": round(r["all_tokens"] / r["all_seconds"], 3),
+                       "acceptance_rate": round(r["all_accepted"] / max(1, r["all_proposed"]), 4)}}
 
 
 def run_batch(hai, E, args, name: str, B: int, P: int, NEW: int, width: int, fp8: bool, rounds: int) -> dict:
     """A batched configuration of BASELINE.json (C4 / C5): B sequences of
-    P-token synthetic prompts decoded in lockstep speculative rounds; bf16
-    GEMMs of 4 or more rows run on the MFMA GEMMs (tolerance mode)."""
+    P-token synthetic prompts decoded in lockstep speculative rounds; GEMMs
+    of 4 or more rows run on the MFMA GEMMs (tolerance mode).  Two legs over
+    the whole NEW-token decode, each with `rounds` timed rounds spread over
+    it after two warmup rounds: the MTP head's own proposals (random weights
+    accept none), then forced acceptance -- the proposals are each
+    sequence's continuation from the first leg (speculative greedy decoding
+    is lossless, so that is the sequence's greedy continuation) with
+    --forced-perturb of the positions changed, so that partial acceptance
+    and the per-sequence state rollback are timed."""
     cfg = E.QWEN27B
     t0 = time.perf_counter()
     cap = P + (width + 2) * NEW + 32
@@ -435,40 +483,59 @@ def run_batch(hai, E, args, name: str, B: int, P: int, NEW: int, width: int, fp8
     prefill_s = time.perf_counter() - t0
     log(f"[{name}] prefill of {B} x {P} tokens: {prefill_s:.2f}s ({B * P / prefill_s:.0f} tok/s)")
     out = np.zeros((B, NEW), np.int32)
-    n0, _ = eng.spec_rounds(2, width, out)
-    hai.synchronize()
-    t0 = time.perf_counter()
-    n1, st = eng.spec_rounds(rounds, width, out)
-    hai.synchronize()
-    dt = time.perf_counter() - t0
-    emitted = n1 - n0
+    nat = sample_rounds(eng, width, out, 2, rounds)
     prof = eng.profile_verify(width + 1, 3)
-    eng.close()
+    natural = out.copy()
     gemm_gbs = prof["gemm_bytes"] / (prof["gemm_ms"] * 1e-3) / 1e9
     step_gbs = prof["step_bytes"] / (prof["verify_ms"] * 1e-3) / 1e9
     res = {
-        "workload": f"{name}: 27B shape, batch {B} x {P}-token prompts, MTP k={width}, "
-                    f"{'FP8 E4M3 128x128-block weights' if fp8 else 'bf16 weights'}; GEMMs of 4 or more rows "
-                    f"(verify, correction, draft) on the MFMA GEMMs (FP8 codes decoded to bf16 in LDS)",
-        "value": round(emitted / dt, 2), "unit": "tok/s (all sequences)", "rounds": st["rounds"],
-        "ms_per_round": round(dt / max(1, st["rounds"]) * 1e3, 3),
+        "workload": f"{name}: 27B shape, batch {B} x {P}-token prompts, MTP k={width}, {NEW} new tokens per "
+                    f"sequence, {'FP8 E4M3 128x128-block weights' if fp8 else 'bf16 weights'}; GEMMs of 4 or more "
+                    f"rows (verify, correction, draft) on the MFMA GEMMs (FP8 codes decoded to bf16 in LDS)",
+        "value": round(nat["value"], 2), "unit": "tok/s (all sequences)", "rounds": nat["rounds"],
+        "ms_per_round": round(nat["seconds"] / nat["rounds"] * 1e3, 3),
         "verify_ms": round(prof["verify_ms"], 3), "verify_rows": B * (width + 1),
         "verify_bytes": round(prof["step_bytes"]), "verify_hbm_frac": round(step_gbs / HBM_PEAK_GBS, 4),
         "gemm_gb_s": round(gemm_gbs, 1), "gemm_launches": prof["gemm_launches"],
         "draft_ms": round(prof["draft_ms"], 3), "prefill_s": round(prefill_s, 3),
         "prefill_tok_s": round(B * P / prefill_s, 1), "prefill_rows_per_chunk": args.batch_prefill_rows,
-        "acceptance_rate": round(st["accepted"] / max(1, st["proposed"]), 4),
+        "acceptance_rate": round(nat["accepted"] / max(1, nat["proposed"]), 4),
     }
-    log(f"[{name}] {emitted} tokens in {dt:.2f}s -> {res['value']} tok/s; verify {prof['verify_ms']:.2f} ms "
-        f"({step_gbs:.0f} GB/s), GEMM {gemm_gbs:.0f} GB/s, draft {prof['draft_ms']:.2f} ms")
+    log(f"[{name}] natural proposals: {nat['tokens']} tokens in {nat['seconds']:.2f}s over {nat['rounds']} sampled "
+        f"rounds -> {res['value']} tok/s; verify {prof['verify_ms']:.2f} ms ({step_gbs:.0f} GB/s), "
+        f"GEMM {gemm_gbs:.0f} GB/s, draft {prof['draft_ms']:.2f} ms")
+    if not args.natural_only:
+        eng.prefill(prompts, NEW)
+        eng.set_draft_override(perturbed(natural, args.forced_perturb, cfg["vocab"]))
+        out = np.zeros((B, NEW), np.int32)
+        fr = sample_rounds(eng, width, out, 2, rounds)
+        eng.set_draft_override(None)
+        same = [bool(np.array_equal(out[b], natural[b])) for b in range(B)]
+        acc = fr["accepted"] / max(1, fr["proposed"])
+        res["forced"] = {
+            "value": round(fr["value"], 2), "unit": "tok/s (all sequences)", "rounds": fr["rounds"],
+            "tokens": fr["tokens"], "ms_per_round": round(fr["seconds"] / fr["rounds"] * 1e3, 3),
+            "acceptance_rate": round(acc, 4), "tokens_per_round": round(fr["tokens"] / fr["rounds"], 3),
+            "perturbed_fraction": args.forced_perturb,
+            "decode_tok_s": round(fr["all_tokens"] / fr["all_seconds"], 2),
+            "decode_acceptance_rate": round(fr["all_accepted"] / max(1, fr["all_proposed"]), 4),
+            "sequences_equal_natural": sum(same),
+        }
+        log(f"[{name}] forced acceptance: {fr['tokens']} tokens in {fr['seconds']:.2f}s over {fr['rounds']} sampled "
+            f"rounds -> {fr['value']:.2f} tok/s (accepted {fr['accepted']}/{fr['proposed']} = {acc:.3f}; "
+            f"whole decode {res['forced']['decode_tok_s']} tok/s); {sum(same)}/{B} sequences equal the first leg's")
+    eng.close()
     return res
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=100, help="timed speculative rounds")
-    ap.add_argument("--warmup", type=int, default=8, help="untimed rounds before timing")
+    ap.add_argument("--steps", type=int, default=20,
+                    help="timed speculative rounds of the headline leg, spread evenly over its decode")
+    ap.add_argument("--warmup", type=int, default=5, help="untimed rounds before the timed ones")
+    ap.add_argument("--natural-rounds", type=int, default=20,
+                    help="timed rounds with the MTP head's own proposals (natural_acceptance)")
     ap.add_argument("--prompt", type=int, default=1024)
     ap.add_argument("--prefill-rows", type=int, default=1024,
                     help="prompt rows per fast-prefill chunk of the bs=1 engines (the verify-path prefill is "
@@ -478,9 +545,8 @@ def main():
     ap.add_argument("--new", type=int, default=256)
     ap.add_argument("--width", type=int, default=1)
     ap.add_argument("--profile-iters", type=int, default=5)
-    ap.add_argument("--forced-rounds", type=int, default=60,
-                    help="timed rounds of the forced-acceptance leg (0 skips it; the line's value then comes from "
-                         "the natural-acceptance rounds)")
+    ap.add_argument("--natural-only", action="store_true",
+                    help="skip the forced-acceptance legs (the line's value then comes from the natural rounds)")
     ap.add_argument("--forced-perturb", type=float, default=0.05,
                     help="fraction of the greedy continuation's positions changed in the forced drafts")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -493,7 +559,8 @@ def main():
                     help="skip C4 (batch 8 x 8192-token prompts, k=3; reported under batch_c4)")
     ap.add_argument("--no-c5", action="store_true",
                     help="skip C5 (FP8 weights, batch 32 x 512-token prompts, k=1; reported under batch_c5)")
-    ap.add_argument("--batch-rounds", type=int, default=12)
+    ap.add_argument("--batch-rounds", type=int, default=12,
+                    help="timed rounds of each C4 / C5 leg, spread evenly over the decode")
     ap.add_argument("--no-c1", action="store_true", help="skip the C1 tiny-model decode (reported under c1)")
     ap.add_argument("--no-c2", action="store_true", help="skip the C2 op micro-bench (reported under c2_ops)")
     ap.add_argument("--c4-prompt", type=int, default=8192,
@@ -520,7 +587,7 @@ def main():
 
     P, NEW = args.prompt, args.new
     nat_value, dt, rounds, emitted, st, prof, prefill, forced = run_decode(hai, E, args, fp8=False,
-                                                                            steps=args.steps)
+                                                                            steps=args.natural_rounds)
     verify_ms = prof["verify_ms"]
     gemm_gbs = prof["gemm_bytes"] / (prof["gemm_ms"] * 1e-3) / 1e9
     step_gbs = prof["step_bytes"] / (verify_ms * 1e-3) / 1e9
@@ -530,8 +597,9 @@ def main():
     if forced is not None:
         value, v_rounds, v_tokens, v_ms = forced["value"], forced["rounds"], forced["tokens"], forced["ms_per_round"]
         drafts = ("MTP draft forward every round, proposals replaced by the model's own greedy continuation with "
-                  "%.0f%% of positions perturbed (acceptance %.3f; tokens checked equal to greedy decoding)"
-                  % (100 * args.forced_perturb, forced["acceptance_rate"]))
+                  "%.0f%% of positions perturbed (acceptance %.3f; tokens checked equal to greedy decoding); "
+                  "the whole %d-token decode runs, %d rounds after %d warmup rounds timed, spread evenly over it"
+                  % (100 * args.forced_perturb, forced["acceptance_rate"], NEW, forced["rounds"], args.warmup))
     else:
         value, v_rounds, v_tokens, v_ms = nat_value, rounds, emitted, dt / rounds * 1e3
         drafts = "the MTP head's own proposals (random weights: acceptance %.3f)" % (st["accepted"] / max(1, st["proposed"]))
@@ -551,7 +619,7 @@ def main():
         "config": {
             "workload": "C3: 27B-shape hybrid (64 layers 3 DeltaNet:1 GQA, H5120, vocab 248320, 1 MTP layer), "
                         "bs=1, %d-token prompt, greedy speculative decode MTP k=%d" % (P, args.width),
-            "prompt_tokens": P, "new_tokens": v_tokens, "max_new_tokens": NEW, "mtp_k": args.width, "batch": 1,
+            "prompt_tokens": P, "new_tokens": NEW, "timed_tokens": v_tokens, "mtp_k": args.width, "batch": 1,
             "drafts": drafts,
         },
         "natural_acceptance": {
@@ -564,6 +632,7 @@ def main():
         "verify_hbm_frac": round(step_gbs / HBM_PEAK_GBS, 4),
         "draft_ms": round(prof["draft_ms"], 4),
         "acceptance_rate": forced["acceptance_rate"] if forced else round(st["accepted"] / max(1, st["proposed"]), 4),
+        "decode": forced["decode"] if forced else None,
         "tokens_per_round": round(v_tokens / v_rounds, 4),
         "prefill": prefill,
         "roofline": {

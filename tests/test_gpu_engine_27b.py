@@ -139,3 +139,38 @@ def test_27b_mfma_batch_logits_within_rounding_sensitivity(fp8):
     assert d_mfma.mean() <= d_nudge.mean(), (float(d_mfma.mean()), float(d_nudge.mean()))
     assert np.percentile(d_mfma, 99) <= np.percentile(d_nudge, 99)
     assert np.mean(got.argmax(-1) == want.argmax(-1)) >= np.mean(nudged.argmax(-1) == want.argmax(-1))
+
+
+def test_c3_workload_full_decode():
+    """C3 as BASELINE.json configures it: a 1024-token prompt through the fast
+    prefill (1024-row chunks), then 256 new tokens at MTP depth 1.  Greedy
+    decoding gives the reference continuation; the speculative decode with
+    that continuation perturbed at 5 % of positions as drafts (the bench's
+    headline leg: partial acceptance, corrections and rollbacks across the
+    whole 1024 -> 1280 context) equals it token for token with the round
+    bookkeeping adding up, and so does the speculative decode with the MTP
+    head's own proposals."""
+    from hybridai_amd import engine as E
+    P, NEW = 1024, 256
+    V = E.QWEN27B["vocab"]
+    eng = E.Engine(E.QWEN27B, max_context=P + NEW + 32, max_verify_tokens=16, prefill_rows=1024)
+    try:
+        eng.init_synthetic(seed=0, std=0.02)
+        prompt = E.synthetic_prompt(0, P, V)
+        g = eng.greedy(prompt, NEW)
+        assert len(g) == NEW
+        rng = np.random.default_rng(7)
+        drafts = g.copy()
+        flip = rng.random(NEW) < 0.05
+        flip[0] = False
+        drafts[flip] = (drafts[flip] + 1) % V
+        toks, st, log = eng.speculative(prompt, NEW, 1, draft_override=drafts)
+        assert list(toks) == list(g)
+        assert st["proposed"] == st["accepted"] + st["rejected"]
+        assert st["corrections"] == st["rejected"] > 0
+        assert st["accepted"] >= 0.85 * st["proposed"], st
+        toks, st, _ = eng.speculative(prompt, NEW, 1)
+        assert list(toks) == list(g)
+        assert st["proposed"] == st["accepted"] + st["rejected"]
+    finally:
+        eng.close()

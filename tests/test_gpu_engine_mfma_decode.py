@@ -173,3 +173,17 @@ def test_c4_long_prompt_rollback_bookkeeping():
         assert any(0 < r[1]["accepted"] < r[1]["proposed"] for r, k in zip(res, kinds) if k == "partial")
     finally:
         eng.close()
+
+
+def test_c5_workload_prompts_mfma_fp8_decode():
+    """C5's 32 x 512-token prompts with FP8 weights at depth 1 (verify of 64
+    rows): forced full, partial and no acceptance per sequence, every round's
+    bookkeeping exact, and every emitted token within 0.5 of the argmax of a
+    fresh forward over the sequence."""
+    from hybridai_amd import engine as E
+    kinds = (["full", "partial", "none", "full"] * 8)
+    eng, prompts, res = run_forced(E, True, 32, 512, 12, 1, kinds, 400)
+    try:
+        check_27b(eng, prompts, res, kinds, 12)
+    finally:
+        eng.close()
