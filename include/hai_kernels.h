@@ -511,48 +511,6 @@ int hai_gemm_fp8_tiled(void* y, int64_t ldy, const void* x, int64_t ldx,
                        const int32_t* scale_rows, int64_t M, int64_t N,
                        int64_t K, int epilogue, const void* res, int64_t ld_res,
                        void* stream);
-/* The bf16 form of hai_gemm_bf16_tiled through hipBLASLt (the same
- * rocblas_gemm_ex call site, hip_backend.cc:697-809): Y = epilogue(X . W^T)
- * with fp32 accumulation for prompt chunks (a plain library GEMM; 1.6-2x the
- * hand-written tiled kernel's rate at 1024-4096 rows on MI355X).  SwiGLU
- * writes the interleaved gate / up product to a scratch and pairs it in a
- * second kernel.  workspace holds hai_gemm_bf16_blaslt_workspace_bytes(M, N,
- * epilogue) bytes, 16-byte aligned (the algorithm's workspace plus the
- * SwiGLU scratch); one hipBLASLt handle per device and one heuristic
- * algorithm per shape are created on first use and kept.  Tolerance mode. */
-size_t hai_gemm_bf16_blaslt_workspace_bytes(int64_t M, int64_t N, int epilogue);
-/* Loads hipBLASLt on the current device ahead of the first call (about 3 s
- * once per process: handle, solution tables and kernel code objects), so that
- * a caller takes it at set-up instead of in its first prompt.  Runs one tiny
- * GEMM on stream inside `workspace` (at least the algorithm part of
- * hai_gemm_bf16_blaslt_workspace_bytes; its contents are clobbered). */
-int hai_gemm_bf16_blaslt_prepare(void* workspace, size_t workspace_bytes, void* stream);
-int hai_gemm_bf16_blaslt(void* y, int64_t ldy, const void* x, int64_t ldx,
-                         const void* w, int64_t M, int64_t N, int64_t K,
-                         int epilogue, const void* res, int64_t ld_res,
-                         void* workspace, size_t workspace_bytes, void* stream);
-/* FP8 E4M3 weights [N, K] with 128x128 fp32 block scales to bf16 rows
- * out[n][k] = bf16(decode(q) * s): the reference's dequantize_2d
- * (fp8_dequant.cc:12-146; 0x7F / 0xFF decode to +-480) rounded to bf16.
- * Scale rows as in hai_gemm_fp8_mfma: scale_rows[n] when given, else the
- * interleaved gate / up grids when paired, else n / 128.  K % 16 == 0. */
-int hai_fp8_dequant_bf16(void* out, int64_t ld_out, const void* wq,
-                         const float* scales, const int32_t* scale_rows,
-                         int64_t N, int64_t K, int paired, void* stream);
-/* The prompt-chunk FP8 GEMM through hipBLASLt (the rocblas_gemm_ex call
- * site of HipBackend::gemm, hip_backend.cc:697-809, for dequantised
- * weights): the weights expanded by hai_fp8_dequant_bf16 into the front of
- * the workspace, then hai_gemm_bf16_blaslt on them (SwiGLU pairs the
- * interleaved gate / up grids).  Tolerance mode: the scaled weights are
- * rounded to bf16, then summed in fp32.  workspace holds
- * hai_gemm_fp8_blaslt_workspace_bytes(M, N, K, epilogue) bytes, 16-byte
- * aligned. */
-size_t hai_gemm_fp8_blaslt_workspace_bytes(int64_t M, int64_t N, int64_t K, int epilogue);
-int hai_gemm_fp8_blaslt(void* y, int64_t ldy, const void* x, int64_t ldx,
-                        const void* wq, const float* scales,
-                        const int32_t* scale_rows, int64_t M, int64_t N,
-                        int64_t K, int epilogue, const void* res, int64_t ld_res,
-                        void* workspace, size_t workspace_bytes, void* stream);
 /* Epilogue flag for the MFMA GEMMs with HAI_EPI_RESIDUAL: when the call
  * splits K (hai_gemm_mfma_splits > 1) it leaves the fp32 partials
  * [splits][M][N] at the start of the workspace instead of finishing y; the

@@ -104,11 +104,6 @@ _KERNEL_SIGS = {
     "hai_correction_commit_bf16": [VP, VP, VP, I64, I64, VP, VP, VP, VP, VP],
     "hai_gemm_bf16_mfma": [VP, I64, VP, I64, VP, I64, I64, I64, ctypes.c_int, VP, I64, VP, ctypes.c_size_t, VP],
     "hai_gemm_bf16_tiled": [VP, I64, VP, I64, VP, I64, I64, I64, ctypes.c_int, VP, I64, VP],
-    "hai_gemm_bf16_blaslt": [VP, I64, VP, I64, VP, I64, I64, I64, ctypes.c_int, VP, I64, VP, ctypes.c_size_t, VP],
-    "hai_fp8_dequant_bf16": [VP, I64, VP, VP, VP, I64, I64, ctypes.c_int, VP],
-    "hai_gemm_fp8_blaslt": [VP, I64, VP, I64, VP, VP, VP, I64, I64, I64, ctypes.c_int, VP, I64, VP, ctypes.c_size_t,
-                            VP],
-    "hai_gemm_bf16_blaslt_prepare": [VP, ctypes.c_size_t, VP],
     "hai_gemm_fp8_tiled": [VP, I64, VP, I64, VP, VP, VP, I64, I64, I64, ctypes.c_int, VP, I64, VP],
     "hai_gemm_fp8_mfma": [VP, I64, VP, I64, VP, VP, VP, I64, I64, I64, ctypes.c_int, VP, I64, VP, ctypes.c_size_t,
                           VP],
@@ -121,8 +116,6 @@ _KERNEL_SIGS = {
 }
 _SIZE_SIGS = {
     "hai_gemm_mfma_workspace_bytes": [I64, I64],
-    "hai_gemm_bf16_blaslt_workspace_bytes": [I64, I64, ctypes.c_int],
-    "hai_gemm_fp8_blaslt_workspace_bytes": [I64, I64, I64, ctypes.c_int],
     "hai_gqa_scratch_bytes": [I64, I64, I64, I64, I64],
     "hai_gqa_mfma_scratch_bytes": [I64, I64, I64, I64, I64],
     "hai_gqa_mfma_plan_scratch_bytes": [I64, I64, I64, I64, I64, I64],

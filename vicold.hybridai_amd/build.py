@@ -44,7 +44,7 @@ CXX_FLAGS = ["-O2", "-fPIC", "-std=c++20", "-Wall", "-Wextra", "-Wno-unused-para
              f"-I{INCLUDE}", f"-I{HOST}"]
 
 KERNEL_SOURCES = ["hai_runtime.hip", "hai_gemm.hip", "hai_gemm_fp8.hip", "hai_gemm_mfma.hip", "hai_norm.hip", "hai_attention.hip",
-                  "hai_deltanet.hip", "hai_deltanet_prefill.hip", "hai_argmax.hip", "hai_gemm_blaslt.hip"]
+                  "hai_deltanet.hip", "hai_deltanet_prefill.hip", "hai_argmax.hip"]
 
 
 MANIFEST = LIB / "build_manifest.json"
@@ -98,7 +98,7 @@ def build_kernels(jobs: int = 8) -> Path:
         list(ex.map(_run, cmds))
     out = LIB / "libhai_kernels.so"
     tmp = LIB / "libhai_kernels.so.tmp"
-    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs), "-lhipblaslt"])
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)])
     os.replace(tmp, out)
     _record(out.name, digest)
     return out

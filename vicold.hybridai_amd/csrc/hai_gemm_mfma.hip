@@ -1886,85 +1886,6 @@ extern "C" int hai_gemm_bf16_tiled(void* y, int64_t ldy, const void* x, int64_t 
     return tiled_entry<false, false>(a, epilogue, as_stream(stream));
 }
 
-namespace {
-
-// FP8 E4M3 codes [N, K] with 128 x 128 fp32 block scales -> bf16 rows
-// bf16(decode(q) * s): the reference's dequantize_2d (fp8_dequant.cc:12-146,
-// 0x7F / 0xFF as +-480) rounded to bf16, 16 codes per thread; scale rows as
-// the matrix-core kernels find them (a row map, interleaved gate / up grids,
-// or row / 128).
-__global__ __launch_bounds__(256) void fp8_dequant_bf16_kernel(uint16_t* __restrict__ out, int64_t ldo,
-                                                               const uint8_t* __restrict__ q,
-                                                               const float* __restrict__ scales,
-                                                               const int32_t* __restrict__ scale_rows, int paired,
-                                                               int64_t N, int K) {
-    const int64_t ppr = K / 16;
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-    if (i >= N * ppr) return;
-    const int64_t n = i / ppr;
-    const int k0 = static_cast<int>(i - n * ppr) * 16;
-    const int64_t nkb = (K + 127) / 128;
-    const int64_t nsb = ((N >> 1) + 127) / 128;
-    const int64_t sr = scale_rows ? scale_rows[n] : (paired ? (n & 1) * nsb + (n >> 1) / 128 : n / 128);
-    const float sc = scales[sr * nkb + k0 / 128];
-    const u32x4 w = *reinterpret_cast<const u32x4*>(q + n * K + k0);
-    uint32_t o[8];
-#pragma unroll
-    for (int qq = 0; qq < 4; ++qq) {
-        uint32_t lo, hi;
-        e4m3x4_to_bf16<true>(w[qq], lo, hi);  // the codes' exact values in bf16
-        o[2 * qq] = f2bf2(lo_bf(lo) * sc, hi_bf(lo) * sc);
-        o[2 * qq + 1] = f2bf2(lo_bf(hi) * sc, hi_bf(hi) * sc);
-    }
-    u32x4* dst = reinterpret_cast<u32x4*>(out + n * ldo + k0);
-    dst[0] = u32x4{o[0], o[1], o[2], o[3]};
-    dst[1] = u32x4{o[4], o[5], o[6], o[7]};
-}
-
-size_t dequant_bytes(int64_t N, int64_t K) { return (static_cast<size_t>(N) * K * 2 + 255) / 256 * 256; }
-
-}  // namespace
-
-extern "C" int hai_fp8_dequant_bf16(void* out, int64_t ld_out, const void* wq, const float* scales,
-                                    const int32_t* scale_rows, int64_t N, int64_t K, int paired, void* stream) {
-    if (out == nullptr || wq == nullptr || scales == nullptr) return invalid("fp8_dequant: null pointer");
-    if (N < 0 || K <= 0 || K % 16 != 0 || ld_out < K || ld_out % 8 != 0 || K > INT32_MAX)
-        return invalid("fp8_dequant: shape (need K % 16 == 0, ld_out >= K, ld_out % 8 == 0)");
-    if (!aligned16(out) || !aligned16(wq)) return invalid("fp8_dequant: 16-byte alignment");
-    int rc = check_extent(wq, static_cast<size_t>(N) * K, "fp8_dequant codes");
-    if (rc == HAI_OK) rc = check_extent(out, rows_extent(N, K, ld_out, 2), "fp8_dequant out");
-    if (rc != HAI_OK) return rc;
-    if (N == 0) return HAI_OK;
-    const int64_t pieces = N * (K / 16);
-    fp8_dequant_bf16_kernel<<<dim3(static_cast<unsigned>((pieces + 255) / 256)), dim3(256), 0, as_stream(stream)>>>(
-        static_cast<uint16_t*>(out), ld_out, static_cast<const uint8_t*>(wq), scales, scale_rows, paired ? 1 : 0, N,
-        static_cast<int>(K));
-    return launched("fp8_dequant_bf16_kernel");
-}
-
-extern "C" size_t hai_gemm_fp8_blaslt_workspace_bytes(int64_t M, int64_t N, int64_t K, int epilogue) {
-    return dequant_bytes(N, K) + hai_gemm_bf16_blaslt_workspace_bytes(M, N, epilogue & ~HAI_FP8_NO_SPECIAL_CODES);
-}
-
-extern "C" int hai_gemm_fp8_blaslt(void* y, int64_t ldy, const void* x, int64_t ldx, const void* wq,
-                                   const float* scales, const int32_t* scale_rows, int64_t M, int64_t N, int64_t K,
-                                   int epilogue, const void* res, int64_t ld_res, void* workspace,
-                                   size_t workspace_bytes, void* stream) {
-    const int epi = epilogue & ~HAI_FP8_NO_SPECIAL_CODES;
-    if (workspace == nullptr || scales == nullptr) return invalid("gemm_fp8_blaslt: null workspace or scales");
-    if (K % 16 != 0) return invalid("gemm_fp8_blaslt: K % 16 != 0");
-    if (workspace_bytes < hai_gemm_fp8_blaslt_workspace_bytes(M, N, K, epi))
-        return invalid("gemm_fp8_blaslt: workspace below hai_gemm_fp8_blaslt_workspace_bytes");
-    if (!aligned16(workspace)) return invalid("gemm_fp8_blaslt: workspace must be 16-byte aligned");
-    if (M == 0 || N == 0) return HAI_OK;
-    char* ws = static_cast<char*>(workspace);
-    const size_t wb = dequant_bytes(N, K);
-    int rc = hai_fp8_dequant_bf16(ws, K, wq, scales, scale_rows, N, K, epi == HAI_EPI_SILU_MUL ? 1 : 0, stream);
-    if (rc != HAI_OK) return rc;
-    return hai_gemm_bf16_blaslt(y, ldy, x, ldx, ws, M, N, K, epi, res, ld_res, ws + wb, workspace_bytes - wb,
-                                stream);
-}
-
 extern "C" int hai_gemm_fp8_tiled(void* y, int64_t ldy, const void* x, int64_t ldx, const void* wq,
                                   const float* scales, const int32_t* scale_rows, int64_t M, int64_t N, int64_t K,
                                   int epilogue, const void* res, int64_t ld_res, void* stream) {

@@ -357,17 +357,6 @@ int Engine::alloc_all() {
         if (fast_prefill_) {
             dn_ws_bytes_ = static_cast<int64_t>(hai_deltanet_prefill_workspace_bytes(B_, pchunk_cap_, d.nv, d.dv));
             dn_ws_ = cv.take<char>(static_cast<size_t>(dn_ws_bytes_));
-            if (prefill_blaslt()) {
-                // the largest prompt-chunk GEMM's needs: the SwiGLU scratch
-                // of the MLP, and with FP8 weights also the bf16 copy of the
-                // gate|up weights (the largest matrix) dequantised into it
-                const int64_t rows = B_ * pchunk_cap_;
-                blaslt_ws_bytes_ =
-                    fp8_ ? std::max(hai_gemm_bf16_blaslt_workspace_bytes(rows, d.H, HAI_EPI_STORE),
-                                    hai_gemm_fp8_blaslt_workspace_bytes(rows, 2 * d.F, d.H, HAI_EPI_SILU_MUL))
-                         : hai_gemm_bf16_blaslt_workspace_bytes(rows, 2 * d.F, HAI_EPI_SILU_MUL);
-                blaslt_ws_ = cv.take<char>(blaslt_ws_bytes_);
-            }
         }
         argmax_scratch_ = cv.take<char>(hai_argmax_scratch_bytes(R, d.V));
         rope_cos_ = cv.take<float>(cap_ * std::max<int64_t>(1, d.R / 2));
@@ -379,8 +368,6 @@ int Engine::alloc_all() {
         HAI_TRY(hai_malloc(&work_, sizing.used()));
         Carver real(static_cast<char*>(work_));
         carve_work(real);
-        // hipBLASLt's one-time load at set-up rather than in the first prompt
-        if (blaslt_ws_ != nullptr) HAI_TRY(hai_gemm_bf16_blaslt_prepare(blaslt_ws_, blaslt_ws_bytes_, stream_));
         HAI_TRY(hai_memset(work_, 0, sizing.used(), stream_));
     }
     return sync();
@@ -563,21 +550,11 @@ int Engine::gemm(uint16_t* y, int64_t ldy, const uint16_t* x, int64_t ldx, const
     HAI_TRY(flush_pending());  // the workspace is about to be reused
     if (prof_record_) prof_calls_.push_back({y, ldy, x, ldx, w, M, N, K, epi, res, ldres, nullptr, nullptr});
     if (use_mfma(M) && M > kTiledMinRows && K % 64 == 0) {
-        // prompt-sized row counts: both operands tiled, compute bound
-        if (w.q != nullptr) {
-            // FP8: dequantised to bf16 in the workspace, then hipBLASLt
-            // (C5's 32 x 512 prompts: 430 TFLOP/s on the tiled kernel)
-            if (blaslt_ws_ != nullptr && M <= B_ * pchunk_cap_ &&
-                hai_gemm_fp8_blaslt_workspace_bytes(M, N, K, epi) <= blaslt_ws_bytes_)
-                return hai_gemm_fp8_blaslt(y, ldy, x, ldx, w.q, w.s, w.map, M, N, K, epi, res, ldres, blaslt_ws_,
-                                           blaslt_ws_bytes_, stream_);
+        // prompt-sized row counts: both operands tiled on the matrix cores,
+        // compute bound (FP8 codes decoded exactly as they are staged)
+        if (w.q != nullptr)
             return hai_gemm_fp8_tiled(y, ldy, x, ldx, w.q, w.s, w.map, M, N, K, epi | HAI_FP8_NO_SPECIAL_CODES, res,
                                       ldres, stream_);
-        }
-        if (blaslt_ws_ != nullptr && M <= B_ * pchunk_cap_ &&
-            (epi != HAI_EPI_SILU_MUL || hai_gemm_bf16_blaslt_workspace_bytes(M, N, epi) <= blaslt_ws_bytes_))
-            return hai_gemm_bf16_blaslt(y, ldy, x, ldx, w.w, M, N, K, epi, res, ldres, blaslt_ws_, blaslt_ws_bytes_,
-                                        stream_);
         return hai_gemm_bf16_tiled(y, ldy, x, ldx, w.w, M, N, K, epi, res, ldres, stream_);
     }
     if (use_mfma(M) && epi == HAI_EPI_RESIDUAL && res == y && ldres == ldy && M <= 128 && N % 8 == 0 && N <= 8192 &&

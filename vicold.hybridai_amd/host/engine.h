@@ -288,19 +288,6 @@ private:
     bool fast_ = false;          // inside such a chunk: matrix-core GEMMs and attention
     char* dn_ws_ = nullptr;      // prefill DeltaNet outputs before the gated norm
     int64_t dn_ws_bytes_ = 0;
-    // bf16 prompt-chunk GEMMs through hipBLASLt (hai_gemm_bf16_blaslt): its
-    // algorithm workspace and SwiGLU scratch; null: the tiled kernel
-    char* blaslt_ws_ = nullptr;
-    size_t blaslt_ws_bytes_ = 0;
-    // hipBLASLt for the bf16 prompt-chunk GEMMs unless the environment sets
-    // HAI_PREFILL_BLASLT=0 (the hand-written tiled kernel then; read once)
-    static bool prefill_blaslt() {
-        static const bool on = [] {
-            const char* e = std::getenv("HAI_PREFILL_BLASLT");
-            return e == nullptr || e[0] != '0';
-        }();
-        return on;
-    }
     bool mfma_ = false;   // tolerance mode: MFMA GEMMs (4+ rows) and attention
     int64_t ring_ = 0;
     int64_t nslots_ = 0;
