@@ -558,13 +558,15 @@ def test_deltanet_verify_rollback(nk, nv, dk, dv, steps, split):
 @pytest.mark.parametrize("nk,nv,dk,T,Kc", [(2, 6, 64, 37, 4), (16, 48, 128, 100, 4), (4, 4, 64, 16, 3),
                                          (16, 48, 128, 32, 4)])
 def test_deltanet_prefill_against_oracle(nk, nv, dk, T, Kc):
-    """hai_deltanet_prefill_bf16 (prompt chunks, 16 threads per value column,
-    tolerance mode) against the oracle's conv + recurrence of the same T
-    tokens for two sequences with different histories (conv inputs from the
-    ring, initial state from slot L % nslots): outputs within the bf16 / fp32
-    reassociation bound, the state within 1e-4 of its scale, and the conv
-    ring's entries for the chunk's last positions bit for bit.  T = 32
-    wraps the 32-entry ring onto the entries the chunk reads first."""
+    """hai_deltanet_prefill_bf16 (the chunkwise form of the gated delta rule:
+    32-token chunks, a triangular solve per chunk and the state carried from
+    chunk to chunk; tolerance mode) against the oracle's token-by-token conv
+    + recurrence of the same T tokens for two sequences with different
+    histories (conv inputs from the ring, initial state from slot L % nslots):
+    outputs within the bf16 / fp32 reassociation bound, the state within 1e-4
+    of its scale, and the conv ring's entries for the chunk's last positions
+    bit for bit.  T = 37 and 100 end in a ragged chunk; T = 32 wraps the
+    32-entry ring onto the entries the chunk reads first."""
     rng = np.random.default_rng(nv * 7 + T)
     B, dv = 2, dk
     kw, vw = nk * dk, nv * dv

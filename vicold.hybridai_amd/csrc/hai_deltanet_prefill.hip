@@ -2,37 +2,57 @@
 // prefill's deltanet_grouped_conv_kernel + deltanet_recurrent_kernel,
 // hip_kernels.hip:871-912, 985-1095, and the gated RMSNorm), tolerance mode.
 //
-// The verify kernel keeps a head's state in one block, 4 threads per value
-// column, and walks the tokens one after another: each token is a chain of
-// two 32-long fma sums, so a prompt costs ~1.5 us per token and layer.  The
-// recurrence is independent per value column, so here
-//   * a head's columns are split over DV / 32 blocks and every column over
-//     16 threads (8 key dims each at dk = 128): the dependent chain of a
-//     token is 8 fmas and a 16-lane sum (DPP: row rotates, then quad
-//     swaps), and four times as many CUs work on a head;
-//   * the tokens run in groups of 16: the group's conv outputs (from the
-//     projection rows, the first ones reading the conv ring), gates and q/k
-//     norms are computed in parallel, then the group's recurrence; the state
-//     stays in registers across groups and is stored once, to slot
-//     (L + T) % nslots, with the conv ring's last entries;
-//   * the unrounded outputs go to a workspace, and a second kernel applies
-//     the gated RMSNorm per (token, head).
-// The sums are regrouped (16 lanes instead of 4), so results equal the
-// canonical recurrence to fp32 reassociation, not bit for bit.
+// The recurrence per token (v-head h; normalised key k_t, scaled query q_t,
+// decay a_t, beta_t; S [dk][dv] fp32):
+//   S_t = a_t S_{t-1} + beta_t k_t (v_t - a_t S_{t-1}^T k_t)^T,  o_t = S_t^T q_t.
+// Walked token by token it is a chain of dependent dot products (~0.8 us
+// per token and layer at the 27B shape).  Here the tokens go in chunks of
+// kChunk and the recurrence is restated per chunk -- the chunkwise form of
+// the gated delta rule (Yang, Kautz and Hatamizadeh, "Gated Delta Networks",
+// 2024): with g_t = sum_{u<=t} log a_u inside the chunk, S the state before
+// it, L[t][s] = beta_t e^{g_t - g_s} k_t.k_s (s < t) and w_t the value token
+// t writes (S_t = a_t S_{t-1} + k_t w_t^T),
+//   (I + L) w = diag(beta) V - diag(beta e^g) K S,   so   w = U - W^ S  with
+//   U = (I + L)^-1 diag(beta) V,   W^ = (I + L)^-1 diag(beta e^g) K;
+//   o_t = e^{g_t} S^T q_t + sum_{s<=t} e^{g_t - g_s} (q_t.k_s) w_s;
+//   S'  = e^{g_last} S + sum_s e^{g_last - g_s} k_s w_s^T.
+// Everything but the last two lines is independent of S, so the work splits
+// into three launches:
+//   1. deltanet_chunk_prep_kernel, one block per (chunk, head, sequence), all
+//      chunks at once: conv + SiLU of the chunk's inputs, gates, q / k norms,
+//      the Gram matrices, the triangular solve for U and W^ (one thread per
+//      right-hand column, in order of t), and the scaled keys / queries
+//      K~ = e^{g_last - g} K, Q~ = e^{g} Q and P[t][s] = e^{g_t - g_s} q_t.k_s
+//      into a workspace;
+//   2. deltanet_chunk_state_kernel, one block per (head, 32 value columns,
+//      sequence), the chunks in order: W = U - W^ S, O = Q~ S + P W,
+//      S = e^{g_last} S + K~^T W -- three dense products per chunk, the state
+//      in LDS;
+//   3. deltanet_gated_norm_kernel: the gated RMSNorm per (token, head).
+// The state is stored once, to slot (L + T) % nslots, and the conv ring's
+// last entries by deltanet_ring_update_kernel.  The sums are reassociated
+// (and the gates use the hardware exp), so results equal the canonical
+// recurrence to fp32 rounding, not bit for bit.
 #include "hai_common.h"
 #include "hai_device.h"
+
+#include <atomic>
 
 namespace {
 
 using namespace hai;
 
-constexpr int kGroup = 16;   // tokens per group
-constexpr int kTpc = 16;     // threads per value column
-constexpr int kCols = 32;    // value columns per block
+constexpr int kChunk = 32;   // tokens per chunk
+// value columns per block of the state pass (every block loads its chunk's
+// whole record: 16 columns per block measured slower than 32 on MI355X,
+// 307 against 207 us per 1024-token call at the 27B shape)
+template <int DK>
+constexpr int state_cols() { return 32; }
 constexpr int kMaxKc = 8;
 
 struct PrefillArgs {
     float* o_ws;            // [B*T][nv*dv] unrounded outputs
+    float* chunks;          // per (sequence, head, chunk): chunk_floats<DK, DV>() floats
     const uint16_t* proj;   // rows b*T + t: [qkv | z | a | b] at the offsets
     int64_t ld_proj, off_qkv, off_a, off_b;
     const uint16_t* conv_w;
@@ -45,190 +65,380 @@ struct PrefillArgs {
     int B, T, nk, nv, Kc;
 };
 
-// sum over the 16 lanes of a DPP row, the same value in every lane
-__device__ __forceinline__ float row16_sum(float v) {
-    v = v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xF, 0xF, false));  // row_ror:8
-    v = v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x124, 0xF, 0xF, false));  // row_ror:4
-    v = v + quad_xor2(v);
-    return v + quad_xor1(v);
+// Per-chunk record: U [C][DV], W^ [C][DK], K~ [C][DK], Q~ [C][DK], P [C][C],
+// then e^{g_last} (padded to 16 floats).
+template <int DK, int DV>
+__host__ __device__ constexpr int64_t chunk_floats() {
+    return static_cast<int64_t>(kChunk) * (DV + 3 * DK + kChunk) + 16;
 }
 
-// grid (nv, DV / kCols, B); block kCols * kTpc threads.  Thread (jl, g)
-// holds keys g*GI .. g*GI + GI - 1 of column j0 + jl.
-template <int DK, int DV>
-__global__ __launch_bounds__(kCols * kTpc) void deltanet_prefill_kernel(PrefillArgs A) {
-    constexpr int NT = kCols * kTpc;
+// tolerance mode: the hardware exp and reciprocal
+__device__ __forceinline__ float fast_silu(float x) { return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
+
+// ---- pass 1: one block (256 threads) per (chunk c, head h, sequence b);
+// KC: the conv taps (0: any count up to kMaxKc, read from the arguments) ----
+template <int DK, int DV, int KC>
+__global__ __launch_bounds__(256) void deltanet_chunk_prep_kernel(PrefillArgs A) {
+    constexpr int KM = KC > 0 ? KC : kMaxKc;  // tap registers
+    constexpr int NT = 256;
     constexpr int NW = NT / 64;
-    constexpr int GI = DK / kTpc;          // key dims per thread
-    constexpr int QPT = kTpc / 4;          // threads per quarter of the keys
-    constexpr int NCH = 2 * DK + kCols;    // conv channels: q, k, this block's v columns
-    static_assert(GI % 4 == 0 && NCH <= NT, "layout");
-    __shared__ __align__(16) float qs[kGroup][DK];
-    __shared__ __align__(16) float ks[kGroup][DK];
-    __shared__ __align__(16) float bks[kGroup][DK];
-    __shared__ float vs[kGroup][kCols];
-    __shared__ float s_q[kGroup], s_k[kGroup], s_decay[kGroup], s_beta[kGroup];
+    constexpr int DKP = DK + 4;  // padded LDS rows (the Gram's column reads spread over banks)
+    constexpr int NCH = 2 * DK + DV;
+    constexpr int NRHS = DV + DK;
+    static_assert(NRHS <= NT && NRHS >= kChunk, "one thread per right-hand column");
+    __shared__ __align__(16) float qs[kChunk][DKP];
+    __shared__ __align__(16) float ks[kChunk][DKP];
+    __shared__ float vs[kChunk][DV];
+    __shared__ __align__(16) float Lm[kChunk][kChunk + 4];  // rows read as float4
+    __shared__ float s_lg[kChunk], s_g[kChunk], s_beta[kChunk], s_q[kChunk], s_k[kChunk];
+
+    const int c = blockIdx.x;
+    const int h = blockIdx.y;
+    const int b = blockIdx.z;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int nv = A.nv;
+    const int gq = h / (nv / A.nk);
+    const int64_t kw = static_cast<int64_t>(A.nk) * DK;
+    const int64_t vw = static_cast<int64_t>(nv) * DV;
+    const int64_t C = 2 * kw + vw;
+    const int Kc = KC > 0 ? KC : A.Kc;
+    const int hist = Kc - 1;
+    const int T = A.T;
+    const int t0 = c * kChunk;
+    const int TS = min(kChunk, T - t0);
+    const int64_t row0 = static_cast<int64_t>(b) * T;
+    const int64_t p0 = static_cast<int64_t>(A.lens ? A.lens[b] : 0) + A.pos_add;
+
+    // ---- conv + SiLU: input at prompt-chunk row t0 + tt - hist + i, rows
+    // before the prompt chunk from the conv ring (positions before 0: zero) ----
+    for (int ch = tid; ch < NCH; ch += NT) {
+        int64_t chan;
+        if (ch < DK) chan = static_cast<int64_t>(gq) * DK + ch;
+        else if (ch < 2 * DK) chan = kw + static_cast<int64_t>(gq) * DK + (ch - DK);
+        else chan = 2 * kw + static_cast<int64_t>(h) * DV + (ch - 2 * DK);
+        float wc[KM];
+#pragma unroll
+        for (int i = 0; i < KM; ++i) wc[i] = i < Kc ? bf2f(A.conv_w[chan * Kc + i]) : 0.0f;
+        float win[KM];  // the last Kc - 1 inputs, oldest first
+#pragma unroll
+        for (int i = 0; i < KM; ++i) {
+            float v = 0.0f;
+            if (i < hist) {
+                const int r = t0 - hist + i;
+                if (r >= 0) v = bf2f(A.proj[(row0 + r) * A.ld_proj + A.off_qkv + chan]);
+                else if (p0 + r >= 0)
+                    v = bf2f(A.ring[(static_cast<int64_t>(b) * A.ring_n + (p0 + r) % A.ring_n) * C + chan]);
+            }
+            win[i] = v;
+        }
+        uint16_t xr[kChunk];  // every input of the chunk requested before the first use
+#pragma unroll
+        for (int tt = 0; tt < kChunk; ++tt)
+            xr[tt] = tt < TS ? A.proj[(row0 + t0 + tt) * A.ld_proj + A.off_qkv + chan] : uint16_t{0};
+#pragma unroll
+        for (int tt = 0; tt < kChunk; ++tt) {
+            if (tt >= TS) continue;
+            const float xin = bf2f(xr[tt]);
+            float acc = (hist > 0 ? win[0] : xin) * wc[0];
+#pragma unroll
+            for (int i = 1; i < KM; ++i) {
+                if (i < hist) acc = fma_(win[i], wc[i], acc);
+                else if (i == hist) acc = fma_(xin, wc[i], acc);
+            }
+#pragma unroll
+            for (int i = 0; i + 1 < KM; ++i)
+                if (i + 1 < hist) win[i] = win[i + 1];
+#pragma unroll
+            for (int i = 0; i < KM; ++i)
+                if (i == hist - 1) win[i] = xin;
+            const float y = bfr(fast_silu(acc));
+            if (ch < DK) qs[tt][ch] = y;
+            else if (ch < 2 * DK) ks[tt][ch - DK] = y;
+            else vs[tt][ch - 2 * DK] = y;
+        }
+    }
+    // ---- gates (last wave, lane = token): log of the decay
+    // exp(-exp(A_log) softplus(dt_bias + a)), beta = sigmoid(b) ----
+    if (wave == NW - 1 && lane < TS) {
+        const float a_in = bf2f(A.proj[(row0 + t0 + lane) * A.ld_proj + A.off_a + h]);
+        const float b_in = bf2f(A.proj[(row0 + t0 + lane) * A.ld_proj + A.off_b + h]);
+        const float dtv = bf2f(A.dt_bias[h]) + a_in;
+        const float sp = fmaxf(dtv, 0.0f) + log1pf(__expf(-fabsf(dtv)));
+        s_lg[lane] = -(__expf(bf2f(A.a_log[h])) * sp);
+        s_beta[lane] = __builtin_amdgcn_rcpf(1.0f + __expf(-b_in));
+    }
+    __syncthreads();
+    // ---- L2 norms of q and k (one wave per vector); cumulative log decay ----
+    const float rs_dk = 1.0f / csqrt(static_cast<float>(DK));
+    for (int task = wave; task < 2 * TS; task += NW) {
+        const int t = task >> 1;
+        if ((task & 1) == 0) {
+            const float ssq = l64_sumsq_f32(qs[t], DK, lane);
+            if (lane == 0) s_q[t] = (1.0f / csqrt(ssq + 1.0e-6f)) * rs_dk;
+        } else {
+            const float ssk = l64_sumsq_f32(ks[t], DK, lane);
+            if (lane == 0) s_k[t] = 1.0f / csqrt(ssk + 1.0e-6f);
+        }
+    }
+    if (tid == NT - 1) {
+        float gg = 0.0f;
+        for (int t = 0; t < TS; ++t) {
+            gg += s_lg[t];
+            s_g[t] = gg;
+        }
+    }
+    __syncthreads();
+    for (int e = tid; e < kChunk * DK; e += NT) {
+        const int t = e / DK, d = e % DK;
+        if (t < TS) {
+            qs[t][d] = qs[t][d] * s_q[t];
+            ks[t][d] = ks[t][d] * s_k[t];
+        } else {
+            qs[t][d] = 0.0f;  // rows past the chunk's tokens take no part
+            ks[t][d] = 0.0f;
+        }
+    }
+    for (int e = tid; e < (kChunk - TS) * DV; e += NT) vs[TS + e / DV][e % DV] = 0.0f;
+    __syncthreads();
+
+    float* rec = A.chunks + ((static_cast<int64_t>(b) * nv + h) * ((T + kChunk - 1) / kChunk) + c) * chunk_floats<DK, DV>();
+    float* rU = rec;
+    float* rW = rU + kChunk * DV;
+    float* rK = rW + kChunk * DK;
+    float* rQ = rK + kChunk * DK;
+    float* rP = rQ + kChunk * DK;
+    const float glast = s_g[TS - 1];
+
+    // ---- Gram matrices: thread (t4 = tid / 32, s = tid % 32) takes rows
+    // t4, t4 + 8, t4 + 16, t4 + 24 against key s ----
+    {
+        const int sc = tid % kChunk;
+        const int t4 = tid / kChunk;
+        float kk[4] = {0.0f, 0.0f, 0.0f, 0.0f}, qk[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int d = 0; d < DK; d += 4) {
+            const float4 c4 = *reinterpret_cast<const float4*>(&ks[sc][d]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float4 a4 = *reinterpret_cast<const float4*>(&ks[t4 + 8 * r][d]);
+                const float4 b4 = *reinterpret_cast<const float4*>(&qs[t4 + 8 * r][d]);
+                kk[r] = fma_(a4.x, c4.x, kk[r]); kk[r] = fma_(a4.y, c4.y, kk[r]);
+                kk[r] = fma_(a4.z, c4.z, kk[r]); kk[r] = fma_(a4.w, c4.w, kk[r]);
+                qk[r] = fma_(b4.x, c4.x, qk[r]); qk[r] = fma_(b4.y, c4.y, qk[r]);
+                qk[r] = fma_(b4.z, c4.z, qk[r]); qk[r] = fma_(b4.w, c4.w, qk[r]);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int t = t4 + 8 * r;
+            const bool live = t < TS && sc < TS && sc <= t;
+            const float ratio = live ? __expf(s_g[t] - s_g[sc]) : 0.0f;
+            Lm[t][sc] = (live && sc < t) ? s_beta[t] * ratio * kk[r] : 0.0f;
+            rP[t * kChunk + sc] = ratio * qk[r];
+        }
+    }
+    __syncthreads();
+
+    // ---- (I + L) X = R by forward substitution, one thread per right-hand
+    // column: R = beta * V (U) or beta e^g K (W^) ----
+    if (tid < NRHS) {
+        float x[kChunk];
+        const bool isv = tid < DV;
+        const int col = isv ? tid : tid - DV;
+#pragma unroll
+        for (int t = 0; t < kChunk; ++t) {
+            float acc = 0.0f;
+            if (t < TS) {
+                acc = isv ? s_beta[t] * vs[t][col] : (s_beta[t] * __expf(s_g[t])) * ks[t][col];
+#pragma unroll
+                for (int s4 = 0; s4 < t; s4 += 4) {
+                    const float4 l4 = *reinterpret_cast<const float4*>(&Lm[t][s4]);
+                    const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+#pragma unroll
+                    for (int u = 0; u < 4; ++u)
+                        if (s4 + u < t) acc = fma_(-lv[u], x[s4 + u], acc);
+                }
+            }
+            x[t] = acc;
+        }
+        float* dst = isv ? rU + col : rW + col;
+        const int ld = isv ? DV : DK;
+#pragma unroll
+        for (int t = 0; t < kChunk; ++t) dst[t * ld] = x[t];
+    }
+    // ---- K~ = e^{g_last - g} K and Q~ = e^{g} Q ----
+    for (int e = tid; e < kChunk * DK; e += NT) {
+        const int t = e / DK, d = e % DK;
+        const bool live = t < TS;
+        rK[e] = live ? __expf(glast - s_g[t]) * ks[t][d] : 0.0f;
+        rQ[e] = live ? __expf(s_g[t]) * qs[t][d] : 0.0f;
+    }
+    if (tid == 0) rP[kChunk * kChunk] = __expf(glast);
+}
+
+// ---- pass 2: one block (512 threads) per (head h, 32 value columns, sequence b),
+// the chunks in order ----
+// LDS of the state pass: the block's state columns, the chunk's w, and the
+// chunk's record (W^, K~, Q~, P, e^{g_last}; the block's U columns).
+template <int DK>
+__host__ __device__ constexpr size_t state_lds_floats() {
+    constexpr int kCols = state_cols<DK>();
+    return static_cast<size_t>(kCols) * (DK + 4) + kChunk * (kCols + 1) + (3 * kChunk * DK + kChunk * kChunk + 16) +
+           kChunk * kCols;
+}
+
+template <int DK, int DV>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void deltanet_chunk_state_kernel(PrefillArgs A) {
+    constexpr int NT = 512;
+    constexpr int DKP = DK + 4;
+    constexpr int kCols = state_cols<DK>();
+    constexpr int TPC = NT / kCols;             // threads per column
+    constexpr int RPT = kChunk / TPC;           // rows of W / O per thread
+    constexpr int IB = DK / TPC;                // state keys per thread in the update
+    static_assert(RPT * TPC == kChunk && IB % 4 == 0, "state pass layout");
+    constexpr int RF = 3 * kChunk * DK + kChunk * kChunk + 16;  // W^ .. e^{g_last} of a record
+    extern __shared__ __align__(16) float lds_f[];
+    float (*St)[DKP] = reinterpret_cast<float (*)[DKP]>(lds_f);                         // St[j][i] = S[i][j0 + j]
+    float (*Wm)[kCols + 1] = reinterpret_cast<float (*)[kCols + 1]>(lds_f + kCols * DKP);
+    float* Rs = lds_f + kCols * DKP + kChunk * (kCols + 1);                              // the record from W^ on
+    float (*Us)[kCols] = reinterpret_cast<float (*)[kCols]>(Rs + RF);                    // U of the block's columns
 
     const int h = blockIdx.x;
     const int j0 = blockIdx.y * kCols;
     const int b = blockIdx.z;
     const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int jl = tid / kTpc;
-    const int g = tid % kTpc;
-    const int j = j0 + jl;
     const int nv = A.nv;
-    const int group = nv / A.nk;
-    const int gq = h / group;
-    const int64_t kw = static_cast<int64_t>(A.nk) * DK;
-    const int64_t vw = static_cast<int64_t>(nv) * DV;
-    const int64_t C = 2 * kw + vw;
-    const int hist = A.Kc - 1;
     const int T = A.T;
+    const int nchunks = (T + kChunk - 1) / kChunk;
+    const int64_t vw = static_cast<int64_t>(nv) * DV;
     const int64_t row0 = static_cast<int64_t>(b) * T;
     const int64_t p0 = static_cast<int64_t>(A.lens ? A.lens[b] : 0) + A.pos_add;
+    const int jc = tid % kCols;   // column of the products
+    const int tg = tid / kCols;   // rows tg + TPC r (W, O), key block tg (update)
 
-    // conv channel of this thread: [0, DK) q, [DK, 2DK) k, then the block's v columns
-    const bool has_ch = tid < NCH;
-    int64_t chan = 0;
-    if (tid < DK) chan = static_cast<int64_t>(gq) * DK + tid;
-    else if (tid < 2 * DK) chan = kw + static_cast<int64_t>(gq) * DK + (tid - DK);
-    else chan = 2 * kw + static_cast<int64_t>(h) * DV + j0 + (tid - 2 * DK);
-    float wc[kMaxKc];
-#pragma unroll
-    for (int i = 0; i < kMaxKc; ++i) wc[i] = (has_ch && i < A.Kc) ? bf2f(A.conv_w[chan * A.Kc + i]) : 0.0f;
-    const float dtb = bf2f(A.dt_bias[h]);
-    const float alog = bf2f(A.a_log[h]);
-
-    // state: keys g*GI + u of column j, from slot p0 % nslots (column-tiled
-    // layout: key i = q4*(DK/4) + 4m + e at float ((m*DV + j)*4 + q4)*4 + e)
-    const int q4 = g / QPT;
-    const int m0 = (g % QPT) * (GI / 4);
-    float S[GI];
-    {
-        const float* src = A.state + ((p0 % A.nslots) * A.B + b) * static_cast<int64_t>(nv) * DV * DK +
-                           static_cast<int64_t>(h) * DV * DK;
-#pragma unroll
-        for (int mm = 0; mm < GI / 4; ++mm) {
-            const float4 v4 = *reinterpret_cast<const float4*>(src + ((static_cast<int64_t>(m0 + mm) * DV + j) * 4 + q4) * 4);
-            S[4 * mm] = v4.x; S[4 * mm + 1] = v4.y; S[4 * mm + 2] = v4.z; S[4 * mm + 3] = v4.w;
-        }
+    // state of the block's columns from slot p0 % nslots (column-tiled head:
+    // key i = q4*(DK/4) + 4m + e of column j at float ((m*DV + j)*4 + q4)*4 + e)
+    const float* hs = A.state + ((p0 % A.nslots) * A.B + b) * static_cast<int64_t>(nv) * DV * DK +
+                      static_cast<int64_t>(h) * DV * DK;
+    for (int e = tid; e < kCols * DK; e += NT) {
+        const int jl = e / DK, i = e % DK;
+        const int q4 = i / (DK / 4), m = (i % (DK / 4)) / 4, ee = i % 4;
+        St[jl][i] = hs[((static_cast<int64_t>(m) * DV + j0 + jl) * 4 + q4) * 4 + ee];
     }
-    const float rs_dk = 1.0f / csqrt(static_cast<float>(DK));
+    __syncthreads();
 
-    for (int t0 = 0; t0 < T; t0 += kGroup) {
-        const int TS = min(kGroup, T - t0);
-        // ---- conv + SiLU of the group's tokens: input at chunk position
-        // t0 - hist + i from the projection rows, before the chunk from the
-        // conv ring (positions before 0 read as zero) ----
-        if (has_ch) {
-            uint16_t x[kGroup + kMaxKc - 1];
-#pragma unroll
-            for (int i = 0; i < kGroup + kMaxKc - 1; ++i) {
-                const int r = t0 - hist + i;
-                uint16_t v = 0;
-                if (i < TS + hist) {
-                    if (r >= 0) {
-                        v = A.proj[(row0 + r) * A.ld_proj + A.off_qkv + chan];
-                    } else if (p0 + r >= 0) {
-                        int64_t rp = (p0 + r) % A.ring_n;
-                        v = A.ring[(static_cast<int64_t>(b) * A.ring_n + rp) * C + chan];
-                    }
-                }
-                x[i] = v;
-            }
-#pragma unroll
-            for (int tt = 0; tt < kGroup; ++tt) {
-                if (tt < TS) {
-                    // taps: x[tt + hist - (Kc - 1) + i] * w[i], i.e. the verify kernel's window
-                    float acc = bf2f(x[tt]) * wc[0];
-#pragma unroll
-                    for (int i = 1; i < kMaxKc; ++i)
-                        if (i < A.Kc) acc = fma_(bf2f(x[tt + i]), wc[i], acc);
-                    const float y = bfr(csilu(acc));
-                    if (tid < DK) qs[tt][tid] = y;
-                    else if (tid < 2 * DK) ks[tt][tid - DK] = y;
-                    else vs[tt][tid - 2 * DK] = y;
-                }
-            }
-        }
-        // ---- gates of the group's tokens (last wave, lane = token) ----
-        if (wave == NW - 1 && lane < TS) {
-            const float a_in = bf2f(A.proj[(row0 + t0 + lane) * A.ld_proj + A.off_a + h]);
-            const float b_in = bf2f(A.proj[(row0 + t0 + lane) * A.ld_proj + A.off_b + h]);
-            const float dtv = dtb + a_in;
-            const float sp = fmaxf(dtv, 0.0f) + clog1p(cexp(-fabsf(dtv)));
-            s_decay[lane] = cexp(-(cexp(alog) * sp));
-            s_beta[lane] = csigmoid(b_in);
-        }
-        __syncthreads();
-        // ---- L2 norms of q and k (one wave per vector) ----
-        for (int task = wave; task < 2 * TS; task += NW) {
-            const int t = task >> 1;
-            if ((task & 1) == 0) {
-                const float ssq = l64_sumsq_f32(qs[t], DK, lane);
-                if (lane == 0) s_q[t] = (1.0f / csqrt(ssq + 1.0e-6f)) * rs_dk;
-            } else {
-                const float ssk = l64_sumsq_f32(ks[t], DK, lane);
-                if (lane == 0) s_k[t] = 1.0f / csqrt(ssk + 1.0e-6f);
-            }
-        }
-        __syncthreads();
-        for (int e = tid; e < TS * DK; e += NT) {
-            const int t = e / DK, d = e % DK;
-            qs[t][d] = qs[t][d] * s_q[t];
-            const float kh = ks[t][d] * s_k[t];
-            ks[t][d] = kh;
-            bks[t][d] = s_beta[t] * kh;
-        }
-        __syncthreads();
-        // ---- the group's recurrence (column-local: no block barrier) ----
-        for (int tt = 0; tt < TS; ++tt) {
-            const float decay = s_decay[tt];
-            const float4* kt = reinterpret_cast<const float4*>(&ks[tt][g * GI]);
-            const float4* bt = reinterpret_cast<const float4*>(&bks[tt][g * GI]);
-            const float4* qt = reinterpret_cast<const float4*>(&qs[tt][g * GI]);
-            float r = 0.0f;
-#pragma unroll
-            for (int mm = 0; mm < GI / 4; ++mm) {
-                const float4 k4 = kt[mm];
-                const float kv[4] = {k4.x, k4.y, k4.z, k4.w};
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    S[4 * mm + e] = S[4 * mm + e] * decay;
-                    r = fma_(kv[e], S[4 * mm + e], r);
-                }
-            }
-            r = row16_sum(r);
-            const float cj = vs[tt][jl] - r;
-            float o = 0.0f;
-#pragma unroll
-            for (int mm = 0; mm < GI / 4; ++mm) {
-                const float4 b4 = bt[mm], q4v = qt[mm];
-                const float bv[4] = {b4.x, b4.y, b4.z, b4.w}, qv[4] = {q4v.x, q4v.y, q4v.z, q4v.w};
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    S[4 * mm + e] = fma_(bv[e], cj, S[4 * mm + e]);
-                    o = fma_(qv[e], S[4 * mm + e], o);
-                }
-            }
-            o = row16_sum(o);
-            if (g == 0) A.o_ws[(row0 + t0 + tt) * vw + static_cast<int64_t>(h) * DV + j] = o;
-        }
-        __syncthreads();  // the next group rewrites the LDS rows
+    // A chunk's record goes through registers: the next chunk's loads are
+    // issued before the current chunk is computed, and stored to LDS after it.
+    constexpr int RP = (RF / 4 + NT - 1) / NT;   // record float4 per thread
+    constexpr int UP = (kChunk * kCols / 4 + NT - 1) / NT;
+    static_assert(RP <= 8 && UP == 1, "record pieces per thread");
+    u32x4 rr[RP], ur;  // native vectors (HIP's float4 struct stays in memory here)
+    // (unrolled by hand, up to 8 pieces: indices the compiler sees as constants
+    // keep rr / ur in registers)
+#define HAI_REC_LOAD1(U)                                                                                         \
+    if constexpr (RP > (U)) {                                                                                    \
+        const int e = tid + (U) * NT;                                                                            \
+        if (e < RF / 4) rr[(U) < RP ? (U) : 0] = src_[e];                                                        \
     }
-
-    // ---- the state after the chunk, and the conv ring's last entries ----
-    {
-        float* dst = A.state + (((p0 + T) % A.nslots) * A.B + b) * static_cast<int64_t>(nv) * DV * DK +
-                     static_cast<int64_t>(h) * DV * DK;
+#define HAI_LOAD_RECORD(CI)                                                                                      \
+    do {                                                                                                         \
+        const float* rec_ = A.chunks + ((static_cast<int64_t>(b) * nv + h) * nchunks + (CI)) * chunk_floats<DK, DV>(); \
+        const u32x4* src_ = reinterpret_cast<const u32x4*>(rec_ + kChunk * DV);                                \
+        HAI_REC_LOAD1(0) HAI_REC_LOAD1(1) HAI_REC_LOAD1(2) HAI_REC_LOAD1(3)                                      \
+        HAI_REC_LOAD1(4) HAI_REC_LOAD1(5) HAI_REC_LOAD1(6) HAI_REC_LOAD1(7)                                      \
+        if (tid < kChunk * kCols / 4) {                                                                          \
+            const int t_ = tid / (kCols / 4), q_ = tid % (kCols / 4);                                            \
+            ur = *reinterpret_cast<const u32x4*>(rec_ + t_ * DV + j0 + 4 * q_);                                 \
+        }                                                                                                        \
+    } while (0)
+    HAI_LOAD_RECORD(0);
+    for (int c = 0; c < nchunks; ++c) {
+        const int t0 = c * kChunk;
+        const int TS = min(kChunk, T - t0);
+#define HAI_REC_STORE1(U)                                                                                        \
+    if constexpr (RP > (U)) {                                                                                    \
+        const int e = tid + (U) * NT;                                                                            \
+        if (e < RF / 4) reinterpret_cast<u32x4*>(Rs)[e] = rr[(U) < RP ? (U) : 0];                                \
+    }
+        HAI_REC_STORE1(0) HAI_REC_STORE1(1) HAI_REC_STORE1(2) HAI_REC_STORE1(3)
+        HAI_REC_STORE1(4) HAI_REC_STORE1(5) HAI_REC_STORE1(6) HAI_REC_STORE1(7)
+#undef HAI_REC_STORE1
+        if (tid < kChunk * kCols / 4) reinterpret_cast<u32x4*>(&Us[0][0])[tid] = ur;
+        __syncthreads();
+        if (c + 1 < nchunks) HAI_LOAD_RECORD(c + 1);
+        const float* rW = Rs;
+        const float* rK = rW + kChunk * DK;
+        const float* rQ = rK + kChunk * DK;
+        const float* rP = rQ + kChunk * DK;
+        // ---- W = U - W^ S and Q~ S for rows tg + TPC r of column jc ----
+        float wv[RPT], ov[RPT];
 #pragma unroll
-        for (int mm = 0; mm < GI / 4; ++mm)
-            *reinterpret_cast<float4*>(dst + ((static_cast<int64_t>(m0 + mm) * DV + j) * 4 + q4) * 4) =
-                make_float4(S[4 * mm], S[4 * mm + 1], S[4 * mm + 2], S[4 * mm + 3]);
+        for (int r = 0; r < RPT; ++r) wv[r] = ov[r] = 0.0f;
+#pragma unroll 4
+        for (int i = 0; i < DK; i += 4) {
+            const float4 s4 = *reinterpret_cast<const float4*>(&St[jc][i]);
+#pragma unroll
+            for (int r = 0; r < RPT; ++r) {
+                const float4 x4 = *reinterpret_cast<const float4*>(rW + (tg + TPC * r) * DK + i);
+                const float4 y4 = *reinterpret_cast<const float4*>(rQ + (tg + TPC * r) * DK + i);
+                wv[r] = fma_(x4.x, s4.x, wv[r]); wv[r] = fma_(x4.y, s4.y, wv[r]);
+                wv[r] = fma_(x4.z, s4.z, wv[r]); wv[r] = fma_(x4.w, s4.w, wv[r]);
+                ov[r] = fma_(y4.x, s4.x, ov[r]); ov[r] = fma_(y4.y, s4.y, ov[r]);
+                ov[r] = fma_(y4.z, s4.z, ov[r]); ov[r] = fma_(y4.w, s4.w, ov[r]);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < RPT; ++r) Wm[tg + TPC * r][jc] = Us[tg + TPC * r][jc] - wv[r];
+        __syncthreads();
+        // ---- outputs O = Q~ S + P W ----
+#pragma unroll
+        for (int r = 0; r < RPT; ++r) {
+            const int t = tg + TPC * r;
+            if (t < TS) {
+                float o = ov[r];
+                const float* pr = rP + t * kChunk;
+                for (int s2 = 0; s2 <= t; ++s2) o = fma_(pr[s2], Wm[s2][jc], o);
+                A.o_ws[(row0 + t0 + t) * vw + static_cast<int64_t>(h) * DV + j0 + jc] = o;
+            }
+        }
+        // ---- S = e^{g_last} S + K~^T W: thread (tg, jc) updates keys tg*IB .. + IB - 1 ----
+        {
+            const float gl = rP[kChunk * kChunk];
+            float sv[IB];
+#pragma unroll
+            for (int u = 0; u < IB; u += 4) {
+                const float4 s4 = *reinterpret_cast<const float4*>(&St[jc][tg * IB + u]);
+                sv[u] = s4.x * gl; sv[u + 1] = s4.y * gl; sv[u + 2] = s4.z * gl; sv[u + 3] = s4.w * gl;
+            }
+            for (int t = 0; t < TS; ++t) {
+                const float wt = Wm[t][jc];
+                const float* kr = rK + t * DK + tg * IB;
+#pragma unroll
+                for (int u = 0; u < IB; u += 4) {
+                    const float4 k4 = *reinterpret_cast<const float4*>(kr + u);
+                    sv[u] = fma_(k4.x, wt, sv[u]); sv[u + 1] = fma_(k4.y, wt, sv[u + 1]);
+                    sv[u + 2] = fma_(k4.z, wt, sv[u + 2]); sv[u + 3] = fma_(k4.w, wt, sv[u + 3]);
+                }
+            }
+            __syncthreads();  // every thread's reads of S and W for this chunk are done
+#pragma unroll
+            for (int u = 0; u < IB; u += 4)
+                *reinterpret_cast<float4*>(&St[jc][tg * IB + u]) = make_float4(sv[u], sv[u + 1], sv[u + 2], sv[u + 3]);
+        }
+        __syncthreads();
+    }
+    // ---- the state after the prompt chunk, to slot (p0 + T) % nslots ----
+    float* hd = A.state + (((p0 + T) % A.nslots) * A.B + b) * static_cast<int64_t>(nv) * DV * DK +
+                static_cast<int64_t>(h) * DV * DK;
+    for (int e = tid; e < kCols * DK; e += NT) {
+        const int jl = e / DK, i = e % DK;
+        const int q4 = i / (DK / 4), m = (i % (DK / 4)) / 4, ee = i % 4;
+        hd[((static_cast<int64_t>(m) * DV + j0 + jl) * 4 + q4) * 4 + ee] = St[jl][i];
     }
 }
+#undef HAI_LOAD_RECORD
+#undef HAI_REC_LOAD1
 
 // The conv ring's entries for the chunk's last Kc - 1 positions (the only
 // ones a later step reads), after every block has read the entries before
@@ -276,8 +486,26 @@ __global__ __launch_bounds__(256) void deltanet_gated_norm_kernel(uint16_t* __re
 template <int DK, int DV>
 int launch_prefill(const PrefillArgs& a, uint16_t* out, int64_t ld_out, int64_t off_z, const uint16_t* norm_w,
                    float eps, hipStream_t s) {
-    deltanet_prefill_kernel<DK, DV><<<dim3(a.nv, DV / kCols, a.B), dim3(kCols * kTpc), 0, s>>>(a);
-    int rc = launched("deltanet_prefill_kernel");
+    const unsigned nchunks = static_cast<unsigned>((a.T + kChunk - 1) / kChunk);
+    const dim3 pgrid(nchunks, a.nv, a.B);
+    if (a.Kc == 4) deltanet_chunk_prep_kernel<DK, DV, 4><<<pgrid, dim3(256), 0, s>>>(a);
+    else if (a.Kc == 3) deltanet_chunk_prep_kernel<DK, DV, 3><<<pgrid, dim3(256), 0, s>>>(a);
+    else deltanet_chunk_prep_kernel<DK, DV, 0><<<pgrid, dim3(256), 0, s>>>(a);
+    int rc = launched("deltanet_chunk_prep_kernel");
+    if (rc != HAI_OK) return rc;
+    constexpr size_t shmem = state_lds_floats<DK>() * sizeof(float);
+    static std::atomic<uint8_t> allowed[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return invalid("deltanet_prefill: device ordinal");
+    if (!allowed[dev].load(std::memory_order_acquire)) {
+        rc = check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(deltanet_chunk_state_kernel<DK, DV>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(shmem)),
+                       "hipFuncSetAttribute");
+        if (rc != HAI_OK) return rc;
+        allowed[dev].store(1, std::memory_order_release);
+    }
+    deltanet_chunk_state_kernel<DK, DV><<<dim3(a.nv, DV / state_cols<DK>(), a.B), dim3(512), shmem, s>>>(a);
+    rc = launched("deltanet_chunk_state_kernel");
     if (rc != HAI_OK) return rc;
     const int hist = a.Kc - 1;
     if (hist > 0) {
@@ -295,9 +523,18 @@ int launch_prefill(const PrefillArgs& a, uint16_t* out, int64_t ld_out, int64_t 
 
 }  // namespace
 
+// The unrounded outputs [B*T][nv*dv], then the per-chunk records (dk = dv).
+static size_t chunk_record_bytes(int64_t B, int64_t T, int64_t nv, int64_t dv) {
+    const int64_t per = dv == 64 ? chunk_floats<64, 64>() : chunk_floats<128, 128>();
+    return static_cast<size_t>(B * nv * ((T + kChunk - 1) / kChunk) * per) * sizeof(float);
+}
+static size_t output_bytes(int64_t B, int64_t T, int64_t nv, int64_t dv) {
+    return (static_cast<size_t>(B * T * nv * dv) * sizeof(float) + 255) / 256 * 256;
+}
+
 extern "C" size_t hai_deltanet_prefill_workspace_bytes(int64_t B, int64_t T, int64_t nv, int64_t dv) {
     if (B < 0 || T < 0 || nv < 0 || dv < 0) return 0;
-    return static_cast<size_t>(B * T * nv * dv) * sizeof(float);
+    return output_bytes(B, T, nv, dv) + chunk_record_bytes(B, T, nv, dv);
 }
 
 extern "C" int hai_deltanet_prefill_bf16(void* out, int64_t ld_out, const void* proj, int64_t ld_proj,
@@ -321,6 +558,7 @@ extern "C" int hai_deltanet_prefill_bf16(void* out, int64_t ld_out, const void* 
     if (B == 0 || T == 0) return HAI_OK;
     PrefillArgs a{};
     a.o_ws = static_cast<float*>(workspace);
+    a.chunks = reinterpret_cast<float*>(static_cast<char*>(workspace) + output_bytes(B, T, nv, dv));
     a.proj = static_cast<const uint16_t*>(proj);
     a.ld_proj = ld_proj;
     a.off_qkv = off_qkv;
