@@ -94,6 +94,9 @@ typedef struct hai_spec_stats {
     double draft_seconds;         /* host wall time, includes queueing */
     double verify_seconds;
     double correction_seconds;
+    int64_t host_syncs;           /* waits of the host on the stream during
+                                     the rounds: one per round, plus one for
+                                     each round that ends in a correction */
 } hai_spec_stats;
 
 /* Per-round record, int32 x 16: [proposal_count, accepted, full,

@@ -454,6 +454,17 @@ int hai_verify_argmax_accept_bf16(const void* logits, int64_t V,
  * bookkeeping, attention.h:11-42, delta_net.h:11-55). */
 int hai_add_i32(int32_t* dst, const int32_t* delta, int32_t add, int64_t n, void* stream);
 
+/* Draft i (0 <= i < T - 1) of a round's chained MTP proposals, counted on the
+ * device (the proposal loop of generator.cc:760-849, its EOS break at
+ * :845-847): ndraft[b] becomes i + 1 when i == 0 and cap[b] > 0, or when
+ * ndraft[b] == i, i < cap[b] and vids[b*T + i] (the candidate draft i - 1
+ * wrote, [B][T] verify layout) is not one of the n_eos ids in eos; otherwise
+ * it stays.  After the chain ndraft[b] is the proposal count that
+ * hai_verify_argmax_accept_bf16 takes, with no host read per draft. */
+int hai_draft_chain_count(int64_t i, const int64_t* vids, int64_t T, const int32_t* cap,
+                          const int64_t* eos, int64_t n_eos, int32_t* ndraft, int64_t B,
+                          void* stream);
+
 /* dst[i * dst_stride] = src[i * src_stride] for i < n (token ids between the
  * [B][T] verify layout and per-sequence [B] vectors). */
 int hai_copy_i64_strided(int64_t* dst, int64_t dst_stride, const int64_t* src,

@@ -137,6 +137,46 @@ def test_eos_stops_like_reference(engines):
     assert np.array_equal(log, rlog)
 
 
+def test_eos_draft_ends_the_chain_on_the_device(engines):
+    """Width 3 with drafts forced to the greedy continuation: every round
+    emits next_target and three accepted drafts, so output position j with
+    j % 4 == 2 is the second draft of a chain.  With that token as the only
+    EOS id the chain stops after it (generator.cc:845-847): the last round
+    proposes 2, not 3, its second candidate is the EOS id, and tokens and
+    round logs equal the oracle's.  The chain is counted on the device, so a
+    round waits on the stream once (no correction happens)."""
+    eng, ref, prompt = engines
+    g = ref.greedy(prompt, NEW)
+    j = next(j for j in range(6, NEW - 4) if j % 4 == 2 and g[j] not in g[:j])
+    eos = [int(g[j])]
+    toks, st, log = eng.speculative(prompt, NEW, 3, eos=eos, draft_override=g)
+    rtoks, rst, rlog = ref.speculative(prompt, NEW, 3, eos=eos, draft_override=g)
+    assert list(toks) == list(rtoks) == list(g[:j + 1])
+    assert np.array_equal(log, rlog)
+    assert log[-1][0] == 2 and log[-1][9] == eos[0] and log[-1][2] == 1
+    assert st["corrections"] == 0 and st["host_syncs"] == st["rounds"] == (j + 2) // 4
+    for key in ("rounds", "proposed", "accepted", "rejected"):
+        assert st[key] == rst[key], key
+
+
+def test_eos_set_with_natural_drafts_matches_reference(engines):
+    """The MTP head's own proposals (random weights: mostly rejected) with an
+    EOS set that holds a draft seen mid-chain in an EOS-free run: tokens and
+    round logs equal the oracle's, and the host waits once per round plus
+    once per correction."""
+    eng, ref, prompt = engines
+    _, _, free_log = ref.speculative(prompt, NEW, 3)
+    mids = [int(r[8 + 1]) for r in free_log if r[0] == 3]
+    eos = [mids[len(mids) // 2]]
+    toks, st, log = eng.speculative(prompt, NEW, 3, eos=eos)
+    rtoks, rst, rlog = ref.speculative(prompt, NEW, 3, eos=eos)
+    assert any(r[0] == 2 and r[9] == eos[0] for r in log[:-1]), "no chain ended on the EOS draft"
+    assert list(toks) == list(rtoks)
+    assert np.array_equal(log, rlog)
+    # a correction that ends the generation runs no correction step
+    assert st["rounds"] + st["corrections"] - 1 <= st["host_syncs"] <= st["rounds"] + st["corrections"]
+
+
 def test_token_ids_outside_vocabulary_are_rejected(engines):
     """Prompt and draft-override ids index the embedding table: ids outside
     [0, vocab) are an argument error before anything runs, and the engine

@@ -751,6 +751,32 @@ def test_argmax_rows_ties_nan():
     assert got[1] == 100 and got[2] == 0 and got[3] == 0 and got[4] == 9 and got[5] == 10 and got[6] == 248319
 
 
+def test_draft_chain_count_kernel():
+    """hai_draft_chain_count over a width-3 round: a chain counts its drafts
+    up to its cap, keeps an EOS candidate and stops after it
+    (generator.cc:845-847); the last draft's candidate is never checked and a
+    cap of 0 counts nothing."""
+    EOS = [900, 901]
+    T = 4  # next_target + 3 drafts
+    vids = np.array([[5, 10, 11, 12],     # no EOS: 3
+                     [5, 10, 11, 12],     # cap 0: 0
+                     [5, 900, 11, 12],    # first draft EOS: 1
+                     [5, 10, 901, 12],    # second draft EOS: 2
+                     [5, 10, 11, 12],     # cap 2: 2
+                     [5, 10, 11, 900]],   # last draft EOS: 3
+                    np.int64)
+    cap = np.array([3, 0, 3, 3, 2, 3], np.int32)
+    B = len(cap)
+    dv, dc, de = dev(vids), dev(cap), dev(np.array(EOS, np.int64))
+    for eos_ptr, n_eos, want in ((de.ptr, 2, [3, 0, 1, 2, 2, 3]), (None, 0, [3, 0, 3, 3, 2, 3])):
+        dn = dev(np.full(B, 7, np.int32))  # stale counts of an earlier round
+        for i in range(3):
+            hai.check(kern().hai_draft_chain_count(i, dv.ptr, T, dc.ptr, eos_ptr, n_eos, dn.ptr, B, None), "count")
+        assert list(dn.download(np.int32)) == want
+    with pytest.raises(hai.HaiError, match="draft_chain_count"):
+        hai.check(kern().hai_draft_chain_count(3, dv.ptr, T, dc.ptr, de.ptr, 2, dn.ptr, B, None), "count")
+
+
 def test_verify_accept_kernel():
     rng = np.random.default_rng(9)
     T, V, H = 4, 1000, 64
@@ -1368,9 +1394,9 @@ def test_gemm_mfma_stream_k_matches_plain_grid(fp8, M, N, K, epi):
     split (two partial planes for the tiles two blocks share): the result is
     deterministic and equals the plain grid (no workspace) up to fp32
     regrouping of the K sum, whose error (~1e-7 of the partial sums) is many
-    bf16 ulps only for outputs that cancel to near zero."""
-    if fp8 and K % 16:
-        pytest.skip("FP8 needs K % 16 == 0")
+    bf16 ulps only for outputs that cancel to near zero.  The FP8 kernels
+    read codes in 16-byte groups: K % 16 != 0 is rejected on the host before
+    any launch, and the output stays untouched."""
     rng = np.random.default_rng(N + K + M + epi)
     x, xb = rand_bf16(rng, (M, K))
     ncols = N // 2 if epi == hai.EPI_SILU_MUL else N
@@ -1391,6 +1417,14 @@ def test_gemm_mfma_stream_k_matches_plain_grid(fp8, M, N, K, epi):
         dw = dev(wb)
     wsb = kern().hai_gemm_mfma_workspace_bytes(M, N)
     dws = out_buf(max(wsb, 16))
+    if fp8 and K % 16:
+        dy = dev(hb)
+        with pytest.raises(hai.HaiError, match=r"K % 16 != 0"):
+            hai.check(kern().hai_gemm_fp8_mfma(dy.ptr, ncols, dx.ptr, K, dq.ptr, ds.ptr, None, M, N, K,
+                                               epi | hai.FP8_NO_SPECIAL_CODES, dy.ptr, ncols, dws.ptr, wsb, None),
+                      "fp8 mfma")
+        np.testing.assert_array_equal(dy.download(np.uint16).reshape(M, ncols), hb)
+        return
     outs = []
     for ws, n in ((dws.ptr, wsb), (dws.ptr, wsb), (None, 0)):
         dy = dev(hb) if epi == hai.EPI_RESIDUAL else out_buf(M * ncols * 2)

@@ -100,6 +100,7 @@ _KERNEL_SIGS = {
     "hai_argmax_rows_bf16": [VP, VP, I64, I64, I64, VP, VP],
     "hai_verify_argmax_accept_bf16": [VP, I64, VP, I64, VP, VP, I64, I64, VP, VP, VP, VP, VP, VP, VP, VP, VP],
     "hai_add_i32": [VP, VP, I32, I64, VP],
+    "hai_draft_chain_count": [I64, VP, I64, VP, VP, I64, VP, I64, VP],
     "hai_copy_i64_strided": [VP, I64, VP, I64, I64, VP],
     "hai_correction_commit_bf16": [VP, VP, VP, I64, I64, VP, VP, VP, VP, VP],
     "hai_gemm_bf16_mfma": [VP, I64, VP, I64, VP, I64, I64, I64, ctypes.c_int, VP, I64, VP, ctypes.c_size_t, VP],

@@ -150,9 +150,42 @@ __global__ void correction_commit_kernel(const int32_t* __restrict__ result, con
     }
 }
 
+// Counts draft i of a chained proposal per sequence.  Sequence b drafts
+// again while every earlier draft of the round counted (ndraft[b] == i), its
+// cap allows (i < cap[b]) and the candidate its previous draft wrote
+// (vids[b*T + i]) is no end-of-sequence id: the reference keeps an EOS
+// candidate as a proposal and ends the chain after it (generator.cc:845-847).
+// Draft 0 starts every count.
+__global__ void draft_chain_count_kernel(int64_t i, const int64_t* __restrict__ vids, int64_t T,
+                                         const int32_t* __restrict__ cap, const int64_t* __restrict__ eos,
+                                         int64_t n_eos, int32_t* ndraft, int64_t B) {
+    const int64_t b = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (b >= B) return;
+    if (i == 0) {
+        ndraft[b] = cap[b] > 0 ? 1 : 0;
+        return;
+    }
+    if (ndraft[b] != i || i >= cap[b]) return;
+    const int64_t tok = vids[b * T + i];
+    for (int64_t e = 0; e < n_eos; ++e)
+        if (eos[e] == tok) return;
+    ndraft[b] = static_cast<int32_t>(i + 1);
+}
+
 }  // namespace
 
 extern "C" {
+
+int hai_draft_chain_count(int64_t i, const int64_t* vids, int64_t T, const int32_t* cap, const int64_t* eos,
+                          int64_t n_eos, int32_t* ndraft, int64_t B, void* stream) {
+    if (vids == nullptr || cap == nullptr || ndraft == nullptr || (eos == nullptr && n_eos > 0) || n_eos < 0 ||
+        B < 0 || T < 2 || i < 0 || i >= T - 1)
+        return invalid("draft_chain_count");
+    if (B == 0) return HAI_OK;
+    draft_chain_count_kernel<<<dim3(static_cast<unsigned>((B + 255) / 256)), dim3(256), 0, as_stream(stream)>>>(
+        i, vids, T, cap, eos, n_eos, ndraft, B);
+    return launched("draft_chain_count_kernel");
+}
 
 int hai_add_i32(int32_t* dst, const int32_t* delta, int32_t add, int64_t n, void* stream) {
     if (dst == nullptr || n < 0) return invalid("add_i32");

@@ -32,7 +32,8 @@ class SpecStats(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int64) for n in (
         "rounds", "proposed", "accepted", "rejected", "corrections", "replay_tokens", "mtp_recovery_tokens",
         "max_proposal_width", "emitted")] + [(n, ctypes.c_double) for n in (
-            "prefill_seconds", "decode_seconds", "draft_seconds", "verify_seconds", "correction_seconds")]
+            "prefill_seconds", "decode_seconds", "draft_seconds", "verify_seconds", "correction_seconds")] + [
+                ("host_syncs", ctypes.c_int64)]
 
     def as_dict(self):
         return {n: getattr(self, n) for n, _ in self._fields_}

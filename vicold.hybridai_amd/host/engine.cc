@@ -136,6 +136,9 @@ Engine::~Engine() {
     if (caches_) hai_free(caches_);
     if (work_) hai_free(work_);
     if (d_override_) hai_free(d_override_);
+    if (d_gen_ov_) hai_free(d_gen_ov_);
+    if (d_eos_) hai_free(d_eos_);
+    if (h_stage_) hai_host_free(h_stage_);
     if (stream_) hai_stream_destroy(stream_);
 }
 
@@ -321,6 +324,7 @@ int Engine::alloc_all() {
         d_delta_ = cv.take<int32_t>(B_);
         d_plen_ = cv.take<int32_t>(7 * B_);
         d_pnext_ = cv.take<int64_t>(B_);
+        d_pcap_ = cv.take<int32_t>(B_);
         h_ = cv.take<uint16_t>(R * H);
         xn_ = cv.take<uint16_t>(R * 2 * H);
         emb_ = cv.take<uint16_t>(R * H);
@@ -370,6 +374,11 @@ int Engine::alloc_all() {
         carve_work(real);
         HAI_TRY(hai_memset(work_, 0, sizing.used(), stream_));
     }
+    // Pinned staging for the per-round uploads: a round writes each slice at
+    // most once, and the previous round's copies ended with its closing sync.
+    void* pin = nullptr;
+    HAI_TRY(hai_host_malloc(&pin, static_cast<size_t>(3 * B_) * sizeof(int32_t)));
+    h_stage_ = static_cast<int32_t*>(pin);
     return sync();
 }
 
@@ -392,6 +401,7 @@ int Engine::upload_rope_tables() {
 }
 
 int Engine::sync() {
+    ++syncs_;
     const int rc = hai_stream_synchronize(stream_);
     if (rc != HAI_OK) return lib_fail(rc, "stream synchronize");
     return HAI_OK;
@@ -400,6 +410,23 @@ int Engine::sync() {
 int Engine::read_i64(const int64_t* d, int64_t* h, int64_t n) {
     HAI_TRY(hai_memcpy_d2h(h, d, static_cast<size_t>(n) * 8, stream_));
     return sync();
+}
+
+int Engine::upload_ids(int64_t** table, int64_t* cap, const int32_t* ids, int64_t n) {
+    if (n <= 0) return HAI_OK;
+    if (n > *cap || *table == nullptr) {
+        HAI_TRY(sync());  // the old table may still be read by queued work
+        if (*table) HAI_TRY(hai_free(*table));
+        *table = nullptr;
+        *cap = 0;
+        void* p = nullptr;
+        HAI_TRY(hai_malloc(&p, static_cast<size_t>(n) * 8));
+        *table = static_cast<int64_t*>(p);
+        *cap = n;
+    }
+    std::vector<int64_t> wide(ids, ids + n);
+    HAI_TRY(hai_memcpy_h2d(*table, wide.data(), wide.size() * 8, stream_));
+    return sync();  // wide lives on the host stack
 }
 
 int Engine::init_synthetic(uint64_t seed, float std_dev) {
@@ -1024,55 +1051,57 @@ int Engine::one_round(int64_t width, const RoundIo& io, bool* any_live) {
     HAI_TRY(hai_copy_i64_strided(d_vids_, T, d_next_, 1, B_, stream_));
 
     // ---- draft (chained MTP proposals) ----
+    // With an EOS set a chain can end early (generator.cc:845-847); the
+    // counts then live on the device (hai_draft_chain_count) and come back
+    // with the verify result, so the round still syncs once.  Without one
+    // every chain runs to its cap and the host knows the counts.
     auto t0 = Clock::now();
-    std::vector<int64_t> kd(Bz, 0);  // drafts counted per sequence (EOS cuts a chain short)
-    std::vector<bool> open(Bz);
-    for (size_t b = 0; b < Bz; ++b) open[b] = pc[b] > 0;
+    const int64_t syncs0 = syncs_;
+    const bool chain_on_device = io.n_eos > 0;
+    int32_t* h_cap = h_stage_;
+    int32_t* h_nd = h_stage_ + Bz;
+    int32_t* h_delta = h_stage_ + 2 * Bz;
+    if (chain_on_device) {
+        for (size_t b = 0; b < Bz; ++b) h_cap[b] = static_cast<int32_t>(pc[b]);
+        HAI_TRY(hai_memcpy_h2d(d_pcap_, h_cap, Bz * 4, stream_));
+    }
     for (int64_t i = 0; i < k; ++i) {
         HAI_TRY(draft_step_at(i, T));
-        bool need_read = false;
-        for (size_t b = 0; b < Bz; ++b) {
-            if (!open[b]) continue;
-            const int64_t pos = rs_[b].emitted + 1 + i;
-            if (io.override_tokens != nullptr && pos < io.n_override) {
-                const int64_t tok = io.override_tokens[static_cast<int64_t>(b) * io.n_override + pos];
-                HAI_TRY(hai_memcpy_h2d(d_vids_ + static_cast<int64_t>(b) * T + i + 1, &tok, 8, stream_));
-                HAI_TRY(sync());  // tok lives on the host stack
-            } else if (io.device_override && pos < n_override_) {
-                HAI_TRY(hai_memcpy_d2d(d_vids_ + static_cast<int64_t>(b) * T + i + 1,
-                                       d_override_ + static_cast<int64_t>(b) * n_override_ + pos, 8, stream_));
+        if (io.ov != nullptr)
+            for (size_t b = 0; b < Bz; ++b) {
+                const int64_t pos = rs_[b].emitted + 1 + i;
+                if (i < pc[b] && pos < io.n_ov)
+                    HAI_TRY(hai_memcpy_d2d(d_vids_ + static_cast<int64_t>(b) * T + i + 1,
+                                           io.ov + static_cast<int64_t>(b) * io.n_ov + pos, 8, stream_));
             }
-            ++kd[b];
-            ++io.stats[b].proposed;
-            need_read = need_read || io.n_eos > 0;
-        }
-        if (need_read) {
-            std::vector<int64_t> cand(Bz);
-            HAI_TRY(hai_copy_i64_strided(d_cand_, 1, d_vids_ + i + 1, T, B_, stream_));
-            HAI_TRY(read_i64(d_cand_, cand.data(), B_));
-            for (size_t b = 0; b < Bz; ++b)
-                if (open[b] && in_set(io.eos, io.n_eos, cand[b])) open[b] = false;
-        }
-        for (size_t b = 0; b < Bz; ++b)
-            if (open[b] && kd[b] >= pc[b]) open[b] = false;
+        if (chain_on_device)
+            HAI_TRY(hai_draft_chain_count(i, d_vids_, T, d_pcap_, d_eos_, io.n_eos, d_ndraft_, B_, stream_));
     }
     // Drafts beyond a sequence's own count leave MTP rows the accept kernel
-    // must not see: roll the lengths back and pass the counts.
-    std::vector<int32_t> nd(Bz), delta(Bz);
-    bool uneven = false;
-    for (size_t b = 0; b < Bz; ++b) {
-        nd[b] = static_cast<int32_t>(kd[b]);
-        delta[b] = static_cast<int32_t>(kd[b] - k);
-        uneven = uneven || delta[b] != 0;
-    }
-    if (uneven) {
-        HAI_TRY(hai_memcpy_h2d(d_delta_, delta.data(), Bz * 4, stream_));
-        HAI_TRY(hai_add_i32(d_mlen_, d_delta_, 0, B_, stream_));
-    }
-    if (nd != ndraft_host_) {
-        HAI_TRY(hai_memcpy_h2d(d_ndraft_, nd.data(), Bz * 4, stream_));
-        HAI_TRY(sync());  // nd lives on the host stack
-        ndraft_host_ = nd;
+    // must not see: roll the lengths back (mtp_len += count - k) and pass
+    // the counts.
+    std::vector<int64_t> kd(Bz);
+    if (chain_on_device) {
+        HAI_TRY(hai_add_i32(d_mlen_, d_ndraft_, static_cast<int32_t>(-k), B_, stream_));
+        ndraft_host_.clear();  // the device counts are read back with the verify result
+    } else {
+        std::vector<int32_t> nd(Bz);
+        bool uneven = false;
+        for (size_t b = 0; b < Bz; ++b) {
+            kd[b] = pc[b];
+            nd[b] = static_cast<int32_t>(pc[b]);
+            h_delta[b] = static_cast<int32_t>(pc[b] - k);
+            uneven = uneven || h_delta[b] != 0;
+        }
+        if (uneven) {
+            HAI_TRY(hai_memcpy_h2d(d_delta_, h_delta, Bz * 4, stream_));
+            HAI_TRY(hai_add_i32(d_mlen_, d_delta_, 0, B_, stream_));
+        }
+        if (nd != ndraft_host_) {
+            std::copy(nd.begin(), nd.end(), h_nd);
+            HAI_TRY(hai_memcpy_h2d(d_ndraft_, h_nd, Bz * 4, stream_));
+            ndraft_host_ = nd;
+        }
     }
     const double draft_s = seconds_since(t0);
 
@@ -1084,7 +1113,10 @@ int Engine::one_round(int64_t width, const RoundIo& io, bool* any_live) {
     HAI_TRY(hai_memcpy_d2h(res.data(), d_result_, res.size() * 4, stream_));
     HAI_TRY(hai_memcpy_d2h(preds.data(), d_preds_, preds.size() * 8, stream_));
     HAI_TRY(hai_memcpy_d2h(ids.data(), d_vids_, ids.size() * 8, stream_));
+    if (chain_on_device) HAI_TRY(hai_memcpy_d2h(h_nd, d_ndraft_, Bz * 4, stream_));
     HAI_TRY(sync());
+    if (chain_on_device)
+        for (size_t b = 0; b < Bz; ++b) kd[b] = h_nd[b];
     const double verify_s = seconds_since(t0);
 
     std::vector<bool> correct(Bz, false);
@@ -1097,6 +1129,7 @@ int Engine::one_round(int64_t width, const RoundIo& io, bool* any_live) {
         int32_t* out = io.out + static_cast<int64_t>(b) * io.out_ld;
         const int64_t kb = kd[b];
         stats.max_proposal_width = std::max(stats.max_proposal_width, pc[b]);
+        stats.proposed += kb;
         ++stats.rounds;
         stats.draft_seconds += draft_s;
         stats.verify_seconds += verify_s;
@@ -1172,6 +1205,7 @@ int Engine::one_round(int64_t width, const RoundIo& io, bool* any_live) {
         }
         const int32_t* out = io.out + static_cast<int64_t>(b) * io.out_ld;
         if (!st.done && (st.emitted >= st.max_new || in_set(io.eos, io.n_eos, out[st.emitted - 1]))) st.done = true;
+        io.stats[b].host_syncs += syncs_ - syncs0;
     }
     return HAI_OK;
 }
@@ -1201,8 +1235,12 @@ int Engine::generate_speculative(const int32_t* prompts, int64_t P, int64_t max_
     RoundIo io;
     io.eos = eos;
     io.n_eos = n_eos;
-    io.override_tokens = override_tokens;
-    io.n_override = override_tokens ? n_override : 0;
+    if (override_tokens != nullptr && n_override > 0) {
+        HAI_TRY(upload_ids(&d_gen_ov_, &gen_ov_cap_, override_tokens, B_ * n_override));
+        io.ov = d_gen_ov_;
+        io.n_ov = n_override;
+    }
+    HAI_TRY(upload_ids(&d_eos_, &eos_cap_, eos, n_eos));
     io.out = out;
     io.out_ld = max_new;
     io.stats = st.data();
@@ -1274,7 +1312,10 @@ int Engine::spec_rounds(int64_t rounds, int64_t width, int32_t* out, int64_t cap
     io.out = out;
     io.out_ld = cap;
     io.stats = st.data();
-    io.device_override = n_override_ > 0;
+    if (n_override_ > 0) {
+        io.ov = d_override_;
+        io.n_ov = n_override_;
+    }
     auto t0 = Clock::now();
     bool live = true;
     for (int64_t r = 0; r < rounds && live; ++r) HAI_TRY(one_round(width, io, &live));
@@ -1291,6 +1332,7 @@ int Engine::spec_rounds(int64_t rounds, int64_t width, int32_t* out, int64_t cap
         sum.replay_tokens += s.replay_tokens;
         sum.mtp_recovery_tokens += s.mtp_recovery_tokens;
         sum.max_proposal_width = std::max(sum.max_proposal_width, s.max_proposal_width);
+        sum.host_syncs = std::max(sum.host_syncs, s.host_syncs);
         sum.emitted += rs_[b].emitted - start[b];
         if (n_out) n_out[b] = rs_[b].emitted;
     }
@@ -1305,6 +1347,7 @@ int Engine::spec_rounds(int64_t rounds, int64_t width, int32_t* out, int64_t cap
         stats->mtp_recovery_tokens += sum.mtp_recovery_tokens;
         stats->max_proposal_width = std::max(stats->max_proposal_width, sum.max_proposal_width);
         stats->emitted += sum.emitted;
+        stats->host_syncs += sum.host_syncs;
         stats->decode_seconds += dt;
     }
     return HAI_OK;

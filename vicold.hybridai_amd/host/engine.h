@@ -196,17 +196,16 @@ private:
     };
     // Inputs of one lockstep round that vary per sequence.
     struct RoundIo {
-        const int32_t* eos = nullptr;
-        int64_t n_eos = 0;
-        const int32_t* override_tokens = nullptr;  // [B][n_override]
-        int64_t n_override = 0;
+        const int32_t* eos = nullptr;              // host copy (round-start and correction checks)
+        int64_t n_eos = 0;                         // > 0: the draft chains end on the device (d_eos_)
+        const int64_t* ov = nullptr;               // device [B][n_ov] draft overrides, or null
+        int64_t n_ov = 0;
         int32_t* out = nullptr;                    // [B][out_ld]
         int64_t out_ld = 0;
         hai_spec_stats* stats = nullptr;           // [B]
         int32_t* round_log = nullptr;              // [B][log_cap][HAI_ROUND_RECORD]
         int64_t log_cap = 0;
         int64_t* n_log = nullptr;                  // [B] records written
-        bool device_override = false;              // drafts from d_override_ (spec_rounds)
     };
 
     int fail(int rc, const std::string& what);       // the engine's own message
@@ -258,6 +257,8 @@ private:
     int one_round(int64_t width, const RoundIo& io, bool* any_live);
     int sync();
     int read_i64(const int64_t* d, int64_t* h, int64_t n);
+    // ids (int32, host) widened into an engine-owned device table that grows on demand
+    int upload_ids(int64_t** table, int64_t* cap, const int32_t* ids, int64_t n);
     // Replays the captured graph in *slot (capturing `enqueue` on first use)
     // when graphs are enabled; otherwise launches `enqueue` directly.
     template <typename F>
@@ -322,6 +323,13 @@ private:
     int64_t* d_pnext_ = nullptr;  // [B] profiling scratch tokens
     int64_t* d_override_ = nullptr;  // [B][n_override_] draft overrides of spec_rounds (own allocation)
     int64_t n_override_ = 0;
+    int64_t* d_gen_ov_ = nullptr;    // [B][n] draft overrides of one generate_speculative call (own allocation)
+    int64_t gen_ov_cap_ = 0;         // int64 entries of d_gen_ov_
+    int64_t* d_eos_ = nullptr;       // end-of-sequence ids of the running generate call (own allocation)
+    int64_t eos_cap_ = 0;
+    int32_t* d_pcap_ = nullptr;      // [B] proposal caps of the round (device chain counting)
+    int32_t* h_stage_ = nullptr;     // pinned [3B]: caps, draft counts, MTP length corrections of a round
+    int64_t syncs_ = 0;              // host synchronisations with the stream so far
     uint16_t* h_ = nullptr;       // [rows, H] residual stream
     uint16_t* xn_ = nullptr;      // [rows, 2H]
     uint16_t* emb_ = nullptr;     // [rows, H]
