@@ -85,8 +85,11 @@ int hai_graph_destroy(void* graph_exec);
  * Y[m, n] = sum_k X[m, k] W[n, k] with W stored [N, K] row-major
  * (Linear::forward_into, linear.cc:117-179; rocblas_gemm_ex at
  * hip_backend.cc:784-789).  Requirements: K % 8 == 0, ldx % 8 == 0,
- * 16-byte aligned X and W, M <= 16 per call (callers split larger M; rows
- * are independent so the split does not change any bit).
+ * 16-byte aligned X and W.  Any M: a call of more than 16 rows runs them in
+ * 16-row batches within one launch, the batches of a weight row group on
+ * one XCD one after another, so each weight is read from HBM about once per
+ * launch; rows are independent and every row's sum is in the same order, so
+ * the batching does not change any bit.
  * Epilogues:
  *   HAI_EPI_STORE     y = bf16(acc)
  *   HAI_EPI_RESIDUAL  y = bf16(res + bf16(acc))   (make_residual fused,
@@ -105,7 +108,7 @@ int hai_gemm_bf16(void* y, int64_t ldy, const void* x, int64_t ldx,
  * projection of every sub-layer, and the final norm before lm_head).
  * y = epilogue(rmsnorm(x; norm_w, eps, unit_offset) . W^T), bit-identical to
  * hai_rmsnorm_bf16 then hai_gemm_bf16.  xn_out, if not null, also receives
- * the normalised rows (ld_xn).  When M * K exceeds
+ * the normalised rows (ld_xn).  When M > 16 or M * K exceeds
  * HAI_GEMM_RMSNORM_FUSED_MAX the rows do not fit the on-chip prologue: the
  * call then runs the two kernels and needs xn_out as their intermediate. */
 #define HAI_GEMM_RMSNORM_FUSED_MAX 16384

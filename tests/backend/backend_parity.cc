@@ -121,8 +121,11 @@ void check_gpu(Backend* be) {
     Dev d{be};
     std::mt19937 rng(1234);
 
-    {  // gemm: Linear Y = X W^T, 20 rows (two 16-row launches)
-        const int64_t M = 20, N = 300, K = 256;
+    // gemm: Linear Y = X W^T; 20 rows (two 16-row batches of one launch) and
+    // a 512-row prompt at the 27B hidden size (32 batches, the weights
+    // streamed once by the launch)
+    for (const int64_t M : {int64_t{20}, int64_t{512}}) {
+        const int64_t N = M == 20 ? 300 : 5120, K = M == 20 ? 256 : 5120;
         auto x = random_bf16(rng, M * K), w = random_bf16(rng, N * K, 0.05f);
         auto dx = d.up(x.bits), dw = d.up(w.bits), dy = d.make(M * N * 2);
         expect_ok(be->gemm(dy.get(), dx.get(), dw.get(), DType::BF16, DType::BF16, DType::BF16, DType::FP32, false,
@@ -130,7 +133,7 @@ void check_gpu(Backend* be) {
                   "gemm");
         std::vector<float> want(M * N);
         orc_gemm(x.f.data(), w.f.data(), want.data(), M, N, K, 1);
-        same_bits(d.down<uint16_t>(dy.get(), M * N), want, "gemm");
+        same_bits(d.down<uint16_t>(dy.get(), M * N), want, "gemm M=" + std::to_string(M));
     }
     {  // add, silu_mul
         const int64_t n = 1000;

@@ -162,7 +162,60 @@ def test_gemm_silu_mul(M, F, K_):
 def test_gemm_rejects_bad_shapes():
     d = out_buf(64)
     assert kern().hai_gemm_bf16(d.ptr, 4, d.ptr, 12, d.ptr, 2, 4, 12, 0, None, 0, None) == 1  # K % 8
-    assert kern().hai_gemm_bf16(d.ptr, 4, d.ptr, 8, d.ptr, 17, 4, 8, 0, None, 0, None) == 1   # M > 16
+    assert kern().hai_gemm_bf16(d.ptr, 4, d.ptr, 4, d.ptr, 2, 4, 8, 0, None, 0, None) == 1    # ldx < K
+    assert kern().hai_gemm_bf16(d.ptr, 4, d.ptr, 8, d.ptr, -1, 4, 8, 0, None, 0, None) == 1   # M < 0
+    # a fused-norm launch of more than 16 rows needs xn_out for the two-kernel form
+    assert kern().hai_gemm_rmsnorm_bf16(d.ptr, 4, d.ptr, 8, d.ptr, 1e-6, 1, None, 0, d.ptr, 17, 4, 8, 0,
+                                        None, 0, None) == 1
+
+
+@pytest.mark.parametrize("M,N,K_,epi,ldx", [(17, 300, 256, 0, 256), (37, 1000, 520, 1, 528), (300, 77, 8, 0, 8),
+                                            (100, 1200, 1024, 2, 1024), (512, 1536, 2048, 0, 2048),
+                                            (64, 8200, 1024, 1, 1040), (40, 5120, 17408, 1, 17408)])
+def test_gemm_row_batches(M, N, K_, epi, ldx):
+    """Launches of more than 16 rows (prompt-sized M through Backend::gemm,
+    hip_backend.cc:697-809): one launch whose blocks each take a weight row
+    group and a 16-row batch, ragged last batch and row pitches included;
+    every row bit-identical to the oracle's canonical-order sum."""
+    rng = np.random.default_rng(M * 7 + N + K_)
+    xp, xpb = rand_bf16(rng, (M, ldx))
+    x = xp[:, :K_]
+    if epi == hai.EPI_SILU_MUL:
+        F = N // 2
+        g, gb = rand_bf16(rng, (F, K_), 0.05)
+        u, ub = rand_bf16(rng, (F, K_), 0.05)
+        wb = np.empty((N, K_), np.uint16)
+        wb[0::2], wb[1::2] = gb, ub
+        want = orc.silu_mul(orc.gemm(x, g), orc.gemm(x, u))
+        ncols = F
+    else:
+        w, wb = rand_bf16(rng, (N, K_), 0.05)
+        want = orc.gemm(x, w)
+        ncols = N
+    h, hb = rand_bf16(rng, (M, ncols))
+    if epi == hai.EPI_RESIDUAL:
+        want = orc.add(h, want)
+    dx, dw, dy = dev(xpb), dev(wb), dev(hb)
+    res = dy.ptr if epi == hai.EPI_RESIDUAL else None
+    hai.check(kern().hai_gemm_bf16(dy.ptr, ncols, dx.ptr, ldx, dw.ptr, M, N, K_, epi, res, ncols, None),
+              "gemm row batches")
+    assert_bits_equal(dy.download(np.uint16), want, f"gemm {M}x{N}x{K_} epi {epi}")
+
+
+def test_gemm_rmsnorm_row_batches():
+    """The fused-norm entry with more than 16 rows: the norm into xn_out,
+    then one batched launch, bit-identical to rmsnorm then gemm."""
+    M, N, K_ = 48, 640, 1024
+    rng = np.random.default_rng(5)
+    x, xb = rand_bf16(rng, (M, K_))
+    nw, nwb = rand_bf16(rng, (K_,), 0.02)
+    w, wb = rand_bf16(rng, (N, K_), 0.05)
+    dx, dn, dw, dy, dxn = dev(xb), dev(nwb), dev(wb), out_buf(M * N * 2), out_buf(M * K_ * 2)
+    hai.check(kern().hai_gemm_rmsnorm_bf16(dy.ptr, N, dx.ptr, K_, dn.ptr, 1e-6, 1, dxn.ptr, K_, dw.ptr, M, N, K_,
+                                           hai.EPI_STORE, None, 0, None), "gemm_rmsnorm 48 rows")
+    xn = orc.rmsnorm(x, nw, 1e-6, True)
+    assert_bits_equal(dxn.download(np.uint16), xn, "xn")
+    assert_bits_equal(dy.download(np.uint16), orc.gemm(xn, w), "gemm after norm")
 
 
 @pytest.mark.parametrize("M,N,K_,epi", [(1, 4096, 256, 0), (2, 16480, 5120, 0), (2, 17408, 5120, 2),

@@ -133,6 +133,14 @@ __device__ __forceinline__ u32x4 bload_w(__amdgpu_buffer_rsrc_t r, uint32_t voff
     return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(voff),
                                                                            static_cast<int>(soff), HAI_WLOAD_AUX));
 }
+// The weight loads of a launch that reads each weight several times (row
+// batches): cached, so that the batches after the first find them in L2.
+template <bool kStream>
+__device__ __forceinline__ u32x4 bload_wp(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(voff),
+                                                                           static_cast<int>(soff),
+                                                                           kStream ? HAI_WLOAD_AUX : 0));
+}
 
 // Index of the calling wave in its block, as a wave-uniform (scalar) value:
 // derived from threadIdx.x, the compiler would otherwise treat it as

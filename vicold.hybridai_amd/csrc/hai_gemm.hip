@@ -19,6 +19,7 @@
 //     SwiGLU product for interleaved gate/up rows.
 #include "hai_gemm_common.h"
 
+#include <algorithm>
 #include <atomic>
 #include <cstdlib>
 #include <mutex>
@@ -31,23 +32,60 @@ using namespace hai;
 
 // Prologue of gemm_bf16_kernel: none (activation rows read from global
 // memory per chunk group), the fused RMSNorm (rows and norm weight staged in
-// LDS and normalised there), or rows already normalised staged in LDS as
-// they are (a two-row launch whose input a residual launch's norm tail
-// wrote).
-enum { kProNone = 0, kProNorm = 1, kProStage = 2 };
+// LDS and normalised there), the rows staged in LDS as they are (two-row
+// launches of the wide layers), or a row batch: a launch of more than MB
+// rows whose blocks each take one weight row group and one batch of MB rows
+// (activations read from global memory, as with none).
+enum { kProNone = 0, kProNorm = 1, kProStage = 2, kProBatch = 3 };
+
+// Blocks go to the XCDs round-robin by block index, and each XCD has its own
+// L2.
+constexpr int kXcds = 8;
 
 template <int MB, int RW, int U, int EPI, int PRO>
 __global__ __launch_bounds__(256) void gemm_bf16_kernel(
     uint16_t* __restrict__ y, int64_t ldy, const uint16_t* __restrict__ x, int64_t ldx,
     const uint16_t* w, const uint16_t* res, int64_t ldres, int M, int N, int K, NormArgs na) {
     // NORM: the rows are read from LDS (staged by the prologue)
-    constexpr bool NORM = PRO != kProNone;
+    constexpr bool NORM = PRO == kProNorm || PRO == kProStage;
     constexpr bool kNormalize = PRO == kProNorm;
+    constexpr bool kBatch = PRO == kProBatch;
     static_assert(PRO != kProStage || MB == 2, "the stage-only prologue is the two-row copy-staged one");
     const int lane = threadIdx.x & 63;
     const int wave = wave_index();
     extern __shared__ u32x4 xs[];  // NORM: [M][K/8] (normalised) rows, then the norm weight
     const int npr = K >> 3;        // 16-byte pieces per row
+
+    // Row groups (4 waves x RW rows) strided over the grid; the plain kernel
+    // is launched with one block per group, the NORM kernel with a grid sized
+    // to the machine so that the prologue is paid once per resident block.
+    const int64_t ngroups = (static_cast<int64_t>(N) + 4 * RW - 1) / (4 * RW);
+    int64_t grp = blockIdx.x;
+    if constexpr (kBatch) {
+        // Block b runs on XCD b % 8 and takes slot s = b / 8 there; the XCD
+        // owns the groups g = 8 * lg + b % 8.  Its slots walk tiles of 16
+        // groups, each tile batch by batch with the groups minor, so the
+        // resident blocks of an XCD (64-96) share 16 groups' weights and a
+        // few batches' rows in its L2, and the weights are loaded cached
+        // (bload_wp): each weight comes from beyond L2 about once and the
+        // rows once per tile (MI355X, 512 x 5120 x 5120: 125 MiB fetched for
+        // 55 MiB of operands, against 1034 MiB with the blocks spread over
+        // the XCDs and 555 MiB with non-temporal weight loads).  Each row's
+        // sum is in the canonical order whatever its batch.
+        constexpr uint32_t kTileGroups = 16;
+        const uint32_t nb = static_cast<uint32_t>((M + MB - 1) / MB);
+        const uint32_t ngl = static_cast<uint32_t>((ngroups + kXcds - 1) / kXcds);
+        const uint32_t slot = blockIdx.x / kXcds;
+        const uint32_t tile = slot / (kTileGroups * nb);
+        const uint32_t r = slot - tile * kTileGroups * nb;
+        const uint32_t gsz = min(kTileGroups, ngl - tile * kTileGroups);
+        const int bt = static_cast<int>(r / gsz);
+        grp = static_cast<int64_t>(tile * kTileGroups + r % gsz) * kXcds + blockIdx.x % kXcds;
+        x += static_cast<int64_t>(bt) * MB * ldx;
+        y += static_cast<int64_t>(bt) * MB * ldy;
+        if (EPI == HAI_EPI_RESIDUAL) res += static_cast<int64_t>(bt) * MB * ldres;
+        M = min(MB, M - bt * MB);
+    }
 
     // Byte offsets fit 32 bits: the caller bounds N*K*2 and M*ldx*2 below 4 GiB.
     const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, static_cast<uint32_t>(static_cast<int64_t>(N) * K * 2));
@@ -57,11 +95,6 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(
     for (int m = 0; m < MB; ++m) xoff[m] = static_cast<uint32_t>((static_cast<int64_t>(m) * ldx + lane * 8) * 2);
     const int nck = (K + 511) / 512;
     const int nfull = K / 512;
-
-    // Row groups (4 waves x RW rows) strided over the grid; the plain kernel
-    // is launched with one block per group, the NORM kernel with a grid sized
-    // to the machine so that the prologue is paid once per resident block.
-    const int64_t ngroups = (static_cast<int64_t>(N) + 4 * RW - 1) / (4 * RW);
 
     // The block's first weight chunks do not depend on the activations: with
     // the fused RMSNorm they are requested before the prologue, whose
@@ -77,7 +110,7 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(
     constexpr bool kDmaStage = NORM && MB == 2;
     constexpr int PG = kDmaStage ? 2 : 1;
     u32x4 wpre[PG * U][RW];
-    const int64_t grp0 = blockIdx.x;
+    const int64_t grp0 = grp;
     if constexpr (NORM) {
         const int64_t row0 = (grp0 * 4 + wave) * RW;
         const bool pre_ok = grp0 < ngroups && row0 < N;
@@ -95,7 +128,7 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(
             const ChunkOffset co(u < nfull && pre_ok, ok && pre_ok, static_cast<uint32_t>(u) * 1024u);
 #pragma unroll
             for (int r = 0; r < RW; ++r)
-                wpre[u][r] = bload_w(rw,
+                wpre[u][r] = bload_wp<!kBatch>(rw,
                                      co.v(pre_ok ? static_cast<uint32_t>(((row0 + r) * static_cast<int64_t>(K) + lane * 8) * 2)
                                                  : kOutOfRange),
                                      co.s);
@@ -262,7 +295,7 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(
 #pragma unroll
             for (int u = 0; u < U; ++u)
 #pragma unroll
-                for (int r = 0; r < RW; ++r) wv[u][r] = bload_w(rw, woff[r], static_cast<uint32_t>(cg + u) * 1024u);
+                for (int r = 0; r < RW; ++r) wv[u][r] = bload_wp<!kBatch>(rw, woff[r], static_cast<uint32_t>(cg + u) * 1024u);
         };
         constexpr bool kPipe = NORM && MB == 2;
         if (!kPipe) {
@@ -305,7 +338,7 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(
                 const bool ok = c < nfull || (c < nck && c * 512 + lane * 8 < K);
                 const ChunkOffset co(c < nfull, ok, static_cast<uint32_t>(c) * 1024u);
 #pragma unroll
-                for (int r = 0; r < RW; ++r) wv[u][r] = bload_w(rw, co.v(woff[r]), co.s);
+                for (int r = 0; r < RW; ++r) wv[u][r] = bload_wp<!kBatch>(rw, co.v(woff[r]), co.s);
             }
             step(c0, wv, xv, std::false_type{});
         }
@@ -342,7 +375,10 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(
                 }
         }
     };
-    int64_t grp = blockIdx.x;
+    if constexpr (kBatch) {
+        if (grp < ngroups) run_group(grp, std::false_type{});
+        return;
+    }
     if constexpr (NORM) {
         if (grp < ngroups) run_group(grp, std::true_type{});
         grp += gridDim.x;
@@ -665,7 +701,9 @@ void launch_gemm(const GemmArgs& a, hipStream_t s) {
                          : PRO == kProStage ? static_cast<size_t>(a.M) * a.K * 2
                                             : 0;
     int64_t blocks = groups;
-    if (PRO != kProNone) {
+    if (PRO == kProBatch) {
+        blocks = (groups + kXcds - 1) / kXcds * kXcds * ((a.M + MB - 1) / MB);
+    } else if (PRO != kProNone) {
         const int64_t resident = resident_blocks(reinterpret_cast<const void*>(kern), shmem);
         if (resident > 0 && resident < blocks) blocks = resident;
     }
@@ -743,9 +781,38 @@ bool use_stage_rows(const GemmArgs& a) {
     return on && a.M == 2 && a.N > 8192 && static_cast<int64_t>(a.M) * a.K <= kNormMaxElems;
 }
 
+// More than 16 rows: row batches in one launch (kProBatch), at most 2^31
+// threads per launch.  Batches of 8 rows up to K = 8192, of 16 above: on
+// MI355X at 512 x 5120 x 5120, 8-row batches take 583 us against 726 us
+// (more waves resident), with the same 125 MiB fetched from beyond L2; at
+// K = 17408 the larger rows of 8 waves' batches no longer fit the XCD's L2
+// and 16-row batches win (1780 against 1964 us).
+template <int EPI>
+void launch_batches(const GemmArgs& a, hipStream_t s) {
+    const int64_t groups = (static_cast<int64_t>(a.N) + 7) / 8;
+    const int64_t per_batch = (groups + kXcds - 1) / kXcds * kXcds;
+    const int mb = a.K <= 8192 ? 8 : 16;
+    const int64_t max_rows = std::max<int64_t>(1, (INT32_MAX / 256) / per_batch) * mb;
+    for (int64_t r0 = 0; r0 < a.M; r0 += max_rows) {
+        GemmArgs b = a;
+        b.M = static_cast<int>(std::min<int64_t>(max_rows, a.M - r0));
+        b.x = a.x + r0 * a.ldx;
+        b.y = a.y + r0 * a.ldy;
+        if (a.res) b.res = a.res + r0 * a.ldres;
+        if (mb == 8) launch_gemm<8, 2, EPI, kProBatch>(b, s);
+        else launch_gemm<16, 2, EPI, kProBatch>(b, s);
+    }
+}
+
 template <int EPI, bool NORM>
 int dispatch_mb(const GemmArgs& a, hipStream_t s) {
     constexpr int PRO = NORM ? kProNorm : kProNone;
+    if constexpr (!NORM) {
+        if (a.M > 16) {
+            launch_batches<EPI>(a, s);
+            return HAI_OK;
+        }
+    }
     if constexpr (!NORM && EPI != HAI_EPI_SILU_MUL) {
         if (use_staged(a)) return launch_staged<EPI>(a, s);
     }
@@ -790,12 +857,14 @@ int dispatch_epi(const GemmArgs& a, int epilogue, hipStream_t s) {
     return launched("gemm_bf16_kernel");
 }
 
+// Any M: launches of more than 16 rows run in batches of 16 rows whose X
+// offsets stay inside the 4 GiB range.
 int check_shape(const void* y, const void* x, const void* w, int64_t M, int64_t N, int64_t K, int64_t ldx) {
     if (y == nullptr || x == nullptr || w == nullptr) return invalid("gemm: null pointer");
-    if (M < 0 || M > 16 || N < 0 || K <= 0 || K % 8 != 0 || ldx % 8 != 0 || ldx < K)
-        return invalid("gemm: shape (need 0<=M<=16, K%8==0, ldx%8==0, ldx>=K)");
+    if (M < 0 || M > INT32_MAX || N < 0 || K <= 0 || K % 8 != 0 || ldx % 8 != 0 || ldx < K)
+        return invalid("gemm: shape (need 0<=M<2^31, K%8==0, ldx%8==0, ldx>=K)");
     if (N > INT32_MAX || K > INT32_MAX) return invalid("gemm: dimension too large");
-    if ((N + 4) * K * 2 >= (int64_t{1} << 32) || M * ldx * 2 >= (int64_t{1} << 32))
+    if ((N + 4) * K * 2 >= (int64_t{1} << 32) || std::min<int64_t>(M, 16) * ldx * 2 >= (int64_t{1} << 32))
         return invalid("gemm: W or X exceeds the 4 GiB buffer-offset range");
     if (!aligned16(x) || !aligned16(w)) return invalid("gemm: x and w must be 16-byte aligned");
     return HAI_OK;
@@ -858,9 +927,9 @@ extern "C" int hai_gemm_rmsnorm_bf16(void* y, int64_t ldy, const void* x, int64_
     if (!aligned16(norm_w)) return invalid("gemm_rmsnorm: norm weight must be 16-byte aligned");
     if (M == 0) return HAI_OK;
     const hipStream_t s = as_stream(stream);
-    if (M * K > kNormMaxElems) {
+    if (M * K > kNormMaxElems || M > 16) {
         // Rows too large for the LDS prologue: normalise into xn_out, then multiply.
-        if (xn_out == nullptr) return invalid("gemm_rmsnorm: M*K above the fused limit needs xn_out");
+        if (xn_out == nullptr) return invalid("gemm_rmsnorm: M > 16 or M*K above the fused limit needs xn_out");
         const int r = hai_rmsnorm_bf16(xn_out, ld_xn, x, ldx, norm_w, M, K, eps, unit_offset, stream);
         if (r != HAI_OK) return r;
         return hai_gemm_bf16(y, ldy, xn_out, ld_xn, w, M, N, K, epilogue, res, ld_res, stream);

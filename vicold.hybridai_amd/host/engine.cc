@@ -614,19 +614,18 @@ int Engine::gemm(uint16_t* y, int64_t ldy, const uint16_t* x, int64_t ldx, const
         }
         return HAI_OK;
     }
-    // the skinny kernels take 16 rows per launch; rows are independent, so
-    // the split does not change a bit
+    // bf16 weights: one launch for any M (16-row batches inside it);
+    // the FP8 skinny kernel takes 16 rows per launch.  Rows are
+    // independent, so neither split changes a bit.
+    if (w.q == nullptr) return hai_gemm_bf16(y, ldy, x, ldx, w.w, M, N, K, epi, res, ldres, stream_);
     for (int64_t m0 = 0; m0 < M; m0 += 16) {
         const int64_t mm = std::min<int64_t>(16, M - m0);
         uint16_t* ym = y + m0 * ldy;
         const uint16_t* xm = x + m0 * ldx;
         const uint16_t* rm = res ? res + m0 * ldres : nullptr;
         // the engine's codes come from the saturating quantiser: never 0x7F / 0xFF
-        if (w.q != nullptr)
-            HAI_TRY(hai_gemm_fp8_bf16(ym, ldy, xm, ldx, w.q, w.s, w.map, mm, N, K, epi | HAI_FP8_NO_SPECIAL_CODES, rm,
-                                      ldres, stream_));
-        else
-            HAI_TRY(hai_gemm_bf16(ym, ldy, xm, ldx, w.w, mm, N, K, epi, rm, ldres, stream_));
+        HAI_TRY(hai_gemm_fp8_bf16(ym, ldy, xm, ldx, w.q, w.s, w.map, mm, N, K, epi | HAI_FP8_NO_SPECIAL_CODES, rm,
+                                  ldres, stream_));
     }
     return HAI_OK;
 }
