@@ -251,8 +251,9 @@ int hai_append_kv_bf16(void* k_cache, void* v_cache, int64_t cap,
  * cache of sequence b holds L_b = (lens ? lens[b] : 0) + len_add rows
  * including the T new ones; query t attends keys 0..L_b-T+t.  q/gate/out
  * are [B*T][nq][D]; gate may be NULL.  scratch must hold
- * hai_gqa_scratch_bytes(B, T, nq, D, max_len) bytes; max_len bounds every
- * L_b and sizes the launch. */
+ * hai_gqa_scratch_bytes(B, T, nq, D, max_len) bytes (SIZE_MAX when the size
+ * overflows or an argument is negative); max_len bounds every L_b and sizes
+ * the launch. */
 size_t hai_gqa_scratch_bytes(int64_t B, int64_t T, int64_t nq, int64_t D,
                              int64_t max_len);
 int hai_gqa_verify_bf16(void* out, const void* q, const void* gate,

@@ -39,7 +39,9 @@ def test_argument_checks_need_no_device():
     k = hai.kernels()
     p = ctypes.c_void_p(16)  # never dereferenced: every call below fails its host-side checks
     assert k.hai_gemm_bf16(p, 4, p, 12, p, 2, 4, 12, 0, None, 0, None) == hai.ERR_INVALID  # K % 8
-    assert k.hai_gemm_bf16(p, 4, p, 8, p, 17, 4, 8, 0, None, 0, None) == hai.ERR_INVALID   # M > 16
+    assert k.hai_gemm_bf16(p, 4, p, 8, p, -1, 4, 8, 0, None, 0, None) == hai.ERR_INVALID   # M < 0
+    assert k.hai_gemm_rmsnorm_bf16(p, 8, p, 8, p, 1e-6, 1, None, 0, p, 17, 8, 8, 0, None, 0,
+                                   None) == hai.ERR_INVALID  # more than 16 rows without xn_out
     assert k.hai_gemm_bf16(None, 4, p, 8, p, 1, 4, 8, 0, None, 0, None) == hai.ERR_INVALID
     assert k.hai_gemm_rmsnorm_bf16(p, 8, p, 5120, p, 1e-6, 1, None, 0, p, 4, 8, 5120, 0, None, 0,
                                    None) == hai.ERR_INVALID  # above the fused limit without xn_out
@@ -47,3 +49,22 @@ def test_argument_checks_need_no_device():
                                       128, 128, 4, 1e-6, None) == hai.ERR_INVALID  # T > 16
     assert k.hai_gqa_verify_bf16(p, p, p, p, p, 8, p, 1, 4, 4, 3, 64, None, 4, 8, None) == hai.ERR_INVALID
     assert b"gqa_verify" in k.hai_last_error()
+
+
+def test_noalloc_attention_bounds_its_shape_before_sizing():
+    """hai_gqa_verify_noalloc_bf16 checks every operand of the scratch size
+    before computing it: a batch past int32, a bad head_dim or nkv, or a
+    size above the fixed 16 MiB array is refused on the host, before the
+    device array is looked up; the size function reports overflow as
+    SIZE_MAX instead of wrapping."""
+    k = hai.kernels()
+    p = ctypes.c_void_p(16)  # never dereferenced
+    big = 1 << 40
+    for B, nkv, D, what in ((big, 4, 256, b"shape"), (1, 0, 256, b"shape"), (1, 4, 100, b"head_dim"),
+                            (100000, 4, 256, b"16 MiB")):
+        assert k.hai_gqa_verify_noalloc_bf16(p, p, p, p, p, 4096, B, 2, 24, nkv, D, None, 2, 4096,
+                                             None) == hai.ERR_INVALID, (B, nkv, D)
+        assert what in k.hai_last_error(), k.hai_last_error()
+    assert k.hai_gqa_scratch_bytes(big, big, 24, 256, 4096) == 2 ** 64 - 1
+    # 2 rows x 24 heads x 64 chunks of 64 keys x (256 + 2) floats
+    assert k.hai_gqa_scratch_bytes(1, 2, 24, 256, 4096) == 2 * 24 * 64 * 258 * 4

@@ -163,6 +163,30 @@ def test_mixed_dense_and_fp8_linears_are_refused(E, tiny_dir, tmp_path):
     assert code_of(E, tmp_path, True) == UNSUPPORTED_DTYPE
 
 
+def test_dense_tensors_must_hold_bf16_values(E, tiny_dir, tmp_path):
+    """The non-Linear tensors are stored as BF16, the dtype the reference's
+    GPU ops take them in (delta_net.cc:477-478): an F16 A_log, or an F32
+    A_log whose values are not bf16 numbers, is refused before any device
+    work with UNSUPPORTED_DTYPE and the tensor's name; F32 holding bf16
+    values loads as before."""
+    from safetensors.torch import load_file
+    t = load_file(str(tiny_dir / "model.safetensors"))
+    name = "model.language_model.layers.0.linear_attn.A_log"
+    base = t[name].float()
+    cases = (("f16", base.to(torch.float16), UNSUPPORTED_DTYPE, "is F16"),
+             ("f32_off", (base.double() * (1 + 2.0 ** -10) + 2.0 ** -20).float(), UNSUPPORTED_DTYPE,
+              "not bf16 numbers"),
+             ("f32_exact", base, 0, ""))
+    for tag, value, want, text in cases:
+        d = write_config(tmp_path / tag)
+        save_file(dict(t, **{name: value.contiguous()}), str(d / "model.safetensors"))
+        assert code_of(E, d, True) == want, tag
+        if want:
+            with pytest.raises(E.CheckpointError, match=text) as ei:
+                E.model_config_load(d, True)
+            assert name in str(ei.value)
+
+
 def with_metadata_text(src, dst, text_json_literal):
     """Copy of a safetensors file whose header gains
     "__metadata__": {"note": <literal>} (the literal written as given)."""

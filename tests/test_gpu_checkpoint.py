@@ -97,12 +97,16 @@ def test_format_mismatch_and_bf16_scales(dirs, tmp_path):
         eng.close()
 
 
+def _generator_run(model_dir, mode, prompt, max_new, width=1, layout="plain", **env_extra):
+    subprocess.run(["make", "-s", "-C", str(ROOT / "tests" / "backend")], check=True, capture_output=True)
+    env = dict(os.environ, HYBRIDAI_SPECULATIVE_WIDTH=str(width), **env_extra)
+    return subprocess.run([str(ROOT / "tests" / "backend" / "_build" / "generator_run"), str(model_dir), mode, prompt,
+                           str(max_new), layout], capture_output=True, text=True, timeout=300, env=env)
+
+
 def _generator(model_dir, mode, prompt, max_new, width=1, layout="plain"):
     """(tokens, stats, text) of hybridai::Generator through tests/backend/generator_run."""
-    subprocess.run(["make", "-s", "-C", str(ROOT / "tests" / "backend")], check=True, capture_output=True)
-    env = dict(os.environ, HYBRIDAI_SPECULATIVE_WIDTH=str(width))
-    r = subprocess.run([str(ROOT / "tests" / "backend" / "_build" / "generator_run"), str(model_dir), mode, prompt,
-                        str(max_new), layout], capture_output=True, text=True, timeout=300, env=env)
+    r = _generator_run(model_dir, mode, prompt, max_new, width, layout)
     assert r.returncode == 0, r.stdout + r.stderr
     lines = dict(line.split(" ", 1) for line in r.stdout.strip().splitlines())
     stats = dict(kv.split("=") for kv in lines["stats"].split())
@@ -153,3 +157,18 @@ def test_generator_stop_ids_from_config_and_generation_config(tmp_path):
         assert _generator(d, mode, TEXT, NEW)[0] == g[:g.index(b) + 1]
     d = ckpt.write_tiny_checkpoint(tmp_path / "eos2", eos=a, generation_eos=orc.TINY["vocab"] - 2)
     assert _generator(d, "spec", TEXT, NEW)[0] == g[:g.index(a) + 1]
+
+
+def test_generator_context_bound_is_max_position_embeddings(dirs):
+    """A checkpoint engine takes prompt + max_new_tokens up to
+    max_position_embeddings (4096 in the test config), with the reference's
+    check and message (generator.cc:481-485); HYBRIDAI_MAX_CONTEXT caps the
+    positions (the KV memory) and a request above the cap names it."""
+    d = dirs["bf16"]
+    n = len(tok.hf(d).encode(TEXT).ids)
+    r = _generator_run(d, "greedy", TEXT, 4097 - n)
+    assert r.returncode == 1 and "generate failed" in r.stdout and "prompt exceeds model context" in r.stdout, r.stdout
+    r = _generator_run(d, "spec", TEXT, 64 - n, width=3, HYBRIDAI_MAX_CONTEXT="64")
+    assert r.returncode == 0, r.stdout + r.stderr
+    r = _generator_run(d, "spec", TEXT, 65 - n, width=3, HYBRIDAI_MAX_CONTEXT="64")
+    assert r.returncode == 1 and "exceed HYBRIDAI_MAX_CONTEXT (64 positions)" in r.stdout, r.stdout

@@ -22,6 +22,8 @@
 // on T, on the batch or on how many blocks run: verify rows and replayed
 // rows are bit-identical, and the CPU oracle follows the same order.
 #include <atomic>
+#include <cstdint>
+#include <initializer_list>
 #include <mutex>
 #include <string>
 
@@ -885,6 +887,15 @@ constexpr int kMaxNoAllocDevices = 64;
 std::atomic<float*> g_noalloc_ptr[kMaxNoAllocDevices];
 std::mutex g_noalloc_mu;
 
+// The product of the factors as a byte count, or SIZE_MAX when a factor is
+// negative or the product overflows.
+size_t checked_product(std::initializer_list<int64_t> factors) {
+    uint64_t p = 1;
+    for (const int64_t v : factors)
+        if (v < 0 || __builtin_mul_overflow(p, static_cast<uint64_t>(v), &p)) return SIZE_MAX;
+    return static_cast<size_t>(p);
+}
+
 int noalloc_scratch(float** out) {
     int dev = 0;
     int rc = check_hip(hipGetDevice(&dev), "hipGetDevice");
@@ -913,7 +924,11 @@ extern "C" {
 int hai_gqa_verify_noalloc_bf16(void* out, const void* q, const void* gate, const void* k_cache,
                                 const void* v_cache, int64_t cap, int64_t B, int64_t T, int64_t nq, int64_t nkv,
                                 int64_t D, const int32_t* lens, int32_t len_add, int64_t max_len, void* stream) {
-    if (B < 0 || T < 0 || nq <= 0 || max_len <= 0) return invalid("gqa_verify_noalloc: shape");
+    // every operand of the size bounded before the size is computed
+    if (B < 0 || T < 0 || nq <= 0 || nkv <= 0 || max_len <= 0 || B > INT32_MAX || T > INT32_MAX ||
+        nq > INT32_MAX || max_len > INT32_MAX)
+        return invalid("gqa_verify_noalloc: shape");
+    if (D != 64 && D != 128 && D != 256) return invalid("gqa_verify_noalloc: head_dim must be 64, 128 or 256");
     const size_t need = hai_gqa_scratch_bytes(B, T, nq, D, max_len);
     if (need > kGqaNoAllocScratchBytes)
         return invalid(("gqa_verify_noalloc: the partials need " + std::to_string(need) +
@@ -927,9 +942,9 @@ int hai_gqa_verify_noalloc_bf16(void* out, const void* q, const void* gate, cons
 }
 
 size_t hai_gqa_scratch_bytes(int64_t B, int64_t T, int64_t nq, int64_t D, int64_t max_len) {
+    if (D < 0 || D > INT32_MAX || max_len < 0) return SIZE_MAX;
     const int64_t nchunk = (max_len + kChunk - 1) / kChunk;
-    return static_cast<size_t>(B * T * nq * (nchunk < 1 ? 1 : nchunk) * partial_stride(int(D))) *
-           sizeof(float);
+    return checked_product({B, T, nq, nchunk < 1 ? 1 : nchunk, partial_stride(int(D)), int64_t{sizeof(float)}});
 }
 
 int hai_gqa_verify_bf16(void* out, const void* q, const void* gate, const void* k_cache,
@@ -939,7 +954,7 @@ int hai_gqa_verify_bf16(void* out, const void* q, const void* gate, const void* 
     if (out == nullptr || q == nullptr || k_cache == nullptr || v_cache == nullptr || scratch == nullptr)
         return invalid("gqa_verify: null pointer");
     if (B < 0 || T < 0 || nq <= 0 || nkv <= 0 || nq % nkv != 0 || cap <= 0 || max_len <= 0 ||
-        max_len > cap || T > max_len)
+        max_len > cap || T > max_len || B > INT32_MAX || nq > INT32_MAX || max_len > INT32_MAX)
         return invalid("gqa_verify: shape");
     if (lens == nullptr && (len_add < T || len_add > max_len))
         return invalid("gqa_verify: cache length must cover the T new rows and stay within max_len");

@@ -3,6 +3,7 @@
 
 #include <sys/stat.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <fstream>
@@ -453,6 +454,46 @@ int detect_weight_format(const SafeTensors& st, const hai_model_config& cfg, int
     if (dense > 0 && fp8 > 0)
         return fail(err, HAI_ERR_NOT_IMPLEMENTED,
                     "checkpoint mixes dense BF16 and FP8 Linears; this engine stores them all one way");
+    // The other tensors (embedding, norms, conv, A_log, dt_bias, in_proj_a|b,
+    // lm_head, the MTP fc) are stored as BF16, the dtype the reference's GPU
+    // ops take them in (delta_net.cc:477-478 requires a_log and dt_bias in
+    // the activations' dtype): BF16, or F32 whose every value is a bf16
+    // number.  Small F32 tensors are checked here; the engine checks the
+    // large ones as it loads them.
+    auto dense_ok = [&](const std::string& name) -> int {
+        const StTensor* t = st.find(name);
+        if (t == nullptr || t->dtype == StDType::BF16) return HAI_OK;  // a missing one is the load's error
+        if (t->dtype != StDType::F32)
+            return fail(err, HAI_ERR_UNSUPPORTED_DTYPE,
+                        "Qwen weight " + name + " is " + st_dtype_name(t->dtype) +
+                            "; this engine stores it as BF16 (BF16, or F32 holding bf16 values)");
+        if (t->numel() > (int64_t{1} << 20)) return HAI_OK;
+        std::vector<float> f(static_cast<size_t>(t->numel()));
+        if (const int rc = st.read(*t, f.data(), err); rc != HAI_OK) return rc;
+        uint16_t bits = 0;
+        for (float v : f)
+            if (!exact_bf16(v, &bits))
+                return fail(err, HAI_ERR_UNSUPPORTED_DTYPE,
+                            "Qwen weight " + name + " is F32 with values that are not bf16 numbers; this engine "
+                                                    "stores it as BF16");
+        return HAI_OK;
+    };
+    static const uint32_t kLinearKinds[] = {2, 3, 10, 11, 12, 13, 14, 17, 18, 19};  // checked above
+    std::vector<uint32_t> slots = {kSlotShared};
+    for (int32_t i = 0; i < cfg.num_layers; ++i) slots.push_back(kSlotLayer0 + static_cast<uint32_t>(i));
+    if (cfg.mtp_layers > 0) {
+        slots.push_back(kSlotMtpShared);
+        slots.push_back(kSlotMtpLayer0);
+    }
+    for (uint32_t slot : slots)
+        for (uint32_t kind = 0; kind < 64; ++kind) {
+            const bool layer = slot >= kSlotLayer0;
+            if (layer && std::find(std::begin(kLinearKinds), std::end(kLinearKinds), kind) != std::end(kLinearKinds))
+                continue;
+            const std::string name = checkpoint_name(slot * 64u + kind);
+            if (name.empty()) continue;
+            if (const int rc = dense_ok(name); rc != HAI_OK) return rc;
+        }
     *format = fp8 > 0 ? HAI_WEIGHTS_FP8_BLOCK128 : HAI_WEIGHTS_BF16;
     return HAI_OK;
 }

@@ -102,6 +102,19 @@ int64_t speculative_width_from_env() {
     return static_cast<int64_t>(n);
 }
 
+// Positions a checkpoint engine accepts (prompt + max_new_tokens):
+// max_position_embeddings, the bound of generator.cc:481-485, unless
+// HYBRIDAI_MAX_CONTEXT (a positive integer) caps it to bound the KV memory
+// (64 KiB per position at the 27B shape).  0: not set or not a number.
+int64_t max_context_from_env() {
+    const char* v = std::getenv("HYBRIDAI_MAX_CONTEXT");
+    if (v == nullptr || v[0] == '\0') return 0;
+    char* end = nullptr;
+    const long long n = std::strtoll(v, &end, 10);
+    if (end == v || *end != '\0' || n <= 0) return 0;
+    return static_cast<int64_t>(n);
+}
+
 }  // namespace
 
 class Generator::Impl {
@@ -158,13 +171,15 @@ public:
             return {api_code(rc), "synthetic weights: " + why};
         }
         context_ = context;
+        position_limit_ = 0;
+        limit_capped_ = false;
         return {};
     }
 
     // generator.cc:390-431 for a Qwen checkpoint directory: config.json,
     // the weights (the MTP layer's when enable_mtp), the EOS ids of the
-    // config; the engine's KV capacity is the smaller of
-    // max_position_embeddings and 32768 positions.
+    // config; the engine holds max_position_embeddings positions (or
+    // HYBRIDAI_MAX_CONTEXT, when that is smaller) plus the verify rows.
     ApiStatus load_checkpoint_dir(const std::string& dir) {
         struct stat sb{};
         if (dir.empty() || stat(dir.c_str(), &sb) != 0 || !S_ISDIR(sb.st_mode))
@@ -183,8 +198,12 @@ public:
             return {ApiStatusCode::InvalidModel, "Checkpoint does not contain Qwen MTP layers"};
         if (cfg_.mtp_layers > 1)
             return {ApiStatusCode::NotImplemented, "checkpoints with more than one MTP layer are not supported"};
+        const int64_t env_cap = max_context_from_env();
+        const int64_t limit = env_cap > 0 ? std::min(max_pos, env_cap) : max_pos;
+        if (limit <= 0 || limit > INT32_MAX - mi355x::kMaxVerifyRows)
+            return {ApiStatusCode::InvalidModel, "max_position_embeddings out of range"};
         hai_engine_options eo{};
-        eo.max_context = static_cast<int32_t>(std::min<int64_t>(max_pos, 32768));
+        eo.max_context = static_cast<int32_t>(limit + mi355x::kMaxVerifyRows);
         eo.max_verify_tokens = static_cast<int32_t>(mi355x::kMaxVerifyRows);
         eo.device = 0;
         eo.use_graphs = 0;
@@ -213,6 +232,8 @@ public:
         std::sort(eos_.begin(), eos_.end());
         eos_.erase(std::unique(eos_.begin(), eos_.end()), eos_.end());
         context_ = eo.max_context;
+        position_limit_ = limit;
+        limit_capped_ = limit < max_pos;
         mtp_loaded_ = options_.enable_mtp;
         return {};
     }
@@ -242,8 +263,17 @@ public:
         }
         for (int32_t id : prompt)
             if (id >= cfg_.vocab) return {ApiStatusCode::InvalidArgument, "prompt id outside the vocabulary"};
-        if (static_cast<int64_t>(prompt.size()) + o.max_new_tokens + mi355x::kMaxVerifyRows > context_)
+        const int64_t positions = static_cast<int64_t>(prompt.size()) + o.max_new_tokens;
+        if (position_limit_ > 0) {
+            // a checkpoint: the reference's bound and message (generator.cc:481-485)
+            if (positions > position_limit_)
+                return {ApiStatusCode::InvalidArgument,
+                        limit_capped_ ? "prompt + max_new_tokens exceed HYBRIDAI_MAX_CONTEXT (" +
+                                            std::to_string(position_limit_) + " positions)"
+                                      : std::string("prompt exceeds model context")};
+        } else if (positions + mi355x::kMaxVerifyRows > context_) {
             return {ApiStatusCode::InvalidArgument, "prompt + max_new_tokens exceed the model context"};
+        }
         *result = GenerationResult{};
         std::vector<int32_t> out(static_cast<size_t>(std::max(1, o.max_new_tokens)));
         int64_t n = 0;
@@ -307,6 +337,8 @@ private:
     GeneratorOptions options_;
     hai_model_config cfg_{};
     int32_t context_ = 0;
+    int64_t position_limit_ = 0;  // checkpoints: prompt + max_new_tokens bound (0 for synthetic models)
+    bool limit_capped_ = false;   // position_limit_ comes from HYBRIDAI_MAX_CONTEXT
     bool mtp_loaded_ = true;     // synthetic models always carry their MTP layer
     std::vector<int32_t> eos_;   // the checkpoint's stop ids (config and generation config)
     mi355x::QwenTokenizer tokenizer_;  // loaded for checkpoint directories only
