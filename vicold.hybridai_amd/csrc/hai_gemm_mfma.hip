@@ -30,6 +30,7 @@
 //     interleaved (gate_f, up_f) rows.
 #include <atomic>
 #include <cstdlib>
+#include <type_traits>
 
 #include "hai_common.h"
 #include "hai_device.h"
@@ -41,6 +42,7 @@ using namespace hai;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kMaxMfmaRows = 128;
 constexpr int kChunk = 256;           // k elements per chunk
@@ -49,6 +51,14 @@ constexpr int kBlockRows = 64;        // weight rows per block
 
 __device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+}
+// 32 x 32 x 16: lane l holds A row l % 32 (B column l % 32), k 8 (l / 32) .. +7;
+// result element r of lane l is row 8 (r / 4) + 4 (l / 32) + r % 4, column
+// l % 32.  On MI355X this form issues at 2.1-2.2 PFLOP/s against 0.8-1.3
+// for the 16 x 16 x 32 one (register-operand probe, 1-4 blocks per CU).
+__device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
                                                    0, 0, 0);
 }
 
@@ -1584,19 +1594,22 @@ extern "C" int hai_gemm_fp8_mfma(void* y, int64_t ldy, const void* x, int64_t ld
 // The weight-streaming kernel above re-reads every weight once per 128 rows;
 // here both operands are tiled and the layer is compute bound.
 //   * block = 4 waves, output tile 128 rows of X x BN rows of W (BN = 128, or
-//     64 when the 128-wide grid would not give every CU two tiles); wave
-//     (wm, wn) owns 64 x BN/2 outputs, 4 x BN/32 tiles of the 16x16x32 bf16
-//     MFMA with fp32 accumulators;
+//     64 when 128-wide tiles would leave CUs without one); wave (wm, wn) owns
+//     64 x BN/2 outputs as 32 x 32 tiles of v_mfma_f32_32x32x16_bf16 (on
+//     MI355X this form issues at twice the rate of the 16 x 16 x 32 one)
+//     with fp32 accumulators;
 //   * K in steps of 64: both operand tiles staged in LDS (two buffers, rows
-//     padded by 16 bytes), the next step's global loads in flight in
-//     registers while the current step is multiplied, one barrier per step;
+//     padded by 16 bytes), a step's global loads requested two steps ahead
+//     into registers, and the next step's pieces written to the other buffer
+//     between the current step's k-slices of MFMAs; one barrier per step;
 //   * FP8 weights: codes decoded exactly to bf16 as they are staged, each
 //     128-k scale block summed on its own and scaled in fp32 (the arithmetic
 //     of hai_gemm_fp8_mfma);
 //   * workgroups are dispatched to the 8 XCDs in turn, so block b is given
-//     tile base(b % 8) + b / 8: every XCD takes a contiguous range of tiles
-//     in weight-panel order, and the row tiles sharing a weight panel run on
-//     one XCD together and fetch it into that XCD's L2 once;
+//     tile base(b % 8) + b / 8: every XCD takes a contiguous range of the tile
+//     order, which runs in groups of 4 row tiles with the weight panels
+//     sweeping inside a group, so the blocks resident on one XCD share a few
+//     row tiles and weight panels in its L2;
 //   * the epilogues of the other GEMMs (store, residual add, SwiGLU over
 //     interleaved gate / up rows).
 // Tolerance mode, as the other matrix-core GEMMs.
@@ -1621,22 +1634,26 @@ struct TiledArgs {
     int64_t ldres;
     int M, N, K;
     int mtiles, ntiles;
+    int group_m;  // tile order: groups of group_m row tiles (0: panel by panel)
 };
 
-template <int WN>
+// WM / WN: 16-row MFMA tiles per wave along X rows / weight rows; block =
+// 2 x 2 waves, output tile (32 WM) x (32 WN).
+template <int WM, int WN>
 __host__ __device__ constexpr size_t tiled_lds_bytes() {
-    return static_cast<size_t>(2) * (kTileM + 32 * WN) * kTileRow * 2;
+    return static_cast<size_t>(2) * (32 * WM + 32 * WN) * kTileRow * 2;
 }
 
-template <int WN, int EPI, bool FP8, bool CHECK>
+template <int WM, int WN, int EPI, bool FP8, bool CHECK, bool M32, int PIPE>
 __global__ __launch_bounds__(256) void gemm_tiled_kernel(TiledArgs a) {
+    constexpr int BM = 32 * WM;
     constexpr int BN = 32 * WN;
-    constexpr int XP = kTileM * kTileK / 8 / 256;             // 16-byte X pieces per thread
+    constexpr int XP = BM * kTileK / 8 / 256;                 // 16-byte X pieces per thread
     constexpr int WP = FP8 ? BN * kTileK / 16 / 256 : BN * kTileK / 8 / 256;  // W pieces per thread
     static_assert(XP >= 1 && WP >= 1, "tile must split over the block");
     extern __shared__ __align__(16) uint16_t lds[];
-    uint16_t* xs = lds;                          // [2][kTileM][kTileRow]
-    uint16_t* ws = lds + 2 * kTileM * kTileRow;  // [2][BN][kTileRow]
+    uint16_t* xs = lds;                      // [2][BM][kTileRow]
+    uint16_t* ws = lds + 2 * BM * kTileRow;  // [2][BN][kTileRow]
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = wave_index();
@@ -1645,14 +1662,29 @@ __global__ __launch_bounds__(256) void gemm_tiled_kernel(TiledArgs a) {
     const int wm = wave >> 1;
     const int wn = wave & 1;
 
-    // XCD-aware tile of this block (tiles in weight-panel order, row tiles fastest)
+    // XCD-aware tile of this block: each XCD takes a contiguous range of the
+    // tile order; GM > 0 orders the tiles in groups of GM row tiles, the
+    // weight panels sweeping inside a group (row tiles fastest), so the
+    // blocks resident on an XCD cover about GM row tiles x (blocks / GM)
+    // panels; GM = 0: all row tiles of a panel, then the next panel.
     const int nb = static_cast<int>(gridDim.x);
     const int bid = static_cast<int>(blockIdx.x);
     const int xcd = bid % kXcds;
     const int tile = xcd * (nb / kXcds) + min(xcd, nb % kXcds) + bid / kXcds;
-    const int tm = tile % a.mtiles;
-    const int tn = tile / a.mtiles;
-    const int64_t m0 = static_cast<int64_t>(tm) * kTileM;
+    int tm, tn;
+    if (a.group_m > 0) {
+        const int per_group = a.group_m * a.ntiles;
+        const int g = tile / per_group;
+        const int first = g * a.group_m;
+        const int gsize = min(a.mtiles - first, a.group_m);
+        const int r = tile - g * per_group;
+        tm = first + r % gsize;
+        tn = r / gsize;
+    } else {
+        tm = tile % a.mtiles;
+        tn = tile / a.mtiles;
+    }
+    const int64_t m0 = static_cast<int64_t>(tm) * BM;
     const int64_t n0 = static_cast<int64_t>(tn) * BN;
     const int M = a.M, N = a.N, K = a.K;
 
@@ -1694,8 +1726,27 @@ __global__ __launch_bounds__(256) void gemm_tiled_kernel(TiledArgs a) {
 #pragma unroll
         for (int i = 0; i < WP; ++i) wv[i] = bload(rw, woff[i], FP8 ? k0 : k0 * 2);
     };
+    // one staged piece: X pieces 0 .. XP-1, then W pieces
+    auto stage_piece = [&](const u32x4 (&xv)[XP], const u32x4 (&wv)[WP], int buf, int p) {
+        uint16_t* xb = xs + buf * BM * kTileRow;
+        uint16_t* wb = ws + buf * BN * kTileRow;
+        if (p < XP) {
+            *reinterpret_cast<u32x4*>(xb + xdst[p]) = xv[p];
+            return;
+        }
+        const int i = p - XP;
+        if constexpr (FP8) {
+            uint32_t d[8];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) e4m3x4_to_bf16<CHECK>(wv[i][q], d[2 * q], d[2 * q + 1]);
+            *reinterpret_cast<u32x4*>(wb + wdst[i]) = u32x4{d[0], d[1], d[2], d[3]};
+            *reinterpret_cast<u32x4*>(wb + wdst[i] + 8) = u32x4{d[4], d[5], d[6], d[7]};
+        } else {
+            *reinterpret_cast<u32x4*>(wb + wdst[i]) = wv[i];
+        }
+    };
     auto stage = [&](const u32x4 (&xv)[XP], const u32x4 (&wv)[WP], int buf) {
-        uint16_t* xb = xs + buf * kTileM * kTileRow;
+        uint16_t* xb = xs + buf * BM * kTileRow;
         uint16_t* wb = ws + buf * BN * kTileRow;
 #pragma unroll
         for (int i = 0; i < XP; ++i) *reinterpret_cast<u32x4*>(xb + xdst[i]) = xv[i];
@@ -1713,61 +1764,104 @@ __global__ __launch_bounds__(256) void gemm_tiled_kernel(TiledArgs a) {
         }
     };
 
+    // MFMA tiles per wave: 16 x 16 (WM x WN of them) or 32 x 32 (M32: half
+    // as many each way); lane (li, kg) of a 16-tile, column lc of a 32-tile
+    constexpr int TM = M32 ? WM / 2 : WM;
+    constexpr int TN = M32 ? WN / 2 : WN;
+    constexpr int TS = M32 ? 32 : 16;
+    using Acc = typename std::conditional<M32, f32x16, f32x4>::type;
+    constexpr int AE = M32 ? 16 : 4;  // accumulator elements per lane and tile
+    const int lc = lane & 31;
+    const int lh = lane >> 5;
+    const int colx = M32 ? lc : li;   // the lane's column within a tile
+
     // FP8: the scale row of each of the lane's output columns
     const int nkb = (K + 127) / 128;
-    const float* srow[WN];
+    const float* srow[TN];
     if constexpr (FP8) {
         const int64_t nsb = ((N >> 1) + 127) / 128;
 #pragma unroll
-        for (int ni = 0; ni < WN; ++ni) {
-            const int64_t n = min(n0 + wn * 16 * WN + ni * 16 + li, static_cast<int64_t>(N) - 1);
+        for (int ni = 0; ni < TN; ++ni) {
+            const int64_t n = min(n0 + wn * 16 * WN + ni * TS + colx, static_cast<int64_t>(N) - 1);
             const int64_t sr = a.scale_rows ? a.scale_rows[n] : (a.paired ? (n & 1) * nsb + (n >> 1) / 128 : n / 128);
             srow[ni] = a.scales + sr * nkb;
         }
     }
 
-    f32x4 acc[4][WN];   // the current 128-k scale block (FP8) or the whole sum (bf16)
-    f32x4 tot[4][WN];   // FP8: the scaled sum of the finished blocks
+    Acc acc[TM][TN];   // the current 128-k scale block (FP8) or the whole sum (bf16)
+    Acc tot[TM][TN];   // FP8: the scaled sum of the finished blocks
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi)
+    for (int mi = 0; mi < TM; ++mi)
 #pragma unroll
-        for (int ni = 0; ni < WN; ++ni) {
-            acc[mi][ni] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            tot[mi][ni] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        }
+        for (int ni = 0; ni < TN; ++ni)
+#pragma unroll
+            for (int e = 0; e < AE; ++e) {
+                acc[mi][ni][e] = 0.0f;
+                tot[mi][ni][e] = 0.0f;
+            }
 
     const int nsteps = K / kTileK;
-    auto compute = [&](int step) {
+    constexpr int NP = XP + WP;  // staged pieces per thread and step
+    // PIPE 1: the next step's pieces (xn, wnx) are written to the other
+    // buffer (nbuf) between the k-slices' MFMAs, not after all of them
+    auto compute = [&](int step, const u32x4 (*xn)[XP], const u32x4 (*wnx)[WP], int nbuf) {
         const int buf = step & 1;
-        const uint16_t* xb = xs + buf * kTileM * kTileRow;
+        const uint16_t* xb = xs + buf * BM * kTileRow;
         const uint16_t* wb = ws + buf * BN * kTileRow;
+        if constexpr (M32) {
 #pragma unroll
-        for (int j = 0; j < kTileK / 32; ++j) {
-            u32x4 af[4], bf[WN];
+            for (int j = 0; j < kTileK / 16; ++j) {
+                u32x4 af[TM], bf[TN];
 #pragma unroll
-            for (int mi = 0; mi < 4; ++mi)
-                af[mi] = *reinterpret_cast<const u32x4*>(xb + (wm * 64 + mi * 16 + li) * kTileRow + 32 * j + 8 * kg);
+                for (int mi = 0; mi < TM; ++mi)
+                    af[mi] = *reinterpret_cast<const u32x4*>(xb + (wm * 16 * WM + mi * 32 + lc) * kTileRow + 16 * j +
+                                                             8 * lh);
 #pragma unroll
-            for (int ni = 0; ni < WN; ++ni)
-                bf[ni] = *reinterpret_cast<const u32x4*>(wb + (wn * 16 * WN + ni * 16 + li) * kTileRow + 32 * j + 8 * kg);
+                for (int ni = 0; ni < TN; ++ni)
+                    bf[ni] = *reinterpret_cast<const u32x4*>(wb + (wn * 16 * WN + ni * 32 + lc) * kTileRow + 16 * j +
+                                                             8 * lh);
 #pragma unroll
-            for (int mi = 0; mi < 4; ++mi)
+                for (int mi = 0; mi < TM; ++mi)
 #pragma unroll
-                for (int ni = 0; ni < WN; ++ni) acc[mi][ni] = mfma16(af[mi], bf[ni], acc[mi][ni]);
+                    for (int ni = 0; ni < TN; ++ni) acc[mi][ni] = mfma32(af[mi], bf[ni], acc[mi][ni]);
+                if constexpr (PIPE == 1) {
+                    constexpr int NS = kTileK / 16;
+#pragma unroll
+                    for (int p = j * NP / NS; p < (j + 1) * NP / NS; ++p) stage_piece(*xn, *wnx, nbuf, p);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < kTileK / 32; ++j) {
+                u32x4 af[TM], bf[TN];
+#pragma unroll
+                for (int mi = 0; mi < TM; ++mi)
+                    af[mi] = *reinterpret_cast<const u32x4*>(xb + (wm * 16 * WM + mi * 16 + li) * kTileRow + 32 * j +
+                                                             8 * kg);
+#pragma unroll
+                for (int ni = 0; ni < TN; ++ni)
+                    bf[ni] = *reinterpret_cast<const u32x4*>(wb + (wn * 16 * WN + ni * 16 + li) * kTileRow + 32 * j +
+                                                             8 * kg);
+#pragma unroll
+                for (int mi = 0; mi < TM; ++mi)
+#pragma unroll
+                    for (int ni = 0; ni < TN; ++ni) acc[mi][ni] = mfma16(af[mi], bf[ni], acc[mi][ni]);
+            }
         }
         if constexpr (FP8) {
             // a 128-k scale block ends every second step (and at the end of K)
             if ((step & 1) == 1 || step + 1 == nsteps) {
                 const int kb = step >> 1;
 #pragma unroll
-                for (int ni = 0; ni < WN; ++ni) {
+                for (int ni = 0; ni < TN; ++ni) {
                     const float sc = srow[ni][kb];
 #pragma unroll
-                    for (int mi = 0; mi < 4; ++mi) {
+                    for (int mi = 0; mi < TM; ++mi)
 #pragma unroll
-                        for (int i = 0; i < 4; ++i) tot[mi][ni][i] = fma_(sc, acc[mi][ni][i], tot[mi][ni][i]);
-                        acc[mi][ni] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-                    }
+                        for (int i = 0; i < AE; ++i) {
+                            tot[mi][ni][i] = fma_(sc, acc[mi][ni][i], tot[mi][ni][i]);
+                            acc[mi][ni][i] = 0.0f;
+                        }
                 }
             }
         }
@@ -1787,10 +1881,14 @@ __global__ __launch_bounds__(256) void gemm_tiled_kernel(TiledArgs a) {
         load(xl, wl, clamps(st + 2));
         pin_memory_order();
         __builtin_amdgcn_sched_barrier(0);
-        compute(st);
-        pin_memory_order();
-        __builtin_amdgcn_sched_barrier(0);
-        stage(xn, wn_, (st + 1) & 1);
+        if constexpr (PIPE == 1 && M32) {
+            compute(st, &xn, &wn_, (st + 1) & 1);
+        } else {
+            compute(st, nullptr, nullptr, 0);
+            pin_memory_order();
+            __builtin_amdgcn_sched_barrier(0);
+            stage(xn, wn_, (st + 1) & 1);
+        }
         lds_barrier();
     };
     int st = 0;
@@ -1800,23 +1898,35 @@ __global__ __launch_bounds__(256) void gemm_tiled_kernel(TiledArgs a) {
     }
     if (st < nsteps) step(st, xA, wA, xB, wB);
 
-    // lane (li, kg) holds rows 4 kg + i of each 16-row tile, column li of each 16-column tile
+    // 16-tiles: lane (li, kg) holds rows 4 kg + i, column li; 32-tiles:
+    // rows 8 (i / 4) + 4 lh + i % 4, column lc
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi)
+    for (int mi = 0; mi < TM; ++mi)
 #pragma unroll
-        for (int ni = 0; ni < WN; ++ni)
+        for (int ni = 0; ni < TN; ++ni)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int m = static_cast<int>(m0) + wm * 64 + mi * 16 + 4 * kg + i;
-                const int64_t n = n0 + wn * 16 * WN + ni * 16 + li;
-                mfma_store<EPI>(a.y, a.ldy, a.res, a.ldres, FP8 ? tot[mi][ni][i] : acc[mi][ni][i], m, n, M, N, li);
+            for (int i = 0; i < AE; ++i) {
+                const int r = M32 ? 8 * (i >> 2) + 4 * lh + (i & 3) : 4 * kg + i;
+                const int m = static_cast<int>(m0) + wm * 16 * WM + mi * TS + r;
+                const int64_t n = n0 + wn * 16 * WN + ni * TS + colx;
+                mfma_store<EPI>(a.y, a.ldy, a.res, a.ldres, FP8 ? tot[mi][ni][i] : acc[mi][ni][i], m, n, M, N, colx);
             }
 }
 
-template <int WN, int EPI, bool FP8, bool CHECK>
+// Row tiles per group of the tile order (HAI_TILED_GROUP, read once per
+// process, overrides the default of 4 for measurements; 0 = panel by panel).
+int tiled_group_m() {
+    static const int v = [] {
+        const char* e = std::getenv("HAI_TILED_GROUP");
+        return e == nullptr ? 4 : std::atoi(e);
+    }();
+    return v;
+}
+
+template <int WM, int WN, int EPI, bool FP8, bool CHECK, bool M32 = false, int PIPE = 0>
 int launch_tiled(TiledArgs a, hipStream_t s) {
-    constexpr size_t shmem = tiled_lds_bytes<WN>();
-    auto* kern = gemm_tiled_kernel<WN, EPI, FP8, CHECK>;
+    constexpr size_t shmem = tiled_lds_bytes<WM, WN>();
+    auto* kern = gemm_tiled_kernel<WM, WN, EPI, FP8, CHECK, M32, PIPE>;
     static std::atomic<uint8_t> allowed[64];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return invalid("gemm_tiled: device ordinal");
@@ -1826,18 +1936,47 @@ int launch_tiled(TiledArgs a, hipStream_t s) {
         if (rc != HAI_OK) return rc;
         allowed[dev].store(1, std::memory_order_release);
     }
+    a.mtiles = static_cast<int>((a.M + 32 * WM - 1) / (32 * WM));
     a.ntiles = static_cast<int>((a.N + 32 * WN - 1) / (32 * WN));
+    a.group_m = tiled_group_m();
     const int64_t blocks = static_cast<int64_t>(a.mtiles) * a.ntiles;
     kern<<<dim3(static_cast<unsigned>(blocks)), dim3(256), shmem, s>>>(a);
     return launched("gemm_tiled_kernel");
 }
 
+// HAI_TILED (read once per process) forces a tile form for measurements:
+// 1 = 128 x 64, 2 = 128 x 128 on 16 x 16 MFMAs, staged after the step's
+// MFMAs (the earlier kernel); 9 = 128 x 128, 10 = 128 x 64 on 32 x 32 MFMAs,
+// staged between them (the default forms).
+int tiled_force() {
+    static const int v = [] {
+        const char* e = std::getenv("HAI_TILED");
+        return e == nullptr ? 0 : std::atoi(e);
+    }();
+    return v;
+}
+
+// Measured on MI355X (bf16 / FP8 TFLOP/s, 27B prompt GEMMs at 1024 | 4096
+// rows; the earlier 16 x 16 kernel in brackets): in_proj 824 | 951 (672 |
+// 786), FP8 664 | 805 (394 | 454); gate|up 830 | 929 (737 | 802), FP8 780 |
+// 836 (476 | 478); down 723 | 968 (576 | 784).  The 32 x 32 MFMA issues at
+// about twice the rate of the 16 x 16 one, writing the next step's operands
+// between the k-slices' MFMAs hides the stores, the FP8 form then fits two
+// blocks per CU, and ordering the tiles in groups of 4 row tiles halves the
+// bytes fetched beyond L2 (2.7 -> 1.2-1.4 GiB at 4096 x 16480 x 5120).
 template <int EPI, bool FP8, bool CHECK>
 int dispatch_tiled(TiledArgs a, hipStream_t s) {
-    // 128-wide weight tiles when they give every CU at least two tiles
-    const int64_t tiles128 = static_cast<int64_t>(a.mtiles) * ((a.N + 127) / 128);
-    if (tiles128 >= 512) return launch_tiled<4, EPI, FP8, CHECK>(a, s);
-    return launch_tiled<2, EPI, FP8, CHECK>(a, s);
+    switch (tiled_force()) {
+        case 1: return launch_tiled<4, 2, EPI, FP8, CHECK>(a, s);
+        case 2: return launch_tiled<4, 4, EPI, FP8, CHECK>(a, s);
+        case 10: return launch_tiled<4, 2, EPI, FP8, CHECK, true, 1>(a, s);
+        default: break;
+    }
+    // 128-wide weight tiles unless they leave CUs without a tile
+    const int64_t mt = (static_cast<int64_t>(a.M) + kTileM - 1) / kTileM;
+    const int64_t tiles128 = mt * ((a.N + 127) / 128);
+    if (tiles128 >= 256 || tiled_force() == 9) return launch_tiled<4, 4, EPI, FP8, CHECK, true, 1>(a, s);
+    return launch_tiled<4, 2, EPI, FP8, CHECK, true, 1>(a, s);
 }
 
 template <bool FP8, bool CHECK>
@@ -1882,7 +2021,7 @@ extern "C" int hai_gemm_bf16_tiled(void* y, int64_t ldy, const void* x, int64_t 
     if (M == 0 || N == 0) return HAI_OK;
     TiledArgs a{static_cast<uint16_t*>(y), ldy, static_cast<const uint16_t*>(x), ldx, w, nullptr, nullptr, 0,
                 static_cast<const uint16_t*>(res), ld_res, int(M), int(N), int(K),
-                static_cast<int>((M + kTileM - 1) / kTileM), 0};
+                static_cast<int>((M + kTileM - 1) / kTileM), 0, 0};
     return tiled_entry<false, false>(a, epilogue, as_stream(stream));
 }
 
@@ -1897,7 +2036,7 @@ extern "C" int hai_gemm_fp8_tiled(void* y, int64_t ldy, const void* x, int64_t l
     if (M == 0 || N == 0) return HAI_OK;
     TiledArgs a{static_cast<uint16_t*>(y), ldy, static_cast<const uint16_t*>(x), ldx, wq, scales, scale_rows, 0,
                 static_cast<const uint16_t*>(res), ld_res, int(M), int(N), int(K),
-                static_cast<int>((M + kTileM - 1) / kTileM), 0};
+                static_cast<int>((M + kTileM - 1) / kTileM), 0, 0};
     if ((epilogue & HAI_FP8_NO_SPECIAL_CODES) != 0) return tiled_entry<true, false>(a, epi, as_stream(stream));
     return tiled_entry<true, true>(a, epi, as_stream(stream));
 }
