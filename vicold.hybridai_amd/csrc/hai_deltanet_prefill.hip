@@ -36,18 +36,12 @@
 #include "hai_common.h"
 #include "hai_device.h"
 
-#include <atomic>
 
 namespace {
 
 using namespace hai;
 
 constexpr int kChunk = 32;   // tokens per chunk
-// value columns per block of the state pass (every block loads its chunk's
-// whole record: 16 columns per block measured slower than 32 on MI355X,
-// 307 against 207 us per 1024-token call at the 27B shape)
-template <int DK>
-constexpr int state_cols() { return 32; }
 constexpr int kMaxKc = 8;
 
 struct PrefillArgs {
@@ -75,6 +69,39 @@ __host__ __device__ constexpr int64_t chunk_floats() {
 // tolerance mode: the hardware exp and reciprocal
 __device__ __forceinline__ float fast_silu(float x) { return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
 
+// ---- matrix-core operands (v_mfma_f32_32x32x16_bf16) ----
+typedef __bf16 dn_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float dn_f32x16 __attribute__((ext_vector_type(16)));
+
+// Position in a 16-k step of the operand slot q (0..7) of lane half lh: the
+// k index 16s + op_slot(lh, q) of step s sits in k-slot 8 lh + q.  Elements
+// 8s .. 8s + 7 of a lane's 32x32 result tile hold rows 16s + op_slot(lh, q),
+// so a result tile is the B operand of the next product as it stands.
+__host__ __device__ constexpr int op_slot(int lh, int q) { return 4 * lh + (q & 3) + 8 * (q >> 2); }
+
+// Operand tables: per 16-k step (or tile block) blk, the 64 lanes' 8 bf16 of
+// the high parts, then of the low parts (x = hi + lo, hi = bf16(x),
+// lo = bf16(x - hi)).  Word e = (blk * 64 + lane) * 4 + pair.
+__device__ __forceinline__ void put_split(uint32_t* tab, int e, float x0, float x1) {
+    const uint32_t hp = f2bf2(x0, x1);
+    const int at = e + ((e >> 8) << 8);
+    tab[at] = hp;
+    tab[at + 256] = f2bf2(x0 - lo_bf(hp), x1 - hi_bf(hp));
+}
+// elements off .. off + 7 of an accumulator tile, split the same way
+__device__ __forceinline__ void dn_split8(const dn_f32x16& x, int off, u32x4& hi, u32x4& lo) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t hp = f2bf2(x[off + 2 * q], x[off + 2 * q + 1]);
+        hi[q] = hp;
+        lo[q] = f2bf2(x[off + 2 * q] - lo_bf(hp), x[off + 2 * q + 1] - hi_bf(hp));
+    }
+}
+__device__ __forceinline__ dn_f32x16 dn_mfma(u32x4 a, u32x4 b, dn_f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(dn_bf16x8, a), __builtin_bit_cast(dn_bf16x8, b),
+                                                   c, 0, 0, 0);
+}
+
 // ---- pass 1: one block (256 threads) per (chunk c, head h, sequence b);
 // KC: the conv taps (0: any count up to kMaxKc, read from the arguments) ----
 template <int DK, int DV, int KC>
@@ -90,7 +117,8 @@ __global__ __launch_bounds__(256) void deltanet_chunk_prep_kernel(PrefillArgs A)
     __shared__ __align__(16) float ks[kChunk][DKP];
     __shared__ float vs[kChunk][DV];
     __shared__ __align__(16) float Lm[kChunk][kChunk + 4];  // rows read as float4
-    __shared__ float s_lg[kChunk], s_g[kChunk], s_beta[kChunk], s_q[kChunk], s_k[kChunk];
+    __shared__ float Ps[kChunk][kChunk + 1];
+    __shared__ float s_lg[kChunk], s_g[kChunk], s_beta[kChunk], s_q[kChunk], s_k[kChunk], s_ek[kChunk], s_eq[kChunk];
 
     const int c = blockIdx.x;
     const int h = blockIdx.y;
@@ -111,41 +139,66 @@ __global__ __launch_bounds__(256) void deltanet_chunk_prep_kernel(PrefillArgs A)
     const int64_t row0 = static_cast<int64_t>(b) * T;
     const int64_t p0 = static_cast<int64_t>(A.lens ? A.lens[b] : 0) + A.pos_add;
 
-    // ---- conv + SiLU: input at prompt-chunk row t0 + tt - hist + i, rows
-    // before the prompt chunk from the conv ring (positions before 0: zero) ----
-    for (int ch = tid; ch < NCH; ch += NT) {
+    // ---- gate inputs (last wave, lane = token), requested first ----
+    float a_in = 0.0f, b_in = 0.0f, dt_b = 0.0f, a_lg = 0.0f;
+    if (wave == NW - 1 && lane < TS) {
+        a_in = bf2f(A.proj[(row0 + t0 + lane) * A.ld_proj + A.off_a + h]);
+        b_in = bf2f(A.proj[(row0 + t0 + lane) * A.ld_proj + A.off_b + h]);
+        dt_b = bf2f(A.dt_bias[h]);
+        a_lg = bf2f(A.a_log[h]);
+    }
+    // ---- conv + SiLU: thread p < NCH / 2 takes the channel pair 2p, 2p + 1
+    // (within one of q, k, v: their widths are even); input at prompt-chunk
+    // row t0 + tt - hist + i, rows before the prompt chunk from the conv ring
+    // (positions before 0: zero).  Every load is issued before the first use.
+    constexpr int NP = NCH / 2;
+    static_assert(NCH % 2 == 0 && NP <= NT - 64, "channel pairs leave the last wave to the gates");
+    if (tid < NP) {
+        const int ch = 2 * tid;
         int64_t chan;
         if (ch < DK) chan = static_cast<int64_t>(gq) * DK + ch;
         else if (ch < 2 * DK) chan = kw + static_cast<int64_t>(gq) * DK + (ch - DK);
         else chan = 2 * kw + static_cast<int64_t>(h) * DV + (ch - 2 * DK);
-        float wc[KM];
-#pragma unroll
-        for (int i = 0; i < KM; ++i) wc[i] = i < Kc ? bf2f(A.conv_w[chan * Kc + i]) : 0.0f;
-        float win[KM];  // the last Kc - 1 inputs, oldest first
+        float wc0[KM], wc1[KM];
 #pragma unroll
         for (int i = 0; i < KM; ++i) {
-            float v = 0.0f;
+            wc0[i] = i < Kc ? bf2f(A.conv_w[chan * Kc + i]) : 0.0f;
+            wc1[i] = i < Kc ? bf2f(A.conv_w[(chan + 1) * Kc + i]) : 0.0f;
+        }
+        auto pair_at = [&](const uint16_t* p) { return *reinterpret_cast<const uint32_t*>(p); };
+        uint32_t win[KM];  // the last Kc - 1 input pairs, oldest first
+#pragma unroll
+        for (int i = 0; i < KM; ++i) {
+            uint32_t v = 0;
             if (i < hist) {
                 const int r = t0 - hist + i;
-                if (r >= 0) v = bf2f(A.proj[(row0 + r) * A.ld_proj + A.off_qkv + chan]);
+                if (r >= 0) v = pair_at(A.proj + (row0 + r) * A.ld_proj + A.off_qkv + chan);
                 else if (p0 + r >= 0)
-                    v = bf2f(A.ring[(static_cast<int64_t>(b) * A.ring_n + (p0 + r) % A.ring_n) * C + chan]);
+                    v = pair_at(A.ring + (static_cast<int64_t>(b) * A.ring_n + (p0 + r) % A.ring_n) * C + chan);
             }
             win[i] = v;
         }
-        uint16_t xr[kChunk];  // every input of the chunk requested before the first use
+        uint32_t xr[kChunk];
 #pragma unroll
         for (int tt = 0; tt < kChunk; ++tt)
-            xr[tt] = tt < TS ? A.proj[(row0 + t0 + tt) * A.ld_proj + A.off_qkv + chan] : uint16_t{0};
+            xr[tt] = tt < TS ? pair_at(A.proj + (row0 + t0 + tt) * A.ld_proj + A.off_qkv + chan) : 0u;
+        float* col = ch < DK ? &qs[0][ch] : ch < 2 * DK ? &ks[0][ch - DK] : &vs[0][ch - 2 * DK];
+        const int ld = ch < 2 * DK ? DKP : DV;
 #pragma unroll
         for (int tt = 0; tt < kChunk; ++tt) {
             if (tt >= TS) continue;
-            const float xin = bf2f(xr[tt]);
-            float acc = (hist > 0 ? win[0] : xin) * wc[0];
+            const uint32_t xin = xr[tt];
+            float acc0 = lo_bf(hist > 0 ? win[0] : xin) * wc0[0];
+            float acc1 = hi_bf(hist > 0 ? win[0] : xin) * wc1[0];
 #pragma unroll
             for (int i = 1; i < KM; ++i) {
-                if (i < hist) acc = fma_(win[i], wc[i], acc);
-                else if (i == hist) acc = fma_(xin, wc[i], acc);
+                if (i < hist) {
+                    acc0 = fma_(lo_bf(win[i]), wc0[i], acc0);
+                    acc1 = fma_(hi_bf(win[i]), wc1[i], acc1);
+                } else if (i == hist) {
+                    acc0 = fma_(lo_bf(xin), wc0[i], acc0);
+                    acc1 = fma_(hi_bf(xin), wc1[i], acc1);
+                }
             }
 #pragma unroll
             for (int i = 0; i + 1 < KM; ++i)
@@ -153,33 +206,37 @@ __global__ __launch_bounds__(256) void deltanet_chunk_prep_kernel(PrefillArgs A)
 #pragma unroll
             for (int i = 0; i < KM; ++i)
                 if (i == hist - 1) win[i] = xin;
-            const float y = bfr(fast_silu(acc));
-            if (ch < DK) qs[tt][ch] = y;
-            else if (ch < 2 * DK) ks[tt][ch - DK] = y;
-            else vs[tt][ch - 2 * DK] = y;
+            *reinterpret_cast<float2*>(col + tt * ld) = make_float2(bfr(fast_silu(acc0)), bfr(fast_silu(acc1)));
         }
     }
-    // ---- gates (last wave, lane = token): log of the decay
-    // exp(-exp(A_log) softplus(dt_bias + a)), beta = sigmoid(b) ----
+    // ---- gates: log of the decay exp(-exp(A_log) softplus(dt_bias + a)),
+    // beta = sigmoid(b) ----
     if (wave == NW - 1 && lane < TS) {
-        const float a_in = bf2f(A.proj[(row0 + t0 + lane) * A.ld_proj + A.off_a + h]);
-        const float b_in = bf2f(A.proj[(row0 + t0 + lane) * A.ld_proj + A.off_b + h]);
-        const float dtv = bf2f(A.dt_bias[h]) + a_in;
+        const float dtv = dt_b + a_in;
         const float sp = fmaxf(dtv, 0.0f) + log1pf(__expf(-fabsf(dtv)));
-        s_lg[lane] = -(__expf(bf2f(A.a_log[h])) * sp);
+        s_lg[lane] = -(__expf(a_lg) * sp);
         s_beta[lane] = __builtin_amdgcn_rcpf(1.0f + __expf(-b_in));
     }
     __syncthreads();
-    // ---- L2 norms of q and k (one wave per vector); cumulative log decay ----
-    const float rs_dk = 1.0f / csqrt(static_cast<float>(DK));
-    for (int task = wave; task < 2 * TS; task += NW) {
-        const int t = task >> 1;
-        if ((task & 1) == 0) {
-            const float ssq = l64_sumsq_f32(qs[t], DK, lane);
-            if (lane == 0) s_q[t] = (1.0f / csqrt(ssq + 1.0e-6f)) * rs_dk;
-        } else {
-            const float ssk = l64_sumsq_f32(ks[t], DK, lane);
-            if (lane == 0) s_k[t] = 1.0f / csqrt(ssk + 1.0e-6f);
+    // ---- L2 norms of q and k (four threads per vector); cumulative log decay ----
+    {
+        static_assert(NT == 8 * kChunk && DK % 16 == 0, "four threads per q / k vector");
+        const float rs_dk = 1.0f / csqrt(static_cast<float>(DK));
+        const int vec = tid >> 2, part = tid & 3;
+        const int t = vec >> 1;
+        const float* x = ((vec & 1) ? ks[t] : qs[t]) + part * (DK / 4);
+        float acc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < DK / 4; k += 4) {
+            const float4 v4 = *reinterpret_cast<const float4*>(x + k);
+            acc = fma_(v4.x, v4.x, acc); acc = fma_(v4.y, v4.y, acc);
+            acc = fma_(v4.z, v4.z, acc); acc = fma_(v4.w, v4.w, acc);
+        }
+        acc += __shfl_xor(acc, 1);
+        acc += __shfl_xor(acc, 2);
+        if (part == 0 && t < TS) {
+            if (vec & 1) s_k[t] = 1.0f / csqrt(acc + 1.0e-6f);
+            else s_q[t] = (1.0f / csqrt(acc + 1.0e-6f)) * rs_dk;
         }
     }
     if (tid == NT - 1) {
@@ -201,15 +258,20 @@ __global__ __launch_bounds__(256) void deltanet_chunk_prep_kernel(PrefillArgs A)
         }
     }
     for (int e = tid; e < (kChunk - TS) * DV; e += NT) vs[TS + e / DV][e % DV] = 0.0f;
+    const float glast = s_g[TS - 1];
+    if (tid < kChunk) {
+        const bool live = tid < TS;
+        s_ek[tid] = live ? __expf(glast - s_g[tid]) : 0.0f;
+        s_eq[tid] = live ? __expf(s_g[tid]) : 0.0f;
+    }
     __syncthreads();
 
     float* rec = A.chunks + ((static_cast<int64_t>(b) * nv + h) * ((T + kChunk - 1) / kChunk) + c) * chunk_floats<DK, DV>();
     float* rU = rec;
-    float* rW = rU + kChunk * DV;
-    float* rK = rW + kChunk * DK;
-    float* rQ = rK + kChunk * DK;
-    float* rP = rQ + kChunk * DK;
-    const float glast = s_g[TS - 1];
+    uint32_t* rW = reinterpret_cast<uint32_t*>(rU + kChunk * DV);
+    uint32_t* rK = rW + kChunk * DK;
+    uint32_t* rQ = rK + kChunk * DK;
+    uint32_t* rP = rQ + kChunk * DK;
 
     // ---- Gram matrices: thread (t4 = tid / 32, s = tid % 32) takes rows
     // t4, t4 + 8, t4 + 16, t4 + 24 against key s ----
@@ -235,13 +297,32 @@ __global__ __launch_bounds__(256) void deltanet_chunk_prep_kernel(PrefillArgs A)
             const bool live = t < TS && sc < TS && sc <= t;
             const float ratio = live ? __expf(s_g[t] - s_g[sc]) : 0.0f;
             Lm[t][sc] = (live && sc < t) ? s_beta[t] * ratio * kk[r] : 0.0f;
-            rP[t * kChunk + sc] = ratio * qk[r];
+            Ps[t][sc] = ratio * qk[r];
         }
     }
     __syncthreads();
 
+    // ---- K~ = e^{g_last - g} K, Q~ = e^{g} Q and P, split, in operand order ----
+    for (int e = tid; e < 16 * DK; e += NT) {
+        const int qp = e & 3, ln = (e >> 2) & 63, blk = e >> 8;
+        const int t = ln & 31, r0 = op_slot(ln >> 5, 2 * qp);
+        const int kq = 16 * blk + r0;  // Q~ (A of Q~ S): token t, keys kq, kq + 1
+        put_split(rQ, e, s_eq[t] * qs[t][kq], s_eq[t] * qs[t][kq + 1]);
+        const int kk = 32 * (blk >> 1) + t;  // K~ (A of K~^T w): key kk, tokens tk, tk + 1
+        const int tk = 16 * (blk & 1) + r0;
+        put_split(rK, e, s_ek[tk] * ks[tk][kk], s_ek[tk + 1] * ks[tk + 1][kk]);
+    }
+    for (int e = tid; e < 16 * kChunk; e += NT) {
+        const int qp = e & 3, ln = (e >> 2) & 63, blk = e >> 8;
+        const int t = ln & 31, sc = 16 * blk + op_slot(ln >> 5, 2 * qp);
+        put_split(rP, e, Ps[t][sc], Ps[t][sc + 1]);
+    }
+    if (tid == 0) rP[kChunk * kChunk] = __float_as_uint(__expf(glast));
+    __syncthreads();  // qs is reused for W^
+
     // ---- (I + L) X = R by forward substitution, one thread per right-hand
-    // column: R = beta * V (U) or beta e^g K (W^) ----
+    // column: R = beta * V (U, to the record) or beta e^g K (W^, to LDS) ----
+    float (*Xw)[DKP] = qs;
     if (tid < NRHS) {
         float x[kChunk];
         const bool isv = tid < DV;
@@ -262,183 +343,158 @@ __global__ __launch_bounds__(256) void deltanet_chunk_prep_kernel(PrefillArgs A)
             }
             x[t] = acc;
         }
-        float* dst = isv ? rU + col : rW + col;
-        const int ld = isv ? DV : DK;
+        if (isv) {
 #pragma unroll
-        for (int t = 0; t < kChunk; ++t) dst[t * ld] = x[t];
+            for (int t = 0; t < kChunk; ++t) rU[t * DV + col] = x[t];
+        } else {
+#pragma unroll
+            for (int t = 0; t < kChunk; ++t) Xw[t][col] = x[t];
+        }
     }
-    // ---- K~ = e^{g_last - g} K and Q~ = e^{g} Q ----
-    for (int e = tid; e < kChunk * DK; e += NT) {
-        const int t = e / DK, d = e % DK;
-        const bool live = t < TS;
-        rK[e] = live ? __expf(glast - s_g[t]) * ks[t][d] : 0.0f;
-        rQ[e] = live ? __expf(s_g[t]) * qs[t][d] : 0.0f;
+    __syncthreads();
+    for (int e = tid; e < 16 * DK; e += NT) {  // W^ (A of W^ S): token t, keys kw, kw + 1
+        const int qp = e & 3, ln = (e >> 2) & 63, blk = e >> 8;
+        const int t = ln & 31, kw2 = 16 * blk + op_slot(ln >> 5, 2 * qp);
+        put_split(rW, e, Xw[t][kw2], Xw[t][kw2 + 1]);
     }
-    if (tid == 0) rP[kChunk * kChunk] = __expf(glast);
 }
 
-// ---- pass 2: one block (512 threads) per (head h, 32 value columns, sequence b),
-// the chunks in order ----
-// LDS of the state pass: the block's state columns, the chunk's w, and the
-// chunk's record (W^, K~, Q~, P, e^{g_last}; the block's U columns).
-template <int DK>
-__host__ __device__ constexpr size_t state_lds_floats() {
-    constexpr int kCols = state_cols<DK>();
-    return static_cast<size_t>(kCols) * (DK + 4) + kChunk * (kCols + 1) + (3 * kChunk * DK + kChunk * kChunk + 16) +
-           kChunk * kCols;
-}
-
+// ---- pass 2 on the matrix cores: one block per (head h, sequence b), one
+// wave per 32 value columns, the chunks in order ----
+// The state columns of a wave are DK/32 accumulator tiles of
+// v_mfma_f32_32x32x16_bf16: tile m, lane l, element i holds
+// S[32m + 8(i/4) + 4(l/32) + i%4][j0 + l%32], so elements 8s .. 8s + 7 of a
+// tile are the B operand of the 16-k step over keys 32m + 16s + op_slot(.):
+// W^ S and Q~ S take S straight from the accumulators, and w = U - W^ S comes
+// out in the layout that makes it, in turn, the B operand of P w and K~^T w.
+// The A operands (W^, Q~, K~, P) are written by pass 1 in exactly that order,
+// split into bf16 pairs; every fp32 product is hi.hi + hi.lo + lo.hi (the
+// small terms first), within ~2^-16 of it.
 template <int DK, int DV>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void deltanet_chunk_state_kernel(PrefillArgs A) {
-    constexpr int NT = 512;
-    constexpr int DKP = DK + 4;
-    constexpr int kCols = state_cols<DK>();
-    constexpr int TPC = NT / kCols;             // threads per column
-    constexpr int RPT = kChunk / TPC;           // rows of W / O per thread
-    constexpr int IB = DK / TPC;                // state keys per thread in the update
-    static_assert(RPT * TPC == kChunk && IB % 4 == 0, "state pass layout");
-    constexpr int RF = 3 * kChunk * DK + kChunk * kChunk + 16;  // W^ .. e^{g_last} of a record
-    extern __shared__ __align__(16) float lds_f[];
-    float (*St)[DKP] = reinterpret_cast<float (*)[DKP]>(lds_f);                         // St[j][i] = S[i][j0 + j]
-    float (*Wm)[kCols + 1] = reinterpret_cast<float (*)[kCols + 1]>(lds_f + kCols * DKP);
-    float* Rs = lds_f + kCols * DKP + kChunk * (kCols + 1);                              // the record from W^ on
-    float (*Us)[kCols] = reinterpret_cast<float (*)[kCols]>(Rs + RF);                    // U of the block's columns
+__global__ __launch_bounds__(64 * (DV / 32)) void deltanet_chunk_state_kernel(PrefillArgs A) {
+    constexpr int NW = DV / 32;
+    constexpr int NT = 64 * NW;
+    constexpr int MT = DK / 32;                             // state tiles per wave
+    constexpr int RW = 3 * kChunk * DK + kChunk * kChunk;  // operand words of a record
+    constexpr int RP = (RW / 4 + NT - 1) / NT;              // record pieces per thread
+    static_assert(DK % 32 == 0 && DV % 32 == 0 && kChunk == 32 && RP <= 16, "state pass tiles");
+    __shared__ __align__(16) uint32_t ops[RW];
 
     const int h = blockIdx.x;
-    const int j0 = blockIdx.y * kCols;
     const int b = blockIdx.z;
     const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int j0 = 32 * wave_index();
+    const int lc = lane & 31;
+    const int lh = lane >> 5;
     const int nv = A.nv;
     const int T = A.T;
     const int nchunks = (T + kChunk - 1) / kChunk;
     const int64_t vw = static_cast<int64_t>(nv) * DV;
     const int64_t row0 = static_cast<int64_t>(b) * T;
     const int64_t p0 = static_cast<int64_t>(A.lens ? A.lens[b] : 0) + A.pos_add;
-    const int jc = tid % kCols;   // column of the products
-    const int tg = tid / kCols;   // rows tg + TPC r (W, O), key block tg (update)
+    auto row_of = [&](int i) { return 8 * (i >> 2) + 4 * lh + (i & 3); };
+    // column-tiled head: key i = q4*(DK/4) + 4m + e of column j at float ((m*DV + j)*4 + q4)*4 + e
+    auto tiled = [&](int key, int col) {
+        const int q4 = key / (DK / 4), m = (key % (DK / 4)) / 4, ee = key % 4;
+        return ((static_cast<int64_t>(m) * DV + col) * 4 + q4) * 4 + ee;
+    };
 
-    // state of the block's columns from slot p0 % nslots (column-tiled head:
-    // key i = q4*(DK/4) + 4m + e of column j at float ((m*DV + j)*4 + q4)*4 + e)
     const float* hs = A.state + ((p0 % A.nslots) * A.B + b) * static_cast<int64_t>(nv) * DV * DK +
                       static_cast<int64_t>(h) * DV * DK;
-    for (int e = tid; e < kCols * DK; e += NT) {
-        const int jl = e / DK, i = e % DK;
-        const int q4 = i / (DK / 4), m = (i % (DK / 4)) / 4, ee = i % 4;
-        St[jl][i] = hs[((static_cast<int64_t>(m) * DV + j0 + jl) * 4 + q4) * 4 + ee];
-    }
-    __syncthreads();
+    dn_f32x16 S[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) S[m][i] = hs[tiled(32 * m + row_of(i), j0 + lc)];
 
-    // A chunk's record goes through registers: the next chunk's loads are
-    // issued before the current chunk is computed, and stored to LDS after it.
-    constexpr int RP = (RF / 4 + NT - 1) / NT;   // record float4 per thread
-    constexpr int UP = (kChunk * kCols / 4 + NT - 1) / NT;
-    static_assert(RP <= 8 && UP == 1, "record pieces per thread");
-    u32x4 rr[RP], ur;  // native vectors (HIP's float4 struct stays in memory here)
-    // (unrolled by hand, up to 8 pieces: indices the compiler sees as constants
-    // keep rr / ur in registers)
-#define HAI_REC_LOAD1(U)                                                                                         \
-    if constexpr (RP > (U)) {                                                                                    \
-        const int e = tid + (U) * NT;                                                                            \
-        if (e < RF / 4) rr[(U) < RP ? (U) : 0] = src_[e];                                                        \
-    }
-#define HAI_LOAD_RECORD(CI)                                                                                      \
-    do {                                                                                                         \
-        const float* rec_ = A.chunks + ((static_cast<int64_t>(b) * nv + h) * nchunks + (CI)) * chunk_floats<DK, DV>(); \
-        const u32x4* src_ = reinterpret_cast<const u32x4*>(rec_ + kChunk * DV);                                \
-        HAI_REC_LOAD1(0) HAI_REC_LOAD1(1) HAI_REC_LOAD1(2) HAI_REC_LOAD1(3)                                      \
-        HAI_REC_LOAD1(4) HAI_REC_LOAD1(5) HAI_REC_LOAD1(6) HAI_REC_LOAD1(7)                                      \
-        if (tid < kChunk * kCols / 4) {                                                                          \
-            const int t_ = tid / (kCols / 4), q_ = tid % (kCols / 4);                                            \
-            ur = *reinterpret_cast<const u32x4*>(rec_ + t_ * DV + j0 + 4 * q_);                                 \
-        }                                                                                                        \
-    } while (0)
-    HAI_LOAD_RECORD(0);
+    // the next chunk's operands, U values and e^{g_last} go through registers
+    // (issued before the current chunk is computed, stored to LDS after it)
+    u32x4 rr[RP];
+    float un[16], gn = 0.0f;
+    auto load_record = [&](int ci) {
+        const float* rec = A.chunks + ((static_cast<int64_t>(b) * nv + h) * nchunks + ci) * chunk_floats<DK, DV>();
+        const u32x4* src = reinterpret_cast<const u32x4*>(rec + kChunk * DV);
+#pragma unroll
+        for (int u = 0; u < RP; ++u)
+            if (RW / 4 % NT == 0 || tid + u * NT < RW / 4) rr[u] = src[tid + u * NT];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) un[i] = rec[row_of(i) * DV + j0 + lc];
+        gn = rec[kChunk * DV + RW];
+    };
+    load_record(0);
     for (int c = 0; c < nchunks; ++c) {
         const int t0 = c * kChunk;
         const int TS = min(kChunk, T - t0);
-#define HAI_REC_STORE1(U)                                                                                        \
-    if constexpr (RP > (U)) {                                                                                    \
-        const int e = tid + (U) * NT;                                                                            \
-        if (e < RF / 4) reinterpret_cast<u32x4*>(Rs)[e] = rr[(U) < RP ? (U) : 0];                                \
+#pragma unroll
+        for (int u = 0; u < RP; ++u)
+            if (RW / 4 % NT == 0 || tid + u * NT < RW / 4) reinterpret_cast<u32x4*>(ops)[tid + u * NT] = rr[u];
+        float uc[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) uc[i] = un[i];
+        const float gl = gn;
+        __syncthreads();
+        if (c + 1 < nchunks) load_record(c + 1);
+        const u32x4* opW = reinterpret_cast<const u32x4*>(ops);
+        const u32x4* opK = opW + kChunk * DK / 4;
+        const u32x4* opQ = opK + kChunk * DK / 4;
+        const u32x4* opP = opQ + kChunk * DK / 4;
+        // ---- W^ S and Q~ S (row t = lane % 32 of the A operands) ----
+        dn_f32x16 Wa, Oa;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) Wa[i] = Oa[i] = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < 2 * MT; ++ks) {
+            u32x4 bh, bl;
+            dn_split8(S[ks >> 1], 8 * (ks & 1), bh, bl);
+            const u32x4 wh = opW[(2 * ks) * 64 + lane], wl = opW[(2 * ks + 1) * 64 + lane];
+            const u32x4 qh = opQ[(2 * ks) * 64 + lane], ql = opQ[(2 * ks + 1) * 64 + lane];
+            Wa = dn_mfma(wl, bh, Wa);
+            Oa = dn_mfma(ql, bh, Oa);
+            Wa = dn_mfma(wh, bl, Wa);
+            Oa = dn_mfma(qh, bl, Oa);
+            Wa = dn_mfma(wh, bh, Wa);
+            Oa = dn_mfma(qh, bh, Oa);
+        }
+        // ---- w = U - W^ S, then O = Q~ S + P w ----
+#pragma unroll
+        for (int i = 0; i < 16; ++i) Wa[i] = uc[i] - Wa[i];
+        u32x4 wh[2], wl[2];
+        dn_split8(Wa, 0, wh[0], wl[0]);
+        dn_split8(Wa, 8, wh[1], wl[1]);
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+            const u32x4 ph = opP[(2 * st) * 64 + lane], pl = opP[(2 * st + 1) * 64 + lane];
+            Oa = dn_mfma(pl, wh[st], Oa);
+            Oa = dn_mfma(ph, wl[st], Oa);
+            Oa = dn_mfma(ph, wh[st], Oa);
+        }
+        float* orow = A.o_ws + (row0 + t0) * vw + static_cast<int64_t>(h) * DV + j0 + lc;
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            if (row_of(i) < TS) orow[row_of(i) * vw] = Oa[i];
+        // ---- S = e^{g_last} S + K~^T w (row = key 32m + lane % 32, k = tokens) ----
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) S[m][i] *= gl;
+#pragma unroll
+            for (int st = 0; st < 2; ++st) {
+                const u32x4 kh = opK[(4 * m + 2 * st) * 64 + lane], kl = opK[(4 * m + 2 * st + 1) * 64 + lane];
+                S[m] = dn_mfma(kl, wh[st], S[m]);
+                S[m] = dn_mfma(kh, wl[st], S[m]);
+                S[m] = dn_mfma(kh, wh[st], S[m]);
+            }
+        }
+        __syncthreads();  // every wave's reads of this chunk's operands are done
     }
-        HAI_REC_STORE1(0) HAI_REC_STORE1(1) HAI_REC_STORE1(2) HAI_REC_STORE1(3)
-        HAI_REC_STORE1(4) HAI_REC_STORE1(5) HAI_REC_STORE1(6) HAI_REC_STORE1(7)
-#undef HAI_REC_STORE1
-        if (tid < kChunk * kCols / 4) reinterpret_cast<u32x4*>(&Us[0][0])[tid] = ur;
-        __syncthreads();
-        if (c + 1 < nchunks) HAI_LOAD_RECORD(c + 1);
-        const float* rW = Rs;
-        const float* rK = rW + kChunk * DK;
-        const float* rQ = rK + kChunk * DK;
-        const float* rP = rQ + kChunk * DK;
-        // ---- W = U - W^ S and Q~ S for rows tg + TPC r of column jc ----
-        float wv[RPT], ov[RPT];
-#pragma unroll
-        for (int r = 0; r < RPT; ++r) wv[r] = ov[r] = 0.0f;
-#pragma unroll 4
-        for (int i = 0; i < DK; i += 4) {
-            const float4 s4 = *reinterpret_cast<const float4*>(&St[jc][i]);
-#pragma unroll
-            for (int r = 0; r < RPT; ++r) {
-                const float4 x4 = *reinterpret_cast<const float4*>(rW + (tg + TPC * r) * DK + i);
-                const float4 y4 = *reinterpret_cast<const float4*>(rQ + (tg + TPC * r) * DK + i);
-                wv[r] = fma_(x4.x, s4.x, wv[r]); wv[r] = fma_(x4.y, s4.y, wv[r]);
-                wv[r] = fma_(x4.z, s4.z, wv[r]); wv[r] = fma_(x4.w, s4.w, wv[r]);
-                ov[r] = fma_(y4.x, s4.x, ov[r]); ov[r] = fma_(y4.y, s4.y, ov[r]);
-                ov[r] = fma_(y4.z, s4.z, ov[r]); ov[r] = fma_(y4.w, s4.w, ov[r]);
-            }
-        }
-#pragma unroll
-        for (int r = 0; r < RPT; ++r) Wm[tg + TPC * r][jc] = Us[tg + TPC * r][jc] - wv[r];
-        __syncthreads();
-        // ---- outputs O = Q~ S + P W ----
-#pragma unroll
-        for (int r = 0; r < RPT; ++r) {
-            const int t = tg + TPC * r;
-            if (t < TS) {
-                float o = ov[r];
-                const float* pr = rP + t * kChunk;
-                for (int s2 = 0; s2 <= t; ++s2) o = fma_(pr[s2], Wm[s2][jc], o);
-                A.o_ws[(row0 + t0 + t) * vw + static_cast<int64_t>(h) * DV + j0 + jc] = o;
-            }
-        }
-        // ---- S = e^{g_last} S + K~^T W: thread (tg, jc) updates keys tg*IB .. + IB - 1 ----
-        {
-            const float gl = rP[kChunk * kChunk];
-            float sv[IB];
-#pragma unroll
-            for (int u = 0; u < IB; u += 4) {
-                const float4 s4 = *reinterpret_cast<const float4*>(&St[jc][tg * IB + u]);
-                sv[u] = s4.x * gl; sv[u + 1] = s4.y * gl; sv[u + 2] = s4.z * gl; sv[u + 3] = s4.w * gl;
-            }
-            for (int t = 0; t < TS; ++t) {
-                const float wt = Wm[t][jc];
-                const float* kr = rK + t * DK + tg * IB;
-#pragma unroll
-                for (int u = 0; u < IB; u += 4) {
-                    const float4 k4 = *reinterpret_cast<const float4*>(kr + u);
-                    sv[u] = fma_(k4.x, wt, sv[u]); sv[u + 1] = fma_(k4.y, wt, sv[u + 1]);
-                    sv[u + 2] = fma_(k4.z, wt, sv[u + 2]); sv[u + 3] = fma_(k4.w, wt, sv[u + 3]);
-                }
-            }
-            __syncthreads();  // every thread's reads of S and W for this chunk are done
-#pragma unroll
-            for (int u = 0; u < IB; u += 4)
-                *reinterpret_cast<float4*>(&St[jc][tg * IB + u]) = make_float4(sv[u], sv[u + 1], sv[u + 2], sv[u + 3]);
-        }
-        __syncthreads();
-    }
-    // ---- the state after the prompt chunk, to slot (p0 + T) % nslots ----
     float* hd = A.state + (((p0 + T) % A.nslots) * A.B + b) * static_cast<int64_t>(nv) * DV * DK +
                 static_cast<int64_t>(h) * DV * DK;
-    for (int e = tid; e < kCols * DK; e += NT) {
-        const int jl = e / DK, i = e % DK;
-        const int q4 = i / (DK / 4), m = (i % (DK / 4)) / 4, ee = i % 4;
-        hd[((static_cast<int64_t>(m) * DV + j0 + jl) * 4 + q4) * 4 + ee] = St[jl][i];
-    }
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) hd[tiled(32 * m + row_of(i), j0 + lc)] = S[m][i];
 }
-#undef HAI_LOAD_RECORD
-#undef HAI_REC_LOAD1
 
 // The conv ring's entries for the chunk's last Kc - 1 positions (the only
 // ones a later step reads), after every block has read the entries before
@@ -493,18 +549,7 @@ int launch_prefill(const PrefillArgs& a, uint16_t* out, int64_t ld_out, int64_t 
     else deltanet_chunk_prep_kernel<DK, DV, 0><<<pgrid, dim3(256), 0, s>>>(a);
     int rc = launched("deltanet_chunk_prep_kernel");
     if (rc != HAI_OK) return rc;
-    constexpr size_t shmem = state_lds_floats<DK>() * sizeof(float);
-    static std::atomic<uint8_t> allowed[64];
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return invalid("deltanet_prefill: device ordinal");
-    if (!allowed[dev].load(std::memory_order_acquire)) {
-        rc = check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(deltanet_chunk_state_kernel<DK, DV>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(shmem)),
-                       "hipFuncSetAttribute");
-        if (rc != HAI_OK) return rc;
-        allowed[dev].store(1, std::memory_order_release);
-    }
-    deltanet_chunk_state_kernel<DK, DV><<<dim3(a.nv, DV / state_cols<DK>(), a.B), dim3(512), shmem, s>>>(a);
+    deltanet_chunk_state_kernel<DK, DV><<<dim3(a.nv, 1, a.B), dim3(64 * (DV / 32)), 0, s>>>(a);
     rc = launched("deltanet_chunk_state_kernel");
     if (rc != HAI_OK) return rc;
     const int hist = a.Kc - 1;
@@ -552,6 +597,10 @@ extern "C" int hai_deltanet_prefill_bf16(void* out, int64_t ld_out, const void* 
         return invalid("deltanet_prefill: shape");
     if (lens == nullptr && pos_add < 0) return invalid("deltanet_prefill: negative position");
     if (!aligned16(state) || !aligned16(workspace)) return invalid("deltanet_prefill: alignment");
+    // the conv reads channel pairs as one dword
+    if ((reinterpret_cast<uintptr_t>(proj) & 3u) != 0 || (reinterpret_cast<uintptr_t>(conv_ring) & 3u) != 0 ||
+        (ld_proj & 1) != 0 || (off_qkv & 1) != 0)
+        return invalid("deltanet_prefill: proj and conv_ring must be 4-byte aligned, ld_proj and off_qkv even");
     if (workspace_bytes < 0 ||
         static_cast<size_t>(workspace_bytes) < hai_deltanet_prefill_workspace_bytes(B, T, nv, dv))
         return invalid("deltanet_prefill: workspace smaller than hai_deltanet_prefill_workspace_bytes");
