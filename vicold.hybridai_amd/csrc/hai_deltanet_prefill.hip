@@ -35,6 +35,9 @@
 // recurrence to fp32 rounding, not bit for bit.
 #include "hai_common.h"
 #include "hai_device.h"
+#include "hai_gemm_common.h"
+
+#include <atomic>
 
 
 namespace {
@@ -88,6 +91,15 @@ __device__ __forceinline__ void put_split(uint32_t* tab, int e, float x0, float 
     tab[at] = hp;
     tab[at + 256] = f2bf2(x0 - lo_bf(hp), x1 - hi_bf(hp));
 }
+// eight values, split the same way
+__device__ __forceinline__ void dn_split8(const float (&x)[8], u32x4& hi, u32x4& lo) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t hp = f2bf2(x[2 * q], x[2 * q + 1]);
+        hi[q] = hp;
+        lo[q] = f2bf2(x[2 * q] - lo_bf(hp), x[2 * q + 1] - hi_bf(hp));
+    }
+}
 // elements off .. off + 7 of an accumulator tile, split the same way
 __device__ __forceinline__ void dn_split8(const dn_f32x16& x, int off, u32x4& hi, u32x4& lo) {
 #pragma unroll
@@ -96,6 +108,10 @@ __device__ __forceinline__ void dn_split8(const dn_f32x16& x, int off, u32x4& hi
         hi[q] = hp;
         lo[q] = f2bf2(x[off + 2 * q] - lo_bf(hp), x[off + 2 * q + 1] - hi_bf(hp));
     }
+}
+// one global -> LDS copy of 16 bytes per lane (to lds + lane; lds wave-uniform)
+__device__ __forceinline__ void dn_copy16(const u32x4* src, u32x4* lds) {
+    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
 }
 __device__ __forceinline__ dn_f32x16 dn_mfma(u32x4 a, u32x4 b, dn_f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(dn_bf16x8, a), __builtin_bit_cast(dn_bf16x8, b),
@@ -115,7 +131,7 @@ __global__ __launch_bounds__(256) void deltanet_chunk_prep_kernel(PrefillArgs A)
     static_assert(NRHS <= NT && NRHS >= kChunk, "one thread per right-hand column");
     __shared__ __align__(16) float qs[kChunk][DKP];
     __shared__ __align__(16) float ks[kChunk][DKP];
-    __shared__ float vs[kChunk][DV];
+    __shared__ uint32_t vs2[kChunk][DV / 2];  // v as bf16 pairs (the conv output is bf16-exact)
     __shared__ __align__(16) float Lm[kChunk][kChunk + 4];  // rows read as float4
     __shared__ float Ps[kChunk][kChunk + 1];
     __shared__ float s_lg[kChunk], s_g[kChunk], s_beta[kChunk], s_q[kChunk], s_k[kChunk], s_ek[kChunk], s_eq[kChunk];
@@ -182,8 +198,7 @@ __global__ __launch_bounds__(256) void deltanet_chunk_prep_kernel(PrefillArgs A)
 #pragma unroll
         for (int tt = 0; tt < kChunk; ++tt)
             xr[tt] = tt < TS ? pair_at(A.proj + (row0 + t0 + tt) * A.ld_proj + A.off_qkv + chan) : 0u;
-        float* col = ch < DK ? &qs[0][ch] : ch < 2 * DK ? &ks[0][ch - DK] : &vs[0][ch - 2 * DK];
-        const int ld = ch < 2 * DK ? DKP : DV;
+        float* col = ch < DK ? &qs[0][ch] : &ks[0][ch - DK];  // (q and k rows)
 #pragma unroll
         for (int tt = 0; tt < kChunk; ++tt) {
             if (tt >= TS) continue;
@@ -206,7 +221,9 @@ __global__ __launch_bounds__(256) void deltanet_chunk_prep_kernel(PrefillArgs A)
 #pragma unroll
             for (int i = 0; i < KM; ++i)
                 if (i == hist - 1) win[i] = xin;
-            *reinterpret_cast<float2*>(col + tt * ld) = make_float2(bfr(fast_silu(acc0)), bfr(fast_silu(acc1)));
+            const float y0 = bfr(fast_silu(acc0)), y1 = bfr(fast_silu(acc1));
+            if (ch < 2 * DK) *reinterpret_cast<float2*>(col + tt * DKP) = make_float2(y0, y1);
+            else vs2[tt][(ch - 2 * DK) / 2] = f2bf2(y0, y1);
         }
     }
     // ---- gates: log of the decay exp(-exp(A_log) softplus(dt_bias + a)),
@@ -257,7 +274,7 @@ __global__ __launch_bounds__(256) void deltanet_chunk_prep_kernel(PrefillArgs A)
             ks[t][d] = 0.0f;
         }
     }
-    for (int e = tid; e < (kChunk - TS) * DV; e += NT) vs[TS + e / DV][e % DV] = 0.0f;
+    for (int e = tid; e < (kChunk - TS) * (DV / 2); e += NT) vs2[TS + e / (DV / 2)][e % (DV / 2)] = 0u;
     const float glast = s_g[TS - 1];
     if (tid < kChunk) {
         const bool live = tid < TS;
@@ -273,31 +290,41 @@ __global__ __launch_bounds__(256) void deltanet_chunk_prep_kernel(PrefillArgs A)
     uint32_t* rQ = rK + kChunk * DK;
     uint32_t* rP = rQ + kChunk * DK;
 
-    // ---- Gram matrices: thread (t4 = tid / 32, s = tid % 32) takes rows
-    // t4, t4 + 8, t4 + 16, t4 + 24 against key s ----
-    {
-        const int sc = tid % kChunk;
-        const int t4 = tid / kChunk;
-        float kk[4] = {0.0f, 0.0f, 0.0f, 0.0f}, qk[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int d = 0; d < DK; d += 4) {
-            const float4 c4 = *reinterpret_cast<const float4*>(&ks[sc][d]);
+    // ---- Gram matrices on the matrix cores: wave 0 K K^T, wave 1 Q K^T, each
+    // over all of d in 16-wide k steps (k slot q of lane l: d = 16 step +
+    // 8 (l / 32) + q; K's row t is the A operand and its column t the B
+    // operand in the same registers); result element i of lane l: row
+    // t = 8 (i / 4) + 4 (l / 32) + i % 4, key s = l % 32 ----
+    if (wave < 2) {
+        const int r = lane & 31;
+        const float* arow = wave == 0 ? ks[r] : qs[r];
+        dn_f32x16 G;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float4 a4 = *reinterpret_cast<const float4*>(&ks[t4 + 8 * r][d]);
-                const float4 b4 = *reinterpret_cast<const float4*>(&qs[t4 + 8 * r][d]);
-                kk[r] = fma_(a4.x, c4.x, kk[r]); kk[r] = fma_(a4.y, c4.y, kk[r]);
-                kk[r] = fma_(a4.z, c4.z, kk[r]); kk[r] = fma_(a4.w, c4.w, kk[r]);
-                qk[r] = fma_(b4.x, c4.x, qk[r]); qk[r] = fma_(b4.y, c4.y, qk[r]);
-                qk[r] = fma_(b4.z, c4.z, qk[r]); qk[r] = fma_(b4.w, c4.w, qk[r]);
-            }
+        for (int i = 0; i < 16; ++i) G[i] = 0.0f;
+#pragma unroll
+        for (int kst = 0; kst < DK / 16; ++kst) {
+            const int d0 = 16 * kst + 8 * (lane >> 5);
+            const float4 k0 = *reinterpret_cast<const float4*>(&ks[r][d0]);
+            const float4 k1 = *reinterpret_cast<const float4*>(&ks[r][d0 + 4]);
+            const float4 a0 = *reinterpret_cast<const float4*>(arow + d0);
+            const float4 a1 = *reinterpret_cast<const float4*>(arow + d0 + 4);
+            const float kv[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+            const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+            u32x4 kh, kl, ah, al;
+            dn_split8(kv, kh, kl);
+            dn_split8(av, ah, al);
+            G = dn_mfma(al, kh, G);
+            G = dn_mfma(ah, kl, G);
+            G = dn_mfma(ah, kh, G);
         }
+        const int sc = lane & 31;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int t = t4 + 8 * r;
+        for (int i = 0; i < 16; ++i) {
+            const int t = 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
             const bool live = t < TS && sc < TS && sc <= t;
             const float ratio = live ? __expf(s_g[t] - s_g[sc]) : 0.0f;
-            Lm[t][sc] = (live && sc < t) ? s_beta[t] * ratio * kk[r] : 0.0f;
-            Ps[t][sc] = ratio * qk[r];
+            if (wave == 0) Lm[t][sc] = (live && sc < t) ? s_beta[t] * ratio * G[i] : 0.0f;
+            else Ps[t][sc] = ratio * G[i];
         }
     }
     __syncthreads();
@@ -331,15 +358,19 @@ __global__ __launch_bounds__(256) void deltanet_chunk_prep_kernel(PrefillArgs A)
         for (int t = 0; t < kChunk; ++t) {
             float acc = 0.0f;
             if (t < TS) {
-                acc = isv ? s_beta[t] * vs[t][col] : (s_beta[t] * __expf(s_g[t])) * ks[t][col];
+                // four partial sums (s = u mod 4) shorten the dependent chain
+                float part[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                 for (int s4 = 0; s4 < t; s4 += 4) {
                     const float4 l4 = *reinterpret_cast<const float4*>(&Lm[t][s4]);
                     const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
 #pragma unroll
                     for (int u = 0; u < 4; ++u)
-                        if (s4 + u < t) acc = fma_(-lv[u], x[s4 + u], acc);
+                        if (s4 + u < t) part[u] = fma_(-lv[u], x[s4 + u], part[u]);
                 }
+                const uint32_t vp = vs2[t][col >> 1];
+                acc = isv ? s_beta[t] * ((col & 1) ? hi_bf(vp) : lo_bf(vp)) : (s_beta[t] * __expf(s_g[t])) * ks[t][col];
+                acc += (part[0] + part[1]) + (part[2] + part[3]);
             }
             x[t] = acc;
         }
@@ -370,21 +401,38 @@ __global__ __launch_bounds__(256) void deltanet_chunk_prep_kernel(PrefillArgs A)
 // The A operands (W^, Q~, K~, P) are written by pass 1 in exactly that order,
 // split into bf16 pairs; every fp32 product is hi.hi + hi.lo + lo.hi (the
 // small terms first), within ~2^-16 of it.
+// Records reach LDS by global -> LDS copies (16 bytes per lane, no
+// registers), one chunk ahead into the other of two buffers; each wave issues
+// the same number of copies per chunk (pieces past the record repeat its
+// last piece into the buffer's tail), so s_waitcnt vmcnt(kCopies) leaves
+// exactly the next chunk's copies in flight.
+template <int DK, int DV>
+__host__ __device__ constexpr int state_copies() {  // copy instructions per wave per chunk
+    return static_cast<int>((chunk_floats<DK, DV>() / 4 + 64 * (DV / 32) - 1) / (64 * (DV / 32)));
+}
+template <int DK, int DV>
+__host__ __device__ constexpr size_t state_lds_bytes() {  // two record buffers
+    return 2 * static_cast<size_t>(state_copies<DK, DV>()) * 64 * (DV / 32) * 16;
+}
+
 template <int DK, int DV>
 __global__ __launch_bounds__(64 * (DV / 32)) void deltanet_chunk_state_kernel(PrefillArgs A) {
     constexpr int NW = DV / 32;
     constexpr int NT = 64 * NW;
     constexpr int MT = DK / 32;                             // state tiles per wave
     constexpr int RW = 3 * kChunk * DK + kChunk * kChunk;  // operand words of a record
-    constexpr int RP = (RW / 4 + NT - 1) / NT;              // record pieces per thread
-    static_assert(DK % 32 == 0 && DV % 32 == 0 && kChunk == 32 && RP <= 16, "state pass tiles");
-    __shared__ __align__(16) uint32_t ops[RW];
+    constexpr int NPC = static_cast<int>(chunk_floats<DK, DV>() / 4);  // 16-byte pieces of a record
+    constexpr int kCopies = state_copies<DK, DV>();
+    constexpr int BUF = kCopies * NT;                       // pieces per buffer
+    static_assert(DK % 32 == 0 && DV % 32 == 0 && kChunk == 32 && chunk_floats<DK, DV>() % 4 == 0 && kCopies < 48,
+                  "state pass tiles");
+    extern __shared__ __align__(16) u32x4 recs[];  // [2][BUF]: U [C][DV] f32, operands, e^{g_last}
 
     const int h = blockIdx.x;
     const int b = blockIdx.z;
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int j0 = 32 * wave_index();
+    const int lane = threadIdx.x & 63;
+    const int w = wave_index();
+    const int j0 = 32 * w;
     const int lc = lane & 31;
     const int lh = lane >> 5;
     const int nv = A.nv;
@@ -399,6 +447,18 @@ __global__ __launch_bounds__(64 * (DV / 32)) void deltanet_chunk_state_kernel(Pr
         const int q4 = key / (DK / 4), m = (key % (DK / 4)) / 4, ee = key % 4;
         return ((static_cast<int64_t>(m) * DV + col) * 4 + q4) * 4 + ee;
     };
+    const u32x4* recs0 = reinterpret_cast<const u32x4*>(A.chunks) +
+                         (static_cast<int64_t>(b) * nv + h) * nchunks * static_cast<int64_t>(NPC);
+    // pieces (i * NW + w) * 64 + lane: in the record for i < kCopies - 1
+    static_assert((kCopies - 1) * NT < NPC, "only the last copy runs past the record");
+    const int last_piece = min(((kCopies - 1) * NW + w) * 64 + lane, NPC - 1) - ((kCopies - 1) * NW + w) * 64;
+    auto copy_record = [&](int ci, int buf) {
+        const u32x4* src = recs0 + static_cast<int64_t>(min(ci, nchunks - 1)) * NPC + w * 64;
+        u32x4* dst = recs + buf * BUF + w * 64;
+#pragma unroll
+        for (int i = 0; i < kCopies - 1; ++i) dn_copy16(src + i * NT + lane, dst + i * NT);
+        dn_copy16(src + (kCopies - 1) * NT + last_piece, dst + (kCopies - 1) * NT);
+    };
 
     const float* hs = A.state + ((p0 % A.nslots) * A.B + b) * static_cast<int64_t>(nv) * DV * DK +
                       static_cast<int64_t>(h) * DV * DK;
@@ -407,35 +467,23 @@ __global__ __launch_bounds__(64 * (DV / 32)) void deltanet_chunk_state_kernel(Pr
     for (int m = 0; m < MT; ++m)
 #pragma unroll
         for (int i = 0; i < 16; ++i) S[m][i] = hs[tiled(32 * m + row_of(i), j0 + lc)];
+    pin_memory_order();
+    copy_record(0, 0);
 
-    // the next chunk's operands, U values and e^{g_last} go through registers
-    // (issued before the current chunk is computed, stored to LDS after it)
-    u32x4 rr[RP];
-    float un[16], gn = 0.0f;
-    auto load_record = [&](int ci) {
-        const float* rec = A.chunks + ((static_cast<int64_t>(b) * nv + h) * nchunks + ci) * chunk_floats<DK, DV>();
-        const u32x4* src = reinterpret_cast<const u32x4*>(rec + kChunk * DV);
-#pragma unroll
-        for (int u = 0; u < RP; ++u)
-            if (RW / 4 % NT == 0 || tid + u * NT < RW / 4) rr[u] = src[tid + u * NT];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) un[i] = rec[row_of(i) * DV + j0 + lc];
-        gn = rec[kChunk * DV + RW];
-    };
-    load_record(0);
     for (int c = 0; c < nchunks; ++c) {
         const int t0 = c * kChunk;
         const int TS = min(kChunk, T - t0);
-#pragma unroll
-        for (int u = 0; u < RP; ++u)
-            if (RW / 4 % NT == 0 || tid + u * NT < RW / 4) reinterpret_cast<u32x4*>(ops)[tid + u * NT] = rr[u];
-        float uc[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) uc[i] = un[i];
-        const float gl = gn;
-        __syncthreads();
-        if (c + 1 < nchunks) load_record(c + 1);
-        const u32x4* opW = reinterpret_cast<const u32x4*>(ops);
+        const int cur = c & 1;
+        pin_memory_order();
+        __builtin_amdgcn_sched_barrier(0);
+        copy_record(c + 1, cur ^ 1);  // (the last chunk copies itself again into the idle buffer)
+        pin_memory_order();
+        __builtin_amdgcn_sched_barrier(0);
+        wait_vmcnt<kCopies>();  // this chunk's copies (and every older request) are done
+        __builtin_amdgcn_sched_barrier(0);
+        lds_barrier();          // ... for every wave
+        const float* rf = reinterpret_cast<const float*>(recs + cur * BUF);
+        const u32x4* opW = reinterpret_cast<const u32x4*>(rf + kChunk * DV);
         const u32x4* opK = opW + kChunk * DK / 4;
         const u32x4* opQ = opK + kChunk * DK / 4;
         const u32x4* opP = opQ + kChunk * DK / 4;
@@ -443,12 +491,19 @@ __global__ __launch_bounds__(64 * (DV / 32)) void deltanet_chunk_state_kernel(Pr
         dn_f32x16 Wa, Oa;
 #pragma unroll
         for (int i = 0; i < 16; ++i) Wa[i] = Oa[i] = 0.0f;
+        // (the next step's operands are read from LDS before this step's products)
+        u32x4 nwh = opW[lane], nwl = opW[64 + lane], nqh = opQ[lane], nql = opQ[64 + lane];
 #pragma unroll
         for (int ks = 0; ks < 2 * MT; ++ks) {
+            const u32x4 wh = nwh, wl = nwl, qh = nqh, ql = nql;
+            if (ks + 1 < 2 * MT) {
+                nwh = opW[(2 * ks + 2) * 64 + lane];
+                nwl = opW[(2 * ks + 3) * 64 + lane];
+                nqh = opQ[(2 * ks + 2) * 64 + lane];
+                nql = opQ[(2 * ks + 3) * 64 + lane];
+            }
             u32x4 bh, bl;
             dn_split8(S[ks >> 1], 8 * (ks & 1), bh, bl);
-            const u32x4 wh = opW[(2 * ks) * 64 + lane], wl = opW[(2 * ks + 1) * 64 + lane];
-            const u32x4 qh = opQ[(2 * ks) * 64 + lane], ql = opQ[(2 * ks + 1) * 64 + lane];
             Wa = dn_mfma(wl, bh, Wa);
             Oa = dn_mfma(ql, bh, Oa);
             Wa = dn_mfma(wh, bl, Wa);
@@ -458,7 +513,7 @@ __global__ __launch_bounds__(64 * (DV / 32)) void deltanet_chunk_state_kernel(Pr
         }
         // ---- w = U - W^ S, then O = Q~ S + P w ----
 #pragma unroll
-        for (int i = 0; i < 16; ++i) Wa[i] = uc[i] - Wa[i];
+        for (int i = 0; i < 16; ++i) Wa[i] = rf[row_of(i) * DV + j0 + lc] - Wa[i];
         u32x4 wh[2], wl[2];
         dn_split8(Wa, 0, wh[0], wl[0]);
         dn_split8(Wa, 8, wh[1], wl[1]);
@@ -474,6 +529,7 @@ __global__ __launch_bounds__(64 * (DV / 32)) void deltanet_chunk_state_kernel(Pr
         for (int i = 0; i < 16; ++i)
             if (row_of(i) < TS) orow[row_of(i) * vw] = Oa[i];
         // ---- S = e^{g_last} S + K~^T w (row = key 32m + lane % 32, k = tokens) ----
+        const float gl = rf[kChunk * DV + RW];
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
 #pragma unroll
@@ -486,8 +542,9 @@ __global__ __launch_bounds__(64 * (DV / 32)) void deltanet_chunk_state_kernel(Pr
                 S[m] = dn_mfma(kh, wh[st], S[m]);
             }
         }
-        __syncthreads();  // every wave's reads of this chunk's operands are done
+        lds_barrier();  // every wave's reads of this buffer are done before it is refilled
     }
+    wait_vmcnt<0>();
     float* hd = A.state + (((p0 + T) % A.nslots) * A.B + b) * static_cast<int64_t>(nv) * DV * DK +
                 static_cast<int64_t>(h) * DV * DK;
 #pragma unroll
@@ -549,7 +606,18 @@ int launch_prefill(const PrefillArgs& a, uint16_t* out, int64_t ld_out, int64_t 
     else deltanet_chunk_prep_kernel<DK, DV, 0><<<pgrid, dim3(256), 0, s>>>(a);
     int rc = launched("deltanet_chunk_prep_kernel");
     if (rc != HAI_OK) return rc;
-    deltanet_chunk_state_kernel<DK, DV><<<dim3(a.nv, 1, a.B), dim3(64 * (DV / 32)), 0, s>>>(a);
+    constexpr size_t shmem = state_lds_bytes<DK, DV>();
+    static std::atomic<uint8_t> allowed[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return invalid("deltanet_prefill: device ordinal");
+    if (!allowed[dev].load(std::memory_order_acquire)) {
+        rc = check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(deltanet_chunk_state_kernel<DK, DV>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(shmem)),
+                       "hipFuncSetAttribute");
+        if (rc != HAI_OK) return rc;
+        allowed[dev].store(1, std::memory_order_release);
+    }
+    deltanet_chunk_state_kernel<DK, DV><<<dim3(a.nv, 1, a.B), dim3(64 * (DV / 32)), shmem, s>>>(a);
     rc = launched("deltanet_chunk_state_kernel");
     if (rc != HAI_OK) return rc;
     const int hist = a.Kc - 1;
