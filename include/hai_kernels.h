@@ -377,16 +377,20 @@ int hai_deltanet_verify_ab_bf16(void* out, int64_t ld_out, const void* proj,
                                 int64_t T, int64_t nk, int64_t nv, int64_t dk,
                                 int64_t dv, int64_t Kc, float eps, void* stream);
 /* The same layer over a prompt chunk (the prefill's conv + recurrence +
- * gated RMSNorm, hip_kernels.hip:871-912, 985-1095), tolerance mode: each
- * value column's recurrence over 16 threads (a head over dv/32 blocks), the
- * tokens in groups of 16 with the state in registers between groups, the
- * gated norm in a second kernel.  Sums regrouped, so equal to the canonical
- * recurrence to fp32 reassociation.  Arguments as hai_deltanet_verify_bf16
- * (proj columns [qkv | z | a | b] at the offsets, rows b*T + t); only the
- * final state is written (slot (L + T) % nslots), and the conv ring's
- * entries for the chunk's last Kc - 1 positions.  workspace holds the
- * unrounded outputs: hai_deltanet_prefill_workspace_bytes(B, T, nv, dv)
- * bytes, 16-byte aligned. */
+ * gated RMSNorm, hip_kernels.hip:871-912, 985-1095), tolerance mode: the
+ * chunkwise form of the gated delta rule over 32-token chunks (per chunk, in
+ * parallel: conv, gates, norms, Gram matrices and the triangular solve; then
+ * the state carried from chunk to chunk through dense products on the
+ * matrix cores, split-bf16 operands within ~2^-16 of fp32 products), the
+ * gated norm in a third kernel.  Sums regrouped, so equal to the canonical
+ * recurrence to fp32 rounding, not bit for bit.  Arguments as
+ * hai_deltanet_verify_bf16 (proj columns [qkv | z | a | b] at the offsets,
+ * rows b*T + t; proj and conv_ring 4-byte aligned, ld_proj and off_qkv
+ * even); only the final state is written (slot (L + T) % nslots), and the
+ * conv ring's entries for the chunk's last Kc - 1 positions.  workspace
+ * holds the unrounded outputs and the per-chunk records:
+ * hai_deltanet_prefill_workspace_bytes(B, T, nv, dv) bytes, 16-byte
+ * aligned. */
 size_t hai_deltanet_prefill_workspace_bytes(int64_t B, int64_t T, int64_t nv, int64_t dv);
 int hai_deltanet_prefill_bf16(void* out, int64_t ld_out, const void* proj,
                               int64_t ld_proj, int64_t off_qkv, int64_t off_z,

@@ -49,6 +49,14 @@ def test_argument_checks_need_no_device():
                                       128, 128, 4, 1e-6, None) == hai.ERR_INVALID  # T > 16
     assert k.hai_gqa_verify_bf16(p, p, p, p, p, 8, p, 1, 4, 4, 3, 64, None, 4, 8, None) == hai.ERR_INVALID
     assert b"gqa_verify" in k.hai_last_error()
+    # the prefill's conv reads channel pairs as dwords: proj and the ring 4-byte aligned, ld_proj and
+    # off_qkv even (B = 1, T = 4, one 128 x 128 head, 4 taps; the workspace size is checked after)
+    def prefill(proj, ld_proj, off_qkv, ring_ptr):
+        return k.hai_deltanet_prefill_bf16(p, 128, proj, ld_proj, off_qkv, 384, 512, 513, p, ring_ptr, 4, p, 1, p,
+                                           p, p, None, 0, 1, 4, 1, 1, 128, 128, 4, 1e-6, p, 1 << 30, None)
+    for args in ((ctypes.c_void_p(18), 514, 0, p), (p, 515, 0, p), (p, 514, 1, p), (p, 514, 0, ctypes.c_void_p(18))):
+        assert prefill(*args) == hai.ERR_INVALID
+        assert b"4-byte aligned" in k.hai_last_error(), k.hai_last_error()
 
 
 def test_noalloc_attention_bounds_its_shape_before_sizing():

@@ -20,14 +20,15 @@
 // into three launches:
 //   1. deltanet_chunk_prep_kernel, one block per (chunk, head, sequence), all
 //      chunks at once: conv + SiLU of the chunk's inputs, gates, q / k norms,
-//      the Gram matrices, the triangular solve for U and W^ (one thread per
-//      right-hand column, in order of t), and the scaled keys / queries
-//      K~ = e^{g_last - g} K, Q~ = e^{g} Q and P[t][s] = e^{g_t - g_s} q_t.k_s
-//      into a workspace;
-//   2. deltanet_chunk_state_kernel, one block per (head, 32 value columns,
-//      sequence), the chunks in order: W = U - W^ S, O = Q~ S + P W,
-//      S = e^{g_last} S + K~^T W -- three dense products per chunk, the state
-//      in LDS;
+//      the Gram matrices (matrix cores), the triangular solve for U and W^
+//      (one thread per right-hand column, in order of t), and the scaled keys
+//      / queries K~ = e^{g_last - g} K, Q~ = e^{g} Q and P[t][s] =
+//      e^{g_t - g_s} q_t.k_s into a per-chunk record, W^ / K~ / Q~ / P already
+//      split into bf16 pairs in the operand order of the next pass;
+//   2. deltanet_chunk_state_kernel, one block per (head, sequence), the chunks
+//      in order: W = U - W^ S, O = Q~ S + P W, S = e^{g_last} S + K~^T W --
+//      dense products on the matrix cores with the state held in their
+//      accumulators, each record copied global -> LDS one chunk ahead;
 //   3. deltanet_gated_norm_kernel: the gated RMSNorm per (token, head).
 // The state is stored once, to slot (L + T) % nslots, and the conv ring's
 // last entries by deltanet_ring_update_kernel.  The sums are reassociated
