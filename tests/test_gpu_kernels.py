@@ -503,7 +503,10 @@ def _attention_f64(q, g, kc, vc, T, L, nq, nkv, D):
     (8, 1, 24, 4, 256, [8190, 8000, 1, 63, 64, 127, 128, 4097]),  # C4 draft-like
     (6, 2, 24, 4, 256, [580, 10, 600, 511, 512, 513]),  # C5 verify-like
     (4, 4, 24, 4, 128, [8186, 300, 7000, 1]),
-    (8, 6, 8, 2, 64, [8100, 8000, 3, 64, 128, 4000, 8120, 500])])
+    (8, 6, 8, 2, 64, [8100, 8000, 3, 64, 128, 4000, 8120, 500]),
+    (1, 32, 24, 4, 256, [64]),  # prompt chunk, 192 query rows per KV head: the flash form, two blocks
+    (2, 24, 24, 4, 256, [500, 0]),  # flash form, ragged histories, a chunk with none
+    (1, 64, 24, 4, 256, [1000])])  # three flash blocks over 1064 keys
 def test_gqa_verify_mfma(B, T, nq, nkv, D, lens):
     """Tolerance-mode attention on the matrix cores against float64.  P is
     rounded to bf16 (unit roundoff 2^-8 per weight) before P.V, so an output

@@ -23,6 +23,7 @@
 // rows are bit-identical, and the CPU oracle follows the same order.
 #include <atomic>
 #include <cstdint>
+#include <cstdlib>
 #include <initializer_list>
 #include <mutex>
 #include <string>
@@ -378,6 +379,7 @@ int launch(uint16_t* out, const uint16_t* q, const uint16_t* gate, const uint16_
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kMfmaWaves = 4;
 constexpr int kCombineBlockSplits = 16;  // splits per query row from which the merge takes a block per row
@@ -813,6 +815,260 @@ __global__ __launch_bounds__(256) void gqa_mfma_combine_wave_kernel(uint16_t* __
     }
 }
 
+// ---------------------------------------------------------------------------
+// Prompt chunks: flash attention with a block's K / V tiles shared by its
+// waves.  Block = 4 waves x 32 query rows (one KV head, one sequence); each
+// wave walks every key its rows see, 64 keys per tile (two 32-key score tiles):
+//   S^T = K Q^T  on v_mfma_f32_32x32x16_bf16 (K rows the A operand from LDS,
+//                Q^T the B operand held in registers for the whole kernel);
+//   online softmax per query (base 2, the running max moved only past the
+//                same slack as gqa_mfma_partial_kernel, P rounded to bf16);
+//   O^T += V^T P^T  (V^T staged transposed in LDS; the result tile of S^T is
+//                the B operand of this product as it stands, under the key
+//                order 4 lh + q % 4 + 8 (q / 4) of k slot q).
+// K reaches LDS by global -> LDS copies, 16-byte piece p of key row r at
+// slot (D / 8) r + (p ^ (r % 16)); V through registers, transposed 8 keys x 8
+// dims per thread.  One barrier per tile.  The gated output O / l *
+// sigmoid(gate) is written directly: no split partials and no merge pass.
+// Same tolerance mode as the matrix-core verify attention.
+// ---------------------------------------------------------------------------
+constexpr int kFaRows = 128;  // query rows per block
+constexpr int kFaKeys = 64;   // keys per tile (two 32-key score tiles)
+
+template <int D>
+struct FaShape {
+    static constexpr int KP = D / 8;               // 16-byte pieces of a K row
+    static constexpr int K_SLOTS = kFaKeys * KP;   // K tile, 16-byte slots
+    static constexpr int VTR = kFaKeys + 8;        // V^T row: the tile's keys + 16-byte pad (bf16)
+    static constexpr int STAGE_BYTES = K_SLOTS * 16 + D * VTR * 2;
+    static constexpr int LDS_BYTES = 2 * STAGE_BYTES;
+    static constexpr int KCOPY = K_SLOTS / 256;    // copy instructions per thread and tile
+    static constexpr int NKK = D / 16;             // 16-dim k steps of S^T
+    static constexpr int NDT = D / 32;             // 32-dim tiles of O^T
+    static constexpr int NST = kFaKeys / 32;       // score tiles per key tile
+};
+
+template <int D>
+__global__ __launch_bounds__(256) void gqa_fa_kernel(uint16_t* __restrict__ out, const uint16_t* __restrict__ q,
+                                                     const uint16_t* __restrict__ gate, const uint16_t* kc,
+                                                     const uint16_t* vc, int64_t cap, int T, int nq, int nkv,
+                                                     const int32_t* lens, int len_add, float scale_log2) {
+    using S = FaShape<D>;
+    constexpr int NST = S::NST;
+    static_assert(D % 32 == 0 && S::K_SLOTS % 256 == 0 && kFaKeys % 32 == 0, "tile shapes");
+    constexpr float kNegInf = -__builtin_huge_valf();
+    extern __shared__ __align__(16) unsigned char fa_lds[];
+    const int qblk = blockIdx.x;
+    const int kvh = blockIdx.y;
+    const int b = blockIdx.z;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = wave_index();
+    const int lc = lane & 31;
+    const int lh = lane >> 5;
+    const int group = nq / nkv;
+    const int nqry = T * group;
+    const int64_t L = static_cast<int64_t>(lens ? lens[b] : 0) + len_add;
+    const int q0 = qblk * kFaRows;
+    // the lane's query (padding rows past nqry take the last token and are not stored)
+    const int qi = q0 + 32 * wave + lc;
+    const int tq = qi < nqry ? qi / group : T - 1;
+    const int64_t lim = L - T + tq + 1;  // keys [0, lim) are visible
+    const int t_last = (min(q0 + kFaRows, nqry) - 1) / group;
+    const int64_t nkeys = L - T + t_last + 1;  // keys any query of the block sees
+    const int ntiles = static_cast<int>((nkeys + kFaKeys - 1) / kFaKeys);
+
+    // Q^T operand: k step kk holds dims 16 kk + 8 lh + [0, 8) of the lane's query
+    u32x4 qr[S::NKK];
+    {
+        const int64_t row = (static_cast<int64_t>(b) * T + tq) * nq + kvh * group + (qi < nqry ? qi % group : 0);
+        const uint16_t* qp = q + row * D + 8 * lh;
+#pragma unroll
+        for (int kk = 0; kk < S::NKK; ++kk) qr[kk] = *reinterpret_cast<const u32x4*>(qp + 16 * kk);
+    }
+
+    const uint16_t* kbase = kc + (static_cast<int64_t>(b) * cap * nkv + kvh) * D;
+    const uint16_t* vbase = vc + (static_cast<int64_t>(b) * cap * nkv + kvh) * D;
+    const int64_t kstride = static_cast<int64_t>(nkv) * D;  // elements between consecutive keys
+    auto key_row = [&](int64_t key) { return min(key, L - 1) * kstride; };  // keys past L: the last row (masked)
+    // K copies: instruction i of this wave covers slots (4 i + wave) * 64 + lane
+    auto copy_k = [&](int tile, int buf) {
+        u32x4* dst = reinterpret_cast<u32x4*>(fa_lds + buf * S::STAGE_BYTES);
+#pragma unroll
+        for (int i = 0; i < S::KCOPY; ++i) {
+            const int s = (4 * i + wave) * 64 + lane;
+            const int r = s / S::KP, p = (s % S::KP) ^ (r & 15);
+            const uint16_t* src = kbase + key_row(static_cast<int64_t>(tile) * kFaKeys + r) + 8 * p;
+            __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(dst + (4 * i + wave) * 64),
+                                             16, 0, 0);
+        }
+    };
+    // V: thread (kq = tid / (D / 8), dp = tid % (D / 8)) loads keys VK kq + [0, VK) x dims 8 dp + [0, 8)
+    constexpr int VT_DIMS = D / 8;
+    constexpr int VK = kFaKeys * VT_DIMS / 256;  // keys per thread (8 at D = 256)
+    static_assert(VK == 4 || VK == 8, "V block per thread");
+    const int vkq = tid / VT_DIMS, vdp = tid % VT_DIMS;
+    u32x4 vr[VK];
+    auto load_v = [&](int tile) {
+#pragma unroll
+        for (int i = 0; i < VK; ++i)
+            vr[i] = *reinterpret_cast<const u32x4*>(
+                vbase + key_row(static_cast<int64_t>(tile) * kFaKeys + VK * vkq + i) + 8 * vdp);
+    };
+    auto stage_v = [&](int buf) {
+        uint16_t* vt = reinterpret_cast<uint16_t*>(fa_lds + buf * S::STAGE_BYTES + S::K_SLOTS * 16);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            // keys VK kq .. VK kq + VK - 1 of dim 8 dp + j
+            const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+            uint32_t d[VK / 2];
+#pragma unroll
+            for (int w = 0; w < VK / 2; ++w) d[w] = __builtin_amdgcn_perm(vr[2 * w + 1][j >> 1], vr[2 * w][j >> 1], sel);
+            uint16_t* dst = vt + (8 * vdp + j) * S::VTR + VK * vkq;
+            if constexpr (VK == 8) *reinterpret_cast<u32x4*>(dst) = u32x4{d[0], d[1], d[2], d[3]};
+            else *reinterpret_cast<uint2*>(dst) = make_uint2(d[0], d[1]);
+        }
+    };
+
+    float m = kNegInf, l = 0.0f;
+    f32x16 o[S::NDT];
+#pragma unroll
+    for (int dt = 0; dt < S::NDT; ++dt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[dt][i] = 0.0f;
+
+    if (ntiles > 0) {
+        copy_k(0, 0);
+        load_v(0);
+        stage_v(0);
+    }
+    __syncthreads();
+    const int ksw = lc & 15;  // swizzle of the lane's K rows
+    for (int j = 0; j < ntiles; ++j) {
+        const int buf = j & 1;
+        if (j + 1 < ntiles) {
+            copy_k(j + 1, buf ^ 1);
+            load_v(j + 1);
+        }
+        const u32x4* ks = reinterpret_cast<const u32x4*>(fa_lds + buf * S::STAGE_BYTES);
+        const uint16_t* vt = reinterpret_cast<const uint16_t*>(fa_lds + buf * S::STAGE_BYTES + S::K_SLOTS * 16);
+        // ---- S^T = K Q^T per 32-key score tile t: row = key 32 t + 8 (i / 4) + 4 lh + i % 4, column = the
+        // lane's query; the tiles' chains interleaved ----
+        f32x16 st[NST];
+#pragma unroll
+        for (int t = 0; t < NST; ++t)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) st[t][i] = 0.0f;
+#pragma unroll
+        for (int kk = 0; kk < S::NKK; ++kk)
+#pragma unroll
+            for (int t = 0; t < NST; ++t) {
+                const u32x4 ka = ks[(32 * t + lc) * S::KP + ((2 * kk + lh) ^ ksw)];
+                st[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, ka),
+                                                               __builtin_bit_cast(bf16x8, qr[kk]), st[t], 0, 0, 0);
+            }
+        // ---- online softmax of the lane's query over the tile ----
+        const int64_t k0 = static_cast<int64_t>(j) * kFaKeys;
+        float mx = kNegInf;
+#pragma unroll
+        for (int t = 0; t < NST; ++t)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int64_t key = k0 + 32 * t + 8 * (i >> 2) + 4 * lh + (i & 3);
+                const float x = key < lim ? st[t][i] * scale_log2 : kNegInf;
+                st[t][i] = x;
+                mx = fmaxf(mx, x);
+            }
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const bool grow = mx > m + kRescaleSlack;  // true for the first visible key
+        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+            const float mn = grow ? mx : m;
+            const float alpha = grow ? __builtin_amdgcn_exp2f(m - mn) : 1.0f;  // 0 from -inf
+            l *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < S::NDT; ++dt) o[dt] *= alpha;
+            m = mn;
+        }
+        const float sub = m == kNegInf ? 0.0f : m;  // no visible key yet: every p is 0
+        float ps = 0.0f;
+#pragma unroll
+        for (int t = 0; t < NST; ++t)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const float p = __builtin_amdgcn_exp2f(st[t][i] - sub);
+                st[t][i] = p;
+                ps += p;
+            }
+        l += ps;
+        // ---- O^T += V^T P^T: k step s covers keys 16 s + (4 lh + q % 4 + 8 (q / 4)), q the k slot ----
+#pragma unroll
+        for (int s = 0; s < 2 * NST; ++s) {
+            const f32x16& sp = st[s >> 1];
+            const int e = 8 * (s & 1);
+            const bf16x8 pb = bf16x8{static_cast<__bf16>(sp[e]), static_cast<__bf16>(sp[e + 1]),
+                                     static_cast<__bf16>(sp[e + 2]), static_cast<__bf16>(sp[e + 3]),
+                                     static_cast<__bf16>(sp[e + 4]), static_cast<__bf16>(sp[e + 5]),
+                                     static_cast<__bf16>(sp[e + 6]), static_cast<__bf16>(sp[e + 7])};
+#pragma unroll
+            for (int dt = 0; dt < S::NDT; ++dt) {
+                const uint16_t* vrow = vt + (32 * dt + lc) * S::VTR + 16 * s + 4 * lh;
+                const uint2 lo = *reinterpret_cast<const uint2*>(vrow);
+                const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 8);
+                const u32x4 va = u32x4{lo.x, lo.y, hi.x, hi.y};
+                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, va), pb, o[dt], 0, 0, 0);
+            }
+        }
+        if (j + 1 < ntiles) stage_v(buf ^ 1);
+        __syncthreads();  // the next tile is staged; this tile's buffer is free
+    }
+
+    // ---- O / l * sigmoid(gate), rounded: lane holds dims 32 dt + 8 (i / 4) + 4 lh + i % 4 ----
+    if (qi >= nqry) return;
+    l += __shfl_xor(l, 32);
+    const int64_t row = (static_cast<int64_t>(b) * T + tq) * nq + kvh * group + qi % group;
+#pragma unroll
+    for (int dt = 0; dt < S::NDT; ++dt)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+            const int d = 32 * dt + 8 * g4 + 4 * lh;
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = o[dt][4 * g4 + e] / l;
+            if (gate != nullptr) {
+                const uint2 gv = *reinterpret_cast<const uint2*>(gate + row * D + d);
+                v[0] *= csigmoid(lo_bf(gv.x));
+                v[1] *= csigmoid(hi_bf(gv.x));
+                v[2] *= csigmoid(lo_bf(gv.y));
+                v[3] *= csigmoid(hi_bf(gv.y));
+            }
+            *reinterpret_cast<uint2*>(out + row * D + d) = make_uint2(f2bf2(v[0], v[1]), f2bf2(v[2], v[3]));
+        }
+}
+
+// Compute units of the current device (one GPU model per process).
+inline int attn_device_cus() {
+    static std::atomic<int> cached{0};
+    const int known = cached.load(std::memory_order_relaxed);
+    if (known > 0) return known;
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0) {
+        cached.store(cus, std::memory_order_relaxed);
+        return cus;
+    }
+    return 256;  // MI355X
+}
+
+// The flash form for prompt chunks (HAI_ATTN_FA=0, read once per process,
+// keeps the split form for every shape).
+inline bool fa_enabled() {
+    static const bool on = [] {
+        const char* e = std::getenv("HAI_ATTN_FA");
+        return e == nullptr || e[0] != '0';
+    }();
+    return on;
+}
+
 // Split plan of the matrix-core path: steps per wave (block = 4 waves x steps
 // x KS keys) and the number of splits covering max_len.
 struct MfmaPlan {
@@ -845,6 +1101,30 @@ int launch_mfma(uint16_t* out, const uint16_t* q, const uint16_t* gate, const ui
                 int64_t cap, float* scratch, int B, int T, int nq, int nkv, const int32_t* lens, int len_add,
                 int64_t max_len, hipStream_t s) {
     const int64_t nqry = static_cast<int64_t>(T) * (nq / nkv);
+    if constexpr (D == 256) {
+        // prompt chunks: whole key ranges per block of 128 query rows, when
+        // those blocks fill the device (fewer, and the split form's key
+        // splits spread the work wider: 1 x 1024 rows 105 against 111 us)
+        constexpr size_t shmem = FaShape<D>::LDS_BYTES;
+        const int64_t fa_blocks = (nqry + kFaRows - 1) / kFaRows * nkv * B;
+        if (nqry >= kFaRows && fa_enabled() && fa_blocks >= attn_device_cus()) {
+            static std::atomic<uint8_t> allowed[64];
+            int dev = 0;
+            if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return invalid("gqa_verify_mfma: device");
+            if (!allowed[dev].load(std::memory_order_acquire)) {
+                const int rc = check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(gqa_fa_kernel<D>),
+                                                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                             static_cast<int>(shmem)),
+                                         "hipFuncSetAttribute");
+                if (rc != HAI_OK) return rc;
+                allowed[dev].store(1, std::memory_order_release);
+            }
+            const dim3 grid(static_cast<unsigned>((nqry + kFaRows - 1) / kFaRows), nkv, B);
+            const float sl2 = 1.4426950408889634f / __builtin_sqrtf(static_cast<float>(D));
+            gqa_fa_kernel<D><<<grid, dim3(256), shmem, s>>>(out, q, gate, kc, vc, cap, T, nq, nkv, lens, len_add, sl2);
+            return launched("gqa_fa_kernel");
+        }
+    }
     const void* kern = nqry <= 16 ? reinterpret_cast<const void*>(gqa_mfma_partial_kernel<D, 1>)
                                   : reinterpret_cast<const void*>(gqa_mfma_partial_kernel<D, 2>);
     const int64_t resident = resident_blocks(kern, 0);
