@@ -1639,17 +1639,18 @@ struct TiledArgs {
 
 // WM / WN: 16-row MFMA tiles per wave along X rows / weight rows; block =
 // 2 x 2 waves, output tile (32 WM) x (32 WN).
-template <int WM, int WN>
+template <int WM, int WN, int NWV = 4>
 __host__ __device__ constexpr size_t tiled_lds_bytes() {
-    return static_cast<size_t>(2) * (32 * WM + 32 * WN) * kTileRow * 2;
+    return static_cast<size_t>(2) * (16 * WM * (NWV / 2) + 32 * WN) * kTileRow * 2;
 }
 
-template <int WM, int WN, int EPI, bool FP8, bool CHECK, bool M32, int PIPE>
-__global__ __launch_bounds__(256) void gemm_tiled_kernel(TiledArgs a) {
-    constexpr int BM = 32 * WM;
+template <int WM, int WN, int EPI, bool FP8, bool CHECK, bool M32, int PIPE, int NWV>
+__global__ __launch_bounds__(64 * NWV) void gemm_tiled_kernel(TiledArgs a) {
+    constexpr int NT = 64 * NWV;
+    constexpr int BM = 16 * WM * (NWV / 2);
     constexpr int BN = 32 * WN;
-    constexpr int XP = BM * kTileK / 8 / 256;                 // 16-byte X pieces per thread
-    constexpr int WP = FP8 ? BN * kTileK / 16 / 256 : BN * kTileK / 8 / 256;  // W pieces per thread
+    constexpr int XP = BM * kTileK / 8 / NT;                 // 16-byte X pieces per thread
+    constexpr int WP = FP8 ? BN * kTileK / 16 / NT : BN * kTileK / 8 / NT;  // W pieces per thread
     static_assert(XP >= 1 && WP >= 1, "tile must split over the block");
     extern __shared__ __align__(16) uint16_t lds[];
     uint16_t* xs = lds;                      // [2][BM][kTileRow]
@@ -1699,14 +1700,14 @@ __global__ __launch_bounds__(256) void gemm_tiled_kernel(TiledArgs a) {
     int xdst[XP], wdst[WP];
 #pragma unroll
     for (int i = 0; i < XP; ++i) {
-        const int e = tid + 256 * i;
+        const int e = tid + NT * i;
         const int r = e >> 3, c = (e & 7) * 8;
         xoff[i] = static_cast<uint32_t>((r * a.ldx + c) * 2);
         xdst[i] = r * kTileRow + c;
     }
 #pragma unroll
     for (int i = 0; i < WP; ++i) {
-        const int e = tid + 256 * i;
+        const int e = tid + NT * i;
         if constexpr (FP8) {
             const int r = e >> 2, c = (e & 3) * 16;
             woff[i] = static_cast<uint32_t>(r * K + c);
@@ -1923,10 +1924,11 @@ int tiled_group_m() {
     return v;
 }
 
-template <int WM, int WN, int EPI, bool FP8, bool CHECK, bool M32 = false, int PIPE = 0>
+template <int WM, int WN, int EPI, bool FP8, bool CHECK, bool M32 = false, int PIPE = 0, int NWV = 4>
 int launch_tiled(TiledArgs a, hipStream_t s) {
-    constexpr size_t shmem = tiled_lds_bytes<WM, WN>();
-    auto* kern = gemm_tiled_kernel<WM, WN, EPI, FP8, CHECK, M32, PIPE>;
+    constexpr size_t shmem = tiled_lds_bytes<WM, WN, NWV>();
+    constexpr int BM = 16 * WM * (NWV / 2);
+    auto* kern = gemm_tiled_kernel<WM, WN, EPI, FP8, CHECK, M32, PIPE, NWV>;
     static std::atomic<uint8_t> allowed[64];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return invalid("gemm_tiled: device ordinal");
@@ -1936,18 +1938,19 @@ int launch_tiled(TiledArgs a, hipStream_t s) {
         if (rc != HAI_OK) return rc;
         allowed[dev].store(1, std::memory_order_release);
     }
-    a.mtiles = static_cast<int>((a.M + 32 * WM - 1) / (32 * WM));
+    a.mtiles = static_cast<int>((a.M + BM - 1) / BM);
     a.ntiles = static_cast<int>((a.N + 32 * WN - 1) / (32 * WN));
     a.group_m = tiled_group_m();
     const int64_t blocks = static_cast<int64_t>(a.mtiles) * a.ntiles;
-    kern<<<dim3(static_cast<unsigned>(blocks)), dim3(256), shmem, s>>>(a);
+    kern<<<dim3(static_cast<unsigned>(blocks)), dim3(64 * NWV), shmem, s>>>(a);
     return launched("gemm_tiled_kernel");
 }
 
 // HAI_TILED (read once per process) forces a tile form for measurements:
 // 1 = 128 x 64, 2 = 128 x 128 on 16 x 16 MFMAs, staged after the step's
 // MFMAs (the earlier kernel); 9 = 128 x 128, 10 = 128 x 64 on 32 x 32 MFMAs,
-// staged between them (the default forms).
+// staged between them; 30 = 256 x 256, 31 = 256 x 128 on 8-wave blocks
+// (bf16).  0 / unset: the choice below.
 int tiled_force() {
     static const int v = [] {
         const char* e = std::getenv("HAI_TILED");
@@ -1956,6 +1959,10 @@ int tiled_force() {
     return v;
 }
 
+// 8-wave forms (bf16, TFLOP/s at 1024 | 4096 rows; 128 x 128 in brackets):
+// 256 x 256 in_proj 707 | 1028 (810 | 936), q|gate|k|v 1120 | 1116 (794 |
+// 987), gate|up 778 | 1032 (816 | 932), out 416 | 769 (606 | 901); 256 x 128
+// out 668 | 876, down 791 | 957 (710 | 960).
 // Measured on MI355X (bf16 / FP8 TFLOP/s, 27B prompt GEMMs at 1024 | 4096
 // rows; the earlier 16 x 16 kernel in brackets): in_proj 824 | 951 (672 |
 // 786), FP8 664 | 805 (394 | 454); gate|up 830 | 929 (737 | 802), FP8 780 |
@@ -1970,11 +1977,31 @@ int dispatch_tiled(TiledArgs a, hipStream_t s) {
         case 1: return launch_tiled<4, 2, EPI, FP8, CHECK>(a, s);
         case 2: return launch_tiled<4, 4, EPI, FP8, CHECK>(a, s);
         case 10: return launch_tiled<4, 2, EPI, FP8, CHECK, true, 1>(a, s);
+        case 30:
+            if constexpr (!FP8) return launch_tiled<4, 8, EPI, FP8, CHECK, true, 1, 8>(a, s);
+            break;
+        case 31:
+            if constexpr (!FP8) return launch_tiled<4, 4, EPI, FP8, CHECK, true, 1, 8>(a, s);
+            break;
         default: break;
     }
     // 128-wide weight tiles unless they leave CUs without a tile
     const int64_t mt = (static_cast<int64_t>(a.M) + kTileM - 1) / kTileM;
     const int64_t tiles128 = mt * ((a.N + 127) / 128);
+    if constexpr (!FP8) {
+        // bf16: 8-wave blocks (2 waves per SIMD, one block per CU) with
+        // 256-row tiles read LDS half as often per product as the 4-wave
+        // 128 x 128 form; 256 x 256 where its tiles fill whole rounds of the
+        // CUs to 80 % or more, 256 x 128 where they fit one round
+        const int64_t cus = device_cus();
+        const int64_t mt256 = (static_cast<int64_t>(a.M) + 255) / 256;
+        const int64_t t256 = mt256 * ((a.N + 255) / 256);
+        const int64_t rounds = (t256 + cus - 1) / cus;
+        if (tiled_force() == 0 && tiles128 >= cus) {
+            if (5 * t256 >= 4 * rounds * cus) return launch_tiled<4, 8, EPI, FP8, CHECK, true, 1, 8>(a, s);
+            if (mt256 * ((a.N + 127) / 128) <= cus) return launch_tiled<4, 4, EPI, FP8, CHECK, true, 1, 8>(a, s);
+        }
+    }
     if (tiles128 >= 256 || tiled_force() == 9) return launch_tiled<4, 4, EPI, FP8, CHECK, true, 1>(a, s);
     return launch_tiled<4, 2, EPI, FP8, CHECK, true, 1>(a, s);
 }
