@@ -1949,8 +1949,8 @@ int launch_tiled(TiledArgs a, hipStream_t s) {
 // HAI_TILED (read once per process) forces a tile form for measurements:
 // 1 = 128 x 64, 2 = 128 x 128 on 16 x 16 MFMAs, staged after the step's
 // MFMAs (the earlier kernel); 9 = 128 x 128, 10 = 128 x 64 on 32 x 32 MFMAs,
-// staged between them; 30 = 256 x 256, 31 = 256 x 128 on 8-wave blocks
-// (bf16).  0 / unset: the choice below.
+// staged between them; 30 = 256 x 256 (bf16), 31 = 256 x 128 on 8-wave
+// blocks.  0 / unset: the choice below.
 int tiled_force() {
     static const int v = [] {
         const char* e = std::getenv("HAI_TILED");
@@ -1962,7 +1962,9 @@ int tiled_force() {
 // 8-wave forms (bf16, TFLOP/s at 1024 | 4096 rows; 128 x 128 in brackets):
 // 256 x 256 in_proj 707 | 1028 (810 | 936), q|gate|k|v 1120 | 1116 (794 |
 // 987), gate|up 778 | 1032 (816 | 932), out 416 | 769 (606 | 901); 256 x 128
-// out 668 | 876, down 791 | 957 (710 | 960).
+// out 668 | 876, down 791 | 957 (710 | 960); FP8 256 x 128: in_proj 664 |
+// 903 (649 | 814), q|gate|k|v 830 | 964 (688 | 847), gate|up 848 | 950
+// (793 | 833), out 679 | 842 (565 | 830), down 746 | 911 (615 | 852).
 // Measured on MI355X (bf16 / FP8 TFLOP/s, 27B prompt GEMMs at 1024 | 4096
 // rows; the earlier 16 x 16 kernel in brackets): in_proj 824 | 951 (672 |
 // 786), FP8 664 | 805 (394 | 454); gate|up 830 | 929 (737 | 802), FP8 780 |
@@ -1980,15 +1982,18 @@ int dispatch_tiled(TiledArgs a, hipStream_t s) {
         case 30:
             if constexpr (!FP8) return launch_tiled<4, 8, EPI, FP8, CHECK, true, 1, 8>(a, s);
             break;
-        case 31:
-            if constexpr (!FP8) return launch_tiled<4, 4, EPI, FP8, CHECK, true, 1, 8>(a, s);
-            break;
+        case 31: return launch_tiled<4, 4, EPI, FP8, CHECK, true, 1, 8>(a, s);
         default: break;
     }
     // 128-wide weight tiles unless they leave CUs without a tile
     const int64_t mt = (static_cast<int64_t>(a.M) + kTileM - 1) / kTileM;
     const int64_t tiles128 = mt * ((a.N + 127) / 128);
-    if constexpr (!FP8) {
+    if constexpr (FP8) {
+        // FP8: 256 x 128 on 8-wave blocks wherever 128 x 128 tiles fill the
+        // CUs (every 27B shape measured faster, 256 x 256 needs twice the
+        // accumulators: the per-scale-block sums are kept apart)
+        if (tiled_force() == 0 && tiles128 >= device_cus()) return launch_tiled<4, 4, EPI, FP8, CHECK, true, 1, 8>(a, s);
+    } else {
         // bf16: 8-wave blocks (2 waves per SIMD, one block per CU) with
         // 256-row tiles read LDS half as often per product as the 4-wave
         // 128 x 128 form; 256 x 256 where its tiles fill whole rounds of the
