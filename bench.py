@@ -471,8 +471,8 @@ def run_batch(hai, E, args, name: str, B: int, P: int, NEW: int, width: int, fp8
     cfg = E.QWEN27B
     t0 = time.perf_counter()
     cap = P + (width + 2) * NEW + 32
-    eng = E.Engine(cfg, max_context=cap, max_verify_tokens=16, fp8=fp8, batch=B, mfma=True,
-                   prefill_rows=args.batch_prefill_rows)
+    prows = min(args.batch_prefill_rows, P)
+    eng = E.Engine(cfg, max_context=cap, max_verify_tokens=16, fp8=fp8, batch=B, mfma=True, prefill_rows=prows)
     eng.init_synthetic(seed=0, std=0.02)
     hai.synchronize()
     log(f"[{name}] engine up: B={B}, {eng.weight_bytes() / 1e9:.2f} GB weights, {time.perf_counter() - t0:.1f}s")
@@ -498,7 +498,7 @@ def run_batch(hai, E, args, name: str, B: int, P: int, NEW: int, width: int, fp8
         "verify_bytes": round(prof["step_bytes"]), "verify_hbm_frac": round(step_gbs / HBM_PEAK_GBS, 4),
         "gemm_gb_s": round(gemm_gbs, 1), "gemm_launches": prof["gemm_launches"],
         "draft_ms": round(prof["draft_ms"], 3), "prefill_s": round(prefill_s, 3),
-        "prefill_tok_s": round(B * P / prefill_s, 1), "prefill_rows_per_chunk": args.batch_prefill_rows,
+        "prefill_tok_s": round(B * P / prefill_s, 1), "prefill_rows_per_chunk": prows,
         "acceptance_rate": round(nat["accepted"] / max(1, nat["proposed"]), 4),
     }
     log(f"[{name}] natural proposals: {nat['tokens']} tokens in {nat['seconds']:.2f}s over {nat['rounds']} sampled "
@@ -540,8 +540,9 @@ def main():
     ap.add_argument("--prefill-rows", type=int, default=1024,
                     help="prompt rows per fast-prefill chunk of the bs=1 engines (the verify-path prefill is "
                          "timed beside it)")
-    ap.add_argument("--batch-prefill-rows", type=int, default=512,
-                    help="prompt rows per sequence and fast-prefill chunk of the C4 / C5 engines")
+    ap.add_argument("--batch-prefill-rows", type=int, default=1024,
+                    help="prompt rows per sequence and fast-prefill chunk of the C4 / C5 engines (C4 8 x 8192: "
+                         "512 rows 3.85 s, 1024 rows 3.60 s, 2048 rows 3.57 s)")
     ap.add_argument("--new", type=int, default=256)
     ap.add_argument("--width", type=int, default=1)
     ap.add_argument("--profile-iters", type=int, default=5)
