@@ -376,6 +376,41 @@ int hai_deltanet_verify_ab_bf16(void* out, int64_t ld_out, const void* proj,
                                 const int32_t* lens, int32_t pos_add, int64_t B,
                                 int64_t T, int64_t nk, int64_t nv, int64_t dk,
                                 int64_t dv, int64_t Kc, float eps, void* stream);
+/* hai_deltanet_verify_bf16 (or, with w_ab non-null, hai_deltanet_verify_ab_bf16:
+ * off_a / off_b are then unused) with rollback records in place of the
+ * per-token states: the rollback that deltanet_recurrent_kernel's callers
+ * get from the reference's state snapshots (generator.cc:909-1021), at 1 KB
+ * per token instead of a dk x dv fp32 state.
+ *   records is [nslots][B][nv][dk + dv + 4] fp32
+ *     (hai_deltanet_records_bytes, 16-byte aligned): every token at position
+ *     p leaves in slot p % nslots the update it applied to the state,
+ *     beta * k^ (dk floats), c_j = v_j - k^T (decay * S)_j for every value
+ *     column j (dv) and decay, so that S' = fma(beta * k^, c, S * decay);
+ *   only the final state of the call is stored (slot (L + T) % nslots);
+ *   replay = 0: the call starts from the state held in slot L % nslots and
+ *     stores its start positions L in base[b];
+ *   replay = 1 (T <= 4): the call starts from the state of position base[b]
+ *     (slot base[b] % nslots, as a replay = 0 call left it) and re-applies
+ *     the records of positions base[b] .. L - 1 (written by that call), bit
+ *     for bit the updates it made, before its own tokens; base is not
+ *     changed.  A sequence with L - base[b] outside [0, min(nslots - 1, 16)]
+ *     starts from slot L % nslots instead.
+ * So after a replay = 0 call of T tokens, keeping any prefix of a + 1 of
+ * them needs no copy: a replay = 1 call at L = base + a + 1 continues from
+ * the state after that prefix.  Needs nslots > T; other arguments and
+ * checks as hai_deltanet_verify_bf16 / _ab_bf16. */
+size_t hai_deltanet_records_bytes(int64_t nslots, int64_t B, int64_t nv, int64_t dk, int64_t dv);
+int hai_deltanet_verify_rec_bf16(void* out, int64_t ld_out, const void* proj,
+                                 int64_t ld_proj, int64_t off_qkv, int64_t off_z,
+                                 int64_t off_a, int64_t off_b, const void* xn,
+                                 int64_t ld_xn, const void* w_ab, int64_t H,
+                                 const void* conv_w, void* conv_ring, int64_t ring,
+                                 float* state, int64_t nslots, float* records,
+                                 int32_t* base, int replay, const void* a_log,
+                                 const void* dt_bias, const void* norm_w,
+                                 const int32_t* lens, int32_t pos_add, int64_t B,
+                                 int64_t T, int64_t nk, int64_t nv, int64_t dk,
+                                 int64_t dv, int64_t Kc, float eps, void* stream);
 /* The same layer over a prompt chunk (the prefill's conv + recurrence +
  * gated RMSNorm, hip_kernels.hip:871-912, 985-1095), tolerance mode: the
  * chunkwise form of the gated delta rule over 32-token chunks (per chunk, in

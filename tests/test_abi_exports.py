@@ -59,6 +59,29 @@ def test_argument_checks_need_no_device():
         assert b"4-byte aligned" in k.hai_last_error(), k.hai_last_error()
 
 
+def test_deltanet_records_checks_need_no_device():
+    """hai_deltanet_verify_rec_bf16 rejects, before any device call: no
+    records or base buffer, unaligned records, nslots <= T (the final state
+    would overwrite the replay's start slot), replay outside {0, 1} and a
+    replay call of more than 4 tokens; the records size is
+    nslots x B x nv x (dk + dv + 4) floats, SIZE_MAX on overflow."""
+    k = hai.kernels()
+    p = ctypes.c_void_p(16)  # never dereferenced
+    assert k.hai_deltanet_records_bytes(5, 2, 48, 128, 128) == 5 * 2 * 48 * 260 * 4
+    assert k.hai_deltanet_records_bytes(1 << 40, 1 << 40, 48, 128, 128) == 2 ** 64 - 1
+
+    def call(records, base, replay, T, nslots):
+        return k.hai_deltanet_verify_rec_bf16(p, 512, p, 1280, 0, 768, 1024, 1028, None, 0, None, 0, p, p, 8, p,
+                                              nslots, records, base, replay, p, p, p, p, 0, 1, T, 2, 4, 64, 64, 4,
+                                              1e-6, None)
+    for args, what in (((None, p, 0, 2, 5), b"null records"), ((p, None, 0, 2, 5), b"null base"),
+                       ((ctypes.c_void_p(24), p, 0, 2, 5), b"records alignment"),
+                       ((p, p, 0, 5, 5), b"nslots > T"), ((p, p, 2, 2, 5), b"replay must be"),
+                       ((p, p, 1, 5, 8), b"at most 4 tokens")):
+        assert call(*args) == hai.ERR_INVALID, what
+        assert what in k.hai_last_error(), (what, k.hai_last_error())
+
+
 def test_noalloc_attention_bounds_its_shape_before_sizing():
     """hai_gqa_verify_noalloc_bf16 checks every operand of the scratch size
     before computing it: a batch past int32, a bad head_dim or nkv, or a

@@ -611,6 +611,95 @@ def test_deltanet_verify_rollback(nk, nv, dk, dv, steps, split):
         assert np.array_equal(dev_state.view(np.uint32), want_state.view(np.uint32)), f"state after step {si}"
 
 
+@pytest.mark.parametrize("nk,nv,dk,B,ab,rounds", [
+    (4, 4, 64, 2, False, [(2, [1, 2]), (3, [3, 1]), (4, [2, 4]), (1, [1, 1]), (4, [1, 3])]),
+    (16, 48, 128, 2, True, [(2, [1, 2]), (2, [2, 2]), (4, [3, 1]), (2, [1, 1])]),
+    (2, 6, 64, 3, True, [(3, [1, 2, 3]), (4, [4, 4, 1]), (1, [1, 1, 1])]),
+])
+def test_deltanet_records_replay_equals_per_token_slots(nk, nv, dk, B, ab, rounds):
+    """Verify rounds of B sequences, each keeping its own prefix of the T
+    tokens (a + 1 of them) followed by a one-token correction, run twice:
+    with per-token state slots (write_all_slots: the correction reads the
+    kept prefix's slot) and with rollback records (hai_deltanet_verify_rec_bf16:
+    only the final state, replay = 1 for the correction from the verify's
+    start).  Outputs of every call, the committed states and the conv rings
+    bit for bit.  A round in which every sequence keeps all T tokens goes
+    straight to the next verify; in the other rounds every sequence takes the
+    correction, also one that kept all T (the engine's lockstep batches: its
+    replay re-applies all T records).  With ab: the a|b projection formed in
+    the kernel."""
+    rng = np.random.default_rng(nk * 100 + nv * 10 + B)
+    dv = dk
+    kw, vw = nk * dk, nv * dv
+    C = 2 * kw + vw
+    H = 128
+    Kc = 4
+    width = C + vw + 2 * nv
+    ring, nslots = 16, 5
+    cw, cwb = rand_bf16(rng, (C, Kc), 0.3)
+    al, alb = rand_bf16(rng, (nv,), 0.5)
+    dt, dtb = rand_bf16(rng, (nv,), 0.5)
+    nw, nwb = rand_bf16(rng, (dv,), 0.5)
+    wab, wabb = rand_bf16(rng, (2 * nv, H), 0.05)
+    st0 = (rng.standard_normal(nslots * B * nv * dk * dv) * 0.1).astype(np.float32)
+    lens0 = np.array([2 + 3 * b for b in range(B)], np.int32)
+    dcw, dal, ddt, dnw, dwab = dev(cwb), dev(alb), dev(dtb), dev(nwb), dev(wabb)
+    rec_bytes = kern().hai_deltanet_records_bytes(nslots, B, nv, dk, dv)
+    assert rec_bytes == nslots * B * nv * (dk + dv + 4) * 4
+    inputs = []
+    for T, keep in rounds:
+        _, pb = rand_bf16(rng, (B * T, width))
+        _, xnb = rand_bf16(rng, (B * T, H))
+        _, cpb = rand_bf16(rng, (B, width))
+        _, cxb = rand_bf16(rng, (B, H))
+        inputs.append((T, keep, pb, xnb, cpb, cxb))
+
+    def run(records):
+        dstate, dring, lens = dev(st0), out_buf(B * ring * C * 2), dev(lens0)
+        drec, dbase = (out_buf(rec_bytes), out_buf(B * 4)) if records else (None, None)
+        L = lens0.astype(np.int64).copy()
+        outs = []
+
+        def call(T, pb, xnb, mode):
+            dout, dproj, dxn = out_buf(B * T * vw * 2), dev(pb), dev(xnb)
+            common = (dout.ptr, vw, dproj.ptr, width, 0, C)
+            if records:
+                hai.check(kern().hai_deltanet_verify_rec_bf16(
+                    *common, C + vw, C + vw + nv, dxn.ptr if ab else None, H if ab else 0, dwab.ptr if ab else None,
+                    H if ab else 0, dcw.ptr, dring.ptr, ring, dstate.ptr, nslots, drec.ptr, dbase.ptr,
+                    1 if mode == "correction" else 0, dal.ptr, ddt.ptr, dnw.ptr, lens.ptr, 0, B, T, nk, nv, dk, dv,
+                    Kc, 1e-6, None), "deltanet rec")
+            else:
+                tail = (dcw.ptr, dring.ptr, ring, dstate.ptr, nslots, 1 if mode == "verify" else 0, dal.ptr,
+                        ddt.ptr, dnw.ptr, lens.ptr, 0, B, T, nk, nv, dk, dv, Kc, 1e-6)
+                if ab:
+                    hai.check(kern().hai_deltanet_verify_ab_bf16(*common, dxn.ptr, H, dwab.ptr, H, *tail, None), "ab")
+                else:
+                    hai.check(kern().hai_deltanet_verify_bf16(*common, C + vw, C + vw + nv, *tail, None), "dn")
+            outs.append(dout.download(np.uint16))
+
+        for T, keep, pb, xnb, cpb, cxb in inputs:
+            lens.upload(L.astype(np.int32))
+            call(T, pb, xnb, "verify")
+            L = L + np.array(keep)
+            if not all(k == T for k in keep):
+                lens.upload(L.astype(np.int32))
+                call(1, cpb, cxb, "correction")
+                L = L + 1
+        lens_np = L
+        st = dstate.download(np.float32).reshape(nslots, B, nv * dk * dv)
+        committed = np.stack([st[lens_np[b] % nslots, b] for b in range(B)])
+        return outs, committed, dring.download(np.uint16)
+
+    o_ref, st_ref, ring_ref = run(False)
+    o_rec, st_rec, ring_rec = run(True)
+    assert len(o_ref) == len(o_rec)
+    for i, (a, b) in enumerate(zip(o_ref, o_rec)):
+        assert np.array_equal(a, b), f"call {i}: outputs differ"
+    assert np.array_equal(st_ref.view(np.uint32), st_rec.view(np.uint32)), "committed states differ"
+    assert np.array_equal(ring_ref, ring_rec), "conv rings differ"
+
+
 @pytest.mark.parametrize("nk,nv,dk,T,Kc", [(2, 6, 64, 37, 4), (16, 48, 128, 100, 4), (4, 4, 64, 16, 3),
                                          (16, 48, 128, 32, 4)])
 def test_deltanet_prefill_against_oracle(nk, nv, dk, T, Kc):

@@ -95,6 +95,8 @@ _KERNEL_SIGS = {
                                     VP, VP, VP, I32, I64, I64, I64, I64, I64, I64, I64, F32, VP, I64, VP],
     "hai_deltanet_verify_ab_bf16": [VP, I64, VP, I64, I64, I64, VP, I64, VP, I64, VP, VP, I64, VP, I64, ctypes.c_int,
                                     VP, VP, VP, VP, I32, I64, I64, I64, I64, I64, I64, I64, F32, VP],
+    "hai_deltanet_verify_rec_bf16": [VP, I64, VP, I64, I64, I64, I64, I64, VP, I64, VP, I64, VP, VP, I64, VP, I64, VP,
+                                     VP, ctypes.c_int, VP, VP, VP, VP, I32, I64, I64, I64, I64, I64, I64, I64, F32, VP],
     "hai_deltanet_prefill_bf16": [VP, I64, VP, I64, I64, I64, I64, I64, VP, VP, I64, VP, I64, VP, VP, VP, VP, I32,
                                   I64, I64, I64, I64, I64, I64, I64, F32, VP, I64, VP],
     "hai_argmax_rows_bf16": [VP, VP, I64, I64, I64, VP, VP],
@@ -123,6 +125,7 @@ _SIZE_SIGS = {
     "hai_argmax_scratch_bytes": [I64, I64],
     "hai_deltanet_workspace_bytes": [I64, I64, I64],
     "hai_deltanet_prefill_workspace_bytes": [I64, I64, I64, I64],
+    "hai_deltanet_records_bytes": [I64, I64, I64, I64, I64],
 }
 
 _kern = None

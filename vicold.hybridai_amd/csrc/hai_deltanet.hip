@@ -17,7 +17,15 @@
 //     instruction of the block covers one contiguous span;
 //   * rollback needs no copies: the state after sequence length L is kept in
 //     slot L % nslots and the conv inputs in a ring indexed by position, so
-//     accepting a prefix only moves the committed length.
+//     accepting a prefix only moves the committed length;
+//   * or (records mode) only the final state is stored, and every token
+//     leaves a record of its rank-1 update instead -- beta * k^ (dk floats),
+//     the correction c_j = v_j - k^T (decay S)_j of every value column (dv)
+//     and the decay -- in slot position % nslots of a record buffer.  A later
+//     call that starts at a committed length inside that span reads the
+//     state the span started from and re-applies the kept records,
+//     S = fma(beta k^, c, S * decay): the operations of the token loop, so
+//     the state is the same to the bit, for 1 KB per token instead of 64 KB.
 // No MFMA: the update is a rank-1 correction per token, bandwidth and latency
 // bound.
 #include "hai_common.h"
@@ -29,6 +37,7 @@ using namespace hai;
 
 constexpr int kMaxT = 16;   // tokens per launch (verify width k + 1 <= 16)
 constexpr int kMaxKc = 8;   // conv taps
+constexpr int kMaxReplayT = 4;  // tokens of a call that replays records
 
 struct DnArgs {
     uint16_t* out;
@@ -57,7 +66,18 @@ struct DnArgs {
     // kMaxT tokens runs as launches of kMaxT; each sees its own T but the
     // whole call's row layout.
     int64_t seq_rows;
+    // records mode (rec non-null): [nslots][B][nv][dk + dv + 4] update
+    // records, written for every token; only the final state is stored.
+    // base [B]: replay = 0 stores each sequence's start position there
+    // (base_out); replay = 1 starts from the state at base[b] and re-applies
+    // the records of positions base[b] .. p0 - 1 first.
+    float* rec;
+    int32_t* base;
+    int replay, base_out;
 };
+
+// floats per update record: beta * k^ (DK), the column corrections (DV), decay, pad
+__host__ __device__ constexpr int64_t record_floats(int64_t dk, int64_t dv) { return dk + dv + 4; }
 
 constexpr int kSeg = 2048;  // the linear layers' fma segment (elements)
 
@@ -69,12 +89,13 @@ constexpr int kSeg = 2048;  // the linear layers' fma segment (elements)
 // REF = true: the reference's deltanet_recurrent contract -- q, k, v already
 //   convolved, a/b/z in their own [T, ...] buffers, one fp32 state
 //   [nv][dk][dv] (hip_kernels.hip:985-1095) updated in place.
-template <int DK, int DV, bool REF>
+// TM bounds T (registers per thread for the inputs and outputs of all tokens).
+template <int DK, int DV, bool REF, int TM>
 __global__ __launch_bounds__(DV * 4) void deltanet_kernel(DnArgs A) {
     constexpr int NT = DV * 4;
     constexpr int NW = NT / 64;
     constexpr int GI = DK / 4;            // key dims per thread
-    constexpr int ZP = kMaxT * DV / NT;   // output elements per thread (all tokens)
+    constexpr int ZP = (TM * DV + NT - 1) / NT;  // output elements per thread (all tokens)
     const int T = A.T;
     extern __shared__ __align__(16) float smem[];
     float* qs = smem;                  // [T][DK] conv output, q channels (then q * q-norm scale)
@@ -83,6 +104,7 @@ __global__ __launch_bounds__(DV * 4) void deltanet_kernel(DnArgs A) {
     float* os = vs + T * DV;           // [T][DV] unrounded recurrent output
     float* bks = os + T * DV;          // [T][DK] beta * normalised k
     float* abp = bks + T * DK;         // w_ab: [T][2][nseg][64] lane partials of the a / b dot segments
+    float* rls = abp + (A.w_ab != nullptr ? 2 * T * ((A.H + kSeg - 1) / kSeg) * 64 : 0);  // replayed records
     __shared__ float s_q[kMaxT], s_k[kMaxT], s_decay[kMaxT], s_beta[kMaxT], s_rms[kMaxT];
 
     const int h = blockIdx.x;
@@ -111,9 +133,9 @@ __global__ __launch_bounds__(DV * 4) void deltanet_kernel(DnArgs A) {
     if (cl >= DK && cl < 2 * DK) { dst = ks; di = cl - DK; }
     else if (cl >= 2 * DK) { dst = vs; di = cl - 2 * DK; dstride = DV; }
     // window: vals[i] = input at position p0 - hist + i (history, then the T new tokens)
-    uint16_t vals[kMaxT + kMaxKc - 1];
+    uint16_t vals[TM + kMaxKc - 1];
 #pragma unroll
-    for (int i = 0; i < kMaxT + kMaxKc - 1; ++i) vals[i] = 0;
+    for (int i = 0; i < TM + kMaxKc - 1; ++i) vals[i] = 0;
     float wc[kMaxKc];
     int64_t c = 0;
     if (cl < DK) c = static_cast<int64_t>(gq) * DK + cl;
@@ -128,12 +150,12 @@ __global__ __launch_bounds__(DV * 4) void deltanet_kernel(DnArgs A) {
             else if (cl < 2 * DK) { srcp = A.k; ld = kw; col = static_cast<int64_t>(gq) * DK + cl - DK; }
             else { srcp = A.v; ld = vw; col = static_cast<int64_t>(h) * DV + cl - 2 * DK; }
 #pragma unroll
-            for (int t = 0; t < kMaxT; ++t) vals[t] = t < T ? srcp[t * ld + col] : uint16_t{0};
+            for (int t = 0; t < TM; ++t) vals[t] = t < T ? srcp[t * ld + col] : uint16_t{0};
         } else {
 #pragma unroll
             for (int i = 0; i < kMaxKc; ++i) wc[i] = i < A.Kc ? bf2f(A.conv_w[c * A.Kc + i]) : 0.0f;
 #pragma unroll
-            for (int t = 0; t < kMaxT; ++t) {
+            for (int t = 0; t < TM; ++t) {
                 uint16_t x = 0;
                 if (t < T) x = A.proj[(row0 + t) * A.ld_proj + A.off_qkv + c];
                 // the new tokens go right after the hist history entries
@@ -175,6 +197,28 @@ __global__ __launch_bounds__(DV * 4) void deltanet_kernel(DnArgs A) {
     // ---- then the length-dependent ones: the state slot and the conv
     // history (one modulo each; later positions advance with a wrap) ----
     const int64_t p0 = REF ? 0 : static_cast<int64_t>(A.lens ? A.lens[b] : 0) + A.pos_add;
+    // records mode: the state read is that of position ps, followed by the
+    // nrep records of positions ps .. p0 - 1 (a start outside the record
+    // span reads slot p0 % nslots as the other modes do)
+    int64_t ps = p0;
+    int nrep = 0;
+    if constexpr (!REF) {
+        // (replays are compiled into the short-call instantiations only: the
+        // host runs them with T <= kMaxReplayT)
+        if (TM <= kMaxReplayT && A.replay) {
+            const int64_t pb = A.base[b];
+            if (pb <= p0 && p0 - pb < A.nslots && p0 - pb <= kMaxT) {
+                ps = pb;
+                nrep = static_cast<int>(p0 - pb);
+            }
+        } else if (A.base_out && h == 0 && tid == 0) {
+            A.base[b] = static_cast<int32_t>(p0);
+        }
+    }
+    constexpr int64_t RS = record_floats(DK, DV);
+    constexpr int RQ = static_cast<int>(RS / 4);  // float4 per record
+    float4 rq0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    int64_t rec_r = 0;  // record slot of position ps
     float S[GI];  // column j, key dims [g*GI, g*GI+GI)
     int64_t slot_w = 0, ring_w = 0;  // state slot after token 0, ring entry of token 0
     if constexpr (REF) {
@@ -184,8 +228,9 @@ __global__ __launch_bounds__(DV * 4) void deltanet_kernel(DnArgs A) {
     } else {
         const int64_t slot = p0 % A.nslots;
         slot_w = slot + 1 == A.nslots ? 0 : slot + 1;
+        const int64_t slot_r = slot >= nrep ? slot - nrep : slot - nrep + A.nslots;  // ps % nslots
         const float4* src =
-            reinterpret_cast<const float4*>(A.state + ((slot * A.B + b) * nv + h) * static_cast<int64_t>(DV) * DK) +
+            reinterpret_cast<const float4*>(A.state + ((slot_r * A.B + b) * nv + h) * static_cast<int64_t>(DV) * DK) +
             tid;
 #pragma unroll
         for (int m = 0; m < GI / 4; ++m) {
@@ -210,6 +255,16 @@ __global__ __launch_bounds__(DV * 4) void deltanet_kernel(DnArgs A) {
                 if (i < hist) rp = rp + 1 == A.ring_n ? 0 : rp + 1;
         }
         ring_w = rp;
+        // records mode, replay: the kept records of positions ps .. p0 - 1
+        // are staged in LDS (rls) for the token loop; each thread's first
+        // piece is requested here with the state, the rest (more than 7
+        // records) where they are stored
+        rec_r = slot_r;
+        if (tid < nrep * RQ) {
+            const int i = tid / RQ;
+            const int64_t rs = rec_r + i < A.nslots ? rec_r + i : rec_r + i - A.nslots;
+            rq0 = reinterpret_cast<const float4*>(A.rec + ((rs * A.B + b) * nv + h) * RS)[tid - i * RQ];
+        }
     }
 
     // ---- a|b projection of this head (w_ab mode): the 2T dot products of
@@ -253,13 +308,13 @@ __global__ __launch_bounds__(DV * 4) void deltanet_kernel(DnArgs A) {
     if (has_ch) {
         if constexpr (REF) {
 #pragma unroll
-            for (int t = 0; t < kMaxT; ++t)
+            for (int t = 0; t < TM; ++t)
                 if (t < T) dst[t * dstride + di] = bf2f(vals[t]);
         } else {
             const bool writer = cl >= 2 * DK || (h % group) == 0;
             int64_t rw = ring_w;  // ring entry of position p0 + t
 #pragma unroll
-            for (int t = 0; t < kMaxT; ++t) {
+            for (int t = 0; t < TM; ++t) {
                 if (t < T) {
                     float acc = bf2f(vals[t]) * wc[0];
 #pragma unroll
@@ -284,6 +339,17 @@ __global__ __launch_bounds__(DV * 4) void deltanet_kernel(DnArgs A) {
         const float sp = fmaxf(dtv, 0.0f) + clog1p(cexp(-fabsf(dtv)));
         s_decay[lane] = cexp(-(cexp(alog) * sp));
         s_beta[lane] = csigmoid(b_in);
+    }
+    if constexpr (!REF) {
+        // replayed records into LDS (read before this barrier, so before any
+        // thread of this (sequence, head) rewrites one in the token loop)
+        if (tid < nrep * RQ) reinterpret_cast<float4*>(rls)[tid] = rq0;
+        for (int e = tid + NT; e < nrep * RQ; e += NT) {
+            const int i = e / RQ;
+            const int64_t rs = rec_r + i < A.nslots ? rec_r + i : rec_r + i - A.nslots;
+            reinterpret_cast<float4*>(rls)[e] =
+                reinterpret_cast<const float4*>(A.rec + ((rs * A.B + b) * nv + h) * RS)[e - i * RQ];
+        }
     }
     __syncthreads();
 
@@ -335,7 +401,27 @@ __global__ __launch_bounds__(DV * 4) void deltanet_kernel(DnArgs A) {
     __syncthreads();
 
     // ---- gated delta rule, token by token (column-local: no block barrier) ----
-    for (int t = 0; t < T; ++t) {
+    int64_t rec_slot = p0 % A.nslots;  // records mode: record slot of token t
+    // replayed records first (t < 0, uniform over the block): the update of
+    // the token loop with the kept beta * k^, correction and decay
+    for (int t = -nrep; t < T; ++t) {
+        if (t < 0) {
+            const float* rr = rls + (t + nrep) * RS;
+            const float dc = rr[DK + DV];
+            const float cr = rr[DK + j];
+            const float4* br = reinterpret_cast<const float4*>(rr + g * GI);
+#pragma unroll
+            for (int m = 0; m < GI / 4; ++m) {
+                const float4 b4 = br[m];
+                const float bv[4] = {b4.x, b4.y, b4.z, b4.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    S[4 * m + e] = S[4 * m + e] * dc;
+                    S[4 * m + e] = fma_(bv[e], cr, S[4 * m + e]);
+                }
+            }
+            continue;
+        }
         const float decay = s_decay[t];
         const float4* qt = reinterpret_cast<const float4*>(qs + t * DK + g * GI);
         const float4* kt = reinterpret_cast<const float4*>(ks + t * DK + g * GI);
@@ -354,6 +440,16 @@ __global__ __launch_bounds__(DV * 4) void deltanet_kernel(DnArgs A) {
         r = r + quad_xor1(r);
         r = r + quad_xor2(r);
         const float cj = vs[t * DV + j] - r;
+        if constexpr (!REF) {
+            if (A.rec != nullptr) {
+                float* rr = A.rec + ((rec_slot * A.B + b) * nv + h) * RS;
+                if (tid < DK / 4)
+                    *reinterpret_cast<float4*>(rr + 4 * tid) = *reinterpret_cast<const float4*>(bks + t * DK + 4 * tid);
+                if (g == 0) rr[DK + j] = cj;
+                if (tid == 0) rr[DK + DV] = decay;
+                rec_slot = rec_slot + 1 == A.nslots ? 0 : rec_slot + 1;
+            }
+        }
         float o = 0.0f;
 #pragma unroll
         for (int m = 0; m < GI / 4; ++m) {
@@ -732,12 +828,26 @@ __global__ __launch_bounds__(256) void deltanet_conv_kernel(uint16_t* __restrict
         if (i < hist) st[i] = f2bf(win[i]);
 }
 
+template <int DK, int DV, bool REF, int TM>
+int launch_tm(const DnArgs& a, hipStream_t s) {
+    const size_t ab = a.w_ab != nullptr ? static_cast<size_t>(2 * a.T) * ((a.H + kSeg - 1) / kSeg) * 64 : 0;
+    // replay: up to kMaxT records of the span staged
+    const size_t rq = a.replay && a.T <= kMaxReplayT ? static_cast<size_t>(a.nslots - 1 < kMaxT ? a.nslots - 1 : kMaxT) *
+                                     record_floats(DK, DV) : 0;
+    const size_t shmem = (static_cast<size_t>(a.T) * (3 * DK + 2 * DV) + ab + rq) * sizeof(float);
+    deltanet_kernel<DK, DV, REF, TM><<<dim3(a.nv, REF ? 1 : a.B), dim3(DV * 4), shmem, s>>>(a);
+    return launched(REF ? "deltanet_recurrent_kernel" : "deltanet_verify_kernel");
+}
+
+// the smallest token bound of the instantiations that covers T
 template <int DK, int DV, bool REF>
 int launch(const DnArgs& a, hipStream_t s) {
-    const size_t ab = a.w_ab != nullptr ? static_cast<size_t>(2 * a.T) * ((a.H + kSeg - 1) / kSeg) * 64 : 0;
-    const size_t shmem = (static_cast<size_t>(a.T) * (3 * DK + 2 * DV) + ab) * sizeof(float);
-    deltanet_kernel<DK, DV, REF><<<dim3(a.nv, REF ? 1 : a.B), dim3(DV * 4), shmem, s>>>(a);
-    return launched(REF ? "deltanet_recurrent_kernel" : "deltanet_verify_kernel");
+    if constexpr (!REF) {
+        if (a.T <= 1) return launch_tm<DK, DV, REF, 1>(a, s);
+        if (a.T <= 2) return launch_tm<DK, DV, REF, 2>(a, s);
+        if (a.T <= 4) return launch_tm<DK, DV, REF, 4>(a, s);
+    }
+    return launch_tm<DK, DV, REF, kMaxT>(a, s);
 }
 
 // Workspace of the column-split kernel: one counter per (sequence, head),
@@ -785,7 +895,7 @@ int verify(void* out, int64_t ld_out, const void* proj, int64_t ld_proj, int64_t
            int64_t nslots, int write_all_slots, const void* a_log, const void* dt_bias, const void* norm_w,
            const int32_t* lens, int32_t pos_add, int64_t B, int64_t T, int64_t nk, int64_t nv, int64_t dk, int64_t dv,
            int64_t Kc, float eps, const void* xn, int64_t ld_xn, const void* w_ab, int64_t H, void* ws,
-           int64_t ws_bytes, void* stream) {
+           int64_t ws_bytes, void* stream, float* rec = nullptr, int32_t* base = nullptr, int replay = 0) {
     if (out == nullptr || proj == nullptr || conv_w == nullptr || conv_ring == nullptr || state == nullptr ||
         a_log == nullptr || dt_bias == nullptr || norm_w == nullptr)
         return invalid("deltanet_verify: null pointer");
@@ -834,6 +944,9 @@ int verify(void* out, int64_t ld_out, const void* proj, int64_t ld_proj, int64_t
     a.ld_xn = ld_xn;
     a.w_ab = static_cast<const uint16_t*>(w_ab);
     a.H = w_ab != nullptr ? int(H) : 0;
+    a.rec = rec;
+    a.base = base;
+    if (rec != nullptr) a.write_all = 0;  // the final state only
     if (ws != nullptr && (ws_bytes < cols_workspace_bytes(B, nv, dv) || !aligned16(ws)))
         return invalid("deltanet_verify_ws: workspace smaller than hai_deltanet_workspace_bytes(B, nv, dv) or "
                        "not 16-byte aligned");
@@ -849,6 +962,10 @@ int verify(void* out, int64_t ld_out, const void* proj, int64_t ld_proj, int64_t
         s.proj = a.proj + t0 * ld_proj;
         s.out = a.out + t0 * ld_out;
         if (s.xn != nullptr) s.xn = a.xn + t0 * ld_xn;
+        // records mode: the first launch replays or records the start
+        // positions; the later ones continue from the state it left
+        s.replay = rec != nullptr && t0 == 0 ? replay : 0;
+        s.base_out = rec != nullptr && t0 == 0 && replay == 0 ? 1 : 0;
         const int rc = cols ? dispatch_cols(s, dk, dv, ws, as_stream(stream)) : dispatch<false>(s, dk, dv, as_stream(stream));
         if (rc != HAI_OK) return rc;
     }
@@ -903,6 +1020,42 @@ extern "C" int hai_deltanet_verify_ab_bf16(void* out, int64_t ld_out, const void
     return verify(out, ld_out, proj, ld_proj, off_qkv, off_z, 0, 0, conv_w, conv_ring, ring, state, nslots,
                   write_all_slots, a_log, dt_bias, norm_w, lens, pos_add, B, T, nk, nv, dk, dv, Kc, eps, xn, ld_xn,
                   w_ab, H, nullptr, 0, stream);
+}
+
+extern "C" size_t hai_deltanet_records_bytes(int64_t nslots, int64_t B, int64_t nv, int64_t dk, int64_t dv) {
+    if (nslots < 0 || B < 0 || nv < 0 || dk < 0 || dv < 0) return 0;
+    const int64_t lim = INT64_MAX / 8;
+    int64_t n = record_floats(dk, dv);
+    for (const int64_t f : {nslots, B, nv}) {
+        if (f != 0 && n > lim / f) return SIZE_MAX;
+        n *= f;
+    }
+    return static_cast<size_t>(n) * sizeof(float);
+}
+
+extern "C" int hai_deltanet_verify_rec_bf16(void* out, int64_t ld_out, const void* proj, int64_t ld_proj,
+                                            int64_t off_qkv, int64_t off_z, int64_t off_a, int64_t off_b,
+                                            const void* xn, int64_t ld_xn, const void* w_ab, int64_t H,
+                                            const void* conv_w, void* conv_ring, int64_t ring, float* state,
+                                            int64_t nslots, float* records, int32_t* base, int replay,
+                                            const void* a_log, const void* dt_bias, const void* norm_w,
+                                            const int32_t* lens, int32_t pos_add, int64_t B, int64_t T, int64_t nk,
+                                            int64_t nv, int64_t dk, int64_t dv, int64_t Kc, float eps, void* stream) {
+    if (records == nullptr) return invalid("deltanet_verify_rec: null records");
+    if (base == nullptr) return invalid("deltanet_verify_rec: null base");
+    if (!aligned16(records)) return invalid("deltanet_verify_rec: records alignment");
+    if (nslots <= T) return invalid("deltanet_verify_rec: need nslots > T");
+    if (replay != 0 && replay != 1) return invalid("deltanet_verify_rec: replay must be 0 or 1");
+    if (replay == 1 && T > kMaxReplayT) return invalid("deltanet_verify_rec: replay calls take at most 4 tokens");
+    if (B > 0 && nslots > 0) {
+        const size_t bytes = hai_deltanet_records_bytes(nslots, B, nv, dk, dv);
+        if (bytes == SIZE_MAX) return invalid("deltanet_verify_rec: records size overflows");
+        if (const int rc = check_extent(records, bytes, "deltanet records"); rc != HAI_OK) return rc;
+        if (const int rc = check_extent(base, static_cast<size_t>(B) * 4, "deltanet base"); rc != HAI_OK) return rc;
+    }
+    return verify(out, ld_out, proj, ld_proj, off_qkv, off_z, off_a, off_b, conv_w, conv_ring, ring, state, nslots, 0,
+                  a_log, dt_bias, norm_w, lens, pos_add, B, T, nk, nv, dk, dv, Kc, eps, xn, ld_xn, w_ab, H, nullptr, 0,
+                  stream, records, base, replay);
 }
 
 extern "C" int hai_deltanet_conv_bf16(void* q, void* k, void* v, void* conv_state, const void* qkv,

@@ -292,6 +292,7 @@ int Engine::alloc_all() {
             } else {
                 L.ring = cv.take<uint16_t>(Bz * static_cast<size_t>(ring_ * d.C));
                 L.state = cv.take<float>(Bz * static_cast<size_t>(nslots_ * d.nv * d.dv * d.dk));
+                L.rec = cv.take<float>(hai_deltanet_records_bytes(nslots_, B_, d.nv, d.dk, d.dv) / sizeof(float));
             }
         }
         mtp_.k_cache = cv.take<uint16_t>(Bz * static_cast<size_t>(cap_ * d.kvw));
@@ -319,6 +320,7 @@ int Engine::alloc_all() {
         d_preds_ = cv.take<int64_t>(R);
         d_result_ = cv.take<int32_t>(4 * B_);
         d_tlen_ = cv.take<int32_t>(B_);
+        d_vbase_ = cv.take<int32_t>(B_);
         d_mlen_ = cv.take<int32_t>(B_);
         d_ndraft_ = cv.take<int32_t>(B_);
         d_delta_ = cv.take<int32_t>(B_);
@@ -707,10 +709,32 @@ int Engine::mlp(const LayerWeights& L, int64_t T, uint16_t* h) {
     return gemm(h, d.H, act_, d.F, lin(L.w_down, L.f_down), rows, d.H, d.F, HAI_EPI_RESIDUAL, h, d.H);
 }
 
+// The fused DeltaNet verify layer over the T rows in proj_ (a|b from proj
+// columns off_a / off_b, or formed from the normalised rows xn and w_ab) into
+// dnout_, with the state writes sw asks for.
+int Engine::deltanet(const LayerWeights& L, int64_t T, StateWrites sw, int64_t off_a, int64_t off_b,
+                     const uint16_t* xn, const uint16_t* w_ab) {
+    const auto& d = d_;
+    if (sw == StateWrites::kFinal) {
+        if (w_ab != nullptr)
+            return hai_deltanet_verify_ab_bf16(dnout_, d.vw, proj_, d.Nin, 0, d.C, xn, d.H, w_ab, d.H, L.conv_w,
+                                               L.ring, ring_, L.state, nslots_, 0, L.a_log, L.dt_bias, L.lin_norm,
+                                               d_tlen_, 0, B_, T, d.nk, d.nv, d.dk, d.dv, d.Kc, cfg_.rms_eps, stream_);
+        return hai_deltanet_verify_bf16(dnout_, d.vw, proj_, d.Nin, 0, d.C, off_a, off_b, L.conv_w, L.ring, ring_,
+                                        L.state, nslots_, 0, L.a_log, L.dt_bias, L.lin_norm, d_tlen_, 0, B_, T, d.nk,
+                                        d.nv, d.dk, d.dv, d.Kc, cfg_.rms_eps, stream_);
+    }
+    return hai_deltanet_verify_rec_bf16(dnout_, d.vw, proj_, d.Nin, 0, d.C, off_a, off_b, xn, d.H, w_ab,
+                                        w_ab != nullptr ? d.H : 0, L.conv_w, L.ring, ring_, L.state, nslots_, L.rec,
+                                        d_vbase_, sw == StateWrites::kReplay ? 1 : 0, L.a_log, L.dt_bias,
+                                        L.lin_norm, d_tlen_, 0, B_, T, d.nk, d.nv, d.dk, d.dv, d.Kc, cfg_.rms_eps,
+                                        stream_);
+}
+
 // target_forward (generator.cc:550-634): T rows of every sequence (row b*T+t)
 // on top of its committed caches; hf_ = post-final-norm hidden, logits_ =
 // lm_head.  Committed lengths are not advanced here.
-int Engine::forward_target(const int64_t* d_ids, int64_t T, bool write_all_slots, Logits logits) {
+int Engine::forward_target(const int64_t* d_ids, int64_t T, StateWrites sw, Logits logits) {
     pending_ = PendingResidual{};  // a forward ends with a norm, which completes any residual; only
                                    // a failed one leaves a record, for rows this forward overwrites
     const auto& d = d_;
@@ -751,10 +775,7 @@ int Engine::forward_target(const int64_t* d_ids, int64_t T, bool write_all_slots
                 HAI_TRY(norm_gemm(proj_, d.Nin, h_, L.in_ln, xn_, Lin(L.f_in), rows, d.C + d.vw, HAI_EPI_STORE,
                                   nullptr, 0));
                 HAI_TRY(flush_pending());
-                HAI_TRY(hai_deltanet_verify_ab_bf16(dnout_, d.vw, proj_, d.Nin, 0, d.C, xn_, d.H, L.w_ab, d.H,
-                                                    L.conv_w, L.ring, ring_, L.state, nslots_, write_all_slots ? 1 : 0,
-                                                    L.a_log, L.dt_bias, L.lin_norm, d_tlen_, 0, B_, T, d.nk, d.nv,
-                                                    d.dk, d.dv, d.Kc, cfg_.rms_eps, stream_));
+                HAI_TRY(deltanet(L, T, sw, 0, 0, xn_, L.w_ab));
             } else if (use_mfma(rows)) {
                 // matrix-core mode: the qkv|z rows only (16384 rows at the 27B
                 // shape, whole 64-row tiles that load every CU alike, where
@@ -763,18 +784,11 @@ int Engine::forward_target(const int64_t* d_ids, int64_t T, bool write_all_slots
                 HAI_TRY(norm_gemm(proj_, d.Nin, h_, L.in_ln, xn_, L.w_in, rows, d.C + d.vw, HAI_EPI_STORE, nullptr,
                                   0));
                 HAI_TRY(flush_pending());
-                HAI_TRY(hai_deltanet_verify_ab_bf16(dnout_, d.vw, proj_, d.Nin, 0, d.C, xn_, d.H,
-                                                    L.w_in + (d.C + d.vw) * d.H, d.H, L.conv_w, L.ring, ring_,
-                                                    L.state, nslots_, write_all_slots ? 1 : 0, L.a_log, L.dt_bias,
-                                                    L.lin_norm, d_tlen_, 0, B_, T, d.nk, d.nv, d.dk, d.dv, d.Kc,
-                                                    cfg_.rms_eps, stream_));
+                HAI_TRY(deltanet(L, T, sw, 0, 0, xn_, L.w_in + (d.C + d.vw) * d.H));
             } else {
                 HAI_TRY(norm_gemm(proj_, d.Nin, h_, L.in_ln, nullptr, L.w_in, rows, d.Nin, HAI_EPI_STORE, nullptr,
                                   0));
-                HAI_TRY(hai_deltanet_verify_bf16(dnout_, d.vw, proj_, d.Nin, 0, d.C, d.C + d.vw, d.C + d.vw + d.nv,
-                                                 L.conv_w, L.ring, ring_, L.state, nslots_, write_all_slots ? 1 : 0,
-                                                 L.a_log, L.dt_bias, L.lin_norm, d_tlen_, 0, B_, T, d.nk, d.nv, d.dk,
-                                                 d.dv, d.Kc, cfg_.rms_eps, stream_));
+                HAI_TRY(deltanet(L, T, sw, d.C + d.vw, d.C + d.vw + d.nv, nullptr, nullptr));
             }
             HAI_TRY(gemm(h_, d.H, dnout_, d.vw, lin(L.w_out, L.f_out), rows, d.H, d.vw, HAI_EPI_RESIDUAL, h_, d.H));
         }
@@ -859,7 +873,7 @@ int Engine::prefill_chunks(const int32_t* ids, int64_t P, uint16_t* hidden_out, 
         // when the caller asks for them)
         const bool last_chunk = off + T == P;
         const Logits lg = !fast_prefill_ ? Logits::kAll : last_chunk ? Logits::kLast : Logits::kNone;
-        HAI_TRY(forward_target(d_ids_, T, false, lg));
+        HAI_TRY(forward_target(d_ids_, T, StateWrites::kFinal, lg));
         HAI_TRY(hai_add_i32(d_tlen_, nullptr, static_cast<int32_t>(T), B_, stream_));
         if (last_chunk) {
             // the last prompt row of every sequence: its argmax is the first target
@@ -948,7 +962,7 @@ int Engine::generate_greedy(const int32_t* prompt, int64_t P, int64_t max_new, c
     while (true) {
         out[emitted++] = static_cast<int32_t>(next);
         if (emitted >= max_new || in_set(eos, n_eos, next)) break;
-        HAI_TRY(forward_target(d_next_, 1, false));
+        HAI_TRY(forward_target(d_next_, 1, StateWrites::kFinal));
         HAI_TRY(hai_add_i32(d_tlen_, nullptr, 1, 1, stream_));
         HAI_TRY(hai_argmax_rows_bf16(d_next_, logits_, d_.V, 1, d_.V, argmax_scratch_, stream_));
         HAI_TRY(read_i64(d_next_, &next, 1));
@@ -991,7 +1005,7 @@ int Engine::draft_step_at(int64_t i, int64_t T) {
 // device).  The next target of every sequence lands in d_next_.
 int Engine::verify_step(int64_t T) {
     return replay(&verify_graphs_[static_cast<size_t>(T)], [&]() -> int {
-        HAI_TRY(forward_target(d_vids_, T, true));
+        HAI_TRY(forward_target(d_vids_, T, StateWrites::kRecord));
         HAI_TRY(hai_verify_argmax_accept_bf16(logits_, d_.V, hf_, d_.H, d_vids_, d_ndraft_, B_, T, d_preds_,
                                               d_result_, d_tlen_, d_mlen_, d_next_, rec_hidden_, h_prev_,
                                               argmax_scratch_, stream_));
@@ -1009,7 +1023,7 @@ int Engine::verify_step(int64_t T) {
 int Engine::correction_step() {
     return replay(&corr_graph_, [&]() -> int {
         HAI_TRY(mtp_kv_rows(d_next_, rec_hidden_, 1, false));
-        HAI_TRY(forward_target(d_next_, 1, false));
+        HAI_TRY(forward_target(d_next_, 1, StateWrites::kReplay));
         HAI_TRY(hai_argmax_rows_bf16(d_cand_, logits_, d_.V, B_, d_.V, argmax_scratch_, stream_));
         HAI_TRY(hai_correction_commit_bf16(d_result_, d_cand_, hf_, d_.H, B_, d_next_, h_prev_, d_tlen_, d_mlen_,
                                            stream_));
@@ -1373,7 +1387,7 @@ int Engine::profile_verify(int64_t T, int64_t iters, hai_verify_profile* out) {
         prof_record_ = it == 0;
         if (prof_record_) prof_calls_.clear();
         HAI_TRY(hai_event_record(e0, stream_));
-        HAI_TRY(forward_target(d_ids_, T, true));
+        HAI_TRY(forward_target(d_ids_, T, StateWrites::kRecord));
         HAI_TRY(hai_memcpy_d2d(s_tlen, d_tlen_, static_cast<size_t>(B_) * 4, stream_));
         HAI_TRY(hai_memcpy_d2d(s_mlen, d_mlen_, static_cast<size_t>(B_) * 4, stream_));
         HAI_TRY(hai_verify_argmax_accept_bf16(logits_, d.V, hf_, d.H, d_ids_, nullptr, B_, T, d_preds_, s_res,

@@ -93,6 +93,7 @@ struct LayerWeights {
     uint16_t* v_cache = nullptr;
     uint16_t* ring = nullptr;     // [B][ring][C]
     float* state = nullptr;       // [nslots][B][nv][dk*dv], column-tiled heads
+    float* rec = nullptr;         // [nslots][B][nv][dk + dv + 4] rollback records of verify tokens
 };
 
 // Tensor ids shared with the synthetic generator, the CPU oracle and the
@@ -245,7 +246,14 @@ private:
     int norm_gemm(uint16_t* y, int64_t ldy, const uint16_t* x, const uint16_t* nw, uint16_t* xn_out,
                   const Lin& w, int64_t M, int64_t N, int epi, const uint16_t* res, int64_t ldres);
     Lin lin(const uint16_t* w, const Fp8Linear& f) const { return fp8_ ? Lin(f) : Lin(w); }
-    int forward_target(const int64_t* d_ids, int64_t T, bool write_all_slots, Logits logits = Logits::kAll);
+    // DeltaNet state writes of a forward: the final state only (prompt rows,
+    // greedy steps), rollback records of a verify (final state + one record
+    // per token, start positions in d_vbase_), or a correction that first
+    // re-applies the kept records of the verify's accepted prefix
+    enum class StateWrites { kFinal, kRecord, kReplay };
+    int forward_target(const int64_t* d_ids, int64_t T, StateWrites sw, Logits logits = Logits::kAll);
+    int deltanet(const LayerWeights& L, int64_t T, StateWrites sw, int64_t off_a, int64_t off_b, const uint16_t* xn,
+                 const uint16_t* w_ab);
     int attention_layer(const LayerWeights& L, int64_t T, uint16_t* h, const int32_t* lens,
                         uint16_t* kc, uint16_t* vc);
     int mlp(const LayerWeights& L, int64_t T, uint16_t* h);
@@ -316,6 +324,7 @@ private:
     int64_t* d_preds_ = nullptr;  // [rows]
     int32_t* d_result_ = nullptr; // [B][4]
     int32_t* d_tlen_ = nullptr;   // [B] committed target lengths
+    int32_t* d_vbase_ = nullptr;  // [B] target lengths at the last verify (DeltaNet replay base)
     int32_t* d_mlen_ = nullptr;   // [B] MTP cache lengths
     int32_t* d_ndraft_ = nullptr; // [B] drafts counted per sequence this round
     int32_t* d_delta_ = nullptr;  // [B] MTP length corrections
