@@ -197,20 +197,16 @@ __global__ __launch_bounds__(DV * 4) void deltanet_kernel(DnArgs A) {
     // ---- then the length-dependent ones: the state slot and the conv
     // history (one modulo each; later positions advance with a wrap) ----
     const int64_t p0 = REF ? 0 : static_cast<int64_t>(A.lens ? A.lens[b] : 0) + A.pos_add;
-    // records mode: the state read is that of position ps, followed by the
-    // nrep records of positions ps .. p0 - 1 (a start outside the record
-    // span reads slot p0 % nslots as the other modes do)
-    int64_t ps = p0;
+    // records mode, replay: the state read is that of position base[b],
+    // followed by the nrep records of positions base[b] .. p0 - 1 (a start
+    // outside the record span reads slot p0 % nslots as the other modes do)
     int nrep = 0;
     if constexpr (!REF) {
         // (replays are compiled into the short-call instantiations only: the
         // host runs them with T <= kMaxReplayT)
         if (TM <= kMaxReplayT && A.replay) {
             const int64_t pb = A.base[b];
-            if (pb <= p0 && p0 - pb < A.nslots && p0 - pb <= kMaxT) {
-                ps = pb;
-                nrep = static_cast<int>(p0 - pb);
-            }
+            if (pb <= p0 && p0 - pb < A.nslots && p0 - pb <= kMaxT) nrep = static_cast<int>(p0 - pb);
         } else if (A.base_out && h == 0 && tid == 0) {
             A.base[b] = static_cast<int32_t>(p0);
         }
@@ -218,7 +214,7 @@ __global__ __launch_bounds__(DV * 4) void deltanet_kernel(DnArgs A) {
     constexpr int64_t RS = record_floats(DK, DV);
     constexpr int RQ = static_cast<int>(RS / 4);  // float4 per record
     float4 rq0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    int64_t rec_r = 0;  // record slot of position ps
+    int64_t rec_r = 0;  // record slot of position base[b] (replay)
     float S[GI];  // column j, key dims [g*GI, g*GI+GI)
     int64_t slot_w = 0, ring_w = 0;  // state slot after token 0, ring entry of token 0
     if constexpr (REF) {
@@ -228,7 +224,7 @@ __global__ __launch_bounds__(DV * 4) void deltanet_kernel(DnArgs A) {
     } else {
         const int64_t slot = p0 % A.nslots;
         slot_w = slot + 1 == A.nslots ? 0 : slot + 1;
-        const int64_t slot_r = slot >= nrep ? slot - nrep : slot - nrep + A.nslots;  // ps % nslots
+        const int64_t slot_r = slot >= nrep ? slot - nrep : slot - nrep + A.nslots;  // (p0 - nrep) % nslots
         const float4* src =
             reinterpret_cast<const float4*>(A.state + ((slot_r * A.B + b) * nv + h) * static_cast<int64_t>(DV) * DK) +
             tid;
@@ -255,10 +251,10 @@ __global__ __launch_bounds__(DV * 4) void deltanet_kernel(DnArgs A) {
                 if (i < hist) rp = rp + 1 == A.ring_n ? 0 : rp + 1;
         }
         ring_w = rp;
-        // records mode, replay: the kept records of positions ps .. p0 - 1
-        // are staged in LDS (rls) for the token loop; each thread's first
-        // piece is requested here with the state, the rest (more than 7
-        // records) where they are stored
+        // records mode, replay: the kept records of positions p0 - nrep ..
+        // p0 - 1 are staged in LDS (rls) for the token loop; each thread's
+        // first 16-byte piece is requested here with the state, the pieces
+        // past the first NT (more than 7 records) where they are stored
         rec_r = slot_r;
         if (tid < nrep * RQ) {
             const int i = tid / RQ;
