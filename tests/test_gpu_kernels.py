@@ -339,14 +339,25 @@ def test_rmsnorm(rows, H):
     assert_bits_equal(dy.download(np.uint16), orc.rmsnorm(x, w, 1e-6, True), "rmsnorm")
 
 
-def test_embedding_and_elementwise():
-    rng = np.random.default_rng(5)
-    V, H = 50, 64
+@pytest.mark.parametrize("H,y_off", [(64, 0), (5120, 0), (8200, 0), (100, 0), (64, 1)],
+                         ids=["vec", "vec_27b", "vec_two_passes", "scalar_ragged", "scalar_unaligned"])
+def test_embedding_gather(H, y_off):
+    """Rows of the table copied bit for bit; ids outside [0, V) give zero
+    rows.  16-byte pieces when H % 8 == 0 and both pointers are 16-byte
+    aligned (H = 8200: more pieces than one pass of the block covers),
+    element copies otherwise (ragged H, an output offset by one element)."""
+    rng = np.random.default_rng(5 + H)
+    V = 50
     tab, tb = rand_bf16(rng, (V, H))
     ids = np.array([3, 0, 49, 50, -1, 7], np.int64)
-    dt, di, dy = dev(tb), dev(ids), out_buf(ids.size * H * 2)
-    hai.check(kern().hai_embedding_gather_bf16(dy.ptr, dt.ptr, di.ptr, ids.size, V, H, None), "embedding")
-    assert_bits_equal(dy.download(np.uint16), orc.embedding(tab, ids), "embedding")
+    dt, di, dy = dev(tb), dev(ids), out_buf((ids.size * H + y_off) * 2)
+    hai.check(kern().hai_embedding_gather_bf16(dy.ptr + 2 * y_off, dt.ptr, di.ptr, ids.size, V, H, None), "embedding")
+    got = dy.download(np.uint16)[y_off:]
+    assert_bits_equal(got, orc.embedding(tab, ids), "embedding")
+
+
+def test_embedding_and_elementwise():
+    rng = np.random.default_rng(5)
     a, ab = rand_bf16(rng, (1000,))
     b, bb = rand_bf16(rng, (1000,))
     da, db, dz = dev(ab), dev(bb), out_buf(2000)
@@ -872,28 +883,36 @@ def test_deltanet_column_split_matches_one_block(B, nk, nv, dk, T, Kc):
 
 
 # ----------------------------------------------------------------- argmax / accept
-def test_argmax_rows_ties_nan():
-    rng = np.random.default_rng(3)
-    rows, V = 7, 248320
-    x, xb = rand_bf16(rng, (rows, V))
-    x[1, 100] = x[1, 5000] = 50.0
+@pytest.mark.parametrize("V,ld", [(248320, 248320), (1003, 1008), (1003, 1003), (13, 13)],
+                         ids=["vocab_27b", "ragged_row_aligned", "unaligned_rows", "tiny"])
+def test_argmax_rows_ties_nan(V, ld):
+    """First index on ties, NaN and -inf never win, -0 ties +0; 16-byte
+    logit pieces where the rows allow them (ld % 8 == 0: the last piece of
+    a ragged row read element by element), element loads otherwise."""
+    rng = np.random.default_rng(3 + V)
+    rows = 7
+    x, _ = rand_bf16(rng, (rows, V))
+    hi = V - 1
+    x[1, min(100, hi)] = x[1, min(500, hi - 1)] = 50.0
     x[2, :] = np.nan
     x[3, :] = -np.inf
     x[4, 7] = np.nan
     x[4, 9] = 60.0
-    x[5, 0] = -0.0
     x[5, :] = -1.0
     x[5, 10] = -0.0
     x[5, 11] = 0.0
-    x[6, 248319] = 70.0
-    xb = hai.bf16_bits(x)
-    d, o = dev(xb), out_buf(rows * 8)
+    x[6, hi] = 70.0
+    xp = np.zeros((rows, ld), np.float32)
+    xp[:, :V] = x
+    xpb = hai.bf16_bits(xp)
+    d, o = dev(xpb), out_buf(rows * 8)
     scratch = out_buf(kern().hai_argmax_scratch_bytes(rows, V))
-    hai.check(kern().hai_argmax_rows_bf16(o.ptr, d.ptr, V, rows, V, scratch.ptr, None), "argmax")
+    hai.check(kern().hai_argmax_rows_bf16(o.ptr, d.ptr, ld, rows, V, scratch.ptr, None), "argmax")
     got = o.download(np.int64)
-    want = orc.argmax_rows(hai.bf16_to_f32(xb).reshape(rows, V))
+    want = orc.argmax_rows(hai.bf16_to_f32(xpb).reshape(rows, ld)[:, :V].copy())
     assert list(got) == list(want)
-    assert got[1] == 100 and got[2] == 0 and got[3] == 0 and got[4] == 9 and got[5] == 10 and got[6] == 248319
+    assert got[2] == 0 and got[3] == 0 and got[4] == 9 and got[5] == 10 and got[6] == hi
+    assert got[1] == min(min(100, hi), min(500, hi - 1))  # the first of the two maxima
 
 
 def test_draft_chain_count_kernel():

@@ -48,35 +48,111 @@ __device__ __forceinline__ uint64_t block_max_u64(uint64_t v, uint64_t* sh) {
     return best;
 }
 
+// Elements per slice of a row: a multiple of 8, so that with VEC (rows
+// 16-byte aligned) every slice starts on a 16-byte boundary.
+__host__ __device__ constexpr int64_t slice_len(int64_t V) { return ((V + kSlices - 1) / kSlices + 7) / 8 * 8; }
+constexpr int kArgmaxUnroll = 2;  // 16-byte pieces per thread requested together
+
+// The largest key of the row's slices (64 lanes, one key each): the row's
+// argmax, independent of the slice order.
+__device__ __forceinline__ uint64_t wave_max_slices(const uint64_t* __restrict__ part, int64_t r, int lane) {
+    uint64_t v = lane < kSlices ? part[r * kSlices + lane] : 0ull;
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) {
+        const uint64_t o = shfl_xor_u64(v, s);
+        v = o > v ? o : v;
+    }
+    return v;
+}
+
+// One block per (slice, row).  VEC: 16-byte pieces of 8 logits, the
+// thread's pieces requested before the first compare (one round trip to
+// the just-written logits instead of one per element).
+template <bool VEC>
 __global__ __launch_bounds__(256) void argmax_partial_kernel(uint64_t* __restrict__ part,
                                                              const uint16_t* __restrict__ logits,
                                                              int64_t ld, int64_t V) {
     __shared__ uint64_t sh[4];
     const int64_t row = blockIdx.y;
     const int slice = blockIdx.x;
-    const int64_t per = (V + kSlices - 1) / kSlices;
+    const int64_t per = slice_len(V);
     const int64_t start = static_cast<int64_t>(slice) * per;
     const int64_t end = min(V, start + per);
     const uint16_t* lr = logits + row * ld;
     uint64_t best = 0ull;
-    for (int64_t i = start + threadIdx.x; i < end; i += blockDim.x) {
-        const uint64_t k = make_key(bf2f(lr[i]), i);
-        best = k > best ? k : best;
+    if constexpr (VEC) {
+        const int64_t npc = start < end ? (end - start + 7) / 8 : 0;  // pieces, the last one possibly ragged
+        for (int64_t p0 = threadIdx.x; p0 < npc; p0 += kArgmaxUnroll * blockDim.x) {
+            uint4 v[kArgmaxUnroll];
+#pragma unroll
+            for (int u = 0; u < kArgmaxUnroll; ++u) {
+                const int64_t p = p0 + u * static_cast<int64_t>(blockDim.x);
+                const int64_t i0 = start + 8 * p;
+                v[u] = p < npc && i0 + 8 <= end ? *reinterpret_cast<const uint4*>(lr + i0)
+                                                : make_uint4(0u, 0u, 0u, 0u);
+            }
+#pragma unroll
+            for (int u = 0; u < kArgmaxUnroll; ++u) {
+                const int64_t p = p0 + u * static_cast<int64_t>(blockDim.x);
+                if (p >= npc) continue;
+                const int64_t i0 = start + 8 * p;
+                if (i0 + 8 <= end) {
+                    const uint32_t w[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const float f = __uint_as_float((e & 1) ? (w[e >> 1] & 0xffff0000u) : (w[e >> 1] << 16));
+                        const uint64_t k = make_key(f, i0 + e);
+                        best = k > best ? k : best;
+                    }
+                } else {
+                    for (int64_t i = i0; i < end; ++i) {
+                        const uint64_t k = make_key(bf2f(lr[i]), i);
+                        best = k > best ? k : best;
+                    }
+                }
+            }
+        }
+    } else {
+        for (int64_t i = start + threadIdx.x; i < end; i += blockDim.x) {
+            const uint64_t k = make_key(bf2f(lr[i]), i);
+            best = k > best ? k : best;
+        }
     }
     best = block_max_u64(best, sh);
     if (threadIdx.x == 0) part[row * kSlices + slice] = best;
 }
 
+// One wave per row.
 __global__ __launch_bounds__(256) void argmax_final_kernel(int64_t* __restrict__ out,
                                                            const uint64_t* __restrict__ part, int64_t rows) {
-    for (int64_t r = threadIdx.x; r < rows; r += blockDim.x) {
-        uint64_t best = 0ull;
-        for (int s = 0; s < kSlices; ++s) {
-            const uint64_t k = part[r * kSlices + s];
-            best = k > best ? k : best;
+    const int64_t r = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (r >= rows) return;
+    const uint64_t best = wave_max_slices(part, r, threadIdx.x & 63);
+    if ((threadIdx.x & 63) == 0) out[r] = key_index(best);
+}
+
+// Copies H elements (16-byte pieces when both rows allow them, each
+// thread's pieces requested before its first store).
+__device__ __forceinline__ void copy_row(uint16_t* __restrict__ dst, const uint16_t* __restrict__ src, int64_t H) {
+    const bool vec = (H & 7) == 0 && ((reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(src)) & 15) == 0;
+    if (vec) {
+        const int64_t n8 = H >> 3;
+        for (int64_t k0 = threadIdx.x; k0 < n8; k0 += 4 * blockDim.x) {
+            uint4 v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int64_t k = k0 + u * static_cast<int64_t>(blockDim.x);
+                v[u] = k < n8 ? reinterpret_cast<const uint4*>(src)[k] : make_uint4(0u, 0u, 0u, 0u);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int64_t k = k0 + u * static_cast<int64_t>(blockDim.x);
+                if (k < n8) reinterpret_cast<uint4*>(dst)[k] = v[u];
+            }
         }
-        out[r] = key_index(best);
+        return;
     }
+    for (int64_t k = threadIdx.x; k < H; k += blockDim.x) dst[k] = src[k];
 }
 
 // One block per sequence b: the final argmax of its T verify rows, its
@@ -89,16 +165,14 @@ __global__ __launch_bounds__(256) void verify_accept_kernel(
     __shared__ int64_t pred_sh[kMaxAcceptRows];
     __shared__ int acc_sh, full_sh;
     const int b = blockIdx.x;
-    for (int t = threadIdx.x; t < T; t += blockDim.x) {
+    const int lane = threadIdx.x & 63;
+    for (int t = threadIdx.x >> 6; t < T; t += blockDim.x >> 6) {  // one wave per verify row
         const int64_t r = static_cast<int64_t>(b) * T + t;
-        uint64_t best = 0ull;
-        for (int s = 0; s < kSlices; ++s) {
-            const uint64_t k = part[r * kSlices + s];
-            best = k > best ? k : best;
+        const int64_t p = key_index(wave_max_slices(part, r, lane));
+        if (lane == 0) {
+            preds[r] = p;
+            pred_sh[t] = p;
         }
-        const int64_t p = key_index(best);
-        preds[r] = p;
-        pred_sh[t] = p;
     }
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -119,10 +193,8 @@ __global__ __launch_bounds__(256) void verify_accept_kernel(
     __syncthreads();
     if (hidden == nullptr) return;
     const uint16_t* src = hidden + (static_cast<int64_t>(b) * T + acc_sh) * H;
-    if (rec_hidden)
-        for (int64_t k = threadIdx.x; k < H; k += blockDim.x) rec_hidden[b * H + k] = src[k];
-    if (h_prev && full_sh)
-        for (int64_t k = threadIdx.x; k < H; k += blockDim.x) h_prev[b * H + k] = src[k];
+    if (rec_hidden) copy_row(rec_hidden + b * H, src, H);
+    if (h_prev && full_sh) copy_row(h_prev + b * H, src, H);
 }
 
 __global__ void add_i32_kernel(int32_t* dst, const int32_t* delta, int32_t add, int64_t n) {
@@ -142,7 +214,7 @@ __global__ void correction_commit_kernel(const int32_t* __restrict__ result, con
                                          uint16_t* h_prev, int32_t* target_len, int32_t* mtp_len) {
     const int b = blockIdx.x;
     if (result[b * 4 + 1] != 0) return;
-    for (int64_t i = threadIdx.x; i < H; i += blockDim.x) h_prev[b * H + i] = corr_hidden[b * H + i];
+    copy_row(h_prev + b * H, corr_hidden + b * H, H);
     if (threadIdx.x == 0) {
         next[b] = corr_next[b];
         target_len[b] += 1;
@@ -170,6 +242,14 @@ __global__ void draft_chain_count_kernel(int64_t i, const int64_t* __restrict__ 
     for (int64_t e = 0; e < n_eos; ++e)
         if (eos[e] == tok) return;
     ndraft[b] = static_cast<int32_t>(i + 1);
+}
+
+void launch_partial(uint64_t* part, const uint16_t* logits, int64_t ld, int64_t V, int64_t rows, hipStream_t s) {
+    const dim3 grid(kSlices, static_cast<unsigned>(rows));
+    if (ld % 8 == 0 && aligned16(logits))
+        argmax_partial_kernel<true><<<grid, dim3(256), 0, s>>>(part, logits, ld, V);
+    else
+        argmax_partial_kernel<false><<<grid, dim3(256), 0, s>>>(part, logits, ld, V);
 }
 
 }  // namespace
@@ -229,11 +309,11 @@ int hai_argmax_rows_bf16(int64_t* out, const void* logits, int64_t ld, int64_t r
         return invalid("argmax_rows");
     if (rows == 0) return HAI_OK;
     const auto s = as_stream(stream);
-    argmax_partial_kernel<<<dim3(kSlices, static_cast<unsigned>(rows)), dim3(256), 0, s>>>(
-        static_cast<uint64_t*>(scratch), static_cast<const uint16_t*>(logits), ld, V);
+    launch_partial(static_cast<uint64_t*>(scratch), static_cast<const uint16_t*>(logits), ld, V, rows, s);
     int rc = launched("argmax_partial_kernel");
     if (rc != HAI_OK) return rc;
-    argmax_final_kernel<<<dim3(1), dim3(256), 0, s>>>(out, static_cast<const uint64_t*>(scratch), rows);
+    argmax_final_kernel<<<dim3(static_cast<unsigned>((rows + 3) / 4)), dim3(256), 0, s>>>(
+        out, static_cast<const uint64_t*>(scratch), rows);
     return launched("argmax_final_kernel");
 }
 
@@ -249,8 +329,7 @@ int hai_verify_argmax_accept_bf16(const void* logits, int64_t V, const void* hid
         (hidden != nullptr && H <= 0))
         return invalid("verify_argmax_accept: shape (1 <= B <= 64, 1 <= T <= 64)");
     const auto s = as_stream(stream);
-    argmax_partial_kernel<<<dim3(kSlices, static_cast<unsigned>(B * T)), dim3(256), 0, s>>>(
-        static_cast<uint64_t*>(scratch), static_cast<const uint16_t*>(logits), V, V);
+    launch_partial(static_cast<uint64_t*>(scratch), static_cast<const uint16_t*>(logits), V, V, B * T, s);
     int rc = launched("argmax_partial_kernel");
     if (rc != HAI_OK) return rc;
     verify_accept_kernel<<<dim3(static_cast<unsigned>(B)), dim3(256), 0, s>>>(

@@ -194,13 +194,37 @@ __global__ void silu_mul_kernel(uint16_t* y, const uint16_t* g, const uint16_t* 
 }
 
 // embedding_gather_kernel (hip_kernels.hip:88-103): one block per id.
+// VEC (rows of a multiple of 8 elements, 16-byte aligned): 16-byte pieces,
+// kEmbUnroll per thread requested before the first store, so a row costs
+// one round trip to memory instead of one per element a thread copies.
+constexpr int kEmbUnroll = 4;
+template <bool VEC>
 __global__ void embedding_kernel(uint16_t* __restrict__ y, const uint16_t* __restrict__ table,
                                  const int64_t* __restrict__ ids, int64_t V, int64_t H) {
     const int64_t r = blockIdx.x;
     const int64_t id = ids[r];
     const bool ok = id >= 0 && id < V;
-    for (int64_t k = threadIdx.x; k < H; k += blockDim.x)
-        y[r * H + k] = ok ? table[id * H + k] : static_cast<uint16_t>(0);
+    if constexpr (VEC) {
+        const int64_t n8 = H >> 3;
+        const uint4* src = reinterpret_cast<const uint4*>(table + (ok ? id : 0) * H);
+        uint4* dst = reinterpret_cast<uint4*>(y + r * H);
+        for (int64_t k0 = threadIdx.x; k0 < n8; k0 += kEmbUnroll * blockDim.x) {
+            uint4 v[kEmbUnroll];
+#pragma unroll
+            for (int u = 0; u < kEmbUnroll; ++u) {
+                const int64_t k = k0 + u * static_cast<int64_t>(blockDim.x);
+                v[u] = ok && k < n8 ? src[k] : make_uint4(0u, 0u, 0u, 0u);
+            }
+#pragma unroll
+            for (int u = 0; u < kEmbUnroll; ++u) {
+                const int64_t k = k0 + u * static_cast<int64_t>(blockDim.x);
+                if (k < n8) dst[k] = v[u];
+            }
+        }
+    } else {
+        for (int64_t k = threadIdx.x; k < H; k += blockDim.x)
+            y[r * H + k] = ok ? table[id * H + k] : static_cast<uint16_t>(0);
+    }
 }
 
 // partial_rope_kernel (hip_kernels.hip:192-221): rotate-half on the first R
@@ -280,8 +304,13 @@ int hai_embedding_gather_bf16(void* y, const void* table, const int64_t* ids, in
     if (y == nullptr || table == nullptr || ids == nullptr || n_ids < 0 || V <= 0 || H <= 0)
         return invalid("embedding_gather");
     if (n_ids == 0) return HAI_OK;
-    embedding_kernel<<<dim3(static_cast<unsigned>(n_ids)), dim3(256), 0, as_stream(stream)>>>(
-        static_cast<uint16_t*>(y), static_cast<const uint16_t*>(table), ids, V, H);
+    const dim3 grid(static_cast<unsigned>(n_ids));
+    if (H % 8 == 0 && aligned16(y) && aligned16(table))
+        embedding_kernel<true><<<grid, dim3(256), 0, as_stream(stream)>>>(
+            static_cast<uint16_t*>(y), static_cast<const uint16_t*>(table), ids, V, H);
+    else
+        embedding_kernel<false><<<grid, dim3(256), 0, as_stream(stream)>>>(
+            static_cast<uint16_t*>(y), static_cast<const uint16_t*>(table), ids, V, H);
     return launched("embedding_kernel");
 }
 
