@@ -204,7 +204,8 @@ int hai_q_gate_rmsnorm_rope_bf16(void* q_out, void* gate_out, const void* src,
  * -> partial RoPE -> bf16) fused with append_kv_cache_kernel
  * (hip_kernels.hip:295-308).  Caches are [B][cap][nkv][D]; row t of
  * sequence b goes to position (lens ? lens[b] : 0) + pos_add + t.  Values
- * are copied unchanged. */
+ * are copied unchanged.  src_k and src_v 16-byte aligned, ld_src a multiple
+ * of 8. */
 int hai_kv_rmsnorm_rope_append_bf16(void* k_cache, void* v_cache, int64_t cap,
                                     const void* src_k, const void* src_v,
                                     int64_t ld_src, const void* k_norm,

@@ -39,9 +39,59 @@ __device__ __forceinline__ float rope_at(const float* row, int d, int R, const f
     return fma_(yv, cs[p], xv * sn[p]);
 }
 
+// A head row of D <= kMaxHeadDim bf16 values, 8 per lane: lane l holds
+// elements 8l .. 8l+7 (the L64 order of l64_sumsq_bf16 for one pass).
+struct HeadPiece {
+    uint32_t w[4];
+    __device__ __forceinline__ float at(int e) const { return (e & 1) ? hi_bf(w[e >> 1]) : lo_bf(w[e >> 1]); }
+};
+__device__ __forceinline__ HeadPiece load_piece(const uint16_t* __restrict__ row, int D, int lane) {
+    HeadPiece p{{0u, 0u, 0u, 0u}};
+    if (lane * 8 < D) {
+        const uint4 d = *reinterpret_cast<const uint4*>(row + lane * 8);
+        p.w[0] = d.x; p.w[1] = d.y; p.w[2] = d.z; p.w[3] = d.w;
+    }
+    return p;
+}
+// sum of squares of a head row in l64_sumsq_bf16's order (D <= 512: one pass)
+__device__ __forceinline__ float piece_sumsq(const HeadPiece& p) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc = fma_(p.at(e), p.at(e), acc);
+    return wave_sum64(acc);
+}
+
+// The rotation factors of the lane's dims d = lane + 64 i that RoPE touches
+// (d < R), requested as soon as the position is known.
+constexpr int kRopeSlots = kMaxHeadDim / 64;
+__device__ __forceinline__ void load_rope(float (&cv)[kRopeSlots], float (&sv)[kRopeSlots], const float* cs,
+                                          const float* sn, int D, int R, int lane) {
+    const int half = R / 2;
+#pragma unroll
+    for (int i = 0; i < kRopeSlots; ++i) {
+        const int d = lane + 64 * i;
+        const int p = d < half ? d : d - half;
+        cv[i] = d < D && d < R ? cs[p] : 0.0f;
+        sv[i] = d < D && d < R ? sn[p] : 0.0f;
+    }
+}
+// rope_at with the lane's factors for d = lane + 64 i in registers
+__device__ __forceinline__ float rope_reg(const float* row, int d, int R, float c, float sn) {
+    if (d >= R) return row[d];
+    const int half = R / 2;
+    const int p = d < half ? d : d - half;
+    const float xv = row[p];
+    const float yv = row[p + half];
+    if (d < half) return fma_(xv, c, -(yv * sn));
+    return fma_(yv, c, xv * sn);
+}
+
 // q_gate_rmsnorm_rope_kernel (hip_fused_kernels.hip:87-141): one wave per
 // (row, head); q is normalised with (w+1), rotated and stored once; the gate
 // half is copied.  `pair` = row * nq + head of this wave; qn = its LDS row.
+// Every load that does not depend on the position (q, norm weight, gate,
+// the cache length) is issued first, the rotation factors as soon as the
+// length arrives.
 __device__ __forceinline__ void q_gate_rmsnorm_rope_pair(
     uint16_t* __restrict__ q_out, uint16_t* __restrict__ g_out, const uint16_t* __restrict__ src, int64_t ld_src,
     const uint16_t* __restrict__ wq, const float* __restrict__ rc, const float* __restrict__ rs, int64_t rope_pos,
@@ -50,29 +100,40 @@ __device__ __forceinline__ void q_gate_rmsnorm_rope_pair(
     const bool active = pair < static_cast<int64_t>(B) * T * nq;
     int64_t m = 0;
     int h = 0;
-    float inv = 0.0f;
-    const uint16_t* s = src;
+    HeadPiece gp{{0u, 0u, 0u, 0u}};
+    float cv[kRopeSlots], sv[kRopeSlots];
     if (active) {
         m = pair / nq;
         h = static_cast<int>(pair % nq);
-        s = src + m * ld_src + static_cast<int64_t>(h) * 2 * D;
-        const float ss = l64_sumsq_bf16(s, D, lane);
-        inv = 1.0f / csqrt(ss / static_cast<float>(D) + eps);
-        for (int d = lane; d < D; d += 64) qn[d] = (bf2f(s[d]) * inv) * (bf2f(wq[d]) + 1.0f);
+        const uint16_t* s = src + m * ld_src + static_cast<int64_t>(h) * 2 * D;
+        const HeadPiece qp = load_piece(s, D, lane);
+        gp = load_piece(s + D, D, lane);
+        float wv[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) wv[e] = lane * 8 + e < D ? bf2f(wq[lane * 8 + e]) : 0.0f;
+        const int b = static_cast<int>(m / T);
+        const int t = static_cast<int>(m % T);
+        int64_t pos = static_cast<int64_t>(lens ? lens[b] : 0) + pos_add + t;
+        pos = pos < 0 ? 0 : (pos >= rope_pos ? rope_pos - 1 : pos);
+        load_rope(cv, sv, rc + pos * (R / 2), rs + pos * (R / 2), D, R, lane);
+        const float inv = 1.0f / csqrt(piece_sumsq(qp) / static_cast<float>(D) + eps);
+        if (lane * 8 < D) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) qn[lane * 8 + e] = (qp.at(e) * inv) * (wv[e] + 1.0f);
+        }
     }
     __syncthreads();
     if (!active) return;
-    const int b = static_cast<int>(m / T);
-    const int t = static_cast<int>(m % T);
-    int64_t pos = static_cast<int64_t>(lens ? lens[b] : 0) + pos_add + t;
-    pos = pos < 0 ? 0 : (pos >= rope_pos ? rope_pos - 1 : pos);
-    const float* cs = rc + pos * (R / 2);
-    const float* sn = rs + pos * (R / 2);
     uint16_t* qo = q_out + (m * nq + h) * D;
     uint16_t* go = g_out + (m * nq + h) * D;
-    for (int d = lane; d < D; d += 64) {
-        qo[d] = f2bf(rope_at(qn, d, R, cs, sn));
-        go[d] = s[D + d];
+#pragma unroll
+    for (int i = 0; i < kRopeSlots; ++i) {
+        const int d = lane + 64 * i;
+        if (d < D) qo[d] = f2bf(rope_reg(qn, d, R, cv[i], sv[i]));
+    }
+    if (lane * 8 < D) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) go[lane * 8 + e] = static_cast<uint16_t>(gp.w[e >> 1] >> (16 * (e & 1)));
     }
 }
 
@@ -88,28 +149,42 @@ __device__ __forceinline__ void kv_rmsnorm_rope_append_pair(
     const bool active = pair < static_cast<int64_t>(B) * T * nkv;
     int64_t m = 0;
     int h = 0;
+    int64_t pos = -1;
+    HeadPiece vp{{0u, 0u, 0u, 0u}};
+    float cv[kRopeSlots], svr[kRopeSlots];
     if (active) {
         m = pair / nkv;
         h = static_cast<int>(pair % nkv);
         const uint16_t* s = sk + m * ld_src + static_cast<int64_t>(h) * D;
-        const float ss = l64_sumsq_bf16(s, D, lane);
-        const float inv = 1.0f / csqrt(ss / static_cast<float>(D) + eps);
-        for (int d = lane; d < D; d += 64) kn[d] = bfr((bf2f(s[d]) * inv) * (bf2f(wk[d]) + 1.0f));
+        const HeadPiece kp = load_piece(s, D, lane);
+        vp = load_piece(sv + m * ld_src + static_cast<int64_t>(h) * D, D, lane);
+        float wv[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) wv[e] = lane * 8 + e < D ? bf2f(wk[lane * 8 + e]) : 0.0f;
+        const int b = static_cast<int>(m / T);
+        const int t = static_cast<int>(m % T);
+        pos = static_cast<int64_t>(lens ? lens[b] : 0) + pos_add + t;
+        const int64_t rp = pos < 0 ? 0 : (pos >= rope_pos ? rope_pos - 1 : pos);
+        load_rope(cv, svr, rc + rp * (R / 2), rs + rp * (R / 2), D, R, lane);
+        const float inv = 1.0f / csqrt(piece_sumsq(kp) / static_cast<float>(D) + eps);
+        if (lane * 8 < D) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) kn[lane * 8 + e] = bfr((kp.at(e) * inv) * (wv[e] + 1.0f));
+        }
     }
     __syncthreads();
     if (!active) return;
-    const int b = static_cast<int>(m / T);
-    const int t = static_cast<int>(m % T);
-    const int64_t pos = static_cast<int64_t>(lens ? lens[b] : 0) + pos_add + t;
     if (pos < 0 || pos >= cap) return;
-    const int64_t rp = pos >= rope_pos ? rope_pos - 1 : pos;
-    const float* cs = rc + rp * (R / 2);
-    const float* sn = rs + rp * (R / 2);
+    const int b = static_cast<int>(m / T);
     const int64_t dst = ((static_cast<int64_t>(b) * cap + pos) * nkv + h) * D;
-    const uint16_t* v = sv + m * ld_src + static_cast<int64_t>(h) * D;
-    for (int d = lane; d < D; d += 64) {
-        kc[dst + d] = f2bf(rope_at(kn, d, R, cs, sn));
-        vc[dst + d] = v[d];
+#pragma unroll
+    for (int i = 0; i < kRopeSlots; ++i) {
+        const int d = lane + 64 * i;
+        if (d < D) kc[dst + d] = f2bf(rope_reg(kn, d, R, cv[i], svr[i]));
+    }
+    if (lane * 8 < D) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) vc[dst + lane * 8 + e] = static_cast<uint16_t>(vp.w[e >> 1] >> (16 * (e & 1)));
     }
 }
 
@@ -347,7 +422,8 @@ int hai_kv_rmsnorm_rope_append_bf16(void* k_cache, void* v_cache, int64_t cap, c
     if (cap <= 0 || B < 0 || T < 0 || nkv <= 0 || D <= 0 || D % 8 != 0 || D > kMaxHeadDim || R < 0 ||
         R > D || R % 2 != 0 || ld_src < nkv * D || rope_positions <= 0)
         return invalid("kv_rmsnorm_rope_append: shape");
-    if (!aligned16(src_k) || ld_src % 8 != 0) return invalid("kv_rmsnorm_rope_append: alignment");
+    if (!aligned16(src_k) || !aligned16(src_v) || ld_src % 8 != 0)
+        return invalid("kv_rmsnorm_rope_append: alignment (src_k, src_v 16-byte aligned, ld_src % 8 == 0)");
     const int64_t pairs = B * T * nkv;
     if (pairs == 0) return HAI_OK;
     kv_rmsnorm_rope_append_kernel<<<dim3(static_cast<unsigned>((pairs + 3) / 4)), dim3(256), 0,
