@@ -262,6 +262,27 @@ int hai_gqa_verify_bf16(void* out, const void* q, const void* gate,
                         void* scratch, int64_t B, int64_t T, int64_t nq,
                         int64_t nkv, int64_t D, const int32_t* lens,
                         int32_t len_add, int64_t max_len, void* stream);
+/* hai_qkv_rmsnorm_rope_append_bf16 followed by hai_gqa_verify_bf16 in one
+ * partial pass (+ the merge pass): the partial blocks normalise and rotate
+ * their own query rows from the projection rows proj (ld_proj: [q_h | gate_h]
+ * for the nq heads, then the nkv K heads, then the nkv V heads, rows b*T + t
+ * at position L_b - T + t, L_b = (lens ? lens[b] : 0) + len_add), build the
+ * K / V rows of the T new positions from them for the key chunks that hold
+ * those positions and write them to the caches, and copy the gate halves to
+ * gate_out ([B*T][nq][D]), which the merge pass reads.  Outputs, cache rows
+ * and gate halves are bit-identical to the two calls (the normalised q rows
+ * are not stored).  Removes one dependent launch per attention layer.
+ * proj 16-byte aligned, ld_proj % 8 == 0; other arguments and the scratch
+ * as the two calls. */
+int hai_gqa_verify_fused_bf16(void* out, void* gate_out, const void* proj,
+                              int64_t ld_proj, const void* q_norm,
+                              const void* k_norm, const float* rope_cos,
+                              const float* rope_sin, int64_t rope_positions,
+                              int64_t R, float eps, void* k_cache,
+                              void* v_cache, int64_t cap, void* scratch,
+                              int64_t B, int64_t T, int64_t nq, int64_t nkv,
+                              int64_t D, const int32_t* lens, int32_t len_add,
+                              int64_t max_len, void* stream);
 /* hai_gqa_verify_bf16 for callers that cannot allocate (code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc): the
  * same kernels and bit-identical results, with the split-KV partials in a

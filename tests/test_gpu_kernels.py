@@ -452,6 +452,54 @@ def test_qkv_norm_rope_append_equals_the_two_launches(B, T, nq, nkv, D, R):
         assert np.array_equal(a, b), name
 
 
+@pytest.mark.parametrize("B,T,nq,nkv,D,R,L0", [
+    (1, 2, 24, 4, 256, 64, [1278]),       # C3 verify: both new rows in the last chunk
+    (1, 2, 24, 4, 256, 64, [63]),         # new rows straddle chunks 0 and 1
+    (2, 4, 4, 2, 64, 16, [100, 0]),       # a sequence whose new rows start the cache
+    (1, 16, 4, 2, 128, 128, [200]),       # 16-row chunk over two key chunks, full rotation
+    (3, 1, 24, 4, 256, 64, [4000, 5, 64]),  # correction rows; several query groups per block
+    (1, 4, 24, 4, 256, 64, [1590]),       # 8 queries per block, 2 per wave
+    (2, 4, 24, 4, 256, 64, [6390, 100]),  # all 24 per block, 3 per wave on 8 waves
+])
+def test_gqa_verify_fused_equals_norm_then_attention(B, T, nq, nkv, D, R, L0):
+    """hai_gqa_verify_fused_bf16 against hai_qkv_rmsnorm_rope_append_bf16
+    followed by hai_gqa_verify_bf16 on the same projection rows and caches:
+    the attention output, the gate halves and both whole caches bit for bit
+    (the new K / V rows are built inside the partial pass and appended by
+    its first query group)."""
+    rng = np.random.default_rng(B * 100 + T * 10 + D + L0[0])
+    cap = max(L0) + T + 70
+    base = 1e7
+    ld = (2 * nq + 2 * nkv) * D + 8
+    _, sb = rand_bf16(rng, (B * T, ld))
+    _, wqb = rand_bf16(rng, (D,), 0.02)
+    _, wkb = rand_bf16(rng, (D,), 0.02)
+    _, kcb = rand_bf16(rng, (B * cap * nkv * D,))
+    _, vcb = rand_bf16(rng, (B * cap * nkv * D,))
+    lens = np.array(L0, np.int32)
+    cd, sd = _rope_dev(cap, R, base)
+    dsrc, dwq, dwk, dl = dev(sb), dev(wqb), dev(wkb), dev(lens)
+    sc = out_buf(kern().hai_gqa_scratch_bytes(B, T, nq, D, cap))
+    outs = []
+    for fused in (False, True):
+        kc, vc = dev(kcb), dev(vcb)
+        out, g = out_buf(B * T * nq * D * 2), out_buf(B * T * nq * D * 2)
+        if fused:
+            hai.check(kern().hai_gqa_verify_fused_bf16(out.ptr, g.ptr, dsrc.ptr, ld, dwq.ptr, dwk.ptr, cd.ptr, sd.ptr,
+                                                       cap, R, 1e-6, kc.ptr, vc.ptr, cap, sc.ptr, B, T, nq, nkv, D,
+                                                       dl.ptr, T, cap, None), "fused")
+        else:
+            q = out_buf(B * T * nq * D * 2)
+            hai.check(kern().hai_qkv_rmsnorm_rope_append_bf16(q.ptr, g.ptr, kc.ptr, vc.ptr, cap, dsrc.ptr, ld,
+                                                               dwq.ptr, dwk.ptr, cd.ptr, sd.ptr, cap, B, T, nq, nkv,
+                                                               D, R, dl.ptr, 0, 1e-6, None), "qkv")
+            hai.check(kern().hai_gqa_verify_bf16(out.ptr, q.ptr, g.ptr, kc.ptr, vc.ptr, cap, sc.ptr, B, T, nq, nkv,
+                                                 D, dl.ptr, T, cap, None), "attention")
+        outs.append([buf.download(np.uint16) for buf in (out, g, kc, vc)])
+    for name, a, b in zip(("output", "gate", "k cache", "v cache"), outs[0], outs[1]):
+        assert np.array_equal(a, b), name
+
+
 # ----------------------------------------------------------------- attention
 @pytest.mark.parametrize("B,T,nq,nkv,D,lens", [
     (1, 2, 4, 2, 64, [30]), (1, 1, 4, 2, 64, [0]), (1, 4, 24, 4, 256, [60]), (1, 2, 24, 4, 256, [1278]),

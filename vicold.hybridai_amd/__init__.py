@@ -87,6 +87,8 @@ _KERNEL_SIGS = {
     "hai_qkv_rmsnorm_rope_append_bf16": [VP, VP, VP, VP, I64, VP, I64, VP, VP, VP, VP, I64, I64, I64, I64, I64, I64,
                                          I64, VP, I32, F32, VP],
     "hai_gqa_verify_bf16": [VP, VP, VP, VP, VP, I64, VP, I64, I64, I64, I64, I64, VP, I32, I64, VP],
+    "hai_gqa_verify_fused_bf16": [VP, VP, VP, I64, VP, VP, VP, VP, I64, I64, F32, VP, VP, I64, VP, I64, I64, I64, I64,
+                                  I64, VP, I32, I64, VP],
     "hai_gqa_verify_mfma_bf16": [VP, VP, VP, VP, VP, I64, VP, I64, I64, I64, I64, I64, VP, I32, I64, VP],
     "hai_gqa_verify_noalloc_bf16": [VP, VP, VP, VP, VP, I64, I64, I64, I64, I64, I64, VP, I32, I64, VP],
     "hai_deltanet_verify_bf16": [VP, I64, VP, I64, I64, I64, I64, I64, VP, VP, I64, VP, I64, ctypes.c_int, VP, VP,

@@ -45,15 +45,118 @@ constexpr int64_t kFullGroupBlocks = 256;
 
 __host__ __device__ constexpr int64_t partial_stride(int D) { return D + 2; }
 
+// The q / k RMSNorm(+1) + partial RoPE (+ K/V cache append) of
+// hai_qkv_rmsnorm_rope_append_bf16, done inside the partial kernel (FUSE):
+// projection rows b*T + t hold [q_h | gate_h] for the nq heads, then the nkv
+// K heads, then the nkv V heads.
+struct QkvFuse {
+    const uint16_t* proj;
+    int64_t ld;
+    const uint16_t *wq, *wk;
+    const float *rc, *rs;
+    int64_t rope_pos;
+    int R;
+    float eps;
+    uint16_t* gate_out;  // [B*T][nq][D], the gate halves copied for the merge pass
+    uint16_t *kc, *vc;   // the caches, written at the T new positions
+};
+
+__device__ __forceinline__ void wave_fence_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Query head h of projection row `row` (position pos): the bf16 values
+// q_gate_rmsnorm_rope_pair stores, element lane + 64 r in qv[r]; the gate
+// half copied to gate_out when copy_gate.  scratch: D floats of the wave.
+template <int D>
+__device__ __forceinline__ void fused_q_row(uint16_t (&qv)[D / 64], const QkvFuse& F, int64_t row, int h, int nq,
+                                            int64_t pos, bool copy_gate, float* scratch, int lane) {
+    const uint16_t* src = F.proj + row * F.ld + static_cast<int64_t>(h) * 2 * D;
+    const HeadPiece qp = load_piece(src, D, lane);
+    HeadPiece gp{{0u, 0u, 0u, 0u}};
+    if (copy_gate) gp = load_piece(src + D, D, lane);
+    float wv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) wv[e] = lane * 8 + e < D ? bf2f(F.wq[lane * 8 + e]) : 0.0f;
+    const int64_t rp = pos < 0 ? 0 : (pos >= F.rope_pos ? F.rope_pos - 1 : pos);
+    float cv[kRopeSlots], sv[kRopeSlots];
+    load_rope(cv, sv, F.rc + rp * (F.R / 2), F.rs + rp * (F.R / 2), D, F.R, lane);
+    const float inv = 1.0f / csqrt(piece_sumsq(qp) / static_cast<float>(D) + F.eps);
+    if (lane * 8 < D) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) scratch[lane * 8 + e] = (qp.at(e) * inv) * (wv[e] + 1.0f);
+    }
+    wave_fence_sync();
+#pragma unroll
+    for (int r = 0; r < D / 64; ++r) qv[r] = f2bf(rope_reg(scratch, lane + 64 * r, F.R, cv[r], sv[r]));
+    if (copy_gate && lane * 8 < D) {
+        uint16_t* go = F.gate_out + (row * nq + h) * D + lane * 8;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) go[e] = static_cast<uint16_t>(gp.w[e >> 1] >> (16 * (e & 1)));
+    }
+    wave_fence_sync();  // scratch is rewritten next
+}
+
+// K / V head kvh of projection row `row` at position pos, as
+// kv_rmsnorm_rope_append_pair computes it, into the staged rows ks_row /
+// vs_row (and the caches at pos when append).  scratch: D floats of the wave.
+template <int D>
+__device__ __forceinline__ void fused_kv_row(uint32_t* ks_row, uint32_t* vs_row, const QkvFuse& F, int64_t row,
+                                             int kvh, int nq, int nkv, int64_t pos, int64_t cache_row, bool append,
+                                             float* scratch, int lane) {
+    const uint16_t* sk = F.proj + row * F.ld + static_cast<int64_t>(2 * nq + kvh) * D;
+    const uint16_t* sv = F.proj + row * F.ld + static_cast<int64_t>(2 * nq + nkv + kvh) * D;
+    const HeadPiece kp = load_piece(sk, D, lane);
+    const HeadPiece vp = load_piece(sv, D, lane);
+    float wv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) wv[e] = lane * 8 + e < D ? bf2f(F.wk[lane * 8 + e]) : 0.0f;
+    const int64_t rp = pos < 0 ? 0 : (pos >= F.rope_pos ? F.rope_pos - 1 : pos);
+    float cv[kRopeSlots], sv2[kRopeSlots];
+    load_rope(cv, sv2, F.rc + rp * (F.R / 2), F.rs + rp * (F.R / 2), D, F.R, lane);
+    const float inv = 1.0f / csqrt(piece_sumsq(kp) / static_cast<float>(D) + F.eps);
+    if (lane * 8 < D) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) scratch[lane * 8 + e] = bfr((kp.at(e) * inv) * (wv[e] + 1.0f));
+    }
+    wave_fence_sync();
+    uint16_t* kr = reinterpret_cast<uint16_t*>(ks_row);
+#pragma unroll
+    for (int r = 0; r < D / 64; ++r) {
+        const int d = lane + 64 * r;
+        const uint16_t kv = f2bf(rope_reg(scratch, d, F.R, cv[r], sv2[r]));
+        kr[d] = kv;
+        if (append) F.kc[cache_row * D + d] = kv;
+    }
+    if (lane * 8 < D) {
+        *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(vs_row) + lane * 8) =
+            make_uint4(vp.w[0], vp.w[1], vp.w[2], vp.w[3]);
+        if (append) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                F.vc[cache_row * D + lane * 8 + e] = static_cast<uint16_t>(vp.w[e >> 1] >> (16 * (e & 1)));
+        }
+    }
+    wave_fence_sync();  // scratch is rewritten next
+}
+
 // grid (chunk, query group x KV head, sequence): the block stages one 64-key
 // chunk of one KV head and serves qpb of that head's queries.  Each wave takes
 // up to QG of them at a time: a K or V element is unpacked once and feeds the
 // QG queries' fma chains (each chain keeps its own sequential order).
-template <int D, int QG, int W>
+// FUSE: the queries are normalised and rotated here from the projection rows
+// (fused_q_row), the chunk's rows at the T new positions are built from them
+// (fused_kv_row: the cache is not read there, and the first query group's
+// block writes them to it), and the chunk-0 blocks copy the gate halves; the
+// values are those of hai_qkv_rmsnorm_rope_append_bf16 followed by the plain
+// kernel, bit for bit.
+template <int D, int QG, int W, bool FUSE = false>
 __global__ __launch_bounds__(64 * W) void gqa_partial_kernel(
     float* __restrict__ scratch, const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, int64_t cap, int T, int nq, int nkv, const int32_t* lens,
-    int len_add, int nchunk, float scale, int qpb) {
+    int len_add, int nchunk, float scale, int qpb, QkvFuse F) {
     constexpr int KP = D / 2 + 4;          // dword stride of a staged K row (16-byte pad)
     constexpr int VP = D / 2;              // dword stride of a staged V row
     constexpr int ROW16 = D / 8;           // 16-byte pieces per row
@@ -90,6 +193,7 @@ __global__ __launch_bounds__(64 * W) void gqa_partial_kernel(
     // pass p of wave w serves queries q_begin + (W p + w) QG + [0, QG)
     uint16_t qv[QG][QPL];
     auto load_q = [&](int base) {
+        if constexpr (FUSE) return;  // computed at the start of the pass (fused_q_row)
 #pragma unroll
         for (int qq = 0; qq < QG; ++qq)
             if (base + qq < q_end) {
@@ -127,6 +231,19 @@ __global__ __launch_bounds__(64 * W) void gqa_partial_kernel(
         }
     }
     __syncthreads();
+    if constexpr (FUSE) {
+        // the chunk's rows at the new positions L - T .. L - 1, one wave each
+        const int64_t first_new = L - T;
+        const int j0 = first_new > key0 ? static_cast<int>(first_new - key0) : 0;
+        for (int j = j0 + wave; j < nkeys; j += W) {
+            const int64_t pos = key0 + j;
+            const int64_t t = pos - first_new;
+            fused_kv_row<D>(Ks + j * KP, Vs + j * VP, F, static_cast<int64_t>(b) * T + t, kvh, nq, nkv, pos,
+                            (static_cast<int64_t>(b) * cap + pos) * nkv + kvh, qgrp == 0 && pos < cap,
+                            &Qs[wave][0][0], lane);
+        }
+        __syncthreads();
+    }
 
     auto wave_sync = [] {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -135,6 +252,16 @@ __global__ __launch_bounds__(64 * W) void gqa_partial_kernel(
     };
     for (int base = q_begin + wave * QG; base < q_end; base += W * QG) {
         const int nw = min(QG, q_end - base);
+        if constexpr (FUSE) {
+#pragma unroll
+            for (int qq = 0; qq < QG; ++qq)
+                if (qq < nw) {
+                    const int qi = base + qq;
+                    const int t = qi / group;
+                    fused_q_row<D>(qv[qq], F, static_cast<int64_t>(b) * T + t, kvh * group + qi % group, nq,
+                                   L - T + t, chunk == 0, &Qs[wave][qq][0], lane);
+                }
+        }
 #pragma unroll
         for (int qq = 0; qq < QG; ++qq)
 #pragma unroll
@@ -320,10 +447,10 @@ __global__ __launch_bounds__(D) void gqa_combine_kernel(
     out[qidx * D + tid] = f2bf(o);
 }
 
-template <int D>
+template <int D, bool FUSE = false>
 int launch(uint16_t* out, const uint16_t* q, const uint16_t* gate, const uint16_t* kc, const uint16_t* vc,
            int64_t cap, float* scratch, int B, int T, int nq, int nkv, const int32_t* lens, int len_add,
-           int nchunk, hipStream_t s) {
+           int nchunk, hipStream_t s, const QkvFuse& F = QkvFuse{}) {
     const float scale = 1.0f / __builtin_sqrtf(static_cast<float>(D));
     // Queries per block: all of the KV head's when the chunks alone fill the
     // GPU (K / V read once), else the fewest multiple of four that does.
@@ -339,17 +466,17 @@ int launch(uint16_t* out, const uint16_t* q, const uint16_t* gate, const uint16_
     // V tile shared by all of them); larger groups take several passes.
     const dim3 grid(nchunk, nkv * qgroups, B);
     if (qpb <= 4)
-        gqa_partial_kernel<D, 1, 4><<<grid, dim3(256), 0, s>>>(scratch, q, kc, vc, cap, T, nq, nkv, lens, len_add,
-                                                               nchunk, scale, qpb);
+        gqa_partial_kernel<D, 1, 4, FUSE><<<grid, dim3(256), 0, s>>>(scratch, q, kc, vc, cap, T, nq, nkv, lens,
+                                                                     len_add, nchunk, scale, qpb, F);
     else if (qpb <= 8)
-        gqa_partial_kernel<D, 2, 4><<<grid, dim3(256), 0, s>>>(scratch, q, kc, vc, cap, T, nq, nkv, lens, len_add,
-                                                               nchunk, scale, qpb);
+        gqa_partial_kernel<D, 2, 4, FUSE><<<grid, dim3(256), 0, s>>>(scratch, q, kc, vc, cap, T, nq, nkv, lens,
+                                                                     len_add, nchunk, scale, qpb, F);
     else if (qpb <= 16)
-        gqa_partial_kernel<D, 2, 8><<<grid, dim3(512), 0, s>>>(scratch, q, kc, vc, cap, T, nq, nkv, lens, len_add,
-                                                               nchunk, scale, qpb);
+        gqa_partial_kernel<D, 2, 8, FUSE><<<grid, dim3(512), 0, s>>>(scratch, q, kc, vc, cap, T, nq, nkv, lens,
+                                                                     len_add, nchunk, scale, qpb, F);
     else
-        gqa_partial_kernel<D, 3, 8><<<grid, dim3(512), 0, s>>>(scratch, q, kc, vc, cap, T, nq, nkv, lens, len_add,
-                                                               nchunk, scale, qpb);
+        gqa_partial_kernel<D, 3, 8, FUSE><<<grid, dim3(512), 0, s>>>(scratch, q, kc, vc, cap, T, nq, nkv, lens,
+                                                                     len_add, nchunk, scale, qpb, F);
     int rc = launched("gqa_partial_kernel");
     if (rc != HAI_OK) return rc;
     const int64_t nall = static_cast<int64_t>(B) * T * nq;
@@ -1253,6 +1380,51 @@ int hai_gqa_verify_bf16(void* out, const void* q, const void* gate, const void* 
         case 128: return launch<128>(o, qq, g, kc, vc, cap, sc, int(B), int(T), int(nq), int(nkv), lens, len_add, nchunk, s);
         case 256: return launch<256>(o, qq, g, kc, vc, cap, sc, int(B), int(T), int(nq), int(nkv), lens, len_add, nchunk, s);
         default: return invalid("gqa_verify: head_dim must be 64, 128 or 256");
+    }
+}
+
+int hai_gqa_verify_fused_bf16(void* out, void* gate_out, const void* proj, int64_t ld_proj, const void* q_norm,
+                              const void* k_norm, const float* rope_cos, const float* rope_sin,
+                              int64_t rope_positions, int64_t R, float eps, void* k_cache, void* v_cache,
+                              int64_t cap, void* scratch, int64_t B, int64_t T, int64_t nq, int64_t nkv, int64_t D,
+                              const int32_t* lens, int32_t len_add, int64_t max_len, void* stream) {
+    if (out == nullptr || gate_out == nullptr || proj == nullptr || q_norm == nullptr || k_norm == nullptr ||
+        rope_cos == nullptr || rope_sin == nullptr || k_cache == nullptr || v_cache == nullptr || scratch == nullptr)
+        return invalid("gqa_verify_fused: null pointer");
+    if (B < 0 || T < 0 || nq <= 0 || nkv <= 0 || nq % nkv != 0 || cap <= 0 || max_len <= 0 || max_len > cap ||
+        T > max_len || B > INT32_MAX || nq > INT32_MAX || max_len > INT32_MAX || R < 0 || R > D || R % 2 != 0 ||
+        rope_positions <= 0 || ld_proj < (2 * nq + 2 * nkv) * D)
+        return invalid("gqa_verify_fused: shape");
+    if (lens == nullptr && (len_add < T || len_add > max_len))
+        return invalid("gqa_verify_fused: cache length must cover the T new rows and stay within max_len");
+    if (!aligned16(k_cache) || !aligned16(v_cache) || !aligned16(proj) || ld_proj % 8 != 0)
+        return invalid("gqa_verify_fused: alignment");
+    if (B == 0 || T == 0) return HAI_OK;
+    const int nchunk = static_cast<int>((max_len + kChunk - 1) / kChunk);
+    QkvFuse F;
+    F.proj = static_cast<const uint16_t*>(proj);
+    F.ld = ld_proj;
+    F.wq = static_cast<const uint16_t*>(q_norm);
+    F.wk = static_cast<const uint16_t*>(k_norm);
+    F.rc = rope_cos;
+    F.rs = rope_sin;
+    F.rope_pos = rope_positions;
+    F.R = int(R);
+    F.eps = eps;
+    F.gate_out = static_cast<uint16_t*>(gate_out);
+    F.kc = static_cast<uint16_t*>(k_cache);
+    F.vc = static_cast<uint16_t*>(v_cache);
+    const auto s = as_stream(stream);
+    auto* o = static_cast<uint16_t*>(out);
+    const auto* kc = static_cast<const uint16_t*>(k_cache);
+    const auto* vc = static_cast<const uint16_t*>(v_cache);
+    auto* sc = static_cast<float*>(scratch);
+    const auto* g = static_cast<const uint16_t*>(gate_out);
+    switch (D) {
+        case 64: return launch<64, true>(o, nullptr, g, kc, vc, cap, sc, int(B), int(T), int(nq), int(nkv), lens, len_add, nchunk, s, F);
+        case 128: return launch<128, true>(o, nullptr, g, kc, vc, cap, sc, int(B), int(T), int(nq), int(nkv), lens, len_add, nchunk, s, F);
+        case 256: return launch<256, true>(o, nullptr, g, kc, vc, cap, sc, int(B), int(T), int(nq), int(nkv), lens, len_add, nchunk, s, F);
+        default: return invalid("gqa_verify_fused: head_dim must be 64, 128 or 256");
     }
 }
 

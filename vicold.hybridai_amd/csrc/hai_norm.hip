@@ -10,8 +10,6 @@ namespace {
 
 using namespace hai;
 
-constexpr int kMaxHeadDim = 512;
-
 // rmsnorm_kernel (hip_kernels.hip:105-137): 4 rows per 256-thread block.
 // Rows up to 8192 wide are loaded once into registers (all loads in flight
 // before the first use), reduced in L64 order and normalised from registers.
@@ -37,53 +35,6 @@ __device__ __forceinline__ float rope_at(const float* row, int d, int R, const f
     const float yv = row[p + half];
     if (d < half) return fma_(xv, cs[p], -(yv * sn[p]));
     return fma_(yv, cs[p], xv * sn[p]);
-}
-
-// A head row of D <= kMaxHeadDim bf16 values, 8 per lane: lane l holds
-// elements 8l .. 8l+7 (the L64 order of l64_sumsq_bf16 for one pass).
-struct HeadPiece {
-    uint32_t w[4];
-    __device__ __forceinline__ float at(int e) const { return (e & 1) ? hi_bf(w[e >> 1]) : lo_bf(w[e >> 1]); }
-};
-__device__ __forceinline__ HeadPiece load_piece(const uint16_t* __restrict__ row, int D, int lane) {
-    HeadPiece p{{0u, 0u, 0u, 0u}};
-    if (lane * 8 < D) {
-        const uint4 d = *reinterpret_cast<const uint4*>(row + lane * 8);
-        p.w[0] = d.x; p.w[1] = d.y; p.w[2] = d.z; p.w[3] = d.w;
-    }
-    return p;
-}
-// sum of squares of a head row in l64_sumsq_bf16's order (D <= 512: one pass)
-__device__ __forceinline__ float piece_sumsq(const HeadPiece& p) {
-    float acc = 0.0f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc = fma_(p.at(e), p.at(e), acc);
-    return wave_sum64(acc);
-}
-
-// The rotation factors of the lane's dims d = lane + 64 i that RoPE touches
-// (d < R), requested as soon as the position is known.
-constexpr int kRopeSlots = kMaxHeadDim / 64;
-__device__ __forceinline__ void load_rope(float (&cv)[kRopeSlots], float (&sv)[kRopeSlots], const float* cs,
-                                          const float* sn, int D, int R, int lane) {
-    const int half = R / 2;
-#pragma unroll
-    for (int i = 0; i < kRopeSlots; ++i) {
-        const int d = lane + 64 * i;
-        const int p = d < half ? d : d - half;
-        cv[i] = d < D && d < R ? cs[p] : 0.0f;
-        sv[i] = d < D && d < R ? sn[p] : 0.0f;
-    }
-}
-// rope_at with the lane's factors for d = lane + 64 i in registers
-__device__ __forceinline__ float rope_reg(const float* row, int d, int R, float c, float sn) {
-    if (d >= R) return row[d];
-    const int half = R / 2;
-    const int p = d < half ? d : d - half;
-    const float xv = row[p];
-    const float yv = row[p + half];
-    if (d < half) return fma_(xv, c, -(yv * sn));
-    return fma_(yv, c, xv * sn);
 }
 
 // q_gate_rmsnorm_rope_kernel (hip_fused_kernels.hip:87-141): one wave per

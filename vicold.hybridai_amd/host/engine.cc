@@ -689,13 +689,20 @@ int Engine::attention_layer(const LayerWeights& L, int64_t T, uint16_t* h, const
     const int64_t rows = B_ * T;
     HAI_TRY(norm_gemm(proj_, d.Nqkv, h, L.in_ln, nullptr, lin(L.w_qkv, L.f_qkv), rows, d.Nqkv, HAI_EPI_STORE,
                       nullptr, 0));
-    HAI_TRY(hai_qkv_rmsnorm_rope_append_bf16(q_, gate_, kc, vc, cap_, proj_, d.Nqkv, L.q_norm, L.k_norm, rope_cos_,
-                                             rope_sin_, cap_, B_, T, d.nq, d.nkv, d.D, d.R, lens, 0, cfg_.rms_eps,
-                                             stream_));
-    // tolerance mode: Q.K^T and P.V on the matrix cores
-    const auto attend = (mfma_ || fast_) ? hai_gqa_verify_mfma_bf16 : hai_gqa_verify_bf16;
-    HAI_TRY(attend(att_, q_, gate_, kc, vc, cap_, gqa_scratch_, B_, T, d.nq, d.nkv, d.D, lens,
-                   static_cast<int32_t>(T), cap_, stream_));
+    if (mfma_ || fast_) {
+        // tolerance mode: Q.K^T and P.V on the matrix cores
+        HAI_TRY(hai_qkv_rmsnorm_rope_append_bf16(q_, gate_, kc, vc, cap_, proj_, d.Nqkv, L.q_norm, L.k_norm,
+                                                 rope_cos_, rope_sin_, cap_, B_, T, d.nq, d.nkv, d.D, d.R, lens, 0,
+                                                 cfg_.rms_eps, stream_));
+        HAI_TRY(hai_gqa_verify_mfma_bf16(att_, q_, gate_, kc, vc, cap_, gqa_scratch_, B_, T, d.nq, d.nkv, d.D, lens,
+                                         static_cast<int32_t>(T), cap_, stream_));
+    } else {
+        // the q / k norms, RoPE and the cache append inside the attention's
+        // partial pass (bit-identical to the two launches)
+        HAI_TRY(hai_gqa_verify_fused_bf16(att_, gate_, proj_, d.Nqkv, L.q_norm, L.k_norm, rope_cos_, rope_sin_, cap_,
+                                          d.R, cfg_.rms_eps, kc, vc, cap_, gqa_scratch_, B_, T, d.nq, d.nkv, d.D,
+                                          lens, static_cast<int32_t>(T), cap_, stream_));
+    }
     return gemm(h, d.H, att_, d.qw, lin(L.w_o, L.f_o), rows, d.H, d.qw, HAI_EPI_RESIDUAL, h, d.H);
 }
 
