@@ -139,6 +139,7 @@ Engine::~Engine() {
     if (d_gen_ov_) hai_free(d_gen_ov_);
     if (d_eos_) hai_free(d_eos_);
     if (h_stage_) hai_host_free(h_stage_);
+    if (h_read_) hai_host_free(h_read_);
     if (stream_) hai_stream_destroy(stream_);
 }
 
@@ -381,6 +382,10 @@ int Engine::alloc_all() {
     void* pin = nullptr;
     HAI_TRY(hai_host_malloc(&pin, static_cast<size_t>(3 * B_) * sizeof(int32_t)));
     h_stage_ = static_cast<int32_t*>(pin);
+    // Pinned read-back: copies into pageable memory are staged and wait one
+    // by one; into pinned memory they queue behind the round's kernels and
+    // the round's one sync covers them all.
+    HAI_TRY(hai_host_malloc(&h_read_, static_cast<size_t>(4 * B_) * 4 + static_cast<size_t>(2 * B_ * T + B_) * 8));
     return sync();
 }
 
@@ -410,8 +415,15 @@ int Engine::sync() {
 }
 
 int Engine::read_i64(const int64_t* d, int64_t* h, int64_t n) {
-    HAI_TRY(hai_memcpy_d2h(h, d, static_cast<size_t>(n) * 8, stream_));
-    return sync();
+    if (n > B_ || h_read_ == nullptr) {
+        HAI_TRY(hai_memcpy_d2h(h, d, static_cast<size_t>(n) * 8, stream_));
+        return sync();
+    }
+    int64_t* pin = read_ids() + 2 * B_ * tmax_;
+    HAI_TRY(hai_memcpy_d2h(pin, d, static_cast<size_t>(n) * 8, stream_));
+    HAI_TRY(sync());
+    std::copy(pin, pin + n, h);
+    return HAI_OK;
 }
 
 int Engine::upload_ids(int64_t** table, int64_t* cap, const int32_t* ids, int64_t n) {
@@ -1091,8 +1103,8 @@ int Engine::one_round(int64_t width, const RoundIo& io, bool* any_live) {
             for (size_t b = 0; b < Bz; ++b) {
                 const int64_t pos = rs_[b].emitted + 1 + i;
                 if (i < pc[b] && pos < io.n_ov)
-                    HAI_TRY(hai_memcpy_d2d(d_vids_ + static_cast<int64_t>(b) * T + i + 1,
-                                           io.ov + static_cast<int64_t>(b) * io.n_ov + pos, 8, stream_));
+                    HAI_TRY(hai_copy_i64_strided(d_vids_ + static_cast<int64_t>(b) * T + i + 1, 1,
+                                                 io.ov + static_cast<int64_t>(b) * io.n_ov + pos, 1, 1, stream_));
             }
         if (chain_on_device)
             HAI_TRY(hai_draft_chain_count(i, d_vids_, T, d_pcap_, d_eos_, io.n_eos, d_ndraft_, B_, stream_));
@@ -1128,11 +1140,13 @@ int Engine::one_round(int64_t width, const RoundIo& io, bool* any_live) {
     // ---- verify + fused argmax/accept ----
     t0 = Clock::now();
     HAI_TRY(verify_step(T));
-    std::vector<int32_t> res(4 * Bz);
-    std::vector<int64_t> preds(Bz * static_cast<size_t>(T)), ids(Bz * static_cast<size_t>(T));
-    HAI_TRY(hai_memcpy_d2h(res.data(), d_result_, res.size() * 4, stream_));
-    HAI_TRY(hai_memcpy_d2h(preds.data(), d_preds_, preds.size() * 8, stream_));
-    HAI_TRY(hai_memcpy_d2h(ids.data(), d_vids_, ids.size() * 8, stream_));
+    const int32_t* res = static_cast<const int32_t*>(h_read_);
+    const int64_t* preds = read_ids();
+    const int64_t* ids = preds + Bz * static_cast<size_t>(T);
+    HAI_TRY(hai_memcpy_d2h(h_read_, d_result_, 4 * Bz * 4, stream_));
+    HAI_TRY(hai_memcpy_d2h(read_ids(), d_preds_, Bz * static_cast<size_t>(T) * 8, stream_));
+    HAI_TRY(hai_memcpy_d2h(read_ids() + Bz * static_cast<size_t>(T), d_vids_, Bz * static_cast<size_t>(T) * 8,
+                           stream_));
     if (chain_on_device) HAI_TRY(hai_memcpy_d2h(h_nd, d_ndraft_, Bz * 4, stream_));
     HAI_TRY(sync());
     if (chain_on_device)
@@ -1159,8 +1173,8 @@ int Engine::one_round(int64_t width, const RoundIo& io, bool* any_live) {
         recs[b] = rec;
         const int64_t a = res[4 * b];
         const bool full = res[4 * b + 1] != 0;
-        const int64_t* cands = ids.data() + b * static_cast<size_t>(T) + 1;
-        const int64_t* pr = preds.data() + b * static_cast<size_t>(T);
+        const int64_t* cands = ids + b * static_cast<size_t>(T) + 1;
+        const int64_t* pr = preds + b * static_cast<size_t>(T);
         if (rec != nullptr) {
             std::fill(rec, rec + HAI_ROUND_RECORD, -1);
             rec[0] = static_cast<int32_t>(kb);

@@ -265,6 +265,9 @@ private:
     int one_round(int64_t width, const RoundIo& io, bool* any_live);
     int sync();
     int read_i64(const int64_t* d, int64_t* h, int64_t n);
+    int64_t* read_ids() const {  // the int64 part of h_read_, after the [4B] results
+        return reinterpret_cast<int64_t*>(static_cast<char*>(h_read_) + 16 * B_);
+    }
     // ids (int32, host) widened into an engine-owned device table that grows on demand
     int upload_ids(int64_t** table, int64_t* cap, const int32_t* ids, int64_t n);
     // Replays the captured graph in *slot (capturing `enqueue` on first use)
@@ -338,6 +341,7 @@ private:
     int64_t eos_cap_ = 0;
     int32_t* d_pcap_ = nullptr;      // [B] proposal caps of the round (device chain counting)
     int32_t* h_stage_ = nullptr;     // pinned [3B]: caps, draft counts, MTP length corrections of a round
+    void* h_read_ = nullptr;         // pinned read-back of a round: [4B] results | [B·tmax] predictions | [B·tmax] ids | [B] ids
     int64_t syncs_ = 0;              // host synchronisations with the stream so far
     uint16_t* h_ = nullptr;       // [rows, H] residual stream
     uint16_t* xn_ = nullptr;      // [rows, 2H]
