@@ -1222,13 +1222,20 @@ def test_fp8_synthetic_scales_match_oracle():
         assert np.array_equal(d.download(np.float32), orc.fp8_synthetic_scales(seed, tid, n))
 
 
+@pytest.mark.parametrize("nospecial", [False, True])
 @pytest.mark.parametrize("M,N,K_,epi,with_xn,mapped", [
     (1, 700, 5120, 0, False, False), (2, 2 * 8200, 1000, 2, True, False), (2, 640, 2048, 1, False, True),
-    (3, 300, 5120, 0, True, False), (16, 256, 1024, 2, False, False), (2, 16400, 768, 0, True, True)])
-def test_gemm_rmsnorm_fp8_fused(M, N, K_, epi, with_xn, mapped):
+    (3, 300, 5120, 0, True, False), (16, 256, 1024, 2, False, False), (2, 16400, 768, 0, True, True),
+    (2, 2 * 8200, 5120, 2, False, False),  # four rows per wave, five whole chunk groups
+    (2, 1000, 3384, 0, False, False),      # three whole groups, then a ragged chunk
+    (1, 700, 1024, 1, False, False)])      # one whole group
+def test_gemm_rmsnorm_fp8_fused(M, N, K_, epi, with_xn, mapped, nospecial):
     """hai_gemm_rmsnorm_fp8_bf16 == rmsnorm then the FP8 GEMM (LDS prologue
     below the fused limit, two kernels above it), with and without a
-    per-row scale map (two stacked tensors, the second starting mid-block)."""
+    per-row scale map (two stacked tensors, the second starting mid-block).
+    The saturating quantiser writes no 0x7F / 0xFF, so the same weights also
+    run with HAI_FP8_NO_SPECIAL_CODES (whose fused launches request the next
+    chunk group's codes before computing the current one)."""
     rng = np.random.default_rng(131 + M * 7 + N + K_ + epi)
     x, xb = rand_bf16(rng, (M, K_))
     nw, nwb = rand_bf16(rng, (K_,), 0.02)
@@ -1263,7 +1270,8 @@ def test_gemm_rmsnorm_fp8_fused(M, N, K_, epi, with_xn, mapped):
     dy = dev(hb) if epi == hai.EPI_RESIDUAL else out_buf(M * ncols * 2)
     hai.check(kern().hai_gemm_rmsnorm_fp8_bf16(dy.ptr, ncols, dx.ptr, K_, dnw.ptr, 1e-6, 1,
                                                dxn.ptr if dxn else None, K_, dq.ptr, ds.ptr,
-                                               dm.ptr if dm else None, M, N, K_, epi,
+                                               dm.ptr if dm else None, M, N, K_,
+                                               epi | (hai.FP8_NO_SPECIAL_CODES if nospecial else 0),
                                                dy.ptr if epi == hai.EPI_RESIDUAL else None, ncols, None),
               "gemm_rmsnorm_fp8")
     if epi == hai.EPI_STORE:
