@@ -99,3 +99,24 @@ def test_noalloc_attention_bounds_its_shape_before_sizing():
     assert k.hai_gqa_scratch_bytes(big, big, 24, 256, 4096) == 2 ** 64 - 1
     # 2 rows x 24 heads x 64 chunks of 64 keys x (256 + 2) floats
     assert k.hai_gqa_scratch_bytes(1, 2, 24, 256, 4096) == 2 * 24 * 64 * 258 * 4
+
+
+def test_fused_attention_checks_need_no_device():
+    """hai_gqa_verify_fused_bf16 rejects on the host, before any device
+    call: a null operand, projection rows narrower than [q+gate | k | v],
+    an odd rotary width or one wider than the head, no rotation table, a
+    cache window past the capacity, a host-side length that does not cover
+    the T new rows, unaligned caches or projection rows, and a head_dim
+    other than 64, 128 or 256."""
+    k = hai.kernels()
+    p = ctypes.c_void_p(16)  # never dereferenced
+
+    def call(proj=p, ld=14336, R=64, rope_pos=4096, kc=p, max_len=4096, len_add=2, D=256):
+        return k.hai_gqa_verify_fused_bf16(p, p, proj, ld, p, p, p, p, rope_pos, R, 1e-6, kc, p, 4096, p, 1, 2,
+                                           24, 4, D, None, len_add, max_len, None)
+    for kw, what in (({"proj": None}, b"null pointer"), ({"ld": 14335}, b"shape"), ({"R": 63}, b"shape"),
+                     ({"R": 512}, b"shape"), ({"rope_pos": 0}, b"shape"), ({"max_len": 5000}, b"shape"),
+                     ({"len_add": 1}, b"cache length"), ({"kc": ctypes.c_void_p(24)}, b"alignment"),
+                     ({"ld": 14340}, b"alignment"), ({"D": 100, "ld": 5600}, b"head_dim")):
+        assert call(**kw) == hai.ERR_INVALID, kw
+        assert what in k.hai_last_error(), (kw, k.hai_last_error())
