@@ -42,7 +42,7 @@ ROOT = Path(__file__).resolve().parent
 HBM_PEAK_GBS = 8000.0
 # HBM traffic / algorithmic weight bytes of the verify-step GEMMs (rocprofv3 FETCH_SIZE x 2.0 +
 # WRITE_SIZE, scaled by a known-size copy): profiles/gemm_bf16_kernel_c3_traffic.txt
-GEMM_TRAFFIC_RATIO = 1.0037
+GEMM_TRAFFIC_RATIO = 1.0038
 METRIC = "accepted tok/s + verify steps/s (27B-shape bf16, bs=1, MTP k=1); % HBM peak"
 
 
